@@ -1,0 +1,240 @@
+/* thvm_hip.h -- C-ABI of libthvm_hip.so, the MI355X (gfx950) DEV=hip device
+ * for thvm's tensor track.
+ *
+ * Every entry point takes plain integers, byte counts and host pointers.
+ * Device memory is addressed by buffer ids (u32, 0 = "no buffer"), exactly as
+ * the reference Backend vtable addresses it (reference src/thvm.h:751-829), so
+ * a `struct Backend HIP_BACKEND` in the reference tree wires these functions in
+ * field by field.  Each declaration names the reference entry it replaces.
+ *
+ * Errors: int entry points return 0 on success and -1 on failure; u32 entry
+ * points return 0 on failure.  The reason is kept in a static string
+ * (thvm_hip_last_error) and printed to stderr, as the CUDA backend does
+ * (reference src/backend/cuda/init.c:95-102).
+ *
+ * Threading: one host thread, one device (ordinal 0), one stream.  Launches
+ * are asynchronous; thvm_hip_dispatch_end drains.  buf_read drains first.
+ */
+#ifndef THVM_HIP_H
+#define THVM_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* dtype ids: the reference DT_* numbering (reference src/thvm.h:254-271). */
+enum {
+  THVM_DT_BOOL = 0, THVM_DT_INT8 = 1, THVM_DT_UINT8 = 2, THVM_DT_INT16 = 3,
+  THVM_DT_UINT16 = 4, THVM_DT_INT32 = 5, THVM_DT_UINT32 = 6, THVM_DT_INT64 = 7,
+  THVM_DT_UINT64 = 8, THVM_DT_FP8E4M3 = 9, THVM_DT_FP8E5M2 = 10,
+  THVM_DT_FP16 = 11, THVM_DT_BF16 = 12, THVM_DT_FP32 = 13, THVM_DT_FP64 = 14
+};
+
+/* Backend id the reference reserves for a fourth device: CPU=1, METAL=2,
+ * CUDA=3 (reference src/codegen/hand_opts.c:174, src/thvm.c:676). */
+#define THVM_HIP_BACKEND_ID 4u
+
+/* ===================== lifecycle (Backend.init / .shutdown) ============= */
+
+/* cuda_init (reference src/backend/cuda/init.c:110): pick device 0, create
+ * the dispatch stream.  Idempotent.  -1 when no gfx950 device is present. */
+int         thvm_hip_init(void);
+/* cuda_shutdown: free every buffer, module, graph and the stream. */
+void        thvm_hip_shutdown(void);
+/* cuda available probe (reference src/backend/cuda/_.c:62). */
+int         thvm_hip_available(void);
+/* thvm_cuda_last_error (reference src/backend/cuda/init.c:95-102). */
+const char *thvm_hip_last_error(void);
+/* Library version string, e.g. "thvm-hip 0.1 gfx950". */
+const char *thvm_hip_version(void);
+
+/* ===================== buffers (Backend.buf_*) ========================== */
+
+/* cuda_buf_alloc (reference src/backend/cuda/buf_alloc.c:19): zero-filled
+ * device buffer, best-fit freelist recycle first.  0 on failure. */
+uint32_t thvm_hip_buf_alloc(uint64_t nbytes);
+/* cuda_buf_free (buf_free.c): drop the slot now (stream-ordered free). */
+void     thvm_hip_buf_free(uint32_t buf_id);
+/* cuda_buf_incref / cuda_buf_decref: refcount; decref to 0 parks the block
+ * on the freelist (buf_decref.c, buf_freelist.c). */
+void     thvm_hip_buf_incref(uint32_t buf_id);
+void     thvm_hip_buf_decref(uint32_t buf_id);
+/* cuda_buf_jit_pin / unpin: sticky hold by an active JIT capture. */
+void     thvm_hip_buf_jit_pin(uint32_t buf_id);
+void     thvm_hip_buf_jit_unpin(uint32_t buf_id);
+/* cuda_buf_read / cuda_buf_write / cuda_buf_copy (buf_read.c, buf_write.c,
+ * buf_copy.c).  Byte 0 based; nbytes must fit the buffer. */
+int      thvm_hip_buf_read (uint32_t buf_id, void *dst, uint64_t nbytes);
+int      thvm_hip_buf_write(uint32_t buf_id, const void *src, uint64_t nbytes);
+int      thvm_hip_buf_copy (uint32_t dst_id, uint32_t src_id, uint64_t nbytes);
+/* Backend.buf_write_at / buf_copy_at (reference src/thvm.h:780-787): the
+ * KV-append form, bounds-checked against the destination. */
+int      thvm_hip_buf_write_at(uint32_t buf_id, uint64_t byte_off,
+                               const void *src, uint64_t nbytes);
+int      thvm_hip_buf_copy_at(uint32_t dst_id, uint64_t dst_byte_off,
+                              uint32_t src_id, uint64_t nbytes);
+/* cuda_buf_refcount / freelist_push / freelist_remove / storage_root /
+ * nbytes / zero (reference src/thvm.h:788-815). */
+uint32_t thvm_hip_buf_refcount(uint32_t buf_id);
+void     thvm_hip_buf_freelist_push(uint32_t buf_id);
+void     thvm_hip_buf_freelist_remove(uint32_t buf_id);
+uint32_t thvm_hip_buf_storage_root(uint32_t buf_id);
+uint64_t thvm_hip_buf_nbytes(uint32_t buf_id);
+void     thvm_hip_buf_zero(uint32_t buf_id);
+/* Arena view: a non-owning buffer id aliasing [off, off+nbytes) of parent
+ * (cuda_buf_alloc_arena_view, reference src/backend/cuda/buf_alloc.c:189-205).
+ * Holds a reference on the parent.  0 on failure. */
+uint32_t thvm_hip_buf_view(uint32_t parent_id, uint64_t byte_off, uint64_t nbytes);
+/* Raw device address of a buffer (cuda_buf_dptr), for interop only. */
+uint64_t thvm_hip_buf_device_ptr(uint32_t buf_id);
+/* Live / peak device bytes (cuda_buf_live_bytes / cuda_buf_peak_bytes). */
+uint64_t thvm_hip_mem_live_bytes(void);
+uint64_t thvm_hip_mem_peak_bytes(void);
+
+/* ===================== dispatch (Backend.dispatch_*) ==================== */
+
+void thvm_hip_dispatch_begin(void);
+void thvm_hip_dispatch_flush(void);
+/* cuda_dispatch_end (reference src/backend/cuda/_.c:23-27): drain the
+ * stream; a no-op while a graph capture is open. */
+void thvm_hip_dispatch_end(void);
+
+/* Custom-kernel dispatch: the body of Backend.dispatch_kernel for a
+ * KernelEntry carrying custom_program (cuda_custom_dispatch, reference
+ * src/backend/cuda/jit.c:802; ABI reference src/schedule/kernel_custom.c:14-35).
+ *   name/program : KernelEntry.custom_name / custom_program
+ *   grid/block   : custom_grid[3] / custom_block[3]
+ *   shared_bytes : custom_shared_bytes (dynamic LDS; up to 160 KiB on gfx950)
+ *   buf_ids      : one buffer id per argument slot, n_args <= 64
+ *   outs_mask    : custom_outs_mask (slots the kernel writes)
+ * Two program forms:
+ *   - HIP source: `extern "C" __global__ void <name>(T *arg0, ...)`, compiled
+ *     by hiprtc for gfx950 and cached by source hash (memory + disk);
+ *   - "thvm-builtin:<kernel> key=value ...": a hand-written gfx950 kernel
+ *     linked into this library (GEMV, norms, attention, routing, ...).  The
+ *     library picks its own launch geometry; grid/block are ignored.
+ * Inside a JIT capture the dispatch is also recorded for replay. */
+int thvm_hip_dispatch_custom(const char *name, const char *program,
+                             const uint32_t grid[3], const uint32_t block[3],
+                             uint32_t shared_bytes,
+                             const uint32_t *buf_ids, uint32_t n_args,
+                             uint64_t outs_mask);
+
+/* Compile-only probe of a custom program (hiprtc or builtin parse): 0 when
+ * it would dispatch.  Used by hosts to fail early. */
+int thvm_hip_program_check(const char *name, const char *program);
+
+/* ===================== JIT capture / replay ============================ */
+/* The reference capture API (src/jit/capture.c:644-745, 2687-2884) restricted
+ * to custom dispatches: ops fired between begin and end are recorded, every
+ * argument buffer is JIT-pinned, and jit_replay re-issues the sequence.  The
+ * first replay captures the stream into a hipGraph; later replays are one
+ * hipGraphLaunch.  Slots are 1..15; 0 means failure. */
+uint32_t thvm_hip_jit_capture_begin(void);
+void     thvm_hip_jit_capture_end(void);
+uint32_t thvm_hip_jit_capture_op_count(uint32_t slot);
+int      thvm_hip_jit_replay(uint32_t slot);
+/* jit_replay_with_inputs (capture.c:2615): rebind argument buffer ids
+ * (old -> new) for this and later replays; the graph is re-captured when a
+ * device address moved.  n pairs in old_ids/new_ids. */
+int      thvm_hip_jit_rebind(uint32_t slot, const uint32_t *old_ids,
+                             const uint32_t *new_ids, uint32_t n);
+void     thvm_hip_jit_capture_drop(uint32_t slot);
+int      thvm_hip_jit_is_capturing(void);
+
+/* Backend graph hooks used by the reference's own jit_replay
+ * (cuda_jit_graph_*, reference src/backend/cuda/jit.c:457-615). */
+int  thvm_hip_graph_replay(uint32_t slot);
+int  thvm_hip_graph_capture_begin(void);
+int  thvm_hip_graph_capture_end_and_launch(uint32_t slot);
+void thvm_hip_graph_invalidate(uint32_t slot);
+
+/* ===================== timing =========================================== */
+/* hipEvent pair on the dispatch stream (replaces THVM_CUDA_GPU_TIME,
+ * reference src/backend/cuda/jit.c:990-1016).  Returns a timer id. */
+uint32_t thvm_hip_timer_start(void);
+/* Milliseconds between start and now (drains the stream). */
+double   thvm_hip_timer_stop(uint32_t timer_id);
+/* Per-builtin-kernel time: when enabled, every builtin dispatch brackets
+ * itself with hipEvents on the dispatch stream (not under graph capture)
+ * and accumulates into a table keyed by kernel tag. */
+void     thvm_hip_kprof_enable(int on);
+void     thvm_hip_kprof_reset(void);
+/* Total ms and launch count for kernel tag (e.g. "gemv"); -1 when absent. */
+double   thvm_hip_kprof_query(const char *tag, uint64_t *count_out);
+
+/* ===================== decode models ==================================== */
+/* C counterpart of the reference's decode drivers (bench/dsv2_decode_bench.c
+ * step_build :2328-2430 and the GPT-2 driver bench/gpt2/thvm_gpt2.py): a
+ * synthetic, seeded, random-init decoder whose whole decode step is a list of
+ * custom dispatches, captured once and replayed with a device-resident token
+ * and position (no host values per step). */
+enum {
+  THVM_ARCH_LLAMA = 1,   /* RMSNorm, GQA + RoPE, SwiGLU (config C4)      */
+  THVM_ARCH_GPT2  = 2,   /* LayerNorm, learned positions, GELU (C1, C3)  */
+  THVM_ARCH_DSV2  = 3    /* MLA latent cache + MoE (C5)                  */
+};
+
+typedef struct ThvmDecodeConfig {
+  uint32_t arch;          /* THVM_ARCH_*                                   */
+  uint32_t n_layers;
+  uint32_t dim;           /* d_model                                       */
+  uint32_t n_heads;
+  uint32_t n_kv_heads;    /* GQA; = n_heads for MHA                        */
+  uint32_t head_dim;
+  uint32_t ffn;           /* FFN width (dense layers)                      */
+  uint32_t vocab;
+  uint32_t max_seq;       /* KV capacity (positions)                       */
+  uint32_t batch;         /* rows decoded per step                         */
+  uint32_t wdtype;        /* weight dtype: FP32 / FP16 / BF16 / FP8E4M3    */
+  uint32_t adtype;        /* activation dtype: FP32 / FP16 / BF16          */
+  float    eps;           /* norm epsilon                                  */
+  float    rope_theta;    /* RoPE base (LLAMA, DSV2)                       */
+  float    init_std;      /* weight N(0, init_std)                         */
+  /* DSV2 (MLA + MoE) fields; ignored by the other archs                  */
+  uint32_t kv_lora;       /* latent rank                                   */
+  uint32_t d_nope, d_rope, d_v;
+  uint32_t n_experts, n_shared, top_k, moe_inter, first_dense;
+  uint32_t reserved[8];
+} ThvmDecodeConfig;
+
+/* Build the model on device: allocate, fill weights from `seed` (weights
+ * N(0, init_std); fp8 weights per-row absmax/448 e4m3 with f32 scales; norm
+ * gains 1), compile the step.  Returns a handle > 0, 0 on failure. */
+uint32_t thvm_hip_decoder_create(const ThvmDecodeConfig *cfg, uint64_t seed);
+void     thvm_hip_decoder_destroy(uint32_t dec);
+/* Fill the KV cache rows [0, ctx) of every layer and batch row with N(0,1)
+ * values from `seed` and set the position so the next step writes row ctx. */
+int      thvm_hip_decoder_prefill_synthetic(uint32_t dec, uint32_t ctx, uint64_t seed);
+/* Set the current token of each batch row (n = batch) and the position
+ * (the row the next step writes). */
+int      thvm_hip_decoder_set_state(uint32_t dec, const int32_t *tokens, uint32_t pos);
+/* One eager decode step: every kernel dispatched individually. */
+int      thvm_hip_decoder_step(uint32_t dec);
+/* Capture one step into a JIT slot (runs it once) and return the slot. */
+uint32_t thvm_hip_decoder_capture(uint32_t dec);
+/* Replay the captured step n_steps times (graph launches, no host values).
+ * Each step writes its greedy token into the history buffer. */
+int      thvm_hip_decoder_replay(uint32_t dec, uint32_t n_steps);
+/* Read back the token history rows [0, n) of batch row b (greedy ids), and
+ * the logits [batch, vocab] f32 of the last step. */
+int      thvm_hip_decoder_read_tokens(uint32_t dec, int32_t *dst, uint32_t n);
+int      thvm_hip_decoder_read_logits(uint32_t dec, float *dst, uint64_t nfloats);
+uint32_t thvm_hip_decoder_position(uint32_t dec);
+/* Named tensor of the model (e.g. "l0.wqkv", "l0.kcache", "emb", "x"):
+ * buffer id, dtype and byte size, so a host can read weights back. */
+uint32_t thvm_hip_decoder_tensor(uint32_t dec, const char *name,
+                                 uint32_t *dtype_out, uint64_t *nbytes_out);
+/* Algorithmic HBM bytes one decode step reads+writes at the current
+ * position (weights + KV over the live context + activations). */
+uint64_t thvm_hip_decoder_step_bytes(uint32_t dec);
+/* Number of dispatches in one step. */
+uint32_t thvm_hip_decoder_step_kernels(uint32_t dec);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* THVM_HIP_H */

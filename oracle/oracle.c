@@ -1,0 +1,428 @@
+/* oracle.c -- TEST INFRASTRUCTURE ONLY (see oracle.h).  A CPU restatement of
+ * the reference thvm CPU path for the decode hot path.  Nothing in the
+ * product library links or loads this file; it is the checker.
+ *
+ * Build: oracle/Makefile (gcc -O3 -fno-math-errno -ffp-contract=off, the
+ * reference CPU JIT flags of src/backend/cpu/jit.c:318-345 minus -march). */
+#include "oracle.h"
+
+#include <math.h>
+#include <stdlib.h>
+#include <string.h>
+
+enum { DT_FP8E4M3 = 9, DT_FP8E5M2 = 10, DT_FP16 = 11, DT_BF16 = 12, DT_FP32 = 13 };
+
+static uint32_t f2u(float f) { uint32_t u; memcpy(&u, &f, 4); return u; }
+static float u2f(uint32_t u) { float f; memcpy(&f, &u, 4); return f; }
+
+/* ==== bf16: reference src/dtype/fp_convert.c:113-136 ==================== */
+float or_bf16_to_f32(uint16_t b) { return u2f((uint32_t)b << 16); }
+
+uint16_t or_f32_to_bf16(float v) {
+  uint32_t bits = f2u(v);
+  if (((bits >> 23) & 0xFFu) == 0xFFu && (bits & 0x7FFFFFu) != 0u)
+    return (uint16_t)(((bits & 0x80000000u) | 0x7F800000u | 0x400000u) >> 16);
+  return (uint16_t)(((bits + 0x7FFFu + ((bits >> 16) & 1u)) & 0xFFFF0000u) >> 16);
+}
+
+/* ==== fp16: reference src/dtype/fp_convert.c:26-110 (manual forms) ====== */
+float or_fp16_to_f32(uint16_t h) {
+  uint32_t sign = (uint32_t)(h >> 15) & 1u, exp = (uint32_t)(h >> 10) & 0x1Fu, mant = h & 0x3FFu;
+  uint32_t out;
+  if (exp == 0) {
+    if (mant == 0) {
+      out = sign << 31;
+    } else {
+      uint32_t sh = 0;
+      while ((mant & 0x400u) == 0) { mant <<= 1; sh++; }
+      mant &= 0x3FFu;
+      out = (sign << 31) | ((127u - 14u - sh) << 23) | (mant << 13);
+    }
+  } else if (exp == 0x1F) {
+    out = (sign << 31) | (0xFFu << 23) | (mant ? 0x400000u : 0u) | (mant << 13);
+  } else {
+    out = (sign << 31) | ((exp - 15u + 127u) << 23) | (mant << 13);
+  }
+  return u2f(out);
+}
+
+uint16_t or_f32_to_fp16(float v) {
+  uint32_t b = f2u(v);
+  uint32_t sign = (b >> 16) & 0x8000u, exp = (b >> 23) & 0xFFu, mant = b & 0x7FFFFFu;
+  if (exp == 0xFF) return (uint16_t)(sign | 0x7C00u | (mant ? (0x200u | (mant >> 13)) : 0u));
+  if (exp >= 127 + 16) return (uint16_t)(sign | 0x7C00u);
+  if (exp >= 127 - 14) {
+    uint32_t h = ((exp - 127 + 15) << 10) | (mant >> 13), r = mant & 0x1FFFu;
+    if (r > 0x1000u || (r == 0x1000u && (h & 1u))) h++;
+    return (uint16_t)(sign | h);
+  }
+  if (exp < 127 - 25) return (uint16_t)sign;
+  uint32_t m = mant | 0x800000u, sh = 126 - exp;
+  uint32_t h = m >> sh, rem = m & ((1u << sh) - 1u), half = 1u << (sh - 1u);
+  if (rem > half || (rem == half && (h & 1u))) h++;
+  return (uint16_t)(sign | h);
+}
+
+/* ==== fp8: reference src/dtype/fp8.c:36-175 ============================== */
+typedef struct {
+  uint32_t bias, sig_bits, mmask;
+  uint64_t mindenorm_o2, overflow, minnorm;
+  uint32_t maxnorm, inf_v, nan_v, sat_nan;
+} F8;
+static const F8 E4M3 = {7, 4, 0x7, 0x3F50000000000000ULL, 0x407D000000000000ULL,
+                        0x3F90000000000000ULL, 0x7E, 0x7F, 0x7F, 0x7F};
+static const F8 E5M2 = {15, 3, 0x3, 0x3EE0000000000000ULL, 0x40EE000000000000ULL - 1,
+                        0x3F10000000000000ULL, 0x7B, 0x7C, 0x7F, 0x7C};
+
+static uint8_t f8_enc(float x, const F8 *c, int sat) {
+  double xd = (double)x;
+  uint64_t xb;
+  memcpy(&xb, &xd, 8);
+  uint64_t ax = xb & 0x7FFFFFFFFFFFFFFFULL, inf = 0x7FF0000000000000ULL;
+  uint32_t sign = (uint32_t)((xb >> 63) & 1) << 7;
+  if (ax == inf) return (uint8_t)(sign | (sat ? c->maxnorm : c->inf_v));
+  if (ax > inf) {
+    if (!sat) return (uint8_t)(sign | c->nan_v);
+    uint32_t top = (f2u(x) >> (24 - c->sig_bits)) & c->mmask;
+    return (uint8_t)(sign | c->sat_nan | top);
+  }
+  uint64_t half_ulp = (uint64_t)1 << (53 - c->sig_bits - 1);
+  int32_t e = (int32_t)((xb >> 52) & 0x7FF) - 1023 + (int32_t)c->bias;
+  uint32_t mant = (uint32_t)((xb >> (53 - c->sig_bits)) & c->mmask);
+  uint32_t res;
+  if (ax <= c->mindenorm_o2) {
+    res = 0;
+  } else if (ax > c->overflow) {
+    res = c->maxnorm;
+  } else if (ax >= c->minnorm) {
+    res = ((uint32_t)e << (c->sig_bits - 1)) | mant;
+    uint64_t rb = xb & ((half_ulp << 1) - 1);
+    if (rb > half_ulp || (rb == half_ulp && (mant & 1))) res += 1;
+  } else {
+    int32_t sh = 1 - e;
+    uint32_t m = mant | (1u << (c->sig_bits - 1));
+    res = m >> sh;
+    uint64_t mask = (half_ulp << (sh + 1)) - 1;
+    uint64_t rb = (xb | ((uint64_t)1 << 52)) & mask;
+    uint64_t ulp = half_ulp << sh;
+    if (rb > ulp || (rb == ulp && (res & 1))) res += 1;
+  }
+  return (uint8_t)(res | sign);
+}
+
+uint8_t or_f32_to_fp8e4m3(float v) { return f8_enc(v, &E4M3, 0); }
+uint8_t or_f32_to_fp8e4m3_sat(float v) { return f8_enc(v, &E4M3, 1); }
+uint8_t or_f32_to_fp8e5m2(float v) { return f8_enc(v, &E5M2, 0); }
+uint8_t or_f32_to_fp8e5m2_sat(float v) { return f8_enc(v, &E5M2, 1); }
+
+float or_fp8e5m2_to_f32(uint8_t x) {
+  uint16_t ur = (uint16_t)((uint16_t)x << 8);
+  if ((ur & 0x7FFFu) > 0x7C00u) ur = 0x7FFFu;
+  return or_fp16_to_f32(ur);
+}
+
+float or_fp8e4m3_to_f32(uint8_t x) {
+  uint16_t ur = (uint16_t)((uint16_t)x << 8);
+  uint16_t sign = ur & 0x8000u;
+  uint16_t ex = (uint16_t)((((uint32_t)ur & 0x7800u) >> 1) + 0x2000u);
+  uint16_t ma = (uint16_t)((ur & 0x0700u) >> 1);
+  if ((x & 0x7Fu) == 0x7Fu) {
+    ur = 0x7FFFu;
+  } else if (ex == 0x2000u) {
+    if (ma) {
+      ma <<= 1;
+      while ((ma & 0x0400u) == 0) { ma <<= 1; ex -= 0x0400u; }
+      ma &= 0x03FFu;
+    } else {
+      ex = 0;
+    }
+    ur = (uint16_t)(sign | ex | ma);
+  } else {
+    ur = (uint16_t)(sign | ex | ma);
+  }
+  return or_fp16_to_f32(ur);
+}
+
+static float ld(const void *p, uint64_t i, uint32_t dt) {
+  switch (dt) {
+    case DT_FP32: return ((const float *)p)[i];
+    case DT_BF16: return or_bf16_to_f32(((const uint16_t *)p)[i]);
+    case DT_FP16: return or_fp16_to_f32(((const uint16_t *)p)[i]);
+    case DT_FP8E4M3: return or_fp8e4m3_to_f32(((const uint8_t *)p)[i]);
+    case DT_FP8E5M2: return or_fp8e5m2_to_f32(((const uint8_t *)p)[i]);
+    default: return 0.0f;
+  }
+}
+/* store with the kernel-store narrowing (uop_walk.c:189-205) */
+static void st(void *p, uint64_t i, uint32_t dt, float v) {
+  switch (dt) {
+    case DT_FP32: ((float *)p)[i] = v; break;
+    case DT_BF16: ((uint16_t *)p)[i] = or_f32_to_bf16(v); break;
+    case DT_FP16: ((uint16_t *)p)[i] = or_f32_to_fp16(v); break;
+    case DT_FP8E4M3: ((uint8_t *)p)[i] = or_f32_to_fp8e4m3_sat(v); break;
+    case DT_FP8E5M2: ((uint8_t *)p)[i] = or_f32_to_fp8e5m2_sat(v); break;
+    default: break;
+  }
+}
+/* a value rounded through dtype storage (uop_walk.c:272-284) */
+static float rnd(float v, uint32_t dt) {
+  if (v != v) return v;
+  switch (dt) {
+    case DT_BF16: return or_bf16_to_f32(or_f32_to_bf16(v));
+    case DT_FP16: return or_fp16_to_f32(or_f32_to_fp16(v));
+    case DT_FP8E4M3: return or_fp8e4m3_to_f32(or_f32_to_fp8e4m3_sat(v));
+    default: return v;
+  }
+}
+
+void or_decode(const void *src, uint32_t dt, float *dst, uint64_t n) {
+  for (uint64_t i = 0; i < n; i++) dst[i] = ld(src, i, dt);
+}
+void or_encode(const float *src, uint32_t dt, void *dst, uint64_t n) {
+  for (uint64_t i = 0; i < n; i++) st(dst, i, dt, src[i]);
+}
+
+/* ==== ops ================================================================ */
+
+void or_gemv(float *y, const void *x, uint32_t xdt, uint32_t ldx, const void *w, uint32_t wdt,
+             const float *scale, uint32_t M, uint32_t N, uint32_t K) {
+  float lut[256];
+  if (wdt == DT_FP8E4M3)
+    for (int i = 0; i < 256; i++) lut[i] = or_fp8e4m3_to_f32((uint8_t)i);
+  float *xf = (float *)malloc((size_t)K * sizeof(float));
+  for (uint32_t m = 0; m < M; m++) {
+    for (uint32_t k = 0; k < K; k++) xf[k] = ld(x, (uint64_t)m * ldx + k, xdt);
+    for (uint32_t n = 0; n < N; n++) {
+      float acc = 0.0f;
+      const uint64_t r = (uint64_t)n * K;
+      if (wdt == DT_FP8E4M3) {
+        const uint8_t *q = (const uint8_t *)w + r;
+        const float s = scale[n];
+        for (uint32_t k = 0; k < K; k++) {
+          float wv = lut[q[k]] * s;
+          acc += xf[k] * wv;
+        }
+      } else if (wdt == DT_FP32) {
+        const float *wf = (const float *)w + r;
+        for (uint32_t k = 0; k < K; k++) acc += xf[k] * wf[k];
+      } else {
+        for (uint32_t k = 0; k < K; k++) acc += xf[k] * ld(w, r + k, wdt);
+      }
+      y[(uint64_t)m * N + n] = acc;
+    }
+  }
+  free(xf);
+}
+
+void or_rmsnorm(void *y, uint32_t ydt, const void *x, uint32_t xdt, const float *w, uint32_t M,
+                uint32_t K, float eps) {
+  const float invK = 1.0f / (float)K;
+  for (uint32_t m = 0; m < M; m++) {
+    const uint64_t o = (uint64_t)m * K;
+    float ss = 0.0f;
+    for (uint32_t i = 0; i < K; i++) { float v = ld(x, o + i, xdt); ss += v * v; }
+    float inv = 1.0f / sqrtf(ss * invK + eps);
+    for (uint32_t i = 0; i < K; i++) {
+      float v = ld(x, o + i, xdt) * inv;
+      if (w) v = v * w[i];
+      st(y, o + i, ydt, v);
+    }
+  }
+}
+
+void or_layernorm(void *y, uint32_t ydt, const void *x, uint32_t xdt, const float *w,
+                  const float *b, uint32_t M, uint32_t K, float eps) {
+  const float invK = 1.0f / (float)K;
+  for (uint32_t m = 0; m < M; m++) {
+    const uint64_t o = (uint64_t)m * K;
+    float s = 0.0f;
+    for (uint32_t i = 0; i < K; i++) s += ld(x, o + i, xdt);
+    float mean = s * invK, vs = 0.0f;
+    for (uint32_t i = 0; i < K; i++) { float d = ld(x, o + i, xdt) - mean; vs += d * d; }
+    float r = 1.0f / sqrtf(vs * invK + eps);
+    for (uint32_t i = 0; i < K; i++) {
+      float v = (ld(x, o + i, xdt) - mean) * r;
+      if (w) v = v * w[i];
+      if (b) v = v + b[i];
+      st(y, o + i, ydt, v);
+    }
+  }
+}
+
+void or_softmax(void *y, uint32_t ydt, const void *x, uint32_t xdt, uint32_t M, uint32_t K) {
+  for (uint32_t m = 0; m < M; m++) {
+    const uint64_t o = (uint64_t)m * K;
+    float mx = -INFINITY;
+    for (uint32_t i = 0; i < K; i++) { float v = ld(x, o + i, xdt); if (v > mx) mx = v; }
+    float s = 0.0f;
+    for (uint32_t i = 0; i < K; i++) s += expf(ld(x, o + i, xdt) - mx);
+    float r = 1.0f / s;
+    for (uint32_t i = 0; i < K; i++) st(y, o + i, ydt, expf(ld(x, o + i, xdt) - mx) * r);
+  }
+}
+
+void or_rope(void *x, uint32_t dt, const float *cos_t, const float *sin_t, uint32_t B, uint32_t nh,
+             uint32_t hd, uint32_t pos) {
+  const uint32_t half = hd / 2;
+  for (uint64_t r = 0; r < (uint64_t)B * nh; r++)
+    for (uint32_t j = 0; j < half; j++) {
+      float c = cos_t[(uint64_t)pos * half + j], s = sin_t[(uint64_t)pos * half + j];
+      uint64_t i = r * hd + 2 * j;
+      float xe = ld(x, i, dt), xo = ld(x, i + 1, dt);
+      st(x, i, dt, xe * c - xo * s);
+      st(x, i + 1, dt, xo * c + xe * s);
+    }
+}
+
+void or_attn_decode(void *out, uint32_t odt, const void *q, uint32_t qdt, const void *kcache,
+                    const void *vcache, uint32_t cdt, uint32_t B, uint32_t H, uint32_t Hkv,
+                    uint32_t hd, uint32_t max_seq, uint32_t L, float scale) {
+  const uint32_t G = H / Hkv;
+  float *sc = (float *)malloc((size_t)(L ? L : 1) * sizeof(float));
+  for (uint32_t b = 0; b < B; b++)
+    for (uint32_t h = 0; h < H; h++) {
+      const uint32_t kh = h / G;
+      const uint64_t qo = ((uint64_t)b * H + h) * hd;
+      const uint64_t cb = ((uint64_t)b * Hkv + kh) * max_seq;
+      float mx = -INFINITY;
+      for (uint32_t j = 0; j < L; j++) {
+        float s = 0.0f;
+        for (uint32_t d = 0; d < hd; d++) s += ld(q, qo + d, qdt) * ld(kcache, (cb + j) * hd + d, cdt);
+        sc[j] = s * scale;
+        if (sc[j] > mx) mx = sc[j];
+      }
+      float l = 0.0f;
+      for (uint32_t j = 0; j < L; j++) { sc[j] = expf(sc[j] - mx); l += sc[j]; }
+      for (uint32_t d = 0; d < hd; d++) {
+        float a = 0.0f;
+        for (uint32_t j = 0; j < L; j++) a += sc[j] * ld(vcache, (cb + j) * hd + d, cdt);
+        st(out, qo + d, odt, a / l);
+      }
+    }
+  free(sc);
+}
+
+void or_argmax(int32_t *tok, const float *logits, uint32_t B, uint32_t V) {
+  for (uint32_t b = 0; b < B; b++) {
+    const float *lg = logits + (uint64_t)b * V;
+    float bv = lg[0];
+    int32_t bi = 0;
+    for (uint32_t i = 1; i < V; i++)
+      if (lg[i] > bv) { bv = lg[i]; bi = (int32_t)i; }
+    tok[b] = bi;
+  }
+}
+
+/* ==== whole decode step ================================================== */
+
+static float silu(float g) { return g / (1.0f + expf(-g)); }
+static float gelu(float x) {
+  float u = 0.7978845608f * (x + 0.044715f * x * x * x);
+  return 0.5f * x * (1.0f + tanhf(u));
+}
+
+int or_decode_step(const OrModel *m, const int32_t *tok, uint32_t pos, float *logits, int32_t *next) {
+  if (!m || (m->arch != 1 && m->arch != 2) || pos >= m->max_seq) return -1;
+  const uint32_t D = m->dim, H = m->n_heads, Hkv = m->n_kv_heads ? m->n_kv_heads : m->n_heads;
+  const uint32_t hd = m->head_dim, F = m->ffn, V = m->vocab, adt = m->adt, wdt = m->wdt;
+  const uint32_t nqkv = m->arch == 1 ? (H + 2 * Hkv) * hd : 3 * D;
+  const int gpt2 = m->arch == 2;
+  float *x = (float *)malloc((size_t)D * 4), *xn = (float *)malloc((size_t)D * 4);
+  float *qkv = (float *)malloc((size_t)nqkv * 4), *q = (float *)malloc((size_t)H * hd * 4);
+  float *att = (float *)malloc((size_t)H * hd * 4), *o = (float *)malloc((size_t)D * 4);
+  float *gu = (float *)malloc((size_t)2 * F * 4), *hh = (float *)malloc((size_t)F * 4);
+  const float scale = (float)(1.0 / sqrt((double)hd));
+  for (uint32_t b = 0; b < m->batch; b++) {
+    /* embedding (+ learned position) */
+    int32_t t = tok[b];
+    for (uint32_t i = 0; i < D; i++) {
+      float v = (t >= 0 && (uint32_t)t < V) ? ld(m->emb, (uint64_t)t * D + i, adt) : 0.0f;
+      if (gpt2) v = v + ld(m->pos_emb, (uint64_t)pos * D + i, adt);
+      x[i] = rnd(v, adt);
+    }
+    for (uint32_t l = 0; l < m->n_layers; l++) {
+      const OrLayer *L = &m->layers[l];
+      if (gpt2) or_layernorm(xn, DT_FP32, x, DT_FP32, L->g1, L->b1, 1, D, m->eps);
+      else or_rmsnorm(xn, DT_FP32, x, DT_FP32, L->g1, 1, D, m->eps);
+      for (uint32_t i = 0; i < D; i++) xn[i] = rnd(xn[i], adt);
+      or_gemv(qkv, xn, DT_FP32, D, L->wqkv, wdt, L->sqkv, 1, nqkv, D);
+      for (uint32_t n = 0; n < nqkv; n++) {
+        float v = qkv[n] + (gpt2 ? ld(L->bqkv, n, adt) : 0.0f);
+        qkv[n] = rnd(v, adt);
+      }
+      const uint32_t Hq = H * hd, Hk = Hkv * hd;
+      if (!gpt2) {
+        for (uint32_t n = 0; n < Hq + Hk; n += 2) {
+          uint32_t j = (n % hd) / 2;
+          float c = m->rope_cos[(uint64_t)pos * (hd / 2) + j], s = m->rope_sin[(uint64_t)pos * (hd / 2) + j];
+          float xe = qkv[n], xo = qkv[n + 1];
+          qkv[n] = rnd(xe * c - xo * s, adt);
+          qkv[n + 1] = rnd(xo * c + xe * s, adt);
+        }
+      }
+      memcpy(q, qkv, (size_t)Hq * 4);
+      for (uint32_t kh = 0; kh < Hkv; kh++)
+        for (uint32_t d = 0; d < hd; d++) {
+          uint64_t ci = (((uint64_t)b * Hkv + kh) * m->max_seq + pos) * hd + d;
+          st(L->kcache, ci, adt, qkv[Hq + kh * hd + d]);
+          st(L->vcache, ci, adt, qkv[Hq + Hk + kh * hd + d]);
+        }
+      /* attention for this row: caches hold row b's history */
+      {
+        const uint32_t G = H / Hkv;
+        const uint32_t Lc = pos + 1;
+        float *sc = (float *)malloc((size_t)Lc * 4);
+        for (uint32_t h = 0; h < H; h++) {
+          const uint64_t cb = ((uint64_t)b * Hkv + h / G) * m->max_seq;
+          float mx = -INFINITY;
+          for (uint32_t j = 0; j < Lc; j++) {
+            float s = 0.0f;
+            for (uint32_t d = 0; d < hd; d++) s += q[h * hd + d] * ld(L->kcache, (cb + j) * hd + d, adt);
+            sc[j] = s * scale;
+            if (sc[j] > mx) mx = sc[j];
+          }
+          float den = 0.0f;
+          for (uint32_t j = 0; j < Lc; j++) { sc[j] = expf(sc[j] - mx); den += sc[j]; }
+          for (uint32_t d = 0; d < hd; d++) {
+            float a = 0.0f;
+            for (uint32_t j = 0; j < Lc; j++) a += sc[j] * ld(L->vcache, (cb + j) * hd + d, adt);
+            att[h * hd + d] = rnd(a / den, adt);
+          }
+        }
+        free(sc);
+      }
+      or_gemv(o, att, DT_FP32, Hq, L->wo, wdt, L->so, 1, D, Hq);
+      for (uint32_t i = 0; i < D; i++) {
+        float v = o[i] + (gpt2 ? ld(L->bo, i, adt) : 0.0f);
+        x[i] = rnd(x[i] + rnd(v, adt), adt);
+      }
+      if (gpt2) or_layernorm(xn, DT_FP32, x, DT_FP32, L->g2, L->b2, 1, D, m->eps);
+      else or_rmsnorm(xn, DT_FP32, x, DT_FP32, L->g2, 1, D, m->eps);
+      for (uint32_t i = 0; i < D; i++) xn[i] = rnd(xn[i], adt);
+      if (gpt2) {
+        or_gemv(gu, xn, DT_FP32, D, L->wgu, wdt, L->sgu, 1, F, D);
+        for (uint32_t i = 0; i < F; i++) hh[i] = rnd(gelu(rnd(gu[i] + ld(L->bfc, i, adt), adt)), adt);
+      } else {
+        or_gemv(gu, xn, DT_FP32, D, L->wgu, wdt, L->sgu, 1, 2 * F, D);
+        for (uint32_t i = 0; i < F; i++) {
+          float g = rnd(gu[2 * i], adt), u = rnd(gu[2 * i + 1], adt);
+          hh[i] = rnd(silu(g) * u, adt);
+        }
+      }
+      or_gemv(o, hh, DT_FP32, F, L->wd, wdt, L->sd, 1, D, F);
+      for (uint32_t i = 0; i < D; i++) {
+        float v = o[i] + (gpt2 ? ld(L->bpr, i, adt) : 0.0f);
+        x[i] = rnd(x[i] + rnd(v, adt), adt);
+      }
+    }
+    if (gpt2) or_layernorm(xn, DT_FP32, x, DT_FP32, m->gf, m->bf, 1, D, m->eps);
+    else or_rmsnorm(xn, DT_FP32, x, DT_FP32, m->gf, 1, D, m->eps);
+    for (uint32_t i = 0; i < D; i++) xn[i] = rnd(xn[i], adt);
+    float *lg = logits + (uint64_t)b * V;
+    if (gpt2) or_gemv(lg, xn, DT_FP32, D, m->emb, adt, NULL, 1, V, D);
+    else or_gemv(lg, xn, DT_FP32, D, m->lm, wdt, m->lm_s, 1, V, D);
+    or_argmax(&next[b], lg, 1, V);
+  }
+  free(x); free(xn); free(qkv); free(q); free(att); free(o); free(gu); free(hh);
+  return 0;
+}

@@ -1,0 +1,190 @@
+"""ctypes access to the CPU oracle (oracle/build/liboracle.so) and, when it was
+built here, the reference harness (oracle/_ref/libref.so).  Test
+infrastructure: the checker, never the thing measured."""
+from __future__ import annotations
+
+import ctypes as C
+import subprocess
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parents[1]
+ORACLE_SO = ROOT / "oracle" / "build" / "liboracle.so"
+REF_SO = ROOT / "oracle" / "_ref" / "libref.so"
+
+_f, _u8, _u16, _u32, _u64, _vp, _i = (C.c_float, C.c_uint8, C.c_uint16, C.c_uint32, C.c_uint64,
+                                      C.c_void_p, C.c_int)
+
+
+class OrLayer(C.Structure):
+    _fields_ = [(n, _vp) for n in ("wqkv", "sqkv", "wo", "so", "wgu", "sgu", "wd", "sd",
+                                   "g1", "b1", "g2", "b2", "bqkv", "bo", "bfc", "bpr",
+                                   "kcache", "vcache")]
+
+
+class OrModel(C.Structure):
+    _fields_ = [(n, _u32) for n in ("arch", "n_layers", "dim", "n_heads", "n_kv_heads",
+                                    "head_dim", "ffn", "vocab", "max_seq", "batch", "wdt",
+                                    "adt")] + [("eps", _f)] + [
+        (n, _vp) for n in ("emb", "pos_emb", "gf", "bf", "lm", "lm_s", "rope_cos", "rope_sin")] + [
+        ("layers", C.POINTER(OrLayer))]
+
+
+_OR = None
+_REF = None
+
+
+def oracle() -> C.CDLL:
+    global _OR
+    if _OR is None:
+        if not ORACLE_SO.exists():
+            subprocess.run(["make", "-C", str(ROOT / "oracle"), "build/liboracle.so"], check=True,
+                           capture_output=True)
+        L = C.CDLL(str(ORACLE_SO))
+        sig = {
+            "or_bf16_to_f32": (_f, [_u16]), "or_f32_to_bf16": (_u16, [_f]),
+            "or_fp16_to_f32": (_f, [_u16]), "or_f32_to_fp16": (_u16, [_f]),
+            "or_fp8e4m3_to_f32": (_f, [_u8]), "or_fp8e5m2_to_f32": (_f, [_u8]),
+            "or_f32_to_fp8e4m3": (_u8, [_f]), "or_f32_to_fp8e4m3_sat": (_u8, [_f]),
+            "or_f32_to_fp8e5m2": (_u8, [_f]), "or_f32_to_fp8e5m2_sat": (_u8, [_f]),
+            "or_decode": (None, [_vp, _u32, _vp, _u64]),
+            "or_encode": (None, [_vp, _u32, _vp, _u64]),
+            "or_gemv": (None, [_vp, _vp, _u32, _u32, _vp, _u32, _vp, _u32, _u32, _u32]),
+            "or_rmsnorm": (None, [_vp, _u32, _vp, _u32, _vp, _u32, _u32, _f]),
+            "or_layernorm": (None, [_vp, _u32, _vp, _u32, _vp, _vp, _u32, _u32, _f]),
+            "or_softmax": (None, [_vp, _u32, _vp, _u32, _u32, _u32]),
+            "or_rope": (None, [_vp, _u32, _vp, _vp, _u32, _u32, _u32, _u32]),
+            "or_attn_decode": (None, [_vp, _u32, _vp, _u32, _vp, _vp, _u32, _u32, _u32, _u32,
+                                      _u32, _u32, _u32, _f]),
+            "or_argmax": (None, [_vp, _vp, _u32, _u32]),
+            "or_decode_step": (_i, [C.POINTER(OrModel), _vp, _u32, _vp, _vp]),
+        }
+        for k, (r, a) in sig.items():
+            fn = getattr(L, k)
+            fn.restype, fn.argtypes = r, a
+        _OR = L
+    return _OR
+
+
+def ref():
+    """The compiled reference harness, or None where it was not built."""
+    global _REF
+    if _REF is None and REF_SO.exists():
+        L = C.CDLL(str(REF_SO))
+        sig = {
+            "ref_f32_to_fp8e4m3": (_u8, [_f]), "ref_f32_to_fp8e4m3_sat": (_u8, [_f]),
+            "ref_f32_to_fp8e5m2": (_u8, [_f]), "ref_f32_to_fp8e5m2_sat": (_u8, [_f]),
+            "ref_fp8e4m3_to_f32": (_f, [_u8]), "ref_fp8e5m2_to_f32": (_f, [_u8]),
+            "ref_f32_to_bf16": (_u16, [_f]), "ref_bf16_to_f32": (_f, [_u16]),
+            "ref_f32_to_fp16": (_u16, [_f]), "ref_fp16_to_f32": (_f, [_u16]),
+            "ref_f32_to_fp16_manual": (_u16, [_f]), "ref_fp16_to_f32_manual": (_f, [_u16]),
+            "ref_xexp2f": (_f, [_f]),
+            "ref_linear_f32": (_i, [_vp, _vp, _vp, _u32, _u32, _u32]),
+            "ref_softmax_f32": (_i, [_vp, _vp, _u32, _u32]),
+            "ref_layernorm_f32": (_i, [_vp, _vp, _u32, _u32, C.c_double]),
+            "ref_rmsnorm_f32": (_i, [_vp, _vp, _u32, _u32, C.c_double]),
+        }
+        for k, (r, a) in sig.items():
+            fn = getattr(L, k)
+            fn.restype, fn.argtypes = r, a
+        _REF = L
+    return _REF
+
+
+def ptr(a: np.ndarray):
+    return a.ctypes.data if a is not None else None
+
+
+# ---- numpy conveniences over the oracle codecs ----
+DT_FP8E4M3, DT_FP8E5M2, DT_FP16, DT_BF16, DT_FP32 = 9, 10, 11, 12, 13
+_STORE_NP = {DT_FP32: np.float32, DT_FP16: np.uint16, DT_BF16: np.uint16, DT_FP8E4M3: np.uint8,
+             DT_FP8E5M2: np.uint8}
+
+
+def decode(a: np.ndarray, dt: int) -> np.ndarray:
+    a = np.ascontiguousarray(a)
+    out = np.empty(a.size, np.float32)
+    oracle().or_decode(a.ctypes.data, dt, out.ctypes.data, a.size)
+    return out.reshape(a.shape)
+
+
+def encode(f: np.ndarray, dt: int) -> np.ndarray:
+    f = np.ascontiguousarray(f, np.float32)
+    out = np.empty(f.size, _STORE_NP[dt])
+    oracle().or_encode(f.ctypes.data, dt, out.ctypes.data, f.size)
+    return out.reshape(f.shape)
+
+
+def gemv(x: np.ndarray, xdt: int, w: np.ndarray, wdt: int, scale=None, M=None, N=None, K=None):
+    """y[M,N] f32 = x @ dequant(w)^T (oracle or_gemv)."""
+    x = np.ascontiguousarray(x)
+    w = np.ascontiguousarray(w)
+    y = np.empty((M, N), np.float32)
+    sc = None if scale is None else np.ascontiguousarray(scale, np.float32)
+    oracle().or_gemv(y.ctypes.data, x.ctypes.data, xdt, K, w.ctypes.data, wdt,
+                     sc.ctypes.data if sc is not None else None, M, N, K)
+    return y
+
+
+DT_FP8_W = 9
+
+
+class OracleModel:
+    """OrModel over numpy copies of the decoder's device tensors."""
+
+    def __init__(self, dec, cfg):
+        self.keep = []
+        self.cfg = cfg
+        m = OrModel()
+        arch = cfg["arch"]
+        m.arch = arch
+        for k in ("n_layers", "dim", "n_heads", "head_dim", "ffn", "vocab", "max_seq", "batch"):
+            setattr(m, k, cfg[k])
+        m.n_kv_heads = cfg.get("n_kv_heads", cfg["n_heads"])
+        m.wdt, m.adt, m.eps = cfg["wdtype"], cfg["adtype"], cfg["eps"]
+
+        def t(name):
+            a = dec.read_tensor(name)
+            self.keep.append(a)
+            return a.ctypes.data
+
+        L = cfg["n_layers"]
+        self.layers = (OrLayer * L)()
+        self.caches = []
+        f8 = cfg["wdtype"] == DT_FP8_W
+        for l in range(L):
+            ly = self.layers[l]
+            p = f"l{l}."
+            if arch == 1:
+                ly.wqkv, ly.wo, ly.wgu, ly.wd = (t(p + n) for n in ("wqkv", "wo", "wgu", "wd"))
+                if f8:
+                    ly.sqkv, ly.so, ly.sgu, ly.sd = (t(p + n + ".scale") for n in ("wqkv", "wo", "wgu", "wd"))
+                ly.g1, ly.g2 = t(p + "g_attn"), t(p + "g_ffn")
+            else:
+                ly.wqkv, ly.wo, ly.wgu, ly.wd = (t(p + n) for n in ("c_attn", "c_proj", "c_fc", "mlp_proj"))
+                ly.bqkv, ly.bo, ly.bfc, ly.bpr = (t(p + n + ".b") for n in ("c_attn", "c_proj", "c_fc", "mlp_proj"))
+                ly.g1, ly.b1, ly.g2, ly.b2 = (t(p + n) for n in ("ln1.g", "ln1.b", "ln2.g", "ln2.b"))
+            kc, vc = dec.read_tensor(p + "kcache"), dec.read_tensor(p + "vcache")
+            self.caches += [kc, vc]
+            ly.kcache, ly.vcache = kc.ctypes.data, vc.ctypes.data
+        if arch == 1:
+            m.emb, m.gf, m.lm = t("emb"), t("norm_f"), t("lm")
+            if f8:
+                m.lm_s = t("lm.scale")
+            m.rope_cos, m.rope_sin = t("rope.cos"), t("rope.sin")
+        else:
+            m.emb, m.pos_emb, m.gf, m.bf = t("wte"), t("wpe"), t("lnf.g"), t("lnf.b")
+        m.layers = self.layers
+        self.m = m
+
+    def step(self, tok, pos):
+        B, V = self.cfg["batch"], self.cfg["vocab"]
+        tok = np.ascontiguousarray(tok, np.int32)
+        lg = np.empty((B, V), np.float32)
+        nx = np.empty(B, np.int32)
+        assert oracle().or_decode_step(C.byref(self.m), tok.ctypes.data, pos, lg.ctypes.data,
+                                         nx.ctypes.data) == 0
+        return lg, nx
+
+

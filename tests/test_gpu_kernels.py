@@ -1,0 +1,379 @@
+"""GPU parity of the hand-written gfx950 kernels against the CPU oracle.
+
+Each test prints its case before touching the GPU.  Tolerances follow the
+bit-exact for codecs / integer / index outputs; f32 results
+within 1e-5 relative to sum|x||w| (the per-row floor); values stored in a
+16-bit float within one storage rounding (2^-7 relative) plus that floor."""
+import numpy as np
+import pytest
+
+import _oracle as O
+
+pytestmark = pytest.mark.gpu
+
+DT_FP8, DT_F16, DT_BF16, DT_F32, DT_I32 = 9, 11, 12, 13, 5
+NP_STORE = {DT_F32: np.float32, DT_F16: np.uint16, DT_BF16: np.uint16, DT_FP8: np.uint8}
+SZ = {DT_F32: 4, DT_F16: 2, DT_BF16: 2, DT_FP8: 1}
+
+
+def say(*a):
+    print(*a, flush=True)
+
+
+def up(hip, a):
+    return hip.Buffer.from_numpy(np.ascontiguousarray(a))
+
+
+def rand_store(rng, shape, dt, std=1.0):
+    """random values of dtype dt (as storage) and their f32 value"""
+    f = (rng.standard_normal(shape) * std).astype(np.float32)
+    if dt == DT_F32:
+        return f, f
+    s = O.encode(f, dt)
+    return s, O.decode(s, dt)
+
+
+# ---------------------------------------------------------------- codecs ----
+def test_fp8_decode_all_patterns(hip):
+    say("case: fp8 e4m3 decode, all 256 patterns")
+    src = up(hip, np.arange(256, dtype=np.uint8))
+    dst = hip.Buffer(256 * 4)
+    hip.builtin("cast", [dst, src], n=256, xt=DT_FP8, yt=DT_F32)
+    got = dst.read(np.float32)
+    want = O.decode(np.arange(256, dtype=np.uint8), DT_FP8)
+    nan = np.isnan(want)
+    assert np.array_equal(np.isnan(got), nan)
+    assert np.array_equal(got[~nan].view(np.uint32), want[~nan].view(np.uint32))
+
+
+def _sweep_f32(rng):
+    bits = np.arange(0, 2**32, 65521, dtype=np.uint64).astype(np.uint32)
+    f = bits.view(np.float32)
+    extra = np.array([0.0, -0.0, 448.0, 464.0, 465.0, -464.0, 2**-10, 2**-9, 1.5 * 2**-9,
+                      2**-6, 3.0e38, np.inf, -np.inf, 1e-40], np.float32)
+    g = (rng.standard_normal(20000) * 10.0 ** rng.uniform(-8, 4, 20000)).astype(np.float32)
+    f = np.concatenate([f, extra, g])
+    return f[~np.isnan(f)]
+
+
+@pytest.mark.parametrize("dt", [DT_FP8, DT_BF16, DT_F16])
+def test_encode_sweep(hip, dt):
+    say(f"case: f32 -> dt {dt} store encode sweep")
+    f = _sweep_f32(np.random.default_rng(1))
+    src = up(hip, f)
+    dst = hip.Buffer(f.size * SZ[dt])
+    hip.builtin("cast", [dst, src], n=f.size, xt=DT_F32, yt=dt)
+    got = dst.read(NP_STORE[dt])
+    want = O.encode(f, dt)
+    bad = np.nonzero(got != want)[0]
+    assert bad.size == 0, f"{bad.size} mismatches, e.g. x={f[bad[:4]]} got={got[bad[:4]]} want={want[bad[:4]]}"
+
+
+# ------------------------------------------------------------------ gemv ----
+def _gemv_case(hip, rng, wdt, M, N, K, xdt=DT_BF16, ydt=DT_F32, epi=0, extra=None):
+    xs, xf = rand_store(rng, (M, K), xdt)
+    if wdt == DT_FP8:
+        wf32 = (rng.standard_normal((N, K)) * 0.02).astype(np.float32)
+        scale = (np.abs(wf32).max(1) / 448.0).astype(np.float32)
+        ws = O.encode(wf32 / scale[:, None], DT_FP8)
+        wdq = O.decode(ws, DT_FP8) * scale[:, None]
+    else:
+        ws, wdq = rand_store(rng, (N, K), wdt, 0.02)
+        scale = None
+    ref = O.gemv(xs, xdt, ws, wdt, scale, M=M, N=N, K=K)
+    floor = np.abs(xf) @ np.abs(wdq).T
+    return xs, ws, scale, ref, floor
+
+
+@pytest.mark.parametrize("wdt", [DT_F32, DT_F16, DT_BF16, DT_FP8])
+@pytest.mark.parametrize("M", [1, 2, 3, 4])
+@pytest.mark.parametrize("NK", [(64, 256), (97, 768), (256, 4096), (130, 1600)])
+def test_gemv_store_f32(hip, wdt, M, NK):
+    N, K = NK
+    if (K * SZ[wdt]) % 16:
+        pytest.skip("row bytes not a multiple of 16")
+    say(f"case: gemv wdt={wdt} M={M} N={N} K={K}")
+    rng = np.random.default_rng(1000 * wdt + 10 * M + N)
+    xs, ws, scale, ref, floor = _gemv_case(hip, rng, wdt, M, N, K)
+    y = hip.Buffer(M * N * 4)
+    args = [y, up(hip, xs), up(hip, ws)] + ([up(hip, scale)] if scale is not None else [])
+    hip.builtin("gemv", args, m=M, n=N, k=K, wt=wdt, xt=DT_BF16, yt=DT_F32, epi=0)
+    got = y.read(np.float32).reshape(M, N)
+    err = np.abs(got - ref)
+    assert np.all(err <= 1e-5 * floor + 1e-30), f"max rel {np.max(err / (floor + 1e-30))}"
+
+
+def test_gemv_fp32_matches_reference_linear(hip):
+    """fp32 GEMV against the reference CPU JIT's own linear output (golden)."""
+    g = np.load(O.ROOT / "tests" / "golden" / "ref_ops_f32.npz")
+    x, w, want = g["lin_x"], g["lin_w"], g["lin_y"]
+    M, K = x.shape
+    N = w.shape[0]
+    say(f"case: gemv f32 vs reference linear golden M={M} N={N} K={K}")
+    y = hip.Buffer(M * N * 4)
+    hip.builtin("gemv", [y, up(hip, x), up(hip, w)], m=M, n=N, k=K, wt=DT_F32, xt=DT_F32,
+                yt=DT_F32, epi=0)
+    got = y.read(np.float32).reshape(M, N)
+    floor = np.abs(x) @ np.abs(w).T
+    assert np.all(np.abs(got - want) <= 1e-5 * floor)
+
+
+def _rb(v):      # round through bf16 storage
+    return O.decode(O.encode(np.asarray(v, np.float32), DT_BF16), DT_BF16)
+
+
+def _close16(got, want, floor):
+    err = np.abs(got - want)
+    ok = err <= 2.0 ** -7 * np.abs(want) + 2e-5 * floor + 1e-6
+    return ok
+
+
+@pytest.mark.parametrize("wdt", [DT_BF16, DT_FP8])
+def test_gemv_residual_epilogue(hip, wdt):
+    M, N, K = 2, 256, 512
+    say(f"case: gemv residual wdt={wdt}")
+    rng = np.random.default_rng(7)
+    xs, ws, scale, ref, floor = _gemv_case(hip, rng, wdt, M, N, K)
+    rs, rf = rand_store(rng, (M, N), DT_BF16)
+    y = up(hip, rs)   # in-place residual
+    args = [y, up(hip, xs), up(hip, ws)] + ([up(hip, scale)] if scale is not None else []) + [y]
+    hip.builtin("gemv", args, m=M, n=N, k=K, wt=wdt, xt=DT_BF16, yt=DT_BF16, epi=1)
+    got = O.decode(y.read(np.uint16), DT_BF16).reshape(M, N)
+    want = _rb(rf + _rb(ref))
+    assert np.all(_close16(got, want, floor + np.abs(rf)))
+
+
+@pytest.mark.parametrize("wdt", [DT_BF16, DT_FP8])
+def test_gemv_swiglu_epilogue(hip, wdt):
+    M, F, K = 1, 384, 512
+    say(f"case: gemv swiglu wdt={wdt}")
+    rng = np.random.default_rng(8)
+    xs, ws, scale, ref, floor = _gemv_case(hip, rng, wdt, M, 2 * F, K)
+    y = hip.Buffer(M * F * 2)
+    args = [y, up(hip, xs), up(hip, ws)] + ([up(hip, scale)] if scale is not None else [])
+    hip.builtin("gemv", args, m=M, n=2 * F, k=K, wt=wdt, xt=DT_BF16, yt=DT_BF16, epi=2)
+    got = O.decode(y.read(np.uint16), DT_BF16).reshape(M, F)
+    g, u = _rb(ref[:, 0::2]), _rb(ref[:, 1::2])
+    want = _rb(g / (1 + np.exp(-g)) * u)
+    fl = floor[:, 0::2] + floor[:, 1::2]
+    assert np.all(_close16(got, want, fl))
+
+
+def test_gemv_qkv_rope_epilogue(hip):
+    H, Hkv, hd, D, ms, pos = 4, 2, 64, 256, 32, 5
+    N = (H + 2 * Hkv) * hd
+    say("case: gemv qkv+rope epilogue")
+    rng = np.random.default_rng(9)
+    xs, ws, scale, ref, floor = _gemv_case(hip, rng, DT_FP8, 1, N, D)
+    half = hd // 2
+    f = 1.0 / (500000.0 ** (np.arange(half) * 2.0 / hd))
+    ang = np.arange(ms)[:, None] * f[None, :]
+    cs, sn = np.cos(ang).astype(np.float32), np.sin(ang).astype(np.float32)
+    q = hip.Buffer(H * hd * 2)
+    kc, vc = hip.Buffer(Hkv * ms * hd * 2), hip.Buffer(Hkv * ms * hd * 2)
+    L = up(hip, np.array([pos + 1], np.int32))
+    hip.builtin("gemv", [q, up(hip, xs), up(hip, ws), up(hip, scale), up(hip, cs), up(hip, sn), L,
+                         kc, vc], m=1, n=N, k=D, wt=DT_FP8, xt=DT_BF16, yt=DT_BF16, epi=4, h=H,
+                hkv=Hkv, hd=hd, maxseq=ms)
+    v = _rb(ref[0])
+    c, s = cs[pos], sn[pos]
+    ro = v.copy()
+    for n in range(0, (H + Hkv) * hd, 2):
+        j = (n % hd) // 2
+        ro[n] = _rb(v[n] * c[j] - v[n + 1] * s[j])
+        ro[n + 1] = _rb(v[n + 1] * c[j] + v[n] * s[j])
+    gq = O.decode(q.read(np.uint16), DT_BF16)
+    gk = O.decode(kc.read(np.uint16), DT_BF16).reshape(Hkv, ms, hd)[:, pos].ravel()
+    gv = O.decode(vc.read(np.uint16), DT_BF16).reshape(Hkv, ms, hd)[:, pos].ravel()
+    got = np.concatenate([gq, gk, gv])
+    fl = floor[0] * 2 + 1e-3
+    assert np.all(_close16(got, ro, fl)), np.max(np.abs(got - ro))
+    # other cache rows untouched
+    assert not np.any(kc.read(np.uint16).reshape(Hkv, ms, hd)[:, pos + 1:])
+
+
+def test_gemv_rejects_bad_shapes(hip):
+    say("case: gemv argument validation (host-side errors, no launch)")
+    y, x, w = hip.Buffer(64), hip.Buffer(64), hip.Buffer(64)
+    with pytest.raises(hip.ThvmHipError):
+        hip.builtin("gemv", [y, x, w], m=1, n=64, k=256, wt=DT_F32, xt=DT_F32, yt=DT_F32)
+    with pytest.raises(hip.ThvmHipError):
+        hip.builtin("gemv", [y, x, w], m=9, n=1, k=4, wt=DT_F32, xt=DT_F32, yt=DT_F32)
+
+
+# ------------------------------------------------------------- row ops ----
+@pytest.mark.parametrize("ln", [0, 1])
+@pytest.mark.parametrize("dt", [DT_F32, DT_BF16, DT_F16])
+def test_norm(hip, ln, dt):
+    M, K = 3, 1600
+    say(f"case: norm ln={ln} dt={dt}")
+    rng = np.random.default_rng(11)
+    xs, xf = rand_store(rng, (M, K), dt)
+    g = (1 + 0.1 * rng.standard_normal(K)).astype(np.float32)
+    b = (0.1 * rng.standard_normal(K)).astype(np.float32)
+    y = hip.Buffer(M * K * SZ[dt])
+    args = [y, up(hip, xs), up(hip, g)] + ([up(hip, b)] if ln else [])
+    hip.builtin("norm", args, m=M, k=K, xt=dt, yt=dt, eps=1e-5, ln=ln, bias=ln)
+    want = np.empty(M * K, NP_STORE[dt])
+    if ln:
+        O.oracle().or_layernorm(want.ctypes.data, dt, xs.ctypes.data, dt, g.ctypes.data,
+                                b.ctypes.data, M, K, 1e-5)
+    else:
+        O.oracle().or_rmsnorm(want.ctypes.data, dt, xs.ctypes.data, dt, g.ctypes.data, M, K, 1e-5)
+    gw = O.decode(y.read(NP_STORE[dt]), dt)
+    ww = O.decode(want, dt)
+    tol = 1e-5 if dt == DT_F32 else 2.0 ** -7
+    assert np.all(np.abs(gw - ww) <= tol * np.abs(ww) + 1e-5), np.max(np.abs(gw - ww))
+
+
+def test_softmax(hip):
+    M, K = 4, 4096
+    say("case: softmax f16 [4,4096]")
+    rng = np.random.default_rng(12)
+    xs, xf = rand_store(rng, (M, K), DT_F16)
+    y = hip.Buffer(M * K * 4)
+    hip.builtin("softmax", [y, up(hip, xs)], m=M, k=K, xt=DT_F16, yt=DT_F32)
+    want = np.empty(M * K, np.float32)
+    O.oracle().or_softmax(want.ctypes.data, DT_F32, xs.ctypes.data, DT_F16, M, K)
+    got = y.read(np.float32)
+    assert np.allclose(got, want, rtol=1e-5, atol=1e-9)
+    assert np.allclose(got.reshape(M, K).sum(1), 1.0, atol=1e-5)
+
+
+def test_rope(hip):
+    B, nh, hd, ms, pos = 2, 3, 128, 16, 9
+    say("case: rope")
+    rng = np.random.default_rng(13)
+    xs, xf = rand_store(rng, (B, nh, hd), DT_BF16)
+    half = hd // 2
+    ang = np.arange(ms)[:, None] / (500000.0 ** (np.arange(half) * 2.0 / hd))[None]
+    cs, sn = np.cos(ang).astype(np.float32), np.sin(ang).astype(np.float32)
+    xb = up(hip, xs)
+    hip.builtin("rope", [xb, up(hip, cs), up(hip, sn), up(hip, np.array([pos + 1], np.int32))],
+                b=B, nh=nh, hd=hd, dt=DT_BF16, maxseq=ms)
+    want = xs.copy()
+    O.oracle().or_rope(want.ctypes.data, DT_BF16, cs.ctypes.data, sn.ctypes.data, B, nh, hd, pos)
+    assert np.array_equal(xb.read(np.uint16), want.ravel())
+
+
+@pytest.mark.parametrize("H,Hkv,hd", [(8, 2, 128), (4, 4, 64), (32, 8, 128), (8, 1, 64)])
+@pytest.mark.parametrize("L", [1, 63, 64, 65, 200])
+def test_attention_decode(hip, H, Hkv, hd, L):
+    B, ms = 2, 256
+    say(f"case: attn H={H} Hkv={Hkv} hd={hd} L={L}")
+    rng = np.random.default_rng(H * 1000 + L)
+    qs, qf = rand_store(rng, (B, H, hd), DT_BF16)
+    ks, _ = rand_store(rng, (B, Hkv, ms, hd), DT_BF16)
+    vs, _ = rand_store(rng, (B, Hkv, ms, hd), DT_BF16)
+    nsplit = (ms + 63) // 64
+    out = hip.Buffer(B * H * hd * 2)
+    part = hip.Buffer(B * H * nsplit * (hd + 2) * 4)
+    scale = float(np.float32(1.0 / np.sqrt(hd)))
+    hip.builtin("attn", [out, up(hip, qs), up(hip, ks), up(hip, vs),
+                         up(hip, np.array([L], np.int32)), part],
+                b=B, h=H, hkv=Hkv, hd=hd, maxseq=ms, chunk=64, nsplit=nsplit, qt=DT_BF16,
+                ct=DT_BF16, ot=DT_BF16, scale=scale)
+    want = np.empty(B * H * hd, np.uint16)
+    O.oracle().or_attn_decode(want.ctypes.data, DT_BF16, qs.ctypes.data, DT_BF16, ks.ctypes.data,
+                              vs.ctypes.data, DT_BF16, B, H, Hkv, hd, ms, L, scale)
+    got = O.decode(out.read(np.uint16), DT_BF16)
+    ww = O.decode(want, DT_BF16)
+    assert np.all(np.abs(got - ww) <= 2.0 ** -7 * np.abs(ww) + 2e-3), np.max(np.abs(got - ww))
+
+
+def test_argmax_ties_lowest_index(hip):
+    B, V = 3, 50257
+    say("case: argmax ties")
+    rng = np.random.default_rng(14)
+    lg = rng.standard_normal((B, V)).astype(np.float32)
+    lg[0, [7, 30000, 50000]] = 100.0           # three-way tie -> 7
+    lg[1, [40000, 40001]] = 50.0               # tie -> 40000
+    lg[2, V - 1] = 60.0
+    tok, pv, pi = hip.Buffer(B * 4), hip.Buffer(B * 256 * 4), hip.Buffer(B * 256 * 4)
+    hip.builtin("argmax", [tok, up(hip, lg), pv, pi], b=B, v=V, nb=256)
+    want = np.empty(B, np.int32)
+    O.oracle().or_argmax(want.ctypes.data, lg.ctypes.data, B, V)
+    assert list(tok.read(np.int32)) == list(want) == [7, 40000, V - 1]
+
+
+def test_embed(hip):
+    B, D, V = 2, 768, 1000
+    say("case: embed")
+    rng = np.random.default_rng(15)
+    es, ef = rand_store(rng, (V, D), DT_BF16)
+    tok = np.array([3, 999], np.int32)
+    x = hip.Buffer(B * D * 2)
+    hip.builtin("embed", [x, up(hip, es), up(hip, tok)], b=B, d=D, v=V, et=DT_BF16, xt=DT_BF16)
+    assert np.array_equal(x.read(np.uint16).reshape(B, D), es[tok])
+
+
+def test_len_bump(hip):
+    say("case: len_bump")
+    L = up(hip, np.array([41], np.int32))
+    hip.builtin("len_bump", [L], delta=1)
+    hip.builtin("len_bump", [L], delta=1)
+    assert L.read(np.int32)[0] == 43
+
+
+# ------------------------------------------------ custom kernels + JIT ----
+SRC_ADDONE = """extern "C" __global__ void addone(const float *x, float *y) {
+  unsigned i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < 8) y[i] = x[i] + 1.0f;
+}"""
+SRC_DBL = """extern "C" __global__ void dbl(const float *x, float *s) {
+  unsigned i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < 8) s[i] = x[i] * 2.0f;
+}"""
+SRC_ADD3 = """extern "C" __global__ void add3(const float *s, float *y) {
+  unsigned i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < 8) y[i] = s[i] + 3.0f;
+}"""
+SRC_TWO = """extern "C" __global__ void twoout(const float *x, float *y1, float *y2) {
+  unsigned i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < 8) { y1[i] = x[i] + 1.0f; y2[i] = x[i] * 10.0f; }
+}"""
+
+
+def test_custom_kernel_eager_and_jit_replay(hip):
+    """The reference's custom-kernel CUDA test (tests/test_custom_kernel_cuda.c)
+    on HIP: eager add-one, a 2-kernel chain, a JIT capture of the chain with 3
+    replays over refreshed inputs (replay 1 captures the hipGraph, 2-3 hit it),
+    and a two-output kernel."""
+    say("case: custom hiprtc kernels + jit")
+    g, b = (1, 1, 1), (8, 1, 1)
+    xv = np.arange(8, dtype=np.float32)
+    x, y = up(hip, xv), hip.Buffer(32)
+    hip.dispatch("addone", SRC_ADDONE, [x, y], grid=g, block=b, outs=(1,))
+    assert np.array_equal(y.read(np.float32), xv + 1)
+    cx, s, cy = up(hip, xv), hip.Buffer(32), hip.Buffer(32)
+    hip.dispatch("dbl", SRC_DBL, [cx, s], grid=g, block=b, outs=(1,))
+    hip.dispatch("add3", SRC_ADD3, [s, cy], grid=g, block=b, outs=(1,))
+    assert np.array_equal(cy.read(np.float32), xv * 2 + 3)
+    with hip.Jit() as jit:
+        hip.dispatch("dbl", SRC_DBL, [cx, s], grid=g, block=b, outs=(1,))
+        hip.dispatch("add3", SRC_ADD3, [s, cy], grid=g, block=b, outs=(1,))
+    assert jit.op_count() == 2
+    for rep in (1, 2, 3):
+        xr = (10 * rep + np.arange(8)).astype(np.float32)
+        cx.write(xr)
+        cy.write(np.full(8, -999, np.float32))
+        jit.replay()
+        assert np.array_equal(cy.read(np.float32), xr * 2 + 3), f"replay {rep}"
+    jit.drop()
+    y1, y2 = hip.Buffer(32), hip.Buffer(32)
+    hip.dispatch("twoout", SRC_TWO, [x, y1, y2], grid=g, block=b, outs=(1, 2))
+    assert np.array_equal(y1.read(np.float32), xv + 1)
+    assert np.array_equal(y2.read(np.float32), xv * 10)
+
+
+def test_custom_kernel_errors(hip):
+    say("case: custom kernel error paths")
+    x = hip.Buffer(32)
+    with pytest.raises(hip.ThvmHipError):
+        hip.dispatch("nosuch", "extern \"C\" __global__ void k(float *x) {}", [x])
+    with pytest.raises(hip.ThvmHipError):
+        hip.dispatch("bad", "this is not HIP", [x])
+    with pytest.raises(hip.ThvmHipError):
+        hip.builtin("nosuchkernel", [x])
+    with pytest.raises(hip.ThvmHipError):   # too small a buffer for the shape
+        hip.builtin("cast", [x, x], n=1000, xt=DT_F32, yt=DT_F32)

@@ -1,0 +1,246 @@
+"""Pin the CPU oracle before trusting it (CPU only).
+
+Checks, per oracle function:
+  * golden vectors written by the compiled reference (tests/golden/*.npz,
+    made by tests/golden/make_golden.py from oracle/_ref/libref.so);
+  * the reference test suite's own known answers (tests/test_fp8_nonfinite.c
+    values computed with tinygrad 365f87a8a; tests/test_matvec_blas.c all-ones
+    -> K; tests/test_sym_decode_step.c uniform attention over rows 0..3 = 1.5);
+  * what the mathematics fixes: IEEE binary16 decode (numpy float16),
+    encode(decode(b)) == b on every finite pattern, float64 brute force;
+  * the live reference harness, when it was built in this container."""
+import numpy as np
+import pytest
+
+import _oracle as O
+
+G = O.ROOT / "tests" / "golden"
+DT_FP8, DT_E5M2, DT_F16, DT_BF16, DT_F32 = 9, 10, 11, 12, 13
+
+
+def bits(a):
+    return np.asarray(a, np.float32).view(np.uint32)
+
+
+def same_float(a, b):
+    a, b = np.asarray(a, np.float32), np.asarray(b, np.float32)
+    na, nb = np.isnan(a), np.isnan(b)
+    return np.array_equal(na, nb) and np.array_equal(bits(a[~na]), bits(b[~nb]))
+
+
+@pytest.fixture(scope="module")
+def codecs():
+    return np.load(G / "ref_codecs.npz")
+
+
+# ---------------------------------------------------------------- codecs ----
+def test_fp8_decode_tables_match_reference(codecs):
+    b = np.arange(256, dtype=np.uint8)
+    assert same_float(O.decode(b, DT_FP8), codecs["dec_e4m3"])
+    assert same_float(O.decode(b, DT_E5M2), codecs["dec_e5m2"])
+
+
+def test_fp16_decode_matches_reference_and_ieee(codecs):
+    h = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    d = O.decode(h, DT_F16)
+    assert same_float(d, codecs["dec_fp16"])
+    ieee = h.view(np.float16).astype(np.float32)
+    fin = np.isfinite(ieee)
+    assert np.array_equal(bits(d[fin]), bits(ieee[fin]))
+
+
+def test_e4m3_decode_closed_form():
+    for b in range(256):
+        s, e, m = b >> 7, (b >> 3) & 15, b & 7
+        v = O.oracle().or_fp8e4m3_to_f32(b)
+        if (b & 0x7F) == 0x7F:
+            assert np.isnan(v)
+            continue
+        want = (m / 8.0) * 2.0 ** -6 if e == 0 else (1 + m / 8.0) * 2.0 ** (e - 7)
+        assert v == (-want if s else want), b
+
+
+@pytest.mark.parametrize("name,dt,sat", [("bf16", DT_BF16, None), ("fp16", DT_F16, None),
+                                         ("e4m3", DT_FP8, 0), ("e4m3_sat", DT_FP8, 1),
+                                         ("e5m2", DT_E5M2, 0), ("e5m2_sat", DT_E5M2, 1)])
+def test_encoders_match_reference_sweep(codecs, name, dt, sat):
+    f = codecs["sweep"]
+    R = O.oracle()
+    fn = {"bf16": R.or_f32_to_bf16, "fp16": R.or_f32_to_fp16, "e4m3": R.or_f32_to_fp8e4m3,
+          "e4m3_sat": R.or_f32_to_fp8e4m3_sat, "e5m2": R.or_f32_to_fp8e5m2,
+          "e5m2_sat": R.or_f32_to_fp8e5m2_sat}[name]
+    got = np.array([fn(float(v)) for v in f])
+    assert np.array_equal(got, codecs["enc_" + name].astype(got.dtype))
+
+
+def test_encode_decode_roundtrip_all_finite():
+    b8 = np.arange(256, dtype=np.uint8)
+    d8 = O.decode(b8, DT_FP8)
+    fin = ~np.isnan(d8)
+    assert np.array_equal(O.encode(d8[fin], DT_FP8), b8[fin])
+    h = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    dh = O.decode(h, DT_F16)
+    fin = np.isfinite(dh)
+    assert np.array_equal(O.encode(dh[fin], DT_F16), h[fin])
+
+
+def test_bf16_encode_is_round_to_nearest_even():
+    rng = np.random.default_rng(3)
+    f = (rng.standard_normal(50000) * 10.0 ** rng.uniform(-30, 30, 50000)).astype(np.float32)
+    got = O.encode(f, DT_BF16).astype(np.uint32) << 16
+    got = got.view(np.float32).astype(np.float64)
+    lo = (bits(f) & 0xFFFF0000).view(np.float32).astype(np.float64)
+    hi = ((bits(f) & 0xFFFF0000) + 0x10000).view(np.float32).astype(np.float64)
+    x = f.astype(np.float64)
+    dl, dh = np.abs(x - lo), np.abs(hi - x)
+    nearest = np.where(dl < dh, lo, np.where(dh < dl, hi, np.nan))
+    tie = np.isnan(nearest)
+    assert np.array_equal(got[~tie], nearest[~tie])
+    even = np.where((bits(f[tie]) >> 16) & 1 == 0, lo[tie], hi[tie])
+    assert np.array_equal(got[tie], even)
+
+
+def test_fp8_nonfinite_known_answers():
+    """tests/test_fp8_nonfinite.c:110-192 (values computed with tinygrad)."""
+    R = O.oracle()
+    f32 = lambda u: float(np.array([u], np.uint32).view(np.float32)[0])  # noqa: E731
+    nans = [0x7FC00000, 0x7F800001, 0x7FA00000, 0x7FFFFFFF]
+    neg = [0xFFC00000, 0xFF800001, 0xFFA00000, 0xFFFFFFFF]
+    assert R.or_f32_to_fp8e4m3(float("inf")) == 0x7F and R.or_f32_to_fp8e4m3(float("-inf")) == 0xFF
+    assert R.or_f32_to_fp8e5m2(float("inf")) == 0x7C and R.or_f32_to_fp8e5m2(float("-inf")) == 0xFC
+    for u, v in zip(nans, neg):
+        assert R.or_f32_to_fp8e4m3(f32(u)) == 0x7F and R.or_f32_to_fp8e4m3(f32(v)) == 0xFF
+        assert R.or_f32_to_fp8e5m2(f32(u)) == 0x7F and R.or_f32_to_fp8e5m2(f32(v)) == 0xFF
+    assert R.or_f32_to_fp8e4m3_sat(float("inf")) == 0x7E and R.or_f32_to_fp8e4m3_sat(float("-inf")) == 0xFE
+    assert R.or_f32_to_fp8e5m2_sat(float("inf")) == 0x7B and R.or_f32_to_fp8e5m2_sat(float("-inf")) == 0xFB
+    # the NaN payloads go through memory (a Python float would quiet them)
+    pats = np.array(nans + neg, np.uint32).view(np.float32)
+    assert list(O.encode(pats, DT_FP8)) == [0x7F, 0x7F, 0x7F, 0x7F, 0xFF, 0xFF, 0xFF, 0xFF]
+    assert list(O.encode(pats, DT_E5M2)) == [0x7E, 0x7C, 0x7D, 0x7F, 0xFE, 0xFC, 0xFD, 0xFF]
+    assert R.or_f32_to_fp8e4m3_sat(464.0) == 0x7E
+    assert R.or_f32_to_fp8e4m3_sat(f32(0xFF7FFFFF)) == 0xFE
+    assert R.or_f32_to_fp8e5m2_sat(61440.0) == 0x7B
+    assert R.or_f32_to_fp8e5m2_sat(f32(0x7F7FFFFF)) == 0x7B
+
+
+# ------------------------------------------------------------------- ops ----
+def test_gemv_matches_reference_linear_bit_exact():
+    g = np.load(G / "ref_ops_f32.npz")
+    for p in ("lin", "lin2"):
+        x, w, want = g[p + "_x"], g[p + "_w"], g[p + "_y"]
+        M, K = x.shape
+        y = O.gemv(x, DT_F32, w, DT_F32, None, M=M, N=w.shape[0], K=K)
+        assert np.array_equal(bits(y), bits(want)), p
+
+
+def test_gemv_all_ones_is_k():
+    """tests/test_matvec_blas.c:14-30: a ones matvec sums to K (LM-head shape)."""
+    K, N = 768, 2048
+    y = O.gemv(np.ones((1, K), np.float32), DT_F32, np.ones((N, K), np.float32), DT_F32, None,
+               M=1, N=N, K=K)
+    assert np.all(y == K)
+
+
+@pytest.mark.parametrize("wdt", [DT_F32, DT_F16, DT_BF16, DT_FP8])
+def test_gemv_brute_force(wdt):
+    rng = np.random.default_rng(wdt)
+    M, N, K = 3, 37, 96
+    x = rng.standard_normal((M, K)).astype(np.float32)
+    wf = (rng.standard_normal((N, K)) * 0.02).astype(np.float32)
+    scale = None
+    if wdt == DT_FP8:
+        scale = (np.abs(wf).max(1) / 448).astype(np.float32)
+        ws = O.encode(wf / scale[:, None], DT_FP8)
+        wd = O.decode(ws, DT_FP8).astype(np.float64) * scale[:, None]
+    elif wdt == DT_F32:
+        ws, wd = wf, wf.astype(np.float64)
+    else:
+        ws = O.encode(wf, wdt)
+        wd = O.decode(ws, wdt).astype(np.float64)
+    y = O.gemv(x, DT_F32, ws, wdt, scale, M=M, N=N, K=K)
+    want = x.astype(np.float64) @ wd.T
+    floor = np.abs(x) @ np.abs(wd).T
+    assert np.all(np.abs(y - want) <= 1e-6 * floor * K ** 0.5)
+    # a transposed operand is caught
+    assert not np.allclose(y, (x.astype(np.float64) @ wd[::-1].T), atol=1e-3)
+
+
+def test_softmax_layernorm_rmsnorm_match_reference():
+    g = np.load(G / "ref_ops_f32.npz")
+    x = g["sm_x"]
+    y = np.empty_like(x)
+    O.oracle().or_softmax(y.ctypes.data, DT_F32, x.ctypes.data, DT_F32, *x.shape)
+    assert np.allclose(y, g["sm_y"], rtol=2e-6, atol=0)
+    x = g["ln_x"]
+    y = np.empty_like(x)
+    O.oracle().or_layernorm(y.ctypes.data, DT_F32, x.ctypes.data, DT_F32, None, None, *x.shape, 1e-5)
+    assert np.allclose(y, g["ln_y"], rtol=1e-5, atol=1e-6)
+    x = g["rms_x"]
+    y = np.empty_like(x)
+    O.oracle().or_rmsnorm(y.ctypes.data, DT_F32, x.ctypes.data, DT_F32, None, *x.shape, 1e-6)
+    assert np.allclose(y, g["rms_y"], rtol=1e-5, atol=1e-6)
+
+
+def test_rope_brute_force():
+    rng = np.random.default_rng(4)
+    B, nh, hd, ms, pos = 2, 3, 8, 6, 4
+    x = rng.standard_normal((B, nh, hd)).astype(np.float32)
+    ang = np.arange(ms)[:, None] / (10000.0 ** (np.arange(hd // 2) * 2.0 / hd))[None]
+    cs, sn = np.cos(ang).astype(np.float32), np.sin(ang).astype(np.float32)
+    y = x.copy()
+    O.oracle().or_rope(y.ctypes.data, DT_F32, cs.ctypes.data, sn.ctypes.data, B, nh, hd, pos)
+    z = x[..., 0::2] + 1j * x[..., 1::2]
+    r = z * np.exp(1j * ang[pos])
+    want = np.stack([r.real, r.imag], -1).reshape(B, nh, hd)
+    assert np.allclose(y, want, atol=1e-5)
+    # rotation preserves each pair's norm
+    assert np.allclose(np.abs(y[..., 0::2] + 1j * y[..., 1::2]), np.abs(z), atol=1e-5)
+
+
+def test_attention_closed_form_and_brute_force():
+    """tests/test_sym_decode_step.c: with q=0 the scores tie, the softmax is
+    uniform, and the output is the mean of V rows 0..3 = 1.5."""
+    B, H, Hkv, hd, ms, L = 1, 2, 1, 4, 8, 4
+    q = np.zeros((B, H, hd), np.float32)
+    k = np.random.default_rng(0).standard_normal((B, Hkv, ms, hd)).astype(np.float32)
+    v = np.zeros((B, Hkv, ms, hd), np.float32)
+    v[0, 0, :L, :] = np.arange(L)[:, None]
+    out = np.empty(B * H * hd, np.float32)
+    O.oracle().or_attn_decode(out.ctypes.data, DT_F32, q.ctypes.data, DT_F32, k.ctypes.data,
+                              v.ctypes.data, DT_F32, B, H, Hkv, hd, ms, L, 0.5)
+    assert np.all(out == 1.5)
+    rng = np.random.default_rng(1)
+    B, H, Hkv, hd, ms, L = 2, 8, 2, 16, 40, 33
+    q = rng.standard_normal((B, H, hd)).astype(np.float32)
+    k = rng.standard_normal((B, Hkv, ms, hd)).astype(np.float32)
+    v = rng.standard_normal((B, Hkv, ms, hd)).astype(np.float32)
+    out = np.empty((B, H, hd), np.float32)
+    O.oracle().or_attn_decode(out.ctypes.data, DT_F32, q.ctypes.data, DT_F32, k.ctypes.data,
+                              v.ctypes.data, DT_F32, B, H, Hkv, hd, ms, L, 0.25)
+    for b in range(B):
+        for h in range(H):
+            kk, vv = k[b, h // (H // Hkv), :L].astype(np.float64), v[b, h // (H // Hkv), :L]
+            s = kk @ q[b, h] * 0.25
+            p = np.exp(s - s.max())
+            assert np.allclose(out[b, h], (p / p.sum()) @ vv, atol=1e-5)
+
+
+def test_argmax_lowest_index():
+    lg = np.array([[1, 5, 5, 2], [9, 9, 9, 9]], np.float32)
+    t = np.empty(2, np.int32)
+    O.oracle().or_argmax(t.ctypes.data, lg.ctypes.data, 2, 4)
+    assert list(t) == [1, 0]
+
+
+def test_live_reference_codecs_random():
+    R = O.ref()
+    if R is None:
+        pytest.skip("reference harness not built in this checkout")
+    rng = np.random.default_rng(11)
+    f = (rng.standard_normal(4000) * 10.0 ** rng.uniform(-12, 6, 4000)).astype(np.float32)
+    Or = O.oracle()
+    for v in f:
+        v = float(v)
+        assert Or.or_f32_to_fp8e4m3_sat(v) == R.ref_f32_to_fp8e4m3_sat(v)
+        assert Or.or_f32_to_bf16(v) == R.ref_f32_to_bf16(v)
+        assert Or.or_f32_to_fp16(v) == R.ref_f32_to_fp16_manual(v)

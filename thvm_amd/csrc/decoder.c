@@ -1,0 +1,632 @@
+/* decoder.c -- synthetic decode drivers: the whole decode step of a
+ * random-init model as a list of custom dispatches over builtin gfx950
+ * kernels, captured once and replayed as one hipGraph launch per token.
+ *
+ * Counterpart of the reference DeepSeek-V2 decode driver
+ * (bench/dsv2_decode_bench.c: model_init, step_build :2328-2430, capture +
+ * replay :2898-3008) and of the GPT-2 driver (bench/gpt2/thvm_gpt2.py:96-131).
+ * As there, the token and the position live in device buffers (argmax writes
+ * the next token, len_bump advances L), so a replay needs no host values.
+ *
+ * Step (LLAMA, per layer):
+ *   norm   xn = rms(x) * g_attn                       -> bf16
+ *   gemv   [q|k|v] = xn Wqkv^T, RoPE(q, k) at L-1, k/v appended to the caches
+ *   attn   att = softmax(q K^T / sqrt(hd)) V over rows [0, L)
+ *   gemv   x = x + att Wo^T                           (residual epilogue)
+ *   norm   xn = rms(x) * g_ffn
+ *   gemv   h = silu(xn Wg^T) * (xn Wu^T)              (rows interleaved g/u)
+ *   gemv   x = x + h Wd^T
+ * then final norm, LM head (f32 logits), argmax -> tok / history, len_bump.
+ * GPT2 swaps RMSNorm for LayerNorm (+bias), RoPE for learned positions,
+ * SwiGLU for GELU, and ties the LM head to the token embedding.
+ *
+ * Numerics: activations are rounded to the activation dtype exactly where
+ * the reference decode chain rounds them (matmul outputs before RoPE /
+ * residual use, residual sums, norm outputs: bench/dsv2_decode_bench.c:20-34). */
+#define _GNU_SOURCE
+#include "internal.h"
+
+#include <math.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+typedef struct {
+  char name[40];
+  u32  id;
+  u32  dt;
+  u64  nbytes;
+} DTensor;
+
+typedef struct {
+  char *name;
+  char *prog;
+  u32   args[24];
+  u32   n_args;
+  u64   outs;
+} DOp;
+
+typedef struct {
+  int used;
+  ThvmDecodeConfig c;
+  u64 seed;
+  DTensor t[512];
+  u32 nt;
+  DOp *ops;
+  u32 n_ops, cap_ops;
+  u32 jit_slot;
+  u32 n_split;
+  u64 weight_bytes;       /* streamed weight + scale bytes per step */
+} Decoder;
+
+#define MAX_DEC 8
+static Decoder DEC[MAX_DEC];
+
+static Decoder *dec_get(u32 h) {
+  if (h == 0 || h > MAX_DEC || !DEC[h - 1].used) {
+    hb_set_error("decoder %u: no such decoder", h);
+    return NULL;
+  }
+  return &DEC[h - 1];
+}
+
+static u32 tens_find(Decoder *d, const char *name) {
+  for (u32 i = 0; i < d->nt; i++)
+    if (strcmp(d->t[i].name, name) == 0) return d->t[i].id;
+  return 0;
+}
+
+static u32 tens_new(Decoder *d, const char *name, u32 dt, u64 nbytes) {
+  if (d->nt >= sizeof d->t / sizeof d->t[0]) { hb_set_error("decoder: tensor table full"); return 0; }
+  u32 id = thvm_hip_buf_alloc(nbytes);
+  if (!id) return 0;
+  DTensor *t = &d->t[d->nt++];
+  snprintf(t->name, sizeof t->name, "%s", name);
+  t->id = id;
+  t->dt = dt;
+  t->nbytes = nbytes;
+  return id;
+}
+
+static u64 name_tag(const char *name) { return hb_hash64(name, strlen(name), 0x7468766dull); }
+
+/* run a builtin immediately (set-up work, never recorded) */
+static int run_now(const char *prog, const u32 *ids, u32 n) {
+  return hb_builtin_launch(prog, ids, n, 0);
+}
+
+static u32 weight_normal(Decoder *d, const char *name, u32 dt, u64 n, float mean, float std) {
+  u32 id = tens_new(d, name, dt, n * hb_dt_size(dt));
+  if (!id) return 0;
+  char p[256];
+  snprintf(p, sizeof p, "thvm-builtin:fill_normal n=%llu dt=%u seed=%llu tag=%llu mean=%a std=%a",
+           (unsigned long long)n, dt, (unsigned long long)d->seed,
+           (unsigned long long)name_tag(name), mean, std);
+  if (run_now(p, &id, 1)) return 0;
+  return id;
+}
+
+static u32 weight_const(Decoder *d, const char *name, u64 n, float v) {
+  u32 id = tens_new(d, name, THVM_DT_FP32, n * 4);
+  if (!id) return 0;
+  float *h = (float *)malloc(n * 4);
+  if (!h) { hb_set_error("decoder: out of host memory"); return 0; }
+  for (u64 i = 0; i < n; i++) h[i] = v;
+  int rc = thvm_hip_buf_write(id, h, n * 4);
+  free(h);
+  return rc ? 0 : id;
+}
+
+/* weight matrix [rows, cols] of dtype wdt; fp8 also gets "<name>.scale" */
+static int weight_matrix(Decoder *d, const char *name, u32 rows, u32 cols, u32 *w, u32 *s) {
+  u32 wdt = d->c.wdtype;
+  *s = 0;
+  if (wdt == THVM_DT_FP8E4M3) {
+    *w = tens_new(d, name, wdt, (u64)rows * cols);
+    char sn[48];
+    snprintf(sn, sizeof sn, "%s.scale", name);
+    *s = tens_new(d, sn, THVM_DT_FP32, (u64)rows * 4);
+    if (!*w || !*s) return -1;
+    char p[256];
+    snprintf(p, sizeof p, "thvm-builtin:fill_fp8 rows=%u cols=%u seed=%llu tag=%llu std=%a", rows,
+             cols, (unsigned long long)d->seed, (unsigned long long)name_tag(name), d->c.init_std);
+    u32 ids[2] = {*w, *s};
+    if (run_now(p, ids, 2)) return -1;
+    d->weight_bytes += (u64)rows * cols + (u64)rows * 4;
+    return 0;
+  }
+  *w = weight_normal(d, name, wdt, (u64)rows * cols, 0.0f, d->c.init_std);
+  if (!*w) return -1;
+  d->weight_bytes += (u64)rows * cols * hb_dt_size(wdt);
+  return 0;
+}
+
+static int op_add(Decoder *d, const char *name, const char *prog, const u32 *args, u32 n) {
+  if (n > 24) { hb_set_error("decoder: op %s has too many args", name); return -1; }
+  if (d->n_ops == d->cap_ops) {
+    d->cap_ops = d->cap_ops ? 2 * d->cap_ops : 256;
+    d->ops = (DOp *)realloc(d->ops, d->cap_ops * sizeof(DOp));
+    if (!d->ops) { hb_set_error("decoder: out of memory"); return -1; }
+  }
+  for (u32 i = 0; i < n; i++)
+    if (args[i] == 0) { hb_set_error("decoder: op %s arg %u unset", name, i); return -1; }
+  DOp *o = &d->ops[d->n_ops++];
+  o->name = strdup(name);
+  o->prog = strdup(prog);
+  memcpy(o->args, args, n * sizeof(u32));
+  o->n_args = n;
+  o->outs = 1;
+  if (hb_builtin_launch(prog, args, n, 1)) return -1;   /* validate now */
+  return 0;
+}
+
+static int rope_tables(Decoder *d) {
+  u32 hd = d->c.head_dim, half = hd / 2, ms = d->c.max_seq;
+  u64 n = (u64)ms * half;
+  float *cs = (float *)malloc(n * 4), *sn = (float *)malloc(n * 4);
+  if (!cs || !sn) { free(cs); free(sn); hb_set_error("decoder: out of host memory"); return -1; }
+  for (u32 p = 0; p < ms; p++)
+    for (u32 j = 0; j < half; j++) {
+      double f = 1.0 / pow((double)d->c.rope_theta, (double)(2 * j) / (double)hd);
+      double a = (double)p * f;
+      cs[(u64)p * half + j] = (float)cos(a);
+      sn[(u64)p * half + j] = (float)sin(a);
+    }
+  u32 ci = tens_new(d, "rope.cos", THVM_DT_FP32, n * 4);
+  u32 si = tens_new(d, "rope.sin", THVM_DT_FP32, n * 4);
+  int rc = (!ci || !si || thvm_hip_buf_write(ci, cs, n * 4) || thvm_hip_buf_write(si, sn, n * 4)) ? -1 : 0;
+  free(cs);
+  free(sn);
+  return rc;
+}
+
+static int cfg_check(const ThvmDecodeConfig *c) {
+  if (c->arch != THVM_ARCH_LLAMA && c->arch != THVM_ARCH_GPT2) {
+    hb_set_error("decoder: arch %u not supported by this build", c->arch);
+    return -1;
+  }
+  if (!c->n_layers || !c->dim || !c->n_heads || !c->head_dim || !c->ffn || !c->vocab ||
+      !c->max_seq || !c->batch) {
+    hb_set_error("decoder: zero dimension in config");
+    return -1;
+  }
+  u32 hkv = c->n_kv_heads ? c->n_kv_heads : c->n_heads;
+  if (c->n_heads % hkv) { hb_set_error("decoder: n_heads %% n_kv_heads != 0"); return -1; }
+  if (c->head_dim != 64 && c->head_dim != 128) { hb_set_error("decoder: head_dim must be 64 or 128"); return -1; }
+  if (c->batch > 4) { hb_set_error("decoder: batch %u > 4 needs the small-M GEMM path", c->batch); return -1; }
+  u32 wdt = c->wdtype, adt = c->adtype;
+  if (wdt != THVM_DT_FP32 && wdt != THVM_DT_FP16 && wdt != THVM_DT_BF16 && wdt != THVM_DT_FP8E4M3) {
+    hb_set_error("decoder: weight dtype %u unsupported", wdt);
+    return -1;
+  }
+  if (adt != THVM_DT_FP32 && adt != THVM_DT_FP16 && adt != THVM_DT_BF16) {
+    hb_set_error("decoder: activation dtype %u unsupported", adt);
+    return -1;
+  }
+  if (c->arch == THVM_ARCH_GPT2 && wdt == THVM_DT_FP8E4M3) {
+    hb_set_error("decoder: GPT2 ties the LM head to the embedding; fp8 weights unsupported");
+    return -1;
+  }
+  if (c->arch == THVM_ARCH_GPT2 && (adt == THVM_DT_FP32) != (wdt == THVM_DT_FP32)) {
+    hb_set_error("decoder: GPT2 keeps weights and activations in one dtype");
+    return -1;
+  }
+  return 0;
+}
+
+static int build_llama(Decoder *d);
+static int build_gpt2(Decoder *d);
+
+static void dec_free(Decoder *d) {
+  if (d->jit_slot) thvm_hip_jit_capture_drop(d->jit_slot);
+  for (u32 i = 0; i < d->nt; i++) thvm_hip_buf_free(d->t[i].id);
+  for (u32 i = 0; i < d->n_ops; i++) { free(d->ops[i].name); free(d->ops[i].prog); }
+  free(d->ops);
+  memset(d, 0, sizeof *d);
+}
+
+THVM_API uint32_t thvm_hip_decoder_create(const ThvmDecodeConfig *cfg, uint64_t seed) {
+  if (hb_require_ready("decoder_create")) return 0;
+  if (!cfg || cfg_check(cfg)) return 0;
+  u32 h = 0;
+  for (u32 i = 0; i < MAX_DEC; i++)
+    if (!DEC[i].used) { h = i + 1; break; }
+  if (!h) { hb_set_error("decoder_create: too many decoders"); return 0; }
+  Decoder *d = &DEC[h - 1];
+  memset(d, 0, sizeof *d);
+  d->used = 1;
+  d->c = *cfg;
+  if (!d->c.n_kv_heads) d->c.n_kv_heads = d->c.n_heads;
+  if (d->c.init_std == 0.0f) d->c.init_std = 0.02f;
+  d->seed = seed;
+  d->n_split = (d->c.max_seq + 63) / 64;
+  int rc = d->c.arch == THVM_ARCH_LLAMA ? build_llama(d) : build_gpt2(d);
+  if (rc) { dec_free(d); return 0; }
+  hipError_t e = hipStreamSynchronize(HB_STREAM);
+  if (e != hipSuccess) { hb_set_error("decoder_create: %s", hipGetErrorString(e)); dec_free(d); return 0; }
+  return h;
+}
+
+/* shared state tensors: tok, len, hist, logits, argmax partials, acts */
+static int build_state(Decoder *d) {
+  const ThvmDecodeConfig *c = &d->c;
+  u32 B = c->batch, adt = c->adtype, as = hb_dt_size(adt);
+  u32 hq = c->n_heads * c->head_dim;
+  if (!tens_new(d, "tok", THVM_DT_INT32, (u64)B * 4) || !tens_new(d, "len", THVM_DT_INT32, 4) ||
+      !tens_new(d, "hist", THVM_DT_INT32, (u64)B * (c->max_seq + 1) * 4) ||
+      !tens_new(d, "logits", THVM_DT_FP32, (u64)B * c->vocab * 4) ||
+      !tens_new(d, "am.pv", THVM_DT_FP32, (u64)B * 256 * 4) ||
+      !tens_new(d, "am.pi", THVM_DT_INT32, (u64)B * 256 * 4) ||
+      !tens_new(d, "x", adt, (u64)B * c->dim * as) || !tens_new(d, "xn", adt, (u64)B * c->dim * as) ||
+      !tens_new(d, "q", adt, (u64)B * hq * as) || !tens_new(d, "att", adt, (u64)B * hq * as) ||
+      !tens_new(d, "h", adt, (u64)B * c->ffn * as) ||
+      !tens_new(d, "attn.part", THVM_DT_FP32,
+                thvm_k_attn_part_bytes(B, c->n_heads, c->head_dim, d->n_split)))
+    return -1;
+  for (u32 l = 0; l < c->n_layers; l++) {
+    char kn[32], vn[32];
+    snprintf(kn, sizeof kn, "l%u.kcache", l);
+    snprintf(vn, sizeof vn, "l%u.vcache", l);
+    u64 cb = (u64)B * c->n_kv_heads * c->max_seq * c->head_dim * as;
+    if (!tens_new(d, kn, adt, cb) || !tens_new(d, vn, adt, cb)) return -1;
+  }
+  return 0;
+}
+
+static int op_attn(Decoder *d, u32 l) {
+  const ThvmDecodeConfig *c = &d->c;
+  char p[320], kn[32], vn[32];
+  snprintf(kn, sizeof kn, "l%u.kcache", l);
+  snprintf(vn, sizeof vn, "l%u.vcache", l);
+  snprintf(p, sizeof p,
+           "thvm-builtin:attn b=%u h=%u hkv=%u hd=%u maxseq=%u chunk=64 nsplit=%u qt=%u ct=%u ot=%u scale=%a",
+           c->batch, c->n_heads, c->n_kv_heads, c->head_dim, c->max_seq, d->n_split, c->adtype,
+           c->adtype, c->adtype, (float)(1.0 / sqrt((double)c->head_dim)));
+  u32 a[6] = {tens_find(d, "att"), tens_find(d, "q"), tens_find(d, kn), tens_find(d, vn),
+              tens_find(d, "len"), tens_find(d, "attn.part")};
+  return op_add(d, "attn", p, a, 6);
+}
+
+static int op_tail(Decoder *d, u32 lm_w, u32 lm_s) {
+  const ThvmDecodeConfig *c = &d->c;
+  char p[320];
+  /* LM head -> f32 logits */
+  if (lm_s)
+    snprintf(p, sizeof p, "thvm-builtin:gemv m=%u n=%u k=%u wt=%u xt=%u yt=%u epi=0",
+             c->batch, c->vocab, c->dim, c->wdtype, c->adtype, THVM_DT_FP32);
+  else
+    snprintf(p, sizeof p, "thvm-builtin:gemv m=%u n=%u k=%u wt=%u xt=%u yt=%u epi=0",
+             c->batch, c->vocab, c->dim, c->arch == THVM_ARCH_GPT2 ? c->adtype : c->wdtype,
+             c->adtype, THVM_DT_FP32);
+  u32 a[4] = {tens_find(d, "logits"), tens_find(d, "xn"), lm_w, lm_s};
+  if (op_add(d, "lm_head", p, a, lm_s ? 4 : 3)) return -1;
+  u32 nb = c->vocab >= 256 * 64 ? 256 : (c->vocab + 63) / 64;
+  snprintf(p, sizeof p, "thvm-builtin:argmax b=%u v=%u nb=%u hist=1 hstride=%u", c->batch,
+           c->vocab, nb, c->max_seq + 1);
+  u32 b[6] = {tens_find(d, "tok"), tens_find(d, "logits"), tens_find(d, "am.pv"),
+              tens_find(d, "am.pi"), tens_find(d, "hist"), tens_find(d, "len")};
+  if (op_add(d, "argmax", p, b, 6)) return -1;
+  u32 L = tens_find(d, "len");
+  return op_add(d, "len_bump", "thvm-builtin:len_bump delta=1", &L, 1);
+}
+
+static int build_llama(Decoder *d) {
+  const ThvmDecodeConfig *c = &d->c;
+  u32 D = c->dim, H = c->n_heads, Hkv = c->n_kv_heads, hd = c->head_dim, F = c->ffn;
+  u32 adt = c->adtype, B = c->batch;
+  u32 nqkv = (H + 2 * Hkv) * hd;
+  if (build_state(d)) return -1;
+  if (!weight_normal(d, "emb", adt, (u64)c->vocab * D, 0.0f, c->init_std)) return -1;
+  if (rope_tables(d)) return -1;
+  if (!weight_const(d, "norm_f", D, 1.0f)) return -1;
+  char p[400], nm[48];
+  u32 x = tens_find(d, "x"), xn = tens_find(d, "xn"), q = tens_find(d, "q"),
+      att = tens_find(d, "att"), hb = tens_find(d, "h"), L = tens_find(d, "len");
+
+  snprintf(p, sizeof p, "thvm-builtin:embed b=%u d=%u v=%u et=%u xt=%u", B, D, c->vocab, adt, adt);
+  u32 ea[3] = {x, tens_find(d, "emb"), tens_find(d, "tok")};
+  if (op_add(d, "embed", p, ea, 3)) return -1;
+
+  for (u32 l = 0; l < c->n_layers; l++) {
+    u32 wqkv, sqkv, wo, so, wgu, sgu, wd, sd;
+    snprintf(nm, sizeof nm, "l%u.wqkv", l);
+    if (weight_matrix(d, nm, nqkv, D, &wqkv, &sqkv)) return -1;
+    snprintf(nm, sizeof nm, "l%u.wo", l);
+    if (weight_matrix(d, nm, D, H * hd, &wo, &so)) return -1;
+    snprintf(nm, sizeof nm, "l%u.wgu", l);
+    if (weight_matrix(d, nm, 2 * F, D, &wgu, &sgu)) return -1;
+    snprintf(nm, sizeof nm, "l%u.wd", l);
+    if (weight_matrix(d, nm, D, F, &wd, &sd)) return -1;
+    snprintf(nm, sizeof nm, "l%u.g_attn", l);
+    u32 ga = weight_const(d, nm, D, 1.0f);
+    snprintf(nm, sizeof nm, "l%u.g_ffn", l);
+    u32 gf = weight_const(d, nm, D, 1.0f);
+    if (!ga || !gf) return -1;
+    char kn[32], vn[32];
+    snprintf(kn, sizeof kn, "l%u.kcache", l);
+    snprintf(vn, sizeof vn, "l%u.vcache", l);
+    u32 kc = tens_find(d, kn), vc = tens_find(d, vn);
+    int f8 = c->wdtype == THVM_DT_FP8E4M3;
+
+    snprintf(p, sizeof p, "thvm-builtin:norm m=%u k=%u xt=%u yt=%u eps=%a", B, D, adt, adt, c->eps);
+    u32 n1[3] = {xn, x, ga};
+    if (op_add(d, "norm", p, n1, 3)) return -1;
+
+    snprintf(p, sizeof p,
+             "thvm-builtin:gemv m=%u n=%u k=%u wt=%u xt=%u yt=%u epi=%u h=%u hkv=%u hd=%u maxseq=%u",
+             B, nqkv, D, c->wdtype, adt, adt, THVM_EPI_QKV_ROPE, H, Hkv, hd, c->max_seq);
+    u32 qa[10], qn = 0;
+    qa[qn++] = q; qa[qn++] = xn; qa[qn++] = wqkv;
+    if (f8) qa[qn++] = sqkv;
+    qa[qn++] = tens_find(d, "rope.cos"); qa[qn++] = tens_find(d, "rope.sin");
+    qa[qn++] = L; qa[qn++] = kc; qa[qn++] = vc;
+    if (op_add(d, "gemv_qkv", p, qa, qn)) return -1;
+
+    if (op_attn(d, l)) return -1;
+
+    snprintf(p, sizeof p, "thvm-builtin:gemv m=%u n=%u k=%u wt=%u xt=%u yt=%u epi=%u", B, D, H * hd,
+             c->wdtype, adt, adt, THVM_EPI_RESID);
+    u32 oa[6], on = 0;
+    oa[on++] = x; oa[on++] = att; oa[on++] = wo;
+    if (f8) oa[on++] = so;
+    oa[on++] = x;
+    if (op_add(d, "gemv_o", p, oa, on)) return -1;
+
+    snprintf(p, sizeof p, "thvm-builtin:norm m=%u k=%u xt=%u yt=%u eps=%a", B, D, adt, adt, c->eps);
+    u32 n2[3] = {xn, x, gf};
+    if (op_add(d, "norm", p, n2, 3)) return -1;
+
+    snprintf(p, sizeof p, "thvm-builtin:gemv m=%u n=%u k=%u wt=%u xt=%u yt=%u epi=%u", B, 2 * F, D,
+             c->wdtype, adt, adt, THVM_EPI_SWIGLU);
+    u32 ga2[5], gn = 0;
+    ga2[gn++] = hb; ga2[gn++] = xn; ga2[gn++] = wgu;
+    if (f8) ga2[gn++] = sgu;
+    if (op_add(d, "gemv_gateup", p, ga2, gn)) return -1;
+
+    snprintf(p, sizeof p, "thvm-builtin:gemv m=%u n=%u k=%u wt=%u xt=%u yt=%u epi=%u", B, D, F,
+             c->wdtype, adt, adt, THVM_EPI_RESID);
+    u32 da[6], dn = 0;
+    da[dn++] = x; da[dn++] = hb; da[dn++] = wd;
+    if (f8) da[dn++] = sd;
+    da[dn++] = x;
+    if (op_add(d, "gemv_down", p, da, dn)) return -1;
+  }
+  snprintf(p, sizeof p, "thvm-builtin:norm m=%u k=%u xt=%u yt=%u eps=%a", B, D, adt, adt, c->eps);
+  u32 nf[3] = {xn, x, tens_find(d, "norm_f")};
+  if (op_add(d, "norm", p, nf, 3)) return -1;
+  u32 lw, ls;
+  if (weight_matrix(d, "lm", c->vocab, D, &lw, &ls)) return -1;
+  return op_tail(d, lw, ls);
+}
+
+static int build_gpt2(Decoder *d) {
+  const ThvmDecodeConfig *c = &d->c;
+  u32 D = c->dim, H = c->n_heads, hd = c->head_dim, F = c->ffn, B = c->batch;
+  u32 adt = c->adtype, wdt = c->wdtype;
+  if (H * hd != D) { hb_set_error("decoder: GPT2 needs n_heads*head_dim == dim"); return -1; }
+  if (build_state(d)) return -1;
+  u32 wte = weight_normal(d, "wte", adt, (u64)c->vocab * D, 0.0f, c->init_std);
+  u32 wpe = weight_normal(d, "wpe", adt, (u64)c->max_seq * D, 0.0f, c->init_std);
+  u32 gf = weight_const(d, "lnf.g", D, 1.0f), bf = weight_const(d, "lnf.b", D, 0.0f);
+  if (!wte || !wpe || !gf || !bf) return -1;
+  char p[400], nm[48];
+  u32 x = tens_find(d, "x"), xn = tens_find(d, "xn"), q = tens_find(d, "q"),
+      att = tens_find(d, "att"), hb = tens_find(d, "h"), L = tens_find(d, "len");
+
+  snprintf(p, sizeof p, "thvm-builtin:embed b=%u d=%u v=%u et=%u xt=%u pos=1 maxseq=%u", B, D,
+           c->vocab, adt, adt, c->max_seq);
+  u32 ea[5] = {x, wte, tens_find(d, "tok"), wpe, L};
+  if (op_add(d, "embed", p, ea, 5)) return -1;
+
+  for (u32 l = 0; l < c->n_layers; l++) {
+    u32 wqkv, wo, wfc, wpr, s_unused;
+    snprintf(nm, sizeof nm, "l%u.c_attn", l);
+    if (weight_matrix(d, nm, 3 * D, D, &wqkv, &s_unused)) return -1;
+    snprintf(nm, sizeof nm, "l%u.c_attn.b", l);
+    u32 bqkv = weight_normal(d, nm, adt, 3 * D, 0.0f, c->init_std);
+    snprintf(nm, sizeof nm, "l%u.c_proj", l);
+    if (weight_matrix(d, nm, D, D, &wo, &s_unused)) return -1;
+    snprintf(nm, sizeof nm, "l%u.c_proj.b", l);
+    u32 bo = weight_normal(d, nm, adt, D, 0.0f, c->init_std);
+    snprintf(nm, sizeof nm, "l%u.c_fc", l);
+    if (weight_matrix(d, nm, F, D, &wfc, &s_unused)) return -1;
+    snprintf(nm, sizeof nm, "l%u.c_fc.b", l);
+    u32 bfc = weight_normal(d, nm, adt, F, 0.0f, c->init_std);
+    snprintf(nm, sizeof nm, "l%u.mlp_proj", l);
+    if (weight_matrix(d, nm, D, F, &wpr, &s_unused)) return -1;
+    snprintf(nm, sizeof nm, "l%u.mlp_proj.b", l);
+    u32 bpr = weight_normal(d, nm, adt, D, 0.0f, c->init_std);
+    snprintf(nm, sizeof nm, "l%u.ln1.g", l);
+    u32 g1 = weight_const(d, nm, D, 1.0f);
+    snprintf(nm, sizeof nm, "l%u.ln1.b", l);
+    u32 b1 = weight_const(d, nm, D, 0.0f);
+    snprintf(nm, sizeof nm, "l%u.ln2.g", l);
+    u32 g2 = weight_const(d, nm, D, 1.0f);
+    snprintf(nm, sizeof nm, "l%u.ln2.b", l);
+    u32 b2 = weight_const(d, nm, D, 0.0f);
+    if (!bqkv || !bo || !bfc || !bpr || !g1 || !b1 || !g2 || !b2) return -1;
+    d->weight_bytes += (u64)(3 * D + D + F + D) * hb_dt_size(adt);
+    char kn[32], vn[32];
+    snprintf(kn, sizeof kn, "l%u.kcache", l);
+    snprintf(vn, sizeof vn, "l%u.vcache", l);
+
+    snprintf(p, sizeof p, "thvm-builtin:norm m=%u k=%u xt=%u yt=%u eps=%a ln=1 bias=1", B, D, adt,
+             adt, c->eps);
+    u32 n1[4] = {xn, x, g1, b1};
+    if (op_add(d, "norm", p, n1, 4)) return -1;
+    snprintf(p, sizeof p,
+             "thvm-builtin:gemv m=%u n=%u k=%u wt=%u xt=%u yt=%u epi=%u bias=1 h=%u hkv=%u hd=%u maxseq=%u",
+             B, 3 * D, D, wdt, adt, adt, THVM_EPI_QKV, H, H, hd, c->max_seq);
+    u32 qa[8] = {q, xn, wqkv, bqkv, L, tens_find(d, kn), tens_find(d, vn), 0};
+    if (op_add(d, "gemv_qkv", p, qa, 7)) return -1;
+    if (op_attn(d, l)) return -1;
+    snprintf(p, sizeof p, "thvm-builtin:gemv m=%u n=%u k=%u wt=%u xt=%u yt=%u epi=%u bias=1", B, D,
+             D, wdt, adt, adt, THVM_EPI_RESID);
+    u32 oa[5] = {x, att, wo, bo, x};
+    if (op_add(d, "gemv_o", p, oa, 5)) return -1;
+    snprintf(p, sizeof p, "thvm-builtin:norm m=%u k=%u xt=%u yt=%u eps=%a ln=1 bias=1", B, D, adt,
+             adt, c->eps);
+    u32 n2[4] = {xn, x, g2, b2};
+    if (op_add(d, "norm", p, n2, 4)) return -1;
+    snprintf(p, sizeof p, "thvm-builtin:gemv m=%u n=%u k=%u wt=%u xt=%u yt=%u epi=%u bias=1", B, F,
+             D, wdt, adt, adt, THVM_EPI_GELU);
+    u32 fa[4] = {hb, xn, wfc, bfc};
+    if (op_add(d, "gemv_fc", p, fa, 4)) return -1;
+    snprintf(p, sizeof p, "thvm-builtin:gemv m=%u n=%u k=%u wt=%u xt=%u yt=%u epi=%u bias=1", B, D,
+             F, wdt, adt, adt, THVM_EPI_RESID);
+    u32 pa[5] = {x, hb, wpr, bpr, x};
+    if (op_add(d, "gemv_proj", p, pa, 5)) return -1;
+  }
+  snprintf(p, sizeof p, "thvm-builtin:norm m=%u k=%u xt=%u yt=%u eps=%a ln=1 bias=1", B, D, adt, adt,
+           c->eps);
+  u32 nf[4] = {xn, x, gf, bf};
+  if (op_add(d, "norm", p, nf, 4)) return -1;
+  d->weight_bytes += (u64)c->vocab * D * hb_dt_size(adt);   /* tied LM head */
+  return op_tail(d, wte, 0);
+}
+
+THVM_API void thvm_hip_decoder_destroy(uint32_t h) {
+  Decoder *d = dec_get(h);
+  if (d) dec_free(d);
+}
+
+void hb_decoder_reset(void) {
+  for (u32 i = 0; i < MAX_DEC; i++)
+    if (DEC[i].used) dec_free(&DEC[i]);
+}
+
+THVM_API int thvm_hip_decoder_set_state(uint32_t h, const int32_t *tokens, uint32_t pos) {
+  Decoder *d = dec_get(h);
+  if (!d) return -1;
+  if (pos >= d->c.max_seq) { hb_set_error("decoder_set_state: pos %u >= max_seq %u", pos, d->c.max_seq); return -1; }
+  int32_t L = (int32_t)pos + 1;
+  if (thvm_hip_buf_write(tens_find(d, "tok"), tokens, (u64)d->c.batch * 4)) return -1;
+  if (thvm_hip_buf_write(tens_find(d, "len"), &L, 4)) return -1;
+  u32 hist = tens_find(d, "hist");
+  for (u32 b = 0; b < d->c.batch; b++)
+    if (thvm_hip_buf_write_at(hist, ((u64)b * (d->c.max_seq + 1) + pos) * 4, &tokens[b], 4)) return -1;
+  return 0;
+}
+
+THVM_API int thvm_hip_decoder_prefill_synthetic(uint32_t h, uint32_t ctx, uint64_t seed) {
+  Decoder *d = dec_get(h);
+  if (!d) return -1;
+  const ThvmDecodeConfig *c = &d->c;
+  if (ctx >= c->max_seq) { hb_set_error("prefill: ctx %u >= max_seq", ctx); return -1; }
+  char err[256];
+  for (u32 l = 0; l < c->n_layers; l++) {
+    char kn[32], vn[32];
+    snprintf(kn, sizeof kn, "l%u.kcache", l);
+    snprintf(vn, sizeof vn, "l%u.vcache", l);
+    void *kp = hb_buf_ptr(tens_find(d, kn)), *vp = hb_buf_ptr(tens_find(d, vn));
+    if (!kp || !vp) { hb_set_error("prefill: cache missing"); return -1; }
+    if (thvm_k_fill_cache(kp, c->adtype, c->batch, c->n_kv_heads, c->max_seq, c->head_dim, ctx,
+                          seed, name_tag(kn), HB_STREAM, err, sizeof err) ||
+        thvm_k_fill_cache(vp, c->adtype, c->batch, c->n_kv_heads, c->max_seq, c->head_dim, ctx,
+                          seed, name_tag(vn), HB_STREAM, err, sizeof err)) {
+      hb_set_error("prefill: %s", err);
+      return -1;
+    }
+  }
+  int32_t L = (int32_t)ctx + 1;
+  return thvm_hip_buf_write(tens_find(d, "len"), &L, 4);
+}
+
+static int dec_run_ops(Decoder *d) {
+  for (u32 i = 0; i < d->n_ops; i++) {
+    DOp *o = &d->ops[i];
+    if (thvm_hip_dispatch_custom(o->name, o->prog, NULL, NULL, 0, o->args, o->n_args, o->outs))
+      return -1;
+  }
+  return 0;
+}
+
+THVM_API int thvm_hip_decoder_step(uint32_t h) {
+  Decoder *d = dec_get(h);
+  if (!d) return -1;
+  if (thvm_hip_jit_is_capturing()) { hb_set_error("decoder_step: a JIT capture is open"); return -1; }
+  return dec_run_ops(d);
+}
+
+THVM_API uint32_t thvm_hip_decoder_capture(uint32_t h) {
+  Decoder *d = dec_get(h);
+  if (!d) return 0;
+  if (d->jit_slot) { thvm_hip_jit_capture_drop(d->jit_slot); d->jit_slot = 0; }
+  u32 slot = thvm_hip_jit_capture_begin();
+  if (!slot) return 0;
+  int rc = dec_run_ops(d);
+  thvm_hip_jit_capture_end();
+  if (rc) { thvm_hip_jit_capture_drop(slot); return 0; }
+  d->jit_slot = slot;
+  return slot;
+}
+
+THVM_API int thvm_hip_decoder_replay(uint32_t h, uint32_t n) {
+  Decoder *d = dec_get(h);
+  if (!d) return -1;
+  if (!d->jit_slot) { hb_set_error("decoder_replay: no captured step"); return -1; }
+  for (u32 i = 0; i < n; i++)
+    if (thvm_hip_jit_replay(d->jit_slot)) return -1;
+  return 0;
+}
+
+THVM_API int thvm_hip_decoder_read_tokens(uint32_t h, int32_t *dst, uint32_t n) {
+  Decoder *d = dec_get(h);
+  if (!d) return -1;
+  u32 stride = d->c.max_seq + 1;
+  if (n > stride) { hb_set_error("read_tokens: n %u > %u", n, stride); return -1; }
+  int32_t *tmp = (int32_t *)malloc((u64)d->c.batch * stride * 4);
+  if (!tmp) { hb_set_error("read_tokens: out of host memory"); return -1; }
+  int rc = thvm_hip_buf_read(tens_find(d, "hist"), tmp, (u64)d->c.batch * stride * 4);
+  if (!rc)
+    for (u32 b = 0; b < d->c.batch; b++) memcpy(dst + (u64)b * n, tmp + (u64)b * stride, (u64)n * 4);
+  free(tmp);
+  return rc;
+}
+
+THVM_API int thvm_hip_decoder_read_logits(uint32_t h, float *dst, uint64_t nfloats) {
+  Decoder *d = dec_get(h);
+  if (!d) return -1;
+  u64 have = (u64)d->c.batch * d->c.vocab;
+  if (nfloats > have) nfloats = have;
+  return thvm_hip_buf_read(tens_find(d, "logits"), dst, nfloats * 4);
+}
+
+THVM_API uint32_t thvm_hip_decoder_position(uint32_t h) {
+  Decoder *d = dec_get(h);
+  if (!d) return 0;
+  int32_t L = 0;
+  if (thvm_hip_buf_read(tens_find(d, "len"), &L, 4)) return 0;
+  return L > 0 ? (u32)(L - 1) : 0;
+}
+
+THVM_API uint32_t thvm_hip_decoder_tensor(uint32_t h, const char *name, uint32_t *dtype_out,
+                                          uint64_t *nbytes_out) {
+  Decoder *d = dec_get(h);
+  if (!d || !name) return 0;
+  for (u32 i = 0; i < d->nt; i++)
+    if (strcmp(d->t[i].name, name) == 0) {
+      if (dtype_out) *dtype_out = d->t[i].dt;
+      if (nbytes_out) *nbytes_out = d->t[i].nbytes;
+      return d->t[i].id;
+    }
+  hb_set_error("decoder_tensor: no tensor '%s'", name);
+  return 0;
+}
+
+THVM_API uint64_t thvm_hip_decoder_step_bytes(uint32_t h) {
+  Decoder *d = dec_get(h);
+  if (!d) return 0;
+  const ThvmDecodeConfig *c = &d->c;
+  u32 pos = thvm_hip_decoder_position(h);
+  u64 L = (u64)pos + 1;
+  u64 as = hb_dt_size(c->adtype);
+  /* K and V rows [0, L) of every layer and batch row, plus the new row written */
+  u64 kv = 2ull * c->n_layers * c->batch * c->n_kv_heads * c->head_dim * as * (L + 1);
+  return d->weight_bytes + kv;
+}
+
+THVM_API uint32_t thvm_hip_decoder_step_kernels(uint32_t h) {
+  Decoder *d = dec_get(h);
+  return d ? d->n_ops : 0;
+}

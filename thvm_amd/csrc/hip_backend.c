@@ -1,0 +1,517 @@
+/* hip_backend.c -- the DEV=hip device: lifecycle, buffer table, dispatch
+ * drain, timers.  C11 over the HIP runtime C API.
+ *
+ * Reference counterparts (the CUDA driver-API backend):
+ *   lifecycle        src/backend/cuda/init.c:110-146, _.c:12-53
+ *   buffer table     src/backend/cuda/init.c:40-60 (CudaBuf), buf_alloc.c,
+ *                    buf_free.c, buf_incref.c, buf_decref.c, buf_freelist.c
+ *   read / write     buf_read.c:6-26, buf_write.c:7-17, buf_copy.c
+ *   dispatch_end     _.c:23-27 (drain unless a graph capture is open)
+ * Semantics kept: ids are u32 table indices with 0 = none; fresh buffers read
+ * as zeros; a decref to 0 parks an owning block on a best-fit freelist, and a
+ * recycled block moves to a fresh slot id (the donor id goes dead), so a stale
+ * id can never alias live storage; arena views hold a reference on their
+ * parent.  All transfers and kernels are ordered on one non-blocking stream
+ * created at default priority. */
+#define _GNU_SOURCE
+#include "internal.h"
+
+#include <stdarg.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+char        HB_ERRBUF[512];
+int         HB_READY = 0;
+hipStream_t HB_STREAM = NULL;
+int         HB_GRAPH_CAPTURING = 0;
+
+void hb_set_error(const char *fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(HB_ERRBUF, sizeof HB_ERRBUF, fmt, ap);
+  va_end(ap);
+  if (getenv("THVM_HIP_QUIET") == NULL) fprintf(stderr, "thvm-hip: %s\n", HB_ERRBUF);
+}
+
+THVM_API const char *thvm_hip_last_error(void) { return HB_ERRBUF; }
+THVM_API const char *thvm_hip_version(void) { return "thvm-hip 0.1 gfx950"; }
+
+int hb_require_ready(const char *who) {
+  if (!HB_READY) {
+    hb_set_error("%s: backend not initialised (thvm_hip_init)", who);
+    return -1;
+  }
+  return 0;
+}
+
+u64 hb_hash64(const void *p, size_t n, u64 h) {
+  const u8 *s = (const u8 *)p;
+  if (h == 0) h = 1469598103934665603ull;
+  for (size_t i = 0; i < n; i++) { h ^= s[i]; h *= 1099511628211ull; }
+  return h;
+}
+
+u32 hb_dt_size(u32 dt) {
+  switch (dt) {
+    case THVM_DT_BOOL: case THVM_DT_INT8: case THVM_DT_UINT8:
+    case THVM_DT_FP8E4M3: case THVM_DT_FP8E5M2: return 1;
+    case THVM_DT_INT16: case THVM_DT_UINT16: case THVM_DT_FP16: case THVM_DT_BF16: return 2;
+    case THVM_DT_INT32: case THVM_DT_UINT32: case THVM_DT_FP32: return 4;
+    case THVM_DT_INT64: case THVM_DT_UINT64: case THVM_DT_FP64: return 8;
+    default: return 0;
+  }
+}
+
+/* ======================= buffer table ================================== */
+
+typedef struct {
+  void *dptr;          /* device address (view: parent base + offset) */
+  u64   nbytes;        /* capacity of the block                       */
+  u64   req;           /* requested (logical) size                    */
+  u32   refcount;
+  u32   parent;        /* views: parent id                            */
+  u8    live;
+  u8    owns;          /* 1: hipFree on release                       */
+  u8    parked;        /* on the freelist (refcount 0)                */
+  u8    jit_pinned;
+} HbBuf;
+
+#define HB_BUFS_CAP     (1u << 18)
+#define HB_FREELIST_CAP 4096u
+
+static HbBuf *BUFS = NULL;
+static u32    BUFS_NEXT = 1;
+static u32    FREELIST[HB_FREELIST_CAP];
+static u32    FREELIST_LEN = 0;
+static u64    MEM_LIVE = 0, MEM_PEAK = 0;
+
+static HbBuf *buf_get(u32 id) {
+  if (BUFS == NULL || id == 0 || id >= BUFS_NEXT) return NULL;
+  HbBuf *b = &BUFS[id];
+  return b->live ? b : NULL;
+}
+
+void *hb_buf_ptr(u32 id) {
+  HbBuf *b = buf_get(id);
+  return (b && !b->parked) ? b->dptr : NULL;
+}
+u64 hb_buf_size(u32 id) {
+  HbBuf *b = buf_get(id);
+  return (b && !b->parked) ? b->req : 0;
+}
+
+static u32 slot_new(void) {
+  if (BUFS_NEXT >= HB_BUFS_CAP) {
+    hb_set_error("buf_alloc: out of buffer slots (cap %u)", HB_BUFS_CAP);
+    return 0;
+  }
+  return BUFS_NEXT++;
+}
+
+static void freelist_drop(u32 id) {
+  for (u32 i = 0; i < FREELIST_LEN; i++) {
+    if (FREELIST[i] == id) {
+      FREELIST[i] = FREELIST[--FREELIST_LEN];
+      return;
+    }
+  }
+}
+
+static void real_free(HbBuf *b) {
+  if (b->owns && b->dptr) {
+    hipStreamSynchronize(HB_STREAM);
+    hipFree(b->dptr);
+    MEM_LIVE -= b->nbytes;
+  }
+  memset(b, 0, sizeof *b);
+}
+
+/* best fit among parked blocks with capacity in [n, 2n]; moves the block to a
+ * fresh slot id (reference buf_freelist.c:42-110 slot swap) */
+static u32 freelist_pop(u64 n) {
+  u32 best = 0, best_i = 0;
+  u64 best_sz = ~0ull;
+  for (u32 i = 0; i < FREELIST_LEN; i++) {
+    HbBuf *b = &BUFS[FREELIST[i]];
+    if (b->nbytes >= n && b->nbytes <= 2 * n + 4096 && b->nbytes < best_sz) {
+      best = FREELIST[i];
+      best_i = i;
+      best_sz = b->nbytes;
+    }
+  }
+  if (best == 0) return 0;
+  u32 nid = slot_new();
+  if (nid == 0) return 0;
+  FREELIST[best_i] = FREELIST[--FREELIST_LEN];
+  BUFS[nid] = BUFS[best];
+  memset(&BUFS[best], 0, sizeof(HbBuf));   /* donor id goes dead */
+  HbBuf *b = &BUFS[nid];
+  b->parked = 0;
+  b->refcount = 1;
+  b->req = n;
+  b->jit_pinned = 0;
+  hipMemsetAsync(b->dptr, 0, b->nbytes, HB_STREAM);
+  return nid;
+}
+
+THVM_API uint32_t thvm_hip_buf_alloc(uint64_t nbytes) {
+  if (hb_require_ready("buf_alloc")) return 0;
+  if (HB_GRAPH_CAPTURING) {
+    hb_set_error("buf_alloc: not allowed while a graph capture is open");
+    return 0;
+  }
+  const char *cap = getenv("THVM_MAX_BUF_BYTES");
+  if (cap && cap[0]) {
+    u64 c = strtoull(cap, NULL, 10);
+    if (c != 0 && nbytes > c) {
+      hb_set_error("buf_alloc: refusing %llu-byte allocation (> THVM_MAX_BUF_BYTES %llu)",
+                   (unsigned long long)nbytes, (unsigned long long)c);
+      return 0;
+    }
+  }
+  if (nbytes == 0) nbytes = 1;
+  u32 r = freelist_pop(nbytes);
+  if (r) return r;
+  u32 id = slot_new();
+  if (id == 0) return 0;
+  u64 cap_bytes = (nbytes + 255) & ~255ull;
+  void *p = NULL;
+  hipError_t e = hipMalloc(&p, cap_bytes);
+  if (e != hipSuccess) {
+    BUFS_NEXT--;
+    hb_set_error("hipMalloc(%llu): %s", (unsigned long long)cap_bytes, hipGetErrorString(e));
+    return 0;
+  }
+  e = hipMemsetAsync(p, 0, cap_bytes, HB_STREAM);
+  if (e != hipSuccess) {
+    hipFree(p);
+    BUFS_NEXT--;
+    hb_set_error("hipMemsetAsync: %s", hipGetErrorString(e));
+    return 0;
+  }
+  HbBuf *b = &BUFS[id];
+  memset(b, 0, sizeof *b);
+  b->dptr = p;
+  b->nbytes = cap_bytes;
+  b->req = nbytes;
+  b->refcount = 1;
+  b->live = 1;
+  b->owns = 1;
+  MEM_LIVE += cap_bytes;
+  if (MEM_LIVE > MEM_PEAK) MEM_PEAK = MEM_LIVE;
+  return id;
+}
+
+THVM_API uint32_t thvm_hip_buf_view(uint32_t parent_id, uint64_t byte_off, uint64_t nbytes) {
+  if (hb_require_ready("buf_view")) return 0;
+  HbBuf *p = buf_get(parent_id);
+  if (!p || p->parked) { hb_set_error("buf_view: parent %u not live", parent_id); return 0; }
+  if (byte_off > p->nbytes || nbytes > p->nbytes - byte_off) {
+    hb_set_error("buf_view: [%llu, +%llu) outside parent of %llu bytes",
+                 (unsigned long long)byte_off, (unsigned long long)nbytes,
+                 (unsigned long long)p->nbytes);
+    return 0;
+  }
+  u32 id = slot_new();
+  if (id == 0) return 0;
+  p = &BUFS[parent_id];
+  HbBuf *b = &BUFS[id];
+  memset(b, 0, sizeof *b);
+  b->dptr = (char *)p->dptr + byte_off;
+  b->nbytes = nbytes;
+  b->req = nbytes;
+  b->refcount = 1;
+  b->live = 1;
+  b->owns = 0;
+  b->parent = parent_id;
+  p->refcount++;
+  return id;
+}
+
+static void release(u32 id);
+
+THVM_API void thvm_hip_buf_free(uint32_t buf_id) {
+  HbBuf *b = buf_get(buf_id);
+  if (!b) return;
+  if (b->parked) freelist_drop(buf_id);
+  u32 parent = b->owns ? 0 : b->parent;
+  real_free(b);
+  if (parent) release(parent);
+}
+
+static void release(u32 id) {
+  HbBuf *b = buf_get(id);
+  if (!b || b->refcount == 0) return;
+  if (--b->refcount > 0) return;
+  if (b->jit_pinned) { b->refcount = 1; return; }   /* held by a capture */
+  if (b->owns && FREELIST_LEN < HB_FREELIST_CAP) {
+    b->parked = 1;
+    FREELIST[FREELIST_LEN++] = id;
+    return;
+  }
+  thvm_hip_buf_free(id);
+}
+
+THVM_API void thvm_hip_buf_incref(uint32_t buf_id) {
+  HbBuf *b = buf_get(buf_id);
+  if (b && !b->parked) b->refcount++;
+}
+THVM_API void thvm_hip_buf_decref(uint32_t buf_id) { release(buf_id); }
+
+THVM_API void thvm_hip_buf_jit_pin(uint32_t buf_id) {
+  HbBuf *b = buf_get(buf_id);
+  if (b) b->jit_pinned = 1;
+}
+THVM_API void thvm_hip_buf_jit_unpin(uint32_t buf_id) {
+  HbBuf *b = buf_get(buf_id);
+  if (b) b->jit_pinned = 0;
+}
+THVM_API uint32_t thvm_hip_buf_refcount(uint32_t buf_id) {
+  HbBuf *b = buf_get(buf_id);
+  return (b && !b->parked) ? b->refcount : 0;
+}
+THVM_API void thvm_hip_buf_freelist_push(uint32_t buf_id) {
+  HbBuf *b = buf_get(buf_id);
+  if (!b || b->parked || !b->owns || b->jit_pinned) return;
+  if (FREELIST_LEN >= HB_FREELIST_CAP) return;
+  b->refcount = 0;
+  b->parked = 1;
+  FREELIST[FREELIST_LEN++] = buf_id;
+}
+THVM_API void thvm_hip_buf_freelist_remove(uint32_t buf_id) {
+  HbBuf *b = buf_get(buf_id);
+  if (!b || !b->parked) return;
+  freelist_drop(buf_id);
+  b->parked = 0;
+  b->refcount = 1;
+}
+THVM_API uint32_t thvm_hip_buf_storage_root(uint32_t buf_id) {
+  HbBuf *b = buf_get(buf_id);
+  u32 id = buf_id;
+  while (b && !b->owns && b->parent) {
+    id = b->parent;
+    b = buf_get(id);
+  }
+  return b ? id : 0;
+}
+THVM_API uint64_t thvm_hip_buf_nbytes(uint32_t buf_id) { return hb_buf_size(buf_id); }
+THVM_API uint64_t thvm_hip_buf_device_ptr(uint32_t buf_id) {
+  return (uint64_t)(uintptr_t)hb_buf_ptr(buf_id);
+}
+THVM_API uint64_t thvm_hip_mem_live_bytes(void) { return MEM_LIVE; }
+THVM_API uint64_t thvm_hip_mem_peak_bytes(void) { return MEM_PEAK; }
+
+THVM_API void thvm_hip_buf_zero(uint32_t buf_id) {
+  HbBuf *b = buf_get(buf_id);
+  if (!b || b->parked || !HB_READY) return;
+  hipMemsetAsync(b->dptr, 0, b->req, HB_STREAM);
+}
+
+static int xfer_check(const char *who, u32 id, u64 off, u64 n, HbBuf **out) {
+  if (hb_require_ready(who)) return -1;
+  if (HB_GRAPH_CAPTURING) {
+    hb_set_error("%s: not allowed while a graph capture is open", who);
+    return -1;
+  }
+  HbBuf *b = buf_get(id);
+  if (!b || b->parked) { hb_set_error("%s: buffer %u not live", who, id); return -1; }
+  if (off > b->req || n > b->req - off) {
+    hb_set_error("%s: [%llu, +%llu) outside buffer %u of %llu bytes", who,
+                 (unsigned long long)off, (unsigned long long)n, id, (unsigned long long)b->req);
+    return -1;
+  }
+  *out = b;
+  return 0;
+}
+
+THVM_API int thvm_hip_buf_write_at(uint32_t buf_id, uint64_t off, const void *src, uint64_t n) {
+  HbBuf *b;
+  if (xfer_check("buf_write", buf_id, off, n, &b)) return -1;
+  if (n == 0) return 0;
+  hipError_t e = hipMemcpyAsync((char *)b->dptr + off, src, n, hipMemcpyHostToDevice, HB_STREAM);
+  if (e == hipSuccess) e = hipStreamSynchronize(HB_STREAM);
+  if (e != hipSuccess) { hb_set_error("buf_write: %s", hipGetErrorString(e)); return -1; }
+  return 0;
+}
+THVM_API int thvm_hip_buf_write(uint32_t buf_id, const void *src, uint64_t n) {
+  return thvm_hip_buf_write_at(buf_id, 0, src, n);
+}
+THVM_API int thvm_hip_buf_read(uint32_t buf_id, void *dst, uint64_t n) {
+  HbBuf *b;
+  if (xfer_check("buf_read", buf_id, 0, n, &b)) return -1;
+  if (n == 0) return 0;
+  hipError_t e = hipMemcpyAsync(dst, b->dptr, n, hipMemcpyDeviceToHost, HB_STREAM);
+  if (e == hipSuccess) e = hipStreamSynchronize(HB_STREAM);
+  if (e != hipSuccess) { hb_set_error("buf_read: %s", hipGetErrorString(e)); return -1; }
+  return 0;
+}
+THVM_API int thvm_hip_buf_copy_at(uint32_t dst_id, uint64_t dst_off, uint32_t src_id, uint64_t n) {
+  HbBuf *d, *s;
+  if (xfer_check("buf_copy", dst_id, dst_off, n, &d)) return -1;
+  if (xfer_check("buf_copy", src_id, 0, n, &s)) return -1;
+  if (n == 0) return 0;
+  hipError_t e = hipMemcpyAsync((char *)d->dptr + dst_off, s->dptr, n, hipMemcpyDeviceToDevice,
+                                HB_STREAM);
+  if (e != hipSuccess) { hb_set_error("buf_copy: %s", hipGetErrorString(e)); return -1; }
+  return 0;
+}
+THVM_API int thvm_hip_buf_copy(uint32_t dst_id, uint32_t src_id, uint64_t n) {
+  return thvm_hip_buf_copy_at(dst_id, 0, src_id, n);
+}
+
+/* ======================= lifecycle ===================================== */
+
+THVM_API int thvm_hip_init(void) {
+  if (HB_READY) return 0;
+  int n = 0;
+  hipError_t e = hipGetDeviceCount(&n);
+  if (e != hipSuccess || n < 1) {
+    hb_set_error("init: no HIP device (%s)", hipGetErrorString(e));
+    return -1;
+  }
+  hipDeviceProp_t prop;
+  e = hipGetDeviceProperties(&prop, 0);
+  if (e != hipSuccess) { hb_set_error("init: hipGetDeviceProperties: %s", hipGetErrorString(e)); return -1; }
+  if (strncmp(prop.gcnArchName, "gfx950", 6) != 0) {
+    hb_set_error("init: device 0 is %s, this library is built for gfx950", prop.gcnArchName);
+    return -1;
+  }
+  e = hipSetDevice(0);
+  if (e != hipSuccess) { hb_set_error("init: hipSetDevice: %s", hipGetErrorString(e)); return -1; }
+  e = hipStreamCreateWithFlags(&HB_STREAM, hipStreamNonBlocking);
+  if (e != hipSuccess) { hb_set_error("init: hipStreamCreate: %s", hipGetErrorString(e)); return -1; }
+  if (BUFS == NULL) {
+    BUFS = (HbBuf *)calloc(HB_BUFS_CAP, sizeof(HbBuf));
+    if (!BUFS) { hb_set_error("init: out of host memory"); return -1; }
+  }
+  HB_READY = 1;
+  return 0;
+}
+
+THVM_API int thvm_hip_available(void) { return HB_READY; }
+
+THVM_API void thvm_hip_shutdown(void) {
+  if (!HB_READY) return;
+  hipStreamSynchronize(HB_STREAM);
+  hb_decoder_reset();
+  hb_jit_reset();
+  hb_graph_reset();
+  hb_rtc_reset();
+  for (u32 i = BUFS_NEXT; i-- > 1;) {
+    if (BUFS[i].live && !BUFS[i].owns) memset(&BUFS[i], 0, sizeof(HbBuf));
+  }
+  for (u32 i = 1; i < BUFS_NEXT; i++) {
+    if (BUFS[i].live && BUFS[i].owns && BUFS[i].dptr) hipFree(BUFS[i].dptr);
+    memset(&BUFS[i], 0, sizeof(HbBuf));
+  }
+  BUFS_NEXT = 1;
+  FREELIST_LEN = 0;
+  MEM_LIVE = 0;
+  hipStreamDestroy(HB_STREAM);
+  HB_STREAM = NULL;
+  HB_READY = 0;
+}
+
+/* ======================= dispatch drain ================================ */
+
+THVM_API void thvm_hip_dispatch_begin(void) {}
+THVM_API void thvm_hip_dispatch_flush(void) {}
+THVM_API void thvm_hip_dispatch_end(void) {
+  if (!HB_READY || HB_GRAPH_CAPTURING) return;
+  hipError_t e = hipStreamSynchronize(HB_STREAM);
+  if (e != hipSuccess) hb_set_error("dispatch_end: %s", hipGetErrorString(e));
+}
+
+/* ======================= timers ======================================== */
+
+#define HB_TIMERS 64
+static hipEvent_t TIMER_EV[HB_TIMERS];
+static u32 TIMER_NEXT = 0;
+
+THVM_API uint32_t thvm_hip_timer_start(void) {
+  if (hb_require_ready("timer_start")) return 0;
+  u32 id = (TIMER_NEXT % (HB_TIMERS - 1)) + 1;
+  TIMER_NEXT++;
+  if (TIMER_EV[id] == NULL && hipEventCreate(&TIMER_EV[id]) != hipSuccess) {
+    hb_set_error("timer: hipEventCreate failed");
+    return 0;
+  }
+  hipEventRecord(TIMER_EV[id], HB_STREAM);
+  return id;
+}
+THVM_API double thvm_hip_timer_stop(uint32_t id) {
+  if (!HB_READY || id == 0 || id >= HB_TIMERS || TIMER_EV[id] == NULL) return -1.0;
+  hipEvent_t end;
+  if (hipEventCreate(&end) != hipSuccess) return -1.0;
+  hipEventRecord(end, HB_STREAM);
+  hipEventSynchronize(end);
+  float ms = 0.0f;
+  hipEventElapsedTime(&ms, TIMER_EV[id], end);
+  hipEventDestroy(end);
+  return (double)ms;
+}
+
+/* ---- per-kernel profiling: an event pair around each builtin launch,
+ *      resolved lazily (no per-launch synchronisation) ---- */
+typedef struct { char tag[24]; hipEvent_t e0, e1; u64 bytes; } KpRec;
+static KpRec *KP = NULL;
+static u32 KP_N = 0, KP_CAP = 0;
+static int KP_ON = 0;
+static hipEvent_t *KP_POOL = NULL;
+static u32 KP_POOL_N = 0, KP_POOL_CAP = 0, KP_POOL_USED = 0;
+
+int hb_kprof_on(void) { return KP_ON && !HB_GRAPH_CAPTURING; }
+
+static hipEvent_t kp_event(void) {
+  if (KP_POOL_USED < KP_POOL_N) return KP_POOL[KP_POOL_USED++];
+  if (KP_POOL_N == KP_POOL_CAP) {
+    KP_POOL_CAP = KP_POOL_CAP ? 2 * KP_POOL_CAP : 1024;
+    KP_POOL = (hipEvent_t *)realloc(KP_POOL, KP_POOL_CAP * sizeof(hipEvent_t));
+  }
+  hipEvent_t e = NULL;
+  hipEventCreate(&e);
+  KP_POOL[KP_POOL_N++] = e;
+  KP_POOL_USED++;
+  return e;
+}
+
+void hb_kprof_begin(const char *tag, hipEvent_t *e0) {
+  (void)tag;
+  *e0 = kp_event();
+  hipEventRecord(*e0, HB_STREAM);
+}
+void hb_kprof_end(const char *tag, hipEvent_t e0, u64 bytes) {
+  hipEvent_t e1 = kp_event();
+  hipEventRecord(e1, HB_STREAM);
+  if (KP_N == KP_CAP) {
+    KP_CAP = KP_CAP ? 2 * KP_CAP : 1024;
+    KP = (KpRec *)realloc(KP, KP_CAP * sizeof(KpRec));
+  }
+  KpRec *r = &KP[KP_N++];
+  snprintf(r->tag, sizeof r->tag, "%s", tag);
+  r->e0 = e0;
+  r->e1 = e1;
+  r->bytes = bytes;
+}
+
+THVM_API void thvm_hip_kprof_enable(int on) { KP_ON = on; }
+THVM_API void thvm_hip_kprof_reset(void) {
+  if (HB_READY) hipStreamSynchronize(HB_STREAM);
+  KP_N = 0;
+  KP_POOL_USED = 0;
+}
+THVM_API double thvm_hip_kprof_query(const char *tag, uint64_t *count_out) {
+  if (!HB_READY) return -1.0;
+  hipStreamSynchronize(HB_STREAM);
+  double tot = 0.0;
+  u64 cnt = 0;
+  for (u32 i = 0; i < KP_N; i++) {
+    if (tag != NULL && strcmp(KP[i].tag, tag) != 0) continue;
+    float ms = 0.0f;
+    if (hipEventElapsedTime(&ms, KP[i].e0, KP[i].e1) == hipSuccess) tot += ms;
+    cnt++;
+  }
+  if (count_out) *count_out = cnt;
+  return cnt ? tot : -1.0;
+}

@@ -1,0 +1,131 @@
+/* kern_api.h -- internal launch interface between the C host layer and the
+ * hand-written gfx950 kernels under thvm_amd/csrc/kernels.  C-compatible.
+ * Every launcher validates shapes against the buffers' byte sizes it is
+ * given, returns 0 on success and -1 (with a message in *err) otherwise, and
+ * enqueues on `stream` without synchronising. */
+#ifndef THVM_KERN_API_H
+#define THVM_KERN_API_H
+
+#include <stdint.h>
+#include <hip/hip_runtime_api.h>
+#include "thvm_hip.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* GEMV / small-M GEMM epilogues */
+enum {
+  THVM_EPI_STORE    = 0,  /* y = rnd(acc*s + b)                                 */
+  THVM_EPI_RESID    = 1,  /* y = rnd(res + rnd(acc*s + b))  (y may alias res)   */
+  THVM_EPI_SWIGLU   = 2,  /* rows (2i,2i+1)=(gate_i,up_i): y[i]=rnd(silu(g)*u)  */
+  THVM_EPI_GELU     = 3,  /* y = rnd(gelu(rnd(acc*s + b)))                       */
+  THVM_EPI_QKV_ROPE = 4,  /* q -> y (roped), k (roped) / v -> caches at pos      */
+  THVM_EPI_QKV      = 5   /* as QKV_ROPE without the rotation (GPT-2)          */
+};
+
+typedef struct ThvmGemvArgs {
+  void        *y;
+  const void  *x;
+  const void  *w;          /* [N, K] row-major, K contiguous                   */
+  const float *scale;      /* [N] per-row scale (fp8) or NULL                  */
+  const void  *bias;       /* [N] (ydt) or NULL                                */
+  const void  *res;        /* residual [M, ldy] (ydt) or NULL                  */
+  const float *rope_cos;   /* [max_seq, head_dim/2]                            */
+  const float *rope_sin;
+  const int32_t *len;      /* device length L; the write position is L-1     */
+  void        *kcache;     /* [M][n_kv][max_seq][head_dim] (ydt)               */
+  void        *vcache;
+  uint32_t M, N, K;
+  uint32_t ldx, ldy;       /* row strides in elements                          */
+  uint32_t wdt, xdt, ydt;  /* THVM_DT_*                                        */
+  uint32_t epi;
+  uint32_t n_heads, n_kv_heads, head_dim, max_seq;
+} ThvmGemvArgs;
+int thvm_k_gemv(const ThvmGemvArgs *a, hipStream_t s, char *err, int errlen);
+
+/* Row norms over [M, K]: RMSNorm (y = rnd((x*inv)*w), inv=1/sqrt(ss/K+eps))
+ * or LayerNorm (y = rnd((x-mu)*rsqrt(var+eps)*w + b)).  x may be f32/bf16/f16,
+ * y f32/bf16/f16.  `ldx`/`ldy` are row strides.  For RMSNorm `w` may be NULL
+ * (gain 1). */
+typedef struct ThvmNormArgs {
+  void *y; const void *x; const float *w; const float *b;
+  uint32_t M, K, ldx, ldy, xdt, ydt;
+  float eps;
+  int layernorm;
+} ThvmNormArgs;
+int thvm_k_norm(const ThvmNormArgs *a, hipStream_t s, char *err, int errlen);
+
+/* Row softmax over [M, K] (x f32/bf16/f16 -> y same family). */
+typedef struct ThvmSoftmaxArgs {
+  void *y; const void *x; uint32_t M, K, xdt, ydt;
+} ThvmSoftmaxArgs;
+int thvm_k_softmax(const ThvmSoftmaxArgs *a, hipStream_t s, char *err, int errlen);
+
+/* Split-sequence flash-decode attention over a KV cache.
+ * q [B][H][hd] (qdt), caches [B][Hkv][max_seq][hd] (cdt), live length L (device
+ * scalar, same for all rows).  Phase 1 writes per-split (m, l, acc[hd]); phase
+ * 2 combines into out [B][H*hd] (odt). */
+typedef struct ThvmAttnArgs {
+  void *out; const void *q; const void *kcache; const void *vcache;
+  const int32_t *len;
+  float *part;             /* scratch: [B][H][n_split][hd + 2] f32          */
+  uint32_t B, H, Hkv, hd, max_seq, chunk, n_split;
+  uint32_t qdt, cdt, odt;
+  float scale;             /* 1/sqrt(hd)                                     */
+} ThvmAttnArgs;
+int thvm_k_attn_decode(const ThvmAttnArgs *a, hipStream_t s, char *err, int errlen);
+uint64_t thvm_k_attn_part_bytes(uint32_t B, uint32_t H, uint32_t hd, uint32_t n_split);
+
+/* Embedding gather: x[b][i] = emb[tok[b]][i] (+ pos[L-1][i] when pos != NULL),
+ * tok int32 [B]; out of range ids read a zero row. */
+typedef struct ThvmEmbedArgs {
+  void *x; const void *emb; const void *pos_emb; const int32_t *tok;
+  const int32_t *len;
+  uint32_t B, D, V, max_seq, edt, xdt;
+} ThvmEmbedArgs;
+int thvm_k_embed(const ThvmEmbedArgs *a, hipStream_t s, char *err, int errlen);
+
+/* Greedy argmax over logits [B][V] f32, lowest index on ties (reference
+ * bench/dsv2_decode_bench.c:967-1022).  Writes tok[b]; when `hist` is set
+ * also hist[b*hist_stride + L-1]. */
+typedef struct ThvmArgmaxArgs {
+  int32_t *tok; const float *logits; float *pv; int32_t *pi;
+  int32_t *hist; const int32_t *len;
+  uint32_t B, V, nb, hist_stride;
+} ThvmArgmaxArgs;
+int thvm_k_argmax(const ThvmArgmaxArgs *a, hipStream_t s, char *err, int errlen);
+
+/* L[0] += delta (reference len_bump, bench/dsv2_decode_bench.c:1024-1041). */
+int thvm_k_len_bump(int32_t *len, int32_t delta, hipStream_t s, char *err, int errlen);
+
+/* Synthetic data: counter-based N(mean, std) fill of n elements of dtype dt,
+ * stream id `tag` under `seed`; and per-row fp8 e4m3 quantisation of a
+ * rows x cols N(0,std) matrix: scale[r] = absmax/448, q = sat_e4m3(w/scale). */
+int thvm_k_fill_normal(void *dst, uint32_t dt, uint64_t n, uint64_t seed,
+                       uint64_t tag, float mean, float std, hipStream_t s,
+                       char *err, int errlen);
+int thvm_k_fill_fp8_rows(uint8_t *q, float *scale, uint32_t rows, uint32_t cols,
+                         uint64_t seed, uint64_t tag, float std, hipStream_t s,
+                         char *err, int errlen);
+/* Fill rows [0, ctx) of a [B][Hkv][max_seq][hd] cache with N(0,1). */
+int thvm_k_fill_cache(void *cache, uint32_t dt, uint32_t B, uint32_t Hkv,
+                      uint32_t max_seq, uint32_t hd, uint32_t ctx,
+                      uint64_t seed, uint64_t tag, hipStream_t s,
+                      char *err, int errlen);
+
+/* Element-wise casts / copies (codec probes and glue): y[i] = cvt(x[i]). */
+int thvm_k_cast(void *y, uint32_t ydt, const void *x, uint32_t xdt, uint64_t n,
+                hipStream_t s, char *err, int errlen);
+
+/* RoPE in place on [B][nh][hd] (interleaved pairs) at position L-1. */
+typedef struct ThvmRopeArgs {
+  void *x; const float *cos_t; const float *sin_t; const int32_t *len;
+  uint32_t B, nh, hd, dt, max_seq;   /* tables hold max_seq positions */
+} ThvmRopeArgs;
+int thvm_k_rope(const ThvmRopeArgs *a, hipStream_t s, char *err, int errlen);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,167 @@
+// dev_common.h -- gfx950 device helpers shared by the hand-written decode
+// kernels: narrow-float codecs, wave64 DPP reductions, 128-bit loads.
+//
+// Numerics follow the reference codecs bit for bit:
+//   bf16 <-> f32  reference src/dtype/fp_convert.c:113-136 (RNE, NaN -> quiet
+//                 NaN keeping the sign);
+//   fp16 <-> f32  IEEE RNE (reference src/dtype/fp_convert.c:26-110; the
+//                 gfx950 v_cvt_f16_f32 / v_cvt_f32_f16 pair is IEEE RNE);
+//   e4m3  -> f32  exact decode (reference src/dtype/fp8.c:149-175), done by the
+//                 gfx950 OCP-fp8 converter v_cvt_pk_f32_fp8;
+//   f32 -> e4m3   saturating RNE encode with subnormals (reference
+//                 src/dtype/fp8.c:60-133, the _sat kernel-store form).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+typedef uint16_t bf16_t;
+typedef uint16_t f16_t;
+
+#define THVM_WAVE 64
+
+// ---- bf16 ------------------------------------------------------------------
+__device__ __forceinline__ float bf2f(bf16_t h) {
+  return __uint_as_float(((uint32_t)h) << 16);
+}
+__device__ __forceinline__ bf16_t f2bf(float f) {
+  uint32_t b = __float_as_uint(f);
+  if ((b & 0x7f800000u) == 0x7f800000u && (b & 0x7fffffu) != 0u)
+    return (bf16_t)(((b & 0x80000000u) | 0x7f800000u | 0x400000u) >> 16);
+  return (bf16_t)((b + 0x7fffu + ((b >> 16) & 1u)) >> 16);
+}
+// round a float through bf16 storage
+__device__ __forceinline__ float rbf(float f) { return bf2f(f2bf(f)); }
+
+// ---- fp16 ------------------------------------------------------------------
+__device__ __forceinline__ float h2f(f16_t h) {
+  _Float16 v = __builtin_bit_cast(_Float16, h);
+  return (float)v;
+}
+__device__ __forceinline__ f16_t f2h(float f) {
+  _Float16 v = (_Float16)f;
+  return __builtin_bit_cast(f16_t, v);
+}
+__device__ __forceinline__ float rh(float f) { return h2f(f2h(f)); }
+
+// ---- fp8 e4m3 (OCP e4m3fn, the gfx950 fp8 format) --------------------------
+// Four packed bytes -> four floats.  Exact for every finite pattern; 0x7F /
+// 0xFF decode to NaN, as the reference does (fp8.c:156-158).
+__device__ __forceinline__ void fp8x4_to_f32(uint32_t w, float o[4]) {
+  auto lo = __builtin_amdgcn_cvt_pk_f32_fp8((int)w, false);
+  auto hi = __builtin_amdgcn_cvt_pk_f32_fp8((int)w, true);
+  o[0] = lo[0]; o[1] = lo[1]; o[2] = hi[0]; o[3] = hi[1];
+}
+__device__ __forceinline__ float fp82f(uint8_t b) {
+  auto lo = __builtin_amdgcn_cvt_pk_f32_fp8((int)b, false);
+  return lo[0];
+}
+
+// Saturating e4m3 encode, written from the OCP definition: round to nearest
+// even on the f32 significand, finite overflow and +-inf to +-448 (0x7E/0xFE),
+// NaN to sign|0x7F, subnormals kept (min subnormal 2^-9).
+__device__ __forceinline__ uint8_t f2fp8_sat(float x) {
+  uint32_t u = __float_as_uint(x);
+  uint32_t sign = (u >> 24) & 0x80u;
+  uint32_t a = u & 0x7fffffffu;
+  if (a > 0x7f800000u) return (uint8_t)(sign | 0x7Fu);     // NaN
+  if (a >= 0x43E00000u) {                                   // >= 448 (incl inf)
+    // values in [448, 464) round to 448, >= 464 overflow: both saturate
+    return (uint8_t)(sign | 0x7Eu);
+  }
+  int e = (int)(a >> 23) - 127;                             // unbiased exp
+  if (e < -6) {
+    // subnormal range: value = m * 2^-9, m in [0, 8]
+    // q = round_even(|x| * 2^9)
+    float s = __uint_as_float(a) * 512.0f;                  // exact (power of 2)
+    // round half to even on a float known < 8
+    float r = __builtin_rintf(s);                           // RNE (default mode)
+    uint32_t m = (uint32_t)r;                               // 0..8
+    // m == 8 is the smallest normal 2^-6 = exp field 1, mantissa 0
+    return (uint8_t)(sign | m);
+  }
+  // normal: keep 3 mantissa bits, RNE on the dropped 20 bits
+  uint32_t mant = a & 0x7fffffu;
+  uint32_t q = ((uint32_t)(e + 7) << 3) | (mant >> 20);
+  uint32_t rem = mant & 0xfffffu;
+  if (rem > 0x80000u || (rem == 0x80000u && (q & 1u))) q += 1;
+  if (q > 0x7Eu) q = 0x7Eu;                                 // 464 boundary
+  return (uint8_t)(sign | q);
+}
+
+// ---- wave64 DPP reductions --------------------------------------------------
+// Sum / max over all 64 lanes.  The DPP sequence fixes the association order,
+// so the result is deterministic run to run: quad pairs, quads, half-row
+// mirror, row mirror, then row_bcast:15 and row_bcast:31 carry the partial
+// row sums up to lane 63, whose value is broadcast.
+template <int CTRL, int ROWMASK = 0xf>
+__device__ __forceinline__ float dpp_f(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL,
+                                                    ROWMASK, 0xf, true));
+}
+template <int CTRL, int ROWMASK = 0xf>
+__device__ __forceinline__ float dpp_f_old(float old, float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(old),
+                                                    __float_as_int(v), CTRL,
+                                                    ROWMASK, 0xf, false));
+}
+
+// sum within each row of 16 lanes; every lane of the row holds the row sum
+__device__ __forceinline__ float row16_sum(float v) {
+  v += dpp_f<0xB1>(v);    // quad_perm [1,0,3,2]
+  v += dpp_f<0x4E>(v);    // quad_perm [2,3,0,1]
+  v += dpp_f<0x141>(v);   // row_half_mirror
+  v += dpp_f<0x140>(v);   // row_mirror
+  return v;
+}
+__device__ __forceinline__ float row16_max(float v) {
+  v = fmaxf(v, dpp_f<0xB1>(v));
+  v = fmaxf(v, dpp_f<0x4E>(v));
+  v = fmaxf(v, dpp_f<0x141>(v));
+  v = fmaxf(v, dpp_f<0x140>(v));
+  return v;
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+  v = row16_sum(v);
+  v += dpp_f<0x142, 0xa>(v);   // row_bcast:15 into rows 1 and 3
+  v += dpp_f<0x143, 0xc>(v);   // row_bcast:31 into rows 2 and 3
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+}
+__device__ __forceinline__ float wave_max(float v) {
+  v = row16_max(v);
+  // rows 0/2 keep their own value (old = v) so the max stays correct
+  v = fmaxf(v, dpp_f_old<0x142, 0xa>(v, v));
+  v = fmaxf(v, dpp_f_old<0x143, 0xc>(v, v));
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+}
+
+// lanes l, l^16, l^32, l^48 combined (the 4 rows of a wave), all lanes
+__device__ __forceinline__ float xrow_sum(float v) {
+  v += __shfl_xor(v, 16);
+  v += __shfl_xor(v, 32);
+  return v;
+}
+__device__ __forceinline__ float xrow_max(float v) {
+  v = fmaxf(v, __shfl_xor(v, 16));
+  v = fmaxf(v, __shfl_xor(v, 32));
+  return v;
+}
+
+__device__ __forceinline__ int lane_id() { return (int)(threadIdx.x & 63u); }
+
+// 128-bit global load of streamed (read-once) data
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ uint4 ld_stream16(const void *p) {
+  u32x4_t v = __builtin_nontemporal_load((const u32x4_t *)p);
+  return make_uint4(v[0], v[1], v[2], v[3]);
+}
+__device__ __forceinline__ uint4 ld16(const void *p) {
+  return *(const uint4 *)p;
+}
+
+__device__ __forceinline__ float silu_f(float g) { return g / (1.0f + expf(-g)); }
+__device__ __forceinline__ float gelu_tanh_f(float x) {
+  // tinygrad Tensor.gelu: 0.5 x (1 + tanh(sqrt(2/pi) (x + 0.044715 x^3)))
+  float u = 0.7978845608f * (x + 0.044715f * x * x * x);
+  return 0.5f * x * (1.0f + tanhf(u));
+}

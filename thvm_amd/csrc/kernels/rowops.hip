@@ -1,0 +1,387 @@
+// rowops.hip -- row-wise decode ops on gfx950: RMSNorm / LayerNorm, softmax,
+// RoPE, embedding gather, greedy argmax, the device position bump, and casts.
+//
+// Semantics (reference file:line):
+//   RMSNorm    y = rnd((x * inv) * w), inv = 1/sqrtf(ss * (1/K) + eps)
+//              (bench/dsv2_decode_bench.c:397-433 src_rms; py/thvm/nn.py:211-224)
+//   LayerNorm  (x - mean) * rsqrt(var + eps) * w + b, biased variance
+//              (src/nn/layernorm.c:1-7)
+//   softmax    exp(x - max) * (1 / sum)   (src/nn/softmax.c:1-16)
+//   RoPE       interleaved pairs (2j, 2j+1) rotated by cos/sin[pos][j]
+//              (bench/dsv2_decode_bench.c:435-485 gred_q pe slice)
+//   embed      x = emb[tok] (+ pos_emb[pos])  (:377-395; thvm_gpt2.py:92-95)
+//   argmax     lowest index on ties, two passes (:967-1022)
+//   len_bump   L += 1 (:1024-1041)
+// The reductions are block-wide trees (DPP inside each wave, LDS across the
+// 4-16 waves): a fixed order, so results are reproducible run to run, but not
+// the reference's serial order -- parity is held to the stated tolerances.
+#include "dev_common.h"
+#include "../kern_api.h"
+#include <stdio.h>
+
+__device__ __forceinline__ float ld_a(const void *p, uint64_t i, uint32_t dt) {
+  switch (dt) {
+    case THVM_DT_FP32: return ((const float *)p)[i];
+    case THVM_DT_BF16: return bf2f(((const bf16_t *)p)[i]);
+    case THVM_DT_FP16: return h2f(((const f16_t *)p)[i]);
+    case THVM_DT_FP8E4M3: return fp82f(((const uint8_t *)p)[i]);
+    default: return 0.0f;
+  }
+}
+__device__ __forceinline__ void st_a(void *p, uint64_t i, uint32_t dt, float v) {
+  switch (dt) {
+    case THVM_DT_FP32: ((float *)p)[i] = v; break;
+    case THVM_DT_BF16: ((bf16_t *)p)[i] = f2bf(v); break;
+    case THVM_DT_FP16: ((f16_t *)p)[i] = f2h(v); break;
+    case THVM_DT_FP8E4M3: ((uint8_t *)p)[i] = f2fp8_sat(v); break;
+    default: break;
+  }
+}
+
+#define ROW_THREADS 256
+#define ROW_WAVES (ROW_THREADS / 64)
+
+// block-wide sum of one float per thread (all threads get the result)
+__device__ __forceinline__ float block_sum(float v, float *red) {
+  float w = wave_sum(v);
+  const int wv = threadIdx.x >> 6;
+  __syncthreads();
+  if (lane_id() == 0) red[wv] = w;
+  __syncthreads();
+  float t = 0.0f;
+#pragma unroll
+  for (int i = 0; i < ROW_WAVES; i++) t += red[i];
+  return t;
+}
+__device__ __forceinline__ float block_max(float v, float *red) {
+  float w = wave_max(v);
+  const int wv = threadIdx.x >> 6;
+  __syncthreads();
+  if (lane_id() == 0) red[wv] = w;
+  __syncthreads();
+  float t = red[0];
+#pragma unroll
+  for (int i = 1; i < ROW_WAVES; i++) t = fmaxf(t, red[i]);
+  return t;
+}
+
+__global__ __launch_bounds__(ROW_THREADS) void k_norm(ThvmNormArgs a) {
+  __shared__ float red[ROW_WAVES];
+  const uint32_t m = blockIdx.x;
+  const uint64_t xo = (uint64_t)m * a.ldx, yo = (uint64_t)m * a.ldy;
+  const float invK = 1.0f / (float)a.K;
+  if (!a.layernorm) {
+    float ss = 0.0f;
+    for (uint32_t i = threadIdx.x; i < a.K; i += ROW_THREADS) {
+      float v = ld_a(a.x, xo + i, a.xdt);
+      ss += v * v;
+    }
+    ss = block_sum(ss, red);
+    float inv = 1.0f / sqrtf(ss * invK + a.eps);
+    for (uint32_t i = threadIdx.x; i < a.K; i += ROW_THREADS) {
+      float v = ld_a(a.x, xo + i, a.xdt) * inv;
+      if (a.w) v = v * a.w[i];
+      st_a(a.y, yo + i, a.ydt, v);
+    }
+  } else {
+    float s = 0.0f;
+    for (uint32_t i = threadIdx.x; i < a.K; i += ROW_THREADS) s += ld_a(a.x, xo + i, a.xdt);
+    float mean = block_sum(s, red) * invK;
+    float vs = 0.0f;
+    for (uint32_t i = threadIdx.x; i < a.K; i += ROW_THREADS) {
+      float d = ld_a(a.x, xo + i, a.xdt) - mean;
+      vs += d * d;
+    }
+    float var = block_sum(vs, red) * invK;
+    float r = 1.0f / sqrtf(var + a.eps);
+    for (uint32_t i = threadIdx.x; i < a.K; i += ROW_THREADS) {
+      float v = (ld_a(a.x, xo + i, a.xdt) - mean) * r;
+      if (a.w) v = v * a.w[i];
+      if (a.b) v = v + a.b[i];
+      st_a(a.y, yo + i, a.ydt, v);
+    }
+  }
+}
+
+static int act_dt(uint32_t dt) {
+  return dt == THVM_DT_FP32 || dt == THVM_DT_FP16 || dt == THVM_DT_BF16;
+}
+
+extern "C" int thvm_k_norm(const ThvmNormArgs *a, hipStream_t s, char *err, int errlen) {
+  if (!act_dt(a->xdt) || !act_dt(a->ydt) || a->M == 0 || a->K == 0 || a->ldx < a->K ||
+      a->ldy < a->K) {
+    snprintf(err, errlen, "norm: bad args M=%u K=%u", a->M, a->K);
+    return -1;
+  }
+  hipLaunchKernelGGL(k_norm, dim3(a->M), dim3(ROW_THREADS), 0, s, *a);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) { snprintf(err, errlen, "norm launch: %s", hipGetErrorString(e)); return -1; }
+  return 0;
+}
+
+__global__ __launch_bounds__(ROW_THREADS) void k_softmax(ThvmSoftmaxArgs a) {
+  __shared__ float red[ROW_WAVES];
+  const uint64_t o = (uint64_t)blockIdx.x * a.K;
+  float mx = -INFINITY;
+  for (uint32_t i = threadIdx.x; i < a.K; i += ROW_THREADS) mx = fmaxf(mx, ld_a(a.x, o + i, a.xdt));
+  mx = block_max(mx, red);
+  float s = 0.0f;
+  for (uint32_t i = threadIdx.x; i < a.K; i += ROW_THREADS) s += expf(ld_a(a.x, o + i, a.xdt) - mx);
+  s = block_sum(s, red);
+  float r = 1.0f / s;
+  for (uint32_t i = threadIdx.x; i < a.K; i += ROW_THREADS)
+    st_a(a.y, o + i, a.ydt, expf(ld_a(a.x, o + i, a.xdt) - mx) * r);
+}
+
+extern "C" int thvm_k_softmax(const ThvmSoftmaxArgs *a, hipStream_t s, char *err, int errlen) {
+  if (!act_dt(a->xdt) || !act_dt(a->ydt) || a->M == 0 || a->K == 0) {
+    snprintf(err, errlen, "softmax: bad args");
+    return -1;
+  }
+  hipLaunchKernelGGL(k_softmax, dim3(a->M), dim3(ROW_THREADS), 0, s, *a);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) { snprintf(err, errlen, "softmax launch: %s", hipGetErrorString(e)); return -1; }
+  return 0;
+}
+
+// ---- RoPE (in place) --------------------------------------------------------
+__global__ void k_rope(ThvmRopeArgs a) {
+  const uint32_t half = a.hd / 2;
+  const uint64_t n = (uint64_t)a.B * a.nh * half;
+  const uint64_t t = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= n) return;
+  const uint32_t j = (uint32_t)(t % half);
+  const uint64_t row = t / half;
+  const int32_t pos = a.len[0] - 1;
+  if (pos < 0 || (uint32_t)pos >= a.max_seq) return;
+  const float c = a.cos_t[(uint64_t)pos * half + j], sn = a.sin_t[(uint64_t)pos * half + j];
+  const uint64_t base = row * a.hd + 2 * j;
+  float xe = ld_a(a.x, base, a.dt), xo = ld_a(a.x, base + 1, a.dt);
+  st_a(a.x, base, a.dt, xe * c - xo * sn);
+  st_a(a.x, base + 1, a.dt, xo * c + xe * sn);
+}
+
+extern "C" int thvm_k_rope(const ThvmRopeArgs *a, hipStream_t s, char *err, int errlen) {
+  if (!act_dt(a->dt) || a->hd == 0 || a->hd % 2) { snprintf(err, errlen, "rope: bad args"); return -1; }
+  uint64_t n = (uint64_t)a->B * a->nh * (a->hd / 2);
+  if (n == 0) return 0;
+  hipLaunchKernelGGL(k_rope, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, *a);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) { snprintf(err, errlen, "rope launch: %s", hipGetErrorString(e)); return -1; }
+  return 0;
+}
+
+// ---- embedding --------------------------------------------------------------
+__global__ void k_embed(ThvmEmbedArgs a) {
+  const uint32_t b = blockIdx.y;
+  const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= a.D) return;
+  const int32_t t = a.tok[b];
+  float v = 0.0f;
+  if (t >= 0 && (uint32_t)t < a.V) v = ld_a(a.emb, (uint64_t)t * a.D + i, a.edt);
+  if (a.pos_emb) {
+    const int32_t p = a.len[0] - 1;
+    if (p >= 0 && (uint32_t)p < a.max_seq) v = v + ld_a(a.pos_emb, (uint64_t)p * a.D + i, a.edt);
+  }
+  st_a(a.x, (uint64_t)b * a.D + i, a.xdt, v);
+}
+
+extern "C" int thvm_k_embed(const ThvmEmbedArgs *a, hipStream_t s, char *err, int errlen) {
+  if (a->D == 0 || a->B == 0 || !act_dt(a->xdt) || !act_dt(a->edt) ||
+      (a->pos_emb && a->len == nullptr)) {
+    snprintf(err, errlen, "embed: bad args");
+    return -1;
+  }
+  hipLaunchKernelGGL(k_embed, dim3((a->D + 255) / 256, a->B), dim3(256), 0, s, *a);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) { snprintf(err, errlen, "embed launch: %s", hipGetErrorString(e)); return -1; }
+  return 0;
+}
+
+// ---- argmax -----------------------------------------------------------------
+__device__ __forceinline__ bool am_better(float v, int32_t i, float bv, int32_t bi) {
+  return v > bv || (v == bv && i < bi);
+}
+
+__global__ __launch_bounds__(256) void k_argmax_part(ThvmArgmaxArgs a) {
+  __shared__ float sv[256];
+  __shared__ int32_t si[256];
+  const uint32_t b = blockIdx.y, blk = blockIdx.x, t = threadIdx.x;
+  const uint32_t chunk = (a.V + a.nb - 1) / a.nb;
+  const uint64_t lo = (uint64_t)blk * chunk;
+  uint64_t hi = lo + chunk;
+  if (hi > a.V) hi = a.V;
+  const float *lg = a.logits + (uint64_t)b * a.V;
+  float bv = -INFINITY;
+  int32_t bi = 0x7fffffff;
+  for (uint64_t i = lo + t; i < hi; i += 256) {
+    float x = lg[i];
+    if (am_better(x, (int32_t)i, bv, bi)) { bv = x; bi = (int32_t)i; }
+  }
+  sv[t] = bv; si[t] = bi;
+  __syncthreads();
+  for (uint32_t st = 128; st > 0; st >>= 1) {
+    if (t < st && am_better(sv[t + st], si[t + st], sv[t], si[t])) {
+      sv[t] = sv[t + st]; si[t] = si[t + st];
+    }
+    __syncthreads();
+  }
+  if (t == 0) { a.pv[b * a.nb + blk] = sv[0]; a.pi[b * a.nb + blk] = si[0]; }
+}
+
+__global__ void k_argmax_fin(ThvmArgmaxArgs a) {
+  const uint32_t b = blockIdx.x;
+  if (threadIdx.x != 0) return;
+  float bv = a.pv[b * a.nb];
+  int32_t bi = a.pi[b * a.nb];
+  for (uint32_t k = 1; k < a.nb; k++) {
+    float v = a.pv[b * a.nb + k];
+    int32_t i = a.pi[b * a.nb + k];
+    if (am_better(v, i, bv, bi)) { bv = v; bi = i; }
+  }
+  a.tok[b] = bi;
+  if (a.hist) {
+    int32_t L = a.len[0];
+    if (L >= 0 && (uint32_t)L < a.hist_stride) a.hist[(uint64_t)b * a.hist_stride + L] = bi;
+  }
+}
+
+extern "C" int thvm_k_argmax(const ThvmArgmaxArgs *a, hipStream_t s, char *err, int errlen) {
+  if (a->B == 0 || a->V == 0 || a->nb == 0 || a->nb > a->V || (a->hist && !a->len)) {
+    snprintf(err, errlen, "argmax: bad args");
+    return -1;
+  }
+  hipLaunchKernelGGL(k_argmax_part, dim3(a->nb, a->B), dim3(256), 0, s, *a);
+  hipLaunchKernelGGL(k_argmax_fin, dim3(a->B), dim3(64), 0, s, *a);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) { snprintf(err, errlen, "argmax launch: %s", hipGetErrorString(e)); return -1; }
+  return 0;
+}
+
+__global__ void k_len_bump(int32_t *len, int32_t d) {
+  if (threadIdx.x == 0 && blockIdx.x == 0) len[0] = len[0] + d;
+}
+extern "C" int thvm_k_len_bump(int32_t *len, int32_t delta, hipStream_t s, char *err, int errlen) {
+  hipLaunchKernelGGL(k_len_bump, dim3(1), dim3(64), 0, s, len, delta);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) { snprintf(err, errlen, "len_bump launch: %s", hipGetErrorString(e)); return -1; }
+  return 0;
+}
+
+// ---- casts ------------------------------------------------------------------
+__global__ void k_cast(void *y, uint32_t ydt, const void *x, uint32_t xdt, uint64_t n) {
+  uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  st_a(y, i, ydt, ld_a(x, i, xdt));
+}
+extern "C" int thvm_k_cast(void *y, uint32_t ydt, const void *x, uint32_t xdt, uint64_t n,
+                           hipStream_t s, char *err, int errlen) {
+  bool okx = act_dt(xdt) || xdt == THVM_DT_FP8E4M3, oky = act_dt(ydt) || ydt == THVM_DT_FP8E4M3;
+  if (!okx || !oky) { snprintf(err, errlen, "cast: unsupported dtypes"); return -1; }
+  if (n == 0) return 0;
+  hipLaunchKernelGGL(k_cast, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, y, ydt, x, xdt, n);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) { snprintf(err, errlen, "cast launch: %s", hipGetErrorString(e)); return -1; }
+  return 0;
+}
+
+// ---- synthetic data ---------------------------------------------------------
+// splitmix64 finaliser over (seed, tag, counter): a counter-based generator,
+// so any element is reproducible alone.  Box-Muller on a pair of 24-bit
+// uniforms gives N(0, 1).
+__device__ __forceinline__ uint64_t mix64(uint64_t z) {
+  z += 0x9E3779B97F4A7C15ull;
+  z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+  z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+  return z ^ (z >> 31);
+}
+__device__ __forceinline__ float normal_at(uint64_t seed, uint64_t tag, uint64_t idx) {
+  uint64_t h = mix64(mix64(seed ^ mix64(tag)) + (idx >> 1));
+  float u1 = ((float)(uint32_t)(h >> 40) + 1.0f) * (1.0f / 16777216.0f);   // (0,1]
+  float u2 = (float)(uint32_t)(h & 0xffffffu) * (1.0f / 16777216.0f);      // [0,1)
+  float r = sqrtf(-2.0f * logf(u1));
+  float th = 6.283185307179586f * u2;
+  return r * ((idx & 1) ? sinf(th) : cosf(th));
+}
+
+__global__ void k_fill_normal(void *dst, uint32_t dt, uint64_t n, uint64_t seed, uint64_t tag,
+                              float mean, float std) {
+  uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
+  for (; i < n; i += stride) st_a(dst, i, dt, mean + std * normal_at(seed, tag, i));
+}
+extern "C" int thvm_k_fill_normal(void *dst, uint32_t dt, uint64_t n, uint64_t seed, uint64_t tag,
+                                  float mean, float std, hipStream_t s, char *err, int errlen) {
+  if (!act_dt(dt)) { snprintf(err, errlen, "fill_normal: unsupported dtype %u", dt); return -1; }
+  if (n == 0) return 0;
+  uint64_t blocks = (n + 255) / 256;
+  if (blocks > 65536) blocks = 65536;
+  hipLaunchKernelGGL(k_fill_normal, dim3((unsigned)blocks), dim3(256), 0, s, dst, dt, n, seed, tag,
+                     mean, std);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) { snprintf(err, errlen, "fill launch: %s", hipGetErrorString(e)); return -1; }
+  return 0;
+}
+
+__global__ __launch_bounds__(256) void k_fill_fp8_rows(uint8_t *q, float *scale, uint32_t rows,
+                                                       uint32_t cols, uint64_t seed, uint64_t tag,
+                                                       float std) {
+  __shared__ float red[4];
+  for (uint32_t r = blockIdx.x; r < rows; r += gridDim.x) {
+    const uint64_t base = (uint64_t)r * cols;
+    float mx = 0.0f;
+    for (uint32_t c = threadIdx.x; c < cols; c += 256)
+      mx = fmaxf(mx, fabsf(std * normal_at(seed, tag, base + c)));
+    // block max
+    float w = wave_max(mx);
+    __syncthreads();
+    if (lane_id() == 0) red[threadIdx.x >> 6] = w;
+    __syncthreads();
+    float am = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    float sc = am > 0.0f ? am / 448.0f : 1.0f;
+    if (threadIdx.x == 0) scale[r] = sc;
+    for (uint32_t c = threadIdx.x; c < cols; c += 256)
+      q[base + c] = f2fp8_sat((std * normal_at(seed, tag, base + c)) / sc);
+    __syncthreads();
+  }
+}
+extern "C" int thvm_k_fill_fp8_rows(uint8_t *q, float *scale, uint32_t rows, uint32_t cols,
+                                    uint64_t seed, uint64_t tag, float std, hipStream_t s,
+                                    char *err, int errlen) {
+  if (rows == 0 || cols == 0) return 0;
+  uint32_t blocks = rows < 8192 ? rows : 8192;
+  hipLaunchKernelGGL(k_fill_fp8_rows, dim3(blocks), dim3(256), 0, s, q, scale, rows, cols, seed,
+                     tag, std);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) { snprintf(err, errlen, "fill_fp8 launch: %s", hipGetErrorString(e)); return -1; }
+  return 0;
+}
+
+__global__ void k_fill_cache(void *cache, uint32_t dt, uint32_t B, uint32_t Hkv, uint32_t max_seq,
+                             uint32_t hd, uint32_t ctx, uint64_t seed, uint64_t tag) {
+  // element (b, h, p, d) with p < ctx; the counter is the flat cache index
+  const uint64_t n = (uint64_t)B * Hkv * ctx * hd;
+  const uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
+  for (uint64_t t = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; t < n; t += stride) {
+    uint32_t d = (uint32_t)(t % hd);
+    uint64_t r = t / hd;
+    uint32_t p = (uint32_t)(r % ctx);
+    uint64_t bh = r / ctx;
+    uint64_t idx = (bh * max_seq + p) * hd + d;
+    st_a(cache, idx, dt, normal_at(seed, tag, idx));
+  }
+}
+extern "C" int thvm_k_fill_cache(void *cache, uint32_t dt, uint32_t B, uint32_t Hkv,
+                                 uint32_t max_seq, uint32_t hd, uint32_t ctx, uint64_t seed,
+                                 uint64_t tag, hipStream_t s, char *err, int errlen) {
+  if (!act_dt(dt) || ctx > max_seq) { snprintf(err, errlen, "fill_cache: bad args"); return -1; }
+  uint64_t n = (uint64_t)B * Hkv * ctx * hd;
+  if (n == 0) return 0;
+  uint64_t blocks = (n + 255) / 256;
+  if (blocks > 65536) blocks = 65536;
+  hipLaunchKernelGGL(k_fill_cache, dim3((unsigned)blocks), dim3(256), 0, s, cache, dt, B, Hkv,
+                     max_seq, hd, ctx, seed, tag);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) { snprintf(err, errlen, "fill_cache launch: %s", hipGetErrorString(e)); return -1; }
+  return 0;
+}
