@@ -175,13 +175,13 @@ def test_gemv_qkv_rope_epilogue(hip):
     hip.builtin("gemv", [q, up(hip, xs), up(hip, ws), up(hip, scale), up(hip, cs), up(hip, sn), L,
                          kc, vc], m=1, n=N, k=D, wt=DT_FP8, xt=DT_BF16, yt=DT_BF16, epi=4, h=H,
                 hkv=Hkv, hd=hd, maxseq=ms)
-    v = _rb(ref[0])
+    v = _rb(ref[0]).astype(np.float32)
     c, s = cs[pos], sn[pos]
     ro = v.copy()
     for n in range(0, (H + Hkv) * hd, 2):
         j = (n % hd) // 2
-        ro[n] = _rb(v[n] * c[j] - v[n + 1] * s[j])
-        ro[n + 1] = _rb(v[n + 1] * c[j] + v[n] * s[j])
+        ro[n:n + 2] = _rb(np.array([v[n] * c[j] - v[n + 1] * s[j],
+                                    v[n + 1] * c[j] + v[n] * s[j]], np.float32))
     gq = O.decode(q.read(np.uint16), DT_BF16)
     gk = O.decode(kc.read(np.uint16), DT_BF16).reshape(Hkv, ms, hd)[:, pos].ravel()
     gv = O.decode(vc.read(np.uint16), DT_BF16).reshape(Hkv, ms, hd)[:, pos].ravel()
@@ -256,29 +256,33 @@ def test_rope(hip):
     assert np.array_equal(xb.read(np.uint16), want.ravel())
 
 
+@pytest.mark.parametrize("cdt", [DT_BF16, DT_F32])
 @pytest.mark.parametrize("H,Hkv,hd", [(8, 2, 128), (4, 4, 64), (32, 8, 128), (8, 1, 64)])
 @pytest.mark.parametrize("L", [1, 63, 64, 65, 200])
-def test_attention_decode(hip, H, Hkv, hd, L):
+def test_attention_decode(hip, H, Hkv, hd, L, cdt):
     B, ms = 2, 256
-    say(f"case: attn H={H} Hkv={Hkv} hd={hd} L={L}")
+    say(f"case: attn H={H} Hkv={Hkv} hd={hd} L={L} cache dt={cdt}")
     rng = np.random.default_rng(H * 1000 + L)
-    qs, qf = rand_store(rng, (B, H, hd), DT_BF16)
-    ks, _ = rand_store(rng, (B, Hkv, ms, hd), DT_BF16)
-    vs, _ = rand_store(rng, (B, Hkv, ms, hd), DT_BF16)
+    qs, qf = rand_store(rng, (B, H, hd), cdt)
+    ks, _ = rand_store(rng, (B, Hkv, ms, hd), cdt)
+    vs, _ = rand_store(rng, (B, Hkv, ms, hd), cdt)
     nsplit = (ms + 63) // 64
-    out = hip.Buffer(B * H * hd * 2)
+    out = hip.Buffer(B * H * hd * SZ[cdt])
     part = hip.Buffer(B * H * nsplit * (hd + 2) * 4)
     scale = float(np.float32(1.0 / np.sqrt(hd)))
     hip.builtin("attn", [out, up(hip, qs), up(hip, ks), up(hip, vs),
                          up(hip, np.array([L], np.int32)), part],
-                b=B, h=H, hkv=Hkv, hd=hd, maxseq=ms, chunk=64, nsplit=nsplit, qt=DT_BF16,
-                ct=DT_BF16, ot=DT_BF16, scale=scale)
-    want = np.empty(B * H * hd, np.uint16)
-    O.oracle().or_attn_decode(want.ctypes.data, DT_BF16, qs.ctypes.data, DT_BF16, ks.ctypes.data,
-                              vs.ctypes.data, DT_BF16, B, H, Hkv, hd, ms, L, scale)
-    got = O.decode(out.read(np.uint16), DT_BF16)
-    ww = O.decode(want, DT_BF16)
-    assert np.all(np.abs(got - ww) <= 2.0 ** -7 * np.abs(ww) + 2e-3), np.max(np.abs(got - ww))
+                b=B, h=H, hkv=Hkv, hd=hd, maxseq=ms, chunk=64, nsplit=nsplit, qt=cdt,
+                ct=cdt, ot=cdt, scale=scale)
+    want = np.empty(B * H * hd, NP_STORE[cdt])
+    O.oracle().or_attn_decode(want.ctypes.data, cdt, qs.ctypes.data, cdt, ks.ctypes.data,
+                              vs.ctypes.data, cdt, B, H, Hkv, hd, ms, L, scale)
+    got = O.decode(out.read(NP_STORE[cdt]), cdt)
+    ww = O.decode(want, cdt)
+    if cdt == DT_F32:   # f32: 1e-5 relative to the magnitude of the V rows mixed
+        assert np.all(np.abs(got - ww) <= 1e-5 * (np.abs(ww) + 1.0)), np.max(np.abs(got - ww))
+    else:
+        assert np.all(np.abs(got - ww) <= 2.0 ** -7 * np.abs(ww) + 2e-3), np.max(np.abs(got - ww))
 
 
 def test_argmax_ties_lowest_index(hip):

@@ -166,8 +166,12 @@ int hb_builtin_launch(const char *program, const u32 *ids, u32 n, int check_only
          spec_u32(&sp, "epi", &a.epi, 0, THVM_EPI_STORE) || spec_u32(&sp, "bias", &bias, 0, 0) ||
          spec_u32(&sp, "h", &a.n_heads, 0, 0) || spec_u32(&sp, "hkv", &a.n_kv_heads, 0, 0) ||
          spec_u32(&sp, "hd", &a.head_dim, 0, 0) || spec_u32(&sp, "maxseq", &a.max_seq, 0, 0));
-    NEED(spec_u32(&sp, "ldx", &a.ldx, 0, a.K) ||
-         spec_u32(&sp, "ldy", &a.ldy, 0, a.epi == THVM_EPI_SWIGLU ? a.N / 2 : a.N));
+    {
+      u32 ldy0 = a.epi == THVM_EPI_SWIGLU ? a.N / 2
+               : (a.epi == THVM_EPI_QKV || a.epi == THVM_EPI_QKV_ROPE) ? a.n_heads * a.head_dim
+               : a.N;
+      NEED(spec_u32(&sp, "ldx", &a.ldx, 0, a.K) || spec_u32(&sp, "ldy", &a.ldy, 0, ldy0));
+    }
     u32 wsz = hb_dt_size(a.wdt), xsz = hb_dt_size(a.xdt), ysz = hb_dt_size(a.ydt);
     if (!wsz || !is_act(a.xdt) || !is_act(a.ydt) || a.M == 0) {
       hb_set_error("builtin gemv: bad dtypes/shape");

@@ -34,37 +34,46 @@ __device__ __forceinline__ float ldq(const void *p, uint64_t i, uint32_t dt) {
        : ((const float *)p)[i];
 }
 
-// 8 consecutive 16-bit cache elements (one 16-byte chunk) -> floats
-__device__ __forceinline__ void chunk8(const uint4 &q, uint32_t dt, float o[8]) {
+// one 16-byte chunk of cache elements -> floats (ES = element bytes: 2 or 4)
+template <int ES>
+__device__ __forceinline__ void chunk_f(const uint4 &q, uint32_t dt, float *o) {
   uint32_t w[4] = {q.x, q.y, q.z, q.w};
+  if (ES == 4) {
 #pragma unroll
-  for (int i = 0; i < 4; i++) {
-    if (dt == THVM_DT_BF16) {
-      o[2 * i] = __uint_as_float(w[i] << 16);
-      o[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
-    } else {
-      o[2 * i] = h2f((f16_t)(w[i] & 0xffffu));
-      o[2 * i + 1] = h2f((f16_t)(w[i] >> 16));
+    for (int i = 0; i < 4; i++) o[i] = __uint_as_float(w[i]);
+  } else {
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      if (dt == THVM_DT_BF16) {
+        o[2 * i] = __uint_as_float(w[i] << 16);
+        o[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
+      } else {
+        o[2 * i] = h2f((f16_t)(w[i] & 0xffffu));
+        o[2 * i + 1] = h2f((f16_t)(w[i] >> 16));
+      }
     }
   }
 }
 
-// sum over the LPR lanes of a row group (LPR in {8, 16}); all lanes get it
+// sum over the LPR lanes of a row group (LPR in {8, 16, 32}); all lanes get it
 template <int LPR>
 __device__ __forceinline__ float group_sum(float v) {
   v += dpp_f<0xB1>(v);
   v += dpp_f<0x4E>(v);
   v += dpp_f<0x141>(v);
-  if (LPR == 16) v += dpp_f<0x140>(v);
+  if (LPR >= 16) v += dpp_f<0x140>(v);
+  if (LPR == 32) v += __shfl_xor(v, 16);
   return v;
 }
 
-template <int HD, int G>
+template <int HD, int G, int ES>
 __global__ __launch_bounds__(ATT_THREADS) void k_attn_split(ThvmAttnArgs a) {
-  constexpr int LPR = HD / 8;            // lanes per cache row
+  constexpr int EPL = 16 / ES;           // elements per lane chunk
+  constexpr int LPR = HD / EPL;          // lanes per cache row
   constexpr int RPW = 64 / LPR;          // rows per wave-wide load
   constexpr int PPW = ATT_CHUNK / ATT_WAVES;
   constexpr int IT = PPW / RPW;          // loads per wave
+  static_assert(LPR >= 8 && LPR <= 32 && IT >= 1, "attention geometry");
   __shared__ float wm[ATT_WAVES][G], wl[ATT_WAVES][G];
   __shared__ float wacc[ATT_WAVES][G][HD];
 
@@ -75,8 +84,9 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attn_split(ThvmAttnArgs a) {
 
   const int lane = lane_id(), wv = threadIdx.x >> 6;
   const int rg = lane / LPR, li = lane % LPR;
-  const uint32_t d0 = li * 8;
+  const uint32_t d0 = li * EPL;
   const uint64_t cbase = ((uint64_t)b * a.Hkv + kvh) * a.max_seq;
+  const char *kb = (const char *)a.kcache, *vb = (const char *)a.vcache;
 
   // issue every K/V load of this wave first
   uint4 kq[IT], vq[IT];
@@ -85,29 +95,29 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attn_split(ThvmAttnArgs a) {
   for (int it = 0; it < IT; it++) {
     uint32_t j = p0 + wv * PPW + it * RPW + rg;
     ok[it] = (int32_t)j < L && j < a.max_seq;
-    uint64_t off = (cbase + (ok[it] ? j : 0)) * HD + d0;
-    kq[it] = ld_stream16((const uint16_t *)a.kcache + off);
-    vq[it] = ld_stream16((const uint16_t *)a.vcache + off);
+    uint64_t off = ((cbase + (ok[it] ? j : 0)) * HD + d0) * ES;
+    kq[it] = ld_stream16(kb + off);
+    vq[it] = ld_stream16(vb + off);
   }
-  // query fragment: G heads x 8 dims
-  float qf[G][8];
+  // query fragment: G heads x EPL dims
+  float qf[G][EPL];
 #pragma unroll
   for (int g = 0; g < G; g++) {
     uint64_t qo = ((uint64_t)b * a.H + kvh * G + g) * HD + d0;
 #pragma unroll
-    for (int i = 0; i < 8; i++) qf[g][i] = ldq(a.q, qo + i, a.qdt);
+    for (int i = 0; i < EPL; i++) qf[g][i] = ldq(a.q, qo + i, a.qdt);
   }
 
   float sc[IT][G];
 #pragma unroll
   for (int it = 0; it < IT; it++) {
-    float kf[8];
-    chunk8(kq[it], a.cdt, kf);
+    float kf[EPL];
+    chunk_f<ES>(kq[it], a.cdt, kf);
 #pragma unroll
     for (int g = 0; g < G; g++) {
       float s = 0.0f;
 #pragma unroll
-      for (int i = 0; i < 8; i++) s += qf[g][i] * kf[i];
+      for (int i = 0; i < EPL; i++) s += qf[g][i] * kf[i];
       s = group_sum<LPR>(s) * a.scale;
       sc[it][g] = ok[it] ? s : -INFINITY;
     }
@@ -122,23 +132,23 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attn_split(ThvmAttnArgs a) {
     for (int off = LPR; off < 64; off *= 2) m = fmaxf(m, __shfl_xor(m, off));
     mw[g] = m;
   }
-  float acc[G][8];
+  float acc[G][EPL];
 #pragma unroll
   for (int g = 0; g < G; g++) {
     lw[g] = 0.0f;
 #pragma unroll
-    for (int i = 0; i < 8; i++) acc[g][i] = 0.0f;
+    for (int i = 0; i < EPL; i++) acc[g][i] = 0.0f;
   }
 #pragma unroll
   for (int it = 0; it < IT; it++) {
-    float vf[8];
-    chunk8(vq[it], a.cdt, vf);
+    float vf[EPL];
+    chunk_f<ES>(vq[it], a.cdt, vf);
 #pragma unroll
     for (int g = 0; g < G; g++) {
       float p = (ok[it] && mw[g] != -INFINITY) ? expf(sc[it][g] - mw[g]) : 0.0f;
       lw[g] += p;
 #pragma unroll
-      for (int i = 0; i < 8; i++) acc[g][i] += p * vf[i];
+      for (int i = 0; i < EPL; i++) acc[g][i] += p * vf[i];
     }
   }
   // combine the row groups of the wave (lanes li, li+LPR, ...)
@@ -148,14 +158,14 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attn_split(ThvmAttnArgs a) {
     for (int off = LPR; off < 64; off *= 2) {
       lw[g] += __shfl_xor(lw[g], off);
 #pragma unroll
-      for (int i = 0; i < 8; i++) acc[g][i] += __shfl_xor(acc[g][i], off);
+      for (int i = 0; i < EPL; i++) acc[g][i] += __shfl_xor(acc[g][i], off);
     }
   }
   if (rg == 0) {
 #pragma unroll
     for (int g = 0; g < G; g++) {
 #pragma unroll
-      for (int i = 0; i < 8; i++) wacc[wv][g][d0 + i] = acc[g][i];
+      for (int i = 0; i < EPL; i++) wacc[wv][g][d0 + i] = acc[g][i];
       if (li == 0) { wm[wv][g] = mw[g]; wl[wv][g] = lw[g]; }
     }
   }
@@ -204,13 +214,13 @@ __global__ void k_attn_combine(ThvmAttnArgs a) {
 }
 
 typedef void (*attn_fn)(ThvmAttnArgs);
-template <int HD>
+template <int HD, int ES>
 static attn_fn attn_pick(uint32_t G) {
   switch (G) {
-    case 1: return k_attn_split<HD, 1>;
-    case 2: return k_attn_split<HD, 2>;
-    case 4: return k_attn_split<HD, 4>;
-    case 8: return k_attn_split<HD, 8>;
+    case 1: return k_attn_split<HD, 1, ES>;
+    case 2: return k_attn_split<HD, 2, ES>;
+    case 4: return k_attn_split<HD, 4, ES>;
+    case 8: return k_attn_split<HD, 8, ES>;
     default: return nullptr;
   }
 }
@@ -224,8 +234,8 @@ extern "C" int thvm_k_attn_decode(const ThvmAttnArgs *a, hipStream_t s, char *er
     snprintf(err, errlen, "attn: bad head geometry H=%u Hkv=%u", a->H, a->Hkv);
     return -1;
   }
-  if (a->cdt != THVM_DT_BF16 && a->cdt != THVM_DT_FP16) {
-    snprintf(err, errlen, "attn: cache dtype must be bf16/fp16");
+  if (a->cdt != THVM_DT_BF16 && a->cdt != THVM_DT_FP16 && a->cdt != THVM_DT_FP32) {
+    snprintf(err, errlen, "attn: cache dtype must be bf16/fp16/f32");
     return -1;
   }
   if (a->chunk != ATT_CHUNK || a->n_split * ATT_CHUNK < a->max_seq) {
@@ -234,8 +244,9 @@ extern "C" int thvm_k_attn_decode(const ThvmAttnArgs *a, hipStream_t s, char *er
   }
   attn_fn f = nullptr;
   uint32_t G = a->H / a->Hkv;
-  if (a->hd == 128) f = attn_pick<128>(G);
-  else if (a->hd == 64) f = attn_pick<64>(G);
+  const bool f32 = a->cdt == THVM_DT_FP32;
+  if (a->hd == 128) f = f32 ? attn_pick<128, 4>(G) : attn_pick<128, 2>(G);
+  else if (a->hd == 64) f = f32 ? attn_pick<64, 4>(G) : attn_pick<64, 2>(G);
   if (!f) {
     snprintf(err, errlen, "attn: no kernel for hd=%u G=%u", a->hd, G);
     return -1;
