@@ -85,20 +85,22 @@ def cpu_baseline(thvm, dec, cfg, n_steps: int):
     om = O.OracleModel(dec, dict(cfg))
     log(f"[bench] cpu baseline: read back {sum(a.nbytes for a in om.keep) / 1e9:.2f} GB of "
         f"weights + {sum(a.nbytes for a in om.caches) / 1e9:.2f} GB KV in {time.time() - t_read:.1f}s")
-    o_ids, t_cpu = [], 0.0
+    t_cpu, errs, match = 0.0, [], True
     cur = tok
     for s in range(n_steps):
         t0 = time.perf_counter()
-        _, nx = om.step(cur, pos + s)
+        olg, onx = om.step(cur, pos + s)
         t_cpu += time.perf_counter() - t0
-        o_ids.append(nx.copy())
-        cur = nx
-        log(f"[bench] cpu oracle step {s}: {t_cpu:.1f}s cumulative")
-    dec.replay(n_steps)
-    g = dec.tokens(pos + n_steps + 1)[:, pos + 1:pos + n_steps + 1]
-    match = bool(np.array_equal(np.stack(o_ids, 1), g))
+        dec.replay(1)                              # the same step on the device
+        glg = dec.logits()
+        gnx = dec.tokens(pos + s + 2)[:, pos + s + 1]
+        errs.append(float(np.abs(glg - olg).max() / np.abs(olg).max()))
+        match = match and bool(np.array_equal(gnx, onx))
+        log(f"[bench] cpu oracle step {s}: {t_cpu:.1f}s cumulative, logits rel err {errs[-1]:.2e}, "
+            f"ids gpu={gnx.tolist()} oracle={onx.tolist()}")
+        cur = gnx.astype(np.int32)                 # lockstep on the device's token
     tps = cfg["batch"] * n_steps / t_cpu
-    return tps, match, t_cpu
+    return tps, match, t_cpu, max(errs)
 
 
 def main() -> int:
@@ -165,13 +167,14 @@ def main() -> int:
 
     cpu = None
     if not args.no_cpu:
-        tps_cpu, match, secs = cpu_baseline(thvm, dec, cfg, args.cpu_steps)
+        tps_cpu, match, secs, lerr = cpu_baseline(thvm, dec, cfg, args.cpu_steps)
         cpu = {"value": round(tps_cpu, 4), "unit": "tokens/s", "cores": 1, "kind": "port",
                "sample": f"{args.cpu_steps} greedy decode steps of the same C4 model at context "
                          f"~{dec.position - args.cpu_steps}, oracle/oracle.c or_decode_step on one "
-                         f"core of {cpu_model_name()} ({os.cpu_count()} visible); "
-                         f"ids equal to the device's: {match}",
-               "seconds": round(secs, 2), "ids_match": match}
+                         f"core of {cpu_model_name()} ({os.cpu_count()} visible), in lockstep with "
+                         f"the device on the same inputs",
+               "seconds": round(secs, 2), "ids_match": match,
+               "logits_max_rel_err": lerr}
 
     out = {
         "metric": METRIC, "value": round(tps, 2), "unit": "tokens/s", "n_gpus": 1,

@@ -192,6 +192,58 @@ def test_gemv_qkv_rope_epilogue(hip):
     assert not np.any(kc.read(np.uint16).reshape(Hkv, ms, hd)[:, pos + 1:])
 
 
+@pytest.mark.parametrize("kind", [1, 2])
+@pytest.mark.parametrize("wdt,xdt", [(DT_FP8, DT_BF16), (DT_F16, DT_F16), (DT_F32, DT_F32)])
+def test_gemv_fused_norm(hip, kind, wdt, xdt):
+    """GEMV with the RMSNorm (1) / LayerNorm (2) prologue == norm kernel
+    semantics (oracle or_rmsnorm / or_layernorm, output rounded to x's dtype)
+    followed by the GEMV."""
+    M, N, K = 2, 192, 1600
+    say(f"case: gemv fused norm kind={kind} wdt={wdt} xdt={xdt}")
+    rng = np.random.default_rng(40 + kind + wdt)
+    xs, xf = rand_store(rng, (M, K), xdt)
+    g = (1 + 0.1 * rng.standard_normal(K)).astype(np.float32)
+    b = (0.1 * rng.standard_normal(K)).astype(np.float32)
+    xn = np.empty((M, K), NP_STORE[xdt])
+    if kind == 1:
+        O.oracle().or_rmsnorm(xn.ctypes.data, xdt, xs.ctypes.data, xdt, g.ctypes.data, M, K, 1e-5)
+    else:
+        O.oracle().or_layernorm(xn.ctypes.data, xdt, xs.ctypes.data, xdt, g.ctypes.data,
+                                b.ctypes.data, M, K, 1e-5)
+    xnf = O.decode(xn, xdt)
+    if wdt == DT_FP8:
+        wf32 = (rng.standard_normal((N, K)) * 0.02).astype(np.float32)
+        scale = (np.abs(wf32).max(1) / 448.0).astype(np.float32)
+        ws = O.encode(wf32 / scale[:, None], DT_FP8)
+        wdq = O.decode(ws, DT_FP8) * scale[:, None]
+    else:
+        ws, wdq = rand_store(rng, (N, K), wdt, 0.02)
+        scale = None
+    ref = O.gemv(xn, xdt, ws, wdt, scale, M=M, N=N, K=K)
+    floor = np.abs(xnf) @ np.abs(wdq).T
+    y = hip.Buffer(M * N * 4)
+    args = [y, up(hip, xs), up(hip, ws)] + ([up(hip, scale)] if scale is not None else [])
+    args += [up(hip, g)] + ([up(hip, b)] if kind == 2 else [])
+    hip.builtin("gemv", args, m=M, n=N, k=K, wt=wdt, xt=xdt, yt=DT_F32, epi=0, norm=kind, eps=1e-5)
+    got = y.read(np.float32).reshape(M, N)
+    # the norm's own rounding may differ by one storage ulp per element
+    ulp = 1e-5 if xdt == DT_F32 else 2.0 ** -7
+    assert np.all(np.abs(got - ref) <= (1e-5 + ulp) * floor + 1e-6), np.max(np.abs(got - ref) / floor)
+
+
+@pytest.mark.parametrize("waves,r,u", [(1, 1, 4), (2, 2, 8), (8, 1, 8), (16, 2, 4)])
+def test_gemv_tuning_knobs_agree(hip, waves, r, u):
+    M, N, K = 1, 512, 4096
+    say(f"case: gemv tuning waves={waves} r={r} u={u}")
+    rng = np.random.default_rng(77)
+    xs, ws, scale, ref, floor = _gemv_case(hip, rng, DT_FP8, M, N, K)
+    y = hip.Buffer(M * N * 4)
+    hip.builtin("gemv", [y, up(hip, xs), up(hip, ws), up(hip, scale)], m=M, n=N, k=K, wt=DT_FP8,
+                xt=DT_BF16, yt=DT_F32, epi=0, waves=waves, r=r, u=u, blocks=7)
+    got = y.read(np.float32).reshape(M, N)
+    assert np.all(np.abs(got - ref) <= 1e-5 * floor)
+
+
 def test_gemv_rejects_bad_shapes(hip):
     say("case: gemv argument validation (host-side errors, no launch)")
     y, x, w = hip.Buffer(64), hip.Buffer(64), hip.Buffer(64)
@@ -268,7 +320,7 @@ def test_attention_decode(hip, H, Hkv, hd, L, cdt):
     vs, _ = rand_store(rng, (B, Hkv, ms, hd), cdt)
     nsplit = (ms + 63) // 64
     out = hip.Buffer(B * H * hd * SZ[cdt])
-    part = hip.Buffer(B * H * nsplit * (hd + 2) * 4)
+    part = hip.Buffer(B * H * nsplit * (hd + 2) * 4 + B * Hkv * 4)
     scale = float(np.float32(1.0 / np.sqrt(hd)))
     hip.builtin("attn", [out, up(hip, qs), up(hip, ks), up(hip, vs),
                          up(hip, np.array([L], np.int32)), part],

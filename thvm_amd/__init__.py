@@ -208,8 +208,10 @@ class Jit:
             raise ThvmHipError(f"jit_capture_begin: {last_error()}")
         return self
 
-    def __exit__(self, *exc):
+    def __exit__(self, exc_type, exc, tb):
         lib().thvm_hip_jit_capture_end()
+        if exc_type is not None:      # a failed capture leaves no slot behind
+            self.drop()
         return False
 
     def op_count(self) -> int:

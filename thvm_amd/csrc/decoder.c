@@ -261,7 +261,7 @@ static int build_state(Decoder *d) {
       !tens_new(d, "q", adt, (u64)B * hq * as) || !tens_new(d, "att", adt, (u64)B * hq * as) ||
       !tens_new(d, "h", adt, (u64)B * c->ffn * as) ||
       !tens_new(d, "attn.part", THVM_DT_FP32,
-                thvm_k_attn_part_bytes(B, c->n_heads, c->head_dim, d->n_split)))
+                thvm_k_attn_part_bytes(B, c->n_heads, c->n_kv_heads, c->head_dim, d->n_split)))
     return -1;
   for (u32 l = 0; l < c->n_layers; l++) {
     char kn[32], vn[32];
@@ -287,19 +287,52 @@ static int op_attn(Decoder *d, u32 l) {
   return op_add(d, "attn", p, a, 6);
 }
 
-static int op_tail(Decoder *d, u32 lm_w, u32 lm_s) {
+/* The norm feeding a GEMV: fused into the GEMV's x staging (default), or as
+ * a separate norm kernel writing xn (THVM_HIP_UNFUSED_NORM=1, for A/B).
+ * Writes the GEMV's input id to *gin and its norm spec fragment to nspec;
+ * gains are appended to the GEMV's argument list by the caller via gargs. */
+typedef struct { int kind; u32 g, b; } NormSpec;
+
+static int fused_norms(void) {
+  const char *e = getenv("THVM_HIP_UNFUSED_NORM");
+  return !(e && e[0] == '1');
+}
+
+static int emit_norm(Decoder *d, const NormSpec *ns, u32 *gin, char *nspec, size_t nlen,
+                     u32 *gargs, u32 *ng) {
   const ThvmDecodeConfig *c = &d->c;
-  char p[320];
+  u32 x = tens_find(d, "x"), xn = tens_find(d, "xn");
+  *ng = 0;
+  if (fused_norms()) {
+    snprintf(nspec, nlen, " norm=%d eps=%a", ns->kind, c->eps);
+    gargs[(*ng)++] = ns->g;
+    if (ns->kind == 2) gargs[(*ng)++] = ns->b;
+    *gin = x;
+    return 0;
+  }
+  char p[200];
+  nspec[0] = 0;
+  snprintf(p, sizeof p, "thvm-builtin:norm m=%u k=%u xt=%u yt=%u eps=%a ln=%d bias=%d", c->batch,
+           c->dim, c->adtype, c->adtype, c->eps, ns->kind == 2, ns->kind == 2);
+  u32 a[4] = {xn, x, ns->g, ns->b};
+  *gin = xn;
+  return op_add(d, "norm", p, a, ns->kind == 2 ? 4 : 3);
+}
+
+static int op_tail(Decoder *d, u32 lm_w, u32 lm_s, const NormSpec *fn) {
+  const ThvmDecodeConfig *c = &d->c;
+  char p[400], nsp[96];
+  u32 gin, gargs[2], ng;
+  if (emit_norm(d, fn, &gin, nsp, sizeof nsp, gargs, &ng)) return -1;
   /* LM head -> f32 logits */
-  if (lm_s)
-    snprintf(p, sizeof p, "thvm-builtin:gemv m=%u n=%u k=%u wt=%u xt=%u yt=%u epi=0",
-             c->batch, c->vocab, c->dim, c->wdtype, c->adtype, THVM_DT_FP32);
-  else
-    snprintf(p, sizeof p, "thvm-builtin:gemv m=%u n=%u k=%u wt=%u xt=%u yt=%u epi=0",
-             c->batch, c->vocab, c->dim, c->arch == THVM_ARCH_GPT2 ? c->adtype : c->wdtype,
-             c->adtype, THVM_DT_FP32);
-  u32 a[4] = {tens_find(d, "logits"), tens_find(d, "xn"), lm_w, lm_s};
-  if (op_add(d, "lm_head", p, a, lm_s ? 4 : 3)) return -1;
+  snprintf(p, sizeof p, "thvm-builtin:gemv m=%u n=%u k=%u wt=%u xt=%u yt=%u epi=0%s",
+           c->batch, c->vocab, c->dim, c->arch == THVM_ARCH_GPT2 ? c->adtype : c->wdtype,
+           c->adtype, THVM_DT_FP32, nsp);
+  u32 a[8], n = 0;
+  a[n++] = tens_find(d, "logits"); a[n++] = gin; a[n++] = lm_w;
+  if (lm_s) a[n++] = lm_s;
+  for (u32 i = 0; i < ng; i++) a[n++] = gargs[i];
+  if (op_add(d, "lm_head", p, a, n)) return -1;
   u32 nb = c->vocab >= 256 * 64 ? 256 : (c->vocab + 63) / 64;
   snprintf(p, sizeof p, "thvm-builtin:argmax b=%u v=%u nb=%u hist=1 hstride=%u", c->batch,
            c->vocab, nb, c->max_seq + 1);
@@ -320,7 +353,7 @@ static int build_llama(Decoder *d) {
   if (rope_tables(d)) return -1;
   if (!weight_const(d, "norm_f", D, 1.0f)) return -1;
   char p[400], nm[48];
-  u32 x = tens_find(d, "x"), xn = tens_find(d, "xn"), q = tens_find(d, "q"),
+  u32 x = tens_find(d, "x"), q = tens_find(d, "q"),
       att = tens_find(d, "att"), hb = tens_find(d, "h"), L = tens_find(d, "len");
 
   snprintf(p, sizeof p, "thvm-builtin:embed b=%u d=%u v=%u et=%u xt=%u", B, D, c->vocab, adt, adt);
@@ -348,16 +381,17 @@ static int build_llama(Decoder *d) {
     u32 kc = tens_find(d, kn), vc = tens_find(d, vn);
     int f8 = c->wdtype == THVM_DT_FP8E4M3;
 
-    snprintf(p, sizeof p, "thvm-builtin:norm m=%u k=%u xt=%u yt=%u eps=%a", B, D, adt, adt, c->eps);
-    u32 n1[3] = {xn, x, ga};
-    if (op_add(d, "norm", p, n1, 3)) return -1;
-
+    char nsp[96];
+    u32 gin, gargs[2], ng;
+    NormSpec n1 = {1, ga, 0};
+    if (emit_norm(d, &n1, &gin, nsp, sizeof nsp, gargs, &ng)) return -1;
     snprintf(p, sizeof p,
-             "thvm-builtin:gemv m=%u n=%u k=%u wt=%u xt=%u yt=%u epi=%u h=%u hkv=%u hd=%u maxseq=%u",
-             B, nqkv, D, c->wdtype, adt, adt, THVM_EPI_QKV_ROPE, H, Hkv, hd, c->max_seq);
-    u32 qa[10], qn = 0;
-    qa[qn++] = q; qa[qn++] = xn; qa[qn++] = wqkv;
+             "thvm-builtin:gemv m=%u n=%u k=%u wt=%u xt=%u yt=%u epi=%u h=%u hkv=%u hd=%u maxseq=%u%s",
+             B, nqkv, D, c->wdtype, adt, adt, THVM_EPI_QKV_ROPE, H, Hkv, hd, c->max_seq, nsp);
+    u32 qa[12], qn = 0;
+    qa[qn++] = q; qa[qn++] = gin; qa[qn++] = wqkv;
     if (f8) qa[qn++] = sqkv;
+    for (u32 i = 0; i < ng; i++) qa[qn++] = gargs[i];
     qa[qn++] = tens_find(d, "rope.cos"); qa[qn++] = tens_find(d, "rope.sin");
     qa[qn++] = L; qa[qn++] = kc; qa[qn++] = vc;
     if (op_add(d, "gemv_qkv", p, qa, qn)) return -1;
@@ -372,15 +406,14 @@ static int build_llama(Decoder *d) {
     oa[on++] = x;
     if (op_add(d, "gemv_o", p, oa, on)) return -1;
 
-    snprintf(p, sizeof p, "thvm-builtin:norm m=%u k=%u xt=%u yt=%u eps=%a", B, D, adt, adt, c->eps);
-    u32 n2[3] = {xn, x, gf};
-    if (op_add(d, "norm", p, n2, 3)) return -1;
-
-    snprintf(p, sizeof p, "thvm-builtin:gemv m=%u n=%u k=%u wt=%u xt=%u yt=%u epi=%u", B, 2 * F, D,
-             c->wdtype, adt, adt, THVM_EPI_SWIGLU);
-    u32 ga2[5], gn = 0;
-    ga2[gn++] = hb; ga2[gn++] = xn; ga2[gn++] = wgu;
+    NormSpec n2 = {1, gf, 0};
+    if (emit_norm(d, &n2, &gin, nsp, sizeof nsp, gargs, &ng)) return -1;
+    snprintf(p, sizeof p, "thvm-builtin:gemv m=%u n=%u k=%u wt=%u xt=%u yt=%u epi=%u%s", B, 2 * F,
+             D, c->wdtype, adt, adt, THVM_EPI_SWIGLU, nsp);
+    u32 ga2[7], gn = 0;
+    ga2[gn++] = hb; ga2[gn++] = gin; ga2[gn++] = wgu;
     if (f8) ga2[gn++] = sgu;
+    for (u32 i = 0; i < ng; i++) ga2[gn++] = gargs[i];
     if (op_add(d, "gemv_gateup", p, ga2, gn)) return -1;
 
     snprintf(p, sizeof p, "thvm-builtin:gemv m=%u n=%u k=%u wt=%u xt=%u yt=%u epi=%u", B, D, F,
@@ -391,12 +424,10 @@ static int build_llama(Decoder *d) {
     da[dn++] = x;
     if (op_add(d, "gemv_down", p, da, dn)) return -1;
   }
-  snprintf(p, sizeof p, "thvm-builtin:norm m=%u k=%u xt=%u yt=%u eps=%a", B, D, adt, adt, c->eps);
-  u32 nf[3] = {xn, x, tens_find(d, "norm_f")};
-  if (op_add(d, "norm", p, nf, 3)) return -1;
   u32 lw, ls;
   if (weight_matrix(d, "lm", c->vocab, D, &lw, &ls)) return -1;
-  return op_tail(d, lw, ls);
+  NormSpec nf = {1, tens_find(d, "norm_f"), 0};
+  return op_tail(d, lw, ls, &nf);
 }
 
 static int build_gpt2(Decoder *d) {
@@ -410,7 +441,7 @@ static int build_gpt2(Decoder *d) {
   u32 gf = weight_const(d, "lnf.g", D, 1.0f), bf = weight_const(d, "lnf.b", D, 0.0f);
   if (!wte || !wpe || !gf || !bf) return -1;
   char p[400], nm[48];
-  u32 x = tens_find(d, "x"), xn = tens_find(d, "xn"), q = tens_find(d, "q"),
+  u32 x = tens_find(d, "x"), q = tens_find(d, "q"),
       att = tens_find(d, "att"), hb = tens_find(d, "h"), L = tens_find(d, "len");
 
   snprintf(p, sizeof p, "thvm-builtin:embed b=%u d=%u v=%u et=%u xt=%u pos=1 maxseq=%u", B, D,
@@ -450,39 +481,40 @@ static int build_gpt2(Decoder *d) {
     snprintf(kn, sizeof kn, "l%u.kcache", l);
     snprintf(vn, sizeof vn, "l%u.vcache", l);
 
-    snprintf(p, sizeof p, "thvm-builtin:norm m=%u k=%u xt=%u yt=%u eps=%a ln=1 bias=1", B, D, adt,
-             adt, c->eps);
-    u32 n1[4] = {xn, x, g1, b1};
-    if (op_add(d, "norm", p, n1, 4)) return -1;
+    char nsp[96];
+    u32 gin, gargs[2], ng;
+    NormSpec n1 = {2, g1, b1};
+    if (emit_norm(d, &n1, &gin, nsp, sizeof nsp, gargs, &ng)) return -1;
     snprintf(p, sizeof p,
-             "thvm-builtin:gemv m=%u n=%u k=%u wt=%u xt=%u yt=%u epi=%u bias=1 h=%u hkv=%u hd=%u maxseq=%u",
-             B, 3 * D, D, wdt, adt, adt, THVM_EPI_QKV, H, H, hd, c->max_seq);
-    u32 qa[8] = {q, xn, wqkv, bqkv, L, tens_find(d, kn), tens_find(d, vn), 0};
-    if (op_add(d, "gemv_qkv", p, qa, 7)) return -1;
+             "thvm-builtin:gemv m=%u n=%u k=%u wt=%u xt=%u yt=%u epi=%u bias=1 h=%u hkv=%u hd=%u maxseq=%u%s",
+             B, 3 * D, D, wdt, adt, adt, THVM_EPI_QKV, H, H, hd, c->max_seq, nsp);
+    u32 qa[10], qn = 0;
+    qa[qn++] = q; qa[qn++] = gin; qa[qn++] = wqkv;
+    for (u32 i = 0; i < ng; i++) qa[qn++] = gargs[i];
+    qa[qn++] = bqkv; qa[qn++] = L; qa[qn++] = tens_find(d, kn); qa[qn++] = tens_find(d, vn);
+    if (op_add(d, "gemv_qkv", p, qa, qn)) return -1;
     if (op_attn(d, l)) return -1;
     snprintf(p, sizeof p, "thvm-builtin:gemv m=%u n=%u k=%u wt=%u xt=%u yt=%u epi=%u bias=1", B, D,
              D, wdt, adt, adt, THVM_EPI_RESID);
     u32 oa[5] = {x, att, wo, bo, x};
     if (op_add(d, "gemv_o", p, oa, 5)) return -1;
-    snprintf(p, sizeof p, "thvm-builtin:norm m=%u k=%u xt=%u yt=%u eps=%a ln=1 bias=1", B, D, adt,
-             adt, c->eps);
-    u32 n2[4] = {xn, x, g2, b2};
-    if (op_add(d, "norm", p, n2, 4)) return -1;
-    snprintf(p, sizeof p, "thvm-builtin:gemv m=%u n=%u k=%u wt=%u xt=%u yt=%u epi=%u bias=1", B, F,
-             D, wdt, adt, adt, THVM_EPI_GELU);
-    u32 fa[4] = {hb, xn, wfc, bfc};
-    if (op_add(d, "gemv_fc", p, fa, 4)) return -1;
+    NormSpec n2 = {2, g2, b2};
+    if (emit_norm(d, &n2, &gin, nsp, sizeof nsp, gargs, &ng)) return -1;
+    snprintf(p, sizeof p, "thvm-builtin:gemv m=%u n=%u k=%u wt=%u xt=%u yt=%u epi=%u bias=1%s", B,
+             F, D, wdt, adt, adt, THVM_EPI_GELU, nsp);
+    u32 fa[6], fn = 0;
+    fa[fn++] = hb; fa[fn++] = gin; fa[fn++] = wfc;
+    for (u32 i = 0; i < ng; i++) fa[fn++] = gargs[i];
+    fa[fn++] = bfc;
+    if (op_add(d, "gemv_fc", p, fa, fn)) return -1;
     snprintf(p, sizeof p, "thvm-builtin:gemv m=%u n=%u k=%u wt=%u xt=%u yt=%u epi=%u bias=1", B, D,
              F, wdt, adt, adt, THVM_EPI_RESID);
     u32 pa[5] = {x, hb, wpr, bpr, x};
     if (op_add(d, "gemv_proj", p, pa, 5)) return -1;
   }
-  snprintf(p, sizeof p, "thvm-builtin:norm m=%u k=%u xt=%u yt=%u eps=%a ln=1 bias=1", B, D, adt, adt,
-           c->eps);
-  u32 nf[4] = {xn, x, gf, bf};
-  if (op_add(d, "norm", p, nf, 4)) return -1;
   d->weight_bytes += (u64)c->vocab * D * hb_dt_size(adt);   /* tied LM head */
-  return op_tail(d, wte, 0);
+  NormSpec nf = {2, gf, bf};
+  return op_tail(d, wte, 0, &nf);
 }
 
 THVM_API void thvm_hip_decoder_destroy(uint32_t h) {

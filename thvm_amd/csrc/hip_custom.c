@@ -159,13 +159,17 @@ int hb_builtin_launch(const char *program, const u32 *ids, u32 n, int check_only
   if (strcmp(K, "gemv") == 0) {
     ThvmGemvArgs a;
     memset(&a, 0, sizeof a);
-    u32 bias = 0;
+    u32 bias = 0, ngain = 1, nbias = 0;
     NEED(spec_u32(&sp, "m", &a.M, 1, 0) || spec_u32(&sp, "n", &a.N, 1, 0) ||
          spec_u32(&sp, "k", &a.K, 1, 0) || spec_u32(&sp, "wt", &a.wdt, 1, 0) ||
          spec_u32(&sp, "xt", &a.xdt, 0, THVM_DT_BF16) || spec_u32(&sp, "yt", &a.ydt, 0, THVM_DT_BF16) ||
          spec_u32(&sp, "epi", &a.epi, 0, THVM_EPI_STORE) || spec_u32(&sp, "bias", &bias, 0, 0) ||
          spec_u32(&sp, "h", &a.n_heads, 0, 0) || spec_u32(&sp, "hkv", &a.n_kv_heads, 0, 0) ||
-         spec_u32(&sp, "hd", &a.head_dim, 0, 0) || spec_u32(&sp, "maxseq", &a.max_seq, 0, 0));
+         spec_u32(&sp, "hd", &a.head_dim, 0, 0) || spec_u32(&sp, "maxseq", &a.max_seq, 0, 0) ||
+         spec_u32(&sp, "norm", &a.norm, 0, 0) || spec_f32(&sp, "eps", &a.norm_eps, 0, 1e-6f) ||
+         spec_u32(&sp, "ngain", &ngain, 0, 1) || spec_u32(&sp, "nbias", &nbias, 0, a.norm == 2) ||
+         spec_u32(&sp, "waves", &a.tune_waves, 0, 0) || spec_u32(&sp, "r", &a.tune_r, 0, 0) ||
+         spec_u32(&sp, "u", &a.tune_u, 0, 0) || spec_u32(&sp, "blocks", &a.tune_blocks, 0, 0));
     {
       u32 ldy0 = a.epi == THVM_EPI_SWIGLU ? a.N / 2
                : (a.epi == THVM_EPI_QKV || a.epi == THVM_EPI_QKV_ROPE) ? a.n_heads * a.head_dim
@@ -186,6 +190,8 @@ int hb_builtin_launch(const char *program, const u32 *ids, u32 n, int check_only
     a.x = arg(&c, slot++, ((u64)(a.M - 1) * a.ldx + a.K) * xsz);
     a.w = arg(&c, slot++, (u64)a.N * a.K * wsz);
     if (a.wdt == THVM_DT_FP8E4M3) a.scale = (const float *)arg(&c, slot++, (u64)a.N * 4);
+    if (a.norm && ngain) a.norm_w = (const float *)arg(&c, slot++, (u64)a.K * 4);
+    if (a.norm == 2 && nbias) a.norm_b = (const float *)arg(&c, slot++, (u64)a.K * 4);
     if (bias) a.bias = arg(&c, slot++, (u64)a.N * ysz);
     if (a.epi == THVM_EPI_RESID) a.res = arg(&c, slot++, ybytes);
     if (a.epi == THVM_EPI_QKV_ROPE) {
@@ -257,7 +263,7 @@ int hb_builtin_launch(const char *program, const u32 *ids, u32 n, int check_only
     a.kcache = arg(&c, 2, cb);
     a.vcache = arg(&c, 3, cb);
     a.len = (const int32_t *)arg(&c, 4, 4);
-    a.part = (float *)arg(&c, 5, thvm_k_attn_part_bytes(a.B, a.H, a.hd, a.n_split));
+    a.part = (float *)arg(&c, 5, thvm_k_attn_part_bytes(a.B, a.H, a.Hkv, a.hd, a.n_split));
     if (c.bad) return -1;
     bytes = 0; /* live-length dependent: the decoder accounts for it */
     if (check_only) return 0;

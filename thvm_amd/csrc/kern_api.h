@@ -41,6 +41,15 @@ typedef struct ThvmGemvArgs {
   uint32_t wdt, xdt, ydt;  /* THVM_DT_*                                        */
   uint32_t epi;
   uint32_t n_heads, n_kv_heads, head_dim, max_seq;
+  /* fused norm prologue on x: 0 none, 1 RMSNorm, 2 LayerNorm; the normalised
+   * row is rounded to xdt, as the standalone norm kernel would store it */
+  uint32_t norm;
+  float    norm_eps;
+  const float *norm_w;     /* [K] gain or NULL                                */
+  const float *norm_b;     /* [K] LayerNorm bias or NULL                      */
+  /* launch tuning (0 = heuristic): waves per block, rows per wave, chunks per
+   * lane in flight, grid blocks */
+  uint32_t tune_waves, tune_r, tune_u, tune_blocks;
 } ThvmGemvArgs;
 int thvm_k_gemv(const ThvmGemvArgs *a, hipStream_t s, char *err, int errlen);
 
@@ -75,7 +84,7 @@ typedef struct ThvmAttnArgs {
   float scale;             /* 1/sqrt(hd)                                     */
 } ThvmAttnArgs;
 int thvm_k_attn_decode(const ThvmAttnArgs *a, hipStream_t s, char *err, int errlen);
-uint64_t thvm_k_attn_part_bytes(uint32_t B, uint32_t H, uint32_t hd, uint32_t n_split);
+uint64_t thvm_k_attn_part_bytes(uint32_t B, uint32_t H, uint32_t Hkv, uint32_t hd, uint32_t n_split);
 
 /* Embedding gather: x[b][i] = emb[tok[b]][i] (+ pos[L-1][i] when pos != NULL),
  * tok int32 [B]; out of range ids read a zero row. */

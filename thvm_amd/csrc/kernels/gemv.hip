@@ -1,27 +1,34 @@
 // gemv.hip -- bandwidth-bound decode projection y[m,n] = sum_k x[m,k] W[n,k]
 // for small M (1..4), W in f32 / fp16 / bf16 / fp8-e4m3 (+ per-row f32 scale),
-// fp32 accumulation, with fused epilogues (residual, SwiGLU, GELU, q/k RoPE +
-// KV-cache append).
+// fp32 accumulation, with an optional fused RMSNorm / LayerNorm prologue on x
+// and fused epilogues (residual, SwiGLU, GELU, q/k RoPE + KV-cache append).
 //
 // Replaces the reference's two-phase split-K GEMV + fold kernels
 // (bench/dsv2_decode_bench.c:1043-1125 src_gemv/src_gred, and the folds fused
 // into gred_q :435-485, kv_prep :487-556, gred_o_rms :558-611, gred_down
-// :613-636) and the renderer's GROUP_REDUCE matvec (src/codegen/hand_opts.c:
-// 413-470).  Design for gfx950 instead of a translation:
+// :613-636), its fused RMSNorm (src_rms :397-433) and the renderer's
+// GROUP_REDUCE matvec (src/codegen/hand_opts.c:413-470).  Design for gfx950:
 //   * W is [N, K] with K contiguous; one wave64 owns R consecutive rows and
 //     streams them with 128-bit loads (lane l takes 16-byte chunks l, l+64, ..),
 //     U chunks per row in flight per lane before any arithmetic;
-//   * x (M rows) is staged once per block into LDS as f32, quad-swizzled so the
-//     64 lanes' 16-byte reads hit distinct banks;
-//   * fp8 decodes with v_cvt_pk_f32_fp8 (OCP e4m3, exact), scale applied once
-//     per row after the reduction;
-//   * the K-reduction ends in a DPP wave reduction (fixed order, deterministic),
-//     so no partial buffer and no second fold kernel exist.
+//   * the first batch of weight loads is issued BEFORE x is staged, so the x
+//     staging (and the fused norm's block reduction) hides under HBM latency,
+//     and the next batch is prefetched while the current one is consumed;
+//   * x (M rows) is staged once per block into LDS in its storage type
+//     (bf16/fp16 as 16-bit, f32 as f32), chunk-swizzled so the 64 lanes'
+//     16-byte LDS reads hit distinct banks; a fused norm writes the normalised
+//     row there already rounded to the activation dtype, exactly as the
+//     separate norm kernel would store it;
+//   * fp8 decodes with v_cvt_pk_f32_fp8 (OCP e4m3, exact), the per-row scale
+//     is applied once after the reduction;
+//   * the K reduction ends in a DPP wave reduction (fixed order,
+//     deterministic): no partial buffer and no second fold kernel.
 #include "dev_common.h"
 #include "../kern_api.h"
 #include <stdio.h>
 
 enum { WT_F32 = 0, WT_F16 = 1, WT_BF16 = 2, WT_FP8 = 3 };
+enum { XT_BF16 = 0, XT_F16 = 1, XT_F32 = 2 };
 
 template <int WT> struct WTr;
 template <> struct WTr<WT_F32>  { static constexpr int E = 4;  };
@@ -29,7 +36,7 @@ template <> struct WTr<WT_F16>  { static constexpr int E = 8;  };
 template <> struct WTr<WT_BF16> { static constexpr int E = 8;  };
 template <> struct WTr<WT_FP8>  { static constexpr int E = 16; };
 
-// decode the 4 elements of quad j of a 16-byte chunk
+// decode the 4 elements of quad j of a 16-byte weight chunk
 template <int WT>
 __device__ __forceinline__ void quad_decode(const uint4 &q, int j, float o[4]);
 
@@ -77,32 +84,196 @@ __device__ __forceinline__ float rnd_any(float v, uint32_t dt) {
   return dt == THVM_DT_BF16 ? rbf(v) : dt == THVM_DT_FP16 ? rh(v) : v;
 }
 
-#define GEMV_WAVES 4
-#define GEMV_THREADS (GEMV_WAVES * 64)
+// ---- LDS x layout -----------------------------------------------------------
+// 16-bit x: element e of row m lives at halfword  m*K + ((e%E)/8 * C + e/E)*8 + e%8
+// f32 x:    element e of row m lives at float     m*K + ((e%E)/4 * C + e/E)*4 + e%4
+// (C = K/E chunks per row): the 8 (or 4) elements a lane needs for one quad
+// pair are one aligned 16-byte LDS word, and lanes c, c+1 read adjacent words.
+template <int XT> struct XTr;
+template <> struct XTr<XT_BF16> { static constexpr int B = 2, G = 8; };
+template <> struct XTr<XT_F16>  { static constexpr int B = 2, G = 8; };
+template <> struct XTr<XT_F32>  { static constexpr int B = 4, G = 4; };
 
-template <int WT, int M, int R, int U>
-__global__ __launch_bounds__(GEMV_THREADS) void k_gemv(ThvmGemvArgs a) {
+template <int XT, int E>
+__device__ __forceinline__ uint32_t xs_index(uint32_t K, uint32_t C, uint32_t m, uint32_t e) {
+  constexpr int G = XTr<XT>::G;
+  const uint32_t c = e / E, r = e - c * E;
+  return m * K + ((r / G) * C + c) * G + (r % G);
+}
+
+// 8 x elements of a 16-bit group -> floats
+template <int XT>
+__device__ __forceinline__ void x8_decode(const uint4 &q, float o[8]) {
+  uint32_t w[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    if (XT == XT_BF16) {
+      o[2 * i] = __uint_as_float(w[i] << 16);
+      o[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
+    } else {
+      o[2 * i] = h2f((f16_t)(w[i] & 0xffffu));
+      o[2 * i + 1] = h2f((f16_t)(w[i] >> 16));
+    }
+  }
+}
+
+template <int XT>
+__device__ __forceinline__ void xs_store(void *xs, uint32_t idx, float v) {
+  if (XT == XT_BF16) ((bf16_t *)xs)[idx] = f2bf(v);
+  else if (XT == XT_F16) ((f16_t *)xs)[idx] = f2h(v);
+  else ((float *)xs)[idx] = v;
+}
+
+__device__ __forceinline__ float block_sum_g(float v, float *red, int nwaves) {
+  float w = wave_sum(v);
+  __syncthreads();
+  if (lane_id() == 0) red[threadIdx.x >> 6] = w;
+  __syncthreads();
+  float t = 0.0f;
+  for (int i = 0; i < nwaves; i++) t += red[i];
+  return t;
+}
+
+#define GEMV_MAX_WAVES 16
+#define XREG 16   /* x elements per thread kept in registers by the staging */
+
+// input x dtype (compile time): vector loads of 16 bytes
+enum { XD_BF16 = 0, XD_F16 = 1, XD_F32 = 2 };
+template <int XD> struct XDr { static constexpr int VE = XD == XD_F32 ? 4 : 8, B = XD == XD_F32 ? 4 : 2; };
+
+template <int XD>
+__device__ __forceinline__ void xvec(const void *x, uint64_t e, float *o) {
+  const uint4 q = ld16((const char *)x + e * XDr<XD>::B);
+  const uint32_t w[4] = {q.x, q.y, q.z, q.w};
+  if (XD == XD_F32) {
+#pragma unroll
+    for (int i = 0; i < 4; i++) o[i] = __uint_as_float(w[i]);
+  } else {
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      if (XD == XD_BF16) {
+        o[2 * i] = __uint_as_float(w[i] << 16);
+        o[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
+      } else {
+        o[2 * i] = h2f((f16_t)(w[i] & 0xffffu));
+        o[2 * i + 1] = h2f((f16_t)(w[i] >> 16));
+      }
+    }
+  }
+}
+template <int XD>
+__device__ __forceinline__ float rnd_x(float v) {
+  return XD == XD_BF16 ? rbf(v) : XD == XD_F16 ? rh(v) : v;
+}
+
+template <int WT, int XD, int M, int R, int U>
+__global__ __launch_bounds__(1024) void k_gemv(ThvmGemvArgs a) {
   constexpr int E = WTr<WT>::E;
-  extern __shared__ float xs[];          // [M][K] f32, quad-swizzled
+  // LDS keeps x in its 16-bit storage type unless weights or x are f32
+  constexpr int XT = (WT == WT_F32 || XD == XD_F32) ? XT_F32 : (XD == XD_BF16 ? XT_BF16 : XT_F16);
+  constexpr int VE = XDr<XD>::VE;
+  extern __shared__ __align__(16) unsigned char xs_raw[];
+  __shared__ float red[GEMV_MAX_WAVES];
   const uint32_t K = a.K, N = a.N;
-  const uint32_t C = K / E;              // 16-byte chunks per row
+  const uint32_t C = K / E;              // 16-byte weight chunks per row
   const int lane = lane_id();
   const int wv = threadIdx.x >> 6;
-
-  // ---- stage x into LDS: element k of row m at m*K + ((k%E)/4*C + k/E)*4 + k%4
-  for (uint32_t e = threadIdx.x; e < (uint32_t)M * K; e += GEMV_THREADS) {
-    uint32_t m = e / K, k = e - m * K;
-    uint32_t c = k / E, r = k - c * E;
-    float v = ld_any(a.x, (uint64_t)m * a.ldx + k, a.xdt);
-    xs[m * K + ((r >> 2) * C + c) * 4 + (r & 3)] = v;
-  }
-  __syncthreads();
-
+  const int nw = blockDim.x >> 6;
   const uint32_t G = (N + R - 1) / R;
   const uint64_t rowbytes = (uint64_t)K * (16 / E);
   const char *wb = (const char *)a.w;
 
-  for (uint32_t g = blockIdx.x * GEMV_WAVES + wv; g < G; g += gridDim.x * GEMV_WAVES) {
+  // ---- 1. first weight batch in flight before anything else ----
+  uint32_t g = blockIdx.x * nw + wv;
+  uint4 wq[R][U];
+  auto load_batch = [&](uint32_t gg, uint32_t c0) {
+    const uint32_t n0 = gg * R;
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+      const bool rok = gg < G && (n0 + r) < N;
+      const char *rp = wb + (uint64_t)(n0 + r) * rowbytes;
+#pragma unroll
+      for (int u = 0; u < U; u++) {
+        const uint32_t c = c0 + u * 64 + lane;
+        if (rok && c < C) wq[r][u] = ld_stream16(rp + (uint64_t)c * 16);
+        else wq[r][u] = make_uint4(0, 0, 0, 0);
+      }
+    }
+  };
+  load_batch(g, 0);
+
+  // ---- 2. stage x into LDS (16-byte loads), with the fused norm if asked ----
+  const uint32_t nthr = blockDim.x;
+  const uint32_t NVt = K / VE;           // x vectors per row
+  for (int m = 0; m < M; m++) {
+    const uint64_t xo = (uint64_t)m * a.ldx;
+    if (a.norm == 0) {
+      for (uint32_t v = threadIdx.x; v < NVt; v += nthr) {
+        float f[VE];
+        xvec<XD>(a.x, xo + (uint64_t)v * VE, f);
+#pragma unroll
+        for (int i = 0; i < VE; i++) xs_store<XT>(xs_raw, xs_index<XT, E>(K, C, m, v * VE + i), f[i]);
+      }
+    } else {
+      constexpr int NV = XREG / VE;
+      float xv[NV][VE];
+#pragma unroll
+      for (int j = 0; j < NV; j++) {
+        const uint32_t v = threadIdx.x + j * nthr;
+        if (v < NVt) xvec<XD>(a.x, xo + (uint64_t)v * VE, xv[j]);
+        else {
+#pragma unroll
+          for (int i = 0; i < VE; i++) xv[j][i] = 0.0f;
+        }
+      }
+      const float invK = 1.0f / (float)K;
+      float mean = 0.0f, s1 = 0.0f, s2 = 0.0f;
+      if (a.norm == 2) {
+#pragma unroll
+        for (int j = 0; j < NV; j++)
+#pragma unroll
+          for (int i = 0; i < VE; i++) s1 += xv[j][i];
+        mean = block_sum_g(s1, red, nw) * invK;
+      }
+#pragma unroll
+      for (int j = 0; j < NV; j++) {
+        const bool vok = threadIdx.x + j * nthr < NVt;
+#pragma unroll
+        for (int i = 0; i < VE; i++) {
+          const float d = xv[j][i] - mean;
+          s2 += vok ? d * d : 0.0f;
+        }
+      }
+      const float inv = 1.0f / sqrtf(block_sum_g(s2, red, nw) * invK + a.norm_eps);
+#pragma unroll
+      for (int j = 0; j < NV; j++) {
+        const uint32_t v = threadIdx.x + j * nthr;
+        if (v < NVt) {
+          float gw[VE], gb[VE];
+#pragma unroll
+          for (int i = 0; i < VE; i += 4) {
+            float4 t = a.norm_w ? *(const float4 *)(a.norm_w + v * VE + i) : make_float4(1.f, 1.f, 1.f, 1.f);
+            gw[i] = t.x; gw[i + 1] = t.y; gw[i + 2] = t.z; gw[i + 3] = t.w;
+            float4 u = (a.norm == 2 && a.norm_b) ? *(const float4 *)(a.norm_b + v * VE + i)
+                                                 : make_float4(0.f, 0.f, 0.f, 0.f);
+            gb[i] = u.x; gb[i + 1] = u.y; gb[i + 2] = u.z; gb[i + 3] = u.w;
+          }
+#pragma unroll
+          for (int i = 0; i < VE; i++) {
+            // (x - mean) * inv * w (+ b), the norm kernel's own formula
+            float val = (xv[j][i] - mean) * inv;
+            if (a.norm_w) val = val * gw[i];
+            if (a.norm == 2 && a.norm_b) val = val + gb[i];
+            xs_store<XT>(xs_raw, xs_index<XT, E>(K, C, m, v * VE + i), rnd_x<XD>(val));
+          }
+        }
+      }
+    }
+  }
+  __syncthreads();
+
+  // ---- 3. stream the weight rows ----
+  for (; g < G; g += gridDim.x * nw) {
     const uint32_t n0 = g * R;
     float acc[R][M];
 #pragma unroll
@@ -111,38 +282,62 @@ __global__ __launch_bounds__(GEMV_THREADS) void k_gemv(ThvmGemvArgs a) {
       for (int m = 0; m < M; m++) acc[r][m] = 0.0f;
 
     for (uint32_t c0 = 0; c0 < C; c0 += 64 * U) {
-      uint4 wq[R][U];
+      uint4 cur[R][U];
 #pragma unroll
-      for (int r = 0; r < R; r++) {
-        const bool rok = (n0 + r) < N;
-        const char *rp = wb + (uint64_t)(n0 + r) * rowbytes;
+      for (int r = 0; r < R; r++)
 #pragma unroll
-        for (int u = 0; u < U; u++) {
-          uint32_t c = c0 + u * 64 + lane;
-          if (rok && c < C) wq[r][u] = ld_stream16(rp + (uint64_t)c * 16);
-          else wq[r][u] = make_uint4(0, 0, 0, 0);
-        }
-      }
+        for (int u = 0; u < U; u++) cur[r][u] = wq[r][u];
+      // prefetch the next batch (next chunk block, else the next row group)
+      if (c0 + 64 * U < C) load_batch(g, c0 + 64 * U);
+      else load_batch(g + gridDim.x * nw, 0);
 #pragma unroll
       for (int u = 0; u < U; u++) {
-        uint32_t c = c0 + u * 64 + lane;
+        const uint32_t c = c0 + u * 64 + lane;
         if (c < C) {
+          if (XT == XT_F32) {
 #pragma unroll
-          for (int j = 0; j < E / 4; j++) {
-            float4 xv[M];
+            for (int j = 0; j < E / 4; j++) {
+              float4 xv[M];
 #pragma unroll
-            for (int m = 0; m < M; m++)
-              xv[m] = *(const float4 *)&xs[m * K + (j * C + c) * 4];
+              for (int m = 0; m < M; m++)
+                xv[m] = *(const float4 *)((const float *)xs_raw + m * K + (j * C + c) * 4);
 #pragma unroll
-            for (int r = 0; r < R; r++) {
-              float wf[4];
-              quad_decode<WT>(wq[r][u], j, wf);
+              for (int r = 0; r < R; r++) {
+                float wf[4];
+                quad_decode<WT>(cur[r][u], j, wf);
+#pragma unroll
+                for (int m = 0; m < M; m++) {
+                  acc[r][m] += xv[m].x * wf[0];
+                  acc[r][m] += xv[m].y * wf[1];
+                  acc[r][m] += xv[m].z * wf[2];
+                  acc[r][m] += xv[m].w * wf[3];
+                }
+              }
+            }
+          } else {
+#pragma unroll
+            for (int h = 0; h < (E + 7) / 8; h++) {     // 8-element x groups
+              float xf[M][8];
 #pragma unroll
               for (int m = 0; m < M; m++) {
-                acc[r][m] += xv[m].x * wf[0];
-                acc[r][m] += xv[m].y * wf[1];
-                acc[r][m] += xv[m].z * wf[2];
-                acc[r][m] += xv[m].w * wf[3];
+                uint4 q = *(const uint4 *)((const uint16_t *)xs_raw + m * K + (h * C + c) * 8);
+                x8_decode<XT>(q, xf[m]);
+              }
+#pragma unroll
+              for (int jj = 0; jj < 2 && (h * 2 + jj) < E / 4; jj++) {
+                const int j = h * 2 + jj;
+#pragma unroll
+                for (int r = 0; r < R; r++) {
+                  float wf[4];
+                  quad_decode<WT>(cur[r][u], j, wf);
+#pragma unroll
+                  for (int m = 0; m < M; m++) {
+                    acc[r][m] += xf[m][jj * 4 + 0] * wf[0];
+                    acc[r][m] += xf[m][jj * 4 + 1] * wf[1];
+                    acc[r][m] += xf[m][jj * 4 + 2] * wf[2];
+                    acc[r][m] += xf[m][jj * 4 + 3] * wf[3];
+                  }
+                }
               }
             }
           }
@@ -198,44 +393,53 @@ __global__ __launch_bounds__(GEMV_THREADS) void k_gemv(ThvmGemvArgs a) {
                      gelu_tanh_f(rnd_any(v[r][m], ydt)));
         break;
       case THVM_EPI_SWIGLU:
-        if (R == 2 && n0 + 1 < N) {
+        if (R % 2 == 0) {
 #pragma unroll
-          for (int m = 0; m < M; m++) {
-            float gg = rnd_any(v[0][m], ydt), uu = rnd_any(v[R - 1][m], ydt);
-            st_any(a.y, (uint64_t)m * a.ldy + n0 / 2, ydt, silu_f(gg) * uu);
+          for (int r = 0; r + 1 < R; r += 2) {
+            if (n0 + r + 1 >= N) break;
+#pragma unroll
+            for (int m = 0; m < M; m++) {
+              float gg = rnd_any(v[r][m], ydt), uu = rnd_any(v[r + 1][m], ydt);
+              st_any(a.y, (uint64_t)m * a.ldy + (n0 + r) / 2, ydt, silu_f(gg) * uu);
+            }
           }
         }
         break;
       case THVM_EPI_QKV_ROPE:
       case THVM_EPI_QKV: {
-        if (R != 2 || n0 + 1 >= N) break;
+        if (R % 2) break;
         const uint32_t hd = a.head_dim;
         const uint32_t Hq = a.n_heads * hd, Hk = a.n_kv_heads * hd;
         const int32_t pos = a.len[0] - 1;
         if (pos < 0 || (uint32_t)pos >= a.max_seq) break;   // no live row to write
         const bool rope = a.epi == THVM_EPI_QKV_ROPE;
-        const uint32_t d = n0 % hd;
-        float c = 1.0f, sn = 0.0f;
-        if (rope && n0 < Hq + Hk) {
-          c = a.rope_cos[(uint64_t)pos * (hd / 2) + d / 2];
-          sn = a.rope_sin[(uint64_t)pos * (hd / 2) + d / 2];
-        }
 #pragma unroll
-        for (int m = 0; m < M; m++) {
-          float xe = rnd_any(v[0][m], ydt), xo = rnd_any(v[R - 1][m], ydt);
-          float oe = xe, oo = xo;
-          if (rope && n0 < Hq + Hk) { oe = xe * c - xo * sn; oo = xo * c + xe * sn; }
-          if (n0 < Hq) {
-            st_any(a.y, (uint64_t)m * a.ldy + n0, ydt, oe);
-            st_any(a.y, (uint64_t)m * a.ldy + n0 + 1, ydt, oo);
-          } else {
-            const bool isk = n0 < Hq + Hk;
-            const uint32_t off = isk ? n0 - Hq : n0 - Hq - Hk;
-            const uint32_t h = off / hd;
-            uint64_t ci = (((uint64_t)m * a.n_kv_heads + h) * a.max_seq + (uint32_t)pos) * hd + d;
-            void *cache = isk ? a.kcache : a.vcache;
-            st_any(cache, ci, ydt, oe);
-            st_any(cache, ci + 1, ydt, oo);
+        for (int r = 0; r + 1 < R; r += 2) {
+          const uint32_t nn = n0 + r;
+          if (nn + 1 >= N) break;
+          const uint32_t d = nn % hd;
+          float c = 1.0f, sn = 0.0f;
+          if (rope && nn < Hq + Hk) {
+            c = a.rope_cos[(uint64_t)pos * (hd / 2) + d / 2];
+            sn = a.rope_sin[(uint64_t)pos * (hd / 2) + d / 2];
+          }
+#pragma unroll
+          for (int m = 0; m < M; m++) {
+            float xe = rnd_any(v[r][m], ydt), xo = rnd_any(v[r + 1][m], ydt);
+            float oe = xe, oo = xo;
+            if (rope && nn < Hq + Hk) { oe = xe * c - xo * sn; oo = xo * c + xe * sn; }
+            if (nn < Hq) {
+              st_any(a.y, (uint64_t)m * a.ldy + nn, ydt, oe);
+              st_any(a.y, (uint64_t)m * a.ldy + nn + 1, ydt, oo);
+            } else {
+              const bool isk = nn < Hq + Hk;
+              const uint32_t off = isk ? nn - Hq : nn - Hq - Hk;
+              const uint32_t h = off / hd;
+              uint64_t ci = (((uint64_t)m * a.n_kv_heads + h) * a.max_seq + (uint32_t)pos) * hd + d;
+              void *cache = isk ? a.kcache : a.vcache;
+              st_any(cache, ci, ydt, oe);
+              st_any(cache, ci + 1, ydt, oo);
+            }
           }
         }
       } break;
@@ -247,19 +451,29 @@ __global__ __launch_bounds__(GEMV_THREADS) void k_gemv(ThvmGemvArgs a) {
 // -------------------------------------------------------------------------
 typedef void (*gemv_fn)(ThvmGemvArgs);
 
-template <int WT, int R>
+template <int WT, int XD, int R, int U>
 static gemv_fn pick_m(uint32_t M) {
   switch (M) {
-    case 1: return k_gemv<WT, 1, R, 4>;
-    case 2: return k_gemv<WT, 2, R, 4>;
-    case 3: return k_gemv<WT, 3, R, 4>;
-    case 4: return k_gemv<WT, 4, R, 4>;
+    case 1: return k_gemv<WT, XD, 1, R, U>;
+    case 2: return k_gemv<WT, XD, 2, R, U>;
+    case 3: return k_gemv<WT, XD, 3, R, U>;
+    case 4: return k_gemv<WT, XD, 4, R, U>;
     default: return nullptr;
   }
 }
+template <int WT, int XD>
+static gemv_fn pick_ru(uint32_t M, int R, int U) {
+  if (R == 1) return U == 8 ? pick_m<WT, XD, 1, 8>(M) : pick_m<WT, XD, 1, 4>(M);
+  return U == 8 ? pick_m<WT, XD, 2, 8>(M) : pick_m<WT, XD, 2, 4>(M);
+}
 template <int WT>
-static gemv_fn pick_r(uint32_t M, int R) {
-  return R == 1 ? pick_m<WT, 1>(M) : pick_m<WT, 2>(M);
+static gemv_fn pick_x(uint32_t xdt, uint32_t M, int R, int U) {
+  switch (xdt) {
+    case THVM_DT_BF16: return pick_ru<WT, XD_BF16>(M, R, U);
+    case THVM_DT_FP16: return pick_ru<WT, XD_F16>(M, R, U);
+    case THVM_DT_FP32: return pick_ru<WT, XD_F32>(M, R, U);
+    default: return nullptr;
+  }
 }
 
 static int dt_size(uint32_t dt) {
@@ -298,19 +512,39 @@ extern "C" int thvm_k_gemv(const ThvmGemvArgs *a, hipStream_t s, char *err, int 
     return -1;
   }
   if (a->ldx < a->K) { snprintf(err, errlen, "gemv: ldx < K"); return -1; }
+  {
+    const uint32_t xs = a->xdt == THVM_DT_FP32 ? 4 : 2, ve = 16 / xs;
+    if (a->K % ve || ((uint64_t)a->ldx * xs) % 16 || ((uintptr_t)a->x & 15) ||
+        ((uintptr_t)a->norm_w & 15) || ((uintptr_t)a->norm_b & 15)) {
+      snprintf(err, errlen, "gemv: x rows and norm vectors must be 16-byte aligned and K a multiple of %u", ve);
+      return -1;
+    }
+  }
+  if (a->norm > 2) { snprintf(err, errlen, "gemv: unknown norm %u", a->norm); return -1; }
+  // defaults from the gfx950 sweep over the C4 projection shapes (8 waves per
+  // block, one row per wave unless the epilogue pairs rows, U=4, <= 512 blocks)
+  uint32_t waves = a->tune_waves ? a->tune_waves : 8;
+  if (waves != 1 && waves != 2 && waves != 4 && waves != 8 && waves != 16) {
+    snprintf(err, errlen, "gemv: waves per block must be 1,2,4,8 or 16");
+    return -1;
+  }
+  if (a->norm && a->K > (uint64_t)XREG * 64 * waves) {
+    snprintf(err, errlen, "gemv: fused norm needs K <= %u for %u waves", XREG * 64 * waves, waves);
+    return -1;
+  }
   int R = 1;
+  int pairs = 0;
   switch (a->epi) {
-    case THVM_EPI_STORE: case THVM_EPI_GELU:
-      R = (a->N % 2 == 0) ? 2 : 1;
-      if (a->ldy < a->N && a->M > 1) { snprintf(err, errlen, "gemv: ldy < N"); return -1; }
-      break;
-    case THVM_EPI_RESID:
-      if (a->res == nullptr) { snprintf(err, errlen, "gemv: residual epilogue without res"); return -1; }
-      R = (a->N % 2 == 0) ? 2 : 1;
+    case THVM_EPI_STORE: case THVM_EPI_GELU: case THVM_EPI_RESID:
+      if (a->epi == THVM_EPI_RESID && a->res == nullptr) {
+        snprintf(err, errlen, "gemv: residual epilogue without res");
+        return -1;
+      }
+      R = 1;
       break;
     case THVM_EPI_SWIGLU:
       if (a->N % 2) { snprintf(err, errlen, "gemv: swiglu needs even N"); return -1; }
-      R = 2;
+      R = 2; pairs = 1;
       break;
     case THVM_EPI_QKV_ROPE: case THVM_EPI_QKV: {
       uint32_t hd = a->head_dim;
@@ -321,34 +555,50 @@ extern "C" int thvm_k_gemv(const ThvmGemvArgs *a, hipStream_t s, char *err, int 
         snprintf(err, errlen, "gemv: bad qkv epilogue geometry");
         return -1;
       }
-      R = 2;
+      R = 2; pairs = 1;
     } break;
     default:
       snprintf(err, errlen, "gemv: unknown epilogue %u", a->epi);
       return -1;
   }
-  uint64_t lds = (uint64_t)a->M * a->K * 4;
+  if (a->tune_r) {
+    if (a->tune_r != 1 && a->tune_r != 2) { snprintf(err, errlen, "gemv: r must be 1 or 2"); return -1; }
+    if ((pairs && a->tune_r == 1) || a->N % a->tune_r) { snprintf(err, errlen, "gemv: r=%u does not tile N/epilogue", a->tune_r); return -1; }
+    R = (int)a->tune_r;
+  }
+  int U = a->tune_u ? (int)a->tune_u : 4;
+  if (U != 4 && U != 8) { snprintf(err, errlen, "gemv: u must be 4 or 8"); return -1; }
+  uint32_t xsz = (a->xdt == THVM_DT_FP32 || a->wdt == THVM_DT_FP32) ? 4 : 2;
+  uint64_t lds = (uint64_t)a->M * a->K * xsz;
   if (lds > 160 * 1024) {
-    snprintf(err, errlen, "gemv: M*K=%llu floats exceed LDS (use the MFMA GEMM)",
+    snprintf(err, errlen, "gemv: M*K=%llu x elements exceed LDS (use the MFMA GEMM)",
              (unsigned long long)a->M * a->K);
     return -1;
   }
   gemv_fn f = nullptr;
   switch (a->wdt) {
-    case THVM_DT_FP32: f = pick_r<WT_F32>(a->M, R); break;
-    case THVM_DT_FP16: f = pick_r<WT_F16>(a->M, R); break;
-    case THVM_DT_BF16: f = pick_r<WT_BF16>(a->M, R); break;
-    case THVM_DT_FP8E4M3: f = pick_r<WT_FP8>(a->M, R); break;
+    case THVM_DT_FP32: f = pick_x<WT_F32>(a->xdt, a->M, R, U); break;
+    case THVM_DT_FP16: f = pick_x<WT_F16>(a->xdt, a->M, R, U); break;
+    case THVM_DT_BF16: f = pick_x<WT_BF16>(a->xdt, a->M, R, U); break;
+    case THVM_DT_FP8E4M3: f = pick_x<WT_FP8>(a->xdt, a->M, R, U); break;
   }
-  if (!f) { snprintf(err, errlen, "gemv: no kernel instance"); return -1; }
-  uint32_t G = (a->N + R - 1) / R;
-  uint32_t need = (G + GEMV_WAVES - 1) / GEMV_WAVES;
-  // blocks resident per CU bounded by LDS (160 KiB) and 8 blocks of 4 waves
-  uint32_t per_cu = (uint32_t)((160u * 1024u) / (lds ? lds : 1));
-  if (per_cu > 8) per_cu = 8;
-  if (per_cu < 1) per_cu = 1;
-  uint32_t cap = 256u * per_cu;
-  uint32_t grid = need < cap ? need : cap;
+  if (!f) { snprintf(err, errlen, "gemv: no kernel instance (R=%d U=%d)", R, U); return -1; }
+  uint32_t Gr = (a->N + R - 1) / R;
+  uint32_t need = (Gr + waves - 1) / waves;
+  uint32_t grid = need;
+  if (a->tune_blocks) {
+    grid = a->tune_blocks < need ? a->tune_blocks : need;
+  } else {
+    // blocks resident per CU bounded by LDS (160 KiB) and 32 waves; beyond
+    // 2 blocks of 8 waves per CU the grid-stride loop is as fast
+    uint32_t per_cu = (uint32_t)((160u * 1024u) / (lds ? lds : 1));
+    uint32_t wcap = 32u / waves;
+    if (per_cu > wcap) per_cu = wcap;
+    if (per_cu > 2) per_cu = 2;
+    if (per_cu < 1) per_cu = 1;
+    uint32_t cap = 256u * per_cu;
+    if (grid > cap) grid = cap;
+  }
   if (lds > 64 * 1024) {
     hipError_t e = hipFuncSetAttribute((const void *)f,
                                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
@@ -357,7 +607,7 @@ extern "C" int thvm_k_gemv(const ThvmGemvArgs *a, hipStream_t s, char *err, int 
       return -1;
     }
   }
-  hipLaunchKernelGGL(f, dim3(grid), dim3(GEMV_THREADS), (size_t)lds, s, *a);
+  hipLaunchKernelGGL(f, dim3(grid), dim3(64 * waves), (size_t)lds, s, *a);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) {
     snprintf(err, errlen, "gemv launch: %s", hipGetErrorString(e));

@@ -65,6 +65,48 @@ __device__ __forceinline__ float block_max(float v, float *red) {
   return t;
 }
 
+// rows of K <= 16*256: every element loaded once into registers, all loads
+// issued together
+#define NORM_REG 16
+__global__ __launch_bounds__(ROW_THREADS) void k_norm_reg(ThvmNormArgs a) {
+  __shared__ float red[ROW_WAVES];
+  const uint32_t m = blockIdx.x;
+  const uint64_t xo = (uint64_t)m * a.ldx, yo = (uint64_t)m * a.ldy;
+  const float invK = 1.0f / (float)a.K;
+  float xv[NORM_REG];
+#pragma unroll
+  for (int i = 0; i < NORM_REG; i++) {
+    const uint32_t e = threadIdx.x + i * ROW_THREADS;
+    xv[i] = e < a.K ? ld_a(a.x, xo + e, a.xdt) : 0.0f;
+  }
+  float mean = 0.0f, s2 = 0.0f;
+  if (a.layernorm) {
+    float s1 = 0.0f;
+#pragma unroll
+    for (int i = 0; i < NORM_REG; i++) s1 += xv[i];
+    mean = block_sum(s1, red) * invK;
+#pragma unroll
+    for (int i = 0; i < NORM_REG; i++) {
+      const float d = xv[i] - mean;
+      s2 += (threadIdx.x + i * ROW_THREADS) < a.K ? d * d : 0.0f;
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < NORM_REG; i++) s2 += xv[i] * xv[i];
+  }
+  const float inv = 1.0f / sqrtf(block_sum(s2, red) * invK + a.eps);
+#pragma unroll
+  for (int i = 0; i < NORM_REG; i++) {
+    const uint32_t e = threadIdx.x + i * ROW_THREADS;
+    if (e < a.K) {
+      float v = (xv[i] - mean) * inv;
+      if (a.w) v = v * a.w[e];
+      if (a.layernorm && a.b) v = v + a.b[e];
+      st_a(a.y, yo + e, a.ydt, v);
+    }
+  }
+}
+
 __global__ __launch_bounds__(ROW_THREADS) void k_norm(ThvmNormArgs a) {
   __shared__ float red[ROW_WAVES];
   const uint32_t m = blockIdx.x;
@@ -113,7 +155,10 @@ extern "C" int thvm_k_norm(const ThvmNormArgs *a, hipStream_t s, char *err, int 
     snprintf(err, errlen, "norm: bad args M=%u K=%u", a->M, a->K);
     return -1;
   }
-  hipLaunchKernelGGL(k_norm, dim3(a->M), dim3(ROW_THREADS), 0, s, *a);
+  if (a->K <= NORM_REG * ROW_THREADS)
+    hipLaunchKernelGGL(k_norm_reg, dim3(a->M), dim3(ROW_THREADS), 0, s, *a);
+  else
+    hipLaunchKernelGGL(k_norm, dim3(a->M), dim3(ROW_THREADS), 0, s, *a);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) { snprintf(err, errlen, "norm launch: %s", hipGetErrorString(e)); return -1; }
   return 0;
@@ -229,16 +274,25 @@ __global__ __launch_bounds__(256) void k_argmax_part(ThvmArgmaxArgs a) {
   if (t == 0) { a.pv[b * a.nb + blk] = sv[0]; a.pi[b * a.nb + blk] = si[0]; }
 }
 
+// one wave per batch row: lanes scan the block partials, then a shuffle
+// reduction keeps (max value, lowest index)
 __global__ void k_argmax_fin(ThvmArgmaxArgs a) {
   const uint32_t b = blockIdx.x;
-  if (threadIdx.x != 0) return;
-  float bv = a.pv[b * a.nb];
-  int32_t bi = a.pi[b * a.nb];
-  for (uint32_t k = 1; k < a.nb; k++) {
+  const int lane = lane_id();
+  float bv = -INFINITY;
+  int32_t bi = 0x7fffffff;
+  for (uint32_t k = lane; k < a.nb; k += 64) {
     float v = a.pv[b * a.nb + k];
     int32_t i = a.pi[b * a.nb + k];
     if (am_better(v, i, bv, bi)) { bv = v; bi = i; }
   }
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) {
+    float ov = __shfl_xor(bv, off);
+    int32_t oi = __shfl_xor(bi, off);
+    if (am_better(ov, oi, bv, bi)) { bv = ov; bi = oi; }
+  }
+  if (lane != 0) return;
   a.tok[b] = bi;
   if (a.hist) {
     int32_t L = a.len[0];
