@@ -131,7 +131,7 @@ def main() -> int:
     log(f"[bench] model built in {time.time() - t0:.1f}s, {dec.step_kernels()} kernels/step, "
         f"{thvm.lib().thvm_hip_mem_live_bytes() / 1e9:.2f} GB on device")
 
-    dec.capture()                                  # step 1 (eager, recorded)
+    slot = dec.capture()                           # step 1 (eager, recorded)
     dec.replay(max(args.warmup, 1))                # graph capture + warmup
     thvm.synchronize()
     pos0 = dec.position
@@ -147,17 +147,22 @@ def main() -> int:
     tps = cfg["batch"] * args.steps / (ms / 1000.0)
     log(f"[bench] timed {args.steps} steps: {ms_per_step:.3f} ms/step (wall {wall * 1000 / args.steps:.3f})")
 
-    # live per-kernel timing of the dominant kernel: one eager step with a HIP
-    # event pair around every builtin dispatch on the dispatch stream
+    # live per-kernel timing of the dominant kernel: a bounded sleep kernel
+    # (~10 ms) goes first so the host enqueues a whole eager step behind it;
+    # the step then runs back to back on the dispatch stream with a HIP event
+    # pair around every builtin launch (no host gaps inside the pairs)
+    dummy = thvm.Buffer(64)
+    prof_steps = 2
     thvm.kprof(True)
     thvm.kprof_reset()
-    prof_steps = 2
     for _ in range(prof_steps):
+        thvm.builtin("delay", [dummy], n=3000)
         dec.step()
     g_ms, g_n = thvm.kprof_query("gemv")
     a_ms, a_n = thvm.kprof_query("attn")
     n_ms, n_n = thvm.kprof_query("norm")
     thvm.kprof(False)
+    dummy.free()
     L_prof = dec.position - 1
     gemv_gbs = gemv_bytes_per_step(cfg) * prof_steps / (g_ms / 1000.0) / 1e9
     attn_gbs = (attn_bytes_per_step(cfg, L_prof) * prof_steps) / (a_ms / 1000.0) / 1e9

@@ -461,7 +461,10 @@ static int KP_ON = 0;
 static hipEvent_t *KP_POOL = NULL;
 static u32 KP_POOL_N = 0, KP_POOL_CAP = 0, KP_POOL_USED = 0;
 
-int hb_kprof_on(void) { return KP_ON && !HB_GRAPH_CAPTURING; }
+/* Under a graph capture the event records become graph nodes, so a replay
+ * re-times every builtin launch inside the graph (events keep the last
+ * replay's timestamps). */
+int hb_kprof_on(void) { return KP_ON; }
 
 static hipEvent_t kp_event(void) {
   if (KP_POOL_USED < KP_POOL_N) return KP_POOL[KP_POOL_USED++];

@@ -321,6 +321,12 @@ int hb_builtin_launch(const char *program, const u32 *ids, u32 n, int check_only
     if (check_only) return 0;
     if (prof) hb_kprof_begin(K, &e0);
     rc = thvm_k_len_bump(L, (int32_t)d, HB_STREAM, err, sizeof err);
+  } else if (strcmp(K, "delay") == 0) {
+    u32 nper = 0;
+    NEED(spec_u32(&sp, "n", &nper, 1, 0));
+    if (!arg(&c, 0, 0)) return -1;      /* the ABI needs one argument slot */
+    if (check_only) return 0;
+    rc = thvm_k_delay(nper, HB_STREAM, err, sizeof err);
   } else if (strcmp(K, "rope") == 0) {
     ThvmRopeArgs a;
     memset(&a, 0, sizeof a);

@@ -105,6 +105,10 @@ typedef struct ThvmArgmaxArgs {
 } ThvmArgmaxArgs;
 int thvm_k_argmax(const ThvmArgmaxArgs *a, hipStream_t s, char *err, int errlen);
 
+/* One wave sleeping n fixed periods (~3.4 us each): lets a host enqueue work
+ * behind it so back-to-back kernels can be timed without host gaps. */
+int thvm_k_delay(uint32_t n, hipStream_t s, char *err, int errlen);
+
 /* L[0] += delta (reference len_bump, bench/dsv2_decode_bench.c:1024-1041). */
 int thvm_k_len_bump(int32_t *len, int32_t delta, hipStream_t s, char *err, int errlen);
 

@@ -137,6 +137,105 @@ __device__ __forceinline__ float block_sum_g(float v, float *red, int nwaves) {
 #define GEMV_MAX_WAVES 16
 #define XREG 16   /* x elements per thread kept in registers by the staging */
 
+// the output stage of one row group (one lane, wave-uniform values)
+template <int R, int M>
+__device__ __forceinline__ void gemv_epilogue(const ThvmGemvArgs &a, const uint32_t n0,
+                                              const float (&tot)[R][M]) {
+  const uint32_t N = a.N;
+  float v[R][M];
+#pragma unroll
+  for (int r = 0; r < R; r++) {
+    uint32_t n = n0 + r;
+    float s = (a.scale != nullptr && n < N) ? a.scale[n] : 1.0f;
+    float bv = (a.bias != nullptr && n < N) ? ld_any(a.bias, n, a.ydt) : 0.0f;
+#pragma unroll
+    for (int m = 0; m < M; m++) v[r][m] = tot[r][m] * s + bv;
+  }
+  const uint32_t ydt = a.ydt;
+  switch (a.epi) {
+    case THVM_EPI_STORE:
+#pragma unroll
+      for (int r = 0; r < R; r++)
+        if (n0 + r < N)
+#pragma unroll
+          for (int m = 0; m < M; m++)
+            st_any(a.y, (uint64_t)m * a.ldy + n0 + r, ydt, v[r][m]);
+      break;
+    case THVM_EPI_RESID:
+#pragma unroll
+      for (int r = 0; r < R; r++)
+        if (n0 + r < N)
+#pragma unroll
+          for (int m = 0; m < M; m++) {
+            uint64_t i = (uint64_t)m * a.ldy + n0 + r;
+            float rv = ld_any(a.res, i, ydt);
+            st_any(a.y, i, ydt, rv + rnd_any(v[r][m], ydt));
+          }
+      break;
+    case THVM_EPI_GELU:
+#pragma unroll
+      for (int r = 0; r < R; r++)
+        if (n0 + r < N)
+#pragma unroll
+          for (int m = 0; m < M; m++)
+            st_any(a.y, (uint64_t)m * a.ldy + n0 + r, ydt,
+                   gelu_tanh_f(rnd_any(v[r][m], ydt)));
+      break;
+    case THVM_EPI_SWIGLU:
+      if (R % 2 == 0) {
+#pragma unroll
+        for (int r = 0; r + 1 < R; r += 2) {
+          if (n0 + r + 1 >= N) break;
+#pragma unroll
+          for (int m = 0; m < M; m++) {
+            float gg = rnd_any(v[r][m], ydt), uu = rnd_any(v[r + 1][m], ydt);
+            st_any(a.y, (uint64_t)m * a.ldy + (n0 + r) / 2, ydt, silu_f(gg) * uu);
+          }
+        }
+      }
+      break;
+    case THVM_EPI_QKV_ROPE:
+    case THVM_EPI_QKV: {
+      if (R % 2) break;
+      const uint32_t hd = a.head_dim;
+      const uint32_t Hq = a.n_heads * hd, Hk = a.n_kv_heads * hd;
+      const int32_t pos = a.len[0] - 1;
+      if (pos < 0 || (uint32_t)pos >= a.max_seq) break;   // no live row to write
+      const bool rope = a.epi == THVM_EPI_QKV_ROPE;
+#pragma unroll
+      for (int r = 0; r + 1 < R; r += 2) {
+        const uint32_t nn = n0 + r;
+        if (nn + 1 >= N) break;
+        const uint32_t d = nn % hd;
+        float c = 1.0f, sn = 0.0f;
+        if (rope && nn < Hq + Hk) {
+          c = a.rope_cos[(uint64_t)pos * (hd / 2) + d / 2];
+          sn = a.rope_sin[(uint64_t)pos * (hd / 2) + d / 2];
+        }
+#pragma unroll
+        for (int m = 0; m < M; m++) {
+          float xe = rnd_any(v[r][m], ydt), xo = rnd_any(v[r + 1][m], ydt);
+          float oe = xe, oo = xo;
+          if (rope && nn < Hq + Hk) { oe = xe * c - xo * sn; oo = xo * c + xe * sn; }
+          if (nn < Hq) {
+            st_any(a.y, (uint64_t)m * a.ldy + nn, ydt, oe);
+            st_any(a.y, (uint64_t)m * a.ldy + nn + 1, ydt, oo);
+          } else {
+            const bool isk = nn < Hq + Hk;
+            const uint32_t off = isk ? nn - Hq : nn - Hq - Hk;
+            const uint32_t h = off / hd;
+            uint64_t ci = (((uint64_t)m * a.n_kv_heads + h) * a.max_seq + (uint32_t)pos) * hd + d;
+            void *cache = isk ? a.kcache : a.vcache;
+            st_any(cache, ci, ydt, oe);
+            st_any(cache, ci + 1, ydt, oo);
+          }
+        }
+      }
+    } break;
+    default: break;
+  }
+}
+
 // input x dtype (compile time): vector loads of 16 bytes
 enum { XD_BF16 = 0, XD_F16 = 1, XD_F32 = 2 };
 template <int XD> struct XDr { static constexpr int VE = XD == XD_F32 ? 4 : 8, B = XD == XD_F32 ? 4 : 2; };
@@ -273,70 +372,69 @@ __global__ __launch_bounds__(1024) void k_gemv(ThvmGemvArgs a) {
   __syncthreads();
 
   // ---- 3. stream the weight rows ----
-  for (; g < G; g += gridDim.x * nw) {
-    const uint32_t n0 = g * R;
-    float acc[R][M];
+  // A flat sequence of (row group, chunk batch) steps per wave; two register
+  // sets ping-pong so the next batch is in flight while one is consumed (the
+  // wait before a consume covers only the older batch's loads).
+  const uint32_t NB = (C + 64 * U - 1) / (64 * U);      // batches per row group
+  const uint32_t gstride = gridDim.x * nw;
+  const uint32_t g0 = g;
+  const uint32_t ngw = g0 < G ? (G - 1 - g0) / gstride + 1 : 0;
+  const uint32_t T = ngw * NB;
+  float acc[R][M];
 #pragma unroll
-    for (int r = 0; r < R; r++)
+  for (int r = 0; r < R; r++)
 #pragma unroll
-      for (int m = 0; m < M; m++) acc[r][m] = 0.0f;
+    for (int m = 0; m < M; m++) acc[r][m] = 0.0f;
 
-    for (uint32_t c0 = 0; c0 < C; c0 += 64 * U) {
-      uint4 cur[R][U];
+  auto consume = [&](const uint4 (&X)[R][U], uint32_t t) {
+    const uint32_t gi = t / NB, bi = t - gi * NB;
+    const uint32_t c0 = bi * 64 * U;
 #pragma unroll
-      for (int r = 0; r < R; r++)
+    for (int u = 0; u < U; u++) {
+      const uint32_t c = c0 + u * 64 + lane;
+      if (c < C) {
+        if (XT == XT_F32) {
 #pragma unroll
-        for (int u = 0; u < U; u++) cur[r][u] = wq[r][u];
-      // prefetch the next batch (next chunk block, else the next row group)
-      if (c0 + 64 * U < C) load_batch(g, c0 + 64 * U);
-      else load_batch(g + gridDim.x * nw, 0);
+          for (int j = 0; j < E / 4; j++) {
+            float4 xv[M];
 #pragma unroll
-      for (int u = 0; u < U; u++) {
-        const uint32_t c = c0 + u * 64 + lane;
-        if (c < C) {
-          if (XT == XT_F32) {
+            for (int m = 0; m < M; m++)
+              xv[m] = *(const float4 *)((const float *)xs_raw + m * K + (j * C + c) * 4);
 #pragma unroll
-            for (int j = 0; j < E / 4; j++) {
-              float4 xv[M];
+            for (int r = 0; r < R; r++) {
+              float wf[4];
+              quad_decode<WT>(X[r][u], j, wf);
 #pragma unroll
-              for (int m = 0; m < M; m++)
-                xv[m] = *(const float4 *)((const float *)xs_raw + m * K + (j * C + c) * 4);
+              for (int m = 0; m < M; m++) {
+                acc[r][m] += xv[m].x * wf[0];
+                acc[r][m] += xv[m].y * wf[1];
+                acc[r][m] += xv[m].z * wf[2];
+                acc[r][m] += xv[m].w * wf[3];
+              }
+            }
+          }
+        } else {
+#pragma unroll
+          for (int h = 0; h < (E + 7) / 8; h++) {     // 8-element x groups
+            float xf[M][8];
+#pragma unroll
+            for (int m = 0; m < M; m++) {
+              uint4 q = *(const uint4 *)((const uint16_t *)xs_raw + m * K + (h * C + c) * 8);
+              x8_decode<XT>(q, xf[m]);
+            }
+#pragma unroll
+            for (int jj = 0; jj < 2 && (h * 2 + jj) < E / 4; jj++) {
+              const int j = h * 2 + jj;
 #pragma unroll
               for (int r = 0; r < R; r++) {
                 float wf[4];
-                quad_decode<WT>(cur[r][u], j, wf);
+                quad_decode<WT>(X[r][u], j, wf);
 #pragma unroll
                 for (int m = 0; m < M; m++) {
-                  acc[r][m] += xv[m].x * wf[0];
-                  acc[r][m] += xv[m].y * wf[1];
-                  acc[r][m] += xv[m].z * wf[2];
-                  acc[r][m] += xv[m].w * wf[3];
-                }
-              }
-            }
-          } else {
-#pragma unroll
-            for (int h = 0; h < (E + 7) / 8; h++) {     // 8-element x groups
-              float xf[M][8];
-#pragma unroll
-              for (int m = 0; m < M; m++) {
-                uint4 q = *(const uint4 *)((const uint16_t *)xs_raw + m * K + (h * C + c) * 8);
-                x8_decode<XT>(q, xf[m]);
-              }
-#pragma unroll
-              for (int jj = 0; jj < 2 && (h * 2 + jj) < E / 4; jj++) {
-                const int j = h * 2 + jj;
-#pragma unroll
-                for (int r = 0; r < R; r++) {
-                  float wf[4];
-                  quad_decode<WT>(cur[r][u], j, wf);
-#pragma unroll
-                  for (int m = 0; m < M; m++) {
-                    acc[r][m] += xf[m][jj * 4 + 0] * wf[0];
-                    acc[r][m] += xf[m][jj * 4 + 1] * wf[1];
-                    acc[r][m] += xf[m][jj * 4 + 2] * wf[2];
-                    acc[r][m] += xf[m][jj * 4 + 3] * wf[3];
-                  }
+                  acc[r][m] += xf[m][jj * 4 + 0] * wf[0];
+                  acc[r][m] += xf[m][jj * 4 + 1] * wf[1];
+                  acc[r][m] += xf[m][jj * 4 + 2] * wf[2];
+                  acc[r][m] += xf[m][jj * 4 + 3] * wf[3];
                 }
               }
             }
@@ -344,107 +442,40 @@ __global__ __launch_bounds__(1024) void k_gemv(ThvmGemvArgs a) {
         }
       }
     }
-
-    float tot[R][M];
+    if (bi == NB - 1) {
+      float tot[R][M];
 #pragma unroll
-    for (int r = 0; r < R; r++)
+      for (int r = 0; r < R; r++)
 #pragma unroll
-      for (int m = 0; m < M; m++) tot[r][m] = wave_sum(acc[r][m]);
-
-    if (lane != 0) continue;
-    // ---- epilogue (one lane, wave-uniform values) ----
-    float v[R][M];
+        for (int m = 0; m < M; m++) {
+          tot[r][m] = wave_sum(acc[r][m]);
+          acc[r][m] = 0.0f;
+        }
+      if (lane == 0) gemv_epilogue<R, M>(a, (g0 + gi * gstride) * R, tot);
+    }
+  };
+  auto load_step = [&](uint4 (&X)[R][U], uint32_t t) {
+    const uint32_t gi = t / NB, bi = t - gi * NB;
+    const uint32_t gg = g0 + gi * gstride, n0 = gg * R, c0 = bi * 64 * U;
 #pragma unroll
     for (int r = 0; r < R; r++) {
-      uint32_t n = n0 + r;
-      float s = (a.scale != nullptr && n < N) ? a.scale[n] : 1.0f;
-      float bv = (a.bias != nullptr && n < N) ? ld_any(a.bias, n, a.ydt) : 0.0f;
+      const bool rok = gg < G && (n0 + r) < N;
+      const char *rp = wb + (uint64_t)(n0 + r) * rowbytes;
 #pragma unroll
-      for (int m = 0; m < M; m++) v[r][m] = tot[r][m] * s + bv;
+      for (int u = 0; u < U; u++) {
+        const uint32_t c = c0 + u * 64 + lane;
+        if (rok && c < C) X[r][u] = ld_stream16(rp + (uint64_t)c * 16);
+        else X[r][u] = make_uint4(0, 0, 0, 0);
+      }
     }
-    const uint32_t ydt = a.ydt;
-    switch (a.epi) {
-      case THVM_EPI_STORE:
-#pragma unroll
-        for (int r = 0; r < R; r++)
-          if (n0 + r < N)
-#pragma unroll
-            for (int m = 0; m < M; m++)
-              st_any(a.y, (uint64_t)m * a.ldy + n0 + r, ydt, v[r][m]);
-        break;
-      case THVM_EPI_RESID:
-#pragma unroll
-        for (int r = 0; r < R; r++)
-          if (n0 + r < N)
-#pragma unroll
-            for (int m = 0; m < M; m++) {
-              uint64_t i = (uint64_t)m * a.ldy + n0 + r;
-              float rv = ld_any(a.res, i, ydt);
-              st_any(a.y, i, ydt, rv + rnd_any(v[r][m], ydt));
-            }
-        break;
-      case THVM_EPI_GELU:
-#pragma unroll
-        for (int r = 0; r < R; r++)
-          if (n0 + r < N)
-#pragma unroll
-            for (int m = 0; m < M; m++)
-              st_any(a.y, (uint64_t)m * a.ldy + n0 + r, ydt,
-                     gelu_tanh_f(rnd_any(v[r][m], ydt)));
-        break;
-      case THVM_EPI_SWIGLU:
-        if (R % 2 == 0) {
-#pragma unroll
-          for (int r = 0; r + 1 < R; r += 2) {
-            if (n0 + r + 1 >= N) break;
-#pragma unroll
-            for (int m = 0; m < M; m++) {
-              float gg = rnd_any(v[r][m], ydt), uu = rnd_any(v[r + 1][m], ydt);
-              st_any(a.y, (uint64_t)m * a.ldy + (n0 + r) / 2, ydt, silu_f(gg) * uu);
-            }
-          }
-        }
-        break;
-      case THVM_EPI_QKV_ROPE:
-      case THVM_EPI_QKV: {
-        if (R % 2) break;
-        const uint32_t hd = a.head_dim;
-        const uint32_t Hq = a.n_heads * hd, Hk = a.n_kv_heads * hd;
-        const int32_t pos = a.len[0] - 1;
-        if (pos < 0 || (uint32_t)pos >= a.max_seq) break;   // no live row to write
-        const bool rope = a.epi == THVM_EPI_QKV_ROPE;
-#pragma unroll
-        for (int r = 0; r + 1 < R; r += 2) {
-          const uint32_t nn = n0 + r;
-          if (nn + 1 >= N) break;
-          const uint32_t d = nn % hd;
-          float c = 1.0f, sn = 0.0f;
-          if (rope && nn < Hq + Hk) {
-            c = a.rope_cos[(uint64_t)pos * (hd / 2) + d / 2];
-            sn = a.rope_sin[(uint64_t)pos * (hd / 2) + d / 2];
-          }
-#pragma unroll
-          for (int m = 0; m < M; m++) {
-            float xe = rnd_any(v[r][m], ydt), xo = rnd_any(v[r + 1][m], ydt);
-            float oe = xe, oo = xo;
-            if (rope && nn < Hq + Hk) { oe = xe * c - xo * sn; oo = xo * c + xe * sn; }
-            if (nn < Hq) {
-              st_any(a.y, (uint64_t)m * a.ldy + nn, ydt, oe);
-              st_any(a.y, (uint64_t)m * a.ldy + nn + 1, ydt, oo);
-            } else {
-              const bool isk = nn < Hq + Hk;
-              const uint32_t off = isk ? nn - Hq : nn - Hq - Hk;
-              const uint32_t h = off / hd;
-              uint64_t ci = (((uint64_t)m * a.n_kv_heads + h) * a.max_seq + (uint32_t)pos) * hd + d;
-              void *cache = isk ? a.kcache : a.vcache;
-              st_any(cache, ci, ydt, oe);
-              st_any(cache, ci + 1, ydt, oo);
-            }
-          }
-        }
-      } break;
-      default: break;
-    }
+  };
+  uint4 wq2[R][U];
+  for (uint32_t t = 0; t < T; t += 2) {          // step 0 is already in wq
+    if (t + 1 < T) load_step(wq2, t + 1);
+    consume(wq, t);
+    if (t + 1 >= T) break;
+    if (t + 2 < T) load_step(wq, t + 2);
+    consume(wq2, t + 1);
   }
 }
 

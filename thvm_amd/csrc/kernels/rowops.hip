@@ -322,6 +322,20 @@ extern "C" int thvm_k_len_bump(int32_t *len, int32_t delta, hipStream_t s, char 
   return 0;
 }
 
+// ---- delay: one wave sleeps a fixed number of s_sleep(127) periods (~8k
+// cycles each), so a host can enqueue work behind it; the trip count is the
+// only exit condition and is bounded by the launcher ----
+__global__ void k_delay(uint32_t n) {
+  for (uint32_t i = 0; i < n; i++) __builtin_amdgcn_s_sleep(127);
+}
+extern "C" int thvm_k_delay(uint32_t n, hipStream_t s, char *err, int errlen) {
+  if (n > 200000) { snprintf(err, errlen, "delay: %u periods exceed the 200000 cap", n); return -1; }
+  hipLaunchKernelGGL(k_delay, dim3(1), dim3(64), 0, s, n);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) { snprintf(err, errlen, "delay launch: %s", hipGetErrorString(e)); return -1; }
+  return 0;
+}
+
 // ---- casts ------------------------------------------------------------------
 __global__ void k_cast(void *y, uint32_t ydt, const void *x, uint32_t xdt, uint64_t n) {
   uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
