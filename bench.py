@@ -103,6 +103,41 @@ def cpu_baseline(thvm, dec, cfg, n_steps: int):
     return tps, match, t_cpu, max(errs)
 
 
+COPY_BYTES = 1 << 30
+
+
+def copy_calibration(thvm) -> int:
+    """A plain copy of COPY_BYTES, 4 launches: each reads and writes exactly
+    COPY_BYTES, so a counter's reading per dispatch over COPY_BYTES/1024 is
+    its KiB scale."""
+    src, dst = thvm.Buffer(COPY_BYTES), thvm.Buffer(COPY_BYTES)
+    thvm.kprof(True)
+    thvm.kprof_reset()
+    for _ in range(4):
+        thvm.builtin("copy", [dst, src], n=COPY_BYTES)
+    ms, n = thvm.kprof_query("copy")
+    thvm.kprof(False)
+    src.free()
+    dst.free()
+    us = ms / n * 1000
+    print(json.dumps({"calibration": "copy", "bytes_read": COPY_BYTES, "bytes_written": COPY_BYTES,
+                      "launches": n, "avg_launch_us": round(us, 2),
+                      "gbs": round(2 * COPY_BYTES / (us * 1e-6) / 1e9, 1)}), flush=True)
+    thvm.shutdown()
+    return 0
+
+
+def measured_traffic():
+    """HBM bytes per k_gemv launch from the committed counter passes
+    (FETCH_SIZE, WRITE_SIZE, each scaled by the plain-copy calibration), or
+    None when that summary is absent."""
+    p = ROOT / "profiles" / "gemv_fp8_c4_traffic.json"
+    try:
+        return int(json.loads(p.read_text())["traffic_bytes_per_launch"])
+    except (OSError, ValueError, KeyError):
+        return None
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -111,6 +146,9 @@ def main() -> int:
     ap.add_argument("--cpu-steps", type=int, default=2)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--layers", type=int, default=None, help="debug only: fewer layers (invalid metric)")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="run only the plain 1 GiB copy kernel that calibrates the HBM traffic "
+                         "counters (FETCH_SIZE/WRITE_SIZE) and print its timing")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}); "
@@ -119,6 +157,8 @@ def main() -> int:
 
     import thvm_amd as thvm
     thvm.init()
+    if args.copy_calibration:
+        return copy_calibration(thvm)
     cfg = dict(C4)
     if args.layers:
         cfg["n_layers"] = args.layers
@@ -193,7 +233,9 @@ def main() -> int:
                    "vocab": cfg["vocab"], "batch": cfg["batch"], "context": CTX,
                    "parallelism": "single GPU"},
         "roofline": {"bound": "hbm", "achieved": round(gemv_gbs, 1), "peak": PEAK_GBS,
-                     "unit": "GB/s", "frac": round(gemv_gbs / PEAK_GBS, 4), "traffic": None,
+                     "unit": "GB/s", "frac": round(gemv_gbs / PEAK_GBS, 4),
+                     "traffic": measured_traffic() if not args.layers else None,
+                     "algorithmic_bytes_per_launch": gemv_bytes_per_step(cfg) // (g_n // prof_steps),
                      "kernel": "k_gemv (fp8 e4m3 weight GEMV, all projections + LM head)",
                      "launches_per_step": g_n // prof_steps,
                      "avg_launch_us": round(g_ms / g_n * 1000, 2)},

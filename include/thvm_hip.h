@@ -157,11 +157,11 @@ void thvm_hip_graph_invalidate(uint32_t slot);
 uint32_t thvm_hip_timer_start(void);
 /* Milliseconds between start and now (drains the stream). */
 double   thvm_hip_timer_stop(uint32_t timer_id);
-/* Per-builtin-kernel time: when enabled, every builtin dispatch brackets
- * itself with hipEvents on the dispatch stream and accumulates into a table
- * keyed by kernel tag.  Dispatches recorded while a graph capture is open
- * become event nodes of the graph: each replay re-times them, and a query
- * reads the last replay's durations. */
+/* Per-builtin-kernel time: when enabled, every eager builtin dispatch binds
+ * a hipEvent pair to the start of its first kernel and the end of its last
+ * (hipExtLaunchKernel) and accumulates into a table keyed by kernel tag, so
+ * the figures are kernel execution time, as a kernel trace reports it.
+ * Dispatches made while a graph capture is open are not timed. */
 void     thvm_hip_kprof_enable(int on);
 void     thvm_hip_kprof_reset(void);
 /* Total ms and launch count for kernel tag (e.g. "gemv"); -1 when absent. */

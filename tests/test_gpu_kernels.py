@@ -371,6 +371,30 @@ def test_len_bump(hip):
     assert L.read(np.int32)[0] == 43
 
 
+def test_copy_and_kernel_timing(hip):
+    """The plain copy kernel is byte-exact (odd 16-byte multiples, a partial
+    grid-stride pass), rejects unaligned sizes, and the per-kernel timer binds
+    its events to the kernel: an enabled timer records one positive duration
+    per launch, a disabled one records nothing."""
+    say("case: copy + kprof")
+    rng = np.random.default_rng(16)
+    for n in (16, 4096 + 48, (256 * 256 * 16 + 3) * 16):
+        src = rng.integers(0, 256, n, dtype=np.uint8)
+        x, y = up(hip, src), hip.Buffer(n)
+        hip.kprof(True)
+        hip.kprof_reset()
+        hip.builtin("copy", [y, x], n=n)
+        ms, cnt = hip.kprof_query("copy")
+        hip.kprof(False)
+        assert cnt == 1 and 0.0 < ms < 1000.0
+        assert np.array_equal(y.read(np.uint8), src)
+    hip.kprof_reset()
+    hip.builtin("copy", [y, x], n=16)
+    assert hip.kprof_query("copy")[1] == 0
+    with pytest.raises(hip.ThvmHipError):
+        hip.builtin("copy", [y, x], n=24)
+
+
 # ------------------------------------------------ custom kernels + JIT ----
 SRC_ADDONE = """extern "C" __global__ void addone(const float *x, float *y) {
   unsigned i = blockIdx.x * blockDim.x + threadIdx.x;

@@ -461,10 +461,16 @@ static int KP_ON = 0;
 static hipEvent_t *KP_POOL = NULL;
 static u32 KP_POOL_N = 0, KP_POOL_CAP = 0, KP_POOL_USED = 0;
 
-/* Under a graph capture the event records become graph nodes, so a replay
- * re-times every builtin launch inside the graph (events keep the last
- * replay's timestamps). */
-int hb_kprof_on(void) { return KP_ON; }
+/* Each profiled builtin launch binds an event pair to its own kernels
+ * (thvm_k_time_next), so a record's elapsed time is the kernels' execution
+ * alone.  Launches made while the stream is being captured are not
+ * profiled. */
+int hb_kprof_on(void) {
+  if (!KP_ON) return 0;
+  hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing(HB_STREAM, &st) != hipSuccess) return 0;
+  return st == hipStreamCaptureStatusNone;
+}
 
 static hipEvent_t kp_event(void) {
   if (KP_POOL_USED < KP_POOL_N) return KP_POOL[KP_POOL_USED++];
@@ -479,14 +485,13 @@ static hipEvent_t kp_event(void) {
   return e;
 }
 
-void hb_kprof_begin(const char *tag, hipEvent_t *e0) {
+void hb_kprof_begin(const char *tag, hipEvent_t *e0, hipEvent_t *e1) {
   (void)tag;
   *e0 = kp_event();
-  hipEventRecord(*e0, HB_STREAM);
+  *e1 = kp_event();
+  thvm_k_time_next(*e0, *e1);
 }
-void hb_kprof_end(const char *tag, hipEvent_t e0, u64 bytes) {
-  hipEvent_t e1 = kp_event();
-  hipEventRecord(e1, HB_STREAM);
+void hb_kprof_end(const char *tag, hipEvent_t e0, hipEvent_t e1, u64 bytes) {
   if (KP_N == KP_CAP) {
     KP_CAP = KP_CAP ? 2 * KP_CAP : 1024;
     KP = (KpRec *)realloc(KP, KP_CAP * sizeof(KpRec));

@@ -151,7 +151,7 @@ int hb_builtin_launch(const char *program, const u32 *ids, u32 n, int check_only
   char err[256] = {0};
   int rc = -1;
   u64 bytes = 0;                     /* algorithmic bytes, for kprof */
-  hipEvent_t e0 = NULL;
+  hipEvent_t e0 = NULL, e1 = NULL;
   int prof = !check_only && hb_kprof_on();
   const char *K = sp.kernel;
 
@@ -208,7 +208,7 @@ int hb_builtin_launch(const char *program, const u32 *ids, u32 n, int check_only
     bytes = (u64)a.N * a.K * wsz + (a.scale ? (u64)a.N * 4 : 0) + (u64)a.M * a.K * xsz +
             (u64)a.M * ncols_out * ysz * (a.res ? 2 : 1);
     if (check_only) return 0;
-    if (prof) hb_kprof_begin(K, &e0);
+    if (prof) hb_kprof_begin(K, &e0, &e1);
     rc = thvm_k_gemv(&a, HB_STREAM, err, sizeof err);
   } else if (strcmp(K, "norm") == 0) {
     ThvmNormArgs a;
@@ -230,7 +230,7 @@ int hb_builtin_launch(const char *program, const u32 *ids, u32 n, int check_only
     if (c.bad) return -1;
     bytes = (u64)a.M * a.K * (xsz + ysz) + (gain ? (u64)a.K * 4 : 0);
     if (check_only) return 0;
-    if (prof) hb_kprof_begin(K, &e0);
+    if (prof) hb_kprof_begin(K, &e0, &e1);
     rc = thvm_k_norm(&a, HB_STREAM, err, sizeof err);
   } else if (strcmp(K, "softmax") == 0) {
     ThvmSoftmaxArgs a;
@@ -244,7 +244,7 @@ int hb_builtin_launch(const char *program, const u32 *ids, u32 n, int check_only
     if (c.bad) return -1;
     bytes = ne * (hb_dt_size(a.xdt) + hb_dt_size(a.ydt));
     if (check_only) return 0;
-    if (prof) hb_kprof_begin(K, &e0);
+    if (prof) hb_kprof_begin(K, &e0, &e1);
     rc = thvm_k_softmax(&a, HB_STREAM, err, sizeof err);
   } else if (strcmp(K, "attn") == 0) {
     ThvmAttnArgs a;
@@ -267,7 +267,7 @@ int hb_builtin_launch(const char *program, const u32 *ids, u32 n, int check_only
     if (c.bad) return -1;
     bytes = 0; /* live-length dependent: the decoder accounts for it */
     if (check_only) return 0;
-    if (prof) hb_kprof_begin(K, &e0);
+    if (prof) hb_kprof_begin(K, &e0, &e1);
     rc = thvm_k_attn_decode(&a, HB_STREAM, err, sizeof err);
   } else if (strcmp(K, "embed") == 0) {
     ThvmEmbedArgs a;
@@ -289,7 +289,7 @@ int hb_builtin_launch(const char *program, const u32 *ids, u32 n, int check_only
     if (c.bad) return -1;
     bytes = (u64)a.B * a.D * (hb_dt_size(a.edt) * (pos ? 2 : 1) + hb_dt_size(a.xdt));
     if (check_only) return 0;
-    if (prof) hb_kprof_begin(K, &e0);
+    if (prof) hb_kprof_begin(K, &e0, &e1);
     rc = thvm_k_embed(&a, HB_STREAM, err, sizeof err);
   } else if (strcmp(K, "argmax") == 0) {
     ThvmArgmaxArgs a;
@@ -311,7 +311,7 @@ int hb_builtin_launch(const char *program, const u32 *ids, u32 n, int check_only
     if (c.bad) return -1;
     bytes = (u64)a.B * a.V * 4;
     if (check_only) return 0;
-    if (prof) hb_kprof_begin(K, &e0);
+    if (prof) hb_kprof_begin(K, &e0, &e1);
     rc = thvm_k_argmax(&a, HB_STREAM, err, sizeof err);
   } else if (strcmp(K, "len_bump") == 0) {
     u32 d = 1;
@@ -319,7 +319,7 @@ int hb_builtin_launch(const char *program, const u32 *ids, u32 n, int check_only
     int32_t *L = (int32_t *)arg(&c, 0, 4);
     if (c.bad) return -1;
     if (check_only) return 0;
-    if (prof) hb_kprof_begin(K, &e0);
+    if (prof) hb_kprof_begin(K, &e0, &e1);
     rc = thvm_k_len_bump(L, (int32_t)d, HB_STREAM, err, sizeof err);
   } else if (strcmp(K, "delay") == 0) {
     u32 nper = 0;
@@ -342,7 +342,7 @@ int hb_builtin_launch(const char *program, const u32 *ids, u32 n, int check_only
     a.len = (const int32_t *)arg(&c, 3, 4);
     if (c.bad) return -1;
     if (check_only) return 0;
-    if (prof) hb_kprof_begin(K, &e0);
+    if (prof) hb_kprof_begin(K, &e0, &e1);
     rc = thvm_k_rope(&a, HB_STREAM, err, sizeof err);
   } else if (strcmp(K, "cast") == 0) {
     u64 ne = 0;
@@ -353,8 +353,18 @@ int hb_builtin_launch(const char *program, const u32 *ids, u32 n, int check_only
     void *x = arg(&c, 1, ne * hb_dt_size(xt));
     if (c.bad) return -1;
     if (check_only) return 0;
-    if (prof) hb_kprof_begin(K, &e0);
+    if (prof) hb_kprof_begin(K, &e0, &e1);
     rc = thvm_k_cast(y, yt, x, xt, ne, HB_STREAM, err, sizeof err);
+  } else if (strcmp(K, "copy") == 0) {
+    u64 nb = 0;
+    NEED(spec_u64(&sp, "n", &nb, 1, 0));
+    void *y = arg(&c, 0, nb);
+    const void *x = arg(&c, 1, nb);
+    if (c.bad) return -1;
+    bytes = 2 * nb;
+    if (check_only) return 0;
+    if (prof) hb_kprof_begin(K, &e0, &e1);
+    rc = thvm_k_copy(y, x, nb, HB_STREAM, err, sizeof err);
   } else if (strcmp(K, "fill_normal") == 0) {
     u64 ne = 0, seed = 0, tag = 0;
     u32 dt = 0;
@@ -384,10 +394,11 @@ int hb_builtin_launch(const char *program, const u32 *ids, u32 n, int check_only
   }
 #undef NEED
   if (rc != 0) {
+    if (prof) thvm_k_time_next(NULL, NULL);
     hb_set_error("builtin %s: %s", K, err);
     return -1;
   }
-  if (prof) hb_kprof_end(K, e0, bytes);
+  if (prof) hb_kprof_end(K, e0, e1, bytes);
   return 0;
 }
 

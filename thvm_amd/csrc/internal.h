@@ -51,8 +51,8 @@ void hb_decoder_reset(void);
 
 /* kernel profiling hooks (builtin dispatches only, never under capture) */
 int  hb_kprof_on(void);
-void hb_kprof_begin(const char *tag, hipEvent_t *e0);
-void hb_kprof_end(const char *tag, hipEvent_t e0, u64 bytes);
+void hb_kprof_begin(const char *tag, hipEvent_t *e0, hipEvent_t *e1);
+void hb_kprof_end(const char *tag, hipEvent_t e0, hipEvent_t e1, u64 bytes);
 
 /* small helpers */
 u64 hb_hash64(const void *p, size_t n, u64 h);

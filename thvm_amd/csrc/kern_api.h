@@ -14,6 +14,16 @@
 extern "C" {
 #endif
 
+/* Kernel-only timing of the next launcher call: `start` is bound to the
+ * start of its first kernel and `stop` to the end of its last kernel
+ * (hipExtLaunchKernel), so hipEventElapsedTime over the pair covers the
+ * kernels alone, without the dispatch latency that event records placed
+ * around the launch would add.  The pair is consumed by that call; passing
+ * NULLs clears it.  Not for stream capture. */
+void thvm_k_time_next(hipEvent_t start, hipEvent_t stop);
+hipEvent_t thvm_k_take_start(void);
+hipEvent_t thvm_k_take_stop(void);
+
 /* GEMV / small-M GEMM epilogues */
 enum {
   THVM_EPI_STORE    = 0,  /* y = rnd(acc*s + b)                                 */
@@ -126,6 +136,10 @@ int thvm_k_fill_cache(void *cache, uint32_t dt, uint32_t B, uint32_t Hkv,
                       uint32_t max_seq, uint32_t hd, uint32_t ctx,
                       uint64_t seed, uint64_t tag, hipStream_t s,
                       char *err, int errlen);
+
+/* Plain device copy of nbytes (16-byte aligned pointers and size), each
+ * byte read once and written once: the calibration of HBM traffic counters. */
+int thvm_k_copy(void *y, const void *x, uint64_t nbytes, hipStream_t s, char *err, int errlen);
 
 /* Element-wise casts / copies (codec probes and glue): y[i] = cvt(x[i]). */
 int thvm_k_cast(void *y, uint32_t ydt, const void *x, uint32_t xdt, uint64_t n,

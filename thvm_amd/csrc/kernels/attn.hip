@@ -26,6 +26,7 @@
 //     3x slower on gfx950: the fences write back / invalidate L2 across XCDs.)
 #include "dev_common.h"
 #include "../kern_api.h"
+#include "launch.h"
 #include <stdio.h>
 
 #define ATT_WAVES 8
@@ -326,8 +327,8 @@ extern "C" int thvm_k_attn_decode(const ThvmAttnArgs *a, hipStream_t s, char *er
     snprintf(err, errlen, "attn: no kernel for hd=%u G=%u", a->hd, G);
     return -1;
   }
-  hipLaunchKernelGGL(f, dim3(a->Hkv, a->n_split, a->B), dim3(ATT_THREADS), 0, s, *a);
-  hipLaunchKernelGGL(fm, dim3(a->B * a->H), dim3(256), 0, s, *a);
+  thvm_launch(true, false, f, dim3(a->Hkv, a->n_split, a->B), dim3(ATT_THREADS), 0, s, *a);
+  thvm_launch(false, true, fm, dim3(a->B * a->H), dim3(256), 0, s, *a);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) { snprintf(err, errlen, "attn launch: %s", hipGetErrorString(e)); return -1; }
   return 0;

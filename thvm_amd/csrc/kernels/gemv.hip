@@ -25,6 +25,7 @@
 //     deterministic): no partial buffer and no second fold kernel.
 #include "dev_common.h"
 #include "../kern_api.h"
+#include "launch.h"
 #include <stdio.h>
 
 enum { WT_F32 = 0, WT_F16 = 1, WT_BF16 = 2, WT_FP8 = 3 };
@@ -638,7 +639,7 @@ extern "C" int thvm_k_gemv(const ThvmGemvArgs *a, hipStream_t s, char *err, int 
       return -1;
     }
   }
-  hipLaunchKernelGGL(f, dim3(grid), dim3(64 * waves), (size_t)lds, s, *a);
+  thvm_launch(true, true, f, dim3(grid), dim3(64 * waves), (uint32_t)lds, s, *a);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) {
     snprintf(err, errlen, "gemv launch: %s", hipGetErrorString(e));

@@ -17,6 +17,7 @@
 // the reference's serial order -- parity is held to the stated tolerances.
 #include "dev_common.h"
 #include "../kern_api.h"
+#include "launch.h"
 #include <stdio.h>
 
 __device__ __forceinline__ float ld_a(const void *p, uint64_t i, uint32_t dt) {
@@ -156,9 +157,9 @@ extern "C" int thvm_k_norm(const ThvmNormArgs *a, hipStream_t s, char *err, int 
     return -1;
   }
   if (a->K <= NORM_REG * ROW_THREADS)
-    hipLaunchKernelGGL(k_norm_reg, dim3(a->M), dim3(ROW_THREADS), 0, s, *a);
+    thvm_launch(true, true, k_norm_reg, dim3(a->M), dim3(ROW_THREADS), 0, s, *a);
   else
-    hipLaunchKernelGGL(k_norm, dim3(a->M), dim3(ROW_THREADS), 0, s, *a);
+    thvm_launch(true, true, k_norm, dim3(a->M), dim3(ROW_THREADS), 0, s, *a);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) { snprintf(err, errlen, "norm launch: %s", hipGetErrorString(e)); return -1; }
   return 0;
@@ -183,7 +184,7 @@ extern "C" int thvm_k_softmax(const ThvmSoftmaxArgs *a, hipStream_t s, char *err
     snprintf(err, errlen, "softmax: bad args");
     return -1;
   }
-  hipLaunchKernelGGL(k_softmax, dim3(a->M), dim3(ROW_THREADS), 0, s, *a);
+  thvm_launch(true, true, k_softmax, dim3(a->M), dim3(ROW_THREADS), 0, s, *a);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) { snprintf(err, errlen, "softmax launch: %s", hipGetErrorString(e)); return -1; }
   return 0;
@@ -210,7 +211,7 @@ extern "C" int thvm_k_rope(const ThvmRopeArgs *a, hipStream_t s, char *err, int 
   if (!act_dt(a->dt) || a->hd == 0 || a->hd % 2) { snprintf(err, errlen, "rope: bad args"); return -1; }
   uint64_t n = (uint64_t)a->B * a->nh * (a->hd / 2);
   if (n == 0) return 0;
-  hipLaunchKernelGGL(k_rope, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, *a);
+  thvm_launch(true, true, k_rope, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, *a);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) { snprintf(err, errlen, "rope launch: %s", hipGetErrorString(e)); return -1; }
   return 0;
@@ -237,7 +238,7 @@ extern "C" int thvm_k_embed(const ThvmEmbedArgs *a, hipStream_t s, char *err, in
     snprintf(err, errlen, "embed: bad args");
     return -1;
   }
-  hipLaunchKernelGGL(k_embed, dim3((a->D + 255) / 256, a->B), dim3(256), 0, s, *a);
+  thvm_launch(true, true, k_embed, dim3((a->D + 255) / 256, a->B), dim3(256), 0, s, *a);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) { snprintf(err, errlen, "embed launch: %s", hipGetErrorString(e)); return -1; }
   return 0;
@@ -305,18 +306,36 @@ extern "C" int thvm_k_argmax(const ThvmArgmaxArgs *a, hipStream_t s, char *err, 
     snprintf(err, errlen, "argmax: bad args");
     return -1;
   }
-  hipLaunchKernelGGL(k_argmax_part, dim3(a->nb, a->B), dim3(256), 0, s, *a);
-  hipLaunchKernelGGL(k_argmax_fin, dim3(a->B), dim3(64), 0, s, *a);
+  thvm_launch(true, false, k_argmax_part, dim3(a->nb, a->B), dim3(256), 0, s, *a);
+  thvm_launch(false, true, k_argmax_fin, dim3(a->B), dim3(64), 0, s, *a);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) { snprintf(err, errlen, "argmax launch: %s", hipGetErrorString(e)); return -1; }
   return 0;
+}
+
+// ---- pending kernel-timing events of the next launcher call (the backend
+// dispatches from one host thread) ----
+static hipEvent_t TN_START = nullptr, TN_STOP = nullptr;
+extern "C" void thvm_k_time_next(hipEvent_t start, hipEvent_t stop) {
+  TN_START = start;
+  TN_STOP = stop;
+}
+extern "C" hipEvent_t thvm_k_take_start(void) {
+  hipEvent_t e = TN_START;
+  TN_START = nullptr;
+  return e;
+}
+extern "C" hipEvent_t thvm_k_take_stop(void) {
+  hipEvent_t e = TN_STOP;
+  TN_STOP = nullptr;
+  return e;
 }
 
 __global__ void k_len_bump(int32_t *len, int32_t d) {
   if (threadIdx.x == 0 && blockIdx.x == 0) len[0] = len[0] + d;
 }
 extern "C" int thvm_k_len_bump(int32_t *len, int32_t delta, hipStream_t s, char *err, int errlen) {
-  hipLaunchKernelGGL(k_len_bump, dim3(1), dim3(64), 0, s, len, delta);
+  thvm_launch(true, true, k_len_bump, dim3(1), dim3(64), 0, s, len, delta);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) { snprintf(err, errlen, "len_bump launch: %s", hipGetErrorString(e)); return -1; }
   return 0;
@@ -350,6 +369,30 @@ extern "C" int thvm_k_cast(void *y, uint32_t ydt, const void *x, uint32_t xdt, u
   hipLaunchKernelGGL(k_cast, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, y, ydt, x, xdt, n);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) { snprintf(err, errlen, "cast launch: %s", hipGetErrorString(e)); return -1; }
+  return 0;
+}
+
+// ---- plain copy: n16 16-byte units, read once and written once (the
+// reference for HBM traffic counters: FETCH = WRITE = 16*n16 bytes) ----
+__global__ __launch_bounds__(256) void k_copy16(uint4 *y, const uint4 *x, uint64_t n16) {
+  const uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
+  for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n16; i += stride)
+    y[i] = ld_stream16(x + i);
+}
+extern "C" int thvm_k_copy(void *y, const void *x, uint64_t nbytes, hipStream_t s, char *err,
+                           int errlen) {
+  if ((nbytes & 15u) || ((uintptr_t)y & 15u) || ((uintptr_t)x & 15u)) {
+    snprintf(err, errlen, "copy: pointers and size must be 16-byte aligned");
+    return -1;
+  }
+  uint64_t n16 = nbytes / 16;
+  if (n16 == 0) return 0;
+  uint64_t blocks = (n16 + 255) / 256;
+  if (blocks > 256 * 16) blocks = 256 * 16;
+  thvm_launch(true, true, k_copy16, dim3((unsigned)blocks), dim3(256), 0, s, (uint4 *)y,
+              (const uint4 *)x, n16);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) { snprintf(err, errlen, "copy launch: %s", hipGetErrorString(e)); return -1; }
   return 0;
 }
 
