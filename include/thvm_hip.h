@@ -189,7 +189,7 @@ typedef struct ThvmDecodeConfig {
   uint32_t ffn;           /* FFN width (dense layers)                      */
   uint32_t vocab;
   uint32_t max_seq;       /* KV capacity (positions)                       */
-  uint32_t batch;         /* rows decoded per step                         */
+  uint32_t batch;         /* rows decoded per step, 1..64 (above 4: MFMA GEMM projections) */
   uint32_t wdtype;        /* weight dtype: FP32 / FP16 / BF16 / FP8E4M3    */
   uint32_t adtype;        /* activation dtype: FP32 / FP16 / BF16          */
   float    eps;           /* norm epsilon                                  */

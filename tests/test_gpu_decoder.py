@@ -102,3 +102,17 @@ def test_gpt2_fp32_greedy_ids_identical(hip):
 
 def test_gpt2_fp16_decode_parity(hip):
     run_parity(hip, dict(GPT2, wdtype=DT_F16, adtype=DT_F16, batch=2), steps=5, ctx=0)
+
+
+@pytest.mark.parametrize("batch", [8, 16])
+def test_llama_fp8_batched_mfma(hip, batch):
+    """Batches above 4 rows: separate norm kernels and MFMA GEMM projections
+    (the C4 B=16 path at a small shape)."""
+    cfg = dict(LLAMA, batch=batch, wdtype=DT_FP8, adtype=DT_BF16)
+    run_parity(hip, cfg, steps=4, ctx=30)
+
+
+def test_gpt2_fp16_batch8_mfma(hip):
+    """The GPT-2 XL B=8 path (LayerNorm kernels, fp16 MFMA GEMM with bias and
+    GELU epilogues) at a small shape."""
+    run_parity(hip, dict(GPT2, wdtype=DT_F16, adtype=DT_F16, batch=8), steps=4, ctx=0)

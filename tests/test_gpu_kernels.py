@@ -244,6 +244,129 @@ def test_gemv_tuning_knobs_agree(hip, waves, r, u):
     assert np.all(np.abs(got - ref) <= 1e-5 * floor)
 
 
+# ------------------------------------------------------------- MFMA GEMM ----
+MFMA_TYPES = [(DT_F16, DT_F16), (DT_BF16, DT_BF16), (DT_FP8, DT_BF16), (DT_FP8, DT_F16)]
+
+
+@pytest.mark.parametrize("wx", MFMA_TYPES)
+@pytest.mark.parametrize("M", [1, 5, 8, 16, 17, 32, 33, 64])
+@pytest.mark.parametrize("NK", [(64, 256), (97, 768), (256, 4096), (130, 1600)])
+def test_gemm_mfma_store_f32(hip, wx, M, NK):
+    """The MFMA small-M GEMM (forced with path=2, the default above M=4)
+    against the oracle's f32 serial dot products; N not a multiple of the
+    16-row tile and M not a multiple of 16 exercise the padded edges."""
+    wdt, xdt = wx
+    N, K = NK
+    say(f"case: gemm mfma wdt={wdt} xdt={xdt} M={M} N={N} K={K}")
+    rng = np.random.default_rng(5000 + 100 * wdt + 10 * xdt + M + N)
+    xs, ws, scale, ref, floor = _gemv_case(hip, rng, wdt, M, N, K, xdt=xdt)
+    y = hip.Buffer(M * N * 4)
+    args = [y, up(hip, xs), up(hip, ws)] + ([up(hip, scale)] if scale is not None else [])
+    hip.builtin("gemv", args, m=M, n=N, k=K, wt=wdt, xt=xdt, yt=DT_F32, epi=0, path=2)
+    got = y.read(np.float32).reshape(M, N)
+    err = np.abs(got - ref)
+    assert np.all(err <= 1e-5 * floor + 1e-30), f"max rel {np.max(err / (floor + 1e-30))}"
+
+
+@pytest.mark.parametrize("nt", [1, 2, 4])
+@pytest.mark.parametrize("M", [16, 64])
+def test_gemm_mfma_tile_counts_agree(hip, nt, M):
+    N, K = 200, 2048
+    say(f"case: gemm mfma nt={nt} M={M}")
+    rng = np.random.default_rng(91 + M)
+    xs, ws, scale, ref, floor = _gemv_case(hip, rng, DT_FP8, M, N, K)
+    y = hip.Buffer(M * N * 4)
+    hip.builtin("gemv", [y, up(hip, xs), up(hip, ws), up(hip, scale)], m=M, n=N, k=K,
+                wt=DT_FP8, xt=DT_BF16, yt=DT_F32, epi=0, path=2, r=nt)
+    got = y.read(np.float32).reshape(M, N)
+    assert np.all(np.abs(got - ref) <= 1e-5 * floor)
+
+
+@pytest.mark.parametrize("M", [5, 16, 40])
+def test_gemm_mfma_epilogues(hip, M):
+    """Residual (in place), SwiGLU, GELU+bias and q/k RoPE + KV append through
+    the MFMA path, each against the oracle GEMV output finished on the host
+    with the same rounding points."""
+    say(f"case: gemm mfma epilogues M={M}")
+    rng = np.random.default_rng(300 + M)
+    N, K = 256, 512
+    # residual, bf16 weights
+    xs, ws, _, ref, floor = _gemv_case(hip, rng, DT_BF16, M, N, K)
+    rs, rf = rand_store(rng, (M, N), DT_BF16)
+    y = up(hip, rs)
+    hip.builtin("gemv", [y, up(hip, xs), up(hip, ws), y], m=M, n=N, k=K, wt=DT_BF16,
+                xt=DT_BF16, yt=DT_BF16, epi=1)
+    got = O.decode(y.read(np.uint16), DT_BF16).reshape(M, N)
+    assert np.all(_close16(got, _rb(rf + _rb(ref)), floor + np.abs(rf)))
+    # swiglu, fp8 weights
+    F = 192
+    xs, ws, scale, ref, floor = _gemv_case(hip, rng, DT_FP8, M, 2 * F, K)
+    y = hip.Buffer(M * F * 2)
+    hip.builtin("gemv", [y, up(hip, xs), up(hip, ws), up(hip, scale)], m=M, n=2 * F, k=K,
+                wt=DT_FP8, xt=DT_BF16, yt=DT_BF16, epi=2)
+    got = O.decode(y.read(np.uint16), DT_BF16).reshape(M, F)
+    g, u = _rb(ref[:, 0::2]), _rb(ref[:, 1::2])
+    assert np.all(_close16(got, _rb(g / (1 + np.exp(-g)) * u), floor[:, 0::2] + floor[:, 1::2]))
+    # gelu + bias, fp16
+    xs, ws, _, ref, floor = _gemv_case(hip, rng, DT_F16, M, N, K, xdt=DT_F16)
+    bs, bf = rand_store(rng, (N,), DT_F16, 0.1)
+    y = hip.Buffer(M * N * 2)
+    hip.builtin("gemv", [y, up(hip, xs), up(hip, ws), up(hip, bs)], m=M, n=N, k=K, wt=DT_F16,
+                xt=DT_F16, yt=DT_F16, epi=3, bias=1)
+    got = O.decode(y.read(np.uint16), DT_F16).reshape(M, N)
+    v = O.decode(O.encode((ref + bf[None, :]).astype(np.float32), DT_F16), DT_F16)
+    want = 0.5 * v * (1 + np.tanh(0.7978845608 * (v + 0.044715 * v ** 3)))
+    assert np.all(np.abs(got - want) <= 2.0 ** -10 * np.abs(want) + 2e-5 * floor + 1e-4)
+    # q/k rope + kv append, fp8
+    H, Hkv, hd, ms, pos = 4, 2, 64, 32, 9
+    Nq = (H + 2 * Hkv) * hd
+    xs, ws, scale, ref, floor = _gemv_case(hip, rng, DT_FP8, M, Nq, K)
+    half = hd // 2
+    f = 1.0 / (500000.0 ** (np.arange(half) * 2.0 / hd))
+    ang = np.arange(ms)[:, None] * f[None, :]
+    cs, sn = np.cos(ang).astype(np.float32), np.sin(ang).astype(np.float32)
+    q = hip.Buffer(M * H * hd * 2)
+    kc, vc = hip.Buffer(M * Hkv * ms * hd * 2), hip.Buffer(M * Hkv * ms * hd * 2)
+    L = up(hip, np.array([pos + 1], np.int32))
+    hip.builtin("gemv", [q, up(hip, xs), up(hip, ws), up(hip, scale), up(hip, cs), up(hip, sn), L,
+                         kc, vc], m=M, n=Nq, k=K, wt=DT_FP8, xt=DT_BF16, yt=DT_BF16, epi=4, h=H,
+                hkv=Hkv, hd=hd, maxseq=ms)
+    v = _rb(ref)
+    c, s = cs[pos], sn[pos]
+    ro = v.copy()
+    nr = (H + Hkv) * hd
+    j = (np.arange(0, nr, 2) % hd) // 2
+    ro[:, 0:nr:2] = _rb(v[:, 0:nr:2] * c[j] - v[:, 1:nr:2] * s[j])
+    ro[:, 1:nr:2] = _rb(v[:, 1:nr:2] * c[j] + v[:, 0:nr:2] * s[j])
+    gq = O.decode(q.read(np.uint16), DT_BF16).reshape(M, H * hd)
+    gk = O.decode(kc.read(np.uint16), DT_BF16).reshape(M, Hkv, ms, hd)[:, :, pos].reshape(M, -1)
+    gv = O.decode(vc.read(np.uint16), DT_BF16).reshape(M, Hkv, ms, hd)[:, :, pos].reshape(M, -1)
+    got = np.concatenate([gq, gk, gv], 1)
+    assert np.all(_close16(got, ro, floor * 2 + 1e-3)), np.max(np.abs(got - ro))
+    assert not np.any(kc.read(np.uint16).reshape(M, Hkv, ms, hd)[:, :, pos + 1:])
+
+
+@pytest.mark.parametrize("NK", [(4096, 4096), (14336, 4096), (50257, 768)])
+@pytest.mark.parametrize("M", [8, 64])
+def test_gemm_mfma_c2_shapes(hip, NK, M):
+    """The single-op sweep's fp16 GEMM shapes at full size (W N(0,0.02), x
+    N(0,1)), against a float64 product; the f32-accumulation bar is 1e-5 of
+    sum|x||w| per output."""
+    N, K = NK
+    say(f"case: gemm c2 fp16 M={M} N={N} K={K}")
+    rng = np.random.default_rng(N + M)
+    xs = O.encode(rng.standard_normal((M, K)).astype(np.float32), DT_F16)
+    ws = O.encode((rng.standard_normal((N, K)) * 0.02).astype(np.float32), DT_F16)
+    xf, wf = O.decode(xs, DT_F16).astype(np.float64), O.decode(ws, DT_F16).astype(np.float64)
+    want = xf @ wf.T
+    floor = np.abs(xf) @ np.abs(wf).T
+    y = hip.Buffer(M * N * 4)
+    hip.builtin("gemv", [y, up(hip, xs), up(hip, ws)], m=M, n=N, k=K, wt=DT_F16, xt=DT_F16,
+                yt=DT_F32, epi=0)
+    got = y.read(np.float32).reshape(M, N).astype(np.float64)
+    assert np.all(np.abs(got - want) <= 1e-5 * floor)
+
+
 def test_gemv_rejects_bad_shapes(hip):
     say("case: gemv argument validation (host-side errors, no launch)")
     y, x, w = hip.Buffer(64), hip.Buffer(64), hip.Buffer(64)

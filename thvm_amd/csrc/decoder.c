@@ -193,8 +193,21 @@ static int cfg_check(const ThvmDecodeConfig *c) {
   u32 hkv = c->n_kv_heads ? c->n_kv_heads : c->n_heads;
   if (c->n_heads % hkv) { hb_set_error("decoder: n_heads %% n_kv_heads != 0"); return -1; }
   if (c->head_dim != 64 && c->head_dim != 128) { hb_set_error("decoder: head_dim must be 64 or 128"); return -1; }
-  if (c->batch > 4) { hb_set_error("decoder: batch %u > 4 needs the small-M GEMM path", c->batch); return -1; }
   u32 wdt = c->wdtype, adt = c->adtype;
+  if (c->batch > 64) { hb_set_error("decoder: batch %u > 64", c->batch); return -1; }
+  if (c->batch > 4) {   /* projections run on the MFMA GEMM */
+    int ok = (wdt == THVM_DT_FP8E4M3 && (adt == THVM_DT_BF16 || adt == THVM_DT_FP16)) ||
+             (wdt == THVM_DT_BF16 && adt == THVM_DT_BF16) || (wdt == THVM_DT_FP16 && adt == THVM_DT_FP16);
+    if (!ok) {
+      hb_set_error("decoder: batch %u > 4 runs the MFMA GEMM, which takes fp8 weights with bf16/fp16 "
+                   "activations or 16-bit weights of the activation dtype", c->batch);
+      return -1;
+    }
+    if (c->dim % 64 || (c->n_heads * c->head_dim) % 64 || c->ffn % 64) {
+      hb_set_error("decoder: batch %u > 4 needs dim, heads*head_dim and ffn multiples of 64", c->batch);
+      return -1;
+    }
+  }
   if (wdt != THVM_DT_FP32 && wdt != THVM_DT_FP16 && wdt != THVM_DT_BF16 && wdt != THVM_DT_FP8E4M3) {
     hb_set_error("decoder: weight dtype %u unsupported", wdt);
     return -1;
@@ -288,14 +301,15 @@ static int op_attn(Decoder *d, u32 l) {
 }
 
 /* The norm feeding a GEMV: fused into the GEMV's x staging (default), or as
- * a separate norm kernel writing xn (THVM_HIP_UNFUSED_NORM=1, for A/B).
+ * a separate norm kernel writing xn (batches above 4 rows, whose projections
+ * run on the MFMA GEMM, or THVM_HIP_UNFUSED_NORM=1 for A/B).
  * Writes the GEMV's input id to *gin and its norm spec fragment to nspec;
  * gains are appended to the GEMV's argument list by the caller via gargs. */
 typedef struct { int kind; u32 g, b; } NormSpec;
 
-static int fused_norms(void) {
+static int fused_norms(const Decoder *d) {
   const char *e = getenv("THVM_HIP_UNFUSED_NORM");
-  return !(e && e[0] == '1');
+  return d->c.batch <= 4 && !(e && e[0] == '1');
 }
 
 static int emit_norm(Decoder *d, const NormSpec *ns, u32 *gin, char *nspec, size_t nlen,
@@ -303,7 +317,7 @@ static int emit_norm(Decoder *d, const NormSpec *ns, u32 *gin, char *nspec, size
   const ThvmDecodeConfig *c = &d->c;
   u32 x = tens_find(d, "x"), xn = tens_find(d, "xn");
   *ng = 0;
-  if (fused_norms()) {
+  if (fused_norms(d)) {
     snprintf(nspec, nlen, " norm=%d eps=%a", ns->kind, c->eps);
     gargs[(*ng)++] = ns->g;
     if (ns->kind == 2) gargs[(*ng)++] = ns->b;

@@ -169,7 +169,8 @@ int hb_builtin_launch(const char *program, const u32 *ids, u32 n, int check_only
          spec_u32(&sp, "norm", &a.norm, 0, 0) || spec_f32(&sp, "eps", &a.norm_eps, 0, 1e-6f) ||
          spec_u32(&sp, "ngain", &ngain, 0, 1) || spec_u32(&sp, "nbias", &nbias, 0, a.norm == 2) ||
          spec_u32(&sp, "waves", &a.tune_waves, 0, 0) || spec_u32(&sp, "r", &a.tune_r, 0, 0) ||
-         spec_u32(&sp, "u", &a.tune_u, 0, 0) || spec_u32(&sp, "blocks", &a.tune_blocks, 0, 0));
+         spec_u32(&sp, "u", &a.tune_u, 0, 0) || spec_u32(&sp, "blocks", &a.tune_blocks, 0, 0) ||
+         spec_u32(&sp, "path", &a.tune_path, 0, 0));
     {
       u32 ldy0 = a.epi == THVM_EPI_SWIGLU ? a.N / 2
                : (a.epi == THVM_EPI_QKV || a.epi == THVM_EPI_QKV_ROPE) ? a.n_heads * a.head_dim

@@ -57,11 +57,16 @@ typedef struct ThvmGemvArgs {
   float    norm_eps;
   const float *norm_w;     /* [K] gain or NULL                                */
   const float *norm_b;     /* [K] LayerNorm bias or NULL                      */
-  /* launch tuning (0 = heuristic): waves per block, rows per wave, chunks per
-   * lane in flight, grid blocks */
-  uint32_t tune_waves, tune_r, tune_u, tune_blocks;
+  /* launch tuning (0 = heuristic): waves per block, rows per wave (MFMA path:
+   * 16-row weight tiles per block), chunks per lane in flight, grid blocks,
+   * path (1 GEMV, 2 MFMA GEMM; 0 picks the MFMA GEMM for M > 4) */
+  uint32_t tune_waves, tune_r, tune_u, tune_blocks, tune_path;
 } ThvmGemvArgs;
+/* y = epi(x . W^T): the GEMV for M <= 4, the MFMA GEMM for M <= 64 (fp16 W
+ * with fp16 x, bf16 W with bf16 x, fp8 W with bf16/fp16 x; K % 64 == 0; no
+ * fused norm). */
 int thvm_k_gemv(const ThvmGemvArgs *a, hipStream_t s, char *err, int errlen);
+int thvm_k_gemm_mfma(const ThvmGemvArgs *a, hipStream_t s, char *err, int errlen);
 
 /* Row norms over [M, K]: RMSNorm (y = rnd((x*inv)*w), inv=1/sqrt(ss/K+eps))
  * or LayerNorm (y = rnd((x-mu)*rsqrt(var+eps)*w + b)).  x may be f32/bf16/f16,

@@ -1,0 +1,129 @@
+// epilogue.h -- output stage shared by the GEMV and the MFMA GEMM: per-row
+// fp8 scale and bias, then store / residual add / GELU / SwiGLU over row
+// pairs / q,k RoPE with KV-cache append at position L-1.  Rounding points
+// follow the reference decode chain (bench/dsv2_decode_bench.c:20-34): a
+// projection output is rounded to the activation dtype before it feeds a
+// residual add, an activation or the rotation.
+#pragma once
+#include "dev_common.h"
+#include "../kern_api.h"
+
+__device__ __forceinline__ float ld_any(const void *p, uint64_t i, uint32_t dt) {
+  switch (dt) {
+    case THVM_DT_FP32: return ((const float *)p)[i];
+    case THVM_DT_BF16: return bf2f(((const bf16_t *)p)[i]);
+    case THVM_DT_FP16: return h2f(((const f16_t *)p)[i]);
+    default: return 0.0f;
+  }
+}
+__device__ __forceinline__ void st_any(void *p, uint64_t i, uint32_t dt, float v) {
+  switch (dt) {
+    case THVM_DT_FP32: ((float *)p)[i] = v; break;
+    case THVM_DT_BF16: ((bf16_t *)p)[i] = f2bf(v); break;
+    case THVM_DT_FP16: ((f16_t *)p)[i] = f2h(v); break;
+    default: break;
+  }
+}
+__device__ __forceinline__ float rnd_any(float v, uint32_t dt) {
+  return dt == THVM_DT_BF16 ? rbf(v) : dt == THVM_DT_FP16 ? rh(v) : v;
+}
+
+// Rows n0..n0+R-1 of batch rows mb..mb+M-1; tot[r][m] is the raw f32 sum.
+template <int R, int M>
+__device__ __forceinline__ void gemv_epilogue(const ThvmGemvArgs &a, const uint32_t n0,
+                                              const float (&tot)[R][M],
+                                              const uint32_t mb = 0) {
+  const uint32_t N = a.N;
+  float v[R][M];
+#pragma unroll
+  for (int r = 0; r < R; r++) {
+    uint32_t n = n0 + r;
+    float s = (a.scale != nullptr && n < N) ? a.scale[n] : 1.0f;
+    float bv = (a.bias != nullptr && n < N) ? ld_any(a.bias, n, a.ydt) : 0.0f;
+#pragma unroll
+    for (int m = 0; m < M; m++) v[r][m] = tot[r][m] * s + bv;
+  }
+  const uint32_t ydt = a.ydt;
+  switch (a.epi) {
+    case THVM_EPI_STORE:
+#pragma unroll
+      for (int r = 0; r < R; r++)
+        if (n0 + r < N)
+#pragma unroll
+          for (int m = 0; m < M; m++)
+            st_any(a.y, (uint64_t)(mb + m) * a.ldy + n0 + r, ydt, v[r][m]);
+      break;
+    case THVM_EPI_RESID:
+#pragma unroll
+      for (int r = 0; r < R; r++)
+        if (n0 + r < N)
+#pragma unroll
+          for (int m = 0; m < M; m++) {
+            uint64_t i = (uint64_t)(mb + m) * a.ldy + n0 + r;
+            float rv = ld_any(a.res, i, ydt);
+            st_any(a.y, i, ydt, rv + rnd_any(v[r][m], ydt));
+          }
+      break;
+    case THVM_EPI_GELU:
+#pragma unroll
+      for (int r = 0; r < R; r++)
+        if (n0 + r < N)
+#pragma unroll
+          for (int m = 0; m < M; m++)
+            st_any(a.y, (uint64_t)(mb + m) * a.ldy + n0 + r, ydt,
+                   gelu_tanh_f(rnd_any(v[r][m], ydt)));
+      break;
+    case THVM_EPI_SWIGLU:
+      if (R % 2 == 0) {
+#pragma unroll
+        for (int r = 0; r + 1 < R; r += 2) {
+          if (n0 + r + 1 >= N) break;
+#pragma unroll
+          for (int m = 0; m < M; m++) {
+            float gg = rnd_any(v[r][m], ydt), uu = rnd_any(v[r + 1][m], ydt);
+            st_any(a.y, (uint64_t)(mb + m) * a.ldy + (n0 + r) / 2, ydt, silu_f(gg) * uu);
+          }
+        }
+      }
+      break;
+    case THVM_EPI_QKV_ROPE:
+    case THVM_EPI_QKV: {
+      if (R % 2) break;
+      const uint32_t hd = a.head_dim;
+      const uint32_t Hq = a.n_heads * hd, Hk = a.n_kv_heads * hd;
+      const int32_t pos = a.len[0] - 1;
+      if (pos < 0 || (uint32_t)pos >= a.max_seq) break;   // no live row to write
+      const bool rope = a.epi == THVM_EPI_QKV_ROPE;
+#pragma unroll
+      for (int r = 0; r + 1 < R; r += 2) {
+        const uint32_t nn = n0 + r;
+        if (nn + 1 >= N) break;
+        const uint32_t d = nn % hd;
+        float c = 1.0f, sn = 0.0f;
+        if (rope && nn < Hq + Hk) {
+          c = a.rope_cos[(uint64_t)pos * (hd / 2) + d / 2];
+          sn = a.rope_sin[(uint64_t)pos * (hd / 2) + d / 2];
+        }
+#pragma unroll
+        for (int m = 0; m < M; m++) {
+          float xe = rnd_any(v[r][m], ydt), xo = rnd_any(v[r + 1][m], ydt);
+          float oe = xe, oo = xo;
+          if (rope && nn < Hq + Hk) { oe = xe * c - xo * sn; oo = xo * c + xe * sn; }
+          if (nn < Hq) {
+            st_any(a.y, (uint64_t)(mb + m) * a.ldy + nn, ydt, oe);
+            st_any(a.y, (uint64_t)(mb + m) * a.ldy + nn + 1, ydt, oo);
+          } else {
+            const bool isk = nn < Hq + Hk;
+            const uint32_t off = isk ? nn - Hq : nn - Hq - Hk;
+            const uint32_t h = off / hd;
+            uint64_t ci = (((uint64_t)(mb + m) * a.n_kv_heads + h) * a.max_seq + (uint32_t)pos) * hd + d;
+            void *cache = isk ? a.kcache : a.vcache;
+            st_any(cache, ci, ydt, oe);
+            st_any(cache, ci + 1, ydt, oo);
+          }
+        }
+      }
+    } break;
+    default: break;
+  }
+}

@@ -26,6 +26,7 @@
 #include "dev_common.h"
 #include "../kern_api.h"
 #include "launch.h"
+#include "epilogue.h"
 #include <stdio.h>
 
 enum { WT_F32 = 0, WT_F16 = 1, WT_BF16 = 2, WT_FP8 = 3 };
@@ -63,26 +64,6 @@ __device__ __forceinline__ void quad_decode<WT_F32>(const uint4 &q, int j, float
   (void)j;
   o[0] = __uint_as_float(q.x); o[1] = __uint_as_float(q.y);
   o[2] = __uint_as_float(q.z); o[3] = __uint_as_float(q.w);
-}
-
-__device__ __forceinline__ float ld_any(const void *p, uint64_t i, uint32_t dt) {
-  switch (dt) {
-    case THVM_DT_FP32: return ((const float *)p)[i];
-    case THVM_DT_BF16: return bf2f(((const bf16_t *)p)[i]);
-    case THVM_DT_FP16: return h2f(((const f16_t *)p)[i]);
-    default: return 0.0f;
-  }
-}
-__device__ __forceinline__ void st_any(void *p, uint64_t i, uint32_t dt, float v) {
-  switch (dt) {
-    case THVM_DT_FP32: ((float *)p)[i] = v; break;
-    case THVM_DT_BF16: ((bf16_t *)p)[i] = f2bf(v); break;
-    case THVM_DT_FP16: ((f16_t *)p)[i] = f2h(v); break;
-    default: break;
-  }
-}
-__device__ __forceinline__ float rnd_any(float v, uint32_t dt) {
-  return dt == THVM_DT_BF16 ? rbf(v) : dt == THVM_DT_FP16 ? rh(v) : v;
 }
 
 // ---- LDS x layout -----------------------------------------------------------
@@ -139,104 +120,6 @@ __device__ __forceinline__ float block_sum_g(float v, float *red, int nwaves) {
 #define XREG 16   /* x elements per thread kept in registers by the staging */
 
 // the output stage of one row group (one lane, wave-uniform values)
-template <int R, int M>
-__device__ __forceinline__ void gemv_epilogue(const ThvmGemvArgs &a, const uint32_t n0,
-                                              const float (&tot)[R][M]) {
-  const uint32_t N = a.N;
-  float v[R][M];
-#pragma unroll
-  for (int r = 0; r < R; r++) {
-    uint32_t n = n0 + r;
-    float s = (a.scale != nullptr && n < N) ? a.scale[n] : 1.0f;
-    float bv = (a.bias != nullptr && n < N) ? ld_any(a.bias, n, a.ydt) : 0.0f;
-#pragma unroll
-    for (int m = 0; m < M; m++) v[r][m] = tot[r][m] * s + bv;
-  }
-  const uint32_t ydt = a.ydt;
-  switch (a.epi) {
-    case THVM_EPI_STORE:
-#pragma unroll
-      for (int r = 0; r < R; r++)
-        if (n0 + r < N)
-#pragma unroll
-          for (int m = 0; m < M; m++)
-            st_any(a.y, (uint64_t)m * a.ldy + n0 + r, ydt, v[r][m]);
-      break;
-    case THVM_EPI_RESID:
-#pragma unroll
-      for (int r = 0; r < R; r++)
-        if (n0 + r < N)
-#pragma unroll
-          for (int m = 0; m < M; m++) {
-            uint64_t i = (uint64_t)m * a.ldy + n0 + r;
-            float rv = ld_any(a.res, i, ydt);
-            st_any(a.y, i, ydt, rv + rnd_any(v[r][m], ydt));
-          }
-      break;
-    case THVM_EPI_GELU:
-#pragma unroll
-      for (int r = 0; r < R; r++)
-        if (n0 + r < N)
-#pragma unroll
-          for (int m = 0; m < M; m++)
-            st_any(a.y, (uint64_t)m * a.ldy + n0 + r, ydt,
-                   gelu_tanh_f(rnd_any(v[r][m], ydt)));
-      break;
-    case THVM_EPI_SWIGLU:
-      if (R % 2 == 0) {
-#pragma unroll
-        for (int r = 0; r + 1 < R; r += 2) {
-          if (n0 + r + 1 >= N) break;
-#pragma unroll
-          for (int m = 0; m < M; m++) {
-            float gg = rnd_any(v[r][m], ydt), uu = rnd_any(v[r + 1][m], ydt);
-            st_any(a.y, (uint64_t)m * a.ldy + (n0 + r) / 2, ydt, silu_f(gg) * uu);
-          }
-        }
-      }
-      break;
-    case THVM_EPI_QKV_ROPE:
-    case THVM_EPI_QKV: {
-      if (R % 2) break;
-      const uint32_t hd = a.head_dim;
-      const uint32_t Hq = a.n_heads * hd, Hk = a.n_kv_heads * hd;
-      const int32_t pos = a.len[0] - 1;
-      if (pos < 0 || (uint32_t)pos >= a.max_seq) break;   // no live row to write
-      const bool rope = a.epi == THVM_EPI_QKV_ROPE;
-#pragma unroll
-      for (int r = 0; r + 1 < R; r += 2) {
-        const uint32_t nn = n0 + r;
-        if (nn + 1 >= N) break;
-        const uint32_t d = nn % hd;
-        float c = 1.0f, sn = 0.0f;
-        if (rope && nn < Hq + Hk) {
-          c = a.rope_cos[(uint64_t)pos * (hd / 2) + d / 2];
-          sn = a.rope_sin[(uint64_t)pos * (hd / 2) + d / 2];
-        }
-#pragma unroll
-        for (int m = 0; m < M; m++) {
-          float xe = rnd_any(v[r][m], ydt), xo = rnd_any(v[r + 1][m], ydt);
-          float oe = xe, oo = xo;
-          if (rope && nn < Hq + Hk) { oe = xe * c - xo * sn; oo = xo * c + xe * sn; }
-          if (nn < Hq) {
-            st_any(a.y, (uint64_t)m * a.ldy + nn, ydt, oe);
-            st_any(a.y, (uint64_t)m * a.ldy + nn + 1, ydt, oo);
-          } else {
-            const bool isk = nn < Hq + Hk;
-            const uint32_t off = isk ? nn - Hq : nn - Hq - Hk;
-            const uint32_t h = off / hd;
-            uint64_t ci = (((uint64_t)m * a.n_kv_heads + h) * a.max_seq + (uint32_t)pos) * hd + d;
-            void *cache = isk ? a.kcache : a.vcache;
-            st_any(cache, ci, ydt, oe);
-            st_any(cache, ci + 1, ydt, oo);
-          }
-        }
-      }
-    } break;
-    default: break;
-  }
-}
-
 // input x dtype (compile time): vector loads of 16 bytes
 enum { XD_BF16 = 0, XD_F16 = 1, XD_F32 = 2 };
 template <int XD> struct XDr { static constexpr int VE = XD == XD_F32 ? 4 : 8, B = XD == XD_F32 ? 4 : 2; };
@@ -526,8 +409,8 @@ extern "C" int thvm_k_gemv(const ThvmGemvArgs *a, hipStream_t s, char *err, int 
     snprintf(err, errlen, "gemv: unsupported dtypes w=%u x=%u y=%u", a->wdt, a->xdt, a->ydt);
     return -1;
   }
-  if (a->M < 1 || a->M > 4 || a->N == 0 || a->K == 0) {
-    snprintf(err, errlen, "gemv: M=%u N=%u K=%u out of range (M in 1..4)", a->M, a->N, a->K);
+  if (a->M < 1 || a->M > 64 || a->N == 0 || a->K == 0) {
+    snprintf(err, errlen, "gemv: M=%u N=%u K=%u out of range (M in 1..64)", a->M, a->N, a->K);
     return -1;
   }
   if (((uint64_t)a->K * wsz) % 16 != 0) {
@@ -592,6 +475,15 @@ extern "C" int thvm_k_gemv(const ThvmGemvArgs *a, hipStream_t s, char *err, int 
     default:
       snprintf(err, errlen, "gemv: unknown epilogue %u", a->epi);
       return -1;
+  }
+  // path: the MFMA GEMM for batches above 4 rows (or x too large for LDS
+  // staging), the GEMV otherwise; tune_path 1/2 forces GEMV/MFMA
+  if (a->tune_path > 2) { snprintf(err, errlen, "gemv: path must be 0, 1 or 2"); return -1; }
+  {
+    const uint64_t xlds = (uint64_t)a->M * a->K * ((a->xdt == THVM_DT_FP32 || a->wdt == THVM_DT_FP32) ? 4 : 2);
+    const bool mfma = a->tune_path == 2 || (a->tune_path == 0 && (a->M > 4 || xlds > 160 * 1024));
+    if (mfma) return thvm_k_gemm_mfma(a, s, err, errlen);
+    if (a->M > 4) { snprintf(err, errlen, "gemv: the GEMV path takes M <= 4 (M=%u)", a->M); return -1; }
   }
   if (a->tune_r) {
     if (a->tune_r != 1 && a->tune_r != 2) { snprintf(err, errlen, "gemv: r must be 1 or 2"); return -1; }
