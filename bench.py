@@ -1,20 +1,27 @@
-"""Decode throughput of the MI355X DEV=hip device on the BASELINE.json metric:
-batch-1 decode tokens/s of the Llama-8B-shape fp8 model (config C4) and the
-achieved HBM bandwidth of its dominant kernel (the fp8 GEMV) against 8 TB/s.
+"""Decode throughput of the MI355X DEV=hip device on the BASELINE.json metric.
 
-One "step" is one greedy decode token: one hipGraph replay of the captured
-decode step (32 layers: RMSNorm, fused QKV GEMV + RoPE + KV append,
-split-sequence flash-decode attention, O GEMV + residual, RMSNorm, gate/up
-GEMV + SwiGLU, down GEMV + residual; final norm, LM head, argmax, position
-bump).  Weights are synthetic N(0, 0.02) quantised per row to fp8 e4m3
-(scale = absmax/448), the KV cache is prefilled with N(0, 1) bf16 rows up to
-context 2048, all generated on the device from a fixed seed.
+Default (the headline line): batch-1 greedy decode of the Llama-8B-shape fp8
+model (config C4) in tokens/s, with the achieved HBM bandwidth of its dominant
+kernel (the fp8 GEMV) against 8 TB/s.  `--config` selects another workload:
 
-Prints ONE JSON line (see the contract in the repository's build brief).
-The cpu_baseline leg times the CPU oracle (oracle/oracle.c, a port of the
-reference CPU path) on one core on a bounded sample: 2 decode steps of the
-same model at the same context, on weights read back from the device; it also
-checks that those steps' greedy ids equal the device's."""
+  C1  GPT-2 small fp32 (12L, D768, V50257), context 16, batch 1
+  C2  single-op sweep: fp16 GEMV/GEMM (M 1/8/64) at the three weight shapes,
+      fp16 softmax and RMSNorm over [M, 4096]
+  C3  GPT-2 XL fp16 (48L, D1600, H25, F6400, V50257), context 128, batch 1 or 8
+  C4  Llama-8B shape fp8 weight-only, bf16 activations, context 2048, batch 1 or 16
+
+One "step" is one greedy decode token for every batch row: one hipGraph
+replay of the captured decode step (embedding, per-layer norm + projections +
+RoPE/KV append + split-sequence attention + residuals + FFN, final norm, LM
+head, argmax, position bump).  Weights are synthetic N(0, 0.02) (fp8: per-row
+absmax/448 e4m3), the KV cache is prefilled with N(0, 1) rows up to the
+context, all generated on the device from fixed seeds.
+
+Prints ONE JSON line per run.  The cpu_baseline leg times the CPU oracle
+(oracle/oracle.c, the restatement of the reference CPU path) on one core on a
+bounded sample of steps of the same model at the same context, on weights
+read back from the device, in lockstep with the device (its greedy ids are
+checked equal)."""
 from __future__ import annotations
 
 import argparse
@@ -30,11 +37,26 @@ sys.path.insert(0, str(ROOT))
 
 METRIC = "decode tokens/s at batch 1 and achieved HBM GB/s vs 8 TB/s peak (8B fp8)"
 PEAK_GBS = 8000.0
+DT_FP8, DT_F16, DT_BF16, DT_F32 = 9, 11, 12, 13
+DT_NAME = {DT_FP8: "fp8e4m3", DT_F16: "fp16", DT_BF16: "bf16", DT_F32: "fp32"}
 
-C4 = dict(arch=1, n_layers=32, dim=4096, n_heads=32, n_kv_heads=8, head_dim=128, ffn=14336,
-          vocab=128256, batch=1, wdtype=9, adtype=12, eps=1e-5, rope_theta=500000.0,
-          init_std=0.02)
-CTX = 2048
+MODELS = {
+    "C1": dict(cfg=dict(arch=2, n_layers=12, dim=768, n_heads=12, n_kv_heads=12, head_dim=64,
+                        ffn=3072, vocab=50257, wdtype=DT_F32, adtype=DT_F32, eps=1e-5,
+                        init_std=0.02),
+               ctx=16, cpu_steps=4,
+               name="C1 GPT-2 small fp32 greedy decode, context 16 (prompt length)"),
+    "C3": dict(cfg=dict(arch=2, n_layers=48, dim=1600, n_heads=25, n_kv_heads=25, head_dim=64,
+                        ffn=6400, vocab=50257, wdtype=DT_F16, adtype=DT_F16, eps=1e-5,
+                        init_std=0.02),
+               ctx=128, cpu_steps=2,
+               name="C3 GPT-2 XL-shape fp16 greedy decode, KV prefilled to context 128 (prompt length)"),
+    "C4": dict(cfg=dict(arch=1, n_layers=32, dim=4096, n_heads=32, n_kv_heads=8, head_dim=128,
+                        ffn=14336, vocab=128256, wdtype=DT_FP8, adtype=DT_BF16, eps=1e-5,
+                        rope_theta=500000.0, init_std=0.02),
+               ctx=2048, cpu_steps=2,
+               name="C4 Llama-8B-shape fp8 weight-only decode, KV prefilled to context 2048"),
+}
 
 
 def log(*a):
@@ -51,34 +73,20 @@ def cpu_model_name() -> str:
     return platform.processor() or "unknown"
 
 
-def gemv_bytes_per_step(cfg) -> int:
-    """Algorithmic bytes of the GEMV launches of one step: every fp8 weight
-    byte and f32 scale read once, x read, y written (B rows)."""
-    D, H, Hkv, hd, F, V, B = (cfg[k] for k in ("dim", "n_heads", "n_kv_heads", "head_dim", "ffn",
-                                                "vocab", "batch"))
-    shapes = [((H + 2 * Hkv) * hd, D, (H + 2 * Hkv) * hd), (D, H * hd, 2 * D), (2 * F, D, F),
-              (D, F, 2 * D)]
-    tot = 0
-    for N, K, ycols in shapes:                     # ycols: output elements (resid reads+writes)
-        tot += N * K + 4 * N + 2 * B * K + 2 * B * ycols
-    tot *= cfg["n_layers"]
-    tot += V * D + 4 * V + 2 * B * D + 4 * B * V   # LM head (f32 logits)
-    return tot
-
-
 def attn_bytes_per_step(cfg, L) -> int:
-    """K and V rows [0, L) of every layer (bf16) plus q read and out written."""
+    """K and V rows [0, L) of every layer and batch row, plus q read and the
+    attention output written."""
     B, Hkv, hd, H = cfg["batch"], cfg["n_kv_heads"], cfg["head_dim"], cfg["n_heads"]
-    return cfg["n_layers"] * B * (2 * Hkv * L * hd * 2 + 2 * H * hd * 2)
+    es = 4 if cfg["adtype"] == DT_F32 else 2
+    return cfg["n_layers"] * B * (2 * Hkv * L * hd * es + 2 * H * hd * es)
 
 
-def cpu_baseline(thvm, dec, cfg, n_steps: int):
+def cpu_baseline(dec, cfg, n_steps: int):
     """Oracle decode on 1 core from the device's current state; returns
-    (tokens/s, ids_match, seconds, sample description)."""
+    (tokens/s, ids_match, seconds, max logit error relative to max|logit|)."""
     sys.path.insert(0, str(ROOT / "tests"))
     import numpy as np
     import _oracle as O
-    os.environ.setdefault("OMP_NUM_THREADS", "1")
     pos = dec.position
     tok = dec.tokens(pos + 1)[:, pos].astype(np.int32)
     t_read = time.time()
@@ -97,10 +105,178 @@ def cpu_baseline(thvm, dec, cfg, n_steps: int):
         errs.append(float(np.abs(glg - olg).max() / np.abs(olg).max()))
         match = match and bool(np.array_equal(gnx, onx))
         log(f"[bench] cpu oracle step {s}: {t_cpu:.1f}s cumulative, logits rel err {errs[-1]:.2e}, "
-            f"ids gpu={gnx.tolist()} oracle={onx.tolist()}")
+            f"ids equal {bool(np.array_equal(gnx, onx))}")
         cur = gnx.astype(np.int32)                 # lockstep on the device's token
-    tps = cfg["batch"] * n_steps / t_cpu
-    return tps, match, t_cpu, max(errs)
+    return cfg["batch"] * n_steps / t_cpu, match, t_cpu, max(errs)
+
+
+def run_decode(thvm, key: str, batch: int, args) -> dict:
+    spec = MODELS[key]
+    cfg = dict(spec["cfg"], batch=batch)
+    if args.layers:
+        cfg["n_layers"] = args.layers
+    ctx = spec["ctx"]
+    cpu_steps = 0 if args.no_cpu else (args.cpu_steps or (spec["cpu_steps"] if batch <= 4 else 1))
+    cfg["max_seq"] = ((ctx + args.warmup + args.steps + cpu_steps + 4 + 63) // 64) * 64
+    t0 = time.time()
+    dec = thvm.Decoder(seed=1234, **cfg)
+    dec.prefill_synthetic(ctx, seed=99)
+    dec.set_state(list(range(1, batch + 1)), ctx)
+    thvm.synchronize()
+    log(f"[bench] {key} B={batch}: model built in {time.time() - t0:.1f}s, {dec.step_kernels()} "
+        f"kernels/step, {thvm.lib().thvm_hip_mem_live_bytes() / 1e9:.2f} GB on device")
+
+    dec.capture()                                  # step 1 (eager, recorded)
+    dec.replay(max(args.warmup, 1))                # graph capture + warmup
+    thvm.synchronize()
+    L_mid = dec.position + args.steps // 2 + 1
+    t = thvm.lib().thvm_hip_timer_start()
+    t_wall = time.perf_counter()
+    dec.replay(args.steps)
+    ms = thvm.lib().thvm_hip_timer_stop(t)
+    wall = time.perf_counter() - t_wall
+    ms_per_step = ms / args.steps
+    tps = batch * args.steps / (ms / 1000.0)
+    log(f"[bench] timed {args.steps} steps: {ms_per_step:.3f} ms/step (wall {wall * 1000 / args.steps:.3f})")
+
+    # live per-kernel timing: a bounded sleep kernel (~10 ms) goes first so the
+    # host enqueues whole eager steps behind it and they run back to back; each
+    # builtin launch carries a hipEvent pair bound to its kernels' own start and
+    # end (hipExtLaunchKernel)
+    dummy = thvm.Buffer(64)
+    prof_steps = 2
+    thvm.kprof(True)
+    thvm.kprof_reset()
+    for _ in range(prof_steps):
+        thvm.builtin("delay", [dummy], n=3000)
+        dec.step()
+    g_ms, g_n = thvm.kprof_query("gemv")
+    g_bytes = thvm.kprof_bytes("gemv")
+    a_ms, a_n = thvm.kprof_query("attn")
+    thvm.kprof(False)
+    dummy.free()
+    L_prof = dec.position - 1
+    gemv_gbs = g_bytes / (g_ms / 1000.0) / 1e9
+    attn_gbs = attn_bytes_per_step(cfg, L_prof) * prof_steps / (a_ms / 1000.0) / 1e9
+    log(f"[bench] gemv: {g_n} launches, {g_ms / g_n * 1000:.1f} us avg, {gemv_gbs:.0f} GB/s; "
+        f"attn: {a_n} launches, {a_ms / a_n * 1000:.1f} us avg, {attn_gbs:.0f} GB/s")
+    step_bytes = g_bytes // prof_steps + attn_bytes_per_step(cfg, L_mid)
+
+    cpu = None
+    if cpu_steps:
+        tps_cpu, match, secs, lerr = cpu_baseline(dec, cfg, cpu_steps)
+        cpu = {"value": round(tps_cpu, 4), "unit": "tokens/s", "cores": 1, "kind": "port",
+               "sample": f"{cpu_steps} greedy decode steps x batch {batch} of the same model at "
+                         f"context ~{dec.position - cpu_steps}, oracle/oracle.c or_decode_step on "
+                         f"one core of {cpu_model_name()} ({os.cpu_count()} visible), in lockstep "
+                         f"with the device on the same inputs",
+               "seconds": round(secs, 2), "ids_match": match, "logits_max_rel_err": lerr}
+    mfma = batch > 4
+    gkern = ("k_gemm (MFMA v_mfma_f32_16x16x32, %s weights)" if mfma else
+             "k_gemv (%s weight GEMV)") % DT_NAME[cfg["wdtype"]]
+    out = {
+        "metric": METRIC, "value": round(tps, 2), "unit": "tokens/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": f"{DT_NAME[cfg['wdtype']]} weights x {DT_NAME[cfg['adtype']]} activations, "
+                 "f32 accumulate",
+        "data": "synthetic",
+        "config": {"workload": f"{spec['name']}, batch {batch}, greedy, hipGraph replay per token",
+                   "layers": cfg["n_layers"], "d_model": cfg["dim"], "heads": cfg["n_heads"],
+                   "kv_heads": cfg["n_kv_heads"], "head_dim": cfg["head_dim"], "ffn": cfg["ffn"],
+                   "vocab": cfg["vocab"], "batch": batch, "context": ctx,
+                   "parallelism": "single GPU"},
+        "roofline": {"bound": "hbm", "achieved": round(gemv_gbs, 1), "peak": PEAK_GBS,
+                     "unit": "GB/s", "frac": round(gemv_gbs / PEAK_GBS, 4),
+                     "traffic": (measured_traffic() if key == "C4" and batch == 1 and not args.layers
+                                 else None),
+                     "kernel": gkern,
+                     "algorithmic_bytes_per_launch": g_bytes // max(g_n, 1),
+                     "launches_per_step": g_n // prof_steps,
+                     "avg_launch_us": round(g_ms / g_n * 1000, 2)},
+        "attention": {"achieved_gbs": round(attn_gbs, 1), "frac": round(attn_gbs / PEAK_GBS, 4),
+                      "avg_launch_us": round(a_ms / max(a_n, 1) * 1000, 2)},
+        "step_hbm_gbs": round(step_bytes / (ms_per_step / 1000.0) / 1e9, 1),
+        "step_bytes": step_bytes,
+        "kernels_per_step": dec.step_kernels(),
+        "cpu_baseline": cpu,
+    }
+    if args.layers:
+        out["config"]["note"] = "DEBUG: reduced layer count, not the configured model"
+    dec.close()
+    return out
+
+
+def run_c2(thvm, args) -> dict:
+    """Single-op sweep: each op launched `reps` times back to back behind a
+    sleep kernel, kernel time from the event pairs bound to each launch."""
+    import numpy as np
+    rng = np.random.default_rng(7)
+    reps = 20
+    ops = []
+
+    def timed(tag, fn):
+        dummy = thvm.Buffer(64)
+        fn()                                       # warm (code object load)
+        thvm.synchronize()
+        thvm.kprof(True)
+        thvm.kprof_reset()
+        thvm.builtin("delay", [dummy], n=1000)
+        for _ in range(reps):
+            fn()
+        ms, n = thvm.kprof_query(tag)
+        nb = thvm.kprof_bytes(tag)
+        thvm.kprof(False)
+        dummy.free()
+        return ms / n * 1000.0, nb / n
+
+    def f16(a):
+        return a.astype(np.float16).view(np.uint16)
+
+    for N, K in ((4096, 4096), (14336, 4096), (50257, 768)):
+        w = thvm.Buffer.from_numpy(f16(rng.standard_normal((N, K), np.float32) * 0.02))
+        for M in (1, 8, 64):
+            x = thvm.Buffer.from_numpy(f16(rng.standard_normal((M, K), np.float32)))
+            y = thvm.Buffer(M * N * 4)
+            us, nb = timed("gemv", lambda: thvm.builtin("gemv", [y, x, w], m=M, n=N, k=K, wt=DT_F16,
+                                                        xt=DT_F16, yt=DT_F32, epi=0))
+            gbs = nb / (us * 1e-6) / 1e9
+            ops.append({"op": "gemv" if M <= 4 else "gemm_mfma", "N": N, "K": K, "M": M,
+                        "us": round(us, 2), "bytes": int(nb), "gbs": round(gbs, 1),
+                        "frac": round(gbs / PEAK_GBS, 4),
+                        "tflops": round(2.0 * M * N * K / (us * 1e-6) / 1e12, 2)})
+            x.free()
+            y.free()
+        w.free()
+    K = 4096
+    g = thvm.Buffer.from_numpy(np.ones(K, np.float32))
+    for M in (1, 8, 64):
+        x = thvm.Buffer.from_numpy(f16(rng.standard_normal((M, K), np.float32)))
+        y = thvm.Buffer(M * K * 2)
+        us, nb = timed("softmax", lambda: thvm.builtin("softmax", [y, x], m=M, k=K, xt=DT_F16,
+                                                       yt=DT_F16))
+        ops.append({"op": "softmax", "M": M, "K": K, "us": round(us, 2), "bytes": int(nb),
+                    "gbs": round(nb / (us * 1e-6) / 1e9, 1)})
+        us, nb = timed("norm", lambda: thvm.builtin("norm", [y, x, g], m=M, k=K, xt=DT_F16,
+                                                    yt=DT_F16, eps=1e-6))
+        ops.append({"op": "rmsnorm", "M": M, "K": K, "us": round(us, 2), "bytes": int(nb),
+                    "gbs": round(nb / (us * 1e-6) / 1e9, 1)})
+        x.free()
+        y.free()
+    g.free()
+    mats = [o for o in ops if o["op"] in ("gemv", "gemm_mfma")]
+    best = max(mats, key=lambda o: o["gbs"])
+    return {"metric": "C2 single-op sweep: kernel time and achieved HBM GB/s vs 8 TB/s",
+            "value": best["gbs"], "unit": "GB/s (best GEMV/GEMM)", "n_gpus": 1, "steps": reps,
+            "warmup": 1, "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+            "dtype": "fp16 in, f32 accumulate", "data": "synthetic",
+            "config": {"workload": "C2 fp16 GEMV/GEMM y=x.W^T (N,K) in {(4096,4096),(14336,4096),"
+                                   "(50257,768)}, M in {1,8,64}; softmax and RMSNorm eps 1e-6 over "
+                                   "[M,4096] fp16"},
+            "roofline": {"bound": "hbm", "achieved": best["gbs"], "peak": PEAK_GBS, "unit": "GB/s",
+                         "frac": best["frac"], "traffic": None,
+                         "kernel": f"{best['op']} N={best['N']} K={best['K']} M={best['M']}"},
+            "ops": ops, "cpu_baseline": None}
 
 
 COPY_BYTES = 1 << 30
@@ -123,14 +299,13 @@ def copy_calibration(thvm) -> int:
     print(json.dumps({"calibration": "copy", "bytes_read": COPY_BYTES, "bytes_written": COPY_BYTES,
                       "launches": n, "avg_launch_us": round(us, 2),
                       "gbs": round(2 * COPY_BYTES / (us * 1e-6) / 1e9, 1)}), flush=True)
-    thvm.shutdown()
     return 0
 
 
 def measured_traffic():
-    """HBM bytes per k_gemv launch from the committed counter passes
-    (FETCH_SIZE, WRITE_SIZE, each scaled by the plain-copy calibration), or
-    None when that summary is absent."""
+    """HBM bytes per k_gemv launch of the C4 batch-1 step from the committed
+    counter passes (FETCH_SIZE, WRITE_SIZE, each scaled by the plain-copy
+    calibration), or None when that summary is absent."""
     p = ROOT / "profiles" / "gemv_fp8_c4_traffic.json"
     try:
         return int(json.loads(p.read_text())["traffic_bytes_per_launch"])
@@ -143,7 +318,9 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=64)
     ap.add_argument("--warmup", type=int, default=4)
-    ap.add_argument("--cpu-steps", type=int, default=2)
+    ap.add_argument("--config", default="C4", choices=["C1", "C2", "C3", "C4", "all"])
+    ap.add_argument("--batch", type=int, default=1)
+    ap.add_argument("--cpu-steps", type=int, default=0, help="oracle steps (0: the config's default)")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--layers", type=int, default=None, help="debug only: fewer layers (invalid metric)")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -157,100 +334,18 @@ def main() -> int:
 
     import thvm_amd as thvm
     thvm.init()
-    if args.copy_calibration:
-        return copy_calibration(thvm)
-    cfg = dict(C4)
-    if args.layers:
-        cfg["n_layers"] = args.layers
-    cfg["max_seq"] = ((CTX + args.warmup + args.steps + args.cpu_steps + 2 + 63) // 64) * 64
-    t0 = time.time()
-    dec = thvm.Decoder(seed=1234, **cfg)
-    dec.prefill_synthetic(CTX, seed=99)
-    dec.set_state([1], CTX)
-    thvm.synchronize()
-    log(f"[bench] model built in {time.time() - t0:.1f}s, {dec.step_kernels()} kernels/step, "
-        f"{thvm.lib().thvm_hip_mem_live_bytes() / 1e9:.2f} GB on device")
-
-    slot = dec.capture()                           # step 1 (eager, recorded)
-    dec.replay(max(args.warmup, 1))                # graph capture + warmup
-    thvm.synchronize()
-    pos0 = dec.position
-    L_mid = pos0 + args.steps // 2 + 1
-    step_bytes = gemv_bytes_per_step(cfg) + attn_bytes_per_step(cfg, L_mid)
-
-    t = thvm.lib().thvm_hip_timer_start()
-    t_wall = time.perf_counter()
-    dec.replay(args.steps)
-    ms = thvm.lib().thvm_hip_timer_stop(t)
-    wall = time.perf_counter() - t_wall
-    ms_per_step = ms / args.steps
-    tps = cfg["batch"] * args.steps / (ms / 1000.0)
-    log(f"[bench] timed {args.steps} steps: {ms_per_step:.3f} ms/step (wall {wall * 1000 / args.steps:.3f})")
-
-    # live per-kernel timing of the dominant kernel: a bounded sleep kernel
-    # (~10 ms) goes first so the host enqueues a whole eager step behind it;
-    # the step then runs back to back on the dispatch stream with a HIP event
-    # pair around every builtin launch (no host gaps inside the pairs)
-    dummy = thvm.Buffer(64)
-    prof_steps = 2
-    thvm.kprof(True)
-    thvm.kprof_reset()
-    for _ in range(prof_steps):
-        thvm.builtin("delay", [dummy], n=3000)
-        dec.step()
-    g_ms, g_n = thvm.kprof_query("gemv")
-    a_ms, a_n = thvm.kprof_query("attn")
-    n_ms, n_n = thvm.kprof_query("norm")
-    thvm.kprof(False)
-    dummy.free()
-    L_prof = dec.position - 1
-    gemv_gbs = gemv_bytes_per_step(cfg) * prof_steps / (g_ms / 1000.0) / 1e9
-    attn_gbs = (attn_bytes_per_step(cfg, L_prof) * prof_steps) / (a_ms / 1000.0) / 1e9
-    log(f"[bench] gemv: {g_n} launches, {g_ms / g_n * 1000:.1f} us avg, {gemv_gbs:.0f} GB/s; "
-        f"attn: {a_n} launches, {a_ms / a_n * 1000:.1f} us avg, {attn_gbs:.0f} GB/s; "
-        f"norm {n_ms / max(n_n, 1) * 1000:.1f} us avg")
-
-    cpu = None
-    if not args.no_cpu:
-        tps_cpu, match, secs, lerr = cpu_baseline(thvm, dec, cfg, args.cpu_steps)
-        cpu = {"value": round(tps_cpu, 4), "unit": "tokens/s", "cores": 1, "kind": "port",
-               "sample": f"{args.cpu_steps} greedy decode steps of the same C4 model at context "
-                         f"~{dec.position - args.cpu_steps}, oracle/oracle.c or_decode_step on one "
-                         f"core of {cpu_model_name()} ({os.cpu_count()} visible), in lockstep with "
-                         f"the device on the same inputs",
-               "seconds": round(secs, 2), "ids_match": match,
-               "logits_max_rel_err": lerr}
-
-    out = {
-        "metric": METRIC, "value": round(tps, 2), "unit": "tokens/s", "n_gpus": 1,
-        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms_per_step, 4),
-        "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
-        "dtype": "fp8e4m3 weights x bf16 activations, f32 accumulate", "data": "synthetic",
-        "config": {"workload": "C4 Llama-8B-shape fp8 weight-only decode, batch 1, KV prefilled "
-                               "to context 2048, greedy, hipGraph replay per token",
-                   "layers": cfg["n_layers"], "d_model": cfg["dim"], "heads": cfg["n_heads"],
-                   "kv_heads": cfg["n_kv_heads"], "head_dim": cfg["head_dim"], "ffn": cfg["ffn"],
-                   "vocab": cfg["vocab"], "batch": cfg["batch"], "context": CTX,
-                   "parallelism": "single GPU"},
-        "roofline": {"bound": "hbm", "achieved": round(gemv_gbs, 1), "peak": PEAK_GBS,
-                     "unit": "GB/s", "frac": round(gemv_gbs / PEAK_GBS, 4),
-                     "traffic": measured_traffic() if not args.layers else None,
-                     "algorithmic_bytes_per_launch": gemv_bytes_per_step(cfg) // (g_n // prof_steps),
-                     "kernel": "k_gemv (fp8 e4m3 weight GEMV, all projections + LM head)",
-                     "launches_per_step": g_n // prof_steps,
-                     "avg_launch_us": round(g_ms / g_n * 1000, 2)},
-        "attention": {"achieved_gbs": round(attn_gbs, 1), "frac": round(attn_gbs / PEAK_GBS, 4),
-                      "avg_launch_us": round(a_ms / max(a_n, 1) * 1000, 2)},
-        "step_hbm_gbs": round(step_bytes / (ms_per_step / 1000.0) / 1e9, 1),
-        "step_bytes": step_bytes,
-        "kernels_per_step": dec.step_kernels(),
-        "cpu_baseline": cpu,
-    }
-    if args.layers:
-        out["config"]["note"] = "DEBUG: reduced layer count, not the C4 metric"
-    dec.close()
-    thvm.shutdown()
-    print(json.dumps(out), flush=True)
+    try:
+        if args.copy_calibration:
+            return copy_calibration(thvm)
+        if args.config == "all":
+            runs = [("C4", 1), ("C4", 16), ("C3", 1), ("C3", 8), ("C1", 1), ("C2", 0)]
+        else:
+            runs = [(args.config, args.batch)]
+        for key, batch in runs:
+            out = run_c2(thvm, args) if key == "C2" else run_decode(thvm, key, batch, args)
+            print(json.dumps(out), flush=True)
+    finally:
+        thvm.shutdown()
     return 0
 
 

@@ -166,6 +166,10 @@ void     thvm_hip_kprof_enable(int on);
 void     thvm_hip_kprof_reset(void);
 /* Total ms and launch count for kernel tag (e.g. "gemv"); -1 when absent. */
 double   thvm_hip_kprof_query(const char *tag, uint64_t *count_out);
+/* Algorithmic bytes credited to the timed launches of `tag` (weights, scales,
+ * activations read and outputs written, each once; 0 for kernels whose bytes
+ * depend on a device-resident length, e.g. attention). */
+uint64_t thvm_hip_kprof_bytes(const char *tag);
 
 /* ===================== decode models ==================================== */
 /* C counterpart of the reference's decode drivers (bench/dsv2_decode_bench.c

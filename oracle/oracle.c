@@ -426,3 +426,200 @@ int or_decode_step(const OrModel *m, const int32_t *tok, uint32_t pos, float *lo
   free(x); free(xn); free(qkv); free(q); free(att); free(o); free(gu); free(hh);
   return 0;
 }
+
+/* ==== DeepSeek-V2 decode (bench/dsv2_decode_bench.c) ====================== */
+
+/* sum_k x[k] * w~[row][k], w~ = decode(w) * scale[row] (scale NULL: 1), serial */
+static float wdot(const float *x, const void *w, uint32_t wdt, const float *scale, uint64_t row,
+                  uint32_t K) {
+  const float s = scale ? scale[row] : 1.0f;
+  float acc = 0.0f;
+  for (uint32_t k = 0; k < K; k++) {
+    float wv = ld(w, row * K + k, wdt);
+    if (scale) wv = wv * s;
+    acc += x[k] * wv;
+  }
+  return acc;
+}
+
+void or_mla_prep(uint16_t *qpe, float *qlat, uint16_t *ckv_row, uint16_t *kpe_row,
+                 const uint16_t *qkv_raw, const void *wuk, uint32_t wdt, const float *suk,
+                 const float *wkvn, const float *cos_row, const float *sin_row,
+                 uint32_t H, uint32_t dn, uint32_t dr, uint32_t kv, float eps) {
+  const uint32_t half = dr / 2, qs = dn + dr, qoff = H * qs;
+  float *qn = (float *)malloc((size_t)dn * sizeof(float));
+  float *v = (float *)malloc((size_t)kv * sizeof(float));
+  for (uint32_t h = 0; h < H; h++) {
+    const uint32_t base = h * qs;
+    for (uint32_t j = 0; j < half; j++) {           /* gred_q pe pairs :474-483 */
+      float xe = or_bf16_to_f32(qkv_raw[base + dn + 2 * j]);
+      float xo = or_bf16_to_f32(qkv_raw[base + dn + 2 * j + 1]);
+      float c = cos_row[j], sv = sin_row[j];
+      qpe[h * dr + j] = or_f32_to_bf16(xe * c - xo * sv);
+      qpe[h * dr + half + j] = or_f32_to_bf16(xo * c + xe * sv);
+    }
+    for (uint32_t d = 0; d < dn; d++) qn[d] = or_bf16_to_f32(qkv_raw[base + d]);
+    for (uint32_t k = 0; k < kv; k++)                /* mla_qlat :658-666 */
+      qlat[h * kv + k] = wdot(qn, wuk, wdt, suk, (uint64_t)h * kv + k, dn);
+  }
+  float ss = 0.0f;                                   /* kv_prep :531-540 */
+  for (uint32_t t = 0; t < kv; t++) {
+    v[t] = or_bf16_to_f32(qkv_raw[qoff + t]);
+    ss += v[t] * v[t];
+  }
+  const float inv = 1.0f / sqrtf(ss * (1.0f / (float)kv) + eps);
+  for (uint32_t t = 0; t < kv; t++) ckv_row[t] = or_f32_to_bf16((v[t] * inv) * wkvn[t]);
+  for (uint32_t j = 0; j < half; j++) {
+    float xe = or_bf16_to_f32(qkv_raw[qoff + kv + 2 * j]);
+    float xo = or_bf16_to_f32(qkv_raw[qoff + kv + 2 * j + 1]);
+    float c = cos_row[j], sv = sin_row[j];
+    kpe_row[j] = or_f32_to_bf16(xe * c - xo * sv);
+    kpe_row[half + j] = or_f32_to_bf16(xo * c + xe * sv);
+  }
+  free(qn);
+  free(v);
+}
+
+void or_mla_attn(uint16_t *o, const float *qlat, const uint16_t *qpe, const uint16_t *ckv,
+                 const uint16_t *kpe, uint32_t L, const void *wuv, uint32_t wdt,
+                 const float *suv, uint32_t H, uint32_t kv, uint32_t dr, uint32_t dv,
+                 float scale) {
+  float *sc = (float *)malloc((size_t)(L ? L : 1) * sizeof(float));
+  float *olat = (float *)malloc((size_t)kv * sizeof(float));
+  for (uint32_t h = 0; h < H; h++) {
+    float gmax = -1e30f;                             /* mla_score C twin :707-719 */
+    for (uint32_t j = 0; j < L; j++) {
+      float s = 0.0f;
+      for (uint32_t k = 0; k < kv; k++) s += qlat[h * kv + k] * or_bf16_to_f32(ckv[(uint64_t)j * kv + k]);
+      for (uint32_t r = 0; r < dr; r++) s += or_bf16_to_f32(qpe[h * dr + r]) * or_bf16_to_f32(kpe[(uint64_t)j * dr + r]);
+      sc[j] = s * scale;
+      if (sc[j] > gmax) gmax = sc[j];
+    }
+    float gsum = 0.0f;
+    for (uint32_t j = 0; j < L; j++) { sc[j] = expf(sc[j] - gmax); gsum += sc[j]; }
+    for (uint32_t j = 0; j < L; j++) sc[j] = sc[j] / gsum;
+    for (uint32_t k = 0; k < kv; k++) {              /* mla_mix :741-748 */
+      float a = 0.0f;
+      for (uint32_t j = 0; j < L; j++) a += sc[j] * or_bf16_to_f32(ckv[(uint64_t)j * kv + k]);
+      olat[k] = a;
+    }
+    for (uint32_t mm = 0; mm < dv; mm++)             /* mla_o :775-783 */
+      o[h * dv + mm] = or_f32_to_bf16(wdot(olat, wuv, wdt, suv, (uint64_t)h * dv + mm, kv));
+  }
+  free(sc);
+  free(olat);
+}
+
+void or_route(int32_t *sel, float *probs, const float *g, uint32_t E, uint32_t K) {
+  float mx = g[0];                                   /* route C twin :845-860 */
+  for (uint32_t e = 1; e < E; e++) if (g[e] > mx) mx = g[e];
+  float sum = 0.0f;
+  for (uint32_t e = 0; e < E; e++) sum += expf(g[e] - mx);
+  for (uint32_t kk = 0; kk < K; kk++) {
+    int32_t best = -1;
+    float bv = -3.4e38f;
+    for (uint32_t e = 0; e < E; e++) {
+      int used = 0;
+      for (uint32_t j = 0; j < kk; j++) if (sel[j] == (int32_t)e) used = 1;
+      if (!used && g[e] > bv) { bv = g[e]; best = (int32_t)e; }
+    }
+    sel[kk] = best;
+    probs[kk] = expf(g[best] - mx) / sum;
+  }
+}
+
+void or_moe(float *out, const uint16_t *xb, const int32_t *sel, const float *probs,
+            const void *wgu_e, const float *sgu_e, const void *wd_e, const float *sd_e,
+            const void *wgu_s, const float *sgu_s, const void *wd_s, const float *sd_s,
+            uint32_t wdt, uint32_t D, uint32_t I, uint32_t S, uint32_t K) {
+  float *x = (float *)malloc((size_t)D * sizeof(float));
+  float *h = (float *)malloc(((size_t)K * I + S) * sizeof(float));
+  for (uint32_t k = 0; k < D; k++) x[k] = or_bf16_to_f32(xb[k]);
+  for (uint32_t e = 0; e < K; e++)                   /* moe_full_h C twin :895-908 */
+    for (uint32_t i = 0; i < I; i++) {
+      const uint64_t r = (uint64_t)sel[e] * 2 * I + 2 * i;
+      float g = wdot(x, wgu_e, wdt, sgu_e, r, D), u = wdot(x, wgu_e, wdt, sgu_e, r + 1, D);
+      h[e * I + i] = silu(g) * u;
+    }
+  for (uint32_t i = 0; i < S; i++) {
+    float g = wdot(x, wgu_s, wdt, sgu_s, 2 * i, D), u = wdot(x, wgu_s, wdt, sgu_s, 2 * i + 1, D);
+    h[K * I + i] = silu(g) * u;
+  }
+  for (uint32_t d = 0; d < D; d++) {                 /* moe_full_out C twin :947-963 */
+    float acc = 0.0f;
+    for (uint32_t e = 0; e < K; e++)
+      acc += probs[e] * wdot(h + e * I, wd_e, wdt, sd_e, (uint64_t)sel[e] * D + d, I);
+    acc += wdot(h + K * I, wd_s, wdt, sd_s, d, S);
+    out[d] = acc;
+  }
+  free(x);
+  free(h);
+}
+
+int or_dsv2_step(const OrDsv2 *m, const int32_t *tok, uint32_t pos, float *logits, int32_t *next) {
+  if (!m || pos >= m->max_seq || m->top_k > m->n_experts || m->top_k > 64 || m->d_rope % 2)
+    return -1;
+  const uint32_t D = m->dim, H = m->n_heads, kv = m->kv_lora, dn = m->d_nope, dr = m->d_rope;
+  const uint32_t dv = m->d_v, I = m->moe_inter, S = m->n_shared * m->moe_inter, K = m->top_k;
+  const uint32_t F = m->dense_inter, V = m->vocab, E = m->n_experts, wdt = m->wdt;
+  const uint32_t nqkv = H * (dn + dr) + kv + dr;
+  float *x = (float *)malloc((size_t)D * 4), *xn = (float *)malloc((size_t)D * 4);
+  float *qkv = (float *)malloc((size_t)nqkv * 4), *qlat = (float *)malloc((size_t)H * kv * 4);
+  uint16_t *qraw = (uint16_t *)malloc((size_t)nqkv * 2), *qpe = (uint16_t *)malloc((size_t)H * dr * 2);
+  uint16_t *o = (uint16_t *)malloc((size_t)H * dv * 2), *xb = (uint16_t *)malloc((size_t)D * 2);
+  float *of = (float *)malloc((size_t)(H * dv > D ? H * dv : D) * 4), *tmp = (float *)malloc((size_t)D * 4);
+  float *gu = (float *)malloc((size_t)2 * F * 4), *hh = (float *)malloc((size_t)F * 4);
+  float *lg = (float *)malloc((size_t)E * 4);
+  int32_t sel[64];
+  float probs[64];
+  for (uint32_t b = 0; b < m->batch; b++) {
+    int32_t t = tok[b];                              /* embed_row :377-395 */
+    for (uint32_t i = 0; i < D; i++)
+      x[i] = (t >= 0 && (uint32_t)t < V) ? or_bf16_to_f32(m->emb[(uint64_t)t * D + i]) : 0.0f;
+    for (uint32_t l = 0; l < m->n_layers; l++) {
+      const OrDsv2Layer *Ly = &m->layers[l];
+      uint16_t *ckv = Ly->ckv + (uint64_t)b * m->max_seq * kv;
+      uint16_t *kpe = Ly->kpe + (uint64_t)b * m->max_seq * dr;
+      or_rmsnorm(xn, DT_FP32, x, DT_FP32, Ly->win, 1, D, m->eps);
+      for (uint32_t i = 0; i < D; i++) xn[i] = rnd(xn[i], DT_BF16);   /* rms1 out bf16 */
+      or_gemv(qkv, xn, DT_FP32, D, Ly->wqkv, wdt, Ly->sqkv, 1, nqkv, D);
+      for (uint32_t n = 0; n < nqkv; n++) qraw[n] = or_f32_to_bf16(qkv[n]);
+      or_mla_prep(qpe, qlat, ckv + (uint64_t)pos * kv, kpe + (uint64_t)pos * dr, qraw, Ly->wuk, wdt,
+                  Ly->suk, Ly->wkvn, m->rope_cos + (uint64_t)pos * (dr / 2),
+                  m->rope_sin + (uint64_t)pos * (dr / 2), H, dn, dr, kv, m->eps);
+      or_mla_attn(o, qlat, qpe, ckv, kpe, pos + 1, Ly->wuv, wdt, Ly->suv, H, kv, dr, dv, m->scale);
+      for (uint32_t i = 0; i < H * dv; i++) of[i] = or_bf16_to_f32(o[i]);
+      or_gemv(tmp, of, DT_FP32, H * dv, Ly->wo, wdt, Ly->so, 1, D, H * dv);
+      for (uint32_t i = 0; i < D; i++) x[i] = rnd(x[i] + rnd(tmp[i], DT_BF16), DT_BF16);  /* x1 */
+      or_rmsnorm(xn, DT_FP32, x, DT_FP32, Ly->wpost, 1, D, m->eps);                       /* xn2f */
+      for (uint32_t i = 0; i < D; i++) xb[i] = or_f32_to_bf16(xn[i]);                     /* xn2b */
+      if (l < m->first_dense) {
+        for (uint32_t i = 0; i < D; i++) tmp[i] = or_bf16_to_f32(xb[i]);
+        or_gemv(gu, tmp, DT_FP32, D, Ly->wgu, wdt, Ly->sgu, 1, 2 * F, D);
+        for (uint32_t i = 0; i < F; i++) {
+          float g = rnd(gu[2 * i], DT_BF16), u = rnd(gu[2 * i + 1], DT_BF16);
+          hh[i] = rnd(silu(g) * u, DT_BF16);
+        }
+        or_gemv(tmp, hh, DT_FP32, F, Ly->wd, wdt, Ly->sd, 1, D, F);
+      } else {
+        for (uint32_t e = 0; e < E; e++) lg[e] = wdot(xn, Ly->gate, DT_FP32, NULL, e, D);
+        or_route(sel, probs, lg, E, K);
+        if (m->gate_out) memcpy(m->gate_out + (uint64_t)b * E, lg, E * sizeof(float));
+        if (m->sel_out) {
+          memcpy(m->sel_out + (uint64_t)b * K, sel, K * sizeof(int32_t));
+          memcpy(m->probs_out + (uint64_t)b * K, probs, K * sizeof(float));
+        }
+        or_moe(tmp, xb, sel, probs, Ly->wgu_e, Ly->sgu_e, Ly->wd_e, Ly->sd_e, Ly->wgu_s, Ly->sgu_s,
+               Ly->wd_s, Ly->sd_s, wdt, D, I, S, K);
+      }
+      for (uint32_t i = 0; i < D; i++) x[i] = rnd(x[i] + rnd(tmp[i], DT_BF16), DT_BF16);
+    }
+    or_rmsnorm(xn, DT_FP32, x, DT_FP32, m->gf, 1, D, m->eps);                             /* rms_f f32 */
+    float *lgb = logits + (uint64_t)b * V;
+    or_gemv(lgb, xn, DT_FP32, D, m->lm, wdt, m->lm_s, 1, V, D);
+    or_argmax(&next[b], lgb, 1, V);
+  }
+  free(x); free(xn); free(qkv); free(qlat); free(qraw); free(qpe); free(o); free(xb);
+  free(of); free(tmp); free(gu); free(hh); free(lg);
+  return 0;
+}

@@ -92,6 +92,90 @@ typedef struct OrModel {
 int or_decode_step(const OrModel *m, const int32_t *tok, uint32_t pos,
                    float *logits, int32_t *next);
 
+/* ---- DeepSeek-V2 (MLA + MoE) decode: stages and whole step ----
+ * Restates the reference's DSV2 decode step, bench/dsv2_decode_bench.c
+ * step_build :2328-2411 with the plain-C custom-kernel twins of each stage
+ * (PRE_C dialect, :355-364).  Weights are fp8 e4m3 with per-row f32 scales
+ * (the C5 configuration) or bf16 (scale NULL); layouts are this build's:
+ *   wqkv [H(dn+dr) + kv + dr][D]   q heads (dn nope rows, dr pe rows), then
+ *                                  the latent kv rows and the k pe rows
+ *   wuk  [H][kv][dn]  suk [H*kv]   absorbed k up-projection, row (h, k)
+ *   wuv  [H][dv][kv]  suv [H*dv]   absorbed v up-projection, row (h, m)
+ *   wo   [D][H dv]
+ *   dense: wgu [2F][D] rows (gate_i, up_i) interleaved, wd [D][F]
+ *   MoE: gate [E][D] f32; wgu_e [E][2I][D] interleaved, sgu_e [E][2I];
+ *        wd_e [E][D][I], sd_e [E][D]; shared wgu_s [2S][D], wd_s [D][S]
+ *        (S = n_shared * I)
+ *   caches: ckv [B][max_seq][kv], kpe [B][max_seq][dr] bf16
+ *   rope tables [max_seq][dr/2] f32 (YaRN, :312-343). */
+
+/* q/kv fold for one batch row (gred_q :435-485 + kv_prep :487-556 + mla_qlat
+ * :638-667 C twins).  qkv_raw holds the q|kv GEMV output rounded to bf16.
+ * q pe pairs (2j, 2j+1) rotate into halves j and dr/2+j; the latent row is
+ * RMS-normed (serial sum of squares) with gain wkvn; qlat[h][k] =
+ * sum_d qn[h][d] * wuk~[h][k][d] (f32).  Writes qpe [H][dr] bf16, qlat
+ * [H][kv] f32, and the cache rows ckv_row [kv], kpe_row [dr] bf16. */
+void or_mla_prep(uint16_t *qpe, float *qlat, uint16_t *ckv_row, uint16_t *kpe_row,
+                 const uint16_t *qkv_raw, const void *wuk, uint32_t wdt, const float *suk,
+                 const float *wkvn, const float *cos_row, const float *sin_row,
+                 uint32_t H, uint32_t dn, uint32_t dr, uint32_t kv, float eps);
+/* absorbed MLA attention for one batch row over cache rows [0, L) (mla_score
+ * :669-723, mla_mix :725-750, mla_o :752-785 C twins): s_j = (qlat.ckv_j +
+ * qpe.kpe_j) * scale, p = softmax(s), olat = sum_j p_j ckv_j (f32),
+ * o[h][m] = bf16(sum_k olat[h][k] * wuv~[h][m][k]). */
+void or_mla_attn(uint16_t *o, const float *qlat, const uint16_t *qpe, const uint16_t *ckv,
+                 const uint16_t *kpe, uint32_t L, const void *wuv, uint32_t wdt,
+                 const float *suv, uint32_t H, uint32_t kv, uint32_t dr, uint32_t dv,
+                 float scale);
+/* router (route C twin :836-862): greedy top-K over E logits, ties to the
+ * lowest expert id; probs over the softmax of all E logits, no renorm. */
+void or_route(int32_t *sel, float *probs, const float *logits, uint32_t E, uint32_t K);
+/* routed + shared experts for one batch row (moe_full_h :865-910,
+ * moe_full_out :912-965 C twins): h = silu(g)*u in f32 with g, u the
+ * unrounded f32 dots; out[d] = sum_e probs[e] (h_e . wd_e~[d]) + h_s .
+ * wd_s~[d] (f32, before the residual add). */
+void or_moe(float *out, const uint16_t *xb, const int32_t *sel, const float *probs,
+            const void *wgu_e, const float *sgu_e, const void *wd_e, const float *sd_e,
+            const void *wgu_s, const float *sgu_s, const void *wd_s, const float *sd_s,
+            uint32_t wdt, uint32_t D, uint32_t I, uint32_t S, uint32_t K);
+
+typedef struct OrDsv2Layer {
+  const float *win, *wkvn, *wpost;       /* norm gains [D], [kv], [D]             */
+  const void *wqkv; const float *sqkv;
+  const void *wuk;  const float *suk;
+  const void *wuv;  const float *suv;
+  const void *wo;   const float *so;
+  const void *wgu;  const float *sgu;    /* dense layers                          */
+  const void *wd;   const float *sd;
+  const float *gate;                     /* MoE layers                            */
+  const void *wgu_e; const float *sgu_e;
+  const void *wd_e;  const float *sd_e;
+  const void *wgu_s; const float *sgu_s;
+  const void *wd_s;  const float *sd_s;
+  uint16_t *ckv, *kpe;
+} OrDsv2Layer;
+
+typedef struct OrDsv2 {
+  uint32_t n_layers, dim, n_heads, kv_lora, d_nope, d_rope, d_v;
+  uint32_t n_experts, n_shared, top_k, moe_inter, dense_inter, first_dense;
+  uint32_t vocab, max_seq, batch, wdt;
+  float eps, scale;
+  const uint16_t *emb;                   /* [V][D] bf16                           */
+  const float *gf;                       /* final norm gain                       */
+  const void *lm; const float *lm_s;     /* [V][D]                                */
+  const float *rope_cos, *rope_sin;      /* [max_seq][dr/2]                       */
+  OrDsv2Layer *layers;
+  int32_t *sel_out; float *probs_out;    /* optional [B][K]: routing of the last MoE layer */
+  float *gate_out;                       /* optional [B][E]: its router logits    */
+} OrDsv2;
+
+/* One DSV2 decode step for every batch row (step_build :2328-2411): writes
+ * the cache rows at pos, logits [B][V] f32 and next[b].  The residual stream
+ * and the rms1 / dense-FFN / attention outputs are bf16; the post-attention
+ * norm feeds the router in f32 and the experts in bf16; the final norm feeds
+ * the LM head in f32 (:2394-2397, rms_f out f32). */
+int or_dsv2_step(const OrDsv2 *m, const int32_t *tok, uint32_t pos, float *logits, int32_t *next);
+
 #ifdef __cplusplus
 }
 #endif

@@ -31,6 +31,23 @@ class OrModel(C.Structure):
         ("layers", C.POINTER(OrLayer))]
 
 
+class OrDsv2Layer(C.Structure):
+    _fields_ = [(n, _vp) for n in (
+        "win", "wkvn", "wpost", "wqkv", "sqkv", "wuk", "suk", "wuv", "suv", "wo", "so",
+        "wgu", "sgu", "wd", "sd", "gate", "wgu_e", "sgu_e", "wd_e", "sd_e",
+        "wgu_s", "sgu_s", "wd_s", "sd_s", "ckv", "kpe")]
+
+
+class OrDsv2(C.Structure):
+    _fields_ = [(n, _u32) for n in (
+        "n_layers", "dim", "n_heads", "kv_lora", "d_nope", "d_rope", "d_v", "n_experts",
+        "n_shared", "top_k", "moe_inter", "dense_inter", "first_dense", "vocab", "max_seq",
+        "batch", "wdt")] + [("eps", _f), ("scale", _f)] + [
+        (n, _vp) for n in ("emb", "gf", "lm", "lm_s", "rope_cos", "rope_sin")] + [
+        ("layers", C.POINTER(OrDsv2Layer)), ("sel_out", _vp), ("probs_out", _vp),
+        ("gate_out", _vp)]
+
+
 _OR = None
 _REF = None
 
@@ -59,6 +76,14 @@ def oracle() -> C.CDLL:
                                       _u32, _u32, _u32, _f]),
             "or_argmax": (None, [_vp, _vp, _u32, _u32]),
             "or_decode_step": (_i, [C.POINTER(OrModel), _vp, _u32, _vp, _vp]),
+            "or_mla_prep": (None, [_vp, _vp, _vp, _vp, _vp, _vp, _u32, _vp, _vp, _vp, _vp,
+                                   _u32, _u32, _u32, _u32, _f]),
+            "or_mla_attn": (None, [_vp, _vp, _vp, _vp, _vp, _u32, _vp, _u32, _vp, _u32, _u32,
+                                   _u32, _u32, _f]),
+            "or_route": (None, [_vp, _vp, _vp, _u32, _u32]),
+            "or_moe": (None, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
+                              _u32, _u32, _u32, _u32, _u32]),
+            "or_dsv2_step": (_i, [C.POINTER(OrDsv2), _vp, _u32, _vp, _vp]),
         }
         for k, (r, a) in sig.items():
             fn = getattr(L, k)
@@ -188,3 +213,73 @@ class OracleModel:
         return lg, nx
 
 
+def dsv2_scale(cfg) -> float:
+    """(dn+dr)^-1/2 * mscale^2 with mscale = 0.1*0.707*ln(40) + 1 (YaRN)."""
+    ms = 0.1 * 0.707 * np.log(40.0) + 1.0
+    return float((cfg["d_nope"] + cfg["d_rope"]) ** -0.5 * ms * ms)
+
+
+class OracleDsv2:
+    """OrDsv2 over numpy copies of a DSV2 decoder's device tensors."""
+
+    def __init__(self, dec, cfg):
+        self.keep, self.caches, self.cfg = [], [], cfg
+        m = OrDsv2()
+        for k in ("n_layers", "dim", "n_heads", "kv_lora", "d_nope", "d_rope", "d_v", "n_experts",
+                  "n_shared", "top_k", "moe_inter", "first_dense", "vocab", "max_seq", "batch"):
+            setattr(m, k, cfg.get(k, 0))
+        m.dense_inter, m.wdt, m.eps = cfg.get("ffn", 0), cfg["wdtype"], cfg["eps"]
+        m.scale = dsv2_scale(cfg)
+        f8 = cfg["wdtype"] == DT_FP8_W
+
+        def t(name):
+            a = dec.read_tensor(name)
+            self.keep.append(a)
+            return a.ctypes.data
+
+        def w(ly, field, name):
+            setattr(ly, field, t(name))
+            if f8:
+                setattr(ly, "s" + field[1:], t(name + ".scale"))
+
+        L = cfg["n_layers"]
+        self.layers = (OrDsv2Layer * L)()
+        for l in range(L):
+            ly, p = self.layers[l], f"l{l}."
+            ly.win, ly.wkvn, ly.wpost = t(p + "win"), t(p + "wkvn"), t(p + "wpost")
+            for f in ("wqkv", "wuk", "wuv", "wo"):
+                w(ly, f, p + f)
+            if l < cfg.get("first_dense", 0):
+                w(ly, "wgu", p + "wgu")
+                w(ly, "wd", p + "wd")
+            else:
+                ly.gate = t(p + "gate")
+                w(ly, "wgu_e", p + "wgu_e")
+                w(ly, "wd_e", p + "wd_e")
+                if cfg.get("n_shared", 0):
+                    w(ly, "wgu_s", p + "wgu_s")
+                    w(ly, "wd_s", p + "wd_s")
+            ck, kp = dec.read_tensor(p + "ckv"), dec.read_tensor(p + "kpe")
+            self.caches += [ck, kp]
+            ly.ckv, ly.kpe = ck.ctypes.data, kp.ctypes.data
+        m.emb, m.gf, m.lm = t("emb"), t("norm_f"), t("lm")
+        if f8:
+            m.lm_s = t("lm.scale")
+        m.rope_cos, m.rope_sin = t("rope.cos"), t("rope.sin")
+        m.layers = self.layers
+        B, K = cfg["batch"], cfg["top_k"]
+        self.sel = np.zeros((B, K), np.int32)
+        self.probs = np.zeros((B, K), np.float32)
+        self.gate = np.zeros((B, cfg["n_experts"]), np.float32)
+        m.sel_out, m.probs_out = self.sel.ctypes.data, self.probs.ctypes.data
+        m.gate_out = self.gate.ctypes.data
+        self.m = m
+
+    def step(self, tok, pos):
+        B, V = self.cfg["batch"], self.cfg["vocab"]
+        tok = np.ascontiguousarray(tok, np.int32)
+        lg = np.empty((B, V), np.float32)
+        nx = np.empty(B, np.int32)
+        assert oracle().or_dsv2_step(C.byref(self.m), tok.ctypes.data, pos, lg.ctypes.data,
+                                       nx.ctypes.data) == 0
+        return lg, nx

@@ -1,0 +1,285 @@
+"""GPU parity of the DeepSeek-V2 decode path (MLA latent attention, MoE
+routing and expert FFN, the whole DSV2 decoder) against the CPU oracle
+(oracle/oracle.c or_mla_prep / or_mla_attn / or_route / or_moe /
+or_dsv2_step).  Bars: routing ids bit-exact; f32 results within 1e-5 of the
+magnitude sum; bf16 outputs within one storage rounding (2^-7 relative) plus
+that floor; decoder logits within 2e-2 relative (fp8 weights) or 1e-2
+absolute (bf16 weights)."""
+import numpy as np
+import pytest
+
+import _oracle as O
+
+pytestmark = pytest.mark.gpu
+
+DT_FP8, DT_BF16, DT_F32 = 9, 12, 13
+
+
+def say(*a):
+    print(*a, flush=True)
+
+
+def up(hip, a):
+    return hip.Buffer.from_numpy(np.ascontiguousarray(a))
+
+
+def bf(a):
+    return O.encode(np.asarray(a, np.float32), DT_BF16)
+
+
+def unbf(a):
+    return O.decode(a, DT_BF16)
+
+
+def fp8_rows(rng, rows, cols, std=0.02):
+    w = (rng.standard_normal((rows, cols)) * std).astype(np.float32)
+    s = (np.abs(w).max(1) / 448.0).astype(np.float32)
+    q = O.encode(w / s[:, None], DT_FP8)
+    return q, s, O.decode(q, DT_FP8) * s[:, None]
+
+
+def weights(rng, rows, cols, wdt):
+    if wdt == DT_FP8:
+        return fp8_rows(rng, rows, cols)
+    w = bf(rng.standard_normal((rows, cols)) * 0.02)
+    return w, None, unbf(w)
+
+
+def close_bf16(got, want, floor=0.0):
+    return np.abs(got - want) <= 2.0 ** -7 * np.abs(want) + 1e-5 * floor + 1e-6
+
+
+MLA_SHAPES = [dict(H=16, dn=128, dr=64, kv=512, dv=128, B=2, ms=256, L=130),
+              dict(H=8, dn=32, dr=16, kv=64, dv=32, B=1, ms=128, L=64),
+              dict(H=8, dn=32, dr=16, kv=128, dv=32, B=3, ms=64, L=1)]
+
+
+@pytest.mark.parametrize("wdt", [DT_FP8, DT_BF16])
+@pytest.mark.parametrize("shape", MLA_SHAPES, ids=["c5", "smoke", "L1"])
+def test_mla_prep_and_attn(hip, shape, wdt):
+    H, dn, dr, kv, dv, B, ms, L = (shape[k] for k in ("H", "dn", "dr", "kv", "dv", "B", "ms", "L"))
+    say(f"case: mla {shape} wdt={wdt}")
+    rng = np.random.default_rng(H * 100 + kv + L + wdt)
+    ldq = H * (dn + dr) + kv + dr
+    qkv = bf(rng.standard_normal((B, ldq)))
+    wuk, suk, wukf = weights(rng, H * kv, dn, wdt)
+    wuv, suv, wuvf = weights(rng, H * dv, kv, wdt)
+    wkvn = (1 + 0.1 * rng.standard_normal(kv)).astype(np.float32)
+    ang = rng.uniform(0, 6.3, (ms, dr // 2))
+    cs, sn = np.cos(ang).astype(np.float32), np.sin(ang).astype(np.float32)
+    ckv0 = bf(rng.standard_normal((B, ms, kv)))
+    kpe0 = bf(rng.standard_normal((B, ms, dr)))
+    pos = L - 1
+    ckv, kpe = up(hip, ckv0), up(hip, kpe0)
+    qlat, qpe = hip.Buffer(B * H * kv * 4), hip.Buffer(B * H * dr * 2)
+    Lb = up(hip, np.array([L], np.int32))
+    f8 = wdt == DT_FP8
+    args = [up(hip, qkv), up(hip, wuk)] + ([up(hip, suk)] if f8 else []) + [
+        up(hip, wkvn), up(hip, cs), up(hip, sn), Lb, ckv, kpe, qlat, qpe]
+    hip.builtin("mla_prep", args, b=B, h=H, dn=dn, dr=dr, kv=kv, dv=dv, maxseq=ms, wt=wdt, eps=1e-6)
+    g_qlat = qlat.read(np.float32).reshape(B, H, kv)
+    g_qpe = qpe.read(np.uint16).reshape(B, H, dr)
+    g_ckv = ckv.read(np.uint16).reshape(B, ms, kv)
+    g_kpe = kpe.read(np.uint16).reshape(B, ms, dr)
+    for b in range(B):
+        w_qpe = np.empty((H, dr), np.uint16)
+        w_qlat = np.empty((H, kv), np.float32)
+        w_crow, w_prow = np.empty(kv, np.uint16), np.empty(dr, np.uint16)
+        O.oracle().or_mla_prep(w_qpe.ctypes.data, w_qlat.ctypes.data, w_crow.ctypes.data,
+                               w_prow.ctypes.data, np.ascontiguousarray(qkv[b]).ctypes.data,
+                               wuk.ctypes.data, wdt, suk.ctypes.data if f8 else None,
+                               wkvn.ctypes.data, np.ascontiguousarray(cs[pos]).ctypes.data,
+                               np.ascontiguousarray(sn[pos]).ctypes.data, H, dn, dr, kv, 1e-6)
+        assert np.all(close_bf16(unbf(g_qpe[b]), unbf(w_qpe)))
+        qn = unbf(qkv[b, :H * (dn + dr)].reshape(H, dn + dr)[:, :dn])
+        floor = (np.abs(wukf.reshape(H, kv, dn)) @ np.abs(qn)[:, :, None])[..., 0]
+        assert np.all(np.abs(g_qlat[b] - w_qlat) <= 1e-5 * floor + 1e-30)
+        assert np.all(close_bf16(unbf(g_ckv[b, pos]), unbf(w_crow)))
+        assert np.all(close_bf16(unbf(g_kpe[b, pos]), unbf(w_prow)))
+        # rows other than pos untouched
+        keep = np.arange(ms) != pos
+        assert np.array_equal(g_ckv[b, keep], ckv0[b, keep])
+        assert np.array_equal(g_kpe[b, keep], kpe0[b, keep])
+
+    scale = 0.1352
+    nsplit = (ms + 63) // 64
+    o = hip.Buffer(B * H * dv * 2)
+    part = hip.Buffer(B * nsplit * H * (kv + 2) * 4)
+    args = [o, qlat, qpe, ckv, kpe, Lb, part, up(hip, wuv)] + ([up(hip, suv)] if f8 else [])
+    hip.builtin("mla_attn", args, b=B, h=H, dn=dn, dr=dr, kv=kv, dv=dv, maxseq=ms, nsplit=nsplit,
+                wt=wdt, scale=scale)
+    g_o = unbf(o.read(np.uint16).reshape(B, H, dv))
+    for b in range(B):
+        w_o = np.empty((H, dv), np.uint16)
+        O.oracle().or_mla_attn(w_o.ctypes.data, np.ascontiguousarray(g_qlat[b]).ctypes.data,
+                               np.ascontiguousarray(g_qpe[b]).ctypes.data,
+                               np.ascontiguousarray(g_ckv[b]).ctypes.data,
+                               np.ascontiguousarray(g_kpe[b]).ctypes.data, L, wuv.ctypes.data, wdt,
+                               suv.ctypes.data if f8 else None, H, kv, dr, dv, scale)
+        # floor: |olat| <= max_j |ckv_j| per column
+        cmax = np.abs(unbf(g_ckv[b, :L])).max(0)
+        floor = np.abs(wuvf.reshape(H, dv, kv)) @ cmax
+        assert np.all(close_bf16(g_o[b], unbf(w_o), floor)), np.max(np.abs(g_o[b] - unbf(w_o)))
+
+
+def test_mla_closed_form_equal_rows(hip):
+    """Every live latent row equal: the softmax weights sum to one, so olat is
+    that row whatever the scores, and o = W_uv . row (independent of q)."""
+    H, dn, dr, kv, dv, B, ms, L = 16, 128, 64, 512, 128, 1, 192, 150
+    say("case: mla closed form (equal latent rows)")
+    rng = np.random.default_rng(5)
+    row = bf(rng.standard_normal(kv))
+    ckv = np.tile(row, (B, ms, 1))
+    kpe = bf(rng.standard_normal((B, ms, dr)))
+    qlat = rng.standard_normal((B, H, kv)).astype(np.float32)
+    qpe = bf(rng.standard_normal((B, H, dr)))
+    wuv = bf(rng.standard_normal((H * dv, kv)) * 0.02)
+    nsplit = 3
+    o = hip.Buffer(B * H * dv * 2)
+    hip.builtin("mla_attn", [o, up(hip, qlat), up(hip, qpe), up(hip, ckv), up(hip, kpe),
+                             up(hip, np.array([L], np.int32)), hip.Buffer(B * nsplit * H * (kv + 2) * 4),
+                             up(hip, wuv)],
+                b=B, h=H, dn=dn, dr=dr, kv=kv, dv=dv, maxseq=ms, nsplit=nsplit, wt=DT_BF16, scale=0.2)
+    got = unbf(o.read(np.uint16).reshape(H, dv))
+    want = (unbf(wuv).astype(np.float64) @ unbf(row).astype(np.float64)).reshape(H, dv)
+    floor = (np.abs(unbf(wuv)) @ np.abs(unbf(row))).reshape(H, dv)
+    assert np.all(np.abs(got - want) <= 2.0 ** -7 * np.abs(want) + 1e-5 * floor)
+
+
+def test_route_topk_ties_bit_exact(hip):
+    B, E, K = 4, 64, 6
+    say("case: route top-k with ties")
+    rng = np.random.default_rng(11)
+    lg = rng.standard_normal((B, E)).astype(np.float32)
+    lg[0, [5, 9, 40]] = 3.0          # three-way tie at the top
+    lg[1, :] = 1.0                   # all equal: ids 0..K-1
+    lg[2, [63, 0]] = 4.0             # tie across the ends
+    sel, probs = hip.Buffer(B * K * 4), hip.Buffer(B * K * 4)
+    hip.builtin("route", [sel, probs, up(hip, lg)], b=B, e=E, k=K)
+    g_sel = sel.read(np.int32).reshape(B, K)
+    g_p = probs.read(np.float32).reshape(B, K)
+    for b in range(B):
+        ws, wp = np.empty(K, np.int32), np.empty(K, np.float32)
+        O.oracle().or_route(ws.ctypes.data, wp.ctypes.data, np.ascontiguousarray(lg[b]).ctypes.data, E, K)
+        assert np.array_equal(g_sel[b], ws)
+        order = np.lexsort((np.arange(E), -lg[b]))[:K]    # brute force: value desc, id asc
+        assert np.array_equal(g_sel[b], order)
+        assert np.all(np.abs(g_p[b] - wp) <= 1e-6 * np.abs(wp) + 1e-9)
+    assert list(g_sel[0, :3]) == [5, 9, 40] and list(g_sel[1]) == list(range(K))
+    assert list(g_sel[2, :2]) == [0, 63]
+
+
+@pytest.mark.parametrize("wdt", [DT_FP8, DT_BF16])
+@pytest.mark.parametrize("shape", [dict(D=256, E=8, K=3, I=128, S=256, B=2),
+                                   dict(D=2048, E=8, K=6, I=1408, S=2816, B=1)], ids=["small", "c5"])
+def test_moe_gateup_down(hip, shape, wdt):
+    D, E, K, I, S, B = (shape[k] for k in ("D", "E", "K", "I", "S", "B"))
+    say(f"case: moe {shape} wdt={wdt}")
+    rng = np.random.default_rng(D + E + wdt)
+    f8 = wdt == DT_FP8
+    wgue, sgue, _ = weights(rng, E * 2 * I, D, wdt)
+    wde, sde, _ = weights(rng, E * D, I, wdt)
+    wgus, sgus, _ = weights(rng, 2 * S, D, wdt)
+    wds, sds, _ = weights(rng, D, S, wdt)
+    x = rng.standard_normal((B, D)).astype(np.float32)
+    res0 = bf(rng.standard_normal((B, D)))
+    sel = np.stack([rng.permutation(E)[:K] for _ in range(B)]).astype(np.int32)
+    probs = rng.uniform(0.05, 0.3, (B, K)).astype(np.float32)
+    h = hip.Buffer(B * (K * I + S) * 4)
+    selb, pb = up(hip, sel), up(hip, probs)
+    args = [h, up(hip, x), selb, up(hip, wgue)] + ([up(hip, sgue)] if f8 else []) + \
+        [up(hip, wgus)] + ([up(hip, sgus)] if f8 else [])
+    hip.builtin("moe_gateup", args, b=B, d=D, e=E, k=K, i=I, s=S, wt=wdt)
+    res = up(hip, res0)
+    args = [res, h, selb, pb, up(hip, wde)] + ([up(hip, sde)] if f8 else []) + \
+        [up(hip, wds)] + ([up(hip, sds)] if f8 else [])
+    hip.builtin("moe_down", args, b=B, d=D, e=E, k=K, i=I, s=S, wt=wdt)
+    got = unbf(res.read(np.uint16).reshape(B, D))
+    for b in range(B):
+        out = np.empty(D, np.float32)
+        xb = bf(x[b])
+        O.oracle().or_moe(out.ctypes.data, xb.ctypes.data, np.ascontiguousarray(sel[b]).ctypes.data,
+                          np.ascontiguousarray(probs[b]).ctypes.data, wgue.ctypes.data,
+                          sgue.ctypes.data if f8 else None, wde.ctypes.data,
+                          sde.ctypes.data if f8 else None, wgus.ctypes.data,
+                          sgus.ctypes.data if f8 else None, wds.ctypes.data,
+                          sds.ctypes.data if f8 else None, wdt, D, I, S, K)
+        r = unbf(res0[b])
+        want = unbf(bf(r + unbf(bf(out))))
+        # each step of the chain within one bf16 rounding of the oracle's
+        tol = 2.0 ** -7 * (np.abs(want) + np.abs(out)) + 1e-4 * np.abs(out).max() + 1e-6
+        assert np.all(np.abs(got[b] - want) <= tol), np.max(np.abs(got[b] - want) - tol)
+
+
+DSV2 = dict(arch=3, n_layers=3, dim=256, n_heads=8, n_kv_heads=8, head_dim=48, ffn=512,
+            vocab=512, max_seq=128, eps=1e-6, rope_theta=10000.0, init_std=0.02, kv_lora=64,
+            d_nope=32, d_rope=16, d_v=32, n_experts=8, n_shared=2, top_k=3, moe_inter=64,
+            first_dense=1, adtype=DT_BF16)
+
+
+@pytest.mark.parametrize("wdt,batch", [(DT_FP8, 1), (DT_FP8, 2), (DT_BF16, 1)])
+def test_dsv2_decoder_parity(hip, wdt, batch):
+    """The DSV2 decoder (1 dense + 2 MoE layers at the reference's CPU smoke
+    shape) against or_dsv2_step, eager and captured; the last MoE layer's
+    routing must match the oracle's exactly."""
+    cfg = dict(DSV2, wdtype=wdt, batch=batch)
+    steps, ctx = 5, 20
+    say(f"case: dsv2 decoder {cfg}")
+    dec = hip.Decoder(seed=21, **cfg)
+    try:
+        dec.prefill_synthetic(ctx, seed=4)
+        rng = np.random.default_rng(3)
+        tok = rng.integers(0, cfg["vocab"], batch).astype(np.int32)
+        dec.set_state(tok, ctx)
+        om = O.OracleDsv2(dec, cfg)
+        g_tok, o_tok = tok.copy(), tok.copy()
+        agree, compare = 0, True
+        for s in range(steps):         # the device runs every step; comparison stops at a fork
+            pos = ctx + s
+            dec.step()
+            if not compare:
+                continue
+            glg = dec.logits()
+            gnx = dec.tokens(pos + 2)[:, pos + 1]
+            olg, onx = om.step(o_tok, pos)
+            if not np.array_equal(g_tok, o_tok):
+                compare = False
+                continue
+            gsel = dec.read_tensor("sel").reshape(batch, -1)
+            if not np.array_equal(gsel, om.sel):
+                # a routing fork is only acceptable at a near tie: the oracle's
+                # K-th / (K+1)-th logit gap lies within the device-vs-oracle
+                # logit drift of this step (the route kernel itself is
+                # bit-exact on equal logits); the trajectories part here
+                ggl = dec.read_tensor("gate_logits").reshape(batch, -1)
+                K = cfg["top_k"]
+                for b in np.nonzero((gsel != om.sel).any(1))[0]:
+                    srt = np.sort(om.gate[b])[::-1]
+                    gap, drift = srt[K - 1] - srt[K], np.abs(ggl[b] - om.gate[b]).max()
+                    say(f"  step {s} row {b}: routing fork at a near tie, gap {gap:.3g} drift {drift:.3g}")
+                    assert gap <= 2 * drift, f"step {s}: routing {gsel[b]} vs {om.sel[b]}, gap {gap} > drift {drift}"
+                assert s >= 1, "the first step must route identically"
+                compare = False
+                continue
+            err = np.abs(glg - olg)
+            if wdt == DT_FP8:
+                assert err.max() <= 2e-2 * np.abs(olg).max(), f"step {s}: rel {err.max() / np.abs(olg).max()}"
+            else:
+                assert err.max() <= 1e-2, f"step {s}: abs {err.max()}"
+            assert np.array_equal(gnx, np.argmax(glg, 1))
+            g_tok, o_tok = gnx.astype(np.int32), onx
+            agree += int(np.array_equal(g_tok, o_tok))
+        say(f"  steps with equal ids: {agree}/{steps}")
+        assert agree >= 1
+        eager = dec.tokens(ctx + steps + 1)
+    finally:
+        dec.close()
+    dec = hip.Decoder(seed=21, **cfg)
+    try:
+        dec.prefill_synthetic(ctx, seed=4)
+        dec.set_state(tok, ctx)
+        dec.capture()
+        dec.replay(steps - 1)
+        assert np.array_equal(dec.tokens(ctx + steps + 1), eager)
+    finally:
+        dec.close()

@@ -78,6 +78,7 @@ _SIGS = {
     "thvm_hip_timer_start": (_u32, []), "thvm_hip_timer_stop": (_d, [_u32]),
     "thvm_hip_kprof_enable": (None, [_i32]), "thvm_hip_kprof_reset": (None, []),
     "thvm_hip_kprof_query": (_d, [_cp, C.POINTER(_u64)]),
+    "thvm_hip_kprof_bytes": (_u64, [_cp]),
     "thvm_hip_decoder_create": (_u32, [C.POINTER(DecodeConfig), _u64]),
     "thvm_hip_decoder_destroy": (None, [_u32]),
     "thvm_hip_decoder_prefill_synthetic": (_i32, [_u32, _u32, _u64]),
@@ -316,6 +317,10 @@ def kprof_query(tag: str) -> tuple[float, int]:
     n = C.c_uint64()
     ms = lib().thvm_hip_kprof_query(tag.encode(), C.byref(n))
     return ms, n.value
+
+
+def kprof_bytes(tag: str) -> int:
+    return int(lib().thvm_hip_kprof_bytes(tag.encode()))
 
 
 def device_from_env() -> str:

@@ -17,7 +17,8 @@ LIB = PKG / "lib" / "libthvm_hip.so"
 ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
 
 C_SOURCES = ["hip_backend.c", "hip_custom.c", "decoder.c"]
-HIP_SOURCES = ["kernels/gemv.hip", "kernels/gemm.hip", "kernels/rowops.hip", "kernels/attn.hip"]
+HIP_SOURCES = ["kernels/gemv.hip", "kernels/gemm.hip", "kernels/rowops.hip", "kernels/attn.hip",
+               "kernels/mla.hip", "kernels/moe.hip"]
 
 CFLAGS = ["-std=c11", "-O2", "-fPIC", "-Wall", "-Wextra", "-Wno-unused-parameter",
           "-fvisibility=hidden", "-D__HIP_PLATFORM_AMD__",

@@ -50,7 +50,7 @@ typedef struct {
   int used;
   ThvmDecodeConfig c;
   u64 seed;
-  DTensor t[512];
+  DTensor t[2048];
   u32 nt;
   DOp *ops;
   u32 n_ops, cap_ops;
@@ -181,9 +181,24 @@ static int rope_tables(Decoder *d) {
 }
 
 static int cfg_check(const ThvmDecodeConfig *c) {
-  if (c->arch != THVM_ARCH_LLAMA && c->arch != THVM_ARCH_GPT2) {
+  if (c->arch != THVM_ARCH_LLAMA && c->arch != THVM_ARCH_GPT2 && c->arch != THVM_ARCH_DSV2) {
     hb_set_error("decoder: arch %u not supported by this build", c->arch);
     return -1;
+  }
+  if (c->arch == THVM_ARCH_DSV2) {
+    if (!c->n_layers || !c->dim || !c->n_heads || !c->vocab || !c->max_seq || !c->batch ||
+        !c->kv_lora || !c->d_nope || !c->d_rope || !c->d_v || !c->n_experts || !c->top_k ||
+        !c->moe_inter || (c->first_dense && !c->ffn)) {
+      hb_set_error("decoder: zero dimension in DSV2 config");
+      return -1;
+    }
+    if (c->batch > 4) { hb_set_error("decoder: DSV2 decodes batches of up to 4 rows in this build"); return -1; }
+    if (c->wdtype != THVM_DT_FP8E4M3 && c->wdtype != THVM_DT_BF16) {
+      hb_set_error("decoder: DSV2 weights must be fp8 e4m3 or bf16");
+      return -1;
+    }
+    if (c->adtype != THVM_DT_BF16) { hb_set_error("decoder: DSV2 activations are bf16"); return -1; }
+    return 0;
   }
   if (!c->n_layers || !c->dim || !c->n_heads || !c->head_dim || !c->ffn || !c->vocab ||
       !c->max_seq || !c->batch) {
@@ -229,6 +244,7 @@ static int cfg_check(const ThvmDecodeConfig *c) {
 
 static int build_llama(Decoder *d);
 static int build_gpt2(Decoder *d);
+static int build_dsv2(Decoder *d);
 
 static void dec_free(Decoder *d) {
   if (d->jit_slot) thvm_hip_jit_capture_drop(d->jit_slot);
@@ -253,7 +269,8 @@ THVM_API uint32_t thvm_hip_decoder_create(const ThvmDecodeConfig *cfg, uint64_t 
   if (d->c.init_std == 0.0f) d->c.init_std = 0.02f;
   d->seed = seed;
   d->n_split = (d->c.max_seq + 63) / 64;
-  int rc = d->c.arch == THVM_ARCH_LLAMA ? build_llama(d) : build_gpt2(d);
+  int rc = d->c.arch == THVM_ARCH_LLAMA ? build_llama(d)
+         : d->c.arch == THVM_ARCH_GPT2  ? build_gpt2(d) : build_dsv2(d);
   if (rc) { dec_free(d); return 0; }
   hipError_t e = hipStreamSynchronize(HB_STREAM);
   if (e != hipSuccess) { hb_set_error("decoder_create: %s", hipGetErrorString(e)); dec_free(d); return 0; }
@@ -531,6 +548,245 @@ static int build_gpt2(Decoder *d) {
   return op_tail(d, wte, 0, &nf);
 }
 
+/* ---- DeepSeek-V2 (MLA + MoE), the C5 shape ------------------------------
+ * Step (reference bench/dsv2_decode_bench.c step_build :2328-2411): embed ->
+ * per layer [RMSNorm + q|kv GEMV -> mla_prep -> mla_attn (split + merge +
+ * W_uv) -> o GEMV + residual -> post-attention RMSNorm -> dense SwiGLU FFN
+ * (first_dense layers) or router GEMV + route + expert gate/up + expert down
+ * with residual] -> final RMSNorm (f32) -> LM head -> argmax -> len_bump. */
+
+/* YaRN-corrected RoPE tables for the pe dims, [max_seq][d_rope/2]: the
+ * DeepSeek-V2-Lite rope scaling (factor 40 over an original 4096-position
+ * window, beta_fast 32, beta_slow 1), as the reference builds them
+ * (rope_tables :312-343). */
+static int rope_tables_yarn(Decoder *d) {
+  const u32 dr = d->c.d_rope, half = dr / 2, ms = d->c.max_seq;
+  const double theta = d->c.rope_theta > 0.0f ? (double)d->c.rope_theta : 10000.0;
+  const double factor = 40.0, orig = 4096.0, beta_fast = 32.0, beta_slow = 1.0;
+  double lo = floor(dr * log(orig / (beta_fast * 2.0 * M_PI)) / (2.0 * log(theta)));
+  double hi = ceil(dr * log(orig / (beta_slow * 2.0 * M_PI)) / (2.0 * log(theta)));
+  if (lo < 0.0) lo = 0.0;
+  if (hi > dr - 1.0) hi = dr - 1.0;
+  const double span = (hi - lo) > 1e-3 ? (hi - lo) : 1e-3;
+  u64 n = (u64)ms * half;
+  float *cs = (float *)malloc(n * 4), *sn = (float *)malloc(n * 4);
+  if (!cs || !sn) { free(cs); free(sn); hb_set_error("decoder: out of host memory"); return -1; }
+  for (u32 j = 0; j < half; j++) {
+    const double inv = 1.0 / pow(theta, (double)(2 * j) / (double)dr);
+    double ramp = ((double)j - lo) / span;
+    ramp = ramp < 0.0 ? 0.0 : ramp > 1.0 ? 1.0 : ramp;
+    const double f = (inv / factor) * ramp + inv * (1.0 - ramp);
+    for (u32 p = 0; p < ms; p++) {
+      cs[(u64)p * half + j] = (float)cos((double)p * f);
+      sn[(u64)p * half + j] = (float)sin((double)p * f);
+    }
+  }
+  u32 ci = tens_new(d, "rope.cos", THVM_DT_FP32, n * 4);
+  u32 si = tens_new(d, "rope.sin", THVM_DT_FP32, n * 4);
+  int rc = (!ci || !si || thvm_hip_buf_write(ci, cs, n * 4) || thvm_hip_buf_write(si, sn, n * 4)) ? -1 : 0;
+  free(cs);
+  free(sn);
+  return rc;
+}
+
+/* softmax scale with the YaRN mscale correction: (dn+dr)^-1/2 * mscale^2,
+ * mscale = 0.1 * 0.707 * ln(40) + 1 (reference cfg_init :141-147) */
+static float dsv2_scale(const ThvmDecodeConfig *c) {
+  const double ms = 0.1 * 0.707 * log(40.0) + 1.0;
+  return (float)(pow((double)(c->d_nope + c->d_rope), -0.5) * ms * ms);
+}
+
+static int build_dsv2(Decoder *d) {
+  const ThvmDecodeConfig *c = &d->c;
+  const u32 D = c->dim, H = c->n_heads, dn = c->d_nope, dr = c->d_rope, kv = c->kv_lora;
+  const u32 dv = c->d_v, E = c->n_experts, K = c->top_k, I = c->moe_inter, F = c->ffn;
+  const u32 S = c->n_shared * I, B = c->batch, V = c->vocab, wdt = c->wdtype;
+  const u32 nqkv = H * (dn + dr) + kv + dr, P = K * I + S;
+  const int f8 = wdt == THVM_DT_FP8E4M3;
+  const float scale = dsv2_scale(c);
+  d->n_split = (c->max_seq + 63) / 64;
+  if (!tens_new(d, "tok", THVM_DT_INT32, (u64)B * 4) || !tens_new(d, "len", THVM_DT_INT32, 4) ||
+      !tens_new(d, "hist", THVM_DT_INT32, (u64)B * (c->max_seq + 1) * 4) ||
+      !tens_new(d, "logits", THVM_DT_FP32, (u64)B * V * 4) ||
+      !tens_new(d, "am.pv", THVM_DT_FP32, (u64)B * 256 * 4) ||
+      !tens_new(d, "am.pi", THVM_DT_INT32, (u64)B * 256 * 4) ||
+      !tens_new(d, "x", THVM_DT_BF16, (u64)B * D * 2) || !tens_new(d, "xn", THVM_DT_BF16, (u64)B * D * 2) ||
+      !tens_new(d, "qkv", THVM_DT_BF16, (u64)B * nqkv * 2) ||
+      !tens_new(d, "qlat", THVM_DT_FP32, (u64)B * H * kv * 4) ||
+      !tens_new(d, "qpe", THVM_DT_BF16, (u64)B * H * dr * 2) ||
+      !tens_new(d, "o", THVM_DT_BF16, (u64)B * H * dv * 2) ||
+      !tens_new(d, "xnf", THVM_DT_FP32, (u64)B * D * 4) ||
+      !tens_new(d, "gate_logits", THVM_DT_FP32, (u64)B * E * 4) ||
+      !tens_new(d, "sel", THVM_DT_INT32, (u64)B * K * 4) ||
+      !tens_new(d, "probs", THVM_DT_FP32, (u64)B * K * 4) ||
+      !tens_new(d, "hmoe", THVM_DT_FP32, (u64)B * P * 4) ||
+      !tens_new(d, "h", THVM_DT_BF16, (u64)B * (F ? F : 1) * 2) ||
+      !tens_new(d, "mla.part", THVM_DT_FP32, thvm_k_mla_part_bytes(B, H, kv, d->n_split)))
+    return -1;
+  if (!weight_normal(d, "emb", THVM_DT_BF16, (u64)V * D, 0.0f, c->init_std)) return -1;
+  if (rope_tables_yarn(d) || !weight_const(d, "norm_f", D, 1.0f)) return -1;
+  char p[512], nm[48];
+  const u32 x = tens_find(d, "x"), L = tens_find(d, "len"), qkv = tens_find(d, "qkv");
+  const u32 qlat = tens_find(d, "qlat"), qpe = tens_find(d, "qpe"), o = tens_find(d, "o");
+  const u32 xnf = tens_find(d, "xnf"), gl = tens_find(d, "gate_logits"), sel = tens_find(d, "sel");
+  const u32 probs = tens_find(d, "probs"), hmoe = tens_find(d, "hmoe"), hd = tens_find(d, "h");
+  const u32 cosb = tens_find(d, "rope.cos"), sinb = tens_find(d, "rope.sin");
+
+  snprintf(p, sizeof p, "thvm-builtin:embed b=%u d=%u v=%u et=%u xt=%u", B, D, V, THVM_DT_BF16,
+           THVM_DT_BF16);
+  u32 ea[3] = {x, tens_find(d, "emb"), tens_find(d, "tok")};
+  if (op_add(d, "embed", p, ea, 3)) return -1;
+
+  for (u32 l = 0; l < c->n_layers; l++) {
+    u32 wqkv, sqkv, wuk, suk, wuv, suv, wo, so;
+#define WM(nmfmt, rows, cols, w, s) \
+    do { snprintf(nm, sizeof nm, nmfmt, l); if (weight_matrix(d, nm, rows, cols, w, s)) return -1; } while (0)
+    WM("l%u.wqkv", nqkv, D, &wqkv, &sqkv);
+    WM("l%u.wuk", H * kv, dn, &wuk, &suk);
+    WM("l%u.wuv", H * dv, kv, &wuv, &suv);
+    WM("l%u.wo", D, H * dv, &wo, &so);
+    snprintf(nm, sizeof nm, "l%u.win", l);
+    const u32 win = weight_const(d, nm, D, 1.0f);
+    snprintf(nm, sizeof nm, "l%u.wkvn", l);
+    const u32 wkvn = weight_const(d, nm, kv, 1.0f);
+    snprintf(nm, sizeof nm, "l%u.wpost", l);
+    const u32 wpost = weight_const(d, nm, D, 1.0f);
+    char cn[32], pn[32];
+    snprintf(cn, sizeof cn, "l%u.ckv", l);
+    snprintf(pn, sizeof pn, "l%u.kpe", l);
+    const u32 ckv = tens_new(d, cn, THVM_DT_BF16, (u64)B * c->max_seq * kv * 2);
+    const u32 kpe = tens_new(d, pn, THVM_DT_BF16, (u64)B * c->max_seq * dr * 2);
+    if (!win || !wkvn || !wpost || !ckv || !kpe) return -1;
+
+    /* RMSNorm (rms1) fused into the q|kv projection, output rounded to bf16 */
+    char nsp[96];
+    u32 gin, gargs[2], ng;
+    NormSpec n1 = {1, win, 0};
+    if (emit_norm(d, &n1, &gin, nsp, sizeof nsp, gargs, &ng)) return -1;
+    snprintf(p, sizeof p, "thvm-builtin:gemv m=%u n=%u k=%u wt=%u xt=%u yt=%u epi=0%s", B, nqkv, D,
+             wdt, THVM_DT_BF16, THVM_DT_BF16, nsp);
+    u32 qa[8], qn = 0;
+    qa[qn++] = qkv; qa[qn++] = gin; qa[qn++] = wqkv;
+    if (f8) qa[qn++] = sqkv;
+    for (u32 i = 0; i < ng; i++) qa[qn++] = gargs[i];
+    if (op_add(d, "gemv_qkv", p, qa, qn)) return -1;
+
+    snprintf(p, sizeof p, "thvm-builtin:mla_prep b=%u h=%u dn=%u dr=%u kv=%u dv=%u maxseq=%u wt=%u eps=%a",
+             B, H, dn, dr, kv, dv, c->max_seq, wdt, c->eps);
+    u32 pa[12], pnn = 0;
+    pa[pnn++] = qkv; pa[pnn++] = wuk;
+    if (f8) pa[pnn++] = suk;
+    pa[pnn++] = wkvn; pa[pnn++] = cosb; pa[pnn++] = sinb; pa[pnn++] = L;
+    pa[pnn++] = ckv; pa[pnn++] = kpe; pa[pnn++] = qlat; pa[pnn++] = qpe;
+    if (op_add(d, "mla_prep", p, pa, pnn)) return -1;
+
+    snprintf(p, sizeof p,
+             "thvm-builtin:mla_attn b=%u h=%u dn=%u dr=%u kv=%u dv=%u maxseq=%u nsplit=%u wt=%u scale=%a",
+             B, H, dn, dr, kv, dv, c->max_seq, d->n_split, wdt, scale);
+    u32 aa[10], an = 0;
+    aa[an++] = o; aa[an++] = qlat; aa[an++] = qpe; aa[an++] = ckv; aa[an++] = kpe; aa[an++] = L;
+    aa[an++] = tens_find(d, "mla.part"); aa[an++] = wuv;
+    if (f8) aa[an++] = suv;
+    if (op_add(d, "mla_attn", p, aa, an)) return -1;
+
+    snprintf(p, sizeof p, "thvm-builtin:gemv m=%u n=%u k=%u wt=%u xt=%u yt=%u epi=%u", B, D, H * dv,
+             wdt, THVM_DT_BF16, THVM_DT_BF16, THVM_EPI_RESID);
+    u32 oa[6], on = 0;
+    oa[on++] = x; oa[on++] = o; oa[on++] = wo;
+    if (f8) oa[on++] = so;
+    oa[on++] = x;
+    if (op_add(d, "gemv_o", p, oa, on)) return -1;
+
+    if (l < c->first_dense) {   /* dense SwiGLU FFN with the post-attention norm fused */
+      u32 wgu, sgu, wd, sd;
+      WM("l%u.wgu", 2 * F, D, &wgu, &sgu);
+      WM("l%u.wd", D, F, &wd, &sd);
+      NormSpec n2 = {1, wpost, 0};
+      if (emit_norm(d, &n2, &gin, nsp, sizeof nsp, gargs, &ng)) return -1;
+      snprintf(p, sizeof p, "thvm-builtin:gemv m=%u n=%u k=%u wt=%u xt=%u yt=%u epi=%u%s", B, 2 * F,
+               D, wdt, THVM_DT_BF16, THVM_DT_BF16, THVM_EPI_SWIGLU, nsp);
+      u32 ga[7], gn = 0;
+      ga[gn++] = hd; ga[gn++] = gin; ga[gn++] = wgu;
+      if (f8) ga[gn++] = sgu;
+      for (u32 i = 0; i < ng; i++) ga[gn++] = gargs[i];
+      if (op_add(d, "gemv_gateup", p, ga, gn)) return -1;
+      snprintf(p, sizeof p, "thvm-builtin:gemv m=%u n=%u k=%u wt=%u xt=%u yt=%u epi=%u", B, D, F, wdt,
+               THVM_DT_BF16, THVM_DT_BF16, THVM_EPI_RESID);
+      u32 da[6], dnn = 0;
+      da[dnn++] = x; da[dnn++] = hd; da[dnn++] = wd;
+      if (f8) da[dnn++] = sd;
+      da[dnn++] = x;
+      if (op_add(d, "gemv_down", p, da, dnn)) return -1;
+      continue;
+    }
+    /* MoE: post-attention norm in f32 (router input), router GEMV, top-K */
+    snprintf(nm, sizeof nm, "l%u.gate", l);
+    const u32 gate = weight_normal(d, nm, THVM_DT_FP32, (u64)E * D, 0.0f, c->init_std);
+    if (!gate) return -1;
+    d->weight_bytes += (u64)E * D * 4;
+    u32 wgue, sgue, wde, sde, wgus = 0, sgus = 0, wds = 0, sds = 0;
+    const u64 wb0 = d->weight_bytes;
+    WM("l%u.wgu_e", E * 2 * I, D, &wgue, &sgue);
+    WM("l%u.wd_e", E * D, I, &wde, &sde);
+    /* only the selected experts stream per step: count K (of E) per row */
+    {
+      const u64 all = d->weight_bytes - wb0;
+      const u32 used = K * B < E ? K * B : E;
+      d->weight_bytes = wb0 + all / E * used;
+    }
+    if (S) {
+      WM("l%u.wgu_s", 2 * S, D, &wgus, &sgus);
+      WM("l%u.wd_s", D, S, &wds, &sds);
+    }
+#undef WM
+    snprintf(p, sizeof p, "thvm-builtin:norm m=%u k=%u xt=%u yt=%u eps=%a", B, D, THVM_DT_BF16,
+             THVM_DT_FP32, c->eps);
+    u32 na[3] = {xnf, x, wpost};
+    if (op_add(d, "norm_post", p, na, 3)) return -1;
+    snprintf(p, sizeof p, "thvm-builtin:gemv m=%u n=%u k=%u wt=%u xt=%u yt=%u epi=0", B, E, D,
+             THVM_DT_FP32, THVM_DT_FP32, THVM_DT_FP32);
+    u32 ra[3] = {gl, xnf, gate};
+    if (op_add(d, "gemv_gate", p, ra, 3)) return -1;
+    snprintf(p, sizeof p, "thvm-builtin:route b=%u e=%u k=%u", B, E, K);
+    u32 rb[3] = {sel, probs, gl};
+    if (op_add(d, "route", p, rb, 3)) return -1;
+    snprintf(p, sizeof p, "thvm-builtin:moe_gateup b=%u d=%u e=%u k=%u i=%u s=%u wt=%u", B, D, E, K, I,
+             S, wdt);
+    u32 ma[8], mn = 0;
+    ma[mn++] = hmoe; ma[mn++] = xnf; ma[mn++] = sel; ma[mn++] = wgue;
+    if (f8) ma[mn++] = sgue;
+    if (S) { ma[mn++] = wgus; if (f8) ma[mn++] = sgus; }
+    if (op_add(d, "moe_gateup", p, ma, mn)) return -1;
+    snprintf(p, sizeof p, "thvm-builtin:moe_down b=%u d=%u e=%u k=%u i=%u s=%u wt=%u", B, D, E, K, I, S,
+             wdt);
+    u32 mb[9], mbn = 0;
+    mb[mbn++] = x; mb[mbn++] = hmoe; mb[mbn++] = sel; mb[mbn++] = probs; mb[mbn++] = wde;
+    if (f8) mb[mbn++] = sde;
+    if (S) { mb[mbn++] = wds; if (f8) mb[mbn++] = sds; }
+    if (op_add(d, "moe_down", p, mb, mbn)) return -1;
+  }
+  /* final norm in f32 (rms_f) -> LM head */
+  u32 lw, ls;
+  if (weight_matrix(d, "lm", V, D, &lw, &ls)) return -1;
+  snprintf(p, sizeof p, "thvm-builtin:norm m=%u k=%u xt=%u yt=%u eps=%a", B, D, THVM_DT_BF16,
+           THVM_DT_FP32, c->eps);
+  u32 fa[3] = {xnf, x, tens_find(d, "norm_f")};
+  if (op_add(d, "norm_f", p, fa, 3)) return -1;
+  snprintf(p, sizeof p, "thvm-builtin:gemv m=%u n=%u k=%u wt=%u xt=%u yt=%u epi=0", B, V, D, wdt,
+           THVM_DT_FP32, THVM_DT_FP32);
+  u32 la[4], ln = 0;
+  la[ln++] = tens_find(d, "logits"); la[ln++] = xnf; la[ln++] = lw;
+  if (f8) la[ln++] = ls;
+  if (op_add(d, "lm_head", p, la, ln)) return -1;
+  const u32 nb = V >= 256 * 64 ? 256 : (V + 63) / 64;
+  snprintf(p, sizeof p, "thvm-builtin:argmax b=%u v=%u nb=%u hist=1 hstride=%u", B, V, nb,
+           c->max_seq + 1);
+  u32 am[6] = {tens_find(d, "tok"), tens_find(d, "logits"), tens_find(d, "am.pv"),
+               tens_find(d, "am.pi"), tens_find(d, "hist"), L};
+  if (op_add(d, "argmax", p, am, 6)) return -1;
+  return op_add(d, "len_bump", "thvm-builtin:len_bump delta=1", &L, 1);
+}
+
 THVM_API void thvm_hip_decoder_destroy(uint32_t h) {
   Decoder *d = dec_get(h);
   if (d) dec_free(d);
@@ -560,10 +816,23 @@ THVM_API int thvm_hip_decoder_prefill_synthetic(uint32_t h, uint32_t ctx, uint64
   const ThvmDecodeConfig *c = &d->c;
   if (ctx >= c->max_seq) { hb_set_error("prefill: ctx %u >= max_seq", ctx); return -1; }
   char err[256];
+  const int mla = c->arch == THVM_ARCH_DSV2;
   for (u32 l = 0; l < c->n_layers; l++) {
     char kn[32], vn[32];
-    snprintf(kn, sizeof kn, "l%u.kcache", l);
-    snprintf(vn, sizeof vn, "l%u.vcache", l);
+    snprintf(kn, sizeof kn, mla ? "l%u.ckv" : "l%u.kcache", l);
+    snprintf(vn, sizeof vn, mla ? "l%u.kpe" : "l%u.vcache", l);
+    if (mla) {   /* latent rows [B][max_seq][kv] and pe rows [B][max_seq][dr] */
+      void *kp = hb_buf_ptr(tens_find(d, kn)), *vp = hb_buf_ptr(tens_find(d, vn));
+      if (!kp || !vp) { hb_set_error("prefill: cache missing"); return -1; }
+      if (thvm_k_fill_cache(kp, c->adtype, c->batch, 1, c->max_seq, c->kv_lora, ctx, seed,
+                            name_tag(kn), HB_STREAM, err, sizeof err) ||
+          thvm_k_fill_cache(vp, c->adtype, c->batch, 1, c->max_seq, c->d_rope, ctx, seed,
+                            name_tag(vn), HB_STREAM, err, sizeof err)) {
+        hb_set_error("prefill: %s", err);
+        return -1;
+      }
+      continue;
+    }
     void *kp = hb_buf_ptr(tens_find(d, kn)), *vp = hb_buf_ptr(tens_find(d, vn));
     if (!kp || !vp) { hb_set_error("prefill: cache missing"); return -1; }
     if (thvm_k_fill_cache(kp, c->adtype, c->batch, c->n_kv_heads, c->max_seq, c->head_dim, ctx,
@@ -669,6 +938,8 @@ THVM_API uint64_t thvm_hip_decoder_step_bytes(uint32_t h) {
   u64 as = hb_dt_size(c->adtype);
   /* K and V rows [0, L) of every layer and batch row, plus the new row written */
   u64 kv = 2ull * c->n_layers * c->batch * c->n_kv_heads * c->head_dim * as * (L + 1);
+  if (c->arch == THVM_ARCH_DSV2)   /* latent + pe rows; experts counted as selected */
+    kv = (u64)c->n_layers * c->batch * (c->kv_lora + c->d_rope) * as * (L + 1);
   return d->weight_bytes + kv;
 }
 

@@ -509,6 +509,12 @@ THVM_API void thvm_hip_kprof_reset(void) {
   KP_N = 0;
   KP_POOL_USED = 0;
 }
+THVM_API uint64_t thvm_hip_kprof_bytes(const char *tag) {
+  u64 tot = 0;
+  for (u32 i = 0; i < KP_N; i++)
+    if (tag == NULL || strcmp(KP[i].tag, tag) == 0) tot += KP[i].bytes;
+  return tot;
+}
 THVM_API double thvm_hip_kprof_query(const char *tag, uint64_t *count_out) {
   if (!HB_READY) return -1.0;
   hipStreamSynchronize(HB_STREAM);

@@ -270,6 +270,107 @@ int hb_builtin_launch(const char *program, const u32 *ids, u32 n, int check_only
     if (check_only) return 0;
     if (prof) hb_kprof_begin(K, &e0, &e1);
     rc = thvm_k_attn_decode(&a, HB_STREAM, err, sizeof err);
+  } else if (strcmp(K, "mla_prep") == 0 || strcmp(K, "mla_attn") == 0) {
+    ThvmMlaArgs a;
+    memset(&a, 0, sizeof a);
+    const int prep = strcmp(K, "mla_prep") == 0;
+    NEED(spec_u32(&sp, "b", &a.B, 1, 0) || spec_u32(&sp, "h", &a.H, 1, 0) ||
+         spec_u32(&sp, "dn", &a.dn, 1, 0) || spec_u32(&sp, "dr", &a.dr, 1, 0) ||
+         spec_u32(&sp, "kv", &a.kv, 1, 0) || spec_u32(&sp, "dv", &a.dv, 1, 0) ||
+         spec_u32(&sp, "maxseq", &a.max_seq, 1, 0) || spec_u32(&sp, "wt", &a.wdt, 0, THVM_DT_FP8E4M3) ||
+         spec_f32(&sp, "eps", &a.eps, 0, 1e-6f) || spec_f32(&sp, "scale", &a.scale, !prep, 0));
+    NEED(spec_u32(&sp, "ldq", &a.ldq, 0, a.H * (a.dn + a.dr) + a.kv + a.dr) ||
+         spec_u32(&sp, "nsplit", &a.n_split, 0, (a.max_seq + 63) / 64));
+    const u32 wsz = hb_dt_size(a.wdt);
+    const int fp8 = a.wdt == THVM_DT_FP8E4M3;
+    if (!wsz) { hb_set_error("builtin %s: bad weight dtype", K); return -1; }
+    const u64 ckvb = (u64)a.B * a.max_seq * a.kv * 2, kpeb = (u64)a.B * a.max_seq * a.dr * 2;
+    u32 slot = 0;
+    if (prep) {
+      a.qkv = arg(&c, slot++, (u64)a.B * a.ldq * 2);
+      a.wuk = arg(&c, slot++, (u64)a.H * a.kv * a.dn * wsz);
+      if (fp8) a.suk = (const float *)arg(&c, slot++, (u64)a.H * a.kv * 4);
+      a.wkvn = (const float *)arg(&c, slot++, (u64)a.kv * 4);
+      a.rope_cos = (const float *)arg(&c, slot++, (u64)a.max_seq * (a.dr / 2) * 4);
+      a.rope_sin = (const float *)arg(&c, slot++, (u64)a.max_seq * (a.dr / 2) * 4);
+      a.len = (const int32_t *)arg(&c, slot++, 4);
+      a.ckv = arg(&c, slot++, ckvb);
+      a.kpe = arg(&c, slot++, kpeb);
+      a.qlat = (float *)arg(&c, slot++, (u64)a.B * a.H * a.kv * 4);
+      a.qpe = arg(&c, slot++, (u64)a.B * a.H * a.dr * 2);
+      bytes = (u64)a.H * a.kv * a.dn * wsz + (u64)a.B * a.ldq * 2;
+    } else {
+      a.o = arg(&c, slot++, (u64)a.B * a.H * a.dv * 2);
+      a.qlat = (float *)arg(&c, slot++, (u64)a.B * a.H * a.kv * 4);
+      a.qpe = arg(&c, slot++, (u64)a.B * a.H * a.dr * 2);
+      a.ckv = arg(&c, slot++, ckvb);
+      a.kpe = arg(&c, slot++, kpeb);
+      a.len = (const int32_t *)arg(&c, slot++, 4);
+      a.part = (float *)arg(&c, slot++, thvm_k_mla_part_bytes(a.B, a.H, a.kv, a.n_split));
+      a.wuv = arg(&c, slot++, (u64)a.H * a.dv * a.kv * wsz);
+      if (fp8) a.suv = (const float *)arg(&c, slot++, (u64)a.H * a.dv * 4);
+      bytes = 0; /* live-length dependent: the decoder accounts for it */
+    }
+    if (c.bad) return -1;
+    if (check_only) return 0;
+    if (prof) hb_kprof_begin(K, &e0, &e1);
+    rc = prep ? thvm_k_mla_prep(&a, HB_STREAM, err, sizeof err)
+              : thvm_k_mla_attn(&a, HB_STREAM, err, sizeof err);
+  } else if (strcmp(K, "route") == 0) {
+    ThvmRouteArgs a;
+    memset(&a, 0, sizeof a);
+    NEED(spec_u32(&sp, "b", &a.B, 1, 0) || spec_u32(&sp, "e", &a.E, 1, 0) ||
+         spec_u32(&sp, "k", &a.K, 1, 0));
+    a.sel = (int32_t *)arg(&c, 0, (u64)a.B * a.K * 4);
+    a.probs = (float *)arg(&c, 1, (u64)a.B * a.K * 4);
+    a.logits = (const float *)arg(&c, 2, (u64)a.B * a.E * 4);
+    if (c.bad) return -1;
+    bytes = (u64)a.B * (a.E * 4 + a.K * 8);
+    if (check_only) return 0;
+    if (prof) hb_kprof_begin(K, &e0, &e1);
+    rc = thvm_k_route(&a, HB_STREAM, err, sizeof err);
+  } else if (strcmp(K, "moe_gateup") == 0 || strcmp(K, "moe_down") == 0) {
+    ThvmMoeArgs a;
+    memset(&a, 0, sizeof a);
+    const int gu = strcmp(K, "moe_gateup") == 0;
+    NEED(spec_u32(&sp, "b", &a.B, 1, 0) || spec_u32(&sp, "d", &a.D, 1, 0) ||
+         spec_u32(&sp, "e", &a.E, 1, 0) || spec_u32(&sp, "k", &a.K, 1, 0) ||
+         spec_u32(&sp, "i", &a.I, 1, 0) || spec_u32(&sp, "s", &a.S, 0, 0) ||
+         spec_u32(&sp, "wt", &a.wdt, 0, THVM_DT_FP8E4M3));
+    const u32 wsz = hb_dt_size(a.wdt);
+    const int fp8 = a.wdt == THVM_DT_FP8E4M3;
+    if (!wsz) { hb_set_error("builtin %s: bad weight dtype", K); return -1; }
+    const u64 hb = (u64)a.B * (a.K * a.I + a.S) * 4;
+    u32 slot = 0;
+    if (gu) {
+      a.h = (float *)arg(&c, slot++, hb);
+      a.x = (const float *)arg(&c, slot++, (u64)a.B * a.D * 4);
+      a.sel = (const int32_t *)arg(&c, slot++, (u64)a.B * a.K * 4);
+      a.wgu_e = arg(&c, slot++, (u64)a.E * 2 * a.I * a.D * wsz);
+      if (fp8) a.sgu_e = (const float *)arg(&c, slot++, (u64)a.E * 2 * a.I * 4);
+      if (a.S) {
+        a.wgu_s = arg(&c, slot++, (u64)2 * a.S * a.D * wsz);
+        if (fp8) a.sgu_s = (const float *)arg(&c, slot++, (u64)2 * a.S * 4);
+      }
+      bytes = (u64)a.B * ((u64)a.K * 2 * a.I + 2 * a.S) * a.D * wsz + hb;
+    } else {
+      a.res = arg(&c, slot++, (u64)a.B * a.D * 2);
+      a.h = (float *)arg(&c, slot++, hb);
+      a.sel = (const int32_t *)arg(&c, slot++, (u64)a.B * a.K * 4);
+      a.probs = (const float *)arg(&c, slot++, (u64)a.B * a.K * 4);
+      a.wd_e = arg(&c, slot++, (u64)a.E * a.D * a.I * wsz);
+      if (fp8) a.sd_e = (const float *)arg(&c, slot++, (u64)a.E * a.D * 4);
+      if (a.S) {
+        a.wd_s = arg(&c, slot++, (u64)a.D * a.S * wsz);
+        if (fp8) a.sd_s = (const float *)arg(&c, slot++, (u64)a.D * 4);
+      }
+      bytes = (u64)a.B * ((u64)a.K * a.I + a.S) * a.D * wsz + hb + (u64)a.B * a.D * 4;
+    }
+    if (c.bad) return -1;
+    if (check_only) return 0;
+    if (prof) hb_kprof_begin(K, &e0, &e1);
+    rc = gu ? thvm_k_moe_gateup(&a, HB_STREAM, err, sizeof err)
+            : thvm_k_moe_down(&a, HB_STREAM, err, sizeof err);
   } else if (strcmp(K, "embed") == 0) {
     ThvmEmbedArgs a;
     memset(&a, 0, sizeof a);

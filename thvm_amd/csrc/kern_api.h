@@ -101,6 +101,67 @@ typedef struct ThvmAttnArgs {
 int thvm_k_attn_decode(const ThvmAttnArgs *a, hipStream_t s, char *err, int errlen);
 uint64_t thvm_k_attn_part_bytes(uint32_t B, uint32_t H, uint32_t Hkv, uint32_t hd, uint32_t n_split);
 
+/* DeepSeek-V2 multi-head latent attention (absorbed form) for decode.
+ * qkv [B][ldq] bf16 is the q|kv projection output: per head dn nope + dr pe
+ * values, then kv latent values and dr k-pe values.  Caches ckv
+ * [B][max_seq][kv], kpe [B][max_seq][dr] bf16; rope tables [max_seq][dr/2].
+ * mla_prep: qpe [B][H][dr] bf16 (pairs (2j,2j+1) rotated into halves j and
+ * dr/2+j), the latent row RMS-normed with gain wkvn and the rotated k pe row
+ * appended at L-1, and qlat [B][H][kv] f32 = q_nope . W_uk (W_uk [H][kv][dn]).
+ * mla_attn: split-sequence scores over rows [0, L) (s = (qlat.ckv + qpe.kpe)
+ * * scale), partials part [B][n_split][H][kv+2], then the merge and the V
+ * up-projection o [B][H*dv] bf16 = olat . W_uv (W_uv [H][dv][kv]).  W_uk /
+ * W_uv are fp8 e4m3 with per-row scales (suk [H*kv], suv [H*dv]) or bf16. */
+typedef struct ThvmMlaArgs {
+  const void *qkv;
+  const void *wuk; const float *suk;
+  const void *wuv; const float *suv;
+  const float *wkvn;
+  const float *rope_cos, *rope_sin;
+  const int32_t *len;
+  void *ckv, *kpe;
+  float *qlat;
+  void *qpe;
+  float *part;
+  void *o;
+  uint32_t B, H, dn, dr, kv, dv, max_seq, ldq, n_split, wdt;
+  float eps, scale;
+} ThvmMlaArgs;
+int thvm_k_mla_prep(const ThvmMlaArgs *a, hipStream_t s, char *err, int errlen);
+int thvm_k_mla_attn(const ThvmMlaArgs *a, hipStream_t s, char *err, int errlen);
+uint64_t thvm_k_mla_part_bytes(uint32_t B, uint32_t H, uint32_t kv, uint32_t n_split);
+
+/* MoE routing (reference bench/dsv2_decode_bench.c route :787-863): per
+ * batch row, greedy top-K of E gate logits (ties to the lowest expert id),
+ * probs = softmax over all E logits at the chosen ids, no renormalisation.
+ * logits [B][E] f32 -> sel [B][K] int32, probs [B][K] f32.  E <= 64. */
+typedef struct ThvmRouteArgs {
+  int32_t *sel; float *probs; const float *logits;
+  uint32_t B, E, K;
+} ThvmRouteArgs;
+int thvm_k_route(const ThvmRouteArgs *a, hipStream_t s, char *err, int errlen);
+
+/* Routed + shared expert FFN (reference moe_full_h / moe_full_out
+ * :865-965).  x [B][D] f32 (rounded to bf16 as the experts' input); h
+ * [B][K*I + S] f32 scratch; gate/up rows interleaved (gate_i, up_i):
+ * wgu_e [E][2I][D] (+ sgu_e [E][2I]), wgu_s [2S][D] (+ sgu_s [2S]); down
+ * rows wd_e [E][D][I] (+ sd_e [E][D]), wd_s [D][S] (+ sd_s [D]); weights
+ * fp8 e4m3 (scales required) or bf16 (scales NULL).
+ * gateup: h[b][e*I+i] = silu(g)*u (f32) for slot e < K and h[b][K*I+i] for
+ * the shared rows.  down: res[b][d] = bf16(res + bf16(sum_e probs[b][e] *
+ * (h_e . wd_e[sel][d]) + h_s . wd_s[d])). */
+typedef struct ThvmMoeArgs {
+  const float *x; float *h; void *res;
+  const int32_t *sel; const float *probs;
+  const void *wgu_e; const float *sgu_e;
+  const void *wd_e;  const float *sd_e;
+  const void *wgu_s; const float *sgu_s;
+  const void *wd_s;  const float *sd_s;
+  uint32_t B, D, E, K, I, S, wdt;
+} ThvmMoeArgs;
+int thvm_k_moe_gateup(const ThvmMoeArgs *a, hipStream_t s, char *err, int errlen);
+int thvm_k_moe_down(const ThvmMoeArgs *a, hipStream_t s, char *err, int errlen);
+
 /* Embedding gather: x[b][i] = emb[tok[b]][i] (+ pos[L-1][i] when pos != NULL),
  * tok int32 [B]; out of range ids read a zero row. */
 typedef struct ThvmEmbedArgs {

@@ -213,7 +213,10 @@ extern "C" int thvm_k_gemm_mfma(const ThvmGemvArgs *a, hipStream_t s, char *err,
     return -1;
   }
   const int MT = a->M <= 16 ? 1 : a->M <= 32 ? 2 : 4;
-  int NT = a->tune_r ? (int)a->tune_r : (MT == 4 ? 1 : 2);
+  // 16-row weight tiles per block, from the gfx950 sweep over the C4 shapes at
+  // M=16: more tiles amortise the x tile reads over more weight rows (wide N),
+  // fewer keep enough blocks in flight (N <= 4096)
+  int NT = a->tune_r ? (int)a->tune_r : (a->N >= 16384 ? 4 : a->N <= 4096 ? 1 : 2);
   if (NT != 1 && NT != 2 && NT != 4) { snprintf(err, errlen, "gemm: n tiles per block must be 1, 2 or 4"); return -1; }
   const int xbf = a->xdt == THVM_DT_BF16, xf16 = a->xdt == THVM_DT_FP16;
   if (a->wdt == THVM_DT_FP8E4M3) {

@@ -1,0 +1,371 @@
+// mla.hip -- DeepSeek-V2 multi-head latent attention for decode on gfx950:
+// the absorbed form over a shared latent cache (one ckv row of kv_lora
+// values and one roped k-pe row per position, read by every query head).
+//
+// Replaces the reference's MLA kernels (bench/dsv2_decode_bench.c gred_q
+// :435-485, kv_prep :487-556, mla_qlat :638-667, mla_score :669-723, mla_mix
+// :725-750, mla_o :752-785): five single-purpose launches and a materialised
+// [H, max_seq] score matrix become three kernels:
+//   k_mla_prep   q pe rotation, latent-row RMSNorm + k pe rotation + cache
+//                append at L-1, and qlat = q_nope . W_uk (fp8/bf16 rows, per
+//                row scale) -- one launch, blocks split between the jobs;
+//   k_mla_split  split-sequence flash decode: a block owns 64 cache rows of
+//                one batch row, stages them in LDS once, scores all H heads
+//                against them (lanes split the latent dimension, DPP wave
+//                sums), and writes per-split (olat partial, max, sum) --
+//                the latent rows are read from HBM exactly once per step;
+//   k_mla_out    merges the live splits per (row, head) in fixed order and
+//                applies the absorbed V up-projection W_uv, rounding o to
+//                bf16.
+// The live length L is read from device memory, so one captured graph
+// serves every position.
+#include "dev_common.h"
+#include "../kern_api.h"
+#include "launch.h"
+#include <stdio.h>
+
+#define MLA_CHUNK 64
+#define MLA_THREADS 512
+
+__device__ __forceinline__ float bfv(const void *p, uint64_t i) {
+  return bf2f(((const bf16_t *)p)[i]);
+}
+
+// 16 weights of one row chunk (fp8 or bf16 storage) as f32
+template <bool FP8>
+__device__ __forceinline__ void w16(const uint4 &q0, const uint4 &q1, float o[16]) {
+  if (FP8) {
+    const uint32_t w[4] = {q0.x, q0.y, q0.z, q0.w};
+#pragma unroll
+    for (int i = 0; i < 4; i++) fp8x4_to_f32(w[i], o + 4 * i);
+  } else {
+    const uint32_t w[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+      o[2 * i] = __uint_as_float(w[i] << 16);
+      o[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
+    }
+  }
+}
+
+// sum over aligned groups of G lanes (G a power of two <= 64)
+__device__ __forceinline__ float group_sum(float v, int G) {
+  for (int o = 1; o < G; o <<= 1) v += __shfl_xor(v, o);
+  return v;
+}
+
+// ---- k_mla_prep ---------------------------------------------------------
+// blocks [0, H*QB): qlat rows (h, 64 latent rows each) for every batch row;
+// blocks [H*QB, H*QB + B): batch row b's q pe rotation, latent norm and cache
+// append.  256 threads.
+template <bool FP8>
+__global__ __launch_bounds__(256) void k_mla_prep(ThvmMlaArgs a) {
+  extern __shared__ float sm[];
+  const uint32_t H = a.H, dn = a.dn, dr = a.dr, kv = a.kv, half = dr / 2, qs = dn + dr;
+  const uint32_t qoff = H * qs, QB = kv / 64;
+  const int32_t pos = a.len[0] - 1;
+  if (blockIdx.x < H * QB) {
+    const uint32_t h = blockIdx.x / QB, k0 = (blockIdx.x % QB) * 64;
+    // q nope of every batch row into LDS (f32)
+    for (uint32_t i = threadIdx.x; i < a.B * dn; i += blockDim.x) {
+      const uint32_t b = i / dn, d = i % dn;
+      sm[i] = bfv(a.qkv, (uint64_t)b * a.ldq + h * qs + d);
+    }
+    __syncthreads();
+    const uint32_t rowb = dn * (FP8 ? 1 : 2), LPR = rowb / 16;     // lanes per row
+    const uint32_t lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    const uint32_t rpp = 64 / LPR;                                 // rows per wave pass
+    const uint32_t sub = lane / LPR, c = lane % LPR;
+    for (uint32_t r0 = wv * rpp; r0 < 64; r0 += 4 * rpp) {
+      const uint32_t k = k0 + r0 + sub;
+      const bool ok = r0 + sub < 64 && k < kv;
+      const uint64_t row = (uint64_t)h * kv + (ok ? k : 0);
+      const char *wp = (const char *)a.wuk + row * rowb + (uint64_t)c * 16;
+      uint4 q0 = ok ? ld_stream16(wp) : make_uint4(0, 0, 0, 0), q1 = make_uint4(0, 0, 0, 0);
+      float w[16];
+      w16<FP8>(q0, q1, w);
+      const uint32_t e0 = c * (FP8 ? 16 : 8), ne = FP8 ? 16 : 8;
+      const float s = a.suk ? a.suk[row] : 1.0f;
+      for (uint32_t b = 0; b < a.B; b++) {
+        float acc = 0.0f;
+        for (uint32_t i = 0; i < ne; i++) acc += sm[b * dn + e0 + i] * w[i];
+        acc = group_sum(acc, (int)LPR);
+        if (ok && c == 0) a.qlat[((uint64_t)b * H + h) * kv + k] = acc * s;
+      }
+    }
+    return;
+  }
+  const uint32_t b = blockIdx.x - H * QB;
+  if (b >= a.B || pos < 0 || (uint32_t)pos >= a.max_seq) return;
+  const uint64_t qb = (uint64_t)b * a.ldq;
+  // q pe pairs (2j, 2j+1) -> halves j and half+j, after rounding through bf16
+  for (uint32_t i = threadIdx.x; i < H * half; i += blockDim.x) {
+    const uint32_t h = i / half, j = i % half, base = h * qs + dn;
+    const float xe = bfv(a.qkv, qb + base + 2 * j), xo = bfv(a.qkv, qb + base + 2 * j + 1);
+    const float c = a.rope_cos[(uint64_t)pos * half + j], sn = a.rope_sin[(uint64_t)pos * half + j];
+    bf16_t *q = (bf16_t *)a.qpe + ((uint64_t)b * H + h) * dr;
+    q[j] = f2bf(xe * c - xo * sn);
+    q[half + j] = f2bf(xo * c + xe * sn);
+  }
+  // latent row: RMSNorm over kv values, gain wkvn, append at pos
+  float ss = 0.0f;
+  for (uint32_t t = threadIdx.x; t < kv; t += blockDim.x) {
+    const float v = bfv(a.qkv, qb + qoff + t);
+    sm[t] = v;
+    ss += v * v;
+  }
+  ss = wave_sum(ss);
+  float *red = sm + kv;
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
+  __syncthreads();
+  float tot = 0.0f;
+  for (uint32_t w = 0; w < blockDim.x / 64; w++) tot += red[w];
+  const float inv = 1.0f / sqrtf(tot * (1.0f / (float)kv) + a.eps);
+  bf16_t *crow = (bf16_t *)a.ckv + ((uint64_t)b * a.max_seq + (uint32_t)pos) * kv;
+  for (uint32_t t = threadIdx.x; t < kv; t += blockDim.x) crow[t] = f2bf((sm[t] * inv) * a.wkvn[t]);
+  bf16_t *prow = (bf16_t *)a.kpe + ((uint64_t)b * a.max_seq + (uint32_t)pos) * dr;
+  for (uint32_t j = threadIdx.x; j < half; j += blockDim.x) {
+    const float xe = bfv(a.qkv, qb + qoff + kv + 2 * j), xo = bfv(a.qkv, qb + qoff + kv + 2 * j + 1);
+    const float c = a.rope_cos[(uint64_t)pos * half + j], sn = a.rope_sin[(uint64_t)pos * half + j];
+    prow[j] = f2bf(xe * c - xo * sn);
+    prow[half + j] = f2bf(xo * c + xe * sn);
+  }
+}
+
+// ---- k_mla_split --------------------------------------------------------
+// grid (n_split, B), 512 threads.  HT heads (8 or 16), KPL latent values per
+// lane (kv = 64 * KPL).
+template <int HT, int KPL>
+__global__ __launch_bounds__(MLA_THREADS) void k_mla_split(ThvmMlaArgs a) {
+  extern __shared__ float smem[];
+  constexpr uint32_t KV = 64 * KPL;
+  bf16_t *cs = (bf16_t *)smem;                          // [64][KV]
+  float *sp = smem + (MLA_CHUNK * KV) / 2;              // [HT][64]
+  const uint32_t split = blockIdx.x, b = blockIdx.y, dr = a.dr;
+  const int32_t L = min(a.len[0], (int32_t)a.max_seq);   // rows [0, L) are live
+  const uint32_t j0 = split * MLA_CHUNK;
+  if (L <= 0 || j0 >= (uint32_t)L) return;
+  const uint32_t nj = min((uint32_t)L - j0, (uint32_t)MLA_CHUNK);
+  const uint32_t lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+
+  // this lane's slice of every head's qlat and q pe
+  float ql[HT][KPL], qp[HT];
+#pragma unroll
+  for (int h = 0; h < HT; h++) {
+    const float *src = a.qlat + ((uint64_t)b * HT + h) * KV + lane * KPL;
+#pragma unroll
+    for (int i = 0; i < KPL; i++) ql[h][i] = src[i];
+    qp[h] = lane < dr ? bfv(a.qpe, ((uint64_t)b * HT + h) * dr + lane) : 0.0f;
+  }
+  // scores: wave wv takes rows wv, wv+8, ...; loads first, then arithmetic
+  constexpr int RPW = MLA_CHUNK / 8;
+  uint32_t cw[RPW][(KPL + 1) / 2];
+  float pv[RPW];
+  const bf16_t *cb = (const bf16_t *)a.ckv + ((uint64_t)b * a.max_seq + j0) * KV;
+  const bf16_t *pb = (const bf16_t *)a.kpe + ((uint64_t)b * a.max_seq + j0) * dr;
+#pragma unroll
+  for (int r = 0; r < RPW; r++) {
+    const uint32_t j = wv + 8 * r;
+    const bool ok = j < nj;
+    const bf16_t *row = cb + (uint64_t)(ok ? j : 0) * KV + lane * KPL;
+    if (KPL == 8) {
+      uint4 v = ok ? *(const uint4 *)row : make_uint4(0, 0, 0, 0);
+      cw[r][0] = v.x; cw[r][1] = v.y; cw[r][2] = v.z; cw[r][3] = v.w;
+    } else if (KPL == 4) {
+      uint2 v = ok ? *(const uint2 *)row : make_uint2(0, 0);
+      cw[r][0] = v.x; cw[r][1] = v.y;
+    } else if (KPL == 2) {
+      cw[r][0] = ok ? *(const uint32_t *)row : 0u;
+    } else {
+      cw[r][0] = ok ? (uint32_t)row[0] : 0u;
+    }
+    pv[r] = (ok && lane < dr) ? bf2f(pb[(uint64_t)j * dr + lane]) : 0.0f;
+  }
+#pragma unroll
+  for (int r = 0; r < RPW; r++) {
+    const uint32_t j = wv + 8 * r;
+    if (j >= nj) break;                                  // wave-uniform
+    float c[KPL];
+    if (KPL == 1) {
+      c[0] = __uint_as_float(cw[r][0] << 16);
+      cs[j * KV + lane] = (bf16_t)cw[r][0];
+    } else {
+#pragma unroll
+      for (int i = 0; i < KPL / 2; i++) {
+        c[2 * i] = __uint_as_float(cw[r][i] << 16);
+        c[2 * i + 1] = __uint_as_float(cw[r][i] & 0xffff0000u);
+      }
+      uint32_t *dst = (uint32_t *)(cs + j * KV + lane * KPL);
+#pragma unroll
+      for (int i = 0; i < KPL / 2; i++) dst[i] = cw[r][i];
+    }
+#pragma unroll
+    for (int h = 0; h < HT; h++) {
+      float s = qp[h] * pv[r];
+#pragma unroll
+      for (int i = 0; i < KPL; i++) s += ql[h][i] * c[i];
+      s = wave_sum(s);
+      if (lane == 0) sp[h * MLA_CHUNK + j] = s * a.scale;
+    }
+  }
+  __syncthreads();
+  // per-head softmax partial over this block's rows
+  float *part = a.part + ((uint64_t)b * a.n_split + split) * HT * (KV + 2);
+  for (uint32_t h = wv; h < HT; h += 8) {
+    const float s = lane < nj ? sp[h * MLA_CHUNK + lane] : -INFINITY;
+    const float m = wave_max(s);
+    const float e = lane < nj ? expf(s - m) : 0.0f;
+    const float l = wave_sum(e);
+    sp[h * MLA_CHUNK + lane] = e;
+    if (lane == 0) {
+      part[h * (KV + 2) + KV] = m;
+      part[h * (KV + 2) + KV + 1] = l;
+    }
+  }
+  __syncthreads();
+  // olat partial: thread t owns latent column t for every head
+  const uint32_t t = threadIdx.x;
+  if (t < KV) {
+    float acc[HT];
+#pragma unroll
+    for (int h = 0; h < HT; h++) acc[h] = 0.0f;
+    for (uint32_t j = 0; j < nj; j++) {
+      const float c = bf2f(cs[j * KV + t]);
+#pragma unroll
+      for (int h = 0; h < HT; h++) acc[h] += sp[h * MLA_CHUNK + j] * c;
+    }
+#pragma unroll
+    for (int h = 0; h < HT; h++) part[h * (KV + 2) + t] = acc[h];
+  }
+}
+
+// ---- k_mla_out ----------------------------------------------------------
+// grid (B*H, ceil(dv/32)), 256 threads: merge the live splits of (b, h) into
+// olat (LDS), then o[b][h][m] = bf16(scale_m * sum_k olat[k] W_uv[h][m][k]).
+template <bool FP8>
+__global__ __launch_bounds__(256) void k_mla_out(ThvmMlaArgs a) {
+  extern __shared__ float ol[];
+  const uint32_t bh = blockIdx.x, b = bh / a.H, h = bh % a.H, kv = a.kv, dv = a.dv;
+  const int32_t L = min(a.len[0], (int32_t)a.max_seq);
+  const uint32_t ns = L > 0 ? ((uint32_t)L + MLA_CHUNK - 1) / MLA_CHUNK : 0;
+  const uint64_t pst = (uint64_t)a.H * (kv + 2);
+  const float *p0 = a.part + (uint64_t)b * a.n_split * pst + (uint64_t)h * (kv + 2);
+  float M = -INFINITY;
+  for (uint32_t s = 0; s < ns; s++) M = fmaxf(M, p0[s * pst + kv]);
+  float den = 0.0f;
+  for (uint32_t s = 0; s < ns; s++) den += expf(p0[s * pst + kv] - M) * p0[s * pst + kv + 1];
+  const float rden = 1.0f / den;
+  for (uint32_t k = threadIdx.x; k < kv; k += blockDim.x) {
+    float acc = 0.0f;
+    for (uint32_t s = 0; s < ns; s++) acc += expf(p0[s * pst + kv] - M) * p0[s * pst + k];
+    ol[k] = acc * rden;
+  }
+  __syncthreads();
+  const uint32_t rowb = kv * (FP8 ? 1 : 2), LPR = rowb / 16 < 64 ? rowb / 16 : 64;
+  const uint32_t CPL = rowb / 16 / LPR;                 // chunks per lane (kv > 1024 fp8)
+  const uint32_t lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const uint32_t rpp = 64 / LPR, sub = lane / LPR, c = lane % LPR;
+  const uint32_t m0 = blockIdx.y * 32, m1 = min(m0 + 32, dv);
+  for (uint32_t r0 = m0 + wv * rpp; r0 < m1; r0 += 4 * rpp) {
+    const uint32_t mm = r0 + sub;
+    const bool ok = mm < m1;
+    const uint64_t row = (uint64_t)h * dv + (ok ? mm : m0);
+    float acc = 0.0f;
+    for (uint32_t q = 0; q < CPL; q++) {
+      const uint32_t ch = c + q * LPR;
+      const char *wp = (const char *)a.wuv + row * rowb + (uint64_t)ch * 16;
+      uint4 q0 = ok ? ld_stream16(wp) : make_uint4(0, 0, 0, 0);
+      float w[16];
+      w16<FP8>(q0, make_uint4(0, 0, 0, 0), w);
+      const uint32_t e0 = ch * (FP8 ? 16 : 8), ne = FP8 ? 16 : 8;
+      for (uint32_t i = 0; i < ne; i++) acc += ol[e0 + i] * w[i];
+    }
+    acc = group_sum(acc, (int)LPR);
+    if (ok && c == 0) {
+      const float s = a.suv ? a.suv[row] : 1.0f;
+      ((bf16_t *)a.o)[(uint64_t)b * a.H * dv + (uint64_t)h * dv + mm] = f2bf(acc * s);
+    }
+  }
+}
+
+// -------------------------------------------------------------------------
+static int mla_common(const ThvmMlaArgs *a, char *err, int errlen) {
+  if (a->B == 0 || a->H == 0 || a->dn == 0 || a->dr == 0 || a->dr % 2 || a->dr > 64 ||
+      (a->kv != 64 && a->kv != 128 && a->kv != 256 && a->kv != 512) || a->dv == 0 ||
+      a->max_seq == 0) {
+    snprintf(err, errlen, "mla: bad geometry B=%u H=%u dn=%u dr=%u kv=%u dv=%u", a->B, a->H,
+             a->dn, a->dr, a->kv, a->dv);
+    return -1;
+  }
+  if (a->wdt != THVM_DT_FP8E4M3 && a->wdt != THVM_DT_BF16) {
+    snprintf(err, errlen, "mla: absorbed weights must be fp8 e4m3 or bf16");
+    return -1;
+  }
+  return 0;
+}
+
+extern "C" int thvm_k_mla_prep(const ThvmMlaArgs *a, hipStream_t s, char *err, int errlen) {
+  if (mla_common(a, err, errlen)) return -1;
+  const uint32_t wsz = a->wdt == THVM_DT_FP8E4M3 ? 1 : 2;
+  const uint32_t lpr = a->dn * wsz / 16;
+  if ((a->dn * wsz) % 16 || lpr > 64 || (lpr & (lpr - 1)) ||
+      a->ldq < a->H * (a->dn + a->dr) + a->kv + a->dr || ((uintptr_t)a->wuk & 15)) {
+    snprintf(err, errlen, "mla_prep: d_nope rows must be a power-of-two number of 16-byte chunks "
+             "(<= 64) and ldq hold the q|kv row");
+    return -1;
+  }
+  const uint32_t QB = a->kv / 64;
+  uint64_t lds = (uint64_t)a->B * a->dn * 4;
+  if ((uint64_t)a->kv * 4 + 64 > lds) lds = (uint64_t)a->kv * 4 + 64;
+  if (lds > 64 * 1024) { snprintf(err, errlen, "mla_prep: batch too large for LDS staging"); return -1; }
+  const dim3 grid(a->H * QB + a->B);
+  if (a->wdt == THVM_DT_FP8E4M3) thvm_launch(true, true, k_mla_prep<true>, grid, dim3(256), (uint32_t)lds, s, *a);
+  else thvm_launch(true, true, k_mla_prep<false>, grid, dim3(256), (uint32_t)lds, s, *a);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) { snprintf(err, errlen, "mla_prep launch: %s", hipGetErrorString(e)); return -1; }
+  return 0;
+}
+
+typedef void (*mla_split_fn)(ThvmMlaArgs);
+template <int HT>
+static mla_split_fn pick_kpl(uint32_t kv) {
+  switch (kv / 64) {
+    case 1: return k_mla_split<HT, 1>;
+    case 2: return k_mla_split<HT, 2>;
+    case 4: return k_mla_split<HT, 4>;
+    case 8: return k_mla_split<HT, 8>;
+    default: return nullptr;
+  }
+}
+
+extern "C" uint64_t thvm_k_mla_part_bytes(uint32_t B, uint32_t H, uint32_t kv, uint32_t n_split) {
+  return (uint64_t)B * n_split * H * (kv + 2) * 4;
+}
+
+extern "C" int thvm_k_mla_attn(const ThvmMlaArgs *a, hipStream_t s, char *err, int errlen) {
+  if (mla_common(a, err, errlen)) return -1;
+  const uint32_t wsz = a->wdt == THVM_DT_FP8E4M3 ? 1 : 2;
+  if (a->n_split * MLA_CHUNK < a->max_seq) {
+    snprintf(err, errlen, "mla_attn: n_split %u * %u < max_seq %u", a->n_split, MLA_CHUNK, a->max_seq);
+    return -1;
+  }
+  if ((a->kv * wsz) % 16 || (a->kv * wsz / 16 > 64 && (a->kv * wsz / 16) % 64) || ((uintptr_t)a->wuv & 15)) {
+    snprintf(err, errlen, "mla_attn: W_uv rows must be 16-byte multiples");
+    return -1;
+  }
+  mla_split_fn f = a->H == 16 ? pick_kpl<16>(a->kv) : a->H == 8 ? pick_kpl<8>(a->kv) : nullptr;
+  if (!f) { snprintf(err, errlen, "mla_attn: no kernel for H=%u kv=%u (H in {8,16})", a->H, a->kv); return -1; }
+  const uint32_t lds = (uint32_t)(MLA_CHUNK * a->kv * 2 + a->H * MLA_CHUNK * 4);
+  if (lds > 64 * 1024) {
+    hipError_t e = hipFuncSetAttribute((const void *)f, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    if (e != hipSuccess) { snprintf(err, errlen, "mla_attn: hipFuncSetAttribute: %s", hipGetErrorString(e)); return -1; }
+  }
+  thvm_launch(true, false, f, dim3(a->n_split, a->B), dim3(MLA_THREADS), lds, s, *a);
+  const dim3 g2(a->B * a->H, (a->dv + 31) / 32);
+  const uint32_t lds2 = a->kv * 4;
+  if (a->wdt == THVM_DT_FP8E4M3) thvm_launch(false, true, k_mla_out<true>, g2, dim3(256), lds2, s, *a);
+  else thvm_launch(false, true, k_mla_out<false>, g2, dim3(256), lds2, s, *a);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) { snprintf(err, errlen, "mla_attn launch: %s", hipGetErrorString(e)); return -1; }
+  return 0;
+}

@@ -1,0 +1,264 @@
+// moe.hip -- DeepSeek-V2 mixture-of-experts decode on gfx950: router top-K
+// and the routed + shared expert FFN with an index gather on the weights.
+//
+// Replaces the reference's route (bench/dsv2_decode_bench.c :787-863),
+// moe_full_h (:865-910) and moe_full_out (:912-965).  Design for gfx950:
+//   * k_route: one wave per batch row; lane e holds gate logit e, the max and
+//     the softmax denominator are DPP wave reductions, each of the K rounds is
+//     a butterfly arg-max over (value desc, index asc) -- the same winner as
+//     the reference's serial scan (ties to the lowest expert id);
+//   * k_moe_gateup: one wave per (gate_i, up_i) row pair of a selected (or
+//     shared) expert; the expert id is read from sel on the device, so the
+//     gather is an address computation, not a copy; the row loads are issued
+//     before x is staged into LDS (x rounded to bf16, the experts' input
+//     dtype), 16-byte nontemporal loads, fp8 decoded with v_cvt_pk_f32_fp8,
+//     h = silu(g)*u kept in f32 as the reference keeps it;
+//   * k_moe_down: one wave per output row d; the K routed segments (row d of
+//     each selected expert's down matrix) and the shared segment are all in
+//     flight before any arithmetic, h sits in LDS, the weighted sum follows
+//     the reference's order (routed slots ascending, then shared) and the
+//     residual add rounds like the reference's mm-out + add chain.
+#include "dev_common.h"
+#include "../kern_api.h"
+#include "launch.h"
+#include <stdio.h>
+#include <limits.h>
+
+#define MOE_WAVES 8
+#define MOE_THREADS (64 * MOE_WAVES)
+#define MOE_MAXC 4      /* 16-byte chunks per lane per row: rows up to 4 KiB */
+#define MOE_MAXCS 8     /* the shared-expert down row: up to 8 KiB */
+#define MOE_MAXK 8      /* routed experts per token */
+
+// ---- router ---------------------------------------------------------------
+__global__ __launch_bounds__(64) void k_route(ThvmRouteArgs a) {
+  const uint32_t b = blockIdx.x, lane = threadIdx.x, E = a.E;
+  const float g = lane < E ? a.logits[(uint64_t)b * E + lane] : -INFINITY;
+  const float mx = wave_max(g);
+  const float sum = wave_sum(lane < E ? expf(g - mx) : 0.0f);
+  bool used = lane >= E;
+  for (uint32_t kk = 0; kk < a.K; kk++) {
+    float bv = used ? -INFINITY : g;
+    int bi = used ? INT_MAX : (int)lane;
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+      const float ov = __shfl_xor(bv, o);
+      const int oi = __shfl_xor(bi, o);
+      if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
+    }
+    if ((int)lane == bi) used = true;
+    if (lane == 0) {
+      a.sel[(uint64_t)b * a.K + kk] = bi;
+      a.probs[(uint64_t)b * a.K + kk] = expf(bv - mx) / sum;
+    }
+  }
+}
+
+// decode one 16-byte chunk: 16 fp8 or 8 bf16 weights
+template <bool FP8>
+__device__ __forceinline__ void chunk_f32(const uint4 &q, float o[16]) {
+  if (FP8) {
+    fp8x4_to_f32(q.x, o); fp8x4_to_f32(q.y, o + 4);
+    fp8x4_to_f32(q.z, o + 8); fp8x4_to_f32(q.w, o + 12);
+  } else {
+    const uint32_t w[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      o[2 * i] = __uint_as_float(w[i] << 16);
+      o[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
+    }
+  }
+}
+
+// dot of one row's chunks held by this lane with LDS vector v (elements of
+// chunk ch start at ch*EPC)
+template <bool FP8, int NC>
+__device__ __forceinline__ float chunk_dot(const uint4 (&q)[NC], const float *v,
+                                           uint32_t lane, uint32_t nch) {
+  constexpr uint32_t EPC = FP8 ? 16 : 8;
+  float acc = 0.0f;
+#pragma unroll
+  for (int c = 0; c < NC; c++) {
+    const uint32_t ch = lane + 64u * c;
+    if (ch < nch) {
+      float w[16];
+      chunk_f32<FP8>(q[c], w);
+#pragma unroll
+      for (uint32_t i = 0; i < EPC; i++) acc += v[ch * EPC + i] * w[i];
+    }
+  }
+  return acc;
+}
+
+template <int NC>
+__device__ __forceinline__ void load_row(uint4 (&q)[NC], const char *row, uint32_t lane,
+                                         uint32_t nch, bool ok) {
+#pragma unroll
+  for (int c = 0; c < NC; c++) {
+    const uint32_t ch = lane + 64u * c;
+    q[c] = (ok && ch < nch) ? ld_stream16(row + (uint64_t)ch * 16) : make_uint4(0, 0, 0, 0);
+  }
+}
+
+// ---- gate/up --------------------------------------------------------------
+// grid (ceil(P / 8), B) with P = K*I + S row pairs per batch row
+template <bool FP8>
+__global__ __launch_bounds__(MOE_THREADS) void k_moe_gateup(ThvmMoeArgs a) {
+  extern __shared__ float xs[];
+  const uint32_t b = blockIdx.y, D = a.D, I = a.I, K = a.K;
+  const uint32_t P = K * I + a.S;
+  const uint32_t lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const uint32_t p = blockIdx.x * MOE_WAVES + wv;
+  const uint64_t rowb = (uint64_t)D * (FP8 ? 1 : 2);
+  const uint32_t nch = (uint32_t)(rowb / 16);
+  const bool live = p < P;
+  const char *base;
+  const float *sc;
+  uint64_t row0;
+  if (live && p < K * I) {
+    const uint32_t e = p / I, i = p % I;
+    int32_t id = a.sel[(uint64_t)b * K + e];
+    id = id < 0 ? 0 : id >= (int32_t)a.E ? (int32_t)a.E - 1 : id;   // a valid expert row
+    row0 = (uint64_t)id * 2 * I + 2 * i;
+    base = (const char *)a.wgu_e;
+    sc = a.sgu_e;
+  } else {
+    row0 = live ? 2ull * (p - K * I) : 0;
+    base = (const char *)a.wgu_s;
+    sc = a.sgu_s;
+  }
+  uint4 gq[MOE_MAXC], uq[MOE_MAXC];
+  load_row(gq, base + row0 * rowb, lane, nch, live);
+  load_row(uq, base + (row0 + 1) * rowb, lane, nch, live);
+  for (uint32_t i = threadIdx.x; i < D; i += MOE_THREADS) xs[i] = rbf(a.x[(uint64_t)b * D + i]);
+  __syncthreads();
+  if (!live) return;
+  float G = wave_sum(chunk_dot<FP8>(gq, xs, lane, nch));
+  float U = wave_sum(chunk_dot<FP8>(uq, xs, lane, nch));
+  if (lane == 0) {
+    if (sc) { G *= sc[row0]; U *= sc[row0 + 1]; }
+    a.h[(uint64_t)b * P + p] = silu_f(G) * U;
+  }
+}
+
+// ---- down + residual ------------------------------------------------------
+// grid (ceil(D / 8), B): wave per output row d
+template <bool FP8>
+__global__ __launch_bounds__(MOE_THREADS) void k_moe_down(ThvmMoeArgs a) {
+  extern __shared__ float hs[];
+  const uint32_t b = blockIdx.y, D = a.D, I = a.I, K = a.K, S = a.S;
+  const uint32_t P = K * I + S;
+  const uint32_t lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const uint32_t d = blockIdx.x * MOE_WAVES + wv;
+  const bool live = d < D;
+  const uint64_t rI = (uint64_t)I * (FP8 ? 1 : 2), rS = (uint64_t)S * (FP8 ? 1 : 2);
+  const uint32_t nI = (uint32_t)(rI / 16), nS = (uint32_t)(rS / 16);
+  uint4 q[MOE_MAXK][MOE_MAXC], qs[MOE_MAXCS];
+  int32_t ids[MOE_MAXK];
+#pragma unroll
+  for (int e = 0; e < MOE_MAXK; e++) {
+    ids[e] = (e < (int)K) ? a.sel[(uint64_t)b * K + e] : 0;
+    ids[e] = ids[e] < 0 ? 0 : ids[e] >= (int32_t)a.E ? (int32_t)a.E - 1 : ids[e];
+    const bool ok = live && e < (int)K;
+    const uint64_t row = (uint64_t)(ok ? ids[e] : 0) * D + (live ? d : 0);
+    load_row(q[e], (const char *)a.wd_e + row * rI, lane, nI, ok);
+  }
+  load_row(qs, (const char *)a.wd_s + (uint64_t)(live ? d : 0) * rS, lane, nS, live && S > 0);
+  for (uint32_t i = threadIdx.x; i < P; i += MOE_THREADS) hs[i] = a.h[(uint64_t)b * P + i];
+  __syncthreads();
+  if (!live) return;
+  float acc = 0.0f;
+#pragma unroll
+  for (int e = 0; e < MOE_MAXK; e++) {
+    if (e >= (int)K) break;
+    float s = wave_sum(chunk_dot<FP8>(q[e], hs + e * I, lane, nI));
+    if (a.sd_e) s *= a.sd_e[(uint64_t)ids[e] * D + d];
+    acc += a.probs[(uint64_t)b * K + e] * s;
+  }
+  if (S > 0) {
+    float s = wave_sum(chunk_dot<FP8>(qs, hs + K * I, lane, nS));
+    if (a.sd_s) s *= a.sd_s[d];
+    acc += s;
+  }
+  if (lane == 0) {
+    bf16_t *r = (bf16_t *)a.res + (uint64_t)b * D + d;
+    r[0] = f2bf(bf2f(r[0]) + rbf(acc));
+  }
+}
+
+// -------------------------------------------------------------------------
+extern "C" int thvm_k_route(const ThvmRouteArgs *a, hipStream_t s, char *err, int errlen) {
+  if (a->B == 0 || a->E == 0 || a->E > 64 || a->K == 0 || a->K > a->E) {
+    snprintf(err, errlen, "route: need 1 <= K <= E <= 64 (E=%u K=%u)", a->E, a->K);
+    return -1;
+  }
+  thvm_launch(true, true, k_route, dim3(a->B), dim3(64), 0, s, *a);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) { snprintf(err, errlen, "route launch: %s", hipGetErrorString(e)); return -1; }
+  return 0;
+}
+
+static int moe_check(const ThvmMoeArgs *a, int gateup, char *err, int errlen) {
+  const uint32_t wsz = a->wdt == THVM_DT_FP8E4M3 ? 1 : a->wdt == THVM_DT_BF16 ? 2 : 0;
+  if (!wsz) { snprintf(err, errlen, "moe: weights must be fp8 e4m3 or bf16"); return -1; }
+  if (a->B == 0 || a->D == 0 || a->E == 0 || a->K == 0 || a->K > MOE_MAXK || a->K > a->E ||
+      a->I == 0) {
+    snprintf(err, errlen, "moe: bad geometry (K <= %u)", MOE_MAXK);
+    return -1;
+  }
+  const uint64_t rd = (uint64_t)a->D * wsz, ri = (uint64_t)a->I * wsz, rs = (uint64_t)a->S * wsz;
+  const bool rows_ok = gateup ? (rd % 16 == 0 && rd <= 64 * 16 * MOE_MAXC)
+                               : (ri % 16 == 0 && rs % 16 == 0 && ri <= 64 * 16 * MOE_MAXC &&
+                                  rs <= 64 * 16 * MOE_MAXCS);
+  if (!rows_ok) {
+    snprintf(err, errlen, "moe: weight rows must be 16-byte multiples up to %u bytes (%u for the "
+             "shared down row)", 64 * 16 * MOE_MAXC, 64 * 16 * MOE_MAXCS);
+    return -1;
+  }
+  const void *we = gateup ? a->wgu_e : a->wd_e, *ws = gateup ? a->wgu_s : a->wd_s;
+  const float *se = gateup ? a->sgu_e : a->sd_e, *ss = gateup ? a->sgu_s : a->sd_s;
+  if (!we || (a->S && !ws) || (((uintptr_t)we | (uintptr_t)ws) & 15)) {
+    snprintf(err, errlen, "moe: weights missing or not 16-byte aligned");
+    return -1;
+  }
+  if (a->wdt == THVM_DT_FP8E4M3 && (!se || (a->S && !ss))) {
+    snprintf(err, errlen, "moe: fp8 weights need their row scales");
+    return -1;
+  }
+  if (gateup ? (!a->h || !a->x || !a->sel) : (!a->h || !a->res || !a->sel || !a->probs)) {
+    snprintf(err, errlen, "moe: missing operand");
+    return -1;
+  }
+  return 0;
+}
+
+extern "C" int thvm_k_moe_gateup(const ThvmMoeArgs *a, hipStream_t s, char *err, int errlen) {
+  if (moe_check(a, 1, err, errlen)) return -1;
+  const uint32_t P = a->K * a->I + a->S;
+  const dim3 grid((P + MOE_WAVES - 1) / MOE_WAVES, a->B);
+  const uint32_t lds = a->D * 4;
+  if (lds > 64 * 1024) { snprintf(err, errlen, "moe: D too large"); return -1; }
+  if (a->wdt == THVM_DT_FP8E4M3) thvm_launch(true, true, k_moe_gateup<true>, grid, dim3(MOE_THREADS), lds, s, *a);
+  else thvm_launch(true, true, k_moe_gateup<false>, grid, dim3(MOE_THREADS), lds, s, *a);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) { snprintf(err, errlen, "moe_gateup launch: %s", hipGetErrorString(e)); return -1; }
+  return 0;
+}
+
+extern "C" int thvm_k_moe_down(const ThvmMoeArgs *a, hipStream_t s, char *err, int errlen) {
+  if (moe_check(a, 0, err, errlen)) return -1;
+  const uint32_t P = a->K * a->I + a->S;
+  const uint32_t lds = P * 4;
+  if (lds > 160 * 1024) { snprintf(err, errlen, "moe: K*I+S too large for LDS"); return -1; }
+  const dim3 grid((a->D + MOE_WAVES - 1) / MOE_WAVES, a->B);
+  typedef void (*down_fn)(ThvmMoeArgs);
+  const down_fn f = a->wdt == THVM_DT_FP8E4M3 ? k_moe_down<true> : k_moe_down<false>;
+  if (lds > 64 * 1024) {
+    hipError_t e = hipFuncSetAttribute((const void *)f, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    if (e != hipSuccess) { snprintf(err, errlen, "moe_down: hipFuncSetAttribute: %s", hipGetErrorString(e)); return -1; }
+  }
+  thvm_launch(true, true, f, grid, dim3(MOE_THREADS), lds, s, *a);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) { snprintf(err, errlen, "moe_down launch: %s", hipGetErrorString(e)); return -1; }
+  return 0;
+}
