@@ -9,6 +9,8 @@ kernel (the fp8 GEMV) against 8 TB/s.  `--config` selects another workload:
       fp16 softmax and RMSNorm over [M, 4096]
   C3  GPT-2 XL fp16 (48L, D1600, H25, F6400, V50257), context 128, batch 1 or 8
   C4  Llama-8B shape fp8 weight-only, bf16 activations, context 2048, batch 1 or 16
+  C5  DeepSeek-V2-Lite shape (27L, D2048, MLA kv_lora 512, 64 experts top-6 + 2
+      shared, V102400) fp8 weights, bf16 latent cache at context 4096, batch 1
 
 One "step" is one greedy decode token for every batch row: one hipGraph
 replay of the captured decode step (embedding, per-layer norm + projections +
@@ -51,6 +53,13 @@ MODELS = {
                         init_std=0.02),
                ctx=128, cpu_steps=2,
                name="C3 GPT-2 XL-shape fp16 greedy decode, KV prefilled to context 128 (prompt length)"),
+    "C5": dict(cfg=dict(arch=3, n_layers=27, dim=2048, n_heads=16, n_kv_heads=16, head_dim=192,
+                        ffn=10944, vocab=102400, wdtype=DT_FP8, adtype=DT_BF16, eps=1e-6,
+                        rope_theta=10000.0, init_std=0.02, kv_lora=512, d_nope=128, d_rope=64,
+                        d_v=128, n_experts=64, n_shared=2, top_k=6, moe_inter=1408, first_dense=1),
+               ctx=4096, cpu_steps=2,
+               name="C5 DeepSeek-V2-Lite-shape MLA + MoE fp8 decode, latent cache prefilled to "
+                    "context 4096"),
     "C4": dict(cfg=dict(arch=1, n_layers=32, dim=4096, n_heads=32, n_kv_heads=8, head_dim=128,
                         ffn=14336, vocab=128256, wdtype=DT_FP8, adtype=DT_BF16, eps=1e-5,
                         rope_theta=500000.0, init_std=0.02),
@@ -75,8 +84,14 @@ def cpu_model_name() -> str:
 
 def attn_bytes_per_step(cfg, L) -> int:
     """K and V rows [0, L) of every layer and batch row, plus q read and the
-    attention output written."""
-    B, Hkv, hd, H = cfg["batch"], cfg["n_kv_heads"], cfg["head_dim"], cfg["n_heads"]
+    attention output written.  MLA (arch 3): the latent and k-pe rows [0, L),
+    the absorbed W_uv (fp8 + row scales), qlat/q-pe read and o written."""
+    B, H = cfg["batch"], cfg["n_heads"]
+    if cfg["arch"] == 3:
+        kv, dr, dv = cfg["kv_lora"], cfg["d_rope"], cfg["d_v"]
+        per = B * (L * (kv + dr) * 2 + H * (kv * 4 + dr * 2 + dv * 2)) + H * dv * (kv + 4)
+        return cfg["n_layers"] * per
+    Hkv, hd = cfg["n_kv_heads"], cfg["head_dim"]
     es = 4 if cfg["adtype"] == DT_F32 else 2
     return cfg["n_layers"] * B * (2 * Hkv * L * hd * es + 2 * H * hd * es)
 
@@ -90,7 +105,7 @@ def cpu_baseline(dec, cfg, n_steps: int):
     pos = dec.position
     tok = dec.tokens(pos + 1)[:, pos].astype(np.int32)
     t_read = time.time()
-    om = O.OracleModel(dec, dict(cfg))
+    om = O.OracleDsv2(dec, dict(cfg)) if cfg["arch"] == 3 else O.OracleModel(dec, dict(cfg))
     log(f"[bench] cpu baseline: read back {sum(a.nbytes for a in om.keep) / 1e9:.2f} GB of "
         f"weights + {sum(a.nbytes for a in om.caches) / 1e9:.2f} GB KV in {time.time() - t_read:.1f}s")
     t_cpu, errs, match = 0.0, [], True
@@ -150,17 +165,28 @@ def run_decode(thvm, key: str, batch: int, args) -> dict:
     for _ in range(prof_steps):
         thvm.builtin("delay", [dummy], n=3000)
         dec.step()
-    g_ms, g_n = thvm.kprof_query("gemv")
-    g_bytes = thvm.kprof_bytes("gemv")
-    a_ms, a_n = thvm.kprof_query("attn")
+    mla = cfg["arch"] == 3
+    atag = "mla_attn" if mla else "attn"
+    kern = {}
+    for tag in ("gemv", "moe_gateup", "moe_down", "mla_prep", "route", "norm", atag):
+        ms_t, n_t = thvm.kprof_query(tag)
+        if n_t:
+            kern[tag] = (ms_t, n_t, thvm.kprof_bytes(tag))
     thvm.kprof(False)
     dummy.free()
     L_prof = dec.position - 1
+    a_ms, a_n, _ = kern[atag]
+    kern[atag] = (a_ms, a_n, attn_bytes_per_step(cfg, L_prof) * prof_steps)
+    for tag, (ms_t, n_t, b_t) in kern.items():
+        log(f"[bench] {tag}: {n_t // prof_steps} launches/step, {ms_t / n_t * 1000:.1f} us avg"
+            + (f", {b_t / (ms_t / 1000.0) / 1e9:.0f} GB/s" if b_t else ""))
+    # the dominant kernel: the one moving the most algorithmic bytes per step
+    dom = max((t for t in kern if t != atag), key=lambda t: kern[t][2])
+    g_ms, g_n, g_bytes = kern[dom]
     gemv_gbs = g_bytes / (g_ms / 1000.0) / 1e9
-    attn_gbs = attn_bytes_per_step(cfg, L_prof) * prof_steps / (a_ms / 1000.0) / 1e9
-    log(f"[bench] gemv: {g_n} launches, {g_ms / g_n * 1000:.1f} us avg, {gemv_gbs:.0f} GB/s; "
-        f"attn: {a_n} launches, {a_ms / a_n * 1000:.1f} us avg, {attn_gbs:.0f} GB/s")
-    step_bytes = g_bytes // prof_steps + attn_bytes_per_step(cfg, L_mid)
+    attn_gbs = kern[atag][2] / (a_ms / 1000.0) / 1e9
+    step_bytes = sum(b for t, (_, _, b) in kern.items() if t != atag) // prof_steps + \
+        attn_bytes_per_step(cfg, L_mid)
 
     cpu = None
     if cpu_steps:
@@ -172,8 +198,11 @@ def run_decode(thvm, key: str, batch: int, args) -> dict:
                          f"with the device on the same inputs",
                "seconds": round(secs, 2), "ids_match": match, "logits_max_rel_err": lerr}
     mfma = batch > 4
-    gkern = ("k_gemm (MFMA v_mfma_f32_16x16x32, %s weights)" if mfma else
-             "k_gemv (%s weight GEMV)") % DT_NAME[cfg["wdtype"]]
+    if dom == "gemv":
+        gkern = ("k_gemm (MFMA v_mfma_f32_16x16x32, %s weights)" if mfma else
+                 "k_gemv (%s weight GEMV)") % DT_NAME[cfg["wdtype"]]
+    else:
+        gkern = f"k_{dom} ({DT_NAME[cfg['wdtype']]} expert weights gathered by the router)"
     out = {
         "metric": METRIC, "value": round(tps, 2), "unit": "tokens/s", "n_gpus": 1,
         "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms_per_step, 4),
@@ -194,8 +223,13 @@ def run_decode(thvm, key: str, batch: int, args) -> dict:
                      "algorithmic_bytes_per_launch": g_bytes // max(g_n, 1),
                      "launches_per_step": g_n // prof_steps,
                      "avg_launch_us": round(g_ms / g_n * 1000, 2)},
-        "attention": {"achieved_gbs": round(attn_gbs, 1), "frac": round(attn_gbs / PEAK_GBS, 4),
+        "attention": {"kernel": "k_mla_split + k_mla_out" if mla else "k_attn + k_attn_merge",
+                      "achieved_gbs": round(attn_gbs, 1), "frac": round(attn_gbs / PEAK_GBS, 4),
                       "avg_launch_us": round(a_ms / max(a_n, 1) * 1000, 2)},
+        "kernels": {t: {"launches_per_step": n_t // prof_steps,
+                        "avg_launch_us": round(ms_t / n_t * 1000, 2),
+                        "gbs": round(b_t / (ms_t / 1000.0) / 1e9, 1) if b_t else None}
+                    for t, (ms_t, n_t, b_t) in kern.items()},
         "step_hbm_gbs": round(step_bytes / (ms_per_step / 1000.0) / 1e9, 1),
         "step_bytes": step_bytes,
         "kernels_per_step": dec.step_kernels(),
@@ -318,7 +352,7 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=64)
     ap.add_argument("--warmup", type=int, default=4)
-    ap.add_argument("--config", default="C4", choices=["C1", "C2", "C3", "C4", "all"])
+    ap.add_argument("--config", default="C4", choices=["C1", "C2", "C3", "C4", "C5", "all"])
     ap.add_argument("--batch", type=int, default=1)
     ap.add_argument("--cpu-steps", type=int, default=0, help="oracle steps (0: the config's default)")
     ap.add_argument("--no-cpu", action="store_true")
@@ -338,7 +372,7 @@ def main() -> int:
         if args.copy_calibration:
             return copy_calibration(thvm)
         if args.config == "all":
-            runs = [("C4", 1), ("C4", 16), ("C3", 1), ("C3", 8), ("C1", 1), ("C2", 0)]
+            runs = [("C4", 1), ("C4", 16), ("C5", 1), ("C3", 1), ("C3", 8), ("C1", 1), ("C2", 0)]
         else:
             runs = [(args.config, args.batch)]
         for key, batch in runs:

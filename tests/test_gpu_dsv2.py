@@ -104,7 +104,7 @@ def test_mla_prep_and_attn(hip, shape, wdt):
     scale = 0.1352
     nsplit = (ms + 63) // 64
     o = hip.Buffer(B * H * dv * 2)
-    part = hip.Buffer(B * nsplit * H * (kv + 2) * 4)
+    part = hip.Buffer(B * nsplit * H * (kv + 4) * 4)
     args = [o, qlat, qpe, ckv, kpe, Lb, part, up(hip, wuv)] + ([up(hip, suv)] if f8 else [])
     hip.builtin("mla_attn", args, b=B, h=H, dn=dn, dr=dr, kv=kv, dv=dv, maxseq=ms, nsplit=nsplit,
                 wt=wdt, scale=scale)
@@ -137,7 +137,7 @@ def test_mla_closed_form_equal_rows(hip):
     nsplit = 3
     o = hip.Buffer(B * H * dv * 2)
     hip.builtin("mla_attn", [o, up(hip, qlat), up(hip, qpe), up(hip, ckv), up(hip, kpe),
-                             up(hip, np.array([L], np.int32)), hip.Buffer(B * nsplit * H * (kv + 2) * 4),
+                             up(hip, np.array([L], np.int32)), hip.Buffer(B * nsplit * H * (kv + 4) * 4),
                              up(hip, wuv)],
                 b=B, h=H, dn=dn, dr=dr, kv=kv, dv=dv, maxseq=ms, nsplit=nsplit, wt=DT_BF16, scale=0.2)
     got = unbf(o.read(np.uint16).reshape(H, dv))

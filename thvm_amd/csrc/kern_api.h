@@ -109,7 +109,7 @@ uint64_t thvm_k_attn_part_bytes(uint32_t B, uint32_t H, uint32_t Hkv, uint32_t h
  * dr/2+j), the latent row RMS-normed with gain wkvn and the rotated k pe row
  * appended at L-1, and qlat [B][H][kv] f32 = q_nope . W_uk (W_uk [H][kv][dn]).
  * mla_attn: split-sequence scores over rows [0, L) (s = (qlat.ckv + qpe.kpe)
- * * scale), partials part [B][n_split][H][kv+2], then the merge and the V
+ * * scale), partials part [B][n_split][H][kv+4] (m, l at kv, kv+1), then the merge and the V
  * up-projection o [B][H*dv] bf16 = olat . W_uv (W_uv [H][dv][kv]).  W_uk /
  * W_uv are fp8 e4m3 with per-row scales (suk [H*kv], suv [H*dv]) or bf16. */
 typedef struct ThvmMlaArgs {

@@ -159,6 +159,16 @@ __device__ __forceinline__ uint4 ld16(const void *p) {
   return *(const uint4 *)p;
 }
 
+// LDS slot of element k of a vector that lanes read in 16-byte weight chunks
+// of EPC elements (chunk ch = k / EPC belongs to one lane, consecutive chunks
+// to consecutive lanes): quad q of every chunk is stored contiguously across
+// chunks, so one lane's float4 read of quad q and its neighbours' reads fall on
+// consecutive 16-byte LDS words (no bank conflicts).  nch = chunks in the vector.
+template <int EPC>
+__device__ __forceinline__ uint32_t chunk_swz(uint32_t k, uint32_t nch) {
+  return (((k % EPC) >> 2) * nch + k / EPC) * 4 + (k & 3);
+}
+
 __device__ __forceinline__ float silu_f(float g) { return g / (1.0f + expf(-g)); }
 __device__ __forceinline__ float gelu_tanh_f(float x) {
   // tinygrad Tensor.gelu: 0.5 x (1 + tanh(sqrt(2/pi) (x + 0.044715 x^3)))

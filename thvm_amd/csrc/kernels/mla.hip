@@ -10,10 +10,11 @@
 //                append at L-1, and qlat = q_nope . W_uk (fp8/bf16 rows, per
 //                row scale) -- one launch, blocks split between the jobs;
 //   k_mla_split  split-sequence flash decode: a block owns 64 cache rows of
-//                one batch row, stages them in LDS once, scores all H heads
-//                against them (lanes split the latent dimension, DPP wave
-//                sums), and writes per-split (olat partial, max, sum) --
-//                the latent rows are read from HBM exactly once per step;
+//                one batch row and a group of 4 heads, stages the rows in LDS
+//                once, scores the group against them (lanes split the latent
+//                dimension, DPP wave sums), and writes per-split (olat
+//                partial, max, sum); the head groups of a split re-read its
+//                rows from L2, so HBM sees each latent row once per step;
 //   k_mla_out    merges the live splits per (row, head) in fixed order and
 //                applies the absorbed V up-projection W_uv, rounding o to
 //                bf16.
@@ -133,54 +134,68 @@ __global__ __launch_bounds__(256) void k_mla_prep(ThvmMlaArgs a) {
 }
 
 // ---- k_mla_split --------------------------------------------------------
-// grid (n_split, B), 512 threads.  HT heads (8 or 16), KPL latent values per
-// lane (kv = 64 * KPL).
-template <int HT, int KPL>
+// grid (n_split, H / MLA_HG, B), 512 threads: 64 cache rows of batch row b
+// against a group of MLA_HG heads (the latent rows of a split are re-read by
+// the H / MLA_HG head groups from L2, which buys 4x the blocks).  KPL latent
+// values per lane (kv = 64 * KPL).
+#define MLA_HG 4
+template <int KPL>
 __global__ __launch_bounds__(MLA_THREADS) void k_mla_split(ThvmMlaArgs a) {
   extern __shared__ float smem[];
   constexpr uint32_t KV = 64 * KPL;
+  constexpr int HG = MLA_HG;
   bf16_t *cs = (bf16_t *)smem;                          // [64][KV]
-  float *sp = smem + (MLA_CHUNK * KV) / 2;              // [HT][64]
-  const uint32_t split = blockIdx.x, b = blockIdx.y, dr = a.dr;
+  float *sp = smem + (MLA_CHUNK * KV) / 2;              // [64][HG]: scores, then weights
+  const uint32_t split = blockIdx.x, h0 = blockIdx.y * HG, b = blockIdx.z, dr = a.dr, H = a.H;
   const int32_t L = min(a.len[0], (int32_t)a.max_seq);   // rows [0, L) are live
   const uint32_t j0 = split * MLA_CHUNK;
   if (L <= 0 || j0 >= (uint32_t)L) return;
   const uint32_t nj = min((uint32_t)L - j0, (uint32_t)MLA_CHUNK);
   const uint32_t lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
 
-  // this lane's slice of every head's qlat and q pe
-  float ql[HT][KPL], qp[HT];
-#pragma unroll
-  for (int h = 0; h < HT; h++) {
-    const float *src = a.qlat + ((uint64_t)b * HT + h) * KV + lane * KPL;
-#pragma unroll
-    for (int i = 0; i < KPL; i++) ql[h][i] = src[i];
-    qp[h] = lane < dr ? bfv(a.qpe, ((uint64_t)b * HT + h) * dr + lane) : 0.0f;
-  }
-  // scores: wave wv takes rows wv, wv+8, ...; loads first, then arithmetic
+  // issue the cache-row loads first: wave wv takes rows wv, wv+8, ...  The
+  // loads are unconditional from clamped, always-live addresses (row j0 and
+  // lane 0 exist) and masked afterwards: a guarded load whose value is used
+  // inside its branch makes the compiler drain every outstanding load there.
   constexpr int RPW = MLA_CHUNK / 8;
   uint32_t cw[RPW][(KPL + 1) / 2];
-  float pv[RPW];
+  bf16_t pr[RPW];
   const bf16_t *cb = (const bf16_t *)a.ckv + ((uint64_t)b * a.max_seq + j0) * KV;
   const bf16_t *pb = (const bf16_t *)a.kpe + ((uint64_t)b * a.max_seq + j0) * dr;
+  const uint32_t pl_lane = lane < dr ? lane : 0;
 #pragma unroll
   for (int r = 0; r < RPW; r++) {
     const uint32_t j = wv + 8 * r;
-    const bool ok = j < nj;
-    const bf16_t *row = cb + (uint64_t)(ok ? j : 0) * KV + lane * KPL;
+    const uint32_t jc = j < nj ? j : 0;
+    const bf16_t *row = cb + (uint64_t)jc * KV + lane * KPL;
     if (KPL == 8) {
-      uint4 v = ok ? *(const uint4 *)row : make_uint4(0, 0, 0, 0);
+      uint4 v = ld_stream16(row);
       cw[r][0] = v.x; cw[r][1] = v.y; cw[r][2] = v.z; cw[r][3] = v.w;
     } else if (KPL == 4) {
-      uint2 v = ok ? *(const uint2 *)row : make_uint2(0, 0);
+      uint2 v = *(const uint2 *)row;
       cw[r][0] = v.x; cw[r][1] = v.y;
     } else if (KPL == 2) {
-      cw[r][0] = ok ? *(const uint32_t *)row : 0u;
+      cw[r][0] = *(const uint32_t *)row;
     } else {
-      cw[r][0] = ok ? (uint32_t)row[0] : 0u;
+      cw[r][0] = (uint32_t)row[0];
     }
-    pv[r] = (ok && lane < dr) ? bf2f(pb[(uint64_t)j * dr + lane]) : 0.0f;
+    pr[r] = pb[(uint64_t)jc * dr + pl_lane];
   }
+  float pv[RPW];
+#pragma unroll
+  for (int r = 0; r < RPW; r++) pv[r] = (wv + 8 * r < nj && lane < dr) ? bf2f(pr[r]) : 0.0f;
+  // this lane's slice of the group's qlat and q pe
+  float ql[HG][KPL], qp[HG];
+  bf16_t qr[HG];
+#pragma unroll
+  for (int h = 0; h < HG; h++) {
+    const float *src = a.qlat + ((uint64_t)b * H + h0 + h) * KV + lane * KPL;
+#pragma unroll
+    for (int i = 0; i < KPL; i++) ql[h][i] = src[i];
+    qr[h] = ((const bf16_t *)a.qpe)[((uint64_t)b * H + h0 + h) * dr + pl_lane];
+  }
+#pragma unroll
+  for (int h = 0; h < HG; h++) qp[h] = lane < dr ? bf2f(qr[h]) : 0.0f;
 #pragma unroll
   for (int r = 0; r < RPW; r++) {
     const uint32_t j = wv + 8 * r;
@@ -200,90 +215,160 @@ __global__ __launch_bounds__(MLA_THREADS) void k_mla_split(ThvmMlaArgs a) {
       for (int i = 0; i < KPL / 2; i++) dst[i] = cw[r][i];
     }
 #pragma unroll
-    for (int h = 0; h < HT; h++) {
+    for (int h = 0; h < HG; h++) {
       float s = qp[h] * pv[r];
 #pragma unroll
       for (int i = 0; i < KPL; i++) s += ql[h][i] * c[i];
       s = wave_sum(s);
-      if (lane == 0) sp[h * MLA_CHUNK + j] = s * a.scale;
+      if (lane == 0) sp[j * HG + h] = s * a.scale;
     }
   }
   __syncthreads();
-  // per-head softmax partial over this block's rows
-  float *part = a.part + ((uint64_t)b * a.n_split + split) * HT * (KV + 2);
-  for (uint32_t h = wv; h < HT; h += 8) {
-    const float s = lane < nj ? sp[h * MLA_CHUNK + lane] : -INFINITY;
+  // per-head softmax partial over this block's rows (wave h, lane = row)
+  float *part = a.part + ((uint64_t)b * a.n_split + split) * H * (KV + 4);
+  if (wv < HG) {
+    const uint32_t h = wv;
+    const float s = lane < nj ? sp[lane * HG + h] : -INFINITY;
     const float m = wave_max(s);
     const float e = lane < nj ? expf(s - m) : 0.0f;
     const float l = wave_sum(e);
-    sp[h * MLA_CHUNK + lane] = e;
+    sp[lane * HG + h] = e;
     if (lane == 0) {
-      part[h * (KV + 2) + KV] = m;
-      part[h * (KV + 2) + KV + 1] = l;
+      part[(h0 + h) * (KV + 4) + KV] = m;
+      part[(h0 + h) * (KV + 4) + KV + 1] = l;
     }
   }
   __syncthreads();
-  // olat partial: thread t owns latent column t for every head
+  // olat partial: thread t owns latent column t for the group's heads; lane j
+  // holds row j's HG softmax weights and v_readlane broadcasts them (a
+  // wave-wide LDS read of one address would serialise on its banks)
   const uint32_t t = threadIdx.x;
-  if (t < KV) {
-    float acc[HT];
+  if (t < KV) {                                        // whole waves: KV is a multiple of 64
+    float acc[HG];
 #pragma unroll
-    for (int h = 0; h < HT; h++) acc[h] = 0.0f;
-    for (uint32_t j = 0; j < nj; j++) {
-      const float c = bf2f(cs[j * KV + t]);
+    for (int h = 0; h < HG; h++) acc[h] = 0.0f;
+    const float4 pl = ((const float4 *)sp)[lane];      // HG == 4 weights of row `lane`
+    for (uint32_t j0r = 0; j0r < nj; j0r += 8) {     // eight rows of LDS reads in flight
+      float c[8];
 #pragma unroll
-      for (int h = 0; h < HT; h++) acc[h] += sp[h * MLA_CHUNK + j] * c;
+      for (int u = 0; u < 8; u++) {
+        const uint32_t j = j0r + u;
+        c[u] = j < nj ? bf2f(cs[j * KV + t]) : 0.0f;
+      }
+#pragma unroll
+      for (int u = 0; u < 8; u++) {
+        const int j = (int)(j0r + u);                  // rows past nj carry weight 0
+        acc[0] += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(pl.x), j)) * c[u];
+        acc[1] += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(pl.y), j)) * c[u];
+        acc[2] += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(pl.z), j)) * c[u];
+        acc[3] += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(pl.w), j)) * c[u];
+      }
     }
 #pragma unroll
-    for (int h = 0; h < HT; h++) part[h * (KV + 2) + t] = acc[h];
+    for (int h = 0; h < HG; h++) part[(h0 + h) * (KV + 4) + t] = acc[h];
   }
 }
 
 // ---- k_mla_out ----------------------------------------------------------
-// grid (B*H, ceil(dv/32)), 256 threads: merge the live splits of (b, h) into
-// olat (LDS), then o[b][h][m] = bf16(scale_m * sum_k olat[k] W_uv[h][m][k]).
+// grid (B*H, MLA_OUT_SPLIT), 512 threads: merge the live splits of (b, h)
+// into olat -- split weights computed once, threads split into (float4
+// column, split group) so each issues a few 16-byte loads, groups summed in
+// order in LDS -- then o[b][h][m] = bf16(scale_m * sum_k olat[k] W_uv[h][m][k])
+// for this block's share of the dv rows, whose weight loads are issued before
+// the merge (they do not depend on it).
+#define MLA_MAX_SPLITS 512
+#define MLA_OUT_THREADS 512
+#define MLA_OUT_SPLIT 2
+#define MLA_WPASS 8
 template <bool FP8>
-__global__ __launch_bounds__(256) void k_mla_out(ThvmMlaArgs a) {
-  extern __shared__ float ol[];
+__global__ __launch_bounds__(MLA_OUT_THREADS) void k_mla_out(ThvmMlaArgs a) {
+  extern __shared__ float ol[];                       // [kv] olat | [ns] weights | [nsg][kv]
+  constexpr uint32_t EPC = FP8 ? 16 : 8;
   const uint32_t bh = blockIdx.x, b = bh / a.H, h = bh % a.H, kv = a.kv, dv = a.dv;
+  const uint32_t tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  constexpr uint32_t nw = MLA_OUT_THREADS / 64;
+  const uint32_t rowb = kv * (FP8 ? 1 : 2), LPR = rowb / 16;     // kv <= 512: LPR <= 64
+  const uint32_t rpp = 64 / LPR, sub = lane / LPR, c = lane % LPR;
+  const uint32_t rows_pb = (dv + gridDim.y - 1) / gridDim.y;
+  const uint32_t m0 = blockIdx.y * rows_pb, m1 = min(m0 + rows_pb, dv);
+  uint4 wq[MLA_WPASS];
+#pragma unroll
+  for (int q = 0; q < MLA_WPASS; q++) {
+    const uint32_t mm = m0 + (wv + q * nw) * rpp + sub;
+    wq[q] = mm < m1 ? ld_stream16((const char *)a.wuv + ((uint64_t)h * dv + mm) * rowb + (uint64_t)c * 16)
+                    : make_uint4(0, 0, 0, 0);
+  }
   const int32_t L = min(a.len[0], (int32_t)a.max_seq);
   const uint32_t ns = L > 0 ? ((uint32_t)L + MLA_CHUNK - 1) / MLA_CHUNK : 0;
-  const uint64_t pst = (uint64_t)a.H * (kv + 2);
-  const float *p0 = a.part + (uint64_t)b * a.n_split * pst + (uint64_t)h * (kv + 2);
-  float M = -INFINITY;
-  for (uint32_t s = 0; s < ns; s++) M = fmaxf(M, p0[s * pst + kv]);
+  const uint64_t pst = (uint64_t)a.H * (kv + 4);
+  const float *p0 = a.part + (uint64_t)b * a.n_split * pst + (uint64_t)h * (kv + 4);
+  float *wsp = ol + kv, *grp = wsp + MLA_MAX_SPLITS;
+  __shared__ float red[16];
+  // split weights w_s = exp(m_s - M) / sum_s exp(m_s - M) l_s (one split per thread)
+  float ms = -INFINITY, ls = 0.0f;
+  if (tid < ns) { ms = p0[tid * pst + kv]; ls = p0[tid * pst + kv + 1]; }
+  float M = wave_max(ms);
+  if (lane == 0) red[wv] = M;
+  __syncthreads();
+  M = red[0];
+  for (uint32_t w = 1; w < MLA_OUT_THREADS / 64; w++) M = fmaxf(M, red[w]);
+  const float ws = tid < ns ? expf(ms - M) : 0.0f;
+  const float dsum = wave_sum(ws * ls);
+  if (lane == 0) red[8 + wv] = dsum;
+  __syncthreads();
   float den = 0.0f;
-  for (uint32_t s = 0; s < ns; s++) den += expf(p0[s * pst + kv] - M) * p0[s * pst + kv + 1];
-  const float rden = 1.0f / den;
-  for (uint32_t k = threadIdx.x; k < kv; k += blockDim.x) {
-    float acc = 0.0f;
-    for (uint32_t s = 0; s < ns; s++) acc += expf(p0[s * pst + kv] - M) * p0[s * pst + k];
-    ol[k] = acc * rden;
+  for (uint32_t w = 0; w < MLA_OUT_THREADS / 64; w++) den += red[8 + w];
+  if (tid < ns) wsp[tid] = ws / den;
+  __syncthreads();
+  // partial merge: thread -> (float4 column c4, split group g); groups stride the splits
+  const uint32_t nc4 = kv / 4, nsg = MLA_OUT_THREADS / nc4;
+  const uint32_t c4 = tid % nc4, g = tid / nc4;
+  float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+  for (uint32_t s0 = g; s0 < ns; s0 += 4 * nsg) {     // four 16-byte loads in flight
+    float4 v[4];
+#pragma unroll
+    for (int u = 0; u < 4; u++) {
+      const uint32_t s = s0 + u * nsg;
+      v[u] = s < ns ? *(const float4 *)(p0 + s * pst + 4 * c4) : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+#pragma unroll
+    for (int u = 0; u < 4; u++) {
+      const uint32_t s = s0 + u * nsg;
+      const float w = s < ns ? wsp[s] : 0.0f;
+      acc.x += w * v[u].x; acc.y += w * v[u].y; acc.z += w * v[u].z; acc.w += w * v[u].w;
+    }
+  }
+  ((float4 *)grp)[g * nc4 + c4] = acc;
+  __syncthreads();
+  const uint32_t nchk = kv / EPC;
+  if (tid < nc4) {
+    float4 s = ((const float4 *)grp)[tid];
+    for (uint32_t q = 1; q < nsg; q++) {
+      const float4 v = ((const float4 *)grp)[q * nc4 + tid];
+      s.x += v.x; s.y += v.y; s.z += v.z; s.w += v.w;
+    }
+    ((float4 *)ol)[chunk_swz<EPC>(4 * tid, nchk) / 4] = s;   // W_uv chunk order
   }
   __syncthreads();
-  const uint32_t rowb = kv * (FP8 ? 1 : 2), LPR = rowb / 16 < 64 ? rowb / 16 : 64;
-  const uint32_t CPL = rowb / 16 / LPR;                 // chunks per lane (kv > 1024 fp8)
-  const uint32_t lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
-  const uint32_t rpp = 64 / LPR, sub = lane / LPR, c = lane % LPR;
-  const uint32_t m0 = blockIdx.y * 32, m1 = min(m0 + 32, dv);
-  for (uint32_t r0 = m0 + wv * rpp; r0 < m1; r0 += 4 * rpp) {
+#pragma unroll
+  for (int q = 0; q < MLA_WPASS; q++) {
+    const uint32_t r0 = m0 + (wv + q * nw) * rpp;
+    if (r0 >= m1) break;                               // wave-uniform
     const uint32_t mm = r0 + sub;
-    const bool ok = mm < m1;
-    const uint64_t row = (uint64_t)h * dv + (ok ? mm : m0);
-    float acc = 0.0f;
-    for (uint32_t q = 0; q < CPL; q++) {
-      const uint32_t ch = c + q * LPR;
-      const char *wp = (const char *)a.wuv + row * rowb + (uint64_t)ch * 16;
-      uint4 q0 = ok ? ld_stream16(wp) : make_uint4(0, 0, 0, 0);
-      float w[16];
-      w16<FP8>(q0, make_uint4(0, 0, 0, 0), w);
-      const uint32_t e0 = ch * (FP8 ? 16 : 8), ne = FP8 ? 16 : 8;
-      for (uint32_t i = 0; i < ne; i++) acc += ol[e0 + i] * w[i];
+    float w[16];
+    w16<FP8>(wq[q], make_uint4(0, 0, 0, 0), w);
+    const float4 *o4 = (const float4 *)ol;
+    float accw = 0.0f;
+#pragma unroll
+    for (uint32_t qd = 0; qd < EPC / 4; qd++) {
+      const float4 x = o4[qd * nchk + c];
+      accw += x.x * w[4 * qd] + x.y * w[4 * qd + 1] + x.z * w[4 * qd + 2] + x.w * w[4 * qd + 3];
     }
-    acc = group_sum(acc, (int)LPR);
-    if (ok && c == 0) {
+    accw = group_sum(accw, (int)LPR);
+    if (mm < m1 && c == 0) {
+      const uint64_t row = (uint64_t)h * dv + mm;
       const float s = a.suv ? a.suv[row] : 1.0f;
-      ((bf16_t *)a.o)[(uint64_t)b * a.H * dv + (uint64_t)h * dv + mm] = f2bf(acc * s);
+      ((bf16_t *)a.o)[(uint64_t)b * a.H * dv + row] = f2bf(accw * s);
     }
   }
 }
@@ -327,19 +412,18 @@ extern "C" int thvm_k_mla_prep(const ThvmMlaArgs *a, hipStream_t s, char *err, i
 }
 
 typedef void (*mla_split_fn)(ThvmMlaArgs);
-template <int HT>
 static mla_split_fn pick_kpl(uint32_t kv) {
   switch (kv / 64) {
-    case 1: return k_mla_split<HT, 1>;
-    case 2: return k_mla_split<HT, 2>;
-    case 4: return k_mla_split<HT, 4>;
-    case 8: return k_mla_split<HT, 8>;
+    case 1: return k_mla_split<1>;
+    case 2: return k_mla_split<2>;
+    case 4: return k_mla_split<4>;
+    case 8: return k_mla_split<8>;
     default: return nullptr;
   }
 }
 
 extern "C" uint64_t thvm_k_mla_part_bytes(uint32_t B, uint32_t H, uint32_t kv, uint32_t n_split) {
-  return (uint64_t)B * n_split * H * (kv + 2) * 4;
+  return (uint64_t)B * n_split * H * (kv + 4) * 4;
 }
 
 extern "C" int thvm_k_mla_attn(const ThvmMlaArgs *a, hipStream_t s, char *err, int errlen) {
@@ -353,18 +437,27 @@ extern "C" int thvm_k_mla_attn(const ThvmMlaArgs *a, hipStream_t s, char *err, i
     snprintf(err, errlen, "mla_attn: W_uv rows must be 16-byte multiples");
     return -1;
   }
-  mla_split_fn f = a->H == 16 ? pick_kpl<16>(a->kv) : a->H == 8 ? pick_kpl<8>(a->kv) : nullptr;
-  if (!f) { snprintf(err, errlen, "mla_attn: no kernel for H=%u kv=%u (H in {8,16})", a->H, a->kv); return -1; }
-  const uint32_t lds = (uint32_t)(MLA_CHUNK * a->kv * 2 + a->H * MLA_CHUNK * 4);
+  mla_split_fn f = a->H % MLA_HG == 0 ? pick_kpl(a->kv) : nullptr;
+  if (!f) { snprintf(err, errlen, "mla_attn: no kernel for H=%u kv=%u (H a multiple of %d)", a->H, a->kv, MLA_HG); return -1; }
+  if (a->n_split > MLA_MAX_SPLITS) { snprintf(err, errlen, "mla_attn: more than %d splits", MLA_MAX_SPLITS); return -1; }
+  const uint32_t lds = (uint32_t)(MLA_CHUNK * a->kv * 2 + MLA_HG * MLA_CHUNK * 4);
   if (lds > 64 * 1024) {
     hipError_t e = hipFuncSetAttribute((const void *)f, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     if (e != hipSuccess) { snprintf(err, errlen, "mla_attn: hipFuncSetAttribute: %s", hipGetErrorString(e)); return -1; }
   }
-  thvm_launch(true, false, f, dim3(a->n_split, a->B), dim3(MLA_THREADS), lds, s, *a);
-  const dim3 g2(a->B * a->H, (a->dv + 31) / 32);
-  const uint32_t lds2 = a->kv * 4;
-  if (a->wdt == THVM_DT_FP8E4M3) thvm_launch(false, true, k_mla_out<true>, g2, dim3(256), lds2, s, *a);
-  else thvm_launch(false, true, k_mla_out<false>, g2, dim3(256), lds2, s, *a);
+  thvm_launch(true, false, f, dim3(a->n_split, a->H / MLA_HG, a->B), dim3(MLA_THREADS), lds, s, *a);
+  {
+    const uint32_t lpr = a->kv * wsz / 16, rpp = 64 / lpr;
+    const uint32_t rows_pb = (a->dv + MLA_OUT_SPLIT - 1) / MLA_OUT_SPLIT;
+    if ((rows_pb + 8 * rpp - 1) / (8 * rpp) > MLA_WPASS) {
+      snprintf(err, errlen, "mla_attn: d_v %u too large for the V projection tiling", a->dv);
+      return -1;
+    }
+  }
+  const dim3 g2(a->B * a->H, MLA_OUT_SPLIT);
+  const uint32_t lds2 = (a->kv + MLA_MAX_SPLITS + MLA_OUT_THREADS * 4) * 4;
+  if (a->wdt == THVM_DT_FP8E4M3) thvm_launch(false, true, k_mla_out<true>, g2, dim3(MLA_OUT_THREADS), lds2, s, *a);
+  else thvm_launch(false, true, k_mla_out<false>, g2, dim3(MLA_OUT_THREADS), lds2, s, *a);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) { snprintf(err, errlen, "mla_attn launch: %s", hipGetErrorString(e)); return -1; }
   return 0;

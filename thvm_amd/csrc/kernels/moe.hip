@@ -70,12 +70,13 @@ __device__ __forceinline__ void chunk_f32(const uint4 &q, float o[16]) {
   }
 }
 
-// dot of one row's chunks held by this lane with LDS vector v (elements of
-// chunk ch start at ch*EPC)
+// dot of one row's chunks held by this lane with the chunk-swizzled LDS
+// vector v of nch chunks (chunk_swz layout)
 template <bool FP8, int NC>
 __device__ __forceinline__ float chunk_dot(const uint4 (&q)[NC], const float *v,
                                            uint32_t lane, uint32_t nch) {
   constexpr uint32_t EPC = FP8 ? 16 : 8;
+  const float4 *v4 = (const float4 *)v;
   float acc = 0.0f;
 #pragma unroll
   for (int c = 0; c < NC; c++) {
@@ -84,7 +85,10 @@ __device__ __forceinline__ float chunk_dot(const uint4 (&q)[NC], const float *v,
       float w[16];
       chunk_f32<FP8>(q[c], w);
 #pragma unroll
-      for (uint32_t i = 0; i < EPC; i++) acc += v[ch * EPC + i] * w[i];
+      for (uint32_t qd = 0; qd < EPC / 4; qd++) {
+        const float4 x = v4[qd * nch + ch];
+        acc += x.x * w[4 * qd] + x.y * w[4 * qd + 1] + x.z * w[4 * qd + 2] + x.w * w[4 * qd + 3];
+      }
     }
   }
   return acc;
@@ -100,44 +104,86 @@ __device__ __forceinline__ void load_row(uint4 (&q)[NC], const char *row, uint32
   }
 }
 
+// LDS <- f32 vector of n elements (optionally rounded through bf16), laid
+// out in chunk_swz order per segment: elements [0, nseg*seg) form nseg
+// segments of seg elements (chunk count seg/EPC each), the rest one tail
+// segment.  Four 16-byte loads are in flight per thread before any store.
+template <bool RBF, int EPC>
+__device__ __forceinline__ void stage_swz(float *dst, const float *src, uint32_t n, uint32_t nseg,
+                                          uint32_t seg) {
+  const uint32_t tid = threadIdx.x, nt = blockDim.x, n4 = n / 4, head = nseg * seg;
+  const float4 *s4 = (const float4 *)src;
+  float4 *d4 = (float4 *)dst;
+  for (uint32_t i = tid; i < n4; i += 4 * nt) {
+    float4 v[4];
+#pragma unroll
+    for (int u = 0; u < 4; u++) {
+      const uint32_t j = i + u * nt;
+      v[u] = j < n4 ? s4[j] : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+#pragma unroll
+    for (int u = 0; u < 4; u++) {
+      const uint32_t j = i + u * nt;
+      if (j >= n4) continue;
+      float4 w = v[u];
+      if (RBF) { w.x = rbf(w.x); w.y = rbf(w.y); w.z = rbf(w.z); w.w = rbf(w.w); }
+      const uint32_t k = 4 * j;
+      uint32_t base, kk, nch;
+      if (k < head) { base = (k / seg) * seg; kk = k - base; nch = seg / EPC; }
+      else { base = head; kk = k - head; nch = (n - head) / EPC; }
+      d4[(base + chunk_swz<EPC>(kk, nch)) / 4] = w;
+    }
+  }
+}
+
 // ---- gate/up --------------------------------------------------------------
-// grid (ceil(P / 8), B) with P = K*I + S row pairs per batch row
-template <bool FP8>
+// grid (ceil(P / (8 * PPW)), B) with P = K*I + S row pairs per batch row;
+// each wave owns PPW consecutive pairs, NC 16-byte chunks per lane per row,
+// all its rows in flight before x is staged
+template <bool FP8, int NC, int PPW>
 __global__ __launch_bounds__(MOE_THREADS) void k_moe_gateup(ThvmMoeArgs a) {
   extern __shared__ float xs[];
   const uint32_t b = blockIdx.y, D = a.D, I = a.I, K = a.K;
   const uint32_t P = K * I + a.S;
   const uint32_t lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
-  const uint32_t p = blockIdx.x * MOE_WAVES + wv;
+  const uint32_t p0 = (blockIdx.x * MOE_WAVES + wv) * PPW;
   const uint64_t rowb = (uint64_t)D * (FP8 ? 1 : 2);
   const uint32_t nch = (uint32_t)(rowb / 16);
-  const bool live = p < P;
-  const char *base;
-  const float *sc;
-  uint64_t row0;
-  if (live && p < K * I) {
-    const uint32_t e = p / I, i = p % I;
-    int32_t id = a.sel[(uint64_t)b * K + e];
-    id = id < 0 ? 0 : id >= (int32_t)a.E ? (int32_t)a.E - 1 : id;   // a valid expert row
-    row0 = (uint64_t)id * 2 * I + 2 * i;
-    base = (const char *)a.wgu_e;
-    sc = a.sgu_e;
-  } else {
-    row0 = live ? 2ull * (p - K * I) : 0;
-    base = (const char *)a.wgu_s;
-    sc = a.sgu_s;
+  uint4 gq[PPW][NC], uq[PPW][NC];
+  uint64_t row0[PPW];
+  const float *scp[PPW];
+#pragma unroll
+  for (int i = 0; i < PPW; i++) {
+    const uint32_t p = p0 + i;
+    const bool live = p < P;
+    const char *base;
+    if (live && p < K * I) {
+      const uint32_t e = p / I, r = p % I;
+      int32_t id = a.sel[(uint64_t)b * K + e];
+      id = id < 0 ? 0 : id >= (int32_t)a.E ? (int32_t)a.E - 1 : id;   // a valid expert row
+      row0[i] = (uint64_t)id * 2 * I + 2 * r;
+      base = (const char *)a.wgu_e;
+      scp[i] = a.sgu_e;
+    } else {
+      row0[i] = live ? 2ull * (p - K * I) : 0;
+      base = (const char *)a.wgu_s;
+      scp[i] = a.sgu_s;
+    }
+    load_row(gq[i], base + row0[i] * rowb, lane, nch, live);
+    load_row(uq[i], base + (row0[i] + 1) * rowb, lane, nch, live);
   }
-  uint4 gq[MOE_MAXC], uq[MOE_MAXC];
-  load_row(gq, base + row0 * rowb, lane, nch, live);
-  load_row(uq, base + (row0 + 1) * rowb, lane, nch, live);
-  for (uint32_t i = threadIdx.x; i < D; i += MOE_THREADS) xs[i] = rbf(a.x[(uint64_t)b * D + i]);
+  stage_swz<true, FP8 ? 16 : 8>(xs, a.x + (uint64_t)b * D, D, 0, 1);
   __syncthreads();
-  if (!live) return;
-  float G = wave_sum(chunk_dot<FP8>(gq, xs, lane, nch));
-  float U = wave_sum(chunk_dot<FP8>(uq, xs, lane, nch));
-  if (lane == 0) {
-    if (sc) { G *= sc[row0]; U *= sc[row0 + 1]; }
-    a.h[(uint64_t)b * P + p] = silu_f(G) * U;
+#pragma unroll
+  for (int i = 0; i < PPW; i++) {
+    const uint32_t p = p0 + i;
+    if (p >= P) break;                                   // wave-uniform
+    float G = wave_sum(chunk_dot<FP8>(gq[i], xs, lane, nch));
+    float U = wave_sum(chunk_dot<FP8>(uq[i], xs, lane, nch));
+    if (lane == 0) {
+      if (scp[i]) { G *= scp[i][row0[i]]; U *= scp[i][row0[i] + 1]; }
+      a.h[(uint64_t)b * P + p] = silu_f(G) * U;
+    }
   }
 }
 
@@ -164,7 +210,7 @@ __global__ __launch_bounds__(MOE_THREADS) void k_moe_down(ThvmMoeArgs a) {
     load_row(q[e], (const char *)a.wd_e + row * rI, lane, nI, ok);
   }
   load_row(qs, (const char *)a.wd_s + (uint64_t)(live ? d : 0) * rS, lane, nS, live && S > 0);
-  for (uint32_t i = threadIdx.x; i < P; i += MOE_THREADS) hs[i] = a.h[(uint64_t)b * P + i];
+  stage_swz<false, FP8 ? 16 : 8>(hs, a.h + (uint64_t)b * P, P, K, I);
   __syncthreads();
   if (!live) return;
   float acc = 0.0f;
@@ -225,6 +271,14 @@ static int moe_check(const ThvmMoeArgs *a, int gateup, char *err, int errlen) {
     snprintf(err, errlen, "moe: fp8 weights need their row scales");
     return -1;
   }
+  if (a->D % 16 || a->I % 16 || a->S % 16) {
+    snprintf(err, errlen, "moe: D, I and S must be multiples of 16");
+    return -1;
+  }
+  if (((uintptr_t)a->x | (uintptr_t)a->h) & 15) {
+    snprintf(err, errlen, "moe: x and h must be 16-byte aligned");
+    return -1;
+  }
   if (gateup ? (!a->h || !a->x || !a->sel) : (!a->h || !a->res || !a->sel || !a->probs)) {
     snprintf(err, errlen, "moe: missing operand");
     return -1;
@@ -232,14 +286,25 @@ static int moe_check(const ThvmMoeArgs *a, int gateup, char *err, int errlen) {
   return 0;
 }
 
+typedef void (*moe_fn)(ThvmMoeArgs);
+template <bool FP8>
+static moe_fn pick_gateup(uint32_t nch, uint32_t *ppw) {
+  if (nch <= 64) { *ppw = 8; return k_moe_gateup<FP8, 1, 8>; }
+  if (nch <= 128) { *ppw = 4; return k_moe_gateup<FP8, 2, 4>; }
+  *ppw = 2;
+  return k_moe_gateup<FP8, 4, 2>;
+}
+
 extern "C" int thvm_k_moe_gateup(const ThvmMoeArgs *a, hipStream_t s, char *err, int errlen) {
   if (moe_check(a, 1, err, errlen)) return -1;
   const uint32_t P = a->K * a->I + a->S;
-  const dim3 grid((P + MOE_WAVES - 1) / MOE_WAVES, a->B);
+  const uint32_t nch = a->D * (a->wdt == THVM_DT_FP8E4M3 ? 1 : 2) / 16;
+  uint32_t ppw = 1;
+  const moe_fn f = a->wdt == THVM_DT_FP8E4M3 ? pick_gateup<true>(nch, &ppw) : pick_gateup<false>(nch, &ppw);
+  const dim3 grid((P + MOE_WAVES * ppw - 1) / (MOE_WAVES * ppw), a->B);
   const uint32_t lds = a->D * 4;
   if (lds > 64 * 1024) { snprintf(err, errlen, "moe: D too large"); return -1; }
-  if (a->wdt == THVM_DT_FP8E4M3) thvm_launch(true, true, k_moe_gateup<true>, grid, dim3(MOE_THREADS), lds, s, *a);
-  else thvm_launch(true, true, k_moe_gateup<false>, grid, dim3(MOE_THREADS), lds, s, *a);
+  thvm_launch(true, true, f, grid, dim3(MOE_THREADS), lds, s, *a);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) { snprintf(err, errlen, "moe_gateup launch: %s", hipGetErrorString(e)); return -1; }
   return 0;
@@ -251,8 +316,7 @@ extern "C" int thvm_k_moe_down(const ThvmMoeArgs *a, hipStream_t s, char *err, i
   const uint32_t lds = P * 4;
   if (lds > 160 * 1024) { snprintf(err, errlen, "moe: K*I+S too large for LDS"); return -1; }
   const dim3 grid((a->D + MOE_WAVES - 1) / MOE_WAVES, a->B);
-  typedef void (*down_fn)(ThvmMoeArgs);
-  const down_fn f = a->wdt == THVM_DT_FP8E4M3 ? k_moe_down<true> : k_moe_down<false>;
+  const moe_fn f = a->wdt == THVM_DT_FP8E4M3 ? k_moe_down<true> : k_moe_down<false>;
   if (lds > 64 * 1024) {
     hipError_t e = hipFuncSetAttribute((const void *)f, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     if (e != hipSuccess) { snprintf(err, errlen, "moe_down: hipFuncSetAttribute: %s", hipGetErrorString(e)); return -1; }
