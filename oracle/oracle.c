@@ -556,6 +556,36 @@ void or_moe(float *out, const uint16_t *xb, const int32_t *sel, const float *pro
   free(h);
 }
 
+/* The reference's M=1 projection is a two-phase split-K GEMV: phase 1 sums
+ * each of sk contiguous K-chunks into a partial, phase 2 folds the partials in
+ * chunk order (gemv_pick_sk :1043-1048, src_gemv C twin :1073-1084, the folds
+ * of src_gred :1100-1107 / gred_q / kv_prep / gred_o_rms / route).  sk
+ * doubles while ceil(N/256)*sk < 232 and sk*64 < K. */
+static uint32_t gemv_pick_sk(uint32_t K, uint32_t N) {
+  const uint32_t gx = (N + 255) / 256;
+  uint32_t sk = 1;
+  while (gx * sk < 232u && sk * 64u < K) sk *= 2;
+  return sk;
+}
+static void gemv_sk(float *y, const float *x, const void *w, uint32_t wdt, const float *scale,
+                    uint32_t N, uint32_t K, uint32_t sk) {
+  const uint32_t chunk = (K + sk - 1) / sk;
+  for (uint32_t n = 0; n < N; n++) {
+    float s = 0.0f;
+    for (uint32_t i = 0; i < sk; i++) {
+      const uint32_t k0 = i * chunk, k1 = k0 + chunk > K ? K : k0 + chunk;
+      float acc = 0.0f;
+      for (uint32_t k = k0; k < k1; k++) {
+        float wv = ld(w, (uint64_t)n * K + k, wdt);
+        if (scale) wv = wv * scale[n];
+        acc += x[k] * wv;
+      }
+      s += acc;
+    }
+    y[n] = s;
+  }
+}
+
 int or_dsv2_step(const OrDsv2 *m, const int32_t *tok, uint32_t pos, float *logits, int32_t *next) {
   if (!m || pos >= m->max_seq || m->top_k > m->n_experts || m->top_k > 64 || m->d_rope % 2)
     return -1;
@@ -582,27 +612,27 @@ int or_dsv2_step(const OrDsv2 *m, const int32_t *tok, uint32_t pos, float *logit
       uint16_t *kpe = Ly->kpe + (uint64_t)b * m->max_seq * dr;
       or_rmsnorm(xn, DT_FP32, x, DT_FP32, Ly->win, 1, D, m->eps);
       for (uint32_t i = 0; i < D; i++) xn[i] = rnd(xn[i], DT_BF16);   /* rms1 out bf16 */
-      or_gemv(qkv, xn, DT_FP32, D, Ly->wqkv, wdt, Ly->sqkv, 1, nqkv, D);
+      gemv_sk(qkv, xn, Ly->wqkv, wdt, Ly->sqkv, nqkv, D, gemv_pick_sk(D, H * (dn + dr)));
       for (uint32_t n = 0; n < nqkv; n++) qraw[n] = or_f32_to_bf16(qkv[n]);
       or_mla_prep(qpe, qlat, ckv + (uint64_t)pos * kv, kpe + (uint64_t)pos * dr, qraw, Ly->wuk, wdt,
                   Ly->suk, Ly->wkvn, m->rope_cos + (uint64_t)pos * (dr / 2),
                   m->rope_sin + (uint64_t)pos * (dr / 2), H, dn, dr, kv, m->eps);
       or_mla_attn(o, qlat, qpe, ckv, kpe, pos + 1, Ly->wuv, wdt, Ly->suv, H, kv, dr, dv, m->scale);
       for (uint32_t i = 0; i < H * dv; i++) of[i] = or_bf16_to_f32(o[i]);
-      or_gemv(tmp, of, DT_FP32, H * dv, Ly->wo, wdt, Ly->so, 1, D, H * dv);
+      gemv_sk(tmp, of, Ly->wo, wdt, Ly->so, D, H * dv, gemv_pick_sk(H * dv, D));
       for (uint32_t i = 0; i < D; i++) x[i] = rnd(x[i] + rnd(tmp[i], DT_BF16), DT_BF16);  /* x1 */
       or_rmsnorm(xn, DT_FP32, x, DT_FP32, Ly->wpost, 1, D, m->eps);                       /* xn2f */
       for (uint32_t i = 0; i < D; i++) xb[i] = or_f32_to_bf16(xn[i]);                     /* xn2b */
       if (l < m->first_dense) {
         for (uint32_t i = 0; i < D; i++) tmp[i] = or_bf16_to_f32(xb[i]);
-        or_gemv(gu, tmp, DT_FP32, D, Ly->wgu, wdt, Ly->sgu, 1, 2 * F, D);
+        gemv_sk(gu, tmp, Ly->wgu, wdt, Ly->sgu, 2 * F, D, gemv_pick_sk(D, F));
         for (uint32_t i = 0; i < F; i++) {
           float g = rnd(gu[2 * i], DT_BF16), u = rnd(gu[2 * i + 1], DT_BF16);
           hh[i] = rnd(silu(g) * u, DT_BF16);
         }
-        or_gemv(tmp, hh, DT_FP32, F, Ly->wd, wdt, Ly->sd, 1, D, F);
+        gemv_sk(tmp, hh, Ly->wd, wdt, Ly->sd, D, F, gemv_pick_sk(F, D));
       } else {
-        for (uint32_t e = 0; e < E; e++) lg[e] = wdot(xn, Ly->gate, DT_FP32, NULL, e, D);
+        gemv_sk(lg, xn, Ly->gate, DT_FP32, NULL, E, D, gemv_pick_sk(D, E));
         or_route(sel, probs, lg, E, K);
         if (m->gate_out) memcpy(m->gate_out + (uint64_t)b * E, lg, E * sizeof(float));
         if (m->sel_out) {
@@ -616,7 +646,7 @@ int or_dsv2_step(const OrDsv2 *m, const int32_t *tok, uint32_t pos, float *logit
     }
     or_rmsnorm(xn, DT_FP32, x, DT_FP32, m->gf, 1, D, m->eps);                             /* rms_f f32 */
     float *lgb = logits + (uint64_t)b * V;
-    or_gemv(lgb, xn, DT_FP32, D, m->lm, wdt, m->lm_s, 1, V, D);
+    gemv_sk(lgb, xn, m->lm, wdt, m->lm_s, V, D, gemv_pick_sk(D, V));
     or_argmax(&next[b], lgb, 1, V);
   }
   free(x); free(xn); free(qkv); free(qlat); free(qraw); free(qpe); free(o); free(xb);

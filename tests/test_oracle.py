@@ -9,6 +9,8 @@ Checks, per oracle function:
   * what the mathematics fixes: IEEE binary16 decode (numpy float16),
     encode(decode(b)) == b on every finite pattern, float64 brute force;
   * the live reference harness, when it was built in this container."""
+import sys
+
 import numpy as np
 import pytest
 
@@ -244,3 +246,108 @@ def test_live_reference_codecs_random():
         assert Or.or_f32_to_fp8e4m3_sat(v) == R.ref_f32_to_fp8e4m3_sat(v)
         assert Or.or_f32_to_bf16(v) == R.ref_f32_to_bf16(v)
         assert Or.or_f32_to_fp16(v) == R.ref_f32_to_fp16_manual(v)
+
+
+# ------------------------------------------------------------ DeepSeek-V2 ----
+class _Tensors:
+    """A decoder-like view of numpy tensors for the oracle models."""
+
+    def __init__(self, t):
+        self.t = t
+
+    def read_tensor(self, name):
+        return self.t[name]
+
+
+def _dsv2_run(t, cfg, prompt, count):
+    om = O.OracleDsv2(_Tensors(t), dict(cfg, wdtype=12))
+    ids, top = [], []
+    tok = np.array([prompt[0]], np.int32)
+    for pos in range(len(prompt) + count - 1):
+        lg, nx = om.step(tok, pos)
+        if pos >= len(prompt) - 1:
+            ids.append(int(nx[0]))
+            o = np.argsort(-lg[0], kind="stable")[:2]
+            top.append((o[0], lg[0, o[0]], o[1], lg[0, o[1]]))
+        tok = np.array([prompt[pos + 1] if pos + 1 < len(prompt) else nx[0]], np.int32)
+    return ids, top
+
+
+def test_dsv2_oracle_reproduces_reference_trajectory():
+    """The oracle's DeepSeek-V2 step (or_dsv2_step: MLA prep/attention, router,
+    routed + shared experts, split-K projections) against the compiled
+    reference DSV2 decode bench on the same seeded model (fixture written by
+    tests/golden/make_dsv2_golden.py through a DSV2PK01 weight pack): the
+    greedy ids are identical and the top-2 logits agree to 1e-5."""
+    import _dsv2_weights as W
+    sys.path.insert(0, str(O.ROOT / "tests" / "golden"))
+    import make_dsv2_golden as G
+    g = np.load(O.ROOT / "tests" / "golden" / "dsv2_ref.npz")
+    t = W.make_dsv2(G.CFG, int(g["seed"]))
+    assert G.weight_digest(t) == str(g["digest"]), "weight generator drifted from the fixture"
+    ids, top = _dsv2_run(t, G.CFG, list(g["prompt"]), len(g["gen_ids"]))
+    assert ids == list(g["gen_ids"])
+    for (i1, v1, i2, v2), ref in zip(top[1:], g["top2"]):
+        assert (i1, i2) == (int(ref[1]), int(ref[3]))
+        assert abs(v1 - ref[2]) <= 1e-5 and abs(v2 - ref[4]) <= 1e-5
+
+
+def test_route_brute_force_and_ties():
+    rng = np.random.default_rng(3)
+    for E, K in ((64, 6), (8, 3), (5, 5)):
+        g = rng.standard_normal(E).astype(np.float32)
+        g[[1, E - 1]] = g.max() + 1.0                    # a tie at the top -> lower id first
+        sel, pr = np.empty(K, np.int32), np.empty(K, np.float32)
+        O.oracle().or_route(sel.ctypes.data, pr.ctypes.data, g.ctypes.data, E, K)
+        assert list(sel) == list(np.lexsort((np.arange(E), -g))[:K])
+        p = np.exp(g.astype(np.float64) - g.max())
+        p /= p.sum()
+        assert np.allclose(pr, p[sel], rtol=1e-6)
+
+
+def test_mla_attn_closed_forms():
+    """One live row: softmax weight 1, olat = that latent row, o = W_uv . row;
+    equal rows: the same for any scores."""
+    rng = np.random.default_rng(4)
+    H, kv, dr, dv = 4, 64, 16, 32
+    bf = lambda a: O.encode(np.asarray(a, np.float32), 12)
+    wuv = bf(rng.standard_normal((H * dv, kv)) * 0.1)
+    qlat = rng.standard_normal((H, kv)).astype(np.float32)
+    qpe = bf(rng.standard_normal((H, dr)))
+    for L, same in ((1, False), (9, True)):
+        row = bf(rng.standard_normal(kv))
+        ckv = np.tile(row, (L, 1)) if same else row[None, :].copy()
+        kpe = bf(rng.standard_normal((L, dr)))
+        o = np.empty((H, dv), np.uint16)
+        O.oracle().or_mla_attn(o.ctypes.data, qlat.ctypes.data, qpe.ctypes.data, ckv.ctypes.data,
+                               kpe.ctypes.data, L, wuv.ctypes.data, 12, None, H, kv, dr, dv, 0.3)
+        want = O.decode(wuv, 12).astype(np.float64) @ O.decode(row, 12).astype(np.float64)
+        got = O.decode(o, 12).ravel()
+        assert np.all(np.abs(got - want) <= 2.0 ** -8 * np.abs(want) + 1e-6)
+
+
+def test_moe_brute_force():
+    """or_moe against a float64 restatement written from the expert-FFN
+    definition (gate/up interleaved per expert, probs-weighted routed sum plus
+    the shared expert)."""
+    rng = np.random.default_rng(5)
+    D, E, K, I, S = 64, 6, 2, 32, 64
+    bf = lambda a: O.encode(np.asarray(a, np.float32), 12)
+    wgu, wd = bf(rng.standard_normal((E, 2 * I, D)) * 0.1), bf(rng.standard_normal((E, D, I)) * 0.1)
+    wgs, wds = bf(rng.standard_normal((2 * S, D)) * 0.1), bf(rng.standard_normal((D, S)) * 0.1)
+    xb = bf(rng.standard_normal(D))
+    sel, probs = np.array([4, 1], np.int32), np.array([0.6, 0.3], np.float32)
+    out = np.empty(D, np.float32)
+    O.oracle().or_moe(out.ctypes.data, xb.ctypes.data, sel.ctypes.data, probs.ctypes.data,
+                      wgu.ctypes.data, None, wd.ctypes.data, None, wgs.ctypes.data, None,
+                      wds.ctypes.data, None, 12, D, I, S, K)
+    f = lambda a: O.decode(a, 12).astype(np.float64)
+    x = f(xb)
+    silu = lambda v: v / (1 + np.exp(-v))
+    want = np.zeros(D)
+    for e, p in zip(sel, probs):
+        g, u = f(wgu[e, 0::2]) @ x, f(wgu[e, 1::2]) @ x
+        want += p * (f(wd[e]) @ (silu(g) * u))
+    g, u = f(wgs[0::2]) @ x, f(wgs[1::2]) @ x
+    want += f(wds) @ (silu(g) * u)
+    assert np.allclose(out, want, rtol=1e-4, atol=1e-6)
