@@ -159,6 +159,25 @@ __device__ __forceinline__ uint4 ld16(const void *p) {
   return *(const uint4 *)p;
 }
 
+// Raw buffer loads through a buffer resource over [p, p + bytes) (stride 0,
+// the gfx9 untyped-access word): an offset at or beyond `bytes` reads zero by
+// the hardware range check, so masked loads need neither branches nor selects
+// (a guarded load lets the compiler sink it into a branch and wait for it
+// there).  BUF_OOB is an offset that is always out of range.
+#define BUF_OOB 0x80000000u
+typedef __amdgpu_buffer_rsrc_t buf_t;
+__device__ __forceinline__ buf_t buf_rsrc(const void *p, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc((void *)p, 0, (int)bytes, 0x00020000);
+}
+__device__ __forceinline__ uint4 buf_ld16(buf_t r, uint32_t off) {
+  u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
+  return make_uint4(v[0], v[1], v[2], v[3]);
+}
+__device__ __forceinline__ uint4 buf_ld_stream16(buf_t r, uint32_t off) {   // nontemporal
+  u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 2);
+  return make_uint4(v[0], v[1], v[2], v[3]);
+}
+
 // LDS slot of element k of a vector that lanes read in 16-byte weight chunks
 // of EPC elements (chunk ch = k / EPC belongs to one lane, consecutive chunks
 // to consecutive lanes): quad q of every chunk is stored contiguously across

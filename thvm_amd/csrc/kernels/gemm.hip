@@ -66,11 +66,22 @@ __device__ __forceinline__ f32x4_t mfma16(const uint4 &A, const uint4 &B, f32x4_
                                                 __builtin_bit_cast(f16x8_t, B), c, 0, 0, 0);
 }
 
-// MT 16-row tiles of x, NT 16-row tiles of W per block, U 64-k steps in flight
+// MT 16-row tiles of x, NT 16-row tiles of W per block, U 64-k steps in flight.
+// Each wave stages its own slice of x into a private LDS region, GEMM_SC(MT)
+// 64-k steps of its 16*MT rows at a time, with row-contiguous 16-byte loads
+// (8*SC lanes per row); the MFMA B operand is then read from LDS, rows padded
+// by 16 bytes so the 16 rows of one read fall in different banks.
+#ifndef GEMM_XSTAGE
+#define GEMM_XSTAGE 8                              // 64-k steps x 16-row tiles staged
+#endif
+#define GEMM_SC(MT) (GEMM_XSTAGE / (MT))
+#define GEMM_XROW(MT) (GEMM_SC(MT) * 128 + 16)
 template <int WT, int XT, int MT, int NT, int U>
 __global__ __launch_bounds__(GEMM_THREADS) void k_gemm(ThvmGemvArgs a) {
-  extern __shared__ float4 red[];                 // [GEMM_WAVES][NT*MT][64]
+  extern __shared__ float4 red[];                 // x staging, then [GEMM_WAVES][NT*MT][64]
   constexpr int WB = WT == GW_FP8 ? 1 : 2;        // uint4 per lane per step per W tile
+  constexpr int SC = GEMM_SC(MT), XROW = GEMM_XROW(MT);
+  static_assert(SC % U == 0, "sub-chunks hold whole prefetch rounds");
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
   const int li = lane & 15, lg = lane >> 4;
   const uint32_t N = a.N, K = a.K, M = a.M;
@@ -79,23 +90,15 @@ __global__ __launch_bounds__(GEMM_THREADS) void k_gemm(ThvmGemvArgs a) {
   const uint32_t s0 = (uint32_t)(((uint64_t)S * wv) / GEMM_WAVES);
   const uint32_t s1 = (uint32_t)(((uint64_t)S * (wv + 1)) / GEMM_WAVES);
   const uint64_t wrow_b = (uint64_t)K * (WT == GW_FP8 ? 1 : 2);
+  char *xs = (char *)red + (size_t)wv * (16 * MT * XROW);
 
-  const char *wp[NT];
-  bool wok[NT];
+  // this block's weight rows; rows past N read zero
+  const buf_t wrs = buf_rsrc((const char *)a.w + (uint64_t)n0 * wrow_b,
+                             (uint32_t)(min(N - n0, 16u * NT) * wrow_b));
+  const buf_t xrs = buf_rsrc(a.x, (uint32_t)(((uint64_t)(M - 1) * a.ldx + K) * 2));
+  uint32_t wo[NT];
 #pragma unroll
-  for (int t = 0; t < NT; t++) {
-    const uint32_t n = n0 + 16u * t + li;
-    wok[t] = n < N;
-    wp[t] = (const char *)a.w + (uint64_t)(wok[t] ? n : 0) * wrow_b + (uint64_t)lg * 16 * WB;
-  }
-  const char *xp[MT];
-  bool xok[MT];
-#pragma unroll
-  for (int mt = 0; mt < MT; mt++) {
-    const uint32_t m = 16u * mt + li;
-    xok[mt] = m < M;
-    xp[mt] = (const char *)a.x + (uint64_t)(xok[mt] ? m : 0) * a.ldx * 2 + (uint64_t)lg * 32;
-  }
+  for (int t = 0; t < NT; t++) wo[t] = (uint32_t)((16u * t + li) * wrow_b) + lg * 16 * WB;
 
   f32x4_t acc[NT][MT];
 #pragma unroll
@@ -104,22 +107,44 @@ __global__ __launch_bounds__(GEMM_THREADS) void k_gemm(ThvmGemvArgs a) {
     for (int mt = 0; mt < MT; mt++) acc[t][mt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
   uint4 wr[U][NT][WB];
-  uint4 xr[U][MT][2];
-  const uint4 z4 = make_uint4(0, 0, 0, 0);
   auto load = [&](int u, uint32_t s) {
-    const bool live = s < s1;
+    const uint32_t so = s < s1 ? s * 64 * WB : BUF_OOB;
 #pragma unroll
     for (int t = 0; t < NT; t++)
 #pragma unroll
-      for (int j = 0; j < WB; j++)
-        wr[u][t][j] = (live && wok[t]) ? ld_stream16(wp[t] + (uint64_t)s * 64 * WB + j * 16) : z4;
+      for (int j = 0; j < WB; j++) wr[u][t][j] = buf_ld_stream16(wrs, wo[t] + so + j * 16);
+  };
+  // x rows [0, 16*MT) x steps [sc0, sc0 + SC), RPI rows per load instruction,
+  // 8*SC lanes per row (16 bytes each), held in registers until stored to
+  // LDS: the next sub-chunk is loaded while this one is consumed, so waiting
+  // for it never waits for the weight loads issued after it.  Rows >= M and
+  // k >= K read zero (out of range); steps past the wave's slice are real x
+  // values that meet zero weights.
+  constexpr int RPI = 8 / SC, NI = 16 * MT / RPI;
+  static_assert(SC <= 8 && RPI * SC == 8 && NI * RPI == 16 * MT, "staging shape");
+  const uint32_t sr = lane / (8 * SC), sl = lane % (8 * SC);
+  uint4 xv[NI];
+  auto xload = [&](uint32_t sc0, bool live) {
+    const uint32_t k = sc0 * 64 + sl * 8;
+    const uint32_t base = live && k < K ? (sr * a.ldx + k) * 2 : BUF_OOB;
+#pragma unroll
+    for (int i = 0; i < NI; i++) xv[i] = buf_ld16(xrs, base + i * RPI * a.ldx * 2);
+  };
+  auto xstore = [&]() {
+#pragma unroll
+    for (int i = 0; i < NI; i++) *(uint4 *)(xs + (i * RPI + sr) * XROW + sl * 16) = xv[i];
+    // one wave writes and reads its region, and a wave's LDS operations
+    // complete in order: only the compiler must keep the order
+    __builtin_amdgcn_wave_barrier();
+    asm volatile("" ::: "memory");
+  };
+  auto compute = [&](int u, uint32_t so) {
+    uint4 B[MT][2];
 #pragma unroll
     for (int mt = 0; mt < MT; mt++)
 #pragma unroll
       for (int j = 0; j < 2; j++)
-        xr[u][mt][j] = (live && xok[mt]) ? ld16(xp[mt] + (uint64_t)s * 128 + j * 16) : z4;
-  };
-  auto compute = [&](int u) {
+        B[mt][j] = *(const uint4 *)(xs + (16 * mt + li) * XROW + so * 128 + lg * 32 + j * 16);
 #pragma unroll
     for (int t = 0; t < NT; t++) {
       uint4 A0, A1;
@@ -135,21 +160,32 @@ __global__ __launch_bounds__(GEMM_THREADS) void k_gemm(ThvmGemvArgs a) {
       }
 #pragma unroll
       for (int mt = 0; mt < MT; mt++) {
-        acc[t][mt] = mfma16<XT>(A0, xr[u][mt][0], acc[t][mt]);
-        acc[t][mt] = mfma16<XT>(A1, xr[u][mt][1], acc[t][mt]);
+        acc[t][mt] = mfma16<XT>(A0, B[mt][0], acc[t][mt]);
+        acc[t][mt] = mfma16<XT>(A1, B[mt][1], acc[t][mt]);
       }
     }
   };
 
+  // whole sub-chunks, also past s1 (zero weights), so the step loop is
+  // straight-line code and every wait counts only the loads it needs
+  const uint32_t nsub = (s1 - s0 + SC - 1) / SC;
+  xload(s0, true);
 #pragma unroll
   for (int u = 0; u < U; u++) load(u, s0 + u);
-  for (uint32_t s = s0; s < s1; s += U) {
+  for (uint32_t c = 0; c < nsub; c++) {
+    const uint32_t sb = s0 + c * SC;
+    xstore();
+    xload(sb + SC, c + 1 < nsub);
+    __builtin_amdgcn_sched_barrier(0);            // issue them before this sub-chunk's weight loads
 #pragma unroll
-    for (int u = 0; u < U; u++) {
-      if (s + u < s1) compute(u);
-      load(u, s + u + U);
-    }
+    for (int g = 0; g < SC / U; g++)
+#pragma unroll
+      for (int u = 0; u < U; u++) {
+        compute(u, g * U + u);
+        load(u, sb + g * U + u + U);
+      }
   }
+  __syncthreads();                                // the staging area becomes the reduction buffer
 
   // partial tiles -> LDS, summed in wave order
 #pragma unroll
@@ -183,11 +219,13 @@ typedef void (*gemm_fn)(ThvmGemvArgs);
 
 template <int WT, int XT, int MT>
 static gemm_fn pick_nt(int NT) {
-  constexpr int U = MT >= 4 ? 2 : 4;
+  constexpr int SC = GEMM_SC(MT);
+  constexpr int U = (MT >= 4 ? 2 : 4) < SC ? (MT >= 4 ? 2 : 4) : SC;
+  constexpr int U4 = MT >= 2 && U > 2 ? 2 : U;
   switch (NT) {
     case 1: return k_gemm<WT, XT, MT, 1, U>;
     case 2: return k_gemm<WT, XT, MT, 2, U>;
-    case 4: return k_gemm<WT, XT, MT, 4, (MT >= 2 ? 2 : U)>;
+    case 4: return k_gemm<WT, XT, MT, 4, U4>;
     default: return nullptr;
   }
 }
@@ -212,6 +250,12 @@ extern "C" int thvm_k_gemm_mfma(const ThvmGemvArgs *a, hipStream_t s, char *err,
     snprintf(err, errlen, "gemm: x rows and W must be 16-byte aligned");
     return -1;
   }
+  // buffer-resource ranges (x whole, W per block) and offsets are 31-bit
+  if (64ull * a->ldx * 2 >= (1ull << 31) ||
+      64ull * a->K * (a->wdt == THVM_DT_FP8E4M3 ? 1 : 2) >= (1ull << 30)) {
+    snprintf(err, errlen, "gemm: x or a 64-row weight panel exceeds 1 GiB");
+    return -1;
+  }
   const int MT = a->M <= 16 ? 1 : a->M <= 32 ? 2 : 4;
   // 16-row weight tiles per block, from the gfx950 sweep over the C4 shapes at
   // M=16: more tiles amortise the x tile reads over more weight rows (wide N),
@@ -231,7 +275,9 @@ extern "C" int thvm_k_gemm_mfma(const ThvmGemvArgs *a, hipStream_t s, char *err,
              "fp8 W bf16/fp16 x)", a->wdt, a->xdt);
     return -1;
   }
-  const uint32_t lds = (uint32_t)(GEMM_WAVES * NT * MT * 64 * sizeof(float4));
+  uint32_t lds = (uint32_t)(GEMM_WAVES * NT * MT * 64 * sizeof(float4));
+  const uint32_t xlds = (uint32_t)(GEMM_WAVES * 16 * MT * (GEMM_XSTAGE / MT * 128 + 16));
+  if (xlds > lds) lds = xlds;
   if (lds > 64 * 1024) {
     hipError_t e = hipFuncSetAttribute((const void *)f, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     if (e != hipSuccess) { snprintf(err, errlen, "gemm: hipFuncSetAttribute: %s", hipGetErrorString(e)); return -1; }
