@@ -126,6 +126,53 @@ int thvm_hip_dispatch_custom(const char *name, const char *program,
  * it would dispatch.  Used by hosts to fail early. */
 int thvm_hip_program_check(const char *name, const char *program);
 
+/* ===================== renderer target ================================= */
+/* One node of a kernel's lifted uop DAG, flattened for the C ABI, sources
+ * before users.  `op` is the reference's UOP_* number (src/thvm.h:302-512);
+ * a reference-side adapter walks its Term DAG (the root that
+ * cg_render_uop_kernel_cuda_root takes, src/codegen/render_uop.c:4964) once
+ * and fills this array.  Payloads:
+ *   CONST(2)        arg0 = bits (an f32 pattern for every float dtype, the
+ *                   integer value otherwise), as UOP_CONST holds them
+ *   RANGE(25)       arg0 = axis id, arg1 = KAX_* axis type, arg2 = extent,
+ *                   or src0 = an extent expression (symbolic)
+ *   REDUCE(17)      src0 = value, src1..3 = the RANGEs reduced,
+ *                   arg0 = REDUCE_SUM(0) / REDUCE_MAX(1)
+ *   DEFINE_VAR(18)  arg0 = index into the kernel's int32 variable buffer,
+ *                   arg1 / arg2 = min / max of the variable
+ *   BUFFER(36)      arg0 = argument slot (0 = the output), dtype = element,
+ *                   arg1 = capacity in elements (> 0: every load outside
+ *                   reads 0 and every store outside is dropped)
+ *   INDEX_E(26)     src0 = BUFFER, src1 = element index; LOAD(21) src0 = INDEX
+ *   STORE(37)       src0 = BUFFER slot 0, src1 = index, src2 = value (root,
+ *                   the last node)
+ *   CAST(23) / BITCAST(24): dtype = the target type
+ *   ALU: ADD MUL NEG RECIP EXP2 LOG2 SQRT SIN CMPLT CMPEQ, IADD ISUB IMUL
+ *   IDIV IMOD ILT IAND IOR IXOR ISHL ISHR IWHERE (src0 ? src1 : src2). */
+typedef struct ThvmUop {
+  uint32_t op;
+  uint32_t dtype;
+  int32_t  src[4];   /* earlier node indices, -1 = none */
+  int64_t  arg[4];
+} ThvmUop;
+
+typedef struct ThvmRenderInfo {
+  uint32_t n_slots;    /* argument slots: buffers 0..k-1, then the variable buffer */
+  uint32_t kvar_slot;  /* slot of the int32 variable buffer, 0 = no variables */
+  uint32_t group;      /* 1: one block per output element (group reduce) */
+  uint32_t block;      /* threads per block */
+  uint64_t grid_max;   /* blocks to launch (variables at their maxima) */
+} ThvmRenderInfo;
+
+/* cg_render_uop_kernel_cuda_root + the CUDA dispatch geometry (reference
+ * src/codegen/render_uop.c:4964-5113, src/backend/cuda/jit.c:634-787) for
+ * gfx950: writes `extern "C" __global__ void <name>(out, in1.., kv)` HIP
+ * source into `out` (NUL-terminated) for thvm_hip_dispatch_custom with
+ * grid = {grid_max,1,1}, block = {block,1,1}.  Pure host code (no device
+ * needed).  0 / -1. */
+int thvm_hip_render_kernel(const ThvmUop *nodes, uint32_t n, const char *name,
+                           char *out, uint64_t cap, ThvmRenderInfo *info);
+
 /* ===================== JIT capture / replay ============================ */
 /* The reference capture API (src/jit/capture.c:644-745, 2687-2884) restricted
  * to custom dispatches: ops fired between begin and end are recorded, every

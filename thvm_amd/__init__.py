@@ -47,6 +47,18 @@ class DecodeConfig(C.Structure):
         ("reserved", C.c_uint32 * 8)]
 
 
+class Uop(C.Structure):
+    """ThvmUop (include/thvm_hip.h): one node of a kernel's lifted DAG."""
+    _fields_ = [("op", C.c_uint32), ("dtype", C.c_uint32), ("src", C.c_int32 * 4),
+                ("arg", C.c_int64 * 4)]
+
+
+class RenderInfo(C.Structure):
+    """ThvmRenderInfo (include/thvm_hip.h)."""
+    _fields_ = [("n_slots", C.c_uint32), ("kvar_slot", C.c_uint32), ("group", C.c_uint32),
+                ("block", C.c_uint32), ("grid_max", C.c_uint64)]
+
+
 _u32, _u64, _i32, _vp, _cp, _d = C.c_uint32, C.c_uint64, C.c_int, C.c_void_p, C.c_char_p, C.c_double
 _SIGS = {
     "thvm_hip_init": (_i32, []), "thvm_hip_shutdown": (None, []),
@@ -68,6 +80,7 @@ _SIGS = {
     "thvm_hip_dispatch_end": (None, []),
     "thvm_hip_dispatch_custom": (_i32, [_cp, _cp, _vp, _vp, _u32, _vp, _u32, _u64]),
     "thvm_hip_program_check": (_i32, [_cp, _cp]),
+    "thvm_hip_render_kernel": (_i32, [C.POINTER(Uop), _u32, _cp, _vp, _u64, C.POINTER(RenderInfo)]),
     "thvm_hip_jit_capture_begin": (_u32, []), "thvm_hip_jit_capture_end": (None, []),
     "thvm_hip_jit_capture_op_count": (_u32, [_u32]), "thvm_hip_jit_replay": (_i32, [_u32]),
     "thvm_hip_jit_rebind": (_i32, [_u32, _vp, _vp, _u32]),
@@ -317,6 +330,24 @@ def kprof_query(tag: str) -> tuple[float, int]:
     n = C.c_uint64()
     ms = lib().thvm_hip_kprof_query(tag.encode(), C.byref(n))
     return ms, n.value
+
+
+def render_kernel(nodes, name: str, cap: int = 1 << 20) -> tuple[str, RenderInfo]:
+    """HIP source + launch geometry of one lifted-DAG kernel (the renderer
+    target, reference src/codegen/render_uop.c:4964-5113).  `nodes` is a
+    sequence of (op, dtype, (src..), (arg..)) in topological order."""
+    arr = (Uop * len(nodes))()
+    for i, (op, dt, srcs, args) in enumerate(nodes):
+        u = arr[i]
+        u.op, u.dtype = op, dt
+        for k in range(4):
+            u.src[k] = srcs[k] if k < len(srcs) else -1
+            u.arg[k] = args[k] if k < len(args) else 0
+    buf = C.create_string_buffer(cap)
+    info = RenderInfo()
+    _check(lib().thvm_hip_render_kernel(arr, len(nodes), name.encode(), buf, cap, C.byref(info)),
+           "render_kernel")
+    return buf.value.decode(), info
 
 
 def kprof_bytes(tag: str) -> int:

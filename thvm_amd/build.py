@@ -16,7 +16,7 @@ OBJ = PKG / "_build"
 LIB = PKG / "lib" / "libthvm_hip.so"
 ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
 
-C_SOURCES = ["hip_backend.c", "hip_custom.c", "decoder.c"]
+C_SOURCES = ["hip_backend.c", "hip_custom.c", "decoder.c", "render.c"]
 HIP_SOURCES = ["kernels/gemv.hip", "kernels/gemm.hip", "kernels/rowops.hip", "kernels/attn.hip",
                "kernels/mla.hip", "kernels/moe.hip"]
 

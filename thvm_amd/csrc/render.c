@@ -1,0 +1,597 @@
+/* render.c -- renderer target: one kernel's lifted uop DAG -> HIP source for
+ * gfx950 plus its launch geometry.
+ *
+ * Replaces the reference's CUDA target cg_render_uop_kernel_cuda_root
+ * (src/codegen/render_uop.c:4964-5113), its term emitter rmu_emit_term
+ * (:454-815) and the CUDA dispatch geometry (src/backend/cuda/jit.c:634-787).
+ * The DAG arrives flattened (ThvmUop, sources before users) with the
+ * reference's UOP_* op numbers (src/thvm.h:302-512), RANGE axis types
+ * (KAX_*, :686-692) and reduce kinds (REDUCE_SUM / REDUCE_MAX, :515-516).
+ *
+ * gfx950 choices:
+ *   - values are SSA locals emitted once per scope; a node that does not read
+ *     a reduce loop's axes is hoisted out of that loop;
+ *   - fp16 / bf16 values compute in f32 and round to their storage type after
+ *     every op (the storage precision of each intermediate);
+ *   - geometry: a kernel whose reductions are all un-nested and at least
+ *     RENDER_GROUP_MIN long runs one 256-thread block per output element
+ *     (strided partial sums, wave64 DPP-free shuffle tree, LDS across the 4
+ *     waves: the GROUP_REDUCE form); any other kernel runs one thread per
+ *     output element with serial reduce loops;
+ *   - symbolic extents (DEFINE_VAR) are read from an int32 buffer argument,
+ *     not passed by value, so a captured graph stays correct when a bound
+ *     variable changes; the grid is sized at the variables' upper bounds and
+ *     surplus threads exit.
+ * Pure host code: no device is touched. */
+#include "internal.h"
+#include "thvm_hip.h"
+
+#include <stdarg.h>
+#include <stdint.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+/* reference op numbers (src/thvm.h) */
+enum {
+  U_CONST = 2, U_ADD = 9, U_MUL = 10, U_NEG = 11, U_RECIP = 12, U_EXP2 = 13, U_LOG2 = 14,
+  U_SQRT = 15, U_CMPLT = 16, U_REDUCE = 17, U_DEFINE_VAR = 18, U_CMPEQ = 20, U_LOAD = 21,
+  U_CAST = 23, U_BITCAST = 24, U_RANGE = 25, U_INDEX_E = 26, U_IADD = 27, U_ISUB = 28,
+  U_IMUL = 29, U_IDIV = 30, U_IMOD = 31, U_ILT = 32, U_IAND = 33, U_IWHERE = 34,
+  U_BUFFER = 36, U_STORE = 37, U_IOR = 41, U_IXOR = 42, U_ISHL = 44, U_ISHR = 51, U_SIN = 55
+};
+enum { RED_SUM = 0, RED_MAX = 1 };
+
+#define RENDER_BLOCK 256
+#define RENDER_GROUP_MIN 256
+#define RENDER_MAX_RANGES 64
+#define RENDER_MAX_SLOTS 64
+
+typedef struct {
+  char *p;
+  size_t n, cap;
+  int bad;
+} Sb;
+
+static void sb_put(Sb *s, const char *fmt, ...) __attribute__((format(printf, 2, 3)));
+static void sb_put(Sb *s, const char *fmt, ...) {
+  if (s->bad) return;
+  va_list ap;
+  va_start(ap, fmt);
+  int k = vsnprintf(s->p + s->n, s->cap - s->n, fmt, ap);
+  va_end(ap);
+  if (k < 0 || (size_t)k >= s->cap - s->n) { s->bad = 1; return; }
+  s->n += (size_t)k;
+}
+
+typedef struct {
+  const ThvmUop *u;
+  uint32_t n;
+  uint64_t *dep;       /* bit k: reads reduce axis k (index into red_rng) */
+  int *level;          /* scope level a node's local lives in, -1 = none */
+  int *is_red_axis;    /* RANGE node: its reduce-axis index, or -1 */
+  int cur_level;
+  int group;
+  Sb *s;
+  char err[160];
+  int depth;
+} R;
+
+static int is_float(uint32_t dt) {
+  return dt == THVM_DT_FP16 || dt == THVM_DT_BF16 || dt == THVM_DT_FP32 || dt == THVM_DT_FP64 ||
+         dt == THVM_DT_FP8E4M3;
+}
+
+/* storage type of a buffer element */
+static const char *store_t(uint32_t dt) {
+  switch (dt) {
+    case THVM_DT_BOOL: case THVM_DT_UINT8: case THVM_DT_FP8E4M3: return "unsigned char";
+    case THVM_DT_INT8: return "signed char";
+    case THVM_DT_INT16: return "short";
+    case THVM_DT_UINT16: case THVM_DT_BF16: return "unsigned short";
+    case THVM_DT_INT32: return "int";
+    case THVM_DT_UINT32: return "unsigned";
+    case THVM_DT_INT64: return "long long";
+    case THVM_DT_UINT64: return "unsigned long long";
+    case THVM_DT_FP16: return "_Float16";
+    case THVM_DT_FP32: return "float";
+    case THVM_DT_FP64: return "double";
+    default: return NULL;
+  }
+}
+/* type a value of dtype `dt` computes in */
+static const char *alu_t(uint32_t dt) {
+  switch (dt) {
+    case THVM_DT_FP16: case THVM_DT_BF16: case THVM_DT_FP32: case THVM_DT_FP8E4M3: return "float";
+    case THVM_DT_FP64: return "double";
+    case THVM_DT_INT64: return "long long";
+    case THVM_DT_UINT64: return "unsigned long long";
+    case THVM_DT_UINT32: return "unsigned";
+    default: return "int";
+  }
+}
+/* rounding of an f32 value to the storage precision of dt */
+static const char *round_fn(uint32_t dt) {
+  if (dt == THVM_DT_FP16) return "rt_f16";
+  if (dt == THVM_DT_BF16) return "rt_bf16";
+  return "";
+}
+
+static const char *PRELUDE =
+    "typedef unsigned int uint;\n"
+    "#ifndef INFINITY\n#define INFINITY __builtin_inff()\n#endif\n"
+    "__device__ __forceinline__ float bf2f(unsigned short h) { return __uint_as_float(((uint)h) << 16); }\n"
+    "__device__ __forceinline__ unsigned short f2bf(float f) {\n"
+    "  uint u = __float_as_uint(f);\n"
+    "  if ((u & 0x7fffffffu) > 0x7f800000u) return (unsigned short)((u >> 16) | 0x40u);\n"
+    "  return (unsigned short)((u + 0x7fffu + ((u >> 16) & 1u)) >> 16);\n"
+    "}\n"
+    "__device__ __forceinline__ float rt_bf16(float f) { return bf2f(f2bf(f)); }\n"
+    "__device__ __forceinline__ float rt_f16(float f) { return (float)(_Float16)f; }\n"
+    /* e4m3 (bias 7, no infinities, S.1111.111 = NaN) decoded from its fields */
+    "__device__ __forceinline__ float fp8e4m3_f(unsigned char b) {\n"
+    "  uint e = (b >> 3) & 15u, m = b & 7u;\n"
+    "  float v = e ? __uint_as_float(((e + 120u) << 23) | (m << 20)) : (float)m * 0.001953125f;\n"
+    "  if (e == 15u && m == 7u) v = __uint_as_float(0x7fc00000u);\n"
+    "  return (b & 0x80u) ? -v : v;\n"
+    "}\n"
+    "__device__ __forceinline__ float wsum(float v) {\n"
+    "  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);\n"
+    "  return v;\n"
+    "}\n"
+    "__device__ __forceinline__ float wmax(float v) {\n"
+    "  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));\n"
+    "  return v;\n"
+    "}\n"
+    "__device__ __forceinline__ int wsumi(int v) {\n"
+    "  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);\n"
+    "  return v;\n"
+    "}\n"
+    "__device__ __forceinline__ int wmaxi(int v) {\n"
+    "  for (int o = 32; o > 0; o >>= 1) { const int t = __shfl_xor(v, o, 64); v = t > v ? t : v; }\n"
+    "  return v;\n"
+    "}\n";
+
+static int emit(R *r, int i);
+
+static int src_ok(const R *r, int i, int k) {
+  const int s = r->u[i].src[k];
+  return s >= 0 && s < i;
+}
+
+/* float literal of an f32 bit pattern */
+static void emit_const(R *r, int i) {
+  const ThvmUop *u = &r->u[i];
+  if (is_float(u->dtype)) {
+    sb_put(r->s, "  const float v%d = __uint_as_float(0x%08xu);\n", i, (uint32_t)u->arg[0]);
+  } else {
+    sb_put(r->s, "  const %s v%d = (%s)%lldll;\n", alu_t(u->dtype), i, alu_t(u->dtype),
+           (long long)u->arg[0]);
+  }
+}
+
+static int emit_reduce(R *r, int i) {
+  const ThvmUop *u = &r->u[i];
+  const int kind = (int)u->arg[0];
+  if (kind != RED_SUM && kind != RED_MAX) {
+    snprintf(r->err, sizeof r->err, "node %d: reduce kind %d", i, kind);
+    return -1;
+  }
+  int axes[3], na = 0;
+  uint64_t mask = 0;
+  for (int k = 1; k < 4; k++) {
+    if (u->src[k] < 0) continue;
+    if (!src_ok(r, i, k) || r->u[u->src[k]].op != U_RANGE) {
+      snprintf(r->err, sizeof r->err, "node %d: reduce axis %d is not a RANGE", i, k);
+      return -1;
+    }
+    axes[na++] = u->src[k];
+    mask |= 1ull << r->is_red_axis[u->src[k]];
+  }
+  if (na == 0) { snprintf(r->err, sizeof r->err, "node %d: reduce over no axis", i); return -1; }
+  /* hoist what does not read these axes */
+  const int v = u->src[0];
+  /* extents first (they read only variables and constants) */
+  for (int k = 0; k < na; k++) {
+    const ThvmUop *rg = &r->u[axes[k]];
+    if (rg->src[0] >= 0 && emit(r, rg->src[0]) < 0) return -1;
+  }
+  /* pre-emit every node of the body that is independent of the loop */
+  {
+    int *stack = (int *)malloc(sizeof(int) * r->n), sp = 0;
+    char *seen = (char *)calloc(r->n, 1);
+    if (!stack || !seen) { free(stack); free(seen); snprintf(r->err, sizeof r->err, "out of memory"); return -1; }
+    stack[sp++] = v;
+    while (sp) {
+      const int x = stack[--sp];
+      if (seen[x]) continue;
+      seen[x] = 1;
+      if ((r->dep[x] & mask) == 0) {
+        if (emit(r, x) < 0) { free(stack); free(seen); return -1; }
+        continue;
+      }
+      for (int k = 0; k < 4; k++)
+        if (r->u[x].src[k] >= 0 && !(r->u[x].op == U_REDUCE && k > 0)) stack[sp++] = r->u[x].src[k];
+    }
+    free(stack);
+    free(seen);
+  }
+  const char *acc_t = is_float(r->u[v].dtype) ? "float" : alu_t(r->u[v].dtype);
+  const char *init = kind == RED_SUM ? "0" : (is_float(r->u[v].dtype) ? "-INFINITY" : "(-2147483647 - 1)");
+  sb_put(r->s, "  %s v%d = %s;\n", acc_t, i, init);
+  const int group = r->group;
+  if (group) {
+    sb_put(r->s, "  {\n  const int rn%d = 1", i);
+    for (int k = 0; k < na; k++) {
+      const ThvmUop *rg = &r->u[axes[k]];
+      if (rg->src[0] >= 0) sb_put(r->s, " * (int)v%d", rg->src[0]);
+      else sb_put(r->s, " * %lld", (long long)rg->arg[2]);
+    }
+    sb_put(r->s, ";\n  for (int rr = (int)threadIdx.x; rr < rn%d; rr += %d) {\n    int rq = rr;\n", i,
+           RENDER_BLOCK);
+    for (int k = na - 1; k >= 0; k--) {
+      const ThvmUop *rg = &r->u[axes[k]];
+      char ext[48];
+      if (rg->src[0] >= 0) snprintf(ext, sizeof ext, "(int)v%d", rg->src[0]);
+      else snprintf(ext, sizeof ext, "%lld", (long long)rg->arg[2]);
+      sb_put(r->s, "    const int a%lld = rq %% %s; rq /= %s;\n", (long long)rg->arg[0], ext, ext);
+    }
+  } else {
+    for (int k = 0; k < na; k++) {
+      const ThvmUop *rg = &r->u[axes[k]];
+      if (rg->src[0] >= 0)
+        sb_put(r->s, "  for (int a%lld = 0; a%lld < (int)v%d; a%lld++) {\n", (long long)rg->arg[0],
+               (long long)rg->arg[0], rg->src[0], (long long)rg->arg[0]);
+      else
+        sb_put(r->s, "  for (int a%lld = 0; a%lld < %lld; a%lld++) {\n", (long long)rg->arg[0],
+               (long long)rg->arg[0], (long long)rg->arg[2], (long long)rg->arg[0]);
+    }
+  }
+  r->cur_level++;
+  if (emit(r, v) < 0) return -1;
+  if (kind == RED_SUM) sb_put(r->s, "  v%d += (%s)v%d;\n", i, acc_t, v);
+  else if (is_float(r->u[v].dtype)) sb_put(r->s, "  v%d = fmaxf(v%d, (float)v%d);\n", i, i, v);
+  else sb_put(r->s, "  v%d = v%d > v%d ? v%d : v%d;\n", i, i, v, i, v);
+  /* leave the loop scope */
+  for (uint32_t x = 0; x < r->n; x++)
+    if (r->level[x] >= r->cur_level) r->level[x] = -1;
+  r->cur_level--;
+  if (group) {
+    sb_put(r->s, "  }\n  }\n");
+    /* block combine: wave tree, then the 4 waves through LDS */
+    const int fl = is_float(r->u[v].dtype);
+    if (!fl && strcmp(acc_t, "int") != 0) {
+      snprintf(r->err, sizeof r->err, "node %d: group reduce of a %s value", i, acc_t);
+      return -1;
+    }
+    const char *wf = kind == RED_SUM ? (fl ? "wsum" : "wsumi") : (fl ? "wmax" : "wmaxi");
+    const char *ra = fl ? "red_" : "redi_";
+    char fold[64];
+    if (kind == RED_SUM) snprintf(fold, sizeof fold, "v%d + %s[w]", i, ra);
+    else if (fl) snprintf(fold, sizeof fold, "fmaxf(v%d, red_[w])", i);
+    else snprintf(fold, sizeof fold, "(redi_[w] > v%d ? redi_[w] : v%d)", i, i);
+    sb_put(r->s,
+           "  v%d = %s(v%d);\n"
+           "  if ((threadIdx.x & 63u) == 0) %s[threadIdx.x >> 6] = v%d;\n"
+           "  __syncthreads();\n"
+           "  v%d = %s[0];\n"
+           "  for (int w = 1; w < %d; w++) v%d = %s;\n"
+           "  __syncthreads();\n",
+           i, wf, i, ra, i, i, ra, RENDER_BLOCK / 64, i, fold);
+  } else {
+    for (int k = 0; k < na; k++) sb_put(r->s, "  }\n");
+  }
+  r->level[i] = r->cur_level;
+  return i;
+}
+
+static const char *bin_op(uint32_t op) {
+  switch (op) {
+    case U_ADD: case U_IADD: return "+";
+    case U_MUL: case U_IMUL: return "*";
+    case U_ISUB: return "-";
+    case U_IDIV: return "/";
+    case U_IMOD: return "%";
+    case U_IAND: return "&";
+    case U_IOR: return "|";
+    case U_IXOR: return "^";
+    case U_ISHL: return "<<";
+    case U_ISHR: return ">>";
+    default: return NULL;
+  }
+}
+
+static int emit(R *r, int i) {
+  if (i < 0 || (uint32_t)i >= r->n) { snprintf(r->err, sizeof r->err, "bad node index %d", i); return -1; }
+  if (r->level[i] >= 0) return i;
+  if (++r->depth > 4000) { snprintf(r->err, sizeof r->err, "DAG too deep"); return -1; }
+  const ThvmUop *u = &r->u[i];
+  for (int k = 0; k < 4; k++)
+    if (u->src[k] >= i) { snprintf(r->err, sizeof r->err, "node %d: source %d is not earlier", i, u->src[k]); return -1; }
+  const char *at = alu_t(u->dtype);
+  const char *rf = round_fn(u->dtype);
+  int rc = 0;
+  switch (u->op) {
+    case U_CONST: emit_const(r, i); break;
+    case U_DEFINE_VAR:
+      sb_put(r->s, "  const int v%d = kv_[%lld];\n", i, (long long)u->arg[0]);
+      break;
+    case U_RANGE:
+      if (r->is_red_axis[i] >= 0 && r->cur_level == 0) {
+        snprintf(r->err, sizeof r->err, "node %d: reduce axis %lld read outside its reduce", i, (long long)u->arg[0]);
+        return -1;
+      }
+      sb_put(r->s, "  const int v%d = a%lld;\n", i, (long long)u->arg[0]);
+      break;
+    case U_REDUCE: rc = emit_reduce(r, i); break;
+    case U_BUFFER: break;   /* named by its slot */
+    case U_INDEX_E:
+      if (emit(r, u->src[1]) < 0) return -1;
+      sb_put(r->s, "  const long long v%d = (long long)v%d;\n", i, u->src[1]);
+      break;
+    case U_LOAD: {
+      const int ix = u->src[0];
+      if (ix < 0 || r->u[ix].op != U_INDEX_E) { snprintf(r->err, sizeof r->err, "node %d: LOAD of a non-INDEX", i); return -1; }
+      const ThvmUop *b = &r->u[r->u[ix].src[0]];
+      if (r->u[ix].src[0] < 0 || b->op != U_BUFFER) { snprintf(r->err, sizeof r->err, "node %d: INDEX of a non-BUFFER", i); return -1; }
+      if (emit(r, ix) < 0) return -1;
+      const char *conv = b->dtype == THVM_DT_BF16 ? "bf2f" : b->dtype == THVM_DT_FP8E4M3 ? "fp8e4m3_f" : "";
+      if (b->arg[1] > 0)   /* capacity known: an index outside the buffer reads 0 */
+        sb_put(r->s, "  const %s v%d = (unsigned long long)v%d < %lldull ? (%s)%s(s%lld[v%d]) : (%s)0;\n",
+               alu_t(b->dtype), i, ix, (long long)b->arg[1], alu_t(b->dtype), conv, (long long)b->arg[0], ix,
+               alu_t(b->dtype));
+      else
+        sb_put(r->s, "  const %s v%d = (%s)%s(s%lld[v%d]);\n", alu_t(b->dtype), i, alu_t(b->dtype), conv,
+               (long long)b->arg[0], ix);
+      break;
+    }
+    case U_NEG: case U_RECIP: case U_EXP2: case U_LOG2: case U_SQRT: case U_SIN: {
+      if (emit(r, u->src[0]) < 0) return -1;
+      const int a = u->src[0];
+      const char *f = u->op == U_NEG ? "-" : u->op == U_RECIP ? "1.0f / " : u->op == U_EXP2 ? "exp2f" :
+                      u->op == U_LOG2 ? "log2f" : u->op == U_SQRT ? "sqrtf" : "sinf";
+      if (!is_float(u->dtype) && u->op != U_NEG) { snprintf(r->err, sizeof r->err, "node %d: float op on an int", i); return -1; }
+      sb_put(r->s, "  const %s v%d = %s(%s(v%d));\n", at, i, rf, f, a);
+      break;
+    }
+    case U_ADD: case U_MUL: case U_IADD: case U_ISUB: case U_IMUL: case U_IDIV: case U_IMOD:
+    case U_IAND: case U_IOR: case U_IXOR: case U_ISHL: case U_ISHR: {
+      if (emit(r, u->src[0]) < 0 || emit(r, u->src[1]) < 0) return -1;
+      sb_put(r->s, "  const %s v%d = %s((%s)v%d %s (%s)v%d);\n", at, i, rf, at, u->src[0], bin_op(u->op), at,
+             u->src[1]);
+      break;
+    }
+    case U_CMPLT: case U_CMPEQ: case U_ILT: {
+      if (emit(r, u->src[0]) < 0 || emit(r, u->src[1]) < 0) return -1;
+      sb_put(r->s, "  const %s v%d = (v%d %s v%d) ? (%s)1 : (%s)0;\n", at, i, u->src[0],
+             u->op == U_CMPEQ ? "==" : "<", u->src[1], at, at);
+      break;
+    }
+    case U_IWHERE: {
+      if (emit(r, u->src[0]) < 0 || emit(r, u->src[1]) < 0 || emit(r, u->src[2]) < 0) return -1;
+      sb_put(r->s, "  const %s v%d = (v%d != 0) ? (%s)v%d : (%s)v%d;\n", at, i, u->src[0], at, u->src[1], at,
+             u->src[2]);
+      break;
+    }
+    case U_CAST: {
+      if (emit(r, u->src[0]) < 0) return -1;
+      const uint32_t sd = r->u[u->src[0]].dtype;
+      if (u->dtype == THVM_DT_BOOL)
+        sb_put(r->s, "  const int v%d = (v%d != 0) ? 1 : 0;\n", i, u->src[0]);
+      else if (is_float(u->dtype))
+        sb_put(r->s, "  const %s v%d = %s((%s)v%d);\n", at, i, rf, at, u->src[0]);
+      else if (is_float(sd))   /* float -> int truncates toward zero */
+        sb_put(r->s, "  const %s v%d = (%s)v%d;\n", at, i, at, u->src[0]);
+      else
+        sb_put(r->s, "  const %s v%d = (%s)v%d;\n", at, i, at, u->src[0]);
+      break;
+    }
+    case U_BITCAST: {
+      if (emit(r, u->src[0]) < 0) return -1;
+      const uint32_t sd = r->u[u->src[0]].dtype;
+      if (sd == THVM_DT_FP32 && (u->dtype == THVM_DT_INT32 || u->dtype == THVM_DT_UINT32))
+        sb_put(r->s, "  const %s v%d = (%s)__float_as_uint(v%d);\n", at, i, at, u->src[0]);
+      else if ((sd == THVM_DT_INT32 || sd == THVM_DT_UINT32) && u->dtype == THVM_DT_FP32)
+        sb_put(r->s, "  const float v%d = __uint_as_float((uint)v%d);\n", i, u->src[0]);
+      else { snprintf(r->err, sizeof r->err, "node %d: bitcast %u -> %u", i, sd, u->dtype); return -1; }
+      break;
+    }
+    default:
+      snprintf(r->err, sizeof r->err, "node %d: op %u is not rendered by this target", i, u->op);
+      return -1;
+  }
+  r->depth--;
+  if (rc < 0) return -1;
+  r->level[i] = r->cur_level;
+  return i;
+}
+
+/* upper bound of an integer extent expression at the variables' maxima */
+static int64_t ubound(const ThvmUop *u, int i, int *ok) {
+  const ThvmUop *x = &u[i];
+  switch (x->op) {
+    case U_CONST: return x->arg[0];
+    case U_DEFINE_VAR: return x->arg[2];
+    case U_IADD: return ubound(u, x->src[0], ok) + ubound(u, x->src[1], ok);
+    case U_IMUL: return ubound(u, x->src[0], ok) * ubound(u, x->src[1], ok);
+    default: *ok = 0; return 0;
+  }
+}
+
+THVM_API int thvm_hip_render_kernel(const ThvmUop *nodes, uint32_t n, const char *name, char *out,
+                                    uint64_t cap, ThvmRenderInfo *info) {
+  if (!nodes || n == 0 || !name || !out || cap < 1024 || !info) {
+    hb_set_error("render: bad arguments");
+    return -1;
+  }
+  memset(info, 0, sizeof *info);
+  const int root = (int)n - 1;
+  const ThvmUop *st = &nodes[root];
+  if (st->op != U_STORE || st->src[0] < 0 || nodes[st->src[0]].op != U_BUFFER || nodes[st->src[0]].arg[0] != 0) {
+    hb_set_error("render: the last node must be a STORE into buffer slot 0");
+    return -1;
+  }
+  R r;
+  memset(&r, 0, sizeof r);
+  r.u = nodes;
+  r.n = n;
+  r.dep = (uint64_t *)calloc(n, sizeof(uint64_t));
+  r.level = (int *)malloc(n * sizeof(int));
+  r.is_red_axis = (int *)malloc(n * sizeof(int));
+  Sb sb = {out, 0, cap, 0};
+  r.s = &sb;
+  int rc = -1;
+  if (!r.dep || !r.level || !r.is_red_axis) { hb_set_error("render: out of memory"); goto done; }
+  for (uint32_t i = 0; i < n; i++) { r.level[i] = -1; r.is_red_axis[i] = -1; }
+
+  /* slots and variables */
+  uint32_t slot_dt[RENDER_MAX_SLOTS];
+  int slot_used[RENDER_MAX_SLOTS] = {0};
+  int nvar = 0, nslot = 0;
+  for (uint32_t i = 0; i < n; i++) {
+    const ThvmUop *u = &nodes[i];
+    for (int k = 0; k < 4; k++)
+      if (u->src[k] >= (int32_t)i) { hb_set_error("render: node %u reads a later node", i); goto done; }
+    if (u->op == U_BUFFER) {
+      const int64_t sl = u->arg[0];
+      if (sl < 0 || sl >= RENDER_MAX_SLOTS || !store_t(u->dtype)) { hb_set_error("render: buffer slot %lld / dtype %u", (long long)sl, u->dtype); goto done; }
+      if (slot_used[sl] && slot_dt[sl] != u->dtype) { hb_set_error("render: slot %lld has two dtypes", (long long)sl); goto done; }
+      slot_used[sl] = 1;
+      slot_dt[sl] = u->dtype;
+      if ((int)sl + 1 > nslot) nslot = (int)sl + 1;
+    } else if (u->op == U_DEFINE_VAR) {
+      if (u->arg[0] < 0 || u->arg[0] >= 64) { hb_set_error("render: variable index %lld", (long long)u->arg[0]); goto done; }
+      if ((int)u->arg[0] + 1 > nvar) nvar = (int)u->arg[0] + 1;
+    }
+  }
+  for (int k = 0; k < nslot; k++)
+    if (!slot_used[k]) { hb_set_error("render: buffer slot %d is never declared", k); goto done; }
+
+  /* reduce axes, dependence masks, nesting */
+  int nred = 0;
+  for (uint32_t i = 0; i < n; i++)
+    if (nodes[i].op == U_REDUCE)
+      for (int k = 1; k < 4; k++) {
+        const int a = nodes[i].src[k];
+        if (a < 0) continue;
+        if (nodes[a].op != U_RANGE) { hb_set_error("render: reduce %u axis is not a RANGE", i); goto done; }
+        if (r.is_red_axis[a] < 0) {
+          if (nred >= RENDER_MAX_RANGES) { hb_set_error("render: too many reduce axes"); goto done; }
+          r.is_red_axis[a] = nred++;
+        }
+      }
+  int nested = 0, has_red = 0;
+  int64_t red_len_min = INT64_MAX;
+  for (uint32_t i = 0; i < n; i++) {
+    const ThvmUop *u = &nodes[i];
+    uint64_t d = 0;
+    if (u->op == U_RANGE && r.is_red_axis[i] >= 0) d = 1ull << r.is_red_axis[i];
+    for (int k = 0; k < 4; k++) {
+      if (u->src[k] < 0) continue;
+      if (u->op == U_REDUCE && k > 0) continue;
+      d |= r.dep[u->src[k]];
+    }
+    if (u->op == U_REDUCE) {
+      for (int k = 1; k < 4; k++)
+        if (u->src[k] >= 0) d &= ~(1ull << r.is_red_axis[u->src[k]]);
+      if (d) nested = 1;
+      has_red = 1;
+      int ok = 1;
+      int64_t len = 1;
+      for (int k = 1; k < 4; k++) {
+        const int a = u->src[k];
+        if (a < 0) continue;
+        len *= nodes[a].src[0] >= 0 ? ubound(nodes, nodes[a].src[0], &ok) : nodes[a].arg[2];
+      }
+      if (ok && len < red_len_min) red_len_min = len;
+    }
+    r.dep[i] = d;
+  }
+  r.group = has_red && !nested && red_len_min >= RENDER_GROUP_MIN;
+
+  /* parallel axes: every RANGE that no REDUCE binds, in axis-id order */
+  int par[RENDER_MAX_RANGES], npar = 0;
+  for (uint32_t i = 0; i < n; i++)
+    if (nodes[i].op == U_RANGE && r.is_red_axis[i] < 0) {
+      if (npar >= RENDER_MAX_RANGES) { hb_set_error("render: too many axes"); goto done; }
+      par[npar++] = (int)i;
+    }
+  for (int a = 1; a < npar; a++)     /* insertion sort by axis id */
+    for (int b = a; b > 0 && nodes[par[b]].arg[0] < nodes[par[b - 1]].arg[0]; b--) {
+      int t = par[b]; par[b] = par[b - 1]; par[b - 1] = t;
+    }
+  uint64_t total_max = 1;
+  for (int a = 0; a < npar; a++) {
+    const ThvmUop *rg = &nodes[par[a]];
+    int ok = 1;
+    const int64_t e = rg->src[0] >= 0 ? ubound(nodes, rg->src[0], &ok) : rg->arg[2];
+    if (!ok || e < 0) { hb_set_error("render: axis %lld has no upper bound", (long long)rg->arg[0]); goto done; }
+    total_max *= (uint64_t)e;
+  }
+  if (total_max > (1ull << 31)) { hb_set_error("render: %llu output elements", (unsigned long long)total_max); goto done; }
+
+  /* source */
+  sb_put(&sb, "%s\n", PRELUDE);
+  sb_put(&sb, "extern \"C\" __global__ void __launch_bounds__(%d) %s(\n", RENDER_BLOCK, name);
+  for (int k = 0; k < nslot; k++)
+    sb_put(&sb, "    %s%s *__restrict__ s%d%s\n", k ? "const " : "", store_t(slot_dt[k]), k,
+           (k + 1 < nslot || nvar) ? "," : "");
+  if (nvar) sb_put(&sb, "    const int *__restrict__ kv_\n");
+  sb_put(&sb, ") {\n");
+  if (r.group)
+    sb_put(&sb, "  __shared__ float red_[%d];\n  __shared__ int redi_[%d];\n  (void)red_; (void)redi_;\n"
+           "  const long long gid = blockIdx.x;\n", RENDER_BLOCK / 64, RENDER_BLOCK / 64);
+  else sb_put(&sb, "  const long long gid = (long long)blockIdx.x * %d + threadIdx.x;\n", RENDER_BLOCK);
+  /* extents of the parallel axes, then the element decomposition */
+  for (int a = 0; a < npar; a++) {
+    const ThvmUop *rg = &nodes[par[a]];
+    if (rg->src[0] >= 0) {
+      if (emit(&r, rg->src[0]) < 0) goto bad;
+      sb_put(&sb, "  const long long e%d = (long long)v%d;\n", a, rg->src[0]);
+    } else {
+      sb_put(&sb, "  const long long e%d = %lldll;\n", a, (long long)rg->arg[2]);
+    }
+  }
+  sb_put(&sb, "  if (gid >= 1ll");
+  for (int a = 0; a < npar; a++) sb_put(&sb, " * e%d", a);
+  sb_put(&sb, ") return;\n  long long q_ = gid;\n");
+  for (int a = npar - 1; a >= 0; a--)
+    sb_put(&sb, "  const int a%lld = (int)(q_ %% e%d); q_ /= e%d;\n", (long long)nodes[par[a]].arg[0], a, a);
+  sb_put(&sb, "  (void)q_;\n");
+  if (emit(&r, st->src[1]) < 0 || emit(&r, st->src[2]) < 0) goto bad;
+  {
+    const uint32_t odt = slot_dt[0];
+    const uint32_t vdt = nodes[st->src[2]].dtype;
+    char val[64];
+    if (odt == THVM_DT_BF16) snprintf(val, sizeof val, "f2bf((float)v%d)", st->src[2]);
+    else if (odt == THVM_DT_FP16) snprintf(val, sizeof val, "(_Float16)(float)v%d", st->src[2]);
+    else if (odt == THVM_DT_BOOL) snprintf(val, sizeof val, "(unsigned char)(v%d != 0)", st->src[2]);
+    else if (odt == THVM_DT_FP8E4M3) { hb_set_error("render: fp8 stores are not rendered"); goto done; }
+    else snprintf(val, sizeof val, "(%s)v%d", store_t(odt), st->src[2]);
+    (void)vdt;
+    char guard[96] = "";
+    const int64_t cap0 = nodes[st->src[0]].arg[1];
+    if (cap0 > 0) snprintf(guard, sizeof guard, "(unsigned long long)v%d < %lldull", st->src[1], (long long)cap0);
+    if (r.group || guard[0])
+      sb_put(&sb, "  if (%s%s%s) s0[v%d] = %s;\n}\n", r.group ? "threadIdx.x == 0" : "",
+             r.group && guard[0] ? " && " : "", guard, st->src[1], val);
+    else
+      sb_put(&sb, "  s0[v%d] = %s;\n}\n", st->src[1], val);
+  }
+  if (sb.bad) { hb_set_error("render: source exceeds %llu bytes", (unsigned long long)cap); goto done; }
+  info->n_slots = (uint32_t)nslot + (nvar ? 1u : 0u);
+  info->kvar_slot = nvar ? (uint32_t)nslot : 0u;
+  info->group = (uint32_t)r.group;
+  info->block = RENDER_BLOCK;
+  info->grid_max = r.group ? total_max : (total_max + RENDER_BLOCK - 1) / RENDER_BLOCK;
+  if (info->grid_max == 0) info->grid_max = 1;
+  rc = 0;
+  goto done;
+bad:
+  hb_set_error("render: %s", r.err[0] ? r.err : "emit failed");
+done:
+  free(r.dep);
+  free(r.level);
+  free(r.is_red_axis);
+  return rc;
+}
