@@ -355,6 +355,79 @@ def measured_traffic():
         return None
 
 
+def run_host_gpt2(thvm, key: str, args) -> dict:
+    """C1 / C3 through the Python Tensor host (thvm_amd.tensor + TinyJit):
+    the reference's GPT-2 driver path (bench/gpt2/thvm_gpt2.py) rather than
+    the C decoder.  A step is one greedy token end to end: token upload,
+    TinyJit replay of the captured graph, token read-back."""
+    import numpy as np
+    from thvm_amd import tensor as T
+    from thvm_amd.gpt2 import GPT2
+    spec = MODELS[key]
+    c = spec["cfg"]
+    L = args.layers or c["n_layers"]
+    ctx = spec["ctx"]
+    max_ctx = ((ctx + args.warmup + args.steps + 8 + 63) // 64) * 64
+    w = GPT2.synthetic_weights(L, c["dim"], c["vocab"], max_ctx, seed=1234, std=c["init_std"])
+    if c["wdtype"] == DT_F16:
+        w = {k: v.astype(np.float16) for k, v in w.items()}
+    g = GPT2.build(L, c["n_heads"], c["dim"], c["vocab"], max_ctx, max_ctx, w)
+    prompt = [(7 * i + 3) % c["vocab"] for i in range(ctx)]
+    t0 = time.time()
+    cur = np.array([prompt[0]], np.int32)
+    for pos in range(ctx - 1):                      # prompt, one token at a time (captures the JIT)
+        g.step(cur, pos)
+        cur = np.array([prompt[pos + 1]], np.int32)
+    pos = ctx - 1
+    for _ in range(args.warmup):
+        cur = g.step(cur, pos).astype(np.int32)
+        pos += 1
+    log(f"[bench] host {key}: prompt + warmup {time.time() - t0:.1f}s, "
+        f"{T.GlobalCounters.kernel_count} rendered + {T.GlobalCounters.gemv_count} GEMV dispatches so far")
+    thvm.synchronize()
+    t1 = time.perf_counter()
+    for _ in range(args.steps):
+        cur = g.step(cur, pos).astype(np.int32)
+        pos += 1
+    thvm.synchronize()
+    dt = time.perf_counter() - t1
+    jit = g.model.forward_jit
+    cpu = None
+    if not args.no_cpu:
+        sys.path.insert(0, str(ROOT / "tests"))
+        import _oracle as O
+
+        class _W:
+            def __init__(s):
+                s.t = {k: np.ascontiguousarray(v, np.float32) for k, v in w.items()}
+                hd = c["dim"] // c["n_heads"]
+                for l in range(L):
+                    s.t[f"l{l}.kcache"] = np.zeros((1, c["n_heads"], max_ctx, hd), np.float32)
+                    s.t[f"l{l}.vcache"] = np.zeros((1, c["n_heads"], max_ctx, hd), np.float32)
+
+            def read_tensor(s, name):
+                return s.t[name]
+        ocfg = dict(c, n_layers=L, batch=1, max_seq=max_ctx, wdtype=DT_F32, adtype=DT_F32)
+        om = O.OracleModel(_W(), ocfg)
+        n_cpu = args.cpu_steps or 2
+        tc = time.perf_counter()
+        for s in range(n_cpu):
+            om.step(np.array([prompt[s]], np.int32), s)
+        tcpu = time.perf_counter() - tc
+        cpu = {"value": round(n_cpu / tcpu, 4), "unit": "tokens/s", "cores": 1, "kind": "port",
+               "sample": f"{n_cpu} decode steps of the same model (fp32) from position 0 on the C oracle"}
+    return {"metric": METRIC, "value": round(args.steps / dt, 2), "unit": "tokens/s", "n_gpus": 1,
+            "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(dt / args.steps * 1e3, 4),
+            "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+            "dtype": f"{DT_NAME[c['wdtype']]} weights and activations, f32 accumulate",
+            "data": "synthetic",
+            "config": {"workload": spec["name"] + ", through the Python Tensor host (TinyJit replay)",
+                       "layers": L, "d_model": c["dim"], "heads": c["n_heads"], "vocab": c["vocab"],
+                       "batch": 1, "context": ctx, "parallelism": "single GPU", "path": "tensor-host"},
+            "jit_kernels_per_step": int(jit.jit.op_count()) if jit.jit is not None else None,
+            "cpu_baseline": cpu}
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -365,6 +438,9 @@ def main() -> int:
     ap.add_argument("--cpu-steps", type=int, default=0, help="oracle steps (0: the config's default)")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--layers", type=int, default=None, help="debug only: fewer layers (invalid metric)")
+    ap.add_argument("--host", action="store_true",
+                    help="C1/C3: run the GPT-2 driver on the Python Tensor host (TinyJit) "
+                         "instead of the C decoder")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run only the plain 1 GiB copy kernel that calibrates the HBM traffic "
                          "counters (FETCH_SIZE/WRITE_SIZE) and print its timing")
@@ -384,7 +460,10 @@ def main() -> int:
         else:
             runs = [(args.config, args.batch)]
         for key, batch in runs:
-            out = run_c2(thvm, args) if key == "C2" else run_decode(thvm, key, batch, args)
+            if args.host and key in ("C1", "C3"):
+                out = run_host_gpt2(thvm, key, args)
+            else:
+                out = run_c2(thvm, args) if key == "C2" else run_decode(thvm, key, batch, args)
             print(json.dumps(out), flush=True)
     finally:
         thvm.shutdown()

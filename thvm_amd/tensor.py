@@ -1221,9 +1221,7 @@ class Tensor:
         nb = max(len(bx), len(bw))
         bx, bw = (1,) * (nb - len(bx)) + tuple(bx), (1,) * (nb - len(bw)) + tuple(bw)
         batch = tuple(a if not _eq(a, 1) else b for a, b in zip(bx, bw))
-        x = x.reshape(bx + x.shape[-2:])
-        w = w.reshape(bw + w.shape[-2:])
-        dt = _promote(x.dtype, w.dtype)
+        dt = _promote(x.dtype, w.dtype)     # operands keep their rank: lowering broadcasts
         return Tensor(LNode("MATMUL", (x.node, w.node), None, batch + (x.shape[-2], w.shape[-1]), dt))
 
     def dot(self, w): return self.matmul(w)
