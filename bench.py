@@ -130,9 +130,15 @@ def run_decode(thvm, key: str, batch: int, args) -> dict:
     cfg = dict(spec["cfg"], batch=batch)
     if args.layers:
         cfg["n_layers"] = args.layers
+    # --step-mode 1: the persistent step (one launch per token; LLAMA, batch
+    # 1/2/4, fp8 or bf16 weights).  The default is one launch per op, which
+    # measures faster at these shapes.
+    persist = args.step_mode == "1"
+    if persist:
+        cfg["step_mode"] = 1
     ctx = spec["ctx"]
     cpu_steps = 0 if args.no_cpu else (args.cpu_steps or (spec["cpu_steps"] if batch <= 4 else 1))
-    cfg["max_seq"] = ((ctx + args.warmup + args.steps + cpu_steps + 4 + 63) // 64) * 64
+    cfg["max_seq"] = ((ctx + args.warmup + args.steps + cpu_steps + 8 + 63) // 64) * 64
     t0 = time.time()
     dec = thvm.Decoder(seed=1234, **cfg)
     dec.prefill_synthetic(ctx, seed=99)
@@ -154,6 +160,31 @@ def run_decode(thvm, key: str, batch: int, args) -> dict:
     tps = batch * args.steps / (ms / 1000.0)
     log(f"[bench] timed {args.steps} steps: {ms_per_step:.3f} ms/step (wall {wall * 1000 / args.steps:.3f})")
 
+    stages = None
+    if persist:
+        # block 0's stage clock over 4 replays: per stage type, the time between
+        # barrier openings, and within a stage the wait for its barrier, the
+        # block's own work and the drain of its stores
+        import numpy as np
+        NL = cfg["n_layers"]
+        nb, ns = 5 * NL + 2, 5 * NL + 1
+        names = ["qkv", "attn", "o", "gate_up", "down"]
+        acc = {}
+        for _ in range(4):
+            dec.replay(1)
+            c = dec.stage_clock()
+            bar, det = c[:nb], c[nb:].reshape(ns, 4)
+            span = np.diff(bar)
+            for st in range(ns):
+                nm = "lm_head+tail" if st == ns - 1 else names[st % 5]
+                acc.setdefault(nm, []).append((span[st], det[st, 1] - det[st, 0],
+                                               det[st, 2] - det[st, 1], det[st, 3] - det[st, 2]))
+        stages = {nm: dict(zip(("span_us", "wait_us", "work_us", "drain_us"),
+                               [round(float(x), 2) for x in np.mean(v, 0)]))
+                  for nm, v in acc.items()}
+        for nm, v in stages.items():
+            log(f"[bench] stage {nm}: {v}")
+
     # live per-kernel timing: a bounded sleep kernel (~10 ms) goes first so the
     # host enqueues whole eager steps behind it and they run back to back; each
     # builtin launch carries a hipEvent pair bound to its kernels' own start and
@@ -168,25 +199,39 @@ def run_decode(thvm, key: str, batch: int, args) -> dict:
     mla = cfg["arch"] == 3
     atag = "mla_attn" if mla else "attn"
     kern = {}
-    for tag in ("gemv", "moe_gateup", "moe_down", "mla_prep", "route", "norm", atag):
+    for tag in ("gemv", "moe_gateup", "moe_down", "mla_prep", "route", "norm", atag, "llama_step"):
         ms_t, n_t = thvm.kprof_query(tag)
         if n_t:
             kern[tag] = (ms_t, n_t, thvm.kprof_bytes(tag))
     thvm.kprof(False)
     dummy.free()
     L_prof = dec.position - 1
+    if persist:
+        # one launch holds every stage: its bytes are the weights (counted by
+        # the dispatcher) plus the live KV rows of the two profiled steps
+        s_ms, s_n, s_b = kern["llama_step"]
+        kern["llama_step"] = (s_ms, s_n, s_b + sum(attn_bytes_per_step(cfg, L_prof - i)
+                                                   for i in range(prof_steps)))
+        kern[atag] = (0.0, 0, 0)
     a_ms, a_n, _ = kern[atag]
-    kern[atag] = (a_ms, a_n, attn_bytes_per_step(cfg, L_prof) * prof_steps)
+    if not persist:
+        kern[atag] = (a_ms, a_n, attn_bytes_per_step(cfg, L_prof) * prof_steps)
     for tag, (ms_t, n_t, b_t) in kern.items():
-        log(f"[bench] {tag}: {n_t // prof_steps} launches/step, {ms_t / n_t * 1000:.1f} us avg"
-            + (f", {b_t / (ms_t / 1000.0) / 1e9:.0f} GB/s" if b_t else ""))
+        if n_t:
+            log(f"[bench] {tag}: {n_t // prof_steps} launches/step, {ms_t / n_t * 1000:.1f} us avg"
+                + (f", {b_t / (ms_t / 1000.0) / 1e9:.0f} GB/s" if b_t else ""))
     # the dominant kernel: the one moving the most algorithmic bytes per step
     dom = max((t for t in kern if t != atag), key=lambda t: kern[t][2])
     g_ms, g_n, g_bytes = kern[dom]
     gemv_gbs = g_bytes / (g_ms / 1000.0) / 1e9
-    attn_gbs = kern[atag][2] / (a_ms / 1000.0) / 1e9
-    step_bytes = sum(b for t, (_, _, b) in kern.items() if t != atag) // prof_steps + \
-        attn_bytes_per_step(cfg, L_mid)
+    attn_gbs = kern[atag][2] / (a_ms / 1000.0) / 1e9 if a_ms else None
+    if persist:
+        step_bytes = (kern["llama_step"][2] - sum(attn_bytes_per_step(cfg, L_prof - i)
+                                                  for i in range(prof_steps))) // prof_steps + \
+            attn_bytes_per_step(cfg, L_mid)
+    else:
+        step_bytes = sum(b for t, (_, _, b) in kern.items() if t != atag) // prof_steps + \
+            attn_bytes_per_step(cfg, L_mid)
 
     cpu = None
     if cpu_steps:
@@ -198,7 +243,10 @@ def run_decode(thvm, key: str, batch: int, args) -> dict:
                          f"with the device on the same inputs",
                "seconds": round(secs, 2), "ids_match": match, "logits_max_rel_err": lerr}
     mfma = batch > 4
-    if dom == "gemv":
+    if dom == "llama_step":
+        gkern = ("k_llama_step (the whole decode step in one persistent launch: %s weight GEMVs, "
+                 "split-sequence attention, LM head and argmax)" % DT_NAME[cfg["wdtype"]])
+    elif dom == "gemv":
         gkern = ("k_gemm (MFMA v_mfma_f32_16x16x32, %s weights)" if mfma else
                  "k_gemv (%s weight GEMV)") % DT_NAME[cfg["wdtype"]]
     else:
@@ -217,19 +265,23 @@ def run_decode(thvm, key: str, batch: int, args) -> dict:
                    "parallelism": "single GPU"},
         "roofline": {"bound": "hbm", "achieved": round(gemv_gbs, 1), "peak": PEAK_GBS,
                      "unit": "GB/s", "frac": round(gemv_gbs / PEAK_GBS, 4),
-                     "traffic": (measured_traffic() if key == "C4" and batch == 1 and not args.layers
+                     "traffic": (measured_traffic() if key == "C4" and batch == 1 and not args.layers and not persist
                                  else None),
                      "kernel": gkern,
                      "algorithmic_bytes_per_launch": g_bytes // max(g_n, 1),
                      "launches_per_step": g_n // prof_steps,
                      "avg_launch_us": round(g_ms / g_n * 1000, 2)},
-        "attention": {"kernel": "k_mla_split + k_mla_out" if mla else "k_attn + k_attn_merge",
-                      "achieved_gbs": round(attn_gbs, 1), "frac": round(attn_gbs / PEAK_GBS, 4),
-                      "avg_launch_us": round(a_ms / max(a_n, 1) * 1000, 2)},
+        "attention": ({"kernel": "a stage of k_llama_step (its bytes are in the roofline line)"}
+                      if persist else
+                      {"kernel": "k_mla_split + k_mla_out" if mla else "k_attn + k_attn_merge",
+                       "achieved_gbs": round(attn_gbs, 1), "frac": round(attn_gbs / PEAK_GBS, 4),
+                       "avg_launch_us": round(a_ms / max(a_n, 1) * 1000, 2)}),
         "kernels": {t: {"launches_per_step": n_t // prof_steps,
                         "avg_launch_us": round(ms_t / n_t * 1000, 2),
                         "gbs": round(b_t / (ms_t / 1000.0) / 1e9, 1) if b_t else None}
-                    for t, (ms_t, n_t, b_t) in kern.items()},
+                    for t, (ms_t, n_t, b_t) in kern.items() if n_t},
+        "step_mode": "persistent (one launch per step)" if persist else "one launch per op (hipGraph)",
+        **({"stage_clock": stages} if stages else {}),
         "step_hbm_gbs": round(step_bytes / (ms_per_step / 1000.0) / 1e9, 1),
         "step_bytes": step_bytes,
         "kernels_per_step": dec.step_kernels(),
@@ -437,6 +489,8 @@ def main() -> int:
     ap.add_argument("--batch", type=int, default=1)
     ap.add_argument("--cpu-steps", type=int, default=0, help="oracle steps (0: the config's default)")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--step-mode", default="0", choices=["0", "1"],
+                    help="0: one launch per op (hipGraph); 1: the persistent one-launch step (LLAMA)")
     ap.add_argument("--layers", type=int, default=None, help="debug only: fewer layers (invalid metric)")
     ap.add_argument("--host", action="store_true",
                     help="C1/C3: run the GPT-2 driver on the Python Tensor host (TinyJit) "

@@ -250,7 +250,12 @@ typedef struct ThvmDecodeConfig {
   uint32_t kv_lora;       /* latent rank                                   */
   uint32_t d_nope, d_rope, d_v;
   uint32_t n_experts, n_shared, top_k, moe_inter, first_dense;
-  uint32_t reserved[8];
+  /* LLAMA only: 1 runs the step as ONE persistent launch (one block per CU,
+   * stages separated by grid barriers) instead of one launch per op; outputs
+   * are identical.  Batch 1, 2 or 4; fp8 or bf16 weights, bf16 activations;
+   * head_dim 64/128; 1, 2 or 4 query heads per kv head.                    */
+  uint32_t step_mode;
+  uint32_t reserved[7];
 } ThvmDecodeConfig;
 
 /* Build the model on device: allocate, fill weights from `seed` (weights
@@ -285,6 +290,13 @@ uint32_t thvm_hip_decoder_tensor(uint32_t dec, const char *name,
 uint64_t thvm_hip_decoder_step_bytes(uint32_t dec);
 /* Number of dispatches in one step. */
 uint32_t thvm_hip_decoder_step_kernels(uint32_t dec);
+/* Persistent step (step_mode 1) only: the stage clock of the last step, in
+ * microseconds after its start, as recorded by block 0: the opening of each
+ * grid barrier and the end of the step (5 n_layers + 2 values), then for each
+ * stage (l*5 + QKV, ATTN, O, GU, DOWN; then the LM head) its entry, barrier
+ * open, work done and stores drained (4 values each).  Writes up to n values
+ * and returns how many the step has (0 for a per-op decoder, -1 on error). */
+int      thvm_hip_decoder_stage_clock(uint32_t dec, double *us_out, uint32_t n);
 
 #ifdef __cplusplus
 }

@@ -43,8 +43,8 @@ class DecodeConfig(C.Structure):
         "max_seq", "batch", "wdtype", "adtype")] + [
         ("eps", C.c_float), ("rope_theta", C.c_float), ("init_std", C.c_float)] + [
         (n, C.c_uint32) for n in ("kv_lora", "d_nope", "d_rope", "d_v", "n_experts",
-                                  "n_shared", "top_k", "moe_inter", "first_dense")] + [
-        ("reserved", C.c_uint32 * 8)]
+                                  "n_shared", "top_k", "moe_inter", "first_dense", "step_mode")] + [
+        ("reserved", C.c_uint32 * 7)]
 
 
 class Uop(C.Structure):
@@ -104,6 +104,7 @@ _SIGS = {
     "thvm_hip_decoder_tensor": (_u32, [_u32, _cp, C.POINTER(_u32), C.POINTER(_u64)]),
     "thvm_hip_decoder_step_bytes": (_u64, [_u32]),
     "thvm_hip_decoder_step_kernels": (_u32, [_u32]),
+    "thvm_hip_decoder_stage_clock": (C.c_int, [_u32, C.c_void_p, _u32]),
 }
 
 _LIB = None
@@ -311,6 +312,18 @@ class Decoder:
 
     def step_kernels(self) -> int:
         return lib().thvm_hip_decoder_step_kernels(self.h)
+
+    def stage_clock(self) -> np.ndarray:
+        """Persistent step only: microseconds after the last step's start at
+        which each grid barrier opened and the step's end (5 L + 2 values),
+        then per stage (5 L + 1) its entry, barrier open, work done and stores
+        drained -- block 0's clock."""
+        n = self.cfg.n_layers * 5 + 2 + 4 * (self.cfg.n_layers * 5 + 1)
+        out = np.zeros(n, np.float64)
+        got = lib().thvm_hip_decoder_stage_clock(self.h, out.ctypes.data, n)
+        if got < 0:
+            raise ThvmHipError(f"stage_clock: {last_error()}")
+        return out[:got]
 
     def close(self) -> None:
         if self.h:

@@ -18,7 +18,8 @@ ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
 
 C_SOURCES = ["hip_backend.c", "hip_custom.c", "decoder.c", "render.c"]
 HIP_SOURCES = ["kernels/gemv.hip", "kernels/gemm.hip", "kernels/rowops.hip", "kernels/attn.hip",
-               "kernels/mla.hip", "kernels/moe.hip"]
+               "kernels/mla.hip", "kernels/moe.hip", "kernels/step.hip", "kernels/step_m1.hip",
+               "kernels/step_m2.hip", "kernels/step_m4.hip"]
 
 CFLAGS = ["-std=c11", "-O2", "-fPIC", "-Wall", "-Wextra", "-Wno-unused-parameter",
           "-fvisibility=hidden", "-D__HIP_PLATFORM_AMD__",

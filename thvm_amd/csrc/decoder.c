@@ -185,6 +185,10 @@ static int cfg_check(const ThvmDecodeConfig *c) {
     hb_set_error("decoder: arch %u not supported by this build", c->arch);
     return -1;
   }
+  if (c->step_mode > 1 || (c->step_mode && c->arch != THVM_ARCH_LLAMA)) {
+    hb_set_error("decoder: step_mode 1 (persistent step) is for the LLAMA architecture");
+    return -1;
+  }
   if (c->arch == THVM_ARCH_DSV2) {
     if (!c->n_layers || !c->dim || !c->n_heads || !c->vocab || !c->max_seq || !c->batch ||
         !c->kv_lora || !c->d_nope || !c->d_rope || !c->d_v || !c->n_experts || !c->top_k ||
@@ -374,6 +378,81 @@ static int op_tail(Decoder *d, u32 lm_w, u32 lm_s, const NormSpec *fn) {
   return op_add(d, "len_bump", "thvm-builtin:len_bump delta=1", &L, 1);
 }
 
+/* The persistent step (step_mode 1): the same weights and state as the op
+ * list just built, which it replaces by one llama_step dispatch.  Its first
+ * slot is a device table of per-layer weight / cache pointers. */
+static int build_llama_step(Decoder *d) {
+  const ThvmDecodeConfig *c = &d->c;
+  const u32 NL = c->n_layers, B = c->batch, nb = thvm_k_step_blocks();
+  const int f8 = c->wdtype == THVM_DT_FP8E4M3;
+  if (!nb) { hb_set_error("decoder: step_mode needs a device"); return -1; }
+  ThvmStepLayer *tab = (ThvmStepLayer *)calloc(NL, sizeof *tab);
+  if (!tab) { hb_set_error("decoder: out of host memory"); return -1; }
+  char nm[48];
+#define TP(fmt) (snprintf(nm, sizeof nm, fmt, l), hb_buf_ptr(tens_find(d, nm)))
+  for (u32 l = 0; l < NL; l++) {
+    ThvmStepLayer *t = &tab[l];
+    t->wqkv = TP("l%u.wqkv"); t->wo = TP("l%u.wo"); t->wgu = TP("l%u.wgu"); t->wd = TP("l%u.wd");
+    if (f8) {
+      t->sqkv = (const float *)TP("l%u.wqkv.scale"); t->so = (const float *)TP("l%u.wo.scale");
+      t->sgu = (const float *)TP("l%u.wgu.scale"); t->sd = (const float *)TP("l%u.wd.scale");
+    }
+    t->g_attn = (const float *)TP("l%u.g_attn"); t->g_ffn = (const float *)TP("l%u.g_ffn");
+    t->kcache = TP("l%u.kcache"); t->vcache = TP("l%u.vcache");
+    if (!t->wqkv || !t->wo || !t->wgu || !t->wd || !t->g_attn || !t->g_ffn || !t->kcache ||
+        !t->vcache || (f8 && (!t->sqkv || !t->so || !t->sgu || !t->sd))) {
+      free(tab);
+      hb_set_error("decoder: layer %u tensors missing for the persistent step", l);
+      return -1;
+    }
+  }
+#undef TP
+  const u32 tb = tens_new(d, "step.layers", THVM_DT_UINT8, (u64)NL * sizeof *tab);
+  const int wrc = tb ? thvm_hip_buf_write(tb, tab, (u64)NL * sizeof *tab) : -1;
+  free(tab);
+  if (wrc) return -1;
+  /* argmax partials per block, the grid-barrier words (zero-filled) */
+  if (!tens_new(d, "step.pv", THVM_DT_FP32, (u64)B * nb * 4) ||
+      !tens_new(d, "step.pi", THVM_DT_INT32, (u64)B * nb * 4) ||
+      !tens_new(d, "step.sync", THVM_DT_UINT32, thvm_k_step_sync_bytes()))
+    return -1;
+  for (u32 i = 0; i < d->n_ops; i++) { free(d->ops[i].name); free(d->ops[i].prog); }
+  d->n_ops = 0;
+  char p[400];
+  snprintf(p, sizeof p,
+           "thvm-builtin:llama_step l=%u m=%u d=%u h=%u hkv=%u hd=%u f=%u v=%u maxseq=%u nsplit=%u "
+           "wt=%u at=%u eps=%a scale=%a hstride=%u",
+           NL, B, c->dim, c->n_heads, c->n_kv_heads, c->head_dim, c->ffn, c->vocab, c->max_seq,
+           d->n_split, c->wdtype, c->adtype, c->eps, (float)(1.0 / sqrt((double)c->head_dim)),
+           c->max_seq + 1);
+  u32 a[24], n = 0;
+  a[n++] = tb; a[n++] = tens_find(d, "emb"); a[n++] = tens_find(d, "norm_f"); a[n++] = tens_find(d, "lm");
+  if (f8) a[n++] = tens_find(d, "lm.scale");
+  a[n++] = tens_find(d, "rope.cos"); a[n++] = tens_find(d, "rope.sin"); a[n++] = tens_find(d, "tok");
+  a[n++] = tens_find(d, "len"); a[n++] = tens_find(d, "hist"); a[n++] = tens_find(d, "logits");
+  a[n++] = tens_find(d, "x"); a[n++] = tens_find(d, "q"); a[n++] = tens_find(d, "att");
+  a[n++] = tens_find(d, "h"); a[n++] = tens_find(d, "attn.part"); a[n++] = tens_find(d, "step.pv");
+  a[n++] = tens_find(d, "step.pi"); a[n++] = tens_find(d, "step.sync");
+  return op_add(d, "llama_step", p, a, n);
+}
+
+/* 0, or -1 when a persistent step of this decoder failed (a grid barrier
+ * expired: the step's outputs are not valid) */
+static int step_status(Decoder *d) {
+  const u32 sy = tens_find(d, "step.sync");
+  if (!sy) return 0;
+  const u64 nbytes = thvm_k_step_sync_bytes();
+  uint32_t *w = (uint32_t *)malloc(nbytes);
+  if (!w) { hb_set_error("decoder: out of host memory"); return -1; }
+  int rc = thvm_hip_buf_read(sy, w, nbytes);
+  if (!rc && w[thvm_k_step_err_word()]) {
+    hb_set_error("decoder: a persistent step failed (a grid barrier expired); its outputs are invalid");
+    rc = -1;
+  }
+  free(w);
+  return rc;
+}
+
 static int build_llama(Decoder *d) {
   const ThvmDecodeConfig *c = &d->c;
   u32 D = c->dim, H = c->n_heads, Hkv = c->n_kv_heads, hd = c->head_dim, F = c->ffn;
@@ -458,7 +537,8 @@ static int build_llama(Decoder *d) {
   u32 lw, ls;
   if (weight_matrix(d, "lm", c->vocab, D, &lw, &ls)) return -1;
   NormSpec nf = {1, tens_find(d, "norm_f"), 0};
-  return op_tail(d, lw, ls, &nf);
+  if (op_tail(d, lw, ls, &nf)) return -1;
+  return c->step_mode ? build_llama_step(d) : 0;
 }
 
 static int build_gpt2(Decoder *d) {
@@ -801,6 +881,11 @@ THVM_API int thvm_hip_decoder_set_state(uint32_t h, const int32_t *tokens, uint3
   Decoder *d = dec_get(h);
   if (!d) return -1;
   if (pos >= d->c.max_seq) { hb_set_error("decoder_set_state: pos %u >= max_seq %u", pos, d->c.max_seq); return -1; }
+  for (u32 b = 0; b < d->c.batch; b++)
+    if (tokens[b] < 0 || (u32)tokens[b] >= d->c.vocab) {
+      hb_set_error("decoder_set_state: token %d of row %u outside [0, %u)", tokens[b], b, d->c.vocab);
+      return -1;
+    }
   int32_t L = (int32_t)pos + 1;
   if (thvm_hip_buf_write(tens_find(d, "tok"), tokens, (u64)d->c.batch * 4)) return -1;
   if (thvm_hip_buf_write(tens_find(d, "len"), &L, 4)) return -1;
@@ -887,7 +972,7 @@ THVM_API int thvm_hip_decoder_replay(uint32_t h, uint32_t n) {
 
 THVM_API int thvm_hip_decoder_read_tokens(uint32_t h, int32_t *dst, uint32_t n) {
   Decoder *d = dec_get(h);
-  if (!d) return -1;
+  if (!d || step_status(d)) return -1;
   u32 stride = d->c.max_seq + 1;
   if (n > stride) { hb_set_error("read_tokens: n %u > %u", n, stride); return -1; }
   int32_t *tmp = (int32_t *)malloc((u64)d->c.batch * stride * 4);
@@ -901,7 +986,7 @@ THVM_API int thvm_hip_decoder_read_tokens(uint32_t h, int32_t *dst, uint32_t n) 
 
 THVM_API int thvm_hip_decoder_read_logits(uint32_t h, float *dst, uint64_t nfloats) {
   Decoder *d = dec_get(h);
-  if (!d) return -1;
+  if (!d || step_status(d)) return -1;
   u64 have = (u64)d->c.batch * d->c.vocab;
   if (nfloats > have) nfloats = have;
   return thvm_hip_buf_read(tens_find(d, "logits"), dst, nfloats * 4);
@@ -946,4 +1031,28 @@ THVM_API uint64_t thvm_hip_decoder_step_bytes(uint32_t h) {
 THVM_API uint32_t thvm_hip_decoder_step_kernels(uint32_t h) {
   Decoder *d = dec_get(h);
   return d ? d->n_ops : 0;
+}
+
+THVM_API int thvm_hip_decoder_stage_clock(uint32_t h, double *us_out, uint32_t n) {
+  Decoder *d = dec_get(h);
+  if (!d) return -1;
+  const u32 sy = tens_find(d, "step.sync");
+  if (!sy) return 0;
+  const u64 nbytes = thvm_k_step_sync_bytes();
+  uint32_t *w = (uint32_t *)malloc(nbytes);
+  if (!w) { hb_set_error("stage_clock: out of host memory"); return -1; }
+  if (thvm_hip_buf_read(sy, w, nbytes)) { free(w); return -1; }
+  /* barrier openings (5 L + 2 slots), then 4 detail events per stage
+   * (5 L + 1 stages): entry, barrier open, work done, stores drained */
+  const u32 nb = d->c.n_layers * 5 + 2, ns = d->c.n_layers * 5 + 1;
+  const u32 base = thvm_k_step_clock_word(), dbase = thvm_k_step_dclock_word();
+  const u32 slots = nb + 4 * ns;
+  const uint64_t t0 = (uint64_t)w[base] | ((uint64_t)w[base + 1] << 32);
+  for (u32 i = 0; i < slots && i < n; i++) {
+    const u32 wi = i < nb ? base + 2 * i : dbase + 2 * (i - nb);
+    const uint64_t t = (uint64_t)w[wi] | ((uint64_t)w[wi + 1] << 32);
+    us_out[i] = (double)(int64_t)(t - t0) / 100.0;   /* 100 MHz wall clock */
+  }
+  free(w);
+  return (int)slots;
 }

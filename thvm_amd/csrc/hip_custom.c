@@ -446,6 +446,58 @@ int hb_builtin_launch(const char *program, const u32 *ids, u32 n, int check_only
     if (check_only) return 0;
     if (prof) hb_kprof_begin(K, &e0, &e1);
     rc = thvm_k_rope(&a, HB_STREAM, err, sizeof err);
+  } else if (strcmp(K, "llama_step") == 0) {
+    /* the persistent LLAMA decode step; slot 0 is the per-layer table of
+     * device pointers (ThvmStepLayer[l]), built by its owner from live
+     * buffers, the other slots are checked against the shapes here */
+    ThvmStepArgs a;
+    memset(&a, 0, sizeof a);
+    NEED(spec_u32(&sp, "l", &a.n_layers, 1, 0) || spec_u32(&sp, "m", &a.M, 1, 0) ||
+         spec_u32(&sp, "d", &a.D, 1, 0) || spec_u32(&sp, "h", &a.H, 1, 0) ||
+         spec_u32(&sp, "hkv", &a.Hkv, 1, 0) || spec_u32(&sp, "hd", &a.hd, 1, 0) ||
+         spec_u32(&sp, "f", &a.F, 1, 0) || spec_u32(&sp, "v", &a.V, 1, 0) ||
+         spec_u32(&sp, "maxseq", &a.max_seq, 1, 0) || spec_u32(&sp, "wt", &a.wdt, 1, 0) ||
+         spec_u32(&sp, "at", &a.adt, 0, THVM_DT_BF16) || spec_f32(&sp, "eps", &a.eps, 1, 0) ||
+         spec_f32(&sp, "scale", &a.attn_scale, 1, 0) || spec_u32(&sp, "hstride", &a.hist_stride, 1, 0));
+    NEED(spec_u32(&sp, "nsplit", &a.n_split, 0, (a.max_seq + 63) / 64));
+    const u32 wsz = hb_dt_size(a.wdt), as = hb_dt_size(a.adt), nb = thvm_k_step_blocks();
+    const int fp8 = a.wdt == THVM_DT_FP8E4M3;
+    if (!wsz || !is_act(a.adt) || !nb) { hb_set_error("builtin llama_step: bad dtypes or no device"); return -1; }
+    const u64 hq = (u64)a.H * a.hd;
+    u32 slot = 0;
+    a.layers = (const ThvmStepLayer *)arg(&c, slot++, (u64)a.n_layers * sizeof(ThvmStepLayer));
+    a.emb = arg(&c, slot++, (u64)a.V * a.D * as);
+    a.norm_f = (const float *)arg(&c, slot++, (u64)a.D * 4);
+    a.lm = arg(&c, slot++, (u64)a.V * a.D * wsz);
+    if (fp8) a.slm = (const float *)arg(&c, slot++, (u64)a.V * 4);
+    a.rope_cos = (const float *)arg(&c, slot++, (u64)a.max_seq * (a.hd / 2) * 4);
+    a.rope_sin = (const float *)arg(&c, slot++, (u64)a.max_seq * (a.hd / 2) * 4);
+    a.tok = (int32_t *)arg(&c, slot++, (u64)a.M * 4);
+    a.len = (int32_t *)arg(&c, slot++, 4);
+    a.hist = (int32_t *)arg(&c, slot++, (u64)a.M * a.hist_stride * 4);
+    a.logits = (float *)arg(&c, slot++, (u64)a.M * a.V * 4);
+    a.x = arg(&c, slot++, (u64)a.M * a.D * as);
+    a.q = arg(&c, slot++, (u64)a.M * hq * as);
+    a.att = arg(&c, slot++, (u64)a.M * hq * as);
+    a.h = arg(&c, slot++, (u64)a.M * a.F * as);
+    a.part = (float *)arg(&c, slot++, thvm_k_attn_part_bytes(a.M, a.H, a.Hkv, a.hd, a.n_split));
+    a.am_pv = (float *)arg(&c, slot++, (u64)a.M * nb * 4);
+    a.am_pi = (int32_t *)arg(&c, slot++, (u64)a.M * nb * 4);
+    a.sync = (uint32_t *)arg(&c, slot++, thvm_k_step_sync_bytes());
+    if (c.bad) return -1;
+    {
+      /* weight (+ row scale) bytes per step: qkv, o, gate/up, down, LM head;
+       * the live KV rows are added by the caller, which knows L */
+      const u64 nqkv = (u64)(a.H + 2 * a.Hkv) * a.hd;
+      const u64 elems = nqkv * a.D + (u64)a.D * hq + 2ull * a.F * a.D + (u64)a.D * a.F;
+      const u64 rows = nqkv + a.D + 2ull * a.F + a.D;
+      bytes = (u64)a.n_layers * (elems * wsz + (fp8 ? rows * 4 : 0)) + (u64)a.V * a.D * wsz +
+              (fp8 ? (u64)a.V * 4 : 0);
+    }
+    if (thvm_k_llama_step_check(&a, err, sizeof err)) { hb_set_error("builtin llama_step: %s", err); return -1; }
+    if (check_only) return 0;
+    if (prof) hb_kprof_begin(K, &e0, &e1);
+    rc = thvm_k_llama_step(&a, HB_STREAM, err, sizeof err);
   } else if (strcmp(K, "cast") == 0) {
     u64 ne = 0;
     u32 xt = 0, yt = 0;
@@ -593,10 +645,15 @@ static hipFunction_t rtc_get(const char *name, const char *source) {
   hipModule_t mod;
   hipError_t e = hipModuleLoadData(&mod, co);
   free(co);
-  if (e != hipSuccess) { hb_set_error("hipModuleLoadData(%s): %s", name, hipGetErrorString(e)); return NULL; }
+  if (e != hipSuccess) {
+    (void)hipGetLastError();   /* handled here: do not leave it for the next launch check */
+    hb_set_error("hipModuleLoadData(%s): %s", name, hipGetErrorString(e));
+    return NULL;
+  }
   hipFunction_t fn;
   e = hipModuleGetFunction(&fn, mod, name);
   if (e != hipSuccess) {
+    (void)hipGetLastError();
     hipModuleUnload(mod);
     hb_set_error("hipModuleGetFunction(%s): %s", name, hipGetErrorString(e));
     return NULL;

@@ -218,6 +218,55 @@ typedef struct ThvmRopeArgs {
 } ThvmRopeArgs;
 int thvm_k_rope(const ThvmRopeArgs *a, hipStream_t s, char *err, int errlen);
 
+/* Persistent decode step of the LLAMA architecture: the whole step (embed,
+ * per layer RMSNorm + q|k|v + RoPE + KV append, attention, o + residual,
+ * RMSNorm + gate/up + SwiGLU, down + residual; final RMSNorm, LM head,
+ * argmax, history, L += 1) in one launch of one block per CU, the stages
+ * separated by grid barriers.  Every output equals the multi-kernel step's
+ * bit for bit (same device functions, same orders).  Per-layer weights come
+ * from a device-resident table. */
+typedef struct ThvmStepLayer {
+  const void *wqkv; const float *sqkv;   /* [(H+2Hkv)hd, D] (+ row scales)  */
+  const void *wo;   const float *so;     /* [D, H hd]                       */
+  const void *wgu;  const float *sgu;    /* [2F, D], gate/up rows interleaved */
+  const void *wd;   const float *sd;     /* [D, F]                          */
+  const float *g_attn, *g_ffn;           /* [D] RMSNorm gains               */
+  void *kcache, *vcache;                 /* [M][Hkv][max_seq][hd]           */
+} ThvmStepLayer;
+
+typedef struct ThvmStepArgs {
+  const ThvmStepLayer *layers;           /* device array [n_layers]        */
+  const void *emb;                       /* [V, D] (adt)                   */
+  const float *norm_f;                   /* [D]                            */
+  const void *lm; const float *slm;      /* [V, D] (+ row scales)          */
+  const float *rope_cos, *rope_sin;      /* [max_seq][hd/2]                */
+  int32_t *tok, *len, *hist;             /* [M], [1], [M][hist_stride]     */
+  float *logits;                         /* [M][V]                         */
+  void *x, *q, *att, *h;                 /* [M][D], [M][H hd] x2, [M][F]   */
+  float *part;                           /* attention partials             */
+  float *am_pv; int32_t *am_pi;          /* [M][thvm_k_step_blocks()]      */
+  uint32_t *sync;                        /* thvm_k_step_sync_bytes(), zeroed once */
+  uint32_t n_layers, M, D, H, Hkv, hd, F, V, max_seq, n_split, hist_stride;
+  uint32_t wdt, adt;
+  float eps, attn_scale;
+} ThvmStepArgs;
+int thvm_k_llama_step(const ThvmStepArgs *a, hipStream_t s, char *err, int errlen);
+/* grid of the persistent step (one block per CU) and its sync area bytes */
+uint32_t thvm_k_step_blocks(void);
+uint32_t thvm_k_step_sync_bytes(void);
+/* index of the sync area's error word (nonzero: a grid barrier expired) */
+uint32_t thvm_k_step_err_word(void);
+/* index of the stage clock: 64-bit wall-clock ticks (100 MHz) that block 0
+ * of the last launch recorded at its start (slot 0), at the opening of each
+ * grid barrier k (slot k + 1) and at the end of the tail (slot barriers + 1) */
+uint32_t thvm_k_step_clock_word(void);
+/* index of the detail clock: 4 events per stage (entry, barrier open, work
+ * done, stores drained) of block 0, stage id l*5 + {0 QKV, 1 ATTN, 2 O, 3 GU,
+ * 4 DOWN}, then the LM stage */
+uint32_t thvm_k_step_dclock_word(void);
+/* check a step configuration without launching (0 / -1 with *err) */
+int thvm_k_llama_step_check(const ThvmStepArgs *a, char *err, int errlen);
+
 #ifdef __cplusplus
 }
 #endif

@@ -6,6 +6,7 @@
 // residual add, an activation or the rotation.
 #pragma once
 #include "dev_common.h"
+#include "coh.h"
 #include "../kern_api.h"
 
 __device__ __forceinline__ float ld_any(const void *p, uint64_t i, uint32_t dt) {
@@ -24,12 +25,35 @@ __device__ __forceinline__ void st_any(void *p, uint64_t i, uint32_t dt, float v
     default: break;
   }
 }
+// COH: system-scope accesses (buffers shared between the blocks of one
+// launch); byte offsets stay below 2 GiB
+template <bool COH>
+__device__ __forceinline__ float ld_anyc(const void *p, uint64_t i, uint32_t dt) {
+  if (!COH) return ld_any(p, i, dt);
+  switch (dt) {
+    case THVM_DT_FP32: return coh_ldf(p, (uint32_t)(i * 4));
+    case THVM_DT_BF16: return bf2f(coh_ld2(p, (uint32_t)(i * 2)));
+    case THVM_DT_FP16: return h2f(coh_ld2(p, (uint32_t)(i * 2)));
+    default: return 0.0f;
+  }
+}
+template <bool COH>
+__device__ __forceinline__ void st_anyc(void *p, uint64_t i, uint32_t dt, float v) {
+  if (!COH) { st_any(p, i, dt, v); return; }
+  switch (dt) {
+    case THVM_DT_FP32: coh_stf(p, (uint32_t)(i * 4), v); break;
+    case THVM_DT_BF16: coh_st2(p, (uint32_t)(i * 2), f2bf(v)); break;
+    case THVM_DT_FP16: coh_st2(p, (uint32_t)(i * 2), f2h(v)); break;
+    default: break;
+  }
+}
 __device__ __forceinline__ float rnd_any(float v, uint32_t dt) {
   return dt == THVM_DT_BF16 ? rbf(v) : dt == THVM_DT_FP16 ? rh(v) : v;
 }
 
 // Rows n0..n0+R-1 of batch rows mb..mb+M-1; tot[r][m] is the raw f32 sum.
-template <int R, int M>
+// COH: y, res and the caches are read/written with system-scope accesses.
+template <int R, int M, bool COH = false>
 __device__ __forceinline__ void gemv_epilogue(const ThvmGemvArgs &a, const uint32_t n0,
                                               const float (&tot)[R][M],
                                               const uint32_t mb = 0) {
@@ -51,7 +75,7 @@ __device__ __forceinline__ void gemv_epilogue(const ThvmGemvArgs &a, const uint3
         if (n0 + r < N)
 #pragma unroll
           for (int m = 0; m < M; m++)
-            st_any(a.y, (uint64_t)(mb + m) * a.ldy + n0 + r, ydt, v[r][m]);
+            st_anyc<COH>(a.y, (uint64_t)(mb + m) * a.ldy + n0 + r, ydt, v[r][m]);
       break;
     case THVM_EPI_RESID:
 #pragma unroll
@@ -60,8 +84,8 @@ __device__ __forceinline__ void gemv_epilogue(const ThvmGemvArgs &a, const uint3
 #pragma unroll
           for (int m = 0; m < M; m++) {
             uint64_t i = (uint64_t)(mb + m) * a.ldy + n0 + r;
-            float rv = ld_any(a.res, i, ydt);
-            st_any(a.y, i, ydt, rv + rnd_any(v[r][m], ydt));
+            float rv = ld_anyc<COH>(a.res, i, ydt);
+            st_anyc<COH>(a.y, i, ydt, rv + rnd_any(v[r][m], ydt));
           }
       break;
     case THVM_EPI_GELU:
@@ -70,7 +94,7 @@ __device__ __forceinline__ void gemv_epilogue(const ThvmGemvArgs &a, const uint3
         if (n0 + r < N)
 #pragma unroll
           for (int m = 0; m < M; m++)
-            st_any(a.y, (uint64_t)(mb + m) * a.ldy + n0 + r, ydt,
+            st_anyc<COH>(a.y, (uint64_t)(mb + m) * a.ldy + n0 + r, ydt,
                    gelu_tanh_f(rnd_any(v[r][m], ydt)));
       break;
     case THVM_EPI_SWIGLU:
@@ -81,7 +105,7 @@ __device__ __forceinline__ void gemv_epilogue(const ThvmGemvArgs &a, const uint3
 #pragma unroll
           for (int m = 0; m < M; m++) {
             float gg = rnd_any(v[r][m], ydt), uu = rnd_any(v[r + 1][m], ydt);
-            st_any(a.y, (uint64_t)(mb + m) * a.ldy + (n0 + r) / 2, ydt, silu_f(gg) * uu);
+            st_anyc<COH>(a.y, (uint64_t)(mb + m) * a.ldy + (n0 + r) / 2, ydt, silu_f(gg) * uu);
           }
         }
       }
@@ -110,16 +134,16 @@ __device__ __forceinline__ void gemv_epilogue(const ThvmGemvArgs &a, const uint3
           float oe = xe, oo = xo;
           if (rope && nn < Hq + Hk) { oe = xe * c - xo * sn; oo = xo * c + xe * sn; }
           if (nn < Hq) {
-            st_any(a.y, (uint64_t)(mb + m) * a.ldy + nn, ydt, oe);
-            st_any(a.y, (uint64_t)(mb + m) * a.ldy + nn + 1, ydt, oo);
+            st_anyc<COH>(a.y, (uint64_t)(mb + m) * a.ldy + nn, ydt, oe);
+            st_anyc<COH>(a.y, (uint64_t)(mb + m) * a.ldy + nn + 1, ydt, oo);
           } else {
             const bool isk = nn < Hq + Hk;
             const uint32_t off = isk ? nn - Hq : nn - Hq - Hk;
             const uint32_t h = off / hd;
             uint64_t ci = (((uint64_t)(mb + m) * a.n_kv_heads + h) * a.max_seq + (uint32_t)pos) * hd + d;
             void *cache = isk ? a.kcache : a.vcache;
-            st_any(cache, ci, ydt, oe);
-            st_any(cache, ci + 1, ydt, oo);
+            st_anyc<COH>(cache, ci, ydt, oe);
+            st_anyc<COH>(cache, ci + 1, ydt, oo);
           }
         }
       }

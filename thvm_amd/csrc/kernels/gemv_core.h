@@ -1,0 +1,397 @@
+// gemv_core.h -- the decode projection y[m,n] = sum_k x[m,k] W[n,k] as a
+// block-level device function, shared by the standalone GEMV kernel
+// (gemv.hip) and the persistent decode step (step.hip), so both compute every
+// output row with the same instructions in the same order.
+//
+// W is [N, K] with K contiguous, in f32 / fp16 / bf16 / fp8-e4m3 (+ per-row
+// f32 scale), M in 1..4 rows of x, fp32 accumulation:
+//   * one wave64 owns R consecutive rows and streams them with 128-bit loads
+//     (lane l takes 16-byte chunks l, l+64, ..), U chunks per row in flight
+//     per lane before any arithmetic;
+//   * the first batch of weight loads is issued BEFORE x is staged -- and, in
+//     the persistent kernel, before the grid barrier that makes x valid -- so
+//     the staging (and a fused norm's block reduction) hides under HBM
+//     latency; the next batch is prefetched while the current one is consumed;
+//   * x (M rows) is staged once per block into LDS in its storage type, chunk-
+//     swizzled so the 64 lanes' 16-byte LDS reads hit distinct banks; a fused
+//     RMSNorm / LayerNorm writes the normalised row there already rounded to
+//     the activation dtype, exactly as the separate norm kernel would store it;
+//   * fp8 decodes with v_cvt_pk_f32_fp8 (OCP e4m3, exact); the per-row scale
+//     is applied once after the reduction;
+//   * each row's K reduction ends in a DPP wave reduction (fixed order,
+//     deterministic): no partial buffer and no second fold kernel.
+// A row's sum depends only on the chunk order of its lanes, not on which wave,
+// block or launch computes it.
+#pragma once
+#include "dev_common.h"
+#include "coh.h"
+#include "../kern_api.h"
+#include "epilogue.h"
+
+enum { WT_F32 = 0, WT_F16 = 1, WT_BF16 = 2, WT_FP8 = 3 };
+enum { XT_BF16 = 0, XT_F16 = 1, XT_F32 = 2 };
+
+template <int WT> struct WTr;
+template <> struct WTr<WT_F32>  { static constexpr int E = 4;  };
+template <> struct WTr<WT_F16>  { static constexpr int E = 8;  };
+template <> struct WTr<WT_BF16> { static constexpr int E = 8;  };
+template <> struct WTr<WT_FP8>  { static constexpr int E = 16; };
+
+// decode the 4 elements of quad j of a 16-byte weight chunk
+template <int WT>
+__device__ __forceinline__ void quad_decode(const uint4 &q, int j, float o[4]);
+
+template <>
+__device__ __forceinline__ void quad_decode<WT_FP8>(const uint4 &q, int j, float o[4]) {
+  uint32_t w = j == 0 ? q.x : j == 1 ? q.y : j == 2 ? q.z : q.w;
+  fp8x4_to_f32(w, o);
+}
+template <>
+__device__ __forceinline__ void quad_decode<WT_F16>(const uint4 &q, int j, float o[4]) {
+  uint32_t a = j == 0 ? q.x : q.z, b = j == 0 ? q.y : q.w;
+  o[0] = h2f((f16_t)(a & 0xffffu)); o[1] = h2f((f16_t)(a >> 16));
+  o[2] = h2f((f16_t)(b & 0xffffu)); o[3] = h2f((f16_t)(b >> 16));
+}
+template <>
+__device__ __forceinline__ void quad_decode<WT_BF16>(const uint4 &q, int j, float o[4]) {
+  uint32_t a = j == 0 ? q.x : q.z, b = j == 0 ? q.y : q.w;
+  o[0] = __uint_as_float(a << 16); o[1] = __uint_as_float(a & 0xffff0000u);
+  o[2] = __uint_as_float(b << 16); o[3] = __uint_as_float(b & 0xffff0000u);
+}
+template <>
+__device__ __forceinline__ void quad_decode<WT_F32>(const uint4 &q, int j, float o[4]) {
+  (void)j;
+  o[0] = __uint_as_float(q.x); o[1] = __uint_as_float(q.y);
+  o[2] = __uint_as_float(q.z); o[3] = __uint_as_float(q.w);
+}
+
+// ---- LDS x layout -----------------------------------------------------------
+// 16-bit x: element e of row m lives at halfword  m*K + ((e%E)/8 * C + e/E)*8 + e%8
+// f32 x:    element e of row m lives at float     m*K + ((e%E)/4 * C + e/E)*4 + e%4
+// (C = K/E chunks per row): the 8 (or 4) elements a lane needs for one quad
+// pair are one aligned 16-byte LDS word, and lanes c, c+1 read adjacent words.
+template <int XT> struct XTr;
+template <> struct XTr<XT_BF16> { static constexpr int B = 2, G = 8; };
+template <> struct XTr<XT_F16>  { static constexpr int B = 2, G = 8; };
+template <> struct XTr<XT_F32>  { static constexpr int B = 4, G = 4; };
+
+template <int XT, int E>
+__device__ __forceinline__ uint32_t xs_index(uint32_t K, uint32_t C, uint32_t m, uint32_t e) {
+  constexpr int G = XTr<XT>::G;
+  const uint32_t c = e / E, r = e - c * E;
+  return m * K + ((r / G) * C + c) * G + (r % G);
+}
+
+// 8 x elements of a 16-bit group -> floats
+template <int XT>
+__device__ __forceinline__ void x8_decode(const uint4 &q, float o[8]) {
+  uint32_t w[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    if (XT == XT_BF16) {
+      o[2 * i] = __uint_as_float(w[i] << 16);
+      o[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
+    } else {
+      o[2 * i] = h2f((f16_t)(w[i] & 0xffffu));
+      o[2 * i + 1] = h2f((f16_t)(w[i] >> 16));
+    }
+  }
+}
+
+template <int XT>
+__device__ __forceinline__ void xs_store(void *xs, uint32_t idx, float v) {
+  if (XT == XT_BF16) ((bf16_t *)xs)[idx] = f2bf(v);
+  else if (XT == XT_F16) ((f16_t *)xs)[idx] = f2h(v);
+  else ((float *)xs)[idx] = v;
+}
+
+__device__ __forceinline__ float block_sum_g(float v, float *red, int nwaves) {
+  float w = wave_sum(v);
+  __syncthreads();
+  if (lane_id() == 0) red[threadIdx.x >> 6] = w;
+  __syncthreads();
+  float t = 0.0f;
+  for (int i = 0; i < nwaves; i++) t += red[i];
+  return t;
+}
+
+#define GEMV_MAX_WAVES 16
+#define XREG 16   /* x elements per thread kept in registers by the staging */
+
+// the output stage of one row group (one lane, wave-uniform values)
+// input x dtype (compile time): vector loads of 16 bytes
+enum { XD_BF16 = 0, XD_F16 = 1, XD_F32 = 2 };
+template <int XD> struct XDr { static constexpr int VE = XD == XD_F32 ? 4 : 8, B = XD == XD_F32 ? 4 : 2; };
+
+// 16 bytes of x at element e of the row at x (COH: a system-scope load, for
+// rows written by other blocks of the same launch)
+template <int XD, bool COH = false>
+__device__ __forceinline__ void xvec(const void *x, uint64_t e, float *o) {
+  const uint4 q = COH ? coh_ld16(x, (uint32_t)(e * XDr<XD>::B)) : ld16((const char *)x + e * XDr<XD>::B);
+  const uint32_t w[4] = {q.x, q.y, q.z, q.w};
+  if (XD == XD_F32) {
+#pragma unroll
+    for (int i = 0; i < 4; i++) o[i] = __uint_as_float(w[i]);
+  } else {
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      if (XD == XD_BF16) {
+        o[2 * i] = __uint_as_float(w[i] << 16);
+        o[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
+      } else {
+        o[2 * i] = h2f((f16_t)(w[i] & 0xffffu));
+        o[2 * i + 1] = h2f((f16_t)(w[i] >> 16));
+      }
+    }
+  }
+}
+template <int XD>
+__device__ __forceinline__ float rnd_x(float v) {
+  return XD == XD_BF16 ? rbf(v) : XD == XD_F16 ? rh(v) : v;
+}
+
+// One block's share of a GEMV.  The calling wave owns row groups g, g +
+// gstride, ...; `wait()` runs after the first weight batch is in flight and
+// before x is read (return false to abandon the call); `xrow(m)` gives the
+// start of x row m; `hook(n0, tot)` runs on lane 0 after each row group's
+// epilogue with the raw sums.  COH selects system-scope x loads and epilogue
+// accesses (data shared between the blocks of one launch).  x staging uses
+// the first nthr threads (nw = nthr / 64 waves reduce a fused norm); the rest
+// of the block only joins its barriers.  Returns false when wait() did.
+template <int WT, int XD, int M, int R, int U, bool COH, class WaitF, class XRowF, class HookF>
+__device__ __forceinline__ bool gemv_core(const ThvmGemvArgs &a, unsigned char *xs_raw, float *red,
+                                          const uint32_t g, const uint32_t gstride,
+                                          const uint32_t nthr, const int nw, WaitF &&wait,
+                                          XRowF &&xrow, HookF &&hook) {
+  constexpr int E = WTr<WT>::E;
+  // LDS keeps x in its 16-bit storage type unless weights or x are f32
+  constexpr int XT = (WT == WT_F32 || XD == XD_F32) ? XT_F32 : (XD == XD_BF16 ? XT_BF16 : XT_F16);
+  constexpr int VE = XDr<XD>::VE;
+  const uint32_t K = a.K, N = a.N;
+  const uint32_t C = K / E;              // 16-byte weight chunks per row
+  const int lane = lane_id();
+  const uint32_t G = (N + R - 1) / R;
+  const uint64_t rowbytes = (uint64_t)K * (16 / E);
+  const char *wb = (const char *)a.w;
+
+  // ---- 1. first weight batch in flight before anything else ----
+  uint4 wq[R][U];
+  auto load_batch = [&](uint32_t gg, uint32_t c0) {
+    const uint32_t n0 = gg * R;
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+      const bool rok = gg < G && (n0 + r) < N;
+      const char *rp = wb + (uint64_t)(n0 + r) * rowbytes;
+#pragma unroll
+      for (int u = 0; u < U; u++) {
+        const uint32_t c = c0 + u * 64 + lane;
+        if (rok && c < C) wq[r][u] = ld_stream16(rp + (uint64_t)c * 16);
+        else wq[r][u] = make_uint4(0, 0, 0, 0);
+      }
+    }
+  };
+  // (in a persistent kernel, wave 0 polls the grid barrier inside wait():
+  // its own loads are issued after the wait, so the poll does not queue
+  // behind them)
+  const bool early = !COH || (threadIdx.x >> 6) != 0;
+  if (early) load_batch(g, 0);
+  if (!wait()) return false;
+  if (!early) load_batch(g, 0);
+
+  // ---- 2. stage x into LDS (16-byte loads), with the fused norm if asked ----
+  // (with a fused norm, threads at or beyond nthr take no part in the staging
+  // but join its block barriers: the norm's reduction order is that of an
+  // nthr-thread block)
+  const uint32_t NVt = K / VE;           // x vectors per row
+  const uint32_t tid = threadIdx.x < nthr ? threadIdx.x : NVt;
+  for (int m = 0; m < M; m++) {
+    const void *xr = xrow(m);
+    if (a.norm == 0) {
+      // no reduction: every thread of the block stages, XN vectors of x in
+      // flight per thread before the first LDS store
+      constexpr int XN = 4;
+      for (uint32_t v0 = threadIdx.x; v0 < NVt; v0 += XN * blockDim.x) {
+        float f[XN][VE];
+#pragma unroll
+        for (int j = 0; j < XN; j++) {
+          const uint32_t v = v0 + j * blockDim.x;
+          if (v < NVt) xvec<XD, COH>(xr, (uint64_t)v * VE, f[j]);
+        }
+#pragma unroll
+        for (int j = 0; j < XN; j++) {
+          const uint32_t v = v0 + j * blockDim.x;
+          if (v < NVt) {
+#pragma unroll
+            for (int i = 0; i < VE; i++) xs_store<XT>(xs_raw, xs_index<XT, E>(K, C, m, v * VE + i), f[j][i]);
+          }
+        }
+      }
+    } else {
+      constexpr int NV = XREG / VE;
+      float xv[NV][VE];
+#pragma unroll
+      for (int j = 0; j < NV; j++) {
+        const uint32_t v = tid + j * nthr;
+        if (v < NVt) xvec<XD, COH>(xr, (uint64_t)v * VE, xv[j]);
+        else {
+#pragma unroll
+          for (int i = 0; i < VE; i++) xv[j][i] = 0.0f;
+        }
+      }
+      const float invK = 1.0f / (float)K;
+      float mean = 0.0f, s1 = 0.0f, s2 = 0.0f;
+      if (a.norm == 2) {
+#pragma unroll
+        for (int j = 0; j < NV; j++)
+#pragma unroll
+          for (int i = 0; i < VE; i++) s1 += xv[j][i];
+        mean = block_sum_g(s1, red, nw) * invK;
+      }
+#pragma unroll
+      for (int j = 0; j < NV; j++) {
+        const bool vok = tid + j * nthr < NVt;
+#pragma unroll
+        for (int i = 0; i < VE; i++) {
+          const float d = xv[j][i] - mean;
+          s2 += vok ? d * d : 0.0f;
+        }
+      }
+      const float inv = 1.0f / sqrtf(block_sum_g(s2, red, nw) * invK + a.norm_eps);
+#pragma unroll
+      for (int j = 0; j < NV; j++) {
+        const uint32_t v = tid + j * nthr;
+        if (v < NVt) {
+          float gw[VE], gb[VE];
+#pragma unroll
+          for (int i = 0; i < VE; i += 4) {
+            float4 t = a.norm_w ? *(const float4 *)(a.norm_w + v * VE + i) : make_float4(1.f, 1.f, 1.f, 1.f);
+            gw[i] = t.x; gw[i + 1] = t.y; gw[i + 2] = t.z; gw[i + 3] = t.w;
+            float4 u = (a.norm == 2 && a.norm_b) ? *(const float4 *)(a.norm_b + v * VE + i)
+                                                 : make_float4(0.f, 0.f, 0.f, 0.f);
+            gb[i] = u.x; gb[i + 1] = u.y; gb[i + 2] = u.z; gb[i + 3] = u.w;
+          }
+#pragma unroll
+          for (int i = 0; i < VE; i++) {
+            // (x - mean) * inv * w (+ b), the norm kernel's own formula
+            float val = (xv[j][i] - mean) * inv;
+            if (a.norm_w) val = val * gw[i];
+            if (a.norm == 2 && a.norm_b) val = val + gb[i];
+            xs_store<XT>(xs_raw, xs_index<XT, E>(K, C, m, v * VE + i), rnd_x<XD>(val));
+          }
+        }
+      }
+    }
+  }
+  __syncthreads();
+
+  // ---- 3. stream the weight rows ----
+  // A flat sequence of (row group, chunk batch) steps per wave; two register
+  // sets ping-pong so the next batch is in flight while one is consumed (the
+  // wait before a consume covers only the older batch's loads).
+  const uint32_t NB = (C + 64 * U - 1) / (64 * U);      // batches per row group
+  const uint32_t g0 = g;
+  const uint32_t ngw = g0 < G ? (G - 1 - g0) / gstride + 1 : 0;
+  const uint32_t T = ngw * NB;
+  float acc[R][M];
+#pragma unroll
+  for (int r = 0; r < R; r++)
+#pragma unroll
+    for (int m = 0; m < M; m++) acc[r][m] = 0.0f;
+
+  auto consume = [&](const uint4 (&X)[R][U], uint32_t t) {
+    const uint32_t gi = t / NB, bi = t - gi * NB;
+    const uint32_t c0 = bi * 64 * U;
+#pragma unroll
+    for (int u = 0; u < U; u++) {
+      const uint32_t c = c0 + u * 64 + lane;
+      if (c < C) {
+        if (XT == XT_F32) {
+#pragma unroll
+          for (int j = 0; j < E / 4; j++) {
+            float4 xv[M];
+#pragma unroll
+            for (int m = 0; m < M; m++)
+              xv[m] = *(const float4 *)((const float *)xs_raw + m * K + (j * C + c) * 4);
+#pragma unroll
+            for (int r = 0; r < R; r++) {
+              float wf[4];
+              quad_decode<WT>(X[r][u], j, wf);
+#pragma unroll
+              for (int m = 0; m < M; m++) {
+                acc[r][m] += xv[m].x * wf[0];
+                acc[r][m] += xv[m].y * wf[1];
+                acc[r][m] += xv[m].z * wf[2];
+                acc[r][m] += xv[m].w * wf[3];
+              }
+            }
+          }
+        } else {
+#pragma unroll
+          for (int h = 0; h < (E + 7) / 8; h++) {     // 8-element x groups
+            float xf[M][8];
+#pragma unroll
+            for (int m = 0; m < M; m++) {
+              uint4 q = *(const uint4 *)((const uint16_t *)xs_raw + m * K + (h * C + c) * 8);
+              x8_decode<XT>(q, xf[m]);
+            }
+#pragma unroll
+            for (int jj = 0; jj < 2 && (h * 2 + jj) < E / 4; jj++) {
+              const int j = h * 2 + jj;
+#pragma unroll
+              for (int r = 0; r < R; r++) {
+                float wf[4];
+                quad_decode<WT>(X[r][u], j, wf);
+#pragma unroll
+                for (int m = 0; m < M; m++) {
+                  acc[r][m] += xf[m][jj * 4 + 0] * wf[0];
+                  acc[r][m] += xf[m][jj * 4 + 1] * wf[1];
+                  acc[r][m] += xf[m][jj * 4 + 2] * wf[2];
+                  acc[r][m] += xf[m][jj * 4 + 3] * wf[3];
+                }
+              }
+            }
+          }
+        }
+      }
+    }
+    if (bi == NB - 1) {
+      float tot[R][M];
+#pragma unroll
+      for (int r = 0; r < R; r++)
+#pragma unroll
+        for (int m = 0; m < M; m++) {
+          tot[r][m] = wave_sum(acc[r][m]);
+          acc[r][m] = 0.0f;
+        }
+      if (lane == 0) {
+        const uint32_t n0 = (g0 + gi * gstride) * R;
+        gemv_epilogue<R, M, COH>(a, n0, tot);
+        hook(n0, tot);
+      }
+    }
+  };
+  auto load_step = [&](uint4 (&X)[R][U], uint32_t t) {
+    const uint32_t gi = t / NB, bi = t - gi * NB;
+    const uint32_t gg = g0 + gi * gstride, n0 = gg * R, c0 = bi * 64 * U;
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+      const bool rok = gg < G && (n0 + r) < N;
+      const char *rp = wb + (uint64_t)(n0 + r) * rowbytes;
+#pragma unroll
+      for (int u = 0; u < U; u++) {
+        const uint32_t c = c0 + u * 64 + lane;
+        if (rok && c < C) X[r][u] = ld_stream16(rp + (uint64_t)c * 16);
+        else X[r][u] = make_uint4(0, 0, 0, 0);
+      }
+    }
+  };
+  uint4 wq2[R][U];
+  for (uint32_t t = 0; t < T; t += 2) {          // step 0 is already in wq
+    if (t + 1 < T) load_step(wq2, t + 1);
+    consume(wq, t);
+    if (t + 1 >= T) break;
+    if (t + 2 < T) load_step(wq, t + 2);
+    consume(wq2, t + 1);
+  }
+  return true;
+}

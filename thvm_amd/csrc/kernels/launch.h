@@ -11,6 +11,9 @@
 template <typename F, typename... Args>
 static inline void thvm_launch(bool first, bool last, F f, dim3 grid, dim3 block,
                                uint32_t shared, hipStream_t s, Args... args) {
+  // the launchers check hipGetLastError() after their launches: drop a stale
+  // error an earlier, already handled runtime call left behind
+  if (first) (void)hipGetLastError();
   hipEvent_t e0 = first ? thvm_k_take_start() : nullptr;
   hipEvent_t e1 = last ? thvm_k_take_stop() : nullptr;
   if (e0 || e1)

@@ -349,6 +349,7 @@ __global__ void k_delay(uint32_t n) {
 }
 extern "C" int thvm_k_delay(uint32_t n, hipStream_t s, char *err, int errlen) {
   if (n > 200000) { snprintf(err, errlen, "delay: %u periods exceed the 200000 cap", n); return -1; }
+  (void)hipGetLastError();   // drop a stale, already handled error
   hipLaunchKernelGGL(k_delay, dim3(1), dim3(64), 0, s, n);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) { snprintf(err, errlen, "delay launch: %s", hipGetErrorString(e)); return -1; }
@@ -366,6 +367,7 @@ extern "C" int thvm_k_cast(void *y, uint32_t ydt, const void *x, uint32_t xdt, u
   bool okx = act_dt(xdt) || xdt == THVM_DT_FP8E4M3, oky = act_dt(ydt) || ydt == THVM_DT_FP8E4M3;
   if (!okx || !oky) { snprintf(err, errlen, "cast: unsupported dtypes"); return -1; }
   if (n == 0) return 0;
+  (void)hipGetLastError();   // drop a stale, already handled error
   hipLaunchKernelGGL(k_cast, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, y, ydt, x, xdt, n);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) { snprintf(err, errlen, "cast launch: %s", hipGetErrorString(e)); return -1; }
@@ -427,6 +429,7 @@ extern "C" int thvm_k_fill_normal(void *dst, uint32_t dt, uint64_t n, uint64_t s
   if (n == 0) return 0;
   uint64_t blocks = (n + 255) / 256;
   if (blocks > 65536) blocks = 65536;
+  (void)hipGetLastError();   // drop a stale, already handled error
   hipLaunchKernelGGL(k_fill_normal, dim3((unsigned)blocks), dim3(256), 0, s, dst, dt, n, seed, tag,
                      mean, std);
   hipError_t e = hipGetLastError();
@@ -461,6 +464,7 @@ extern "C" int thvm_k_fill_fp8_rows(uint8_t *q, float *scale, uint32_t rows, uin
                                     char *err, int errlen) {
   if (rows == 0 || cols == 0) return 0;
   uint32_t blocks = rows < 8192 ? rows : 8192;
+  (void)hipGetLastError();   // drop a stale, already handled error
   hipLaunchKernelGGL(k_fill_fp8_rows, dim3(blocks), dim3(256), 0, s, q, scale, rows, cols, seed,
                      tag, std);
   hipError_t e = hipGetLastError();
@@ -490,6 +494,7 @@ extern "C" int thvm_k_fill_cache(void *cache, uint32_t dt, uint32_t B, uint32_t 
   if (n == 0) return 0;
   uint64_t blocks = (n + 255) / 256;
   if (blocks > 65536) blocks = 65536;
+  (void)hipGetLastError();   // drop a stale, already handled error
   hipLaunchKernelGGL(k_fill_cache, dim3((unsigned)blocks), dim3(256), 0, s, cache, dt, B, Hkv,
                      max_seq, hd, ctx, seed, tag);
   hipError_t e = hipGetLastError();
