@@ -196,7 +196,14 @@ static int cfg_check(const ThvmDecodeConfig *c) {
       hb_set_error("decoder: zero dimension in DSV2 config");
       return -1;
     }
-    if (c->batch > 4) { hb_set_error("decoder: DSV2 decodes batches of up to 4 rows in this build"); return -1; }
+    if (c->batch > 64 || (c->batch > 4 && c->batch % 4)) {
+      hb_set_error("decoder: DSV2 batch %u (1..4, or a multiple of 4 up to 64)", c->batch);
+      return -1;
+    }
+    if (c->batch > 4 && (c->dim % 64 || (c->n_heads * c->d_v) % 64 || (c->first_dense && c->ffn % 64))) {
+      hb_set_error("decoder: DSV2 batch above 4 runs the MFMA GEMM: dim, heads*d_v and ffn multiples of 64");
+      return -1;
+    }
     if (c->wdtype != THVM_DT_FP8E4M3 && c->wdtype != THVM_DT_BF16) {
       hb_set_error("decoder: DSV2 weights must be fp8 e4m3 or bf16");
       return -1;
@@ -703,6 +710,13 @@ static int build_dsv2(Decoder *d) {
       !tens_new(d, "h", THVM_DT_BF16, (u64)B * (F ? F : 1) * 2) ||
       !tens_new(d, "mla.part", THVM_DT_FP32, thvm_k_mla_part_bytes(B, H, kv, d->n_split)))
     return -1;
+  /* batches above 4 rows: expert-grouped MoE scratch and its live-expert
+   * counter; projections on the MFMA GEMM (bf16 inputs from separate norms) */
+  const int grp = B > 4;
+  if (grp && (!tens_new(d, "moe.plan", THVM_DT_INT32, thvm_k_moe_plan_bytes(B, E, K)) ||
+              !tens_new(d, "moe.part", THVM_DT_FP32, thvm_k_moe_part_bytes(B, K, D)) ||
+              !tens_new(d, "moe.live", THVM_DT_INT32, 4)))
+    return -1;
   if (!weight_normal(d, "emb", THVM_DT_BF16, (u64)V * D, 0.0f, c->init_std)) return -1;
   if (rope_tables_yarn(d) || !weight_const(d, "norm_f", D, 1.0f)) return -1;
   char p[512], nm[48];
@@ -830,32 +844,35 @@ static int build_dsv2(Decoder *d) {
     snprintf(p, sizeof p, "thvm-builtin:route b=%u e=%u k=%u", B, E, K);
     u32 rb[3] = {sel, probs, gl};
     if (op_add(d, "route", p, rb, 3)) return -1;
-    snprintf(p, sizeof p, "thvm-builtin:moe_gateup b=%u d=%u e=%u k=%u i=%u s=%u wt=%u", B, D, E, K, I,
-             S, wdt);
-    u32 ma[8], mn = 0;
+    snprintf(p, sizeof p, "thvm-builtin:moe_gateup b=%u d=%u e=%u k=%u i=%u s=%u wt=%u grouped=%d", B, D,
+             E, K, I, S, wdt, grp);
+    u32 ma[10], mn = 0;
     ma[mn++] = hmoe; ma[mn++] = xnf; ma[mn++] = sel; ma[mn++] = wgue;
     if (f8) ma[mn++] = sgue;
     if (S) { ma[mn++] = wgus; if (f8) ma[mn++] = sgus; }
+    if (grp) { ma[mn++] = tens_find(d, "moe.plan"); ma[mn++] = tens_find(d, "moe.live"); }
     if (op_add(d, "moe_gateup", p, ma, mn)) return -1;
-    snprintf(p, sizeof p, "thvm-builtin:moe_down b=%u d=%u e=%u k=%u i=%u s=%u wt=%u", B, D, E, K, I, S,
-             wdt);
-    u32 mb[9], mbn = 0;
+    snprintf(p, sizeof p, "thvm-builtin:moe_down b=%u d=%u e=%u k=%u i=%u s=%u wt=%u grouped=%d", B, D, E,
+             K, I, S, wdt, grp);
+    u32 mb[11], mbn = 0;
     mb[mbn++] = x; mb[mbn++] = hmoe; mb[mbn++] = sel; mb[mbn++] = probs; mb[mbn++] = wde;
     if (f8) mb[mbn++] = sde;
     if (S) { mb[mbn++] = wds; if (f8) mb[mbn++] = sds; }
+    if (grp) { mb[mbn++] = tens_find(d, "moe.plan"); mb[mbn++] = tens_find(d, "moe.part"); }
     if (op_add(d, "moe_down", p, mb, mbn)) return -1;
   }
-  /* final norm in f32 (rms_f) -> LM head */
+  /* final norm in f32 (rms_f) -> LM head; batches above 4 rows feed the
+   * MFMA GEMM, which takes 16-bit x: their normed rows are rounded to bf16 */
   u32 lw, ls;
   if (weight_matrix(d, "lm", V, D, &lw, &ls)) return -1;
-  snprintf(p, sizeof p, "thvm-builtin:norm m=%u k=%u xt=%u yt=%u eps=%a", B, D, THVM_DT_BF16,
-           THVM_DT_FP32, c->eps);
-  u32 fa[3] = {xnf, x, tens_find(d, "norm_f")};
+  const u32 lmx = grp ? tens_find(d, "xn") : xnf, lmt = grp ? THVM_DT_BF16 : THVM_DT_FP32;
+  snprintf(p, sizeof p, "thvm-builtin:norm m=%u k=%u xt=%u yt=%u eps=%a", B, D, THVM_DT_BF16, lmt, c->eps);
+  u32 fa[3] = {lmx, x, tens_find(d, "norm_f")};
   if (op_add(d, "norm_f", p, fa, 3)) return -1;
-  snprintf(p, sizeof p, "thvm-builtin:gemv m=%u n=%u k=%u wt=%u xt=%u yt=%u epi=0", B, V, D, wdt,
-           THVM_DT_FP32, THVM_DT_FP32);
+  snprintf(p, sizeof p, "thvm-builtin:gemv m=%u n=%u k=%u wt=%u xt=%u yt=%u epi=0", B, V, D, wdt, lmt,
+           THVM_DT_FP32);
   u32 la[4], ln = 0;
-  la[ln++] = tens_find(d, "logits"); la[ln++] = xnf; la[ln++] = lw;
+  la[ln++] = tens_find(d, "logits"); la[ln++] = lmx; la[ln++] = lw;
   if (f8) la[ln++] = ls;
   if (op_add(d, "lm_head", p, la, ln)) return -1;
   const u32 nb = V >= 256 * 64 ? 256 : (V + 63) / 64;

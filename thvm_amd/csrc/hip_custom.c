@@ -336,7 +336,7 @@ int hb_builtin_launch(const char *program, const u32 *ids, u32 n, int check_only
     NEED(spec_u32(&sp, "b", &a.B, 1, 0) || spec_u32(&sp, "d", &a.D, 1, 0) ||
          spec_u32(&sp, "e", &a.E, 1, 0) || spec_u32(&sp, "k", &a.K, 1, 0) ||
          spec_u32(&sp, "i", &a.I, 1, 0) || spec_u32(&sp, "s", &a.S, 0, 0) ||
-         spec_u32(&sp, "wt", &a.wdt, 0, THVM_DT_FP8E4M3));
+         spec_u32(&sp, "wt", &a.wdt, 0, THVM_DT_FP8E4M3) || spec_u32(&sp, "grouped", &a.grouped, 0, 0));
     const u32 wsz = hb_dt_size(a.wdt);
     const int fp8 = a.wdt == THVM_DT_FP8E4M3;
     if (!wsz) { hb_set_error("builtin %s: bad weight dtype", K); return -1; }
@@ -353,6 +353,11 @@ int hb_builtin_launch(const char *program, const u32 *ids, u32 n, int check_only
         if (fp8) a.sgu_s = (const float *)arg(&c, slot++, (u64)2 * a.S * 4);
       }
       bytes = (u64)a.B * ((u64)a.K * 2 * a.I + 2 * a.S) * a.D * wsz + hb;
+      if (a.grouped) {   /* plan scratch, then the live-expert counter it adds to */
+        a.plan = (int32_t *)arg(&c, slot++, thvm_k_moe_plan_bytes(a.B, a.E, a.K));
+        a.live = (int32_t *)arg(&c, slot++, 4);
+        bytes = 0;       /* the experts streamed are known on the device only (live) */
+      }
     } else {
       a.res = arg(&c, slot++, (u64)a.B * a.D * 2);
       a.h = (float *)arg(&c, slot++, hb);
@@ -365,6 +370,11 @@ int hb_builtin_launch(const char *program, const u32 *ids, u32 n, int check_only
         if (fp8) a.sd_s = (const float *)arg(&c, slot++, (u64)a.D * 4);
       }
       bytes = (u64)a.B * ((u64)a.K * a.I + a.S) * a.D * wsz + hb + (u64)a.B * a.D * 4;
+      if (a.grouped) {   /* the gate/up's plan, then the per-slot down outputs */
+        a.plan = (int32_t *)arg(&c, slot++, thvm_k_moe_plan_bytes(a.B, a.E, a.K));
+        a.part = (float *)arg(&c, slot++, thvm_k_moe_part_bytes(a.B, a.K, a.D));
+        bytes = 0;
+      }
     }
     if (c.bad) return -1;
     if (check_only) return 0;

@@ -158,7 +158,20 @@ typedef struct ThvmMoeArgs {
   const void *wgu_s; const float *sgu_s;
   const void *wd_s;  const float *sd_s;
   uint32_t B, D, E, K, I, S, wdt;
+  /* expert-grouped form (grouped = 1; any B, meant for B > 4): every live
+   * expert's weights are streamed once for all the rows routed to it.
+   * plan [E + E*B*K] int32 scratch: rows per expert, then each expert's
+   * (b*K + slot) list in ascending order; part [B*K*D + B*D] f32 scratch: the
+   * per-slot down outputs, then the shared ones, summed by a combine kernel
+   * in the per-row kernels' order (outputs are identical to theirs). */
+  uint32_t grouped;
+  int32_t *plan;
+  float *part;
+  int32_t *live;           /* grouped gate/up: += experts with rows (optional) */
 } ThvmMoeArgs;
+/* plan / part scratch sizes in bytes for the grouped form */
+uint64_t thvm_k_moe_plan_bytes(uint32_t B, uint32_t E, uint32_t K);
+uint64_t thvm_k_moe_part_bytes(uint32_t B, uint32_t K, uint32_t D);
 int thvm_k_moe_gateup(const ThvmMoeArgs *a, hipStream_t s, char *err, int errlen);
 int thvm_k_moe_down(const ThvmMoeArgs *a, hipStream_t s, char *err, int errlen);
 

@@ -16,12 +16,21 @@
 #include <stdio.h>
 
 // The standalone kernel: waves own row groups blockIdx*nw + wave, grid-stride.
+// blockIdx.y selects a chunk of M batch rows (x, y and res advance by M rows
+// per chunk): batches above 4 rows whose operands the MFMA GEMM does not take
+// run as chunks of 4, each output row computed exactly as at M <= 4.
 template <int WT, int XD, int M, int R, int U>
 __global__ __launch_bounds__(1024) void k_gemv(ThvmGemvArgs a) {
   extern __shared__ __align__(16) unsigned char xs_raw[];
   __shared__ float red[GEMV_MAX_WAVES];
   const int nw = blockDim.x >> 6;
   const uint32_t g = blockIdx.x * nw + (threadIdx.x >> 6);
+  if (blockIdx.y) {
+    const uint64_t m0 = (uint64_t)blockIdx.y * M, ys = a.ydt == THVM_DT_FP32 ? 4 : 2;
+    a.x = (const char *)a.x + m0 * a.ldx * XDr<XD>::B;
+    a.y = (char *)a.y + m0 * a.ldy * ys;
+    if (a.res) a.res = (const char *)a.res + m0 * a.ldy * ys;
+  }
   gemv_core<WT, XD, M, R, U, false>(
       a, xs_raw, red, g, gridDim.x * nw, blockDim.x, nw, [] { return true; },
       [&](int m) { return (const void *)((const char *)a.x + (uint64_t)m * a.ldx * XDr<XD>::B); },
@@ -144,11 +153,25 @@ extern "C" int thvm_k_gemv(const ThvmGemvArgs *a, hipStream_t s, char *err, int 
   // path: the MFMA GEMM for batches above 4 rows (or x too large for LDS
   // staging), the GEMV otherwise; tune_path 1/2 forces GEMV/MFMA
   if (a->tune_path > 2) { snprintf(err, errlen, "gemv: path must be 0, 1 or 2"); return -1; }
+  // row chunks: M > 4 with operands the MFMA GEMM does not take (f32 weights
+  // or x, mixed 16-bit types, a fused norm) runs as M/4 chunks of 4 rows
+  uint32_t Mk = a->M, chunks = 1;
   {
     const uint64_t xlds = (uint64_t)a->M * a->K * ((a->xdt == THVM_DT_FP32 || a->wdt == THVM_DT_FP32) ? 4 : 2);
-    const bool mfma = a->tune_path == 2 || (a->tune_path == 0 && (a->M > 4 || xlds > 160 * 1024));
+    const bool mfma_types = !a->norm && a->K % 64 == 0 &&
+        ((a->wdt == THVM_DT_FP16 && a->xdt == THVM_DT_FP16) || (a->wdt == THVM_DT_BF16 && a->xdt == THVM_DT_BF16) ||
+         (a->wdt == THVM_DT_FP8E4M3 && (a->xdt == THVM_DT_BF16 || a->xdt == THVM_DT_FP16)));
+    const bool mfma = a->tune_path == 2 || (a->tune_path == 0 && mfma_types && (a->M > 4 || xlds > 160 * 1024));
     if (mfma) return thvm_k_gemm_mfma(a, s, err, errlen);
-    if (a->M > 4) { snprintf(err, errlen, "gemv: the GEMV path takes M <= 4 (M=%u)", a->M); return -1; }
+    if (a->M > 4) {
+      if (a->M % 4 || a->epi == THVM_EPI_QKV || a->epi == THVM_EPI_QKV_ROPE) {
+        snprintf(err, errlen, "gemv: M=%u rows of these dtypes run in chunks of 4: M must be a multiple "
+                 "of 4 and the epilogue not a KV append", a->M);
+        return -1;
+      }
+      Mk = 4;
+      chunks = a->M / 4;
+    }
   }
   if (a->tune_r) {
     if (a->tune_r != 1 && a->tune_r != 2) { snprintf(err, errlen, "gemv: r must be 1 or 2"); return -1; }
@@ -158,18 +181,18 @@ extern "C" int thvm_k_gemv(const ThvmGemvArgs *a, hipStream_t s, char *err, int 
   int U = a->tune_u ? (int)a->tune_u : 4;
   if (U != 4 && U != 8) { snprintf(err, errlen, "gemv: u must be 4 or 8"); return -1; }
   uint32_t xsz = (a->xdt == THVM_DT_FP32 || a->wdt == THVM_DT_FP32) ? 4 : 2;
-  uint64_t lds = (uint64_t)a->M * a->K * xsz;
+  uint64_t lds = (uint64_t)Mk * a->K * xsz;
   if (lds > 160 * 1024) {
     snprintf(err, errlen, "gemv: M*K=%llu x elements exceed LDS (use the MFMA GEMM)",
-             (unsigned long long)a->M * a->K);
+             (unsigned long long)Mk * a->K);
     return -1;
   }
   gemv_fn f = nullptr;
   switch (a->wdt) {
-    case THVM_DT_FP32: f = pick_x<WT_F32>(a->xdt, a->M, R, U); break;
-    case THVM_DT_FP16: f = pick_x<WT_F16>(a->xdt, a->M, R, U); break;
-    case THVM_DT_BF16: f = pick_x<WT_BF16>(a->xdt, a->M, R, U); break;
-    case THVM_DT_FP8E4M3: f = pick_x<WT_FP8>(a->xdt, a->M, R, U); break;
+    case THVM_DT_FP32: f = pick_x<WT_F32>(a->xdt, Mk, R, U); break;
+    case THVM_DT_FP16: f = pick_x<WT_F16>(a->xdt, Mk, R, U); break;
+    case THVM_DT_BF16: f = pick_x<WT_BF16>(a->xdt, Mk, R, U); break;
+    case THVM_DT_FP8E4M3: f = pick_x<WT_FP8>(a->xdt, Mk, R, U); break;
   }
   if (!f) { snprintf(err, errlen, "gemv: no kernel instance (R=%d U=%d)", R, U); return -1; }
   uint32_t Gr = (a->N + R - 1) / R;
@@ -196,7 +219,7 @@ extern "C" int thvm_k_gemv(const ThvmGemvArgs *a, hipStream_t s, char *err, int 
       return -1;
     }
   }
-  thvm_launch(true, true, f, dim3(grid), dim3(64 * waves), (uint32_t)lds, s, *a);
+  thvm_launch(true, true, f, dim3(grid, chunks), dim3(64 * waves), (uint32_t)lds, s, *a);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) {
     snprintf(err, errlen, "gemv launch: %s", hipGetErrorString(e));

@@ -232,6 +232,156 @@ __global__ __launch_bounds__(MOE_THREADS) void k_moe_down(ThvmMoeArgs a) {
   }
 }
 
+// ---- expert-grouped form (batches above 4 rows) ---------------------------
+// Rows routed to each expert, in ascending (b, slot) order: one thread per
+// expert scans the B*K routing entries.
+__global__ __launch_bounds__(64) void k_moe_plan(ThvmMoeArgs a) {
+  const uint32_t e = threadIdx.x, n = a.B * a.K;
+  if (e >= a.E) return;
+  int32_t *lst = a.plan + a.E + (uint64_t)e * n;
+  int32_t c = 0;
+  for (uint32_t i = 0; i < n; i++)
+    if (a.sel[i] == (int32_t)e) lst[c++] = (int32_t)i;
+  a.plan[e] = c;
+  if (a.live && c > 0) atomicAdd(a.live, 1);     // experts streamed (measurement)
+}
+
+#define MOE_RG 8        /* x / h rows staged in LDS per pass */
+
+// grid (ceil(max(I, S) / (8 * PPW)), E + 1): blockIdx.y < E is routed expert
+// e over the rows the plan lists for it; blockIdx.y == E is the shared expert
+// (S row pairs) over every batch row.  Each wave's PPW (gate, up) row pairs
+// are loaded once; the rows' x are staged MOE_RG at a time.  Per (row,
+// pair) the arithmetic is k_moe_gateup's.
+template <bool FP8, int NC, int PPW>
+__global__ __launch_bounds__(MOE_THREADS) void k_moe_gateup_g(ThvmMoeArgs a) {
+  extern __shared__ float xs[];
+  const uint32_t e = blockIdx.y, D = a.D, I = a.I, K = a.K;
+  const bool shared = e == a.E;
+  const uint32_t npair = shared ? a.S : I;
+  const uint32_t nrows = shared ? a.B : (uint32_t)a.plan[e];
+  const uint32_t pb = blockIdx.x * MOE_WAVES * PPW;
+  if (nrows == 0 || pb >= npair) return;                   // block-uniform
+  const int32_t *lst = a.plan + a.E + (uint64_t)e * a.B * K;
+  const uint32_t P = K * I + a.S;
+  const uint32_t lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const uint32_t p0 = pb + wv * PPW;
+  const uint64_t rowb = (uint64_t)D * (FP8 ? 1 : 2);
+  const uint32_t nch = (uint32_t)(rowb / 16);
+  const char *base = shared ? (const char *)a.wgu_s : (const char *)a.wgu_e;
+  const float *scp = shared ? a.sgu_s : a.sgu_e;
+  uint4 gq[PPW][NC], uq[PPW][NC];
+#pragma unroll
+  for (int i = 0; i < PPW; i++) {
+    const uint32_t p = p0 + i;
+    const bool live = p < npair;
+    const uint64_t r0 = shared ? 2ull * p : (uint64_t)e * 2 * I + 2 * p;
+    load_row(gq[i], base + (live ? r0 : 0) * rowb, lane, nch, live);
+    load_row(uq[i], base + (live ? r0 + 1 : 0) * rowb, lane, nch, live);
+  }
+  for (uint32_t g0 = 0; g0 < nrows; g0 += MOE_RG) {
+    const uint32_t ng = min((uint32_t)MOE_RG, nrows - g0);
+    __syncthreads();                                       // the previous pass's reads
+    for (uint32_t j = 0; j < ng; j++) {
+      const uint32_t b = shared ? g0 + j : (uint32_t)lst[g0 + j] / K;
+      stage_swz<true, FP8 ? 16 : 8>(xs + j * D, a.x + (uint64_t)b * D, D, 0, 1);
+    }
+    __syncthreads();
+    for (uint32_t j = 0; j < ng; j++) {
+      const uint32_t ent = shared ? 0u : (uint32_t)lst[g0 + j];
+      const uint32_t b = shared ? g0 + j : ent / K, slot = ent % K;
+#pragma unroll
+      for (int i = 0; i < PPW; i++) {
+        const uint32_t p = p0 + i;
+        if (p >= npair) break;                             // wave-uniform
+        float G = wave_sum(chunk_dot<FP8>(gq[i], xs + j * D, lane, nch));
+        float U = wave_sum(chunk_dot<FP8>(uq[i], xs + j * D, lane, nch));
+        if (lane == 0) {
+          const uint64_t r0 = shared ? 2ull * p : (uint64_t)e * 2 * I + 2 * p;
+          if (scp) { G *= scp[r0]; U *= scp[r0 + 1]; }
+          a.h[(uint64_t)b * P + (shared ? K * I : slot * I) + p] = silu_f(G) * U;
+        }
+      }
+    }
+  }
+}
+
+// grid (ceil(D / (8 * RPW)), E + 1): routed expert e (rows d of its down
+// matrix, over the plan's rows) or the shared expert (every batch row); the
+// weights are loaded once, the rows' h staged MOE_RG at a time, and each
+// (row, d) down value -- k_moe_down's per-segment value, scale included -- is
+// written to part[b][slot][d] (shared: part[B*K*D + b*D + d]).
+template <bool FP8, int NC, int RPW>
+__global__ __launch_bounds__(MOE_THREADS) void k_moe_down_g(ThvmMoeArgs a) {
+  extern __shared__ float hs[];
+  const uint32_t e = blockIdx.y, D = a.D, I = a.I, K = a.K, S = a.S;
+  const bool shared = e == a.E;
+  const uint32_t nrows = shared ? a.B : (uint32_t)a.plan[e];
+  const uint32_t db = blockIdx.x * MOE_WAVES * RPW;
+  if (nrows == 0 || db >= D) return;                       // block-uniform
+  const int32_t *lst = a.plan + a.E + (uint64_t)e * a.B * K;
+  const uint32_t P = K * I + S, W = shared ? S : I;
+  const uint32_t lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const uint32_t d0 = db + wv * RPW;
+  const uint64_t rowb = (uint64_t)W * (FP8 ? 1 : 2);
+  const uint32_t nch = (uint32_t)(rowb / 16);
+  uint4 q[RPW][NC];
+#pragma unroll
+  for (int r = 0; r < RPW; r++) {
+    const uint32_t d = d0 + r;
+    const bool live = d < D;
+    const uint64_t row = shared ? (uint64_t)(live ? d : 0) : (uint64_t)e * D + (live ? d : 0);
+    load_row(q[r], (shared ? (const char *)a.wd_s : (const char *)a.wd_e) + row * rowb, lane, nch, live);
+  }
+  const float *scl = shared ? a.sd_s : a.sd_e;
+  for (uint32_t g0 = 0; g0 < nrows; g0 += MOE_RG) {
+    const uint32_t ng = min((uint32_t)MOE_RG, nrows - g0);
+    __syncthreads();
+    for (uint32_t j = 0; j < ng; j++) {
+      const uint32_t ent = shared ? 0u : (uint32_t)lst[g0 + j];
+      const uint32_t b = shared ? g0 + j : ent / K, slot = ent % K;
+      const float *src = a.h + (uint64_t)b * P + (shared ? K * I : slot * I);
+      stage_swz<false, FP8 ? 16 : 8>(hs + j * W, src, W, 0, 1);
+    }
+    __syncthreads();
+    for (uint32_t j = 0; j < ng; j++) {
+      const uint32_t ent = shared ? 0u : (uint32_t)lst[g0 + j];
+      const uint32_t b = shared ? g0 + j : ent / K, slot = ent % K;
+#pragma unroll
+      for (int r = 0; r < RPW; r++) {
+        const uint32_t d = d0 + r;
+        if (d >= D) break;                                 // wave-uniform
+        float sv = wave_sum(chunk_dot<FP8>(q[r], hs + j * W, lane, nch));
+        if (scl) sv *= shared ? scl[d] : scl[(uint64_t)e * D + d];
+        if (lane == 0) {
+          const uint64_t o = shared ? (uint64_t)a.B * K * D + (uint64_t)b * D + d
+                                    : ((uint64_t)b * K + slot) * D + d;
+          a.part[o] = sv;
+        }
+      }
+    }
+  }
+}
+
+// res[b][d] = bf16(res + bf16(sum_slot probs * part + shared)), k_moe_down's
+// sum order; grid (ceil(D / 256), B)
+__global__ __launch_bounds__(256) void k_moe_combine(ThvmMoeArgs a) {
+  const uint32_t b = blockIdx.y, d = blockIdx.x * 256 + threadIdx.x, D = a.D, K = a.K;
+  if (d >= D) return;
+  float acc = 0.0f;
+  for (uint32_t e = 0; e < K; e++) acc += a.probs[(uint64_t)b * K + e] * a.part[((uint64_t)b * K + e) * D + d];
+  if (a.S > 0) acc += a.part[(uint64_t)a.B * K * D + (uint64_t)b * D + d];
+  bf16_t *r = (bf16_t *)a.res + (uint64_t)b * D + d;
+  r[0] = f2bf(bf2f(r[0]) + rbf(acc));
+}
+
+extern "C" uint64_t thvm_k_moe_plan_bytes(uint32_t B, uint32_t E, uint32_t K) {
+  return ((uint64_t)E + (uint64_t)E * B * K) * 4;
+}
+extern "C" uint64_t thvm_k_moe_part_bytes(uint32_t B, uint32_t K, uint32_t D) {
+  return ((uint64_t)B * K * D + (uint64_t)B * D) * 4;
+}
+
 // -------------------------------------------------------------------------
 extern "C" int thvm_k_route(const ThvmRouteArgs *a, hipStream_t s, char *err, int errlen) {
   if (a->B == 0 || a->E == 0 || a->E > 64 || a->K == 0 || a->K > a->E) {
@@ -295,8 +445,44 @@ static moe_fn pick_gateup(uint32_t nch, uint32_t *ppw) {
   return k_moe_gateup<FP8, 4, 2>;
 }
 
+template <bool FP8>
+static moe_fn pick_gateup_g(uint32_t nch, uint32_t *ppw) {
+  if (nch <= 64) { *ppw = 4; return k_moe_gateup_g<FP8, 1, 4>; }
+  if (nch <= 128) { *ppw = 2; return k_moe_gateup_g<FP8, 2, 2>; }
+  *ppw = 1;
+  return k_moe_gateup_g<FP8, 4, 1>;
+}
+
+static int moe_grouped_check(const ThvmMoeArgs *a, int gateup, char *err, int errlen) {
+  if (!a->plan || (!gateup && !a->part)) {
+    snprintf(err, errlen, "moe: the grouped form needs the plan (and, for down, the part) scratch");
+    return -1;
+  }
+  if (a->E > 64) { snprintf(err, errlen, "moe: grouped form takes E <= 64"); return -1; }
+  return 0;
+}
+
 extern "C" int thvm_k_moe_gateup(const ThvmMoeArgs *a, hipStream_t s, char *err, int errlen) {
   if (moe_check(a, 1, err, errlen)) return -1;
+  if (a->grouped) {
+    if (moe_grouped_check(a, 1, err, errlen)) return -1;
+    const uint32_t nch = a->D * (a->wdt == THVM_DT_FP8E4M3 ? 1 : 2) / 16;
+    uint32_t ppw = 1;
+    const moe_fn f = a->wdt == THVM_DT_FP8E4M3 ? pick_gateup_g<true>(nch, &ppw) : pick_gateup_g<false>(nch, &ppw);
+    const uint32_t np = a->I > a->S ? a->I : a->S;
+    const dim3 grid((np + MOE_WAVES * ppw - 1) / (MOE_WAVES * ppw), a->E + (a->S ? 1 : 0));
+    const uint32_t lds = MOE_RG * a->D * 4;
+    if (lds > 160 * 1024) { snprintf(err, errlen, "moe: D too large for the grouped form"); return -1; }
+    if (lds > 64 * 1024) {
+      hipError_t e = hipFuncSetAttribute((const void *)f, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+      if (e != hipSuccess) { snprintf(err, errlen, "moe_gateup: hipFuncSetAttribute: %s", hipGetErrorString(e)); return -1; }
+    }
+    thvm_launch(true, false, k_moe_plan, dim3(1), dim3(64), 0, s, *a);
+    thvm_launch(false, true, f, grid, dim3(MOE_THREADS), lds, s, *a);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) { snprintf(err, errlen, "moe_gateup launch: %s", hipGetErrorString(e)); return -1; }
+    return 0;
+  }
   const uint32_t P = a->K * a->I + a->S;
   const uint32_t nch = a->D * (a->wdt == THVM_DT_FP8E4M3 ? 1 : 2) / 16;
   uint32_t ppw = 1;
@@ -312,6 +498,32 @@ extern "C" int thvm_k_moe_gateup(const ThvmMoeArgs *a, hipStream_t s, char *err,
 
 extern "C" int thvm_k_moe_down(const ThvmMoeArgs *a, hipStream_t s, char *err, int errlen) {
   if (moe_check(a, 0, err, errlen)) return -1;
+  if (a->grouped) {
+    if (moe_grouped_check(a, 0, err, errlen)) return -1;
+    const uint32_t wsz = a->wdt == THVM_DT_FP8E4M3 ? 1 : 2;
+    const uint32_t W = a->I > a->S ? a->I : a->S, nch = W * wsz / 16;
+    if (nch > 64 * 6) { snprintf(err, errlen, "moe: down rows above 6 KiB"); return -1; }
+    const bool f8 = a->wdt == THVM_DT_FP8E4M3;
+    // rows per wave 4 up to 4 KiB rows, 2 beyond (register budget)
+    const int RPW = nch <= 256 ? 4 : 2;
+    moe_fn f = nch <= 64 ? (f8 ? k_moe_down_g<true, 1, 4> : k_moe_down_g<false, 1, 4>)
+             : nch <= 128 ? (f8 ? k_moe_down_g<true, 2, 4> : k_moe_down_g<false, 2, 4>)
+             : nch <= 192 ? (f8 ? k_moe_down_g<true, 3, 4> : k_moe_down_g<false, 3, 4>)
+             : nch <= 256 ? (f8 ? k_moe_down_g<true, 4, 4> : k_moe_down_g<false, 4, 4>)
+                          : (f8 ? k_moe_down_g<true, 6, 2> : k_moe_down_g<false, 6, 2>);
+    const dim3 grid((a->D + MOE_WAVES * RPW - 1) / (MOE_WAVES * RPW), a->E + (a->S ? 1 : 0));
+    const uint32_t lds = MOE_RG * W * 4;
+    if (lds > 160 * 1024) { snprintf(err, errlen, "moe: I / S too large for the grouped form"); return -1; }
+    if (lds > 64 * 1024) {
+      hipError_t e = hipFuncSetAttribute((const void *)f, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+      if (e != hipSuccess) { snprintf(err, errlen, "moe_down: hipFuncSetAttribute: %s", hipGetErrorString(e)); return -1; }
+    }
+    thvm_launch(true, false, f, grid, dim3(MOE_THREADS), lds, s, *a);
+    thvm_launch(false, true, k_moe_combine, dim3((a->D + 255) / 256, a->B), dim3(256), 0, s, *a);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) { snprintf(err, errlen, "moe_down launch: %s", hipGetErrorString(e)); return -1; }
+    return 0;
+  }
   const uint32_t P = a->K * a->I + a->S;
   const uint32_t lds = P * 4;
   if (lds > 160 * 1024) { snprintf(err, errlen, "moe: K*I+S too large for LDS"); return -1; }
