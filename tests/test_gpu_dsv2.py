@@ -51,11 +51,12 @@ def close_bf16(got, want, floor=0.0):
 
 MLA_SHAPES = [dict(H=16, dn=128, dr=64, kv=512, dv=128, B=2, ms=256, L=130),
               dict(H=8, dn=32, dr=16, kv=64, dv=32, B=1, ms=128, L=64),
-              dict(H=8, dn=32, dr=16, kv=128, dv=32, B=3, ms=64, L=1)]
+              dict(H=8, dn=32, dr=16, kv=128, dv=32, B=3, ms=64, L=1),
+              dict(H=16, dn=128, dr=64, kv=512, dv=128, B=8, ms=192, L=150)]   # all heads per block
 
 
 @pytest.mark.parametrize("wdt", [DT_FP8, DT_BF16])
-@pytest.mark.parametrize("shape", MLA_SHAPES, ids=["c5", "smoke", "L1"])
+@pytest.mark.parametrize("shape", MLA_SHAPES, ids=["c5", "smoke", "L1", "c5_b8"])
 def test_mla_prep_and_attn(hip, shape, wdt):
     H, dn, dr, kv, dv, B, ms, L = (shape[k] for k in ("H", "dn", "dr", "kv", "dv", "B", "ms", "L"))
     say(f"case: mla {shape} wdt={wdt}")

@@ -235,18 +235,43 @@ __global__ __launch_bounds__(MOE_THREADS) void k_moe_down(ThvmMoeArgs a) {
 // ---- expert-grouped form (batches above 4 rows) ---------------------------
 // Rows routed to each expert, in ascending (b, slot) order: one thread per
 // expert scans the B*K routing entries.
+#define MOE_PLAN_MAX 4096   /* B*K routing entries staged in LDS */
 __global__ __launch_bounds__(64) void k_moe_plan(ThvmMoeArgs a) {
+  __shared__ int32_t sl[MOE_PLAN_MAX];
   const uint32_t e = threadIdx.x, n = a.B * a.K;
+  for (uint32_t i = threadIdx.x; i < n; i += 64) sl[i] = a.sel[i];   // loads in flight together
+  __syncthreads();
   if (e >= a.E) return;
   int32_t *lst = a.plan + a.E + (uint64_t)e * n;
   int32_t c = 0;
   for (uint32_t i = 0; i < n; i++)
-    if (a.sel[i] == (int32_t)e) lst[c++] = (int32_t)i;
+    if (sl[i] == (int32_t)e) lst[c++] = (int32_t)i;
   a.plan[e] = c;
   if (a.live && c > 0) atomicAdd(a.live, 1);     // experts streamed (measurement)
 }
 
-#define MOE_RG 8        /* x / h rows staged in LDS per pass */
+#define MOE_RG 4        /* x / h rows staged in LDS per pass */
+
+// Stage ng <= MOE_RG rows of n f32 each (row j from src(j)) into dst + j*n,
+// each row in stage_swz's single-segment layout (chunk_swz over n/EPC
+// chunks); every row's 16-byte loads are in flight before the first store.
+template <bool RBF, int EPC, class SrcF>
+__device__ __forceinline__ void stage_rows(float *dst, uint32_t ng, uint32_t n, SrcF &&src) {
+  const uint32_t tid = threadIdx.x, nt = blockDim.x, n4 = n / 4, nch = n / EPC;
+  for (uint32_t i = tid; i < n4; i += nt) {
+    float4 v[MOE_RG];
+#pragma unroll
+    for (int j = 0; j < MOE_RG; j++)
+      v[j] = (uint32_t)j < ng ? ((const float4 *)src(j))[i] : make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+    for (int j = 0; j < MOE_RG; j++) {
+      if ((uint32_t)j >= ng) break;
+      float4 w = v[j];
+      if (RBF) { w.x = rbf(w.x); w.y = rbf(w.y); w.z = rbf(w.z); w.w = rbf(w.w); }
+      ((float4 *)(dst + j * n))[chunk_swz<EPC>(4 * i, nch) / 4] = w;
+    }
+  }
+}
 
 // grid (ceil(max(I, S) / (8 * PPW)), E + 1): blockIdx.y < E is routed expert
 // e over the rows the plan lists for it; blockIdx.y == E is the shared expert
@@ -282,10 +307,10 @@ __global__ __launch_bounds__(MOE_THREADS) void k_moe_gateup_g(ThvmMoeArgs a) {
   for (uint32_t g0 = 0; g0 < nrows; g0 += MOE_RG) {
     const uint32_t ng = min((uint32_t)MOE_RG, nrows - g0);
     __syncthreads();                                       // the previous pass's reads
-    for (uint32_t j = 0; j < ng; j++) {
+    stage_rows<true, FP8 ? 16 : 8>(xs, ng, D, [&](uint32_t j) {
       const uint32_t b = shared ? g0 + j : (uint32_t)lst[g0 + j] / K;
-      stage_swz<true, FP8 ? 16 : 8>(xs + j * D, a.x + (uint64_t)b * D, D, 0, 1);
-    }
+      return a.x + (uint64_t)b * D;
+    });
     __syncthreads();
     for (uint32_t j = 0; j < ng; j++) {
       const uint32_t ent = shared ? 0u : (uint32_t)lst[g0 + j];
@@ -337,12 +362,11 @@ __global__ __launch_bounds__(MOE_THREADS) void k_moe_down_g(ThvmMoeArgs a) {
   for (uint32_t g0 = 0; g0 < nrows; g0 += MOE_RG) {
     const uint32_t ng = min((uint32_t)MOE_RG, nrows - g0);
     __syncthreads();
-    for (uint32_t j = 0; j < ng; j++) {
+    stage_rows<false, FP8 ? 16 : 8>(hs, ng, W, [&](uint32_t j) {
       const uint32_t ent = shared ? 0u : (uint32_t)lst[g0 + j];
       const uint32_t b = shared ? g0 + j : ent / K, slot = ent % K;
-      const float *src = a.h + (uint64_t)b * P + (shared ? K * I : slot * I);
-      stage_swz<false, FP8 ? 16 : 8>(hs + j * W, src, W, 0, 1);
-    }
+      return a.h + (uint64_t)b * P + (shared ? K * I : slot * I);
+    });
     __syncthreads();
     for (uint32_t j = 0; j < ng; j++) {
       const uint32_t ent = shared ? 0u : (uint32_t)lst[g0 + j];
@@ -454,6 +478,10 @@ static moe_fn pick_gateup_g(uint32_t nch, uint32_t *ppw) {
 }
 
 static int moe_grouped_check(const ThvmMoeArgs *a, int gateup, char *err, int errlen) {
+  if ((uint64_t)a->B * a->K > MOE_PLAN_MAX) {
+    snprintf(err, errlen, "moe: grouped form takes B*K <= %d routing entries", MOE_PLAN_MAX);
+    return -1;
+  }
   if (!a->plan || (!gateup && !a->part)) {
     snprintf(err, errlen, "moe: the grouped form needs the plan (and, for down, the part) scratch");
     return -1;
