@@ -458,6 +458,42 @@ def test_attention_decode(hip, H, Hkv, hd, L, cdt):
         assert np.all(np.abs(got - ww) <= 1e-5 * (np.abs(ww) + 1.0)), np.max(np.abs(got - ww))
     else:
         assert np.all(np.abs(got - ww) <= 2.0 ** -7 * np.abs(ww) + 2e-3), np.max(np.abs(got - ww))
+    # the one-launch form (split + last-unit merge) equals the two-kernel form
+    # bit for bit, and leaves its merge counters zero for the next launch
+    out2 = hip.Buffer(B * H * hd * SZ[cdt])
+    part2 = hip.Buffer(B * H * nsplit * (hd + 2) * 4 + B * Hkv * 4)
+    hip.builtin("attn", [out2, up(hip, qs), up(hip, ks), up(hip, vs),
+                         up(hip, np.array([L], np.int32)), part2],
+                b=B, h=H, hkv=Hkv, hd=hd, maxseq=ms, chunk=64, nsplit=nsplit, qt=cdt,
+                ct=cdt, ot=cdt, scale=scale, fused=1)
+    assert np.array_equal(out.read(np.uint8), out2.read(np.uint8))
+    ctr = part2.read(np.uint32)[B * H * nsplit * (hd + 2):]
+    assert not ctr.any(), ctr
+
+
+def test_attention_fused_repeated(hip):
+    """Ten launches on one partial buffer at changing lengths: every merge
+    finds its counter at zero and the outputs match the two-kernel form."""
+    B, H, Hkv, hd, ms, cdt = 1, 32, 8, 128, 2176, DT_BF16
+    say("case: fused attention, 10 launches on one partial buffer")
+    rng = np.random.default_rng(5)
+    qs, _ = rand_store(rng, (B, H, hd), cdt)
+    ks, _ = rand_store(rng, (B, Hkv, ms, hd), cdt)
+    vs, _ = rand_store(rng, (B, Hkv, ms, hd), cdt)
+    nsplit = (ms + 63) // 64
+    qb, kb, vb = up(hip, qs), up(hip, ks), up(hip, vs)
+    part = hip.Buffer(B * H * nsplit * (hd + 2) * 4 + B * Hkv * 4)
+    part2 = hip.Buffer(B * H * nsplit * (hd + 2) * 4 + B * Hkv * 4)
+    scale = float(np.float32(1.0 / np.sqrt(hd)))
+    for L in (2049, 2050, 1, 64, 65, 2176, 700, 129, 2048, 3):
+        outs = []
+        for fused, pb in ((1, part), (0, part2)):
+            o = hip.Buffer(B * H * hd * 2)
+            hip.builtin("attn", [o, qb, kb, vb, up(hip, np.array([L], np.int32)), pb], b=B, h=H,
+                        hkv=Hkv, hd=hd, maxseq=ms, chunk=64, nsplit=nsplit, qt=cdt, ct=cdt, ot=cdt,
+                        scale=scale, fused=fused)
+            outs.append(o.read(np.uint16))
+        assert np.array_equal(outs[0], outs[1]), L
 
 
 def test_argmax_ties_lowest_index(hip):

@@ -93,10 +93,15 @@ int thvm_k_softmax(const ThvmSoftmaxArgs *a, hipStream_t s, char *err, int errle
 typedef struct ThvmAttnArgs {
   void *out; const void *q; const void *kcache; const void *vcache;
   const int32_t *len;
-  float *part;             /* scratch: [B][H][n_split][hd + 2] f32          */
+  float *part;             /* scratch: [B][H][n_split][hd + 2] f32, then B*Hkv
+                            * merge counters that must be zero before the first
+                            * launch (a zero-filled buffer); every launch leaves
+                            * them zero                                       */
   uint32_t B, H, Hkv, hd, max_seq, chunk, n_split;
   uint32_t qdt, cdt, odt;
   float scale;             /* 1/sqrt(hd)                                     */
+  uint32_t fused;          /* 1: split and merge in one launch (the last unit
+                            * of a (row, kv head) merges); 0: two launches   */
 } ThvmAttnArgs;
 int thvm_k_attn_decode(const ThvmAttnArgs *a, hipStream_t s, char *err, int errlen);
 uint64_t thvm_k_attn_part_bytes(uint32_t B, uint32_t H, uint32_t Hkv, uint32_t hd, uint32_t n_split);

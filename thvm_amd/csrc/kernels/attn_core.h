@@ -100,7 +100,10 @@ struct MergeLds {
   __align__(16) float4 red4[256];
 };
 
-template <int HD, int G, int AT, bool COH>
+// COH: q, the partials (and, in attn_merge, the output) use system-scope
+// accesses; LATE: the cache row L-1 is written by another block of the same
+// launch and is loaded in finish() with a system-scope load.
+template <int HD, int G, int AT, bool COH, bool LATE = COH>
 struct AttnSplit {
   static constexpr int ES = ATr<AT>::ES;
   static constexpr int EPL = 16 / ES;           // elements per lane chunk
@@ -128,7 +131,7 @@ struct AttnSplit {
     for (int it = 0; it < IT; it++) {
       const uint32_t j = p0 + wv * PPW + it * RPW + rg;
       ok[it] = (int32_t)j < L && j < a.max_seq;
-      const bool early = ok[it] && !(COH && (int32_t)j == L - 1);
+      const bool early = ok[it] && !(LATE && (int32_t)j == L - 1);
       const uint64_t off = row_off(a, b, kvh, early ? j : 0);
       kq[it] = ld_stream16(kb + off);
       vq[it] = ld_stream16(vb + off);
@@ -145,7 +148,7 @@ struct AttnSplit {
     const uint32_t d0 = li * EPL;
     float mw[G], lw[G], acc[G][EPL];
     if (active) {
-      if (COH) {   // the row appended at L-1 by another block of this launch
+      if (LATE) {   // the row appended at L-1 by another block of this launch
         const uint32_t p0 = split * ATT_CHUNK;
 #pragma unroll
         for (int it = 0; it < IT; it++) {
