@@ -11,6 +11,7 @@ kernel (the fp8 GEMV) against 8 TB/s.  `--config` selects another workload:
   C4  Llama-8B shape fp8 weight-only, bf16 activations, context 2048, batch 1 or 16
   C5  DeepSeek-V2-Lite shape (27L, D2048, MLA kv_lora 512, 64 experts top-6 + 2
       shared, V102400) fp8 weights, bf16 latent cache at context 4096, batch 1
+      or 32 (above 4 rows: expert-grouped MoE, MFMA projections)
 
 One "step" is one greedy decode token for every batch row: one hipGraph
 replay of the captured decode step (embedding, per-layer norm + projections +
@@ -137,7 +138,11 @@ def run_decode(thvm, key: str, batch: int, args) -> dict:
     if persist:
         cfg["step_mode"] = 1
     ctx = spec["ctx"]
-    cpu_steps = 0 if args.no_cpu else (args.cpu_steps or (spec["cpu_steps"] if batch <= 4 else 1))
+    # the oracle decodes batch rows one after another on one core, so its rate
+    # is the batch-1 rate; batches above 16 rows would take minutes and are
+    # not run (cpu_baseline null with that note)
+    cpu_steps = 0 if (args.no_cpu or batch > 16) else \
+        (args.cpu_steps or (spec["cpu_steps"] if batch <= 4 else 1))
     cfg["max_seq"] = ((ctx + args.warmup + args.steps + cpu_steps + 8 + 63) // 64) * 64
     t0 = time.time()
     dec = thvm.Decoder(seed=1234, **cfg)
@@ -191,6 +196,10 @@ def run_decode(thvm, key: str, batch: int, args) -> dict:
     # end (hipExtLaunchKernel)
     dummy = thvm.Buffer(64)
     prof_steps = 2
+    grouped = cfg["arch"] == 3 and batch > 4
+    if grouped:   # experts the grouped MoE streams: counted on the device
+        import numpy as np
+        dec.write_tensor("moe.live", np.zeros(1, np.int32))
     thvm.kprof(True)
     thvm.kprof_reset()
     for _ in range(prof_steps):
@@ -206,6 +215,23 @@ def run_decode(thvm, key: str, batch: int, args) -> dict:
     thvm.kprof(False)
     dummy.free()
     L_prof = dec.position - 1
+    live_per_step = None
+    if grouped:
+        # each live expert's gate/up and down rows (+ fp8 row scales) once per
+        # layer, the shared experts once per layer, h / x / out traffic
+        live = int(dec.read_tensor("moe.live")[0])
+        live_per_step = live / prof_steps
+        D, I, S, K, E = cfg["dim"], cfg["moe_inter"], cfg["n_shared"] * cfg["moe_inter"], cfg["top_k"], cfg["n_experts"]
+        ws = 1 if cfg["wdtype"] == DT_FP8 else 2
+        f8 = cfg["wdtype"] == DT_FP8
+        nmoe = cfg["n_layers"] - cfg["first_dense"]
+        gu_e, dn_e = 2 * I * D * ws + (8 * I if f8 else 0), D * I * ws + (4 * D if f8 else 0)
+        gu_s, dn_s = 2 * S * D * ws + (8 * S if f8 else 0), D * S * ws + (4 * D if f8 else 0)
+        act = batch * (K * I + S) * 4
+        for tag, per_e, per_s, extra in (("moe_gateup", gu_e, gu_s, act + batch * D * 4),
+                                         ("moe_down", dn_e, dn_s, act + batch * D * 4 + batch * D * 2)):
+            ms_t, n_t, _ = kern[tag]
+            kern[tag] = (ms_t, n_t, live * per_e + prof_steps * nmoe * (per_s + extra))
     if persist:
         # one launch holds every stage: its bytes are the weights (counted by
         # the dispatcher) plus the live KV rows of the two profiled steps
@@ -285,7 +311,11 @@ def run_decode(thvm, key: str, batch: int, args) -> dict:
         "step_hbm_gbs": round(step_bytes / (ms_per_step / 1000.0) / 1e9, 1),
         "step_bytes": step_bytes,
         "kernels_per_step": dec.step_kernels(),
-        "cpu_baseline": cpu,
+        **({"moe_live_experts_per_layer": round(live_per_step / (cfg["n_layers"] - cfg["first_dense"]), 2)}
+           if live_per_step is not None else {}),
+        "cpu_baseline": cpu if cpu or batch <= 16 else
+        {"value": None, "note": "not run above 16 rows: the oracle decodes rows serially on one core, "
+                                "so its tokens/s is the batch-1 configuration's"},
     }
     if args.layers:
         out["config"]["note"] = "DEBUG: reduced layer count, not the configured model"
@@ -510,7 +540,7 @@ def main() -> int:
         if args.copy_calibration:
             return copy_calibration(thvm)
         if args.config == "all":
-            runs = [("C4", 1), ("C4", 16), ("C5", 1), ("C3", 1), ("C3", 8), ("C1", 1), ("C2", 0)]
+            runs = [("C4", 1), ("C4", 16), ("C5", 1), ("C5", 32), ("C3", 1), ("C3", 8), ("C1", 1), ("C2", 0)]
         else:
             runs = [(args.config, args.batch)]
         for key, batch in runs:

@@ -134,12 +134,9 @@ __global__ __launch_bounds__(256) void k_mla_prep(ThvmMlaArgs a) {
 }
 
 // ---- k_mla_split --------------------------------------------------------
-// grid (n_split, H / (MLA_HG * NG), B), 512 threads: 64 cache rows of batch
-// row b against NG groups of MLA_HG heads, one group after another on the
-// same loaded rows.  At small batches NG = 1 (the latent rows of a split are
-// re-read by the head groups from L2, which buys H / MLA_HG times the
-// blocks); at large batches one block takes every head, so each latent row
-// leaves HBM once.  A head's arithmetic does not depend on NG.  KPL latent
+// grid (n_split, H / MLA_HG, B), 512 threads: 64 cache rows of batch row b
+// against a group of MLA_HG heads (the latent rows of a split are re-read by
+// the H / MLA_HG head groups from L2, which buys 4x the blocks).  KPL latent
 // values per lane (kv = 64 * KPL).
 #define MLA_HG 4
 template <int KPL>
@@ -149,8 +146,7 @@ __global__ __launch_bounds__(MLA_THREADS) void k_mla_split(ThvmMlaArgs a) {
   constexpr int HG = MLA_HG;
   bf16_t *cs = (bf16_t *)smem;                          // [64][KV]
   float *sp = smem + (MLA_CHUNK * KV) / 2;              // [64][HG]: scores, then weights
-  const uint32_t split = blockIdx.x, b = blockIdx.z, dr = a.dr, H = a.H;
-  const uint32_t NG = H / (HG * gridDim.y);
+  const uint32_t split = blockIdx.x, h0 = blockIdx.y * HG, b = blockIdx.z, dr = a.dr, H = a.H;
   const int32_t L = min(a.len[0], (int32_t)a.max_seq);   // rows [0, L) are live
   const uint32_t j0 = split * MLA_CHUNK;
   if (L <= 0 || j0 >= (uint32_t)L) return;
@@ -188,94 +184,88 @@ __global__ __launch_bounds__(MLA_THREADS) void k_mla_split(ThvmMlaArgs a) {
   float pv[RPW];
 #pragma unroll
   for (int r = 0; r < RPW; r++) pv[r] = (wv + 8 * r < nj && lane < dr) ? bf2f(pr[r]) : 0.0f;
-  for (uint32_t hg = 0; hg < NG; hg++) {
-    const uint32_t h0 = (blockIdx.y * NG + hg) * HG;
-    // this lane's slice of the group's qlat and q pe
-    float ql[HG][KPL], qp[HG];
-    bf16_t qr[HG];
+  // this lane's slice of the group's qlat and q pe
+  float ql[HG][KPL], qp[HG];
+  bf16_t qr[HG];
+#pragma unroll
+  for (int h = 0; h < HG; h++) {
+    const float *src = a.qlat + ((uint64_t)b * H + h0 + h) * KV + lane * KPL;
+#pragma unroll
+    for (int i = 0; i < KPL; i++) ql[h][i] = src[i];
+    qr[h] = ((const bf16_t *)a.qpe)[((uint64_t)b * H + h0 + h) * dr + pl_lane];
+  }
+#pragma unroll
+  for (int h = 0; h < HG; h++) qp[h] = lane < dr ? bf2f(qr[h]) : 0.0f;
+#pragma unroll
+  for (int r = 0; r < RPW; r++) {
+    const uint32_t j = wv + 8 * r;
+    if (j >= nj) break;                                  // wave-uniform
+    float c[KPL];
+    if (KPL == 1) {
+      c[0] = __uint_as_float(cw[r][0] << 16);
+      cs[j * KV + lane] = (bf16_t)cw[r][0];
+    } else {
+#pragma unroll
+      for (int i = 0; i < KPL / 2; i++) {
+        c[2 * i] = __uint_as_float(cw[r][i] << 16);
+        c[2 * i + 1] = __uint_as_float(cw[r][i] & 0xffff0000u);
+      }
+      uint32_t *dst = (uint32_t *)(cs + j * KV + lane * KPL);
+#pragma unroll
+      for (int i = 0; i < KPL / 2; i++) dst[i] = cw[r][i];
+    }
 #pragma unroll
     for (int h = 0; h < HG; h++) {
-      const float *src = a.qlat + ((uint64_t)b * H + h0 + h) * KV + lane * KPL;
+      float s = qp[h] * pv[r];
 #pragma unroll
-      for (int i = 0; i < KPL; i++) ql[h][i] = src[i];
-      qr[h] = ((const bf16_t *)a.qpe)[((uint64_t)b * H + h0 + h) * dr + pl_lane];
+      for (int i = 0; i < KPL; i++) s += ql[h][i] * c[i];
+      s = wave_sum(s);
+      if (lane == 0) sp[j * HG + h] = s * a.scale;
     }
+  }
+  __syncthreads();
+  // per-head softmax partial over this block's rows (wave h, lane = row)
+  float *part = a.part + ((uint64_t)b * a.n_split + split) * H * (KV + 4);
+  if (wv < HG) {
+    const uint32_t h = wv;
+    const float s = lane < nj ? sp[lane * HG + h] : -INFINITY;
+    const float m = wave_max(s);
+    const float e = lane < nj ? expf(s - m) : 0.0f;
+    const float l = wave_sum(e);
+    sp[lane * HG + h] = e;
+    if (lane == 0) {
+      part[(h0 + h) * (KV + 4) + KV] = m;
+      part[(h0 + h) * (KV + 4) + KV + 1] = l;
+    }
+  }
+  __syncthreads();
+  // olat partial: thread t owns latent column t for the group's heads; lane j
+  // holds row j's HG softmax weights and v_readlane broadcasts them (a
+  // wave-wide LDS read of one address would serialise on its banks)
+  const uint32_t t = threadIdx.x;
+  if (t < KV) {                                        // whole waves: KV is a multiple of 64
+    float acc[HG];
 #pragma unroll
-    for (int h = 0; h < HG; h++) qp[h] = lane < dr ? bf2f(qr[h]) : 0.0f;
+    for (int h = 0; h < HG; h++) acc[h] = 0.0f;
+    const float4 pl = ((const float4 *)sp)[lane];      // HG == 4 weights of row `lane`
+    for (uint32_t j0r = 0; j0r < nj; j0r += 8) {     // eight rows of LDS reads in flight
+      float c[8];
 #pragma unroll
-    for (int r = 0; r < RPW; r++) {
-      const uint32_t j = wv + 8 * r;
-      if (j >= nj) break;                                  // wave-uniform
-      float c[KPL];
-      if (KPL == 1) {
-        c[0] = __uint_as_float(cw[r][0] << 16);
-        if (hg == 0) cs[j * KV + lane] = (bf16_t)cw[r][0];
-      } else {
-#pragma unroll
-        for (int i = 0; i < KPL / 2; i++) {
-          c[2 * i] = __uint_as_float(cw[r][i] << 16);
-          c[2 * i + 1] = __uint_as_float(cw[r][i] & 0xffff0000u);
-        }
-        if (hg == 0) {
-          uint32_t *dst = (uint32_t *)(cs + j * KV + lane * KPL);
-#pragma unroll
-          for (int i = 0; i < KPL / 2; i++) dst[i] = cw[r][i];
-        }
+      for (int u = 0; u < 8; u++) {
+        const uint32_t j = j0r + u;
+        c[u] = j < nj ? bf2f(cs[j * KV + t]) : 0.0f;
       }
 #pragma unroll
-      for (int h = 0; h < HG; h++) {
-        float s = qp[h] * pv[r];
-#pragma unroll
-        for (int i = 0; i < KPL; i++) s += ql[h][i] * c[i];
-        s = wave_sum(s);
-        if (lane == 0) sp[j * HG + h] = s * a.scale;
+      for (int u = 0; u < 8; u++) {
+        const int j = (int)(j0r + u);                  // rows past nj carry weight 0
+        acc[0] += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(pl.x), j)) * c[u];
+        acc[1] += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(pl.y), j)) * c[u];
+        acc[2] += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(pl.z), j)) * c[u];
+        acc[3] += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(pl.w), j)) * c[u];
       }
     }
-    __syncthreads();
-    // per-head softmax partial over this block's rows (wave h, lane = row)
-    float *part = a.part + ((uint64_t)b * a.n_split + split) * H * (KV + 4);
-    if (wv < HG) {
-      const uint32_t h = wv;
-      const float s = lane < nj ? sp[lane * HG + h] : -INFINITY;
-      const float m = wave_max(s);
-      const float e = lane < nj ? expf(s - m) : 0.0f;
-      const float l = wave_sum(e);
-      sp[lane * HG + h] = e;
-      if (lane == 0) {
-        part[(h0 + h) * (KV + 4) + KV] = m;
-        part[(h0 + h) * (KV + 4) + KV + 1] = l;
-      }
-    }
-    __syncthreads();
-    // olat partial: thread t owns latent column t for the group's heads; lane j
-    // holds row j's HG softmax weights and v_readlane broadcasts them (a
-    // wave-wide LDS read of one address would serialise on its banks)
-    const uint32_t t = threadIdx.x;
-    if (t < KV) {                                        // whole waves: KV is a multiple of 64
-      float acc[HG];
 #pragma unroll
-      for (int h = 0; h < HG; h++) acc[h] = 0.0f;
-      const float4 pl = ((const float4 *)sp)[lane];      // HG == 4 weights of row `lane`
-      for (uint32_t j0r = 0; j0r < nj; j0r += 8) {     // eight rows of LDS reads in flight
-        float c[8];
-#pragma unroll
-        for (int u = 0; u < 8; u++) {
-          const uint32_t j = j0r + u;
-          c[u] = j < nj ? bf2f(cs[j * KV + t]) : 0.0f;
-        }
-#pragma unroll
-        for (int u = 0; u < 8; u++) {
-          const int j = (int)(j0r + u);                  // rows past nj carry weight 0
-          acc[0] += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(pl.x), j)) * c[u];
-          acc[1] += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(pl.y), j)) * c[u];
-          acc[2] += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(pl.z), j)) * c[u];
-          acc[3] += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(pl.w), j)) * c[u];
-        }
-      }
-#pragma unroll
-      for (int h = 0; h < HG; h++) part[(h0 + h) * (KV + 4) + t] = acc[h];
-    }
-    __syncthreads();                                     // sp is rewritten by the next group
+    for (int h = 0; h < HG; h++) part[(h0 + h) * (KV + 4) + t] = acc[h];
   }
 }
 
@@ -455,11 +445,7 @@ extern "C" int thvm_k_mla_attn(const ThvmMlaArgs *a, hipStream_t s, char *err, i
     hipError_t e = hipFuncSetAttribute((const void *)f, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     if (e != hipSuccess) { snprintf(err, errlen, "mla_attn: hipFuncSetAttribute: %s", hipGetErrorString(e)); return -1; }
   }
-  // head groups per block: one (more blocks; the re-reads of a split's rows
-  // by the other groups hit L2).  All groups in one block (ng = ngroups)
-  // measured slower at batch 32, where this kernel is VALU-bound.
-  const uint32_t ngroups = a->H / MLA_HG, ng = 1;
-  thvm_launch(true, false, f, dim3(a->n_split, ngroups / ng, a->B), dim3(MLA_THREADS), lds, s, *a);
+  thvm_launch(true, false, f, dim3(a->n_split, a->H / MLA_HG, a->B), dim3(MLA_THREADS), lds, s, *a);
   {
     const uint32_t lpr = a->kv * wsz / 16, rpp = 64 / lpr;
     const uint32_t rows_pb = (a->dv + MLA_OUT_SPLIT - 1) / MLA_OUT_SPLIT;
