@@ -255,7 +255,10 @@ typedef struct ThvmDecodeConfig {
    * are identical.  Batch 1, 2 or 4; fp8 or bf16 weights, bf16 activations;
    * head_dim 64/128; 1, 2 or 4 query heads per kv head.                    */
   uint32_t step_mode;
-  uint32_t reserved[7];
+  /* DSV2 above 4 rows: the expert-grouped MoE on MFMA (0 or 2, the default)
+   * or on the VALU (1); at 4 rows and below the per-row kernels run.      */
+  uint32_t moe_mode;
+  uint32_t reserved[6];
 } ThvmDecodeConfig;
 
 /* Build the model on device: allocate, fill weights from `seed` (weights

@@ -219,7 +219,7 @@ def run_moe(hip, grouped, B, D, E, K, I, S, wdt, x, sel, probs, res0, w):
     h = hip.Buffer(B * (K * I + S) * 4)
     selb, pb = up(hip, sel), up(hip, probs)
     extra_gu, extra_dn, live = [], [], None
-    if grouped:
+    if grouped:                     # 1: VALU grouped kernels, 2: MFMA
         plan = hip.Buffer((E + E * B * K) * 4)
         live = up(hip, np.zeros(1, np.int32))
         part = hip.Buffer((B * K * D + B * D) * 4)
@@ -257,6 +257,45 @@ def test_moe_grouped_equals_per_row(hip, shape, wdt):
     h1, r1, live = run_moe(hip, True, B, D, E, K, I, S, wdt, x, sel, probs, res0, w)
     assert np.array_equal(h0.view(np.uint32), h1.view(np.uint32)), "gate/up outputs differ"
     assert np.array_equal(r0, r1), "residual outputs differ"
+    assert live == len(np.unique(sel)), (live, len(np.unique(sel)))
+
+
+@pytest.mark.parametrize("wdt", [DT_FP8, DT_BF16])
+@pytest.mark.parametrize("shape", [dict(D=256, E=8, K=3, I=128, S=256, B=40),
+                                   dict(D=2048, E=16, K=6, I=1408, S=2816, B=32),
+                                   dict(D=2048, E=16, K=6, I=1408, S=2816, B=8)],
+                         ids=["small_b40", "c5_b32", "c5_b8"])
+def test_moe_mfma_close_to_per_row(hip, shape, wdt):
+    """The expert-grouped MoE on MFMA (grouped=2) against the per-row kernels
+    on the same routing.  Gate/up: the same bf16-rounded x against the same
+    exactly decoded weights, only the f32 summation order differs, so h agrees
+    to 1e-4 relative (of the row's largest |h|).  Down: h enters as bf16 hi +
+    lo (about 16 significant bits).  The residual output is
+    bf16(res + bf16(acc)): a near-tie of either rounding may flip one bf16
+    ulp of acc or of the result, so it is bounded by 2^-6 (|res| + |out|)
+    and almost all entries are equal.  Expert 0 takes every row (two column
+    tiles at 32 rows, two column groups at 40), half the experts none."""
+    D, E, K, I, S, B = (shape[k] for k in ("D", "E", "K", "I", "S", "B"))
+    say(f"case: mfma moe {shape} wdt={wdt}")
+    rng = np.random.default_rng(11 * D + E + wdt + B)
+    w = weights(rng, E * 2 * I, D, wdt)[:2] + weights(rng, E * D, I, wdt)[:2] + \
+        weights(rng, 2 * S, D, wdt)[:2] + weights(rng, D, S, wdt)[:2]
+    x = rng.standard_normal((B, D)).astype(np.float32)
+    res0 = bf(rng.standard_normal((B, D)))
+    pool = np.arange(E // 2)
+    sel = np.stack([np.concatenate([[0], rng.permutation(pool[1:])[:K - 1]]) for _ in range(B)]).astype(np.int32)
+    probs = rng.uniform(0.05, 0.3, (B, K)).astype(np.float32)
+    h0, r0, _ = run_moe(hip, 0, B, D, E, K, I, S, wdt, x, sel, probs, res0, w)
+    h2, r2, live = run_moe(hip, 2, B, D, E, K, I, S, wdt, x, sel, probs, res0, w)
+    P = K * I + S
+    h0, h2 = h0.reshape(B, P), h2.reshape(B, P)
+    scale = np.abs(h0).max(axis=1, keepdims=True)
+    err = np.abs(h2 - h0) / scale
+    assert err.max() <= 1e-4, f"h: max relative error {err.max():.3g}"
+    f0, f2, fr = unbf(r0), unbf(r2), unbf(res0).reshape(-1)
+    bound = 2.0 ** -6 * (np.abs(fr) + np.abs(f0)) + 1e-6
+    assert (np.abs(f2 - f0) <= bound).all(), f"residual: max diff {np.abs(f2 - f0).max():.3g}"
+    assert (r0 == r2).mean() >= 0.95, f"residual: only {(r0 == r2).mean():.3f} equal"
     assert live == len(np.unique(sel)), (live, len(np.unique(sel)))
 
 

@@ -43,8 +43,9 @@ class DecodeConfig(C.Structure):
         "max_seq", "batch", "wdtype", "adtype")] + [
         ("eps", C.c_float), ("rope_theta", C.c_float), ("init_std", C.c_float)] + [
         (n, C.c_uint32) for n in ("kv_lora", "d_nope", "d_rope", "d_v", "n_experts",
-                                  "n_shared", "top_k", "moe_inter", "first_dense", "step_mode")] + [
-        ("reserved", C.c_uint32 * 7)]
+                                  "n_shared", "top_k", "moe_inter", "first_dense", "step_mode",
+                                  "moe_mode")] + [
+        ("reserved", C.c_uint32 * 6)]
 
 
 class Uop(C.Structure):

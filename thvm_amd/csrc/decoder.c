@@ -189,6 +189,10 @@ static int cfg_check(const ThvmDecodeConfig *c) {
     hb_set_error("decoder: step_mode 1 (persistent step) is for the LLAMA architecture");
     return -1;
   }
+  if (c->moe_mode > 2) {
+    hb_set_error("decoder: moe_mode is 0 (auto), 1 (VALU grouped) or 2 (MFMA grouped)");
+    return -1;
+  }
   if (c->arch == THVM_ARCH_DSV2) {
     if (!c->n_layers || !c->dim || !c->n_heads || !c->vocab || !c->max_seq || !c->batch ||
         !c->kv_lora || !c->d_nope || !c->d_rope || !c->d_v || !c->n_experts || !c->top_k ||
@@ -712,7 +716,10 @@ static int build_dsv2(Decoder *d) {
     return -1;
   /* batches above 4 rows: expert-grouped MoE scratch and its live-expert
    * counter; projections on the MFMA GEMM (bf16 inputs from separate norms) */
-  const int grp = B > 4;
+  /* (the MFMA form takes D in multiples of 128 and I, S of 64 for fp8
+   * weights, 64 and 32 for bf16; other shapes run the VALU form) */
+  const u32 mk = wdt == THVM_DT_FP8E4M3 ? 128 : 64;
+  const int grp = B <= 4 ? 0 : (c->moe_mode == 1 || D % mk || I % (mk / 2) || S % (mk / 2)) ? 1 : 2;
   if (grp && (!tens_new(d, "moe.plan", THVM_DT_INT32, thvm_k_moe_plan_bytes(B, E, K)) ||
               !tens_new(d, "moe.part", THVM_DT_FP32, thvm_k_moe_part_bytes(B, K, D)) ||
               !tens_new(d, "moe.live", THVM_DT_INT32, 4)))

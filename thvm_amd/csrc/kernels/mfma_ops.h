@@ -1,0 +1,36 @@
+// mfma_ops.h -- gfx950 MFMA operand helpers shared by the small-M GEMM and
+// the expert-grouped MoE: exact fp8 e4m3 -> 16-bit operand decode and the
+// 16x16x32 bf16 / f16 MFMA with f32 accumulation.
+#pragma once
+#include "dev_common.h"
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+
+enum { GW_F16 = 0, GW_BF16 = 1, GW_FP8 = 2 };   // weight storage
+enum { GX_BF16 = 0, GX_F16 = 1 };               // x storage = MFMA operand type
+
+// four e4m3 bytes -> four 16-bit operand values (two u32), exact
+template <int XT>
+__device__ __forceinline__ void fp8x4_op(uint32_t w, uint32_t &lo, uint32_t &hi) {
+  typedef float f2_t __attribute__((ext_vector_type(2)));
+  f2_t a = __builtin_amdgcn_cvt_pk_f32_fp8(w, false);
+  f2_t b = __builtin_amdgcn_cvt_pk_f32_fp8(w, true);
+  if (XT == GX_BF16) {   // an e4m3 value has <= 4 significant bits: truncation is exact
+    lo = (__float_as_uint(a[0]) >> 16) | (__float_as_uint(a[1]) & 0xffff0000u);
+    hi = (__float_as_uint(b[0]) >> 16) | (__float_as_uint(b[1]) & 0xffff0000u);
+  } else {               // and is exact in fp16 (normal range 2^-14..2^15)
+    lo = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(a[0], a[1]));
+    hi = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(b[0], b[1]));
+  }
+}
+
+template <int XT>
+__device__ __forceinline__ f32x4_t mfma16(const uint4 &A, const uint4 &B, f32x4_t c) {
+  if (XT == GX_BF16)
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, A),
+                                                   __builtin_bit_cast(bf16x8_t, B), c, 0, 0, 0);
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8_t, A),
+                                                __builtin_bit_cast(f16x8_t, B), c, 0, 0, 0);
+}

@@ -19,6 +19,7 @@
 //     the reference's order (routed slots ascending, then shared) and the
 //     residual add rounds like the reference's mm-out + add chain.
 #include "dev_common.h"
+#include "mfma_ops.h"
 #include "../kern_api.h"
 #include "launch.h"
 #include <stdio.h>
@@ -387,6 +388,167 @@ __global__ __launch_bounds__(MOE_THREADS) void k_moe_down_g(ThvmMoeArgs a) {
   }
 }
 
+// ---- expert-grouped form on MFMA (grouped = 2) ----------------------------
+// The same plan / part contract as the VALU grouped kernels, with each
+// expert's rows as a small GEMM on v_mfma_f32_16x16x32_bf16: the weights are
+// the A operand (NT 16-row tiles per block, fp8 decoded exactly into bf16),
+// 16 of the expert's routed batch rows the B operand (blockIdx.z picks which
+// 16: column j is the plan's (16 z + j)-th row; columns past the row count
+// read zero through an out-of-range buffer offset and are never stored).
+// Gate/up (KIND 0): B = x rounded to bf16, the experts' input dtype, one MFMA
+// per 32 k.  Down (KIND 1): B = the f32 h split into bf16 hi + lo, two MFMAs
+// per 32 k, so h keeps about 16 significant bits.  The MM_WAVES waves split K
+// into contiguous slices and keep NU steps of loads in flight (a step
+// is consumed, then the slot refilled); steps past a wave's slice read zero,
+// so the loop is straight-line code.  Partial tiles are summed in wave order
+// through LDS; the epilogue is the VALU kernels' (scale, silu(g)*u into h /
+// the scaled down value into part).
+// A lane (li = lane & 15, lg = lane >> 4) supplies row li, k in
+// [KL lg, KL lg + KL) of each step to both operands (KL = LB weight bytes
+// per lane as elements), 8 k per MFMA; a result tile's entry (weight row ii,
+// column m) is lane (ii / 4) * 16 + m, element ii % 4.  Measured at the C5
+// batch-32 shape: gate/up fastest with 32-byte lanes and one step in flight
+// (whole 128-byte lines per row), down with 16-byte lanes and two steps.
+#ifndef MM_WAVES
+#define MM_WAVES 4
+#endif
+#ifndef MM_NT
+#define MM_NT 4         /* 16-row weight tiles per block */
+#endif
+template <int KIND, bool FP8, int LB, int NU>
+__global__ __launch_bounds__(64 * MM_WAVES) void k_moe_mm(ThvmMoeArgs a) {
+  constexpr int NT = MM_NT;
+  __shared__ float4 red[MM_WAVES * NT * 64];
+  const uint32_t e = blockIdx.y, D = a.D, I = a.I, K = a.K, S = a.S;
+  const bool shared = e == a.E;
+  const uint32_t nrows = shared ? a.B : (uint32_t)a.plan[e];
+  const uint32_t NR = KIND == 0 ? (shared ? 2 * S : 2 * I) : D;      // weight rows
+  const uint32_t KK = KIND == 0 ? D : (shared ? S : I);              // reduction length
+  const uint32_t n0 = blockIdx.x * 16u * NT, c0 = blockIdx.z * 16u;
+  if (c0 >= nrows || n0 >= NR) return;                                // block-uniform
+  const int32_t *lst = a.plan + a.E + (uint64_t)e * a.B * K;
+  const uint32_t P = K * I + S;
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, li = lane & 15, lg = lane >> 4;
+  // per step a lane reads LB contiguous weight bytes of its row (k = KL lg ..
+  // KL lg + KL - 1), the 4 lanes of a row 4 LB bytes; KL / 8 MFMAs per tile
+  constexpr uint32_t KL = FP8 ? LB : LB / 2, KS = 4 * KL, NMF = KL / 8, NC = LB / 16;
+  const uint64_t rowb = (uint64_t)KK * (FP8 ? 1 : 2);
+  // this block's weight rows (rows past NR read zero)
+  const char *wbase = KIND == 0 ? (shared ? (const char *)a.wgu_s : (const char *)a.wgu_e + (uint64_t)e * 2 * I * rowb)
+                                : (shared ? (const char *)a.wd_s : (const char *)a.wd_e + (uint64_t)e * D * rowb);
+  const buf_t wrs = buf_rsrc(wbase + n0 * rowb, (uint32_t)(min(NR - n0, 16u * NT) * rowb));
+  uint32_t wo[NT];
+#pragma unroll
+  for (int t = 0; t < NT; t++) wo[t] = (uint32_t)((16u * t + li) * rowb) + lg * LB;
+  // this lane's x / h row (byte offset; out of range for columns past nrows)
+  const buf_t xrs = KIND == 0 ? buf_rsrc(a.x, a.B * D * 4) : buf_rsrc(a.h, a.B * P * 4);
+  uint32_t xo = BUF_OOB;
+  if (c0 + li < nrows) {
+    const uint32_t ent = shared ? c0 + li : (uint32_t)lst[c0 + li];
+    const uint32_t b = shared ? ent : ent / K, slot = shared ? 0 : ent % K;
+    xo = (KIND == 0 ? b * D : b * P + (shared ? K * I : slot * I)) * 4 + lg * KL * 4;
+  }
+  const uint32_t NS = KK / KS;
+  const uint32_t s0 = (uint32_t)(((uint64_t)NS * wv) / MM_WAVES), s1 = (uint32_t)(((uint64_t)NS * (wv + 1)) / MM_WAVES);
+  f32x4_t acc[NT];
+#pragma unroll
+  for (int t = 0; t < NT; t++) acc[t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  uint4 wq[NU][NT][NC], xq[NU][KL / 4];
+  auto load = [&](int u, uint32_t st) {
+    const bool in = st < s1;
+    const uint32_t so = in ? st * 4 * LB : BUF_OOB;                   // 4 LB weight bytes per row per step
+#pragma unroll
+    for (int t = 0; t < NT; t++)
+#pragma unroll
+      for (int jj = 0; jj < (int)NC; jj++) wq[u][t][jj] = buf_ld_stream16(wrs, wo[t] + so + jj * 16);
+    const uint32_t xs = in && xo != BUF_OOB ? xo + st * KS * 4 : BUF_OOB;
+#pragma unroll
+    for (int q = 0; q < (int)KL / 4; q++) xq[u][q] = buf_ld16(xrs, xs + 16 * q);
+  };
+  auto compute = [&](int u) {
+#pragma unroll
+    for (int j = 0; j < (int)NMF; j++) {
+      const float *xf = (const float *)&xq[u][2 * j];
+      uint32_t hb[4], lb[4];
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        const bf16_t h0 = f2bf(xf[2 * i]), h1 = f2bf(xf[2 * i + 1]);
+        hb[i] = (uint32_t)h0 | ((uint32_t)h1 << 16);
+        if (KIND == 1) {
+          const bf16_t l0 = f2bf(xf[2 * i] - bf2f(h0)), l1 = f2bf(xf[2 * i + 1] - bf2f(h1));
+          lb[i] = (uint32_t)l0 | ((uint32_t)l1 << 16);
+        }
+      }
+      const uint4 H = make_uint4(hb[0], hb[1], hb[2], hb[3]), L = make_uint4(lb[0], lb[1], lb[2], lb[3]);
+#pragma unroll
+      for (int t = 0; t < NT; t++) {
+        uint4 A;
+        if (FP8) {
+          const uint4 q = wq[u][t][j / 2];
+          fp8x4_op<GX_BF16>(j % 2 ? q.z : q.x, A.x, A.y);
+          fp8x4_op<GX_BF16>(j % 2 ? q.w : q.y, A.z, A.w);
+        } else {
+          A = wq[u][t][j];
+        }
+        acc[t] = mfma16<GX_BF16>(A, H, acc[t]);
+        if (KIND == 1) acc[t] = mfma16<GX_BF16>(A, L, acc[t]);
+      }
+    }
+  };
+#pragma unroll
+  for (int u = 0; u < NU; u++) load(u, s0 + u);
+  for (uint32_t sb = s0; sb < s1; sb += NU) {
+#pragma unroll
+    for (int u = 0; u < NU; u++) {
+      compute(u);
+      load(u, sb + u + NU);
+    }
+  }
+#pragma unroll
+  for (int t = 0; t < NT; t++) {
+    const f32x4_t v = acc[t];
+    red[((uint32_t)wv * NT + t) * 64 + lane] = make_float4(v[0], v[1], v[2], v[3]);
+  }
+  __syncthreads();
+  const uint32_t ncols = min(nrows - c0, 16u);
+  const uint32_t per = KIND == 0 ? 8 * NT : 16 * NT;                  // row pairs / rows per column
+  for (uint32_t task = threadIdx.x; task < per * ncols; task += 64 * MM_WAVES) {
+    const uint32_t p = task % per, m = task / per;
+    const uint32_t ent = shared ? c0 + m : (uint32_t)lst[c0 + m];
+    const uint32_t b = shared ? ent : ent / K, slot = shared ? 0 : ent % K;
+    auto tile_val = [&](uint32_t ii_all) {                            // sum over waves, in order
+      const uint32_t t = ii_all / 16, ii = ii_all % 16, ln = (ii / 4) * 16 + m, r = ii % 4;
+      float sum = 0.0f;
+#pragma unroll
+      for (int w = 0; w < MM_WAVES; w++) {
+        const float4 q = red[((uint32_t)w * NT + t) * 64 + ln];
+        sum += r == 0 ? q.x : r == 1 ? q.y : r == 2 ? q.z : q.w;
+      }
+      return sum;
+    };
+    if (KIND == 0) {
+      const uint32_t i0 = 2 * p, n = n0 + i0;
+      if (n >= NR) continue;                                          // NR is even
+      float G = tile_val(i0), U = tile_val(i0 + 1);
+      const float *scp = shared ? a.sgu_s : a.sgu_e;
+      if (scp) {
+        const uint64_t r0 = shared ? (uint64_t)n : (uint64_t)e * 2 * I + n;
+        G *= scp[r0];
+        U *= scp[r0 + 1];
+      }
+      a.h[(uint64_t)b * P + (shared ? K * I : slot * I) + n / 2] = silu_f(G) * U;
+    } else {
+      const uint32_t n = n0 + p;
+      if (n >= NR) continue;
+      float sv = tile_val(p);
+      const float *scl = shared ? a.sd_s : a.sd_e;
+      if (scl) sv *= shared ? scl[n] : scl[(uint64_t)e * D + n];
+      const uint64_t o = shared ? (uint64_t)a.B * K * D + (uint64_t)b * D + n : ((uint64_t)b * K + slot) * D + n;
+      a.part[o] = sv;
+    }
+  }
+}
+
 // res[b][d] = bf16(res + bf16(sum_slot probs * part + shared)), k_moe_down's
 // sum order; grid (ceil(D / 256), B)
 __global__ __launch_bounds__(256) void k_moe_combine(ThvmMoeArgs a) {
@@ -478,6 +640,7 @@ static moe_fn pick_gateup_g(uint32_t nch, uint32_t *ppw) {
 }
 
 static int moe_grouped_check(const ThvmMoeArgs *a, int gateup, char *err, int errlen) {
+  if (a->grouped > 2) { snprintf(err, errlen, "moe: grouped is 0, 1 (VALU) or 2 (MFMA)"); return -1; }
   if ((uint64_t)a->B * a->K > MOE_PLAN_MAX) {
     snprintf(err, errlen, "moe: grouped form takes B*K <= %d routing entries", MOE_PLAN_MAX);
     return -1;
@@ -490,8 +653,40 @@ static int moe_grouped_check(const ThvmMoeArgs *a, int gateup, char *err, int er
   return 0;
 }
 
+static int moe_mm_launch(const ThvmMoeArgs *a, int gateup, hipStream_t s, char *err, int errlen) {
+  const bool f8 = a->wdt == THVM_DT_FP8E4M3;
+  // k per step: gate/up 32-byte lanes (128 k fp8, 64 k bf16), down 16-byte
+  const uint32_t ks = gateup ? (f8 ? 128 : 64) : (f8 ? 64 : 32);
+  if (gateup ? a->D % ks : (a->I % ks || a->S % ks)) {
+    snprintf(err, errlen, "moe: the MFMA grouped form needs %s multiples of %u", gateup ? "D" : "I and S", ks);
+    return -1;
+  }
+  const moe_fn f = gateup ? (f8 ? k_moe_mm<0, true, 32, 1> : k_moe_mm<0, false, 32, 1>)
+                          : (f8 ? k_moe_mm<1, true, 16, 2> : k_moe_mm<1, false, 16, 2>);
+  // 16 routed rows per column group (blockIdx.z): a group past an expert's
+  // row count exits at once; groups beyond the first re-read that expert's
+  // weights, which only experts with more than 16 rows need
+  const uint32_t nr = gateup ? 2 * (a->I > a->S ? a->I : a->S) : a->D;
+  const dim3 grid((nr + 16 * MM_NT - 1) / (16 * MM_NT), a->E + (a->S ? 1 : 0), (a->B + 15) / 16);
+  const uint32_t lds = 0;
+  if ((uint64_t)a->B * (a->K * a->I + a->S) * 4 >= BUF_OOB || (uint64_t)a->B * a->D * 4 >= BUF_OOB) {
+    snprintf(err, errlen, "moe: x / h above 2 GiB");
+    return -1;
+  }
+  if (gateup) thvm_launch(true, false, k_moe_plan, dim3(1), dim3(64), 0, s, *a);
+  thvm_launch(!gateup, gateup, f, grid, dim3(64 * MM_WAVES), lds, s, *a);
+  if (!gateup) thvm_launch(false, true, k_moe_combine, dim3((a->D + 255) / 256, a->B), dim3(256), 0, s, *a);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) { snprintf(err, errlen, "moe mm launch: %s", hipGetErrorString(e)); return -1; }
+  return 0;
+}
+
 extern "C" int thvm_k_moe_gateup(const ThvmMoeArgs *a, hipStream_t s, char *err, int errlen) {
   if (moe_check(a, 1, err, errlen)) return -1;
+  if (a->grouped == 2) {
+    if (moe_grouped_check(a, 1, err, errlen)) return -1;
+    return moe_mm_launch(a, 1, s, err, errlen);
+  }
   if (a->grouped) {
     if (moe_grouped_check(a, 1, err, errlen)) return -1;
     const uint32_t nch = a->D * (a->wdt == THVM_DT_FP8E4M3 ? 1 : 2) / 16;
@@ -526,6 +721,10 @@ extern "C" int thvm_k_moe_gateup(const ThvmMoeArgs *a, hipStream_t s, char *err,
 
 extern "C" int thvm_k_moe_down(const ThvmMoeArgs *a, hipStream_t s, char *err, int errlen) {
   if (moe_check(a, 0, err, errlen)) return -1;
+  if (a->grouped == 2) {
+    if (moe_grouped_check(a, 0, err, errlen)) return -1;
+    return moe_mm_launch(a, 0, s, err, errlen);
+  }
   if (a->grouped) {
     if (moe_grouped_check(a, 0, err, errlen)) return -1;
     const uint32_t wsz = a->wdt == THVM_DT_FP8E4M3 ? 1 : 2;
