@@ -204,6 +204,25 @@ __device__ __forceinline__ bool gemv_core(const ThvmGemvArgs &a, unsigned char *
   // nthr-thread block)
   const uint32_t NVt = K / VE;           // x vectors per row
   const uint32_t tid = threadIdx.x < nthr ? threadIdx.x : NVt;
+  // a fused norm's gain (and LayerNorm bias) vectors: loaded with the first
+  // x loads, not after the reduction, so they cost no round trip of their
+  // own (clamped indices; lanes past the row never use them)
+  constexpr int NVN = XREG / VE;
+  float gw[NVN][VE], gb[NVN][VE];
+  if (a.norm != 0) {
+    const bool hw = a.norm_w != nullptr, hb = a.norm == 2 && a.norm_b != nullptr;
+#pragma unroll
+    for (int j = 0; j < NVN; j++) {
+      const uint32_t v = tid + j * nthr, vc = v < NVt ? v : 0;
+#pragma unroll
+      for (int i = 0; i < VE; i += 4) {
+        const float4 t = hw ? *(const float4 *)(a.norm_w + vc * VE + i) : make_float4(1.f, 1.f, 1.f, 1.f);
+        gw[j][i] = t.x; gw[j][i + 1] = t.y; gw[j][i + 2] = t.z; gw[j][i + 3] = t.w;
+        const float4 u = hb ? *(const float4 *)(a.norm_b + vc * VE + i) : make_float4(0.f, 0.f, 0.f, 0.f);
+        gb[j][i] = u.x; gb[j][i + 1] = u.y; gb[j][i + 2] = u.z; gb[j][i + 3] = u.w;
+      }
+    }
+  }
   for (int m = 0; m < M; m++) {
     const void *xr = xrow(m);
     if (a.norm == 0) {
@@ -261,21 +280,12 @@ __device__ __forceinline__ bool gemv_core(const ThvmGemvArgs &a, unsigned char *
       for (int j = 0; j < NV; j++) {
         const uint32_t v = tid + j * nthr;
         if (v < NVt) {
-          float gw[VE], gb[VE];
-#pragma unroll
-          for (int i = 0; i < VE; i += 4) {
-            float4 t = a.norm_w ? *(const float4 *)(a.norm_w + v * VE + i) : make_float4(1.f, 1.f, 1.f, 1.f);
-            gw[i] = t.x; gw[i + 1] = t.y; gw[i + 2] = t.z; gw[i + 3] = t.w;
-            float4 u = (a.norm == 2 && a.norm_b) ? *(const float4 *)(a.norm_b + v * VE + i)
-                                                 : make_float4(0.f, 0.f, 0.f, 0.f);
-            gb[i] = u.x; gb[i + 1] = u.y; gb[i + 2] = u.z; gb[i + 3] = u.w;
-          }
 #pragma unroll
           for (int i = 0; i < VE; i++) {
             // (x - mean) * inv * w (+ b), the norm kernel's own formula
             float val = (xv[j][i] - mean) * inv;
-            if (a.norm_w) val = val * gw[i];
-            if (a.norm == 2 && a.norm_b) val = val + gb[i];
+            if (a.norm_w) val = val * gw[j][i];
+            if (a.norm == 2 && a.norm_b) val = val + gb[j][i];
             xs_store<XT>(xs_raw, xs_index<XT, E>(K, C, m, v * VE + i), rnd_x<XD>(val));
           }
         }

@@ -74,11 +74,15 @@ __global__ __launch_bounds__(ROW_THREADS) void k_norm_reg(ThvmNormArgs a) {
   const uint32_t m = blockIdx.x;
   const uint64_t xo = (uint64_t)m * a.ldx, yo = (uint64_t)m * a.ldy;
   const float invK = 1.0f / (float)a.K;
-  float xv[NORM_REG];
+  float xv[NORM_REG], wv[NORM_REG], bv[NORM_REG];
+  // gain and bias loads go out with the x loads (clamped indices), so they
+  // cost no round trip after the reduction
 #pragma unroll
   for (int i = 0; i < NORM_REG; i++) {
-    const uint32_t e = threadIdx.x + i * ROW_THREADS;
+    const uint32_t e = threadIdx.x + i * ROW_THREADS, ec = e < a.K ? e : 0;
     xv[i] = e < a.K ? ld_a(a.x, xo + e, a.xdt) : 0.0f;
+    wv[i] = a.w ? a.w[ec] : 1.0f;
+    bv[i] = a.layernorm && a.b ? a.b[ec] : 0.0f;
   }
   float mean = 0.0f, s2 = 0.0f;
   if (a.layernorm) {
@@ -101,8 +105,8 @@ __global__ __launch_bounds__(ROW_THREADS) void k_norm_reg(ThvmNormArgs a) {
     const uint32_t e = threadIdx.x + i * ROW_THREADS;
     if (e < a.K) {
       float v = (xv[i] - mean) * inv;
-      if (a.w) v = v * a.w[e];
-      if (a.layernorm && a.b) v = v + a.b[e];
+      if (a.w) v = v * wv[i];
+      if (a.layernorm && a.b) v = v + bv[i];
       st_a(a.y, yo + e, a.ydt, v);
     }
   }
