@@ -471,6 +471,74 @@ def test_attention_decode(hip, H, Hkv, hd, L, cdt):
     assert not ctr.any(), ctr
 
 
+def run_attn(hip, qs, ks, vs, B, H, Hkv, hd, ms, L, cdt, part=None, **kw):
+    nsplit = (ms + 63) // 64
+    out = hip.Buffer(B * H * hd * SZ[cdt])
+    if part is None:
+        part = hip.Buffer(B * H * nsplit * (hd + 2) * 4 + B * Hkv * 4)
+    scale = float(np.float32(1.0 / np.sqrt(hd)))
+    hip.builtin("attn", [out, up(hip, qs), up(hip, ks), up(hip, vs),
+                         up(hip, np.array([L], np.int32)), part],
+                b=B, h=H, hkv=Hkv, hd=hd, maxseq=ms, chunk=64, nsplit=nsplit, qt=cdt,
+                ct=cdt, ot=cdt, scale=scale, **kw)
+    want = np.empty(B * H * hd, NP_STORE[cdt])
+    O.oracle().or_attn_decode(want.ctypes.data, cdt, qs.ctypes.data, cdt, ks.ctypes.data,
+                              vs.ctypes.data, cdt, B, H, Hkv, hd, ms, L, scale)
+    return O.decode(out.read(NP_STORE[cdt]), cdt), O.decode(want, cdt)
+
+
+def attn_close(got, ww, cdt):
+    if cdt == DT_F32:   # f32: 1e-5 relative to the magnitude of the V rows mixed
+        return np.all(np.abs(got - ww) <= 1e-5 * (np.abs(ww) + 1.0))
+    return np.all(np.abs(got - ww) <= 2.0 ** -7 * np.abs(ww) + 2e-3)
+
+
+@pytest.mark.parametrize("cdt", [DT_BF16, DT_F32])
+@pytest.mark.parametrize("H,Hkv,hd", [(32, 8, 128), (4, 4, 64), (8, 2, 128)])
+@pytest.mark.parametrize("L", [1, 63, 64, 65, 129, 200, 256])
+@pytest.mark.parametrize("cpb", [2, 4])
+def test_attention_multi_chunk(hip, H, Hkv, hd, L, cdt, cpb):
+    """Blocks of 2 or 4 consecutive chunks (online softmax per row group, one
+    partial per block) against the oracle, at the one-chunk form's bars;
+    lengths inside, at and past chunk and block edges."""
+    B, ms = 3, 256
+    say(f"case: attn multi-chunk cpb={cpb} H={H} Hkv={Hkv} hd={hd} L={L} dt={cdt}")
+    rng = np.random.default_rng(H * 1000 + L + 7 * cpb)
+    qs, _ = rand_store(rng, (B, H, hd), cdt)
+    ks, _ = rand_store(rng, (B, Hkv, ms, hd), cdt)
+    vs, _ = rand_store(rng, (B, Hkv, ms, hd), cdt)
+    got, ww = run_attn(hip, qs, ks, vs, B, H, Hkv, hd, ms, L, cdt, cpb=cpb)
+    assert attn_close(got, ww, cdt), np.max(np.abs(got - ww))
+
+
+def test_attention_multi_chunk_auto_repeated(hip):
+    """The batched C4 head shape at 12 rows picks 4 chunks per block by
+    itself; one partial buffer across launches at changing lengths (stale
+    partials of a longer launch are never read)."""
+    B, H, Hkv, hd, ms, cdt = 12, 32, 8, 128, 2176, DT_BF16
+    say("case: attn multi-chunk auto, 12 rows, 5 launches")
+    rng = np.random.default_rng(9)
+    qs, _ = rand_store(rng, (B, H, hd), cdt)
+    ks, _ = rand_store(rng, (B, Hkv, ms, hd), cdt)
+    vs, _ = rand_store(rng, (B, Hkv, ms, hd), cdt)
+    nsplit = (ms + 63) // 64
+    part = hip.Buffer(B * H * nsplit * (hd + 2) * 4 + B * Hkv * 4)
+    for L in (2100, 700, 2176, 1, 257):
+        got, ww = run_attn(hip, qs, ks, vs, B, H, Hkv, hd, ms, L, cdt, part=part)
+        assert attn_close(got, ww, cdt), (L, np.max(np.abs(got - ww)))
+
+
+def test_attention_cpb_errors(hip):
+    B, H, Hkv, hd, ms, cdt = 1, 16, 2, 64, 128, DT_BF16
+    z = np.zeros(B * H * hd, np.uint16)
+    kv = np.zeros(B * Hkv * ms * hd, np.uint16)
+    for kw in (dict(cpb=3), dict(cpb=8), dict(cpb=2, fused=1)):
+        with pytest.raises(hip.ThvmHipError):
+            run_attn(hip, z, kv, kv, B, H, Hkv, hd, ms, 5, cdt, **kw)
+    with pytest.raises(hip.ThvmHipError):        # 8 heads per kv head: one chunk per block only
+        run_attn(hip, z, kv, kv, B, H, Hkv, hd, ms, 5, cdt, cpb=2)
+
+
 def test_attention_fused_repeated(hip):
     """Ten launches on one partial buffer at changing lengths: every merge
     finds its counter at zero and the outputs match the two-kernel form."""

@@ -255,7 +255,7 @@ int hb_builtin_launch(const char *program, const u32 *ids, u32 n, int check_only
          spec_u32(&sp, "maxseq", &a.max_seq, 1, 0) || spec_u32(&sp, "chunk", &a.chunk, 0, 64) ||
          spec_u32(&sp, "qt", &a.qdt, 0, THVM_DT_BF16) || spec_u32(&sp, "ct", &a.cdt, 0, THVM_DT_BF16) ||
          spec_u32(&sp, "ot", &a.odt, 0, THVM_DT_BF16) || spec_f32(&sp, "scale", &a.scale, 1, 0) ||
-         spec_u32(&sp, "fused", &a.fused, 0, 0));
+         spec_u32(&sp, "fused", &a.fused, 0, 0) || spec_u32(&sp, "cpb", &a.cpb, 0, 0));
     if (a.chunk == 0) { hb_set_error("builtin attn: chunk=0"); return -1; }
     NEED(spec_u32(&sp, "nsplit", &a.n_split, 0, (a.max_seq + a.chunk - 1) / a.chunk));
     if (!is_act(a.qdt) || !is_act(a.odt)) { hb_set_error("builtin attn: bad dtypes"); return -1; }

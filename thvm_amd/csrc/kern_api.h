@@ -102,6 +102,10 @@ typedef struct ThvmAttnArgs {
   float scale;             /* 1/sqrt(hd)                                     */
   uint32_t fused;          /* 1: split and merge in one launch (the last unit
                             * of a (row, kv head) merges); 0: two launches   */
+  uint32_t cpb;            /* chunks per split block: 0 picks from the unit
+                            * count, 1 one chunk per block, 2 or 4 a block
+                            * runs that many consecutive chunks (two
+                            * launches only); the partials are per block   */
 } ThvmAttnArgs;
 int thvm_k_attn_decode(const ThvmAttnArgs *a, hipStream_t s, char *err, int errlen);
 uint64_t thvm_k_attn_part_bytes(uint32_t B, uint32_t H, uint32_t Hkv, uint32_t hd, uint32_t n_split);

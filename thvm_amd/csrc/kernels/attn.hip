@@ -80,7 +80,188 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attn_fused(ThvmAttnArgs a) {
   }
 }
 
+// Batched split: one block runs CPB consecutive chunks of a (kv head, row),
+// the next chunk's K/V loads in flight while the current one is consumed.
+// The per-chunk work of the one-chunk unit is dominated by its fixed part at
+// large unit counts (the q decode, the wave-wide max and the row-group
+// shuffles, the LDS merge of the 8 waves): here q is decoded once, each row
+// group (LPR lanes holding one cache row) keeps its own running max, sum and
+// accumulator across the block's chunks (online softmax: rescaled by
+// exp2(m_old - m_new) when the max grows), and the row groups and waves are
+// combined once per block.  The block writes one partial (acc, m, l) at slot
+// blockIdx.y of the merge's [n_split] rows; the merge reads ceil(L/(64 CPB))
+// of them.  Used when B * Hkv * n_split is large (batched decode).
+template <int HD, int G, int AT, int CPB>
+__global__ __launch_bounds__(ATT_THREADS, 4) void k_attn_multi(ThvmAttnArgs a) {   // 2 blocks per CU
+  __shared__ AttnLds<HD, G> s;
+  typedef AttnSplit<HD, G, AT, false> SU;
+  constexpr int EPL = SU::EPL, LPR = SU::LPR, RPW = SU::RPW, PPW = SU::PPW, IT = SU::IT, ES = SU::ES;
+  const uint32_t kvh = blockIdx.x, grp = blockIdx.y, b = blockIdx.z;
+  const int32_t L = a.len[0];
+  const uint32_t c0 = grp * CPB;
+  if ((int32_t)(c0 * ATT_CHUNK) >= L) return;      // the merge reads only live partials
+  const int tid = threadIdx.x, wv = tid >> 6, lane = lane_id();
+  const int rg = lane / LPR, li = lane % LPR;
+  const uint32_t d0 = li * EPL;
+  // this (row, kv head)'s cache rows as buffer resources: rows past L read
+  // zero through an out-of-range offset, with no memory access, so the loads
+  // of a chunk past the block's last are issued unconditionally
+  const uint64_t cbase = ((uint64_t)b * a.Hkv + kvh) * a.max_seq * HD * ES;
+  const buf_t krs = buf_rsrc((const char *)a.kcache + cbase, a.max_seq * HD * ES);
+  const buf_t vrs = buf_rsrc((const char *)a.vcache + cbase, a.max_seq * HD * ES);
+  uint4 kq[2][IT], vq[2][IT];
+  bool ok[2][IT];
+  auto issue = [&](int buf, uint32_t c) {
+#pragma unroll
+    for (int it = 0; it < IT; it++) {
+      const uint32_t j = c * ATT_CHUNK + wv * PPW + it * RPW + rg;
+      ok[buf][it] = (int32_t)j < L && j < a.max_seq;
+      const uint32_t off = ok[buf][it] ? (j * HD + d0) * ES : BUF_OOB;
+      kq[buf][it] = buf_ld_stream16(krs, off);
+      vq[buf][it] = buf_ld_stream16(vrs, off);
+    }
+  };
+  issue(0, c0);
+  // q, decoded and pre-scaled into the log2 domain once
+  const float qs = a.scale * LOG2E;
+  float qf[G][EPL];
+#pragma unroll
+  for (int g = 0; g < G; g++) {
+    const uint64_t qo = ((uint64_t)b * a.H + kvh * G + g) * HD + d0;
+    chunk_f<AT>(ld16((const char *)a.q + qo * ES), qf[g]);
+#pragma unroll
+    for (int i = 0; i < EPL; i++) qf[g][i] *= qs;
+  }
+  float m[G], l[G], acc[G][EPL];
+#pragma unroll
+  for (int g = 0; g < G; g++) {
+    m[g] = -INFINITY;
+    l[g] = 0.0f;
+#pragma unroll
+    for (int i = 0; i < EPL; i++) acc[g][i] = 0.0f;
+  }
+  auto consume = [&](int buf) {
+    float sc[IT][G];
+#pragma unroll
+    for (int it = 0; it < IT; it++) {
+      float kf[EPL];
+      chunk_f<AT>(kq[buf][it], kf);
+#pragma unroll
+      for (int g = 0; g < G; g++) {
+        float sv = 0.0f;
+#pragma unroll
+        for (int i = 0; i < EPL; i++) sv += qf[g][i] * kf[i];
+        sv = group_sum<LPR>(sv);
+        sc[it][g] = ok[buf][it] ? sv : -INFINITY;
+      }
+    }
+#pragma unroll
+    for (int g = 0; g < G; g++) {
+      float mn = m[g];
+#pragma unroll
+      for (int it = 0; it < IT; it++) mn = fmaxf(mn, sc[it][g]);
+      const float f = m[g] == -INFINITY ? 0.0f : fexp2(m[g] - mn);
+      l[g] *= f;
+#pragma unroll
+      for (int i = 0; i < EPL; i++) acc[g][i] *= f;
+      m[g] = mn;
+    }
+#pragma unroll
+    for (int it = 0; it < IT; it++) {
+      float vf[EPL];
+      chunk_f<AT>(vq[buf][it], vf);
+#pragma unroll
+      for (int g = 0; g < G; g++) {
+        const float p = (ok[buf][it] && m[g] != -INFINITY) ? fexp2(sc[it][g] - m[g]) : 0.0f;
+        l[g] += p;
+#pragma unroll
+        for (int i = 0; i < EPL; i++) acc[g][i] += p * vf[i];
+      }
+    }
+  };
+  const uint32_t nlive = (uint32_t)((L + ATT_CHUNK - 1) / ATT_CHUNK);
+  const uint32_t nc = min((uint32_t)CPB, nlive - c0);   // block-uniform
+  for (uint32_t c = 0; c < nc; c += 2) {               // two register sets, ping-pong
+    issue(1, c0 + c + 1);
+    consume(0);
+    if (c + 1 >= nc) break;
+    issue(0, c0 + c + 2);
+    consume(1);
+  }
+  // row groups of the wave -> one (m, l, acc) per head: rescale to the wave
+  // max, then sum (all lanes)
+  float mw[G];
+#pragma unroll
+  for (int g = 0; g < G; g++) {
+    float M = m[g];
+#pragma unroll
+    for (int off = LPR; off < 64; off *= 2) M = fmaxf(M, __shfl_xor(M, off));
+    const float f = m[g] == -INFINITY ? 0.0f : fexp2(m[g] - M);
+    l[g] *= f;
+#pragma unroll
+    for (int i = 0; i < EPL; i++) acc[g][i] *= f;
+#pragma unroll
+    for (int off = LPR; off < 64; off *= 2) {
+      l[g] += __shfl_xor(l[g], off);
+#pragma unroll
+      for (int i = 0; i < EPL; i++) acc[g][i] += __shfl_xor(acc[g][i], off);
+    }
+    mw[g] = M;
+  }
+  // waves -> the block's partial, as the one-chunk unit does
+  if (lane == 0) {
+#pragma unroll
+    for (int g = 0; g < G; g++) { s.wm[wv][g] = mw[g]; s.wl[wv][g] = l[g]; }
+  }
+  __syncthreads();
+  {
+    float f[G];
+#pragma unroll
+    for (int g = 0; g < G; g++) {
+      float M = s.wm[0][g];
+#pragma unroll
+      for (int w = 1; w < ATT_WAVES; w++) M = fmaxf(M, s.wm[w][g]);
+      f[g] = mw[g] == -INFINITY ? 0.0f : fexp2(mw[g] - M);
+      if (lane == 0) s.wf[wv][g] = f[g];
+    }
+    if (rg == 0) {
+#pragma unroll
+      for (int g = 0; g < G; g++)
+#pragma unroll
+        for (int i = 0; i < EPL; i++) s.wacc[wv][g][d0 + i] = acc[g][i] * f[g];
+    }
+  }
+  __syncthreads();
+  for (int o = tid; o < G * HD; o += ATT_THREADS) {
+    const int g = o / HD, d = o % HD;
+    float sv = 0.0f, lt = 0.0f, M = s.wm[0][g];
+#pragma unroll
+    for (int w = 0; w < ATT_WAVES; w++) {
+      sv += s.wacc[w][g][d];
+      lt += s.wf[w][g] * s.wl[w][g];
+      M = fmaxf(M, s.wm[w][g]);
+    }
+    float *pp = a.part + (((uint64_t)b * a.H + kvh * G + g) * a.n_split + grp) * (HD + 2);
+    pp[d] = sv;
+    if (d == 0) { pp[HD] = M; pp[HD + 1] = lt; }
+  }
+}
+
 typedef void (*attn_fn)(ThvmAttnArgs);
+// (G = 8 heads per kv head would spill its accumulators: one chunk per block)
+template <int HD, int AT, int CPB>
+static attn_fn attn_pick_multi(uint32_t G) {
+  switch (G) {
+    case 1: return k_attn_multi<HD, 1, AT, CPB>;
+    case 2: return k_attn_multi<HD, 2, AT, CPB>;
+    case 4: return k_attn_multi<HD, 4, AT, CPB>;
+    default: return nullptr;
+  }
+}
+template <int HD, int AT>
+static attn_fn attn_pick_cpb(uint32_t G, uint32_t cpb) {
+  return cpb == 2 ? attn_pick_multi<HD, AT, 2>(G) : attn_pick_multi<HD, AT, 4>(G);
+}
 template <int HD, int AT>
 static attn_fn attn_pick(uint32_t G, bool fused) {
   switch (G) {
@@ -122,14 +303,28 @@ extern "C" int thvm_k_attn_decode(const ThvmAttnArgs *a, hipStream_t s, char *er
   // block per kv head then runs all of its heads' merges, where the merge
   // kernel spreads one head per block.
   const bool fused = a->fused != 0;
+  // chunks per split block: one at small unit counts (every CU needs a
+  // block); at batched shapes 2 or 4, so each block's fixed work is shared
+  // by more cache rows
+  uint32_t cpb = a->cpb;
+  if (cpb > 4 || cpb == 3 || (fused && cpb > 1)) {
+    snprintf(err, errlen, "attn: cpb must be 0, 1, 2 or 4 (1 with fused)");
+    return -1;
+  }
+  if (cpb == 0) {
+    const uint64_t units = (uint64_t)a->B * a->Hkv * a->n_split;
+    cpb = (fused || a->H / a->Hkv > 4) ? 1 : units >= 3072 ? 4 : units >= 1536 ? 2 : 1;
+  }
   attn_fn f = nullptr, fm = nullptr;
   const uint32_t G = a->H / a->Hkv;
   const int at = a->cdt == THVM_DT_BF16 ? AT_BF16 : a->cdt == THVM_DT_FP16 ? AT_F16 : AT_F32;
   if (a->hd == 128) {
-    f = at == AT_BF16 ? attn_pick<128, AT_BF16>(G, fused) : at == AT_F16 ? attn_pick<128, AT_F16>(G, fused) : attn_pick<128, AT_F32>(G, fused);
+    f = cpb > 1 ? (at == AT_BF16 ? attn_pick_cpb<128, AT_BF16>(G, cpb) : at == AT_F16 ? attn_pick_cpb<128, AT_F16>(G, cpb) : attn_pick_cpb<128, AT_F32>(G, cpb))
+        : at == AT_BF16 ? attn_pick<128, AT_BF16>(G, fused) : at == AT_F16 ? attn_pick<128, AT_F16>(G, fused) : attn_pick<128, AT_F32>(G, fused);
     fm = at == AT_BF16 ? k_attn_merge<128, AT_BF16> : at == AT_F16 ? k_attn_merge<128, AT_F16> : k_attn_merge<128, AT_F32>;
   } else if (a->hd == 64) {
-    f = at == AT_BF16 ? attn_pick<64, AT_BF16>(G, fused) : at == AT_F16 ? attn_pick<64, AT_F16>(G, fused) : attn_pick<64, AT_F32>(G, fused);
+    f = cpb > 1 ? (at == AT_BF16 ? attn_pick_cpb<64, AT_BF16>(G, cpb) : at == AT_F16 ? attn_pick_cpb<64, AT_F16>(G, cpb) : attn_pick_cpb<64, AT_F32>(G, cpb))
+        : at == AT_BF16 ? attn_pick<64, AT_BF16>(G, fused) : at == AT_F16 ? attn_pick<64, AT_F16>(G, fused) : attn_pick<64, AT_F32>(G, fused);
     fm = at == AT_BF16 ? k_attn_merge<64, AT_BF16> : at == AT_F16 ? k_attn_merge<64, AT_F16> : k_attn_merge<64, AT_F32>;
   }
   if (!f) {
@@ -140,8 +335,10 @@ extern "C" int thvm_k_attn_decode(const ThvmAttnArgs *a, hipStream_t s, char *er
     snprintf(err, errlen, "attn: partials of 2 GiB or more");
     return -1;
   }
-  thvm_launch(true, fused, f, dim3(a->Hkv, a->n_split, a->B), dim3(ATT_THREADS), 0, s, *a);
-  if (!fused) thvm_launch(false, true, fm, dim3(a->B * a->H), dim3(256), 0, s, *a);
+  ThvmAttnArgs ak = *a;
+  ak.cpb = cpb;
+  thvm_launch(true, fused, f, dim3(a->Hkv, (a->n_split + cpb - 1) / cpb, a->B), dim3(ATT_THREADS), 0, s, ak);
+  if (!fused) thvm_launch(false, true, fm, dim3(a->B * a->H), dim3(256), 0, s, ak);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) { snprintf(err, errlen, "attn launch: %s", hipGetErrorString(e)); return -1; }
   return 0;

@@ -15,8 +15,8 @@
 // scale*log2 e) so the softmax uses the hardware exp2.  Row-group sums use
 // DPP, the 8 waves merge through LDS with one rescale per wave, and the unit
 // writes (acc[hd], m, l) for its split.
-// Merge (batch row b, q head h), 256 threads: the ceil(L/CHUNK) live splits in
-// a fixed order (deterministic).
+// Merge (batch row b, q head h), 256 threads: the ceil(L/(CHUNK*cpb)) live
+// partials in a fixed order (deterministic).
 //
 // COH (persistent kernel): q, the partials and the output are read/written
 // with system-scope accesses, and the cache row L-1 -- appended by another
@@ -281,7 +281,8 @@ __device__ __forceinline__ void attn_merge(const ThvmAttnArgs &a, uint32_t bh, i
                                            bool active, MergeLds &s) {
   constexpr int U4 = HD / 4;
   constexpr int SQ = 256 / U4;
-  uint32_t n_live = L > 0 ? (uint32_t)((L + ATT_CHUNK - 1) / ATT_CHUNK) : 0u;
+  const int32_t span = ATT_CHUNK * (a.cpb > 1 ? (int32_t)a.cpb : 1);   // cache rows per partial
+  uint32_t n_live = L > 0 ? (uint32_t)((L + span - 1) / span) : 0u;
   if (n_live > a.n_split) n_live = a.n_split;
   const uint64_t pbi = (uint64_t)bh * a.n_split * (HD + 2);
   const float *pb = a.part + pbi;
