@@ -17,6 +17,11 @@ LIB = PKG / "lib" / "libthvm_hip.so"
 ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
 
 C_SOURCES = ["hip_backend.c", "hip_custom.c", "decoder.c", "render.c"]
+# (source, object stem, extra flags): the GEMV kernel instances are one unit
+# per (weight type, x type) so the twelve compile in parallel
+GEMV_UNITS = [("kernels/gemv_inst.hip", f"gemv_inst_{w}_{x}",
+               [f"-DGEMV_WT={w}", f"-DGEMV_XD={x}", f"-DGEMV_PICK=gemv_pick_{w}_{x}"])
+              for w in range(4) for x in range(3)]
 HIP_SOURCES = ["kernels/gemv.hip", "kernels/gemm.hip", "kernels/rowops.hip", "kernels/attn.hip",
                "kernels/mla.hip", "kernels/moe.hip", "kernels/step.hip", "kernels/step_m1.hip",
                "kernels/step_m2.hip", "kernels/step_m4.hip"]
@@ -47,14 +52,16 @@ def build(verbose: bool = True) -> Path:
     for s in C_SOURCES:
         o = OBJ / (Path(s).stem + ".o")
         jobs.append(["gcc", *CFLAGS, "-c", str(CSRC / s), "-o", str(o)])
-    for s in HIP_SOURCES:
-        o = OBJ / (Path(s).stem + ".hip.o")
-        jobs.append([f"{ROCM}/bin/hipcc", *HIPFLAGS, "-c", str(CSRC / s), "-o", str(o)])
+    units = [(s, Path(s).stem, []) for s in HIP_SOURCES] + GEMV_UNITS
+    for s, stem, extra in units:
+        o = OBJ / (stem + ".hip.o")
+        jobs.append([f"{ROCM}/bin/hipcc", *HIPFLAGS, *extra, "-c", str(CSRC / s), "-o", str(o)])
+    jobs.sort(key=lambda j: "gemv_inst" not in " ".join(j))    # the long units first
     workers = min(len(jobs), int(os.environ.get("MAX_JOBS", "8")))
     with cf.ThreadPoolExecutor(max_workers=workers) as ex:
         list(ex.map(_run, jobs))
     objs = [str(OBJ / (Path(s).stem + ".o")) for s in C_SOURCES] + \
-           [str(OBJ / (Path(s).stem + ".hip.o")) for s in HIP_SOURCES]
+           [str(OBJ / (stem + ".hip.o")) for _, stem, _ in units]
     tmp = LIB.with_suffix(".so.tmp")
     _run([f"{ROCM}/bin/hipcc", "--offload-arch=gfx950", "-shared", "-fPIC", "-o", str(tmp), *objs,
           f"-L{ROCM}/lib", "-lamdhip64", "-lhiprtc", "-lm", f"-Wl,-rpath,{ROCM}/lib"])

@@ -15,54 +15,23 @@
 #include "launch.h"
 #include <stdio.h>
 
-// The standalone kernel: waves own row groups blockIdx*nw + wave, grid-stride.
-// blockIdx.y selects a chunk of M batch rows (x, y and res advance by M rows
-// per chunk): batches above 4 rows whose operands the MFMA GEMM does not take
-// run as chunks of 4, each output row computed exactly as at M <= 4.
-template <int WT, int XD, int M, int R, int U>
-__global__ __launch_bounds__(1024) void k_gemv(ThvmGemvArgs a) {
-  extern __shared__ __align__(16) unsigned char xs_raw[];
-  __shared__ float red[GEMV_MAX_WAVES];
-  const int nw = blockDim.x >> 6;
-  const uint32_t g = blockIdx.x * nw + (threadIdx.x >> 6);
-  if (blockIdx.y) {
-    const uint64_t m0 = (uint64_t)blockIdx.y * M, ys = a.ydt == THVM_DT_FP32 ? 4 : 2;
-    a.x = (const char *)a.x + m0 * a.ldx * XDr<XD>::B;
-    a.y = (char *)a.y + m0 * a.ldy * ys;
-    if (a.res) a.res = (const char *)a.res + m0 * a.ldy * ys;
-  }
-  gemv_core<WT, XD, M, R, U, false>(
-      a, xs_raw, red, g, gridDim.x * nw, blockDim.x, nw, [] { return true; },
-      [&](int m) { return (const void *)((const char *)a.x + (uint64_t)m * a.ldx * XDr<XD>::B); },
-      [](uint32_t, const float (&)[R][M]) {});
-}
-
-// -------------------------------------------------------------------------
 typedef void (*gemv_fn)(ThvmGemvArgs);
 
-template <int WT, int XD, int R, int U>
-static gemv_fn pick_m(uint32_t M) {
-  switch (M) {
-    case 1: return k_gemv<WT, XD, 1, R, U>;
-    case 2: return k_gemv<WT, XD, 2, R, U>;
-    case 3: return k_gemv<WT, XD, 3, R, U>;
-    case 4: return k_gemv<WT, XD, 4, R, U>;
-    default: return nullptr;
-  }
-}
-template <int WT, int XD>
-static gemv_fn pick_ru(uint32_t M, int R, int U) {
-  if (R == 1) return U == 8 ? pick_m<WT, XD, 1, 8>(M) : pick_m<WT, XD, 1, 4>(M);
-  return U == 8 ? pick_m<WT, XD, 2, 8>(M) : pick_m<WT, XD, 2, 4>(M);
-}
+// one picker per (weight type, x type), each in its own gemv_inst.hip unit
+#define GEMV_PICKERS(X) \
+  X(0, 0) X(0, 1) X(0, 2) X(1, 0) X(1, 1) X(1, 2) X(2, 0) X(2, 1) X(2, 2) X(3, 0) X(3, 1) X(3, 2)
+#define GEMV_DECL(w, x) gemv_fn gemv_pick_##w##_##x(uint32_t M, int R, int U);
+GEMV_PICKERS(GEMV_DECL)
+#undef GEMV_DECL
+
 template <int WT>
 static gemv_fn pick_x(uint32_t xdt, uint32_t M, int R, int U) {
-  switch (xdt) {
-    case THVM_DT_BF16: return pick_ru<WT, XD_BF16>(M, R, U);
-    case THVM_DT_FP16: return pick_ru<WT, XD_F16>(M, R, U);
-    case THVM_DT_FP32: return pick_ru<WT, XD_F32>(M, R, U);
-    default: return nullptr;
-  }
+  static_assert(WT_F32 == 0 && WT_FP8 == 3 && XD_BF16 == 0 && XD_F32 == 2, "picker numbering");
+  const int xd = xdt == THVM_DT_BF16 ? XD_BF16 : xdt == THVM_DT_FP16 ? XD_F16 : xdt == THVM_DT_FP32 ? XD_F32 : -1;
+#define GEMV_CASE(w, x) if (WT == w && xd == x) return gemv_pick_##w##_##x(M, R, U);
+  GEMV_PICKERS(GEMV_CASE)
+#undef GEMV_CASE
+  return nullptr;
 }
 
 static int dt_size(uint32_t dt) {

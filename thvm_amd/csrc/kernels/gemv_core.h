@@ -123,11 +123,9 @@ __device__ __forceinline__ float block_sum_g(float v, float *red, int nwaves) {
 enum { XD_BF16 = 0, XD_F16 = 1, XD_F32 = 2 };
 template <int XD> struct XDr { static constexpr int VE = XD == XD_F32 ? 4 : 8, B = XD == XD_F32 ? 4 : 2; };
 
-// 16 bytes of x at element e of the row at x (COH: a system-scope load, for
-// rows written by other blocks of the same launch)
-template <int XD, bool COH = false>
-__device__ __forceinline__ void xvec(const void *x, uint64_t e, float *o) {
-  const uint4 q = COH ? coh_ld16(x, (uint32_t)(e * XDr<XD>::B)) : ld16((const char *)x + e * XDr<XD>::B);
+// 16 bytes of x (its storage type) -> VE floats
+template <int XD>
+__device__ __forceinline__ void xdec(const uint4 &q, float *o) {
   const uint32_t w[4] = {q.x, q.y, q.z, q.w};
   if (XD == XD_F32) {
 #pragma unroll
@@ -144,6 +142,13 @@ __device__ __forceinline__ void xvec(const void *x, uint64_t e, float *o) {
       }
     }
   }
+}
+// 16 bytes of x at element e of the row at x (COH: a system-scope load, for
+// rows written by other blocks of the same launch)
+template <int XD, bool COH = false>
+__device__ __forceinline__ void xvec(const void *x, uint64_t e, float *o) {
+  const uint4 q = COH ? coh_ld16(x, (uint32_t)(e * XDr<XD>::B)) : ld16((const char *)x + e * XDr<XD>::B);
+  xdec<XD>(q, o);
 }
 template <int XD>
 __device__ __forceinline__ float rnd_x(float v) {
@@ -174,7 +179,15 @@ __device__ __forceinline__ bool gemv_core(const ThvmGemvArgs &a, unsigned char *
   const uint64_t rowbytes = (uint64_t)K * (16 / E);
   const char *wb = (const char *)a.w;
 
-  // ---- 1. first weight batch in flight before anything else ----
+  // ---- 1. loads in flight before any arithmetic ----
+  // Each wave's loads return in issue order.  Standalone at M = 1: x and a
+  // fused norm's gain / bias vectors are issued first, then the first weight
+  // batch, so the staging and the norm's block reductions run while the
+  // weights are in flight (measured on gfx950: 1.2-1.3 us less per fused-norm
+  // launch at the C4 shapes; no change without a norm).  With more rows (x
+  // would hold too many registers across the weight loads) and in the
+  // persistent kernel (COH: x is written by other blocks of the launch and is
+  // read only after wait()), the weights go first.
   uint4 wq[R][U];
   auto load_batch = [&](uint32_t gg, uint32_t c0) {
     const uint32_t n0 = gg * R;
@@ -190,26 +203,38 @@ __device__ __forceinline__ bool gemv_core(const ThvmGemvArgs &a, unsigned char *
       }
     }
   };
-  // (in a persistent kernel, wave 0 polls the grid barrier inside wait():
-  // its own loads are issued after the wait, so the poll does not queue
-  // behind them)
-  const bool early = !COH || (threadIdx.x >> 6) != 0;
-  if (early) load_batch(g, 0);
-  if (!wait()) return false;
-  if (!early) load_batch(g, 0);
-
-  // ---- 2. stage x into LDS (16-byte loads), with the fused norm if asked ----
+  const uint32_t NVt = K / VE;           // x vectors per row
   // (with a fused norm, threads at or beyond nthr take no part in the staging
   // but join its block barriers: the norm's reduction order is that of an
   // nthr-thread block)
-  const uint32_t NVt = K / VE;           // x vectors per row
   const uint32_t tid = threadIdx.x < nthr ? threadIdx.x : NVt;
+  constexpr int XN = 4;                  // no norm: x vectors per thread per staging pass
+  constexpr int NVN = XREG / VE;         // fused norm: x vectors per thread
+  constexpr int NPRE = XN > NVN ? XN : NVN;
+  // x row 0 as raw 16-byte vectors (!COH): the norm path's vectors tid + j*nthr,
+  // or the no-norm path's first pass threadIdx.x + j*blockDim.x (clamped
+  // indices; out-of-row vectors are never stored)
+  constexpr bool XPRE = !COH && M == 1;
+  uint4 xpre[NPRE];
+  if (XPRE) {
+    const char *x0 = (const char *)xrow(0);
+#pragma unroll
+    for (int j = 0; j < NPRE; j++) {
+      // (a uniform skip of vectors past the row for every thread: K below
+      // the staging's reach needs fewer loads)
+      const uint32_t stride = a.norm == 0 ? blockDim.x : nthr;
+      if ((a.norm == 0 ? j >= XN : j >= NVN) || j * stride >= NVt) break;
+      const uint32_t v = (a.norm == 0 ? threadIdx.x : tid) + j * stride;
+      const uint32_t vc = v < NVt ? v : 0;
+      xpre[j] = ld16(x0 + (uint64_t)vc * VE * XDr<XD>::B);
+    }
+  }
   // a fused norm's gain (and LayerNorm bias) vectors: loaded with the first
   // x loads, not after the reduction, so they cost no round trip of their
   // own (clamped indices; lanes past the row never use them)
-  constexpr int NVN = XREG / VE;
   float gw[NVN][VE], gb[NVN][VE];
-  if (a.norm != 0) {
+  auto load_gains = [&] {
+    if (a.norm == 0) return;
     const bool hw = a.norm_w != nullptr, hb = a.norm == 2 && a.norm_b != nullptr;
 #pragma unroll
     for (int j = 0; j < NVN; j++) {
@@ -222,19 +247,34 @@ __device__ __forceinline__ bool gemv_core(const ThvmGemvArgs &a, unsigned char *
         gb[j][i] = u.x; gb[j][i + 1] = u.y; gb[j][i + 2] = u.z; gb[j][i + 3] = u.w;
       }
     }
-  }
+  };
+  if (XPRE) load_gains();
+  // (in a persistent kernel, wave 0 polls the grid barrier inside wait():
+  // its own loads are issued after the wait, so the poll does not queue
+  // behind them)
+  const bool early = !COH || (threadIdx.x >> 6) != 0;
+  if (early) load_batch(g, 0);
+  if (!wait()) return false;
+  if (!early) load_batch(g, 0);
+  if (!XPRE) load_gains();
+
+  // ---- 2. stage x into LDS (16-byte loads), with the fused norm if asked ----
   for (int m = 0; m < M; m++) {
     const void *xr = xrow(m);
+    const bool pre = XPRE && m == 0;     // row 0 already in xpre
     if (a.norm == 0) {
       // no reduction: every thread of the block stages, XN vectors of x in
       // flight per thread before the first LDS store
-      constexpr int XN = 4;
       for (uint32_t v0 = threadIdx.x; v0 < NVt; v0 += XN * blockDim.x) {
         float f[XN][VE];
+        const bool first = v0 == threadIdx.x;
 #pragma unroll
         for (int j = 0; j < XN; j++) {
           const uint32_t v = v0 + j * blockDim.x;
-          if (v < NVt) xvec<XD, COH>(xr, (uint64_t)v * VE, f[j]);
+          if (v < NVt) {
+            if (pre && first) xdec<XD>(xpre[j], f[j]);
+            else xvec<XD, COH>(xr, (uint64_t)v * VE, f[j]);
+          }
         }
 #pragma unroll
         for (int j = 0; j < XN; j++) {
@@ -246,13 +286,15 @@ __device__ __forceinline__ bool gemv_core(const ThvmGemvArgs &a, unsigned char *
         }
       }
     } else {
-      constexpr int NV = XREG / VE;
+      constexpr int NV = NVN;
       float xv[NV][VE];
 #pragma unroll
       for (int j = 0; j < NV; j++) {
         const uint32_t v = tid + j * nthr;
-        if (v < NVt) xvec<XD, COH>(xr, (uint64_t)v * VE, xv[j]);
-        else {
+        if (v < NVt) {
+          if (pre) xdec<XD>(xpre[j], xv[j]);
+          else xvec<XD, COH>(xr, (uint64_t)v * VE, xv[j]);
+        } else {
 #pragma unroll
           for (int i = 0; i < VE; i++) xv[j][i] = 0.0f;
         }
