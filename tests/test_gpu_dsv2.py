@@ -52,11 +52,21 @@ def close_bf16(got, want, floor=0.0):
 MLA_SHAPES = [dict(H=16, dn=128, dr=64, kv=512, dv=128, B=2, ms=256, L=130),
               dict(H=8, dn=32, dr=16, kv=64, dv=32, B=1, ms=128, L=64),
               dict(H=8, dn=32, dr=16, kv=128, dv=32, B=3, ms=64, L=1),
-              dict(H=16, dn=128, dr=64, kv=512, dv=128, B=8, ms=192, L=150)]   # all heads per block
+              dict(H=16, dn=128, dr=64, kv=512, dv=128, B=8, ms=192, L=150),   # all heads per block
+              dict(H=16, dn=128, dr=64, kv=512, dv=128, B=1, ms=320, L=257)]   # chunk groups + 1-row tail
+
+# split kernels of mla_attn: (mode, cpb); the MFMA split exists for the
+# DeepSeek-V2 shape (16 heads, kv 512, rope 64) only
+MLA_SPLITS = [(0, 0), (1, 0), (2, 1), (2, 2), (2, 3), (2, 4)]
+
+
+def mla_splits(H, kv, dr):
+    mf = H == 16 and kv == 512 and dr == 64
+    return [(m, c) for m, c in MLA_SPLITS if m != 2 or mf]
 
 
 @pytest.mark.parametrize("wdt", [DT_FP8, DT_BF16])
-@pytest.mark.parametrize("shape", MLA_SHAPES, ids=["c5", "smoke", "L1", "c5_b8"])
+@pytest.mark.parametrize("shape", MLA_SHAPES, ids=["c5", "smoke", "L1", "c5_b8", "c5_tail"])
 def test_mla_prep_and_attn(hip, shape, wdt):
     H, dn, dr, kv, dv, B, ms, L = (shape[k] for k in ("H", "dn", "dr", "kv", "dv", "B", "ms", "L"))
     say(f"case: mla {shape} wdt={wdt}")
@@ -104,23 +114,27 @@ def test_mla_prep_and_attn(hip, shape, wdt):
 
     scale = 0.1352
     nsplit = (ms + 63) // 64
-    o = hip.Buffer(B * H * dv * 2)
-    part = hip.Buffer(B * nsplit * H * (kv + 4) * 4)
-    args = [o, qlat, qpe, ckv, kpe, Lb, part, up(hip, wuv)] + ([up(hip, suv)] if f8 else [])
-    hip.builtin("mla_attn", args, b=B, h=H, dn=dn, dr=dr, kv=kv, dv=dv, maxseq=ms, nsplit=nsplit,
-                wt=wdt, scale=scale)
-    g_o = unbf(o.read(np.uint16).reshape(B, H, dv))
+    w_o = np.empty((B, H, dv), np.uint16)
     for b in range(B):
-        w_o = np.empty((H, dv), np.uint16)
-        O.oracle().or_mla_attn(w_o.ctypes.data, np.ascontiguousarray(g_qlat[b]).ctypes.data,
+        O.oracle().or_mla_attn(w_o[b].ctypes.data, np.ascontiguousarray(g_qlat[b]).ctypes.data,
                                np.ascontiguousarray(g_qpe[b]).ctypes.data,
                                np.ascontiguousarray(g_ckv[b]).ctypes.data,
                                np.ascontiguousarray(g_kpe[b]).ctypes.data, L, wuv.ctypes.data, wdt,
                                suv.ctypes.data if f8 else None, H, kv, dr, dv, scale)
-        # floor: |olat| <= max_j |ckv_j| per column
-        cmax = np.abs(unbf(g_ckv[b, :L])).max(0)
-        floor = np.abs(wuvf.reshape(H, dv, kv)) @ cmax
-        assert np.all(close_bf16(g_o[b], unbf(w_o), floor)), np.max(np.abs(g_o[b] - unbf(w_o)))
+    for mode, cpb in mla_splits(H, kv, dr):
+        say(f"case: mla_attn mode={mode} cpb={cpb}")
+        o = hip.Buffer(B * H * dv * 2)
+        part = hip.Buffer(B * nsplit * H * (kv + 4) * 4)
+        args = [o, qlat, qpe, ckv, kpe, Lb, part, up(hip, wuv)] + ([up(hip, suv)] if f8 else [])
+        hip.builtin("mla_attn", args, b=B, h=H, dn=dn, dr=dr, kv=kv, dv=dv, maxseq=ms, nsplit=nsplit,
+                    wt=wdt, scale=scale, mode=mode, cpb=cpb)
+        g_o = unbf(o.read(np.uint16).reshape(B, H, dv))
+        for b in range(B):
+            # floor: |olat| <= max_j |ckv_j| per column
+            cmax = np.abs(unbf(g_ckv[b, :L])).max(0)
+            floor = np.abs(wuvf.reshape(H, dv, kv)) @ cmax
+            assert np.all(close_bf16(g_o[b], unbf(w_o[b]), floor)), \
+                (mode, cpb, np.max(np.abs(g_o[b] - unbf(w_o[b]))))
 
 
 def test_mla_closed_form_equal_rows(hip):
@@ -136,15 +150,17 @@ def test_mla_closed_form_equal_rows(hip):
     qpe = bf(rng.standard_normal((B, H, dr)))
     wuv = bf(rng.standard_normal((H * dv, kv)) * 0.02)
     nsplit = 3
-    o = hip.Buffer(B * H * dv * 2)
-    hip.builtin("mla_attn", [o, up(hip, qlat), up(hip, qpe), up(hip, ckv), up(hip, kpe),
-                             up(hip, np.array([L], np.int32)), hip.Buffer(B * nsplit * H * (kv + 4) * 4),
-                             up(hip, wuv)],
-                b=B, h=H, dn=dn, dr=dr, kv=kv, dv=dv, maxseq=ms, nsplit=nsplit, wt=DT_BF16, scale=0.2)
-    got = unbf(o.read(np.uint16).reshape(H, dv))
     want = (unbf(wuv).astype(np.float64) @ unbf(row).astype(np.float64)).reshape(H, dv)
     floor = (np.abs(unbf(wuv)) @ np.abs(unbf(row))).reshape(H, dv)
-    assert np.all(np.abs(got - want) <= 2.0 ** -7 * np.abs(want) + 1e-5 * floor)
+    for mode, cpb in mla_splits(H, kv, dr):
+        o = hip.Buffer(B * H * dv * 2)
+        hip.builtin("mla_attn", [o, up(hip, qlat), up(hip, qpe), up(hip, ckv), up(hip, kpe),
+                                 up(hip, np.array([L], np.int32)), hip.Buffer(B * nsplit * H * (kv + 4) * 4),
+                                 up(hip, wuv)],
+                    b=B, h=H, dn=dn, dr=dr, kv=kv, dv=dv, maxseq=ms, nsplit=nsplit, wt=DT_BF16, scale=0.2,
+                    mode=mode, cpb=cpb)
+        got = unbf(o.read(np.uint16).reshape(H, dv))
+        assert np.all(np.abs(got - want) <= 2.0 ** -7 * np.abs(want) + 1e-5 * floor), (mode, cpb)
 
 
 def test_route_topk_ties_bit_exact(hip):
@@ -404,3 +420,16 @@ def test_dsv2_decoder_parity(hip, wdt, batch):
         assert np.array_equal(dec.tokens(ctx + steps + 1), eager)
     finally:
         dec.close()
+
+
+def test_mla_split_mode_errors(hip):
+    """mla_attn rejects the MFMA split outside the shape it is built for, and
+    chunk counts it has no kernel for."""
+    H, dn, dr, kv, dv, B, ms = 8, 32, 16, 64, 32, 1, 128
+    args = [hip.Buffer(B * H * dv * 2), hip.Buffer(B * H * kv * 4), hip.Buffer(B * H * dr * 2),
+            hip.Buffer(B * ms * kv * 2), hip.Buffer(B * ms * dr * 2), up(hip, np.array([5], np.int32)),
+            hip.Buffer(B * 2 * H * (kv + 4) * 4), hip.Buffer(H * dv * kv * 2)]
+    for bad in (dict(mode=2), dict(mode=3), dict(mode=1, cpb=2)):
+        with pytest.raises(hip.ThvmHipError):
+            hip.builtin("mla_attn", args, b=B, h=H, dn=dn, dr=dr, kv=kv, dv=dv, maxseq=ms, nsplit=2,
+                        wt=DT_BF16, scale=0.2, **bad)

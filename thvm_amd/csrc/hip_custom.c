@@ -281,7 +281,8 @@ int hb_builtin_launch(const char *program, const u32 *ids, u32 n, int check_only
          spec_u32(&sp, "maxseq", &a.max_seq, 1, 0) || spec_u32(&sp, "wt", &a.wdt, 0, THVM_DT_FP8E4M3) ||
          spec_f32(&sp, "eps", &a.eps, 0, 1e-6f) || spec_f32(&sp, "scale", &a.scale, !prep, 0));
     NEED(spec_u32(&sp, "ldq", &a.ldq, 0, a.H * (a.dn + a.dr) + a.kv + a.dr) ||
-         spec_u32(&sp, "nsplit", &a.n_split, 0, (a.max_seq + 63) / 64));
+         spec_u32(&sp, "nsplit", &a.n_split, 0, (a.max_seq + 63) / 64) ||
+         spec_u32(&sp, "mode", &a.mode, 0, 0) || spec_u32(&sp, "cpb", &a.cpb, 0, 0));
     const u32 wsz = hb_dt_size(a.wdt);
     const int fp8 = a.wdt == THVM_DT_FP8E4M3;
     if (!wsz) { hb_set_error("builtin %s: bad weight dtype", K); return -1; }

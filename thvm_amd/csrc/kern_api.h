@@ -135,6 +135,10 @@ typedef struct ThvmMlaArgs {
   void *o;
   uint32_t B, H, dn, dr, kv, dv, max_seq, ldq, n_split, wdt;
   float eps, scale;
+  /* mla_attn: split kernel (0 auto: the MFMA split for 16 heads x kv 512 x
+   * rope 64, the VALU split otherwise; 1 VALU; 2 MFMA) and 64-row chunks per
+   * split block (0 auto; the MFMA split takes 1, 2 or 4) */
+  uint32_t mode, cpb;
 } ThvmMlaArgs;
 int thvm_k_mla_prep(const ThvmMlaArgs *a, hipStream_t s, char *err, int errlen);
 int thvm_k_mla_attn(const ThvmMlaArgs *a, hipStream_t s, char *err, int errlen);

@@ -23,6 +23,7 @@
 #include "dev_common.h"
 #include "../kern_api.h"
 #include "launch.h"
+#include "mfma_ops.h"
 #include <stdio.h>
 
 #define MLA_CHUNK 64
@@ -269,6 +270,223 @@ __global__ __launch_bounds__(MLA_THREADS) void k_mla_split(ThvmMlaArgs a) {
   }
 }
 
+// ---- k_mla_split_mf -----------------------------------------------------
+// The split on MFMA for the DeepSeek-V2 attention shape (16 heads, kv_lora
+// 512, rope 64): the 16 heads are the M side of v_mfma_f32_16x16x32_bf16.
+//   scores  S[h][row] = qlat[h] . c_row + qpe[h] . pe_row over k = 576 (18
+//           steps of 32): A = q (16 heads x 32 k), B = the cache rows (32 k x
+//           16 rows), one 16-row tile per wave; a lane's B operand is 8
+//           consecutive values of one row, one 16-byte load straight from HBM;
+//   mix     olat[h][:] += p[h][row] c_row: A = p (16 heads x 32 rows), B =
+//           the latent rows staged in LDS (32 rows x 16 columns), 8 column
+//           tiles per wave.  The rows are staged column-major within each
+//           group of 8 rows ([row / 8][column][row % 8]), so a lane's B
+//           operand -- 8 rows of one column -- is one 16-byte LDS read; the
+//           transposing 2-byte writes need no wait.
+// q and p (f32) enter as bf16 hi + lo pairs (two MFMAs each), so a product
+// keeps ~16 significant bits of the f32 operand against the exact bf16 cache
+// value: f32-level agreement with the VALU split.  A block runs cpb
+// consecutive 64-row chunks of one batch row with an online softmax (olat and
+// the running sum rescaled by exp(m_old - m_new)), the next chunk's rows in
+// flight during the current chunk's softmax and mix, and writes one partial
+// (olat, m, l) at slot blockIdx.x; k_mla_out merges ceil(L / (64 cpb)) of
+// them.  MFMA operand k order: A and B give lane group g the same 8 k values
+// (k = 32 step + 8 g + j), so each instruction adds a full partial dot product.
+#define MF_H 16
+#define MF_KV 512
+#define MF_DR 64
+#define MF_KS ((MF_KV + MF_DR) / 32)       /* 18 k-steps */
+#define MF_RGP (512 * 16 + 16)             /* LDS pitch of a staged 8-row group (bytes) */
+#define MF_PWP 68                          /* LDS pitch of a head's softmax weights (floats) */
+#define MF_THREADS 256
+#define MF_LDS (8 * MF_RGP + MF_KS * 2 * 64 * 16 + MF_H * MF_PWP * 4 + 2 * 4 * MF_H * 4)
+
+// eight f32 -> bf16 hi (RNE) and lo = bf16(v - hi), packed in operand order
+__device__ __forceinline__ void split8(const float4 &a, const float4 &b, uint4 &hi, uint4 &lo) {
+  const float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+  uint32_t h[4], l[4];
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    const bf16_t h0 = f2bf(v[2 * i]), h1 = f2bf(v[2 * i + 1]);
+    const bf16_t l0 = f2bf(v[2 * i] - bf2f(h0)), l1 = f2bf(v[2 * i + 1] - bf2f(h1));
+    h[i] = (uint32_t)h0 | ((uint32_t)h1 << 16);
+    l[i] = (uint32_t)l0 | ((uint32_t)l1 << 16);
+  }
+  hi = make_uint4(h[0], h[1], h[2], h[3]);
+  lo = make_uint4(l[0], l[1], l[2], l[3]);
+}
+
+// grid (ceil(n_split / cpb), B), 256 threads (4 waves), cpb = a.cpb chunks
+// per block, two chunks' rows in flight
+__global__ __launch_bounds__(MF_THREADS) void k_mla_split_mf(ThvmMlaArgs a) {
+  extern __shared__ __align__(16) unsigned char lds_mf[];
+  unsigned char *cl = lds_mf;                                        // [8][MF_RGP]: [row/8][col][row%8]
+  uint4 *qa = (uint4 *)(lds_mf + 8 * MF_RGP);                        // [MF_KS][hi, lo][64 lanes]
+  float *pw = (float *)(lds_mf + 8 * MF_RGP + MF_KS * 2 * 64 * 16);  // [16 heads][MF_PWP]
+  float *rmax = pw + MF_H * MF_PWP, *rsum = rmax + 4 * MF_H;         // [4 waves][16 heads]
+  const uint32_t cpb = a.cpb, grp = blockIdx.x, b = blockIdx.y;
+  const int32_t L = min(a.len[0], (int32_t)a.max_seq);               // rows [0, L) are live
+  const uint32_t cbeg = grp * cpb;
+  if (L <= 0 || cbeg * 64 >= (uint32_t)L) return;                    // block-uniform
+  const uint32_t cend = min(cbeg + cpb, ((uint32_t)L + 63) / 64);
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, li = lane & 15, lg = lane >> 4;
+  const char *ckv = (const char *)a.ckv + (uint64_t)b * a.max_seq * (MF_KV * 2);
+  const char *kpe = (const char *)a.kpe + (uint64_t)b * a.max_seq * (MF_DR * 2);
+
+  // q first (its staging waits for these loads only), then the first two
+  // chunks' rows.  q as A operands (hi, lo) in LDS: fragment f = 64 ks +
+  // lane holds head lane % 16, k = 32 ks + 8 (lane / 16) + j; k-steps 0..15
+  // from qlat (f32), 16..17 from qpe (bf16: exact, lo = 0)
+  const float *ql = a.qlat + (uint64_t)b * MF_H * MF_KV;
+  const bf16_t *qp = (const bf16_t *)a.qpe + (uint64_t)b * MF_H * MF_DR;
+  float4 qv[4][2];
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    const uint32_t f = tid + MF_THREADS * i, l = f & 63;
+    const uint32_t k0 = (f >> 6) * 32 + (l >> 4) * 8;
+    qv[i][0] = *(const float4 *)(ql + (l & 15) * MF_KV + k0);
+    qv[i][1] = *(const float4 *)(ql + (l & 15) * MF_KV + k0 + 4);
+  }
+  const uint32_t fp = 16 * 64 + (tid & 127), lp = fp & 63;
+  const uint4 qpv = *(const uint4 *)(qp + (lp & 15) * MF_DR + ((fp >> 6) - 16) * 32 + (lp >> 4) * 8);
+
+  // the B operands of chunk c for this wave's 16-row tile: 16 k-steps of the
+  // latent row, 2 of the pe row (rows past L load a live row of the chunk
+  // and are masked out of the softmax)
+  uint4 cfa[MF_KS], cfb[MF_KS];
+  auto issue = [&](uint4 (&cf)[MF_KS], uint32_t c) {
+    const uint32_t j = c * 64 + wv * 16 + li;
+    const uint32_t jc = j < (uint32_t)L ? j : c * 64;
+    const char *cr = ckv + (uint64_t)jc * (MF_KV * 2) + lg * 16;
+    const char *pr = kpe + (uint64_t)jc * (MF_DR * 2) + lg * 16;
+#pragma unroll
+    for (int ks = 0; ks < 16; ks++) cf[ks] = ld_stream16(cr + ks * 64);
+    cf[16] = ld_stream16(pr);
+    cf[17] = ld_stream16(pr + 64);
+  };
+  issue(cfa, cbeg);
+  if (cbeg + 1 < cend) issue(cfb, cbeg + 1);
+
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    const uint32_t f = tid + MF_THREADS * i;
+    uint4 hi, lo;
+    split8(qv[i][0], qv[i][1], hi, lo);
+    qa[(f >> 6) * 128 + (f & 63)] = hi;
+    qa[(f >> 6) * 128 + 64 + (f & 63)] = lo;
+  }
+  if (tid < 128) {
+    qa[(fp >> 6) * 128 + lp] = qpv;
+    qa[(fp >> 6) * 128 + 64 + lp] = make_uint4(0, 0, 0, 0);
+  }
+  __syncthreads();
+
+  float m_run[4], l_run[4];
+  f32x4_t oacc[8];
+#pragma unroll
+  for (int i = 0; i < 4; i++) { m_run[i] = -INFINITY; l_run[i] = 0.0f; }
+#pragma unroll
+  for (int t = 0; t < 8; t++) oacc[t] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+
+  // one chunk: its rows are in cf; chunk c + 2 goes into cf once the scores
+  // have consumed it
+  auto chunk = [&](uint4 (&cf)[MF_KS], uint32_t c) {
+    const uint32_t nj = min((uint32_t)L - c * 64, 64u);
+    // 1. scores of the wave's tile: lane holds S[head 4 lg + i][row 16 wv + li]
+    //    (four independent accumulator chains: q hi / lo x even / odd steps)
+    f32x4_t sc[4];
+#pragma unroll
+    for (int u = 0; u < 4; u++) sc[u] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int ks = 0; ks < MF_KS; ks++) {
+      sc[(ks & 1) * 2] = mfma16<GX_BF16>(qa[ks * 128 + lane], cf[ks], sc[(ks & 1) * 2]);
+      sc[(ks & 1) * 2 + 1] = mfma16<GX_BF16>(qa[ks * 128 + 64 + lane], cf[ks], sc[(ks & 1) * 2 + 1]);
+    }
+    // the latent part of the tile's rows into LDS for the mix: row r, column
+    // k at [r / 8][k][r % 8]
+    {
+      const uint32_t r = wv * 16 + li;
+      unsigned char *dst = cl + (r >> 3) * MF_RGP + (r & 7) * 2 + lg * 8 * 16;
+#pragma unroll
+      for (int ks = 0; ks < 16; ks++) {
+        const uint32_t w[4] = {cf[ks].x, cf[ks].y, cf[ks].z, cf[ks].w};
+#pragma unroll
+        for (int e = 0; e < 8; e++)
+          *(uint16_t *)(dst + (ks * 32 + e) * 16) = (uint16_t)(w[e >> 1] >> ((e & 1) * 16));
+      }
+    }
+    if (c + 2 < cend) issue(cf, c + 2);   // in flight during two chunks' softmax and mix
+
+    // 2. softmax over the chunk's rows, online across the block's chunks
+    const bool rok = (uint32_t)(wv * 16 + li) < nj;
+    float sv[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const float st = (sc[0][i] + sc[1][i]) + (sc[2][i] + sc[3][i]);
+      sv[i] = rok ? st * a.scale : -INFINITY;
+      const float m = row16_max(sv[i]);
+      if (li == 0) rmax[wv * MF_H + 4 * lg + i] = m;
+    }
+    __syncthreads();
+    float mn[4], al[4], p[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const int h = 4 * lg + i;
+      const float m = fmaxf(fmaxf(rmax[h], rmax[MF_H + h]), fmaxf(rmax[2 * MF_H + h], rmax[3 * MF_H + h]));
+      mn[i] = fmaxf(m_run[i], m);
+      al[i] = m_run[i] == -INFINITY ? 0.0f : expf(m_run[i] - mn[i]);
+      p[i] = rok ? expf(sv[i] - mn[i]) : 0.0f;
+      const float ps = row16_sum(p[i]);
+      if (li == 0) rsum[wv * MF_H + h] = ps;
+      pw[h * MF_PWP + wv * 16 + li] = p[i];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const int h = 4 * lg + i;
+      const float l = rsum[h] + rsum[MF_H + h] + rsum[2 * MF_H + h] + rsum[3 * MF_H + h];
+      l_run[i] = l_run[i] * al[i] + l;
+      m_run[i] = mn[i];
+    }
+    // 3. mix: olat tiles kt = 8 wv + t, lane holds O[head 4 lg + i][16 kt + li]
+#pragma unroll
+    for (int t = 0; t < 8; t++)
+#pragma unroll
+      for (int i = 0; i < 4; i++) oacc[t][i] *= al[i];
+#pragma unroll
+    for (int q = 0; q < 2; q++) {                  // 32-row k-steps
+      const float *pr = pw + li * MF_PWP + q * 32 + lg * 8;
+      uint4 ah, alo;
+      split8(*(const float4 *)pr, *(const float4 *)(pr + 4), ah, alo);
+      const unsigned char *rb = cl + (q * 4 + lg) * MF_RGP + li * 16;
+#pragma unroll
+      for (int t = 0; t < 8; t++) {
+        const uint4 bv = *(const uint4 *)(rb + (wv * 8 + t) * 16 * 16);
+        oacc[t] = mfma16<GX_BF16>(ah, bv, oacc[t]);
+        oacc[t] = mfma16<GX_BF16>(alo, bv, oacc[t]);
+      }
+    }
+    __syncthreads();                               // cl, pw and the reductions are reused
+  };
+  for (uint32_t c = cbeg; c < cend; c += 2) {
+    chunk(cfa, c);
+    if (c + 1 < cend) chunk(cfb, c + 1);
+  }
+
+  float *part = a.part + ((uint64_t)b * a.n_split + grp) * MF_H * (MF_KV + 4);
+#pragma unroll
+  for (int t = 0; t < 8; t++)
+#pragma unroll
+    for (int i = 0; i < 4; i++) part[(4 * lg + i) * (MF_KV + 4) + (wv * 8 + t) * 16 + li] = oacc[t][i];
+  if (wv == 0 && li == 0) {
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      part[(4 * lg + i) * (MF_KV + 4) + MF_KV] = m_run[i];
+      part[(4 * lg + i) * (MF_KV + 4) + MF_KV + 1] = l_run[i];
+    }
+  }
+}
+
 // ---- k_mla_out ----------------------------------------------------------
 // grid (B*H, MLA_OUT_SPLIT), 512 threads: merge the live splits of (b, h)
 // into olat -- split weights computed once, threads split into (float4
@@ -299,7 +517,8 @@ __global__ __launch_bounds__(MLA_OUT_THREADS) void k_mla_out(ThvmMlaArgs a) {
                     : make_uint4(0, 0, 0, 0);
   }
   const int32_t L = min(a.len[0], (int32_t)a.max_seq);
-  const uint32_t ns = L > 0 ? ((uint32_t)L + MLA_CHUNK - 1) / MLA_CHUNK : 0;
+  const uint32_t span = MLA_CHUNK * (a.cpb > 1 ? a.cpb : 1);   // cache rows per partial
+  const uint32_t ns = L > 0 ? ((uint32_t)L + span - 1) / span : 0;
   const uint64_t pst = (uint64_t)a.H * (kv + 4);
   const float *p0 = a.part + (uint64_t)b * a.n_split * pst + (uint64_t)h * (kv + 4);
   float *wsp = ol + kv, *grp = wsp + MLA_MAX_SPLITS;
@@ -437,15 +656,6 @@ extern "C" int thvm_k_mla_attn(const ThvmMlaArgs *a, hipStream_t s, char *err, i
     snprintf(err, errlen, "mla_attn: W_uv rows must be 16-byte multiples");
     return -1;
   }
-  mla_split_fn f = a->H % MLA_HG == 0 ? pick_kpl(a->kv) : nullptr;
-  if (!f) { snprintf(err, errlen, "mla_attn: no kernel for H=%u kv=%u (H a multiple of %d)", a->H, a->kv, MLA_HG); return -1; }
-  if (a->n_split > MLA_MAX_SPLITS) { snprintf(err, errlen, "mla_attn: more than %d splits", MLA_MAX_SPLITS); return -1; }
-  const uint32_t lds = (uint32_t)(MLA_CHUNK * a->kv * 2 + MLA_HG * MLA_CHUNK * 4);
-  if (lds > 64 * 1024) {
-    hipError_t e = hipFuncSetAttribute((const void *)f, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-    if (e != hipSuccess) { snprintf(err, errlen, "mla_attn: hipFuncSetAttribute: %s", hipGetErrorString(e)); return -1; }
-  }
-  thvm_launch(true, false, f, dim3(a->n_split, a->H / MLA_HG, a->B), dim3(MLA_THREADS), lds, s, *a);
   {
     const uint32_t lpr = a->kv * wsz / 16, rpp = 64 / lpr;
     const uint32_t rows_pb = (a->dv + MLA_OUT_SPLIT - 1) / MLA_OUT_SPLIT;
@@ -454,10 +664,43 @@ extern "C" int thvm_k_mla_attn(const ThvmMlaArgs *a, hipStream_t s, char *err, i
       return -1;
     }
   }
+  if (a->n_split > MLA_MAX_SPLITS) { snprintf(err, errlen, "mla_attn: more than %d splits", MLA_MAX_SPLITS); return -1; }
+  const bool mf_shape = a->H == MF_H && a->kv == MF_KV && a->dr == MF_DR;
+  if (a->mode > 2 || (a->mode == 2 && !mf_shape)) {
+    snprintf(err, errlen, "mla_attn: mode %u (0 auto, 1 VALU, 2 MFMA for H=%d kv=%d dr=%d)", a->mode, MF_H, MF_KV, MF_DR);
+    return -1;
+  }
+  ThvmMlaArgs ak = *a;
+  if (a->mode == 2 || (a->mode == 0 && mf_shape)) {
+    // MFMA split: cpb 64-row chunks per block (fewer partials to write and
+    // merge with more rows per block)
+    // (a block holds ~105 KB of LDS, so one block per CU: the smallest chunk
+    // count that keeps the grid within one block per CU of the 256, so the
+    // split runs in a single round)
+    uint32_t cpb = a->cpb;
+    if (cpb == 0) cpb = (uint32_t)(((uint64_t)a->B * a->n_split + 255) / 256);
+    if (cpb > a->n_split) cpb = a->n_split;       // one block takes every chunk
+    ak.cpb = cpb;
+    mla_split_fn f = k_mla_split_mf;
+    hipError_t e = hipFuncSetAttribute((const void *)f, hipFuncAttributeMaxDynamicSharedMemorySize, MF_LDS);
+    if (e != hipSuccess) { snprintf(err, errlen, "mla_attn: hipFuncSetAttribute: %s", hipGetErrorString(e)); return -1; }
+    thvm_launch(true, false, f, dim3((a->n_split + cpb - 1) / cpb, a->B), dim3(MF_THREADS), MF_LDS, s, ak);
+  } else {
+    if (a->cpb > 1) { snprintf(err, errlen, "mla_attn: the VALU split runs one chunk per block"); return -1; }
+    ak.cpb = 1;
+    mla_split_fn f = a->H % MLA_HG == 0 ? pick_kpl(a->kv) : nullptr;
+    if (!f) { snprintf(err, errlen, "mla_attn: no kernel for H=%u kv=%u (H a multiple of %d)", a->H, a->kv, MLA_HG); return -1; }
+    const uint32_t lds = (uint32_t)(MLA_CHUNK * a->kv * 2 + MLA_HG * MLA_CHUNK * 4);
+    if (lds > 64 * 1024) {
+      hipError_t e = hipFuncSetAttribute((const void *)f, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+      if (e != hipSuccess) { snprintf(err, errlen, "mla_attn: hipFuncSetAttribute: %s", hipGetErrorString(e)); return -1; }
+    }
+    thvm_launch(true, false, f, dim3(a->n_split, a->H / MLA_HG, a->B), dim3(MLA_THREADS), lds, s, ak);
+  }
   const dim3 g2(a->B * a->H, MLA_OUT_SPLIT);
   const uint32_t lds2 = (a->kv + MLA_MAX_SPLITS + MLA_OUT_THREADS * 4) * 4;
-  if (a->wdt == THVM_DT_FP8E4M3) thvm_launch(false, true, k_mla_out<true>, g2, dim3(MLA_OUT_THREADS), lds2, s, *a);
-  else thvm_launch(false, true, k_mla_out<false>, g2, dim3(MLA_OUT_THREADS), lds2, s, *a);
+  if (a->wdt == THVM_DT_FP8E4M3) thvm_launch(false, true, k_mla_out<true>, g2, dim3(MLA_OUT_THREADS), lds2, s, ak);
+  else thvm_launch(false, true, k_mla_out<false>, g2, dim3(MLA_OUT_THREADS), lds2, s, ak);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) { snprintf(err, errlen, "mla_attn launch: %s", hipGetErrorString(e)); return -1; }
   return 0;
