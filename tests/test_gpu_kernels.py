@@ -459,7 +459,14 @@ def test_attention_decode(hip, H, Hkv, hd, L, cdt):
     else:
         assert np.all(np.abs(got - ww) <= 2.0 ** -7 * np.abs(ww) + 2e-3), np.max(np.abs(got - ww))
     # the one-launch form (split + last-unit merge) equals the two-kernel form
-    # bit for bit, and leaves its merge counters zero for the next launch
+    # of one chunk per block bit for bit, and leaves its merge counters zero
+    # for the next launch
+    out = hip.Buffer(B * H * hd * SZ[cdt])
+    hip.builtin("attn", [out, up(hip, qs), up(hip, ks), up(hip, vs),
+                         up(hip, np.array([L], np.int32)), part],
+                b=B, h=H, hkv=Hkv, hd=hd, maxseq=ms, chunk=64, nsplit=nsplit, qt=cdt,
+                ct=cdt, ot=cdt, scale=scale, cpb=1)
+    assert attn_close(O.decode(out.read(NP_STORE[cdt]), cdt), ww, cdt)
     out2 = hip.Buffer(B * H * hd * SZ[cdt])
     part2 = hip.Buffer(B * H * nsplit * (hd + 2) * 4 + B * Hkv * 4)
     hip.builtin("attn", [out2, up(hip, qs), up(hip, ks), up(hip, vs),
@@ -541,7 +548,8 @@ def test_attention_cpb_errors(hip):
 
 def test_attention_fused_repeated(hip):
     """Ten launches on one partial buffer at changing lengths: every merge
-    finds its counter at zero and the outputs match the two-kernel form."""
+    finds its counter at zero and the outputs match the two-kernel form of
+    one chunk per block."""
     B, H, Hkv, hd, ms, cdt = 1, 32, 8, 128, 2176, DT_BF16
     say("case: fused attention, 10 launches on one partial buffer")
     rng = np.random.default_rng(5)
@@ -559,7 +567,7 @@ def test_attention_fused_repeated(hip):
             o = hip.Buffer(B * H * hd * 2)
             hip.builtin("attn", [o, qb, kb, vb, up(hip, np.array([L], np.int32)), pb], b=B, h=H,
                         hkv=Hkv, hd=hd, maxseq=ms, chunk=64, nsplit=nsplit, qt=cdt, ct=cdt, ot=cdt,
-                        scale=scale, fused=fused)
+                        scale=scale, fused=fused, cpb=1)
             outs.append(o.read(np.uint16))
         assert np.array_equal(outs[0], outs[1]), L
 

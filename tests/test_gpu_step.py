@@ -27,7 +27,9 @@ CASES = {
 
 
 def make(hip, cfg, mode, ctx, seed=11):
-    dec = hip.Decoder(seed=seed, **dict(cfg, step_mode=mode))
+    # the op list with one-chunk attention blocks: the persistent step's form
+    extra = dict(attn_cpb=1) if mode == 0 else {}
+    dec = hip.Decoder(seed=seed, **dict(cfg, step_mode=mode, **extra))
     dec.prefill_synthetic(ctx, seed=4)
     rng = np.random.default_rng(seed)
     dec.set_state(rng.integers(0, cfg["vocab"], cfg["batch"]).astype(np.int32), ctx)
@@ -95,3 +97,9 @@ def test_step_oracle_parity(hip, wdt):
 def test_step_config_errors(hip, bad):
     with pytest.raises(hip.ThvmHipError):
         hip.Decoder(seed=1, **dict(BASE, step_mode=1, **bad))
+
+
+@pytest.mark.parametrize("cpb", [3, 8])
+def test_attn_cpb_config_errors(hip, cpb):
+    with pytest.raises(hip.ThvmHipError):
+        hip.Decoder(seed=1, **dict(BASE, attn_cpb=cpb))

@@ -44,8 +44,8 @@ class DecodeConfig(C.Structure):
         ("eps", C.c_float), ("rope_theta", C.c_float), ("init_std", C.c_float)] + [
         (n, C.c_uint32) for n in ("kv_lora", "d_nope", "d_rope", "d_v", "n_experts",
                                   "n_shared", "top_k", "moe_inter", "first_dense", "step_mode",
-                                  "moe_mode")] + [
-        ("reserved", C.c_uint32 * 6)]
+                                  "moe_mode", "attn_cpb")] + [
+        ("reserved", C.c_uint32 * 5)]
 
 
 class Uop(C.Structure):

@@ -189,6 +189,10 @@ static int cfg_check(const ThvmDecodeConfig *c) {
     hb_set_error("decoder: step_mode 1 (persistent step) is for the LLAMA architecture");
     return -1;
   }
+  if (c->attn_cpb > 4 || c->attn_cpb == 3) {
+    hb_set_error("decoder: attn_cpb is 0 (auto), 1, 2 or 4");
+    return -1;
+  }
   if (c->moe_mode > 2) {
     hb_set_error("decoder: moe_mode is 0 (auto), 1 (VALU grouped) or 2 (MFMA grouped)");
     return -1;
@@ -324,9 +328,9 @@ static int op_attn(Decoder *d, u32 l) {
   snprintf(kn, sizeof kn, "l%u.kcache", l);
   snprintf(vn, sizeof vn, "l%u.vcache", l);
   snprintf(p, sizeof p,
-           "thvm-builtin:attn b=%u h=%u hkv=%u hd=%u maxseq=%u chunk=64 nsplit=%u qt=%u ct=%u ot=%u scale=%a",
+           "thvm-builtin:attn b=%u h=%u hkv=%u hd=%u maxseq=%u chunk=64 nsplit=%u qt=%u ct=%u ot=%u scale=%a cpb=%u",
            c->batch, c->n_heads, c->n_kv_heads, c->head_dim, c->max_seq, d->n_split, c->adtype,
-           c->adtype, c->adtype, (float)(1.0 / sqrt((double)c->head_dim)));
+           c->adtype, c->adtype, (float)(1.0 / sqrt((double)c->head_dim)), c->attn_cpb);
   u32 a[6] = {tens_find(d, "att"), tens_find(d, "q"), tens_find(d, kn), tens_find(d, vn),
               tens_find(d, "len"), tens_find(d, "attn.part")};
   return op_add(d, "attn", p, a, 6);
