@@ -301,7 +301,11 @@ def run_decode(thvm, key: str, batch: int, args) -> dict:
                      "avg_launch_us": round(g_ms / g_n * 1000, 2)},
         "attention": ({"kernel": "a stage of k_llama_step (its bytes are in the roofline line)"}
                       if persist else
-                      {"kernel": "k_mla_split + k_mla_out" if mla else "k_attn + k_attn_merge",
+                      {"kernel": (("k_mla_split_mf (MFMA) + k_mla_out"
+                                   if (cfg["n_heads"], cfg["kv_lora"], cfg["d_rope"]) == (16, 512, 64)
+                                   else "k_mla_split + k_mla_out") if mla else
+                                  "k_attn_multi + k_attn_merge" if cfg["n_heads"] // cfg["n_kv_heads"] <= 4
+                                  else "k_attn + k_attn_merge"),
                        "achieved_gbs": round(attn_gbs, 1), "frac": round(attn_gbs / PEAK_GBS, 4),
                        "avg_launch_us": round(a_ms / max(a_n, 1) * 1000, 2)}),
         "kernels": {t: {"launches_per_step": n_t // prof_steps,

@@ -180,14 +180,14 @@ __device__ __forceinline__ bool gemv_core(const ThvmGemvArgs &a, unsigned char *
   const char *wb = (const char *)a.w;
 
   // ---- 1. loads in flight before any arithmetic ----
-  // Each wave's loads return in issue order.  Standalone at M = 1: x and a
-  // fused norm's gain / bias vectors are issued first, then the first weight
-  // batch, so the staging and the norm's block reductions run while the
-  // weights are in flight (measured on gfx950: 1.2-1.3 us less per fused-norm
-  // launch at the C4 shapes; no change without a norm).  With more rows (x
-  // would hold too many registers across the weight loads) and in the
-  // persistent kernel (COH: x is written by other blocks of the launch and is
-  // read only after wait()), the weights go first.
+  // Each wave's loads return in issue order.  Standalone at M = 1 with 16-bit
+  // x: x and a fused norm's gain / bias vectors are issued first, then the
+  // first weight batch, so the staging and the norm's block reductions run
+  // while the weights are in flight (measured on gfx950: 1.2-1.3 us less per
+  // fused-norm launch at the C4 shapes; no change without a norm; f32 x
+  // measured slower).  With more rows (x would hold too many registers across
+  // the weight loads) and in the persistent kernel (COH: x is written by other
+  // blocks of the launch and is read only after wait()), the weights go first.
   uint4 wq[R][U];
   auto load_batch = [&](uint32_t gg, uint32_t c0) {
     const uint32_t n0 = gg * R;
@@ -214,7 +214,7 @@ __device__ __forceinline__ bool gemv_core(const ThvmGemvArgs &a, unsigned char *
   // x row 0 as raw 16-byte vectors (!COH): the norm path's vectors tid + j*nthr,
   // or the no-norm path's first pass threadIdx.x + j*blockDim.x (clamped
   // indices; out-of-row vectors are never stored)
-  constexpr bool XPRE = !COH && M == 1;
+  constexpr bool XPRE = !COH && M == 1 && XD != XD_F32;
   uint4 xpre[NPRE];
   if (XPRE) {
     const char *x0 = (const char *)xrow(0);
