@@ -465,7 +465,16 @@ __global__ __launch_bounds__(64 * MM_WAVES) void k_moe_mm(ThvmMoeArgs a) {
 #pragma unroll
     for (int q = 0; q < (int)KL / 4; q++) xq[u][q] = buf_ld16(xrs, xs + 16 * q);
   };
-  auto compute = [&](int u) {
+  // the epilogue's operands, staged while the first loads are in flight:
+  // each column's (row, slot) and the block's row scales
+  __shared__ uint32_t col_b[16], col_slot[16];
+  __shared__ float rsc[16 * NT];
+  // consume step u: x converted once, then tile by tile -- each tile's
+  // weight registers are refilled with step `nxt` right after their last
+  // MFMA, so the next step's loads are in flight during the rest of this
+  // step's arithmetic (x is refilled after the last tile)
+  auto compute_refill = [&](int u, uint32_t nxt) {
+    uint4 H[NMF], L[NMF];
 #pragma unroll
     for (int j = 0; j < (int)NMF; j++) {
       const float *xf = (const float *)&xq[u][2 * j];
@@ -474,14 +483,21 @@ __global__ __launch_bounds__(64 * MM_WAVES) void k_moe_mm(ThvmMoeArgs a) {
       for (int i = 0; i < 4; i++) {
         const bf16_t h0 = f2bf(xf[2 * i]), h1 = f2bf(xf[2 * i + 1]);
         hb[i] = (uint32_t)h0 | ((uint32_t)h1 << 16);
+        lb[i] = 0;
         if (KIND == 1) {
           const bf16_t l0 = f2bf(xf[2 * i] - bf2f(h0)), l1 = f2bf(xf[2 * i + 1] - bf2f(h1));
           lb[i] = (uint32_t)l0 | ((uint32_t)l1 << 16);
         }
       }
-      const uint4 H = make_uint4(hb[0], hb[1], hb[2], hb[3]), L = make_uint4(lb[0], lb[1], lb[2], lb[3]);
+      H[j] = make_uint4(hb[0], hb[1], hb[2], hb[3]);
+      L[j] = make_uint4(lb[0], lb[1], lb[2], lb[3]);
+    }
+    const bool in = nxt < s1;
+    const uint32_t so = in ? nxt * 4 * LB : BUF_OOB;
 #pragma unroll
-      for (int t = 0; t < NT; t++) {
+    for (int t = 0; t < NT; t++) {
+#pragma unroll
+      for (int j = 0; j < (int)NMF; j++) {
         uint4 A;
         if (FP8) {
           const uint4 q = wq[u][t][j / 2];
@@ -490,19 +506,33 @@ __global__ __launch_bounds__(64 * MM_WAVES) void k_moe_mm(ThvmMoeArgs a) {
         } else {
           A = wq[u][t][j];
         }
-        acc[t] = mfma16<GX_BF16>(A, H, acc[t]);
-        if (KIND == 1) acc[t] = mfma16<GX_BF16>(A, L, acc[t]);
+        acc[t] = mfma16<GX_BF16>(A, H[j], acc[t]);
+        if (KIND == 1) acc[t] = mfma16<GX_BF16>(A, L[j], acc[t]);
       }
+#pragma unroll
+      for (int jj = 0; jj < (int)NC; jj++) wq[u][t][jj] = buf_ld_stream16(wrs, wo[t] + so + jj * 16);
     }
+    const uint32_t xs = in && xo != BUF_OOB ? xo + nxt * KS * 4 : BUF_OOB;
+#pragma unroll
+    for (int q = 0; q < (int)KL / 4; q++) xq[u][q] = buf_ld16(xrs, xs + 16 * q);
   };
 #pragma unroll
   for (int u = 0; u < NU; u++) load(u, s0 + u);
+  if (threadIdx.x < 16) {
+    const uint32_t m = threadIdx.x;
+    const uint32_t ent = c0 + m < nrows ? (shared ? c0 + m : (uint32_t)lst[c0 + m]) : 0u;
+    col_b[m] = shared ? ent : ent / K;
+    col_slot[m] = shared ? 0u : ent % K;
+  } else if (threadIdx.x < 16 + 16 * NT) {
+    const uint32_t i = threadIdx.x - 16, n = n0 + i;
+    const float *scp = KIND == 0 ? (shared ? a.sgu_s : a.sgu_e) : (shared ? a.sd_s : a.sd_e);
+    const uint64_t r = KIND == 0 ? (shared ? (uint64_t)n : (uint64_t)e * 2 * I + n)
+                                 : (shared ? (uint64_t)n : (uint64_t)e * D + n);
+    rsc[i] = (scp && n < NR) ? scp[r] : 1.0f;
+  }
   for (uint32_t sb = s0; sb < s1; sb += NU) {
 #pragma unroll
-    for (int u = 0; u < NU; u++) {
-      compute(u);
-      load(u, sb + u + NU);
-    }
+    for (int u = 0; u < NU; u++) compute_refill(u, sb + u + NU);
   }
 #pragma unroll
   for (int t = 0; t < NT; t++) {
@@ -514,8 +544,7 @@ __global__ __launch_bounds__(64 * MM_WAVES) void k_moe_mm(ThvmMoeArgs a) {
   const uint32_t per = KIND == 0 ? 8 * NT : 16 * NT;                  // row pairs / rows per column
   for (uint32_t task = threadIdx.x; task < per * ncols; task += 64 * MM_WAVES) {
     const uint32_t p = task % per, m = task / per;
-    const uint32_t ent = shared ? c0 + m : (uint32_t)lst[c0 + m];
-    const uint32_t b = shared ? ent : ent / K, slot = shared ? 0 : ent % K;
+    const uint32_t b = col_b[m], slot = col_slot[m];
     auto tile_val = [&](uint32_t ii_all) {                            // sum over waves, in order
       const uint32_t t = ii_all / 16, ii = ii_all % 16, ln = (ii / 4) * 16 + m, r = ii % 4;
       float sum = 0.0f;
@@ -530,19 +559,16 @@ __global__ __launch_bounds__(64 * MM_WAVES) void k_moe_mm(ThvmMoeArgs a) {
       const uint32_t i0 = 2 * p, n = n0 + i0;
       if (n >= NR) continue;                                          // NR is even
       float G = tile_val(i0), U = tile_val(i0 + 1);
-      const float *scp = shared ? a.sgu_s : a.sgu_e;
-      if (scp) {
-        const uint64_t r0 = shared ? (uint64_t)n : (uint64_t)e * 2 * I + n;
-        G *= scp[r0];
-        U *= scp[r0 + 1];
+      if (shared ? a.sgu_s : a.sgu_e) {
+        G *= rsc[i0];
+        U *= rsc[i0 + 1];
       }
       a.h[(uint64_t)b * P + (shared ? K * I : slot * I) + n / 2] = silu_f(G) * U;
     } else {
       const uint32_t n = n0 + p;
       if (n >= NR) continue;
       float sv = tile_val(p);
-      const float *scl = shared ? a.sd_s : a.sd_e;
-      if (scl) sv *= shared ? scl[n] : scl[(uint64_t)e * D + n];
+      if (shared ? a.sd_s : a.sd_e) sv *= rsc[p];
       const uint64_t o = shared ? (uint64_t)a.B * K * D + (uint64_t)b * D + n : ((uint64_t)b * K + slot) * D + n;
       a.part[o] = sv;
     }
