@@ -234,12 +234,43 @@ __global__ __launch_bounds__(MOE_THREADS) void k_moe_down(ThvmMoeArgs a) {
 }
 
 // ---- expert-grouped form (batches above 4 rows) ---------------------------
-// Rows routed to each expert, in ascending (b, slot) order: one thread per
-// expert scans the B*K routing entries.
-#define MOE_PLAN_MAX 4096   /* B*K routing entries staged in LDS */
+// Rows routed to each expert, in ascending (b, slot) order.  Up to
+// MOE_PLAN_REG * 64 entries: one wave holds entry c*64 + lane in register c
+// and compacts each expert's entries with a ballot (position = entries of
+// that expert in earlier registers and lower lanes), no serial scan.  Above
+// that: one thread per expert scans the entries from LDS.
+#define MOE_PLAN_MAX 4096   /* B*K routing entries */
+#define MOE_PLAN_REG 16
 __global__ __launch_bounds__(64) void k_moe_plan(ThvmMoeArgs a) {
   __shared__ int32_t sl[MOE_PLAN_MAX];
-  const uint32_t e = threadIdx.x, n = a.B * a.K;
+  const uint32_t lane = threadIdx.x, n = a.B * a.K;
+  if (n <= MOE_PLAN_REG * 64) {
+    int32_t sv[MOE_PLAN_REG];
+#pragma unroll
+    for (int c = 0; c < MOE_PLAN_REG; c++) {      // loads in flight together
+      const uint32_t i = c * 64 + lane;
+      sv[c] = i < n ? a.sel[i] : -1;
+    }
+    const uint64_t below = (1ull << lane) - 1ull;
+    uint32_t live = 0;
+    for (uint32_t e = 0; e < a.E; e++) {
+      int32_t *lst = a.plan + a.E + (uint64_t)e * n;
+      uint32_t base = 0;
+#pragma unroll
+      for (int c = 0; c < MOE_PLAN_REG; c++) {
+        if ((uint32_t)c * 64 >= n) break;           // wave-uniform
+        const bool hit = sv[c] == (int32_t)e;
+        const uint64_t m = __ballot(hit);
+        if (hit) lst[base + __popcll(m & below)] = (int32_t)(c * 64 + lane);
+        base += (uint32_t)__popcll(m);
+      }
+      if (lane == 0) a.plan[e] = (int32_t)base;
+      live += base > 0;
+    }
+    if (a.live && lane == 0 && live) atomicAdd(a.live, (int)live);   // experts streamed (measurement)
+    return;
+  }
+  const uint32_t e = threadIdx.x;
   for (uint32_t i = threadIdx.x; i < n; i += 64) sl[i] = a.sel[i];   // loads in flight together
   __syncthreads();
   if (e >= a.E) return;
