@@ -234,52 +234,37 @@ __global__ __launch_bounds__(MOE_THREADS) void k_moe_down(ThvmMoeArgs a) {
 }
 
 // ---- expert-grouped form (batches above 4 rows) ---------------------------
-// Rows routed to each expert, in ascending (b, slot) order.  Up to
-// MOE_PLAN_REG * 64 entries: one wave holds entry c*64 + lane in register c
-// and compacts each expert's entries with a ballot (position = entries of
-// that expert in earlier registers and lower lanes), no serial scan.  Above
-// that: one thread per expert scans the entries from LDS.
+// Rows routed to each expert, in ascending (b, slot) order.  One wave per
+// expert (grid E): the wave reads the B*K routing entries 64 at a time (four
+// chunks' loads in flight) and compacts its expert's entries with a ballot --
+// position = that expert's entries in earlier chunks and lower lanes -- so
+// every expert's list is built in parallel with no serial scan.
 #define MOE_PLAN_MAX 4096   /* B*K routing entries */
-#define MOE_PLAN_REG 16
 __global__ __launch_bounds__(64) void k_moe_plan(ThvmMoeArgs a) {
-  __shared__ int32_t sl[MOE_PLAN_MAX];
-  const uint32_t lane = threadIdx.x, n = a.B * a.K;
-  if (n <= MOE_PLAN_REG * 64) {
-    int32_t sv[MOE_PLAN_REG];
-#pragma unroll
-    for (int c = 0; c < MOE_PLAN_REG; c++) {      // loads in flight together
-      const uint32_t i = c * 64 + lane;
-      sv[c] = i < n ? a.sel[i] : -1;
-    }
-    const uint64_t below = (1ull << lane) - 1ull;
-    uint32_t live = 0;
-    for (uint32_t e = 0; e < a.E; e++) {
-      int32_t *lst = a.plan + a.E + (uint64_t)e * n;
-      uint32_t base = 0;
-#pragma unroll
-      for (int c = 0; c < MOE_PLAN_REG; c++) {
-        if ((uint32_t)c * 64 >= n) break;           // wave-uniform
-        const bool hit = sv[c] == (int32_t)e;
-        const uint64_t m = __ballot(hit);
-        if (hit) lst[base + __popcll(m & below)] = (int32_t)(c * 64 + lane);
-        base += (uint32_t)__popcll(m);
-      }
-      if (lane == 0) a.plan[e] = (int32_t)base;
-      live += base > 0;
-    }
-    if (a.live && lane == 0 && live) atomicAdd(a.live, (int)live);   // experts streamed (measurement)
-    return;
-  }
-  const uint32_t e = threadIdx.x;
-  for (uint32_t i = threadIdx.x; i < n; i += 64) sl[i] = a.sel[i];   // loads in flight together
-  __syncthreads();
-  if (e >= a.E) return;
+  const uint32_t e = blockIdx.x, lane = threadIdx.x, n = a.B * a.K;
   int32_t *lst = a.plan + a.E + (uint64_t)e * n;
-  int32_t c = 0;
-  for (uint32_t i = 0; i < n; i++)
-    if (sl[i] == (int32_t)e) lst[c++] = (int32_t)i;
-  a.plan[e] = c;
-  if (a.live && c > 0) atomicAdd(a.live, 1);     // experts streamed (measurement)
+  const uint64_t below = (1ull << lane) - 1ull;
+  uint32_t base = 0;
+  for (uint32_t c0 = 0; c0 < n; c0 += 4 * 64) {
+    int32_t v[4];
+#pragma unroll
+    for (int u = 0; u < 4; u++) {            // clamped indices: unconditional loads
+      const uint32_t i = c0 + u * 64 + lane, ic = i < n ? i : 0;
+      v[u] = a.sel[ic];
+    }
+#pragma unroll
+    for (int u = 0; u < 4; u++) {
+      const uint32_t i = c0 + u * 64 + lane;
+      const bool hit = i < n && v[u] == (int32_t)e;
+      const uint64_t m = __ballot(hit);
+      if (hit) lst[base + __popcll(m & below)] = (int32_t)i;
+      base += (uint32_t)__popcll(m);
+    }
+  }
+  if (lane == 0) {
+    a.plan[e] = (int32_t)base;
+    if (a.live && base > 0) atomicAdd(a.live, 1);     // experts streamed (measurement)
+  }
 }
 
 #define MOE_RG 4        /* x / h rows staged in LDS per pass */
@@ -730,7 +715,7 @@ static int moe_mm_launch(const ThvmMoeArgs *a, int gateup, hipStream_t s, char *
     snprintf(err, errlen, "moe: x / h above 2 GiB");
     return -1;
   }
-  if (gateup) thvm_launch(true, false, k_moe_plan, dim3(1), dim3(64), 0, s, *a);
+  if (gateup) thvm_launch(true, false, k_moe_plan, dim3(a->E), dim3(64), 0, s, *a);
   thvm_launch(!gateup, gateup, f, grid, dim3(64 * MM_WAVES), lds, s, *a);
   if (!gateup) thvm_launch(false, true, k_moe_combine, dim3((a->D + 255) / 256, a->B), dim3(256), 0, s, *a);
   hipError_t e = hipGetLastError();
@@ -757,7 +742,7 @@ extern "C" int thvm_k_moe_gateup(const ThvmMoeArgs *a, hipStream_t s, char *err,
       hipError_t e = hipFuncSetAttribute((const void *)f, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
       if (e != hipSuccess) { snprintf(err, errlen, "moe_gateup: hipFuncSetAttribute: %s", hipGetErrorString(e)); return -1; }
     }
-    thvm_launch(true, false, k_moe_plan, dim3(1), dim3(64), 0, s, *a);
+    thvm_launch(true, false, k_moe_plan, dim3(a->E), dim3(64), 0, s, *a);
     thvm_launch(false, true, f, grid, dim3(MOE_THREADS), lds, s, *a);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) { snprintf(err, errlen, "moe_gateup launch: %s", hipGetErrorString(e)); return -1; }
