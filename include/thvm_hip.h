@@ -259,8 +259,8 @@ typedef struct ThvmDecodeConfig {
    * or on the VALU (1); at 4 rows and below the per-row kernels run.      */
   uint32_t moe_mode;
   /* LLAMA / GPT2 attention: 64-row cache chunks per split block (0 auto,
-   * else 1, 2 or 4).  The persistent step's attention is the one-chunk
-   * form; an op-list decoder with attn_cpb 1 computes it bit for bit.     */
+   * else 1..64).  The persistent step's attention is the one-chunk form;
+   * an op-list decoder with attn_cpb 1 computes it bit for bit.           */
   uint32_t attn_cpb;
   uint32_t reserved[5];
 } ThvmDecodeConfig;

@@ -99,7 +99,7 @@ def test_step_config_errors(hip, bad):
         hip.Decoder(seed=1, **dict(BASE, step_mode=1, **bad))
 
 
-@pytest.mark.parametrize("cpb", [3, 8])
+@pytest.mark.parametrize("cpb", [65, 1000])
 def test_attn_cpb_config_errors(hip, cpb):
     with pytest.raises(hip.ThvmHipError):
         hip.Decoder(seed=1, **dict(BASE, attn_cpb=cpb))

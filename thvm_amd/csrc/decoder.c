@@ -189,8 +189,8 @@ static int cfg_check(const ThvmDecodeConfig *c) {
     hb_set_error("decoder: step_mode 1 (persistent step) is for the LLAMA architecture");
     return -1;
   }
-  if (c->attn_cpb > 4 || c->attn_cpb == 3) {
-    hb_set_error("decoder: attn_cpb is 0 (auto), 1, 2 or 4");
+  if (c->attn_cpb > 64) {
+    hb_set_error("decoder: attn_cpb is 0 (auto) or 1..64 chunks per split block");
     return -1;
   }
   if (c->moe_mode > 2) {

@@ -80,7 +80,7 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attn_fused(ThvmAttnArgs a) {
   }
 }
 
-// Batched split: one block runs CPB consecutive chunks of a (kv head, row),
+// Batched split: one block runs cpb (a.cpb) consecutive chunks of a (kv head, row),
 // the next chunk's K/V loads in flight while the current one is consumed.
 // The per-chunk work of the one-chunk unit is dominated by its fixed part at
 // large unit counts (the q decode, the wave-wide max and the row-group
@@ -89,16 +89,16 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attn_fused(ThvmAttnArgs a) {
 // accumulator across the block's chunks (online softmax: rescaled by
 // exp2(m_old - m_new) when the max grows), and the row groups and waves are
 // combined once per block.  The block writes one partial (acc, m, l) at slot
-// blockIdx.y of the merge's [n_split] rows; the merge reads ceil(L/(64 CPB))
+// blockIdx.y of the merge's [n_split] rows; the merge reads ceil(L/(64 cpb))
 // of them.  Used when B * Hkv * n_split is large (batched decode).
-template <int HD, int G, int AT, int CPB>
+template <int HD, int G, int AT>
 __global__ __launch_bounds__(ATT_THREADS, 4) void k_attn_multi(ThvmAttnArgs a) {   // 2 blocks per CU
   __shared__ AttnLds<HD, G> s;
   typedef AttnSplit<HD, G, AT, false> SU;
   constexpr int EPL = SU::EPL, LPR = SU::LPR, RPW = SU::RPW, PPW = SU::PPW, IT = SU::IT, ES = SU::ES;
   const uint32_t kvh = blockIdx.x, grp = blockIdx.y, b = blockIdx.z;
   const int32_t L = a.len[0];
-  const uint32_t c0 = grp * CPB;
+  const uint32_t cpb = a.cpb, c0 = grp * cpb;
   if ((int32_t)(c0 * ATT_CHUNK) >= L) return;      // the merge reads only live partials
   const int tid = threadIdx.x, wv = tid >> 6, lane = lane_id();
   const int rg = lane / LPR, li = lane % LPR;
@@ -180,7 +180,7 @@ __global__ __launch_bounds__(ATT_THREADS, 4) void k_attn_multi(ThvmAttnArgs a) {
     }
   };
   const uint32_t nlive = (uint32_t)((L + ATT_CHUNK - 1) / ATT_CHUNK);
-  const uint32_t nc = min((uint32_t)CPB, nlive - c0);   // block-uniform
+  const uint32_t nc = min(cpb, nlive - c0);            // block-uniform
   for (uint32_t c = 0; c < nc; c += 2) {               // two register sets, ping-pong
     issue(1, c0 + c + 1);
     consume(0);
@@ -249,18 +249,14 @@ __global__ __launch_bounds__(ATT_THREADS, 4) void k_attn_multi(ThvmAttnArgs a) {
 
 typedef void (*attn_fn)(ThvmAttnArgs);
 // (G = 8 heads per kv head would spill its accumulators: one chunk per block)
-template <int HD, int AT, int CPB>
+template <int HD, int AT>
 static attn_fn attn_pick_multi(uint32_t G) {
   switch (G) {
-    case 1: return k_attn_multi<HD, 1, AT, CPB>;
-    case 2: return k_attn_multi<HD, 2, AT, CPB>;
-    case 4: return k_attn_multi<HD, 4, AT, CPB>;
+    case 1: return k_attn_multi<HD, 1, AT>;
+    case 2: return k_attn_multi<HD, 2, AT>;
+    case 4: return k_attn_multi<HD, 4, AT>;
     default: return nullptr;
   }
-}
-template <int HD, int AT>
-static attn_fn attn_pick_cpb(uint32_t G, uint32_t cpb) {
-  return cpb == 2 ? attn_pick_multi<HD, AT, 2>(G) : attn_pick_multi<HD, AT, 4>(G);
 }
 template <int HD, int AT>
 static attn_fn attn_pick(uint32_t G, bool fused) {
@@ -307,27 +303,31 @@ extern "C" int thvm_k_attn_decode(const ThvmAttnArgs *a, hipStream_t s, char *er
   // block); at batched shapes 2 or 4, so each block's fixed work is shared
   // by more cache rows
   uint32_t cpb = a->cpb;
-  if (cpb > 4 || cpb == 3 || (fused && cpb > 1)) {
-    snprintf(err, errlen, "attn: cpb must be 0, 1, 2 or 4 (1 with fused)");
+  if (cpb > a->n_split) cpb = a->n_split;          // one block takes every chunk
+  if (fused && cpb > 1) {
+    snprintf(err, errlen, "attn: the one-launch form runs one chunk per block");
     return -1;
   }
   if (cpb == 0) {
     const uint64_t units = (uint64_t)a->B * a->Hkv * a->n_split;
     // (measured on gfx950 at the C4 shapes: two chunks per block beat one
     // at every unit count -- 11.3 against 12.9 us per launch at batch 1,
-    // where the merge also reads half the partials -- and four win above
-    // ~3000 units)
-    cpb = (fused || a->H / a->Hkv > 4) ? 1 : units >= 3072 ? 4 : 2;
+    // where the merge also reads half the partials.  Above 1024 units the
+    // chunk count keeps the grid within one round of 2 blocks per CU, so
+    // no tail round of a few blocks is left: 9 chunks at C4 batch 16)
+    const uint32_t bh = a->B * a->Hkv, groups = bh >= 512 ? 1u : 512u / bh;   // split blocks per (row, kv head)
+    cpb = (fused || a->H / a->Hkv > 4) ? 1 : units > 1024 ? (a->n_split + groups - 1) / groups : 2;
+    if (cpb > a->n_split) cpb = a->n_split;
   }
   attn_fn f = nullptr, fm = nullptr;
   const uint32_t G = a->H / a->Hkv;
   const int at = a->cdt == THVM_DT_BF16 ? AT_BF16 : a->cdt == THVM_DT_FP16 ? AT_F16 : AT_F32;
   if (a->hd == 128) {
-    f = cpb > 1 ? (at == AT_BF16 ? attn_pick_cpb<128, AT_BF16>(G, cpb) : at == AT_F16 ? attn_pick_cpb<128, AT_F16>(G, cpb) : attn_pick_cpb<128, AT_F32>(G, cpb))
+    f = cpb > 1 ? (at == AT_BF16 ? attn_pick_multi<128, AT_BF16>(G) : at == AT_F16 ? attn_pick_multi<128, AT_F16>(G) : attn_pick_multi<128, AT_F32>(G))
         : at == AT_BF16 ? attn_pick<128, AT_BF16>(G, fused) : at == AT_F16 ? attn_pick<128, AT_F16>(G, fused) : attn_pick<128, AT_F32>(G, fused);
     fm = at == AT_BF16 ? k_attn_merge<128, AT_BF16> : at == AT_F16 ? k_attn_merge<128, AT_F16> : k_attn_merge<128, AT_F32>;
   } else if (a->hd == 64) {
-    f = cpb > 1 ? (at == AT_BF16 ? attn_pick_cpb<64, AT_BF16>(G, cpb) : at == AT_F16 ? attn_pick_cpb<64, AT_F16>(G, cpb) : attn_pick_cpb<64, AT_F32>(G, cpb))
+    f = cpb > 1 ? (at == AT_BF16 ? attn_pick_multi<64, AT_BF16>(G) : at == AT_F16 ? attn_pick_multi<64, AT_F16>(G) : attn_pick_multi<64, AT_F32>(G))
         : at == AT_BF16 ? attn_pick<64, AT_BF16>(G, fused) : at == AT_F16 ? attn_pick<64, AT_F16>(G, fused) : attn_pick<64, AT_F32>(G, fused);
     fm = at == AT_BF16 ? k_attn_merge<64, AT_BF16> : at == AT_F16 ? k_attn_merge<64, AT_F16> : k_attn_merge<64, AT_F32>;
   }
