@@ -41,8 +41,12 @@
 // 64-k steps of its 16*MT rows at a time, with row-contiguous 16-byte loads
 // (8*SC lanes per row); the MFMA B operand is then read from LDS, rows padded
 // by 16 bytes so the 16 rows of one read fall in different banks.
+// GEMM_XSTAGE = 4 keeps a block's x staging at 66 KB, so two blocks share a
+// CU: measured on gfx950 against 8 (133 KB, one block per CU, the gate/up
+// grid of 448 blocks in 1.75 rounds), C4 batch 16 4.78 -> 4.57 ms per step,
+// C3 batch 8 3.30 -> 3.09 ms (4 is the least the 64-row tile takes).
 #ifndef GEMM_XSTAGE
-#define GEMM_XSTAGE 8                              // 64-k steps x 16-row tiles staged
+#define GEMM_XSTAGE 4                              // 64-k steps x 16-row tiles staged
 #endif
 #define GEMM_SC(MT) (GEMM_XSTAGE / (MT))
 #define GEMM_XROW(MT) (GEMM_SC(MT) * 128 + 16)
