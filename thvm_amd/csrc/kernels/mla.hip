@@ -65,21 +65,26 @@ __device__ __forceinline__ float group_sum(float v, int G) {
 }
 
 // ---- k_mla_prep ---------------------------------------------------------
-// blocks [0, H*QB): qlat rows (h, 64 latent rows each) for every batch row;
-// blocks [H*QB, H*QB + B): batch row b's q pe rotation, latent norm and cache
-// append.  256 threads.
+// blocks [0, H*QB*BG): qlat rows (h, 64 latent rows each) for a group of
+// MLA_PREP_ROWS batch rows (BG groups); blocks [H*QB*BG, H*QB*BG + B): batch
+// row b's q pe rotation, latent norm and cache append.  256 threads.  (One
+// block per (h, 64 rows) over all 32 rows of C5 batch 32 left 160 blocks,
+// each a 32-step serial loop: 33.7 us; groups of 8 rows give 512 blocks.)
+#define MLA_PREP_ROWS 8
 template <bool FP8>
 __global__ __launch_bounds__(256) void k_mla_prep(ThvmMlaArgs a) {
   extern __shared__ float sm[];
   const uint32_t H = a.H, dn = a.dn, dr = a.dr, kv = a.kv, half = dr / 2, qs = dn + dr;
-  const uint32_t qoff = H * qs, QB = kv / 64;
+  const uint32_t qoff = H * qs, QB = kv / 64, BG = (a.B + MLA_PREP_ROWS - 1) / MLA_PREP_ROWS;
   const int32_t pos = a.len[0] - 1;
-  if (blockIdx.x < H * QB) {
-    const uint32_t h = blockIdx.x / QB, k0 = (blockIdx.x % QB) * 64;
-    // q nope of every batch row into LDS (f32)
-    for (uint32_t i = threadIdx.x; i < a.B * dn; i += blockDim.x) {
+  if (blockIdx.x < H * QB * BG) {
+    const uint32_t h = blockIdx.x / (QB * BG), rem = blockIdx.x % (QB * BG);
+    const uint32_t k0 = (rem / BG) * 64, b0 = (rem % BG) * MLA_PREP_ROWS;
+    const uint32_t nb = min(a.B - b0, (uint32_t)MLA_PREP_ROWS);
+    // q nope of the group's batch rows into LDS (f32)
+    for (uint32_t i = threadIdx.x; i < nb * dn; i += blockDim.x) {
       const uint32_t b = i / dn, d = i % dn;
-      sm[i] = bfv(a.qkv, (uint64_t)b * a.ldq + h * qs + d);
+      sm[i] = bfv(a.qkv, (uint64_t)(b0 + b) * a.ldq + h * qs + d);
     }
     __syncthreads();
     const uint32_t rowb = dn * (FP8 ? 1 : 2), LPR = rowb / 16;     // lanes per row
@@ -96,16 +101,16 @@ __global__ __launch_bounds__(256) void k_mla_prep(ThvmMlaArgs a) {
       w16<FP8>(q0, q1, w);
       const uint32_t e0 = c * (FP8 ? 16 : 8), ne = FP8 ? 16 : 8;
       const float s = a.suk ? a.suk[row] : 1.0f;
-      for (uint32_t b = 0; b < a.B; b++) {
+      for (uint32_t b = 0; b < nb; b++) {
         float acc = 0.0f;
         for (uint32_t i = 0; i < ne; i++) acc += sm[b * dn + e0 + i] * w[i];
         acc = group_sum(acc, (int)LPR);
-        if (ok && c == 0) a.qlat[((uint64_t)b * H + h) * kv + k] = acc * s;
+        if (ok && c == 0) a.qlat[((uint64_t)(b0 + b) * H + h) * kv + k] = acc * s;
       }
     }
     return;
   }
-  const uint32_t b = blockIdx.x - H * QB;
+  const uint32_t b = blockIdx.x - H * QB * BG;
   if (b >= a.B || pos < 0 || (uint32_t)pos >= a.max_seq) return;
   const uint64_t qb = (uint64_t)b * a.ldq;
   // q pe pairs (2j, 2j+1) -> halves j and half+j, after rounding through bf16
@@ -626,11 +631,11 @@ extern "C" int thvm_k_mla_prep(const ThvmMlaArgs *a, hipStream_t s, char *err, i
              "(<= 64) and ldq hold the q|kv row");
     return -1;
   }
-  const uint32_t QB = a->kv / 64;
-  uint64_t lds = (uint64_t)a->B * a->dn * 4;
+  const uint32_t QB = a->kv / 64, BG = (a->B + MLA_PREP_ROWS - 1) / MLA_PREP_ROWS;
+  uint64_t lds = (uint64_t)(a->B < MLA_PREP_ROWS ? a->B : MLA_PREP_ROWS) * a->dn * 4;
   if ((uint64_t)a->kv * 4 + 64 > lds) lds = (uint64_t)a->kv * 4 + 64;
-  if (lds > 64 * 1024) { snprintf(err, errlen, "mla_prep: batch too large for LDS staging"); return -1; }
-  const dim3 grid(a->H * QB + a->B);
+  if (lds > 64 * 1024) { snprintf(err, errlen, "mla_prep: d_nope too large for LDS staging"); return -1; }
+  const dim3 grid(a->H * QB * BG + a->B);
   if (a->wdt == THVM_DT_FP8E4M3) thvm_launch(true, true, k_mla_prep<true>, grid, dim3(256), (uint32_t)lds, s, *a);
   else thvm_launch(true, true, k_mla_prep<false>, grid, dim3(256), (uint32_t)lds, s, *a);
   hipError_t e = hipGetLastError();
