@@ -290,6 +290,28 @@ __device__ __forceinline__ void attn_merge(const ThvmAttnArgs &a, uint32_t bh, i
     return COH ? coh_ldf(a.part, (uint32_t)((pbi + i) * 4)) : pb[i];
   };
   const int lane = lane_id();
+  // this thread's first MP splits' partial vectors, loaded with wave 0's
+  // (m, l) loads (clamped indices, unconditional): they do not depend on the
+  // split weights, so the merge waits for one memory round trip, not two
+  constexpr int U4P = HD / 4, SQP = 256 / U4P, MP = 4;
+  const int dqp = tid % U4P, sqp = tid / U4P;
+  float2 pv[MP][2];
+  if (active) {
+#pragma unroll
+    for (int j = 0; j < MP; j++) {
+      const uint32_t sp = sqp + j * SQP, spc = sp < n_live ? sp : 0;
+      const uint64_t q = (uint64_t)spc * (HD + 2) + dqp * 4;
+      if (COH) {
+        const uint2 r0 = coh_ld8(a.part, (uint32_t)((pbi + q) * 4));
+        const uint2 r1 = coh_ld8(a.part, (uint32_t)((pbi + q + 2) * 4));
+        pv[j][0] = make_float2(__uint_as_float(r0.x), __uint_as_float(r0.y));
+        pv[j][1] = make_float2(__uint_as_float(r1.x), __uint_as_float(r1.y));
+      } else {
+        pv[j][0] = *(const float2 *)(pb + q);
+        pv[j][1] = *(const float2 *)(pb + q + 2);
+      }
+    }
+  }
   if (active && tid < 64) {
     const float mv0 = lane < (int)n_live ? ldp((uint64_t)lane * (HD + 2) + HD) : -INFINITY;
     const float lv0 = lane < (int)n_live ? ldp((uint64_t)lane * (HD + 2) + HD + 1) : 0.0f;
@@ -307,8 +329,16 @@ __device__ __forceinline__ void attn_merge(const ThvmAttnArgs &a, uint32_t bh, i
   if (active) {
     const int dq = tid % U4, sq = tid / U4;
     float4 s4 = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+    for (int j = 0; j < MP; j++) {                 // the prefetched splits, in order
+      const uint32_t sp = sq + j * SQ;
+      if (sp < n_live) {
+        const float w = s.w[sp];
+        s4.x += w * pv[j][0].x; s4.y += w * pv[j][0].y; s4.z += w * pv[j][1].x; s4.w += w * pv[j][1].y;
+      }
+    }
 #pragma unroll 8
-    for (uint32_t sp = sq; sp < n_live; sp += SQ) {
+    for (uint32_t sp = sq + MP * SQ; sp < n_live; sp += SQ) {
       const float w = s.w[sp];
       const uint64_t q = (uint64_t)sp * (HD + 2) + dq * 4;
       // HD + 2 floats per split: a split's row is 8-byte aligned only
