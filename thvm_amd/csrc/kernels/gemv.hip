@@ -86,9 +86,12 @@ extern "C" int thvm_k_gemv(const ThvmGemvArgs *a, hipStream_t s, char *err, int 
     snprintf(err, errlen, "gemv: waves per block must be 1,2,4,8 or 16");
     return -1;
   }
-  if (a->norm && a->K > (uint64_t)XREG * 64 * waves) {
-    snprintf(err, errlen, "gemv: fused norm needs K <= %u for %u waves", XREG * 64 * waves, waves);
-    return -1;
+  {
+    const uint32_t nw_norm = waves < 8 ? waves : 8;   // the norm runs on at most 512 threads
+    if (a->norm && a->K > (uint64_t)XREG * 64 * nw_norm) {
+      snprintf(err, errlen, "gemv: fused norm needs K <= %u for %u waves", XREG * 64 * nw_norm, waves);
+      return -1;
+    }
   }
   int R = 1;
   int pairs = 0;
@@ -170,6 +173,18 @@ extern "C" int thvm_k_gemv(const ThvmGemvArgs *a, hipStream_t s, char *err, int 
   }
   if (!f) { snprintf(err, errlen, "gemv: no kernel instance (R=%d U=%d)", R, U); return -1; }
   uint32_t Gr = (a->N + R - 1) / R;
+  // 16 waves per block for a single x row whose weight rows are exactly one
+  // batch of chunks (every lane busy), when 8-wave blocks would put more than
+  // one block on some CUs and 16-wave blocks fit one per CU: the x staging
+  // (and a fused norm) then runs once per 16 waves, on every CU alike.
+  // Measured on gfx950 at the C4 shapes (K = 4096 fp8): qkv 10.6 -> 9.6 us,
+  // o 6.8 -> 6.6 us.  Long rows (C4 down, U = 8: 14.0 -> 15.3 us) and rows
+  // that leave lanes idle (C3 K = 1600 fp16, C1 K = 768 f32: slower steps)
+  // keep 8.
+  if (!a->tune_waves && Mk == 1 && chunks == 1 && (uint64_t)a->K * wsz / 16 == 64u * (uint32_t)U &&
+      (Gr + 7) / 8 > 256 && (Gr + 15) / 16 <= 256) {
+    waves = 16;
+  }
   uint32_t need = (Gr + waves - 1) / waves;
   uint32_t grid = need;
   if (a->tune_blocks) {

@@ -25,8 +25,12 @@ __global__ __launch_bounds__(1024) void k_gemv(ThvmGemvArgs a) {
     a.y = (char *)a.y + m0 * a.ldy * ys;
     if (a.res) a.res = (const char *)a.res + m0 * a.ldy * ys;
   }
+  // a fused norm reduces over the first 512 threads whatever the block size,
+  // so its summation order (and the rounded row it stages) is the same at 8
+  // and 16 waves per block, and the same as the persistent step's
+  const uint32_t nthr = blockDim.x < 512 ? blockDim.x : 512;
   gemv_core<WT, XD, M, R, U, false>(
-      a, xs_raw, red, g, gridDim.x * nw, blockDim.x, nw, [] { return true; },
+      a, xs_raw, red, g, gridDim.x * nw, nthr, (int)(nthr >> 6), [] { return true; },
       [&](int m) { return (const void *)((const char *)a.x + (uint64_t)m * a.ldx * XDr<XD>::B); },
       [](uint32_t, const float (&)[R][M]) {});
 }
