@@ -288,10 +288,11 @@ __global__ __launch_bounds__(MLA_THREADS) void k_mla_split(ThvmMlaArgs a) {
 // 512, rope 64): the 16 heads are the M side of v_mfma_f32_16x16x32_bf16.
 //   scores  S[h][row] = qlat[h] . c_row + qpe[h] . pe_row over k = 576 (18
 //           steps of 32): A = q (16 heads x 32 k), B = the cache rows (32 k x
-//           16 rows), one 16-row tile per wave; a lane's B operand is 8
-//           consecutive values of one row, one 16-byte load straight from HBM;
+//           16 rows), two waves per 16-row tile (k-steps 0..8 and 9..17,
+//           summed through LDS); a lane's B operand is 8 consecutive values
+//           of one row, one 16-byte load straight from HBM;
 //   mix     olat[h][:] += p[h][row] c_row: A = p (16 heads x 32 rows), B =
-//           the latent rows staged in LDS (32 rows x 16 columns), 8 column
+//           the latent rows staged in LDS (32 rows x 16 columns), 4 column
 //           tiles per wave.  The rows are staged column-major within each
 //           group of 8 rows ([row / 8][column][row % 8]), so a lane's B
 //           operand -- 8 rows of one column -- is one 16-byte LDS read; the
@@ -311,8 +312,9 @@ __global__ __launch_bounds__(MLA_THREADS) void k_mla_split(ThvmMlaArgs a) {
 #define MF_KS ((MF_KV + MF_DR) / 32)       /* 18 k-steps */
 #define MF_RGP (512 * 16 + 16)             /* LDS pitch of a staged 8-row group (bytes) */
 #define MF_PWP 68                          /* LDS pitch of a head's softmax weights (floats) */
-#define MF_THREADS 256
-#define MF_LDS (8 * MF_RGP + MF_KS * 2 * 64 * 16 + MF_H * MF_PWP * 4 + 2 * 4 * MF_H * 4)
+#define MF_THREADS 512                     /* 8 waves: two per 16-row tile */
+#define MF_KH (MF_KS / 2)                  /* k-steps per wave */
+#define MF_LDS (8 * MF_RGP + MF_KS * 2 * 64 * 16 + MF_H * MF_PWP * 4 + 2 * 4 * MF_H * 4 + 4 * 64 * 16)
 
 // eight f32 -> bf16 hi (RNE) and lo = bf16(v - hi), packed in operand order
 __device__ __forceinline__ void split8(const float4 &a, const float4 &b, uint4 &hi, uint4 &lo) {
@@ -329,20 +331,25 @@ __device__ __forceinline__ void split8(const float4 &a, const float4 &b, uint4 &
   lo = make_uint4(l[0], l[1], l[2], l[3]);
 }
 
-// grid (ceil(n_split / cpb), B), 256 threads (4 waves), cpb = a.cpb chunks
-// per block, two chunks' rows in flight
+// grid (ceil(n_split / cpb), B), 512 threads: wave w computes row tile
+// w % 4 over k-steps [9 (w / 4), 9 (w / 4) + 9) -- the two halves of a tile's
+// 576 k meet through LDS -- and column tiles 4w..4w+3 of the mix; cpb =
+// a.cpb chunks per block, two chunks' rows in flight.  (With one wave per
+// tile, each chunk's phases ran at one wave per SIMD: ~5.5 us per chunk.)
 __global__ __launch_bounds__(MF_THREADS) void k_mla_split_mf(ThvmMlaArgs a) {
   extern __shared__ __align__(16) unsigned char lds_mf[];
   unsigned char *cl = lds_mf;                                        // [8][MF_RGP]: [row/8][col][row%8]
   uint4 *qa = (uint4 *)(lds_mf + 8 * MF_RGP);                        // [MF_KS][hi, lo][64 lanes]
   float *pw = (float *)(lds_mf + 8 * MF_RGP + MF_KS * 2 * 64 * 16);  // [16 heads][MF_PWP]
-  float *rmax = pw + MF_H * MF_PWP, *rsum = rmax + 4 * MF_H;         // [4 waves][16 heads]
+  float *rmax = pw + MF_H * MF_PWP, *rsum = rmax + 4 * MF_H;         // [4 tiles][16 heads]
+  float4 *spart = (float4 *)(rsum + 4 * MF_H);                       // [4 tiles][64 lanes]
   const uint32_t cpb = a.cpb, grp = blockIdx.x, b = blockIdx.y;
   const int32_t L = min(a.len[0], (int32_t)a.max_seq);               // rows [0, L) are live
   const uint32_t cbeg = grp * cpb;
   if (L <= 0 || cbeg * 64 >= (uint32_t)L) return;                    // block-uniform
   const uint32_t cend = min(cbeg + cpb, ((uint32_t)L + 63) / 64);
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, li = lane & 15, lg = lane >> 4;
+  const int rt = wv & 3, kh = wv >> 2;                               // row tile, k half
   const char *ckv = (const char *)a.ckv + (uint64_t)b * a.max_seq * (MF_KV * 2);
   const char *kpe = (const char *)a.kpe + (uint64_t)b * a.max_seq * (MF_DR * 2);
 
@@ -352,9 +359,9 @@ __global__ __launch_bounds__(MF_THREADS) void k_mla_split_mf(ThvmMlaArgs a) {
   // from qlat (f32), 16..17 from qpe (bf16: exact, lo = 0)
   const float *ql = a.qlat + (uint64_t)b * MF_H * MF_KV;
   const bf16_t *qp = (const bf16_t *)a.qpe + (uint64_t)b * MF_H * MF_DR;
-  float4 qv[4][2];
+  float4 qv[2][2];
 #pragma unroll
-  for (int i = 0; i < 4; i++) {
+  for (int i = 0; i < 2; i++) {
     const uint32_t f = tid + MF_THREADS * i, l = f & 63;
     const uint32_t k0 = (f >> 6) * 32 + (l >> 4) * 8;
     qv[i][0] = *(const float4 *)(ql + (l & 15) * MF_KV + k0);
@@ -363,25 +370,27 @@ __global__ __launch_bounds__(MF_THREADS) void k_mla_split_mf(ThvmMlaArgs a) {
   const uint32_t fp = 16 * 64 + (tid & 127), lp = fp & 63;
   const uint4 qpv = *(const uint4 *)(qp + (lp & 15) * MF_DR + ((fp >> 6) - 16) * 32 + (lp >> 4) * 8);
 
-  // the B operands of chunk c for this wave's 16-row tile: 16 k-steps of the
-  // latent row, 2 of the pe row (rows past L load a live row of the chunk
-  // and are masked out of the softmax)
-  uint4 cfa[MF_KS], cfb[MF_KS];
-  auto issue = [&](uint4 (&cf)[MF_KS], uint32_t c) {
-    const uint32_t j = c * 64 + wv * 16 + li;
+  // the B operands of chunk c for this wave's tile and k half: 8 consecutive
+  // values of one row per k-step (latent row for k-steps 0..15, pe row for
+  // 16..17); rows past L load a live row of the chunk and are masked out of
+  // the softmax
+  uint4 cfa[MF_KH], cfb[MF_KH];
+  auto issue = [&](uint4 (&cf)[MF_KH], uint32_t c) {
+    const uint32_t j = c * 64 + rt * 16 + li;
     const uint32_t jc = j < (uint32_t)L ? j : c * 64;
     const char *cr = ckv + (uint64_t)jc * (MF_KV * 2) + lg * 16;
     const char *pr = kpe + (uint64_t)jc * (MF_DR * 2) + lg * 16;
 #pragma unroll
-    for (int ks = 0; ks < 16; ks++) cf[ks] = ld_stream16(cr + ks * 64);
-    cf[16] = ld_stream16(pr);
-    cf[17] = ld_stream16(pr + 64);
+    for (int st = 0; st < MF_KH; st++) {
+      const int ks = kh * MF_KH + st;
+      cf[st] = ld_stream16(ks < 16 ? cr + ks * 64 : pr + (ks - 16) * 64);
+    }
   };
   issue(cfa, cbeg);
   if (cbeg + 1 < cend) issue(cfb, cbeg + 1);
 
 #pragma unroll
-  for (int i = 0; i < 4; i++) {
+  for (int i = 0; i < 2; i++) {
     const uint32_t f = tid + MF_THREADS * i;
     uint4 hi, lo;
     split8(qv[i][0], qv[i][1], hi, lo);
@@ -395,63 +404,79 @@ __global__ __launch_bounds__(MF_THREADS) void k_mla_split_mf(ThvmMlaArgs a) {
   __syncthreads();
 
   float m_run[4], l_run[4];
-  f32x4_t oacc[8];
+  f32x4_t oacc[4];
 #pragma unroll
   for (int i = 0; i < 4; i++) { m_run[i] = -INFINITY; l_run[i] = 0.0f; }
 #pragma unroll
-  for (int t = 0; t < 8; t++) oacc[t] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+  for (int t = 0; t < 4; t++) oacc[t] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
 
   // one chunk: its rows are in cf; chunk c + 2 goes into cf once the scores
   // have consumed it
-  auto chunk = [&](uint4 (&cf)[MF_KS], uint32_t c) {
+  auto chunk = [&](uint4 (&cf)[MF_KH], uint32_t c) {
     const uint32_t nj = min((uint32_t)L - c * 64, 64u);
-    // 1. scores of the wave's tile: lane holds S[head 4 lg + i][row 16 wv + li]
-    //    (four independent accumulator chains: q hi / lo x even / odd steps)
+    // 1. this wave's half of its tile's scores: lane holds S[head 4 lg + i]
+    //    [row 16 rt + li] over its 9 k-steps (four independent chains)
     f32x4_t sc[4];
 #pragma unroll
     for (int u = 0; u < 4; u++) sc[u] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-    for (int ks = 0; ks < MF_KS; ks++) {
-      sc[(ks & 1) * 2] = mfma16<GX_BF16>(qa[ks * 128 + lane], cf[ks], sc[(ks & 1) * 2]);
-      sc[(ks & 1) * 2 + 1] = mfma16<GX_BF16>(qa[ks * 128 + 64 + lane], cf[ks], sc[(ks & 1) * 2 + 1]);
+    for (int st = 0; st < MF_KH; st++) {
+      const int ks = kh * MF_KH + st;
+      sc[(st & 1) * 2] = mfma16<GX_BF16>(qa[ks * 128 + lane], cf[st], sc[(st & 1) * 2]);
+      sc[(st & 1) * 2 + 1] = mfma16<GX_BF16>(qa[ks * 128 + 64 + lane], cf[st], sc[(st & 1) * 2 + 1]);
     }
-    // the latent part of the tile's rows into LDS for the mix: row r, column
-    // k at [r / 8][k][r % 8]
+    // the latent part of the wave's rows into LDS for the mix: row r,
+    // column k at [r / 8][k][r % 8]
     {
-      const uint32_t r = wv * 16 + li;
+      const uint32_t r = rt * 16 + li;
       unsigned char *dst = cl + (r >> 3) * MF_RGP + (r & 7) * 2 + lg * 8 * 16;
 #pragma unroll
-      for (int ks = 0; ks < 16; ks++) {
-        const uint32_t w[4] = {cf[ks].x, cf[ks].y, cf[ks].z, cf[ks].w};
+      for (int st = 0; st < MF_KH; st++) {
+        const int ks = kh * MF_KH + st;
+        if (ks >= 16) break;                         // wave-uniform: the pe k-steps
+        const uint32_t w[4] = {cf[st].x, cf[st].y, cf[st].z, cf[st].w};
 #pragma unroll
         for (int e = 0; e < 8; e++)
           *(uint16_t *)(dst + (ks * 32 + e) * 16) = (uint16_t)(w[e >> 1] >> ((e & 1) * 16));
       }
     }
+    float4 part_s;
+    part_s.x = (sc[0][0] + sc[1][0]) + (sc[2][0] + sc[3][0]);
+    part_s.y = (sc[0][1] + sc[1][1]) + (sc[2][1] + sc[3][1]);
+    part_s.z = (sc[0][2] + sc[1][2]) + (sc[2][2] + sc[3][2]);
+    part_s.w = (sc[0][3] + sc[1][3]) + (sc[2][3] + sc[3][3]);
+    if (kh == 1) spart[rt * 64 + lane] = part_s;
     if (c + 2 < cend) issue(cf, c + 2);   // in flight during two chunks' softmax and mix
+    __syncthreads();
 
-    // 2. softmax over the chunk's rows, online across the block's chunks
-    const bool rok = (uint32_t)(wv * 16 + li) < nj;
+    // 2. softmax over the chunk's rows (the first-half waves hold the full
+    //    scores), online across the block's chunks
+    const bool rok = (uint32_t)(rt * 16 + li) < nj;
     float sv[4];
+    if (kh == 0) {
+      const float4 o = spart[rt * 64 + lane];
+      const float full[4] = {part_s.x + o.x, part_s.y + o.y, part_s.z + o.z, part_s.w + o.w};
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
-      const float st = (sc[0][i] + sc[1][i]) + (sc[2][i] + sc[3][i]);
-      sv[i] = rok ? st * a.scale : -INFINITY;
-      const float m = row16_max(sv[i]);
-      if (li == 0) rmax[wv * MF_H + 4 * lg + i] = m;
+      for (int i = 0; i < 4; i++) {
+        sv[i] = rok ? full[i] * a.scale : -INFINITY;
+        const float m = row16_max(sv[i]);
+        if (li == 0) rmax[rt * MF_H + 4 * lg + i] = m;
+      }
     }
     __syncthreads();
-    float mn[4], al[4], p[4];
+    float mn[4], al[4];
 #pragma unroll
     for (int i = 0; i < 4; i++) {
       const int h = 4 * lg + i;
       const float m = fmaxf(fmaxf(rmax[h], rmax[MF_H + h]), fmaxf(rmax[2 * MF_H + h], rmax[3 * MF_H + h]));
       mn[i] = fmaxf(m_run[i], m);
       al[i] = m_run[i] == -INFINITY ? 0.0f : expf(m_run[i] - mn[i]);
-      p[i] = rok ? expf(sv[i] - mn[i]) : 0.0f;
-      const float ps = row16_sum(p[i]);
-      if (li == 0) rsum[wv * MF_H + h] = ps;
-      pw[h * MF_PWP + wv * 16 + li] = p[i];
+      if (kh == 0) {
+        const float p = rok ? expf(sv[i] - mn[i]) : 0.0f;
+        const float ps = row16_sum(p);
+        if (li == 0) rsum[rt * MF_H + h] = ps;
+        pw[h * MF_PWP + rt * 16 + li] = p;
+      }
     }
     __syncthreads();
 #pragma unroll
@@ -461,9 +486,9 @@ __global__ __launch_bounds__(MF_THREADS) void k_mla_split_mf(ThvmMlaArgs a) {
       l_run[i] = l_run[i] * al[i] + l;
       m_run[i] = mn[i];
     }
-    // 3. mix: olat tiles kt = 8 wv + t, lane holds O[head 4 lg + i][16 kt + li]
+    // 3. mix: olat tiles kt = 4 wv + t, lane holds O[head 4 lg + i][16 kt + li]
 #pragma unroll
-    for (int t = 0; t < 8; t++)
+    for (int t = 0; t < 4; t++)
 #pragma unroll
       for (int i = 0; i < 4; i++) oacc[t][i] *= al[i];
 #pragma unroll
@@ -473,13 +498,13 @@ __global__ __launch_bounds__(MF_THREADS) void k_mla_split_mf(ThvmMlaArgs a) {
       split8(*(const float4 *)pr, *(const float4 *)(pr + 4), ah, alo);
       const unsigned char *rb = cl + (q * 4 + lg) * MF_RGP + li * 16;
 #pragma unroll
-      for (int t = 0; t < 8; t++) {
-        const uint4 bv = *(const uint4 *)(rb + (wv * 8 + t) * 16 * 16);
+      for (int t = 0; t < 4; t++) {
+        const uint4 bv = *(const uint4 *)(rb + (wv * 4 + t) * 16 * 16);
         oacc[t] = mfma16<GX_BF16>(ah, bv, oacc[t]);
         oacc[t] = mfma16<GX_BF16>(alo, bv, oacc[t]);
       }
     }
-    __syncthreads();                               // cl, pw and the reductions are reused
+    __syncthreads();                               // cl, pw, spart and the reductions are reused
   };
   for (uint32_t c = cbeg; c < cend; c += 2) {
     chunk(cfa, c);
@@ -488,9 +513,9 @@ __global__ __launch_bounds__(MF_THREADS) void k_mla_split_mf(ThvmMlaArgs a) {
 
   float *part = a.part + ((uint64_t)b * a.n_split + grp) * MF_H * (MF_KV + 4);
 #pragma unroll
-  for (int t = 0; t < 8; t++)
+  for (int t = 0; t < 4; t++)
 #pragma unroll
-    for (int i = 0; i < 4; i++) part[(4 * lg + i) * (MF_KV + 4) + (wv * 8 + t) * 16 + li] = oacc[t][i];
+    for (int i = 0; i < 4; i++) part[(4 * lg + i) * (MF_KV + 4) + (wv * 4 + t) * 16 + li] = oacc[t][i];
   if (wv == 0 && li == 0) {
 #pragma unroll
     for (int i = 0; i < 4; i++) {
@@ -687,7 +712,7 @@ extern "C" int thvm_k_mla_attn(const ThvmMlaArgs *a, hipStream_t s, char *err, i
   if (a->mode == 2 || (a->mode == 0 && mf_shape)) {
     // MFMA split: cpb 64-row chunks per block (fewer partials to write and
     // merge with more rows per block)
-    // (a block holds ~105 KB of LDS, so one block per CU: the smallest chunk
+    // (a block holds ~109 KB of LDS, so one block per CU: the smallest chunk
     // count that keeps the grid within one block per CU of the 256, so the
     // split runs in a single round)
     uint32_t cpb = a->cpb;
