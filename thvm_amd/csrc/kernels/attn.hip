@@ -314,9 +314,13 @@ extern "C" int thvm_k_attn_decode(const ThvmAttnArgs *a, hipStream_t s, char *er
     // at every unit count -- 11.3 against 12.9 us per launch at batch 1,
     // where the merge also reads half the partials.  Above 1024 units the
     // chunk count keeps the grid within one round of 2 blocks per CU, so
-    // no tail round of a few blocks is left: 9 chunks at C4 batch 16)
+    // no tail round of a few blocks is left: 9 chunks at C4 batch 16.  With
+    // at most 4 chunks per head and a grid of at most one such round, the
+    // merge has little to save and one chunk per block runs the chunks side
+    // by side: C3 batch 1 (4 chunks, 100 units) 1.818 -> 1.785 ms per step)
     const uint32_t bh = a->B * a->Hkv, groups = bh >= 512 ? 1u : 512u / bh;   // split blocks per (row, kv head)
-    cpb = (fused || a->H / a->Hkv > 4) ? 1 : units > 1024 ? (a->n_split + groups - 1) / groups : 2;
+    cpb = (fused || a->H / a->Hkv > 4 || (a->n_split <= 4 && units <= 512)) ? 1
+        : units > 1024 ? (a->n_split + groups - 1) / groups : 2;
     if (cpb > a->n_split) cpb = a->n_split;
   }
   attn_fn f = nullptr, fm = nullptr;
