@@ -316,16 +316,23 @@ __global__ __launch_bounds__(MLA_THREADS) void k_mla_split(ThvmMlaArgs a) {
 #define MF_KH (MF_KS / 2)                  /* k-steps per wave */
 #define MF_LDS (8 * MF_RGP + MF_KS * 2 * 64 * 16 + MF_H * MF_PWP * 4 + 2 * 4 * MF_H * 4 + 4 * 64 * 16)
 
+// two f32 -> a packed bf16 pair, round to nearest even (the rounding of
+// f2bf), in one v_cvt_pk_bf16_f32; element 0 in the low half
+typedef float mf_f2 __attribute__((ext_vector_type(2)));
+typedef __bf16 mf_b2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint32_t pk_bf16(float a, float b) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((mf_f2){a, b}, mf_b2));
+}
+
 // eight f32 -> bf16 hi (RNE) and lo = bf16(v - hi), packed in operand order
+// (v - hi is exact in f32)
 __device__ __forceinline__ void split8(const float4 &a, const float4 &b, uint4 &hi, uint4 &lo) {
   const float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
   uint32_t h[4], l[4];
 #pragma unroll
   for (int i = 0; i < 4; i++) {
-    const bf16_t h0 = f2bf(v[2 * i]), h1 = f2bf(v[2 * i + 1]);
-    const bf16_t l0 = f2bf(v[2 * i] - bf2f(h0)), l1 = f2bf(v[2 * i + 1] - bf2f(h1));
-    h[i] = (uint32_t)h0 | ((uint32_t)h1 << 16);
-    l[i] = (uint32_t)l0 | ((uint32_t)l1 << 16);
+    h[i] = pk_bf16(v[2 * i], v[2 * i + 1]);
+    l[i] = pk_bf16(v[2 * i] - __uint_as_float(h[i] << 16), v[2 * i + 1] - __uint_as_float(h[i] & 0xffff0000u));
   }
   hi = make_uint4(h[0], h[1], h[2], h[3]);
   lo = make_uint4(l[0], l[1], l[2], l[3]);
