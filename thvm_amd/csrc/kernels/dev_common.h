@@ -31,6 +31,13 @@ __device__ __forceinline__ bf16_t f2bf(float f) {
 }
 // round a float through bf16 storage
 __device__ __forceinline__ float rbf(float f) { return bf2f(f2bf(f)); }
+// two f32 -> a packed bf16 pair, round to nearest even (f2bf's rounding for
+// every non-NaN input), in one v_cvt_pk_bf16_f32; element 0 in the low half
+typedef float f32x2_cvt_t __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2_cvt_t __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint32_t pk_bf16(float a, float b) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_cvt_t){a, b}, bf16x2_cvt_t));
+}
 
 // ---- fp16 ------------------------------------------------------------------
 __device__ __forceinline__ float h2f(f16_t h) {

@@ -316,14 +316,6 @@ __global__ __launch_bounds__(MLA_THREADS) void k_mla_split(ThvmMlaArgs a) {
 #define MF_KH (MF_KS / 2)                  /* k-steps per wave */
 #define MF_LDS (8 * MF_RGP + MF_KS * 2 * 64 * 16 + MF_H * MF_PWP * 4 + 2 * 4 * MF_H * 4 + 4 * 64 * 16)
 
-// two f32 -> a packed bf16 pair, round to nearest even (the rounding of
-// f2bf), in one v_cvt_pk_bf16_f32; element 0 in the low half
-typedef float mf_f2 __attribute__((ext_vector_type(2)));
-typedef __bf16 mf_b2 __attribute__((ext_vector_type(2)));
-__device__ __forceinline__ uint32_t pk_bf16(float a, float b) {
-  return __builtin_bit_cast(uint32_t, __builtin_convertvector((mf_f2){a, b}, mf_b2));
-}
-
 // eight f32 -> bf16 hi (RNE) and lo = bf16(v - hi), packed in operand order
 // (v - hi is exact in f32)
 __device__ __forceinline__ void split8(const float4 &a, const float4 &b, uint4 &hi, uint4 &lo) {

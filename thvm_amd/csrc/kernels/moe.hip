@@ -497,12 +497,17 @@ __global__ __launch_bounds__(64 * MM_WAVES) void k_moe_mm(ThvmMoeArgs a) {
       uint32_t hb[4], lb[4];
 #pragma unroll
       for (int i = 0; i < 4; i++) {
-        const bf16_t h0 = f2bf(xf[2 * i]), h1 = f2bf(xf[2 * i + 1]);
-        hb[i] = (uint32_t)h0 | ((uint32_t)h1 << 16);
-        lb[i] = 0;
+        // bf16 hi (and for down lo = v - hi, exact in f32), round to nearest
+        // even.  Down rounds in hardware (76.0 -> 70.4 us per layer at C5
+        // batch 32); gate/up keeps the software form, with which its
+        // instance holds 148 VGPRs (3 waves per SIMD) instead of 222
         if (KIND == 1) {
-          const bf16_t l0 = f2bf(xf[2 * i] - bf2f(h0)), l1 = f2bf(xf[2 * i + 1] - bf2f(h1));
-          lb[i] = (uint32_t)l0 | ((uint32_t)l1 << 16);
+          hb[i] = pk_bf16(xf[2 * i], xf[2 * i + 1]);
+          lb[i] = pk_bf16(xf[2 * i] - __uint_as_float(hb[i] << 16), xf[2 * i + 1] - __uint_as_float(hb[i] & 0xffff0000u));
+        } else {
+          const bf16_t h0 = f2bf(xf[2 * i]), h1 = f2bf(xf[2 * i + 1]);
+          hb[i] = (uint32_t)h0 | ((uint32_t)h1 << 16);
+          lb[i] = 0;
         }
       }
       H[j] = make_uint4(hb[0], hb[1], hb[2], hb[3]);
