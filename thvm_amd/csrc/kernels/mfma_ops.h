@@ -15,12 +15,15 @@ enum { GX_BF16 = 0, GX_F16 = 1 };               // x storage = MFMA operand type
 template <int XT>
 __device__ __forceinline__ void fp8x4_op(uint32_t w, uint32_t &lo, uint32_t &hi) {
   typedef float f2_t __attribute__((ext_vector_type(2)));
-  f2_t a = __builtin_amdgcn_cvt_pk_f32_fp8(w, false);
-  f2_t b = __builtin_amdgcn_cvt_pk_f32_fp8(w, true);
-  if (XT == GX_BF16) {   // an e4m3 value has <= 4 significant bits: truncation is exact
-    lo = (__float_as_uint(a[0]) >> 16) | (__float_as_uint(a[1]) & 0xffff0000u);
-    hi = (__float_as_uint(b[0]) >> 16) | (__float_as_uint(b[1]) & 0xffff0000u);
-  } else {               // and is exact in fp16 (normal range 2^-14..2^15)
+  if (XT == GX_BF16) {
+    // straight to packed bf16, two values per v_cvt_scalef32_pk_bf16_fp8
+    // (scale 1): an e4m3 value has <= 4 significant bits and its exponent
+    // range fits bf16's, so the conversion is exact
+    lo = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w, 1.0f, false));
+    hi = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w, 1.0f, true));
+  } else {               // via f32; exact in fp16 too (normal range 2^-14..2^15)
+    f2_t a = __builtin_amdgcn_cvt_pk_f32_fp8(w, false);
+    f2_t b = __builtin_amdgcn_cvt_pk_f32_fp8(w, true);
     lo = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(a[0], a[1]));
     hi = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(b[0], b[1]));
   }
