@@ -268,6 +268,27 @@ def test_gemm_mfma_store_f32(hip, wx, M, NK):
     assert np.all(err <= 1e-5 * floor + 1e-30), f"max rel {np.max(err / (floor + 1e-30))}"
 
 
+@pytest.mark.parametrize("xdt", [DT_BF16, DT_F16])
+def test_gemm_mfma_fp8_operand_decode_all_patterns(hip, xdt):
+    """Every finite e4m3 pattern through the MFMA GEMM's operand decode:
+    x rows are one-hot (row m = 1.0 at k = m), so y[m][n] is the decoded
+    W[n][m] alone (times a row scale of 1.0) and must equal the table value
+    exactly.  W[n][k] = (n + k) mod 256 puts each pattern at every k; the two
+    NaN patterns are replaced by 0."""
+    N, K, M = 256, 64, 64
+    say(f"case: gemm mfma fp8 operand decode, all patterns, xdt={xdt}")
+    w = ((np.arange(N)[:, None] + np.arange(K)[None, :]) % 256).astype(np.uint8)
+    w[(w & 0x7F) == 0x7F] = 0
+    x = O.encode(np.eye(M, K, dtype=np.float32), xdt)
+    scale = np.ones(N, np.float32)
+    y = hip.Buffer(M * N * 4)
+    hip.builtin("gemv", [y, up(hip, x), up(hip, w), up(hip, scale)], m=M, n=N, k=K, wt=DT_FP8,
+                xt=xdt, yt=DT_F32, epi=0, path=2)
+    got = y.read(np.float32).reshape(M, N)
+    want = O.decode(w, DT_FP8).T[:M]            # y[m][n] = decode(W[n][m])
+    assert np.array_equal(got, want), f"{np.count_nonzero(got != want)} values differ"
+
+
 @pytest.mark.parametrize("nt", [1, 2, 4])
 @pytest.mark.parametrize("M", [16, 64])
 def test_gemm_mfma_tile_counts_agree(hip, nt, M):

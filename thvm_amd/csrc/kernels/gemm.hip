@@ -15,7 +15,8 @@
 //     (lanes 0-15 rows, lanes 16-63 the next k quarters): a wave's load
 //     instruction covers 16 rows x 64 k, nontemporal 16-byte loads;
 //   * fp8 decodes exactly into the x operand type (e4m3 values are exact in
-//     bf16 and fp16) with v_cvt_pk_f32_fp8; the row scale multiplies the
+//     bf16 and fp16): v_cvt_scalef32_pk_bf16_fp8 for bf16, v_cvt_pk_f32_fp8
+//     then a pack for fp16; the row scale multiplies the
 //     finished sum, as in the dequantised reference computation;
 //   * the 8 waves of a block split K into contiguous slices; partial tiles
 //     meet in LDS and are summed in wave order (deterministic), then each
