@@ -63,85 +63,82 @@ uint16_t or_f32_to_fp16(float v) {
   return (uint16_t)(sign | h);
 }
 
-/* ==== fp8: reference src/dtype/fp8.c:36-175 ============================== */
+/* ==== fp8 e4m3 / e5m2 ======================================================
+ * Written from the OCP 8-bit floating point specification (OFP8, v1.0):
+ *   e4m3: bias 7, 3 mantissa bits, no infinities, S.1111.111 is NaN,
+ *         largest finite 0x7E = 448;
+ *   e5m2: bias 15, 2 mantissa bits, IEEE-style inf (S.11111.00) and NaN,
+ *         largest finite 0x7B = 57344.
+ * A finite value rounds to nearest, ties to even, on the f32 significand;
+ * subnormals are kept; a finite value whose rounded magnitude exceeds the
+ * largest finite one stores the largest finite one (both forms).  The
+ * non-finite conventions are the reference's (src/dtype/fp8.c, its store
+ * path and tests/test_fp8_nonfinite.c:110-192): the plain form stores
+ * +-inf and NaN as S.1111.111 (e4m3) and +-inf as S.11111.00, NaN as
+ * S.11111.11 (e5m2); the _sat form stores +-inf as +-max finite and a NaN
+ * as the format's all-ones exponent over the top mantissa bits of the f32
+ * NaN (e4m3: always S.1111.111). */
 typedef struct {
-  uint32_t bias, sig_bits, mmask;
-  uint64_t mindenorm_o2, overflow, minnorm;
-  uint32_t maxnorm, inf_v, nan_v, sat_nan;
-} F8;
-static const F8 E4M3 = {7, 4, 0x7, 0x3F50000000000000ULL, 0x407D000000000000ULL,
-                        0x3F90000000000000ULL, 0x7E, 0x7F, 0x7F, 0x7F};
-static const F8 E5M2 = {15, 3, 0x3, 0x3EE0000000000000ULL, 0x40EE000000000000ULL - 1,
-                        0x3F10000000000000ULL, 0x7B, 0x7C, 0x7F, 0x7C};
+  int mbits, bias;
+  uint32_t max_code, inf_code, nan_code;
+} Ofp8;
+static const Ofp8 OFP8_E4M3 = {3, 7, 0x7E, 0x7F, 0x7F};
+static const Ofp8 OFP8_E5M2 = {2, 15, 0x7B, 0x7C, 0x7F};
 
-static uint8_t f8_enc(float x, const F8 *c, int sat) {
-  double xd = (double)x;
-  uint64_t xb;
-  memcpy(&xb, &xd, 8);
-  uint64_t ax = xb & 0x7FFFFFFFFFFFFFFFULL, inf = 0x7FF0000000000000ULL;
-  uint32_t sign = (uint32_t)((xb >> 63) & 1) << 7;
-  if (ax == inf) return (uint8_t)(sign | (sat ? c->maxnorm : c->inf_v));
-  if (ax > inf) {
-    if (!sat) return (uint8_t)(sign | c->nan_v);
-    uint32_t top = (f2u(x) >> (24 - c->sig_bits)) & c->mmask;
-    return (uint8_t)(sign | c->sat_nan | top);
+static uint8_t ofp8_encode(float x, const Ofp8 *f, int sat) {
+  const uint32_t u = f2u(x), sign = (u >> 24) & 0x80u, a = u & 0x7FFFFFFFu;
+  if (a > 0x7F800000u) { /* NaN */
+    if (!sat || f->mbits == 3) return (uint8_t)(sign | f->nan_code);
+    return (uint8_t)(sign | f->inf_code | ((a >> (23 - f->mbits)) & ((1u << f->mbits) - 1u)));
   }
-  uint64_t half_ulp = (uint64_t)1 << (53 - c->sig_bits - 1);
-  int32_t e = (int32_t)((xb >> 52) & 0x7FF) - 1023 + (int32_t)c->bias;
-  uint32_t mant = (uint32_t)((xb >> (53 - c->sig_bits)) & c->mmask);
-  uint32_t res;
-  if (ax <= c->mindenorm_o2) {
-    res = 0;
-  } else if (ax > c->overflow) {
-    res = c->maxnorm;
-  } else if (ax >= c->minnorm) {
-    res = ((uint32_t)e << (c->sig_bits - 1)) | mant;
-    uint64_t rb = xb & ((half_ulp << 1) - 1);
-    if (rb > half_ulp || (rb == half_ulp && (mant & 1))) res += 1;
+  if (a == 0x7F800000u) return (uint8_t)(sign | (sat ? f->max_code : f->inf_code));
+  /* |x| = sig * 2^(ef - 150) with sig < 2^24 */
+  int ef = (int)(a >> 23);
+  uint32_t sig = a & 0x7FFFFFu;
+  if (ef) sig |= 0x800000u; else ef = 1;
+  const int emin = 1 - f->bias;              /* exponent of the smallest normal */
+  int e = ef - 127;                          /* exponent of the leading bit (normal f32) */
+  if (e < emin) e = emin;                    /* below emin the quantum stays 2^(emin-mbits) */
+  const int sh = (e - f->mbits) - (ef - 150); /* sig / 2^sh = |x| / quantum, sh >= 20 */
+  uint32_t n = 0;
+  if (sh <= 24) {
+    const uint32_t rem = sig & ((1u << sh) - 1u), half = 1u << (sh - 1);
+    n = sig >> sh;
+    if (rem > half || (rem == half && (n & 1u))) n++;
+  } /* sh > 24: |x| is below half a quantum, rounds to zero */
+  /* n counts quanta 2^(e - mbits); the code is ((e + bias - 1) << mbits) + n,
+   * which also covers the subnormals (e = emin) and a carry into the next
+   * binade (n = 2^(mbits+1)). */
+  uint32_t code = ((uint32_t)(e + f->bias - 1) << f->mbits) + n;
+  if (code > f->max_code) code = f->max_code;
+  return (uint8_t)(sign | code);
+}
+
+uint8_t or_f32_to_fp8e4m3(float v) { return ofp8_encode(v, &OFP8_E4M3, 0); }
+uint8_t or_f32_to_fp8e4m3_sat(float v) { return ofp8_encode(v, &OFP8_E4M3, 1); }
+uint8_t or_f32_to_fp8e5m2(float v) { return ofp8_encode(v, &OFP8_E5M2, 0); }
+uint8_t or_f32_to_fp8e5m2_sat(float v) { return ofp8_encode(v, &OFP8_E5M2, 1); }
+
+/* (-1)^s * 2^(E - bias) * (1 + M / 2^mbits), or 2^(1 - bias) * M / 2^mbits
+ * for E = 0 (OFP8 v1.0 value formulas). */
+static float ofp8_decode(uint8_t b, const Ofp8 *f) {
+  const int ebits = 7 - f->mbits;
+  const uint32_t mag = b & 0x7Fu, E = mag >> f->mbits, M = mag & ((1u << f->mbits) - 1u);
+  float v;
+  if (f->mbits == 3 && mag == 0x7Fu) return u2f(0x7FC00000u);
+  if (f->mbits == 2 && E == (1u << ebits) - 1u) {
+    if (M) return u2f(0x7FC00000u);
+    v = INFINITY;
+  } else if (E == 0) {
+    v = ldexpf((float)M, 1 - f->bias - f->mbits);
   } else {
-    int32_t sh = 1 - e;
-    uint32_t m = mant | (1u << (c->sig_bits - 1));
-    res = m >> sh;
-    uint64_t mask = (half_ulp << (sh + 1)) - 1;
-    uint64_t rb = (xb | ((uint64_t)1 << 52)) & mask;
-    uint64_t ulp = half_ulp << sh;
-    if (rb > ulp || (rb == ulp && (res & 1))) res += 1;
+    v = ldexpf((float)((1u << f->mbits) + M), (int)E - f->bias - f->mbits);
   }
-  return (uint8_t)(res | sign);
+  return (b & 0x80u) ? -v : v;
 }
 
-uint8_t or_f32_to_fp8e4m3(float v) { return f8_enc(v, &E4M3, 0); }
-uint8_t or_f32_to_fp8e4m3_sat(float v) { return f8_enc(v, &E4M3, 1); }
-uint8_t or_f32_to_fp8e5m2(float v) { return f8_enc(v, &E5M2, 0); }
-uint8_t or_f32_to_fp8e5m2_sat(float v) { return f8_enc(v, &E5M2, 1); }
-
-float or_fp8e5m2_to_f32(uint8_t x) {
-  uint16_t ur = (uint16_t)((uint16_t)x << 8);
-  if ((ur & 0x7FFFu) > 0x7C00u) ur = 0x7FFFu;
-  return or_fp16_to_f32(ur);
-}
-
-float or_fp8e4m3_to_f32(uint8_t x) {
-  uint16_t ur = (uint16_t)((uint16_t)x << 8);
-  uint16_t sign = ur & 0x8000u;
-  uint16_t ex = (uint16_t)((((uint32_t)ur & 0x7800u) >> 1) + 0x2000u);
-  uint16_t ma = (uint16_t)((ur & 0x0700u) >> 1);
-  if ((x & 0x7Fu) == 0x7Fu) {
-    ur = 0x7FFFu;
-  } else if (ex == 0x2000u) {
-    if (ma) {
-      ma <<= 1;
-      while ((ma & 0x0400u) == 0) { ma <<= 1; ex -= 0x0400u; }
-      ma &= 0x03FFu;
-    } else {
-      ex = 0;
-    }
-    ur = (uint16_t)(sign | ex | ma);
-  } else {
-    ur = (uint16_t)(sign | ex | ma);
-  }
-  return or_fp16_to_f32(ur);
-}
+float or_fp8e4m3_to_f32(uint8_t x) { return ofp8_decode(x, &OFP8_E4M3); }
+float or_fp8e5m2_to_f32(uint8_t x) { return ofp8_decode(x, &OFP8_E5M2); }
 
 static float ld(const void *p, uint64_t i, uint32_t dt) {
   switch (dt) {

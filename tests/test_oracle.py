@@ -62,6 +62,51 @@ def test_e4m3_decode_closed_form():
         assert v == (-want if s else want), b
 
 
+def test_e5m2_decode_closed_form():
+    for b in range(256):
+        s, e, m = b >> 7, (b >> 2) & 31, b & 3
+        v = O.oracle().or_fp8e5m2_to_f32(b)
+        if e == 31:
+            assert (np.isinf(v) and (v < 0) == bool(s)) if m == 0 else np.isnan(v), b
+            continue
+        want = (m / 4.0) * 2.0 ** -14 if e == 0 else (1 + m / 4.0) * 2.0 ** (e - 15)
+        assert v == (-want if s else want), b
+
+
+def _nearest_even_code(x, table, max_code):
+    """Brute force: the finite code whose value is nearest to x (float64),
+    ties to the even code, magnitudes past the largest finite saturated."""
+    ax = abs(x)
+    codes = np.arange(max_code + 1)
+    d = np.abs(table[codes].astype(np.float64) - ax)
+    best = np.flatnonzero(d == d.min())
+    c = int(best[0]) if len(best) == 1 else int(best[best % 2 == 0][0])
+    return c | (0x80 if np.signbit(x) else 0)
+
+
+@pytest.mark.parametrize("dt,max_code", [(DT_FP8, 0x7E), (DT_E5M2, 0x7B)])
+def test_fp8_encoders_brute_force_nearest_even(dt, max_code):
+    """Every midpoint between adjacent codes (a tie), one f32 ulp either side
+    of it, every code value itself, and random values over the whole range,
+    against a nearest-value search over the decode table."""
+    R = O.oracle()
+    table = O.decode(np.arange(256, dtype=np.uint8), dt).astype(np.float64)
+    vals = table[: max_code + 1]
+    mids = ((vals[:-1] + vals[1:]) / 2).astype(np.float32)
+    up = np.nextafter(mids, np.float32(np.inf))
+    dn = np.nextafter(mids, np.float32(0))
+    rng = np.random.default_rng(5)
+    rnd = (rng.standard_normal(4000) * 2.0 ** rng.uniform(-22, 18, 4000)).astype(np.float32)
+    top = np.float32(vals[max_code] * 1.2)
+    xs = np.concatenate([mids, up, dn, vals.astype(np.float32), rnd, [top, -top, 0.0, -0.0]])
+    xs = np.concatenate([xs, -xs]).astype(np.float32)
+    enc = {DT_FP8: (R.or_f32_to_fp8e4m3, R.or_f32_to_fp8e4m3_sat),
+           DT_E5M2: (R.or_f32_to_fp8e5m2, R.or_f32_to_fp8e5m2_sat)}[dt]
+    for x in xs:
+        want = _nearest_even_code(float(x), table, max_code)
+        assert enc[0](float(x)) == want and enc[1](float(x)) == want, (float(x), want)
+
+
 @pytest.mark.parametrize("name,dt,sat", [("bf16", DT_BF16, None), ("fp16", DT_F16, None),
                                          ("e4m3", DT_FP8, 0), ("e4m3_sat", DT_FP8, 1),
                                          ("e5m2", DT_E5M2, 0), ("e5m2_sat", DT_E5M2, 1)])
