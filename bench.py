@@ -459,7 +459,7 @@ def run_host_gpt2(thvm, key: str, args) -> dict:
     w = GPT2.synthetic_weights(L, c["dim"], c["vocab"], max_ctx, seed=1234, std=c["init_std"])
     if c["wdtype"] == DT_F16:
         w = {k: v.astype(np.float16) for k, v in w.items()}
-    g = GPT2.build(L, c["n_heads"], c["dim"], c["vocab"], max_ctx, max_ctx, w)
+    g = GPT2(w, L, c["n_heads"], c["dim"], c["vocab"], max_ctx)
     prompt = [(7 * i + 3) % c["vocab"] for i in range(ctx)]
     t0 = time.time()
     cur = np.array([prompt[0]], np.int32)

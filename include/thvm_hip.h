@@ -75,6 +75,20 @@ int      thvm_hip_buf_write_at(uint32_t buf_id, uint64_t byte_off,
                                const void *src, uint64_t nbytes);
 int      thvm_hip_buf_copy_at(uint32_t dst_id, uint64_t dst_byte_off,
                               uint32_t src_id, uint64_t nbytes);
+/* Inside an open graph capture buf_copy / buf_copy_at are recorded as copy
+ * kernels and buf_zero as a fill kernel (the reference's jit_replay calls
+ * buf_zero and, through tensor_assign, buf_copy_at inside its capture:
+ * src/jit/capture.c:2779-2815); buf_read / buf_write are refused there.
+ *
+ * The KV-append ASSIGN at a symbolic row (capture.c:2797-2801 computes
+ * kvar_runtime(kvar) * strides[0] on the host, which a captured graph would
+ * freeze): copy nbytes of src to dst at byte offset
+ *   base_off + row_bytes * row,  row = the int32 at row_buf + row_buf_off,
+ * read on the device when the copy runs, so a replayed graph appends at the
+ * current row.  A row outside the destination writes nothing.  0 / -1. */
+int      thvm_hip_buf_copy_row(uint32_t dst_id, uint64_t base_off, uint64_t row_bytes,
+                               uint32_t row_buf_id, uint64_t row_buf_off,
+                               uint32_t src_id, uint64_t nbytes);
 /* cuda_buf_refcount / freelist_push / freelist_remove / storage_root /
  * nbytes / zero (reference src/thvm.h:788-815). */
 uint32_t thvm_hip_buf_refcount(uint32_t buf_id);

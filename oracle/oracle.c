@@ -426,6 +426,27 @@ int or_decode_step(const OrModel *m, const int32_t *tok, uint32_t pos, float *lo
 
 /* ==== DeepSeek-V2 decode (bench/dsv2_decode_bench.c) ====================== */
 
+/* The dense layer's h = silu(g) * u as the reference builds it, from bf16
+ * uops (bench/dsv2_decode_bench.c:2042-2049, :2372): x * recip(1 + exp2(x *
+ * c)) * u with c the bf16 CONST -log2(e).  On the reference CPU path the
+ * constant holds its bf16 value (-1.4453125) and, being a non-f32 float
+ * constant, is a double literal, so every op of the chain promotes to double
+ * and exp2 is libm's double one (src/backend/cpu/uop_walk.c:357-409,
+ * :685-730); the bf16 store narrows double -> f32 -> bf16 (:216-229).  Pinned
+ * bit for bit against the reference realizing this DAG
+ * (oracle/ref_harness.c ref_dense_silu_mul_bf16), including exp2 past the
+ * f32 range, and by the dense-layer trajectory fixture. */
+static float silu_bf16_uops(float g, float u) {
+  const double c = (double)or_bf16_to_f32(or_f32_to_bf16(-1.4426950408889634f));
+  const double sig = 1.0 / (1.0 + exp2((double)g * c));
+  return (float)(((double)g * sig) * (double)u);
+}
+
+void or_dsv2_dense_act(const uint16_t *g, const uint16_t *u, uint16_t *h, uint64_t n) {
+  for (uint64_t i = 0; i < n; i++)
+    h[i] = or_f32_to_bf16(silu_bf16_uops(or_bf16_to_f32(g[i]), or_bf16_to_f32(u[i])));
+}
+
 /* sum_k x[k] * w~[row][k], w~ = decode(w) * scale[row] (scale NULL: 1), serial */
 static float wdot(const float *x, const void *w, uint32_t wdt, const float *scale, uint64_t row,
                   uint32_t K) {
@@ -625,16 +646,17 @@ int or_dsv2_step(const OrDsv2 *m, const int32_t *tok, uint32_t pos, float *logit
         gemv_sk(gu, tmp, Ly->wgu, wdt, Ly->sgu, 2 * F, D, gemv_pick_sk(D, F));
         for (uint32_t i = 0; i < F; i++) {
           float g = rnd(gu[2 * i], DT_BF16), u = rnd(gu[2 * i + 1], DT_BF16);
-          hh[i] = rnd(silu(g) * u, DT_BF16);
+          hh[i] = rnd(silu_bf16_uops(g, u), DT_BF16);
         }
         gemv_sk(tmp, hh, Ly->wd, wdt, Ly->sd, D, F, gemv_pick_sk(F, D));
       } else {
         gemv_sk(lg, xn, Ly->gate, DT_FP32, NULL, E, D, gemv_pick_sk(D, E));
         or_route(sel, probs, lg, E, K);
-        if (m->gate_out) memcpy(m->gate_out + (uint64_t)b * E, lg, E * sizeof(float));
+        const uint64_t lb = (uint64_t)l * m->batch + b;     /* [layer][row] records */
+        if (m->gate_out) memcpy(m->gate_out + lb * E, lg, E * sizeof(float));
         if (m->sel_out) {
-          memcpy(m->sel_out + (uint64_t)b * K, sel, K * sizeof(int32_t));
-          memcpy(m->probs_out + (uint64_t)b * K, probs, K * sizeof(float));
+          memcpy(m->sel_out + lb * K, sel, K * sizeof(int32_t));
+          memcpy(m->probs_out + lb * K, probs, K * sizeof(float));
         }
         or_moe(tmp, xb, sel, probs, Ly->wgu_e, Ly->sgu_e, Ly->wd_e, Ly->sd_e, Ly->wgu_s, Ly->sgu_s,
                Ly->wd_s, Ly->sd_s, wdt, D, I, S, K);

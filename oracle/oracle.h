@@ -165,8 +165,8 @@ typedef struct OrDsv2 {
   const void *lm; const float *lm_s;     /* [V][D]                                */
   const float *rope_cos, *rope_sin;      /* [max_seq][dr/2]                       */
   OrDsv2Layer *layers;
-  int32_t *sel_out; float *probs_out;    /* optional [B][K]: routing of the last MoE layer */
-  float *gate_out;                       /* optional [B][E]: its router logits    */
+  int32_t *sel_out; float *probs_out;    /* optional [n_layers][B][K]: each MoE layer's routing */
+  float *gate_out;                       /* optional [n_layers][B][E]: its router logits         */
 } OrDsv2;
 
 /* One DSV2 decode step for every batch row (step_build :2328-2411): writes
@@ -175,6 +175,9 @@ typedef struct OrDsv2 {
  * norm feeds the router in f32 and the experts in bf16; the final norm feeds
  * the LM head in f32 (:2394-2397, rms_f out f32). */
 int or_dsv2_step(const OrDsv2 *m, const int32_t *tok, uint32_t pos, float *logits, int32_t *next);
+/* the dense first layer's activation: h = bf16(silu(g) * u) over bf16 g, u
+ * as the reference's bf16 uop chain evaluates it */
+void or_dsv2_dense_act(const uint16_t *g, const uint16_t *u, uint16_t *h, uint64_t n);
 
 #ifdef __cplusplus
 }

@@ -87,3 +87,30 @@ int ref_rmsnorm_f32(const float *x, float *y, u32 M, u32 K, double eps) {
   Tensor r = nn_elementwise(NN_RSQRT, nn_binop_f(UOP_ADD, ms, eps));
   return ref_read(nn_binop(UOP_MUL, X, r), y, (u64)M * K);
 }
+
+/* The DeepSeek-V2 dense layer's h = silu(g) * u as the reference decode bench
+ * builds it (bench/dsv2_decode_bench.c:2042-2049 silu, :2372 the product,
+ * :2373 rz): bf16 uops over two [1, n] bf16 tensors, realized through the
+ * reference CPU path; h is written as bf16 bits. */
+int ref_dense_silu_mul_bf16(const u16 *g, const u16 *u, u16 *h, u32 n) {
+  ref_init();
+  Shape s = {0};
+  s.ndim = 2;
+  s.dims[0] = 1;
+  s.dims[1] = n;
+  u32 tg = tensor_alloc(&CPU_BACKEND, s, DT_BF16), tu = tensor_alloc(&CPU_BACKEND, s, DT_BF16);
+  CPU_BACKEND.buf_write(TENS[tg].buf_id, (void *)g, (u64)n * 2);
+  CPU_BACKEND.buf_write(TENS[tu].buf_id, (void *)u, (u64)n * 2);
+  u32 d1k[2] = {1, n};
+  union { f32 f; u32 b; } c1 = {.f = -1.4426950408889634f}, c2 = {.f = 1.0f};
+  Term x = term_new(0, TAG_TEN, DT_BF16, tg);
+  Term nlog2e = uop_expand(uop_const(DT_BF16, c1.b), 2, d1k);
+  Term one = uop_expand(uop_const(DT_BF16, c2.b), 2, d1k);
+  Term sig = uop_unary(UOP_RECIP, uop_binary(UOP_ADD, one, uop_unary(UOP_EXP2, uop_binary(UOP_MUL, x, nlog2e))));
+  Term hh = uop_binary(UOP_MUL, uop_binary(UOP_MUL, x, sig), term_new(0, TAG_TEN, DT_BF16, tu));
+  Term r = term_resolve(thvm_realize(hh));
+  if (term_tag(r) != TAG_TEN) return -1;
+  u32 tid = (u32)term_val(r);
+  if (TENS[tid].view.numel != n || TENS[tid].dtype != DT_BF16) return -2;
+  return TENS[tid].backend->buf_read(TENS[tid].buf_id, h, (u64)n * 2);
+}

@@ -84,6 +84,7 @@ def oracle() -> C.CDLL:
             "or_moe": (None, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
                               _u32, _u32, _u32, _u32, _u32]),
             "or_dsv2_step": (_i, [C.POINTER(OrDsv2), _vp, _u32, _vp, _vp]),
+            "or_dsv2_dense_act": (None, [_vp, _vp, _vp, _u64]),
         }
         for k, (r, a) in sig.items():
             fn = getattr(L, k)
@@ -109,6 +110,7 @@ def ref():
             "ref_softmax_f32": (_i, [_vp, _vp, _u32, _u32]),
             "ref_layernorm_f32": (_i, [_vp, _vp, _u32, _u32, C.c_double]),
             "ref_rmsnorm_f32": (_i, [_vp, _vp, _u32, _u32, C.c_double]),
+            "ref_dense_silu_mul_bf16": (_i, [_vp, _vp, _vp, _u32]),
         }
         for k, (r, a) in sig.items():
             fn = getattr(L, k)
@@ -268,9 +270,10 @@ class OracleDsv2:
         m.rope_cos, m.rope_sin = t("rope.cos"), t("rope.sin")
         m.layers = self.layers
         B, K = cfg["batch"], cfg["top_k"]
-        self.sel = np.zeros((B, K), np.int32)
-        self.probs = np.zeros((B, K), np.float32)
-        self.gate = np.zeros((B, cfg["n_experts"]), np.float32)
+        # per layer and row (dense layers keep zeros)
+        self.sel = np.zeros((L, B, K), np.int32)
+        self.probs = np.zeros((L, B, K), np.float32)
+        self.gate = np.zeros((L, B, cfg["n_experts"]), np.float32)
         m.sel_out, m.probs_out = self.sel.ctypes.data, self.probs.ctypes.data
         m.gate_out = self.gate.ctypes.data
         self.m = m

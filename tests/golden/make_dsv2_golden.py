@@ -1,5 +1,6 @@
-"""Write tests/golden/dsv2_ref.npz: the greedy trajectory and top-2 logits of
-the compiled reference DSV2 decode step (bench/dsv2_decode_bench.c, CPU
+"""Write tests/golden/dsv2_ref.npz (2 MoE layers) and dsv2_ref_dense.npz (a
+dense first layer, then 2 MoE layers): the greedy trajectory and top-2
+logits of the compiled reference DSV2 decode step (bench/dsv2_decode_bench.c, CPU
 backend, built by oracle/Makefile into oracle/_ref/dsv2_bench) on a seeded
 synthetic model small enough for the CPU.  The model is regenerated from the
 seed by tests/_dsv2_weights.py (only ids, logits and a weight checksum are
@@ -25,6 +26,9 @@ import _dsv2_weights as W  # noqa: E402
 CFG = dict(n_layers=2, dim=128, n_heads=8, kv_lora=64, d_nope=32, d_rope=16, d_v=32, n_experts=8,
            n_shared=2, top_k=3, moe_inter=64, ffn=256, first_dense=0, vocab=1024, max_seq=64,
            batch=1, eps=1e-6, init_std=0.02)
+# the second fixture pins the dense first layer (its SwiGLU runs as bf16 uops
+# in the reference: bench/dsv2_decode_bench.c:2042-2049, :2370-2378)
+FIXTURES = {"dsv2_ref.npz": CFG, "dsv2_ref_dense.npz": dict(CFG, n_layers=3, first_dense=1)}
 SEED = 20261201
 PROMPT = [5, 17, 300, 911, 42, 7, 640, 128]
 COUNT = 12
@@ -44,6 +48,11 @@ def main():
     exe = ROOT / "oracle" / "_ref" / "dsv2_bench"
     if not exe.exists():
         subprocess.run(["make", "-C", str(ROOT / "oracle"), "_ref/dsv2_bench"], check=True)
+    for name, cfg in FIXTURES.items():
+        write_fixture(exe, name, cfg)
+
+
+def write_fixture(exe, name, CFG):
     t = W.make_dsv2(CFG, SEED)
     with tempfile.TemporaryDirectory() as d:
         pack = os.path.join(d, "dsv2.pack")
@@ -62,11 +71,11 @@ def main():
     ids = [int(x) for x in re.search(r"thvm gen ids: \[([^\]]*)\]", out).group(1).split(",")]
     top2 = [(int(m[0]), int(m[1]), float(m[2]), int(m[3]), float(m[4]))
             for m in re.findall(r"top2 step (\d+): tok=-?\d+\s+(\d+):(-?[\d.]+)\s+(-?\d+):(-?[\d.]+)", out)]
-    np.savez_compressed(ROOT / "tests" / "golden" / "dsv2_ref.npz", seed=SEED, prompt=np.array(PROMPT),
+    np.savez_compressed(ROOT / "tests" / "golden" / name, seed=SEED, prompt=np.array(PROMPT),
                         gen_ids=np.array(ids, np.int32), top2=np.array(top2, np.float64),
                         digest=np.array(weight_digest(t)),
                         cfg=np.array(sorted(CFG.items()), dtype=object).astype(str))
-    print("gen ids", ids)
+    print(name, "gen ids", ids)
 
 
 if __name__ == "__main__":

@@ -79,3 +79,36 @@ def test_product_does_not_reference_oracle():
         if p.is_file() and p.suffix in (".py", ".c", ".h", ".hip"):
             t = p.read_text()
             assert "liboracle" not in t and "or_decode_step" not in t and "oracle/" not in t, p
+
+
+def test_integration_backend_typechecks_against_reference_header(tmp_path):
+    """INTEGRATION.md's HIP_BACKEND initializer, compiled beside the
+    reference's own src/thvm.h (struct Backend, src/thvm.h:751-829) with
+    incompatible pointer types as errors: every vtable slot this library
+    fills has the reference's signature.  Runs where the reference tree is
+    mounted (this container), skipped elsewhere."""
+    import re
+    import shutil
+    import subprocess
+    ref_h = Path("/root/reference/src/thvm.h")
+    if not ref_h.exists() or shutil.which("gcc") is None:
+        pytest.skip("reference header or gcc not available")
+    text = (ROOT / "INTEGRATION.md").read_text()
+    block = re.findall(r"```c\n(.*?)```", text, re.S)[0]
+    assert "Backend HIP_BACKEND" in block
+    block = block.replace('#include "<repo>/include/thvm_hip.h"', '#include "thvm_hip.h"')
+    src = tmp_path / "hip_backend_binding.c"
+    # kernel_custom_primary_out_slot is a static of src/schedule/kernel_custom.c:133,
+    # visible to a backend file in the reference's single translation unit
+    src.write_text(f'#include "{ref_h}"\n'
+                   "u32 kernel_custom_primary_out_slot(KernelEntry const *ke);\n"
+                   "static int hip_dispatch_lifted(KernelEntry *ke, u32 *in_buf_ids, u32 out_buf_id);\n"
+                   + block +
+                   "int hip_dispatch_lifted_stub(KernelEntry *ke, u32 *i, u32 o) "
+                   "{ return hip_dispatch_lifted(ke, i, o); }\n"
+                   "static int hip_dispatch_lifted(KernelEntry *ke, u32 *i, u32 o) "
+                   "{ (void)ke; (void)i; (void)o; return -1; }\n")
+    r = subprocess.run(["gcc", "-std=c11", "-fsyntax-only", "-Werror=incompatible-pointer-types",
+                        "-Werror=implicit-function-declaration", "-Werror=int-conversion",
+                        f"-I{ROOT / 'include'}", str(src)], capture_output=True, text=True)
+    assert r.returncode == 0, r.stderr[-3000:]

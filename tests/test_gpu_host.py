@@ -199,7 +199,7 @@ def test_gpt2_driver_matches_oracle(T):
     from thvm_amd.gpt2 import GPT2
     L, D, H, V, MS = 2, 128, 4, 1000, 32
     w = GPT2.synthetic_weights(L, D, V, MS, seed=7)
-    g = GPT2.build(L, H, D, V, MS, MS, w)
+    g = GPT2(w, L, H, D, V, MS)
     cfg = dict(arch=2, n_layers=L, dim=D, n_heads=H, n_kv_heads=H, head_dim=D // H, ffn=4 * D, vocab=V,
                max_seq=MS, batch=1, wdtype=13, adtype=13, eps=1e-5)
     orc = _oracle_gpt2(w, cfg)
@@ -207,11 +207,11 @@ def test_gpt2_driver_matches_oracle(T):
     cur, n_new = prompt[0], 6
     for pos in range(len(prompt) + n_new - 1):
         nxt = int(g.step(np.array([cur], np.int32), pos)[0])
-        lg_dev = g.model.logits.numpy().reshape(-1)
+        lg_dev = g.logits.numpy().reshape(-1)
         lg_ref, nx_ref = orc.step(np.array([cur], np.int32), pos)
-        err = np.abs(lg_dev - lg_ref[0]).max()
-        say(f"pos {pos}: id {nxt} ref {int(nx_ref[0])} max|dlogit| {err:.2e}")
-        assert err <= 1e-4, err
+        err = np.abs(lg_dev - lg_ref[0]).max() / np.abs(lg_ref[0]).max()
+        say(f"pos {pos}: id {nxt} ref {int(nx_ref[0])} logits rel err {err:.2e}")
+        assert err <= 1e-5, err                  # fp32: 1e-5 relative (north star)
         assert nxt == int(nx_ref[0])
         cur = prompt[pos + 1] if pos + 1 < len(prompt) else nxt
-    assert g.model.forward_jit.cnt == 2, "the one-token forward was not captured"
+    assert g.jit.cnt == 2, "the one-token forward was not captured"

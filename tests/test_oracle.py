@@ -318,23 +318,46 @@ def _dsv2_run(t, cfg, prompt, count):
     return ids, top
 
 
-def test_dsv2_oracle_reproduces_reference_trajectory():
+@pytest.mark.parametrize("fixture", ["dsv2_ref.npz", "dsv2_ref_dense.npz"])
+def test_dsv2_oracle_reproduces_reference_trajectory(fixture):
     """The oracle's DeepSeek-V2 step (or_dsv2_step: MLA prep/attention, router,
-    routed + shared experts, split-K projections) against the compiled
-    reference DSV2 decode bench on the same seeded model (fixture written by
-    tests/golden/make_dsv2_golden.py through a DSV2PK01 weight pack): the
-    greedy ids are identical and the top-2 logits agree to 1e-5."""
+    routed + shared experts, the dense first layer, split-K projections)
+    against the compiled reference DSV2 decode bench on the same seeded model
+    (fixtures written by tests/golden/make_dsv2_golden.py through a DSV2PK01
+    weight pack; the second has a dense first layer): the greedy ids are
+    identical and the top-2 logits agree to 1e-5."""
     import _dsv2_weights as W
     sys.path.insert(0, str(O.ROOT / "tests" / "golden"))
     import make_dsv2_golden as G
-    g = np.load(O.ROOT / "tests" / "golden" / "dsv2_ref.npz")
-    t = W.make_dsv2(G.CFG, int(g["seed"]))
+    cfg = G.FIXTURES[fixture]
+    g = np.load(O.ROOT / "tests" / "golden" / fixture)
+    t = W.make_dsv2(cfg, int(g["seed"]))
     assert G.weight_digest(t) == str(g["digest"]), "weight generator drifted from the fixture"
-    ids, top = _dsv2_run(t, G.CFG, list(g["prompt"]), len(g["gen_ids"]))
+    ids, top = _dsv2_run(t, cfg, list(g["prompt"]), len(g["gen_ids"]))
     assert ids == list(g["gen_ids"])
     for (i1, v1, i2, v2), ref in zip(top[1:], g["top2"]):
         assert (i1, i2) == (int(ref[1]), int(ref[3]))
         assert abs(v1 - ref[2]) <= 1e-5 and abs(v2 - ref[4]) <= 1e-5
+
+
+def test_dsv2_dense_activation_matches_reference_uops():
+    """h = silu(g) * u of the dense first layer, bit for bit against the
+    compiled reference realizing the same bf16 uop DAG
+    (oracle/ref_harness.c ref_dense_silu_mul_bf16) on 60,000 pairs, including
+    large |g| (exp2 overflow / underflow) and signed zeros."""
+    R = O.ref()
+    if R is None:
+        pytest.skip("reference harness not built in this checkout")
+    rng = np.random.default_rng(17)
+    n = 60000
+    gf = (rng.standard_normal(n) * 10.0 ** rng.uniform(-3, 2.2, n)).astype(np.float32)
+    gf[:4] = [0.0, -0.0, 200.0, -200.0]
+    g, u = O.encode(gf, DT_BF16), O.encode(rng.standard_normal(n).astype(np.float32), DT_BF16)
+    want, got = np.zeros(n, np.uint16), np.zeros(n, np.uint16)
+    assert R.ref_dense_silu_mul_bf16(g.ctypes.data, u.ctypes.data, want.ctypes.data, n) == 0
+    O.oracle().or_dsv2_dense_act(g.ctypes.data, u.ctypes.data, got.ctypes.data, n)
+    bad = np.nonzero(got != want)[0]
+    assert bad.size == 0, f"{bad.size} differ, e.g. g={O.decode(g[bad[:3]], DT_BF16)}"
 
 
 def test_route_brute_force_and_ties():

@@ -72,6 +72,7 @@ _SIGS = {
     "thvm_hip_buf_copy": (_i32, [_u32, _u32, _u64]),
     "thvm_hip_buf_write_at": (_i32, [_u32, _u64, _vp, _u64]),
     "thvm_hip_buf_copy_at": (_i32, [_u32, _u64, _u32, _u64]),
+    "thvm_hip_buf_copy_row": (_i32, [_u32, _u64, _u64, _u32, _u64, _u32, _u64]),
     "thvm_hip_buf_refcount": (_u32, [_u32]), "thvm_hip_buf_freelist_push": (None, [_u32]),
     "thvm_hip_buf_freelist_remove": (None, [_u32]), "thvm_hip_buf_storage_root": (_u32, [_u32]),
     "thvm_hip_buf_nbytes": (_u64, [_u32]), "thvm_hip_buf_zero": (None, [_u32]),

@@ -1,6 +1,9 @@
 """Build libthvm_hip.so in-tree: C host layer with gcc, gfx950 kernels with
 hipcc, linked by hipcc.  Run as ``python -m thvm_amd.build`` or through
-``__graft_entry__.build()``.  Always recompiles (the build check)."""
+``__graft_entry__.build()``.  Always recompiles (the build check) unless
+``incremental=True`` (``python -m thvm_amd.build --incremental``): then a
+unit is rebuilt when its source, or any header under csrc/ or include/, is
+newer than its object."""
 from __future__ import annotations
 
 import concurrent.futures as cf
@@ -45,19 +48,29 @@ def _run(cmd: list[str]) -> None:
         print(out, file=sys.stderr)
 
 
-def build(verbose: bool = True) -> Path:
+def _stale(src: Path, obj: Path, headers_mtime: float) -> bool:
+    if not obj.exists():
+        return True
+    t = obj.stat().st_mtime
+    return src.stat().st_mtime > t or headers_mtime > t
+
+
+def build(verbose: bool = True, incremental: bool = False) -> Path:
     OBJ.mkdir(exist_ok=True)
     LIB.parent.mkdir(exist_ok=True)
+    hdr = max(p.stat().st_mtime for d in (CSRC, ROOT / "include") for p in d.rglob("*.h"))
     jobs = []
     for s in C_SOURCES:
         o = OBJ / (Path(s).stem + ".o")
-        jobs.append(["gcc", *CFLAGS, "-c", str(CSRC / s), "-o", str(o)])
+        if not incremental or _stale(CSRC / s, o, hdr):
+            jobs.append(["gcc", *CFLAGS, "-c", str(CSRC / s), "-o", str(o)])
     units = [(s, Path(s).stem, []) for s in HIP_SOURCES] + GEMV_UNITS
     for s, stem, extra in units:
         o = OBJ / (stem + ".hip.o")
-        jobs.append([f"{ROCM}/bin/hipcc", *HIPFLAGS, *extra, "-c", str(CSRC / s), "-o", str(o)])
+        if not incremental or _stale(CSRC / s, o, hdr):
+            jobs.append([f"{ROCM}/bin/hipcc", *HIPFLAGS, *extra, "-c", str(CSRC / s), "-o", str(o)])
     jobs.sort(key=lambda j: "gemv_inst" not in " ".join(j))    # the long units first
-    workers = min(len(jobs), int(os.environ.get("MAX_JOBS", "8")))
+    workers = max(1, min(len(jobs), int(os.environ.get("MAX_JOBS", "8"))))
     with cf.ThreadPoolExecutor(max_workers=workers) as ex:
         list(ex.map(_run, jobs))
     objs = [str(OBJ / (Path(s).stem + ".o")) for s in C_SOURCES] + \
@@ -72,4 +85,4 @@ def build(verbose: bool = True) -> Path:
 
 
 if __name__ == "__main__":
-    build()
+    build(incremental="--incremental" in sys.argv[1:])

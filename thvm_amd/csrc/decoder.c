@@ -711,9 +711,6 @@ static int build_dsv2(Decoder *d) {
       !tens_new(d, "qpe", THVM_DT_BF16, (u64)B * H * dr * 2) ||
       !tens_new(d, "o", THVM_DT_BF16, (u64)B * H * dv * 2) ||
       !tens_new(d, "xnf", THVM_DT_FP32, (u64)B * D * 4) ||
-      !tens_new(d, "gate_logits", THVM_DT_FP32, (u64)B * E * 4) ||
-      !tens_new(d, "sel", THVM_DT_INT32, (u64)B * K * 4) ||
-      !tens_new(d, "probs", THVM_DT_FP32, (u64)B * K * 4) ||
       !tens_new(d, "hmoe", THVM_DT_FP32, (u64)B * P * 4) ||
       !tens_new(d, "h", THVM_DT_BF16, (u64)B * (F ? F : 1) * 2) ||
       !tens_new(d, "mla.part", THVM_DT_FP32, thvm_k_mla_part_bytes(B, H, kv, d->n_split)))
@@ -733,8 +730,7 @@ static int build_dsv2(Decoder *d) {
   char p[512], nm[48];
   const u32 x = tens_find(d, "x"), L = tens_find(d, "len"), qkv = tens_find(d, "qkv");
   const u32 qlat = tens_find(d, "qlat"), qpe = tens_find(d, "qpe"), o = tens_find(d, "o");
-  const u32 xnf = tens_find(d, "xnf"), gl = tens_find(d, "gate_logits"), sel = tens_find(d, "sel");
-  const u32 probs = tens_find(d, "probs"), hmoe = tens_find(d, "hmoe"), hd = tens_find(d, "h");
+  const u32 xnf = tens_find(d, "xnf"), hmoe = tens_find(d, "hmoe"), hd = tens_find(d, "h");
   const u32 cosb = tens_find(d, "rope.cos"), sinb = tens_find(d, "rope.sin");
 
   snprintf(p, sizeof p, "thvm-builtin:embed b=%u d=%u v=%u et=%u xt=%u", B, D, V, THVM_DT_BF16,
@@ -829,6 +825,15 @@ static int build_dsv2(Decoder *d) {
     const u32 gate = weight_normal(d, nm, THVM_DT_FP32, (u64)E * D, 0.0f, c->init_std);
     if (!gate) return -1;
     d->weight_bytes += (u64)E * D * 4;
+    /* each MoE layer keeps its router logits, selected experts and their
+     * probabilities (readable after a step: l<i>.gate_logits/.sel/.probs) */
+    snprintf(nm, sizeof nm, "l%u.gate_logits", l);
+    const u32 gl = tens_new(d, nm, THVM_DT_FP32, (u64)B * E * 4);
+    snprintf(nm, sizeof nm, "l%u.sel", l);
+    const u32 sel = tens_new(d, nm, THVM_DT_INT32, (u64)B * K * 4);
+    snprintf(nm, sizeof nm, "l%u.probs", l);
+    const u32 probs = tens_new(d, nm, THVM_DT_FP32, (u64)B * K * 4);
+    if (!gl || !sel || !probs) return -1;
     u32 wgue, sgue, wde, sde, wgus = 0, sgus = 0, wds = 0, sds = 0;
     const u64 wb0 = d->weight_bytes;
     WM("l%u.wgu_e", E * 2 * I, D, &wgue, &sgue);

@@ -302,15 +302,30 @@ THVM_API uint64_t thvm_hip_buf_device_ptr(uint32_t buf_id) {
 THVM_API uint64_t thvm_hip_mem_live_bytes(void) { return MEM_LIVE; }
 THVM_API uint64_t thvm_hip_mem_peak_bytes(void) { return MEM_PEAK; }
 
+/* 1 while work on the dispatch stream is being recorded into a graph
+ * (the library's own capture or one the caller opened on the stream) */
+int hb_stream_capturing(void) {
+  if (HB_GRAPH_CAPTURING) return 1;
+  hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
+  if (!HB_STREAM || hipStreamIsCapturing(HB_STREAM, &st) != hipSuccess) return 0;
+  return st != hipStreamCaptureStatusNone;
+}
+
+/* A zero-fill kernel, never a memset node: the reference's jit_replay zeroes
+ * recycled outputs inside an open graph capture (src/jit/capture.c:2779-2780). */
 THVM_API void thvm_hip_buf_zero(uint32_t buf_id) {
   HbBuf *b = buf_get(buf_id);
   if (!b || b->parked || !HB_READY) return;
-  hipMemsetAsync(b->dptr, 0, b->req, HB_STREAM);
+  char err[128];
+  if (thvm_k_zero(b->dptr, b->req, HB_STREAM, err, sizeof err)) hb_set_error("buf_zero: %s", err);
 }
 
-static int xfer_check(const char *who, u32 id, u64 off, u64 n, HbBuf **out) {
+/* Host transfers are refused inside a capture; device-to-device copies are
+ * recorded as copy kernels (the reference's KV ASSIGN runs buf_copy_at inside
+ * the capture, src/jit/capture.c:2791-2815, src/tensor/assign.c:89-94). */
+static int xfer_check_any(const char *who, u32 id, u64 off, u64 n, HbBuf **out, int in_capture_ok) {
   if (hb_require_ready(who)) return -1;
-  if (HB_GRAPH_CAPTURING) {
+  if (!in_capture_ok && hb_stream_capturing()) {
     hb_set_error("%s: not allowed while a graph capture is open", who);
     return -1;
   }
@@ -323,6 +338,9 @@ static int xfer_check(const char *who, u32 id, u64 off, u64 n, HbBuf **out) {
   }
   *out = b;
   return 0;
+}
+static int xfer_check(const char *who, u32 id, u64 off, u64 n, HbBuf **out) {
+  return xfer_check_any(who, id, off, n, out, 0);
 }
 
 THVM_API int thvm_hip_buf_write_at(uint32_t buf_id, uint64_t off, const void *src, uint64_t n) {
@@ -348,12 +366,40 @@ THVM_API int thvm_hip_buf_read(uint32_t buf_id, void *dst, uint64_t n) {
 }
 THVM_API int thvm_hip_buf_copy_at(uint32_t dst_id, uint64_t dst_off, uint32_t src_id, uint64_t n) {
   HbBuf *d, *s;
-  if (xfer_check("buf_copy", dst_id, dst_off, n, &d)) return -1;
-  if (xfer_check("buf_copy", src_id, 0, n, &s)) return -1;
+  if (xfer_check_any("buf_copy", dst_id, dst_off, n, &d, 1)) return -1;
+  if (xfer_check_any("buf_copy", src_id, 0, n, &s, 1)) return -1;
   if (n == 0) return 0;
+  if (hb_stream_capturing()) {      /* a kernel node in the graph */
+    char err[128];
+    if (thvm_k_copy_at(d->dptr, d->req, dst_off, 0, NULL, s->dptr, n, HB_STREAM, err, sizeof err)) {
+      hb_set_error("buf_copy: %s", err);
+      return -1;
+    }
+    return 0;
+  }
   hipError_t e = hipMemcpyAsync((char *)d->dptr + dst_off, s->dptr, n, hipMemcpyDeviceToDevice,
                                 HB_STREAM);
   if (e != hipSuccess) { hb_set_error("buf_copy: %s", hipGetErrorString(e)); return -1; }
+  return 0;
+}
+
+THVM_API int thvm_hip_buf_copy_row(uint32_t dst_id, uint64_t base_off, uint64_t row_bytes,
+                                   uint32_t row_buf_id, uint64_t row_buf_off, uint32_t src_id,
+                                   uint64_t n) {
+  HbBuf *d, *s, *r;
+  if (xfer_check_any("buf_copy_row", dst_id, base_off, n, &d, 1)) return -1;
+  if (xfer_check_any("buf_copy_row", src_id, 0, n, &s, 1)) return -1;
+  if (xfer_check_any("buf_copy_row", row_buf_id, row_buf_off, 4, &r, 1)) return -1;
+  if (row_buf_off & 3) { hb_set_error("buf_copy_row: row index offset %llu not 4-byte aligned",
+                                      (unsigned long long)row_buf_off); return -1; }
+  if (n == 0) return 0;
+  char err[128];
+  if (thvm_k_copy_at(d->dptr, d->req, base_off, row_bytes,
+                     (const int32_t *)((const char *)r->dptr + row_buf_off), s->dptr, n, HB_STREAM,
+                     err, sizeof err)) {
+    hb_set_error("buf_copy_row: %s", err);
+    return -1;
+  }
   return 0;
 }
 THVM_API int thvm_hip_buf_copy(uint32_t dst_id, uint32_t src_id, uint64_t n) {

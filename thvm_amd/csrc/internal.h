@@ -24,6 +24,7 @@ extern int         HB_READY;
 extern hipStream_t HB_STREAM;
 extern int         HB_GRAPH_CAPTURING;   /* stream capture open */
 int hb_require_ready(const char *who);
+int hb_stream_capturing(void);           /* HB_STREAM is being recorded */
 
 /* ---- buffer table ---- */
 void *hb_buf_ptr(u32 id);               /* NULL when id is dead/invalid */

@@ -233,6 +233,15 @@ int thvm_k_fill_cache(void *cache, uint32_t dt, uint32_t B, uint32_t Hkv,
  * byte read once and written once: the calibration of HBM traffic counters. */
 int thvm_k_copy(void *y, const void *x, uint64_t nbytes, hipStream_t s, char *err, int errlen);
 
+/* Zero nbytes at y (any alignment) with a kernel, so the fill can sit in a
+ * captured graph as a kernel node. */
+int thvm_k_zero(void *y, uint64_t nbytes, hipStream_t s, char *err, int errlen);
+/* Copy n bytes from x to y + off, off = base + stride * idx[0] with idx[0]
+ * read on the device (idx NULL: off = base); an off whose n bytes do not fit
+ * in cap bytes writes nothing.  Any alignment; a kernel node when captured. */
+int thvm_k_copy_at(void *y, uint64_t cap, uint64_t base, uint64_t stride, const int32_t *idx,
+                   const void *x, uint64_t n, hipStream_t s, char *err, int errlen);
+
 /* Element-wise casts / copies (codec probes and glue): y[i] = cvt(x[i]). */
 int thvm_k_cast(void *y, uint32_t ydt, const void *x, uint32_t xdt, uint64_t n,
                 hipStream_t s, char *err, int errlen);

@@ -402,6 +402,65 @@ extern "C" int thvm_k_copy(void *y, const void *x, uint64_t nbytes, hipStream_t 
   return 0;
 }
 
+// ---- zero fill and byte copies usable inside a stream capture ----------------
+// (a kernel node instead of a memset / memcpy node).  The 16-byte-aligned
+// middle of the range is moved with 16-byte accesses, the unaligned head and
+// tail bytewise by the first wave of block 0.
+__global__ __launch_bounds__(256) void k_zero_bytes(uint8_t *y, uint64_t n) {
+  const uintptr_t p = (uintptr_t)y;
+  const uint64_t head = ((16 - (p & 15)) & 15) < n ? ((16 - (p & 15)) & 15) : n;
+  const uint64_t n16 = (n - head) / 16, tail0 = head + n16 * 16;
+  uint4 *y16 = (uint4 *)(y + head);
+  const uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
+  for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n16; i += stride)
+    y16[i] = make_uint4(0u, 0u, 0u, 0u);
+  if (blockIdx.x == 0 && threadIdx.x < 64) {
+    for (uint64_t i = threadIdx.x; i < head; i += 64) y[i] = 0;
+    for (uint64_t i = tail0 + threadIdx.x; i < n; i += 64) y[i] = 0;
+  }
+}
+extern "C" int thvm_k_zero(void *y, uint64_t nbytes, hipStream_t s, char *err, int errlen) {
+  if (nbytes == 0) return 0;
+  uint64_t blocks = (nbytes / 16 + 255) / 256;
+  if (blocks < 1) blocks = 1;
+  if (blocks > 256 * 16) blocks = 256 * 16;
+  thvm_launch(true, true, k_zero_bytes, dim3((unsigned)blocks), dim3(256), 0, s, (uint8_t *)y,
+              nbytes);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) { snprintf(err, errlen, "zero launch: %s", hipGetErrorString(e)); return -1; }
+  return 0;
+}
+
+// y[off + i] = x[i], i < n, with off = base + stride * idx[0] read on the
+// device (idx == nullptr: off = base).  An offset whose range does not fit
+// in cap bytes writes nothing.  Bytewise: this serves row appends (a few KB)
+// and arbitrary alignment; bulk aligned copies use k_copy16.
+__global__ __launch_bounds__(256) void k_copy_at(uint8_t *y, uint64_t cap, uint64_t base,
+                                                  uint64_t stride, const int32_t *idx,
+                                                  const uint8_t *x, uint64_t n) {
+  int64_t r = idx ? (int64_t)idx[0] : 0;
+  if (r < 0) return;
+  const uint64_t off = base + stride * (uint64_t)r;
+  if (off > cap || n > cap - off) return;
+  const uint64_t step = (uint64_t)gridDim.x * blockDim.x;
+  for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += step)
+    y[off + i] = x[i];
+}
+extern "C" int thvm_k_copy_at(void *y, uint64_t cap, uint64_t base, uint64_t stride,
+                              const int32_t *idx, const void *x, uint64_t n, hipStream_t s,
+                              char *err, int errlen) {
+  if (n == 0) return 0;
+  if (idx == nullptr && !((base | n | (uintptr_t)y | (uintptr_t)x) & 15) && base + n <= cap)
+    return thvm_k_copy((uint8_t *)y + base, x, n, s, err, errlen);
+  uint64_t blocks = (n + 255) / 256;
+  if (blocks > 1024) blocks = 1024;
+  thvm_launch(true, true, k_copy_at, dim3((unsigned)blocks), dim3(256), 0, s, (uint8_t *)y, cap,
+              base, stride, idx, (const uint8_t *)x, n);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) { snprintf(err, errlen, "copy_at launch: %s", hipGetErrorString(e)); return -1; }
+  return 0;
+}
+
 // ---- synthetic data ---------------------------------------------------------
 // splitmix64 finaliser over (seed, tag, counter): a counter-based generator,
 // so any element is reproducible alone.  Box-Muller on a pair of 24-bit
