@@ -140,6 +140,18 @@ int thvm_hip_dispatch_custom(const char *name, const char *program,
  * it would dispatch.  Used by hosts to fail early. */
 int thvm_hip_program_check(const char *name, const char *program);
 
+/* The attention builtin without its workspace: no counterpart in the
+ * reference.  It is for callers that cannot allocate device memory (code
+ * under graph capture, tight serving loops, harnesses that forbid hipMalloc).
+ * `program` is a "thvm-builtin:attn ..." spec exactly as for
+ * thvm_hip_dispatch_custom; buf_ids are its first five slots (out, q, kcache,
+ * vcache, len), and the partials live in a static device array of 16 MiB per
+ * GPU (held until the process ends) instead of slot 5.  A spec whose
+ * partials exceed 16 MiB fails with an error.  Nothing is allocated or freed.
+ * Calls that overlap on one GPU share that array and race.  0 / -1. */
+int thvm_hip_attn_decode_noalloc(const char *program, const uint32_t *buf_ids,
+                                 uint32_t n_args);
+
 /* ===================== renderer target ================================= */
 /* One node of a kernel's lifted uop DAG, flattened for the C ABI, sources
  * before users.  `op` is the reference's UOP_* number (src/thvm.h:302-512);

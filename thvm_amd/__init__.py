@@ -82,6 +82,7 @@ _SIGS = {
     "thvm_hip_dispatch_end": (None, []),
     "thvm_hip_dispatch_custom": (_i32, [_cp, _cp, _vp, _vp, _u32, _vp, _u32, _u64]),
     "thvm_hip_program_check": (_i32, [_cp, _cp]),
+    "thvm_hip_attn_decode_noalloc": (_i32, [_cp, _vp, _u32]),
     "thvm_hip_render_kernel": (_i32, [C.POINTER(Uop), _u32, _cp, _vp, _u64, C.POINTER(RenderInfo)]),
     "thvm_hip_jit_capture_begin": (_u32, []), "thvm_hip_jit_capture_end": (None, []),
     "thvm_hip_jit_capture_op_count": (_u32, [_u32]), "thvm_hip_jit_replay": (_i32, [_u32]),

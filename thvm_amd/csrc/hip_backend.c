@@ -425,6 +425,10 @@ THVM_API int thvm_hip_init(void) {
   }
   e = hipSetDevice(0);
   if (e != hipSuccess) { hb_set_error("init: hipSetDevice: %s", hipGetErrorString(e)); return -1; }
+  {  /* the no-allocation attention's static scratch: its address on this device */
+    char err[256];
+    if (thvm_k_attn_scratch_setup(err, sizeof err)) { hb_set_error("init: %s", err); return -1; }
+  }
   e = hipStreamCreateWithFlags(&HB_STREAM, hipStreamNonBlocking);
   if (e != hipSuccess) { hb_set_error("init: hipStreamCreate: %s", hipGetErrorString(e)); return -1; }
   if (BUFS == NULL) {

@@ -143,6 +143,31 @@ static void *arg(ArgCtx *c, u32 i, u64 bytes) {
 
 static int is_act(u32 dt) { return dt == THVM_DT_FP32 || dt == THVM_DT_FP16 || dt == THVM_DT_BF16; }
 
+/* the attn builtin's spec and buffer slots: out, q, kcache, vcache, len and,
+ * with_part, the partials workspace */
+static int attn_parse(const Spec *sp, ArgCtx *c, ThvmAttnArgs *a, int with_part) {
+  memset(a, 0, sizeof *a);
+  if (spec_u32(sp, "b", &a->B, 1, 0) || spec_u32(sp, "h", &a->H, 1, 0) ||
+      spec_u32(sp, "hkv", &a->Hkv, 1, 0) || spec_u32(sp, "hd", &a->hd, 1, 0) ||
+      spec_u32(sp, "maxseq", &a->max_seq, 1, 0) || spec_u32(sp, "chunk", &a->chunk, 0, 64) ||
+      spec_u32(sp, "qt", &a->qdt, 0, THVM_DT_BF16) || spec_u32(sp, "ct", &a->cdt, 0, THVM_DT_BF16) ||
+      spec_u32(sp, "ot", &a->odt, 0, THVM_DT_BF16) || spec_f32(sp, "scale", &a->scale, 1, 0) ||
+      spec_u32(sp, "fused", &a->fused, 0, 0) || spec_u32(sp, "cpb", &a->cpb, 0, 0))
+    return -1;
+  if (a->chunk == 0) { hb_set_error("builtin attn: chunk=0"); return -1; }
+  if (spec_u32(sp, "nsplit", &a->n_split, 0, (a->max_seq + a->chunk - 1) / a->chunk)) return -1;
+  if (!is_act(a->qdt) || !is_act(a->odt)) { hb_set_error("builtin attn: bad dtypes"); return -1; }
+  u64 cb = (u64)a->B * a->Hkv * a->max_seq * a->hd * hb_dt_size(a->cdt);
+  a->out = arg(c, 0, (u64)a->B * a->H * a->hd * hb_dt_size(a->odt));
+  a->q = arg(c, 1, (u64)a->B * a->H * a->hd * hb_dt_size(a->qdt));
+  a->kcache = arg(c, 2, cb);
+  a->vcache = arg(c, 3, cb);
+  a->len = (const int32_t *)arg(c, 4, 4);
+  if (with_part)
+    a->part = (float *)arg(c, 5, thvm_k_attn_part_bytes(a->B, a->H, a->Hkv, a->hd, a->n_split));
+  return c->bad ? -1 : 0;
+}
+
 /* Launch (or only validate, check_only=1) a builtin program. */
 int hb_builtin_launch(const char *program, const u32 *ids, u32 n, int check_only) {
   Spec sp;
@@ -249,24 +274,7 @@ int hb_builtin_launch(const char *program, const u32 *ids, u32 n, int check_only
     rc = thvm_k_softmax(&a, HB_STREAM, err, sizeof err);
   } else if (strcmp(K, "attn") == 0) {
     ThvmAttnArgs a;
-    memset(&a, 0, sizeof a);
-    NEED(spec_u32(&sp, "b", &a.B, 1, 0) || spec_u32(&sp, "h", &a.H, 1, 0) ||
-         spec_u32(&sp, "hkv", &a.Hkv, 1, 0) || spec_u32(&sp, "hd", &a.hd, 1, 0) ||
-         spec_u32(&sp, "maxseq", &a.max_seq, 1, 0) || spec_u32(&sp, "chunk", &a.chunk, 0, 64) ||
-         spec_u32(&sp, "qt", &a.qdt, 0, THVM_DT_BF16) || spec_u32(&sp, "ct", &a.cdt, 0, THVM_DT_BF16) ||
-         spec_u32(&sp, "ot", &a.odt, 0, THVM_DT_BF16) || spec_f32(&sp, "scale", &a.scale, 1, 0) ||
-         spec_u32(&sp, "fused", &a.fused, 0, 0) || spec_u32(&sp, "cpb", &a.cpb, 0, 0));
-    if (a.chunk == 0) { hb_set_error("builtin attn: chunk=0"); return -1; }
-    NEED(spec_u32(&sp, "nsplit", &a.n_split, 0, (a.max_seq + a.chunk - 1) / a.chunk));
-    if (!is_act(a.qdt) || !is_act(a.odt)) { hb_set_error("builtin attn: bad dtypes"); return -1; }
-    u64 cb = (u64)a.B * a.Hkv * a.max_seq * a.hd * hb_dt_size(a.cdt);
-    a.out = arg(&c, 0, (u64)a.B * a.H * a.hd * hb_dt_size(a.odt));
-    a.q = arg(&c, 1, (u64)a.B * a.H * a.hd * hb_dt_size(a.qdt));
-    a.kcache = arg(&c, 2, cb);
-    a.vcache = arg(&c, 3, cb);
-    a.len = (const int32_t *)arg(&c, 4, 4);
-    a.part = (float *)arg(&c, 5, thvm_k_attn_part_bytes(a.B, a.H, a.Hkv, a.hd, a.n_split));
-    if (c.bad) return -1;
+    NEED(attn_parse(&sp, &c, &a, 1));
     bytes = 0; /* live-length dependent: the decoder accounts for it */
     if (check_only) return 0;
     if (prof) hb_kprof_begin(K, &e0, &e1);
@@ -728,6 +736,33 @@ THVM_API int thvm_hip_program_check(const char *name, const char *program) {
     return spec_parse(program, &sp);
   }
   return rtc_get(name, program) ? 0 : -1;
+}
+
+/* ======================= attention without a workspace ================= */
+
+THVM_API int thvm_hip_attn_decode_noalloc(const char *program, const uint32_t *buf_ids,
+                                          uint32_t n_args) {
+  if (hb_require_ready("attn_decode_noalloc")) return -1;
+  if (!program || !buf_ids) { hb_set_error("attn_decode_noalloc: null program or ids"); return -1; }
+  Spec sp;
+  if (spec_parse(program, &sp)) return -1;
+  if (strcmp(sp.kernel, "attn") != 0) {
+    hb_set_error("attn_decode_noalloc: program is thvm-builtin:%s, want thvm-builtin:attn", sp.kernel);
+    return -1;
+  }
+  if (n_args != 5) {
+    hb_set_error("attn_decode_noalloc: %u buffers, want 5 (out, q, kcache, vcache, len)", n_args);
+    return -1;
+  }
+  ArgCtx c = {buf_ids, n_args, sp.kernel, 0};
+  ThvmAttnArgs a;
+  if (attn_parse(&sp, &c, &a, 0)) return -1;
+  char err[256] = {0};
+  if (thvm_k_attn_decode_scratch(&a, HB_STREAM, err, sizeof err)) {
+    hb_set_error("%s", err);
+    return -1;
+  }
+  return 0;
 }
 
 /* ======================= graph hooks =================================== */

@@ -109,6 +109,14 @@ typedef struct ThvmAttnArgs {
 } ThvmAttnArgs;
 int thvm_k_attn_decode(const ThvmAttnArgs *a, hipStream_t s, char *err, int errlen);
 uint64_t thvm_k_attn_part_bytes(uint32_t B, uint32_t H, uint32_t Hkv, uint32_t hd, uint32_t n_split);
+/* The same attention with a->part ignored: partials and merge counters in a
+ * static device array of THVM_ATTN_SCRATCH_BYTES per GPU (no allocation).
+ * thvm_k_attn_scratch_setup takes the array's address on the current device
+ * (once per device, at init); a call needing more partials than the array
+ * holds fails with an error.  Calls that overlap on one GPU race. */
+#define THVM_ATTN_SCRATCH_BYTES (16u << 20)
+int thvm_k_attn_scratch_setup(char *err, int errlen);
+int thvm_k_attn_decode_scratch(const ThvmAttnArgs *a, hipStream_t s, char *err, int errlen);
 
 /* DeepSeek-V2 multi-head latent attention (absorbed form) for decode.
  * qkv [B][ldq] bf16 is the q|kv projection output: per head dn nope + dr pe

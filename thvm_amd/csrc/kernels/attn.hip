@@ -351,3 +351,61 @@ extern "C" int thvm_k_attn_decode(const ThvmAttnArgs *a, hipStream_t s, char *er
   if (e != hipSuccess) { snprintf(err, errlen, "attn launch: %s", hipGetErrorString(e)); return -1; }
   return 0;
 }
+
+// ---- attention without a caller-provided workspace --------------------------
+// For callers that cannot allocate device memory (code under graph capture,
+// serving loops, harnesses that forbid hipMalloc): the partials and merge
+// counters live in a file-scope device array of THVM_ATTN_SCRATCH_BYTES, one
+// copy per GPU, held until the process ends.  Its device address comes from
+// hipGetSymbolAddress, taken once per device at set-up with that device
+// current; host code never passes the array's name to a kernel (in host code
+// it is a stand-in symbol, not a device address).  Every call on a GPU shares
+// that GPU's array: calls that overlap on one GPU race.
+#define THVM_K_MAX_DEVICES 16
+static __device__ __align__(256) unsigned char scratch[THVM_ATTN_SCRATCH_BYTES];
+static void *SCRATCH_PTR[THVM_K_MAX_DEVICES];
+
+extern "C" int thvm_k_attn_scratch_setup(char *err, int errlen) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess || dev < 0 || dev >= THVM_K_MAX_DEVICES) {
+    snprintf(err, errlen, "attn scratch: current device %d: %s", dev, hipGetErrorString(e));
+    return -1;
+  }
+  if (SCRATCH_PTR[dev]) return 0;
+  void *p = nullptr;
+  e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+  if (e != hipSuccess || p == nullptr) {
+    snprintf(err, errlen, "attn scratch: hipGetSymbolAddress: %s", hipGetErrorString(e));
+    return -1;
+  }
+  SCRATCH_PTR[dev] = p;
+  return 0;
+}
+
+extern "C" int thvm_k_attn_decode_scratch(const ThvmAttnArgs *a, hipStream_t s, char *err,
+                                          int errlen) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= THVM_K_MAX_DEVICES ||
+      SCRATCH_PTR[dev] == nullptr) {
+    snprintf(err, errlen, "attn (no-alloc): scratch not set up on device %d (thvm_hip_init)", dev);
+    return -1;
+  }
+  const uint64_t need = thvm_k_attn_part_bytes(a->B, a->H, a->Hkv, a->hd, a->n_split);
+  if (need > (uint64_t)THVM_ATTN_SCRATCH_BYTES) {
+    snprintf(err, errlen,
+             "attn (no-alloc): needs %llu bytes of partials (B=%u H=%u hd=%u n_split=%u), the "
+             "static scratch holds %u",
+             (unsigned long long)need, a->B, a->H, a->hd, a->n_split, THVM_ATTN_SCRATCH_BYTES);
+    return -1;
+  }
+  ThvmAttnArgs ak = *a;
+  ak.part = (float *)SCRATCH_PTR[dev];
+  // the one-launch form's merge counters (after the partials) must start at
+  // zero; the two-launch form's merge reads only partials this call writes
+  if (ak.fused) {
+    const uint64_t cnt = (uint64_t)a->B * a->Hkv * 4;
+    if (thvm_k_zero((char *)SCRATCH_PTR[dev] + (need - cnt), cnt, s, err, errlen)) return -1;
+  }
+  return thvm_k_attn_decode(&ak, s, err, errlen);
+}
