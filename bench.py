@@ -43,28 +43,17 @@ PEAK_GBS = 8000.0
 DT_FP8, DT_F16, DT_BF16, DT_F32 = 9, 11, 12, 13
 DT_NAME = {DT_FP8: "fp8e4m3", DT_F16: "fp16", DT_BF16: "bf16", DT_F32: "fp32"}
 
+from thvm_amd.configs import DECODERS as _DEC  # noqa: E402
+
 MODELS = {
-    "C1": dict(cfg=dict(arch=2, n_layers=12, dim=768, n_heads=12, n_kv_heads=12, head_dim=64,
-                        ffn=3072, vocab=50257, wdtype=DT_F32, adtype=DT_F32, eps=1e-5,
-                        init_std=0.02),
-               ctx=16, cpu_steps=4,
+    "C1": dict(cfg=_DEC["C1"], ctx=16, cpu_steps=4,
                name="C1 GPT-2 small fp32 greedy decode, context 16 (prompt length)"),
-    "C3": dict(cfg=dict(arch=2, n_layers=48, dim=1600, n_heads=25, n_kv_heads=25, head_dim=64,
-                        ffn=6400, vocab=50257, wdtype=DT_F16, adtype=DT_F16, eps=1e-5,
-                        init_std=0.02),
-               ctx=128, cpu_steps=2,
+    "C3": dict(cfg=_DEC["C3"], ctx=128, cpu_steps=2,
                name="C3 GPT-2 XL-shape fp16 greedy decode, KV prefilled to context 128 (prompt length)"),
-    "C5": dict(cfg=dict(arch=3, n_layers=27, dim=2048, n_heads=16, n_kv_heads=16, head_dim=192,
-                        ffn=10944, vocab=102400, wdtype=DT_FP8, adtype=DT_BF16, eps=1e-6,
-                        rope_theta=10000.0, init_std=0.02, kv_lora=512, d_nope=128, d_rope=64,
-                        d_v=128, n_experts=64, n_shared=2, top_k=6, moe_inter=1408, first_dense=1),
-               ctx=4096, cpu_steps=2,
+    "C5": dict(cfg=_DEC["C5"], ctx=4096, cpu_steps=2,
                name="C5 DeepSeek-V2-Lite-shape MLA + MoE fp8 decode, latent cache prefilled to "
                     "context 4096"),
-    "C4": dict(cfg=dict(arch=1, n_layers=32, dim=4096, n_heads=32, n_kv_heads=8, head_dim=128,
-                        ffn=14336, vocab=128256, wdtype=DT_FP8, adtype=DT_BF16, eps=1e-5,
-                        rope_theta=500000.0, init_std=0.02),
-               ctx=2048, cpu_steps=2,
+    "C4": dict(cfg=_DEC["C4"], ctx=2048, cpu_steps=2,
                name="C4 Llama-8B-shape fp8 weight-only decode, KV prefilled to context 2048"),
 }
 

@@ -97,6 +97,13 @@ void     thvm_hip_buf_freelist_remove(uint32_t buf_id);
 uint32_t thvm_hip_buf_storage_root(uint32_t buf_id);
 uint64_t thvm_hip_buf_nbytes(uint32_t buf_id);
 void     thvm_hip_buf_zero(uint32_t buf_id);
+/* Load nbytes of a file at byte file_off into a buffer at dst_off: the
+ * region is mmapped read-only (page-aligned, as the reference's disk tensor
+ * maps it, src/tensor/mmap.c:1-30) and streamed through a ring of pinned
+ * staging buffers with asynchronous host-to-device copies; returns when the
+ * bytes are on the device.  Refused inside a graph capture.  0 / -1. */
+int      thvm_hip_buf_load_file(uint32_t buf_id, uint64_t dst_off, const char *path,
+                                uint64_t file_off, uint64_t nbytes);
 /* Arena view: a non-owning buffer id aliasing [off, off+nbytes) of parent
  * (cuda_buf_alloc_arena_view, reference src/backend/cuda/buf_alloc.c:189-205).
  * Holds a reference on the parent.  0 on failure. */
@@ -288,7 +295,13 @@ typedef struct ThvmDecodeConfig {
    * else 1..64).  The persistent step's attention is the one-chunk form;
    * an op-list decoder with attn_cpb 1 computes it bit for bit.           */
   uint32_t attn_cpb;
-  uint32_t reserved[5];
+  /* next-token choice: temperature 0 is greedy (argmax, lowest index on
+   * ties); above 0 each step samples an id from softmax(logits / temperature)
+   * with a draw keyed on (sample_seed, row, position), so a replayed step
+   * draws afresh and a rerun from the same state draws the same ids.      */
+  float    temperature;
+  uint32_t sample_seed_lo, sample_seed_hi;
+  uint32_t reserved[2];
 } ThvmDecodeConfig;
 
 /* Build the model on device: allocate, fill weights from `seed` (weights
@@ -296,6 +309,23 @@ typedef struct ThvmDecodeConfig {
  * gains 1), compile the step.  Returns a handle > 0, 0 on failure. */
 uint32_t thvm_hip_decoder_create(const ThvmDecodeConfig *cfg, uint64_t seed);
 void     thvm_hip_decoder_destroy(uint32_t dec);
+/* Generation through the captured step (reference serve mode,
+ * bench/dsv2_decode_bench.c:2749-2897): consume prompts [batch][n_prompt]
+ * from position 0, one position per step (the prompt id written into the
+ * device token), then decode up to max_new ids per row with the token kept
+ * on the device; a row stops at `eos` (not emitted; eos < 0: never).  out
+ * [batch][max_new] gets the ids (-1 after a row stops), n_out[batch] their
+ * counts.  Greedy or sampled as the decoder's temperature says.  The step is
+ * captured on first use.  0 / -1. */
+int      thvm_hip_decoder_generate(uint32_t dec, const int32_t *prompts, uint32_t n_prompt,
+                                   uint32_t max_new, int32_t eos, int32_t *out,
+                                   uint32_t *n_out);
+/* The reference's stdin serve protocol over file descriptors (batch 1):
+ * writes "ready", then per request line "id,id,...[|max_new]" one line
+ * "ids: id,id,..." (timing to stderr) until EOF on in_fd.  Requests with ids
+ * outside the vocabulary get an empty reply.  0 at EOF, -1 on a failure. */
+int      thvm_hip_decoder_serve(uint32_t dec, int in_fd, int out_fd, int32_t eos,
+                                uint32_t default_max_new);
 /* Fill the KV cache rows [0, ctx) of every layer and batch row with N(0,1)
  * values from `seed` and set the position so the next step writes row ctx. */
 int      thvm_hip_decoder_prefill_synthetic(uint32_t dec, uint32_t ctx, uint64_t seed);

@@ -310,6 +310,131 @@ void or_argmax(int32_t *tok, const float *logits, uint32_t B, uint32_t V) {
   }
 }
 
+/* ==== temperature sampling (the device's rule, restated) ================== */
+/* exp by Cody-Waite reduction and a degree-8 Taylor polynomial (Horner, fused
+ * multiply-adds), scaled by ldexpf: only correctly rounded IEEE operations,
+ * so this and the device's sexpf agree bit for bit. */
+float or_sexpf(float x) {
+  if (!(x >= -80.0f)) return 0.0f;
+  const float k = rintf(x * 0x1.715476p+0f);
+  float r = fmaf(-k, 0x1.62e000p-1f, x);
+  r = fmaf(-k, 0x1.0bfbe8p-15f, r);
+  float p = 0x1.a01a02p-16f;
+  p = fmaf(p, r, 0x1.a01a02p-13f);
+  p = fmaf(p, r, 0x1.6c16c2p-10f);
+  p = fmaf(p, r, 0x1.111112p-7f);
+  p = fmaf(p, r, 0x1.555556p-5f);
+  p = fmaf(p, r, 0x1.555556p-3f);
+  p = fmaf(p, r, 0x1.0p-1f);
+  p = fmaf(p, r, 1.0f);
+  p = fmaf(p, r, 1.0f);
+  return ldexpf(p, (int)k);
+}
+
+static uint64_t mix64(uint64_t z) {           /* splitmix64 finaliser */
+  z += 0x9E3779B97F4A7C15ull;
+  z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+  z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+  return z ^ (z >> 31);
+}
+
+float or_sample_u01(uint64_t seed, uint32_t row, int32_t L) {
+  const uint64_t h = mix64(mix64(seed ^ mix64((uint64_t)row + 1)) + (uint64_t)(uint32_t)L);
+  return (float)(uint32_t)(h >> 40) * (1.0f / 16777216.0f);
+}
+
+/* the two-level choice over n weights w(k), lane j of 64 owning [jP, (j+1)P) */
+typedef float (*WFn)(const void *ctx, uint32_t k);
+static int64_t pick2(WFn w, const void *ctx, uint32_t n, uint32_t P, float t, float *base) {
+  float q[64];
+  for (uint32_t j = 0; j < 64; j++) {
+    q[j] = 0.0f;
+    for (uint32_t k = j * P; k < (j + 1) * P && k < n; k++) q[j] += w(ctx, k);
+  }
+  float A = 0.0f, Astar = 0.0f, Al = 0.0f;
+  int js = -1, jl = -1;
+  for (int j = 0; j < 64; j++) {
+    if (q[j] > 0.0f) {
+      if (js < 0 && A + q[j] > t) { js = j; Astar = A; }
+      jl = j; Al = A;
+    }
+    A += q[j];
+  }
+  if (js < 0) { js = jl; Astar = Al; }
+  if (js < 0) { *base = 0.0f; return -1; }
+  float c = Astar, cs = 0.0f, cl = 0.0f;
+  int64_t ks = -1, kl = -1;
+  const uint32_t k0 = (uint32_t)js * P, k1 = k0 + P < n ? k0 + P : n;
+  for (uint32_t k = k0; k < k1; k++) {
+    const float x = w(ctx, k);
+    if (x > 0.0f) {
+      if (ks < 0 && c + x > t) { ks = k; cs = c; }
+      kl = k; cl = c;
+    }
+    c += x;
+  }
+  if (ks < 0) { ks = kl; cs = cl; }
+  *base = cs;
+  return ks;
+}
+
+typedef struct { const float *m, *s; float M; } BlkW;
+static float blk_w(const void *ctx, uint32_t k) {
+  const BlkW *b = (const BlkW *)ctx;
+  return b->m[k] == -INFINITY ? 0.0f : b->s[k] * or_sexpf(b->m[k] - b->M);
+}
+typedef struct { const float *lg; float inv, m; } ElW;
+static float el_w(const void *ctx, uint32_t i) {
+  const ElW *e = (const ElW *)ctx;
+  return or_sexpf(e->lg[i] * e->inv - e->m);
+}
+
+void or_sample(int32_t *tok, const float *logits, uint32_t B, uint32_t V, uint32_t nb,
+               float inv_temp, uint64_t seed, int32_t L) {
+  const uint32_t C = (V + nb - 1) / nb;
+  float *m = (float *)malloc((size_t)nb * 4), *sk = (float *)malloc((size_t)nb * 4);
+  for (uint32_t b = 0; b < B; b++) {
+    const float *lg = logits + (uint64_t)b * V;
+    for (uint32_t k = 0; k < nb; k++) {           /* k_sample_part: one block per chunk */
+      const uint64_t lo = (uint64_t)k * C, hi = lo + C < V ? lo + C : V;
+      float mx = -INFINITY, sv[256];
+      for (uint64_t i = lo; i < hi; i++) mx = fmaxf(mx, lg[i] * inv_temp);
+      for (uint32_t t = 0; t < 256; t++) {
+        sv[t] = 0.0f;
+        if (mx != -INFINITY)
+          for (uint64_t i = lo + t; i < hi; i += 256) sv[t] += or_sexpf(lg[i] * inv_temp - mx);
+      }
+      for (uint32_t st = 128; st > 0; st >>= 1)
+        for (uint32_t t = 0; t < st; t++) sv[t] += sv[t + st];
+      m[k] = mx;
+      sk[k] = sv[0];
+    }
+    float M = -INFINITY;
+    for (uint32_t k = 0; k < nb; k++) M = fmaxf(M, m[k]);
+    BlkW bw = {m, sk, M};
+    float S = 0.0f;
+    const uint32_t P = (nb + 63) / 64;
+    for (uint32_t j = 0; j < 64; j++) {               /* lane sums, then lanes in order */
+      float q = 0.0f;
+      for (uint32_t k = j * P; k < (j + 1) * P && k < nb; k++) q += blk_w(&bw, k);
+      S += q;
+    }
+    const float t = or_sample_u01(seed, b, L) * S;
+    float base;
+    const int64_t ks = pick2(blk_w, &bw, nb, P, t, &base);
+    if (ks < 0) continue;
+    const float r = (t - base) / or_sexpf(m[ks] - M);
+    const uint64_t lo = (uint64_t)ks * C;
+    const uint32_t n = (uint32_t)((lo + C <= V ? lo + C : V) - lo);
+    ElW ew = {lg + lo, inv_temp, m[ks]};
+    float base2;
+    const int64_t is = pick2(el_w, &ew, n, (C + 63) / 64, r, &base2);
+    if (is >= 0) tok[b] = (int32_t)(lo + is);
+  }
+  free(m);
+  free(sk);
+}
+
 /* ==== whole decode step ================================================== */
 
 static float silu(float g) { return g / (1.0f + expf(-g)); }

@@ -61,6 +61,14 @@ void or_attn_decode(void *out, uint32_t odt, const void *q, uint32_t qdt,
                     uint32_t max_seq, uint32_t L, float scale);
 /* argmax, lowest index on ties (dsv2 argmax_part/fin C twins :989-1020). */
 void or_argmax(int32_t *tok, const float *logits, uint32_t B, uint32_t V);
+/* Temperature sampling as the device's argmax builtin runs it with temp > 0
+ * (rowops.hip k_sample_part / k_sample_fin): the same exp (or_sexpf), block
+ * partition into nb chunks, fold orders and two-level choice, and the draw
+ * u = or_sample_u01(seed, row, L).  Rows whose logits are all -inf keep tok. */
+float or_sexpf(float x);
+float or_sample_u01(uint64_t seed, uint32_t row, int32_t L);
+void  or_sample(int32_t *tok, const float *logits, uint32_t B, uint32_t V, uint32_t nb,
+                float inv_temp, uint64_t seed, int32_t L);
 
 /* ---- whole decode step ---- */
 typedef struct OrLayer {

@@ -75,6 +75,8 @@ def oracle() -> C.CDLL:
             "or_attn_decode": (None, [_vp, _u32, _vp, _u32, _vp, _vp, _u32, _u32, _u32, _u32,
                                       _u32, _u32, _u32, _f]),
             "or_argmax": (None, [_vp, _vp, _u32, _u32]),
+            "or_sexpf": (_f, [_f]), "or_sample_u01": (_f, [_u64, _u32, C.c_int32]),
+            "or_sample": (None, [_vp, _vp, _u32, _u32, _u32, _f, _u64, C.c_int32]),
             "or_decode_step": (_i, [C.POINTER(OrModel), _vp, _u32, _vp, _vp]),
             "or_mla_prep": (None, [_vp, _vp, _vp, _vp, _vp, _vp, _u32, _vp, _vp, _vp, _vp,
                                    _u32, _u32, _u32, _u32, _f]),

@@ -419,3 +419,78 @@ def test_moe_brute_force():
     g, u = f(wgs[0::2]) @ x, f(wgs[1::2]) @ x
     want += f(wds) @ (silu(g) * u)
     assert np.allclose(out, want, rtol=1e-4, atol=1e-6)
+
+
+# ------------------------------------------------------------- sampling ----
+def test_sexpf_is_exp_to_float_accuracy():
+    """or_sexpf (Cody-Waite + degree-8 Taylor): within 2 ulp of exp over the
+    range the sampler uses, exact at 0, zero below -80."""
+    R = O.oracle()
+    xs = np.concatenate([np.linspace(-80, 0, 200001), -np.logspace(-8, 1.9, 2000), [0.0, -1e-30]])
+    got = np.array([R.or_sexpf(float(x)) for x in xs], np.float64)
+    want = np.exp(xs.astype(np.float32).astype(np.float64))
+    assert np.all(np.abs(got - want) <= 2.5e-7 * want)
+    assert R.or_sexpf(0.0) == 1.0 and R.or_sexpf(-80.5) == 0.0 and R.or_sexpf(float("-inf")) == 0.0
+
+
+def test_sample_u01_uniform_and_keyed():
+    R = O.oracle()
+    u = np.array([R.or_sample_u01(7, 0, L) for L in range(20000)])
+    assert np.all((u >= 0) & (u < 1))
+    from scipy import stats
+    assert stats.kstest(u, "uniform").pvalue > 1e-3
+    assert R.or_sample_u01(7, 0, 5) == R.or_sample_u01(7, 0, 5)
+    assert R.or_sample_u01(7, 0, 5) != R.or_sample_u01(7, 1, 5) != R.or_sample_u01(8, 0, 5)
+
+
+def _sample(lg, nb, temp, seed, L):
+    B, V = lg.shape
+    tok = np.full(B, -1, np.int32)
+    lg = np.ascontiguousarray(lg, np.float32)
+    O.oracle().or_sample(tok.ctypes.data, lg.ctypes.data, B, V, nb, 1.0 / temp, seed, L)
+    return tok
+
+
+@pytest.mark.parametrize("V,nb", [(50, 1), (1000, 16), (128256, 256)])
+@pytest.mark.parametrize("temp", [0.7, 1.0, 3.0])
+def test_sample_is_the_inverse_cdf_of_the_tempered_softmax(V, nb, temp):
+    """Each sampled id is where the float64 CDF of softmax(z / T), in index
+    order, crosses the same uniform draw u: cdf(i-1) <= u <= cdf(i) up to f32
+    rounding.  A wrong chunk, offset or threshold misses this."""
+    R = O.oracle()
+    rng = np.random.default_rng(V + int(temp * 10))
+    lg = (rng.standard_normal((1, V)) * 2).astype(np.float32)
+    z = lg[0].astype(np.float32) * np.float32(1.0 / temp)
+    p = np.exp(z.astype(np.float64) - z.max())
+    cdf = np.cumsum(p / p.sum())
+    n = 40 if V > 10000 else 300
+    for L in range(n):
+        u = R.or_sample_u01(11, 0, L)
+        i = int(_sample(lg, nb, temp, 11, L)[0])
+        lo_c = cdf[i - 1] if i > 0 else 0.0
+        assert lo_c - 2e-5 <= u <= cdf[i] + 2e-5, (L, i, u, lo_c, cdf[i])
+
+
+def test_sample_frequencies_match_softmax():
+    from scipy import stats
+    V = 12
+    lg = np.array([[0.1, 2.0, -1.0, 0.5, 3.0, 0.0, -2.0, 1.5, 1.0, -0.5, 2.5, 0.2]], np.float32)
+    p = np.exp(lg[0].astype(np.float64) / 1.3)
+    p /= p.sum()
+    ids = np.array([_sample(lg, 1, 1.3, 5, L)[0] for L in range(30000)])
+    counts = np.bincount(ids, minlength=V)
+    assert stats.chisquare(counts, p * len(ids)).pvalue > 1e-4
+
+
+def test_sample_edge_cases():
+    # one overwhelming logit; -inf logits never drawn; a tiny temperature is
+    # the argmax; rows are independent draws
+    lg = np.full((3, 500), -np.inf, np.float32)
+    lg[0, 123] = 0.0
+    lg[1, :] = 0.0
+    lg[1, ::2] = -np.inf
+    lg[2, :] = np.linspace(-1, 1, 500)
+    for L in range(50):
+        t = _sample(lg, 4, 1.0, 3, L)
+        assert t[0] == 123 and t[1] % 2 == 1
+    assert all(_sample(lg[2:3], 4, 1e-4, 3, L)[0] == 499 for L in range(20))

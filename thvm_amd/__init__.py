@@ -45,7 +45,8 @@ class DecodeConfig(C.Structure):
         (n, C.c_uint32) for n in ("kv_lora", "d_nope", "d_rope", "d_v", "n_experts",
                                   "n_shared", "top_k", "moe_inter", "first_dense", "step_mode",
                                   "moe_mode", "attn_cpb")] + [
-        ("reserved", C.c_uint32 * 5)]
+        ("temperature", C.c_float), ("sample_seed_lo", C.c_uint32), ("sample_seed_hi", C.c_uint32),
+        ("reserved", C.c_uint32 * 2)]
 
 
 class Uop(C.Structure):
@@ -73,6 +74,7 @@ _SIGS = {
     "thvm_hip_buf_write_at": (_i32, [_u32, _u64, _vp, _u64]),
     "thvm_hip_buf_copy_at": (_i32, [_u32, _u64, _u32, _u64]),
     "thvm_hip_buf_copy_row": (_i32, [_u32, _u64, _u64, _u32, _u64, _u32, _u64]),
+    "thvm_hip_buf_load_file": (_i32, [_u32, _u64, _cp, _u64, _u64]),
     "thvm_hip_buf_refcount": (_u32, [_u32]), "thvm_hip_buf_freelist_push": (None, [_u32]),
     "thvm_hip_buf_freelist_remove": (None, [_u32]), "thvm_hip_buf_storage_root": (_u32, [_u32]),
     "thvm_hip_buf_nbytes": (_u64, [_u32]), "thvm_hip_buf_zero": (None, [_u32]),
@@ -97,6 +99,8 @@ _SIGS = {
     "thvm_hip_kprof_bytes": (_u64, [_cp]),
     "thvm_hip_decoder_create": (_u32, [C.POINTER(DecodeConfig), _u64]),
     "thvm_hip_decoder_destroy": (None, [_u32]),
+    "thvm_hip_decoder_generate": (_i32, [_u32, _vp, _u32, _u32, C.c_int32, _vp, _vp]),
+    "thvm_hip_decoder_serve": (_i32, [_u32, _i32, _i32, C.c_int32, _u32]),
     "thvm_hip_decoder_prefill_synthetic": (_i32, [_u32, _u32, _u64]),
     "thvm_hip_decoder_set_state": (_i32, [_u32, _vp, _u32]),
     "thvm_hip_decoder_step": (_i32, [_u32]), "thvm_hip_decoder_capture": (_u32, [_u32]),
@@ -295,6 +299,23 @@ class Decoder:
 
     def replay(self, n: int = 1) -> None:
         _check(lib().thvm_hip_decoder_replay(self.h, n), "decoder_replay")
+
+    def generate(self, prompts, max_new: int, eos: int = -1):
+        """prompts [batch][n] (or [n] for every row) -> (ids [batch][max_new]
+        with -1 after a row stops, counts [batch])."""
+        B = self.cfg.batch
+        p = np.asarray(prompts, np.int32)
+        if p.ndim == 1:
+            p = np.tile(p, (B, 1))
+        p = np.ascontiguousarray(p)
+        out = np.empty((B, max_new), np.int32)
+        n = np.empty(B, np.uint32)
+        _check(lib().thvm_hip_decoder_generate(self.h, p.ctypes.data, p.shape[1], max_new, eos,
+                                               out.ctypes.data, n.ctypes.data), "generate")
+        return out, n.astype(np.int64)
+
+    def serve(self, in_fd: int, out_fd: int, eos: int = -1, default_max_new: int = 256) -> None:
+        _check(lib().thvm_hip_decoder_serve(self.h, in_fd, out_fd, eos, default_max_new), "serve")
 
     def tokens(self, n: int) -> np.ndarray:
         out = np.empty((self.cfg.batch, n), np.int32)

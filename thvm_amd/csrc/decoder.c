@@ -180,9 +180,26 @@ static int rope_tables(Decoder *d) {
   return rc;
 }
 
+/* the argmax op's sampling keys: "" (greedy) or " temp=<T> seed=<seed>" */
+static const char *sample_keys(const ThvmDecodeConfig *c, char *buf, size_t n) {
+  buf[0] = 0;
+  if (c->temperature > 0.0f)
+    snprintf(buf, n, " temp=%a seed=%llu", (double)c->temperature,
+             (unsigned long long)(((u64)c->sample_seed_hi << 32) | c->sample_seed_lo));
+  return buf;
+}
+
 static int cfg_check(const ThvmDecodeConfig *c) {
   if (c->arch != THVM_ARCH_LLAMA && c->arch != THVM_ARCH_GPT2 && c->arch != THVM_ARCH_DSV2) {
     hb_set_error("decoder: arch %u not supported by this build", c->arch);
+    return -1;
+  }
+  if (!(c->temperature >= 0.0f) || c->temperature > 1e30f) {
+    hb_set_error("decoder: temperature must be a finite value >= 0");
+    return -1;
+  }
+  if (c->step_mode && c->temperature > 0.0f) {
+    hb_set_error("decoder: the persistent step (step_mode 1) decodes greedily; temperature must be 0");
     return -1;
   }
   if (c->step_mode > 1 || (c->step_mode && c->arch != THVM_ARCH_LLAMA)) {
@@ -384,8 +401,9 @@ static int op_tail(Decoder *d, u32 lm_w, u32 lm_s, const NormSpec *fn) {
   for (u32 i = 0; i < ng; i++) a[n++] = gargs[i];
   if (op_add(d, "lm_head", p, a, n)) return -1;
   u32 nb = c->vocab >= 256 * 64 ? 256 : (c->vocab + 63) / 64;
-  snprintf(p, sizeof p, "thvm-builtin:argmax b=%u v=%u nb=%u hist=1 hstride=%u", c->batch,
-           c->vocab, nb, c->max_seq + 1);
+  char sk[96];
+  snprintf(p, sizeof p, "thvm-builtin:argmax b=%u v=%u nb=%u hist=1 hstride=%u%s", c->batch,
+           c->vocab, nb, c->max_seq + 1, sample_keys(c, sk, sizeof sk));
   u32 b[6] = {tens_find(d, "tok"), tens_find(d, "logits"), tens_find(d, "am.pv"),
               tens_find(d, "am.pi"), tens_find(d, "hist"), tens_find(d, "len")};
   if (op_add(d, "argmax", p, b, 6)) return -1;
@@ -892,8 +910,9 @@ static int build_dsv2(Decoder *d) {
   if (f8) la[ln++] = ls;
   if (op_add(d, "lm_head", p, la, ln)) return -1;
   const u32 nb = V >= 256 * 64 ? 256 : (V + 63) / 64;
-  snprintf(p, sizeof p, "thvm-builtin:argmax b=%u v=%u nb=%u hist=1 hstride=%u", B, V, nb,
-           c->max_seq + 1);
+  char sk[96];
+  snprintf(p, sizeof p, "thvm-builtin:argmax b=%u v=%u nb=%u hist=1 hstride=%u%s", B, V, nb,
+           c->max_seq + 1, sample_keys(c, sk, sizeof sk));
   u32 am[6] = {tens_find(d, "tok"), tens_find(d, "logits"), tens_find(d, "am.pv"),
                tens_find(d, "am.pi"), tens_find(d, "hist"), L};
   if (op_add(d, "argmax", p, am, 6)) return -1;
@@ -972,6 +991,19 @@ static int dec_run_ops(Decoder *d) {
       return -1;
   }
   return 0;
+}
+
+int hb_decoder_dims(u32 h, u32 *batch, u32 *max_seq, u32 *vocab) {
+  Decoder *d = dec_get(h);
+  if (!d) return -1;
+  *batch = d->c.batch;
+  *max_seq = d->c.max_seq;
+  *vocab = d->c.vocab;
+  return 0;
+}
+u32 hb_decoder_slot(u32 h) {
+  Decoder *d = dec_get(h);
+  return d ? d->jit_slot : 0;
 }
 
 THVM_API int thvm_hip_decoder_step(uint32_t h) {

@@ -417,9 +417,13 @@ int hb_builtin_launch(const char *program, const u32 *ids, u32 n, int check_only
     ThvmArgmaxArgs a;
     memset(&a, 0, sizeof a);
     u32 hist = 0;
+    float temp = 0.0f;
     NEED(spec_u32(&sp, "b", &a.B, 1, 0) || spec_u32(&sp, "v", &a.V, 1, 0) ||
          spec_u32(&sp, "nb", &a.nb, 0, 256) || spec_u32(&sp, "hist", &hist, 0, 0) ||
-         spec_u32(&sp, "hstride", &a.hist_stride, 0, 0));
+         spec_u32(&sp, "hstride", &a.hist_stride, 0, 0) || spec_f32(&sp, "temp", &temp, 0, 0.0f) ||
+         spec_u64(&sp, "seed", &a.seed, 0, 0));
+    if (!(temp >= 0.0f) || temp > 1e30f) { hb_set_error("builtin argmax: temp must be >= 0"); return -1; }
+    a.inv_temp = temp > 0.0f ? 1.0f / temp : 0.0f;
     if (a.nb > a.V) a.nb = a.V;
     a.tok = (int32_t *)arg(&c, 0, (u64)a.B * 4);
     a.logits = (const float *)arg(&c, 1, (u64)a.B * a.V * 4);
@@ -429,12 +433,27 @@ int hb_builtin_launch(const char *program, const u32 *ids, u32 n, int check_only
       if (a.hist_stride == 0) { hb_set_error("builtin argmax: hist=1 needs hstride"); return -1; }
       a.hist = (int32_t *)arg(&c, 4, (u64)a.B * a.hist_stride * 4);
       a.len = (const int32_t *)arg(&c, 5, 4);
+    } else if (temp > 0.0f) {       /* sampling keys its draw on the position */
+      a.len = (const int32_t *)arg(&c, 4, 4);
     }
     if (c.bad) return -1;
     bytes = (u64)a.B * a.V * 4;
     if (check_only) return 0;
     if (prof) hb_kprof_begin(K, &e0, &e1);
     rc = thvm_k_argmax(&a, HB_STREAM, err, sizeof err);
+  } else if (strcmp(K, "quant_fp8") == 0) {   /* q, scale, x */
+    u32 rows = 0, cols = 0, xdt = 0;
+    NEED(spec_u32(&sp, "rows", &rows, 1, 0) || spec_u32(&sp, "cols", &cols, 1, 0) ||
+         spec_u32(&sp, "xt", &xdt, 1, 0));
+    if (!is_act(xdt)) { hb_set_error("builtin quant_fp8: xt must be f32 / bf16 / fp16"); return -1; }
+    uint8_t *q = (uint8_t *)arg(&c, 0, (u64)rows * cols);
+    float *scale = (float *)arg(&c, 1, (u64)rows * 4);
+    const void *x = arg(&c, 2, (u64)rows * cols * hb_dt_size(xdt));
+    if (c.bad) return -1;
+    bytes = (u64)rows * cols * (1 + hb_dt_size(xdt)) + (u64)rows * 4;
+    if (check_only) return 0;
+    if (prof) hb_kprof_begin(K, &e0, &e1);
+    rc = thvm_k_quant_fp8_rows(q, scale, x, xdt, rows, cols, HB_STREAM, err, sizeof err);
   } else if (strcmp(K, "len_bump") == 0) {
     u32 d = 1;
     NEED(spec_u32(&sp, "delta", &d, 0, 1));

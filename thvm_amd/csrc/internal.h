@@ -49,6 +49,9 @@ void hb_rtc_reset(void);
 void hb_jit_reset(void);
 void hb_graph_reset(void);
 void hb_decoder_reset(void);
+void hb_loader_reset(void);
+int  hb_decoder_dims(u32 h, u32 *batch, u32 *max_seq, u32 *vocab);   /* -1: no such decoder */
+u32  hb_decoder_slot(u32 h);                                          /* its JIT slot, 0 = none */
 
 /* kernel profiling hooks (builtin dispatches only, never under capture) */
 int  hb_kprof_on(void);

@@ -212,6 +212,10 @@ typedef struct ThvmArgmaxArgs {
   int32_t *tok; const float *logits; float *pv; int32_t *pi;
   int32_t *hist; const int32_t *len;
   uint32_t B, V, nb, hist_stride;
+  float inv_temp;          /* > 0: sample from softmax(logits * inv_temp)
+                            * instead of the argmax (pi then holds f32 block
+                            * sums); the draw is keyed on (seed, row, len[0]) */
+  uint64_t seed;
 } ThvmArgmaxArgs;
 int thvm_k_argmax(const ThvmArgmaxArgs *a, hipStream_t s, char *err, int errlen);
 
@@ -236,6 +240,11 @@ int thvm_k_fill_cache(void *cache, uint32_t dt, uint32_t B, uint32_t Hkv,
                       uint32_t max_seq, uint32_t hd, uint32_t ctx,
                       uint64_t seed, uint64_t tag, hipStream_t s,
                       char *err, int errlen);
+
+/* Per-row fp8 e4m3 quantisation of a loaded matrix x [rows][cols] (f32 /
+ * bf16 / fp16): scale[r] = absmax/448 (1 for a zero row), q = e4m3_sat(x/scale). */
+int thvm_k_quant_fp8_rows(uint8_t *q, float *scale, const void *x, uint32_t xdt, uint32_t rows,
+                          uint32_t cols, hipStream_t s, char *err, int errlen);
 
 /* Plain device copy of nbytes (16-byte aligned pointers and size), each
  * byte read once and written once: the calibration of HBM traffic counters. */

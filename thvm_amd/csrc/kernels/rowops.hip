@@ -305,10 +305,178 @@ __global__ void k_argmax_fin(ThvmArgmaxArgs a) {
   }
 }
 
+// ---- temperature sampling: id ~ softmax(logits / T), replacing argmax ----
+// The draw is exactly specified so that a CPU restatement reproduces every
+// id bit for bit (the oracle's or_sample):
+//  * sexpf: exp by Cody-Waite reduction (x = k ln2 + r, ln2 split into a
+//    20-bit head and a tail) and the degree-8 Taylor polynomial of e^r in
+//    Horner form with fused multiply-adds, scaled by ldexpf -- only
+//    correctly rounded IEEE operations, so any IEEE machine gets the same
+//    bits; arguments below -80 give 0;
+//  * z = l * (1/T); chunk k of C = ceil(V/nb) logits: m_k = max z, s_k =
+//    the 256 thread sums (stride 256) folded 128, 64, ..., 1 of sexpf(z - m_k);
+//  * w_k = s_k * sexpf(m_k - M), M = max m_k; lane j of 64 owns chunks
+//    [jP, (j+1)P), P = ceil(nb/64), q_j their sequential sum, S = sum_j q_j;
+//  * u in [0,1) from a counter hash of (seed, row, L) -- L the device-resident
+//    position, so every replay of a captured step draws afresh; t = u S;
+//  * select: the first lane j with q_j > 0 and A_j + q_j > t (A_j the
+//    sequential sum before it; else the last lane with q_j > 0), then the
+//    same rule over its own chunks; then, inside the chosen chunk, with the
+//    threshold (t - base) / sexpf(m_k - M), the same two levels over lanes
+//    owning E = ceil(C/64) consecutive logits each.
+// No contraction anywhere in this section: every product and sum rounds.
+#pragma clang fp contract(off)
+__device__ __forceinline__ uint64_t mix64(uint64_t z);
+__device__ __forceinline__ float sexpf(float x) {
+  if (!(x >= -80.0f)) return 0.0f;
+  const float k = rintf(x * 0x1.715476p+0f);
+  float r = fmaf(-k, 0x1.62e000p-1f, x);
+  r = fmaf(-k, 0x1.0bfbe8p-15f, r);
+  float p = 0x1.a01a02p-16f;
+  p = fmaf(p, r, 0x1.a01a02p-13f);
+  p = fmaf(p, r, 0x1.6c16c2p-10f);
+  p = fmaf(p, r, 0x1.111112p-7f);
+  p = fmaf(p, r, 0x1.555556p-5f);
+  p = fmaf(p, r, 0x1.555556p-3f);
+  p = fmaf(p, r, 0x1.0p-1f);
+  p = fmaf(p, r, 1.0f);
+  p = fmaf(p, r, 1.0f);
+  return ldexpf(p, (int)k);
+}
+
+__device__ __forceinline__ float sample_u01(uint64_t seed, uint32_t row, int32_t L) {
+  const uint64_t h = mix64(mix64(seed ^ mix64((uint64_t)row + 1)) + (uint64_t)(uint32_t)L);
+  return (float)(uint32_t)(h >> 40) * (1.0f / 16777216.0f);
+}
+
+__global__ __launch_bounds__(256) void k_sample_part(ThvmArgmaxArgs a) {
+  __shared__ float sv[256];
+  const uint32_t b = blockIdx.y, blk = blockIdx.x, t = threadIdx.x;
+  const uint32_t chunk = (a.V + a.nb - 1) / a.nb;
+  const uint64_t lo = (uint64_t)blk * chunk;
+  uint64_t hi = lo + chunk;
+  if (hi > a.V) hi = a.V;
+  const float *lg = a.logits + (uint64_t)b * a.V;
+  float m = -INFINITY;
+  for (uint64_t i = lo + t; i < hi; i += 256) m = fmaxf(m, lg[i] * a.inv_temp);
+  sv[t] = m;
+  __syncthreads();
+  for (uint32_t st = 128; st > 0; st >>= 1) {
+    if (t < st) sv[t] = fmaxf(sv[t], sv[t + st]);
+    __syncthreads();
+  }
+  m = sv[0];
+  __syncthreads();
+  float acc = 0.0f;
+  if (m != -INFINITY)
+    for (uint64_t i = lo + t; i < hi; i += 256) acc += sexpf(lg[i] * a.inv_temp - m);
+  sv[t] = acc;
+  __syncthreads();
+  for (uint32_t st = 128; st > 0; st >>= 1) {
+    if (t < st) sv[t] += sv[t + st];
+    __syncthreads();
+  }
+  if (t == 0) {
+    a.pv[b * a.nb + blk] = m;
+    ((float *)a.pi)[b * a.nb + blk] = sv[0];
+  }
+}
+
+__device__ __forceinline__ float rlane(float v, int j) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), j));
+}
+
+// The two-level choice over n weights held as lane j's range [jP, (j+1)P):
+// q = this lane's sequential sum; returns the chosen index and, in *base,
+// the sequential sum of the weights before it.  Every lane returns the same.
+template <typename W>
+__device__ __forceinline__ int64_t pick2(const W &wt, float q, uint32_t n, uint32_t P, float t,
+                                         float *base) {
+  float A = 0.0f, Astar = 0.0f;
+  int js = -1, jl = -1;
+  float Al = 0.0f;
+  for (int j = 0; j < 64; j++) {
+    const float qj = rlane(q, j);
+    if (qj > 0.0f) {
+      if (js < 0 && A + qj > t) { js = j; Astar = A; }
+      jl = j; Al = A;
+    }
+    A += qj;
+  }
+  if (js < 0) { js = jl; Astar = Al; }
+  if (js < 0) { *base = 0.0f; return -1; }
+  float c = Astar;
+  int64_t ks = -1, kl = -1;
+  float cl = 0.0f, cs = 0.0f;
+  const uint32_t k0 = (uint32_t)js * P, k1 = k0 + P < n ? k0 + P : n;
+  for (uint32_t k = k0; k < k1; k++) {
+    const float w = wt(k);
+    if (w > 0.0f) {
+      if (ks < 0 && c + w > t) { ks = k; cs = c; }
+      kl = k; cl = c;
+    }
+    c += w;
+  }
+  if (ks < 0) { ks = kl; cs = cl; }
+  *base = cs;
+  return ks;
+}
+
+__global__ __launch_bounds__(64) void k_sample_fin(ThvmArgmaxArgs a) {
+  const uint32_t b = blockIdx.x, nb = a.nb;
+  const int lane = threadIdx.x;
+  const float *pv = a.pv + (uint64_t)b * nb;
+  const float *ps = (const float *)a.pi + (uint64_t)b * nb;
+  float M = -INFINITY;
+  for (uint32_t k = lane; k < nb; k += 64) M = fmaxf(M, pv[k]);
+  for (int j = 0; j < 64; j++) M = fmaxf(M, rlane(M, j));
+  auto wk = [&](uint32_t k) { return pv[k] == -INFINITY ? 0.0f : ps[k] * sexpf(pv[k] - M); };
+  const uint32_t P = (nb + 63) / 64;
+  float q = 0.0f;
+  for (uint32_t k = (uint32_t)lane * P; k < (uint32_t)(lane + 1) * P && k < nb; k++) q += wk(k);
+  float S = 0.0f;
+  for (int j = 0; j < 64; j++) S += rlane(q, j);
+  const int32_t L = a.len ? a.len[0] : 0;
+  const float tgt = sample_u01(a.seed, b, L) * S;
+  float base;
+  const int64_t ks = pick2(wk, q, nb, P, tgt, &base);
+  if (ks < 0) return;                              // every weight zero: no finite logit
+  const float r = (tgt - base) / sexpf(pv[ks] - M);
+  const float mk = pv[ks];
+  const uint32_t C = (a.V + nb - 1) / nb;
+  const uint64_t lo = (uint64_t)ks * C;
+  const uint32_t n = (uint32_t)((lo + C <= a.V ? lo + C : a.V) - lo);
+  const float *lg = a.logits + (uint64_t)b * a.V + lo;
+  auto ek = [&](uint32_t i) { return sexpf(lg[i] * a.inv_temp - mk); };
+  const uint32_t E = (C + 63) / 64;
+  float qe = 0.0f;
+  for (uint32_t i = (uint32_t)lane * E; i < (uint32_t)(lane + 1) * E && i < n; i++) qe += ek(i);
+  float base2;
+  const int64_t is = pick2(ek, qe, n, E, r, &base2);
+  if (lane != 0 || is < 0) return;
+  const int32_t id = (int32_t)(lo + is);
+  a.tok[b] = id;
+  if (a.hist) {
+    if (L >= 0 && (uint32_t)L < a.hist_stride) a.hist[(uint64_t)b * a.hist_stride + L] = id;
+  }
+}
+#pragma clang fp contract(fast)   // back to the HIP default for the rest of the file
+
 extern "C" int thvm_k_argmax(const ThvmArgmaxArgs *a, hipStream_t s, char *err, int errlen) {
   if (a->B == 0 || a->V == 0 || a->nb == 0 || a->nb > a->V || (a->hist && !a->len)) {
     snprintf(err, errlen, "argmax: bad args");
     return -1;
+  }
+  if (a->inv_temp > 0.0f) {          // temperature sampling
+    if (a->nb > 4096 || (a->V + a->nb - 1) / a->nb > 64u * 4096u) {
+      snprintf(err, errlen, "sample: nb %u / chunk out of range", a->nb);
+      return -1;
+    }
+    thvm_launch(true, false, k_sample_part, dim3(a->nb, a->B), dim3(256), 0, s, *a);
+    thvm_launch(false, true, k_sample_fin, dim3(a->B), dim3(64), 0, s, *a);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) { snprintf(err, errlen, "sample launch: %s", hipGetErrorString(e)); return -1; }
+    return 0;
   }
   thvm_launch(true, false, k_argmax_part, dim3(a->nb, a->B), dim3(256), 0, s, *a);
   thvm_launch(false, true, k_argmax_fin, dim3(a->B), dim3(64), 0, s, *a);
@@ -532,6 +700,43 @@ extern "C" int thvm_k_fill_fp8_rows(uint8_t *q, float *scale, uint32_t rows, uin
                      tag, std);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) { snprintf(err, errlen, "fill_fp8 launch: %s", hipGetErrorString(e)); return -1; }
+  return 0;
+}
+
+// Per-row weight-only fp8 quantisation of a loaded checkpoint matrix x
+// [rows][cols] (f32 / bf16 / fp16): scale[r] = absmax_r / 448 (1 for an
+// all-zero row), q = e4m3_sat(x / scale) -- the scheme the synthetic fp8
+// weights use, so a converted checkpoint feeds the same kernels.
+__global__ __launch_bounds__(256) void k_quant_fp8_rows(uint8_t *q, float *scale, const void *x,
+                                                        uint32_t xdt, uint32_t rows, uint32_t cols) {
+  __shared__ float red[4];
+  for (uint32_t r = blockIdx.x; r < rows; r += gridDim.x) {
+    const uint64_t base = (uint64_t)r * cols;
+    float mx = 0.0f;
+    for (uint32_t c = threadIdx.x; c < cols; c += 256) mx = fmaxf(mx, fabsf(ld_a(x, base + c, xdt)));
+    float w = wave_max(mx);
+    __syncthreads();
+    if (lane_id() == 0) red[threadIdx.x >> 6] = w;
+    __syncthreads();
+    const float am = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    const float sc = am > 0.0f ? am / 448.0f : 1.0f;
+    if (threadIdx.x == 0) scale[r] = sc;
+    for (uint32_t c = threadIdx.x; c < cols; c += 256) q[base + c] = f2fp8_sat(ld_a(x, base + c, xdt) / sc);
+    __syncthreads();
+  }
+}
+extern "C" int thvm_k_quant_fp8_rows(uint8_t *q, float *scale, const void *x, uint32_t xdt,
+                                     uint32_t rows, uint32_t cols, hipStream_t s, char *err,
+                                     int errlen) {
+  if (xdt != THVM_DT_FP32 && xdt != THVM_DT_BF16 && xdt != THVM_DT_FP16) {
+    snprintf(err, errlen, "quant_fp8: source dtype must be f32 / bf16 / fp16");
+    return -1;
+  }
+  if (rows == 0 || cols == 0) return 0;
+  const uint32_t blocks = rows < 8192 ? rows : 8192;
+  thvm_launch(true, true, k_quant_fp8_rows, dim3(blocks), dim3(256), 0, s, q, scale, x, xdt, rows, cols);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) { snprintf(err, errlen, "quant_fp8 launch: %s", hipGetErrorString(e)); return -1; }
   return 0;
 }
 
