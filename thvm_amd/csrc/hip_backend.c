@@ -448,6 +448,7 @@ THVM_API void thvm_hip_shutdown(void) {
   hb_jit_reset();
   hb_graph_reset();
   hb_rtc_reset();
+  hb_loader_reset();
   for (u32 i = BUFS_NEXT; i-- > 1;) {
     if (BUFS[i].live && !BUFS[i].owns) memset(&BUFS[i], 0, sizeof(HbBuf));
   }
