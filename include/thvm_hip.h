@@ -301,7 +301,16 @@ typedef struct ThvmDecodeConfig {
    * draws afresh and a rerun from the same state draws the same ids.      */
   float    temperature;
   uint32_t sample_seed_lo, sample_seed_hi;
-  uint32_t reserved[2];
+  /* blind speculative decode (reference DSV2_SPEC, bench/dsv2_decode_bench.c:
+   * 56-68, 2255-2745): spec_rows S in 2..4 builds a second step that drafts
+   * S-1 ids from the most recent bigram match in the token history, verifies
+   * the pending id and the drafts as S consecutive positions of one
+   * sequence, and commits the longest verified prefix plus one id (L
+   * advances by 1..S).  Each verify row folds exactly as the one-row step
+   * does, so the committed ids are the greedy ids.  LLAMA, batch 1, greedy,
+   * op-list step only; 0 = off.  spec_forced = 1 drafts the ids the host
+   * seeded after the pending one instead (the acceptance gate).            */
+  uint32_t spec_rows, spec_forced;
 } ThvmDecodeConfig;
 
 /* Build the model on device: allocate, fill weights from `seed` (weights
@@ -339,6 +348,15 @@ uint32_t thvm_hip_decoder_capture(uint32_t dec);
 /* Replay the captured step n_steps times (graph launches, no host values).
  * Each step writes its greedy token into the history buffer. */
 int      thvm_hip_decoder_replay(uint32_t dec, uint32_t n_steps);
+/* Speculative step (spec_rows > 0): one eager draft + verify + commit;
+ * capture it into its own JIT slot (runs it once; returns the slot, 0 on
+ * failure); replay the captured speculative step n_steps times.  Each step
+ * advances the position by 1..spec_rows, written to the token history as
+ * the one-row step writes it.  Reference: step_build_spec and run_spec,
+ * bench/dsv2_decode_bench.c:2419-2745. */
+int      thvm_hip_decoder_spec_step(uint32_t dec);
+uint32_t thvm_hip_decoder_spec_capture(uint32_t dec);
+int      thvm_hip_decoder_spec_replay(uint32_t dec, uint32_t n_steps);
 /* Read back the token history rows [0, n) of batch row b (greedy ids), and
  * the logits [batch, vocab] f32 of the last step. */
 int      thvm_hip_decoder_read_tokens(uint32_t dec, int32_t *dst, uint32_t n);

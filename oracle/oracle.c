@@ -435,6 +435,50 @@ void or_sample(int32_t *tok, const float *logits, uint32_t B, uint32_t V, uint32
   free(sk);
 }
 
+/* ==== blind speculative draft / commit =================================== */
+
+/* draft_prep (bench/dsv2_decode_bench.c:1116-1150): candidate 0 is the
+ * pending id; candidates 1.. continue the most recent earlier occurrence of
+ * the bigram (hist[P-1], hist[P]) -- the largest j with j+1 < P -- while the
+ * continuation stays at or before P; forced takes hist[P+1..] instead. */
+void or_spec_draft(int32_t *ca, int32_t *ce, const int32_t *hist, int32_t L, uint32_t S,
+                   uint32_t V, uint32_t cap, int forced) {
+  const int32_t P = L - 1;
+  if (P < 0 || P >= (int32_t)cap) {
+    for (uint32_t t = 0; t < S; t++) { ca[t] = -1; ce[t] = 0; }
+    return;
+  }
+  const int32_t pend = hist[P];
+  const int32_t pend_ok = pend >= 0 && (uint32_t)pend < V ? pend : 0;
+  int32_t best = -1;
+  if (!forced && P >= 1)
+    for (int32_t j = 0; j + 1 < P; j++)
+      if (hist[j] == hist[P - 1] && hist[j + 1] == pend) best = j;
+  ca[0] = pend;
+  ce[0] = pend_ok;
+  for (uint32_t t = 1; t < S; t++) {
+    int32_t v;
+    if (forced) v = P + (int32_t)t < (int32_t)cap ? hist[P + t] : -1;
+    else v = (best >= 0 && best + 1 + (int32_t)t <= P) ? hist[best + 1 + t] : -1;
+    if (v < 0 || (uint32_t)v >= V) v = -1;
+    ca[t] = v;
+    ce[t] = v >= 0 ? v : pend_ok;
+  }
+}
+
+/* accept_commit (:1152-1170): k = the longest run of drafts equal to the
+ * verify argmax of the row before them; commit them and the bonus am[k]. */
+int32_t or_spec_accept(int32_t *hist, int32_t L, const int32_t *ca, const int32_t *am, uint32_t S,
+                       uint32_t cap) {
+  const int32_t P = L - 1;
+  if (P < 0 || P + (int32_t)S >= (int32_t)cap) return L;
+  uint32_t k = 0;
+  while (k + 1 < S && ca[k + 1] >= 0 && ca[k + 1] == am[k]) k++;
+  for (uint32_t i = 0; i < k; i++) hist[P + 1 + i] = ca[1 + i];
+  hist[P + 1 + k] = am[k];
+  return P + (int32_t)k + 2;
+}
+
 /* ==== whole decode step ================================================== */
 
 static float silu(float g) { return g / (1.0f + expf(-g)); }

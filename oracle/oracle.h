@@ -70,6 +70,16 @@ float or_sample_u01(uint64_t seed, uint32_t row, int32_t L);
 void  or_sample(int32_t *tok, const float *logits, uint32_t B, uint32_t V, uint32_t nb,
                 float inv_temp, uint64_t seed, int32_t L);
 
+/* Blind speculative draft and commit over one sequence's token history
+ * hist[0..cap) with the pending id at P = L-1 (reference draft_prep and
+ * accept_commit, bench/dsv2_decode_bench.c:1116-1170; ids outside [0, V)
+ * become holes).  or_spec_accept writes the committed ids and returns the
+ * new length (L unchanged when P+S >= cap). */
+void    or_spec_draft(int32_t *ca, int32_t *ce, const int32_t *hist, int32_t L, uint32_t S,
+                      uint32_t V, uint32_t cap, int forced);
+int32_t or_spec_accept(int32_t *hist, int32_t L, const int32_t *ca, const int32_t *am, uint32_t S,
+                       uint32_t cap);
+
 /* ---- whole decode step ---- */
 typedef struct OrLayer {
   const void *wqkv; const float *sqkv;   /* [(H+2Hkv)hd, D] (GPT2: c_attn [3D, D]) */

@@ -77,6 +77,8 @@ def oracle() -> C.CDLL:
             "or_argmax": (None, [_vp, _vp, _u32, _u32]),
             "or_sexpf": (_f, [_f]), "or_sample_u01": (_f, [_u64, _u32, C.c_int32]),
             "or_sample": (None, [_vp, _vp, _u32, _u32, _u32, _f, _u64, C.c_int32]),
+            "or_spec_draft": (None, [_vp, _vp, _vp, C.c_int32, _u32, _u32, _u32, _i]),
+            "or_spec_accept": (C.c_int32, [_vp, C.c_int32, _vp, _vp, _u32, _u32]),
             "or_decode_step": (_i, [C.POINTER(OrModel), _vp, _u32, _vp, _vp]),
             "or_mla_prep": (None, [_vp, _vp, _vp, _vp, _vp, _vp, _u32, _vp, _vp, _vp, _vp,
                                    _u32, _u32, _u32, _u32, _f]),
@@ -154,6 +156,24 @@ def gemv(x: np.ndarray, xdt: int, w: np.ndarray, wdt: int, scale=None, M=None, N
     oracle().or_gemv(y.ctypes.data, x.ctypes.data, xdt, K, w.ctypes.data, wdt,
                      sc.ctypes.data if sc is not None else None, M, N, K)
     return y
+
+
+def spec_draft(hist, L, S, V, forced=False):
+    """(cand_acc, cand_emb) of or_spec_draft over one token history."""
+    h = np.ascontiguousarray(hist, np.int32)
+    ca, ce = np.empty(S, np.int32), np.empty(S, np.int32)
+    oracle().or_spec_draft(ca.ctypes.data, ce.ctypes.data, h.ctypes.data, int(L), S, V, h.size,
+                           int(forced))
+    return ca, ce
+
+
+def spec_accept(hist, L, ca, am, S):
+    """(new history, new L) of or_spec_accept."""
+    h = np.array(hist, np.int32)
+    ca = np.ascontiguousarray(ca, np.int32)
+    am = np.ascontiguousarray(am, np.int32)
+    Ln = oracle().or_spec_accept(h.ctypes.data, int(L), ca.ctypes.data, am.ctypes.data, S, h.size)
+    return h, Ln
 
 
 DT_FP8_W = 9

@@ -494,3 +494,74 @@ def test_sample_edge_cases():
         t = _sample(lg, 4, 1.0, 3, L)
         assert t[0] == 123 and t[1] % 2 == 1
     assert all(_sample(lg[2:3], 4, 1e-4, 3, L)[0] == 499 for L in range(20))
+
+
+# ---- blind speculative draft / commit (or_spec_draft, or_spec_accept) ----
+# Known answers worked by hand from the reference's statement of draft_prep
+# and accept_commit (bench/dsv2_decode_bench.c:1116-1170), and the property
+# that makes speculation exact: committing through draft / verify / accept
+# reproduces plain greedy decoding for any deterministic next-token rule.
+
+@pytest.mark.parametrize("hist,L,S,V,forced,want_ca,want_ce", [
+    # bigram (5,6) recurs at j=0; j=4 is the current bigram itself (j+1 = P)
+    ([5, 6, 7, 8, 5, 6], 6, 4, 100, False, [6, 7, 8, 5], [6, 7, 8, 5]),
+    # the most recent earlier match wins (j=3 over j=0)
+    ([1, 2, 3, 1, 2, 4, 1, 2], 8, 4, 100, False, [2, 4, 1, 2], [2, 4, 1, 2]),
+    # the continuation stops at P: later drafts are holes, embedded as the pending id
+    ([9, 9, 9], 3, 3, 100, False, [9, 9, -1], [9, 9, 9]),
+    ([1, 2, 3, 4], 4, 3, 100, False, [4, -1, -1], [4, 4, 4]),            # no match
+    ([5, 6, 70, 5, 6], 5, 3, 50, False, [6, -1, 5], [6, 6, 5]),           # id >= V: a hole
+    ([7], 1, 2, 100, False, [7, -1], [7, 7]),                             # P = 0: no bigram
+    ([1, 2, 3, 10, 11, 12, 0], 4, 3, 100, True, [10, 11, 12], [10, 11, 12]),   # forced drafts
+])
+def test_spec_draft_known_answers(hist, L, S, V, forced, want_ca, want_ce):
+    ca, ce = O.spec_draft(hist, L, S, V, forced)
+    assert ca.tolist() == want_ca and ce.tolist() == want_ce
+
+
+def test_spec_accept_known_answers():
+    h = [5, 6, 7, 8, 5, 6] + [0] * 6
+    # two drafts verified, the third rejected: commit 7, 8 and the bonus am[2]
+    h2, L2 = O.spec_accept(h, 6, [6, 7, 8, 5], [7, 8, 0, 3], 4)
+    assert L2 == 9 and h2[6:9].tolist() == [7, 8, 0] and h2[:6].tolist() == h[:6]
+    # every draft verified: S ids committed
+    h3, L3 = O.spec_accept(h, 6, [6, 1, 2, 3], [1, 2, 3, 4], 4)
+    assert L3 == 10 and h3[6:10].tolist() == [1, 2, 3, 4]
+    # a hole never matches: only the bonus
+    h4, L4 = O.spec_accept(h, 6, [6, -1, 2, 3], [-1, 2, 3, 4], 4)
+    assert L4 == 7 and h4[6] == -1
+    # no room for S rows: unchanged
+    h5, L5 = O.spec_accept(h, 9, [6, 1, 2, 3], [1, 2, 3, 4], 4)
+    assert L5 == 9 and h5.tolist() == h
+
+
+@pytest.mark.parametrize("S", [2, 3, 4])
+@pytest.mark.parametrize("rule", range(4))
+def test_spec_reproduces_greedy(S, rule):
+    rng = np.random.default_rng(rule)
+    V = 12
+    table = rng.integers(0, V, (V, V))
+    def nxt(seq):            # a deterministic "model": a function of the last two ids
+        return int(table[seq[-2] if len(seq) > 1 else 0, seq[-1]])
+    prompt = rng.integers(0, V, 5).tolist()
+    n = 60
+    greedy = list(prompt)
+    while len(greedy) < len(prompt) + n:
+        greedy.append(nxt(greedy))
+    cap = len(prompt) + n + S + 2
+    hist = np.zeros(cap, np.int32)
+    hist[:len(prompt)] = prompt
+    L, steps, advanced = len(prompt), 0, []
+    while L < len(prompt) + n:
+        ca, ce = O.spec_draft(hist, L, S, V)
+        # verify: row s continues the committed history with the embedded candidates 0..s
+        base = hist[:L - 1].tolist()
+        am = [nxt(base + ce[:s + 1].tolist()) for s in range(S)]
+        hist, L2 = O.spec_accept(hist, L, ca, am, S)
+        advanced.append(L2 - L)
+        L = L2
+        steps += 1
+    got = hist[:len(prompt) + n].tolist()
+    assert got == greedy[:len(prompt) + n]
+    assert all(1 <= a <= S for a in advanced)
+    assert steps < n     # a loop-prone rule accepts some drafts

@@ -46,7 +46,7 @@ class DecodeConfig(C.Structure):
                                   "n_shared", "top_k", "moe_inter", "first_dense", "step_mode",
                                   "moe_mode", "attn_cpb")] + [
         ("temperature", C.c_float), ("sample_seed_lo", C.c_uint32), ("sample_seed_hi", C.c_uint32),
-        ("reserved", C.c_uint32 * 2)]
+        ("spec_rows", C.c_uint32), ("spec_forced", C.c_uint32)]
 
 
 class Uop(C.Structure):
@@ -105,6 +105,8 @@ _SIGS = {
     "thvm_hip_decoder_set_state": (_i32, [_u32, _vp, _u32]),
     "thvm_hip_decoder_step": (_i32, [_u32]), "thvm_hip_decoder_capture": (_u32, [_u32]),
     "thvm_hip_decoder_replay": (_i32, [_u32, _u32]),
+    "thvm_hip_decoder_spec_step": (_i32, [_u32]), "thvm_hip_decoder_spec_capture": (_u32, [_u32]),
+    "thvm_hip_decoder_spec_replay": (_i32, [_u32, _u32]),
     "thvm_hip_decoder_read_tokens": (_i32, [_u32, _vp, _u32]),
     "thvm_hip_decoder_read_logits": (_i32, [_u32, _vp, _u64]),
     "thvm_hip_decoder_position": (_u32, [_u32]),
@@ -299,6 +301,19 @@ class Decoder:
 
     def replay(self, n: int = 1) -> None:
         _check(lib().thvm_hip_decoder_replay(self.h, n), "decoder_replay")
+
+    def spec_step(self) -> None:
+        """One eager speculative step (draft, verify, commit)."""
+        _check(lib().thvm_hip_decoder_spec_step(self.h), "decoder_spec_step")
+
+    def spec_capture(self) -> int:
+        s = lib().thvm_hip_decoder_spec_capture(self.h)
+        if s == 0:
+            raise ThvmHipError(f"decoder_spec_capture: {last_error()}")
+        return s
+
+    def spec_replay(self, n: int = 1) -> None:
+        _check(lib().thvm_hip_decoder_spec_replay(self.h, n), "decoder_spec_replay")
 
     def generate(self, prompts, max_new: int, eos: int = -1):
         """prompts [batch][n] (or [n] for every row) -> (ids [batch][max_new]

@@ -57,6 +57,14 @@ typedef struct {
   u32 jit_slot;
   u32 n_split;
   u64 weight_bytes;       /* streamed weight + scale bytes per step */
+  /* op emission: the rows of the step being built, speculative verify, and
+   * the name prefix of its activation tensors ("" for the one-row step) */
+  u32 rows;
+  int spec;
+  char pfx[4];
+  DOp *sops;              /* the speculative step (spec_rows > 0) */
+  u32 n_sops;
+  u32 spec_slot;
 } Decoder;
 
 #define MAX_DEC 8
@@ -86,6 +94,13 @@ static u32 tens_new(Decoder *d, const char *name, u32 dt, u64 nbytes) {
   t->dt = dt;
   t->nbytes = nbytes;
   return id;
+}
+
+/* a per-step activation tensor of the step being built */
+static u32 act(Decoder *d, const char *name) {
+  char nm[48];
+  snprintf(nm, sizeof nm, "%s%s", d->pfx, name);
+  return tens_find(d, nm);
 }
 
 static u64 name_tag(const char *name) { return hb_hash64(name, strlen(name), 0x7468766dull); }
@@ -210,6 +225,15 @@ static int cfg_check(const ThvmDecodeConfig *c) {
     hb_set_error("decoder: attn_cpb is 0 (auto) or 1..64 chunks per split block");
     return -1;
   }
+  if (c->spec_rows == 1 || c->spec_rows > 4 || c->spec_forced > 1) {
+    hb_set_error("decoder: spec_rows is 0 (off) or 2..4, spec_forced 0 or 1");
+    return -1;
+  }
+  if (c->spec_rows && (c->arch != THVM_ARCH_LLAMA || c->batch != 1 || c->temperature > 0.0f ||
+                       c->step_mode)) {
+    hb_set_error("decoder: speculative decode is for the LLAMA op-list step at batch 1, greedy");
+    return -1;
+  }
   if (c->moe_mode > 2) {
     hb_set_error("decoder: moe_mode is 0 (auto), 1 (VALU grouped) or 2 (MFMA grouped)");
     return -1;
@@ -282,11 +306,17 @@ static int build_llama(Decoder *d);
 static int build_gpt2(Decoder *d);
 static int build_dsv2(Decoder *d);
 
+static void ops_free(DOp *ops, u32 n) {
+  for (u32 i = 0; i < n; i++) { free(ops[i].name); free(ops[i].prog); }
+  free(ops);
+}
+
 static void dec_free(Decoder *d) {
   if (d->jit_slot) thvm_hip_jit_capture_drop(d->jit_slot);
+  if (d->spec_slot) thvm_hip_jit_capture_drop(d->spec_slot);
   for (u32 i = 0; i < d->nt; i++) thvm_hip_buf_free(d->t[i].id);
-  for (u32 i = 0; i < d->n_ops; i++) { free(d->ops[i].name); free(d->ops[i].prog); }
-  free(d->ops);
+  ops_free(d->ops, d->n_ops);
+  ops_free(d->sops, d->n_sops);
   memset(d, 0, sizeof *d);
 }
 
@@ -305,6 +335,7 @@ THVM_API uint32_t thvm_hip_decoder_create(const ThvmDecodeConfig *cfg, uint64_t 
   if (d->c.init_std == 0.0f) d->c.init_std = 0.02f;
   d->seed = seed;
   d->n_split = (d->c.max_seq + 63) / 64;
+  d->rows = d->c.batch;
   int rc = d->c.arch == THVM_ARCH_LLAMA ? build_llama(d)
          : d->c.arch == THVM_ARCH_GPT2  ? build_gpt2(d) : build_dsv2(d);
   if (rc) { dec_free(d); return 0; }
@@ -344,12 +375,18 @@ static int op_attn(Decoder *d, u32 l) {
   char p[320], kn[32], vn[32];
   snprintf(kn, sizeof kn, "l%u.kcache", l);
   snprintf(vn, sizeof vn, "l%u.vcache", l);
+  /* a verify row folds the partials as the one-row step does: same split
+   * blocks, so the one-row step's chunks per block */
+  const u32 cpb = d->spec && !c->attn_cpb
+                ? thvm_k_attn_auto_cpb(c->batch, c->n_heads, c->n_kv_heads, d->n_split, 0)
+                : c->attn_cpb;
   snprintf(p, sizeof p,
-           "thvm-builtin:attn b=%u h=%u hkv=%u hd=%u maxseq=%u chunk=64 nsplit=%u qt=%u ct=%u ot=%u scale=%a cpb=%u",
-           c->batch, c->n_heads, c->n_kv_heads, c->head_dim, c->max_seq, d->n_split, c->adtype,
-           c->adtype, c->adtype, (float)(1.0 / sqrt((double)c->head_dim)), c->attn_cpb);
-  u32 a[6] = {tens_find(d, "att"), tens_find(d, "q"), tens_find(d, kn), tens_find(d, vn),
-              tens_find(d, "len"), tens_find(d, "attn.part")};
+           "thvm-builtin:attn b=%u h=%u hkv=%u hd=%u maxseq=%u chunk=64 nsplit=%u qt=%u ct=%u ot=%u scale=%a cpb=%u%s",
+           d->rows, c->n_heads, c->n_kv_heads, c->head_dim, c->max_seq, d->n_split, c->adtype,
+           c->adtype, c->adtype, (float)(1.0 / sqrt((double)c->head_dim)), cpb,
+           d->spec ? " spec=1" : "");
+  u32 a[6] = {act(d, "att"), act(d, "q"), tens_find(d, kn), tens_find(d, vn),
+              tens_find(d, "len"), act(d, "attn.part")};
   return op_add(d, "attn", p, a, 6);
 }
 
@@ -362,13 +399,13 @@ typedef struct { int kind; u32 g, b; } NormSpec;
 
 static int fused_norms(const Decoder *d) {
   const char *e = getenv("THVM_HIP_UNFUSED_NORM");
-  return d->c.batch <= 4 && !(e && e[0] == '1');
+  return d->rows <= 4 && !(e && e[0] == '1');
 }
 
 static int emit_norm(Decoder *d, const NormSpec *ns, u32 *gin, char *nspec, size_t nlen,
                      u32 *gargs, u32 *ng) {
   const ThvmDecodeConfig *c = &d->c;
-  u32 x = tens_find(d, "x"), xn = tens_find(d, "xn");
+  u32 x = act(d, "x"), xn = act(d, "xn");
   *ng = 0;
   if (fused_norms(d)) {
     snprintf(nspec, nlen, " norm=%d eps=%a", ns->kind, c->eps);
@@ -379,7 +416,7 @@ static int emit_norm(Decoder *d, const NormSpec *ns, u32 *gin, char *nspec, size
   }
   char p[200];
   nspec[0] = 0;
-  snprintf(p, sizeof p, "thvm-builtin:norm m=%u k=%u xt=%u yt=%u eps=%a ln=%d bias=%d", c->batch,
+  snprintf(p, sizeof p, "thvm-builtin:norm m=%u k=%u xt=%u yt=%u eps=%a ln=%d bias=%d", d->rows,
            c->dim, c->adtype, c->adtype, c->eps, ns->kind == 2, ns->kind == 2);
   u32 a[4] = {xn, x, ns->g, ns->b};
   *gin = xn;
@@ -393,14 +430,23 @@ static int op_tail(Decoder *d, u32 lm_w, u32 lm_s, const NormSpec *fn) {
   if (emit_norm(d, fn, &gin, nsp, sizeof nsp, gargs, &ng)) return -1;
   /* LM head -> f32 logits */
   snprintf(p, sizeof p, "thvm-builtin:gemv m=%u n=%u k=%u wt=%u xt=%u yt=%u epi=0%s",
-           c->batch, c->vocab, c->dim, c->arch == THVM_ARCH_GPT2 ? c->adtype : c->wdtype,
+           d->rows, c->vocab, c->dim, c->arch == THVM_ARCH_GPT2 ? c->adtype : c->wdtype,
            c->adtype, THVM_DT_FP32, nsp);
   u32 a[8], n = 0;
-  a[n++] = tens_find(d, "logits"); a[n++] = gin; a[n++] = lm_w;
+  a[n++] = act(d, "logits"); a[n++] = gin; a[n++] = lm_w;
   if (lm_s) a[n++] = lm_s;
   for (u32 i = 0; i < ng; i++) a[n++] = gargs[i];
   if (op_add(d, "lm_head", p, a, n)) return -1;
   u32 nb = c->vocab >= 256 * 64 ? 256 : (c->vocab + 63) / 64;
+  if (d->spec) {   /* the verify rows' greedy ids, then the commit */
+    snprintf(p, sizeof p, "thvm-builtin:argmax b=%u v=%u nb=%u", d->rows, c->vocab, nb);
+    u32 b[4] = {act(d, "am"), act(d, "logits"), act(d, "am.pv"), act(d, "am.pi")};
+    if (op_add(d, "argmax", p, b, 4)) return -1;
+    snprintf(p, sizeof p, "thvm-builtin:spec_accept s=%u hcap=%u", d->rows, c->max_seq + 1);
+    u32 e[5] = {tens_find(d, "hist"), tens_find(d, "len"), act(d, "ca"), act(d, "am"),
+                tens_find(d, "tok")};
+    return op_add(d, "spec_accept", p, e, 5);
+  }
   char sk[96];
   snprintf(p, sizeof p, "thvm-builtin:argmax b=%u v=%u nb=%u hist=1 hstride=%u%s", c->batch,
            c->vocab, nb, c->max_seq + 1, sample_keys(c, sk, sizeof sk));
@@ -486,51 +532,45 @@ static int step_status(Decoder *d) {
   return rc;
 }
 
-static int build_llama(Decoder *d) {
+/* The LLAMA step's op list over the weights build_llama made, for d->rows
+ * rows: the one-row (batch) step, or the speculative step (d->spec: draft,
+ * S verify rows of one sequence, commit). */
+static int llama_ops(Decoder *d) {
   const ThvmDecodeConfig *c = &d->c;
   u32 D = c->dim, H = c->n_heads, Hkv = c->n_kv_heads, hd = c->head_dim, F = c->ffn;
-  u32 adt = c->adtype, B = c->batch;
+  u32 adt = c->adtype, B = d->rows;
   u32 nqkv = (H + 2 * Hkv) * hd;
-  if (build_state(d)) return -1;
-  if (!weight_normal(d, "emb", adt, (u64)c->vocab * D, 0.0f, c->init_std)) return -1;
-  if (rope_tables(d)) return -1;
-  if (!weight_const(d, "norm_f", D, 1.0f)) return -1;
+  const int f8 = c->wdtype == THVM_DT_FP8E4M3;
   char p[400], nm[48];
-  u32 x = tens_find(d, "x"), q = tens_find(d, "q"),
-      att = tens_find(d, "att"), hb = tens_find(d, "h"), L = tens_find(d, "len");
+  u32 x = act(d, "x"), q = act(d, "q"), att = act(d, "att"), hb = act(d, "h"),
+      L = tens_find(d, "len");
 
+  if (d->spec) {
+    snprintf(p, sizeof p, "thvm-builtin:spec_draft s=%u v=%u hcap=%u forced=%u", B, c->vocab,
+             c->max_seq + 1, c->spec_forced);
+    u32 da[4] = {act(d, "ca"), act(d, "ce"), tens_find(d, "hist"), L};
+    if (op_add(d, "spec_draft", p, da, 4)) return -1;
+  }
   snprintf(p, sizeof p, "thvm-builtin:embed b=%u d=%u v=%u et=%u xt=%u", B, D, c->vocab, adt, adt);
-  u32 ea[3] = {x, tens_find(d, "emb"), tens_find(d, "tok")};
+  u32 ea[3] = {x, tens_find(d, "emb"), d->spec ? act(d, "ce") : tens_find(d, "tok")};
   if (op_add(d, "embed", p, ea, 3)) return -1;
 
   for (u32 l = 0; l < c->n_layers; l++) {
-    u32 wqkv, sqkv, wo, so, wgu, sgu, wd, sd;
-    snprintf(nm, sizeof nm, "l%u.wqkv", l);
-    if (weight_matrix(d, nm, nqkv, D, &wqkv, &sqkv)) return -1;
-    snprintf(nm, sizeof nm, "l%u.wo", l);
-    if (weight_matrix(d, nm, D, H * hd, &wo, &so)) return -1;
-    snprintf(nm, sizeof nm, "l%u.wgu", l);
-    if (weight_matrix(d, nm, 2 * F, D, &wgu, &sgu)) return -1;
-    snprintf(nm, sizeof nm, "l%u.wd", l);
-    if (weight_matrix(d, nm, D, F, &wd, &sd)) return -1;
-    snprintf(nm, sizeof nm, "l%u.g_attn", l);
-    u32 ga = weight_const(d, nm, D, 1.0f);
-    snprintf(nm, sizeof nm, "l%u.g_ffn", l);
-    u32 gf = weight_const(d, nm, D, 1.0f);
-    if (!ga || !gf) return -1;
-    char kn[32], vn[32];
-    snprintf(kn, sizeof kn, "l%u.kcache", l);
-    snprintf(vn, sizeof vn, "l%u.vcache", l);
-    u32 kc = tens_find(d, kn), vc = tens_find(d, vn);
-    int f8 = c->wdtype == THVM_DT_FP8E4M3;
+#define LT(fmt) (snprintf(nm, sizeof nm, fmt, l), tens_find(d, nm))
+    const u32 wqkv = LT("l%u.wqkv"), wo = LT("l%u.wo"), wgu = LT("l%u.wgu"), wd = LT("l%u.wd");
+    const u32 sqkv = f8 ? LT("l%u.wqkv.scale") : 0, so = f8 ? LT("l%u.wo.scale") : 0,
+              sgu = f8 ? LT("l%u.wgu.scale") : 0, sd = f8 ? LT("l%u.wd.scale") : 0;
+    const u32 ga = LT("l%u.g_attn"), gf = LT("l%u.g_ffn"), kc = LT("l%u.kcache"), vc = LT("l%u.vcache");
+#undef LT
 
     char nsp[96];
     u32 gin, gargs[2], ng;
     NormSpec n1 = {1, ga, 0};
     if (emit_norm(d, &n1, &gin, nsp, sizeof nsp, gargs, &ng)) return -1;
     snprintf(p, sizeof p,
-             "thvm-builtin:gemv m=%u n=%u k=%u wt=%u xt=%u yt=%u epi=%u h=%u hkv=%u hd=%u maxseq=%u%s",
-             B, nqkv, D, c->wdtype, adt, adt, THVM_EPI_QKV_ROPE, H, Hkv, hd, c->max_seq, nsp);
+             "thvm-builtin:gemv m=%u n=%u k=%u wt=%u xt=%u yt=%u epi=%u h=%u hkv=%u hd=%u maxseq=%u%s%s",
+             B, nqkv, D, c->wdtype, adt, adt, THVM_EPI_QKV_ROPE, H, Hkv, hd, c->max_seq, nsp,
+             d->spec ? " spec=1" : "");
     u32 qa[12], qn = 0;
     qa[qn++] = q; qa[qn++] = gin; qa[qn++] = wqkv;
     if (f8) qa[qn++] = sqkv;
@@ -567,10 +607,75 @@ static int build_llama(Decoder *d) {
     da[dn++] = x;
     if (op_add(d, "gemv_down", p, da, dn)) return -1;
   }
+  NormSpec nf = {1, tens_find(d, "norm_f"), 0};
+  return op_tail(d, tens_find(d, "lm"), f8 ? tens_find(d, "lm.scale") : 0, &nf);
+}
+
+/* The speculative step (reference step_build_spec, bench/dsv2_decode_bench.c:
+ * 2419-2620): its own S-row activations ("s." tensors), the one-row step's
+ * weights, caches, token history and length; built as a second op list. */
+static int build_llama_spec(Decoder *d) {
+  const ThvmDecodeConfig *c = &d->c;
+  const u32 S = c->spec_rows, adt = c->adtype, as = hb_dt_size(adt);
+  const u32 hq = c->n_heads * c->head_dim;
+  if (!tens_new(d, "s.x", adt, (u64)S * c->dim * as) || !tens_new(d, "s.xn", adt, (u64)S * c->dim * as) ||
+      !tens_new(d, "s.q", adt, (u64)S * hq * as) || !tens_new(d, "s.att", adt, (u64)S * hq * as) ||
+      !tens_new(d, "s.h", adt, (u64)S * c->ffn * as) ||
+      !tens_new(d, "s.logits", THVM_DT_FP32, (u64)S * c->vocab * 4) ||
+      !tens_new(d, "s.am.pv", THVM_DT_FP32, (u64)S * 256 * 4) ||
+      !tens_new(d, "s.am.pi", THVM_DT_INT32, (u64)S * 256 * 4) ||
+      !tens_new(d, "s.am", THVM_DT_INT32, (u64)S * 4) || !tens_new(d, "s.ca", THVM_DT_INT32, (u64)S * 4) ||
+      !tens_new(d, "s.ce", THVM_DT_INT32, (u64)S * 4) ||
+      !tens_new(d, "s.attn.part", THVM_DT_FP32,
+                thvm_k_attn_part_bytes(S, c->n_heads, c->n_kv_heads, c->head_dim, d->n_split)))
+    return -1;
+  DOp *ops = d->ops;
+  const u32 n = d->n_ops, cap = d->cap_ops;
+  d->ops = NULL;
+  d->n_ops = d->cap_ops = 0;
+  d->rows = S;
+  d->spec = 1;
+  snprintf(d->pfx, sizeof d->pfx, "s.");
+  const int rc = llama_ops(d);
+  d->sops = d->ops;
+  d->n_sops = d->n_ops;
+  d->ops = ops;
+  d->n_ops = n;
+  d->cap_ops = cap;
+  d->rows = c->batch;
+  d->spec = 0;
+  d->pfx[0] = 0;
+  return rc;
+}
+
+static int build_llama(Decoder *d) {
+  const ThvmDecodeConfig *c = &d->c;
+  u32 D = c->dim, H = c->n_heads, Hkv = c->n_kv_heads, hd = c->head_dim, F = c->ffn;
+  u32 nqkv = (H + 2 * Hkv) * hd;
+  if (build_state(d)) return -1;
+  if (!weight_normal(d, "emb", c->adtype, (u64)c->vocab * D, 0.0f, c->init_std)) return -1;
+  if (rope_tables(d)) return -1;
+  if (!weight_const(d, "norm_f", D, 1.0f)) return -1;
+  char nm[48];
+  for (u32 l = 0; l < c->n_layers; l++) {
+    u32 w, sc;
+    snprintf(nm, sizeof nm, "l%u.wqkv", l);
+    if (weight_matrix(d, nm, nqkv, D, &w, &sc)) return -1;
+    snprintf(nm, sizeof nm, "l%u.wo", l);
+    if (weight_matrix(d, nm, D, H * hd, &w, &sc)) return -1;
+    snprintf(nm, sizeof nm, "l%u.wgu", l);
+    if (weight_matrix(d, nm, 2 * F, D, &w, &sc)) return -1;
+    snprintf(nm, sizeof nm, "l%u.wd", l);
+    if (weight_matrix(d, nm, D, F, &w, &sc)) return -1;
+    snprintf(nm, sizeof nm, "l%u.g_attn", l);
+    if (!weight_const(d, nm, D, 1.0f)) return -1;
+    snprintf(nm, sizeof nm, "l%u.g_ffn", l);
+    if (!weight_const(d, nm, D, 1.0f)) return -1;
+  }
   u32 lw, ls;
   if (weight_matrix(d, "lm", c->vocab, D, &lw, &ls)) return -1;
-  NormSpec nf = {1, tens_find(d, "norm_f"), 0};
-  if (op_tail(d, lw, ls, &nf)) return -1;
+  if (llama_ops(d)) return -1;
+  if (c->spec_rows && build_llama_spec(d)) return -1;
   return c->step_mode ? build_llama_step(d) : 0;
 }
 
@@ -984,14 +1089,8 @@ THVM_API int thvm_hip_decoder_prefill_synthetic(uint32_t h, uint32_t ctx, uint64
   return thvm_hip_buf_write(tens_find(d, "len"), &L, 4);
 }
 
-static int dec_run_ops(Decoder *d) {
-  for (u32 i = 0; i < d->n_ops; i++) {
-    DOp *o = &d->ops[i];
-    if (thvm_hip_dispatch_custom(o->name, o->prog, NULL, NULL, 0, o->args, o->n_args, o->outs))
-      return -1;
-  }
-  return 0;
-}
+static int run_list(const DOp *ops, u32 n);
+static int dec_run_ops(Decoder *d) { return run_list(d->ops, d->n_ops); }
 
 int hb_decoder_dims(u32 h, u32 *batch, u32 *max_seq, u32 *vocab) {
   Decoder *d = dec_get(h);
@@ -1033,6 +1132,62 @@ THVM_API int thvm_hip_decoder_replay(uint32_t h, uint32_t n) {
   for (u32 i = 0; i < n; i++)
     if (thvm_hip_jit_replay(d->jit_slot)) return -1;
   return 0;
+}
+
+static int run_list(const DOp *ops, u32 n) {
+  for (u32 i = 0; i < n; i++) {
+    const DOp *o = &ops[i];
+    if (thvm_hip_dispatch_custom(o->name, o->prog, NULL, NULL, 0, o->args, o->n_args, o->outs))
+      return -1;
+  }
+  return 0;
+}
+
+static Decoder *spec_get(uint32_t h, const char *who) {
+  Decoder *d = dec_get(h);
+  if (d && !d->n_sops) {
+    hb_set_error("%s: decoder %u has no speculative step (spec_rows 0)", who, h);
+    return NULL;
+  }
+  return d;
+}
+
+THVM_API int thvm_hip_decoder_spec_step(uint32_t h) {
+  Decoder *d = spec_get(h, "decoder_spec_step");
+  if (!d) return -1;
+  if (thvm_hip_jit_is_capturing()) { hb_set_error("decoder_spec_step: a JIT capture is open"); return -1; }
+  return run_list(d->sops, d->n_sops);
+}
+
+THVM_API uint32_t thvm_hip_decoder_spec_capture(uint32_t h) {
+  Decoder *d = spec_get(h, "decoder_spec_capture");
+  if (!d) return 0;
+  if (d->spec_slot) { thvm_hip_jit_capture_drop(d->spec_slot); d->spec_slot = 0; }
+  u32 slot = thvm_hip_jit_capture_begin();
+  if (!slot) return 0;
+  int rc = run_list(d->sops, d->n_sops);
+  thvm_hip_jit_capture_end();
+  if (rc) { thvm_hip_jit_capture_drop(slot); return 0; }
+  d->spec_slot = slot;
+  return slot;
+}
+
+THVM_API int thvm_hip_decoder_spec_replay(uint32_t h, uint32_t n) {
+  Decoder *d = spec_get(h, "decoder_spec_replay");
+  if (!d) return -1;
+  if (!d->spec_slot) { hb_set_error("decoder_spec_replay: no captured speculative step"); return -1; }
+  for (u32 i = 0; i < n; i++)
+    if (thvm_hip_jit_replay(d->spec_slot)) return -1;
+  return 0;
+}
+
+u32 hb_decoder_spec_rows(u32 h) {
+  Decoder *d = dec_get(h);
+  return d && d->n_sops ? d->c.spec_rows : 0;
+}
+u32 hb_decoder_spec_slot(u32 h) {
+  Decoder *d = dec_get(h);
+  return d ? d->spec_slot : 0;
 }
 
 THVM_API int thvm_hip_decoder_read_tokens(uint32_t h, int32_t *dst, uint32_t n) {

@@ -152,12 +152,13 @@ static int attn_parse(const Spec *sp, ArgCtx *c, ThvmAttnArgs *a, int with_part)
       spec_u32(sp, "maxseq", &a->max_seq, 1, 0) || spec_u32(sp, "chunk", &a->chunk, 0, 64) ||
       spec_u32(sp, "qt", &a->qdt, 0, THVM_DT_BF16) || spec_u32(sp, "ct", &a->cdt, 0, THVM_DT_BF16) ||
       spec_u32(sp, "ot", &a->odt, 0, THVM_DT_BF16) || spec_f32(sp, "scale", &a->scale, 1, 0) ||
-      spec_u32(sp, "fused", &a->fused, 0, 0) || spec_u32(sp, "cpb", &a->cpb, 0, 0))
+      spec_u32(sp, "fused", &a->fused, 0, 0) || spec_u32(sp, "cpb", &a->cpb, 0, 0) ||
+      spec_u32(sp, "spec", &a->spec, 0, 0))
     return -1;
   if (a->chunk == 0) { hb_set_error("builtin attn: chunk=0"); return -1; }
   if (spec_u32(sp, "nsplit", &a->n_split, 0, (a->max_seq + a->chunk - 1) / a->chunk)) return -1;
   if (!is_act(a->qdt) || !is_act(a->odt)) { hb_set_error("builtin attn: bad dtypes"); return -1; }
-  u64 cb = (u64)a->B * a->Hkv * a->max_seq * a->hd * hb_dt_size(a->cdt);
+  u64 cb = (u64)(a->spec ? 1 : a->B) * a->Hkv * a->max_seq * a->hd * hb_dt_size(a->cdt);
   a->out = arg(c, 0, (u64)a->B * a->H * a->hd * hb_dt_size(a->odt));
   a->q = arg(c, 1, (u64)a->B * a->H * a->hd * hb_dt_size(a->qdt));
   a->kcache = arg(c, 2, cb);
@@ -195,7 +196,7 @@ int hb_builtin_launch(const char *program, const u32 *ids, u32 n, int check_only
          spec_u32(&sp, "ngain", &ngain, 0, 1) || spec_u32(&sp, "nbias", &nbias, 0, a.norm == 2) ||
          spec_u32(&sp, "waves", &a.tune_waves, 0, 0) || spec_u32(&sp, "r", &a.tune_r, 0, 0) ||
          spec_u32(&sp, "u", &a.tune_u, 0, 0) || spec_u32(&sp, "blocks", &a.tune_blocks, 0, 0) ||
-         spec_u32(&sp, "path", &a.tune_path, 0, 0));
+         spec_u32(&sp, "path", &a.tune_path, 0, 0) || spec_u32(&sp, "spec", &a.spec, 0, 0));
     {
       u32 ldy0 = a.epi == THVM_EPI_SWIGLU ? a.N / 2
                : (a.epi == THVM_EPI_QKV || a.epi == THVM_EPI_QKV_ROPE) ? a.n_heads * a.head_dim
@@ -225,7 +226,7 @@ int hb_builtin_launch(const char *program, const u32 *ids, u32 n, int check_only
       a.rope_sin = (const float *)arg(&c, slot++, (u64)a.max_seq * (a.head_dim / 2) * 4);
     }
     if (qkv) {
-      u64 cb = (u64)a.M * a.n_kv_heads * a.max_seq * a.head_dim * ysz;
+      u64 cb = (u64)(a.spec ? 1 : a.M) * a.n_kv_heads * a.max_seq * a.head_dim * ysz;
       a.len = (const int32_t *)arg(&c, slot++, 4);
       a.kcache = arg(&c, slot++, cb);
       a.vcache = arg(&c, slot++, cb);
@@ -454,6 +455,31 @@ int hb_builtin_launch(const char *program, const u32 *ids, u32 n, int check_only
     if (check_only) return 0;
     if (prof) hb_kprof_begin(K, &e0, &e1);
     rc = thvm_k_quant_fp8_rows(q, scale, x, xdt, rows, cols, HB_STREAM, err, sizeof err);
+  } else if (strcmp(K, "spec_draft") == 0) {   /* cand_acc, cand_emb, hist, len */
+    u32 S = 0, V = 0, hcap = 0, forced = 0;
+    NEED(spec_u32(&sp, "s", &S, 1, 0) || spec_u32(&sp, "v", &V, 1, 0) ||
+         spec_u32(&sp, "hcap", &hcap, 1, 0) || spec_u32(&sp, "forced", &forced, 0, 0));
+    int32_t *ca = (int32_t *)arg(&c, 0, (u64)S * 4), *ce = (int32_t *)arg(&c, 1, (u64)S * 4);
+    const int32_t *hist = (const int32_t *)arg(&c, 2, (u64)hcap * 4);
+    const int32_t *L = (const int32_t *)arg(&c, 3, 4);
+    if (c.bad) return -1;
+    bytes = (u64)hcap * 4;
+    if (check_only) return 0;
+    if (prof) hb_kprof_begin(K, &e0, &e1);
+    rc = thvm_k_spec_draft(ca, ce, hist, L, S, V, hcap, forced, HB_STREAM, err, sizeof err);
+  } else if (strcmp(K, "spec_accept") == 0) {  /* hist, len, cand_acc, am [, tok] */
+    u32 S = 0, hcap = 0;
+    NEED(spec_u32(&sp, "s", &S, 1, 0) || spec_u32(&sp, "hcap", &hcap, 1, 0));
+    int32_t *hist = (int32_t *)arg(&c, 0, (u64)hcap * 4);
+    int32_t *L = (int32_t *)arg(&c, 1, 4);
+    const int32_t *ca = (const int32_t *)arg(&c, 2, (u64)S * 4);
+    const int32_t *am = (const int32_t *)arg(&c, 3, (u64)S * 4);
+    int32_t *tok = n > 4 ? (int32_t *)arg(&c, 4, 4) : NULL;
+    if (c.bad) return -1;
+    bytes = (u64)S * 12;
+    if (check_only) return 0;
+    if (prof) hb_kprof_begin(K, &e0, &e1);
+    rc = thvm_k_spec_accept(hist, L, tok, ca, am, S, hcap, HB_STREAM, err, sizeof err);
   } else if (strcmp(K, "len_bump") == 0) {
     u32 d = 1;
     NEED(spec_u32(&sp, "delta", &d, 0, 1));

@@ -52,6 +52,8 @@ void hb_decoder_reset(void);
 void hb_loader_reset(void);
 int  hb_decoder_dims(u32 h, u32 *batch, u32 *max_seq, u32 *vocab);   /* -1: no such decoder */
 u32  hb_decoder_slot(u32 h);                                          /* its JIT slot, 0 = none */
+u32  hb_decoder_spec_rows(u32 h);                                     /* S of its speculative step, 0 = none */
+u32  hb_decoder_spec_slot(u32 h);                                     /* that step's JIT slot, 0 = none */
 
 /* kernel profiling hooks (builtin dispatches only, never under capture) */
 int  hb_kprof_on(void);

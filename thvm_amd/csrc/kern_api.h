@@ -61,6 +61,10 @@ typedef struct ThvmGemvArgs {
    * 16-row weight tiles per block), chunks per lane in flight, grid blocks,
    * path (1 GEMV, 2 MFMA GEMM; 0 picks the MFMA GEMM for M > 4) */
   uint32_t tune_waves, tune_r, tune_u, tune_blocks, tune_path;
+  /* speculative verify (the QKV epilogues): the M rows are consecutive
+   * positions of ONE sequence -- row m rotates at and appends to position
+   * L-1+m of cache row 0 -- instead of M independent sequences */
+  uint32_t spec;
 } ThvmGemvArgs;
 /* y = epi(x . W^T): the GEMV for M <= 4, the MFMA GEMM for M <= 64 (fp16 W
  * with fp16 x, bf16 W with bf16 x, fp8 W with bf16/fp16 x; K % 64 == 0; no
@@ -106,8 +110,13 @@ typedef struct ThvmAttnArgs {
                             * count, 1 one chunk per block, 2 or 4 a block
                             * runs that many consecutive chunks (two
                             * launches only); the partials are per block   */
+  uint32_t spec;           /* speculative verify: the B query rows are
+                            * consecutive positions of one sequence; row b
+                            * reads cache row 0 over L+b rows (causal)     */
 } ThvmAttnArgs;
 int thvm_k_attn_decode(const ThvmAttnArgs *a, hipStream_t s, char *err, int errlen);
+/* the chunks per split block thvm_k_attn_decode picks for cpb = 0 */
+uint32_t thvm_k_attn_auto_cpb(uint32_t B, uint32_t H, uint32_t Hkv, uint32_t n_split, uint32_t fused);
 uint64_t thvm_k_attn_part_bytes(uint32_t B, uint32_t H, uint32_t Hkv, uint32_t hd, uint32_t n_split);
 /* The same attention with a->part ignored: partials and merge counters in a
  * static device array of THVM_ATTN_SCRATCH_BYTES per GPU (no allocation).
@@ -222,6 +231,24 @@ int thvm_k_argmax(const ThvmArgmaxArgs *a, hipStream_t s, char *err, int errlen)
 /* One wave sleeping n fixed periods (~3.4 us each): lets a host enqueue work
  * behind it so back-to-back kernels can be timed without host gaps. */
 int thvm_k_delay(uint32_t n, hipStream_t s, char *err, int errlen);
+
+/* Blind speculative decode (reference draft_prep / accept_commit,
+ * bench/dsv2_decode_bench.c:1110-1170).  The token history hist[0..hist_cap)
+ * of one sequence holds the committed ids and, at P = L-1, the pending one.
+ * draft: cand_acc[0] = cand_emb[0] = hist[P]; with j the largest index with
+ * j+1 < P where (hist[j], hist[j+1]) == (hist[P-1], hist[P]), cand_acc[1+t] =
+ * hist[j+2+t] while j+2+t <= P, else -1 (a hole); forced = 1 takes
+ * cand_acc[1+t] = hist[P+1+t] (ids seeded there by the host) instead.  Ids
+ * outside [0, V) are holes; cand_emb = cand_acc with holes replaced by hist[P].
+ * accept: k = the longest prefix with cand_acc[i+1] == am[i] (i < S-1);
+ * hist[P+1..P+k] = cand_acc[1..k], hist[P+1+k] = am[k], tok[0] = am[k] (when
+ * tok is given), L = P+k+2.  A state with P+S >= hist_cap is left unchanged. */
+int thvm_k_spec_draft(int32_t *cand_acc, int32_t *cand_emb, const int32_t *hist, const int32_t *len,
+                      uint32_t S, uint32_t V, uint32_t hist_cap, uint32_t forced, hipStream_t s,
+                      char *err, int errlen);
+int thvm_k_spec_accept(int32_t *hist, int32_t *len, int32_t *tok, const int32_t *cand_acc,
+                       const int32_t *am, uint32_t S, uint32_t hist_cap, hipStream_t s, char *err,
+                       int errlen);
 
 /* L[0] += delta (reference len_bump, bench/dsv2_decode_bench.c:1024-1041). */
 int thvm_k_len_bump(int32_t *len, int32_t delta, hipStream_t s, char *err, int errlen);

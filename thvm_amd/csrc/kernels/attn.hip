@@ -27,7 +27,7 @@ template <int HD, int G, int AT>
 __global__ __launch_bounds__(ATT_THREADS) void k_attn(ThvmAttnArgs a) {
   __shared__ AttnLds<HD, G> s;
   const uint32_t kvh = blockIdx.x, split = blockIdx.y, b = blockIdx.z;
-  const int32_t L = a.len[0];
+  const int32_t L = attn_row_len(a, b);
   if ((int32_t)(split * ATT_CHUNK) >= L) return;   // the merge reads only live splits
   const int wv = threadIdx.x >> 6;
   AttnSplit<HD, G, AT, false> u;
@@ -38,7 +38,7 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attn(ThvmAttnArgs a) {
 template <int HD, int AT>
 __global__ __launch_bounds__(256) void k_attn_merge(ThvmAttnArgs a) {
   __shared__ MergeLds s;
-  attn_merge<HD, AT, false>(a, blockIdx.x, threadIdx.x, a.len[0], true, s);
+  attn_merge<HD, AT, false>(a, blockIdx.x, threadIdx.x, attn_row_len(a, blockIdx.x / a.H), true, s);
 }
 
 // Split and merge in one launch: each split unit publishes its partial with
@@ -54,7 +54,7 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attn_fused(ThvmAttnArgs a) {
   __shared__ MergeLds ms[2];
   __shared__ uint32_t last;
   const uint32_t kvh = blockIdx.x, split = blockIdx.y, b = blockIdx.z;
-  const int32_t L = a.len[0];
+  const int32_t L = attn_row_len(a, b);
   if ((int32_t)(split * ATT_CHUNK) >= L) return;   // dead splits are not counted
   uint32_t n_live = (uint32_t)((L + ATT_CHUNK - 1) / ATT_CHUNK);
   if (n_live > a.n_split) n_live = a.n_split;
@@ -97,7 +97,7 @@ __global__ __launch_bounds__(ATT_THREADS, 4) void k_attn_multi(ThvmAttnArgs a) {
   typedef AttnSplit<HD, G, AT, false> SU;
   constexpr int EPL = SU::EPL, LPR = SU::LPR, RPW = SU::RPW, PPW = SU::PPW, IT = SU::IT, ES = SU::ES;
   const uint32_t kvh = blockIdx.x, grp = blockIdx.y, b = blockIdx.z;
-  const int32_t L = a.len[0];
+  const int32_t L = attn_row_len(a, b);
   const uint32_t cpb = a.cpb, c0 = grp * cpb;
   if ((int32_t)(c0 * ATT_CHUNK) >= L) return;      // the merge reads only live partials
   const int tid = threadIdx.x, wv = tid >> 6, lane = lane_id();
@@ -106,7 +106,7 @@ __global__ __launch_bounds__(ATT_THREADS, 4) void k_attn_multi(ThvmAttnArgs a) {
   // this (row, kv head)'s cache rows as buffer resources: rows past L read
   // zero through an out-of-range offset, with no memory access, so the loads
   // of a chunk past the block's last are issued unconditionally
-  const uint64_t cbase = ((uint64_t)b * a.Hkv + kvh) * a.max_seq * HD * ES;
+  const uint64_t cbase = ((uint64_t)attn_cache_row(a, b) * a.Hkv + kvh) * a.max_seq * HD * ES;
   const buf_t krs = buf_rsrc((const char *)a.kcache + cbase, a.max_seq * HD * ES);
   const buf_t vrs = buf_rsrc((const char *)a.vcache + cbase, a.max_seq * HD * ES);
   uint4 kq[2][IT], vq[2][IT];
@@ -276,6 +276,28 @@ extern "C" uint64_t thvm_k_attn_part_bytes(uint32_t B, uint32_t H, uint32_t Hkv,
   return (uint64_t)B * H * n_split * (hd + 2) * 4 + (uint64_t)B * Hkv * 4;
 }
 
+// chunks per split block for cpb = 0: one at small unit counts (every CU
+// needs a block); at batched shapes 2 or more, so each block's fixed work is
+// shared by more cache rows.  (Measured on gfx950 at the C4 shapes: two
+// chunks per block beat one at every unit count -- 11.3 against 12.9 us per
+// launch at batch 1, where the merge also reads half the partials.  Above
+// 1024 units the chunk count keeps the grid within one round of 2 blocks per
+// CU, so no tail round of a few blocks is left: 9 chunks at C4 batch 16.
+// With at most 4 chunks per head and a grid of at most one such round, the
+// merge has little to save and one chunk per block runs the chunks side by
+// side: C3 batch 1 (4 chunks, 100 units) 1.818 -> 1.785 ms per step.)  A
+// speculative verify passes its base step's value explicitly, so that its
+// rows fold the same partials in the same order as the base step.
+extern "C" uint32_t thvm_k_attn_auto_cpb(uint32_t B, uint32_t H, uint32_t Hkv, uint32_t n_split,
+                                         uint32_t fused) {
+  if (Hkv == 0 || n_split == 0) return 1;
+  const uint64_t units = (uint64_t)B * Hkv * n_split;
+  const uint32_t bh = B * Hkv, groups = bh >= 512 ? 1u : 512u / bh;   // split blocks per (row, kv head)
+  uint32_t cpb = (fused || H / Hkv > 4 || (n_split <= 4 && units <= 512)) ? 1
+               : units > 1024 ? (n_split + groups - 1) / groups : 2;
+  return cpb > n_split ? n_split : cpb;
+}
+
 extern "C" int thvm_k_attn_decode(const ThvmAttnArgs *a, hipStream_t s, char *err, int errlen) {
   if (a->H == 0 || a->Hkv == 0 || a->H % a->Hkv || a->B == 0 || a->max_seq == 0) {
     snprintf(err, errlen, "attn: bad head geometry H=%u Hkv=%u", a->H, a->Hkv);
@@ -299,30 +321,13 @@ extern "C" int thvm_k_attn_decode(const ThvmAttnArgs *a, hipStream_t s, char *er
   // block per kv head then runs all of its heads' merges, where the merge
   // kernel spreads one head per block.
   const bool fused = a->fused != 0;
-  // chunks per split block: one at small unit counts (every CU needs a
-  // block); at batched shapes 2 or 4, so each block's fixed work is shared
-  // by more cache rows
   uint32_t cpb = a->cpb;
   if (cpb > a->n_split) cpb = a->n_split;          // one block takes every chunk
   if (fused && cpb > 1) {
     snprintf(err, errlen, "attn: the one-launch form runs one chunk per block");
     return -1;
   }
-  if (cpb == 0) {
-    const uint64_t units = (uint64_t)a->B * a->Hkv * a->n_split;
-    // (measured on gfx950 at the C4 shapes: two chunks per block beat one
-    // at every unit count -- 11.3 against 12.9 us per launch at batch 1,
-    // where the merge also reads half the partials.  Above 1024 units the
-    // chunk count keeps the grid within one round of 2 blocks per CU, so
-    // no tail round of a few blocks is left: 9 chunks at C4 batch 16.  With
-    // at most 4 chunks per head and a grid of at most one such round, the
-    // merge has little to save and one chunk per block runs the chunks side
-    // by side: C3 batch 1 (4 chunks, 100 units) 1.818 -> 1.785 ms per step)
-    const uint32_t bh = a->B * a->Hkv, groups = bh >= 512 ? 1u : 512u / bh;   // split blocks per (row, kv head)
-    cpb = (fused || a->H / a->Hkv > 4 || (a->n_split <= 4 && units <= 512)) ? 1
-        : units > 1024 ? (a->n_split + groups - 1) / groups : 2;
-    if (cpb > a->n_split) cpb = a->n_split;
-  }
+  if (cpb == 0) cpb = thvm_k_attn_auto_cpb(a->B, a->H, a->Hkv, a->n_split, fused);
   attn_fn f = nullptr, fm = nullptr;
   const uint32_t G = a->H / a->Hkv;
   const int at = a->cdt == THVM_DT_BF16 ? AT_BF16 : a->cdt == THVM_DT_FP16 ? AT_F16 : AT_F32;

@@ -87,6 +87,17 @@ __device__ __forceinline__ float group_sum(float v) {
 
 __device__ __forceinline__ float fexp2(float x) { return exp2f(x); }
 
+// Query row b's cache length and cache row.  Plain decode: L = len[0] over
+// cache row b.  Speculative verify (a.spec): the B query rows are the
+// consecutive positions L-1 .. L-1+B-1 of one sequence, so row b attends
+// causally over the L+b rows of cache row 0.
+__device__ __forceinline__ int32_t attn_row_len(const ThvmAttnArgs &a, uint32_t b) {
+  return a.len[0] + (a.spec ? (int32_t)b : 0);
+}
+__device__ __forceinline__ uint32_t attn_cache_row(const ThvmAttnArgs &a, uint32_t b) {
+  return a.spec ? 0u : b;
+}
+
 // LDS of one split unit
 template <int HD, int G>
 struct AttnLds {
@@ -118,7 +129,7 @@ struct AttnSplit {
 
   __device__ __forceinline__ uint64_t row_off(const ThvmAttnArgs &a, uint32_t b, uint32_t kvh,
                                               uint32_t j) const {
-    const uint64_t cbase = ((uint64_t)b * a.Hkv + kvh) * a.max_seq;
+    const uint64_t cbase = ((uint64_t)attn_cache_row(a, b) * a.Hkv + kvh) * a.max_seq;
     return ((cbase + j) * HD + (lane_id() % LPR) * EPL) * ES;
   }
   // Issue every K / V load of wave wv (0..7) of the unit (kvh, split, b).

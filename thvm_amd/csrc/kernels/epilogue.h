@@ -123,13 +123,16 @@ __device__ __forceinline__ void gemv_epilogue(const ThvmGemvArgs &a, const uint3
         const uint32_t nn = n0 + r;
         if (nn + 1 >= N) break;
         const uint32_t d = nn % hd;
-        float c = 1.0f, sn = 0.0f;
-        if (rope && nn < Hq + Hk) {
-          c = a.rope_cos[(uint64_t)pos * (hd / 2) + d / 2];
-          sn = a.rope_sin[(uint64_t)pos * (hd / 2) + d / 2];
-        }
 #pragma unroll
         for (int m = 0; m < M; m++) {
+          // speculative verify: row m is position pos + m of sequence 0
+          const uint32_t pm = (uint32_t)pos + (a.spec ? mb + m : 0u);
+          if (pm >= a.max_seq) continue;
+          float c = 1.0f, sn = 0.0f;
+          if (rope && nn < Hq + Hk) {
+            c = a.rope_cos[(uint64_t)pm * (hd / 2) + d / 2];
+            sn = a.rope_sin[(uint64_t)pm * (hd / 2) + d / 2];
+          }
           float xe = rnd_any(v[r][m], ydt), xo = rnd_any(v[r + 1][m], ydt);
           float oe = xe, oo = xo;
           if (rope && nn < Hq + Hk) { oe = xe * c - xo * sn; oo = xo * c + xe * sn; }
@@ -140,7 +143,8 @@ __device__ __forceinline__ void gemv_epilogue(const ThvmGemvArgs &a, const uint3
             const bool isk = nn < Hq + Hk;
             const uint32_t off = isk ? nn - Hq : nn - Hq - Hk;
             const uint32_t h = off / hd;
-            uint64_t ci = (((uint64_t)(mb + m) * a.n_kv_heads + h) * a.max_seq + (uint32_t)pos) * hd + d;
+            const uint64_t cb = a.spec ? 0u : (uint64_t)(mb + m);
+            uint64_t ci = ((cb * a.n_kv_heads + h) * a.max_seq + pm) * hd + d;
             void *cache = isk ? a.kcache : a.vcache;
             st_anyc<COH>(cache, ci, ydt, oe);
             st_anyc<COH>(cache, ci + 1, ydt, oo);

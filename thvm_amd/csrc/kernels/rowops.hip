@@ -513,6 +513,89 @@ extern "C" int thvm_k_len_bump(int32_t *len, int32_t delta, hipStream_t s, char 
   return 0;
 }
 
+// ---- blind speculative draft / accept (reference draft_prep and
+// accept_commit, bench/dsv2_decode_bench.c:1110-1170) ----
+// draft: one block; the bigram search over hist[0..P-1] runs strided over
+// the 256 threads, each keeping its last (largest) match, then a block max.
+__global__ __launch_bounds__(256) void k_spec_draft(int32_t *ca, int32_t *ce, const int32_t *hist,
+                                                    const int32_t *len, uint32_t S, uint32_t V,
+                                                    uint32_t cap, uint32_t forced) {
+  __shared__ int32_t wbest[4];
+  const int tid = threadIdx.x;
+  const int32_t P = len[0] - 1;
+  if (P < 0 || P >= (int32_t)cap) {                // no pending token: all holes
+    if (tid < (int)S) { ca[tid] = -1; ce[tid] = 0; }
+    return;
+  }
+  const int32_t pend = hist[P];
+  const int32_t ok_pend = pend >= 0 && (uint32_t)pend < V ? pend : 0;
+  int32_t best = -1;
+  if (!forced && P >= 1) {
+    const int32_t a0 = hist[P - 1];
+    for (int32_t j = tid; j + 1 < P; j += 256)
+      if (hist[j] == a0 && hist[j + 1] == pend) best = j;
+  }
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) best = max(best, __shfl_xor(best, off));
+  if ((tid & 63) == 0) wbest[tid >> 6] = best;
+  __syncthreads();
+  best = max(max(wbest[0], wbest[1]), max(wbest[2], wbest[3]));
+  if (tid < (int)S) {
+    int32_t v;
+    if (tid == 0) {
+      v = pend;
+    } else if (forced) {
+      const int32_t i = P + tid;
+      v = i < (int32_t)cap ? hist[i] : -1;
+    } else {
+      const int32_t i = best + 1 + tid;             // best + 2 + t, t = tid - 1
+      v = (best >= 0 && i <= P) ? hist[i] : -1;
+    }
+    if (v < 0 || (uint32_t)v >= V) v = -1;
+    ca[tid] = tid == 0 ? pend : v;
+    ce[tid] = v >= 0 ? v : ok_pend;
+  }
+}
+// accept: one lane (the commit is a handful of serial compares)
+__global__ void k_spec_accept(int32_t *hist, int32_t *len, int32_t *tok, const int32_t *ca,
+                              const int32_t *am, uint32_t S, uint32_t cap) {
+  if (threadIdx.x != 0 || blockIdx.x != 0) return;
+  const int32_t P = len[0] - 1;
+  if (P < 0 || P + (int32_t)S >= (int32_t)cap) return;
+  uint32_t k = 0;
+  while (k + 1 < S && ca[k + 1] >= 0 && ca[k + 1] == am[k]) k++;
+  for (uint32_t i = 0; i < k; i++) hist[P + 1 + i] = ca[1 + i];
+  hist[P + 1 + k] = am[k];
+  if (tok) tok[0] = am[k];
+  len[0] = P + (int32_t)k + 2;
+}
+extern "C" int thvm_k_spec_draft(int32_t *cand_acc, int32_t *cand_emb, const int32_t *hist,
+                                 const int32_t *len, uint32_t S, uint32_t V, uint32_t hist_cap,
+                                 uint32_t forced, hipStream_t s, char *err, int errlen) {
+  if (S < 2 || S > 256 || V == 0 || hist_cap == 0) {
+    snprintf(err, errlen, "spec_draft: S=%u must be 2..256, V and hist_cap nonzero", S);
+    return -1;
+  }
+  thvm_launch(true, true, k_spec_draft, dim3(1), dim3(256), 0, s, cand_acc, cand_emb, hist, len, S,
+              V, hist_cap, forced);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) { snprintf(err, errlen, "spec_draft launch: %s", hipGetErrorString(e)); return -1; }
+  return 0;
+}
+extern "C" int thvm_k_spec_accept(int32_t *hist, int32_t *len, int32_t *tok, const int32_t *cand_acc,
+                                  const int32_t *am, uint32_t S, uint32_t hist_cap, hipStream_t s,
+                                  char *err, int errlen) {
+  if (S < 2 || hist_cap == 0) {
+    snprintf(err, errlen, "spec_accept: S=%u must be >= 2, hist_cap nonzero", S);
+    return -1;
+  }
+  thvm_launch(true, true, k_spec_accept, dim3(1), dim3(64), 0, s, hist, len, tok, cand_acc, am, S,
+              hist_cap);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) { snprintf(err, errlen, "spec_accept launch: %s", hipGetErrorString(e)); return -1; }
+  return 0;
+}
+
 // ---- delay: one wave sleeps a fixed number of s_sleep(127) periods (~8k
 // cycles each), so a host can enqueue work behind it; the trip count is the
 // only exit condition and is bounded by the launcher ----

@@ -35,6 +35,58 @@ static int gen_step(uint32_t h) {
   return thvm_hip_decoder_capture(h) ? 0 : -1;
 }
 
+/* Generation through the speculative step (reference run_spec /
+ * serve_gen_spec, bench/dsv2_decode_bench.c:2629-2745, 2798-2860): the
+ * prompt's first n_prompt-1 ids go through the one-row step, the last one
+ * becomes the pending id the first speculative step verifies (P = n_prompt-1);
+ * each step then commits 1..S ids (hist[P+1..]), read back once per burst.
+ * A burst of n steps may advance the position by up to n*S, so it is sized
+ * to keep every step's verify rows inside max_seq; when not even one fits,
+ * the one-row step finishes the request. */
+static int generate_spec(uint32_t h, const int32_t *prompt, uint32_t np, uint32_t max_new,
+                         int32_t eos, int32_t *out, uint32_t *n_out, u32 S, u32 max_seq) {
+  int rc = 0;
+  for (u32 i = 0; i + 1 < np && !rc; i++) rc = thvm_hip_decoder_set_state(h, &prompt[i], i) || gen_step(h);
+  if (!rc) rc = thvm_hip_decoder_set_state(h, &prompt[np - 1], np - 1);
+  int32_t *hist = (int32_t *)malloc((u64)(max_seq + 1) * 4);
+  if (!hist) { hb_set_error("decoder_generate: out of host memory"); return -1; }
+  *n_out = 0;
+  for (u32 k = 0; k < max_new; k++) out[k] = -1;
+  u32 L = np;                      /* device length: P = L-1 is the pending position */
+  while (!rc) {
+    /* generated ids: hist[np .. L-1] (the new pending id included) */
+    const u32 have = L - np;
+    if (have > 0) {
+      if (thvm_hip_decoder_read_tokens(h, hist, L)) { rc = -1; break; }
+      int stop = 0;
+      for (u32 k = *n_out; k < have && k < max_new; k++) {
+        if (hist[np + k] == eos) { stop = 1; break; }
+        out[k] = hist[np + k];
+        *n_out = k + 1;
+      }
+      if (stop || *n_out >= max_new) break;
+    }
+    const u32 remaining = max_new - have;
+    u32 burst = remaining < 8 ? remaining : 8;
+    const u32 fit = (L - 1 + S <= max_seq) ? (max_seq - (L - 1)) / S : 0;
+    if (burst > fit) burst = fit;
+    if (burst == 0) {            /* no room for S verify rows: one-row steps */
+      rc = gen_step(h);
+    } else if (!hb_decoder_spec_slot(h)) {
+      rc = thvm_hip_decoder_spec_capture(h) ? 0 : -1;   /* the capture runs step 1 */
+    } else {
+      rc = thvm_hip_decoder_spec_replay(h, burst);
+    }
+    if (!rc) {
+      const u32 pos = thvm_hip_decoder_position(h);
+      if (pos + 1 <= L) { hb_set_error("decoder_generate: the speculative step did not advance"); rc = -1; }
+      L = pos + 1;
+    }
+  }
+  free(hist);
+  return rc;
+}
+
 THVM_API int thvm_hip_decoder_generate(uint32_t h, const int32_t *prompts, uint32_t n_prompt,
                                        uint32_t max_new, int32_t eos, int32_t *out,
                                        uint32_t *n_out) {
@@ -46,6 +98,9 @@ THVM_API int thvm_hip_decoder_generate(uint32_t h, const int32_t *prompts, uint3
     hb_set_error("decoder_generate: prompt %u + %u new ids exceed max_seq %u", n_prompt, max_new, S);
     return -1;
   }
+  const u32 Ssp = hb_decoder_spec_rows(h);
+  if (Ssp && B == 1 && n_prompt >= 2)
+    return generate_spec(h, prompts, n_prompt, max_new, eos, out, n_out, Ssp, S);
   int32_t *tok = (int32_t *)malloc((u64)B * 4);
   int32_t *hist = (int32_t *)malloc((u64)B * (S + 1) * 4);
   if (!tok || !hist) { free(tok); free(hist); hb_set_error("decoder_generate: out of host memory"); return -1; }
