@@ -128,6 +128,8 @@ def run_decode(thvm, key: str, batch: int, args) -> dict:
         cfg["step_mode"] = 1
     if args.moe_mode and spec["cfg"].get("arch") == 3:
         cfg["moe_mode"] = args.moe_mode
+    if args.attn_fused and spec["cfg"].get("arch") != 3:
+        cfg["attn_fused"] = args.attn_fused
     ctx = spec["ctx"]
     # the oracle decodes batch rows one after another on one core, so its rate
     # is the batch-1 rate; batches above 16 rows would take minutes and are
@@ -516,6 +518,8 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--step-mode", default="0", choices=["0", "1"],
                     help="0: one launch per op (hipGraph); 1: the persistent one-launch step (LLAMA)")
+    ap.add_argument("--attn-fused", type=int, default=0, choices=[0, 1, 2],
+                    help="attention form: 0 auto, 1 one launch, 2 split + merge launches")
     ap.add_argument("--moe-mode", type=int, default=0, choices=[0, 1, 2],
                     help="DSV2 above 4 rows: expert-grouped MoE on MFMA (0/2) or on the VALU (1)")
     ap.add_argument("--layers", type=int, default=None, help="debug only: fewer layers (invalid metric)")

@@ -234,6 +234,10 @@ static int cfg_check(const ThvmDecodeConfig *c) {
     hb_set_error("decoder: speculative decode is for the LLAMA op-list step at batch 1, greedy");
     return -1;
   }
+  if (c->attn_fused > 2) {
+    hb_set_error("decoder: attn_fused is 0 (auto), 1 (one launch) or 2 (two launches)");
+    return -1;
+  }
   if (c->moe_mode > 2) {
     hb_set_error("decoder: moe_mode is 0 (auto), 1 (VALU grouped) or 2 (MFMA grouped)");
     return -1;
@@ -381,10 +385,10 @@ static int op_attn(Decoder *d, u32 l) {
                 ? thvm_k_attn_auto_cpb(c->batch, c->n_heads, c->n_kv_heads, d->n_split, 0)
                 : c->attn_cpb;
   snprintf(p, sizeof p,
-           "thvm-builtin:attn b=%u h=%u hkv=%u hd=%u maxseq=%u chunk=64 nsplit=%u qt=%u ct=%u ot=%u scale=%a cpb=%u%s",
+           "thvm-builtin:attn b=%u h=%u hkv=%u hd=%u maxseq=%u chunk=64 nsplit=%u qt=%u ct=%u ot=%u scale=%a cpb=%u fused=%u%s",
            d->rows, c->n_heads, c->n_kv_heads, c->head_dim, c->max_seq, d->n_split, c->adtype,
            c->adtype, c->adtype, (float)(1.0 / sqrt((double)c->head_dim)), cpb,
-           d->spec ? " spec=1" : "");
+           c->attn_fused == 1 ? 1u : c->attn_fused == 2 ? 0u : 2u, d->spec ? " spec=1" : "");
   u32 a[6] = {act(d, "att"), act(d, "q"), tens_find(d, kn), tens_find(d, vn),
               tens_find(d, "len"), act(d, "attn.part")};
   return op_add(d, "attn", p, a, 6);

@@ -104,12 +104,13 @@ typedef struct ThvmAttnArgs {
   uint32_t B, H, Hkv, hd, max_seq, chunk, n_split;
   uint32_t qdt, cdt, odt;
   float scale;             /* 1/sqrt(hd)                                     */
-  uint32_t fused;          /* 1: split and merge in one launch (the last unit
-                            * of a (row, kv head) merges); 0: two launches   */
+  uint32_t fused;          /* 1: split and merge in one launch (the last
+                            * split block of a (row, kv head) merges); 0: two
+                            * launches; 2: picked from the shape            */
   uint32_t cpb;            /* chunks per split block: 0 picks from the unit
-                            * count, 1 one chunk per block, 2 or 4 a block
-                            * runs that many consecutive chunks (two
-                            * launches only); the partials are per block   */
+                            * count, 1 one chunk per block, above 1 a block
+                            * runs that many consecutive chunks (G <= 4);
+                            * the partials are per block                    */
   uint32_t spec;           /* speculative verify: the B query rows are
                             * consecutive positions of one sequence; row b
                             * reads cache row 0 over L+b rows (causal)     */

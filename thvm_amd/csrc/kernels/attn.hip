@@ -35,23 +35,50 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attn(ThvmAttnArgs a) {
   u.finish(a, kvh, split, b, wv, threadIdx.x, L, true, s);
 }
 
-template <int HD, int AT>
-__global__ __launch_bounds__(256) void k_attn_merge(ThvmAttnArgs a) {
-  __shared__ MergeLds s;
-  attn_merge<HD, AT, false>(a, blockIdx.x, threadIdx.x, attn_row_len(a, blockIdx.x / a.H), true, s);
+// live partials of a row of length L: one per cpb chunks
+__device__ __forceinline__ uint32_t attn_live(const ThvmAttnArgs &a, int32_t L) {
+  const int32_t span = ATT_CHUNK * (a.cpb > 1 ? (int32_t)a.cpb : 1);
+  const uint32_t n = L > 0 ? (uint32_t)((L + span - 1) / span) : 0u;
+  return n < a.n_split ? n : a.n_split;
 }
 
-// Split and merge in one launch: each split unit publishes its partial with
-// system-scope stores, drains them, and counts itself on its (row, kv head)
-// counter (one agent-scope atomic); the unit that brings the count to the
-// number of live splits merges the group's G heads (two at a time, 256
-// threads each) and resets the counter.  No fence: the partials never sit
-// in an L2.  Same split and merge code as the two-kernel form, so the same
-// outputs.  Counters: B*Hkv words after the partials, zero between launches.
+// one block per (row, kv head): the group's G heads
+template <int HD, int G, int AT>
+__global__ __launch_bounds__(MERGE_THREADS) void k_attn_merge(ThvmAttnArgs a) {
+  __shared__ MergeFlatLds<HD, G> s;
+  const uint32_t b = blockIdx.x / a.Hkv, kvh = blockIdx.x % a.Hkv;
+  attn_merge_flat<HD, G, AT, false>(a, b, kvh, attn_live(a, attn_row_len(a, b)), threadIdx.x, true, s);
+}
+
+// The one-launch forms' hand-off: publish this block's partial (written
+// with system-scope stores), count it on the (row, kv head) counter -- one
+// agent-scope atomic, B*Hkv words after the partials, zero between launches
+// -- and merge the group when this block brings the count to n_live (then
+// reset the counter).  No fence: the partials never sit in an L2.
+template <int HD, int G, int AT>
+__device__ __forceinline__ void attn_handoff_merge(const ThvmAttnArgs &a, uint32_t b, uint32_t kvh,
+                                                   uint32_t n_live, uint32_t *last,
+                                                   MergeFlatLds<HD, G> &ms) {
+  vm_drain();
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    uint32_t *ctr = (uint32_t *)(a.part + (uint64_t)a.B * a.H * a.n_split * (HD + 2)) + b * a.Hkv + kvh;
+    const uint32_t old = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    *last = old == n_live - 1 ? 1u : 0u;
+    if (*last) __hip_atomic_exchange(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  __syncthreads();
+  if (!*last) return;                              // block-uniform
+  attn_merge_flat<HD, G, AT, true>(a, b, kvh, n_live, threadIdx.x, true, ms);
+}
+
+// Split and merge in one launch, one chunk per block: each split unit
+// publishes its partial and the last one merges (attn_handoff_merge).  Same
+// split and merge code as the two-kernel form, so the same outputs.
 template <int HD, int G, int AT>
 __global__ __launch_bounds__(ATT_THREADS) void k_attn_fused(ThvmAttnArgs a) {
   __shared__ AttnLds<HD, G> s;
-  __shared__ MergeLds ms[2];
+  __shared__ MergeFlatLds<HD, G> ms;
   __shared__ uint32_t last;
   const uint32_t kvh = blockIdx.x, split = blockIdx.y, b = blockIdx.z;
   const int32_t L = attn_row_len(a, b);
@@ -62,22 +89,7 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attn_fused(ThvmAttnArgs a) {
   AttnSplit<HD, G, AT, true, false> u;
   u.issue(a, kvh, split, b, wv, L);
   u.finish(a, kvh, split, b, wv, threadIdx.x, L, true, s);
-  vm_drain();
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    uint32_t *ctr = (uint32_t *)(a.part + (uint64_t)a.B * a.H * a.n_split * (HD + 2)) + b * a.Hkv + kvh;
-    const uint32_t old = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    last = old == n_live - 1 ? 1u : 0u;
-    if (last) __hip_atomic_exchange(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  }
-  __syncthreads();
-  if (!last) return;                               // block-uniform
-  const int half = threadIdx.x >> 8;
-#pragma unroll
-  for (int gb = 0; gb < G; gb += 2) {
-    const int g = gb + half;
-    attn_merge<HD, AT, true>(a, b * a.H + kvh * G + g, threadIdx.x & 255, L, g < G, ms[half]);
-  }
+  attn_handoff_merge<HD, G, AT>(a, b, kvh, n_live, &last, ms);
 }
 
 // Batched split: one block runs cpb (a.cpb) consecutive chunks of a (kv head, row),
@@ -90,10 +102,13 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attn_fused(ThvmAttnArgs a) {
 // exp2(m_old - m_new) when the max grows), and the row groups and waves are
 // combined once per block.  The block writes one partial (acc, m, l) at slot
 // blockIdx.y of the merge's [n_split] rows; the merge reads ceil(L/(64 cpb))
-// of them.  Used when B * Hkv * n_split is large (batched decode).
-template <int HD, int G, int AT>
+// of them.  FUSE: the partial is published with system-scope stores and the
+// last block of the (row, kv head) merges in the same launch.
+template <int HD, int G, int AT, bool FUSE>
 __global__ __launch_bounds__(ATT_THREADS, 4) void k_attn_multi(ThvmAttnArgs a) {   // 2 blocks per CU
   __shared__ AttnLds<HD, G> s;
+  __shared__ MergeFlatLds<HD, G> ms;
+  __shared__ uint32_t last;
   typedef AttnSplit<HD, G, AT, false> SU;
   constexpr int EPL = SU::EPL, LPR = SU::LPR, RPW = SU::RPW, PPW = SU::PPW, IT = SU::IT, ES = SU::ES;
   const uint32_t kvh = blockIdx.x, grp = blockIdx.y, b = blockIdx.z;
@@ -241,20 +256,37 @@ __global__ __launch_bounds__(ATT_THREADS, 4) void k_attn_multi(ThvmAttnArgs a) {
       lt += s.wf[w][g] * s.wl[w][g];
       M = fmaxf(M, s.wm[w][g]);
     }
-    float *pp = a.part + (((uint64_t)b * a.H + kvh * G + g) * a.n_split + grp) * (HD + 2);
-    pp[d] = sv;
-    if (d == 0) { pp[HD] = M; pp[HD + 1] = lt; }
+    const uint64_t pi = (((uint64_t)b * a.H + kvh * G + g) * a.n_split + grp) * (HD + 2);
+    if (FUSE) {
+      coh_stf(a.part, (uint32_t)((pi + d) * 4), sv);
+      if (d == 0) { coh_stf(a.part, (uint32_t)((pi + HD) * 4), M); coh_stf(a.part, (uint32_t)((pi + HD + 1) * 4), lt); }
+    } else {
+      float *pp = a.part + pi;
+      pp[d] = sv;
+      if (d == 0) { pp[HD] = M; pp[HD + 1] = lt; }
+    }
   }
+  if (FUSE) attn_handoff_merge<HD, G, AT>(a, b, kvh, attn_live(a, L), &last, ms);
 }
 
 typedef void (*attn_fn)(ThvmAttnArgs);
 // (G = 8 heads per kv head would spill its accumulators: one chunk per block)
 template <int HD, int AT>
-static attn_fn attn_pick_multi(uint32_t G) {
+static attn_fn attn_pick_multi(uint32_t G, bool fused) {
   switch (G) {
-    case 1: return k_attn_multi<HD, 1, AT>;
-    case 2: return k_attn_multi<HD, 2, AT>;
-    case 4: return k_attn_multi<HD, 4, AT>;
+    case 1: return fused ? k_attn_multi<HD, 1, AT, true> : k_attn_multi<HD, 1, AT, false>;
+    case 2: return fused ? k_attn_multi<HD, 2, AT, true> : k_attn_multi<HD, 2, AT, false>;
+    case 4: return fused ? k_attn_multi<HD, 4, AT, true> : k_attn_multi<HD, 4, AT, false>;
+    default: return nullptr;
+  }
+}
+template <int HD, int AT>
+static attn_fn attn_pick_merge(uint32_t G) {
+  switch (G) {
+    case 1: return k_attn_merge<HD, 1, AT>;
+    case 2: return k_attn_merge<HD, 2, AT>;
+    case 4: return k_attn_merge<HD, 4, AT>;
+    case 8: return k_attn_merge<HD, 8, AT>;
     default: return nullptr;
   }
 }
@@ -293,7 +325,8 @@ extern "C" uint32_t thvm_k_attn_auto_cpb(uint32_t B, uint32_t H, uint32_t Hkv, u
   if (Hkv == 0 || n_split == 0) return 1;
   const uint64_t units = (uint64_t)B * Hkv * n_split;
   const uint32_t bh = B * Hkv, groups = bh >= 512 ? 1u : 512u / bh;   // split blocks per (row, kv head)
-  uint32_t cpb = (fused || H / Hkv > 4 || (n_split <= 4 && units <= 512)) ? 1
+  (void)fused;
+  uint32_t cpb = (H / Hkv > 4 || (n_split <= 4 && units <= 512)) ? 1
                : units > 1024 ? (n_split + groups - 1) / groups : 2;
   return cpb > n_split ? n_split : cpb;
 }
@@ -316,32 +349,28 @@ extern "C" int thvm_k_attn_decode(const ThvmAttnArgs *a, hipStream_t s, char *er
     snprintf(err, errlen, "attn: q, cache and out must share one dtype");
     return -1;
   }
-  // two launches by default; fused = 1 merges in the split launch.  At the C4
-  // shape the fused form measured slower (2.40 vs 2.32 ms per step): one
-  // block per kv head then runs all of its heads' merges, where the merge
-  // kernel spreads one head per block.
-  const bool fused = a->fused != 0;
+  // fused = 1: the last split block of a (row, kv head) merges in the same
+  // launch; 0: a second launch merges; 2: one launch when few (row, kv head)
+  // groups share the merges
+  if (a->fused > 2) { snprintf(err, errlen, "attn: fused must be 0, 1 or 2"); return -1; }
+  const bool fused = a->fused == 1 || (a->fused == 2 && a->B * a->Hkv <= 64);
   uint32_t cpb = a->cpb;
   if (cpb > a->n_split) cpb = a->n_split;          // one block takes every chunk
-  if (fused && cpb > 1) {
-    snprintf(err, errlen, "attn: the one-launch form runs one chunk per block");
-    return -1;
-  }
   if (cpb == 0) cpb = thvm_k_attn_auto_cpb(a->B, a->H, a->Hkv, a->n_split, fused);
   attn_fn f = nullptr, fm = nullptr;
   const uint32_t G = a->H / a->Hkv;
   const int at = a->cdt == THVM_DT_BF16 ? AT_BF16 : a->cdt == THVM_DT_FP16 ? AT_F16 : AT_F32;
   if (a->hd == 128) {
-    f = cpb > 1 ? (at == AT_BF16 ? attn_pick_multi<128, AT_BF16>(G) : at == AT_F16 ? attn_pick_multi<128, AT_F16>(G) : attn_pick_multi<128, AT_F32>(G))
+    f = cpb > 1 ? (at == AT_BF16 ? attn_pick_multi<128, AT_BF16>(G, fused) : at == AT_F16 ? attn_pick_multi<128, AT_F16>(G, fused) : attn_pick_multi<128, AT_F32>(G, fused))
         : at == AT_BF16 ? attn_pick<128, AT_BF16>(G, fused) : at == AT_F16 ? attn_pick<128, AT_F16>(G, fused) : attn_pick<128, AT_F32>(G, fused);
-    fm = at == AT_BF16 ? k_attn_merge<128, AT_BF16> : at == AT_F16 ? k_attn_merge<128, AT_F16> : k_attn_merge<128, AT_F32>;
+    fm = at == AT_BF16 ? attn_pick_merge<128, AT_BF16>(G) : at == AT_F16 ? attn_pick_merge<128, AT_F16>(G) : attn_pick_merge<128, AT_F32>(G);
   } else if (a->hd == 64) {
-    f = cpb > 1 ? (at == AT_BF16 ? attn_pick_multi<64, AT_BF16>(G) : at == AT_F16 ? attn_pick_multi<64, AT_F16>(G) : attn_pick_multi<64, AT_F32>(G))
+    f = cpb > 1 ? (at == AT_BF16 ? attn_pick_multi<64, AT_BF16>(G, fused) : at == AT_F16 ? attn_pick_multi<64, AT_F16>(G, fused) : attn_pick_multi<64, AT_F32>(G, fused))
         : at == AT_BF16 ? attn_pick<64, AT_BF16>(G, fused) : at == AT_F16 ? attn_pick<64, AT_F16>(G, fused) : attn_pick<64, AT_F32>(G, fused);
-    fm = at == AT_BF16 ? k_attn_merge<64, AT_BF16> : at == AT_F16 ? k_attn_merge<64, AT_F16> : k_attn_merge<64, AT_F32>;
+    fm = at == AT_BF16 ? attn_pick_merge<64, AT_BF16>(G) : at == AT_F16 ? attn_pick_merge<64, AT_F16>(G) : attn_pick_merge<64, AT_F32>(G);
   }
-  if (!f) {
-    snprintf(err, errlen, "attn: no kernel for hd=%u G=%u", a->hd, G);
+  if (!f || !fm) {
+    snprintf(err, errlen, "attn: no kernel for hd=%u G=%u cpb=%u", a->hd, G, cpb);
     return -1;
   }
   if ((uint64_t)a->B * a->H * a->n_split * (a->hd + 2) * 4 >= (1ull << 31)) {
@@ -351,7 +380,7 @@ extern "C" int thvm_k_attn_decode(const ThvmAttnArgs *a, hipStream_t s, char *er
   ThvmAttnArgs ak = *a;
   ak.cpb = cpb;
   thvm_launch(true, fused, f, dim3(a->Hkv, (a->n_split + cpb - 1) / cpb, a->B), dim3(ATT_THREADS), 0, s, ak);
-  if (!fused) thvm_launch(false, true, fm, dim3(a->B * a->H), dim3(256), 0, s, ak);
+  if (!fused) thvm_launch(false, true, fm, dim3(a->B * a->Hkv), dim3(MERGE_THREADS), 0, s, ak);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) { snprintf(err, errlen, "attn launch: %s", hipGetErrorString(e)); return -1; }
   return 0;

@@ -15,8 +15,8 @@
 // scale*log2 e) so the softmax uses the hardware exp2.  Row-group sums use
 // DPP, the 8 waves merge through LDS with one rescale per wave, and the unit
 // writes (acc[hd], m, l) for its split.
-// Merge (batch row b, q head h), 256 threads: the ceil(L/(CHUNK*cpb)) live
-// partials in a fixed order (deterministic).
+// Merge (batch row b, kv head), 512 threads: the G heads' ceil(L/(CHUNK*cpb))
+// live partials in a fixed order (deterministic), one memory round trip.
 //
 // COH (persistent kernel): q, the partials and the output are read/written
 // with system-scope accesses, and the cache row L-1 -- appended by another
@@ -104,14 +104,8 @@ struct AttnLds {
   float wm[ATT_WAVES][G], wl[ATT_WAVES][G], wf[ATT_WAVES][G];
   __align__(16) float wacc[ATT_WAVES][G][HD];
 };
-// LDS of one 256-thread merge group
-struct MergeLds {
-  float w[ATT_MAX_SPLITS];
-  float L;
-  __align__(16) float4 red4[256];
-};
 
-// COH: q, the partials (and, in attn_merge, the output) use system-scope
+// COH: q and the partials use system-scope
 // accesses; LATE: the cache row L-1 is written by another block of the same
 // launch and is loaded in finish() with a system-scope load.
 template <int HD, int G, int AT, bool COH, bool LATE = COH>
@@ -281,105 +275,87 @@ struct AttnSplit {
     }
   }
 };
+// ---- one-round-trip merge of a (row, kv head) group ----------------------
+// The G heads of query row b and kv head kvh, by 512 threads: thread t owns
+// the output pair (g, d) = (e / (HD/2), 2 (e % (HD/2))), e = t % PAIRS, and
+// folds the live partials s = p, p + NP, p + 2 NP, ... of its partition
+// p = t / PAIRS (NP = 512 / PAIRS partitions), loading up to MCH of them
+// before any arithmetic (one memory round trip for up to NP * MCH partials);
+// partition 0 then folds partitions 1 .. NP-1 in order.  The fold of (m, l,
+// acc) into (mp, lp, ap): mn = max(mp, m), lp = lp 2^(mp-mn) + l 2^(m-mn),
+// likewise ap; out = ap / lp.  Every caller (the merge kernel, the one-launch
+// form, the persistent step) runs this function, so all give the same bits.
+// COH: system-scope loads of the partials and stores of the output.
+#define MERGE_THREADS 512
+#define MCH 16
+template <int HD, int G>
+struct MergeFlatLds {
+  static constexpr int PAIRS = G * HD / 2, NP = MERGE_THREADS / PAIRS;
+  float m[NP][PAIRS], l[NP][PAIRS];
+  float2 a[NP][PAIRS];
+};
+#define MERGE_LDS_BYTES (MERGE_THREADS * 16)   /* sizeof(MergeFlatLds<HD, G>), every HD and G */
 
-// Merge of the live splits of one (b, q head) bh = b*H + h by 256 threads
-// (tid 0..255): split weights w_s = exp2(m_s - M) and the denominator from one
-// wave, then SQ threads per float4 of the head's output each sum a strided
-// subset of splits, folded in a fixed order.  Every thread of the block calls
-// it (two block barriers inside); `active` false skips the work.
-template <int HD, int AT, bool COH>
-__device__ __forceinline__ void attn_merge(const ThvmAttnArgs &a, uint32_t bh, int tid, int32_t L,
-                                           bool active, MergeLds &s) {
-  constexpr int U4 = HD / 4;
-  constexpr int SQ = 256 / U4;
-  const int32_t span = ATT_CHUNK * (a.cpb > 1 ? (int32_t)a.cpb : 1);   // cache rows per partial
-  uint32_t n_live = L > 0 ? (uint32_t)((L + span - 1) / span) : 0u;
-  if (n_live > a.n_split) n_live = a.n_split;
-  const uint64_t pbi = (uint64_t)bh * a.n_split * (HD + 2);
-  const float *pb = a.part + pbi;
-  auto ldp = [&](uint64_t i) -> float {
-    return COH ? coh_ldf(a.part, (uint32_t)((pbi + i) * 4)) : pb[i];
-  };
-  const int lane = lane_id();
-  // this thread's first MP splits' partial vectors, loaded with wave 0's
-  // (m, l) loads (clamped indices, unconditional): they do not depend on the
-  // split weights, so the merge waits for one memory round trip, not two
-  constexpr int U4P = HD / 4, SQP = 256 / U4P, MP = 4;
-  const int dqp = tid % U4P, sqp = tid / U4P;
-  float2 pv[MP][2];
-  if (active) {
+__device__ __forceinline__ void merge_fold(float &mp, float &lp, float &a0, float &a1, float m,
+                                           float l, float x0, float x1) {
+  const float mn = fmaxf(mp, m);
+  const float fo = mp == -INFINITY ? 0.0f : fexp2(mp - mn);
+  const float fn = m == -INFINITY ? 0.0f : fexp2(m - mn);
+  lp = lp * fo + l * fn;
+  a0 = a0 * fo + x0 * fn;
+  a1 = a1 * fo + x1 * fn;
+  mp = mn;
+}
+
+template <int HD, int G, int AT, bool COH>
+__device__ __forceinline__ void attn_merge_flat(const ThvmAttnArgs &a, uint32_t b, uint32_t kvh,
+                                                uint32_t n_live, int tid, bool active,
+                                                MergeFlatLds<HD, G> &s) {
+  typedef MergeFlatLds<HD, G> FL;
+  constexpr int PAIRS = FL::PAIRS, NP = FL::NP;
+  static_assert(NP >= 1 && MERGE_THREADS % PAIRS == 0, "merge geometry");
+  const int e = tid % PAIRS, p = tid / PAIRS;
+  const int g = e / (HD / 2), d = (e % (HD / 2)) * 2;
+  const uint64_t bh = (uint64_t)b * a.H + kvh * G + g;
+  const uint64_t pbi = bh * a.n_split * (HD + 2);
+  float mp = -INFINITY, lp = 0.0f, a0 = 0.0f, a1 = 0.0f;
+  if (active && p < NP) {
+    for (uint32_t s0 = p; s0 < n_live; s0 += NP * MCH) {
+      float mv[MCH], lv[MCH];
+      float2 av[MCH];
 #pragma unroll
-    for (int j = 0; j < MP; j++) {
-      const uint32_t sp = sqp + j * SQP, spc = sp < n_live ? sp : 0;
-      const uint64_t q = (uint64_t)spc * (HD + 2) + dqp * 4;
-      if (COH) {
-        const uint2 r0 = coh_ld8(a.part, (uint32_t)((pbi + q) * 4));
-        const uint2 r1 = coh_ld8(a.part, (uint32_t)((pbi + q + 2) * 4));
-        pv[j][0] = make_float2(__uint_as_float(r0.x), __uint_as_float(r0.y));
-        pv[j][1] = make_float2(__uint_as_float(r1.x), __uint_as_float(r1.y));
-      } else {
-        pv[j][0] = *(const float2 *)(pb + q);
-        pv[j][1] = *(const float2 *)(pb + q + 2);
+      for (int j = 0; j < MCH; j++) {            // loads first (clamped, unconditional)
+        const uint32_t sp = s0 + j * NP, spc = sp < n_live ? sp : s0;
+        const uint64_t q = pbi + (uint64_t)spc * (HD + 2);
+        if (COH) {
+          const uint2 r = coh_ld8(a.part, (uint32_t)((q + d) * 4));
+          const uint2 ml = coh_ld8(a.part, (uint32_t)((q + HD) * 4));
+          av[j] = make_float2(__uint_as_float(r.x), __uint_as_float(r.y));
+          mv[j] = __uint_as_float(ml.x);
+          lv[j] = __uint_as_float(ml.y);
+        } else {
+          av[j] = *(const float2 *)(a.part + q + d);
+          const float2 ml = *(const float2 *)(a.part + q + HD);
+          mv[j] = ml.x;
+          lv[j] = ml.y;
+        }
       }
+#pragma unroll
+      for (int j = 0; j < MCH; j++)
+        if (s0 + j * NP < n_live) merge_fold(mp, lp, a0, a1, mv[j], lv[j], av[j].x, av[j].y);
     }
   }
-  if (active && tid < 64) {
-    const float mv0 = lane < (int)n_live ? ldp((uint64_t)lane * (HD + 2) + HD) : -INFINITY;
-    const float lv0 = lane < (int)n_live ? ldp((uint64_t)lane * (HD + 2) + HD + 1) : 0.0f;
-    const float mv1 = lane + 64 < (int)n_live ? ldp((uint64_t)(lane + 64) * (HD + 2) + HD) : -INFINITY;
-    const float lv1 = lane + 64 < (int)n_live ? ldp((uint64_t)(lane + 64) * (HD + 2) + HD + 1) : 0.0f;
-    const float M = wave_max(fmaxf(mv0, mv1));
-    const float w0 = mv0 == -INFINITY ? 0.0f : fexp2(mv0 - M);
-    const float w1 = mv1 == -INFINITY ? 0.0f : fexp2(mv1 - M);
-    const float Ls = wave_sum(w0 * lv0 + w1 * lv1);
-    if (lane < (int)n_live) s.w[lane] = w0;
-    if (lane + 64 < (int)n_live) s.w[lane + 64] = w1;
-    if (lane == 0) s.L = Ls;
-  }
-  __syncthreads();
-  if (active) {
-    const int dq = tid % U4, sq = tid / U4;
-    float4 s4 = make_float4(0.f, 0.f, 0.f, 0.f);
+  if (NP > 1) {
+    if (active) { s.m[p][e] = mp; s.l[p][e] = lp; s.a[p][e] = make_float2(a0, a1); }
+    __syncthreads();
+    if (active && p == 0)
 #pragma unroll
-    for (int j = 0; j < MP; j++) {                 // the prefetched splits, in order
-      const uint32_t sp = sq + j * SQ;
-      if (sp < n_live) {
-        const float w = s.w[sp];
-        s4.x += w * pv[j][0].x; s4.y += w * pv[j][0].y; s4.z += w * pv[j][1].x; s4.w += w * pv[j][1].y;
-      }
-    }
-#pragma unroll 8
-    for (uint32_t sp = sq + MP * SQ; sp < n_live; sp += SQ) {
-      const float w = s.w[sp];
-      const uint64_t q = (uint64_t)sp * (HD + 2) + dq * 4;
-      // HD + 2 floats per split: a split's row is 8-byte aligned only
-      float2 v0, v1;
-      if (COH) {
-        const uint2 r0 = coh_ld8(a.part, (uint32_t)((pbi + q) * 4));
-        const uint2 r1 = coh_ld8(a.part, (uint32_t)((pbi + q + 2) * 4));
-        v0 = make_float2(__uint_as_float(r0.x), __uint_as_float(r0.y));
-        v1 = make_float2(__uint_as_float(r1.x), __uint_as_float(r1.y));
-      } else {
-        v0 = *(const float2 *)(pb + q);
-        v1 = *(const float2 *)(pb + q + 2);
-      }
-      s4.x += w * v0.x; s4.y += w * v0.y; s4.z += w * v1.x; s4.w += w * v1.y;
-    }
-    s.red4[tid] = s4;
+      for (int q = 1; q < NP; q++) merge_fold(mp, lp, a0, a1, s.m[q][e], s.l[q][e], s.a[q][e].x, s.a[q][e].y);
   }
-  __syncthreads();
-  if (active && tid < U4) {
-    float4 s4 = s.red4[tid];
-#pragma unroll
-    for (int sq = 1; sq < SQ; sq++) {
-      const float4 r = s.red4[sq * U4 + tid];
-      s4.x += r.x; s4.y += r.y; s4.z += r.z; s4.w += r.w;
-    }
-    const float inv = s.L > 0.0f ? 1.0f / s.L : 0.0f;
-    const uint64_t oi = (uint64_t)bh * HD + tid * 4;
-    st_act<AT, COH>(a.out, oi, s4.x * inv);
-    st_act<AT, COH>(a.out, oi + 1, s4.y * inv);
-    st_act<AT, COH>(a.out, oi + 2, s4.z * inv);
-    st_act<AT, COH>(a.out, oi + 3, s4.w * inv);
+  if (active && p == 0) {
+    const float inv = lp > 0.0f ? 1.0f / lp : 0.0f;
+    const uint64_t oi = bh * HD + d;
+    st_act<AT, COH>(a.out, oi, a0 * inv);
+    st_act<AT, COH>(a.out, oi + 1, a1 * inv);
   }
 }

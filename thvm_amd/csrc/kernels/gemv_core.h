@@ -16,8 +16,11 @@
 //     swizzled so the 64 lanes' 16-byte LDS reads hit distinct banks; a fused
 //     RMSNorm / LayerNorm writes the normalised row there already rounded to
 //     the activation dtype, exactly as the separate norm kernel would store it;
-//   * fp8 decodes with v_cvt_pk_f32_fp8 (OCP e4m3, exact); the per-row scale
-//     is applied once after the reduction;
+//   * 16-bit x against fp8 or same-type 16-bit weights runs on packed dot
+//     products (v_dot2c_f32_bf16 / _f16; fp8 pairs converted exactly with
+//     v_cvt_scalef32_pk_*_fp8); other pairings decode both operands to f32
+//     for FMAs (fp8 with v_cvt_pk_f32_fp8, OCP e4m3, exact); the per-row
+//     scale is applied once after the reduction;
 //   * each row's K reduction ends in a DPP wave reduction (fixed order,
 //     deterministic): no partial buffer and no second fold kernel.
 // A row's sum depends only on the chunk order of its lanes, not on which wave,
@@ -96,6 +99,45 @@ __device__ __forceinline__ void x8_decode(const uint4 &q, float o[8]) {
       o[2 * i + 1] = h2f((f16_t)(w[i] >> 16));
     }
   }
+}
+
+// ---- packed dot products: 16-bit x against fp8 / same-type 16-bit weights --
+// v_dot2c_f32_{bf16,f16} takes an x pair and a weight pair as they sit in
+// registers (two MACs, f32 accumulate, one instruction); fp8 weight pairs go
+// to the x type with one v_cvt_scalef32_pk_{bf16,f16}_fp8 (scale 1: exact, an
+// e4m3 value has <= 4 significant bits and its exponent range fits both).
+// Two to three times fewer VALU instructions per weight byte than decoding
+// both operands to f32 for FMAs: the arithmetic a one-round GEMV does after
+// its weights land, on the critical path at batch 1.
+template <int WT, int XT>
+struct Dot2 {
+  static constexpr bool ok = (XT == XT_BF16 && (WT == WT_FP8 || WT == WT_BF16)) ||
+                             (XT == XT_F16 && (WT == WT_FP8 || WT == WT_F16));
+};
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+// the two element pairs of weight quad j of a 16-byte chunk, in the x type
+template <int WT, int XT>
+__device__ __forceinline__ void quad_pairs(const uint4 &q, int j, uint32_t &p0, uint32_t &p1) {
+  if (WT == WT_FP8) {
+    const uint32_t w = j == 0 ? q.x : j == 1 ? q.y : j == 2 ? q.z : q.w;
+    if (XT == XT_BF16) {
+      p0 = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w, 1.0f, false));
+      p1 = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w, 1.0f, true));
+    } else {
+      p0 = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w, 1.0f, false));
+      p1 = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w, 1.0f, true));
+    }
+  } else {
+    p0 = j == 0 ? q.x : q.z;
+    p1 = j == 0 ? q.y : q.w;
+  }
+}
+template <int XT>
+__device__ __forceinline__ float dot2acc(uint32_t x, uint32_t w, float acc) {
+  if (XT == XT_BF16)
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, x), __builtin_bit_cast(bf16x2_t, w), acc, false);
+  return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2_t, x), __builtin_bit_cast(f16x2_t, w), acc, false);
 }
 
 template <int XT>
@@ -374,6 +416,28 @@ __device__ __forceinline__ bool gemv_core(const ThvmGemvArgs &a, unsigned char *
                 acc[r][m] += xv[m].y * wf[1];
                 acc[r][m] += xv[m].z * wf[2];
                 acc[r][m] += xv[m].w * wf[3];
+              }
+            }
+          }
+        } else if (Dot2<WT, XT>::ok) {
+#pragma unroll
+          for (int h = 0; h < (E + 7) / 8; h++) {     // 8-element x groups: 4 pairs
+            uint4 xq[M];
+#pragma unroll
+            for (int m = 0; m < M; m++)
+              xq[m] = *(const uint4 *)((const uint16_t *)xs_raw + m * K + (h * C + c) * 8);
+#pragma unroll
+            for (int jj = 0; jj < 2 && (h * 2 + jj) < E / 4; jj++) {
+              const int j = h * 2 + jj;
+#pragma unroll
+              for (int r = 0; r < R; r++) {
+                uint32_t w0, w1;
+                quad_pairs<WT, XT>(X[r][u], j, w0, w1);
+#pragma unroll
+                for (int m = 0; m < M; m++) {
+                  acc[r][m] = dot2acc<XT>(jj ? xq[m].z : xq[m].x, w0, acc[r][m]);
+                  acc[r][m] = dot2acc<XT>(jj ? xq[m].w : xq[m].y, w1, acc[r][m]);
+                }
               }
             }
           }

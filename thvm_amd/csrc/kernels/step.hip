@@ -25,7 +25,7 @@ static uint64_t step_lds(const ThvmStepArgs *a) {
   const uint64_t gemv = (uint64_t)a->M * kmax * 2;
   const uint32_t G = a->Hkv ? a->H / a->Hkv : 1;
   const uint64_t attn = 2 * ((uint64_t)3 * ATT_WAVES * G * 4 + (uint64_t)ATT_WAVES * G * a->hd * 4 + 16) +
-                        4 * (uint64_t)sizeof(MergeLds) + 64;
+                        2 * (uint64_t)MERGE_LDS_BYTES + 64;
   return gemv > attn ? gemv : attn;
 }
 

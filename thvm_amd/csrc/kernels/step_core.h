@@ -170,22 +170,21 @@ __device__ __attribute__((noinline)) bool step_gemv(const ThvmStepArgs &a, uint3
 }
 
 // Merge of the G heads of (row ub, kv head uk) by the calling 8-wave half
-// (two 256-thread groups, one head each at a time) when mg is set.
+// (512 threads) when mg is set: the merge every attention form runs.
 template <int WT, int AT, int M, int HD, int G>
 __device__ __attribute__((noinline)) void step_merge(const ThvmStepArgs &a, uint32_t l, uint32_t ub,
                                                      uint32_t uk, bool mg) {
   extern __shared__ __align__(16) unsigned char lds[];
+  static_assert(sizeof(MergeFlatLds<HD, G>) == MERGE_LDS_BYTES, "merge LDS");
   const int wv = threadIdx.x >> 6;
   const int half = wv >> 3, htid = threadIdx.x & 511;
-  MergeLds *ml = (MergeLds *)(lds + 2 * sizeof(AttnLds<HD, G>)) + half * 2 + (htid >> 8);
+  MergeFlatLds<HD, G> *ml = (MergeFlatLds<HD, G> *)(lds + 2 * sizeof(AttnLds<HD, G>)) + half;
   ThvmAttnArgs aa = {};
   aa.out = a.att; aa.part = a.part; aa.H = a.H; aa.n_split = a.n_split;
   const int32_t L = a.len[0];
-#pragma unroll
-  for (int gb = 0; gb < G; gb += 2) {
-    const int g = gb + (htid >> 8);
-    attn_merge<HD, AT, true>(aa, ub * a.H + uk * G + g, htid & 255, L, mg && g < G, *ml);
-  }
+  uint32_t n_live = L > 0 ? (uint32_t)((L + ATT_CHUNK - 1) / ATT_CHUNK) : 0u;
+  if (n_live > a.n_split) n_live = a.n_split;
+  attn_merge_flat<HD, G, AT, true>(aa, ub, uk, n_live, htid, mg, *ml);
 }
 
 // The attention stage of layer l: split units (two at a time per block, one
