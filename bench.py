@@ -201,7 +201,7 @@ def run_decode(thvm, key: str, batch: int, args) -> dict:
     mla = cfg["arch"] == 3
     atag = "mla_attn" if mla else "attn"
     kern = {}
-    for tag in ("gemv", "moe_gateup", "moe_down", "mla_prep", "route", "norm", atag, "llama_step"):
+    for tag in ("gemv", "moe_gateup", "moe_down", "mla_prep", "moe_gate", "route", "norm", atag, "llama_step"):
         ms_t, n_t = thvm.kprof_query(tag)
         if n_t:
             kern[tag] = (ms_t, n_t, thvm.kprof_bytes(tag))

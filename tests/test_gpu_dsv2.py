@@ -363,3 +363,85 @@ def test_mla_split_mode_errors(hip):
         with pytest.raises(hip.ThvmHipError):
             hip.builtin("mla_attn", args, b=B, h=H, dn=dn, dr=dr, kv=kv, dv=dv, maxseq=ms, nsplit=2,
                         wt=DT_BF16, scale=0.2, **bad)
+
+
+def test_moe_mfma_matches_oracle_at_c5_geometry(hip):
+    """The default C5 batch-32 MoE -- expert-grouped, on MFMA -- against the
+    oracle's per-row or_moe at the C5 geometry: 64 experts, top-6, I 1408,
+    2 shared experts (S 2816), D 2048, fp8 weights, 32 rows routed at random
+    (every row 6 distinct experts; about 50 experts live).  Bar: the north
+    star's fp8 tolerance, 2e-2 of the row's largest |MoE output|, on the
+    residual output bf16(res + bf16(moe)); and each element within 2^-6
+    (|res| + |moe|) of the oracle chain, the bf16 roundings' reach."""
+    D, E, K, I, S, B = 2048, 64, 6, 1408, 2816, 32
+    say("case: mfma moe vs or_moe at E=64 K=6 I=1408 B=32")
+    rng = np.random.default_rng(64)
+
+    def f8w(rows, cols):                 # random e4m3 codes (no NaN), per-row scales
+        q = rng.integers(0, 256, (rows, cols), dtype=np.uint8)
+        q[(q & 0x7F) == 0x7F] = 0
+        return q, rng.uniform(0.5, 1.5, rows).astype(np.float32) * 1e-4
+    wgue, sgue = f8w(E * 2 * I, D)
+    wde, sde = f8w(E * D, I)
+    wgus, sgus = f8w(2 * S, D)
+    wds, sds = f8w(D, S)
+    w = (wgue, sgue, wde, sde, wgus, sgus, wds, sds)
+    x = rng.standard_normal((B, D)).astype(np.float32)
+    res0 = bf(rng.standard_normal((B, D)))
+    sel = np.stack([rng.permutation(E)[:K] for _ in range(B)]).astype(np.int32)
+    probs = rng.uniform(0.05, 0.3, (B, K)).astype(np.float32)
+    _, r2, live = run_moe(hip, 2, B, D, E, K, I, S, DT_FP8, x, sel, probs, res0, w)
+    assert live == len(np.unique(sel))
+    got = unbf(r2).reshape(B, D)
+    for b in range(B):
+        out = np.empty(D, np.float32)
+        xb, sb, pb = bf(x[b]), np.ascontiguousarray(sel[b]), np.ascontiguousarray(probs[b])   # kept alive
+        O.oracle().or_moe(out.ctypes.data, xb.ctypes.data, sb.ctypes.data, pb.ctypes.data,
+                          wgue.ctypes.data, sgue.ctypes.data,
+                          wde.ctypes.data, sde.ctypes.data, wgus.ctypes.data, sgus.ctypes.data,
+                          wds.ctypes.data, sds.ctypes.data, DT_FP8, D, I, S, K)
+        r = unbf(res0[b])
+        want = unbf(bf(r + unbf(bf(out))))
+        err = np.abs(got[b] - want)
+        assert err.max() <= 2e-2 * np.abs(out).max(), (b, err.max(), np.abs(out).max())
+        assert (err <= 2.0 ** -6 * (np.abs(r) + np.abs(out)) + 1e-6).all(), b
+
+
+@pytest.mark.parametrize("B,D,E,K", [(1, 2048, 64, 6), (32, 2048, 64, 6), (3, 4096, 64, 8),
+                                     (2, 512, 8, 3), (1, 1008, 20, 4)])
+def test_moe_gate_and_gateup_routing_equal_the_split_kernels(hip, B, D, E, K):
+    """The one-launch gate (RMSNorm f32 out + f32 router GEMV) is bit for bit
+    the norm and GEMV kernels (xn, logits); the top-K picked inside the
+    per-row gate/up (route=1) is the route kernel's (ids, probabilities) and
+    so is the gate/up output.  One row's logits tie at the top (two equal
+    router rows) to hold the lowest-id rule."""
+    say(f"case: moe_gate B={B} D={D} E={E} K={K}")
+    rng = np.random.default_rng(B * D + E)
+    x = bf(rng.standard_normal((B, D)))
+    g = rng.uniform(0.5, 1.5, D).astype(np.float32)
+    gate = (rng.standard_normal((E, D)) * 0.05).astype(np.float32)
+    gate[E - 1] = gate[1]                               # a tie between experts 1 and E-1
+    xb, gb, wb = up(hip, x), up(hip, g), up(hip, gate)
+    I, S = 64, 128
+    wgue, sgue, _ = fp8_rows(rng, E * 2 * I, D)
+    wgus, sgus, _ = fp8_rows(rng, 2 * S, D)
+    wg = [up(hip, wgue), up(hip, sgue), up(hip, wgus), up(hip, sgus)]
+    outs = []
+    for fused in (True, False):
+        xn, lg = hip.Buffer(B * D * 4), hip.Buffer(B * E * 4)
+        sel, pr = hip.Buffer(B * K * 4), hip.Buffer(B * K * 4)
+        h = hip.Buffer(B * (K * I + S) * 4)
+        kw = dict(b=B, d=D, e=E, k=K, i=I, s=S, wt=DT_FP8)
+        if fused:
+            hip.builtin("moe_gate", [xn, lg, xb, gb, wb], outs=(0, 1), b=B, d=D, e=E, eps=1e-6)
+            hip.builtin("moe_gateup", [h, xn, sel] + wg[:2] + wg[2:] + [lg, pr], outs=(0, 2, 6),
+                        route=1, **kw)
+        else:
+            hip.builtin("norm", [xn, xb, gb], m=B, k=D, xt=DT_BF16, yt=DT_F32, eps=1e-6)
+            hip.builtin("gemv", [lg, xn, wb], m=B, n=E, k=D, wt=DT_F32, xt=DT_F32, yt=DT_F32, epi=0)
+            hip.builtin("route", [sel, pr, lg], outs=(0, 1), b=B, e=E, k=K)
+            hip.builtin("moe_gateup", [h, xn, sel] + wg, **kw)
+        outs.append([b.read(np.uint32) for b in (xn, lg, sel, pr, h)])
+    for name, f, s in zip(("xn", "logits", "sel", "probs", "h"), outs[0], outs[1]):
+        assert np.array_equal(f, s), name
+    assert np.isfinite(outs[0][1].view(np.float32)).all()

@@ -976,24 +976,39 @@ static int build_dsv2(Decoder *d) {
       WM("l%u.wd_s", D, S, &wds, &sds);
     }
 #undef WM
-    snprintf(p, sizeof p, "thvm-builtin:norm m=%u k=%u xt=%u yt=%u eps=%a", B, D, THVM_DT_BF16,
-             THVM_DT_FP32, c->eps);
-    u32 na[3] = {xnf, x, wpost};
-    if (op_add(d, "norm_post", p, na, 3)) return -1;
-    snprintf(p, sizeof p, "thvm-builtin:gemv m=%u n=%u k=%u wt=%u xt=%u yt=%u epi=0", B, E, D,
-             THVM_DT_FP32, THVM_DT_FP32, THVM_DT_FP32);
-    u32 ra[3] = {gl, xnf, gate};
-    if (op_add(d, "gemv_gate", p, ra, 3)) return -1;
-    snprintf(p, sizeof p, "thvm-builtin:route b=%u e=%u k=%u", B, E, K);
-    u32 rb[3] = {sel, probs, gl};
-    if (op_add(d, "route", p, rb, 3)) return -1;
-    snprintf(p, sizeof p, "thvm-builtin:moe_gateup b=%u d=%u e=%u k=%u i=%u s=%u wt=%u grouped=%d", B, D,
-             E, K, I, S, wdt, grp);
-    u32 ma[10], mn = 0;
+    /* the norm (f32 out) and the f32 router GEMV in one launch, and the top-K
+     * inside the per-row gate/up: bit for bit the norm -> GEMV -> route
+     * kernels (THVM_HIP_SPLIT_ROUTER=1 runs those three for A/B) */
+    const char *sr = getenv("THVM_HIP_SPLIT_ROUTER");
+    const int fuse_rt = D <= 4096 && D % 4 == 0 && E <= 64 && !(sr && sr[0] == '1');
+    const int route_in_gu = fuse_rt && !grp;
+    if (fuse_rt) {
+      snprintf(p, sizeof p, "thvm-builtin:moe_gate b=%u d=%u e=%u eps=%a", B, D, E, c->eps);
+      u32 ra[5] = {xnf, gl, x, wpost, gate};
+      if (op_add(d, "gate", p, ra, 5)) return -1;
+    } else {
+      snprintf(p, sizeof p, "thvm-builtin:norm m=%u k=%u xt=%u yt=%u eps=%a", B, D, THVM_DT_BF16,
+               THVM_DT_FP32, c->eps);
+      u32 na[3] = {xnf, x, wpost};
+      if (op_add(d, "norm_post", p, na, 3)) return -1;
+      snprintf(p, sizeof p, "thvm-builtin:gemv m=%u n=%u k=%u wt=%u xt=%u yt=%u epi=0", B, E, D,
+               THVM_DT_FP32, THVM_DT_FP32, THVM_DT_FP32);
+      u32 ra[3] = {gl, xnf, gate};
+      if (op_add(d, "gemv_gate", p, ra, 3)) return -1;
+    }
+    if (!route_in_gu) {
+      snprintf(p, sizeof p, "thvm-builtin:route b=%u e=%u k=%u", B, E, K);
+      u32 rb[3] = {sel, probs, gl};
+      if (op_add(d, "route", p, rb, 3)) return -1;
+    }
+    snprintf(p, sizeof p, "thvm-builtin:moe_gateup b=%u d=%u e=%u k=%u i=%u s=%u wt=%u grouped=%d route=%d",
+             B, D, E, K, I, S, wdt, grp, route_in_gu);
+    u32 ma[12], mn = 0;
     ma[mn++] = hmoe; ma[mn++] = xnf; ma[mn++] = sel; ma[mn++] = wgue;
     if (f8) ma[mn++] = sgue;
     if (S) { ma[mn++] = wgus; if (f8) ma[mn++] = sgus; }
     if (grp) { ma[mn++] = tens_find(d, "moe.plan"); ma[mn++] = tens_find(d, "moe.live"); }
+    if (route_in_gu) { ma[mn++] = gl; ma[mn++] = probs; }
     if (op_add(d, "moe_gateup", p, ma, mn)) return -1;
     snprintf(p, sizeof p, "thvm-builtin:moe_down b=%u d=%u e=%u k=%u i=%u s=%u wt=%u grouped=%d", B, D, E,
              K, I, S, wdt, grp);

@@ -340,14 +340,32 @@ int hb_builtin_launch(const char *program, const u32 *ids, u32 n, int check_only
     if (check_only) return 0;
     if (prof) hb_kprof_begin(K, &e0, &e1);
     rc = thvm_k_route(&a, HB_STREAM, err, sizeof err);
+  } else if (strcmp(K, "moe_gate") == 0) {   /* xn, logits, x, gain, gate */
+    ThvmGateArgs a;
+    memset(&a, 0, sizeof a);
+    NEED(spec_u32(&sp, "b", &a.B, 1, 0) || spec_u32(&sp, "d", &a.D, 1, 0) ||
+         spec_u32(&sp, "e", &a.E, 1, 0) || spec_f32(&sp, "eps", &a.eps, 0, 1e-6f));
+    a.xn = (float *)arg(&c, 0, (u64)a.B * a.D * 4);
+    a.logits = (float *)arg(&c, 1, (u64)a.B * a.E * 4);
+    a.x = arg(&c, 2, (u64)a.B * a.D * 2);
+    a.w = (const float *)arg(&c, 3, (u64)a.D * 4);
+    a.gate = (const float *)arg(&c, 4, (u64)a.E * a.D * 4);
+    if (c.bad) return -1;
+    bytes = (u64)a.E * a.D * 4 + (u64)a.B * a.D * 6 + (u64)a.B * a.E * 4;
+    if (check_only) return 0;
+    if (prof) hb_kprof_begin(K, &e0, &e1);
+    rc = thvm_k_moe_gate(&a, HB_STREAM, err, sizeof err);
   } else if (strcmp(K, "moe_gateup") == 0 || strcmp(K, "moe_down") == 0) {
     ThvmMoeArgs a;
     memset(&a, 0, sizeof a);
     const int gu = strcmp(K, "moe_gateup") == 0;
+    u32 route = 0;
     NEED(spec_u32(&sp, "b", &a.B, 1, 0) || spec_u32(&sp, "d", &a.D, 1, 0) ||
          spec_u32(&sp, "e", &a.E, 1, 0) || spec_u32(&sp, "k", &a.K, 1, 0) ||
          spec_u32(&sp, "i", &a.I, 1, 0) || spec_u32(&sp, "s", &a.S, 0, 0) ||
-         spec_u32(&sp, "wt", &a.wdt, 0, THVM_DT_FP8E4M3) || spec_u32(&sp, "grouped", &a.grouped, 0, 0));
+         spec_u32(&sp, "wt", &a.wdt, 0, THVM_DT_FP8E4M3) || spec_u32(&sp, "grouped", &a.grouped, 0, 0) ||
+         spec_u32(&sp, "route", &route, 0, 0));
+    if (route && !gu) { hb_set_error("builtin moe_down: route=1 is a gate/up key"); return -1; }
     const u32 wsz = hb_dt_size(a.wdt);
     const int fp8 = a.wdt == THVM_DT_FP8E4M3;
     if (!wsz) { hb_set_error("builtin %s: bad weight dtype", K); return -1; }
@@ -356,6 +374,8 @@ int hb_builtin_launch(const char *program, const u32 *ids, u32 n, int check_only
     if (gu) {
       a.h = (float *)arg(&c, slot++, hb);
       a.x = (const float *)arg(&c, slot++, (u64)a.B * a.D * 4);
+      /* route=1: this slot receives the picked experts; logits and probs
+       * come last */
       a.sel = (const int32_t *)arg(&c, slot++, (u64)a.B * a.K * 4);
       a.wgu_e = arg(&c, slot++, (u64)a.E * 2 * a.I * a.D * wsz);
       if (fp8) a.sgu_e = (const float *)arg(&c, slot++, (u64)a.E * 2 * a.I * 4);
@@ -368,6 +388,11 @@ int hb_builtin_launch(const char *program, const u32 *ids, u32 n, int check_only
         a.plan = (int32_t *)arg(&c, slot++, thvm_k_moe_plan_bytes(a.B, a.E, a.K));
         a.live = (int32_t *)arg(&c, slot++, 4);
         bytes = 0;       /* the experts streamed are known on the device only (live) */
+      }
+      if (route) {
+        a.logits = (const float *)arg(&c, slot++, (u64)a.B * a.E * 4);
+        a.probs_out = (float *)arg(&c, slot++, (u64)a.B * a.K * 4);
+        a.sel_out = (int32_t *)a.sel;
       }
     } else {
       a.res = arg(&c, slot++, (u64)a.B * a.D * 2);

@@ -171,6 +171,18 @@ typedef struct ThvmRouteArgs {
   uint32_t B, E, K;
 } ThvmRouteArgs;
 int thvm_k_route(const ThvmRouteArgs *a, hipStream_t s, char *err, int errlen);
+/* The post-attention RMSNorm and the router GEMV of a MoE layer in one
+ * launch, bit for bit the norm (f32 out) and f32 GEMV kernels in sequence:
+ * x [B][D] bf16, w [D] f32 gain, gate [E][D] f32 (16-byte aligned) -> xn
+ * [B][D] f32 (the experts' input), logits [B][E] f32.  D <= 4096, a
+ * multiple of 4; E <= 64.  Blocks of 8 experts each renormalise the row. */
+typedef struct ThvmGateArgs {
+  const void *x; const float *w; const float *gate;
+  float *xn; float *logits;
+  uint32_t B, D, E;
+  float eps;
+} ThvmGateArgs;
+int thvm_k_moe_gate(const ThvmGateArgs *a, hipStream_t s, char *err, int errlen);
 
 /* Routed + shared expert FFN (reference moe_full_h / moe_full_out
  * :865-965).  x [B][D] f32 (rounded to bf16 as the experts' input); h
@@ -199,6 +211,12 @@ typedef struct ThvmMoeArgs {
   int32_t *plan;
   float *part;
   int32_t *live;           /* grouped gate/up: += experts with rows (optional) */
+  /* per-row gate/up with logits set: every block picks the row's top-K from
+   * logits [B][E] itself (the route kernel's arithmetic, so the same ids and
+   * probabilities) instead of reading sel; blocks x = 0 write them to
+   * sel_out / probs_out for the down kernel */
+  const float *logits;
+  int32_t *sel_out; float *probs_out;
 } ThvmMoeArgs;
 /* plan / part scratch sizes in bytes for the grouped form */
 uint64_t thvm_k_moe_plan_bytes(uint32_t B, uint32_t E, uint32_t K);

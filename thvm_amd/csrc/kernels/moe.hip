@@ -32,13 +32,17 @@
 #define MOE_MAXK 8      /* routed experts per token */
 
 // ---- router ---------------------------------------------------------------
-__global__ __launch_bounds__(64) void k_route(ThvmRouteArgs a) {
-  const uint32_t b = blockIdx.x, lane = threadIdx.x, E = a.E;
-  const float g = lane < E ? a.logits[(uint64_t)b * E + lane] : -INFINITY;
+// top-K of one row's E <= 64 logits by one wave (lane e holds logit e):
+// every lane ends with the K ids and probabilities (the butterfly leaves the
+// winner in all lanes)
+__device__ __forceinline__ void route_wave(float g, uint32_t lane, uint32_t E, uint32_t K,
+                                           int32_t (&ids)[MOE_MAXK], float (&pr)[MOE_MAXK]) {
   const float mx = wave_max(g);
   const float sum = wave_sum(lane < E ? expf(g - mx) : 0.0f);
   bool used = lane >= E;
-  for (uint32_t kk = 0; kk < a.K; kk++) {
+#pragma unroll
+  for (uint32_t kk = 0; kk < MOE_MAXK; kk++) {
+    if (kk >= K) break;
     float bv = used ? -INFINITY : g;
     int bi = used ? INT_MAX : (int)lane;
 #pragma unroll
@@ -48,11 +52,97 @@ __global__ __launch_bounds__(64) void k_route(ThvmRouteArgs a) {
       if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
     }
     if ((int)lane == bi) used = true;
-    if (lane == 0) {
-      a.sel[(uint64_t)b * a.K + kk] = bi;
-      a.probs[(uint64_t)b * a.K + kk] = expf(bv - mx) / sum;
+    ids[kk] = bi;
+    pr[kk] = expf(bv - mx) / sum;
+  }
+}
+__global__ __launch_bounds__(64) void k_route(ThvmRouteArgs a) {
+  const uint32_t b = blockIdx.x, lane = threadIdx.x, E = a.E;
+  const float g = lane < E ? a.logits[(uint64_t)b * E + lane] : -INFINITY;
+  int32_t ids[MOE_MAXK];
+  float pr[MOE_MAXK];
+  route_wave(g, lane, E, a.K, ids, pr);
+  if (lane == 0)
+#pragma unroll
+    for (uint32_t kk = 0; kk < MOE_MAXK; kk++)
+      if (kk < a.K) { a.sel[(uint64_t)b * a.K + kk] = ids[kk]; a.probs[(uint64_t)b * a.K + kk] = pr[kk]; }
+}
+
+// The post-attention RMSNorm (f32 out) and the f32 router GEMV in one
+// launch: grid (ceil(E / 8), B), 512 threads; each block renormalises its
+// row (the first 256 threads exactly as the norm kernel: the same elements
+// per thread, the same block sum over four waves, the same formula) and its
+// 8 waves take one expert each, lane l folding 16-byte chunks l, l + 64, ...
+// in order (four FMAs each) with one wave sum -- the GEMV's f32 path -- so
+// xn and the logits are those kernels' bits.  The expert row is in flight
+// before the norm starts.
+#define RT_THREADS 512
+#define RT_WAVES (RT_THREADS / 64)
+#define RT_NORM_THREADS 256
+#define RT_NREG 16       /* x elements per norm thread: D <= 4096 */
+template <int NCH>       /* 16-byte router chunks per lane: D <= 256 * NCH */
+__global__ __launch_bounds__(RT_THREADS) void k_moe_gate(ThvmGateArgs a) {
+  __shared__ __align__(16) float xs[RT_NREG * RT_NORM_THREADS];
+  __shared__ float red[RT_NORM_THREADS / 64];
+  const uint32_t b = blockIdx.y, tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const uint32_t D = a.D, E = a.E, C = D / 4;
+  const uint32_t e = blockIdx.x * RT_WAVES + wv;
+  const float4 *W = (const float4 *)a.gate;
+  uint4 wq[NCH];
+#pragma unroll
+  for (int t = 0; t < NCH; t++) {
+    const uint32_t c = lane + 64u * t;
+    wq[t] = (e < E && c < C) ? ld_stream16((const char *)(W + (uint64_t)e * C + c)) : make_uint4(0, 0, 0, 0);
+  }
+  const uint64_t xo = (uint64_t)b * D;
+  const float invK = 1.0f / (float)D;
+  float xv[RT_NREG], gw[RT_NREG];
+  if (tid < RT_NORM_THREADS) {
+#pragma unroll
+    for (int i = 0; i < RT_NREG; i++) {
+      const uint32_t k = tid + i * RT_NORM_THREADS, kc = k < D ? k : 0;
+      xv[i] = k < D ? bf2f(((const bf16_t *)a.x)[xo + k]) : 0.0f;
+      gw[i] = a.w ? a.w[kc] : 1.0f;
+    }
+    float s2 = 0.0f;
+#pragma unroll
+    for (int i = 0; i < RT_NREG; i++) s2 += xv[i] * xv[i];
+    const float w = wave_sum(s2);
+    if (lane == 0) red[wv] = w;
+  }
+  __syncthreads();
+  if (tid < RT_NORM_THREADS) {
+    float t = 0.0f;
+#pragma unroll
+    for (int i = 0; i < RT_NORM_THREADS / 64; i++) t += red[i];
+    const float inv = 1.0f / sqrtf(t * invK + a.eps);
+#pragma unroll
+    for (int i = 0; i < RT_NREG; i++) {
+      const uint32_t k = tid + i * RT_NORM_THREADS;
+      if (k < D) {
+        float v = (xv[i] - 0.0f) * inv;
+        if (a.w) v = v * gw[i];
+        xs[k] = v;
+        if (blockIdx.x == 0) a.xn[xo + k] = v;
+      }
     }
   }
+  __syncthreads();
+  const float4 *x4 = (const float4 *)xs;
+  float acc = 0.0f;
+#pragma unroll
+  for (int t = 0; t < NCH; t++) {
+    const uint32_t c = lane + 64u * t;
+    if (c < C) {
+      const float4 v4 = x4[c];
+      acc += v4.x * __uint_as_float(wq[t].x);
+      acc += v4.y * __uint_as_float(wq[t].y);
+      acc += v4.z * __uint_as_float(wq[t].z);
+      acc += v4.w * __uint_as_float(wq[t].w);
+    }
+  }
+  const float tot = wave_sum(acc);
+  if (e < E && lane == 0) a.logits[(uint64_t)b * E + e] = tot * 1.0f + 0.0f;   // the GEMV epilogue's scale, bias
 }
 
 // decode one 16-byte chunk: 16 fp8 or 8 bf16 weights
@@ -147,6 +237,19 @@ __global__ __launch_bounds__(MOE_THREADS) void k_moe_gateup(ThvmMoeArgs a) {
   const uint32_t b = blockIdx.y, D = a.D, I = a.I, K = a.K;
   const uint32_t P = K * I + a.S;
   const uint32_t lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  // the row's top-K, as the route kernel picks it, by every wave with a
+  // routed pair (no barrier before the weight loads); block 0's wave 0
+  // publishes it for the down kernel
+  int32_t rids[MOE_MAXK];
+  float rpr[MOE_MAXK];
+  const uint32_t pw0 = (blockIdx.x * MOE_WAVES + wv) * PPW;
+  if (a.logits && (pw0 < K * I || (blockIdx.x == 0 && wv == 0))) {
+    route_wave(lane < a.E ? a.logits[(uint64_t)b * a.E + lane] : -INFINITY, lane, a.E, K, rids, rpr);
+    if (blockIdx.x == 0 && wv == 0 && lane == 0)
+#pragma unroll
+      for (uint32_t kk = 0; kk < MOE_MAXK; kk++)
+        if (kk < K) { a.sel_out[(uint64_t)b * K + kk] = rids[kk]; a.probs_out[(uint64_t)b * K + kk] = rpr[kk]; }
+  }
   const uint32_t p0 = (blockIdx.x * MOE_WAVES + wv) * PPW;
   const uint64_t rowb = (uint64_t)D * (FP8 ? 1 : 2);
   const uint32_t nch = (uint32_t)(rowb / 16);
@@ -160,7 +263,13 @@ __global__ __launch_bounds__(MOE_THREADS) void k_moe_gateup(ThvmMoeArgs a) {
     const char *base;
     if (live && p < K * I) {
       const uint32_t e = p / I, r = p % I;
-      int32_t id = a.sel[(uint64_t)b * K + e];
+      int32_t id = 0;
+      if (a.logits) {
+#pragma unroll
+        for (uint32_t kk = 0; kk < MOE_MAXK; kk++) id = kk == e ? rids[kk] : id;
+      } else {
+        id = a.sel[(uint64_t)b * K + e];
+      }
       id = id < 0 ? 0 : id >= (int32_t)a.E ? (int32_t)a.E - 1 : id;   // a valid expert row
       row0[i] = (uint64_t)id * 2 * I + 2 * r;
       base = (const char *)a.wgu_e;
@@ -627,6 +736,24 @@ extern "C" int thvm_k_route(const ThvmRouteArgs *a, hipStream_t s, char *err, in
   return 0;
 }
 
+extern "C" int thvm_k_moe_gate(const ThvmGateArgs *a, hipStream_t s, char *err, int errlen) {
+  if (a->B == 0 || a->E == 0 || a->E > 64 || a->D == 0 || a->D % 4 || a->D > RT_NREG * RT_NORM_THREADS) {
+    snprintf(err, errlen, "moe_gate: need 1 <= E <= 64, D a multiple of 4 up to %d (E=%u D=%u)",
+             RT_NREG * RT_NORM_THREADS, a->E, a->D);
+    return -1;
+  }
+  if (((uintptr_t)a->gate & 15) || !a->x || !a->xn || !a->logits) {
+    snprintf(err, errlen, "moe_gate: null buffers or a router matrix not 16-byte aligned");
+    return -1;
+  }
+  const uint32_t nch = (a->D / 4 + 63) / 64;
+  void (*f)(ThvmGateArgs) = nch <= 4 ? k_moe_gate<4> : nch <= 8 ? k_moe_gate<8> : k_moe_gate<16>;
+  thvm_launch(true, true, f, dim3((a->E + RT_WAVES - 1) / RT_WAVES, a->B), dim3(RT_THREADS), 0, s, *a);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) { snprintf(err, errlen, "moe_gate launch: %s", hipGetErrorString(e)); return -1; }
+  return 0;
+}
+
 static int moe_check(const ThvmMoeArgs *a, int gateup, char *err, int errlen) {
   const uint32_t wsz = a->wdt == THVM_DT_FP8E4M3 ? 1 : a->wdt == THVM_DT_BF16 ? 2 : 0;
   if (!wsz) { snprintf(err, errlen, "moe: weights must be fp8 e4m3 or bf16"); return -1; }
@@ -662,8 +789,13 @@ static int moe_check(const ThvmMoeArgs *a, int gateup, char *err, int errlen) {
     snprintf(err, errlen, "moe: x and h must be 16-byte aligned");
     return -1;
   }
-  if (gateup ? (!a->h || !a->x || !a->sel) : (!a->h || !a->res || !a->sel || !a->probs)) {
+  if (gateup ? (!a->h || !a->x || (!a->sel && !a->logits)) : (!a->h || !a->res || !a->sel || !a->probs)) {
     snprintf(err, errlen, "moe: missing operand");
+    return -1;
+  }
+  if (a->logits && (!gateup || a->grouped || a->E > 64 || !a->sel_out || !a->probs_out)) {
+    snprintf(err, errlen, "moe: routing inside the gate/up is for the per-row form, E <= 64, "
+             "with sel_out and probs_out");
     return -1;
   }
   return 0;
