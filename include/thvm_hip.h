@@ -176,7 +176,9 @@ int thvm_hip_attn_decode_noalloc(const char *program, const uint32_t *buf_ids,
  *   BUFFER(36)      arg0 = argument slot (0 = the output), dtype = element,
  *                   arg1 = capacity in elements (> 0: every load outside
  *                   reads 0 and every store outside is dropped)
- *   INDEX_E(26)     src0 = BUFFER, src1 = element index; LOAD(21) src0 = INDEX
+ *   INDEX_E(26)     src0 = BUFFER, src1 = element index: the element's value
+ *                   (the reference's lifted DAGs read buffers this way);
+ *                   LOAD(21) src0 = INDEX is the same value
  *   STORE(37)       src0 = BUFFER slot 0, src1 = index, src2 = value (root,
  *                   the last node)
  *   CAST(23) / BITCAST(24): dtype = the target type
@@ -192,10 +194,23 @@ typedef struct ThvmUop {
 typedef struct ThvmRenderInfo {
   uint32_t n_slots;    /* argument slots: buffers 0..k-1, then the variable buffer */
   uint32_t kvar_slot;  /* slot of the int32 variable buffer, 0 = no variables */
-  uint32_t group;      /* 1: one block per output element (group reduce) */
+  uint32_t group;      /* threads per output in its reductions (1: one thread) */
   uint32_t block;      /* threads per block */
   uint64_t grid_max;   /* blocks to launch (variables at their maxima) */
+  uint32_t upcast;     /* consecutive outputs per thread */
+  uint32_t reserved;
 } ThvmRenderInfo;
+
+/* Launch geometry of a rendered kernel -- the reference's LOCAL,
+ * GROUP_REDUCE and UPCAST opts (src/thvm.h:433-437, applied by
+ * src/codegen/apply_opt.c) as the gfx950 target realises them: `block`
+ * threads per block (64..1024, a power of 2; 0 = 256), `group` consecutive
+ * threads sharing one output's reductions (a power of 2 <= block, only for
+ * un-nested reductions; 0 or 1 = one thread per output), `upcast`
+ * consecutive outputs per thread (1..8, with group 1; 0 = 1). */
+typedef struct ThvmRenderOpts {
+  uint32_t block, group, upcast, reserved;
+} ThvmRenderOpts;
 
 /* cg_render_uop_kernel_cuda_root + the CUDA dispatch geometry (reference
  * src/codegen/render_uop.c:4964-5113, src/backend/cuda/jit.c:634-787) for
@@ -205,6 +220,23 @@ typedef struct ThvmRenderInfo {
  * needed).  0 / -1. */
 int thvm_hip_render_kernel(const ThvmUop *nodes, uint32_t n, const char *name,
                            char *out, uint64_t cap, ThvmRenderInfo *info);
+/* The same with explicit opts (NULL: the target's hand-coded choice, which
+ * thvm_hip_render_kernel uses). */
+int thvm_hip_render_kernel_opts(const ThvmUop *nodes, uint32_t n, const char *name,
+                                const ThvmRenderOpts *opts, char *out, uint64_t cap,
+                                ThvmRenderInfo *info);
+/* The reference BEAM autotuner's role (src/codegen/autotune.c, candidates of
+ * src/codegen/propose.c:382-415) on the device: search the opts of one
+ * kernel over its own argument buffers (ids as thvm_hip_dispatch_custom
+ * takes them; the kernel must not read its output), each candidate timed
+ * over `reps` launches (0 = 20) and kept only when its output matches the
+ * hand-coded choice's (floats 1e-5 relative, integers exactly).  Writes the
+ * fastest opts and the two mean launch times; the output buffer holds the
+ * winner's result.  Winners are cached by the rows' hash, in the process and
+ * under $THVM_HIP_CACHE_DIR/tune/.  0 / -1. */
+int thvm_hip_render_autotune(const ThvmUop *nodes, uint32_t n, const uint32_t *buf_ids,
+                             uint32_t n_args, uint32_t reps, ThvmRenderOpts *best,
+                             double *best_us, double *base_us);
 
 /* ===================== JIT capture / replay ============================ */
 /* The reference capture API (src/jit/capture.c:644-745, 2687-2884) restricted

@@ -9,9 +9,13 @@
  * Exposed:
  *   codecs    src/dtype/fp_convert.c, src/dtype/fp8.c
  *   xexp2f    src/codegen/xexp2f.c (the CPU JIT's exp2)
- *   linear / softmax / layernorm / rmsnorm on f32 through the reference's
- *             own Tensor graph + rangeify + CPU JIT (src/nn/dot.c,
- *             src/nn/softmax.c, src/nn/layernorm.c, py/thvm/nn.py:211-224). */
+ *   linear / softmax / layernorm / rmsnorm / gelu / causal attention on f32
+ *             through the reference's own Tensor graph + rangeify + CPU JIT
+ *             (src/nn/dot.c, src/nn/softmax.c, src/nn/layernorm.c,
+ *             src/nn/elementwise.c, src/nn/scaled_dot_product_attention.c,
+ *             py/thvm/nn.py:211-224)
+ *   capture   every kernel those dispatch: its lifted DAG as renderer rows,
+ *             its input buffers and the reference CPU output. */
 #include THVM_REF_TU
 
 u8  ref_f32_to_fp8e4m3(f32 v)      { return f32_to_fp8e4m3(v); }
@@ -113,4 +117,335 @@ int ref_dense_silu_mul_bf16(const u16 *g, const u16 *u, u16 *h, u32 n) {
   u32 tid = (u32)term_val(r);
   if (TENS[tid].view.numel != n || TENS[tid].dtype != DT_BF16) return -2;
   return TENS[tid].backend->buf_read(TENS[tid].buf_id, h, (u64)n * 2);
+}
+
+/* ---- kernel capture ------------------------------------------------------
+ * While capture is on, every kernel the reference CPU path dispatches passes
+ * through cap_dispatch, installed in the CPU Backend vtable's dispatch_kernel
+ * slot (src/thvm.h:818): it flattens the kernel's lifted DAG
+ * (KernelEntry.cached_lift.store_root, src/thvm.h:1023) into rows of the
+ * renderer's ThvmUop layout (sources before users), copies the kernel's
+ * input buffers, runs the reference dispatch, and copies its output.  The
+ * rows and buffers are the renderer target's test vectors.
+ * Row payloads: CONST arg0 = bits; RANGE arg0..2 = axis id, KAX type,
+ * extent; REDUCE src1..3 = the RANGE rows reduced, arg0 = kind; BUFFER
+ * arg0 = slot (the DAG's instance: 0 output, i+1 input i), arg1 = element
+ * count; CAST / BITCAST dtype = target.  OPT annotations (src/thvm.h:439-451)
+ * are recorded per kernel and flattened through to their target. */
+typedef struct { uint32_t op, dtype; int32_t src[4]; int64_t arg[4]; } RefUop;
+#define CAP_K 96
+#define CAP_ROWS 4096
+#define CAP_SLOTS 16
+typedef struct {
+  RefUop rows[CAP_ROWS];
+  Term terms[CAP_ROWS];
+  u32 n;
+  u32 n_slots;                       /* 1 + inputs */
+  u32 dt[CAP_SLOTS];
+  u64 numel[CAP_SLOTS];
+  void *buf[CAP_SLOTS];              /* slot 0: the output after the dispatch */
+  u32 n_opt, opt_kind[8], opt_factor[8];
+  int ok;
+  char why[96];
+} CapK;
+static CapK *CAPS;
+static u32 NCAPS;
+static int CAP_ON;
+static int (*CAP_ORIG)(KernelEntry *, u32 *, u32);
+
+static int cap_find(CapK *c, Term t) {
+  for (u32 i = 0; i < c->n; i++)
+    if (c->terms[i] == t) return (int)i;
+  return -1;
+}
+static int cap_row(CapK *c, Term t, u32 op, u32 dt) {
+  if (c->n >= CAP_ROWS) { c->ok = 0; snprintf(c->why, sizeof c->why, "over %d rows", CAP_ROWS); return -1; }
+  RefUop *r = &c->rows[c->n];
+  memset(r, 0, sizeof *r);
+  r->op = op; r->dtype = dt;
+  r->src[0] = r->src[1] = r->src[2] = r->src[3] = -1;
+  c->terms[c->n] = t;
+  return (int)c->n++;
+}
+static int cap_flat(CapK *c, Term t) {
+  if (!c->ok) return -1;
+  if (term_tag(t) != TAG_UOP) { c->ok = 0; snprintf(c->why, sizeof c->why, "a non-UOP term (tag %u)", term_tag(t)); return -1; }
+  const int have = cap_find(c, t);
+  if (have >= 0) return have;
+  const u32 op = term_ext(t);
+  const u64 loc = term_val(t);
+  u32 dt = DT_FP32;
+  (void)term_dtype_in(t, 0, &dt);
+  int s[3] = {-1, -1, -1}, r;
+  switch (op) {
+    case UOP_CONST: {
+      r = cap_row(c, t, op, term_ext(heap_read(loc)));
+      if (r >= 0) c->rows[r].arg[0] = (i64)(u32)term_val(heap_read(loc));
+      return r;
+    }
+    case UOP_RANGE: {
+      const u32 ext = (u32)term_val(heap_read(loc + 2));
+      if (kvar_extent_is_var(ext)) { c->ok = 0; snprintf(c->why, sizeof c->why, "a symbolic extent"); return -1; }
+      r = cap_row(c, t, op, DT_INT32);
+      if (r >= 0) {
+        c->rows[r].arg[0] = (i64)term_val(heap_read(loc));
+        c->rows[r].arg[1] = (i64)term_val(heap_read(loc + 1));
+        c->rows[r].arg[2] = (i64)kvar_extent_static(ext);
+      }
+      return r;
+    }
+    case UOP_BUFFER: {
+      if (term_val(heap_read(loc)) != UOP_SCOPE_GLOBAL) { c->ok = 0; snprintf(c->why, sizeof c->why, "a non-global buffer"); return -1; }
+      const u32 inst = (u32)term_val(heap_read(loc + 3));
+      r = cap_row(c, t, op, (u32)term_val(heap_read(loc + 1)));
+      if (r >= 0) { c->rows[r].arg[0] = inst; c->rows[r].arg[1] = inst < CAP_SLOTS ? (i64)c->numel[inst] : 0; }
+      return r;
+    }
+    case UOP_OPT: {
+      if (c->n_opt < 8) {
+        c->opt_kind[c->n_opt] = (u32)term_val(heap_read(loc + 1));
+        c->opt_factor[c->n_opt] = (u32)term_val(heap_read(loc + 2));
+        c->n_opt++;
+      }
+      return cap_flat(c, heap_read(loc));
+    }
+    case UOP_REDUCE: {
+      s[0] = cap_flat(c, heap_read(loc));
+      const u32 nax = (u32)term_val(heap_read(loc + 2));
+      if (s[0] < 0) return -1;
+      if (nax == 0 || nax > 3) { c->ok = 0; snprintf(c->why, sizeof c->why, "a reduce over %u axes", nax); return -1; }
+      r = cap_row(c, t, op, dt);
+      if (r < 0) return -1;
+      c->rows[r].src[0] = s[0];
+      c->rows[r].arg[0] = (i64)term_val(heap_read(loc + 1));
+      for (u32 k = 0; k < nax; k++) {
+        const i64 axis = (i64)term_val(heap_read(loc + 3 + k));
+        int found = -1;
+        for (u32 j = 0; j < c->n; j++)
+          if (c->rows[j].op == UOP_RANGE && c->rows[j].arg[0] == axis) { found = (int)j; break; }
+        if (found < 0) { c->ok = 0; snprintf(c->why, sizeof c->why, "a reduce axis %lld no RANGE reads", (long long)axis); return -1; }
+        c->rows[r].src[1 + k] = found;
+      }
+      return r;
+    }
+    case UOP_CAST: case UOP_BITCAST: {
+      s[0] = cap_flat(c, heap_read(loc));
+      if (s[0] < 0) return -1;
+      r = cap_row(c, t, op, (u32)term_val(heap_read(loc + 1)));
+      if (r >= 0) c->rows[r].src[0] = s[0];
+      return r;
+    }
+    case UOP_NEG: case UOP_RECIP: case UOP_EXP2: case UOP_LOG2: case UOP_SQRT: case UOP_SIN:
+    case UOP_LOAD: {
+      s[0] = cap_flat(c, heap_read(loc));
+      if (s[0] < 0) return -1;
+      r = cap_row(c, t, op, dt);
+      if (r >= 0) c->rows[r].src[0] = s[0];
+      return r;
+    }
+    case UOP_IWHERE: case UOP_STORE: {
+      for (int k = 0; k < 3; k++) if ((s[k] = cap_flat(c, heap_read(loc + k))) < 0) return -1;
+      /* a select between index values is index arithmetic */
+      if (op == UOP_IWHERE && c->rows[s[1]].dtype == DT_INT32 && c->rows[s[2]].dtype == DT_INT32) dt = DT_INT32;
+      r = cap_row(c, t, op, dt);
+      if (r >= 0) for (int k = 0; k < 3; k++) c->rows[r].src[k] = s[k];
+      return r;
+    }
+    case UOP_ADD: case UOP_MUL: case UOP_CMPLT: case UOP_CMPEQ: case UOP_INDEX_E:
+    case UOP_IADD: case UOP_ISUB: case UOP_IMUL: case UOP_IDIV: case UOP_IMOD: case UOP_ILT:
+    case UOP_IAND: case UOP_IOR: case UOP_IXOR: case UOP_ISHL: case UOP_ISHR: case UOP_POW: {
+      for (int k = 0; k < 2; k++) if ((s[k] = cap_flat(c, heap_read(loc + k))) < 0) return -1;
+      /* the I* ops are index arithmetic: int32 (term_dtype_in reports the
+       * kernel's value type for them) */
+      if (op >= UOP_IADD && op != UOP_INDEX_E && op != UOP_POW) dt = DT_INT32;
+      r = cap_row(c, t, op, dt);
+      if (r >= 0) { c->rows[r].src[0] = s[0]; c->rows[r].src[1] = s[1]; }
+      return r;
+    }
+    default:
+      c->ok = 0;
+      snprintf(c->why, sizeof c->why, "op %u", op);
+      return -1;
+  }
+}
+
+/* The reference renderer folds the inner half of a split reduce axis -- an
+ * UNROLL / UPCAST RANGE that the store address does not read -- into the
+ * innermost REDUCE whose source reads it (render_uop.c:3080-3100,
+ * 3946-3970, tinygrad's expand_reduce).  The rows make that explicit: such a
+ * RANGE is appended to that REDUCE's axes. */
+static void cap_fold_split_axes(CapK *c) {
+  const u32 n = c->n;
+  u64 *dep = (u64 *)calloc(n, sizeof(u64));      /* RANGE rows read, as bits of rng[] */
+  int rng[64], nr = 0;
+  if (!dep) { c->ok = 0; return; }
+  for (u32 i = 0; i < n; i++) {
+    const RefUop *u = &c->rows[i];
+    if (u->op == UOP_RANGE) {
+      if (nr >= 64) { c->ok = 0; snprintf(c->why, sizeof c->why, "over 64 ranges"); free(dep); return; }
+      rng[nr] = (int)i;
+      dep[i] = 1ull << nr++;
+      continue;
+    }
+    for (int k = 0; k < 4; k++)
+      if (u->src[k] >= 0 && !(u->op == UOP_REDUCE && k > 0)) dep[i] |= dep[u->src[k]];
+  }
+  const RefUop *st = &c->rows[n - 1];
+  const u64 addr = st->op == UOP_STORE && st->src[1] >= 0 ? dep[st->src[1]] : 0;
+  u64 owned = 0;
+  for (u32 i = 0; i < n && c->ok; i++) {
+    RefUop *u = &c->rows[i];
+    if (u->op != UOP_REDUCE) continue;
+    u64 named = 0;
+    for (int k = 1; k < 4; k++)
+      for (int j = 0; j < nr; j++)
+        if (u->src[k] == rng[j]) named |= 1ull << j;
+    owned |= named;
+    for (int j = 0; j < nr; j++) {
+      const RefUop *rg = &c->rows[rng[j]];
+      const u64 b = 1ull << j;
+      if ((rg->arg[1] != KAX_UNROLL && rg->arg[1] != KAX_UPCAST) || (addr & b) || (owned & b) ||
+          !(dep[u->src[0]] & b))
+        continue;
+      int slot = -1;
+      for (int k = 1; k < 4; k++) if (u->src[k] < 0) { slot = k; break; }
+      if (slot < 0) { c->ok = 0; snprintf(c->why, sizeof c->why, "a reduce over more than 3 axes"); break; }
+      u->src[slot] = rng[j];
+      owned |= b;
+    }
+    /* the reduce's own value no longer depends on its axes */
+    for (int k = 1; k < 4; k++)
+      for (int j = 0; j < nr; j++)
+        if (u->src[k] == rng[j]) dep[i] &= ~(1ull << j);
+  }
+  free(dep);
+}
+
+static void *cap_copy(u32 buf_id, u32 dt, u64 numel) {
+  const u64 nb = dtype_storage_bytes(dt, numel);
+  void *p = malloc(nb ? nb : 1);
+  if (p && nb && CPU_BACKEND.buf_read(buf_id, p, nb) != 0) { free(p); return NULL; }
+  return p;
+}
+
+static void *cap_gather(u32 buf_id, u32 dt, u64 buf_numel, const View *v) {
+  const u64 es = dtype_storage_bytes(dt, 1);
+  char *raw = (char *)cap_copy(buf_id, dt, buf_numel), *out = (char *)malloc(v->numel * es + 1);
+  if (!raw || !out) { free(raw); free(out); return NULL; }
+  for (u64 e = 0; e < v->numel; e++) {
+    u64 q = e;
+    i64 at = v->offset;
+    for (int d = (int)v->shape.ndim - 1; d >= 0; d--) {
+      const u32 ext = v->shape.dims[d];
+      at += (i64)(q % ext) * v->strides[d];
+      q /= ext;
+    }
+    if (at < 0 || (u64)at >= buf_numel) { free(raw); free(out); return NULL; }
+    memcpy(out + e * es, raw + (u64)at * es, es);
+  }
+  free(raw);
+  return out;
+}
+
+static int cap_dispatch(KernelEntry *ke, u32 *in_ids, u32 out_id) {
+  CapK *c = NULL;
+  if (CAP_ON && NCAPS < CAP_K && !kernel_is_custom(ke) && ke->cached_lift.store_root != 0) {
+    c = &CAPS[NCAPS++];
+    memset(c, 0, sizeof *c);
+    c->ok = 1;
+    c->n_slots = 1 + ke->n_inputs;
+    if (c->n_slots > CAP_SLOTS) { c->ok = 0; snprintf(c->why, sizeof c->why, "%u inputs", ke->n_inputs); }
+    /* a slot holds its whole buffer (a composed strided view indexes it) */
+    c->dt[0] = ke->output_dtype;
+    c->numel[0] = CPU_BUFS[out_id].req_nbytes / dtype_storage_bytes(ke->output_dtype, 1);
+    for (u32 i = 0; c->ok && i < ke->n_inputs; i++) {
+      c->dt[1 + i] = ke->input_dtypes[i];
+      c->numel[1 + i] = CPU_BUFS[in_ids[i]].req_nbytes / dtype_storage_bytes(ke->input_dtypes[i], 1);
+      const int composed = ke->input_chain_composed ? ke->input_chain_composed[i] : 0;
+      const View *v = &ke->input_views[i];
+      const u32 tid = ke->input_tids ? ke->input_tids[i] : 0;
+      if (!composed && !v->contiguous) {
+        /* a single strided view: the DAG indexes it in its logical
+         * row-major order and the reference's renderer maps that index
+         * through the view (KernelEntry.input_views, src/thvm.h:958-969);
+         * the slot holds the view gathered in that order */
+        if (tid == 0 || TENS[tid].nviews != 0) {
+          c->ok = 0;
+          snprintf(c->why, sizeof c->why, "input %u is a chain of views", i);
+          break;
+        }
+        c->buf[1 + i] = cap_gather(in_ids[i], c->dt[1 + i], c->numel[1 + i], v);
+        c->numel[1 + i] = v->numel;
+        if (!c->buf[1 + i]) { c->ok = 0; snprintf(c->why, sizeof c->why, "input %u gather failed", i); break; }
+        continue;
+      }
+      c->buf[1 + i] = cap_copy(in_ids[i], c->dt[1 + i], c->numel[1 + i]);
+    }
+    if (c->ok) cap_flat(c, ke->cached_lift.store_root);
+    if (c->ok) cap_fold_split_axes(c);
+  }
+  const int rc = CAP_ORIG(ke, in_ids, out_id);
+  if (c && c->ok) c->buf[0] = cap_copy(out_id, c->dt[0], c->numel[0]);
+  return rc;
+}
+
+int ref_capture_begin(void) {
+  ref_init();
+  if (!CAPS) CAPS = (CapK *)calloc(CAP_K, sizeof(CapK));
+  if (!CAPS) return -1;
+  for (u32 k = 0; k < NCAPS; k++)
+    for (u32 s = 0; s < CAP_SLOTS; s++) { free(CAPS[k].buf[s]); CAPS[k].buf[s] = NULL; }
+  NCAPS = 0;
+  if (!CAP_ORIG) { CAP_ORIG = CPU_BACKEND.dispatch_kernel; CPU_BACKEND.dispatch_kernel = cap_dispatch; }
+  CAP_ON = 1;
+  return 0;
+}
+int ref_capture_end(void) { CAP_ON = 0; return (int)NCAPS; }
+/* kernel k: rows (n), slot count, opts; status 1 = captured, 0 = not (why) */
+int ref_capture_kernel(u32 k, RefUop *rows, u32 cap, u32 *n, u32 *n_slots, u32 *opts, u32 *n_opt,
+                       char *why, u32 whylen) {
+  if (k >= NCAPS) return -1;
+  CapK *c = &CAPS[k];
+  *n = c->n; *n_slots = c->n_slots; *n_opt = c->n_opt;
+  for (u32 i = 0; i < c->n_opt; i++) { opts[2 * i] = c->opt_kind[i]; opts[2 * i + 1] = c->opt_factor[i]; }
+  snprintf(why, whylen, "%s", c->why);
+  if (c->ok && c->n <= cap) memcpy(rows, c->rows, c->n * sizeof(RefUop));
+  return c->ok;
+}
+/* slot s of kernel k: dtype, element count and (dst != NULL) the bytes */
+int ref_capture_slot(u32 k, u32 s, u32 *dt, u64 *numel, void *dst, u64 cap) {
+  if (k >= NCAPS || s >= CAPS[k].n_slots || s >= CAP_SLOTS) return -1;
+  CapK *c = &CAPS[k];
+  *dt = c->dt[s]; *numel = c->numel[s];
+  if (!dst) return 0;
+  const u64 nb = dtype_storage_bytes(c->dt[s], c->numel[s]);
+  if (!c->buf[s] || nb > cap) return -1;
+  memcpy(dst, c->buf[s], nb);
+  return 0;
+}
+
+/* GELU (tanh form) and scaled dot-product attention on f32 through the
+ * reference Tensor graph (src/nn/elementwise.c, src/nn/scaled_dot_product_attention.c) */
+int ref_gelu_f32(const float *x, float *y, u32 M, u32 K) {
+  ref_init();
+  return ref_read(nn_elementwise(NN_GELU, ref_tensor2(M, K, x)), y, (u64)M * K);
+}
+static Tensor ref_tensor3(u32 d0, u32 d1, u32 d2, const float *data) {
+  Shape sh = {0};
+  sh.ndim = 3; sh.dims[0] = d0; sh.dims[1] = d1; sh.dims[2] = d2;
+  u32 tid = tensor_alloc(&CPU_BACKEND, sh, DT_FP32);
+  CPU_BACKEND.buf_write(TENS[tid].buf_id, (void *)data, (u64)d0 * d1 * d2 * 4);
+  Tensor t;
+  t.t = term_new(0, TAG_TEN, DT_FP32, tid);
+  t.dtype = DT_FP32;
+  t.shape = sh;
+  return t;
+}
+/* q, k, v [H][T][hd] -> out [H][T][hd], causal */
+int ref_sdpa_f32(const float *q, const float *k, const float *v, float *out, u32 H, u32 T, u32 hd) {
+  ref_init();
+  Tensor Q = ref_tensor3(H, T, hd, q), Kt = ref_tensor3(H, T, hd, k), Vt = ref_tensor3(H, T, hd, v);
+  Tensor none;
+  memset(&none, 0, sizeof none);
+  return ref_read(nn_scaled_dot_product_attention(Q, Kt, Vt, none, 1), out, (u64)H * T * hd);
 }

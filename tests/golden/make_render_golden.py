@@ -1,0 +1,102 @@
+"""Write tests/golden/ref_lifted_kernels.npz: every kernel the compiled
+reference schedules for a set of GPT-2 step operations on f32 (linear,
+softmax, layernorm, RMSNorm, GELU, causal attention), captured at its CPU
+dispatch by oracle/ref_harness.c (ref_capture_*): the kernel's lifted DAG as
+renderer rows (op, dtype, src0..3, arg0..3; the reference's UOP_* and DT_*
+numbers), its input buffers, the reference CPU output and the OPT
+annotations the reference's hand opts attached.  Data only: the rows are the
+reference's own DAGs, the buffers its own inputs and outputs.
+
+Run in the build container (the reference tree is not on the GPU box):
+    make -C oracle && python tests/golden/make_render_golden.py
+"""
+import ctypes as C
+import sys
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parents[2]
+sys.path.insert(0, str(ROOT / "tests"))
+import _oracle as O  # noqa: E402
+
+OUT = Path(__file__).with_name("ref_lifted_kernels.npz")
+MAXROWS = 4096
+
+
+class RefUop(C.Structure):
+    _fields_ = [("op", C.c_uint32), ("dtype", C.c_uint32), ("src", C.c_int32 * 4), ("arg", C.c_int64 * 4)]
+
+
+def scenarios(rng):
+    M, K, N = 4, 64, 32
+    x = rng.standard_normal((M, K)).astype(np.float32)
+    w = rng.standard_normal((N, K)).astype(np.float32)
+    H, T, hd = 2, 8, 16
+    q, k, v = (rng.standard_normal((H, T, hd)).astype(np.float32) for _ in range(3))
+    ym, yk = np.empty((M, N), np.float32), np.empty((M, K), np.float32)
+    o = np.empty((H, T, hd), np.float32)
+    keep = [x, w, q, k, v, ym, yk, o]
+    L = O.ref()
+    return keep, [
+        ("linear", lambda: L.ref_linear_f32(x.ctypes.data, w.ctypes.data, ym.ctypes.data, M, N, K)),
+        ("softmax", lambda: L.ref_softmax_f32(x.ctypes.data, yk.ctypes.data, M, K)),
+        ("layernorm", lambda: L.ref_layernorm_f32(x.ctypes.data, yk.ctypes.data, M, K, 1e-5)),
+        ("rmsnorm", lambda: L.ref_rmsnorm_f32(x.ctypes.data, yk.ctypes.data, M, K, 1e-6)),
+        ("gelu", lambda: L.ref_gelu_f32(x.ctypes.data, yk.ctypes.data, M, K)),
+        ("attention", lambda: L.ref_sdpa_f32(q.ctypes.data, k.ctypes.data, v.ctypes.data, o.ctypes.data, H, T, hd)),
+    ]
+
+
+def main():
+    L = O.ref()
+    if L is None:
+        raise SystemExit("oracle/_ref/libref.so is not built (make -C oracle)")
+    rng = np.random.default_rng(20261202)
+    keep, scen = scenarios(rng)
+    out, names, skipped = {}, [], []
+    kid = 0
+    for name, fn in scen:
+        L.ref_capture_begin()
+        rc = fn()
+        n = L.ref_capture_end()
+        if rc != 0:
+            raise SystemExit(f"{name}: the reference returned {rc}")
+        for k in range(n):
+            rows = (RefUop * MAXROWS)()
+            nn, ns, no = C.c_uint32(), C.c_uint32(), C.c_uint32()
+            opts = (C.c_uint32 * 16)()
+            why = C.create_string_buffer(96)
+            st = L.ref_capture_kernel(k, C.cast(rows, C.c_void_p), MAXROWS, C.byref(nn), C.byref(ns),
+                                      C.cast(opts, C.c_void_p), C.byref(no), why, 96)
+            if st != 1:
+                skipped.append(f"{name} kernel {k}: {why.value.decode()}")
+                continue
+            r = np.array([[u.op, u.dtype, *u.src, *u.arg] for u in rows[:nn.value]], np.int64)
+            dts, numels = [], []
+            for s in range(ns.value):
+                dt, ne = C.c_uint32(), C.c_uint64()
+                L.ref_capture_slot(k, s, C.byref(dt), C.byref(ne), None, 0)
+                nb = int(ne.value) * {13: 4, 12: 2, 11: 2, 5: 4, 6: 4, 0: 1, 7: 8}[dt.value]
+                b = np.empty(nb, np.uint8)
+                if L.ref_capture_slot(k, s, C.byref(dt), C.byref(ne), b.ctypes.data, nb) != 0:
+                    raise SystemExit(f"{name} kernel {k}: slot {s} unreadable")
+                out[f"k{kid}_slot{s}"] = b
+                dts.append(dt.value)
+                numels.append(ne.value)
+            out[f"k{kid}_rows"] = r
+            out[f"k{kid}_dt"] = np.array(dts, np.uint32)
+            out[f"k{kid}_numel"] = np.array(numels, np.uint64)
+            out[f"k{kid}_opts"] = np.array([[opts[2 * i], opts[2 * i + 1]] for i in range(no.value)],
+                                           np.uint32).reshape(-1, 2)
+            names.append(f"{name}/{k}")
+            kid += 1
+    out["names"] = np.array(names)
+    out["skipped"] = np.array(skipped)
+    np.savez_compressed(OUT, **out)
+    print(f"{OUT}: {kid} kernels ({len(skipped)} skipped: {skipped})")
+    del keep
+
+
+if __name__ == "__main__":
+    main()

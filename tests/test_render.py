@@ -58,15 +58,46 @@ def row_sum_dag(n_rows, n_cols, symbolic=False):
 
 def test_render_group_and_thread_geometry(tmp_path):
     src, info = hip.render_kernel(row_sum_dag(8, 1024), "k_rowsum")
-    assert info.group == 1 and info.grid_max == 8 and info.block == 256 and info.kvar_slot == 0
+    assert info.group == 256 and info.grid_max == 8 and info.block == 256 and info.kvar_slot == 0
     assert "wsum(" in src and "__syncthreads" in src and "extern \"C\" __global__" in src
     # the row offset does not read the reduce axis: hoisted out of the loop
     loop = src.index("for (int rr")
     assert src.index("((int)v") < loop
     compile_ok(src, tmp_path)
     src2, info2 = hip.render_kernel(row_sum_dag(1000, 16), "k_rowsum_small")
-    assert info2.group == 0 and info2.grid_max == (1000 + 255) // 256
+    assert info2.group == 1 and info2.grid_max == (1000 + 255) // 256
     assert "for (int a1 = 0; a1 < 16; a1++)" in src2
+
+
+@pytest.mark.parametrize("opts,group,grid", [((128, 8, 1), 8, (1000 + 15) // 16), ((64, 64, 1), 64, 1000),
+                                             ((512, 256, 1), 256, 500), ((256, 1, 4), 1, 1),
+                                             ((1024, 1024, 1), 1024, 1000)])
+def test_render_opts_geometry(tmp_path, opts, group, grid):
+    """The LOCAL / GROUP_REDUCE / UPCAST opts: block threads, group threads per
+    output (xor shuffles inside a wave, LDS across waves), upcast outputs per
+    thread; each variant compiles for gfx950."""
+    src, info = hip.render_kernel(row_sum_dag(1000, 1024), "k_opts", opts=opts)
+    assert (info.block, info.group, info.upcast, info.grid_max) == (opts[0], group, opts[2], grid)
+    if group > 64:
+        assert "__syncthreads" in src and "act_" in src
+    elif group > 1:
+        assert "__shfl_xor" in src and "__syncthreads" not in src
+    if opts[2] > 1:
+        assert "for (int uj_ = 0; uj_ < 4; uj_++)" in src
+    compile_ok(src, tmp_path)
+
+
+def test_render_opts_refused():
+    for opts in ((96, 1, 1), (64, 128, 1), (256, 4, 2), (256, 1, 16)):
+        with pytest.raises(hip.ThvmHipError):
+            hip.render_kernel(row_sum_dag(8, 1024), "k_bad", opts=opts)
+    # a group needs a reduction: out[i] = x[i] * x[i]
+    F, I = 13, 5
+    ew = [(BUFFER, F, (), (0, 64)), (BUFFER, F, (), (1, 64)), (RANGE, I, (), (0, 5, 64)),
+          (INDEX, I, (1, 2), ()), (LOAD, F, (3,), ()), (MUL, F, (4, 4), ()), (STORE, F, (0, 2, 5), ())]
+    hip.render_kernel(ew, "k_ew")
+    with pytest.raises(hip.ThvmHipError):
+        hip.render_kernel(ew, "k_bad2", opts=(256, 8, 1))
 
 
 def test_render_symbolic_extent_reads_variable_buffer(tmp_path):
@@ -128,7 +159,8 @@ def test_lowering_softmax_is_three_kernels(fake_host):
     T, rendered = fake_host
     x = T.Tensor(np.zeros((4, 1000), np.float32))
     x.softmax(-1).realize()
-    assert [r[1].group for r in rendered] == [1, 1, 0]      # max, sum(exp), normalise
+    # max and sum(exp) share each row among threads (hand-coded: 1000 / 4 -> 128), normalise is elementwise
+    assert [r[1].group for r in rendered] == [128, 128, 1]
 
 
 def test_lowering_fuses_elementwise_and_mean(fake_host):
@@ -136,10 +168,10 @@ def test_lowering_fuses_elementwise_and_mean(fake_host):
     a = T.Tensor(np.zeros((2, 512), np.float32))
     b = T.Tensor(np.zeros((512,), np.float32))
     ((a * 2.0 + b).exp() - 1.0).realize()
-    assert len(rendered) == 1 and rendered[0][1].group == 0
+    assert len(rendered) == 1 and rendered[0][1].group == 1
     rendered.clear()
     a.mean(-1).realize()                                     # sum and scale in one kernel
-    assert len(rendered) == 1 and rendered[0][1].group == 1
+    assert len(rendered) == 1 and rendered[0][1].group == 128
 
 
 def test_lowering_symbolic_shrink(fake_host):

@@ -58,7 +58,14 @@ class Uop(C.Structure):
 class RenderInfo(C.Structure):
     """ThvmRenderInfo (include/thvm_hip.h)."""
     _fields_ = [("n_slots", C.c_uint32), ("kvar_slot", C.c_uint32), ("group", C.c_uint32),
-                ("block", C.c_uint32), ("grid_max", C.c_uint64)]
+                ("block", C.c_uint32), ("grid_max", C.c_uint64), ("upcast", C.c_uint32),
+                ("reserved", C.c_uint32)]
+
+
+class RenderOpts(C.Structure):
+    """ThvmRenderOpts (include/thvm_hip.h): block, group, upcast."""
+    _fields_ = [("block", C.c_uint32), ("group", C.c_uint32), ("upcast", C.c_uint32),
+                ("reserved", C.c_uint32)]
 
 
 _u32, _u64, _i32, _vp, _cp, _d = C.c_uint32, C.c_uint64, C.c_int, C.c_void_p, C.c_char_p, C.c_double
@@ -86,6 +93,10 @@ _SIGS = {
     "thvm_hip_program_check": (_i32, [_cp, _cp]),
     "thvm_hip_attn_decode_noalloc": (_i32, [_cp, _vp, _u32]),
     "thvm_hip_render_kernel": (_i32, [C.POINTER(Uop), _u32, _cp, _vp, _u64, C.POINTER(RenderInfo)]),
+    "thvm_hip_render_kernel_opts": (_i32, [C.POINTER(Uop), _u32, _cp, C.POINTER(RenderOpts), _vp, _u64,
+                                           C.POINTER(RenderInfo)]),
+    "thvm_hip_render_autotune": (_i32, [C.POINTER(Uop), _u32, _vp, _u32, _u32, C.POINTER(RenderOpts),
+                                        C.POINTER(_d), C.POINTER(_d)]),
     "thvm_hip_jit_capture_begin": (_u32, []), "thvm_hip_jit_capture_end": (None, []),
     "thvm_hip_jit_capture_op_count": (_u32, [_u32]), "thvm_hip_jit_replay": (_i32, [_u32]),
     "thvm_hip_jit_rebind": (_i32, [_u32, _vp, _vp, _u32]),
@@ -384,10 +395,7 @@ def kprof_query(tag: str) -> tuple[float, int]:
     return ms, n.value
 
 
-def render_kernel(nodes, name: str, cap: int = 1 << 20) -> tuple[str, RenderInfo]:
-    """HIP source + launch geometry of one lifted-DAG kernel (the renderer
-    target, reference src/codegen/render_uop.c:4964-5113).  `nodes` is a
-    sequence of (op, dtype, (src..), (arg..)) in topological order."""
+def _uops(nodes):
     arr = (Uop * len(nodes))()
     for i, (op, dt, srcs, args) in enumerate(nodes):
         u = arr[i]
@@ -395,11 +403,37 @@ def render_kernel(nodes, name: str, cap: int = 1 << 20) -> tuple[str, RenderInfo
         for k in range(4):
             u.src[k] = srcs[k] if k < len(srcs) else -1
             u.arg[k] = args[k] if k < len(args) else 0
+    return arr
+
+
+def render_kernel(nodes, name: str, cap: int = 1 << 20, opts=None) -> tuple[str, RenderInfo]:
+    """HIP source + launch geometry of one lifted-DAG kernel (the renderer
+    target, reference src/codegen/render_uop.c:4964-5113).  `nodes` is a
+    sequence of (op, dtype, (src..), (arg..)) in topological order; `opts`
+    (block, group, upcast) overrides the hand-coded geometry."""
+    arr = _uops(nodes)
     buf = C.create_string_buffer(cap)
     info = RenderInfo()
-    _check(lib().thvm_hip_render_kernel(arr, len(nodes), name.encode(), buf, cap, C.byref(info)),
-           "render_kernel")
+    if opts is None:
+        rc = lib().thvm_hip_render_kernel(arr, len(nodes), name.encode(), buf, cap, C.byref(info))
+    else:
+        o = RenderOpts(*[int(v) for v in opts], 0)
+        rc = lib().thvm_hip_render_kernel_opts(arr, len(nodes), name.encode(), C.byref(o), buf, cap,
+                                               C.byref(info))
+    _check(rc, "render_kernel")
     return buf.value.decode(), info
+
+
+def render_autotune(nodes, args, reps: int = 20):
+    """Device search of a kernel's (block, group, upcast) over its argument
+    buffers (reference src/codegen/autotune.c): returns (opts, best_us,
+    hand_coded_us); the output buffer holds the winner's result."""
+    arr = _uops(nodes)
+    ids = _u32arr([a.id if isinstance(a, Buffer) else int(a) for a in args])
+    best, bu, hu = RenderOpts(), C.c_double(), C.c_double()
+    _check(lib().thvm_hip_render_autotune(arr, len(nodes), ids, len(args), reps, C.byref(best),
+                                          C.byref(bu), C.byref(hu)), "render_autotune")
+    return (best.block, best.group, best.upcast), bu.value, hu.value
 
 
 def kprof_bytes(tag: str) -> int:

@@ -19,7 +19,7 @@ OBJ = PKG / "_build"
 LIB = PKG / "lib" / "libthvm_hip.so"
 ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
 
-C_SOURCES = ["hip_backend.c", "hip_custom.c", "decoder.c", "render.c", "serve.c", "loader.c"]
+C_SOURCES = ["hip_backend.c", "hip_custom.c", "decoder.c", "render.c", "tune.c", "serve.c", "loader.c"]
 # (source, object stem, extra flags): the GEMV kernel instances are one unit
 # per (weight type, x type) so the twelve compile in parallel
 GEMV_UNITS = [("kernels/gemv_inst.hip", f"gemv_inst_{w}_{x}",

@@ -688,7 +688,11 @@ static void *read_file(const char *path, size_t *n) {
 }
 
 static hipFunction_t rtc_get(const char *name, const char *source) {
-  u64 key = hb_hash64(source, strlen(source), 0);
+  /* packed FP32 instructions stay off in runtime-compiled code too (as in
+   * the library's own build): part of the code object's key */
+  static const char *opts[] = {"--offload-arch=gfx950", "-O3", "-std=c++17", "-Xclang",
+                               "-target-feature", "-Xclang", "-packed-fp32-ops"};
+  u64 key = hb_hash64(source, strlen(source), 0x70667033ull);
   key = hb_hash64(name, strlen(name), key ^ 0x5bd1e995ull);
   for (u32 i = 0; i < RTC_N; i++)
     if (RTC[i].key == key) return RTC[i].fn;
@@ -703,8 +707,7 @@ static hipFunction_t rtc_get(const char *name, const char *source) {
     hiprtcProgram prog;
     hiprtcResult r = hiprtcCreateProgram(&prog, source, name, 0, NULL, NULL);
     if (r != HIPRTC_SUCCESS) { hb_set_error("hiprtcCreateProgram(%s): %s", name, hiprtcGetErrorString(r)); return NULL; }
-    const char *opts[] = {"--offload-arch=gfx950", "-O3", "-std=c++17"};
-    r = hiprtcCompileProgram(prog, 3, opts);
+    r = hiprtcCompileProgram(prog, (int)(sizeof opts / sizeof opts[0]), opts);
     if (r != HIPRTC_SUCCESS) {
       size_t ln = 0;
       hiprtcGetProgramLogSize(prog, &ln);

@@ -13,11 +13,13 @@
  *     a reduce loop's axes is hoisted out of that loop;
  *   - fp16 / bf16 values compute in f32 and round to their storage type after
  *     every op (the storage precision of each intermediate);
- *   - geometry: a kernel whose reductions are all un-nested and at least
- *     RENDER_GROUP_MIN long runs one 256-thread block per output element
- *     (strided partial sums, wave64 DPP-free shuffle tree, LDS across the 4
- *     waves: the GROUP_REDUCE form); any other kernel runs one thread per
- *     output element with serial reduce loops;
+ *   - geometry (ThvmRenderOpts, the reference's LOCAL / GROUP_REDUCE /
+ *     UPCAST opts): `group` consecutive threads share one output's
+ *     reductions (strided partial terms, a xor-shuffle tree inside a wave, the
+ *     group's waves in order through LDS above 64), `block` threads per
+ *     block, `upcast` consecutive outputs per thread (one thread per output
+ *     otherwise); without opts the hand-coded choice (hand_opts below), and
+ *     thvm_hip_render_autotune searches them on the device;
  *   - symbolic extents (DEFINE_VAR) are read from an int32 buffer argument,
  *     not passed by value, so a captured graph stays correct when a bound
  *     variable changes; the grid is sized at the variables' upper bounds and
@@ -43,7 +45,6 @@ enum {
 enum { RED_SUM = 0, RED_MAX = 1 };
 
 #define RENDER_BLOCK 256
-#define RENDER_GROUP_MIN 256
 #define RENDER_MAX_RANGES 64
 #define RENDER_MAX_SLOTS 64
 
@@ -71,7 +72,8 @@ typedef struct {
   int *level;          /* scope level a node's local lives in, -1 = none */
   int *is_red_axis;    /* RANGE node: its reduce-axis index, or -1 */
   int cur_level;
-  int group;
+  int group;           /* threads per output in a reduction (0: one thread per output) */
+  int block;           /* threads per block */
   Sb *s;
   char err[160];
   int depth;
@@ -227,8 +229,7 @@ static int emit_reduce(R *r, int i) {
       if (rg->src[0] >= 0) sb_put(r->s, " * (int)v%d", rg->src[0]);
       else sb_put(r->s, " * %lld", (long long)rg->arg[2]);
     }
-    sb_put(r->s, ";\n  for (int rr = (int)threadIdx.x; rr < rn%d; rr += %d) {\n    int rq = rr;\n", i,
-           RENDER_BLOCK);
+    sb_put(r->s, ";\n  for (int rr = gl_; rr < rn%d; rr += %d) {\n    int rq = rr;\n", i, group);
     for (int k = na - 1; k >= 0; k--) {
       const ThvmUop *rg = &r->u[axes[k]];
       char ext[48];
@@ -258,26 +259,33 @@ static int emit_reduce(R *r, int i) {
   r->cur_level--;
   if (group) {
     sb_put(r->s, "  }\n  }\n");
-    /* block combine: wave tree, then the 4 waves through LDS */
+    /* the group's combine, every lane of the group ends with the result */
     const int fl = is_float(r->u[v].dtype);
     if (!fl && strcmp(acc_t, "int") != 0) {
       snprintf(r->err, sizeof r->err, "node %d: group reduce of a %s value", i, acc_t);
       return -1;
     }
-    const char *wf = kind == RED_SUM ? (fl ? "wsum" : "wsumi") : (fl ? "wmax" : "wmaxi");
-    const char *ra = fl ? "red_" : "redi_";
-    char fold[64];
-    if (kind == RED_SUM) snprintf(fold, sizeof fold, "v%d + %s[w]", i, ra);
-    else if (fl) snprintf(fold, sizeof fold, "fmaxf(v%d, red_[w])", i);
-    else snprintf(fold, sizeof fold, "(redi_[w] > v%d ? redi_[w] : v%d)", i, i);
-    sb_put(r->s,
-           "  v%d = %s(v%d);\n"
-           "  if ((threadIdx.x & 63u) == 0) %s[threadIdx.x >> 6] = v%d;\n"
-           "  __syncthreads();\n"
-           "  v%d = %s[0];\n"
-           "  for (int w = 1; w < %d; w++) v%d = %s;\n"
-           "  __syncthreads();\n",
-           i, wf, i, ra, i, i, ra, RENDER_BLOCK / 64, i, fold);
+    char comb[96];      /* combine t_ into v */
+    if (kind == RED_SUM) snprintf(comb, sizeof comb, "v%d = v%d + t_", i, i);
+    else if (fl) snprintf(comb, sizeof comb, "v%d = fmaxf(v%d, t_)", i, i);
+    else snprintf(comb, sizeof comb, "v%d = t_ > v%d ? t_ : v%d", i, i, i);
+    const char *ty = fl ? "float" : "int";
+    if (group <= 64) {  /* the group's lanes are one aligned slice of a wave: xor tree */
+      sb_put(r->s, "  for (int o = %d; o > 0; o >>= 1) { const %s t_ = __shfl_xor(v%d, o, 64); %s; }\n",
+             group / 2, ty, i, comb);
+    } else {            /* whole waves: the wave tree, then the group's waves in order through LDS */
+      const char *wf = kind == RED_SUM ? (fl ? "wsum" : "wsumi") : (fl ? "wmax" : "wmaxi");
+      const char *ra = fl ? "red_" : "redi_";
+      sb_put(r->s,
+             "  v%d = %s(v%d);\n"
+             "  if ((threadIdx.x & 63u) == 0) %s[threadIdx.x >> 6] = v%d;\n"
+             "  __syncthreads();\n"
+             "  {\n    const int w0_ = (int)(threadIdx.x / %d) * %d;\n"
+             "    v%d = %s[w0_];\n"
+             "    for (int w = 1; w < %d; w++) { const %s t_ = %s[w0_ + w]; %s; }\n  }\n"
+             "  __syncthreads();\n",
+             i, wf, i, ra, i, group, group / 64, i, ra, group / 64, ty, ra, comb);
+    }
   } else {
     for (int k = 0; k < na; k++) sb_put(r->s, "  }\n");
   }
@@ -325,24 +333,25 @@ static int emit(R *r, int i) {
       break;
     case U_REDUCE: rc = emit_reduce(r, i); break;
     case U_BUFFER: break;   /* named by its slot */
-    case U_INDEX_E:
+    case U_INDEX_E: {      /* the element of buffer src0 at index src1 (a load) */
+      const ThvmUop *b = u->src[0] >= 0 ? &r->u[u->src[0]] : NULL;
+      if (!b || b->op != U_BUFFER) { snprintf(r->err, sizeof r->err, "node %d: INDEX of a non-BUFFER", i); return -1; }
       if (emit(r, u->src[1]) < 0) return -1;
-      sb_put(r->s, "  const long long v%d = (long long)v%d;\n", i, u->src[1]);
-      break;
-    case U_LOAD: {
-      const int ix = u->src[0];
-      if (ix < 0 || r->u[ix].op != U_INDEX_E) { snprintf(r->err, sizeof r->err, "node %d: LOAD of a non-INDEX", i); return -1; }
-      const ThvmUop *b = &r->u[r->u[ix].src[0]];
-      if (r->u[ix].src[0] < 0 || b->op != U_BUFFER) { snprintf(r->err, sizeof r->err, "node %d: INDEX of a non-BUFFER", i); return -1; }
-      if (emit(r, ix) < 0) return -1;
       const char *conv = b->dtype == THVM_DT_BF16 ? "bf2f" : b->dtype == THVM_DT_FP8E4M3 ? "fp8e4m3_f" : "";
       if (b->arg[1] > 0)   /* capacity known: an index outside the buffer reads 0 */
         sb_put(r->s, "  const %s v%d = (unsigned long long)v%d < %lldull ? (%s)%s(s%lld[v%d]) : (%s)0;\n",
-               alu_t(b->dtype), i, ix, (long long)b->arg[1], alu_t(b->dtype), conv, (long long)b->arg[0], ix,
-               alu_t(b->dtype));
+               alu_t(b->dtype), i, u->src[1], (long long)b->arg[1], alu_t(b->dtype), conv,
+               (long long)b->arg[0], u->src[1], alu_t(b->dtype));
       else
         sb_put(r->s, "  const %s v%d = (%s)%s(s%lld[v%d]);\n", alu_t(b->dtype), i, alu_t(b->dtype), conv,
-               (long long)b->arg[0], ix);
+               (long long)b->arg[0], u->src[1]);
+      break;
+    }
+    case U_LOAD: {         /* an explicit read of an INDEX: its value */
+      const int ix = u->src[0];
+      if (ix < 0 || r->u[ix].op != U_INDEX_E) { snprintf(r->err, sizeof r->err, "node %d: LOAD of a non-INDEX", i); return -1; }
+      if (emit(r, ix) < 0) return -1;
+      sb_put(r->s, "  const %s v%d = v%d;\n", alu_t(r->u[r->u[ix].src[0]].dtype), i, ix);
       break;
     }
     case U_NEG: case U_RECIP: case U_EXP2: case U_LOG2: case U_SQRT: case U_SIN: {
@@ -418,8 +427,33 @@ static int64_t ubound(const ThvmUop *u, int i, int *ok) {
   }
 }
 
-THVM_API int thvm_hip_render_kernel(const ThvmUop *nodes, uint32_t n, const char *name, char *out,
-                                    uint64_t cap, ThvmRenderInfo *info) {
+static int is_pow2(uint32_t x) { return x && !(x & (x - 1)); }
+static uint32_t pow2_floor(uint64_t x) {
+  uint32_t p = 1;
+  while ((uint64_t)p * 2 <= x && p < (1u << 30)) p *= 2;
+  return p;
+}
+
+/* The geometry the target picks without a search (the role of the
+ * reference's hand-coded opts, src/codegen/hand_opts.c:337-802, for gfx950):
+ * an un-nested reduction of length R shares each output among
+ * min(256, R / 4) threads (a power of 2, at least 4 partial terms per
+ * thread; one thread per output below 8), in blocks of 256 threads or the
+ * group; everything else runs one output per thread in 256-thread blocks. */
+static void hand_opts(int has_red, int nested, int64_t red_len, ThvmRenderOpts *o) {
+  memset(o, 0, sizeof *o);
+  o->block = RENDER_BLOCK;
+  o->upcast = 1;
+  o->group = 1;
+  if (has_red && !nested && red_len >= 32) {
+    o->group = pow2_floor((uint64_t)red_len / 4);
+    if (o->group > 256) o->group = 256;
+    if (o->group > o->block) o->block = o->group;
+  }
+}
+
+static int render_impl(const ThvmUop *nodes, uint32_t n, const char *name, const ThvmRenderOpts *opts,
+                       char *out, uint64_t cap, ThvmRenderInfo *info) {
   if (!nodes || n == 0 || !name || !out || cap < 1024 || !info) {
     hb_set_error("render: bad arguments");
     return -1;
@@ -464,8 +498,11 @@ THVM_API int thvm_hip_render_kernel(const ThvmUop *nodes, uint32_t n, const char
       if ((int)u->arg[0] + 1 > nvar) nvar = (int)u->arg[0] + 1;
     }
   }
+  /* a slot no BUFFER row names is an argument the kernel does not read (the
+   * reference schedules such inputs): it is declared as bytes */
   for (int k = 0; k < nslot; k++)
-    if (!slot_used[k]) { hb_set_error("render: buffer slot %d is never declared", k); goto done; }
+    if (!slot_used[k]) slot_dt[k] = THVM_DT_UINT8;
+  if (!slot_used[0]) { hb_set_error("render: the output slot 0 is never declared"); goto done; }
 
   /* reduce axes, dependence masks, nesting */
   int nred = 0;
@@ -507,7 +544,28 @@ THVM_API int thvm_hip_render_kernel(const ThvmUop *nodes, uint32_t n, const char
     }
     r.dep[i] = d;
   }
-  r.group = has_red && !nested && red_len_min >= RENDER_GROUP_MIN;
+  ThvmRenderOpts o;
+  if (opts) {
+    o = *opts;
+    if (o.block == 0) o.block = RENDER_BLOCK;
+    if (o.group == 0) o.group = 1;
+    if (o.upcast == 0) o.upcast = 1;
+    if (!is_pow2(o.block) || o.block < 64 || o.block > 1024 || !is_pow2(o.group) || o.group > o.block ||
+        o.upcast > 8) {
+      hb_set_error("render: opts block %u (64..1024, a power of 2), group %u (a power of 2 <= block), "
+                   "upcast %u (1..8)", o.block, o.group, o.upcast);
+      goto done;
+    }
+    if (o.group > 1 && (!has_red || nested)) {
+      hb_set_error("render: a group applies to un-nested reductions");
+      goto done;
+    }
+    if (o.group > 1 && o.upcast > 1) { hb_set_error("render: upcast applies to one thread per output"); goto done; }
+  } else {
+    hand_opts(has_red, nested, red_len_min == INT64_MAX ? 0 : red_len_min, &o);
+  }
+  r.group = o.group > 1 ? (int)o.group : 0;
+  r.block = (int)o.block;
 
   /* parallel axes: every RANGE that no REDUCE binds, in axis-id order */
   int par[RENDER_MAX_RANGES], npar = 0;
@@ -532,16 +590,25 @@ THVM_API int thvm_hip_render_kernel(const ThvmUop *nodes, uint32_t n, const char
 
   /* source */
   sb_put(&sb, "%s\n", PRELUDE);
-  sb_put(&sb, "extern \"C\" __global__ void __launch_bounds__(%d) %s(\n", RENDER_BLOCK, name);
+  sb_put(&sb, "extern \"C\" __global__ void __launch_bounds__(%d) %s(\n", r.block, name);
   for (int k = 0; k < nslot; k++)
     sb_put(&sb, "    %s%s *__restrict__ s%d%s\n", k ? "const " : "", store_t(slot_dt[k]), k,
            (k + 1 < nslot || nvar) ? "," : "");
   if (nvar) sb_put(&sb, "    const int *__restrict__ kv_\n");
   sb_put(&sb, ") {\n");
-  if (r.group)
+  /* group mode: G consecutive threads per output, block/G outputs per block
+   * (gl_ = the thread's place in its group); thread mode: upcast outputs per
+   * thread, consecutive */
+  const int G = r.group, U = (int)o.upcast;
+  if (G)
     sb_put(&sb, "  __shared__ float red_[%d];\n  __shared__ int redi_[%d];\n  (void)red_; (void)redi_;\n"
-           "  const long long gid = blockIdx.x;\n", RENDER_BLOCK / 64, RENDER_BLOCK / 64);
-  else sb_put(&sb, "  const long long gid = (long long)blockIdx.x * %d + threadIdx.x;\n", RENDER_BLOCK);
+           "  const int gl_ = (int)(threadIdx.x %% %d);\n"
+           "  const long long gid = (long long)blockIdx.x * %d + threadIdx.x / %d;\n",
+           r.block / 64, r.block / 64, G, r.block / G, G);
+  else if (U > 1)
+    sb_put(&sb, "  for (int uj_ = 0; uj_ < %d; uj_++) {\n"
+           "  const long long gid = ((long long)blockIdx.x * %d + threadIdx.x) * %d + uj_;\n", U, r.block, U);
+  else sb_put(&sb, "  const long long gid = (long long)blockIdx.x * %d + threadIdx.x;\n", r.block);
   /* extents of the parallel axes, then the element decomposition */
   for (int a = 0; a < npar; a++) {
     const ThvmUop *rg = &nodes[par[a]];
@@ -552,9 +619,14 @@ THVM_API int thvm_hip_render_kernel(const ThvmUop *nodes, uint32_t n, const char
       sb_put(&sb, "  const long long e%d = %lldll;\n", a, (long long)rg->arg[2]);
     }
   }
-  sb_put(&sb, "  if (gid >= 1ll");
+  /* past the last output: a thread returns (one output per thread, or a
+   * group within one wave: no block barrier follows); a group spanning waves
+   * stays for the barriers of its reduction and skips the store */
+  sb_put(&sb, "  const bool act_ = gid < 1ll");
   for (int a = 0; a < npar; a++) sb_put(&sb, " * e%d", a);
-  sb_put(&sb, ") return;\n  long long q_ = gid;\n");
+  sb_put(&sb, ";\n");
+  if (G > 64) sb_put(&sb, "  long long q_ = act_ ? gid : 0;\n");
+  else sb_put(&sb, "  if (!act_) %s;\n  long long q_ = gid;\n", U > 1 ? "break" : "return");
   for (int a = npar - 1; a >= 0; a--)
     sb_put(&sb, "  const int a%lld = (int)(q_ %% e%d); q_ /= e%d;\n", (long long)nodes[par[a]].arg[0], a, a);
   sb_put(&sb, "  (void)q_;\n");
@@ -572,18 +644,23 @@ THVM_API int thvm_hip_render_kernel(const ThvmUop *nodes, uint32_t n, const char
     char guard[96] = "";
     const int64_t cap0 = nodes[st->src[0]].arg[1];
     if (cap0 > 0) snprintf(guard, sizeof guard, "(unsigned long long)v%d < %lldull", st->src[1], (long long)cap0);
-    if (r.group || guard[0])
-      sb_put(&sb, "  if (%s%s%s) s0[v%d] = %s;\n}\n", r.group ? "threadIdx.x == 0" : "",
-             r.group && guard[0] ? " && " : "", guard, st->src[1], val);
-    else
-      sb_put(&sb, "  s0[v%d] = %s;\n}\n", st->src[1], val);
+    char cond[192];
+    snprintf(cond, sizeof cond, "%s%s%s%s%s", G ? "gl_ == 0" : "", G > 64 ? " && act_" : "",
+             (G && guard[0]) ? " && " : "", guard, "");
+    if (cond[0]) sb_put(&sb, "  if (%s) s0[v%d] = %s;\n", cond, st->src[1], val);
+    else sb_put(&sb, "  s0[v%d] = %s;\n", st->src[1], val);
+    sb_put(&sb, "%s}\n", U > 1 && !G ? "  }\n" : "");
   }
   if (sb.bad) { hb_set_error("render: source exceeds %llu bytes", (unsigned long long)cap); goto done; }
   info->n_slots = (uint32_t)nslot + (nvar ? 1u : 0u);
   info->kvar_slot = nvar ? (uint32_t)nslot : 0u;
-  info->group = (uint32_t)r.group;
-  info->block = RENDER_BLOCK;
-  info->grid_max = r.group ? total_max : (total_max + RENDER_BLOCK - 1) / RENDER_BLOCK;
+  info->group = (uint32_t)(G ? G : 1);
+  info->block = (uint32_t)r.block;
+  info->upcast = (uint32_t)U;
+  {
+    const uint64_t per_block = G ? (uint64_t)(r.block / G) : (uint64_t)r.block * (uint64_t)U;
+    info->grid_max = (total_max + per_block - 1) / per_block;
+  }
   if (info->grid_max == 0) info->grid_max = 1;
   rc = 0;
   goto done;
@@ -594,4 +671,15 @@ done:
   free(r.level);
   free(r.is_red_axis);
   return rc;
+}
+
+THVM_API int thvm_hip_render_kernel(const ThvmUop *nodes, uint32_t n, const char *name, char *out,
+                                    uint64_t cap, ThvmRenderInfo *info) {
+  return render_impl(nodes, n, name, NULL, out, cap, info);
+}
+
+THVM_API int thvm_hip_render_kernel_opts(const ThvmUop *nodes, uint32_t n, const char *name,
+                                         const ThvmRenderOpts *opts, char *out, uint64_t cap,
+                                         ThvmRenderInfo *info) {
+  return render_impl(nodes, n, name, opts, out, cap, info);
 }

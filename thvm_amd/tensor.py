@@ -25,6 +25,7 @@ There is no CPU fallback: every kernel runs through libthvm_hip.so."""
 from __future__ import annotations
 
 import math
+import os
 import struct
 from typing import Optional, Sequence, Union
 
@@ -684,6 +685,18 @@ def _dispatch_rendered(kb: _KB):
     if hit is None:
         name = "r_%016x" % (hash(key) & 0xFFFFFFFFFFFFFFFF)
         src, info = _hip.render_kernel(kb.nodes, name)
+        if int(os.environ.get("BEAM", "0") or 0) > 0 and _CAPTURE is None:
+            # the reference's BEAM: search this kernel's geometry once, on its
+            # own buffers (kernels that read their output are not searched)
+            args = [b.id for b in kb.bufs]
+            if info.kvar_slot:
+                _KV.sync()
+                args.append(_KV.get().id)
+            try:
+                opts = _hip.render_autotune(kb.nodes, args)[0]
+                src, info = _hip.render_kernel(kb.nodes, name, opts=opts)
+            except _hip.ThvmHipError:
+                pass
         hit = (name, src, int(info.grid_max), int(info.block), int(info.kvar_slot))
         _RENDER_CACHE[key] = hit
     name, src, grid, block, kvar_slot = hit
