@@ -449,3 +449,55 @@ int ref_sdpa_f32(const float *q, const float *k, const float *v, float *out, u32
   memset(&none, 0, sizeof none);
   return ref_read(nn_scaled_dot_product_attention(Q, Kt, Vt, none, 1), out, (u64)H * T * hd);
 }
+
+/* One GPT-2 transformer block over T tokens (causal prefill), f32, through
+ * the reference Tensor graph (tinygrad's GPT-2 block,
+ * bench/gpt2/thvm_gpt2.py:25-75, with q, k and v from three [D][D]
+ * matrices): h = x + attn(ln1(x)); out = h + mlp(ln2(h)), ln(z) =
+ * layernorm(z) * w + b, mlp(z) = gelu(z Wfc + bfc) Wpr + bpr.  Matrices are
+ * [in][out].  Realized on the CPU path; every kernel it schedules is what
+ * the capture records. */
+static Tensor ref_vec(u32 n, const float *data) {
+  Shape sh = {0};
+  sh.ndim = 1;
+  sh.dims[0] = n;
+  u32 tid = tensor_alloc(&CPU_BACKEND, sh, DT_FP32);
+  CPU_BACKEND.buf_write(TENS[tid].buf_id, (void *)data, (u64)n * 4);
+  Tensor t;
+  t.t = term_new(0, TAG_TEN, DT_FP32, tid);
+  t.dtype = DT_FP32;
+  t.shape = sh;
+  return t;
+}
+static Tensor ref_ln(Tensor z, Tensor w, Tensor b) {
+  u32 ax[1] = {1};
+  return nn_binop(UOP_ADD, nn_binop(UOP_MUL, nn_layernorm(z, 1, ax, 1e-5), w), b);
+}
+static Tensor ref_heads(Tensor z, u32 T, u32 H, u32 hd) {      /* [T][D] -> [H][T][hd] */
+  u32 d3[3] = {T, H, hd}, perm[3] = {1, 0, 2};
+  return nn_permute(nn_reshape(z, 3, d3), 3, perm);
+}
+int ref_gpt2_block_f32(const float *x, const float *const *p, float *out, u32 T, u32 D, u32 H, u32 F) {
+  ref_init();
+  const u32 hd = D / H;
+  Tensor X = ref_tensor2(T, D, x);
+  Tensor ln1w = ref_vec(D, p[0]), ln1b = ref_vec(D, p[1]);
+  Tensor wq = ref_tensor2(D, D, p[2]), bq = ref_vec(D, p[3]);
+  Tensor wk = ref_tensor2(D, D, p[4]), bk = ref_vec(D, p[5]);
+  Tensor wv = ref_tensor2(D, D, p[6]), bv = ref_vec(D, p[7]);
+  Tensor wo = ref_tensor2(D, D, p[8]), bo = ref_vec(D, p[9]);
+  Tensor ln2w = ref_vec(D, p[10]), ln2b = ref_vec(D, p[11]);
+  Tensor wfc = ref_tensor2(D, F, p[12]), bfc = ref_vec(F, p[13]);
+  Tensor wpr = ref_tensor2(F, D, p[14]), bpr = ref_vec(D, p[15]);
+  Tensor z = ref_ln(X, ln1w, ln1b);
+  Tensor q = ref_heads(nn_linear(z, wq, bq), T, H, hd), k = ref_heads(nn_linear(z, wk, bk), T, H, hd),
+         v = ref_heads(nn_linear(z, wv, bv), T, H, hd);
+  Tensor none;
+  memset(&none, 0, sizeof none);
+  Tensor a = nn_scaled_dot_product_attention(q, k, v, none, 1);          /* [H][T][hd] */
+  u32 perm[3] = {1, 0, 2}, d2[2] = {T, D};
+  a = nn_reshape(nn_permute(a, 3, perm), 2, d2);
+  Tensor h = nn_binop(UOP_ADD, X, nn_linear(a, wo, bo));
+  Tensor m = nn_linear(nn_elementwise(NN_GELU, nn_linear(ref_ln(h, ln2w, ln2b), wfc, bfc)), wpr, bpr);
+  return ref_read(nn_binop(UOP_ADD, h, m), out, (u64)T * D);
+}

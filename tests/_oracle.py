@@ -117,6 +117,7 @@ def ref():
             "ref_dense_silu_mul_bf16": (_i, [_vp, _vp, _vp, _u32]),
             "ref_gelu_f32": (_i, [_vp, _vp, _u32, _u32]),
             "ref_sdpa_f32": (_i, [_vp, _vp, _vp, _vp, _u32, _u32, _u32]),
+            "ref_gpt2_block_f32": (_i, [_vp, _vp, _vp, _u32, _u32, _u32, _u32]),
             "ref_capture_begin": (_i, []), "ref_capture_end": (_i, []),
             "ref_capture_kernel": (_i, [_u32, _vp, _u32, C.POINTER(_u32), C.POINTER(_u32), _vp,
                                         C.POINTER(_u32), C.c_char_p, _u32]),

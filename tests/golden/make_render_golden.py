@@ -1,6 +1,7 @@
 """Write tests/golden/ref_lifted_kernels.npz: every kernel the compiled
 reference schedules for a set of GPT-2 step operations on f32 (linear,
-softmax, layernorm, RMSNorm, GELU, causal attention), captured at its CPU
+softmax, layernorm, RMSNorm, GELU, causal attention, one whole GPT-2
+block), captured at its CPU
 dispatch by oracle/ref_harness.c (ref_capture_*): the kernel's lifted DAG as
 renderer rows (op, dtype, src0..3, arg0..3; the reference's UOP_* and DT_*
 numbers), its input buffers, the reference CPU output and the OPT
@@ -36,7 +37,16 @@ def scenarios(rng):
     q, k, v = (rng.standard_normal((H, T, hd)).astype(np.float32) for _ in range(3))
     ym, yk = np.empty((M, N), np.float32), np.empty((M, K), np.float32)
     o = np.empty((H, T, hd), np.float32)
-    keep = [x, w, q, k, v, ym, yk, o]
+    # one GPT-2 block over 8 tokens (causal prefill): D 64, 2 heads, F 256
+    T2, D2, H2, F2 = 8, 64, 2, 256
+    xb = rng.standard_normal((T2, D2)).astype(np.float32)
+    shapes = [(D2,), (D2,), (D2, D2), (D2,), (D2, D2), (D2,), (D2, D2), (D2,), (D2, D2), (D2,),
+              (D2,), (D2,), (D2, F2), (F2,), (F2, D2), (D2,)]
+    params = [(rng.standard_normal(sh) * (0.1 if len(sh) == 2 else 0.5) + (1.0 if i in (0, 10) else 0.0))
+              .astype(np.float32) for i, sh in enumerate(shapes)]
+    pp = (C.c_void_p * 16)(*[a.ctypes.data for a in params])
+    ob = np.empty((T2, D2), np.float32)
+    keep = [x, w, q, k, v, ym, yk, o, xb, params, pp, ob]
     L = O.ref()
     return keep, [
         ("linear", lambda: L.ref_linear_f32(x.ctypes.data, w.ctypes.data, ym.ctypes.data, M, N, K)),
@@ -45,6 +55,8 @@ def scenarios(rng):
         ("rmsnorm", lambda: L.ref_rmsnorm_f32(x.ctypes.data, yk.ctypes.data, M, K, 1e-6)),
         ("gelu", lambda: L.ref_gelu_f32(x.ctypes.data, yk.ctypes.data, M, K)),
         ("attention", lambda: L.ref_sdpa_f32(q.ctypes.data, k.ctypes.data, v.ctypes.data, o.ctypes.data, H, T, hd)),
+        ("gpt2_block", lambda: L.ref_gpt2_block_f32(xb.ctypes.data, C.cast(pp, C.c_void_p), ob.ctypes.data,
+                                                     T2, D2, H2, F2)),
     ]
 
 

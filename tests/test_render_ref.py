@@ -1,6 +1,6 @@
 """The renderer target's test vectors: every kernel the compiled reference
 schedules for GPT-2 step operations (linear, softmax, layernorm, RMSNorm,
-GELU, causal attention), captured at its CPU dispatch with its lifted DAG,
+GELU, causal attention, a whole GPT-2 block), captured at its CPU dispatch with its lifted DAG,
 inputs and output (tests/golden/ref_lifted_kernels.npz, written by
 tests/golden/make_render_golden.py).  On the CPU: a plain numpy evaluation
 of the rows reproduces the reference's own output (pinning what the rows
@@ -34,9 +34,9 @@ def kernel(k):
 
 
 def test_captured_set():
-    assert len(NAMES) >= 12
+    assert len(NAMES) >= 30
     ops = {n.split("/")[0] for n in NAMES}
-    assert ops == {"linear", "softmax", "layernorm", "rmsnorm", "gelu", "attention"}
+    assert ops == {"linear", "softmax", "layernorm", "rmsnorm", "gelu", "attention", "gpt2_block"}
 
 
 @pytest.mark.parametrize("k", range(len(NAMES)), ids=NAMES)

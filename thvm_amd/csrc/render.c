@@ -436,19 +436,27 @@ static uint32_t pow2_floor(uint64_t x) {
 
 /* The geometry the target picks without a search (the role of the
  * reference's hand-coded opts, src/codegen/hand_opts.c:337-802, for gfx950):
- * an un-nested reduction of length R shares each output among
- * min(256, R / 4) threads (a power of 2, at least 4 partial terms per
- * thread; one thread per output below 8), in blocks of 256 threads or the
- * group; everything else runs one output per thread in 256-thread blocks. */
-static void hand_opts(int has_red, int nested, int64_t red_len, ThvmRenderOpts *o) {
+ * an un-nested reduction of length R over O outputs shares each output among
+ * G = min(R / 32, 524288 / O) threads (powers of 2, at most 1024: at least 32
+ * terms per thread, about 512K threads in all), one thread per output below
+ * G = 16; blocks of max(G, 256) threads.  Measured on gfx950 with the search
+ * (f32 rows, thvm_hip_render_autotune): 50257 x 768 wants one thread per
+ * row, 4096 x 4096 a group of 128, 64 x 65536 groups of 1024.  Everything
+ * else runs one output per thread in 256-thread blocks. */
+static void hand_opts(int has_red, int nested, int64_t red_len, uint64_t outputs, ThvmRenderOpts *o) {
   memset(o, 0, sizeof *o);
   o->block = RENDER_BLOCK;
   o->upcast = 1;
   o->group = 1;
-  if (has_red && !nested && red_len >= 32) {
-    o->group = pow2_floor((uint64_t)red_len / 4);
-    if (o->group > 256) o->group = 256;
-    if (o->group > o->block) o->block = o->group;
+  if (has_red && !nested && red_len >= 128) {
+    uint32_t g = pow2_floor((uint64_t)red_len / 32);
+    const uint32_t by_out = pow2_floor(outputs ? (524288 + outputs - 1) / outputs : 1);
+    if (by_out < g) g = by_out;
+    if (g > 1024) g = 1024;
+    if (g >= 16) {
+      o->group = g;
+      if (g > o->block) o->block = g;
+    }
   }
 }
 
@@ -544,28 +552,6 @@ static int render_impl(const ThvmUop *nodes, uint32_t n, const char *name, const
     }
     r.dep[i] = d;
   }
-  ThvmRenderOpts o;
-  if (opts) {
-    o = *opts;
-    if (o.block == 0) o.block = RENDER_BLOCK;
-    if (o.group == 0) o.group = 1;
-    if (o.upcast == 0) o.upcast = 1;
-    if (!is_pow2(o.block) || o.block < 64 || o.block > 1024 || !is_pow2(o.group) || o.group > o.block ||
-        o.upcast > 8) {
-      hb_set_error("render: opts block %u (64..1024, a power of 2), group %u (a power of 2 <= block), "
-                   "upcast %u (1..8)", o.block, o.group, o.upcast);
-      goto done;
-    }
-    if (o.group > 1 && (!has_red || nested)) {
-      hb_set_error("render: a group applies to un-nested reductions");
-      goto done;
-    }
-    if (o.group > 1 && o.upcast > 1) { hb_set_error("render: upcast applies to one thread per output"); goto done; }
-  } else {
-    hand_opts(has_red, nested, red_len_min == INT64_MAX ? 0 : red_len_min, &o);
-  }
-  r.group = o.group > 1 ? (int)o.group : 0;
-  r.block = (int)o.block;
 
   /* parallel axes: every RANGE that no REDUCE binds, in axis-id order */
   int par[RENDER_MAX_RANGES], npar = 0;
@@ -587,6 +573,28 @@ static int render_impl(const ThvmUop *nodes, uint32_t n, const char *name, const
     total_max *= (uint64_t)e;
   }
   if (total_max > (1ull << 31)) { hb_set_error("render: %llu output elements", (unsigned long long)total_max); goto done; }
+  ThvmRenderOpts o;
+  if (opts) {
+    o = *opts;
+    if (o.block == 0) o.block = RENDER_BLOCK;
+    if (o.group == 0) o.group = 1;
+    if (o.upcast == 0) o.upcast = 1;
+    if (!is_pow2(o.block) || o.block < 64 || o.block > 1024 || !is_pow2(o.group) || o.group > o.block ||
+        o.upcast > 8) {
+      hb_set_error("render: opts block %u (64..1024, a power of 2), group %u (a power of 2 <= block), "
+                   "upcast %u (1..8)", o.block, o.group, o.upcast);
+      goto done;
+    }
+    if (o.group > 1 && (!has_red || nested)) {
+      hb_set_error("render: a group applies to un-nested reductions");
+      goto done;
+    }
+    if (o.group > 1 && o.upcast > 1) { hb_set_error("render: upcast applies to one thread per output"); goto done; }
+  } else {
+    hand_opts(has_red, nested, red_len_min == INT64_MAX ? 0 : red_len_min, total_max, &o);
+  }
+  r.group = o.group > 1 ? (int)o.group : 0;
+  r.block = (int)o.block;
 
   /* source */
   sb_put(&sb, "%s\n", PRELUDE);
