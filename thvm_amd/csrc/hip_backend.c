@@ -157,7 +157,7 @@ static u32 freelist_pop(u64 n) {
 
 THVM_API uint32_t thvm_hip_buf_alloc(uint64_t nbytes) {
   if (hb_require_ready("buf_alloc")) return 0;
-  if (HB_GRAPH_CAPTURING) {
+  if (hb_stream_capturing()) {       /* a memset node would enter the graph */
     hb_set_error("buf_alloc: not allowed while a graph capture is open");
     return 0;
   }
