@@ -192,3 +192,23 @@ def test_symbolic_ints():
     assert Variable("sym_test", 1, 100).slot == v.slot
     with pytest.raises(ValueError):
         Variable("sym_test", 1, 100).bind(0)
+
+
+def test_beam_width_env(monkeypatch):
+    """BEAM sets the search width; JITBEAM overrides it inside a TinyJit
+    function's first call (the kernels its graph replays), as the
+    reference's autotune reads them."""
+    import thvm_amd.tensor as T
+    monkeypatch.delenv("BEAM", raising=False)
+    monkeypatch.delenv("JITBEAM", raising=False)
+    assert T._beam_width() == 0
+    monkeypatch.setenv("BEAM", "4")
+    assert T._beam_width() == 4
+    monkeypatch.setenv("JITBEAM", "2")
+    assert T._beam_width() == 4
+    monkeypatch.setattr(T, "_IN_JIT", 1)
+    assert T._beam_width() == 2
+    monkeypatch.delenv("BEAM")
+    assert T._beam_width() == 2
+    monkeypatch.setattr(T, "_IN_JIT", 0)
+    assert T._beam_width() == 0

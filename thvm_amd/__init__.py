@@ -15,6 +15,7 @@ from __future__ import annotations
 import ctypes as C
 import os
 from pathlib import Path
+from typing import Optional
 
 import numpy as np
 
@@ -424,15 +425,27 @@ def render_kernel(nodes, name: str, cap: int = 1 << 20, opts=None) -> tuple[str,
     return buf.value.decode(), info
 
 
-def render_autotune(nodes, args, reps: int = 20):
+def render_autotune(nodes, args, reps: int = 20, beam: Optional[int] = None):
     """Device search of a kernel's (block, group, upcast) over its argument
     buffers (reference src/codegen/autotune.c): returns (opts, best_us,
-    hand_coded_us); the output buffer holds the winner's result."""
+    hand_coded_us); the output buffer holds the winner's result.  `beam`
+    overrides the library's $BEAM width for this call."""
     arr = _uops(nodes)
     ids = _u32arr([a.id if isinstance(a, Buffer) else int(a) for a in args])
     best, bu, hu = RenderOpts(), C.c_double(), C.c_double()
-    _check(lib().thvm_hip_render_autotune(arr, len(nodes), ids, len(args), reps, C.byref(best),
-                                          C.byref(bu), C.byref(hu)), "render_autotune")
+    old = os.environ.get("BEAM")
+    if beam is not None:
+        os.environ["BEAM"] = str(int(beam))
+    try:
+        rc = lib().thvm_hip_render_autotune(arr, len(nodes), ids, len(args), reps, C.byref(best),
+                                            C.byref(bu), C.byref(hu))
+    finally:
+        if beam is not None:
+            if old is None:
+                del os.environ["BEAM"]
+            else:
+                os.environ["BEAM"] = old
+    _check(rc, "render_autotune")
     return (best.block, best.group, best.upcast), bu.value, hu.value
 
 

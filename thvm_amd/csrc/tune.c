@@ -19,7 +19,8 @@
  * floats within 1e-5 relative plus 1e-6 of the largest magnitude (the
  * summation order changes with the group), integers exactly.  The caller's
  * output buffer ends holding the winner's result.  Winners are cached in the
- * process and under $THVM_HIP_CACHE_DIR/tune/ by a hash of the rows. */
+ * process and under $AUTOTUNE_CACHE_DIR (else $THVM_HIP_CACHE_DIR/tune/) by a
+ * hash of the rows. */
 #define _GNU_SOURCE
 #include "internal.h"
 #include "thvm_hip.h"
@@ -42,11 +43,14 @@ static u64 rows_key(const ThvmUop *nodes, uint32_t n) {
   return hb_hash64(nodes, (size_t)n * sizeof *nodes, 0x74756e65ull);
 }
 
+/* $AUTOTUNE_CACHE_DIR (the reference's switch) or $THVM_HIP_CACHE_DIR/tune */
 static int disk_path(u64 key, char *p, size_t cap) {
-  const char *d = getenv("THVM_HIP_CACHE_DIR");
+  const char *a = getenv("AUTOTUNE_CACHE_DIR");
+  const char *d = a && a[0] ? a : getenv("THVM_HIP_CACHE_DIR");
   if (!d || !d[0]) return -1;
   char dir[512];
-  snprintf(dir, sizeof dir, "%s/tune", d);
+  if (a && a[0]) snprintf(dir, sizeof dir, "%s", d);
+  else snprintf(dir, sizeof dir, "%s/tune", d);
   if (mkdir(d, 0755) && errno != EEXIST) return -1;
   if (mkdir(dir, 0755) && errno != EEXIST) return -1;
   snprintf(p, cap, "%s/%016llx.txt", dir, (unsigned long long)key);

@@ -676,6 +676,19 @@ def _deps(root: LNode) -> list:
 
 
 _RENDER_CACHE: dict = {}
+_IN_JIT = 0        # inside a TinyJit function's eager first call
+
+
+def _beam_width() -> int:
+    """Search width for a kernel rendered now: JITBEAM inside a TinyJit
+    function (the kernels its graph will replay), else BEAM; 0 = no search
+    (py/thvm tinygrad semantics, src/codegen/autotune.c:124-131)."""
+    jb = int(os.environ.get("JITBEAM", "0") or 0)
+    if _IN_JIT and jb > 0:
+        return jb
+    return int(os.environ.get("BEAM", "0") or 0)
+
+
 GlobalCounters = type("GlobalCounters", (), {"kernel_count": 0, "gemv_count": 0})
 
 
@@ -685,7 +698,8 @@ def _dispatch_rendered(kb: _KB):
     if hit is None:
         name = "r_%016x" % (hash(key) & 0xFFFFFFFFFFFFFFFF)
         src, info = _hip.render_kernel(kb.nodes, name)
-        if int(os.environ.get("BEAM", "0") or 0) > 0 and _CAPTURE is None:
+        width = _beam_width()
+        if width > 0 and _CAPTURE is None:
             # the reference's BEAM: search this kernel's geometry once, on its
             # own buffers (kernels that read their output are not searched)
             args = [b.id for b in kb.bufs]
@@ -693,7 +707,7 @@ def _dispatch_rendered(kb: _KB):
                 _KV.sync()
                 args.append(_KV.get().id)
             try:
-                opts = _hip.render_autotune(kb.nodes, args)[0]
+                opts = _hip.render_autotune(kb.nodes, args, beam=width)[0]
                 src, info = _hip.render_kernel(kb.nodes, name, opts=opts)
             except _hip.ThvmHipError:
                 pass
@@ -1333,9 +1347,14 @@ class TinyJit:
             if not _is_contig_buf(t.node):
                 t.node = t.contiguous().realize().node
             t.realize()
+        global _IN_JIT
         if self.cnt == 0:
             self.cnt = 1
-            return _realize_ret(self.fxn(*args, **kwargs))
+            _IN_JIT += 1
+            try:
+                return _realize_ret(self.fxn(*args, **kwargs))
+            finally:
+                _IN_JIT -= 1
         if self.cnt == 1:
             _KV.sync()
             _CAPTURE = []
