@@ -33,8 +33,11 @@
 
 // ---- router ---------------------------------------------------------------
 // top-K of one row's E <= 64 logits by one wave (lane e holds logit e):
-// every lane ends with the K ids and probabilities (the butterfly leaves the
-// winner in all lanes)
+// every lane ends with the K ids and probabilities.  Each round takes the
+// wave max of the unused logits (DPP) and the lowest lane holding it (a
+// ballot): the winner of a (value desc, index asc) scan, ties to the lowest
+// expert id as the reference's serial scan picks them, with no cross-lane
+// shuffle round trips.
 __device__ __forceinline__ void route_wave(float g, uint32_t lane, uint32_t E, uint32_t K,
                                            int32_t (&ids)[MOE_MAXK], float (&pr)[MOE_MAXK]) {
   const float mx = wave_max(g);
@@ -43,19 +46,17 @@ __device__ __forceinline__ void route_wave(float g, uint32_t lane, uint32_t E, u
 #pragma unroll
   for (uint32_t kk = 0; kk < MOE_MAXK; kk++) {
     if (kk >= K) break;
-    float bv = used ? -INFINITY : g;
-    int bi = used ? INT_MAX : (int)lane;
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) {
-      const float ov = __shfl_xor(bv, o);
-      const int oi = __shfl_xor(bi, o);
-      if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
-    }
+    const float v = used ? -INFINITY : g;
+    const float bv = wave_max(v);
+    uint64_t m = __ballot(!used && v == bv);
+    if (!m) m = __ballot(!used);            // no unused lane equals the max (NaN logits)
+    const int bi = m ? (int)__builtin_ctzll(m) : 0;
     if ((int)lane == bi) used = true;
     ids[kk] = bi;
     pr[kk] = expf(bv - mx) / sum;
   }
 }
+
 __global__ __launch_bounds__(64) void k_route(ThvmRouteArgs a) {
   const uint32_t b = blockIdx.x, lane = threadIdx.x, E = a.E;
   const float g = lane < E ? a.logits[(uint64_t)b * E + lane] : -INFINITY;
@@ -88,14 +89,10 @@ __global__ __launch_bounds__(RT_THREADS) void k_moe_gate(ThvmGateArgs a) {
   const uint32_t D = a.D, E = a.E, C = D / 4;
   const uint32_t e = blockIdx.x * RT_WAVES + wv;
   const float4 *W = (const float4 *)a.gate;
-  uint4 wq[NCH];
-#pragma unroll
-  for (int t = 0; t < NCH; t++) {
-    const uint32_t c = lane + 64u * t;
-    wq[t] = (e < E && c < C) ? ld_stream16((const char *)(W + (uint64_t)e * C + c)) : make_uint4(0, 0, 0, 0);
-  }
   const uint64_t xo = (uint64_t)b * D;
   const float invK = 1.0f / (float)D;
+  // x and the gains first: the loads return in issue order, so the norm
+  // runs while the expert rows are in flight
   float xv[RT_NREG], gw[RT_NREG];
   if (tid < RT_NORM_THREADS) {
 #pragma unroll
@@ -104,6 +101,14 @@ __global__ __launch_bounds__(RT_THREADS) void k_moe_gate(ThvmGateArgs a) {
       xv[i] = k < D ? bf2f(((const bf16_t *)a.x)[xo + k]) : 0.0f;
       gw[i] = a.w ? a.w[kc] : 1.0f;
     }
+  }
+  uint4 wq[NCH];
+#pragma unroll
+  for (int t = 0; t < NCH; t++) {
+    const uint32_t c = lane + 64u * t;
+    wq[t] = (e < E && c < C) ? ld_stream16((const char *)(W + (uint64_t)e * C + c)) : make_uint4(0, 0, 0, 0);
+  }
+  if (tid < RT_NORM_THREADS) {
     float s2 = 0.0f;
 #pragma unroll
     for (int i = 0; i < RT_NREG; i++) s2 += xv[i] * xv[i];
@@ -227,6 +232,39 @@ __device__ __forceinline__ void stage_swz(float *dst, const float *src, uint32_t
   }
 }
 
+// stage_swz in two halves: the loads into NV float4 registers per thread
+// (n/4 <= NV * blockDim.x), issued early, and the LDS stores, run later --
+// the same elements to the same places
+template <int NV>
+__device__ __forceinline__ void stage_load(float4 (&v)[NV], const float *src, uint32_t n) {
+  const uint32_t tid = threadIdx.x, nt = blockDim.x, n4 = n / 4;
+  const float4 *s4 = (const float4 *)src;
+#pragma unroll
+  for (int u = 0; u < NV; u++) {
+    const uint32_t j = tid + u * nt;
+    v[u] = j < n4 ? s4[j] : make_float4(0.f, 0.f, 0.f, 0.f);
+  }
+}
+template <bool RBF, int EPC, int NV>
+__device__ __forceinline__ void stage_store(float *dst, const float4 (&v)[NV], uint32_t n, uint32_t nseg,
+                                            uint32_t seg) {
+  const uint32_t tid = threadIdx.x, nt = blockDim.x, n4 = n / 4, head = nseg * seg;
+  float4 *d4 = (float4 *)dst;
+#pragma unroll
+  for (int u = 0; u < NV; u++) {
+    const uint32_t j = tid + u * nt;
+    if (j >= n4) continue;
+    float4 w = v[u];
+    if (RBF) { w.x = rbf(w.x); w.y = rbf(w.y); w.z = rbf(w.z); w.w = rbf(w.w); }
+    const uint32_t k = 4 * j;
+    uint32_t base, kk, nch;
+    if (k < head) { base = (k / seg) * seg; kk = k - base; nch = seg / EPC; }
+    else { base = head; kk = k - head; nch = (n - head) / EPC; }
+    d4[(base + chunk_swz<EPC>(kk, nch)) / 4] = w;
+  }
+}
+#define MOE_XPRE 2      /* gate/up: x float4 per thread loaded early (D <= 4096) */
+
 // ---- gate/up --------------------------------------------------------------
 // grid (ceil(P / (8 * PPW)), B) with P = K*I + S row pairs per batch row;
 // each wave owns PPW consecutive pairs, NC 16-byte chunks per lane per row,
@@ -237,6 +275,10 @@ __global__ __launch_bounds__(MOE_THREADS) void k_moe_gateup(ThvmMoeArgs a) {
   const uint32_t b = blockIdx.y, D = a.D, I = a.I, K = a.K;
   const uint32_t P = K * I + a.S;
   const uint32_t lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  // x first (staged into LDS while the rows are in flight)
+  const bool xpre = D / 4 <= MOE_XPRE * blockDim.x;
+  float4 xv[MOE_XPRE];
+  if (xpre) stage_load(xv, a.x + (uint64_t)b * D, D);
   // the row's top-K, as the route kernel picks it, by every wave with a
   // routed pair (no barrier before the weight loads); block 0's wave 0
   // publishes it for the down kernel
@@ -282,7 +324,8 @@ __global__ __launch_bounds__(MOE_THREADS) void k_moe_gateup(ThvmMoeArgs a) {
     load_row(gq[i], base + row0[i] * rowb, lane, nch, live);
     load_row(uq[i], base + (row0[i] + 1) * rowb, lane, nch, live);
   }
-  stage_swz<true, FP8 ? 16 : 8>(xs, a.x + (uint64_t)b * D, D, 0, 1);
+  if (xpre) stage_store<true, FP8 ? 16 : 8>(xs, xv, D, 0, 1);
+  else stage_swz<true, FP8 ? 16 : 8>(xs, a.x + (uint64_t)b * D, D, 0, 1);
   __syncthreads();
 #pragma unroll
   for (int i = 0; i < PPW; i++) {
@@ -298,44 +341,94 @@ __global__ __launch_bounds__(MOE_THREADS) void k_moe_gateup(ThvmMoeArgs a) {
 }
 
 // ---- down + residual ------------------------------------------------------
-// grid (ceil(D / 8), B): wave per output row d
-template <bool FP8>
-__global__ __launch_bounds__(MOE_THREADS) void k_moe_down(ThvmMoeArgs a) {
+// grid (ceil(D / 4), B): two waves per output row d.  The row's segments are
+// split at routed slot c: wave half 0 takes slots [0, c), half 1 slots
+// [c, K) and the shared segment (c balances their bytes, each half at most
+// MOE_HALFK slots), so each wave holds half the rows in flight and a CU runs
+// twice the waves.  Half 0 folds its slots in order from 0 and hands the
+// partial sum to half 1 through LDS; half 1 continues the same sequence --
+// routed slots ascending, then shared -- so every output has the one-wave
+// fold's bits.
+#define MOE_HALFK 4
+__device__ __forceinline__ uint32_t moe_down_split(uint32_t K, uint32_t I, uint32_t S) {
+  uint32_t c = (K * I + S) / (2 * I);
+  if (c + MOE_HALFK < K) c = K - MOE_HALFK;
+  if (c > MOE_HALFK) c = MOE_HALFK;
+  if (c > K) c = K;
+  return c;
+}
+template <bool FP8, int NC, int NCS>   /* 16-byte chunks per lane: routed rows, shared row */
+__global__ __launch_bounds__(MOE_THREADS, 4) void k_moe_down(ThvmMoeArgs a) {
   extern __shared__ float hs[];
+  __shared__ float part[MOE_WAVES / 2];
   const uint32_t b = blockIdx.y, D = a.D, I = a.I, K = a.K, S = a.S;
   const uint32_t P = K * I + S;
-  const uint32_t lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
-  const uint32_t d = blockIdx.x * MOE_WAVES + wv;
+  const uint32_t lane = threadIdx.x & 63, wv = threadIdx.x >> 6, hf = wv & 1, rw = wv >> 1;
+  const uint32_t d = blockIdx.x * (MOE_WAVES / 2) + rw;
   const bool live = d < D;
+  const uint32_t c = moe_down_split(K, I, S);
+  const uint32_t e0 = hf ? c : 0, e1 = hf ? K : c;          // this half's routed slots
   const uint64_t rI = (uint64_t)I * (FP8 ? 1 : 2), rS = (uint64_t)S * (FP8 ? 1 : 2);
   const uint32_t nI = (uint32_t)(rI / 16), nS = (uint32_t)(rS / 16);
-  uint4 q[MOE_MAXK][MOE_MAXC], qs[MOE_MAXCS];
-  int32_t ids[MOE_MAXK];
+  uint4 q[MOE_HALFK][NC], qs[NCS];
+  int32_t ids[MOE_HALFK];
+  // this half's routing ids requested at once (clamped, unconditional loads:
+  // one round trip); the shared row, which needs no routing, goes out before
+  // the routed rows; h is staged into LDS behind them (its registers would
+  // cost the second block per CU)
 #pragma unroll
-  for (int e = 0; e < MOE_MAXK; e++) {
-    ids[e] = (e < (int)K) ? a.sel[(uint64_t)b * K + e] : 0;
-    ids[e] = ids[e] < 0 ? 0 : ids[e] >= (int32_t)a.E ? (int32_t)a.E - 1 : ids[e];
-    const bool ok = live && e < (int)K;
-    const uint64_t row = (uint64_t)(ok ? ids[e] : 0) * D + (live ? d : 0);
-    load_row(q[e], (const char *)a.wd_e + row * rI, lane, nI, ok);
+  for (int j = 0; j < MOE_HALFK; j++) {
+    const uint32_t e = e0 + j;
+    ids[j] = a.sel[(uint64_t)b * K + (e < e1 ? e : 0u)];
   }
-  load_row(qs, (const char *)a.wd_s + (uint64_t)(live ? d : 0) * rS, lane, nS, live && S > 0);
+  load_row(qs, (const char *)a.wd_s + (uint64_t)(live ? d : 0) * rS, lane, nS, live && hf && S > 0);
+#pragma unroll
+  for (int j = 0; j < MOE_HALFK; j++) {
+    const bool ok = live && e0 + j < e1;
+    int32_t id = ok ? ids[j] : 0;
+    id = id < 0 ? 0 : id >= (int32_t)a.E ? (int32_t)a.E - 1 : id;
+    ids[j] = id;
+    const uint64_t row = (uint64_t)id * D + (live ? d : 0);
+    load_row(q[j], (const char *)a.wd_e + row * rI, lane, nI, ok);
+  }
   stage_swz<false, FP8 ? 16 : 8>(hs, a.h + (uint64_t)b * P, P, K, I);
   __syncthreads();
-  if (!live) return;
-  float acc = 0.0f;
+  // this half's segment values, in slot order
+  float sv[MOE_HALFK];
 #pragma unroll
-  for (int e = 0; e < MOE_MAXK; e++) {
-    if (e >= (int)K) break;
-    float s = wave_sum(chunk_dot<FP8>(q[e], hs + e * I, lane, nI));
-    if (a.sd_e) s *= a.sd_e[(uint64_t)ids[e] * D + d];
-    acc += a.probs[(uint64_t)b * K + e] * s;
+  for (int j = 0; j < MOE_HALFK; j++) {
+    const uint32_t e = e0 + j;
+    sv[j] = 0.0f;
+    if (e >= e1) continue;                               // wave-uniform
+    float t = wave_sum(chunk_dot<FP8>(q[j], hs + e * I, lane, nI));
+    if (a.sd_e) t *= a.sd_e[(uint64_t)ids[j] * D + (live ? d : 0)];
+    sv[j] = t;
   }
-  if (S > 0) {
-    float s = wave_sum(chunk_dot<FP8>(qs, hs + K * I, lane, nS));
-    if (a.sd_s) s *= a.sd_s[d];
-    acc += s;
+  float acc = 0.0f;
+  if (hf == 0) {
+#pragma unroll
+    for (int j = 0; j < MOE_HALFK; j++) {
+      const uint32_t e = j;
+      if (e >= e1) break;
+      acc += a.probs[(uint64_t)b * K + e] * sv[j];
+    }
+    if (lane == 0) part[rw] = acc;
   }
+  float ssh = 0.0f;
+  if (hf == 1 && S > 0) {
+    ssh = wave_sum(chunk_dot<FP8>(qs, hs + K * I, lane, nS));
+    if (a.sd_s) ssh *= a.sd_s[live ? d : 0];
+  }
+  __syncthreads();
+  if (hf == 0 || !live) return;
+  acc = part[rw];
+#pragma unroll
+  for (int j = 0; j < MOE_HALFK; j++) {
+    const uint32_t e = e0 + j;
+    if (e >= e1) break;
+    acc += a.probs[(uint64_t)b * K + e] * sv[j];
+  }
+  if (S > 0) acc += ssh;
   if (lane == 0) {
     bf16_t *r = (bf16_t *)a.res + (uint64_t)b * D + d;
     r[0] = f2bf(bf2f(r[0]) + rbf(acc));
@@ -936,8 +1029,17 @@ extern "C" int thvm_k_moe_down(const ThvmMoeArgs *a, hipStream_t s, char *err, i
   const uint32_t P = a->K * a->I + a->S;
   const uint32_t lds = P * 4;
   if (lds > 160 * 1024) { snprintf(err, errlen, "moe: K*I+S too large for LDS"); return -1; }
-  const dim3 grid((a->D + MOE_WAVES - 1) / MOE_WAVES, a->B);
-  const moe_fn f = a->wdt == THVM_DT_FP8E4M3 ? k_moe_down<true> : k_moe_down<false>;
+  const dim3 grid((a->D + MOE_WAVES / 2 - 1) / (MOE_WAVES / 2), a->B);
+  // chunks per lane sized to the rows (registers: two blocks per CU)
+  const uint32_t wsz = a->wdt == THVM_DT_FP8E4M3 ? 1 : 2;
+  const bool nc2 = a->I * wsz / 16 <= 128, ncs4 = a->S * wsz / 16 <= 256;
+  moe_fn f;
+  if (a->wdt == THVM_DT_FP8E4M3)
+    f = nc2 ? (ncs4 ? k_moe_down<true, 2, 4> : k_moe_down<true, 2, 8>)
+            : (ncs4 ? k_moe_down<true, 4, 4> : k_moe_down<true, 4, 8>);
+  else
+    f = nc2 ? (ncs4 ? k_moe_down<false, 2, 4> : k_moe_down<false, 2, 8>)
+            : (ncs4 ? k_moe_down<false, 4, 4> : k_moe_down<false, 4, 8>);
   if (lds > 64 * 1024) {
     hipError_t e = hipFuncSetAttribute((const void *)f, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     if (e != hipSuccess) { snprintf(err, errlen, "moe_down: hipFuncSetAttribute: %s", hipGetErrorString(e)); return -1; }
