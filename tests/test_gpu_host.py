@@ -215,3 +215,40 @@ def test_gpt2_driver_matches_oracle(T):
         assert nxt == int(nx_ref[0])
         cur = prompt[pos + 1] if pos + 1 < len(prompt) else nxt
     assert g.jit.cnt == 2, "the one-token forward was not captured"
+
+
+def test_state_dict_save_load_roundtrip(T, tmp_path):
+    """get_state_dict -> safe_save -> safe_load -> load_state_dict into a
+    fresh model: every tensor bit-equal (f32 and a bf16 one), and the loaded
+    model's forward equals the saved model's; a shape mismatch raises."""
+    say("case: state dict roundtrip")
+    from thvm_amd import nn, state as S
+
+    class Net:
+        def __init__(self):
+            self.l1 = nn.Linear(32, 48)
+            self.ln = nn.LayerNorm(48)
+            self.l2 = nn.Linear(48, 16, bias=False)
+            self.emb = T.Tensor(np.arange(12, dtype=np.float32).reshape(3, 4) / 7, dtype=T.dtypes.bfloat16)
+
+        def __call__(self, x):
+            return self.l2(self.ln(self.l1(x).relu()))
+
+    nn.manual_seed(1)
+    a = Net()
+    nn.manual_seed(2)
+    b = Net()
+    x = T.Tensor(np.random.default_rng(3).standard_normal((5, 32)).astype(np.float32))
+    fn = tmp_path / "net.safetensors"
+    S.safe_save(S.get_state_dict(a), fn)
+    loaded = S.safe_load(fn)
+    assert loaded["emb"].dtype.id == T.dtypes.bfloat16.id
+    got = S.load_state_dict(b, loaded)
+    assert len(got) == len(S.get_parameters(a)) == 6
+    for k, v in S.get_state_dict(a).items():
+        assert np.array_equal(S.get_state_dict(b)[k].numpy(), v.numpy()), k
+    assert np.array_equal(b(x).numpy(), a(x).numpy())
+    bad = dict(loaded)
+    bad["l1.weight"] = np.zeros((32, 48), np.float32)
+    with pytest.raises(ValueError):
+        S.load_state_dict(b, bad)

@@ -192,3 +192,50 @@ def test_hf_rotate_half_rows_become_interleaved_pairs():
     il = np.empty_like(q_il)
     il[:, 0::2], il[:, 1::2] = z.real, z.imag
     assert np.allclose(il[:, 0::2], hf[:, :hd // 2]) and np.allclose(il[:, 1::2], hf[:, hd // 2:])
+
+
+@pytest.mark.parametrize("dt", [W.DT_FP8E4M3, W.DT_FP8E5M2])
+def test_fp8_disk_tensors_decode_like_the_oracle(tmp_path, dt):
+    """fp8 tensors in a safetensors file read back as the OCP values of their
+    codes: every one of the 256 patterns against the oracle's decoder (pinned
+    to the reference's tables), NaNs as NaN."""
+    import _oracle as O
+    codes = np.arange(256, dtype=np.uint8).reshape(16, 16)
+    fn = tmp_path / "f8.safetensors"
+    W.safe_save({"w": (codes, dt)}, fn)
+    got = W.safe_load(fn)["w"].float32()
+    want = O.decode(codes, dt)
+    assert np.array_equal(np.isnan(got), np.isnan(want))
+    ok = ~np.isnan(want)
+    assert np.array_equal(got[ok], want[ok])
+
+
+def test_state_dict_names_follow_the_attribute_paths():
+    """get_state_dict keys are dotted attribute paths, list indices and dict
+    keys (py/thvm/nn_state.py:233-241), built without touching the device."""
+    from thvm_amd import state as S
+    from thvm_amd.tensor import LNode, Tensor, dtypes
+
+    def t():
+        return Tensor(LNode("CONST", (), 0.0, (), dtypes.float32))
+
+    class Block:
+        def __init__(self):
+            self.ln = {"weight": t(), "bias": t()}
+            self.mlp = [t(), t()]
+            self.eps = 1e-5
+
+    class Model:
+        def __init__(self):
+            self.wte = t()
+            self.h = [Block(), Block()]
+
+    m = Model()
+    sd = S.get_state_dict(m)
+    assert list(sd) == ["wte", "h.0.ln.weight", "h.0.ln.bias", "h.0.mlp.0", "h.0.mlp.1",
+                        "h.1.ln.weight", "h.1.ln.bias", "h.1.mlp.0", "h.1.mlp.1"]
+    assert sd["h.1.mlp.0"] is m.h[1].mlp[0]
+    assert list(S.get_state_dict(m, prefix="model."))[0] == "model.wte"
+    assert len(S.get_parameters(m)) == 9
+    with pytest.raises(KeyError):
+        S.load_state_dict(m, {"h.0.ln.weight": np.zeros(())})     # "wte" missing: strict

@@ -7,10 +7,12 @@ layout, which is the row-major [N, K] weight the gfx950 GEMV streams."""
 from __future__ import annotations
 
 import math
+import sys
 from typing import Optional
 
 import numpy as np
 
+from thvm_amd import state as _state
 from thvm_amd.tensor import Tensor, dtypes
 
 _RNG = np.random.default_rng(0)
@@ -71,14 +73,11 @@ class Embedding:
 
 
 def get_parameters(obj) -> list:
-    out = []
-    if isinstance(obj, Tensor):
-        return [obj]
-    if isinstance(obj, (list, tuple)):
-        for o in obj:
-            out += get_parameters(o)
-        return out
-    if hasattr(obj, "__dict__"):
-        for v in vars(obj).values():
-            out += get_parameters(v)
-    return out
+    """Every Tensor under obj (attributes, list items, dict values)."""
+    return _state.get_parameters(obj)
+
+
+# `thvm_amd.nn.state` as the reference's `thvm.nn.state` (safe_load,
+# load_state_dict, ...)
+state = _state
+sys.modules[__name__ + ".state"] = _state

@@ -958,6 +958,15 @@ class Tensor:
     def item(self):
         return self.numpy().reshape(-1)[0].item()
 
+    def replace(self, x) -> "Tensor":
+        """This tensor now stands for x (same shape; x's dtype and data), as
+        tinygrad's replace: the model's attribute keeps its identity."""
+        x = x if isinstance(x, Tensor) else Tensor(x, dtype=self.dtype)
+        if tuple(map(_key, x.shape)) != tuple(map(_key, self.shape)):
+            raise ValueError(f"replace: shape {x.shape} for a tensor of shape {self.shape}")
+        self.node = x.node
+        return self
+
     def assign(self, x) -> "Tensor":
         x = x if isinstance(x, Tensor) else Tensor(x, dtype=self.dtype)
         if tuple(map(_key, x.shape)) != tuple(map(_key, self.shape)):

@@ -61,6 +61,25 @@ def f32_to_bf16(a: np.ndarray) -> np.ndarray:
     return np.where(nan, ((u >> 16) | 0x40).astype(np.uint16), r)
 
 
+def fp8_table(dt: int) -> np.ndarray:
+    """The 256 values of an OCP OFP8 format as f32, from its definition:
+    e4m3 (bias 7, 3 mantissa bits, S.1111.111 NaN, no infinities) or e5m2
+    (bias 15, 2 mantissa bits, IEEE-style infinities and NaNs); subnormals
+    at the smallest exponent."""
+    mb, bias = (3, 7) if dt == DT_FP8E4M3 else (2, 15)
+    b = np.arange(256)
+    s = np.where(b & 0x80, -1.0, 1.0)
+    e = (b >> mb) & ((1 << (7 - mb)) - 1)
+    m = b & ((1 << mb) - 1)
+    v = np.where(e == 0, m / (1 << mb) * 2.0 ** (1 - bias), (1 + m / (1 << mb)) * 2.0 ** (e - bias))
+    if dt == DT_FP8E4M3:
+        v = np.where((b & 0x7F) == 0x7F, np.nan, v)
+    else:
+        top = e == 31
+        v = np.where(top & (m == 0), np.inf, np.where(top, np.nan, v))
+    return (s * v).astype(np.float32)
+
+
 @dataclass
 class DiskTensor:
     """A tensor stored in a file: `nbytes` bytes at `offset`."""
@@ -83,7 +102,11 @@ class DiskTensor:
 
     def float32(self) -> np.ndarray:
         a = self.numpy()
-        return bf16_to_f32(a) if self.dtype == DT_BF16 else np.asarray(a, np.float32)
+        if self.dtype == DT_BF16:
+            return bf16_to_f32(a)
+        if self.dtype in (DT_FP8E4M3, DT_FP8E5M2):
+            return fp8_table(self.dtype)[np.asarray(a)]
+        return np.asarray(a, np.float32)
 
     def upload(self, buf, dst_off: int = 0) -> None:
         """Stream the bytes into a device buffer (id or thvm_amd.Buffer)."""
