@@ -470,7 +470,7 @@ def run_host_gpt2(thvm, key: str, args) -> dict:
         pos += 1
     thvm.synchronize()
     dt = time.perf_counter() - t1
-    jit = g.model.forward_jit
+    jit = g.jit
     cpu = None
     if not args.no_cpu:
         sys.path.insert(0, str(ROOT / "tests"))
@@ -502,7 +502,9 @@ def run_host_gpt2(thvm, key: str, args) -> dict:
             "data": "synthetic",
             "config": {"workload": spec["name"] + ", through the Python Tensor host (TinyJit replay)",
                        "layers": L, "d_model": c["dim"], "heads": c["n_heads"], "vocab": c["vocab"],
-                       "batch": 1, "context": ctx, "parallelism": "single GPU", "path": "tensor-host"},
+                       "batch": 1, "context": ctx, "parallelism": "single GPU", "path": "tensor-host",
+                       "matmul": "rendered" if args.host_rendered else "gemv builtin",
+                       "beam": args.beam},
             "jit_kernels_per_step": int(jit.jit.op_count()) if jit.jit is not None else None,
             "cpu_baseline": cpu}
 
@@ -523,6 +525,11 @@ def main() -> int:
     ap.add_argument("--moe-mode", type=int, default=0, choices=[0, 1, 2],
                     help="DSV2 above 4 rows: expert-grouped MoE on MFMA (0/2) or on the VALU (1)")
     ap.add_argument("--layers", type=int, default=None, help="debug only: fewer layers (invalid metric)")
+    ap.add_argument("--host-rendered", action="store_true",
+                    help="with --host: matmuls rendered like every other kernel (THVM_HOST_GEMV=0), "
+                         "no GEMV builtin")
+    ap.add_argument("--beam", type=int, default=0,
+                    help="with --host: BEAM width for the rendered kernels' geometry search (0: hand-coded)")
     ap.add_argument("--host", action="store_true",
                     help="C1/C3: run the GPT-2 driver on the Python Tensor host (TinyJit) "
                          "instead of the C decoder")
@@ -535,6 +542,10 @@ def main() -> int:
               "the multi-GPU sharding is a design note, not a measured path", file=sys.stderr)
         return 2
 
+    if args.host_rendered:
+        os.environ["THVM_HOST_GEMV"] = "0"
+    if args.beam:
+        os.environ["BEAM"] = str(args.beam)
     import thvm_amd as thvm
     thvm.init()
     try:

@@ -194,8 +194,14 @@ def _oracle_gpt2(weights, cfg):
     return O.OracleModel(Dec(), cfg)
 
 
-def test_gpt2_driver_matches_oracle(T):
-    say("case: gpt2 host vs oracle")
+@pytest.mark.parametrize("host_gemv", ["1", "0"], ids=["gemv-builtin", "rendered-matmul"])
+def test_gpt2_driver_matches_oracle(T, monkeypatch, host_gemv):
+    """The GPT-2 driver against the oracle, with x @ W.T on the GEMV builtin
+    and, THVM_HOST_GEMV=0, rendered through the renderer target like every
+    other kernel (no builtin at all)."""
+    say(f"case: gpt2 host vs oracle, THVM_HOST_GEMV={host_gemv}")
+    monkeypatch.setenv("THVM_HOST_GEMV", host_gemv)
+    n_gemv = T.GlobalCounters.gemv_count
     from thvm_amd.gpt2 import GPT2
     L, D, H, V, MS = 2, 128, 4, 1000, 32
     w = GPT2.synthetic_weights(L, D, V, MS, seed=7)
@@ -215,6 +221,8 @@ def test_gpt2_driver_matches_oracle(T):
         assert nxt == int(nx_ref[0])
         cur = prompt[pos + 1] if pos + 1 < len(prompt) else nxt
     assert g.jit.cnt == 2, "the one-token forward was not captured"
+    if host_gemv == "0":
+        assert T.GlobalCounters.gemv_count == n_gemv, "a matmul reached the GEMV builtin"
 
 
 def test_state_dict_save_load_roundtrip(T, tmp_path):

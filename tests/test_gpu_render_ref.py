@@ -9,8 +9,9 @@ search (row (f)1), on the device.
 * The BEAM search (thvm_hip_render_autotune) on each: the winner's output
   still matches the reference, it is no slower than the hand-coded choice it
   started from, and a second search returns the cached winner.
-* A GPT-2-size matvec (50257 x 768 f32 rows, the LM head) and a 4096-wide
-  row sum: the searched geometry against the hand-coded one, printed."""
+* A GPT-2-size matvec (50257 x 768 f32 rows, the LM head), a square one and
+  long rows: the searched geometry (timed on cold caches) against the
+  hand-coded one, printed."""
 import numpy as np
 import pytest
 

@@ -58,8 +58,8 @@ def row_sum_dag(n_rows, n_cols, symbolic=False):
 
 def test_render_group_and_thread_geometry(tmp_path):
     src, info = hip.render_kernel(row_sum_dag(8, 1024), "k_rowsum")
-    assert info.group == 32 and info.grid_max == 1 and info.block == 256 and info.kvar_slot == 0
-    assert "__shfl_xor" in src and "__syncthreads" not in src and "extern \"C\" __global__" in src
+    assert info.group == 256 and info.grid_max == 8 and info.block == 256 and info.kvar_slot == 0
+    assert "wsum(" in src and "__syncthreads" in src and "extern \"C\" __global__" in src
     # the row offset does not read the reduce axis: hoisted out of the loop
     loop = src.index("for (int rr")
     assert src.index("((int)v") < loop
@@ -159,8 +159,8 @@ def test_lowering_softmax_is_three_kernels(fake_host):
     T, rendered = fake_host
     x = T.Tensor(np.zeros((4, 1000), np.float32))
     x.softmax(-1).realize()
-    # max and sum(exp) share each row among threads (hand-coded: 1000 / 32 -> 16), normalise is elementwise
-    assert [r[1].group for r in rendered] == [16, 16, 1]
+    # max and sum(exp) share each row among threads (hand-coded: 1000 / 4 -> 128), normalise is elementwise
+    assert [r[1].group for r in rendered] == [128, 128, 1]
 
 
 def test_lowering_fuses_elementwise_and_mean(fake_host):
@@ -171,7 +171,7 @@ def test_lowering_fuses_elementwise_and_mean(fake_host):
     assert len(rendered) == 1 and rendered[0][1].group == 1
     rendered.clear()
     a.mean(-1).realize()                                     # sum and scale in one kernel
-    assert len(rendered) == 1 and rendered[0][1].group == 16
+    assert len(rendered) == 1 and rendered[0][1].group == 128
 
 
 def test_lowering_symbolic_shrink(fake_host):

@@ -296,6 +296,11 @@ int thvm_k_quant_fp8_rows(uint8_t *q, float *scale, const void *x, uint32_t xdt,
  * byte read once and written once: the calibration of HBM traffic counters. */
 int thvm_k_copy(void *y, const void *x, uint64_t nbytes, hipStream_t s, char *err, int errlen);
 
+/* Read nbytes at x (16-byte aligned and sized) with streaming loads, one
+ * word per block into sink[nsink] (grid at most nsink blocks): evicts the
+ * caches with clean lines, for timing a kernel on cold caches. */
+int thvm_k_touch(const void *x, uint64_t nbytes, uint32_t *sink, uint32_t nsink, hipStream_t s,
+                 char *err, int errlen);
 /* Zero nbytes at y (any alignment) with a kernel, so the fill can sit in a
  * captured graph as a kernel node. */
 int thvm_k_zero(void *y, uint64_t nbytes, hipStream_t s, char *err, int errlen);

@@ -436,20 +436,23 @@ static uint32_t pow2_floor(uint64_t x) {
 
 /* The geometry the target picks without a search (the role of the
  * reference's hand-coded opts, src/codegen/hand_opts.c:337-802, for gfx950):
- * an un-nested reduction of length R over O outputs shares each output among
- * G = min(R / 32, 524288 / O) threads (powers of 2, at most 1024: at least 32
- * terms per thread, about 512K threads in all), one thread per output below
- * G = 16; blocks of max(G, 256) threads.  Measured on gfx950 with the search
- * (f32 rows, thvm_hip_render_autotune): 50257 x 768 wants one thread per
- * row, 4096 x 4096 a group of 128, 64 x 65536 groups of 1024.  Everything
- * else runs one output per thread in 256-thread blocks. */
+ * an un-nested reduction of length R >= 64 over O outputs shares each output
+ * among G = min(R / 4, 524288 / O, 1024) threads (powers of 2: at least 4
+ * terms per thread, at most about 512K threads in all), one thread per output
+ * where that leaves G below 16 (enough outputs to fill the machine one
+ * thread each); blocks of max(G, 256) threads.  Few outputs get wide groups
+ * (a thread's terms are a serial chain of loads); many outputs get one
+ * thread each.  Measured on gfx950 with the search (f32 rows,
+ * thvm_hip_render_autotune): 50257 x 768 wants one thread per row,
+ * 4096 x 4096 a group of 128, 64 x 65536 groups of 1024.  Everything else
+ * runs one output per thread in 256-thread blocks. */
 static void hand_opts(int has_red, int nested, int64_t red_len, uint64_t outputs, ThvmRenderOpts *o) {
   memset(o, 0, sizeof *o);
   o->block = RENDER_BLOCK;
   o->upcast = 1;
   o->group = 1;
-  if (has_red && !nested && red_len >= 128) {
-    uint32_t g = pow2_floor((uint64_t)red_len / 32);
+  if (has_red && !nested && red_len >= 64) {
+    uint32_t g = pow2_floor((uint64_t)red_len / 4);
     const uint32_t by_out = pow2_floor(outputs ? (524288 + outputs - 1) / outputs : 1);
     if (by_out < g) g = by_out;
     if (g > 1024) g = 1024;

@@ -808,10 +808,17 @@ def _try_gemv(n: LNode) -> bool:
     return True
 
 
+def _host_gemv() -> bool:
+    """THVM_HOST_GEMV=0 renders x @ W.T like every other kernel (a lifted
+    reduce through the renderer target and its opts) instead of calling the
+    GEMV builtin."""
+    return os.environ.get("THVM_HOST_GEMV", "1") != "0"
+
+
 def _realize(n: LNode):
     if n.op == "BUF":
         return
-    if n.op == "MATMUL" and _try_gemv(n):
+    if n.op == "MATMUL" and _host_gemv() and _try_gemv(n):
         return
     if n.op == "ASSIGN":
         target, value = n.srcs
