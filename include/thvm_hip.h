@@ -323,9 +323,10 @@ typedef struct ThvmDecodeConfig {
   /* DSV2 above 4 rows: the expert-grouped MoE on MFMA (0 or 2, the default)
    * or on the VALU (1); at 4 rows and below the per-row kernels run.      */
   uint32_t moe_mode;
-  /* LLAMA / GPT2 attention: 64-row cache chunks per split block (0 auto,
-   * else 1..64).  The persistent step's attention is the one-chunk form;
-   * an op-list decoder with attn_cpb 1 computes it bit for bit.           */
+  /* 64-row cache chunks per attention split block (0 auto, else 1..64):
+   * LLAMA / GPT2 attention, and the DSV2 latent split on MFMA.  The
+   * persistent step's attention is the one-chunk form; an op-list decoder
+   * with attn_cpb 1 computes it bit for bit.                              */
   uint32_t attn_cpb;
   /* next-token choice: temperature 0 is greedy (argmax, lowest index on
    * ties); above 0 each step samples an id from softmax(logits / temperature)

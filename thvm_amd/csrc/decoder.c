@@ -908,9 +908,10 @@ static int build_dsv2(Decoder *d) {
     pa[pnn++] = ckv; pa[pnn++] = kpe; pa[pnn++] = qlat; pa[pnn++] = qpe;
     if (op_add(d, "mla_prep", p, pa, pnn)) return -1;
 
+    /* attn_cpb > 0 also sets the MFMA latent split's chunks per block */
     snprintf(p, sizeof p,
-             "thvm-builtin:mla_attn b=%u h=%u dn=%u dr=%u kv=%u dv=%u maxseq=%u nsplit=%u wt=%u scale=%a",
-             B, H, dn, dr, kv, dv, c->max_seq, d->n_split, wdt, scale);
+             "thvm-builtin:mla_attn b=%u h=%u dn=%u dr=%u kv=%u dv=%u maxseq=%u nsplit=%u wt=%u scale=%a cpb=%u",
+             B, H, dn, dr, kv, dv, c->max_seq, d->n_split, wdt, scale, c->attn_cpb);
     u32 aa[10], an = 0;
     aa[an++] = o; aa[an++] = qlat; aa[an++] = qpe; aa[an++] = ckv; aa[an++] = kpe; aa[an++] = L;
     aa[an++] = tens_find(d, "mla.part"); aa[an++] = wuv;
