@@ -69,18 +69,36 @@ __device__ __forceinline__ float block_max(float v, float *red) {
 // rows of K <= 16*256: every element loaded once into registers, all loads
 // issued together
 #define NORM_REG 16
+// compile-time element access (the runtime switch of ld_a / st_a put every
+// load of a thread in its own branch, each waiting for the one before)
+template <uint32_t DT>
+__device__ __forceinline__ float ld_t(const void *p, uint64_t i) {
+  if (DT == THVM_DT_FP32) return ((const float *)p)[i];
+  if (DT == THVM_DT_BF16) return bf2f(((const bf16_t *)p)[i]);
+  return h2f(((const f16_t *)p)[i]);
+}
+template <uint32_t DT>
+__device__ __forceinline__ void st_t(void *p, uint64_t i, float v) {
+  if (DT == THVM_DT_FP32) ((float *)p)[i] = v;
+  else if (DT == THVM_DT_BF16) ((bf16_t *)p)[i] = f2bf(v);
+  else ((f16_t *)p)[i] = f2h(v);
+}
+// one row per block, thread t holding elements t, t + 256, ... (up to 16):
+// every x, gain and bias load of the thread is issued before any arithmetic
+// (clamped indices, the values past K masked afterwards); the sum of squares
+// (or of deviations) in element order, then the four-wave block sum
+template <uint32_t XT, uint32_t YT>
 __global__ __launch_bounds__(ROW_THREADS) void k_norm_reg(ThvmNormArgs a) {
   __shared__ float red[ROW_WAVES];
   const uint32_t m = blockIdx.x;
   const uint64_t xo = (uint64_t)m * a.ldx, yo = (uint64_t)m * a.ldy;
   const float invK = 1.0f / (float)a.K;
   float xv[NORM_REG], wv[NORM_REG], bv[NORM_REG];
-  // gain and bias loads go out with the x loads (clamped indices), so they
-  // cost no round trip after the reduction
 #pragma unroll
   for (int i = 0; i < NORM_REG; i++) {
     const uint32_t e = threadIdx.x + i * ROW_THREADS, ec = e < a.K ? e : 0;
-    xv[i] = e < a.K ? ld_a(a.x, xo + e, a.xdt) : 0.0f;
+    const float x = ld_t<XT>(a.x, xo + ec);
+    xv[i] = e < a.K ? x : 0.0f;
     wv[i] = a.w ? a.w[ec] : 1.0f;
     bv[i] = a.layernorm && a.b ? a.b[ec] : 0.0f;
   }
@@ -107,9 +125,19 @@ __global__ __launch_bounds__(ROW_THREADS) void k_norm_reg(ThvmNormArgs a) {
       float v = (xv[i] - mean) * inv;
       if (a.w) v = v * wv[i];
       if (a.layernorm && a.b) v = v + bv[i];
-      st_a(a.y, yo + e, a.ydt, v);
+      st_t<YT>(a.y, yo + e, v);
     }
   }
+}
+typedef void (*norm_fn)(ThvmNormArgs);
+template <uint32_t XT>
+static norm_fn norm_pick_y(uint32_t ydt) {
+  return ydt == THVM_DT_FP32 ? k_norm_reg<XT, THVM_DT_FP32>
+       : ydt == THVM_DT_BF16 ? k_norm_reg<XT, THVM_DT_BF16> : k_norm_reg<XT, THVM_DT_FP16>;
+}
+static norm_fn norm_pick(uint32_t xdt, uint32_t ydt) {
+  return xdt == THVM_DT_FP32 ? norm_pick_y<THVM_DT_FP32>(ydt)
+       : xdt == THVM_DT_BF16 ? norm_pick_y<THVM_DT_BF16>(ydt) : norm_pick_y<THVM_DT_FP16>(ydt);
 }
 
 __global__ __launch_bounds__(ROW_THREADS) void k_norm(ThvmNormArgs a) {
@@ -161,7 +189,7 @@ extern "C" int thvm_k_norm(const ThvmNormArgs *a, hipStream_t s, char *err, int 
     return -1;
   }
   if (a->K <= NORM_REG * ROW_THREADS)
-    thvm_launch(true, true, k_norm_reg, dim3(a->M), dim3(ROW_THREADS), 0, s, *a);
+    thvm_launch(true, true, norm_pick(a->xdt, a->ydt), dim3(a->M), dim3(ROW_THREADS), 0, s, *a);
   else
     thvm_launch(true, true, k_norm, dim3(a->M), dim3(ROW_THREADS), 0, s, *a);
   hipError_t e = hipGetLastError();
