@@ -402,6 +402,11 @@ uint32_t thvm_hip_decoder_position(uint32_t dec);
  * buffer id, dtype and byte size, so a host can read weights back. */
 uint32_t thvm_hip_decoder_tensor(uint32_t dec, const char *name,
                                  uint32_t *dtype_out, uint64_t *nbytes_out);
+/* Decoders above 4 rows keep a tiled copy ("<name>.tiled", the MFMA GEMM's
+ * tile layout) of each projection weight: after writing a weight tensor
+ * through its buffer, call this to refresh the copy (name NULL: every
+ * tiled weight).  A tensor with no tiled copy is a no-op.  0 / -1. */
+int      thvm_hip_decoder_sync_weights(uint32_t dec, const char *name);
 /* Algorithmic HBM bytes one decode step reads+writes at the current
  * position (weights + KV over the live context + activations). */
 uint64_t thvm_hip_decoder_step_bytes(uint32_t dec);

@@ -96,3 +96,38 @@ def test_gpt2_fp16_batch8_mfma(hip):
     """The GPT-2 XL B=8 path (LayerNorm kernels, fp16 MFMA GEMM with bias and
     GELU epilogues) at a small shape."""
     run_parity(hip, dict(GPT2, wdtype=DT_F16, adtype=DT_F16, batch=8), steps=4, ctx=0)
+
+
+@pytest.mark.parametrize("arch", ["llama-fp8", "llama-bf16", "gpt2-fp16"])
+def test_batched_decoder_tiled_weights_bit_equal(hip, monkeypatch, arch):
+    """Decoders above 4 rows read their projection weights from tiled copies
+    (the MFMA GEMM's layout); with THVM_HIP_WTILE=0 they read the row-major
+    tensors.  Both give the same bits: 3 steps' logits and ids, and a weight
+    rewritten through write_tensor reaches the tiled copy (sync_weights)."""
+    cfg = {"llama-fp8": dict(LLAMA, batch=8, wdtype=DT_FP8, adtype=DT_BF16),
+           "llama-bf16": dict(LLAMA, batch=8, wdtype=DT_BF16, adtype=DT_BF16),
+           "gpt2-fp16": dict(GPT2, wdtype=DT_F16, adtype=DT_F16, batch=8)}[arch]
+    say(f"case: tiled vs row-major weights, {arch}")
+    tok = np.random.default_rng(4).integers(0, cfg["vocab"], 8).astype(np.int32)
+    runs = []
+    for tile in ("1", "0"):
+        monkeypatch.setenv("THVM_HIP_WTILE", tile)
+        dec = hip.Decoder(seed=9, **cfg)
+        try:
+            try:
+                dec.tensor("lm.tiled" if arch != "gpt2-fp16" else "wte.tiled")
+                has_tiled = True
+            except hip.ThvmHipError:
+                has_tiled = False
+            assert has_tiled == (tile == "1")
+            wn = "l0.wo" if arch != "gpt2-fp16" else "l0.c_proj"
+            w = dec.read_tensor(wn)
+            dec.write_tensor(wn, w[::-1].copy())
+            dec.set_state(tok, 0)
+            for _ in range(3):
+                dec.step()
+            runs.append((dec.tokens(4), dec.logits()))
+        finally:
+            dec.close()
+    assert np.array_equal(runs[0][0], runs[1][0])
+    assert np.array_equal(runs[0][1].view(np.uint32), runs[1][1].view(np.uint32))

@@ -367,6 +367,86 @@ def test_gemm_mfma_epilogues(hip, M):
     assert not np.any(kc.read(np.uint16).reshape(M, Hkv, ms, hd)[:, :, pos + 1:])
 
 
+def _tile_ref(w: np.ndarray, es: int) -> np.ndarray:
+    """The MFMA tile layout written from its definition (kern_api.h,
+    thvm_k_tile_w): for 16-row group g and 64-k step s, es pieces j of 64
+    lanes x 16 bytes; lane l holds row 16 g + l % 16 from element s*64 +
+    (l // 16)*16 + j*16/es; rows past N are zero."""
+    N, Kb = w.shape
+    K = Kb // es
+    npad = (N + 15) // 16 * 16
+    wp = np.zeros((npad, Kb), np.uint8)
+    wp[:N] = w
+    out = np.empty(npad * Kb, np.uint8)
+    o = 0
+    for g in range(npad // 16):
+        for s in range(K // 64):
+            for j in range(es):
+                for l in range(64):
+                    b0 = (s * 64 + (l // 16) * 16 + j * (16 // es)) * es
+                    out[o:o + 16] = wp[g * 16 + l % 16, b0:b0 + 16]
+                    o += 16
+    return out
+
+
+@pytest.mark.parametrize("wx", MFMA_TYPES)
+@pytest.mark.parametrize("N", [40, 97])
+def test_tile_w_layout(hip, wx, N):
+    """tile_w writes the layout's definition byte for byte (a padded last
+    row group included)."""
+    wdt, _ = wx
+    es = 1 if wdt == DT_FP8 else 2
+    K = 192
+    say(f"case: tile_w layout wdt={wdt} N={N}")
+    rng = np.random.default_rng(17 + N + wdt)
+    w = rng.integers(0, 256, (N, K * es), dtype=np.uint8)
+    npad = (N + 15) // 16 * 16
+    t = hip.Buffer(npad * K * es)
+    hip.builtin("tile_w", [t, up(hip, w)], n=N, k=K, wt=wdt)
+    assert np.array_equal(t.read(np.uint8), _tile_ref(w, es))
+
+
+@pytest.mark.parametrize("wx", MFMA_TYPES)
+@pytest.mark.parametrize("M", [8, 16, 40, 64])
+@pytest.mark.parametrize("NK", [(97, 768), (1000, 512), (256, 4096)])
+def test_gemm_mfma_tiled_weights_bit_equal(hip, wx, M, NK):
+    """The MFMA GEMM over tiled weights (tiled=1) gives the row-major
+    launch's bits: the same bytes reach the same lanes, only the addresses
+    change.  Store and residual epilogues, every tile count."""
+    wdt, xdt = wx
+    N, K = NK
+    es = 1 if wdt == DT_FP8 else 2
+    say(f"case: gemm tiled wdt={wdt} xdt={xdt} M={M} N={N} K={K}")
+    rng = np.random.default_rng(7000 + 100 * wdt + M + N)
+    xs, ws, scale, _, _ = _gemv_case(hip, rng, wdt, M, N, K, xdt=xdt)
+    wb = up(hip, ws)
+    tw = hip.Buffer((N + 15) // 16 * 16 * K * es)
+    hip.builtin("tile_w", [tw, wb], n=N, k=K, wt=wdt)
+    xb = up(hip, xs)
+    sc = [up(hip, scale)] if scale is not None else []
+    for r in (1, 2, 4):
+        y0, y1 = hip.Buffer(M * N * 4), hip.Buffer(M * N * 4)
+        hip.builtin("gemv", [y0, xb, wb] + sc, m=M, n=N, k=K, wt=wdt, xt=xdt, yt=DT_F32, epi=0, path=2, r=r)
+        hip.builtin("gemv", [y1, xb, tw] + sc, m=M, n=N, k=K, wt=wdt, xt=xdt, yt=DT_F32, epi=0, path=2, r=r,
+                    tiled=1)
+        assert np.array_equal(y0.read(np.uint32), y1.read(np.uint32)), f"r={r}"
+    rs, _ = rand_store(rng, (M, N), xdt)
+    y0, y1 = up(hip, rs), up(hip, rs)
+    hip.builtin("gemv", [y0, xb, wb] + sc + [y0], m=M, n=N, k=K, wt=wdt, xt=xdt, yt=xdt, epi=1)
+    hip.builtin("gemv", [y1, xb, tw] + sc + [y1], m=M, n=N, k=K, wt=wdt, xt=xdt, yt=xdt, epi=1, tiled=1)
+    assert np.array_equal(y0.read(np.uint16), y1.read(np.uint16))
+
+
+def test_gemv_refuses_tiled_weights(hip):
+    """Tiled weights exist for the MFMA path only: the GEMV (M <= 4) refuses
+    them instead of reading the wrong bytes."""
+    N, K = 64, 256
+    w = np.zeros((N, K), np.uint16)
+    with pytest.raises(hip.ThvmHipError):
+        hip.builtin("gemv", [hip.Buffer(N * 4), up(hip, np.zeros(K, np.uint16)), up(hip, w)], m=1, n=N, k=K,
+                    wt=DT_BF16, xt=DT_BF16, yt=DT_F32, epi=0, tiled=1)
+
+
 @pytest.mark.parametrize("NK", [(4096, 4096), (14336, 4096), (50257, 768)])
 @pytest.mark.parametrize("M", [8, 64])
 def test_gemm_mfma_c2_shapes(hip, NK, M):

@@ -123,6 +123,7 @@ _SIGS = {
     "thvm_hip_decoder_read_logits": (_i32, [_u32, _vp, _u64]),
     "thvm_hip_decoder_position": (_u32, [_u32]),
     "thvm_hip_decoder_tensor": (_u32, [_u32, _cp, C.POINTER(_u32), C.POINTER(_u64)]),
+    "thvm_hip_decoder_sync_weights": (_i32, [_u32, _cp]),
     "thvm_hip_decoder_step_bytes": (_u64, [_u32]),
     "thvm_hip_decoder_step_kernels": (_u32, [_u32]),
     "thvm_hip_decoder_stage_clock": (C.c_int, [_u32, C.c_void_p, _u32]),
@@ -294,6 +295,13 @@ class Decoder:
         if a.nbytes != nb:
             raise ThvmHipError(f"write_tensor {name}: {a.nbytes} bytes, tensor holds {nb}")
         _check(lib().thvm_hip_buf_write(bid, a.ctypes.data, a.nbytes), "buf_write")
+        self.sync_weights(name)
+
+    def sync_weights(self, name: Optional[str] = None) -> None:
+        """Refresh the MFMA GEMM's tiled copy of a weight written through its
+        buffer (decoders above 4 rows; every weight when name is None)."""
+        _check(lib().thvm_hip_decoder_sync_weights(self.h, name.encode() if name else None),
+               "decoder_sync_weights")
 
     def set_state(self, tokens, pos: int) -> None:
         t = np.ascontiguousarray(np.asarray(tokens, np.int32))

@@ -65,6 +65,9 @@ typedef struct {
   DOp *sops;              /* the speculative step (spec_rows > 0) */
   u32 n_sops;
   u32 spec_slot;
+  /* the MFMA GEMM's tiled copies of weight matrices (batches above 4 rows) */
+  struct { u32 src, dst, n, k, wt; } tiles[512];
+  u32 n_tiles;
 } Decoder;
 
 #define MAX_DEC 8
@@ -156,7 +159,73 @@ static int weight_matrix(Decoder *d, const char *name, u32 rows, u32 cols, u32 *
   return 0;
 }
 
+/* The unsigned value of " key=" in a builtin spec (def when absent). */
+static u32 prog_u32(const char *prog, const char *key, u32 def) {
+  char k[24];
+  snprintf(k, sizeof k, " %s=", key);
+  const char *p = strstr(prog, k);
+  return p ? (u32)strtoul(p + strlen(k), NULL, 0) : def;
+}
+
+/* Batches above 4 rows run their projections on the MFMA GEMM, which reads
+ * weights in the tile layout of thvm_k_tile_w (a wave's load instruction
+ * then reads 1 KB contiguous instead of 16 rows x 64 bytes): each weight
+ * matrix such an op names gets a tiled copy "<name>.tiled", made here and
+ * refreshed by thvm_hip_decoder_sync_weights after the row-major tensor is
+ * written.  The row-major tensors stay what the decoder's tensor API reads
+ * and writes.  THVM_HIP_WTILE=0 keeps the row-major reads (A/B). */
+static int wtile_on(void) {
+  const char *e = getenv("THVM_HIP_WTILE");
+  return !(e && e[0] == '0');
+}
+
+static int tile_run(const Decoder *d, u32 i) {
+  char p[128];
+  snprintf(p, sizeof p, "thvm-builtin:tile_w n=%u k=%u wt=%u", d->tiles[i].n, d->tiles[i].k, d->tiles[i].wt);
+  const u32 ids[2] = {d->tiles[i].dst, d->tiles[i].src};
+  return run_now(p, ids, 2);
+}
+
+static u32 tiled_copy(Decoder *d, u32 src, u32 n, u32 k, u32 wt) {
+  for (u32 i = 0; i < d->n_tiles; i++)
+    if (d->tiles[i].src == src && d->tiles[i].n == n && d->tiles[i].k == k) return d->tiles[i].dst;
+  if (d->n_tiles >= sizeof d->tiles / sizeof d->tiles[0]) { hb_set_error("decoder: tiled weight table full"); return 0; }
+  const char *nm = "w";
+  for (u32 i = 0; i < d->nt; i++)
+    if (d->t[i].id == src) { nm = d->t[i].name; break; }
+  char tn[48];
+  snprintf(tn, sizeof tn, "%s.tiled", nm);
+  const u32 dst = tens_new(d, tn, wt, ((u64)n + 15) / 16 * 16 * k * hb_dt_size(wt));
+  if (!dst) return 0;
+  const u32 i = d->n_tiles++;
+  d->tiles[i].src = src; d->tiles[i].dst = dst; d->tiles[i].n = n; d->tiles[i].k = k; d->tiles[i].wt = wt;
+  return tile_run(d, i) ? 0 : dst;
+}
+
+static int op_add_raw(Decoder *d, const char *name, const char *prog, const u32 *args, u32 n);
+
 static int op_add(Decoder *d, const char *name, const char *prog, const u32 *args, u32 n) {
+  if (n >= 3 && d->rows > 4 && wtile_on() && strncmp(prog, "thvm-builtin:gemv ", 18) == 0 &&
+      prog_u32(prog, "norm", 0) == 0 && prog_u32(prog, "path", 0) != 1 && prog_u32(prog, "m", 0) > 4) {
+    const u32 wt = prog_u32(prog, "wt", 0), xt = prog_u32(prog, "xt", THVM_DT_BF16), k = prog_u32(prog, "k", 0);
+    const int mfma = k % 64 == 0 && ((wt == THVM_DT_FP16 && xt == THVM_DT_FP16) ||
+                                     (wt == THVM_DT_BF16 && xt == THVM_DT_BF16) ||
+                                     (wt == THVM_DT_FP8E4M3 && (xt == THVM_DT_BF16 || xt == THVM_DT_FP16)));
+    if (mfma && n <= 24 && strlen(prog) + 10 < 1024) {
+      const u32 tw = tiled_copy(d, args[2], prog_u32(prog, "n", 0), k, wt);
+      if (!tw) return -1;
+      u32 a2[24];
+      memcpy(a2, args, n * sizeof(u32));
+      a2[2] = tw;
+      char p2[1024];
+      snprintf(p2, sizeof p2, "%s tiled=1", prog);
+      return op_add_raw(d, name, p2, a2, n);
+    }
+  }
+  return op_add_raw(d, name, prog, args, n);
+}
+
+static int op_add_raw(Decoder *d, const char *name, const char *prog, const u32 *args, u32 n) {
   if (n > 24) { hb_set_error("decoder: op %s has too many args", name); return -1; }
   if (d->n_ops == d->cap_ops) {
     d->cap_ops = d->cap_ops ? 2 * d->cap_ops : 256;
@@ -1042,6 +1111,17 @@ static int build_dsv2(Decoder *d) {
                tens_find(d, "am.pi"), tens_find(d, "hist"), L};
   if (op_add(d, "argmax", p, am, 6)) return -1;
   return op_add(d, "len_bump", "thvm-builtin:len_bump delta=1", &L, 1);
+}
+
+THVM_API int thvm_hip_decoder_sync_weights(uint32_t h, const char *name) {
+  Decoder *d = dec_get(h);
+  if (!d) return -1;
+  const u32 src = name ? tens_find(d, name) : 0;
+  if (name && !src) { hb_set_error("decoder_sync_weights: no tensor %s", name); return -1; }
+  for (u32 i = 0; i < d->n_tiles; i++)
+    if (!name || d->tiles[i].src == src)
+      if (tile_run(d, i)) return -1;
+  return 0;
 }
 
 THVM_API void thvm_hip_decoder_destroy(uint32_t h) {

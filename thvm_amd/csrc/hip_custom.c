@@ -196,7 +196,8 @@ int hb_builtin_launch(const char *program, const u32 *ids, u32 n, int check_only
          spec_u32(&sp, "ngain", &ngain, 0, 1) || spec_u32(&sp, "nbias", &nbias, 0, a.norm == 2) ||
          spec_u32(&sp, "waves", &a.tune_waves, 0, 0) || spec_u32(&sp, "r", &a.tune_r, 0, 0) ||
          spec_u32(&sp, "u", &a.tune_u, 0, 0) || spec_u32(&sp, "blocks", &a.tune_blocks, 0, 0) ||
-         spec_u32(&sp, "path", &a.tune_path, 0, 0) || spec_u32(&sp, "spec", &a.spec, 0, 0));
+         spec_u32(&sp, "path", &a.tune_path, 0, 0) || spec_u32(&sp, "spec", &a.spec, 0, 0) ||
+         spec_u32(&sp, "tiled", &a.wtiled, 0, 0));
     {
       u32 ldy0 = a.epi == THVM_EPI_SWIGLU ? a.N / 2
                : (a.epi == THVM_EPI_QKV || a.epi == THVM_EPI_QKV_ROPE) ? a.n_heads * a.head_dim
@@ -215,7 +216,7 @@ int hb_builtin_launch(const char *program, const u32 *ids, u32 n, int check_only
                      : ((u64)(a.M - 1) * a.ldy + ncols_out) * ysz;
     a.y = arg(&c, slot++, ybytes);
     a.x = arg(&c, slot++, ((u64)(a.M - 1) * a.ldx + a.K) * xsz);
-    a.w = arg(&c, slot++, (u64)a.N * a.K * wsz);
+    a.w = arg(&c, slot++, (a.wtiled ? ((u64)a.N + 15) / 16 * 16 : (u64)a.N) * a.K * wsz);
     if (a.wdt == THVM_DT_FP8E4M3) a.scale = (const float *)arg(&c, slot++, (u64)a.N * 4);
     if (a.norm && ngain) a.norm_w = (const float *)arg(&c, slot++, (u64)a.K * 4);
     if (a.norm == 2 && nbias) a.norm_b = (const float *)arg(&c, slot++, (u64)a.K * 4);
@@ -237,6 +238,18 @@ int hb_builtin_launch(const char *program, const u32 *ids, u32 n, int check_only
     if (check_only) return 0;
     if (prof) hb_kprof_begin(K, &e0, &e1);
     rc = thvm_k_gemv(&a, HB_STREAM, err, sizeof err);
+  } else if (strcmp(K, "tile_w") == 0) {   /* y (tiled), w (row-major) */
+    u32 n = 0, k = 0, wt = 0;
+    NEED(spec_u32(&sp, "n", &n, 1, 0) || spec_u32(&sp, "k", &k, 1, 0) || spec_u32(&sp, "wt", &wt, 1, 0));
+    const u32 es = hb_dt_size(wt);
+    if (es != 1 && es != 2) { hb_set_error("builtin tile_w: wt must be a 1- or 2-byte type"); return -1; }
+    void *y = arg(&c, 0, ((u64)n + 15) / 16 * 16 * k * es);
+    const void *w = arg(&c, 1, (u64)n * k * es);
+    if (c.bad) return -1;
+    bytes = (u64)n * k * es * 2;
+    if (check_only) return 0;
+    if (prof) hb_kprof_begin(K, &e0, &e1);
+    rc = thvm_k_tile_w(y, w, n, k, es, HB_STREAM, err, sizeof err);
   } else if (strcmp(K, "norm") == 0) {
     ThvmNormArgs a;
     memset(&a, 0, sizeof a);

@@ -65,7 +65,19 @@ typedef struct ThvmGemvArgs {
    * positions of ONE sequence -- row m rotates at and appends to position
    * L-1+m of cache row 0 -- instead of M independent sequences */
   uint32_t spec;
+  /* MFMA path only: W is in the MFMA tile layout of thvm_k_tile_w (rows
+   * padded to a multiple of 16 with zeros) instead of row-major */
+  uint32_t wtiled;
 } ThvmGemvArgs;
+/* W [N, K] (row-major, element size es 1 or 2, K % 64 == 0) -> the MFMA
+ * tile layout: for each 16-row group g and 64-k step s a block of es KB at
+ * byte ((g * K/64 + s) * es) KB, holding es 1 KB pieces j, each 64 lanes x
+ * 16 bytes: lane l's bytes are row 16 g + l % 16, elements s*64 + (l/16)*16 +
+ * j*16/es onwards -- the 16 bytes the MFMA GEMM's lane l loads for that step,
+ * so one load instruction of a wave reads 1 KB contiguous.  Rows N..Npad-1
+ * (Npad = N rounded up to 16) are zero.  y holds Npad*K*es bytes. */
+int thvm_k_tile_w(void *y, const void *w, uint32_t N, uint32_t K, uint32_t es, hipStream_t s, char *err,
+                  int errlen);
 /* y = epi(x . W^T): the GEMV for M <= 4, the MFMA GEMM for M <= 64 (fp16 W
  * with fp16 x, bf16 W with bf16 x, fp8 W with bf16/fp16 x; K % 64 == 0; no
  * fused norm). */

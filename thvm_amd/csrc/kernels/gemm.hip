@@ -67,13 +67,22 @@ __global__ __launch_bounds__(GEMM_THREADS) void k_gemm(ThvmGemvArgs a) {
   const uint64_t wrow_b = (uint64_t)K * (WT == GW_FP8 ? 1 : 2);
   char *xs = (char *)red + (size_t)wv * (16 * MT * XROW);
 
-  // this block's weight rows; rows past N read zero
+  // this block's weight rows; rows past N read zero (row-major: the range
+  // ends at row N; tiled: the padded rows of the last group are zeros)
+  const bool tl = a.wtiled != 0;
+  const uint32_t nrow = tl ? (((N + 15u) & ~15u) - n0) : (N - n0);
   const buf_t wrs = buf_rsrc((const char *)a.w + (uint64_t)n0 * wrow_b,
-                             (uint32_t)(min(N - n0, 16u * NT) * wrow_b));
+                             (uint32_t)(min(nrow, 16u * NT) * wrow_b));
   const buf_t xrs = buf_rsrc(a.x, (uint32_t)(((uint64_t)(M - 1) * a.ldx + K) * 2));
+  // per step: row-major, lane l reads 16*WB bytes of row li at k quarter lg
+  // (an instruction covers 16 rows x 64 bytes); tiled, the same bytes sit at
+  // lane*16 of the step's 1 KB pieces (an instruction reads 1 KB contiguous)
+  const uint32_t sstep = tl ? 1024u * WB : 64u * WB, jstep = tl ? 1024u : 16u;
   uint32_t wo[NT];
 #pragma unroll
-  for (int t = 0; t < NT; t++) wo[t] = (uint32_t)((16u * t + li) * wrow_b) + lg * 16 * WB;
+  for (int t = 0; t < NT; t++)
+    wo[t] = tl ? (uint32_t)(t * S * WB * 1024u) + lane * 16u
+               : (uint32_t)((16u * t + li) * wrow_b) + lg * 16 * WB;
 
   f32x4_t acc[NT][MT];
 #pragma unroll
@@ -83,11 +92,11 @@ __global__ __launch_bounds__(GEMM_THREADS) void k_gemm(ThvmGemvArgs a) {
 
   uint4 wr[U][NT][WB];
   auto load = [&](int u, uint32_t s) {
-    const uint32_t so = s < s1 ? s * 64 * WB : BUF_OOB;
+    const uint32_t so = s < s1 ? s * sstep : BUF_OOB;
 #pragma unroll
     for (int t = 0; t < NT; t++)
 #pragma unroll
-      for (int j = 0; j < WB; j++) wr[u][t][j] = buf_ld_stream16(wrs, wo[t] + so + j * 16);
+      for (int j = 0; j < WB; j++) wr[u][t][j] = buf_ld_stream16(wrs, wo[t] + so + j * jstep);
   };
   // x rows [0, 16*MT) x steps [sc0, sc0 + SC), RPI rows per load instruction,
   // 8*SC lanes per row (16 bytes each), held in registers until stored to
@@ -261,5 +270,39 @@ extern "C" int thvm_k_gemm_mfma(const ThvmGemvArgs *a, hipStream_t s, char *err,
   thvm_launch(true, true, f, dim3(grid), dim3(GEMM_THREADS), lds, s, *a);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) { snprintf(err, errlen, "gemm launch: %s", hipGetErrorString(e)); return -1; }
+  return 0;
+}
+
+// ---- the MFMA tile layout of a weight matrix ------------------------------
+// One thread per 16-byte piece of the tiled matrix (the layout is described
+// at thvm_k_tile_w in kern_api.h).
+__global__ __launch_bounds__(256) void k_tile_w(uint4 *y, const unsigned char *w, uint32_t N, uint32_t K,
+                                                 uint32_t es, uint64_t nchunks) {
+  const uint64_t c = (uint64_t)blockIdx.x * 256 + threadIdx.x;
+  if (c >= nchunks) return;
+  const uint32_t per = 64u * es;                       // 16-byte pieces per (group, step) block
+  const uint64_t blk = c / per;
+  const uint32_t within = (uint32_t)(c % per), j = within / 64, l = within % 64;
+  const uint32_t S = K / 64;
+  const uint64_t g = blk / S;
+  const uint32_t st = (uint32_t)(blk % S);
+  const uint64_t n = g * 16 + (l % 16);
+  const uint32_t k0 = st * 64 + (l / 16) * 16 + j * (16 / es);
+  y[c] = n < N ? *(const uint4 *)(w + (n * K + k0) * es) : make_uint4(0, 0, 0, 0);
+}
+
+extern "C" int thvm_k_tile_w(void *y, const void *w, uint32_t N, uint32_t K, uint32_t es, hipStream_t s,
+                             char *err, int errlen) {
+  if ((es != 1 && es != 2) || N == 0 || K == 0 || K % 64 || ((uintptr_t)w & 15) || ((uintptr_t)y & 15)) {
+    snprintf(err, errlen, "tile_w: need es 1 or 2, K %% 64 == 0, 16-byte aligned buffers (N=%u K=%u es=%u)",
+             N, K, es);
+    return -1;
+  }
+  const uint64_t npad = ((uint64_t)N + 15) / 16 * 16;
+  const uint64_t nchunks = npad * K * es / 16;
+  thvm_launch(true, true, k_tile_w, dim3((unsigned)((nchunks + 255) / 256)), dim3(256), 0, s, (uint4 *)y,
+              (const unsigned char *)w, N, K, es, nchunks);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) { snprintf(err, errlen, "tile_w launch: %s", hipGetErrorString(e)); return -1; }
   return 0;
 }

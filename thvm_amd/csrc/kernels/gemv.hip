@@ -135,6 +135,10 @@ extern "C" int thvm_k_gemv(const ThvmGemvArgs *a, hipStream_t s, char *err, int 
          (a->wdt == THVM_DT_FP8E4M3 && (a->xdt == THVM_DT_BF16 || a->xdt == THVM_DT_FP16)));
     const bool mfma = a->tune_path == 2 || (a->tune_path == 0 && mfma_types && (a->M > 4 || xlds > 160 * 1024));
     if (mfma) return thvm_k_gemm_mfma(a, s, err, errlen);
+    if (a->wtiled) {
+      snprintf(err, errlen, "gemv: tiled weights run on the MFMA path only (M > 4, 16-bit x, K %% 64 == 0)");
+      return -1;
+    }
     if (a->M > 4) {
       if (a->M % 4 || a->epi == THVM_EPI_QKV || a->epi == THVM_EPI_QKV_ROPE) {
         snprintf(err, errlen, "gemv: M=%u rows of these dtypes run in chunks of 4: M must be a multiple "

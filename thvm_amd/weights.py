@@ -390,6 +390,7 @@ def write_weight(dec, name: str, w: np.ndarray) -> None:
                       cols=cols, xt=DT_FP32)
         finally:
             src.free()
+        dec.sync_weights(name)
         return
     if dt == DT_FP32:
         dec.write_tensor(name, w)
