@@ -98,15 +98,17 @@ def test_gpt2_fp16_batch8_mfma(hip):
     run_parity(hip, dict(GPT2, wdtype=DT_F16, adtype=DT_F16, batch=8), steps=4, ctx=0)
 
 
-@pytest.mark.parametrize("arch", ["llama-fp8", "llama-bf16", "gpt2-fp16"])
+@pytest.mark.parametrize("arch", ["llama-fp8", "llama-bf16", "gpt2-fp16", "dsv2-fp8"])
 def test_batched_decoder_tiled_weights_bit_equal(hip, monkeypatch, arch):
     """Decoders above 4 rows read their projection weights from tiled copies
     (the MFMA GEMM's layout); with THVM_HIP_WTILE=0 they read the row-major
     tensors.  Both give the same bits: 3 steps' logits and ids, and a weight
     rewritten through write_tensor reaches the tiled copy (sync_weights)."""
+    from test_gpu_dsv2 import DSV2
     cfg = {"llama-fp8": dict(LLAMA, batch=8, wdtype=DT_FP8, adtype=DT_BF16),
            "llama-bf16": dict(LLAMA, batch=8, wdtype=DT_BF16, adtype=DT_BF16),
-           "gpt2-fp16": dict(GPT2, wdtype=DT_F16, adtype=DT_F16, batch=8)}[arch]
+           "gpt2-fp16": dict(GPT2, wdtype=DT_F16, adtype=DT_F16, batch=8),
+           "dsv2-fp8": dict(DSV2, batch=8, wdtype=DT_FP8)}[arch]
     say(f"case: tiled vs row-major weights, {arch}")
     tok = np.random.default_rng(4).integers(0, cfg["vocab"], 8).astype(np.int32)
     runs = []
@@ -114,13 +116,17 @@ def test_batched_decoder_tiled_weights_bit_equal(hip, monkeypatch, arch):
         monkeypatch.setenv("THVM_HIP_WTILE", tile)
         dec = hip.Decoder(seed=9, **cfg)
         try:
-            try:
-                dec.tensor("lm.tiled" if arch != "gpt2-fp16" else "wte.tiled")
-                has_tiled = True
-            except hip.ThvmHipError:
-                has_tiled = False
-            assert has_tiled == (tile == "1")
-            wn = "l0.wo" if arch != "gpt2-fp16" else "l0.c_proj"
+            tiled_names = ["lm.tiled" if arch != "gpt2-fp16" else "wte.tiled"]
+            if arch == "dsv2-fp8":
+                tiled_names += ["l1.wgu_e.tiled", "l1.wd_e.tiled"]
+            for tn in tiled_names:
+                try:
+                    dec.tensor(tn)
+                    has_tiled = True
+                except hip.ThvmHipError:
+                    has_tiled = False
+                assert has_tiled == (tile == "1"), tn
+            wn = {"gpt2-fp16": "l0.c_proj", "dsv2-fp8": "l1.wd_e"}.get(arch, "l0.wo")
             w = dec.read_tensor(wn)
             dec.write_tensor(wn, w[::-1].copy())
             dec.set_state(tok, 0)

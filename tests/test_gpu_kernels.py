@@ -367,43 +367,43 @@ def test_gemm_mfma_epilogues(hip, M):
     assert not np.any(kc.read(np.uint16).reshape(M, Hkv, ms, hd)[:, :, pos + 1:])
 
 
-def _tile_ref(w: np.ndarray, es: int) -> np.ndarray:
+def _tile_ref(w: np.ndarray, lb: int) -> np.ndarray:
     """The MFMA tile layout written from its definition (kern_api.h,
-    thvm_k_tile_w): for 16-row group g and 64-k step s, es pieces j of 64
-    lanes x 16 bytes; lane l holds row 16 g + l % 16 from element s*64 +
-    (l // 16)*16 + j*16/es; rows past N are zero."""
-    N, Kb = w.shape
-    K = Kb // es
+    thvm_k_tile_w) for lanes reading lb bytes per step (a step is 4 lb bytes
+    of a row): for 16-row group g and step s, lb/16 pieces jj of 64 lanes x
+    16 bytes; lane l holds row 16 g + l % 16, bytes s*4lb + (l // 16)*lb +
+    jj*16; rows past N are zero."""
+    N, RB = w.shape
     npad = (N + 15) // 16 * 16
-    wp = np.zeros((npad, Kb), np.uint8)
+    wp = np.zeros((npad, RB), np.uint8)
     wp[:N] = w
-    out = np.empty(npad * Kb, np.uint8)
+    out = np.empty(npad * RB, np.uint8)
     o = 0
     for g in range(npad // 16):
-        for s in range(K // 64):
-            for j in range(es):
+        for s in range(RB // (4 * lb)):
+            for jj in range(lb // 16):
                 for l in range(64):
-                    b0 = (s * 64 + (l // 16) * 16 + j * (16 // es)) * es
+                    b0 = s * 4 * lb + (l // 16) * lb + jj * 16
                     out[o:o + 16] = wp[g * 16 + l % 16, b0:b0 + 16]
                     o += 16
     return out
 
 
-@pytest.mark.parametrize("wx", MFMA_TYPES)
+@pytest.mark.parametrize("wdt", [DT_FP8, DT_BF16])
+@pytest.mark.parametrize("lb", [0, 16, 32])
 @pytest.mark.parametrize("N", [40, 97])
-def test_tile_w_layout(hip, wx, N):
+def test_tile_w_layout(hip, wdt, lb, N):
     """tile_w writes the layout's definition byte for byte (a padded last
-    row group included)."""
-    wdt, _ = wx
+    row group included); lb 0 is the GEMM's 16 bytes per element byte."""
     es = 1 if wdt == DT_FP8 else 2
-    K = 192
-    say(f"case: tile_w layout wdt={wdt} N={N}")
-    rng = np.random.default_rng(17 + N + wdt)
+    K = 256
+    say(f"case: tile_w layout wdt={wdt} lb={lb} N={N}")
+    rng = np.random.default_rng(17 + N + wdt + lb)
     w = rng.integers(0, 256, (N, K * es), dtype=np.uint8)
     npad = (N + 15) // 16 * 16
     t = hip.Buffer(npad * K * es)
-    hip.builtin("tile_w", [t, up(hip, w)], n=N, k=K, wt=wdt)
-    assert np.array_equal(t.read(np.uint8), _tile_ref(w, es))
+    hip.builtin("tile_w", [t, up(hip, w)], n=N, k=K, wt=wdt, lb=lb)
+    assert np.array_equal(t.read(np.uint8), _tile_ref(w, lb or 16 * es))
 
 
 @pytest.mark.parametrize("wx", MFMA_TYPES)

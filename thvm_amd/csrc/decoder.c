@@ -66,7 +66,7 @@ typedef struct {
   u32 n_sops;
   u32 spec_slot;
   /* the MFMA GEMM's tiled copies of weight matrices (batches above 4 rows) */
-  struct { u32 src, dst, n, k, wt; } tiles[512];
+  struct { u32 src, dst, n, k, wt, lb; } tiles[512];
   u32 n_tiles;
 } Decoder;
 
@@ -181,14 +181,16 @@ static int wtile_on(void) {
 
 static int tile_run(const Decoder *d, u32 i) {
   char p[128];
-  snprintf(p, sizeof p, "thvm-builtin:tile_w n=%u k=%u wt=%u", d->tiles[i].n, d->tiles[i].k, d->tiles[i].wt);
+  snprintf(p, sizeof p, "thvm-builtin:tile_w n=%u k=%u wt=%u lb=%u", d->tiles[i].n, d->tiles[i].k,
+           d->tiles[i].wt, d->tiles[i].lb);
   const u32 ids[2] = {d->tiles[i].dst, d->tiles[i].src};
   return run_now(p, ids, 2);
 }
 
-static u32 tiled_copy(Decoder *d, u32 src, u32 n, u32 k, u32 wt) {
+static u32 tiled_copy(Decoder *d, u32 src, u32 n, u32 k, u32 wt, u32 lb) {
   for (u32 i = 0; i < d->n_tiles; i++)
-    if (d->tiles[i].src == src && d->tiles[i].n == n && d->tiles[i].k == k) return d->tiles[i].dst;
+    if (d->tiles[i].src == src && d->tiles[i].n == n && d->tiles[i].k == k && d->tiles[i].lb == lb)
+      return d->tiles[i].dst;
   if (d->n_tiles >= sizeof d->tiles / sizeof d->tiles[0]) { hb_set_error("decoder: tiled weight table full"); return 0; }
   const char *nm = "w";
   for (u32 i = 0; i < d->nt; i++)
@@ -199,6 +201,7 @@ static u32 tiled_copy(Decoder *d, u32 src, u32 n, u32 k, u32 wt) {
   if (!dst) return 0;
   const u32 i = d->n_tiles++;
   d->tiles[i].src = src; d->tiles[i].dst = dst; d->tiles[i].n = n; d->tiles[i].k = k; d->tiles[i].wt = wt;
+  d->tiles[i].lb = lb;
   return tile_run(d, i) ? 0 : dst;
 }
 
@@ -212,7 +215,7 @@ static int op_add(Decoder *d, const char *name, const char *prog, const u32 *arg
                                      (wt == THVM_DT_BF16 && xt == THVM_DT_BF16) ||
                                      (wt == THVM_DT_FP8E4M3 && (xt == THVM_DT_BF16 || xt == THVM_DT_FP16)));
     if (mfma && n <= 24 && strlen(prog) + 10 < 1024) {
-      const u32 tw = tiled_copy(d, args[2], prog_u32(prog, "n", 0), k, wt);
+      const u32 tw = tiled_copy(d, args[2], prog_u32(prog, "n", 0), k, wt, 16 * hb_dt_size(wt));
       if (!tw) return -1;
       u32 a2[24];
       memcpy(a2, args, n * sizeof(u32));
@@ -1071,8 +1074,19 @@ static int build_dsv2(Decoder *d) {
       u32 rb[3] = {sel, probs, gl};
       if (op_add(d, "route", p, rb, 3)) return -1;
     }
-    snprintf(p, sizeof p, "thvm-builtin:moe_gateup b=%u d=%u e=%u k=%u i=%u s=%u wt=%u grouped=%d route=%d",
-             B, D, E, K, I, S, wdt, grp, route_in_gu);
+    /* the MFMA grouped form reads tiled copies of the expert weights (see
+     * tiled_copy; gate/up 32 bytes per lane, down 16) */
+    const int mtile = grp == 2 && wtile_on() && (2 * I) % 16 == 0 && D % 16 == 0 && (2 * S) % 16 == 0 &&
+                      ((u64)D * hb_dt_size(wdt)) % 128 == 0 && ((u64)I * hb_dt_size(wdt)) % 64 == 0 &&
+                      ((u64)S * hb_dt_size(wdt)) % 64 == 0;
+    if (mtile) {
+      if (!(wgue = tiled_copy(d, wgue, E * 2 * I, D, wdt, 32))) return -1;
+      if (!(wde = tiled_copy(d, wde, E * D, I, wdt, 16))) return -1;
+      if (S && (!(wgus = tiled_copy(d, wgus, 2 * S, D, wdt, 32)) || !(wds = tiled_copy(d, wds, D, S, wdt, 16))))
+        return -1;
+    }
+    snprintf(p, sizeof p, "thvm-builtin:moe_gateup b=%u d=%u e=%u k=%u i=%u s=%u wt=%u grouped=%d route=%d%s",
+             B, D, E, K, I, S, wdt, grp, route_in_gu, mtile ? " tiled=1" : "");
     u32 ma[12], mn = 0;
     ma[mn++] = hmoe; ma[mn++] = xnf; ma[mn++] = sel; ma[mn++] = wgue;
     if (f8) ma[mn++] = sgue;
@@ -1080,8 +1094,8 @@ static int build_dsv2(Decoder *d) {
     if (grp) { ma[mn++] = tens_find(d, "moe.plan"); ma[mn++] = tens_find(d, "moe.live"); }
     if (route_in_gu) { ma[mn++] = gl; ma[mn++] = probs; }
     if (op_add(d, "moe_gateup", p, ma, mn)) return -1;
-    snprintf(p, sizeof p, "thvm-builtin:moe_down b=%u d=%u e=%u k=%u i=%u s=%u wt=%u grouped=%d", B, D, E,
-             K, I, S, wdt, grp);
+    snprintf(p, sizeof p, "thvm-builtin:moe_down b=%u d=%u e=%u k=%u i=%u s=%u wt=%u grouped=%d%s", B, D, E,
+             K, I, S, wdt, grp, mtile ? " tiled=1" : "");
     u32 mb[11], mbn = 0;
     mb[mbn++] = x; mb[mbn++] = hmoe; mb[mbn++] = sel; mb[mbn++] = probs; mb[mbn++] = wde;
     if (f8) mb[mbn++] = sde;

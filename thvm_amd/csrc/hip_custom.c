@@ -239,8 +239,9 @@ int hb_builtin_launch(const char *program, const u32 *ids, u32 n, int check_only
     if (prof) hb_kprof_begin(K, &e0, &e1);
     rc = thvm_k_gemv(&a, HB_STREAM, err, sizeof err);
   } else if (strcmp(K, "tile_w") == 0) {   /* y (tiled), w (row-major) */
-    u32 n = 0, k = 0, wt = 0;
-    NEED(spec_u32(&sp, "n", &n, 1, 0) || spec_u32(&sp, "k", &k, 1, 0) || spec_u32(&sp, "wt", &wt, 1, 0));
+    u32 n = 0, k = 0, wt = 0, lb = 0;
+    NEED(spec_u32(&sp, "n", &n, 1, 0) || spec_u32(&sp, "k", &k, 1, 0) || spec_u32(&sp, "wt", &wt, 1, 0) ||
+         spec_u32(&sp, "lb", &lb, 0, 0));
     const u32 es = hb_dt_size(wt);
     if (es != 1 && es != 2) { hb_set_error("builtin tile_w: wt must be a 1- or 2-byte type"); return -1; }
     void *y = arg(&c, 0, ((u64)n + 15) / 16 * 16 * k * es);
@@ -249,7 +250,7 @@ int hb_builtin_launch(const char *program, const u32 *ids, u32 n, int check_only
     bytes = (u64)n * k * es * 2;
     if (check_only) return 0;
     if (prof) hb_kprof_begin(K, &e0, &e1);
-    rc = thvm_k_tile_w(y, w, n, k, es, HB_STREAM, err, sizeof err);
+    rc = thvm_k_tile_w(y, w, n, k, es, lb, HB_STREAM, err, sizeof err);
   } else if (strcmp(K, "norm") == 0) {
     ThvmNormArgs a;
     memset(&a, 0, sizeof a);
@@ -377,7 +378,7 @@ int hb_builtin_launch(const char *program, const u32 *ids, u32 n, int check_only
          spec_u32(&sp, "e", &a.E, 1, 0) || spec_u32(&sp, "k", &a.K, 1, 0) ||
          spec_u32(&sp, "i", &a.I, 1, 0) || spec_u32(&sp, "s", &a.S, 0, 0) ||
          spec_u32(&sp, "wt", &a.wdt, 0, THVM_DT_FP8E4M3) || spec_u32(&sp, "grouped", &a.grouped, 0, 0) ||
-         spec_u32(&sp, "route", &route, 0, 0));
+         spec_u32(&sp, "route", &route, 0, 0) || spec_u32(&sp, "tiled", &a.wtiled, 0, 0));
     if (route && !gu) { hb_set_error("builtin moe_down: route=1 is a gate/up key"); return -1; }
     const u32 wsz = hb_dt_size(a.wdt);
     const int fp8 = a.wdt == THVM_DT_FP8E4M3;

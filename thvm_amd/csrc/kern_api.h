@@ -69,15 +69,19 @@ typedef struct ThvmGemvArgs {
    * padded to a multiple of 16 with zeros) instead of row-major */
   uint32_t wtiled;
 } ThvmGemvArgs;
-/* W [N, K] (row-major, element size es 1 or 2, K % 64 == 0) -> the MFMA
- * tile layout: for each 16-row group g and 64-k step s a block of es KB at
- * byte ((g * K/64 + s) * es) KB, holding es 1 KB pieces j, each 64 lanes x
- * 16 bytes: lane l's bytes are row 16 g + l % 16, elements s*64 + (l/16)*16 +
- * j*16/es onwards -- the 16 bytes the MFMA GEMM's lane l loads for that step,
- * so one load instruction of a wave reads 1 KB contiguous.  Rows N..Npad-1
- * (Npad = N rounded up to 16) are zero.  y holds Npad*K*es bytes. */
-int thvm_k_tile_w(void *y, const void *w, uint32_t N, uint32_t K, uint32_t es, hipStream_t s, char *err,
-                  int errlen);
+/* W [N, K] (row-major, element size es 1 or 2) -> the MFMA tile layout for
+ * lanes reading lb bytes of a row per k step (lb 16 or 32, 0 = 16 es; a step
+ * is 4 lb bytes of each of 16 rows, and 4 lb must divide a row): for 16-row
+ * group g and step s a block of 64 lb bytes at byte (g * S + s) * 64 lb
+ * (S = steps per row), holding lb / 16 pieces jj of 64 lanes x 16 bytes:
+ * lane l's bytes are row 16 g + l % 16, bytes s*4lb + (l/16)*lb + jj*16 of
+ * the row -- what a kernel's lane l loads for that step, so each load
+ * instruction of a wave reads 1 KB contiguous.  Rows N..Npad-1 (Npad = N
+ * rounded up to 16) are zero; y holds Npad*K*es bytes.  lb = 16 es is the
+ * MFMA GEMM's layout (64 k per step), lb 32 / 16 the grouped MoE's gate/up
+ * and down. */
+int thvm_k_tile_w(void *y, const void *w, uint32_t N, uint32_t K, uint32_t es, uint32_t lb, hipStream_t s,
+                  char *err, int errlen);
 /* y = epi(x . W^T): the GEMV for M <= 4, the MFMA GEMM for M <= 64 (fp16 W
  * with fp16 x, bf16 W with bf16 x, fp8 W with bf16/fp16 x; K % 64 == 0; no
  * fused norm). */
@@ -229,6 +233,10 @@ typedef struct ThvmMoeArgs {
    * sel_out / probs_out for the down kernel */
   const float *logits;
   int32_t *sel_out; float *probs_out;
+  /* grouped = 2 only: the expert weights (routed and shared) are in the
+   * tile layout of thvm_k_tile_w, 32 bytes per lane for gate/up and 16 for
+   * down (each expert's rows a whole number of 16-row groups) */
+  uint32_t wtiled;
 } ThvmMoeArgs;
 /* plan / part scratch sizes in bytes for the grouped form */
 uint64_t thvm_k_moe_plan_bytes(uint32_t B, uint32_t E, uint32_t K);

@@ -276,32 +276,34 @@ extern "C" int thvm_k_gemm_mfma(const ThvmGemvArgs *a, hipStream_t s, char *err,
 // ---- the MFMA tile layout of a weight matrix ------------------------------
 // One thread per 16-byte piece of the tiled matrix (the layout is described
 // at thvm_k_tile_w in kern_api.h).
-__global__ __launch_bounds__(256) void k_tile_w(uint4 *y, const unsigned char *w, uint32_t N, uint32_t K,
-                                                 uint32_t es, uint64_t nchunks) {
+__global__ __launch_bounds__(256) void k_tile_w(uint4 *y, const unsigned char *w, uint32_t N, uint64_t RB,
+                                                 uint32_t lb, uint64_t nchunks) {
   const uint64_t c = (uint64_t)blockIdx.x * 256 + threadIdx.x;
   if (c >= nchunks) return;
-  const uint32_t per = 64u * es;                       // 16-byte pieces per (group, step) block
+  const uint32_t per = 4u * lb;                        // 16-byte pieces per (group, step) block
   const uint64_t blk = c / per;
-  const uint32_t within = (uint32_t)(c % per), j = within / 64, l = within % 64;
-  const uint32_t S = K / 64;
-  const uint64_t g = blk / S;
-  const uint32_t st = (uint32_t)(blk % S);
+  const uint32_t within = (uint32_t)(c % per), jj = within / 64, l = within % 64;
+  const uint64_t S = RB / (4u * lb);
+  const uint64_t g = blk / S, st = blk % S;
   const uint64_t n = g * 16 + (l % 16);
-  const uint32_t k0 = st * 64 + (l / 16) * 16 + j * (16 / es);
-  y[c] = n < N ? *(const uint4 *)(w + (n * K + k0) * es) : make_uint4(0, 0, 0, 0);
+  const uint64_t b0 = st * 4u * lb + (l / 16) * lb + jj * 16;
+  y[c] = n < N ? *(const uint4 *)(w + n * RB + b0) : make_uint4(0, 0, 0, 0);
 }
 
-extern "C" int thvm_k_tile_w(void *y, const void *w, uint32_t N, uint32_t K, uint32_t es, hipStream_t s,
-                             char *err, int errlen) {
-  if ((es != 1 && es != 2) || N == 0 || K == 0 || K % 64 || ((uintptr_t)w & 15) || ((uintptr_t)y & 15)) {
-    snprintf(err, errlen, "tile_w: need es 1 or 2, K %% 64 == 0, 16-byte aligned buffers (N=%u K=%u es=%u)",
-             N, K, es);
+extern "C" int thvm_k_tile_w(void *y, const void *w, uint32_t N, uint32_t K, uint32_t es, uint32_t lb,
+                             hipStream_t s, char *err, int errlen) {
+  if (lb == 0) lb = 16 * es;
+  const uint64_t RB = (uint64_t)K * es;
+  if ((es != 1 && es != 2) || (lb != 16 && lb != 32) || N == 0 || K == 0 || RB % (4 * lb) ||
+      ((uintptr_t)w & 15) || ((uintptr_t)y & 15)) {
+    snprintf(err, errlen, "tile_w: need es 1 or 2, 16 or 32 bytes per lane dividing a quarter row, "
+             "16-byte aligned buffers (N=%u K=%u es=%u lb=%u)", N, K, es, lb);
     return -1;
   }
   const uint64_t npad = ((uint64_t)N + 15) / 16 * 16;
-  const uint64_t nchunks = npad * K * es / 16;
+  const uint64_t nchunks = npad * RB / 16;
   thvm_launch(true, true, k_tile_w, dim3((unsigned)((nchunks + 255) / 256)), dim3(256), 0, s, (uint4 *)y,
-              (const unsigned char *)w, N, K, es, nchunks);
+              (const unsigned char *)w, N, RB, lb, nchunks);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) { snprintf(err, errlen, "tile_w launch: %s", hipGetErrorString(e)); return -1; }
   return 0;

@@ -655,9 +655,15 @@ __global__ __launch_bounds__(64 * MM_WAVES) void k_moe_mm(ThvmMoeArgs a) {
   const char *wbase = KIND == 0 ? (shared ? (const char *)a.wgu_s : (const char *)a.wgu_e + (uint64_t)e * 2 * I * rowb)
                                 : (shared ? (const char *)a.wd_s : (const char *)a.wd_e + (uint64_t)e * D * rowb);
   const buf_t wrs = buf_rsrc(wbase + n0 * rowb, (uint32_t)(min(NR - n0, 16u * NT) * rowb));
+  // row-major: lane l reads LB bytes of row li at quarter lg per step; tiled
+  // (a.wtiled), the same bytes are the lane's 16-byte slots of the step's
+  // 64 LB-byte block, so every load instruction reads 1 KB contiguous
+  const bool tl = a.wtiled != 0;
+  const uint32_t sstep = tl ? 64u * LB : 4u * LB, jstep = tl ? 1024u : 16u;
   uint32_t wo[NT];
 #pragma unroll
-  for (int t = 0; t < NT; t++) wo[t] = (uint32_t)((16u * t + li) * rowb) + lg * LB;
+  for (int t = 0; t < NT; t++)
+    wo[t] = tl ? (uint32_t)(16u * t * rowb) + lane * 16u : (uint32_t)((16u * t + li) * rowb) + lg * LB;
   // this lane's x / h row (byte offset; out of range for columns past nrows)
   const buf_t xrs = KIND == 0 ? buf_rsrc(a.x, a.B * D * 4) : buf_rsrc(a.h, a.B * P * 4);
   uint32_t xo = BUF_OOB;
@@ -674,11 +680,11 @@ __global__ __launch_bounds__(64 * MM_WAVES) void k_moe_mm(ThvmMoeArgs a) {
   uint4 wq[NU][NT][NC], xq[NU][KL / 4];
   auto load = [&](int u, uint32_t st) {
     const bool in = st < s1;
-    const uint32_t so = in ? st * 4 * LB : BUF_OOB;                   // 4 LB weight bytes per row per step
+    const uint32_t so = in ? st * sstep : BUF_OOB;                    // 4 LB weight bytes per row per step
 #pragma unroll
     for (int t = 0; t < NT; t++)
 #pragma unroll
-      for (int jj = 0; jj < (int)NC; jj++) wq[u][t][jj] = buf_ld_stream16(wrs, wo[t] + so + jj * 16);
+      for (int jj = 0; jj < (int)NC; jj++) wq[u][t][jj] = buf_ld_stream16(wrs, wo[t] + so + jj * jstep);
     const uint32_t xs = in && xo != BUF_OOB ? xo + st * KS * 4 : BUF_OOB;
 #pragma unroll
     for (int q = 0; q < (int)KL / 4; q++) xq[u][q] = buf_ld16(xrs, xs + 16 * q);
@@ -716,7 +722,7 @@ __global__ __launch_bounds__(64 * MM_WAVES) void k_moe_mm(ThvmMoeArgs a) {
       L[j] = make_uint4(lb[0], lb[1], lb[2], lb[3]);
     }
     const bool in = nxt < s1;
-    const uint32_t so = in ? nxt * 4 * LB : BUF_OOB;
+    const uint32_t so = in ? nxt * sstep : BUF_OOB;
 #pragma unroll
     for (int t = 0; t < NT; t++) {
 #pragma unroll
@@ -733,7 +739,7 @@ __global__ __launch_bounds__(64 * MM_WAVES) void k_moe_mm(ThvmMoeArgs a) {
         if (KIND == 1) acc[t] = mfma16<GX_BF16>(A, L[j], acc[t]);
       }
 #pragma unroll
-      for (int jj = 0; jj < (int)NC; jj++) wq[u][t][jj] = buf_ld_stream16(wrs, wo[t] + so + jj * 16);
+      for (int jj = 0; jj < (int)NC; jj++) wq[u][t][jj] = buf_ld_stream16(wrs, wo[t] + so + jj * jstep);
     }
     const uint32_t xs = in && xo != BUF_OOB ? xo + nxt * KS * 4 : BUF_OOB;
 #pragma unroll
@@ -850,6 +856,10 @@ extern "C" int thvm_k_moe_gate(const ThvmGateArgs *a, hipStream_t s, char *err, 
 static int moe_check(const ThvmMoeArgs *a, int gateup, char *err, int errlen) {
   const uint32_t wsz = a->wdt == THVM_DT_FP8E4M3 ? 1 : a->wdt == THVM_DT_BF16 ? 2 : 0;
   if (!wsz) { snprintf(err, errlen, "moe: weights must be fp8 e4m3 or bf16"); return -1; }
+  if (a->wtiled && a->grouped != 2) {
+    snprintf(err, errlen, "moe: tiled expert weights are read by the MFMA grouped form (grouped=2) only");
+    return -1;
+  }
   if (a->B == 0 || a->D == 0 || a->E == 0 || a->K == 0 || a->K > MOE_MAXK || a->K > a->E ||
       a->I == 0) {
     snprintf(err, errlen, "moe: bad geometry (K <= %u)", MOE_MAXK);
@@ -925,6 +935,18 @@ static int moe_grouped_check(const ThvmMoeArgs *a, int gateup, char *err, int er
     return -1;
   }
   if (a->E > 64) { snprintf(err, errlen, "moe: grouped form takes E <= 64"); return -1; }
+  if (a->wtiled) {
+    const uint32_t es = a->wdt == THVM_DT_FP8E4M3 ? 1 : 2;
+    // whole 16-row groups per expert; a row a whole number of steps (gate/up
+    // 128-byte steps over D, down 64-byte steps over I and S)
+    const bool ok = a->grouped == 2 && (2 * a->I) % 16 == 0 && a->D % 16 == 0 && (2 * a->S) % 16 == 0 &&
+                    (gateup ? ((uint64_t)a->D * es) % 128 == 0
+                            : ((uint64_t)a->I * es) % 64 == 0 && ((uint64_t)a->S * es) % 64 == 0);
+    if (!ok) {
+      snprintf(err, errlen, "moe: tiled expert weights need the MFMA grouped form and 16-row-group experts");
+      return -1;
+    }
+  }
   return 0;
 }
 
