@@ -344,8 +344,9 @@ typedef struct ThvmDecodeConfig {
    * op-list step only; 0 = off.  spec_forced = 1 drafts the ids the host
    * seeded after the pending one instead (the acceptance gate).            */
   uint32_t spec_rows, spec_forced;
-  /* attention form: 0 auto, 1 one launch (the last split block of a row and
-   * kv head merges), 2 two launches (split, then merge)                    */
+  /* attention form: 0 auto (one launch for caches of at most 512 rows, two
+   * above), 1 one launch (the last split block of a row and kv head
+   * merges), 2 two launches (split, then merge)                            */
   uint32_t attn_fused;
 } ThvmDecodeConfig;
 

@@ -350,11 +350,13 @@ extern "C" int thvm_k_attn_decode(const ThvmAttnArgs *a, hipStream_t s, char *er
     return -1;
   }
   // fused = 1: the last split block of a (row, kv head) merges in the same
-  // launch; 0 and 2 (the shape's pick): a second launch merges
+  // launch; 0: a second launch merges; 2 (the shape's pick): one launch for
+  // caches of at most 8 chunks (512 rows), two above.  Measured in a graph on
+  // gfx950: one launch wins at short caches (C3 B=1 1.809 -> 1.767 ms, C3 B=8
+  // 2.372 -> 2.285, C1 0.396 -> 0.390 ms per step), two launches at long ones
+  // (C4: 11.1 against 11.9 us at L = 2051; B=16 3.50 against 3.59 ms).
   if (a->fused > 2) { snprintf(err, errlen, "attn: fused must be 0, 1 or 2"); return -1; }
-  // (picked: two launches -- in a graph at the C4 head shape they measured
-  // 11.1 against 11.9 us at L = 2051 and 11.8 against 14.0 us at L = 4096)
-  const bool fused = a->fused == 1;
+  const bool fused = a->fused == 1 || (a->fused == 2 && a->n_split <= 8);
   uint32_t cpb = a->cpb;
   if (cpb > a->n_split) cpb = a->n_split;          // one block takes every chunk
   if (cpb == 0) cpb = thvm_k_attn_auto_cpb(a->B, a->H, a->Hkv, a->n_split, fused);
