@@ -260,3 +260,82 @@ def test_state_dict_save_load_roundtrip(T, tmp_path):
     bad["l1.weight"] = np.zeros((32, 48), np.float32)
     with pytest.raises(ValueError):
         S.load_state_dict(b, bad)
+
+
+def test_more_elementwise_and_statistics(T):
+    """The tinygrad-named ops a reference script reaches for: eq/ne, sign,
+    trunc, erf, elu, softmin, bitwise and shifts, var/std, tril/eye,
+    split/chunk, *_like, against numpy."""
+    say("case: more ops")
+    import math
+    rng = np.random.default_rng(21)
+    a = (rng.standard_normal((4, 33)) * 2).astype(np.float32)
+    A, ad = T.Tensor(a), a.astype(np.float64)
+    close(A.sign().numpy(), np.sign(ad))
+    close(A.trunc().numpy(), np.trunc(ad))
+    close(A.erf().numpy(), np.vectorize(math.erf)(ad), rtol=0, atol=1e-6)   # 1.5e-7 method + f32 rounding
+    close(A.elu().numpy(), np.where(ad > 0, ad, np.exp(ad) - 1), rtol=1e-5, atol=1e-6)
+    e = np.exp(-ad - (-ad).max(-1, keepdims=True))
+    close(A.softmin(-1).numpy(), e / e.sum(-1, keepdims=True), rtol=1e-5, atol=1e-8)
+    close(A.var(-1).numpy(), ad.var(-1, ddof=1), rtol=1e-5, atol=1e-6)
+    close(A.std(1, correction=0).numpy(), ad.std(1), rtol=1e-5, atol=1e-6)
+    v, m = A.var_mean(0)
+    close(v.numpy(), ad.var(0, ddof=1), rtol=1e-5, atol=1e-6)
+    close(m.numpy(), ad.mean(0), rtol=1e-5, atol=1e-6)
+    assert np.array_equal(A.eq(A).numpy(), np.ones_like(a, bool)) and not A.ne(A).numpy().any()
+    i = rng.integers(-1000, 1000, (3, 17)).astype(np.int32)
+    I = T.Tensor(i)
+    assert np.array_equal(I.bitwise_and(0x5A).numpy(), i & 0x5A)
+    assert np.array_equal(I.bitwise_or(0x21).numpy(), i | 0x21)
+    assert np.array_equal(I.bitwise_xor(77).numpy(), i ^ 77)
+    assert np.array_equal(I.bitwise_not().numpy(), ~i)
+    assert np.array_equal(I.lshift(3).numpy(), i << 3)
+    assert np.array_equal(I.rshift(2).numpy(), i >> 2)
+    sq = rng.standard_normal((5, 5)).astype(np.float32)
+    assert np.array_equal(T.Tensor(sq).tril(-1).numpy(), np.tril(sq, -1))
+    assert np.array_equal(T.Tensor(sq).tril(1).numpy(), np.tril(sq, 1))
+    assert np.array_equal(T.Tensor.eye(3, 4).numpy(), np.eye(3, 4, dtype=np.float32))
+    parts = A.split([10, 23], dim=1)
+    assert np.array_equal(parts[1].numpy(), a[:, 10:])
+    ch = A.chunk(4, dim=1)
+    assert [c.shape[1] for c in ch] == [9, 9, 9, 6] and np.array_equal(ch[2].numpy(), a[:, 18:27])
+    assert np.array_equal(A.zeros_like().numpy(), np.zeros_like(a))
+    assert np.array_equal(A.full_like(2.5).numpy(), np.full_like(a, 2.5))
+    assert np.array_equal(A.clone().numpy(), a) and A.size(1) == 33 and A.element_size() == 4
+
+
+def test_device_random_and_multinomial(T):
+    """rand / randn / randint / multinomial on the device generator: ranges
+    and moments, reproducible after manual_seed, fresh draws on every call
+    and on every TinyJit replay; multinomial frequencies against the weights
+    (chi-square), without replacement never repeating an index.  Random
+    streams are this generator's own, not the reference's."""
+    say("case: device random")
+    T.Tensor.manual_seed(7)
+    u = T.Tensor.rand(200000).numpy()
+    assert u.min() >= 0.0 and u.max() < 1.0
+    assert abs(u.mean() - 0.5) < 0.005 and abs(u.var() - 1 / 12) < 0.002
+    u2 = T.Tensor.rand(200000).numpy()
+    assert not np.array_equal(u, u2)
+    T.Tensor.manual_seed(7)
+    assert np.array_equal(T.Tensor.rand(200000).numpy(), u)
+    z = T.Tensor.randn(100000).numpy()
+    assert abs(z.mean()) < 0.02 and abs(z.std() - 1) < 0.02
+    r = T.Tensor.randint(50000, low=3, high=9).numpy()
+    assert r.min() == 3 and r.max() == 8
+    p = np.array([0.1, 0.2, 0.3, 0.4], np.float32)
+    draws = T.Tensor(p).multinomial(20000, replacement=True).numpy()
+    cnt = np.bincount(draws, minlength=4)
+    chi2 = (((cnt - 20000 * p) ** 2) / (20000 * p)).sum()
+    assert chi2 < 16.3, (cnt, chi2)          # 3 dof, p = 0.001
+    w = T.Tensor(np.ones((3, 6), np.float32))
+    nr = w.multinomial(6).numpy()
+    assert all(sorted(row) == list(range(6)) for row in nr)
+
+    @T.TinyJit
+    def draw(x):
+        return (x + T.Tensor.rand(64)).realize()
+
+    x = T.Tensor(np.zeros(64, np.float32))
+    outs = [draw(x).numpy().copy() for _ in range(4)]
+    assert all(not np.array_equal(outs[i], outs[i + 1]) for i in range(3))

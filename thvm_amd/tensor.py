@@ -39,6 +39,7 @@ U_CONST, U_ADD, U_MUL, U_NEG, U_RECIP, U_EXP2, U_LOG2, U_SQRT, U_CMPLT = 2, 9, 1
 U_REDUCE, U_DEFINE_VAR, U_CMPEQ, U_LOAD, U_CAST, U_RANGE, U_INDEX_E = 17, 18, 20, 21, 23, 25, 26
 U_IADD, U_ISUB, U_IMUL, U_IDIV, U_IMOD, U_ILT, U_IAND, U_IWHERE = 27, 28, 29, 30, 31, 32, 33, 34
 U_BUFFER, U_STORE, U_IXOR, U_SIN = 36, 37, 42, 55
+U_IOR, U_ISHL, U_ISHR = 41, 44, 51
 KAX_REDUCE, KAX_GLOBAL = 1, 5
 REDUCE_SUM, REDUCE_MAX = 0, 1
 
@@ -57,6 +58,7 @@ class DType:
 class dtypes:
     bool = DType("bool", 0, 1, np.bool_)
     uint8 = DType("uint8", 2, 1, np.uint8)
+    uint32 = DType("uint", 6, 4, np.uint32)
     int32 = DType("int", 5, 4, np.int32)
     float16 = DType("half", 11, 2, np.float16)
     bfloat16 = DType("bfloat16", 12, 2, np.uint16)
@@ -74,7 +76,7 @@ class dtypes:
     @staticmethod
     def from_np(d) -> DType:
         d = np.dtype(d)
-        for t in (dtypes.float32, dtypes.float16, dtypes.int32, dtypes.bool, dtypes.uint8):
+        for t in (dtypes.float32, dtypes.float16, dtypes.int32, dtypes.bool, dtypes.uint8, dtypes.uint32):
             if np.dtype(t.np) == d:
                 return t
         if d == np.float64:
@@ -610,7 +612,8 @@ class _KB:
         fl = dtypes.is_float(dt)
         code = {"ADD": U_ADD if fl else U_IADD, "MUL": U_MUL if fl else U_IMUL, "NEG": U_NEG,
                 "RECIP": U_RECIP, "EXP2": U_EXP2, "LOG2": U_LOG2, "SQRT": U_SQRT, "SIN": U_SIN,
-                "IDIV": U_IDIV, "IMOD": U_IMOD, "XOR": U_IXOR}[name]
+                "IDIV": U_IDIV, "IMOD": U_IMOD, "XOR": U_IXOR, "AND": U_IAND, "OR": U_IOR,
+                "SHL": U_ISHL, "SHR": U_ISHR}[name]
         return self.add(code, dt.id, tuple(srcs))
 
 
@@ -676,6 +679,8 @@ def _deps(root: LNode) -> list:
 
 
 _RENDER_CACHE: dict = {}
+_RNG_SEED = 0          # Tensor.manual_seed
+_RNG_CTR = None        # the generator's device counter (a uint32 Tensor)
 _IN_JIT = 0        # inside a TinyJit function's eager first call
 
 
@@ -1053,6 +1058,7 @@ class Tensor:
     def log2(self): return self._un("LOG2")
     def sqrt(self): return self._un("SQRT")
     def sin(self): return self._un("SIN")
+    def cos(self): return ((math.pi / 2) - self).sin()
     def exp(self): return (self * (1.0 / math.log(2))).exp2()
     def log(self): return self.log2() * math.log(2)
     def rsqrt(self): return self.sqrt().reciprocal()
@@ -1250,6 +1256,193 @@ class Tensor:
         cols = Tensor.arange(int(c)).reshape(1, int(c))
         keep = (rows + diagonal - 1) < cols
         return keep.where(self, 0.0 if dtypes.is_float(self.dtype) else 0)
+
+    def tril(self, diagonal: int = 0) -> "Tensor":
+        r, c = self.shape[-2], self.shape[-1]
+        rows = Tensor.arange(int(r)).reshape(int(r), 1)
+        cols = Tensor.arange(int(c)).reshape(1, int(c))
+        keep = cols < (rows + diagonal + 1)
+        return keep.where(self, 0.0 if dtypes.is_float(self.dtype) else 0)
+
+    @staticmethod
+    def eye(n: int, m: Optional[int] = None, dtype: Optional[DType] = None, **kw) -> "Tensor":
+        m = n if m is None else m
+        dt = dtype or dtypes.float32
+        eq = Tensor.arange(n).reshape(n, 1) == Tensor.arange(m).reshape(1, m)
+        return eq.where(Tensor.full((), 1.0 if dtypes.is_float(dt) else 1, dtype=dt),
+                        Tensor.full((), 0.0 if dtypes.is_float(dt) else 0, dtype=dt))
+
+    def split(self, sizes, dim: int = 0) -> tuple:
+        """Pieces along dim: equal pieces of `sizes` (the last one shorter), or
+        the listed sizes."""
+        dim = dim % self.ndim
+        n = int(self.shape[dim])
+        if isinstance(sizes, int):
+            sizes = [min(sizes, n - i) for i in range(0, n, max(sizes, 1))]
+        if sum(sizes) != n:
+            raise ValueError(f"split: sizes {sizes} do not add up to {n}")
+        out, o = [], 0
+        for sz in sizes:
+            out.append(self.shrink(tuple((o, o + sz) if i == dim else None for i in range(self.ndim))))
+            o += sz
+        return tuple(out)
+
+    def chunk(self, chunks: int, dim: int = 0) -> tuple:
+        n = int(self.shape[dim % self.ndim])
+        return self.split(math.ceil(n / chunks) if n else 1, dim)
+
+    # ---- more elementwise (tinygrad names) ----
+    def eq(self, o): return self == o
+    def ne(self, o): return self != o
+    def neg(self): return -self
+    def recip(self): return self.reciprocal()
+    def pow(self, e): return self ** e
+    def sign(self):
+        one = 1.0 if dtypes.is_float(self.dtype) else 1
+        return (self > 0).where(one, (self < 0).where(-one, 0.0 if dtypes.is_float(self.dtype) else 0))
+    def trunc(self):
+        """Toward zero (|x| < 2^31)."""
+        return self.cast(dtypes.int32).cast(self.dtype) if dtypes.is_float(self.dtype) else self
+    def erf(self):
+        """erf by Abramowitz & Stegun 7.1.26 (|error| <= 1.5e-7 before f32 rounding)."""
+        x = self.abs()
+        t = 1.0 / (1.0 + 0.3275911 * x)
+        y = 1.0 - (((((1.061405429 * t - 1.453152027) * t) + 1.421413741) * t - 0.284496736) * t
+                   + 0.254829592) * t * (-(x * x)).exp()
+        return self.sign() * y
+    def elu(self, alpha: float = 1.0): return self.relu() - alpha * (1.0 - self.exp()).relu()
+    def softmin(self, axis=-1): return (-self).softmax(axis)
+    def bfloat16(self): return self.cast(dtypes.bfloat16)
+    def bitwise_and(self, o): return self._bin(o, "AND")
+    def bitwise_or(self, o): return self._bin(o, "OR")
+    def bitwise_xor(self, o): return self._bin(o, "XOR")
+    def bitwise_not(self):
+        return self.logical_not() if self.dtype.id == 0 else self._bin(-1 if self.dtype.id == 5 else 0xFFFFFFFF, "XOR")
+    def lshift(self, n: int): return self._bin(n, "SHL")
+    def rshift(self, n: int): return self._bin(n, "SHR")
+
+    # ---- statistics ----
+    def var(self, axis=None, keepdim=False, correction=1):
+        nd = self.ndim
+        axes = tuple(range(nd)) if axis is None else tuple(a % nd for a in ((axis,) if isinstance(axis, int) else axis))
+        n = int(_prod([self.shape[a] for a in axes]))
+        d = self - self.mean(axes, keepdim=True)
+        return (d * d).sum(axes, keepdim) * (1.0 / max(n - correction, 0) if n - correction > 0 else math.inf)
+    def std(self, axis=None, keepdim=False, correction=1): return self.var(axis, keepdim, correction).sqrt()
+    def var_mean(self, axis=None, keepdim=False, correction=1):
+        return self.var(axis, keepdim, correction), self.mean(axis, keepdim)
+    def std_mean(self, axis=None, keepdim=False, correction=1):
+        return self.std(axis, keepdim, correction), self.mean(axis, keepdim)
+
+    # ---- like-constructors and housekeeping ----
+    def zeros_like(self, **kw): return Tensor.zeros(*self.shape, dtype=kw.get("dtype", self.dtype))
+    def ones_like(self, **kw): return Tensor.ones(*self.shape, dtype=kw.get("dtype", self.dtype))
+    def full_like(self, v, **kw): return Tensor.full(self.shape, v, dtype=kw.get("dtype", self.dtype))
+    def empty_like(self, **kw): return Tensor.empty(*self.shape, dtype=kw.get("dtype", self.dtype))
+    def clone(self): return Tensor(LNode("CONTIG", (self.node,), None, self.shape, self.dtype)).realize()
+    def detach(self): return self
+    def to(self, device) -> "Tensor":
+        Device.canonicalize(device)
+        return self
+    def to_(self, device) -> "Tensor":
+        Device.canonicalize(device)
+        return self
+    def size(self, dim: Optional[int] = None):
+        return self.shape if dim is None else self.shape[dim]
+    def element_size(self) -> int: return self.dtype.itemsize
+    def is_floating_point(self) -> bool: return dtypes.is_float(self.dtype)
+
+    # ---- random numbers (on the device) ----
+    @staticmethod
+    def manual_seed(seed: int = 0) -> None:
+        """Seed the device generator and restart its stream."""
+        global _RNG_SEED, _RNG_CTR
+        _RNG_SEED, _RNG_CTR = int(seed) & 0xFFFFFFFF, None
+
+    @staticmethod
+    def _bits(n: int) -> "Tensor":
+        """n uniform 32-bit words: a counter-based hash (Wellons' lowbias32
+        finaliser over index, stream counter and seed), the counter a device
+        word read by the kernel and advanced by n afterwards, so a TinyJit
+        replay draws new words.  Its own generator: not the reference's
+        threefry stream."""
+        global _RNG_CTR
+        if _RNG_CTR is None:
+            _RNG_CTR = Tensor(np.zeros(1, np.uint32))
+        u32 = dtypes.uint32
+        c = _RNG_CTR.reshape(1).expand((n,))
+        i = Tensor.arange(n).cast(u32)
+        x = ((i + c) * 0x9E3779B1).bitwise_xor(_RNG_SEED * 0x85EBCA77 & 0xFFFFFFFF)
+        x = x.bitwise_xor(x.rshift(16)) * 0x7FEB352D
+        x = x.bitwise_xor(x.rshift(15)) * 0x846CA68B
+        x = x.bitwise_xor(x.rshift(16)).contiguous().realize()
+        _RNG_CTR.assign(_RNG_CTR + n).realize()
+        return x
+
+    @staticmethod
+    def rand(*shape, dtype: Optional[DType] = None, **kw) -> "Tensor":
+        """Uniform [0, 1): the top 24 bits of each word."""
+        shape = shape[0] if len(shape) == 1 and isinstance(shape[0], (tuple, list)) else shape
+        n = int(_prod(shape)) if shape else 1
+        u = Tensor._bits(n).rshift(8).cast(dtypes.float32) * (1.0 / (1 << 24))
+        u = u.reshape(shape) if shape else u.reshape(())
+        return u.cast(dtype) if dtype is not None and dtype.id != 13 else u
+
+    def rand_like(self, **kw): return Tensor.rand(*self.shape, dtype=kw.get("dtype", self.dtype))
+
+    @staticmethod
+    def randn(*shape, dtype: Optional[DType] = None, **kw) -> "Tensor":
+        """Standard normal by Box-Muller over two uniform draws."""
+        shape = shape[0] if len(shape) == 1 and isinstance(shape[0], (tuple, list)) else shape
+        u = Tensor.rand(2, *shape)
+        u1, u2 = u[0], u[1]
+        z = ((1.0 - u1).log() * -2.0).sqrt() * (u2 * (2 * math.pi)).cos()
+        return z.cast(dtype) if dtype is not None and dtype.id != 13 else z
+
+    def randn_like(self, **kw): return Tensor.randn(*self.shape, dtype=kw.get("dtype", self.dtype))
+
+    @staticmethod
+    def uniform(*shape, low=0.0, high=1.0, dtype: Optional[DType] = None, **kw) -> "Tensor":
+        return Tensor.rand(*shape, dtype=dtype) * (high - low) + low
+
+    @staticmethod
+    def normal(*shape, mean=0.0, std=1.0, dtype: Optional[DType] = None, **kw) -> "Tensor":
+        return Tensor.randn(*shape, dtype=dtype) * std + mean
+
+    @staticmethod
+    def randint(*shape, low=0, high=10, dtype: Optional[DType] = None, **kw) -> "Tensor":
+        shape = shape[0] if len(shape) == 1 and isinstance(shape[0], (tuple, list)) else shape
+        r = (Tensor.rand(*shape) * (high - low)).cast(dtypes.int32) + low
+        return r.cast(dtype) if dtype is not None else r
+
+    def multinomial(self, num_samples: int = 1, replacement: bool = False) -> "Tensor":
+        """num_samples indices per row, drawn with probability proportional to
+        self's weights: each draw is argmax(log w + Gumbel noise) (the
+        Gumbel-max form of a categorical draw); without replacement the drawn
+        entries are masked before the next draw (sequential draws of the same
+        distribution as the reference's Efraimidis-Spirakis keys)."""
+        assert 1 <= self.ndim <= 2 and num_samples > 0
+        w = self.unsqueeze(0) if self.ndim == 1 else self
+        R, N = int(w.shape[0]), int(w.shape[1])
+        assert replacement or num_samples <= N, "no replacement samples must not exceed population size"
+        lw = w.float().log()
+        if replacement or num_samples == 1:        # independent draws, all at once
+            g = -(-(Tensor.rand(num_samples, R, N).maximum(1e-30)).log()).log()
+            idx = (lw.unsqueeze(0) + g).argmax(2).permute(1, 0)
+            return (idx.squeeze(0) if self.ndim == 1 else idx).cast(dtypes.int32)
+        cols, mask = [], None
+        for _ in range(num_samples):
+            g = -(-(Tensor.rand(R, N).maximum(1e-30)).log()).log()
+            key = lw + g
+            if mask is not None:
+                key = mask.where(-math.inf, key)
+            pick = key.argmax(1, keepdim=True)
+            cols.append(pick)
+            if not replacement:
+                hit = Tensor.arange(N).reshape(1, N) == pick
+                mask = hit if mask is None else (mask.cast(dtypes.int32) + hit.cast(dtypes.int32)) > 0
+        idx = cols[0] if num_samples == 1 else cols[0].cat(*cols[1:], dim=1)
+        return (idx.squeeze(0) if self.ndim == 1 else idx).cast(dtypes.int32)
 
     # ---- linear algebra ----
     def matmul(self, w: "Tensor") -> "Tensor":
