@@ -637,6 +637,21 @@ def test_attention_multi_chunk_auto_repeated(hip):
         assert attn_close(got, ww, cdt), (L, np.max(np.abs(got - ww)))
 
 
+@pytest.mark.parametrize("L,ms", [(20000, 20480), (131000, 131072)])
+def test_attention_long_context(hip, L, ms):
+    """Caches far past 8192 rows (up to the 131072-row limit): the automatic
+    chunks per block and a merge of tens of partials per (row, kv head),
+    against the oracle."""
+    B, H, Hkv, hd, cdt = 1, 8, 2, 64, DT_BF16
+    say(f"case: attn long context L={L} max_seq={ms}")
+    rng = np.random.default_rng(L)
+    qs, _ = rand_store(rng, (B, H, hd), cdt)
+    ks, _ = rand_store(rng, (B, Hkv, ms, hd), cdt)
+    vs, _ = rand_store(rng, (B, Hkv, ms, hd), cdt)
+    got, ww = run_attn(hip, qs, ks, vs, B, H, Hkv, hd, ms, L, cdt)
+    assert attn_close(got, ww, cdt), np.max(np.abs(got - ww))
+
+
 def test_attention_cpb_errors(hip):
     B, H, Hkv, hd, ms, cdt = 1, 16, 2, 64, 128, DT_BF16
     z = np.zeros(B * H * hd, np.uint16)

@@ -30,7 +30,7 @@
 #define ATT_WAVES 8
 #define ATT_THREADS (ATT_WAVES * 64)
 #define ATT_CHUNK 64
-#define ATT_MAX_SPLITS 128   /* max_seq <= 8192 */
+#define ATT_MAX_SPLITS 2048  /* max_seq <= 131072 (the merge folds any number of partials) */
 #define LOG2E 1.4426950408889634f
 
 // activation dtype of q, the caches and the output (one compile-time type)
