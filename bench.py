@@ -509,6 +509,71 @@ def run_host_gpt2(thvm, key: str, args) -> dict:
             "cpu_baseline": cpu}
 
 
+def run_spec(thvm, args) -> dict:
+    """Speculative decode at C4 batch 1 (decoder spec_rows S): one captured
+    spec step = a bigram draft of S-1 ids, S verify rows of the sequence,
+    argmax and the commit.  Two measurements on the same model and context:
+    forced acceptance (spec_forced: the drafts are the greedy ids a base run
+    recorded, so every step commits S ids -- the throughput at full
+    acceptance), and the bigram draft on the model's own output (how many
+    ids it commits per step here).  The base one-row step is timed beside."""
+    import numpy as np
+    S = args.spec
+    spec = MODELS["C4"]
+    ctx, n = spec["ctx"], args.steps
+    res = {}
+    for forced in (1, 0):
+        cfg = dict(spec["cfg"], batch=1, spec_rows=S, spec_forced=forced)
+        cfg["max_seq"] = ((ctx + (n + 2) * S + args.warmup * S + 72 + 63) // 64) * 64
+        dec = thvm.Decoder(seed=1234, **cfg)
+        try:
+            dec.prefill_synthetic(ctx, seed=99)
+            dec.set_state([1], ctx)
+            dec.capture()
+            m = (n + args.warmup + 4) * S
+            dec.replay(m - 1)                        # the greedy continuation (base step)
+            thvm.synchronize()
+            greedy = dec.tokens(ctx + m + 1)[0][ctx + 1:].copy()
+            dec.set_state([1], ctx)
+            t = thvm.lib().thvm_hip_timer_start()
+            dec.replay(n)
+            base_ms = thvm.lib().thvm_hip_timer_stop(t) / n
+            dec.set_state([1], ctx)
+            if forced:
+                h = dec.read_tensor("hist")
+                h[ctx + 1:ctx + 1 + len(greedy)] = greedy
+                dec.write_tensor("hist", h)
+            dec.spec_capture()
+            dec.spec_replay(max(args.warmup, 1))
+            thvm.synchronize()
+            p0 = dec.position
+            t = thvm.lib().thvm_hip_timer_start()
+            dec.spec_replay(n)
+            ms = thvm.lib().thvm_hip_timer_stop(t)
+            adv = dec.position - p0
+            got = dec.tokens(dec.position + 1)[0][ctx + 1:]
+            ok = bool(np.array_equal(got, greedy[:len(got)]))
+            res[forced] = dict(ms_per_step=ms / n, ids_per_step=adv / n, tokens_per_s=adv / (ms / 1000.0),
+                               base_ms=base_ms, greedy_equal=ok)
+            log(f"[bench] spec S={S} forced={forced}: {ms / n:.3f} ms per spec step, {adv / n:.2f} ids per step, "
+                f"{adv / (ms / 1000.0):.1f} tok/s (base step {base_ms:.3f} ms); committed ids == greedy: {ok}")
+        finally:
+            dec.close()
+    f, b = res[1], res[0]
+    return {"metric": METRIC, "value": round(f["tokens_per_s"], 2), "unit": "tokens/s", "n_gpus": 1,
+            "steps": n, "warmup": args.warmup, "ms_per_step": round(f["ms_per_step"], 4),
+            "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+            "dtype": "fp8e4m3 weights x bf16 activations, f32 accumulate", "data": "synthetic",
+            "config": {"workload": f"C4 Llama-8B-shape fp8 speculative decode, S={S} verify rows, forced "
+                                   "acceptance (drafts = the recorded greedy ids), KV prefilled to context 2048",
+                       "batch": 1, "context": ctx, "spec_rows": S, "parallelism": "single GPU"},
+            "base_step_ms": round(f["base_ms"], 4),
+            "speedup_vs_base_at_full_acceptance": round(f["tokens_per_s"] * f["base_ms"] / 1000.0, 3),
+            "bigram_draft": {"ids_per_step": round(b["ids_per_step"], 3), "tokens_per_s": round(b["tokens_per_s"], 2),
+                             "ms_per_step": round(b["ms_per_step"], 4)},
+            "committed_ids_equal_greedy": f["greedy_equal"] and b["greedy_equal"]}
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -530,6 +595,9 @@ def main() -> int:
                          "no GEMV builtin")
     ap.add_argument("--beam", type=int, default=0,
                     help="with --host: BEAM width for the rendered kernels' geometry search (0: hand-coded)")
+    ap.add_argument("--spec", type=int, default=0,
+                    help="C4 batch 1 speculative decode with S verify rows (2..4): forced-acceptance "
+                         "throughput and the bigram draft's ids per step")
     ap.add_argument("--host", action="store_true",
                     help="C1/C3: run the GPT-2 driver on the Python Tensor host (TinyJit) "
                          "instead of the C decoder")
@@ -551,6 +619,9 @@ def main() -> int:
     try:
         if args.copy_calibration:
             return copy_calibration(thvm)
+        if args.spec:
+            print(json.dumps(run_spec(thvm, args)), flush=True)
+            return 0
         if args.config == "all":
             runs = [("C4", 1), ("C4", 16), ("C5", 1), ("C5", 32), ("C3", 1), ("C3", 8), ("C1", 1), ("C2", 0)]
         else:
