@@ -158,6 +158,10 @@ extern "C" int thvm_k_gemv(const ThvmGemvArgs *a, hipStream_t s, char *err, int 
       (uint64_t)a->K * wsz / 16 <= 128) {
     R = 2;
   }
+  // four x rows over long weight rows (>= 768 chunks): two rows per wave share
+  // each x read from LDS, which binds at M = 4 (measured on gfx950 at the C4
+  // down shape, 14336-wide fp8 rows: 24.7 -> 22.6 us); bit-identical sums
+  if (!a->tune_r && R == 1 && Mk == 4 && a->N % 2 == 0 && (uint64_t)a->K * wsz / 16 >= 768) R = 2;
   if (a->tune_r) {
     if (a->tune_r != 1 && a->tune_r != 2) { snprintf(err, errlen, "gemv: r must be 1 or 2"); return -1; }
     if ((pairs && a->tune_r == 1) || a->N % a->tune_r) { snprintf(err, errlen, "gemv: r=%u does not tile N/epilogue", a->tune_r); return -1; }
