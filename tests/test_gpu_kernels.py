@@ -367,6 +367,64 @@ def test_gemm_mfma_epilogues(hip, M):
     assert not np.any(kc.read(np.uint16).reshape(M, Hkv, ms, hd)[:, :, pos + 1:])
 
 
+@pytest.mark.parametrize("wdt", [DT_FP8, DT_BF16])
+@pytest.mark.parametrize("M", [5, 16, 17, 33, 64])
+@pytest.mark.parametrize("NK", [(97, 768), (130, 1600), (256, 4096)])
+def test_gemm_mfma_fused_rmsnorm(hip, wdt, M, NK):
+    """RMSNorm fused into the MFMA GEMM (bf16 x, the default above 4 rows)
+    against the norm kernel's semantics (oracle or_rmsnorm, rounded to bf16)
+    followed by the oracle GEMV.  The GEMM rounds x*g and scales the row sums
+    by 1/rms, so each product's one bf16 rounding sits elsewhere: within two
+    storage half-ulps per element, 2^-7 of the row's absolute sum.  K = 1600
+    (25 steps of 64 over 8 waves) gives uneven k slices, whose staging runs
+    past each slice's end."""
+    N, K = NK
+    say(f"case: gemm mfma fused rmsnorm wdt={wdt} M={M} N={N} K={K}")
+    rng = np.random.default_rng(7000 + 10 * wdt + M + K)
+    xs, xf = rand_store(rng, (M, K), DT_BF16, 3.0)
+    g = (1 + 0.2 * rng.standard_normal(K)).astype(np.float32)
+    xn = np.empty((M, K), np.uint16)
+    O.oracle().or_rmsnorm(xn.ctypes.data, DT_BF16, xs.ctypes.data, DT_BF16, g.ctypes.data, M, K, 1e-5)
+    xnf = O.decode(xn, DT_BF16)
+    if wdt == DT_FP8:
+        wf32 = (rng.standard_normal((N, K)) * 0.02).astype(np.float32)
+        scale = (np.abs(wf32).max(1) / 448.0).astype(np.float32)
+        ws = O.encode(wf32 / scale[:, None], DT_FP8)
+        wdq = O.decode(ws, DT_FP8) * scale[:, None]
+    else:
+        ws, wdq = rand_store(rng, (N, K), wdt, 0.02)
+        scale = None
+    ref = O.gemv(xn, DT_BF16, ws, wdt, scale, M=M, N=N, K=K)
+    floor = np.abs(xnf) @ np.abs(wdq).T
+    y = hip.Buffer(M * N * 4)
+    args = [y, up(hip, xs), up(hip, ws)] + ([up(hip, scale)] if scale is not None else []) + [up(hip, g)]
+    hip.builtin("gemv", args, m=M, n=N, k=K, wt=wdt, xt=DT_BF16, yt=DT_F32, epi=0, norm=1, eps=1e-5, path=2)
+    got = y.read(np.float32).reshape(M, N)
+    err = np.abs(got - ref)
+    assert np.all(err <= (1e-5 + 2.0 ** -7) * floor + 1e-6), np.max(err / floor)
+    # and well inside that on the whole: the roundings do not pile up one way
+    assert np.sum(err) <= 2.0 ** -9 * np.sum(floor)
+
+
+def test_gemm_mfma_fused_norm_limits(hip):
+    """The MFMA path fuses RMSNorm over bf16 x only: LayerNorm, fp16 x or a
+    missing gain are refused when path=2 forces it; by default such a batch
+    runs the GEMV in chunks of 4 rows with its own fused norm."""
+    M, N, K = 8, 64, 256
+    say("case: gemm mfma fused norm limits")
+    rng = np.random.default_rng(8)
+    xs, _ = rand_store(rng, (M, K), DT_F16)
+    ws, _ = rand_store(rng, (N, K), DT_F16, 0.02)
+    g = np.ones(K, np.float32)
+    y = hip.Buffer(M * N * 4)
+    with pytest.raises(hip.ThvmHipError, match="RMSNorm"):
+        hip.builtin("gemv", [y, up(hip, xs), up(hip, ws), up(hip, g)], m=M, n=N, k=K, wt=DT_F16,
+                    xt=DT_F16, yt=DT_F32, epi=0, norm=1, eps=1e-5, path=2)
+    hip.builtin("gemv", [y, up(hip, xs), up(hip, ws), up(hip, g)], m=M, n=N, k=K, wt=DT_F16,
+                xt=DT_F16, yt=DT_F32, epi=0, norm=1, eps=1e-5)
+    assert np.isfinite(y.read(np.float32)).all()
+
+
 def _tile_ref(w: np.ndarray, lb: int) -> np.ndarray:
     """The MFMA tile layout written from its definition (kern_api.h,
     thvm_k_tile_w) for lanes reading lb bytes per step (a step is 4 lb bytes

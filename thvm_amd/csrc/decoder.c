@@ -209,9 +209,11 @@ static int op_add_raw(Decoder *d, const char *name, const char *prog, const u32 
 
 static int op_add(Decoder *d, const char *name, const char *prog, const u32 *args, u32 n) {
   if (n >= 3 && d->rows > 4 && wtile_on() && strncmp(prog, "thvm-builtin:gemv ", 18) == 0 &&
-      prog_u32(prog, "norm", 0) == 0 && prog_u32(prog, "path", 0) != 1 && prog_u32(prog, "m", 0) > 4) {
+      prog_u32(prog, "path", 0) != 1 && prog_u32(prog, "m", 0) > 4) {
     const u32 wt = prog_u32(prog, "wt", 0), xt = prog_u32(prog, "xt", THVM_DT_BF16), k = prog_u32(prog, "k", 0);
-    const int mfma = k % 64 == 0 && ((wt == THVM_DT_FP16 && xt == THVM_DT_FP16) ||
+    const u32 nrm = prog_u32(prog, "norm", 0);
+    const int mfma = (nrm == 0 || (nrm == 1 && xt == THVM_DT_BF16)) && k % 64 == 0 &&
+                     ((wt == THVM_DT_FP16 && xt == THVM_DT_FP16) ||
                                      (wt == THVM_DT_BF16 && xt == THVM_DT_BF16) ||
                                      (wt == THVM_DT_FP8E4M3 && (xt == THVM_DT_BF16 || xt == THVM_DT_FP16)));
     if (mfma && n <= 24 && strlen(prog) + 10 < 1024) {
@@ -466,16 +468,20 @@ static int op_attn(Decoder *d, u32 l) {
   return op_add(d, "attn", p, a, 6);
 }
 
-/* The norm feeding a GEMV: fused into the GEMV's x staging (default), or as
- * a separate norm kernel writing xn (batches above 4 rows, whose projections
- * run on the MFMA GEMM, or THVM_HIP_UNFUSED_NORM=1 for A/B).
- * Writes the GEMV's input id to *gin and its norm spec fragment to nspec;
- * gains are appended to the GEMV's argument list by the caller via gargs. */
+/* The norm feeding a GEMV: fused into the GEMV's x staging (default; above
+ * 4 rows the MFMA GEMM's, which fuses RMSNorm over bf16 x), or as a separate
+ * norm kernel writing xn (LayerNorm or fp16 x above 4 rows, or
+ * THVM_HIP_UNFUSED_NORM=1 for A/B).  Above 4 rows every projection a norm
+ * feeds runs on the MFMA GEMM (dim % 64 == 0 and the dtypes are checked at
+ * config time).  Writes the GEMV's input id to *gin and its norm spec
+ * fragment to nspec; gains are appended to the GEMV's argument list by the
+ * caller via gargs. */
 typedef struct { int kind; u32 g, b; } NormSpec;
 
-static int fused_norms(const Decoder *d) {
+static int fused_norms(const Decoder *d, const NormSpec *ns) {
   const char *e = getenv("THVM_HIP_UNFUSED_NORM");
-  return d->rows <= 4 && !(e && e[0] == '1');
+  if (e && e[0] == '1') return 0;
+  return d->rows <= 4 || (ns->kind == 1 && d->c.adtype == THVM_DT_BF16);
 }
 
 static int emit_norm(Decoder *d, const NormSpec *ns, u32 *gin, char *nspec, size_t nlen,
@@ -483,7 +489,7 @@ static int emit_norm(Decoder *d, const NormSpec *ns, u32 *gin, char *nspec, size
   const ThvmDecodeConfig *c = &d->c;
   u32 x = act(d, "x"), xn = act(d, "xn");
   *ng = 0;
-  if (fused_norms(d)) {
+  if (fused_norms(d, ns)) {
     snprintf(nspec, nlen, " norm=%d eps=%a", ns->kind, c->eps);
     gargs[(*ng)++] = ns->g;
     if (ns->kind == 2) gargs[(*ng)++] = ns->b;

@@ -51,8 +51,10 @@ typedef struct ThvmGemvArgs {
   uint32_t wdt, xdt, ydt;  /* THVM_DT_*                                        */
   uint32_t epi;
   uint32_t n_heads, n_kv_heads, head_dim, max_seq;
-  /* fused norm prologue on x: 0 none, 1 RMSNorm, 2 LayerNorm; the normalised
-   * row is rounded to xdt, as the standalone norm kernel would store it */
+  /* fused norm on x: 0 none, 1 RMSNorm, 2 LayerNorm.  The GEMV rounds the
+   * normalised row to xdt, as the standalone norm kernel would store it; the
+   * MFMA GEMM (RMSNorm over bf16 x only) rounds x*gain and scales the row
+   * sums by 1/rms */
   uint32_t norm;
   float    norm_eps;
   const float *norm_w;     /* [K] gain or NULL                                */

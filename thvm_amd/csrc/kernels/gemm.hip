@@ -23,7 +23,14 @@
 //     thread finishes one row pair of one batch row through the shared
 //     epilogue;
 //   * x tiles are read from L2 (x is a few hundred KB at most and every
-//     block reads it), weights once from HBM.
+//     block reads it), weights once from HBM;
+//   * RMSNorm on x fused (NM = 1, bf16 x): the staging stores rnd(x * g[k])
+//     and sums x^2 over the wave's k slice; the slices' sums meet in LDS
+//     (wave order) and inv = 1/sqrtf(ss * (1/K) + eps) scales the finished
+//     row sums.  Each product x*g*w therefore carries one bf16 rounding, as
+//     with the norm kernel's rnd((x * inv) * g), at a different point; bf16
+//     keeps f32's exponent range, so x*g cannot overflow where x*inv*g would
+//     not.  The batched decode step then needs no separate norm launch.
 // MFMA operand k order: both operands give lane group g the same 8 k values
 // per instruction (k = 16g + j, then 16g + 8 + j), so the sum over k is the
 // full dot product whatever order the unit consumes them in.
@@ -51,9 +58,11 @@
 #endif
 #define GEMM_SC(MT) (GEMM_XSTAGE / (MT))
 #define GEMM_XROW(MT) (GEMM_SC(MT) * 128 + 16)
-template <int WT, int XT, int MT, int NT, int U>
+template <int WT, int XT, int MT, int NT, int U, int NM>
 __global__ __launch_bounds__(GEMM_THREADS) void k_gemm(ThvmGemvArgs a) {
   extern __shared__ float4 red[];                 // x staging, then [GEMM_WAVES][NT*MT][64]
+  __shared__ float ssw[NM ? GEMM_WAVES : 1][NM ? 64 : 1];   // per-wave sums of x^2 per x row
+  static_assert(!NM || XT == GX_BF16, "the fused norm stages bf16 x");
   constexpr int WB = WT == GW_FP8 ? 1 : 2;        // uint4 per lane per step per W tile
   constexpr int SC = GEMM_SC(MT), XROW = GEMM_XROW(MT);
   static_assert(SC % U == 0, "sub-chunks hold whole prefetch rounds");
@@ -108,13 +117,46 @@ __global__ __launch_bounds__(GEMM_THREADS) void k_gemm(ThvmGemvArgs a) {
   static_assert(SC <= 8 && RPI * SC == 8 && NI * RPI == 16 * MT, "staging shape");
   const uint32_t sr = lane / (8 * SC), sl = lane % (8 * SC);
   uint4 xv[NI];
+  // fused norm: the gains of the lane's 8 k, whether its step lies in the
+  // wave's slice (steps past s1 are staged for zero weights and must not
+  // count twice), and the lane's running sums of x^2, one per staged row
+  const buf_t grs = buf_rsrc(NM ? (const void *)a.norm_w : (const void *)a.x, NM ? K * 4u : 0u);
+  uint4 gv[2];
+  bool xok = false;
+  float ss[NI];
+#pragma unroll
+  for (int i = 0; i < NI; i++) ss[i] = 0.f;
   auto xload = [&](uint32_t sc0, bool live) {
     const uint32_t k = sc0 * 64 + sl * 8;
     const uint32_t base = live && k < K ? (sr * a.ldx + k) * 2 : BUF_OOB;
 #pragma unroll
     for (int i = 0; i < NI; i++) xv[i] = buf_ld16(xrs, base + i * RPI * a.ldx * 2);
+    if (NM) {
+      const uint32_t go = live && k < K ? k * 4 : BUF_OOB;
+      gv[0] = buf_ld16(grs, go);
+      gv[1] = buf_ld16(grs, go + 16);
+      xok = live && sc0 + sl / 8 < s1;
+    }
   };
   auto xstore = [&]() {
+    if (NM) {
+      const uint32_t gw[8] = {gv[0].x, gv[0].y, gv[0].z, gv[0].w, gv[1].x, gv[1].y, gv[1].z, gv[1].w};
+#pragma unroll
+      for (int i = 0; i < NI; i++) {
+        const uint32_t q[4] = {xv[i].x, xv[i].y, xv[i].z, xv[i].w};
+        uint32_t o[4];
+        float s = ss[i];
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+          const float lo = __uint_as_float(q[j] << 16), hi = __uint_as_float(q[j] & 0xffff0000u);
+          s = fmaf(lo, lo, s);
+          s = fmaf(hi, hi, s);
+          o[j] = pk_bf16(lo * __uint_as_float(gw[2 * j]), hi * __uint_as_float(gw[2 * j + 1]));
+        }
+        if (xok) ss[i] = s;
+        xv[i] = make_uint4(o[0], o[1], o[2], o[3]);
+      }
+    }
 #pragma unroll
     for (int i = 0; i < NI; i++) *(uint4 *)(xs + (i * RPI + sr) * XROW + sl * 16) = xv[i];
     // one wave writes and reads its region, and a wave's LDS operations
@@ -169,6 +211,15 @@ __global__ __launch_bounds__(GEMM_THREADS) void k_gemm(ThvmGemvArgs a) {
         load(u, sb + g * U + u + U);
       }
   }
+  if (NM) {   // a row's sum over the wave's slice: its 8*SC lanes, then LDS
+#pragma unroll
+    for (int i = 0; i < NI; i++) {
+      float s = ss[i];
+#pragma unroll
+      for (int o = 1; o < 8 * SC; o <<= 1) s += __shfl_xor(s, o);
+      if (sl == 0) ssw[wv][i * RPI + sr] = s;
+    }
+  }
   __syncthreads();                                // the staging area becomes the reduction buffer
 
   // partial tiles -> LDS, summed in wave order
@@ -193,6 +244,14 @@ __global__ __launch_bounds__(GEMM_THREADS) void k_gemm(ThvmGemvArgs a) {
       s0v += r == 0 ? q.x : q.z;
       s1v += r == 0 ? q.y : q.w;
     }
+    if (NM) {
+      float t = 0.f;
+#pragma unroll
+      for (int w = 0; w < GEMM_WAVES; w++) t += ssw[w][m];
+      const float inv = 1.0f / sqrtf(t * (1.0f / (float)K) + a.norm_eps);
+      s0v *= inv;
+      s1v *= inv;
+    }
     const float tot[2][1] = {{s0v}, {s1v}};
     gemv_epilogue<2, 1>(a, n0 + i0, tot, (uint32_t)m);
   }
@@ -201,24 +260,24 @@ __global__ __launch_bounds__(GEMM_THREADS) void k_gemm(ThvmGemvArgs a) {
 // -------------------------------------------------------------------------
 typedef void (*gemm_fn)(ThvmGemvArgs);
 
-template <int WT, int XT, int MT>
+template <int WT, int XT, int MT, int NM>
 static gemm_fn pick_nt(int NT) {
   constexpr int SC = GEMM_SC(MT);
   constexpr int U = (MT >= 4 ? 2 : 4) < SC ? (MT >= 4 ? 2 : 4) : SC;
   constexpr int U4 = MT >= 2 && U > 2 ? 2 : U;
   switch (NT) {
-    case 1: return k_gemm<WT, XT, MT, 1, U>;
-    case 2: return k_gemm<WT, XT, MT, 2, U>;
-    case 4: return k_gemm<WT, XT, MT, 4, U4>;
+    case 1: return k_gemm<WT, XT, MT, 1, U, NM>;
+    case 2: return k_gemm<WT, XT, MT, 2, U, NM>;
+    case 4: return k_gemm<WT, XT, MT, 4, U4, NM>;
     default: return nullptr;
   }
 }
-template <int WT, int XT>
+template <int WT, int XT, int NM = 0>
 static gemm_fn pick_mt(int MT, int NT) {
   switch (MT) {
-    case 1: return pick_nt<WT, XT, 1>(NT);
-    case 2: return pick_nt<WT, XT, 2>(NT);
-    case 4: return pick_nt<WT, XT, 4>(NT);
+    case 1: return pick_nt<WT, XT, 1, NM>(NT);
+    case 2: return pick_nt<WT, XT, 2, NM>(NT);
+    case 4: return pick_nt<WT, XT, 4, NM>(NT);
     default: return nullptr;
   }
 }
@@ -227,7 +286,10 @@ static gemm_fn pick_mt(int MT, int NT) {
 // epilogue geometry); validates what only the MFMA path needs.
 extern "C" int thvm_k_gemm_mfma(const ThvmGemvArgs *a, hipStream_t s, char *err, int errlen) {
   gemm_fn f = nullptr;
-  if (a->norm) { snprintf(err, errlen, "gemm: no fused norm on the MFMA path (run the norm kernel first)"); return -1; }
+  if (a->norm && (a->norm != 1 || a->xdt != THVM_DT_BF16 || a->norm_w == nullptr)) {
+    snprintf(err, errlen, "gemm: the MFMA path fuses RMSNorm with a gain over bf16 x only (norm=1, xt=bf16)");
+    return -1;
+  }
   if (a->M == 0 || a->M > 64) { snprintf(err, errlen, "gemm: M=%u out of range 1..64", a->M); return -1; }
   if (a->K % 64) { snprintf(err, errlen, "gemm: K=%u not a multiple of 64", a->K); return -1; }
   if (((uint64_t)a->ldx * 2) % 16 || ((uintptr_t)a->x & 15) || ((uintptr_t)a->w & 15)) {
@@ -247,7 +309,10 @@ extern "C" int thvm_k_gemm_mfma(const ThvmGemvArgs *a, hipStream_t s, char *err,
   int NT = a->tune_r ? (int)a->tune_r : (a->N >= 16384 ? 4 : a->N <= 4096 ? 1 : 2);
   if (NT != 1 && NT != 2 && NT != 4) { snprintf(err, errlen, "gemm: n tiles per block must be 1, 2 or 4"); return -1; }
   const int xbf = a->xdt == THVM_DT_BF16, xf16 = a->xdt == THVM_DT_FP16;
-  if (a->wdt == THVM_DT_FP8E4M3) {
+  if (a->norm) {
+    f = a->wdt == THVM_DT_FP8E4M3 ? pick_mt<GW_FP8, GX_BF16, 1>(MT, NT)
+      : a->wdt == THVM_DT_BF16 ? pick_mt<GW_BF16, GX_BF16, 1>(MT, NT) : nullptr;
+  } else if (a->wdt == THVM_DT_FP8E4M3) {
     f = xbf ? pick_mt<GW_FP8, GX_BF16>(MT, NT) : xf16 ? pick_mt<GW_FP8, GX_F16>(MT, NT) : nullptr;
   } else if (a->wdt == THVM_DT_BF16 && xbf) {
     f = pick_mt<GW_BF16, GX_BF16>(MT, NT);

@@ -86,13 +86,6 @@ extern "C" int thvm_k_gemv(const ThvmGemvArgs *a, hipStream_t s, char *err, int 
     snprintf(err, errlen, "gemv: waves per block must be 1,2,4,8 or 16");
     return -1;
   }
-  {
-    const uint32_t nw_norm = waves < 8 ? waves : 8;   // the norm runs on at most 512 threads
-    if (a->norm && a->K > (uint64_t)XREG * 64 * nw_norm) {
-      snprintf(err, errlen, "gemv: fused norm needs K <= %u for %u waves", XREG * 64 * nw_norm, waves);
-      return -1;
-    }
-  }
   int R = 1;
   int pairs = 0;
   switch (a->epi) {
@@ -126,17 +119,24 @@ extern "C" int thvm_k_gemv(const ThvmGemvArgs *a, hipStream_t s, char *err, int 
   // staging), the GEMV otherwise; tune_path 1/2 forces GEMV/MFMA
   if (a->tune_path > 2) { snprintf(err, errlen, "gemv: path must be 0, 1 or 2"); return -1; }
   // row chunks: M > 4 with operands the MFMA GEMM does not take (f32 weights
-  // or x, mixed 16-bit types, a fused norm) runs as M/4 chunks of 4 rows
+  // or x, mixed 16-bit types, a fused LayerNorm or a norm over 16-bit x
+  // other than bf16) runs as M/4 chunks of 4 rows
   uint32_t Mk = a->M, chunks = 1;
   {
     const uint64_t xlds = (uint64_t)a->M * a->K * ((a->xdt == THVM_DT_FP32 || a->wdt == THVM_DT_FP32) ? 4 : 2);
-    const bool mfma_types = !a->norm && a->K % 64 == 0 &&
+    const bool mfma_norm = !a->norm || (a->norm == 1 && a->xdt == THVM_DT_BF16 && a->norm_w);
+    const bool mfma_types = mfma_norm && a->K % 64 == 0 &&
         ((a->wdt == THVM_DT_FP16 && a->xdt == THVM_DT_FP16) || (a->wdt == THVM_DT_BF16 && a->xdt == THVM_DT_BF16) ||
          (a->wdt == THVM_DT_FP8E4M3 && (a->xdt == THVM_DT_BF16 || a->xdt == THVM_DT_FP16)));
     const bool mfma = a->tune_path == 2 || (a->tune_path == 0 && mfma_types && (a->M > 4 || xlds > 160 * 1024));
     if (mfma) return thvm_k_gemm_mfma(a, s, err, errlen);
     if (a->wtiled) {
       snprintf(err, errlen, "gemv: tiled weights run on the MFMA path only (M > 4, 16-bit x, K %% 64 == 0)");
+      return -1;
+    }
+    const uint32_t nw_norm = waves < 8 ? waves : 8;   // the norm runs on at most 512 threads
+    if (a->norm && a->K > (uint64_t)XREG * 64 * nw_norm) {
+      snprintf(err, errlen, "gemv: fused norm needs K <= %u for %u waves", XREG * 64 * nw_norm, waves);
       return -1;
     }
     if (a->M > 4) {
