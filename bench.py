@@ -252,6 +252,12 @@ def run_decode(thvm, key: str, batch: int, args) -> dict:
         step_bytes = sum(b for t, (_, _, b) in kern.items() if t != atag) // prof_steps + \
             attn_bytes_per_step(cfg, L_mid)
 
+    ceil = None
+    if dom == "gemv" and batch <= 4 and cfg["arch"] == 1 and not persist:
+        ceil = read_ceiling(thvm, dec, cfg)
+        log(f"[bench] read ceiling (k_touch over the same weights, step order): {ceil:.0f} GB/s; "
+            f"the GEMV reaches {gemv_gbs / ceil:.3f} of it")
+
     cpu = None
     if cpu_steps:
         tps_cpu, match, secs, lerr = cpu_baseline(dec, cfg, cpu_steps)
@@ -289,7 +295,12 @@ def run_decode(thvm, key: str, batch: int, args) -> dict:
                      "kernel": gkern,
                      "algorithmic_bytes_per_launch": g_bytes // max(g_n, 1),
                      "launches_per_step": g_n // prof_steps,
-                     "avg_launch_us": round(g_ms / g_n * 1000, 2)},
+                     "avg_launch_us": round(g_ms / g_n * 1000, 2),
+                     "read_ceiling": (None if ceil is None else
+                                      {"kernel": "k_touch: plain 16-byte loads over the same weight "
+                                                 "matrices, one launch each, step order",
+                                       "achieved": round(ceil, 1), "frac": round(ceil / PEAK_GBS, 4),
+                                       "gemv_of_ceiling": round(gemv_gbs / ceil, 4)})},
         "attention": ({"kernel": "a stage of k_llama_step (its bytes are in the roofline line)"}
                       if persist else
                       {"kernel": (("k_mla_split_mf (MFMA) + k_mla_out"
@@ -421,6 +432,31 @@ def copy_calibration(thvm) -> int:
                       "launches": n, "avg_launch_us": round(us, 2),
                       "gbs": round(2 * COPY_BYTES / (us * 1e-6) / 1e9, 1)}), flush=True)
     return 0
+
+
+def read_ceiling(thvm, dec, cfg, passes=2):
+    """What one plain-read launch reaches over the same bytes: k_touch (16-byte
+    loads over the whole range, 1024 blocks of 256 threads, nothing computed)
+    over each weight matrix of the LLAMA step's GEMV launches, in step order
+    (qkv, o, gate/up, down per layer, then the LM head), timed like the GEMV
+    (event pairs on the kernels, queued behind a sleep kernel so they run back
+    to back).  The whole pass reads every weight once, more than the 256 MB
+    last-level cache holds, so each launch reads cold.  Returns GB/s."""
+    names = [f"l{i}.{w}" for i in range(cfg["n_layers"]) for w in ("wqkv", "wo", "wgu", "wd")] + ["lm"]
+    bufs = [dec.tensor(n) for n in names]
+    sink, dummy = thvm.Buffer(1024 * 4), thvm.Buffer(64)
+    thvm.kprof(True)
+    thvm.kprof_reset()
+    for _ in range(passes):
+        thvm.builtin("delay", [dummy], n=3000)
+        for bid, _, nb in bufs:
+            thvm.builtin("touch", [bid, sink], outs=(1,), n=nb, blocks=1024)
+    ms, _ = thvm.kprof_query("touch")
+    nbytes = thvm.kprof_bytes("touch")
+    thvm.kprof(False)
+    sink.free()
+    dummy.free()
+    return nbytes / (ms / 1000.0) / 1e9
 
 
 def measured_traffic():

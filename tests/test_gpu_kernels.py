@@ -781,6 +781,24 @@ def test_len_bump(hip):
     assert L.read(np.int32)[0] == 43
 
 
+def test_touch_reads_and_leaves_data(hip):
+    """The read-only pass (the bench's read ceiling, the autotuner's cache
+    flush): the range is unchanged, the sink is written only on its 1-in-2^32
+    xor value (zero here), and a range that is not whole 16-byte pieces is
+    refused."""
+    say("case: touch")
+    a = np.zeros(1 << 20, np.uint32)            # 2^18 pieces: one per thread of 1024 x 256
+    a[0] = 0x9E3779B9                           # piece 0 xors to the sink value, the rest to 0
+    x = up(hip, a)
+    sink = up(hip, np.zeros(1024, np.uint32))
+    hip.builtin("touch", [x, sink], outs=(1,), n=a.nbytes, blocks=1024)
+    assert np.array_equal(x.read(np.uint32), a)
+    s = sink.read(np.uint32)
+    assert s[0] == 0x9E3779B9 and not s[1:].any()     # thread 0 of block 0 read that piece
+    with pytest.raises(hip.ThvmHipError):
+        hip.builtin("touch", [x, sink], outs=(1,), n=a.nbytes - 8, blocks=1024)
+
+
 def test_copy_and_kernel_timing(hip):
     """The plain copy kernel is byte-exact (odd 16-byte multiples, a partial
     grid-stride pass), rejects unaligned sizes, and the per-kernel timer binds

@@ -527,6 +527,17 @@ int hb_builtin_launch(const char *program, const u32 *ids, u32 n, int check_only
     if (check_only) return 0;
     if (prof) hb_kprof_begin(K, &e0, &e1);
     rc = thvm_k_len_bump(L, (int32_t)d, HB_STREAM, err, sizeof err);
+  } else if (strcmp(K, "touch") == 0) {   /* read a range into the caches */
+    u64 nb = 0;
+    u32 nsink = 0;
+    NEED(spec_u64(&sp, "n", &nb, 1, 0) || spec_u32(&sp, "blocks", &nsink, 0, 1024));
+    const void *x = arg(&c, 0, nb);
+    uint32_t *sink = (uint32_t *)arg(&c, 1, (u64)nsink * 4);
+    if (c.bad) return -1;
+    bytes = nb;
+    if (check_only) return 0;
+    if (prof) hb_kprof_begin(K, &e0, &e1);
+    rc = thvm_k_touch(x, nb, sink, nsink, HB_STREAM, err, sizeof err);
   } else if (strcmp(K, "delay") == 0) {
     u32 nper = 0;
     NEED(spec_u32(&sp, "n", &nper, 1, 0));
