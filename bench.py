@@ -436,7 +436,8 @@ def copy_calibration(thvm) -> int:
 
 def read_ceiling(thvm, dec, cfg, passes=2):
     """What one plain-read launch reaches over the same bytes: k_touch (16-byte
-    loads over the whole range, 1024 blocks of 256 threads, nothing computed)
+    loads over the whole range, 2048 blocks of 256 threads -- the best of a
+    512..8192 sweep at every C4 shape -- nothing computed)
     over each weight matrix of the LLAMA step's GEMV launches, in step order
     (qkv, o, gate/up, down per layer, then the LM head), timed like the GEMV
     (event pairs on the kernels, queued behind a sleep kernel so they run back
@@ -444,13 +445,13 @@ def read_ceiling(thvm, dec, cfg, passes=2):
     last-level cache holds, so each launch reads cold.  Returns GB/s."""
     names = [f"l{i}.{w}" for i in range(cfg["n_layers"]) for w in ("wqkv", "wo", "wgu", "wd")] + ["lm"]
     bufs = [dec.tensor(n) for n in names]
-    sink, dummy = thvm.Buffer(1024 * 4), thvm.Buffer(64)
+    sink, dummy = thvm.Buffer(2048 * 4), thvm.Buffer(64)
     thvm.kprof(True)
     thvm.kprof_reset()
     for _ in range(passes):
         thvm.builtin("delay", [dummy], n=3000)
         for bid, _, nb in bufs:
-            thvm.builtin("touch", [bid, sink], outs=(1,), n=nb, blocks=1024)
+            thvm.builtin("touch", [bid, sink], outs=(1,), n=nb, blocks=2048)
     ms, _ = thvm.kprof_query("touch")
     nbytes = thvm.kprof_bytes("touch")
     thvm.kprof(False)
