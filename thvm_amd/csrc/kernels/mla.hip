@@ -296,7 +296,12 @@ __global__ __launch_bounds__(MLA_THREADS) void k_mla_split(ThvmMlaArgs a) {
 //           tiles per wave.  The rows are staged column-major within each
 //           group of 8 rows ([row / 8][column][row % 8]), so a lane's B
 //           operand -- 8 rows of one column -- is one 16-byte LDS read; the
-//           transposing 2-byte writes need no wait.
+//           transposing 2-byte writes need no wait.  16 bytes of padding
+//           after every 8 columns and a group pitch of 2320 dwords spread
+//           one store instruction's 64 lanes over 32 distinct dwords (two
+//           lanes per dword) with 32 or 64 banks alike: the 4 column groups
+//           of a row land 36 dwords apart, the two 8-row groups 16 banks
+//           apart.
 // q and p (f32) enter as bf16 hi + lo pairs (two MFMAs each), so a product
 // keeps ~16 significant bits of the f32 operand against the exact bf16 cache
 // value: f32-level agreement with the VALU split.  A block runs cpb
@@ -310,7 +315,8 @@ __global__ __launch_bounds__(MLA_THREADS) void k_mla_split(ThvmMlaArgs a) {
 #define MF_KV 512
 #define MF_DR 64
 #define MF_KS ((MF_KV + MF_DR) / 32)       /* 18 k-steps */
-#define MF_RGP (512 * 16 + 16)             /* LDS pitch of a staged 8-row group (bytes) */
+#define MF_CADDR(k) ((k) * 16 + ((k) >> 3) * 16)   /* byte offset of column k in an 8-row group */
+#define MF_RGP (MF_CADDR(512) + 64)        /* LDS pitch of a staged 8-row group (bytes) */
 #define MF_PWP 68                          /* LDS pitch of a head's softmax weights (floats) */
 #define MF_THREADS 512                     /* 8 waves: two per 16-row tile */
 #define MF_KH (MF_KS / 2)                  /* k-steps per wave */
@@ -428,15 +434,15 @@ __global__ __launch_bounds__(MF_THREADS) void k_mla_split_mf(ThvmMlaArgs a) {
     // column k at [r / 8][k][r % 8]
     {
       const uint32_t r = rt * 16 + li;
-      unsigned char *dst = cl + (r >> 3) * MF_RGP + (r & 7) * 2 + lg * 8 * 16;
+      unsigned char *dst = cl + (r >> 3) * MF_RGP + (r & 7) * 2 + MF_CADDR(lg * 8);
 #pragma unroll
       for (int st = 0; st < MF_KH; st++) {
         const int ks = kh * MF_KH + st;
         if (ks >= 16) break;                         // wave-uniform: the pe k-steps
         const uint32_t w[4] = {cf[st].x, cf[st].y, cf[st].z, cf[st].w};
 #pragma unroll
-        for (int e = 0; e < 8; e++)
-          *(uint16_t *)(dst + (ks * 32 + e) * 16) = (uint16_t)(w[e >> 1] >> ((e & 1) * 16));
+        for (int e = 0; e < 8; e++)                  // column ks*32 + lg*8 + e
+          *(uint16_t *)(dst + MF_CADDR(ks * 32) + e * 16) = (uint16_t)(w[e >> 1] >> ((e & 1) * 16));
       }
     }
     float4 part_s;
@@ -495,10 +501,10 @@ __global__ __launch_bounds__(MF_THREADS) void k_mla_split_mf(ThvmMlaArgs a) {
       const float *pr = pw + li * MF_PWP + q * 32 + lg * 8;
       uint4 ah, alo;
       split8(*(const float4 *)pr, *(const float4 *)(pr + 4), ah, alo);
-      const unsigned char *rb = cl + (q * 4 + lg) * MF_RGP + li * 16;
+      const unsigned char *rb = cl + (q * 4 + lg) * MF_RGP + MF_CADDR(li);
 #pragma unroll
-      for (int t = 0; t < 4; t++) {
-        const uint4 bv = *(const uint4 *)(rb + (wv * 4 + t) * 16 * 16);
+      for (int t = 0; t < 4; t++) {                // column (wv*4 + t)*16 + li
+        const uint4 bv = *(const uint4 *)(rb + MF_CADDR((wv * 4 + t) * 16));
         oacc[t] = mfma16<GX_BF16>(ah, bv, oacc[t]);
         oacc[t] = mfma16<GX_BF16>(alo, bv, oacc[t]);
       }
