@@ -541,7 +541,8 @@ __global__ __launch_bounds__(MF_THREADS) void k_mla_split_mf(ThvmMlaArgs a) {
 #define MLA_OUT_THREADS 512
 #define MLA_OUT_SPLIT 2
 #define MLA_WPASS 8
-template <bool FP8>
+#define MLA_OPRE_MAX 20   /* partial vectors per thread loaded up front, long caches */
+template <bool FP8, int OPRE>
 __global__ __launch_bounds__(MLA_OUT_THREADS) void k_mla_out(ThvmMlaArgs a) {
   extern __shared__ float ol[];                       // [kv] olat | [ns] weights | [nsg][kv]
   constexpr uint32_t EPC = FP8 ? 16 : 8;
@@ -569,6 +570,22 @@ __global__ __launch_bounds__(MLA_OUT_THREADS) void k_mla_out(ThvmMlaArgs a) {
   // split weights w_s = exp(m_s - M) / sum_s exp(m_s - M) l_s (one split per thread)
   float ms = -INFINITY, ls = 0.0f;
   if (tid < ns) { ms = p0[tid * pst + kv]; ls = p0[tid * pst + kv + 1]; }
+  // the thread's first OPRE partial vectors go out with m and l (they do not
+  // depend on the weights): thread -> (float4 column c4, split group g),
+  // splits g, g + nsg, ...; the weights' reductions then run while they are
+  // in flight, and the merge waits for one round trip instead of one per
+  // four splits (same splits in the same order: the same sums).  OPRE = 20
+  // (160 VGPRs, one block per CU) where a row has more than 4 nsg partials
+  // (C5 batch 1: 65), else 4 (80 VGPRs; at C5 batch 32, 8 partials per row
+  // and 1024 blocks, 20 measured 66 -> 77 us per layer)
+  const uint32_t nc4 = kv / 4, nsg = MLA_OUT_THREADS / nc4;
+  const uint32_t c4 = tid % nc4, g = tid / nc4;
+  float4 vp[OPRE];
+#pragma unroll
+  for (int u = 0; u < OPRE; u++) {
+    const uint32_t sp = g + u * nsg;
+    vp[u] = sp < ns ? *(const float4 *)(p0 + sp * pst + 4 * c4) : make_float4(0.f, 0.f, 0.f, 0.f);
+  }
   float M = wave_max(ms);
   if (lane == 0) red[wv] = M;
   __syncthreads();
@@ -582,11 +599,15 @@ __global__ __launch_bounds__(MLA_OUT_THREADS) void k_mla_out(ThvmMlaArgs a) {
   for (uint32_t w = 0; w < MLA_OUT_THREADS / 64; w++) den += red[8 + w];
   if (tid < ns) wsp[tid] = ws / den;
   __syncthreads();
-  // partial merge: thread -> (float4 column c4, split group g); groups stride the splits
-  const uint32_t nc4 = kv / 4, nsg = MLA_OUT_THREADS / nc4;
-  const uint32_t c4 = tid % nc4, g = tid / nc4;
+  // partial merge: groups stride the splits
   float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
-  for (uint32_t s0 = g; s0 < ns; s0 += 4 * nsg) {     // four 16-byte loads in flight
+#pragma unroll
+  for (int u = 0; u < OPRE; u++) {
+    const uint32_t sp = g + u * nsg;
+    const float w = sp < ns ? wsp[sp] : 0.0f;
+    acc.x += w * vp[u].x; acc.y += w * vp[u].y; acc.z += w * vp[u].z; acc.w += w * vp[u].w;
+  }
+  for (uint32_t s0 = g + OPRE * nsg; s0 < ns; s0 += 4 * nsg) {     // four 16-byte loads in flight
     float4 v[4];
 #pragma unroll
     for (int u = 0; u < 4; u++) {
@@ -742,8 +763,12 @@ extern "C" int thvm_k_mla_attn(const ThvmMlaArgs *a, hipStream_t s, char *err, i
   }
   const dim3 g2(a->B * a->H, MLA_OUT_SPLIT);
   const uint32_t lds2 = (a->kv + MLA_MAX_SPLITS + MLA_OUT_THREADS * 4) * 4;
-  if (a->wdt == THVM_DT_FP8E4M3) thvm_launch(false, true, k_mla_out<true>, g2, dim3(MLA_OUT_THREADS), lds2, s, ak);
-  else thvm_launch(false, true, k_mla_out<false>, g2, dim3(MLA_OUT_THREADS), lds2, s, ak);
+  // partials per row at most: n_split / cpb; over 4 per split group -> 20 up front
+  const uint32_t nsg = MLA_OUT_THREADS / (a->kv / 4);
+  const bool longp = (a->n_split + ak.cpb - 1) / ak.cpb > 4 * nsg;
+  void (*fo)(ThvmMlaArgs) = a->wdt == THVM_DT_FP8E4M3 ? (longp ? k_mla_out<true, MLA_OPRE_MAX> : k_mla_out<true, 4>)
+                                                      : (longp ? k_mla_out<false, MLA_OPRE_MAX> : k_mla_out<false, 4>);
+  thvm_launch(false, true, fo, g2, dim3(MLA_OUT_THREADS), lds2, s, ak);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) { snprintf(err, errlen, "mla_attn launch: %s", hipGetErrorString(e)); return -1; }
   return 0;
