@@ -212,3 +212,13 @@ def test_beam_width_env(monkeypatch):
     assert T._beam_width() == 2
     monkeypatch.setattr(T, "_IN_JIT", 0)
     assert T._beam_width() == 0
+
+
+def test_autotune_refuses_output_buffer_bound_as_input():
+    """An input slot carrying the output's buffer id is an in-place update:
+    each timed repetition would read what the previous one wrote, so the
+    search refuses it (before touching the device)."""
+    import thvm_amd as H
+    nodes = [(36, 13, (), (0,)), (36, 13, (), (1,)), (37, 13, (1,), ())]
+    with pytest.raises(H.ThvmHipError, match="reads its output buffer"):
+        H.render_autotune(nodes, [7, 7])

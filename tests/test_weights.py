@@ -13,6 +13,7 @@
   block definitions say; an unsupported type raises NotImplementedError.
 * The Hugging Face rotate-half q/k row order converted to interleaved pairs
   gives the same attention scores (the RoPE definitions are equal)."""
+import io
 import os
 import pickle
 import struct
@@ -93,6 +94,55 @@ def test_torch_load_refuses_foreign_globals(tmp_path):
         pickle.dump({"x": Boom()}, f)
     with pytest.raises(pickle.UnpicklingError):
         W.torch_load(fn)
+
+
+def _crafted_ckpt(fn, numel, payload_elems, offset, size, stride):
+    """A zip checkpoint whose pickle claims a view (offset, size, stride) of
+    a float32 storage of `numel` elements holding `payload_elems` floats."""
+    import collections
+    import zipfile
+    torch = _torch()
+
+    class StorageRef:
+        pass
+
+    class View:
+        def __reduce__(self):
+            return (torch._utils._rebuild_tensor_v2,
+                    (StorageRef(), offset, size, stride, False, collections.OrderedDict()))
+
+    class P(pickle.Pickler):
+        def persistent_id(self, obj):
+            if isinstance(obj, StorageRef):
+                return ("storage", torch.FloatStorage, "0", "cpu", numel)
+            return None
+
+    buf = io.BytesIO()
+    P(buf, protocol=2).dump({"w": View()})
+    with zipfile.ZipFile(fn, "w") as zf:
+        zf.writestr("ckpt/data.pkl", buf.getvalue())
+        zf.writestr("ckpt/data/0", np.arange(payload_elems, dtype=np.float32).tobytes())
+
+
+@pytest.mark.parametrize("case", [
+    dict(numel=4, payload_elems=4, offset=0, size=(1 << 20,), stride=(1,)),   # view past the end
+    dict(numel=4, payload_elems=4, offset=3, size=(2,), stride=(1,)),         # off by one
+    dict(numel=4, payload_elems=4, offset=-1, size=(2,), stride=(1,)),        # negative offset
+    dict(numel=4, payload_elems=4, offset=0, size=(2,), stride=(-1,)),        # negative stride
+    dict(numel=8, payload_elems=4, offset=0, size=(8,), stride=(1,)),         # short payload
+])
+def test_torch_load_refuses_views_outside_their_storage(tmp_path, case):
+    fn = tmp_path / "crafted.pt"
+    _crafted_ckpt(fn, **case)
+    with pytest.raises(ValueError):
+        W.torch_load(fn)
+
+
+def test_torch_load_crafted_view_inside_storage_loads(tmp_path):
+    fn = tmp_path / "ok.pt"
+    _crafted_ckpt(fn, numel=6, payload_elems=6, offset=1, size=(2, 2), stride=(3, 1))
+    got = W.torch_load(fn)["w"]
+    assert np.array_equal(got, np.array([[1, 2], [4, 5]], np.float32))
 
 
 def test_dsv2pk_reads_the_pack_writer(tmp_path):

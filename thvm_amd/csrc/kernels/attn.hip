@@ -35,11 +35,13 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attn(ThvmAttnArgs a) {
   u.finish(a, kvh, split, b, wv, threadIdx.x, L, true, s);
 }
 
-// live partials of a row of length L: one per cpb chunks
+// live partials of a row of length L: one per cpb chunks, at most the
+// number of split blocks in the grid (ceil(n_split / cpb))
 __device__ __forceinline__ uint32_t attn_live(const ThvmAttnArgs &a, int32_t L) {
-  const int32_t span = ATT_CHUNK * (a.cpb > 1 ? (int32_t)a.cpb : 1);
-  const uint32_t n = L > 0 ? (uint32_t)((L + span - 1) / span) : 0u;
-  return n < a.n_split ? n : a.n_split;
+  const uint32_t cpb = a.cpb > 1 ? a.cpb : 1u;
+  const int32_t span = ATT_CHUNK * (int32_t)cpb;
+  const uint32_t n = L > 0 ? (uint32_t)((L + span - 1) / span) : 0u, nb = (a.n_split + cpb - 1) / cpb;
+  return n < nb ? n : nb;
 }
 
 // one block per (row, kv head): the group's G heads

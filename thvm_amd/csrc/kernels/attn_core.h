@@ -90,9 +90,12 @@ __device__ __forceinline__ float fexp2(float x) { return exp2f(x); }
 // Query row b's cache length and cache row.  Plain decode: L = len[0] over
 // cache row b.  Speculative verify (a.spec): the B query rows are the
 // consecutive positions L-1 .. L-1+B-1 of one sequence, so row b attends
-// causally over the L+b rows of cache row 0.
+// causally over the L+b rows of cache row 0.  A length past the cache (a
+// replay pushed beyond max_seq) is clamped to max_seq, so the live-split
+// count never exceeds the split blocks the grid holds.
 __device__ __forceinline__ int32_t attn_row_len(const ThvmAttnArgs &a, uint32_t b) {
-  return a.len[0] + (a.spec ? (int32_t)b : 0);
+  const int32_t L = a.len[0] + (a.spec ? (int32_t)b : 0);
+  return L < (int32_t)a.max_seq ? L : (int32_t)a.max_seq;
 }
 __device__ __forceinline__ uint32_t attn_cache_row(const ThvmAttnArgs &a, uint32_t b) {
   return a.spec ? 0u : b;

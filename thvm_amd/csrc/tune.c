@@ -211,8 +211,15 @@ static void keep_top(Cand *top, int *nt, int w, ThvmRenderOpts o, double us) {
 THVM_API int thvm_hip_render_autotune(const ThvmUop *nodes, uint32_t n, const uint32_t *buf_ids,
                                       uint32_t n_args, uint32_t reps, ThvmRenderOpts *best,
                                       double *best_us, double *base_us) {
-  if (hb_require_ready("render_autotune")) return -1;
   if (!nodes || n == 0 || !buf_ids || n_args == 0 || !best) { hb_set_error("render_autotune: bad arguments"); return -1; }
+  /* an input slot bound to the output buffer is an in-place update too: every
+   * repetition would read what the previous one wrote */
+  for (uint32_t i = 1; i < n_args; i++)
+    if (buf_ids[i] == buf_ids[0]) {
+      hb_set_error("render_autotune: the kernel reads its output buffer (slot %u is the output's buffer)", i);
+      return -1;
+    }
+  if (hb_require_ready("render_autotune")) return -1;
   if (hb_stream_capturing() || thvm_hip_jit_is_capturing()) { hb_set_error("render_autotune: not during a capture"); return -1; }
   if (reps == 0) reps = 20;
   const u64 key = rows_key(nodes, n);

@@ -197,12 +197,25 @@ def torch_load(path) -> Dict[str, np.ndarray]:
         sizes[key] = numel * isz
         if key not in data:
             return None
+        size, stride = tuple(int(s) for s in size), tuple(int(s) for s in stride)
+        storage_offset, numel = int(storage_offset), int(numel)
+        if len(size) != len(stride) or any(s < 0 for s in size) or numel < 0:
+            raise ValueError(f"torch_load: tensor view of storage {key!r} has a bad shape "
+                             f"{size} / stride {stride}")
         n = int(np.prod(size)) if len(size) else 1
+        if len(data[key]) < numel * isz:
+            raise ValueError(f"torch_load: storage {key!r} holds {len(data[key])} bytes, "
+                             f"the pickle says {numel} x {isz}")
+        if n > 0:
+            last = storage_offset + sum((s - 1) * st for s, st in zip(size, stride))
+            if storage_offset < 0 or any(st < 0 for st in stride) or last >= numel:
+                raise ValueError(f"torch_load: tensor view (offset {storage_offset}, size {size}, "
+                                 f"stride {stride}) lies outside its storage of {numel} elements")
         flat = np.frombuffer(data[key], dtype=npdt, count=numel)
         if bf:
             flat = bf16_to_f32(flat)
         if n == 0:
-            return np.zeros(tuple(size), flat.dtype)
+            return np.zeros(size, flat.dtype)
         st_b = flat.itemsize
         view = np.lib.stride_tricks.as_strided(flat[storage_offset:], shape=tuple(size),
                                                strides=tuple(s * st_b for s in stride))
