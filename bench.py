@@ -86,6 +86,9 @@ def attn_bytes_per_step(cfg, L) -> int:
     return cfg["n_layers"] * B * (2 * Hkv * L * hd * es + 2 * H * hd * es)
 
 
+CPU_BUILD = None
+
+
 def cpu_baseline(dec, cfg, n_steps: int):
     """Oracle decode on 1 core from the device's current state; returns
     (tokens/s, ids_match, seconds, max logit error relative to max|logit|)."""
@@ -94,6 +97,12 @@ def cpu_baseline(dec, cfg, n_steps: int):
     import _oracle as O
     pos = dec.position
     tok = dec.tokens(pos + 1)[:, pos].astype(np.int32)
+    global CPU_BUILD
+    try:                                       # the reference CPU JIT's flags, for this host
+        CPU_BUILD = O.use_native_build(ROOT / "gpurun_out" / "oracle_native")
+    except Exception as e:                     # no compiler: the shipped build, said so
+        CPU_BUILD = f"shipped build (cc -std=c11 -O3 -fno-math-errno -ffp-contract=off; native build failed: {e})"
+    log(f"[bench] cpu baseline oracle: {CPU_BUILD}")
     t_read = time.time()
     om = O.OracleDsv2(dec, dict(cfg)) if cfg["arch"] == 3 else O.OracleModel(dec, dict(cfg))
     log(f"[bench] cpu baseline: read back {sum(a.nbytes for a in om.keep) / 1e9:.2f} GB of "
@@ -102,7 +111,7 @@ def cpu_baseline(dec, cfg, n_steps: int):
     cur = tok
     for s in range(n_steps):
         t0 = time.perf_counter()
-        olg, onx = om.step(cur, pos + s)
+        olg, onx = om.step(cur, pos + s, threads=1)      # one core, rows one after another
         t_cpu += time.perf_counter() - t0
         dec.replay(1)                              # the same step on the device
         glg = dec.logits()
@@ -266,7 +275,8 @@ def run_decode(thvm, key: str, batch: int, args) -> dict:
                          f"context ~{dec.position - cpu_steps}, oracle/oracle.c or_decode_step on "
                          f"one core of {cpu_model_name()} ({os.cpu_count()} visible), in lockstep "
                          f"with the device on the same inputs",
-               "seconds": round(secs, 2), "ids_match": match, "logits_max_rel_err": lerr}
+               "seconds": round(secs, 2), "ids_match": match, "logits_max_rel_err": lerr,
+               "build": CPU_BUILD}
     mfma = batch > 4
     if dom == "llama_step":
         gkern = ("k_llama_step (the whole decode step in one persistent launch: %s weight GEMVs, "
@@ -524,6 +534,10 @@ def run_host_gpt2(thvm, key: str, args) -> dict:
             def read_tensor(s, name):
                 return s.t[name]
         ocfg = dict(c, n_layers=L, batch=1, max_seq=max_ctx, wdtype=DT_F32, adtype=DT_F32)
+        try:
+            build = O.use_native_build(ROOT / "gpurun_out" / "oracle_native")
+        except Exception as e:
+            build = f"shipped build (native build failed: {e})"
         om = O.OracleModel(_W(), ocfg)
         n_cpu = args.cpu_steps or 2
         tc = time.perf_counter()
@@ -531,7 +545,8 @@ def run_host_gpt2(thvm, key: str, args) -> dict:
             om.step(np.array([prompt[s]], np.int32), s)
         tcpu = time.perf_counter() - tc
         cpu = {"value": round(n_cpu / tcpu, 4), "unit": "tokens/s", "cores": 1, "kind": "port",
-               "sample": f"{n_cpu} decode steps of the same model (fp32) from position 0 on the C oracle"}
+               "sample": f"{n_cpu} decode steps of the same model (fp32) from position 0 on the C oracle",
+               "build": build}
     return {"metric": METRIC, "value": round(args.steps / dt, 2), "unit": "tokens/s", "n_gpus": 1,
             "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(dt / args.steps * 1e3, 4),
             "higher_is_better": True, "scaling": "weak", "vs_baseline": None,

@@ -114,6 +114,47 @@ uint64_t thvm_hip_buf_device_ptr(uint32_t buf_id);
 uint64_t thvm_hip_mem_live_bytes(void);
 uint64_t thvm_hip_mem_peak_bytes(void);
 
+/* ===================== pool watermarks and preserve marks =============== *
+ * The per-realize memory scope of the reference's realize loop
+ * (src/schedule/realize.c:132-152, :296-310, :326-340, :420-450), served by
+ * its backend's buf_pool.c:9-183.  A watermark names every buffer allocated
+ * after it (an allocation sequence number, not a slot index: dead slots are
+ * reused here, with a per-slot generation in the id so a stale id stays
+ * dead).  The caller marks the buffers that must survive, then rolls back. */
+/* cuda_buf_pool_begin (buf_pool.c:9-11). */
+uint32_t thvm_hip_buf_pool_begin(void);
+/* cuda_buf_pool_rollback_with_preserve (:22-47): every buffer since wm that
+ * is not preserved, not JIT-pinned and not already parked: owning blocks are
+ * parked on the freelist (freed when it is full), arena blocks freed, views
+ * freed.  Refcounts are not consulted (the planner knows these are dead). */
+void     thvm_hip_buf_pool_rollback_with_preserve(uint32_t wm);
+/* cuda_buf_pool_free_unpreserved (:54-64): the same set, freed outright. */
+void     thvm_hip_buf_pool_free_unpreserved(uint32_t wm);
+/* cuda_buf_mark_preserved (:66-69); called through tensor_mark_buf_preserved
+ * (src/tensor/mark_buf_preserved.c:22), which also marks an arena view's
+ * parent. */
+void     thvm_hip_buf_mark_preserved(uint32_t buf_id);
+/* cuda_buf_clear_preserved (:105-108): marks of buffers since wm (1: all). */
+void     thvm_hip_buf_clear_preserved(uint32_t wm);
+/* cuda_buf_clear_preserved_arena_views (:172-183): views since wm lose their
+ * mark, and so does each one's parent when it too was allocated since wm. */
+void     thvm_hip_buf_clear_preserved_arena_views(uint32_t wm);
+/* cuda_buf_free_unpreserved_all (:122-160): table-wide, every live owning
+ * buffer neither preserved nor JIT-pinned is parked (arena blocks freed);
+ * views are left to their parent.  Drains the stream first.  Returns bytes. */
+uint64_t thvm_hip_buf_free_unpreserved_all(void);
+/* A per-realize arena block (the reference's skip_freelist CudaBuf,
+ * src/thvm.h:1147-1158; thvm_metal_buf_arena_alloc): never recycled from or
+ * parked on the freelist; a rollback or the sweep frees it outright. */
+uint32_t thvm_hip_buf_arena_alloc(uint64_t nbytes);
+/* Diagnostics: live buffer slots (parked blocks included), and the highest
+ * slot index ever used.  A dead slot is reused with the next generation; a
+ * slot retires after 2^14 generations (so an id is never issued twice), so
+ * the high-water mark grows by one per 2^14 buffer deaths beyond the peak
+ * live count, not by one per allocation. */
+uint32_t thvm_hip_buf_slots_used(void);
+uint32_t thvm_hip_buf_slot_highwater(void);
+
 /* ===================== dispatch (Backend.dispatch_*) ==================== */
 
 void thvm_hip_dispatch_begin(void);
@@ -420,6 +461,19 @@ uint32_t thvm_hip_decoder_step_kernels(uint32_t dec);
  * open, work done and stores drained (4 values each).  Writes up to n values
  * and returns how many the step has (0 for a per-op decoder, -1 on error). */
 int      thvm_hip_decoder_stage_clock(uint32_t dec, double *us_out, uint32_t n);
+/* Per-sublayer probes of one step (counterpart of the reference bench's
+ * DSV2_DUMP per-layer fingerprints, bench/dsv2_decode_bench.c:2516-2556,
+ * which localise the first layer where a numerics change enters).
+ * op_tags writes, for up to n of the step's dispatches, the sublayer each
+ * belongs to: 2l for layer l's attention sublayer, 2l+1 for its FFN
+ * sublayer, -1 before the first layer (embedding), -2 after the last (final
+ * norm, LM head, argmax, length bump); returns the step's dispatch count.
+ * run_ops dispatches ops [first, first + count) of the step eagerly -- the
+ * same kernels the captured step replays -- so a host can run a step one
+ * sublayer at a time and read the activations ("x", "q", "att", "h", ...)
+ * in between.  Not during a JIT capture.  0 / -1. */
+int      thvm_hip_decoder_op_tags(uint32_t dec, int32_t *tags, uint32_t n);
+int      thvm_hip_decoder_run_ops(uint32_t dec, uint32_t first, uint32_t count);
 
 #ifdef __cplusplus
 }

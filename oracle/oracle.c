@@ -498,7 +498,10 @@ int or_decode_step(const OrModel *m, const int32_t *tok, uint32_t pos, float *lo
   float *att = (float *)malloc((size_t)H * hd * 4), *o = (float *)malloc((size_t)D * 4);
   float *gu = (float *)malloc((size_t)2 * F * 4), *hh = (float *)malloc((size_t)F * 4);
   const float scale = (float)(1.0 / sqrt((double)hd));
-  for (uint32_t b = 0; b < m->batch; b++) {
+  const uint32_t B = m->batch, bend = m->b1 ? m->b1 : B;
+  /* teacher input / tap row of sublayer t, batch row b */
+#define TROW(a, t, b, w) ((a) + ((uint64_t)(t) * B + (b)) * (w))
+  for (uint32_t b = m->b0; b < bend; b++) {
     /* embedding (+ learned position) */
     int32_t t = tok[b];
     for (uint32_t i = 0; i < D; i++) {
@@ -508,6 +511,7 @@ int or_decode_step(const OrModel *m, const int32_t *tok, uint32_t pos, float *lo
     }
     for (uint32_t l = 0; l < m->n_layers; l++) {
       const OrLayer *L = &m->layers[l];
+      if (m->tf_x) memcpy(x, TROW(m->tf_x, 2 * l, b, D), (size_t)D * 4);
       if (gpt2) or_layernorm(xn, DT_FP32, x, DT_FP32, L->g1, L->b1, 1, D, m->eps);
       else or_rmsnorm(xn, DT_FP32, x, DT_FP32, L->g1, 1, D, m->eps);
       for (uint32_t i = 0; i < D; i++) xn[i] = rnd(xn[i], adt);
@@ -527,6 +531,7 @@ int or_decode_step(const OrModel *m, const int32_t *tok, uint32_t pos, float *lo
         }
       }
       memcpy(q, qkv, (size_t)Hq * 4);
+      if (m->tp_q) memcpy(TROW(m->tp_q, l, b, Hq), q, (size_t)Hq * 4);
       for (uint32_t kh = 0; kh < Hkv; kh++)
         for (uint32_t d = 0; d < hd; d++) {
           uint64_t ci = (((uint64_t)b * Hkv + kh) * m->max_seq + pos) * hd + d;
@@ -557,11 +562,14 @@ int or_decode_step(const OrModel *m, const int32_t *tok, uint32_t pos, float *lo
         }
         free(sc);
       }
+      if (m->tp_att) memcpy(TROW(m->tp_att, l, b, Hq), att, (size_t)Hq * 4);
       or_gemv(o, att, DT_FP32, Hq, L->wo, wdt, L->so, 1, D, Hq);
       for (uint32_t i = 0; i < D; i++) {
         float v = o[i] + (gpt2 ? ld(L->bo, i, adt) : 0.0f);
         x[i] = rnd(x[i] + rnd(v, adt), adt);
       }
+      if (m->tp_x) memcpy(TROW(m->tp_x, 2 * l, b, D), x, (size_t)D * 4);
+      if (m->tf_x) memcpy(x, TROW(m->tf_x, 2 * l + 1, b, D), (size_t)D * 4);
       if (gpt2) or_layernorm(xn, DT_FP32, x, DT_FP32, L->g2, L->b2, 1, D, m->eps);
       else or_rmsnorm(xn, DT_FP32, x, DT_FP32, L->g2, 1, D, m->eps);
       for (uint32_t i = 0; i < D; i++) xn[i] = rnd(xn[i], adt);
@@ -575,12 +583,15 @@ int or_decode_step(const OrModel *m, const int32_t *tok, uint32_t pos, float *lo
           hh[i] = rnd(silu(g) * u, adt);
         }
       }
+      if (m->tp_h) memcpy(TROW(m->tp_h, l, b, F), hh, (size_t)F * 4);
       or_gemv(o, hh, DT_FP32, F, L->wd, wdt, L->sd, 1, D, F);
       for (uint32_t i = 0; i < D; i++) {
         float v = o[i] + (gpt2 ? ld(L->bpr, i, adt) : 0.0f);
         x[i] = rnd(x[i] + rnd(v, adt), adt);
       }
+      if (m->tp_x) memcpy(TROW(m->tp_x, 2 * l + 1, b, D), x, (size_t)D * 4);
     }
+    if (m->tf_x) memcpy(x, TROW(m->tf_x, 2 * m->n_layers, b, D), (size_t)D * 4);
     if (gpt2) or_layernorm(xn, DT_FP32, x, DT_FP32, m->gf, m->bf, 1, D, m->eps);
     else or_rmsnorm(xn, DT_FP32, x, DT_FP32, m->gf, 1, D, m->eps);
     for (uint32_t i = 0; i < D; i++) xn[i] = rnd(xn[i], adt);
@@ -592,6 +603,7 @@ int or_decode_step(const OrModel *m, const int32_t *tok, uint32_t pos, float *lo
   free(x); free(xn); free(qkv); free(q); free(att); free(o); free(gu); free(hh);
   return 0;
 }
+#undef TROW
 
 /* ==== DeepSeek-V2 decode (bench/dsv2_decode_bench.c) ====================== */
 
@@ -789,7 +801,9 @@ int or_dsv2_step(const OrDsv2 *m, const int32_t *tok, uint32_t pos, float *logit
   float *lg = (float *)malloc((size_t)E * 4);
   int32_t sel[64];
   float probs[64];
-  for (uint32_t b = 0; b < m->batch; b++) {
+  const uint32_t B = m->batch, bend = m->b1 ? m->b1 : B;
+#define TROW(a, t, b, w) ((a) + ((uint64_t)(t) * B + (b)) * (w))
+  for (uint32_t b = m->b0; b < bend; b++) {
     int32_t t = tok[b];                              /* embed_row :377-395 */
     for (uint32_t i = 0; i < D; i++)
       x[i] = (t >= 0 && (uint32_t)t < V) ? or_bf16_to_f32(m->emb[(uint64_t)t * D + i]) : 0.0f;
@@ -797,6 +811,7 @@ int or_dsv2_step(const OrDsv2 *m, const int32_t *tok, uint32_t pos, float *logit
       const OrDsv2Layer *Ly = &m->layers[l];
       uint16_t *ckv = Ly->ckv + (uint64_t)b * m->max_seq * kv;
       uint16_t *kpe = Ly->kpe + (uint64_t)b * m->max_seq * dr;
+      if (m->tf_x) memcpy(x, TROW(m->tf_x, 2 * l, b, D), (size_t)D * 4);
       or_rmsnorm(xn, DT_FP32, x, DT_FP32, Ly->win, 1, D, m->eps);
       for (uint32_t i = 0; i < D; i++) xn[i] = rnd(xn[i], DT_BF16);   /* rms1 out bf16 */
       gemv_sk(qkv, xn, Ly->wqkv, wdt, Ly->sqkv, nqkv, D, gemv_pick_sk(D, H * (dn + dr)));
@@ -806,8 +821,11 @@ int or_dsv2_step(const OrDsv2 *m, const int32_t *tok, uint32_t pos, float *logit
                   m->rope_sin + (uint64_t)pos * (dr / 2), H, dn, dr, kv, m->eps);
       or_mla_attn(o, qlat, qpe, ckv, kpe, pos + 1, Ly->wuv, wdt, Ly->suv, H, kv, dr, dv, m->scale);
       for (uint32_t i = 0; i < H * dv; i++) of[i] = or_bf16_to_f32(o[i]);
+      if (m->tp_o) memcpy(TROW(m->tp_o, l, b, H * dv), of, (size_t)H * dv * 4);
       gemv_sk(tmp, of, Ly->wo, wdt, Ly->so, D, H * dv, gemv_pick_sk(H * dv, D));
       for (uint32_t i = 0; i < D; i++) x[i] = rnd(x[i] + rnd(tmp[i], DT_BF16), DT_BF16);  /* x1 */
+      if (m->tp_x) memcpy(TROW(m->tp_x, 2 * l, b, D), x, (size_t)D * 4);
+      if (m->tf_x) memcpy(x, TROW(m->tf_x, 2 * l + 1, b, D), (size_t)D * 4);
       or_rmsnorm(xn, DT_FP32, x, DT_FP32, Ly->wpost, 1, D, m->eps);                       /* xn2f */
       for (uint32_t i = 0; i < D; i++) xb[i] = or_f32_to_bf16(xn[i]);                     /* xn2b */
       if (l < m->first_dense) {
@@ -827,11 +845,15 @@ int or_dsv2_step(const OrDsv2 *m, const int32_t *tok, uint32_t pos, float *logit
           memcpy(m->sel_out + lb * K, sel, K * sizeof(int32_t));
           memcpy(m->probs_out + lb * K, probs, K * sizeof(float));
         }
-        or_moe(tmp, xb, sel, probs, Ly->wgu_e, Ly->sgu_e, Ly->wd_e, Ly->sd_e, Ly->wgu_s, Ly->sgu_s,
-               Ly->wd_s, Ly->sd_s, wdt, D, I, S, K);
+        const int32_t *use_sel = m->tf_sel ? m->tf_sel + lb * K : sel;
+        const float *use_probs = m->tf_probs ? m->tf_probs + lb * K : probs;
+        or_moe(tmp, xb, use_sel, use_probs, Ly->wgu_e, Ly->sgu_e, Ly->wd_e, Ly->sd_e, Ly->wgu_s,
+               Ly->sgu_s, Ly->wd_s, Ly->sd_s, wdt, D, I, S, K);
       }
       for (uint32_t i = 0; i < D; i++) x[i] = rnd(x[i] + rnd(tmp[i], DT_BF16), DT_BF16);
+      if (m->tp_x) memcpy(TROW(m->tp_x, 2 * l + 1, b, D), x, (size_t)D * 4);
     }
+    if (m->tf_x) memcpy(x, TROW(m->tf_x, 2 * m->n_layers, b, D), (size_t)D * 4);
     or_rmsnorm(xn, DT_FP32, x, DT_FP32, m->gf, 1, D, m->eps);                             /* rms_f f32 */
     float *lgb = logits + (uint64_t)b * V;
     gemv_sk(lgb, xn, m->lm, wdt, m->lm_s, V, D, gemv_pick_sk(D, V));
@@ -841,3 +863,4 @@ int or_dsv2_step(const OrDsv2 *m, const int32_t *tok, uint32_t pos, float *logit
   free(of); free(tmp); free(gu); free(hh); free(lg);
   return 0;
 }
+#undef TROW

@@ -102,6 +102,18 @@ typedef struct OrModel {
   const void *lm; const float *lm_s;     /* LLAMA LM head [V, D]; GPT2 uses emb    */
   const float *rope_cos, *rope_sin;      /* [max_seq, hd/2]                        */
   OrLayer *layers;
+  /* Per-sublayer teacher forcing (all optional, NULL = off).  Sublayer t =
+   * 2l is layer l's attention, 2l+1 its FFN.  tf_x [2L+1][B][D]: the residual
+   * entering each sublayer (t = 2L: entering the final norm), taken from
+   * another implementation; when set, the step restarts every sublayer from
+   * it, so each sublayer's outputs depend only on that sublayer's inputs.
+   * Taps (written): tp_x [2L][B][D] the residual leaving each sublayer;
+   * tp_q [L][B][H hd] q after bias/RoPE and rounding; tp_att [L][B][H hd]
+   * the attention output; tp_h [L][B][F] the FFN hidden (activation dtype
+   * values as f32). */
+  const float *tf_x;
+  float *tp_x, *tp_q, *tp_att, *tp_h;
+  uint32_t b0, b1;                       /* rows [b0, b1) only; b1 = 0: every row  */
 } OrModel;
 
 /* One decode step for every batch row: token tok[b] at position pos (the
@@ -185,6 +197,16 @@ typedef struct OrDsv2 {
   OrDsv2Layer *layers;
   int32_t *sel_out; float *probs_out;    /* optional [n_layers][B][K]: each MoE layer's routing */
   float *gate_out;                       /* optional [n_layers][B][E]: its router logits         */
+  /* Per-sublayer teacher forcing and taps, as in OrModel: tf_x [2L+1][B][D]
+   * (bf16 values as f32), tp_x [2L][B][D], tp_o [L][B][H dv] the attention
+   * output entering the o projection.  tf_sel / tf_probs [L][B][K]: when
+   * set, each MoE layer combines these experts with these weights (another
+   * implementation's routing) instead of its own top-K; sel_out, probs_out
+   * and gate_out still record the oracle's own routing. */
+  const float *tf_x;
+  float *tp_x, *tp_o;
+  const int32_t *tf_sel; const float *tf_probs;
+  uint32_t b0, b1;                       /* rows [b0, b1) only; b1 = 0: every row */
 } OrDsv2;
 
 /* One DSV2 decode step for every batch row (step_build :2328-2411): writes

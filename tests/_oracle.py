@@ -28,7 +28,8 @@ class OrModel(C.Structure):
                                     "head_dim", "ffn", "vocab", "max_seq", "batch", "wdt",
                                     "adt")] + [("eps", _f)] + [
         (n, _vp) for n in ("emb", "pos_emb", "gf", "bf", "lm", "lm_s", "rope_cos", "rope_sin")] + [
-        ("layers", C.POINTER(OrLayer))]
+        ("layers", C.POINTER(OrLayer))] + [
+        (n, _vp) for n in ("tf_x", "tp_x", "tp_q", "tp_att", "tp_h")] + [("b0", _u32), ("b1", _u32)]
 
 
 class OrDsv2Layer(C.Structure):
@@ -45,11 +46,16 @@ class OrDsv2(C.Structure):
         "batch", "wdt")] + [("eps", _f), ("scale", _f)] + [
         (n, _vp) for n in ("emb", "gf", "lm", "lm_s", "rope_cos", "rope_sin")] + [
         ("layers", C.POINTER(OrDsv2Layer)), ("sel_out", _vp), ("probs_out", _vp),
-        ("gate_out", _vp)]
+        ("gate_out", _vp)] + [
+        (n, _vp) for n in ("tf_x", "tp_x", "tp_o", "tf_sel", "tf_probs")] + [("b0", _u32), ("b1", _u32)]
 
 
 _OR = None
 _REF = None
+
+
+# the reference CPU JIT's compile flags (src/backend/cpu/jit.c:318-345)
+REF_JIT_FLAGS = ["-O3", "-fno-math-errno", "-ffp-contract=off", "-march=native", "-mno-avx512f"]
 
 
 def oracle() -> C.CDLL:
@@ -58,43 +64,64 @@ def oracle() -> C.CDLL:
         if not ORACLE_SO.exists():
             subprocess.run(["make", "-C", str(ROOT / "oracle"), "build/liboracle.so"], check=True,
                            capture_output=True)
-        L = C.CDLL(str(ORACLE_SO))
-        sig = {
-            "or_bf16_to_f32": (_f, [_u16]), "or_f32_to_bf16": (_u16, [_f]),
-            "or_fp16_to_f32": (_f, [_u16]), "or_f32_to_fp16": (_u16, [_f]),
-            "or_fp8e4m3_to_f32": (_f, [_u8]), "or_fp8e5m2_to_f32": (_f, [_u8]),
-            "or_f32_to_fp8e4m3": (_u8, [_f]), "or_f32_to_fp8e4m3_sat": (_u8, [_f]),
-            "or_f32_to_fp8e5m2": (_u8, [_f]), "or_f32_to_fp8e5m2_sat": (_u8, [_f]),
-            "or_decode": (None, [_vp, _u32, _vp, _u64]),
-            "or_encode": (None, [_vp, _u32, _vp, _u64]),
-            "or_gemv": (None, [_vp, _vp, _u32, _u32, _vp, _u32, _vp, _u32, _u32, _u32]),
-            "or_rmsnorm": (None, [_vp, _u32, _vp, _u32, _vp, _u32, _u32, _f]),
-            "or_layernorm": (None, [_vp, _u32, _vp, _u32, _vp, _vp, _u32, _u32, _f]),
-            "or_softmax": (None, [_vp, _u32, _vp, _u32, _u32, _u32]),
-            "or_rope": (None, [_vp, _u32, _vp, _vp, _u32, _u32, _u32, _u32]),
-            "or_attn_decode": (None, [_vp, _u32, _vp, _u32, _vp, _vp, _u32, _u32, _u32, _u32,
-                                      _u32, _u32, _u32, _f]),
-            "or_argmax": (None, [_vp, _vp, _u32, _u32]),
-            "or_sexpf": (_f, [_f]), "or_sample_u01": (_f, [_u64, _u32, C.c_int32]),
-            "or_sample": (None, [_vp, _vp, _u32, _u32, _u32, _f, _u64, C.c_int32]),
-            "or_spec_draft": (None, [_vp, _vp, _vp, C.c_int32, _u32, _u32, _u32, _i]),
-            "or_spec_accept": (C.c_int32, [_vp, C.c_int32, _vp, _vp, _u32, _u32]),
-            "or_decode_step": (_i, [C.POINTER(OrModel), _vp, _u32, _vp, _vp]),
-            "or_mla_prep": (None, [_vp, _vp, _vp, _vp, _vp, _vp, _u32, _vp, _vp, _vp, _vp,
-                                   _u32, _u32, _u32, _u32, _f]),
-            "or_mla_attn": (None, [_vp, _vp, _vp, _vp, _vp, _u32, _vp, _u32, _vp, _u32, _u32,
-                                   _u32, _u32, _f]),
-            "or_route": (None, [_vp, _vp, _vp, _u32, _u32]),
-            "or_moe": (None, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
-                              _u32, _u32, _u32, _u32, _u32]),
-            "or_dsv2_step": (_i, [C.POINTER(OrDsv2), _vp, _u32, _vp, _vp]),
-            "or_dsv2_dense_act": (None, [_vp, _vp, _vp, _u64]),
-        }
-        for k, (r, a) in sig.items():
-            fn = getattr(L, k)
-            fn.restype, fn.argtypes = r, a
-        _OR = L
+        _OR = _bind(C.CDLL(str(ORACLE_SO)))
     return _OR
+
+
+def use_native_build(outdir) -> str:
+    """Compile oracle/oracle.c on this machine with the reference CPU JIT's
+    flags (-march=native for this host) into `outdir` and use that build from
+    here on; returns the compile command.  The flags allow no reassociation
+    (-ffp-contract=off, no -ffast-math), so the results are the shipped
+    build's bit for bit; only the instructions chosen differ."""
+    global _OR
+    from pathlib import Path as _P
+    so = _P(outdir) / "liboracle_native.so"
+    so.parent.mkdir(parents=True, exist_ok=True)
+    cmd = ["cc", "-std=c11", *REF_JIT_FLAGS, "-fPIC", "-shared", "-o", str(so),
+           str(ROOT / "oracle" / "oracle.c"), "-lm"]
+    subprocess.run(cmd, check=True, capture_output=True)
+    _OR = _bind(C.CDLL(str(so)))
+    return " ".join(cmd[:-4] + ["oracle/oracle.c", "-lm"])
+
+
+def _bind(L: C.CDLL) -> C.CDLL:
+    """Set the oracle's function signatures on a loaded build."""
+    sig = {
+        "or_bf16_to_f32": (_f, [_u16]), "or_f32_to_bf16": (_u16, [_f]),
+        "or_fp16_to_f32": (_f, [_u16]), "or_f32_to_fp16": (_u16, [_f]),
+        "or_fp8e4m3_to_f32": (_f, [_u8]), "or_fp8e5m2_to_f32": (_f, [_u8]),
+        "or_f32_to_fp8e4m3": (_u8, [_f]), "or_f32_to_fp8e4m3_sat": (_u8, [_f]),
+        "or_f32_to_fp8e5m2": (_u8, [_f]), "or_f32_to_fp8e5m2_sat": (_u8, [_f]),
+        "or_decode": (None, [_vp, _u32, _vp, _u64]),
+        "or_encode": (None, [_vp, _u32, _vp, _u64]),
+        "or_gemv": (None, [_vp, _vp, _u32, _u32, _vp, _u32, _vp, _u32, _u32, _u32]),
+        "or_rmsnorm": (None, [_vp, _u32, _vp, _u32, _vp, _u32, _u32, _f]),
+        "or_layernorm": (None, [_vp, _u32, _vp, _u32, _vp, _vp, _u32, _u32, _f]),
+        "or_softmax": (None, [_vp, _u32, _vp, _u32, _u32, _u32]),
+        "or_rope": (None, [_vp, _u32, _vp, _vp, _u32, _u32, _u32, _u32]),
+        "or_attn_decode": (None, [_vp, _u32, _vp, _u32, _vp, _vp, _u32, _u32, _u32, _u32,
+                                  _u32, _u32, _u32, _f]),
+        "or_argmax": (None, [_vp, _vp, _u32, _u32]),
+        "or_sexpf": (_f, [_f]), "or_sample_u01": (_f, [_u64, _u32, C.c_int32]),
+        "or_sample": (None, [_vp, _vp, _u32, _u32, _u32, _f, _u64, C.c_int32]),
+        "or_spec_draft": (None, [_vp, _vp, _vp, C.c_int32, _u32, _u32, _u32, _i]),
+        "or_spec_accept": (C.c_int32, [_vp, C.c_int32, _vp, _vp, _u32, _u32]),
+        "or_decode_step": (_i, [C.POINTER(OrModel), _vp, _u32, _vp, _vp]),
+        "or_mla_prep": (None, [_vp, _vp, _vp, _vp, _vp, _vp, _u32, _vp, _vp, _vp, _vp,
+                               _u32, _u32, _u32, _u32, _f]),
+        "or_mla_attn": (None, [_vp, _vp, _vp, _vp, _vp, _u32, _vp, _u32, _vp, _u32, _u32,
+                               _u32, _u32, _f]),
+        "or_route": (None, [_vp, _vp, _vp, _u32, _u32]),
+        "or_moe": (None, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
+                          _u32, _u32, _u32, _u32, _u32]),
+        "or_dsv2_step": (_i, [C.POINTER(OrDsv2), _vp, _u32, _vp, _vp]),
+        "or_dsv2_dense_act": (None, [_vp, _vp, _vp, _u64]),
+    }
+    for k, (r, a) in sig.items():
+        fn = getattr(L, k)
+        fn.restype, fn.argtypes = r, a
+    return L
 
 
 def ref():
@@ -186,6 +213,30 @@ def spec_accept(hist, L, ca, am, S):
 DT_FP8_W = 9
 
 
+def _threads(B):
+    import os
+    return max(1, min(B, 16, os.cpu_count() or 1))
+
+
+def _run_rows(fn, m, B, *args, threads=None):
+    """Run `fn(m_rows, *args)` over row ranges on threads (the oracle keeps
+    every row's state apart: caches, logits and taps are indexed by row; ctypes
+    releases the GIL during the call).  `threads` 1 runs every row on the
+    calling thread."""
+    from concurrent.futures import ThreadPoolExecutor
+    nt = _threads(B) if threads is None else max(1, min(int(threads), B))
+    if nt == 1:
+        return [fn(C.byref(m), *args)]
+    cuts = np.linspace(0, B, nt + 1).astype(int)
+    ms = []
+    for i in range(nt):
+        mi = type(m).from_buffer_copy(m)
+        mi.b0, mi.b1 = int(cuts[i]), int(cuts[i + 1])
+        ms.append(mi)
+    with ThreadPoolExecutor(nt) as ex:
+        return list(ex.map(lambda mi: fn(C.byref(mi), *args), ms))
+
+
 class OracleModel:
     """OrModel over numpy copies of the decoder's device tensors."""
 
@@ -234,13 +285,31 @@ class OracleModel:
         m.layers = self.layers
         self.m = m
 
-    def step(self, tok, pos):
-        B, V = self.cfg["batch"], self.cfg["vocab"]
+    def step(self, tok, pos, tf_x=None, taps=False, threads=None):
+        """One step from ids `tok` at `pos`: (logits [B,V], next ids [B]).
+        With `tf_x` ([2L+1, B, D] f32, the residual entering each sublayer
+        taken from another implementation) every sublayer restarts from it.
+        With `tf_x` or `taps`, `self.taps` holds this step's x/q/att/h outputs
+        per sublayer."""
+        cfg = self.cfg
+        B, V, D, L = cfg["batch"], cfg["vocab"], cfg["dim"], cfg["n_layers"]
         tok = np.ascontiguousarray(tok, np.int32)
         lg = np.empty((B, V), np.float32)
         nx = np.empty(B, np.int32)
-        assert oracle().or_decode_step(C.byref(self.m), tok.ctypes.data, pos, lg.ctypes.data,
-                                         nx.ctypes.data) == 0
+        m = self.m
+        if tf_x is not None or taps:
+            hq = cfg["n_heads"] * cfg["head_dim"]
+            self.taps = dict(x=np.zeros((2 * L, B, D), np.float32), q=np.zeros((L, B, hq), np.float32),
+                             att=np.zeros((L, B, hq), np.float32),
+                             h=np.zeros((L, B, cfg["ffn"]), np.float32))
+            m = OrModel.from_buffer_copy(self.m)
+            m.tp_x, m.tp_q, m.tp_att, m.tp_h = (self.taps[k].ctypes.data for k in ("x", "q", "att", "h"))
+        if tf_x is not None:
+            tf = np.ascontiguousarray(tf_x, np.float32).reshape(2 * L + 1, B, D)
+            m.tf_x = tf.ctypes.data
+        rcs = _run_rows(oracle().or_decode_step, m, B, tok.ctypes.data, pos, lg.ctypes.data,
+                        nx.ctypes.data, threads=threads)
+        assert all(r == 0 for r in rcs)
         return lg, nx
 
 
@@ -307,11 +376,35 @@ class OracleDsv2:
         m.gate_out = self.gate.ctypes.data
         self.m = m
 
-    def step(self, tok, pos):
-        B, V = self.cfg["batch"], self.cfg["vocab"]
+    def step(self, tok, pos, tf_x=None, tf_sel=None, tf_probs=None, taps=False, threads=None):
+        """One step: (logits [B,V], next ids [B]); per-layer routing in
+        self.sel / self.probs / self.gate.  With `tf_x` ([2L+1, B, D]) every
+        sublayer restarts from the given residual; with it or `taps`,
+        `self.taps` holds the x / o outputs; with `tf_sel`, `tf_probs`
+        ([L, B, K]) the MoE layers combine those experts instead of their own
+        picks."""
+        cfg = self.cfg
+        B, V, D, L = cfg["batch"], cfg["vocab"], cfg["dim"], cfg["n_layers"]
         tok = np.ascontiguousarray(tok, np.int32)
         lg = np.empty((B, V), np.float32)
         nx = np.empty(B, np.int32)
-        assert oracle().or_dsv2_step(C.byref(self.m), tok.ctypes.data, pos, lg.ctypes.data,
-                                       nx.ctypes.data) == 0
+        m, keep = self.m, []
+        if tf_x is not None or tf_sel is not None or taps:
+            m = OrDsv2.from_buffer_copy(self.m)
+        if tf_x is not None or taps:
+            self.taps = dict(x=np.zeros((2 * L, B, D), np.float32),
+                             o=np.zeros((L, B, cfg["n_heads"] * cfg["d_v"]), np.float32))
+            m.tp_x, m.tp_o = self.taps["x"].ctypes.data, self.taps["o"].ctypes.data
+        if tf_x is not None:
+            tf = np.ascontiguousarray(tf_x, np.float32).reshape(2 * L + 1, B, D)
+            keep.append(tf)
+            m.tf_x = tf.ctypes.data
+        if tf_sel is not None:
+            ts = np.ascontiguousarray(tf_sel, np.int32).reshape(L, B, cfg["top_k"])
+            tp = np.ascontiguousarray(tf_probs, np.float32).reshape(L, B, cfg["top_k"])
+            keep += [ts, tp]
+            m.tf_sel, m.tf_probs = ts.ctypes.data, tp.ctypes.data
+        rcs = _run_rows(oracle().or_dsv2_step, m, B, tok.ctypes.data, pos, lg.ctypes.data,
+                        nx.ctypes.data, threads=threads)
+        assert all(r == 0 for r in rcs)
         return lg, nx

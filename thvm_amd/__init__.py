@@ -88,6 +88,13 @@ _SIGS = {
     "thvm_hip_buf_nbytes": (_u64, [_u32]), "thvm_hip_buf_zero": (None, [_u32]),
     "thvm_hip_buf_view": (_u32, [_u32, _u64, _u64]), "thvm_hip_buf_device_ptr": (_u64, [_u32]),
     "thvm_hip_mem_live_bytes": (_u64, []), "thvm_hip_mem_peak_bytes": (_u64, []),
+    "thvm_hip_buf_pool_begin": (_u32, []),
+    "thvm_hip_buf_pool_rollback_with_preserve": (None, [_u32]),
+    "thvm_hip_buf_pool_free_unpreserved": (None, [_u32]),
+    "thvm_hip_buf_mark_preserved": (None, [_u32]), "thvm_hip_buf_clear_preserved": (None, [_u32]),
+    "thvm_hip_buf_clear_preserved_arena_views": (None, [_u32]),
+    "thvm_hip_buf_free_unpreserved_all": (_u64, []), "thvm_hip_buf_arena_alloc": (_u32, [_u64]),
+    "thvm_hip_buf_slots_used": (_u32, []), "thvm_hip_buf_slot_highwater": (_u32, []),
     "thvm_hip_dispatch_begin": (None, []), "thvm_hip_dispatch_flush": (None, []),
     "thvm_hip_dispatch_end": (None, []),
     "thvm_hip_dispatch_custom": (_i32, [_cp, _cp, _vp, _vp, _u32, _vp, _u32, _u64]),
@@ -127,6 +134,8 @@ _SIGS = {
     "thvm_hip_decoder_step_bytes": (_u64, [_u32]),
     "thvm_hip_decoder_step_kernels": (_u32, [_u32]),
     "thvm_hip_decoder_stage_clock": (C.c_int, [_u32, C.c_void_p, _u32]),
+    "thvm_hip_decoder_op_tags": (C.c_int, [_u32, C.c_void_p, _u32]),
+    "thvm_hip_decoder_run_ops": (_i32, [_u32, _u32, _u32]),
 }
 
 _LIB = None
@@ -383,6 +392,37 @@ class Decoder:
         if got < 0:
             raise ThvmHipError(f"stage_clock: {last_error()}")
         return out[:got]
+
+    def op_tags(self) -> np.ndarray:
+        """The sublayer of each dispatch of the step: 2l (layer l's
+        attention), 2l+1 (its FFN), -1 before the layers, -2 after."""
+        n = lib().thvm_hip_decoder_op_tags(self.h, None, 0)
+        if n < 0:
+            raise ThvmHipError(f"op_tags: {last_error()}")
+        out = np.empty(n, np.int32)
+        if lib().thvm_hip_decoder_op_tags(self.h, out.ctypes.data, n) < 0:
+            raise ThvmHipError(f"op_tags: {last_error()}")
+        return out
+
+    def run_ops(self, first: int, count: int) -> None:
+        """Dispatch ops [first, first + count) of the step eagerly."""
+        _check(lib().thvm_hip_decoder_run_ops(self.h, first, count), "run_ops")
+
+    def step_probed(self, reads, on_boundary):
+        """One eager step run a sublayer at a time.  After the embedding
+        (tag -1) and after each sublayer t, `on_boundary(t, {name: array})`
+        receives the tensors named in `reads(t)` as read from the device;
+        the tail then runs (logits, argmax, length bump)."""
+        tags = self.op_tags()
+        i, n = 0, len(tags)
+        while i < n and tags[i] != -2:
+            j = i
+            while j < n and tags[j] == tags[i]:
+                j += 1
+            self.run_ops(i, j - i)
+            on_boundary(int(tags[i]), {k: self.read_tensor(k) for k in reads(int(tags[i]))})
+            i = j
+        self.run_ops(i, n - i)
 
     def close(self) -> None:
         if self.h:

@@ -44,6 +44,7 @@ typedef struct {
   u32   args[24];
   u32   n_args;
   u64   outs;
+  int32_t tag;   /* 2l: layer l's attention sublayer, 2l+1: its FFN; -1 before the layers, -2 after */
 } DOp;
 
 typedef struct {
@@ -62,6 +63,7 @@ typedef struct {
   u32 rows;
   int spec;
   char pfx[4];
+  int32_t cur_tag;        /* tag of the ops being added */
   DOp *sops;              /* the speculative step (spec_rows > 0) */
   u32 n_sops;
   u32 spec_slot;
@@ -245,6 +247,7 @@ static int op_add_raw(Decoder *d, const char *name, const char *prog, const u32 
   memcpy(o->args, args, n * sizeof(u32));
   o->n_args = n;
   o->outs = 1;
+  o->tag = d->cur_tag;
   if (hb_builtin_launch(prog, args, n, 1)) return -1;   /* validate now */
   return 0;
 }
@@ -414,6 +417,7 @@ THVM_API uint32_t thvm_hip_decoder_create(const ThvmDecodeConfig *cfg, uint64_t 
   d->seed = seed;
   d->n_split = (d->c.max_seq + 63) / 64;
   d->rows = d->c.batch;
+  d->cur_tag = -1;
   int rc = d->c.arch == THVM_ARCH_LLAMA ? build_llama(d)
          : d->c.arch == THVM_ARCH_GPT2  ? build_gpt2(d) : build_dsv2(d);
   if (rc) { dec_free(d); return 0; }
@@ -638,6 +642,7 @@ static int llama_ops(Decoder *d) {
   if (op_add(d, "embed", p, ea, 3)) return -1;
 
   for (u32 l = 0; l < c->n_layers; l++) {
+    d->cur_tag = (int32_t)(2 * l);
 #define LT(fmt) (snprintf(nm, sizeof nm, fmt, l), tens_find(d, nm))
     const u32 wqkv = LT("l%u.wqkv"), wo = LT("l%u.wo"), wgu = LT("l%u.wgu"), wd = LT("l%u.wd");
     const u32 sqkv = f8 ? LT("l%u.wqkv.scale") : 0, so = f8 ? LT("l%u.wo.scale") : 0,
@@ -671,6 +676,7 @@ static int llama_ops(Decoder *d) {
     oa[on++] = x;
     if (op_add(d, "gemv_o", p, oa, on)) return -1;
 
+    d->cur_tag = (int32_t)(2 * l + 1);
     NormSpec n2 = {1, gf, 0};
     if (emit_norm(d, &n2, &gin, nsp, sizeof nsp, gargs, &ng)) return -1;
     snprintf(p, sizeof p, "thvm-builtin:gemv m=%u n=%u k=%u wt=%u xt=%u yt=%u epi=%u%s", B, 2 * F,
@@ -689,8 +695,11 @@ static int llama_ops(Decoder *d) {
     da[dn++] = x;
     if (op_add(d, "gemv_down", p, da, dn)) return -1;
   }
+  d->cur_tag = -2;
   NormSpec nf = {1, tens_find(d, "norm_f"), 0};
-  return op_tail(d, tens_find(d, "lm"), f8 ? tens_find(d, "lm.scale") : 0, &nf);
+  const int rc = op_tail(d, tens_find(d, "lm"), f8 ? tens_find(d, "lm.scale") : 0, &nf);
+  d->cur_tag = -1;
+  return rc;
 }
 
 /* The speculative step (reference step_build_spec, bench/dsv2_decode_bench.c:
@@ -781,6 +790,7 @@ static int build_gpt2(Decoder *d) {
   if (op_add(d, "embed", p, ea, 5)) return -1;
 
   for (u32 l = 0; l < c->n_layers; l++) {
+    d->cur_tag = (int32_t)(2 * l);
     u32 wqkv, wo, wfc, wpr, s_unused;
     snprintf(nm, sizeof nm, "l%u.c_attn", l);
     if (weight_matrix(d, nm, 3 * D, D, &wqkv, &s_unused)) return -1;
@@ -829,6 +839,7 @@ static int build_gpt2(Decoder *d) {
              D, wdt, adt, adt, THVM_EPI_RESID);
     u32 oa[5] = {x, att, wo, bo, x};
     if (op_add(d, "gemv_o", p, oa, 5)) return -1;
+    d->cur_tag = (int32_t)(2 * l + 1);
     NormSpec n2 = {2, g2, b2};
     if (emit_norm(d, &n2, &gin, nsp, sizeof nsp, gargs, &ng)) return -1;
     snprintf(p, sizeof p, "thvm-builtin:gemv m=%u n=%u k=%u wt=%u xt=%u yt=%u epi=%u bias=1%s", B,
@@ -844,8 +855,11 @@ static int build_gpt2(Decoder *d) {
     if (op_add(d, "gemv_proj", p, pa, 5)) return -1;
   }
   d->weight_bytes += (u64)c->vocab * D * hb_dt_size(adt);   /* tied LM head */
+  d->cur_tag = -2;
   NormSpec nf = {2, gf, bf};
-  return op_tail(d, wte, 0, &nf);
+  const int rc = op_tail(d, wte, 0, &nf);
+  d->cur_tag = -1;
+  return rc;
 }
 
 /* ---- DeepSeek-V2 (MLA + MoE), the C5 shape ------------------------------
@@ -944,6 +958,7 @@ static int build_dsv2(Decoder *d) {
   if (op_add(d, "embed", p, ea, 3)) return -1;
 
   for (u32 l = 0; l < c->n_layers; l++) {
+    d->cur_tag = (int32_t)(2 * l);
     u32 wqkv, sqkv, wuk, suk, wuv, suv, wo, so;
 #define WM(nmfmt, rows, cols, w, s) \
     do { snprintf(nm, sizeof nm, nmfmt, l); if (weight_matrix(d, nm, rows, cols, w, s)) return -1; } while (0)
@@ -1004,6 +1019,7 @@ static int build_dsv2(Decoder *d) {
     oa[on++] = x;
     if (op_add(d, "gemv_o", p, oa, on)) return -1;
 
+    d->cur_tag = (int32_t)(2 * l + 1);
     if (l < c->first_dense) {   /* dense SwiGLU FFN with the post-attention norm fused */
       u32 wgu, sgu, wd, sd;
       WM("l%u.wgu", 2 * F, D, &wgu, &sgu);
@@ -1111,6 +1127,7 @@ static int build_dsv2(Decoder *d) {
   }
   /* final norm in f32 (rms_f) -> LM head; batches above 4 rows feed the
    * MFMA GEMM, which takes 16-bit x: their normed rows are rounded to bf16 */
+  d->cur_tag = -2;
   u32 lw, ls;
   if (weight_matrix(d, "lm", V, D, &lw, &ls)) return -1;
   const u32 lmx = grp ? tens_find(d, "xn") : xnf, lmt = grp ? THVM_DT_BF16 : THVM_DT_FP32;
@@ -1130,7 +1147,9 @@ static int build_dsv2(Decoder *d) {
   u32 am[6] = {tens_find(d, "tok"), tens_find(d, "logits"), tens_find(d, "am.pv"),
                tens_find(d, "am.pi"), tens_find(d, "hist"), L};
   if (op_add(d, "argmax", p, am, 6)) return -1;
-  return op_add(d, "len_bump", "thvm-builtin:len_bump delta=1", &L, 1);
+  const int rc = op_add(d, "len_bump", "thvm-builtin:len_bump delta=1", &L, 1);
+  d->cur_tag = -1;
+  return rc;
 }
 
 THVM_API int thvm_hip_decoder_sync_weights(uint32_t h, const char *name) {
@@ -1371,6 +1390,26 @@ THVM_API uint64_t thvm_hip_decoder_step_bytes(uint32_t h) {
 THVM_API uint32_t thvm_hip_decoder_step_kernels(uint32_t h) {
   Decoder *d = dec_get(h);
   return d ? d->n_ops : 0;
+}
+
+THVM_API int thvm_hip_decoder_op_tags(uint32_t h, int32_t *tags, uint32_t n) {
+  Decoder *d = dec_get(h);
+  if (!d) return -1;
+  if (!tags && n) { hb_set_error("decoder_op_tags: no output"); return -1; }
+  const u32 m = n < d->n_ops ? n : d->n_ops;
+  for (u32 i = 0; i < m; i++) tags[i] = d->ops[i].tag;
+  return (int)d->n_ops;
+}
+
+THVM_API int thvm_hip_decoder_run_ops(uint32_t h, uint32_t first, uint32_t count) {
+  Decoder *d = dec_get(h);
+  if (!d) return -1;
+  if (thvm_hip_jit_is_capturing()) { hb_set_error("decoder_run_ops: a JIT capture is open"); return -1; }
+  if (first > d->n_ops || count > d->n_ops - first) {
+    hb_set_error("decoder_run_ops: ops [%u, %u + %u) outside the step's %u", first, first, count, d->n_ops);
+    return -1;
+  }
+  return run_list(d->ops + first, count);
 }
 
 THVM_API int thvm_hip_decoder_stage_clock(uint32_t h, double *us_out, uint32_t n) {

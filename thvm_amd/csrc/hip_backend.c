@@ -7,12 +7,19 @@
  *                    buf_free.c, buf_incref.c, buf_decref.c, buf_freelist.c
  *   read / write     buf_read.c:6-26, buf_write.c:7-17, buf_copy.c
  *   dispatch_end     _.c:23-27 (drain unless a graph capture is open)
- * Semantics kept: ids are u32 table indices with 0 = none; fresh buffers read
- * as zeros; a decref to 0 parks an owning block on a best-fit freelist, and a
- * recycled block moves to a fresh slot id (the donor id goes dead), so a stale
- * id can never alias live storage; arena views hold a reference on their
- * parent.  All transfers and kernels are ordered on one non-blocking stream
- * created at default priority. */
+ *   pool / preserve  buf_pool.c:9-183 (watermark rollback, preserve marks,
+ *                    the table-wide unpreserved sweep)
+ * Semantics kept: ids are u32 with 0 = none; fresh buffers read as zeros; a
+ * decref to 0 parks an owning block on a best-fit freelist, and a recycled
+ * block moves to a fresh id (the donor id goes dead), so a stale id can never
+ * alias live storage; arena views hold a reference on their parent.
+ * Unlike the reference's ever-growing table, dead slots are reused: an id is
+ * the slot index (low HB_IDX_BITS bits) and the slot's generation (high
+ * bits), bumped each time the slot dies, so a stale id fails the generation
+ * check instead of aliasing the slot's next buffer; a slot whose generation
+ * is spent is retired.  Pool watermarks are allocation sequence numbers, not
+ * slot indices.  All transfers and kernels are ordered on one non-blocking
+ * stream created at default priority. */
 #define _GNU_SOURCE
 #include "internal.h"
 
@@ -71,25 +78,45 @@ typedef struct {
   u64   req;           /* requested (logical) size                    */
   u32   refcount;
   u32   parent;        /* views: parent id                            */
+  u32   seq;           /* allocation sequence number (pool watermark) */
+  uint16_t   gen;           /* generation of the slot's current id         */
   u8    live;
   u8    owns;          /* 1: hipFree on release                       */
   u8    parked;        /* on the freelist (refcount 0)                */
   u8    jit_pinned;
+  u8    preserved;     /* survives the current pool rollback          */
+  u8    arena;         /* freed outright at rollback, never parked    */
 } HbBuf;
 
-#define HB_BUFS_CAP     (1u << 18)
+#define HB_IDX_BITS     18u
+#define HB_BUFS_CAP     (1u << HB_IDX_BITS)
+#define HB_IDX_MASK     (HB_BUFS_CAP - 1u)
+#define HB_GEN_MAX      ((1u << (32u - HB_IDX_BITS)) - 1u)
 #define HB_FREELIST_CAP 4096u
 
 static HbBuf *BUFS = NULL;
-static u32    BUFS_NEXT = 1;
+static u32    BUFS_NEXT = 1;          /* slots [1, BUFS_NEXT) have been used */
+static u32   *DEAD = NULL;            /* reusable dead slot indices          */
+static u32    N_DEAD = 0;
+static u32    N_RETIRED = 0;          /* slots whose ids are all spent       */
+static u32    ALLOC_SEQ = 1;          /* next allocation's sequence number   */
 static u32    FREELIST[HB_FREELIST_CAP];
 static u32    FREELIST_LEN = 0;
 static u64    MEM_LIVE = 0, MEM_PEAK = 0;
+/* allocation log: (slot, sequence number) of each buffer issued, in sequence
+ * order, so a pool watermark's buffers are found without scanning the table.
+ * An entry whose slot has died or been reissued no longer matches its slot's
+ * sequence number; compaction drops those. */
+static u32   *LOG_IDX = NULL, *LOG_SEQ = NULL;
+static u32    LOG_N = 0, LOG_CAP = 0;
+
+static u32 id_of(u32 idx) { return idx | ((u32)BUFS[idx].gen << HB_IDX_BITS); }
 
 static HbBuf *buf_get(u32 id) {
-  if (BUFS == NULL || id == 0 || id >= BUFS_NEXT) return NULL;
-  HbBuf *b = &BUFS[id];
-  return b->live ? b : NULL;
+  const u32 idx = id & HB_IDX_MASK;
+  if (BUFS == NULL || idx == 0 || idx >= BUFS_NEXT) return NULL;
+  HbBuf *b = &BUFS[idx];
+  return (b->live && b->gen == (id >> HB_IDX_BITS)) ? b : NULL;
 }
 
 void *hb_buf_ptr(u32 id) {
@@ -101,12 +128,80 @@ u64 hb_buf_size(u32 id) {
   return (b && !b->parked) ? b->req : 0;
 }
 
+/* A slot index for a new buffer: a dead slot if any, else a fresh one.
+ * The caller fills the slot and marks it live. */
 static u32 slot_new(void) {
+  if (N_DEAD) return DEAD[--N_DEAD];
   if (BUFS_NEXT >= HB_BUFS_CAP) {
-    hb_set_error("buf_alloc: out of buffer slots (cap %u)", HB_BUFS_CAP);
+    hb_set_error("buf_alloc: out of buffer slots (cap %u live)", HB_BUFS_CAP - 1);
     return 0;
   }
   return BUFS_NEXT++;
+}
+/* a slot taken by slot_new but never issued goes back unchanged */
+static void slot_unuse(u32 idx) { DEAD[N_DEAD++] = idx; }
+/* the slot's buffer is gone: clear it, bump its generation (every id it
+ * issued goes stale), and reuse it -- or retire it when the generation is
+ * spent, so an id is never issued twice */
+static void slot_kill(u32 idx) {
+  const u32 gen = BUFS[idx].gen + 1u;
+  memset(&BUFS[idx], 0, sizeof(HbBuf));
+  if (gen > HB_GEN_MAX) { N_RETIRED++; return; }
+  BUFS[idx].gen = (uint16_t)gen;
+  DEAD[N_DEAD++] = idx;
+}
+static int log_live(u32 i) {
+  const HbBuf *b = &BUFS[LOG_IDX[i]];
+  return b->live && b->seq == LOG_SEQ[i];
+}
+/* keep the live entries of [start, LOG_N), in order */
+static void log_compact_from(u32 start) {
+  u32 w = start;
+  for (u32 r = start; r < LOG_N; r++)
+    if (log_live(r)) { LOG_IDX[w] = LOG_IDX[r]; LOG_SEQ[w] = LOG_SEQ[r]; w++; }
+  LOG_N = w;
+}
+/* first entry with sequence number >= wm */
+static u32 log_first(u32 wm) {
+  u32 lo = 0, hi = LOG_N;
+  while (lo < hi) {
+    const u32 mid = lo + (hi - lo) / 2;
+    if (LOG_SEQ[mid] < wm) lo = mid + 1; else hi = mid;
+  }
+  return lo;
+}
+static void log_push(u32 idx, u32 seq) {
+  const u32 live = BUFS_NEXT - 1u - N_DEAD - N_RETIRED;
+  if (LOG_N > 2u * live + 1024u) log_compact_from(0);
+  if (LOG_N == LOG_CAP) {
+    const u32 cap = LOG_CAP ? 2u * LOG_CAP : 4096u;
+    u32 *a = (u32 *)realloc(LOG_IDX, cap * sizeof(u32)), *q = a ? (u32 *)realloc(LOG_SEQ, cap * sizeof(u32)) : NULL;
+    if (a) LOG_IDX = a;
+    if (!a || !q) return;      /* out of host memory: this buffer is simply never rolled back */
+    LOG_SEQ = q;
+    LOG_CAP = cap;
+  }
+  LOG_IDX[LOG_N] = idx;
+  LOG_SEQ[LOG_N] = seq;
+  LOG_N++;
+}
+
+/* fill a fresh slot as a live buffer and return its id */
+static u32 slot_issue(u32 idx, void *dptr, u64 nbytes, u64 req, u8 owns, u32 parent) {
+  HbBuf *b = &BUFS[idx];
+  const uint16_t gen = b->gen;
+  memset(b, 0, sizeof *b);
+  b->gen = gen;
+  b->dptr = dptr;
+  b->nbytes = nbytes;
+  b->req = req;
+  b->refcount = 1;
+  b->live = 1;
+  b->owns = owns;
+  b->parent = parent;
+  b->seq = ALLOC_SEQ++;
+  log_push(idx, b->seq);
+  return id_of(idx);
 }
 
 static void freelist_drop(u32 id) {
@@ -118,13 +213,14 @@ static void freelist_drop(u32 id) {
   }
 }
 
-static void real_free(HbBuf *b) {
+static void real_free(u32 idx) {
+  HbBuf *b = &BUFS[idx];
   if (b->owns && b->dptr) {
     hipStreamSynchronize(HB_STREAM);
     hipFree(b->dptr);
     MEM_LIVE -= b->nbytes;
   }
-  memset(b, 0, sizeof *b);
+  slot_kill(idx);
 }
 
 /* best fit among parked blocks with capacity in [n, 2n]; moves the block to a
@@ -133,7 +229,7 @@ static u32 freelist_pop(u64 n) {
   u32 best = 0, best_i = 0;
   u64 best_sz = ~0ull;
   for (u32 i = 0; i < FREELIST_LEN; i++) {
-    HbBuf *b = &BUFS[FREELIST[i]];
+    HbBuf *b = &BUFS[FREELIST[i] & HB_IDX_MASK];
     if (b->nbytes >= n && b->nbytes <= 2 * n + 4096 && b->nbytes < best_sz) {
       best = FREELIST[i];
       best_i = i;
@@ -141,19 +237,24 @@ static u32 freelist_pop(u64 n) {
     }
   }
   if (best == 0) return 0;
-  u32 nid = slot_new();
-  if (nid == 0) return 0;
   FREELIST[best_i] = FREELIST[--FREELIST_LEN];
-  BUFS[nid] = BUFS[best];
-  memset(&BUFS[best], 0, sizeof(HbBuf));   /* donor id goes dead */
-  HbBuf *b = &BUFS[nid];
-  b->parked = 0;
-  b->refcount = 1;
-  b->req = n;
-  b->jit_pinned = 0;
-  hipMemsetAsync(b->dptr, 0, b->nbytes, HB_STREAM);
+  const u32 donor = best & HB_IDX_MASK;
+  void *dptr = BUFS[donor].dptr;
+  const u64 cap = BUFS[donor].nbytes;
+  slot_kill(donor);                        /* donor id goes dead */
+  const u32 idx = slot_new();              /* (at worst the donor's own slot, next generation) */
+  if (idx == 0) {                          /* its generation was spent and no slot is left */
+    hipStreamSynchronize(HB_STREAM);
+    hipFree(dptr);
+    MEM_LIVE -= cap;
+    return 0;
+  }
+  const u32 nid = slot_issue(idx, dptr, cap, n, 1, 0);
+  hipMemsetAsync(dptr, 0, cap, HB_STREAM);
   return nid;
 }
+
+static u32 alloc_fresh(u64 nbytes, u8 arena);
 
 THVM_API uint32_t thvm_hip_buf_alloc(uint64_t nbytes) {
   if (hb_require_ready("buf_alloc")) return 0;
@@ -173,34 +274,46 @@ THVM_API uint32_t thvm_hip_buf_alloc(uint64_t nbytes) {
   if (nbytes == 0) nbytes = 1;
   u32 r = freelist_pop(nbytes);
   if (r) return r;
-  u32 id = slot_new();
-  if (id == 0) return 0;
+  return alloc_fresh(nbytes, 0);
+}
+
+/* hipMalloc a zero-filled block into a new slot */
+static u32 alloc_fresh(u64 nbytes, u8 arena) {
+  u32 idx = slot_new();
+  if (idx == 0) return 0;
   u64 cap_bytes = (nbytes + 255) & ~255ull;
   void *p = NULL;
   hipError_t e = hipMalloc(&p, cap_bytes);
   if (e != hipSuccess) {
-    BUFS_NEXT--;
+    slot_unuse(idx);
     hb_set_error("hipMalloc(%llu): %s", (unsigned long long)cap_bytes, hipGetErrorString(e));
     return 0;
   }
   e = hipMemsetAsync(p, 0, cap_bytes, HB_STREAM);
   if (e != hipSuccess) {
     hipFree(p);
-    BUFS_NEXT--;
+    slot_unuse(idx);
     hb_set_error("hipMemsetAsync: %s", hipGetErrorString(e));
     return 0;
   }
-  HbBuf *b = &BUFS[id];
-  memset(b, 0, sizeof *b);
-  b->dptr = p;
-  b->nbytes = cap_bytes;
-  b->req = nbytes;
-  b->refcount = 1;
-  b->live = 1;
-  b->owns = 1;
+  const u32 id = slot_issue(idx, p, cap_bytes, nbytes, 1, 0);
+  BUFS[idx].arena = arena;
   MEM_LIVE += cap_bytes;
   if (MEM_LIVE > MEM_PEAK) MEM_PEAK = MEM_LIVE;
   return id;
+}
+
+/* A per-realize arena block (the reference's skip_freelist buffers): like
+ * buf_alloc, never recycled from or parked on the freelist -- a pool
+ * rollback or the unpreserved sweep frees it outright, so its bytes do not
+ * sit parked while the next realize allocates a fresh arena. */
+THVM_API uint32_t thvm_hip_buf_arena_alloc(uint64_t nbytes) {
+  if (hb_require_ready("buf_arena_alloc")) return 0;
+  if (hb_stream_capturing()) {
+    hb_set_error("buf_arena_alloc: not allowed while a graph capture is open");
+    return 0;
+  }
+  return alloc_fresh(nbytes ? nbytes : 1, 1);
 }
 
 THVM_API uint32_t thvm_hip_buf_view(uint32_t parent_id, uint64_t byte_off, uint64_t nbytes) {
@@ -213,18 +326,9 @@ THVM_API uint32_t thvm_hip_buf_view(uint32_t parent_id, uint64_t byte_off, uint6
                  (unsigned long long)p->nbytes);
     return 0;
   }
-  u32 id = slot_new();
-  if (id == 0) return 0;
-  p = &BUFS[parent_id];
-  HbBuf *b = &BUFS[id];
-  memset(b, 0, sizeof *b);
-  b->dptr = (char *)p->dptr + byte_off;
-  b->nbytes = nbytes;
-  b->req = nbytes;
-  b->refcount = 1;
-  b->live = 1;
-  b->owns = 0;
-  b->parent = parent_id;
+  u32 idx = slot_new();
+  if (idx == 0) return 0;
+  const u32 id = slot_issue(idx, (char *)p->dptr + byte_off, nbytes, nbytes, 0, parent_id);
   p->refcount++;
   return id;
 }
@@ -236,7 +340,7 @@ THVM_API void thvm_hip_buf_free(uint32_t buf_id) {
   if (!b) return;
   if (b->parked) freelist_drop(buf_id);
   u32 parent = b->owns ? 0 : b->parent;
-  real_free(b);
+  real_free(buf_id & HB_IDX_MASK);
   if (parent) release(parent);
 }
 
@@ -245,8 +349,9 @@ static void release(u32 id) {
   if (!b || b->refcount == 0) return;
   if (--b->refcount > 0) return;
   if (b->jit_pinned) { b->refcount = 1; return; }   /* held by a capture */
-  if (b->owns && FREELIST_LEN < HB_FREELIST_CAP) {
+  if (b->owns && !b->arena && FREELIST_LEN < HB_FREELIST_CAP) {
     b->parked = 1;
+    b->preserved = 0;
     FREELIST[FREELIST_LEN++] = id;
     return;
   }
@@ -273,10 +378,11 @@ THVM_API uint32_t thvm_hip_buf_refcount(uint32_t buf_id) {
 }
 THVM_API void thvm_hip_buf_freelist_push(uint32_t buf_id) {
   HbBuf *b = buf_get(buf_id);
-  if (!b || b->parked || !b->owns || b->jit_pinned) return;
+  if (!b || b->parked || !b->owns || b->arena || b->jit_pinned) return;
   if (FREELIST_LEN >= HB_FREELIST_CAP) return;
   b->refcount = 0;
   b->parked = 1;
+  b->preserved = 0;
   FREELIST[FREELIST_LEN++] = buf_id;
 }
 THVM_API void thvm_hip_buf_freelist_remove(uint32_t buf_id) {
@@ -301,6 +407,109 @@ THVM_API uint64_t thvm_hip_buf_device_ptr(uint32_t buf_id) {
 }
 THVM_API uint64_t thvm_hip_mem_live_bytes(void) { return MEM_LIVE; }
 THVM_API uint64_t thvm_hip_mem_peak_bytes(void) { return MEM_PEAK; }
+THVM_API uint32_t thvm_hip_buf_slots_used(void) { return BUFS ? BUFS_NEXT - 1u - N_DEAD - N_RETIRED : 0u; }
+THVM_API uint32_t thvm_hip_buf_slot_highwater(void) { return BUFS ? BUFS_NEXT - 1u : 0u; }
+
+/* ---- pool watermarks and preserve marks (reference buf_pool.c) ----
+ * A watermark is the sequence number the next allocation will take; "since
+ * wm" means every live buffer whose sequence number is >= wm (wm 0 or 1:
+ * every buffer).  Sequence numbers are 32-bit: a session of more than 2^32
+ * allocations wraps them. */
+static u32 wm_of(u32 wm) { return wm < 1u ? 1u : wm; }
+
+THVM_API uint32_t thvm_hip_buf_pool_begin(void) { return ALLOC_SEQ; }
+
+THVM_API void thvm_hip_buf_mark_preserved(uint32_t buf_id) {
+  HbBuf *b = buf_get(buf_id);
+  if (b && !b->parked) b->preserved = 1;
+}
+
+THVM_API void thvm_hip_buf_clear_preserved(uint32_t wm) {
+  if (!BUFS) return;
+  for (u32 i = log_first(wm_of(wm)); i < LOG_N; i++)
+    if (log_live(i)) BUFS[LOG_IDX[i]].preserved = 0;
+}
+
+/* Arena views since wm lose their mark, and so does their parent when the
+ * parent itself was allocated since wm (an older parent -- a weight a view
+ * reads -- keeps its mark). */
+THVM_API void thvm_hip_buf_clear_preserved_arena_views(uint32_t wm) {
+  if (!BUFS) return;
+  wm = wm_of(wm);
+  for (u32 i = log_first(wm); i < LOG_N; i++) {
+    if (!log_live(i)) continue;
+    HbBuf *b = &BUFS[LOG_IDX[i]];
+    if (b->owns || !b->parent) continue;
+    b->preserved = 0;
+    HbBuf *p = buf_get(b->parent);
+    if (p && p->seq >= wm) p->preserved = 0;
+  }
+}
+
+/* Every buffer allocated since wm that is not preserved, not held by a JIT
+ * capture and not already parked: an arena block is freed, an owning block is
+ * parked on the freelist for the next same-size allocation (freed when the
+ * freelist is full), a view is freed (releasing its parent).  Refcounts are
+ * not consulted: the caller's planner has established that these buffers are
+ * dead. */
+THVM_API void thvm_hip_buf_pool_rollback_with_preserve(uint32_t wm) {
+  if (!BUFS) return;
+  const u32 first = log_first(wm_of(wm));
+  for (u32 i = first; i < LOG_N; i++) {
+    if (!log_live(i)) continue;
+    HbBuf *b = &BUFS[LOG_IDX[i]];
+    if (b->preserved || b->jit_pinned || b->parked) continue;
+    const u32 id = id_of(LOG_IDX[i]);
+    if (b->owns && !b->arena) {
+      thvm_hip_buf_freelist_push(id);
+      if (!b->parked) thvm_hip_buf_free(id);
+    } else {
+      thvm_hip_buf_free(id);
+    }
+  }
+  log_compact_from(first);
+}
+
+/* As the rollback, but every such buffer is freed outright (its storage
+ * returned to the device rather than parked). */
+THVM_API void thvm_hip_buf_pool_free_unpreserved(uint32_t wm) {
+  if (!BUFS) return;
+  const u32 first = log_first(wm_of(wm));
+  for (u32 i = first; i < LOG_N; i++) {
+    if (!log_live(i)) continue;
+    HbBuf *b = &BUFS[LOG_IDX[i]];
+    if (b->preserved || b->jit_pinned || b->parked) continue;
+    thvm_hip_buf_free(id_of(LOG_IDX[i]));
+  }
+  log_compact_from(first);
+}
+
+/* The whole table: every owning buffer that is live, not preserved and not
+ * held by a capture is parked (freed when the freelist is full; an arena
+ * block is always freed).  Views are left alone -- their storage goes with
+ * the parent's entry.  The stream is drained first so no kernel in flight
+ * still reads a reclaimed block.  Returns the bytes reclaimed. */
+THVM_API uint64_t thvm_hip_buf_free_unpreserved_all(void) {
+  if (!HB_READY || !BUFS) return 0;
+  u32 n = 0;
+  for (u32 i = 1; i < BUFS_NEXT; i++) {
+    const HbBuf *b = &BUFS[i];
+    n += b->live && !b->parked && b->owns && !b->preserved && !b->jit_pinned;
+  }
+  if (n == 0) return 0;
+  hipStreamSynchronize(HB_STREAM);
+  u64 freed = 0;
+  for (u32 i = 1; i < BUFS_NEXT; i++) {
+    HbBuf *b = &BUFS[i];
+    if (!b->live || b->parked || !b->owns || b->preserved || b->jit_pinned) continue;
+    freed += b->nbytes;
+    const u32 id = id_of(i);
+    if (!b->arena) thvm_hip_buf_freelist_push(id);
+    if (!b->parked) thvm_hip_buf_free(id);
+  }
+  log_compact_from(0);
+  return freed;
+}
 
 /* 1 while work on the dispatch stream is being recorded into a graph
  * (the library's own capture or one the caller opened on the stream) */
@@ -433,7 +642,8 @@ THVM_API int thvm_hip_init(void) {
   if (e != hipSuccess) { hb_set_error("init: hipStreamCreate: %s", hipGetErrorString(e)); return -1; }
   if (BUFS == NULL) {
     BUFS = (HbBuf *)calloc(HB_BUFS_CAP, sizeof(HbBuf));
-    if (!BUFS) { hb_set_error("init: out of host memory"); return -1; }
+    DEAD = (u32 *)malloc(HB_BUFS_CAP * sizeof(u32));
+    if (!BUFS || !DEAD) { hb_set_error("init: out of host memory"); return -1; }
   }
   HB_READY = 1;
   return 0;
@@ -457,6 +667,9 @@ THVM_API void thvm_hip_shutdown(void) {
     memset(&BUFS[i], 0, sizeof(HbBuf));
   }
   BUFS_NEXT = 1;
+  N_DEAD = 0;
+  N_RETIRED = 0;
+  LOG_N = 0;
   FREELIST_LEN = 0;
   MEM_LIVE = 0;
   hipStreamDestroy(HB_STREAM);
