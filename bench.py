@@ -626,6 +626,142 @@ def run_spec(thvm, args) -> dict:
             "committed_ids_equal_greedy": f["greedy_equal"] and b["greedy_equal"]}
 
 
+PHASES = {
+    "gemv": ["entry", "loads issued", "x staged", "first batch consumed", "rows done", "", "",
+             "end (drained)"],
+    "attn": ["entry", "loads issued + q", "first chunk consumed", "chunks done", "row groups combined",
+             "wave maxima in LDS", "wave partials in LDS", "end (drained)"],
+    "merge": ["entry", "", "", "", "", "", "", "end (drained)"],
+}
+
+
+def _clock_record(rec, name, kern, c):
+    """Fold one launch's clock slots ([2][blocks][10]) into rec: per mark, the
+    median and the maximum over blocks in us after the earliest block's entry,
+    and per XCD the earliest entry (launch stagger across the 8 XCDs)."""
+    import numpy as np
+    parts = [("gemv" if kern == "gemv" else "attn", c[0])]
+    if kern == "attn" and c[1, :, 0].any():
+        parts.append(("merge", c[1]))
+    if not (c[0, :, 0] > 0).any():
+        raise RuntimeError(f"{name}: no phase-clock marks recorded (the kernels come from the "
+                           "measurement build libthvm_hip_pclk.so: python -m thvm_amd.build --variant pclk)")
+    t0 = min(int(p[p[:, 0] > 0, 0].min()) for _, p in parts)
+    for pname, p in parts:
+        live = p[p[:, 0] > 0]
+        key = f"{name}/{pname}" if pname == "merge" else name
+        r = rec.setdefault(key, {"kind": pname, "blocks": len(live), "marks": [], "xcd_entry": []})
+        row = []
+        for m in range(8):
+            v = live[:, m]
+            v = v[v > 0]
+            row.append((float(np.median(v - t0)) / 100.0, float((v - t0).max()) / 100.0)
+                       if len(v) else (None, None))
+        r["marks"].append(row)
+        xe = [float((live[live[:, 8] == x, 0] - t0).min()) / 100.0 if (live[:, 8] == x).any() else None
+              for x in range(8)]
+        r["xcd_entry"].append(xe)
+
+
+def run_phase_clock(thvm, args) -> dict:
+    """Per-phase clock of one layer's kernels inside an eager C4 step: the
+    step runs op by op; the ops of layer `--clock-layer` are re-dispatched
+    with the builtin's clk= option (thread 0 of every block records the 100
+    MHz wall clock at marks; see the kernels' pclk calls).  Per op and mark:
+    the median and the maximum over blocks, in us after the earliest block's
+    entry; over `--steps` steps, the median of those."""
+    import numpy as np
+    spec = MODELS[args.config if args.config != "all" else "C4"]
+    cfg = dict(spec["cfg"], batch=args.batch)
+    ctx = spec["ctx"]
+    cfg["max_seq"] = ((ctx + args.steps + args.warmup + 8 + 63) // 64) * 64
+    dec = thvm.Decoder(seed=1234, **cfg)
+    dec.prefill_synthetic(ctx, seed=99)
+    dec.set_state(list(range(1, args.batch + 1)), ctx)
+    dec.capture()
+    dec.replay(max(args.warmup, 1))
+    thvm.synchronize()
+    layer = args.clock_layer
+    tags = dec.op_tags()
+    ops = [i for i in range(len(tags)) if tags[i] in (2 * layer, 2 * layer + 1)]
+    CAP, NS = 2048, 10
+    clk = thvm.Buffer(CAP * 2 * NS * 8)
+    zero = np.zeros(CAP * 2 * NS, np.uint64)
+    rec, raw = {}, {}
+    if args.clock_graph:
+        # the whole step captured as one graph (as the decoder replays it), the
+        # layer's GEMV / attention ops with clocks of their own
+        bufs, info = {}, []
+        with thvm.Jit() as j:
+            for i in range(len(tags)):
+                name, prog, ids = dec.op_info(i)
+                kern = prog.split()[0].split(":")[1]
+                if i in ops and kern in ("gemv", "attn"):
+                    bufs[i] = thvm.Buffer(CAP * 2 * NS * 8)
+                    bufs[i].write(zero)
+                    thvm.dispatch(name, prog + f" clk={CAP}", ids + [bufs[i].id])
+                    info.append((i, name, kern))
+                else:
+                    thvm.dispatch(name, prog, ids)
+        for s in range(args.steps):
+            for b in bufs.values():
+                b.write(zero)
+            j.replay()
+            thvm.synchronize()
+            for i, name, kern in info:
+                c = bufs[i].read(np.uint64).reshape(2, CAP, NS).astype(np.int64)
+                raw.setdefault(name, []).append(c.copy())
+                _clock_record(rec, name, kern, c)
+        j.drop()
+    for s in range(0 if args.clock_graph else args.steps):
+        i = 0
+        while i < len(tags):
+            if i not in ops:
+                j = i
+                while j < len(tags) and j not in ops:
+                    j += 1
+                dec.run_ops(i, j - i)
+                i = j
+                continue
+            name, prog, ids = dec.op_info(i)
+            kern = prog.split()[0].split(":")[1]
+            if kern not in ("gemv", "attn"):
+                dec.run_ops(i, 1)
+                i += 1
+                continue
+            clk.write(zero)
+            thvm.dispatch(name, prog + f" clk={CAP}", ids + [clk.id])
+            c = clk.read(np.uint64).reshape(2, CAP, NS).astype(np.int64)
+            raw.setdefault(name, []).append(c.copy())
+            _clock_record(rec, name, kern, c)
+            i += 1
+    rdir = ROOT / "gpurun_out"
+    rdir.mkdir(exist_ok=True)
+    np.savez_compressed(rdir / ("phase_clock_graph_raw.npz" if args.clock_graph else "phase_clock_raw.npz"),
+                        **{k: np.stack(v) for k, v in raw.items()})
+    out = {}
+    for key, r in rec.items():
+        names = PHASES[r["kind"]]
+        marks = {}
+        for m in range(8):
+            vals = [row[m] for row in r["marks"] if row[m][0] is not None]
+            if not vals or not names[m]:
+                continue
+            marks[names[m]] = {"median_us": round(float(np.median([v[0] for v in vals])), 2),
+                               "max_us": round(float(np.median([v[1] for v in vals])), 2)}
+        xe = np.array([[v if v is not None else np.nan for v in row] for row in r["xcd_entry"]])
+        stagger = [round(float(v), 2) for v in np.nanmedian(xe, 0)]
+        out[key] = {"blocks": r["blocks"], "marks": marks, "xcd_first_entry_us": stagger}
+        log(f"[clock] {key} ({r['blocks']} blocks): " +
+            ", ".join(f"{k} {v['median_us']}/{v['max_us']}" for k, v in marks.items()) +
+            f"; first entry per XCD {stagger}")
+    dec.close()
+    return {"metric": "phase clock (us after the earliest block's entry: median/max over blocks)",
+            "config": {"workload": spec["name"], "layer": layer, "batch": args.batch, "steps": args.steps,
+                       "context": ctx, "mode": "graph replay" if args.clock_graph else "eager"},
+            "ops": out}
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -650,6 +786,12 @@ def main() -> int:
     ap.add_argument("--spec", type=int, default=0,
                     help="C4 batch 1 speculative decode with S verify rows (2..4): forced-acceptance "
                          "throughput and the bigram draft's ids per step")
+    ap.add_argument("--phase-clock", action="store_true",
+                    help="per-phase wall clock of one layer's GEMV and attention kernels inside an "
+                         "eager step (measurement, not the metric)")
+    ap.add_argument("--clock-layer", type=int, default=16)
+    ap.add_argument("--clock-graph", action="store_true",
+                    help="with --phase-clock: the step captured and replayed as one graph")
     ap.add_argument("--host", action="store_true",
                     help="C1/C3: run the GPT-2 driver on the Python Tensor host (TinyJit) "
                          "instead of the C decoder")
@@ -662,6 +804,8 @@ def main() -> int:
               "the multi-GPU sharding is a design note, not a measured path", file=sys.stderr)
         return 2
 
+    if args.phase_clock:           # the measurement build: kernels with phase-clock marks
+        os.environ["THVM_HIP_LIB_VARIANT"] = "pclk"
     if args.host_rendered:
         os.environ["THVM_HOST_GEMV"] = "0"
     if args.beam:
@@ -673,6 +817,9 @@ def main() -> int:
             return copy_calibration(thvm)
         if args.spec:
             print(json.dumps(run_spec(thvm, args)), flush=True)
+            return 0
+        if args.phase_clock:
+            print(json.dumps(run_phase_clock(thvm, args)), flush=True)
             return 0
         if args.config == "all":
             runs = [("C4", 1), ("C4", 16), ("C5", 1), ("C5", 32), ("C3", 1), ("C3", 8), ("C1", 1), ("C2", 0)]

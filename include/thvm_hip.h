@@ -474,6 +474,12 @@ int      thvm_hip_decoder_stage_clock(uint32_t dec, double *us_out, uint32_t n);
  * in between.  Not during a JIT capture.  0 / -1. */
 int      thvm_hip_decoder_op_tags(uint32_t dec, int32_t *tags, uint32_t n);
 int      thvm_hip_decoder_run_ops(uint32_t dec, uint32_t first, uint32_t count);
+/* Dispatch i of the step as thvm_hip_dispatch_custom would receive it: its
+ * name and program text (NUL-terminated, truncated to the caps) and up to
+ * ids_cap buffer ids; returns the op's buffer count, -1 on error.  A host
+ * can re-dispatch an op with options of its own (e.g. a builtin's clk=). */
+int      thvm_hip_decoder_op_info(uint32_t dec, uint32_t i, char *name, uint32_t name_cap,
+                                  char *prog, uint32_t prog_cap, uint32_t *ids, uint32_t ids_cap);
 
 #ifdef __cplusplus
 }

@@ -136,6 +136,7 @@ typedef struct { uint32_t op, dtype; int32_t src[4]; int64_t arg[4]; } RefUop;
 #define CAP_K 96
 #define CAP_ROWS 4096
 #define CAP_SLOTS 16
+#define CAP_VARS 4
 typedef struct {
   RefUop rows[CAP_ROWS];
   Term terms[CAP_ROWS];
@@ -145,6 +146,9 @@ typedef struct {
   u64 numel[CAP_SLOTS];
   void *buf[CAP_SLOTS];              /* slot 0: the output after the dispatch */
   u32 n_opt, opt_kind[8], opt_factor[8];
+  /* symbolic extents: the kernel's kvars in first-use order (DEFINE_VAR arg0
+   * = the index here), their bounds and the values bound at dispatch */
+  u32 n_var, var_id[CAP_VARS], var_lo[CAP_VARS], var_hi[CAP_VARS], var_val[CAP_VARS];
   int ok;
   char why[96];
 } CapK;
@@ -167,6 +171,18 @@ static int cap_row(CapK *c, Term t, u32 op, u32 dt) {
   c->terms[c->n] = t;
   return (int)c->n++;
 }
+/* the kernel's index of kvar vid (recorded with its bounds and current value) */
+static int cap_var(CapK *c, u32 vid) {
+  for (u32 i = 0; i < c->n_var; i++)
+    if (c->var_id[i] == vid) return (int)i;
+  if (c->n_var >= CAP_VARS) { c->ok = 0; snprintf(c->why, sizeof c->why, "over %d kvars", CAP_VARS); return -1; }
+  const u32 i = c->n_var++;
+  c->var_id[i] = vid;
+  c->var_lo[i] = KVARS[vid].lo;
+  c->var_hi[i] = kvar_hi(vid);
+  c->var_val[i] = kvar_runtime(vid);
+  return (int)i;
+}
 static int cap_flat(CapK *c, Term t) {
   if (!c->ok) return -1;
   if (term_tag(t) != TAG_UOP) { c->ok = 0; snprintf(c->why, sizeof c->why, "a non-UOP term (tag %u)", term_tag(t)); return -1; }
@@ -185,9 +201,22 @@ static int cap_flat(CapK *c, Term t) {
     }
     case UOP_RANGE: {
       const u32 ext = (u32)term_val(heap_read(loc + 2));
-      if (kvar_extent_is_var(ext)) { c->ok = 0; snprintf(c->why, sizeof c->why, "a symbolic extent"); return -1; }
+      int dv = -1;
+      if (kvar_extent_is_var(ext)) {
+        /* a symbolic extent (the reference's kvar loop bound, render_uop.c:
+         * 5055-5090): a DEFINE_VAR row (arg0 = the kernel's var index, arg1 /
+         * arg2 = its bounds) that the RANGE takes as src0 */
+        const int vi = cap_var(c, kvar_extent_var_id(ext));
+        if (vi < 0) return -1;
+        dv = cap_row(c, 0, UOP_DEFINE_VAR, DT_INT32);
+        if (dv < 0) return -1;
+        c->rows[dv].arg[0] = vi;
+        c->rows[dv].arg[1] = c->var_lo[vi];
+        c->rows[dv].arg[2] = c->var_hi[vi];
+      }
       r = cap_row(c, t, op, DT_INT32);
       if (r >= 0) {
+        c->rows[r].src[0] = dv;
         c->rows[r].arg[0] = (i64)term_val(heap_read(loc));
         c->rows[r].arg[1] = (i64)term_val(heap_read(loc + 1));
         c->rows[r].arg[2] = (i64)kvar_extent_static(ext);
@@ -412,6 +441,18 @@ int ref_capture_kernel(u32 k, RefUop *rows, u32 cap, u32 *n, u32 *n_slots, u32 *
   if (c->ok && c->n <= cap) memcpy(rows, c->rows, c->n * sizeof(RefUop));
   return c->ok;
 }
+/* kvars of kernel k: up to cap (value bound at dispatch, lo, hi) triples;
+ * returns the count */
+int ref_capture_vars(u32 k, u32 *vals, u32 cap) {
+  if (k >= NCAPS) return -1;
+  const CapK *c = &CAPS[k];
+  for (u32 i = 0; i < c->n_var && i < cap; i++) {
+    vals[3 * i] = c->var_val[i];
+    vals[3 * i + 1] = c->var_lo[i];
+    vals[3 * i + 2] = c->var_hi[i];
+  }
+  return (int)c->n_var;
+}
 /* slot s of kernel k: dtype, element count and (dst != NULL) the bytes */
 int ref_capture_slot(u32 k, u32 s, u32 *dt, u64 *numel, void *dst, u64 cap) {
   if (k >= NCAPS || s >= CAPS[k].n_slots || s >= CAP_SLOTS) return -1;
@@ -500,4 +541,125 @@ int ref_gpt2_block_f32(const float *x, const float *const *p, float *out, u32 T,
   Tensor h = nn_binop(UOP_ADD, X, nn_linear(a, wo, bo));
   Tensor m = nn_linear(nn_elementwise(NN_GELU, nn_linear(ref_ln(h, ln2w, ln2b), wfc, bfc)), wpr, bpr);
   return ref_read(nn_binop(UOP_ADD, h, m), out, (u64)T * D);
+}
+
+/* ---- narrow-float and symbolic-extent workloads ---------------------------
+ * The same operations on fp16 / bf16 tensors (the reference CPU path
+ * realizes non-f32 kernels through its uop walker, src/backend/cpu/
+ * uop_walk.c:141-293: values evaluated in double, narrowed at CAST / STORE),
+ * and decode attention over a cache whose length is a bound kvar (the
+ * symbolic extent the GPT-2 decode with a bound start_pos schedules,
+ * render_uop.c:5055-5090).  Inputs arrive as f32 and are narrowed with the
+ * reference's own encoders; outputs are written in the tensor's storage
+ * type (2-byte bits for fp16 / bf16). */
+static Tensor ref_tensor_dt(u32 ndim, const u32 *dims, u32 dt, const float *data) {
+  Shape sh = {0};
+  sh.ndim = ndim;
+  u64 n = 1;
+  for (u32 i = 0; i < ndim; i++) { sh.dims[i] = dims[i]; n *= kvar_extent_static(dims[i]); }
+  u32 tid = tensor_alloc(&CPU_BACKEND, sh, dt);
+  if (dt == DT_FP32) {
+    CPU_BACKEND.buf_write(TENS[tid].buf_id, (void *)data, n * 4);
+  } else {
+    u16 *b = (u16 *)malloc(n * 2 + 2);
+    for (u64 i = 0; i < n; i++) b[i] = dt == DT_FP16 ? f32_to_fp16(data[i]) : f32_to_bf16(data[i]);
+    CPU_BACKEND.buf_write(TENS[tid].buf_id, b, n * 2);
+    free(b);
+  }
+  Tensor t;
+  t.t = term_new(0, TAG_TEN, dt, tid);
+  t.dtype = dt;
+  t.shape = sh;
+  return t;
+}
+static int ref_read_dt(Tensor y, void *out, u64 n) {
+  if (y.t == 0) return -1;
+  Term r = term_resolve(thvm_realize(y.t));
+  if (term_tag(r) != TAG_TEN) return -1;
+  u32 tid = (u32)term_val(r);
+  if (TENS[tid].view.numel != n) return -2;
+  return TENS[tid].backend->buf_read(TENS[tid].buf_id, out, dtype_storage_bytes(TENS[tid].dtype, n));
+}
+
+int ref_linear_t(u32 dt, const float *x, const float *w, void *y, u32 M, u32 N, u32 K) {
+  ref_init();
+  u32 dx[2] = {M, K}, dw[2] = {N, K}, perm[2] = {1, 0};
+  Tensor X = ref_tensor_dt(2, dx, dt, x), W = ref_tensor_dt(2, dw, dt, w);
+  return ref_read_dt(nn_dot(X, nn_permute(W, 2, perm)), y, (u64)M * N);
+}
+int ref_softmax_t(u32 dt, const float *x, void *y, u32 M, u32 K) {
+  ref_init();
+  u32 d[2] = {M, K};
+  return ref_read_dt(nn_softmax(ref_tensor_dt(2, d, dt, x), -1, 0), y, (u64)M * K);
+}
+int ref_layernorm_t(u32 dt, const float *x, void *y, u32 M, u32 K, double eps) {
+  ref_init();
+  u32 d[2] = {M, K}, ax[1] = {1};
+  return ref_read_dt(nn_layernorm(ref_tensor_dt(2, d, dt, x), 1, ax, eps), y, (u64)M * K);
+}
+int ref_gelu_t(u32 dt, const float *x, void *y, u32 M, u32 K) {
+  ref_init();
+  u32 d[2] = {M, K};
+  return ref_read_dt(nn_elementwise(NN_GELU, ref_tensor_dt(2, d, dt, x)), y, (u64)M * K);
+}
+
+/* The GPT-2 block of ref_gpt2_block_f32 on dtype dt tensors (inputs and every
+ * parameter stored in dt). */
+int ref_gpt2_block_t(u32 dt, const float *x, const float *const *p, void *out, u32 T, u32 D, u32 H, u32 F) {
+  ref_init();
+  const u32 hd = D / H;
+  u32 dTD[2] = {T, D}, dDD[2] = {D, D}, dDF[2] = {D, F}, dFD[2] = {F, D}, dD[1] = {D}, dF[1] = {F};
+  Tensor X = ref_tensor_dt(2, dTD, dt, x);
+  Tensor ln1w = ref_tensor_dt(1, dD, dt, p[0]), ln1b = ref_tensor_dt(1, dD, dt, p[1]);
+  Tensor wq = ref_tensor_dt(2, dDD, dt, p[2]), bq = ref_tensor_dt(1, dD, dt, p[3]);
+  Tensor wk = ref_tensor_dt(2, dDD, dt, p[4]), bk = ref_tensor_dt(1, dD, dt, p[5]);
+  Tensor wv = ref_tensor_dt(2, dDD, dt, p[6]), bv = ref_tensor_dt(1, dD, dt, p[7]);
+  Tensor wo = ref_tensor_dt(2, dDD, dt, p[8]), bo = ref_tensor_dt(1, dD, dt, p[9]);
+  Tensor ln2w = ref_tensor_dt(1, dD, dt, p[10]), ln2b = ref_tensor_dt(1, dD, dt, p[11]);
+  Tensor wfc = ref_tensor_dt(2, dDF, dt, p[12]), bfc = ref_tensor_dt(1, dF, dt, p[13]);
+  Tensor wpr = ref_tensor_dt(2, dFD, dt, p[14]), bpr = ref_tensor_dt(1, dD, dt, p[15]);
+  Tensor z = ref_ln(X, ln1w, ln1b);
+  Tensor q = ref_heads(nn_linear(z, wq, bq), T, H, hd), k = ref_heads(nn_linear(z, wk, bk), T, H, hd),
+         v = ref_heads(nn_linear(z, wv, bv), T, H, hd);
+  Tensor none;
+  memset(&none, 0, sizeof none);
+  Tensor a = nn_scaled_dot_product_attention(q, k, v, none, 1);
+  u32 perm[3] = {1, 0, 2}, d2[2] = {T, D};
+  a = nn_reshape(nn_permute(a, 3, perm), 2, d2);
+  Tensor h = nn_binop(UOP_ADD, X, nn_linear(a, wo, bo));
+  Tensor m = nn_linear(nn_elementwise(NN_GELU, nn_linear(ref_ln(h, ln2w, ln2b), wfc, bfc)), wpr, bpr);
+  return ref_read_dt(nn_binop(UOP_ADD, h, m), out, (u64)T * D);
+}
+
+/* One decode query per head over a KV cache of a bound length: q [H][hd],
+ * k, v [H][Lmax][hd] of which rows [0, L) are live, L a kvar of bounds
+ * [1, Lmax] bound to L; out [H][hd] = softmax(q k^T * scale) v, built from
+ * uops as the reference's symbolic decode tests build it
+ * (tests/test_sym_decode_step.c, tests/test_sym_attn.c): scores reduce over
+ * hd, the softmax runs over the symbolic axis (exp2 of pre-scaled
+ * differences), the weighted sum reduces over the symbolic axis. */
+int ref_sym_attn_t(u32 dt, const float *q, const float *k, const float *v, void *out, u32 H, u32 Lmax,
+                   u32 L, u32 hd, float scale) {
+  ref_init();
+  const u32 s = kvar_alloc("L", 1, Lmax);
+  if (s == 0) return -3;
+  kvar_set_runtime(s, L);
+  const u32 P = kvar_pack_extent(s);
+  u32 dq[3] = {H, 1, hd}, dk[3] = {H, P, hd};
+  Tensor Q = ref_tensor_dt(3, dq, dt, q), K = ref_tensor_dt(3, dk, dt, k), V = ref_tensor_dt(3, dk, dt, v);
+  u32 hph[3] = {H, P, hd}, hp[2] = {H, P}, h1[2] = {H, 1}, hp1[3] = {H, P, 1};
+  union { f32 f; u32 b; } cs = {.f = scale * 1.4426950408889634f};
+  Term qe = uop_expand(Q.t, 3, hph);
+  Term sc = uop_reduce(REDUCE_SUM, 2, uop_binary(UOP_MUL, qe, K.t));                  /* {H,P} */
+  sc = uop_binary(UOP_MUL, sc, uop_expand(uop_const(dt, cs.b), 2, hp));
+  Term mx = uop_expand(uop_reshape(uop_reduce(REDUCE_MAX, 1, sc), 2, h1), 2, hp);
+  Term e = uop_unary(UOP_EXP2, uop_binary(UOP_ADD, sc, uop_unary(UOP_NEG, mx)));
+  Term den = uop_expand(uop_reshape(uop_reduce(REDUCE_SUM, 1, e), 2, h1), 2, hp);
+  Term w = uop_binary(UOP_MUL, e, uop_unary(UOP_RECIP, den));
+  Term we = uop_expand(uop_reshape(w, 3, hp1), 3, hph);
+  Term o = uop_reduce(REDUCE_SUM, 1, uop_binary(UOP_MUL, we, V.t));                   /* {H,hd} */
+  Tensor y;
+  y.t = o;
+  y.dtype = dt;
+  return ref_read_dt(y, out, (u64)H * hd);
 }

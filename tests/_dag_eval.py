@@ -9,10 +9,17 @@ value is an array over the axes it depends on (one array dimension per
 axis, size 1 where it does not); REDUCE sums or maxes its axes away;
 INDEX_E reads its buffer at the index (0 outside); STORE writes the value at
 the index for every point of the parallel axes.  Float nodes round to
-float32 after each operation; integers are int64 with C division."""
+float32 after each operation, whatever their type, and a CAST into fp16 or
+bf16 narrows to that type (through f32, round to nearest even), as does the
+STORE into an fp16 / bf16 buffer: the reference CPU path's semantics
+(src/backend/cpu/uop_walk.c:272-293, the walker that realizes non-f32
+kernels).  Integers are int64 with C division.  A RANGE whose src0 is a
+DEFINE_VAR row (a symbolic extent) runs to the variable's bound value
+(`vars[arg0]`); only the outputs its points write are defined."""
 import numpy as np
 
 CONST, ADD, MUL, NEG, RECIP, EXP2, LOG2, SQRT, CMPLT, REDUCE = 2, 9, 10, 11, 12, 13, 14, 15, 16, 17
+DEFINE_VAR = 18
 CMPEQ, LOAD, CAST, BITCAST, RANGE, INDEX_E = 20, 21, 23, 24, 25, 26
 IADD, ISUB, IMUL, IDIV, IMOD, ILT, IAND, IWHERE, BUFFER, STORE = 27, 28, 29, 30, 31, 32, 33, 34, 36, 37
 IOR, IXOR, ISHL, ISHR, SIN = 41, 42, 44, 51, 55
@@ -28,22 +35,45 @@ def _bf16_to_f32(u16):
     return (u16.astype(np.uint32) << 16).view(np.float32)
 
 
+def narrow(x, dt):
+    """x (float64 values) stored in float dtype dt and read back: f32 first,
+    then fp16 / bf16 round to nearest even (NaN kept)."""
+    f = np.asarray(x, np.float64).astype(np.float32)
+    if dt == 11:
+        return f.astype(np.float16).astype(np.float64)
+    if dt == 12:
+        u = f.view(np.uint32).astype(np.uint64)
+        r = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint32) << 16
+        r = np.where(np.isnan(f), f.view(np.uint32) | 0x00400000, r).astype(np.uint32)
+        return r.view(np.float32).astype(np.float64)
+    return f.astype(np.float64)
+
+
 def decode_slot(raw: np.ndarray, dt: int) -> np.ndarray:
     if dt == 12:
         return _bf16_to_f32(raw.view(np.uint16))
     return raw.view(NP_OF[dt]).astype(np.float64 if _isf(dt) else np.int64)
 
 
-def evaluate(rows: np.ndarray, slots: dict) -> np.ndarray:
+def evaluate(rows: np.ndarray, slots: dict, vars=(), written=False, narrow_every_op=False):
     """rows [n, 10] int64; slots {slot: decoded 1-D array} for the inputs;
-    returns the output buffer (slot 0) as float64 / int64, sized by the
-    BUFFER row's element count."""
+    vars: the bound values of the DEFINE_VAR rows' variables.  Returns the
+    output buffer (slot 0) as float64 / int64, sized by the BUFFER row's
+    element count, narrowed to its dtype -- and with written=True also the
+    mask of the elements the STORE wrote.  narrow_every_op: the other
+    semantics, every fp16 / bf16 op's value narrowed to its type (a
+    contrast for the tests, not the reference's)."""
     n = len(rows)
     ranges = {}                            # node -> (axis id, extent)
     red_axes = set()
     for i, r in enumerate(rows):
         if r[0] == RANGE:
-            ranges[i] = (int(r[6]), int(r[8]))
+            ext = int(r[8])
+            if r[2] >= 0:                  # symbolic: the variable's bound value
+                vr = rows[int(r[2])]
+                assert vr[0] == DEFINE_VAR, f"row {i}: extent expression op {vr[0]}"
+                ext = int(vars[int(vr[6])])
+            ranges[i] = (int(r[6]), ext)
         if r[0] == REDUCE:
             for k in (3, 4, 5):
                 if r[k] >= 0:
@@ -58,7 +88,9 @@ def evaluate(rows: np.ndarray, slots: dict) -> np.ndarray:
         s[dim[node]] = ranges[node][1]
         return s
 
-    def f32(x):
+    def f32(x, dt=13):
+        if narrow_every_op and dt in (11, 12):
+            return narrow(x, dt)
         return np.asarray(x, np.float64).astype(np.float32).astype(np.float64)
 
     def ev(i):
@@ -75,6 +107,8 @@ def evaluate(rows: np.ndarray, slots: dict) -> np.ndarray:
             out = np.full([1] * nd, v)
         elif op == RANGE:
             out = np.arange(ranges[i][1], dtype=np.int64).reshape(shape_for(i))
+        elif op == DEFINE_VAR:
+            out = np.full([1] * nd, np.int64(vars[a[0]]))
         elif op == BUFFER:
             out = None
         elif op == INDEX_E:
@@ -90,7 +124,7 @@ def evaluate(rows: np.ndarray, slots: dict) -> np.ndarray:
             x = np.broadcast_to(x, np.broadcast_shapes(np.shape(x), tuple(
                 ranges[node][1] if d in axes else 1 for d, node in enumerate(order))))
             out = x.sum(axis=axes, keepdims=True) if a[0] == 0 else x.max(axis=axes, keepdims=True)
-            out = f32(out) if fl else out
+            out = f32(out, dt) if fl else out
         elif op in (ADD, MUL, IADD, ISUB, IMUL, IAND, IOR, IXOR, ISHL, ISHR, IDIV, IMOD):
             x, y = ev(s[0]), ev(s[1])
             if op in (ADD, IADD):
@@ -113,12 +147,12 @@ def evaluate(rows: np.ndarray, slots: dict) -> np.ndarray:
                 out = np.trunc(x / y).astype(np.int64)
             else:
                 out = np.fmod(x, y).astype(np.int64)
-            out = f32(out) if fl else out
+            out = f32(out, dt) if fl else out
         elif op in (NEG, RECIP, EXP2, LOG2, SQRT, SIN):
             x = ev(s[0])
             out = {NEG: lambda v: -v, RECIP: lambda v: 1.0 / v, EXP2: np.exp2, LOG2: np.log2,
                    SQRT: np.sqrt, SIN: np.sin}[op](x)
-            out = f32(out) if fl else out
+            out = f32(out, dt) if fl else out
         elif op in (CMPLT, ILT, CMPEQ):
             x, y = ev(s[0]), ev(s[1])
             out = ((x == y) if op == CMPEQ else (x < y)).astype(np.float64 if fl else np.int64)
@@ -127,7 +161,7 @@ def evaluate(rows: np.ndarray, slots: dict) -> np.ndarray:
             out = np.where(c != 0, x, y)
         elif op == CAST:
             x = ev(s[0])
-            out = f32(x) if fl else np.trunc(x).astype(np.int64)
+            out = narrow(x, dt) if fl else np.trunc(x).astype(np.int64)
         else:
             raise NotImplementedError(f"row {i}: op {op}")
         val[i] = out
@@ -145,4 +179,11 @@ def evaluate(rows: np.ndarray, slots: dict) -> np.ndarray:
     out = np.zeros(out_rows, np.float64)
     ok = (addr >= 0) & (addr < out_rows)
     out[addr[ok]] = v[ok]
+    odt = int(rows[int(root[2])][1])
+    if _isf(odt):
+        out = narrow(out, odt)
+    if written:
+        mask = np.zeros(out_rows, bool)
+        mask[addr[ok]] = True
+        return out, mask
     return out

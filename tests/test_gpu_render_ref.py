@@ -145,3 +145,71 @@ def test_autotune_matvec(hip, rows, cols):
     assert best <= base
     for b in (out, xb, wb):
         b.free()
+
+
+# ---- fp16 / bf16 and symbolic-extent reference kernels ---------------------
+from test_render_narrow import GN, NAMES_N, close_storage  # noqa: E402
+
+
+def run_narrow(hip, k, opts=None, tag=""):
+    """Render kernel k of the narrow fixture and run it; a symbolic kernel
+    gets its bound variable values in an int32 buffer after the slots."""
+    nodes = [(int(r[0]), int(r[1]), tuple(int(x) for x in r[2:6]), tuple(int(x) for x in r[6:10]))
+             for r in GN[f"k{k}_rows"]]
+    name = f"refn_k{k}{tag}"
+    src, info = hip.render_kernel(nodes, name, opts=opts)
+    dts = [int(d) for d in GN[f"k{k}_dt"]]
+    bufs = [hip.Buffer(max(16, GN[f"k{k}_slot0"].nbytes))]
+    for s in range(1, len(dts)):
+        raw = GN[f"k{k}_slot{s}"]
+        b = hip.Buffer(max(16, raw.nbytes))
+        if raw.nbytes:
+            b.write(raw)
+        bufs.append(b)
+    if f"k{k}_vars" in GN.files:
+        bufs.append(hip.Buffer.from_numpy(GN[f"k{k}_vars"][:, 0].astype(np.int32)))
+    hip.dispatch(name, src, bufs, grid=(int(info.grid_max), 1, 1), block=(int(info.block), 1, 1))
+    got = E.decode_slot(bufs[0].read(np.uint8)[:GN[f"k{k}_slot0"].nbytes], dts[0])
+    for b in bufs:
+        b.free()
+    return got, info, dts
+
+
+def _narrow_check(k, got, dts, what):
+    want = E.decode_slot(GN[f"k{k}_slot0"], dts[0])
+    vars_ = [int(v[0]) for v in GN[f"k{k}_vars"]] if f"k{k}_vars" in GN.files else []
+    rows = GN[f"k{k}_rows"]
+    slots = {s: E.decode_slot(GN[f"k{k}_slot{s}"], dts[s]) for s in range(1, len(dts))}
+    _, mask = E.evaluate(rows, slots, vars_, written=True)     # the addresses the kernel writes
+    if dts[0] == 13:
+        assert close(got[mask], want[mask]), f"{NAMES_N[k]} {what}"
+        return 1.0
+    ok, exact = close_storage(got[mask], want[mask], dts[0])
+    assert ok, f"{NAMES_N[k]} {what}: exact fraction {exact}"
+    return exact
+
+
+@pytest.mark.parametrize("k", range(len(NAMES_N)), ids=NAMES_N)
+def test_narrow_reference_kernel_renders_and_matches(hip, k):
+    """fp16 / bf16 kernels within one storage rounding of the reference's
+    walker output (f32 arithmetic, narrowing at CAST / STORE); symbolic
+    kernels at the reference's bound length, on the rows it wrote."""
+    say(f"case: narrow/symbolic reference kernel {NAMES_N[k]}")
+    got, info, dts = run_narrow(hip, k)
+    ex = _narrow_check(k, got, dts, "hand-coded geometry")
+    say(f"  {NAMES_N[k]}: exact {ex:.4f}")
+
+
+@pytest.mark.parametrize("k", range(len(NAMES_N)), ids=NAMES_N)
+def test_narrow_reference_kernel_under_opts(hip, k):
+    say(f"case: narrow/symbolic reference kernel {NAMES_N[k]} opts")
+    variants = [(64, 1, 1), (256, 1, 4)]
+    if any(int(r[0]) == 17 for r in GN[f"k{k}_rows"]):
+        variants += [(256, 16, 1), (1024, 256, 1)]
+    for i, o in enumerate(variants):
+        try:
+            got, info, dts = run_narrow(hip, k, opts=o, tag=f"_o{i}")
+        except hip.ThvmHipError as e:
+            assert "group" in str(e), (o, str(e))
+            continue
+        _narrow_check(k, got, dts, f"opts {o}")

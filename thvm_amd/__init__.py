@@ -22,6 +22,14 @@ import numpy as np
 _PKG = Path(__file__).resolve().parent
 LIB_PATH = _PKG / "lib" / "libthvm_hip.so"
 
+
+def _lib_path() -> Path:
+    """The library lib() loads: the product build, or with
+    THVM_HIP_LIB_VARIANT=pclk (read at the first load) the measurement build
+    whose kernels carry phase-clock marks."""
+    v = os.environ.get("THVM_HIP_LIB_VARIANT")
+    return LIB_PATH.with_name(f"libthvm_hip_{v}.so") if v else LIB_PATH
+
 # dtype ids (reference src/thvm.h:254-271)
 DT = dict(bool=0, int8=1, uint8=2, int16=3, uint16=4, int32=5, uint32=6, int64=7, uint64=8,
           fp8e4m3=9, fp8e5m2=10, fp16=11, bf16=12, fp32=13, fp64=14)
@@ -136,6 +144,7 @@ _SIGS = {
     "thvm_hip_decoder_stage_clock": (C.c_int, [_u32, C.c_void_p, _u32]),
     "thvm_hip_decoder_op_tags": (C.c_int, [_u32, C.c_void_p, _u32]),
     "thvm_hip_decoder_run_ops": (_i32, [_u32, _u32, _u32]),
+    "thvm_hip_decoder_op_info": (_i32, [_u32, _u32, _cp, _u32, _cp, _u32, _vp, _u32]),
 }
 
 _LIB = None
@@ -146,9 +155,10 @@ def lib() -> C.CDLL:
     library has not been built: there is no fallback path."""
     global _LIB
     if _LIB is None:
-        if not LIB_PATH.exists():
-            raise ThvmHipError(f"{LIB_PATH} not built: run `python -m thvm_amd.build`")
-        L = C.CDLL(str(LIB_PATH))
+        path = _lib_path()
+        if not path.exists():
+            raise ThvmHipError(f"{path} not built: run `python -m thvm_amd.build`")
+        L = C.CDLL(str(path))
         for name, (res, args) in _SIGS.items():
             f = getattr(L, name)
             f.restype = res
@@ -403,6 +413,15 @@ class Decoder:
         if lib().thvm_hip_decoder_op_tags(self.h, out.ctypes.data, n) < 0:
             raise ThvmHipError(f"op_tags: {last_error()}")
         return out
+
+    def op_info(self, i: int):
+        """(name, program, buffer ids) of dispatch i of the step."""
+        name, prog = C.create_string_buffer(64), C.create_string_buffer(1024)
+        ids = np.zeros(32, np.uint32)
+        n = lib().thvm_hip_decoder_op_info(self.h, i, name, 64, prog, 1024, ids.ctypes.data, 32)
+        if n < 0:
+            raise ThvmHipError(f"op_info: {last_error()}")
+        return name.value.decode(), prog.value.decode(), [int(v) for v in ids[:n]]
 
     def run_ops(self, first: int, count: int) -> None:
         """Dispatch ops [first, first + count) of the step eagerly."""

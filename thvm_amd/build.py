@@ -55,7 +55,22 @@ def _stale(src: Path, obj: Path, headers_mtime: float) -> bool:
     return src.stat().st_mtime > t or headers_mtime > t
 
 
-def build(verbose: bool = True, incremental: bool = False) -> Path:
+VARIANTS = {
+    # the measurement build: kernels with the phase-clock marks compiled in
+    # (bench.py --phase-clock loads it); the product library has none
+    "pclk": ("_build_pclk", "libthvm_hip_pclk.so", ["-DTHVM_PCLK"]),
+}
+
+
+def build(verbose: bool = True, incremental: bool = False, variant: str | None = None) -> Path:
+    obj_dir, lib, hipflags = OBJ, LIB, HIPFLAGS
+    if variant:
+        d, name, extra = VARIANTS[variant]
+        obj_dir, lib, hipflags = PKG / d, PKG / "lib" / name, HIPFLAGS + extra
+    return _build(obj_dir, lib, hipflags, verbose, incremental)
+
+
+def _build(OBJ: Path, LIB: Path, HIPFLAGS: list, verbose: bool, incremental: bool) -> Path:
     OBJ.mkdir(exist_ok=True)
     LIB.parent.mkdir(exist_ok=True)
     hdr = max(p.stat().st_mtime for d in (CSRC, ROOT / "include") for p in d.rglob("*.h"))
@@ -85,4 +100,5 @@ def build(verbose: bool = True, incremental: bool = False) -> Path:
 
 
 if __name__ == "__main__":
-    build(incremental="--incremental" in sys.argv[1:])
+    v = sys.argv[sys.argv.index("--variant") + 1] if "--variant" in sys.argv else None
+    build(incremental="--incremental" in sys.argv[1:], variant=v)

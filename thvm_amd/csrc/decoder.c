@@ -1401,6 +1401,18 @@ THVM_API int thvm_hip_decoder_op_tags(uint32_t h, int32_t *tags, uint32_t n) {
   return (int)d->n_ops;
 }
 
+THVM_API int thvm_hip_decoder_op_info(uint32_t h, uint32_t i, char *name, uint32_t name_cap,
+                                      char *prog, uint32_t prog_cap, uint32_t *ids, uint32_t ids_cap) {
+  Decoder *d = dec_get(h);
+  if (!d) return -1;
+  if (i >= d->n_ops) { hb_set_error("decoder_op_info: op %u of %u", i, d->n_ops); return -1; }
+  const DOp *o = &d->ops[i];
+  if (name && name_cap) snprintf(name, name_cap, "%s", o->name);
+  if (prog && prog_cap) snprintf(prog, prog_cap, "%s", o->prog);
+  for (u32 k = 0; ids && k < o->n_args && k < ids_cap; k++) ids[k] = o->args[k];
+  return (int)o->n_args;
+}
+
 THVM_API int thvm_hip_decoder_run_ops(uint32_t h, uint32_t first, uint32_t count) {
   Decoder *d = dec_get(h);
   if (!d) return -1;

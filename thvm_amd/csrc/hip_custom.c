@@ -153,7 +153,7 @@ static int attn_parse(const Spec *sp, ArgCtx *c, ThvmAttnArgs *a, int with_part)
       spec_u32(sp, "qt", &a->qdt, 0, THVM_DT_BF16) || spec_u32(sp, "ct", &a->cdt, 0, THVM_DT_BF16) ||
       spec_u32(sp, "ot", &a->odt, 0, THVM_DT_BF16) || spec_f32(sp, "scale", &a->scale, 1, 0) ||
       spec_u32(sp, "fused", &a->fused, 0, 0) || spec_u32(sp, "cpb", &a->cpb, 0, 0) ||
-      spec_u32(sp, "spec", &a->spec, 0, 0))
+      spec_u32(sp, "spec", &a->spec, 0, 0) || spec_u32(sp, "clk", &a->clk_cap, 0, 0))
     return -1;
   if (a->chunk == 0) { hb_set_error("builtin attn: chunk=0"); return -1; }
   if (spec_u32(sp, "nsplit", &a->n_split, 0, (a->max_seq + a->chunk - 1) / a->chunk)) return -1;
@@ -166,6 +166,9 @@ static int attn_parse(const Spec *sp, ArgCtx *c, ThvmAttnArgs *a, int with_part)
   a->len = (const int32_t *)arg(c, 4, 4);
   if (with_part)
     a->part = (float *)arg(c, 5, thvm_k_attn_part_bytes(a->B, a->H, a->Hkv, a->hd, a->n_split));
+  /* clk=<blocks>: a phase-clock buffer after the others (split blocks, then
+   * merge blocks: 2 x blocks x 10 u64) */
+  if (with_part && a->clk_cap) a->clk = (uint64_t *)arg(c, 6, (u64)a->clk_cap * 2 * 80);
   return c->bad ? -1 : 0;
 }
 
@@ -197,7 +200,7 @@ int hb_builtin_launch(const char *program, const u32 *ids, u32 n, int check_only
          spec_u32(&sp, "waves", &a.tune_waves, 0, 0) || spec_u32(&sp, "r", &a.tune_r, 0, 0) ||
          spec_u32(&sp, "u", &a.tune_u, 0, 0) || spec_u32(&sp, "blocks", &a.tune_blocks, 0, 0) ||
          spec_u32(&sp, "path", &a.tune_path, 0, 0) || spec_u32(&sp, "spec", &a.spec, 0, 0) ||
-         spec_u32(&sp, "tiled", &a.wtiled, 0, 0));
+         spec_u32(&sp, "tiled", &a.wtiled, 0, 0) || spec_u32(&sp, "clk", &a.clk_cap, 0, 0));
     {
       u32 ldy0 = a.epi == THVM_EPI_SWIGLU ? a.N / 2
                : (a.epi == THVM_EPI_QKV || a.epi == THVM_EPI_QKV_ROPE) ? a.n_heads * a.head_dim
@@ -232,6 +235,8 @@ int hb_builtin_launch(const char *program, const u32 *ids, u32 n, int check_only
       a.kcache = arg(&c, slot++, cb);
       a.vcache = arg(&c, slot++, cb);
     }
+    /* clk=<blocks>: a phase-clock buffer after the others (blocks x 10 u64) */
+    if (a.clk_cap) a.clk = (uint64_t *)arg(&c, slot++, (u64)a.clk_cap * 80);
     if (c.bad) return -1;
     bytes = (u64)a.N * a.K * wsz + (a.scale ? (u64)a.N * 4 : 0) + (u64)a.M * a.K * xsz +
             (u64)a.M * ncols_out * ysz * (a.res ? 2 : 1);

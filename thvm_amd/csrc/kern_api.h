@@ -70,6 +70,11 @@ typedef struct ThvmGemvArgs {
   /* MFMA path only: W is in the MFMA tile layout of thvm_k_tile_w (rows
    * padded to a multiple of 16 with zeros) instead of row-major */
   uint32_t wtiled;
+  /* phase clock (measurement only; NULL = off): per block 10 u64 slots (8
+   * marks of the 100 MHz wall clock, the XCD, the hardware id), for the
+   * first clk_cap blocks */
+  uint64_t *clk;
+  uint32_t clk_cap;
 } ThvmGemvArgs;
 /* W [N, K] (row-major, element size es 1 or 2) -> the MFMA tile layout for
  * lanes reading lb bytes of a row per k step (lb 16 or 32, 0 = 16 es; a step
@@ -132,6 +137,8 @@ typedef struct ThvmAttnArgs {
   uint32_t spec;           /* speculative verify: the B query rows are
                             * consecutive positions of one sequence; row b
                             * reads cache row 0 over L+b rows (causal)     */
+  uint64_t *clk;           /* phase clock (measurement only; NULL = off)   */
+  uint32_t clk_cap;        /* blocks recorded per launch (split, then merge) */
 } ThvmAttnArgs;
 int thvm_k_attn_decode(const ThvmAttnArgs *a, hipStream_t s, char *err, int errlen);
 /* the chunks per split block thvm_k_attn_decode picks for cpb = 0 */

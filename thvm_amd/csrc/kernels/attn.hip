@@ -49,7 +49,11 @@ template <int HD, int G, int AT>
 __global__ __launch_bounds__(MERGE_THREADS) void k_attn_merge(ThvmAttnArgs a) {
   __shared__ MergeFlatLds<HD, G> s;
   const uint32_t b = blockIdx.x / a.Hkv, kvh = blockIdx.x % a.Hkv;
+  // phase clock: the merge's blocks follow the split's in the clock buffer
+  uint64_t *const clk = a.clk ? a.clk + (uint64_t)a.clk_cap * PCLK_MARKS : nullptr;
+  pclk(clk, a.clk_cap, 0);
   attn_merge_flat<HD, G, AT, false>(a, b, kvh, attn_live(a, attn_row_len(a, b)), threadIdx.x, true, s);
+  pclk_end(clk, a.clk_cap);
 }
 
 // The one-launch forms' hand-off: publish this block's partial (written
@@ -117,6 +121,10 @@ __global__ __launch_bounds__(ATT_THREADS, 4) void k_attn_multi(ThvmAttnArgs a) {
   const int32_t L = attn_row_len(a, b);
   const uint32_t cpb = a.cpb, c0 = grp * cpb;
   if ((int32_t)(c0 * ATT_CHUNK) >= L) return;      // the merge reads only live partials
+  // phase clock: 0 entry, 1 first chunk's loads issued and q decoded, 2 first
+  // chunk consumed, 3 chunks done, 4 row groups combined, 5 wave maxima in
+  // LDS, 6 wave accumulators in LDS, 7 partial stored (drained)
+  pclk(a.clk, a.clk_cap, 0);
   const int tid = threadIdx.x, wv = tid >> 6, lane = lane_id();
   const int rg = lane / LPR, li = lane % LPR;
   const uint32_t d0 = li * EPL;
@@ -149,6 +157,7 @@ __global__ __launch_bounds__(ATT_THREADS, 4) void k_attn_multi(ThvmAttnArgs a) {
 #pragma unroll
     for (int i = 0; i < EPL; i++) qf[g][i] *= qs;
   }
+  pclk(a.clk, a.clk_cap, 1);
   float m[G], l[G], acc[G][EPL];
 #pragma unroll
   for (int g = 0; g < G; g++) {
@@ -201,10 +210,12 @@ __global__ __launch_bounds__(ATT_THREADS, 4) void k_attn_multi(ThvmAttnArgs a) {
   for (uint32_t c = 0; c < nc; c += 2) {               // two register sets, ping-pong
     issue(1, c0 + c + 1);
     consume(0);
+    if (c == 0) pclk(a.clk, a.clk_cap, 2);
     if (c + 1 >= nc) break;
     issue(0, c0 + c + 2);
     consume(1);
   }
+  pclk(a.clk, a.clk_cap, 3);
   // row groups of the wave -> one (m, l, acc) per head: rescale to the wave
   // max, then sum (all lanes)
   float mw[G];
@@ -225,12 +236,14 @@ __global__ __launch_bounds__(ATT_THREADS, 4) void k_attn_multi(ThvmAttnArgs a) {
     }
     mw[g] = M;
   }
+  pclk(a.clk, a.clk_cap, 4);
   // waves -> the block's partial, as the one-chunk unit does
   if (lane == 0) {
 #pragma unroll
     for (int g = 0; g < G; g++) { s.wm[wv][g] = mw[g]; s.wl[wv][g] = l[g]; }
   }
   __syncthreads();
+  pclk(a.clk, a.clk_cap, 5);
   {
     float f[G];
 #pragma unroll
@@ -249,6 +262,7 @@ __global__ __launch_bounds__(ATT_THREADS, 4) void k_attn_multi(ThvmAttnArgs a) {
     }
   }
   __syncthreads();
+  pclk(a.clk, a.clk_cap, 6);
   for (int o = tid; o < G * HD; o += ATT_THREADS) {
     const int g = o / HD, d = o % HD;
     float sv = 0.0f, lt = 0.0f, M = s.wm[0][g];
@@ -269,6 +283,7 @@ __global__ __launch_bounds__(ATT_THREADS, 4) void k_attn_multi(ThvmAttnArgs a) {
     }
   }
   if (FUSE) attn_handoff_merge<HD, G, AT>(a, b, kvh, attn_live(a, L), &last, ms);
+  pclk_end(a.clk, a.clk_cap);
 }
 
 typedef void (*attn_fn)(ThvmAttnArgs);

@@ -201,3 +201,44 @@ __device__ __forceinline__ float gelu_tanh_f(float x) {
   float u = 0.7978845608f * (x + 0.044715f * x * x * x);
   return 0.5f * x * (1.0f + tanhf(u));
 }
+
+// ---- phase clock (measurement build only) -----------------------------------
+// Compiled in only with -DTHVM_PCLK (the library variant libthvm_hip_pclk.so,
+// `python -m thvm_amd.build --variant pclk`): the marks constrain the
+// compiler's scheduling and cost ~2% of a decode step even when off, so the
+// product library has none.  There, with clk set (a kernel argument, so the
+// test is uniform), thread 0 of each of the first cap blocks stores the 100
+// MHz wall clock (s_memrealtime) at mark i (0..7) of its PCLK_MARKS slots;
+// mark 0 also records the block's XCD (slot 8, HW_REG_XCC_ID) and hardware
+// id word (slot 9, HW_REG_HW_ID: SE, CU, SIMD), so launch order across the
+// XCDs shows.  pclk_end first drains the block's memory operations and waits
+// for every wave.
+#define PCLK_MARKS 10
+__device__ __forceinline__ void pclk(uint64_t *clk, uint32_t cap, int i) {
+#ifndef THVM_PCLK
+  (void)clk; (void)cap; (void)i;
+  return;
+#endif
+  if (clk == nullptr || threadIdx.x != 0) return;
+  const uint32_t blk = blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z);
+  if (blk >= cap) return;
+  uint64_t *p = clk + (uint64_t)blk * PCLK_MARKS;
+  p[i] = __builtin_amdgcn_s_memrealtime();
+  if (i == 0) {
+    uint32_t xcc, hw;
+    asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(xcc));
+    asm volatile("s_getreg_b32 %0, hwreg(HW_REG_HW_ID)" : "=s"(hw));
+    p[8] = xcc;
+    p[9] = hw;
+  }
+}
+__device__ __forceinline__ void pclk_end(uint64_t *clk, uint32_t cap) {
+#ifndef THVM_PCLK
+  (void)clk; (void)cap;
+  return;
+#endif
+  if (clk == nullptr) return;
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  pclk(clk, cap, 7);
+}

@@ -294,11 +294,16 @@ __device__ __forceinline__ bool gemv_core(const ThvmGemvArgs &a, unsigned char *
   // (in a persistent kernel, wave 0 polls the grid barrier inside wait():
   // its own loads are issued after the wait, so the poll does not queue
   // behind them)
+  // phase clock (standalone kernel only): 0 entry, 1 first loads issued,
+  // 2 x staged, 3 first weight batch consumed, 4 wave 0's rows done
+  uint64_t *const clk = COH ? nullptr : a.clk;
+  pclk(clk, a.clk_cap, 0);
   const bool early = !COH || (threadIdx.x >> 6) != 0;
   if (early) load_batch(g, 0);
   if (!wait()) return false;
   if (!early) load_batch(g, 0);
   if (!XPRE) load_gains();
+  pclk(clk, a.clk_cap, 1);
 
   // ---- 2. stage x into LDS (16-byte loads), with the fused norm if asked ----
   for (int m = 0; m < M; m++) {
@@ -377,6 +382,7 @@ __device__ __forceinline__ bool gemv_core(const ThvmGemvArgs &a, unsigned char *
     }
   }
   __syncthreads();
+  pclk(clk, a.clk_cap, 2);
 
   // ---- 3. stream the weight rows ----
   // A flat sequence of (row group, chunk batch) steps per wave; two register
@@ -505,9 +511,11 @@ __device__ __forceinline__ bool gemv_core(const ThvmGemvArgs &a, unsigned char *
   for (uint32_t t = 0; t < T; t += 2) {          // step 0 is already in wq
     if (t + 1 < T) load_step(wq2, t + 1);
     consume(wq, t);
+    if (t == 0) pclk(clk, a.clk_cap, 3);
     if (t + 1 >= T) break;
     if (t + 2 < T) load_step(wq, t + 2);
     consume(wq2, t + 1);
   }
+  pclk(clk, a.clk_cap, 4);
   return true;
 }

@@ -11,8 +11,11 @@
  * gfx950 choices:
  *   - values are SSA locals emitted once per scope; a node that does not read
  *     a reduce loop's axes is hoisted out of that loop;
- *   - fp16 / bf16 values compute in f32 and round to their storage type after
- *     every op (the storage precision of each intermediate);
+ *   - fp16 / bf16 values compute in f32 and narrow to their storage type only
+ *     at a CAST into that type and at the STORE -- the reference CPU path's
+ *     semantics for narrow floats (its uop walker rounds each op to f32 and
+ *     narrows at CAST / STORE, src/backend/cpu/uop_walk.c:272-293), pinned by
+ *     kernels of fp16 and bf16 graphs captured from the compiled reference;
  *   - geometry (ThvmRenderOpts, the reference's LOCAL / GROUP_REDUCE /
  *     UPCAST opts): `group` consecutive threads share one output's
  *     reductions (strided partial terms, a xor-shuffle tree inside a wave, the
@@ -317,7 +320,10 @@ static int emit(R *r, int i) {
   for (int k = 0; k < 4; k++)
     if (u->src[k] >= i) { snprintf(r->err, sizeof r->err, "node %d: source %d is not earlier", i, u->src[k]); return -1; }
   const char *at = alu_t(u->dtype);
-  const char *rf = round_fn(u->dtype);
+  /* fp16 / bf16 values narrow only where the reference's CPU path narrows
+   * them (src/backend/cpu/uop_walk.c:272-293, :725-737): at a CAST into the
+   * type and at the STORE; every other op keeps its f32 value */
+  const char *rf = u->op == U_CAST ? round_fn(u->dtype) : "";
   int rc = 0;
   switch (u->op) {
     case U_CONST: emit_const(r, i); break;
