@@ -630,7 +630,7 @@ PHASES = {
     "gemv": ["entry", "loads issued", "x staged", "first batch consumed", "rows done", "", "",
              "end (drained)"],
     "attn": ["entry", "loads issued + q", "first chunk consumed", "chunks done", "row groups combined",
-             "wave maxima in LDS", "wave partials in LDS", "end (drained)"],
+             "waves in LDS", "", "end (drained)"],
     "merge": ["entry", "", "", "", "", "", "", "end (drained)"],
 }
 

@@ -134,26 +134,39 @@ __global__ __launch_bounds__(ATT_THREADS, 4) void k_attn_multi(ThvmAttnArgs a) {
   const uint64_t cbase = ((uint64_t)attn_cache_row(a, b) * a.Hkv + kvh) * a.max_seq * HD * ES;
   const buf_t krs = buf_rsrc((const char *)a.kcache + cbase, a.max_seq * HD * ES);
   const buf_t vrs = buf_rsrc((const char *)a.vcache + cbase, a.max_seq * HD * ES);
+  // the block's chunks c0 .. c0+nc-1; the ping-pong below issues one chunk
+  // ahead unconditionally, and a row at or past jend takes the no-access
+  // offset (past the block's last chunk it would re-read the next block's)
+  const uint32_t nlive = (uint32_t)((L + ATT_CHUNK - 1) / ATT_CHUNK);
+  const uint32_t nc = min(cpb, nlive - c0);            // block-uniform
+  const int32_t jend = min(L, (int32_t)((c0 + nc) * ATT_CHUNK));
   uint4 kq[2][IT], vq[2][IT];
   bool ok[2][IT];
   auto issue = [&](int buf, uint32_t c) {
 #pragma unroll
     for (int it = 0; it < IT; it++) {
       const uint32_t j = c * ATT_CHUNK + wv * PPW + it * RPW + rg;
-      ok[buf][it] = (int32_t)j < L && j < a.max_seq;
+      ok[buf][it] = (int32_t)j < jend && j < a.max_seq;
       const uint32_t off = ok[buf][it] ? (j * HD + d0) * ES : BUF_OOB;
       kq[buf][it] = buf_ld_stream16(krs, off);
       vq[buf][it] = buf_ld_stream16(vrs, off);
     }
   };
+  // q's raw bytes requested ahead of the first chunk, so that decoding q waits
+  // for q alone and the second chunk is issued while the first is in flight
+  uint4 qraw[G];
+#pragma unroll
+  for (int g = 0; g < G; g++) {
+    const uint64_t qo = ((uint64_t)b * a.H + kvh * G + g) * HD + d0;
+    qraw[g] = ld16((const char *)a.q + qo * ES);
+  }
   issue(0, c0);
   // q, decoded and pre-scaled into the log2 domain once
   const float qs = a.scale * LOG2E;
   float qf[G][EPL];
 #pragma unroll
   for (int g = 0; g < G; g++) {
-    const uint64_t qo = ((uint64_t)b * a.H + kvh * G + g) * HD + d0;
-    chunk_f<AT>(ld16((const char *)a.q + qo * ES), qf[g]);
+    chunk_f<AT>(qraw[g], qf[g]);
 #pragma unroll
     for (int i = 0; i < EPL; i++) qf[g][i] *= qs;
   }
@@ -205,8 +218,6 @@ __global__ __launch_bounds__(ATT_THREADS, 4) void k_attn_multi(ThvmAttnArgs a) {
       }
     }
   };
-  const uint32_t nlive = (uint32_t)((L + ATT_CHUNK - 1) / ATT_CHUNK);
-  const uint32_t nc = min(cpb, nlive - c0);            // block-uniform
   for (uint32_t c = 0; c < nc; c += 2) {               // two register sets, ping-pong
     issue(1, c0 + c + 1);
     consume(0);
@@ -217,60 +228,57 @@ __global__ __launch_bounds__(ATT_THREADS, 4) void k_attn_multi(ThvmAttnArgs a) {
   }
   pclk(a.clk, a.clk_cap, 3);
   // row groups of the wave -> one (m, l, acc) per head: rescale to the wave
-  // max, then sum (all lanes)
+  // max, then sum (all lanes).  A row group is LPR lanes, so the groups of a
+  // wave meet across lanes LPR, 2 LPR, .. 32 apart: a butterfly in that order,
+  // 8 apart by a DPP row rotation, 16 and 32 apart by permlane swaps.
+  static_assert(LPR == 8 || LPR == 16 || LPR == 32, "row groups of 8, 16 or 32 lanes");
   float mw[G];
 #pragma unroll
   for (int g = 0; g < G; g++) {
     float M = m[g];
 #pragma unroll
-    for (int off = LPR; off < 64; off *= 2) M = fmaxf(M, __shfl_xor(M, off));
+    for (int off = LPR; off < 64; off *= 2) M = fmaxf(M, attn_xor(M, off));
     const float f = m[g] == -INFINITY ? 0.0f : fexp2(m[g] - M);
     l[g] *= f;
 #pragma unroll
     for (int i = 0; i < EPL; i++) acc[g][i] *= f;
 #pragma unroll
     for (int off = LPR; off < 64; off *= 2) {
-      l[g] += __shfl_xor(l[g], off);
+      l[g] += attn_xor(l[g], off);
 #pragma unroll
-      for (int i = 0; i < EPL; i++) acc[g][i] += __shfl_xor(acc[g][i], off);
+      for (int i = 0; i < EPL; i++) acc[g][i] += attn_xor(acc[g][i], off);
     }
     mw[g] = M;
   }
   pclk(a.clk, a.clk_cap, 4);
-  // waves -> the block's partial, as the one-chunk unit does
+  // waves -> the block's partial in one LDS round: each wave stores its (m, l)
+  // and its accumulator relative to its own max; each output thread rescales
+  // the 8 waves' terms to the block max and sums them in wave order (the same
+  // products and the same order as rescaling first, so the same values)
   if (lane == 0) {
 #pragma unroll
     for (int g = 0; g < G; g++) { s.wm[wv][g] = mw[g]; s.wl[wv][g] = l[g]; }
   }
-  __syncthreads();
-  pclk(a.clk, a.clk_cap, 5);
-  {
-    float f[G];
+  if (rg == 0) {
 #pragma unroll
-    for (int g = 0; g < G; g++) {
-      float M = s.wm[0][g];
+    for (int g = 0; g < G; g++)
 #pragma unroll
-      for (int w = 1; w < ATT_WAVES; w++) M = fmaxf(M, s.wm[w][g]);
-      f[g] = mw[g] == -INFINITY ? 0.0f : fexp2(mw[g] - M);
-      if (lane == 0) s.wf[wv][g] = f[g];
-    }
-    if (rg == 0) {
-#pragma unroll
-      for (int g = 0; g < G; g++)
-#pragma unroll
-        for (int i = 0; i < EPL; i++) s.wacc[wv][g][d0 + i] = acc[g][i] * f[g];
-    }
+      for (int i = 0; i < EPL; i++) s.wacc[wv][g][d0 + i] = acc[g][i];
   }
   __syncthreads();
-  pclk(a.clk, a.clk_cap, 6);
+  pclk(a.clk, a.clk_cap, 5);
   for (int o = tid; o < G * HD; o += ATT_THREADS) {
     const int g = o / HD, d = o % HD;
-    float sv = 0.0f, lt = 0.0f, M = s.wm[0][g];
+    float M = s.wm[0][g];
+#pragma unroll
+    for (int w = 1; w < ATT_WAVES; w++) M = fmaxf(M, s.wm[w][g]);
+    float sv = 0.0f, lt = 0.0f;
 #pragma unroll
     for (int w = 0; w < ATT_WAVES; w++) {
-      sv += s.wacc[w][g][d];
-      lt += s.wf[w][g] * s.wl[w][g];
-      M = fmaxf(M, s.wm[w][g]);
+      const float mwv = s.wm[w][g];
+      const float f = mwv == -INFINITY ? 0.0f : fexp2(mwv - M);
+      sv += s.wacc[w][g][d] * f;
+      lt += f * s.wl[w][g];
     }
     const uint64_t pi = (((uint64_t)b * a.H + kvh * G + g) * a.n_split + grp) * (HD + 2);
     if (FUSE) {

@@ -81,11 +81,19 @@ __device__ __forceinline__ float group_sum(float v) {
   v += dpp_f<0x4E>(v);
   v += dpp_f<0x141>(v);
   if (LPR >= 16) v += dpp_f<0x140>(v);
-  if (LPR == 32) v += __shfl_xor(v, 16);
+  if (LPR == 32) v += xor16_f(v);
   return v;
 }
 
 __device__ __forceinline__ float fexp2(float x) { return exp2f(x); }
+
+// v of lane (lane ^ off), off in {8, 16, 32} (a compile-time constant where
+// it is used): the row groups of a wave meet without an LDS round trip -- a
+// DPP row rotation by 8 (row_ror:8) or a permlane swap across 16 / 32 lanes
+// (a ds_bpermute shuffle costs one LDS round trip each)
+__device__ __forceinline__ float attn_xor(float v, int off) {
+  return off == 8 ? dpp_f<0x128>(v) : off == 16 ? xor16_f(v) : xor32_f(v);
+}
 
 // Query row b's cache length and cache row.  Plain decode: L = len[0] over
 // cache row b.  Speculative verify (a.spec): the B query rows are the
@@ -104,7 +112,7 @@ __device__ __forceinline__ uint32_t attn_cache_row(const ThvmAttnArgs &a, uint32
 // LDS of one split unit
 template <int HD, int G>
 struct AttnLds {
-  float wm[ATT_WAVES][G], wl[ATT_WAVES][G], wf[ATT_WAVES][G];
+  float wm[ATT_WAVES][G], wl[ATT_WAVES][G];
   __align__(16) float wacc[ATT_WAVES][G][HD];
 };
 
@@ -199,7 +207,7 @@ struct AttnSplit {
 #pragma unroll
         for (int it = 1; it < IT; it++) m = fmaxf(m, sc[it][g]);
 #pragma unroll
-        for (int off = LPR; off < 64; off *= 2) m = fmaxf(m, __shfl_xor(m, off));
+        for (int off = LPR; off < 64; off *= 2) m = fmaxf(m, attn_xor(m, off));
         mw[g] = m;
         lw[g] = 0.0f;
 #pragma unroll
@@ -222,45 +230,40 @@ struct AttnSplit {
       for (int g = 0; g < G; g++) {
 #pragma unroll
         for (int off = LPR; off < 64; off *= 2) {
-          lw[g] += __shfl_xor(lw[g], off);
+          lw[g] += attn_xor(lw[g], off);
 #pragma unroll
-          for (int i = 0; i < EPL; i++) acc[g][i] += __shfl_xor(acc[g][i], off);
+          for (int i = 0; i < EPL; i++) acc[g][i] += attn_xor(acc[g][i], off);
         }
       }
+      // each wave publishes its (m, l) and its accumulator relative to its
+      // own max; one barrier, then each output thread rescales the 8 waves'
+      // terms to the unit max and sums them in wave order (the products and
+      // the order of rescaling before publishing, so the same values)
       if (lane == 0) {
 #pragma unroll
         for (int g = 0; g < G; g++) { s.wm[wv][g] = mw[g]; s.wl[wv][g] = lw[g]; }
-      }
-    }
-    __syncthreads();
-    // rescale factor of this wave against the unit max, then publish acc
-    if (active) {
-      float f[G];
-#pragma unroll
-      for (int g = 0; g < G; g++) {
-        float M = s.wm[0][g];
-#pragma unroll
-        for (int w = 1; w < ATT_WAVES; w++) M = fmaxf(M, s.wm[w][g]);
-        f[g] = mw[g] == -INFINITY ? 0.0f : fexp2(mw[g] - M);
-        if (lane == 0) s.wf[wv][g] = f[g];
       }
       if (rg == 0) {
 #pragma unroll
         for (int g = 0; g < G; g++)
 #pragma unroll
-          for (int i = 0; i < EPL; i++) s.wacc[wv][g][d0 + i] = acc[g][i] * f[g];
+          for (int i = 0; i < EPL; i++) s.wacc[wv][g][d0 + i] = acc[g][i];
       }
     }
     __syncthreads();
     if (active) {
       for (int o = tid; o < G * HD; o += ATT_THREADS) {
         const int g = o / HD, d = o % HD;
-        float sv = 0.0f, l = 0.0f, M = s.wm[0][g];
+        float M = s.wm[0][g];
+#pragma unroll
+        for (int w = 1; w < ATT_WAVES; w++) M = fmaxf(M, s.wm[w][g]);
+        float sv = 0.0f, l = 0.0f;
 #pragma unroll
         for (int w = 0; w < ATT_WAVES; w++) {
-          sv += s.wacc[w][g][d];
-          l += s.wf[w][g] * s.wl[w][g];
-          M = fmaxf(M, s.wm[w][g]);
+          const float mwv = s.wm[w][g];
+          const float f = mwv == -INFINITY ? 0.0f : fexp2(mwv - M);
+          sv += s.wacc[w][g][d] * f;
+          l += f * s.wl[w][g];
         }
         const uint64_t pi = (((uint64_t)b * a.H + kvh * G + g) * a.n_split + split) * (HD + 2);
         if (COH) {

@@ -202,6 +202,21 @@ __device__ __forceinline__ float gelu_tanh_f(float x) {
   return 0.5f * x * (1.0f + tanhf(u));
 }
 
+// v of lane (lane ^ 16) / (lane ^ 32) with gfx950's v_permlane16_swap /
+// v_permlane32_swap (VALU: no LDS round trip as a ds_bpermute shuffle takes).
+// permlane32_swap(a, b) swaps lanes 32..63 of a with lanes 0..31 of b, so with
+// a = b = v the new a holds v[lane - 32] in its upper half and the new b
+// v[lane + 32] in its lower half; permlane16_swap does the same between the
+// odd 16-lane rows of a and the even rows of b.
+__device__ __forceinline__ float xor32_f(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float((threadIdx.x & 32u) ? r[0] : r[1]);
+}
+__device__ __forceinline__ float xor16_f(float v) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float((threadIdx.x & 16u) ? r[0] : r[1]);
+}
+
 // ---- phase clock (measurement build only) -----------------------------------
 // Compiled in only with -DTHVM_PCLK (the library variant libthvm_hip_pclk.so,
 // `python -m thvm_amd.build --variant pclk`): the marks constrain the
