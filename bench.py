@@ -627,11 +627,11 @@ def run_spec(thvm, args) -> dict:
 
 
 PHASES = {
-    "gemv": ["entry", "loads issued", "x staged", "first batch consumed", "rows done", "", "",
+    "gemv": ["entry", "loads issued", "x staged", "first batch consumed", "rows done", "partials summed", "",
              "end (drained)"],
     "attn": ["entry", "loads issued + q", "first chunk consumed", "chunks done", "row groups combined",
              "waves in LDS", "", "end (drained)"],
-    "merge": ["entry", "", "", "", "", "", "", "end (drained)"],
+    "merge": ["entry", "partials folded", "partitions combined", "", "", "", "", "end (drained)"],
 }
 
 

@@ -289,18 +289,59 @@ def test_gemm_mfma_fp8_operand_decode_all_patterns(hip, xdt):
     assert np.array_equal(got, want), f"{np.count_nonzero(got != want)} values differ"
 
 
-@pytest.mark.parametrize("nt", [1, 2, 4])
-@pytest.mark.parametrize("M", [16, 64])
+@pytest.mark.parametrize("nt", [1, 2, 4, 7, 8])
+@pytest.mark.parametrize("M", [5, 16, 64])
 def test_gemm_mfma_tile_counts_agree(hip, nt, M):
+    """Every tile count per block (N = 200: 13 tiles, so the last block is
+    partial at every count); 7 and 8 tiles take one x tile (M <= 16) and fp8
+    weights, and are refused above 16 rows."""
     N, K = 200, 2048
     say(f"case: gemm mfma nt={nt} M={M}")
     rng = np.random.default_rng(91 + M)
     xs, ws, scale, ref, floor = _gemv_case(hip, rng, DT_FP8, M, N, K)
     y = hip.Buffer(M * N * 4)
-    hip.builtin("gemv", [y, up(hip, xs), up(hip, ws), up(hip, scale)], m=M, n=N, k=K,
-                wt=DT_FP8, xt=DT_BF16, yt=DT_F32, epi=0, path=2, r=nt)
+    args = [y, up(hip, xs), up(hip, ws), up(hip, scale)]
+    kw = dict(m=M, n=N, k=K, wt=DT_FP8, xt=DT_BF16, yt=DT_F32, epi=0, path=2, r=nt)
+    if nt >= 7 and M > 16:
+        with pytest.raises(hip.ThvmHipError, match="tiles per block"):
+            hip.builtin("gemv", args, **kw)
+        return
+    hip.builtin("gemv", args, **kw)
     got = y.read(np.float32).reshape(M, N)
     assert np.all(np.abs(got - ref) <= 1e-5 * floor)
+
+
+@pytest.mark.parametrize("N", [20000, 40000])
+def test_gemm_mfma_wide_default_tiles_fused_norm(hip, N):
+    """Wide N at 16 rows picks 7 (N = 20000: 1250 tiles) or 8 (40000) tiles
+    per block by default, so the grid is one round of blocks per CU (or
+    whole rounds); with the fused RMSNorm, against the norm kernel's
+    semantics and the oracle GEMV as in the fused-norm test."""
+    M, K = 16, 512
+    say(f"case: gemm mfma wide default tiles N={N}")
+    rng = np.random.default_rng(8100 + N)
+    xs, xf = rand_store(rng, (M, K), DT_BF16, 3.0)
+    g = (1 + 0.2 * rng.standard_normal(K)).astype(np.float32)
+    xn = np.empty((M, K), np.uint16)
+    O.oracle().or_rmsnorm(xn.ctypes.data, DT_BF16, xs.ctypes.data, DT_BF16, g.ctypes.data, M, K, 1e-5)
+    xnf = O.decode(xn, DT_BF16)
+    wf32 = (rng.standard_normal((N, K)) * 0.02).astype(np.float32)
+    scale = (np.abs(wf32).max(1) / 448.0).astype(np.float32)
+    ws = O.encode(wf32 / scale[:, None], DT_FP8)
+    wdq = O.decode(ws, DT_FP8) * scale[:, None]
+    ref = O.gemv(xn, DT_BF16, ws, DT_FP8, scale, M=M, N=N, K=K)
+    floor = np.abs(xnf) @ np.abs(wdq).T
+    y = hip.Buffer(M * N * 4)
+    hip.builtin("gemv", [y, up(hip, xs), up(hip, ws), up(hip, scale), up(hip, g)], m=M, n=N, k=K,
+                wt=DT_FP8, xt=DT_BF16, yt=DT_F32, epi=0, norm=1, eps=1e-5)
+    got = y.read(np.float32).reshape(M, N)
+    err = np.abs(got - ref)
+    assert np.all(err <= (1e-5 + 2.0 ** -7) * floor + 1e-6), np.max(err / floor)
+    # and the same bits as an explicit 4 tiles per block
+    y4 = hip.Buffer(M * N * 4)
+    hip.builtin("gemv", [y4, up(hip, xs), up(hip, ws), up(hip, scale), up(hip, g)], m=M, n=N, k=K,
+                wt=DT_FP8, xt=DT_BF16, yt=DT_F32, epi=0, norm=1, eps=1e-5, r=4)
+    assert np.array_equal(y4.read(np.uint32), y.read(np.uint32))
 
 
 @pytest.mark.parametrize("M", [5, 16, 40])
@@ -482,7 +523,7 @@ def test_gemm_mfma_tiled_weights_bit_equal(hip, wx, M, NK):
     hip.builtin("tile_w", [tw, wb], n=N, k=K, wt=wdt)
     xb = up(hip, xs)
     sc = [up(hip, scale)] if scale is not None else []
-    for r in (1, 2, 4):
+    for r in (1, 2, 4) + ((7, 8) if wdt == DT_FP8 and M <= 16 else ()):
         y0, y1 = hip.Buffer(M * N * 4), hip.Buffer(M * N * 4)
         hip.builtin("gemv", [y0, xb, wb] + sc, m=M, n=N, k=K, wt=wdt, xt=xdt, yt=DT_F32, epi=0, path=2, r=r)
         hip.builtin("gemv", [y1, xb, tw] + sc, m=M, n=N, k=K, wt=wdt, xt=xdt, yt=DT_F32, epi=0, path=2, r=r,

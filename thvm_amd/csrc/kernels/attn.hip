@@ -49,10 +49,13 @@ template <int HD, int G, int AT>
 __global__ __launch_bounds__(MERGE_THREADS) void k_attn_merge(ThvmAttnArgs a) {
   __shared__ MergeFlatLds<HD, G> s;
   const uint32_t b = blockIdx.x / a.Hkv, kvh = blockIdx.x % a.Hkv;
-  // phase clock: the merge's blocks follow the split's in the clock buffer
+  // phase clock: the merge's blocks follow the split's in the clock buffer;
+  // 0 entry, 1 partials folded, 2 partition partials combined, 7 drained
   uint64_t *const clk = a.clk ? a.clk + (uint64_t)a.clk_cap * PCLK_MARKS : nullptr;
   pclk(clk, a.clk_cap, 0);
-  attn_merge_flat<HD, G, AT, false>(a, b, kvh, attn_live(a, attn_row_len(a, b)), threadIdx.x, true, s);
+  const uint32_t cpb = a.cpb > 1 ? a.cpb : 1u;
+  attn_merge_flat<HD, G, AT, false>(a, b, kvh, attn_live(a, attn_row_len(a, b)), threadIdx.x, true, s,
+                                    (a.n_split + cpb - 1) / cpb, clk, a.clk_cap);
   pclk_end(clk, a.clk_cap);
 }
 

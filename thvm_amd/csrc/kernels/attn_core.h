@@ -313,10 +313,15 @@ __device__ __forceinline__ void merge_fold(float &mp, float &lp, float &a0, floa
   mp = mn;
 }
 
+// n_live partials of the (row, kv head) are folded.  n_max >= n_live bounds
+// the slots the first batch of loads may touch (0: n_live): a bound known at
+// launch lets those loads go out before the row length (and so n_live) is
+// back from memory; slots past n_live are read but never folded.
 template <int HD, int G, int AT, bool COH>
 __device__ __forceinline__ void attn_merge_flat(const ThvmAttnArgs &a, uint32_t b, uint32_t kvh,
                                                 uint32_t n_live, int tid, bool active,
-                                                MergeFlatLds<HD, G> &s) {
+                                                MergeFlatLds<HD, G> &s, uint32_t n_max = 0,
+                                                uint64_t *clk = nullptr, uint32_t clk_cap = 0) {
   typedef MergeFlatLds<HD, G> FL;
   constexpr int PAIRS = FL::PAIRS, NP = FL::NP;
   static_assert(NP >= 1 && MERGE_THREADS % PAIRS == 0, "merge geometry");
@@ -324,14 +329,15 @@ __device__ __forceinline__ void attn_merge_flat(const ThvmAttnArgs &a, uint32_t 
   const int g = e / (HD / 2), d = (e % (HD / 2)) * 2;
   const uint64_t bh = (uint64_t)b * a.H + kvh * G + g;
   const uint64_t pbi = bh * a.n_split * (HD + 2);
+  const uint32_t nmax = n_max ? n_max : n_live;
   float mp = -INFINITY, lp = 0.0f, a0 = 0.0f, a1 = 0.0f;
   if (active && p < NP) {
-    for (uint32_t s0 = p; s0 < n_live; s0 += NP * MCH) {
+    for (uint32_t s0 = p; s0 < nmax; s0 += NP * MCH) {
       float mv[MCH], lv[MCH];
       float2 av[MCH];
 #pragma unroll
       for (int j = 0; j < MCH; j++) {            // loads first (clamped, unconditional)
-        const uint32_t sp = s0 + j * NP, spc = sp < n_live ? sp : s0;
+        const uint32_t sp = s0 + j * NP, spc = sp < nmax ? sp : s0;
         const uint64_t q = pbi + (uint64_t)spc * (HD + 2);
         if (COH) {
           const uint2 r = coh_ld8(a.part, (uint32_t)((q + d) * 4));
@@ -349,11 +355,14 @@ __device__ __forceinline__ void attn_merge_flat(const ThvmAttnArgs &a, uint32_t 
 #pragma unroll
       for (int j = 0; j < MCH; j++)
         if (s0 + j * NP < n_live) merge_fold(mp, lp, a0, a1, mv[j], lv[j], av[j].x, av[j].y);
+      if (s0 + NP * MCH >= n_live) break;
     }
   }
+  pclk(clk, clk_cap, 1);
   if (NP > 1) {
     if (active) { s.m[p][e] = mp; s.l[p][e] = lp; s.a[p][e] = make_float2(a0, a1); }
     __syncthreads();
+    pclk(clk, clk_cap, 2);
     if (active && p == 0)
 #pragma unroll
       for (int q = 1; q < NP; q++) merge_fold(mp, lp, a0, a1, s.m[q][e], s.l[q][e], s.a[q][e].x, s.a[q][e].y);

@@ -194,13 +194,20 @@ __global__ __launch_bounds__(GEMM_THREADS) void k_gemm(ThvmGemvArgs a) {
 
   // whole sub-chunks, also past s1 (zero weights), so the step loop is
   // straight-line code and every wait counts only the loads it needs
+  // phase clock (measurement build): 0 entry, 1 first loads issued, 2 first
+  // x sub-chunk staged, 3 first sub-chunk's MFMAs done, 4 K slice done, 5
+  // partial tiles summed, 7 drained
+  pclk(a.clk, a.clk_cap, 0);
   const uint32_t nsub = (s1 - s0 + SC - 1) / SC;
   xload(s0, true);
 #pragma unroll
   for (int u = 0; u < U; u++) load(u, s0 + u);
+  pclk(a.clk, a.clk_cap, 1);
   for (uint32_t c = 0; c < nsub; c++) {
     const uint32_t sb = s0 + c * SC;
     xstore();
+    if (c == 0) pclk(a.clk, a.clk_cap, 2);
+    if (c == 1) pclk(a.clk, a.clk_cap, 3);
     xload(sb + SC, c + 1 < nsub);
     __builtin_amdgcn_sched_barrier(0);            // issue them before this sub-chunk's weight loads
 #pragma unroll
@@ -220,6 +227,7 @@ __global__ __launch_bounds__(GEMM_THREADS) void k_gemm(ThvmGemvArgs a) {
       if (sl == 0) ssw[wv][i * RPI + sr] = s;
     }
   }
+  pclk(a.clk, a.clk_cap, 4);
   __syncthreads();                                // the staging area becomes the reduction buffer
 
   // partial tiles -> LDS, summed in wave order
@@ -253,8 +261,10 @@ __global__ __launch_bounds__(GEMM_THREADS) void k_gemm(ThvmGemvArgs a) {
       s1v *= inv;
     }
     const float tot[2][1] = {{s0v}, {s1v}};
+    if (task == (int)threadIdx.x) pclk(a.clk, a.clk_cap, 5);
     gemv_epilogue<2, 1>(a, n0 + i0, tot, (uint32_t)m);
   }
+  pclk_end(a.clk, a.clk_cap);
 }
 
 // -------------------------------------------------------------------------
@@ -269,6 +279,10 @@ static gemm_fn pick_nt(int NT) {
     case 1: return k_gemm<WT, XT, MT, 1, U, NM>;
     case 2: return k_gemm<WT, XT, MT, 2, U, NM>;
     case 4: return k_gemm<WT, XT, MT, 4, U4, NM>;
+    // 7 or 8 tiles: one x tile and fp8 weights only (more accumulators or
+    // 16-bit weight registers would spill)
+    case 7: return MT == 1 && WT == GW_FP8 ? k_gemm<GW_FP8, XT, 1, 7, 2, NM> : nullptr;
+    case 8: return MT == 1 && WT == GW_FP8 ? k_gemm<GW_FP8, XT, 1, 8, 2, NM> : nullptr;
     default: return nullptr;
   }
 }
@@ -306,8 +320,22 @@ extern "C" int thvm_k_gemm_mfma(const ThvmGemvArgs *a, hipStream_t s, char *err,
   // 16-row weight tiles per block, from the gfx950 sweep over the C4 shapes at
   // M=16: more tiles amortise the x tile reads over more weight rows (wide N),
   // fewer keep enough blocks in flight (N <= 4096)
-  int NT = a->tune_r ? (int)a->tune_r : (a->N >= 16384 ? 4 : a->N <= 4096 ? 1 : 2);
-  if (NT != 1 && NT != 2 && NT != 4) { snprintf(err, errlen, "gemm: n tiles per block must be 1, 2 or 4"); return -1; }
+  // At one x tile (M <= 16) the block count is sized to one block per CU:
+  // these kernels hold more than 128 VGPRs (8 waves: one block per CU), so a
+  // grid of more than 256 blocks runs in rounds -- measured on gfx950, the
+  // C4 batch-16 gate/up at 4 tiles (448 blocks) ran as a first round of 256
+  // blocks and a second of 192, ~15 us each.  Tiles per block: the fewest of
+  // 1, 2, 4, 7, 8 that cover ceil(N/16) tiles in 256 blocks (gate/up 7, the
+  // LM head 8 in several rounds); 7 and 8 with fp8 weights only.
+  const uint32_t tiles = (a->N + 15u) / 16u, need = (tiles + 255u) / 256u;
+  const bool wide = MT == 1 && a->wdt == THVM_DT_FP8E4M3;
+  int NT = a->tune_r ? (int)a->tune_r
+         : MT == 1 ? (need <= 1 ? 1 : need == 2 ? 2 : need <= 4 || !wide ? 4 : need <= 7 ? 7 : 8)
+                   : (a->N >= 16384 ? 4 : a->N <= 4096 ? 1 : 2);
+  if (NT != 1 && NT != 2 && NT != 4 && !(wide && (NT == 7 || NT == 8))) {
+    snprintf(err, errlen, "gemm: n tiles per block must be 1, 2 or 4 (7 or 8 with fp8 weights at M <= 16)");
+    return -1;
+  }
   const int xbf = a->xdt == THVM_DT_BF16, xf16 = a->xdt == THVM_DT_FP16;
   if (a->norm) {
     f = a->wdt == THVM_DT_FP8E4M3 ? pick_mt<GW_FP8, GX_BF16, 1>(MT, NT)
