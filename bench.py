@@ -58,6 +58,16 @@ MODELS = {
 }
 
 
+def _attn_on_mfma(cfg, batch) -> bool:
+    """Whether the attention builtin picks its MFMA split for this decode:
+    16-bit caches, head dim 64 or 128, at most 8 heads per kv head (a power of
+    two), above 1024 split units (rows x kv heads x 64-row chunks)."""
+    G = cfg["n_heads"] // cfg["n_kv_heads"]
+    units = batch * cfg["n_kv_heads"] * ((cfg["max_seq"] + 63) // 64)
+    return (cfg.get("adtype") != 13 and cfg.get("head_dim") in (64, 128) and G <= 8 and (G & (G - 1)) == 0
+            and units > 1024)
+
+
 def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
@@ -316,6 +326,7 @@ def run_decode(thvm, key: str, batch: int, args) -> dict:
                       {"kernel": (("k_mla_split_mf (MFMA) + k_mla_out"
                                    if (cfg["n_heads"], cfg["kv_lora"], cfg["d_rope"]) == (16, 512, 64)
                                    else "k_mla_split + k_mla_out") if mla else
+                                  "k_attn_mf (MFMA) + k_attn_merge" if _attn_on_mfma(cfg, batch) else
                                   "k_attn_multi + k_attn_merge" if cfg["n_heads"] // cfg["n_kv_heads"] <= 4
                                   else "k_attn + k_attn_merge"),
                        "achieved_gbs": round(attn_gbs, 1), "frac": round(attn_gbs / PEAK_GBS, 4),

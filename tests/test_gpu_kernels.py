@@ -751,6 +751,64 @@ def test_attention_long_context(hip, L, ms):
     assert attn_close(got, ww, cdt), np.max(np.abs(got - ww))
 
 
+@pytest.mark.parametrize("cdt", [DT_BF16, DT_F16])
+@pytest.mark.parametrize("H,Hkv,hd", [(32, 8, 128), (8, 8, 64), (16, 2, 64), (8, 4, 128)])
+@pytest.mark.parametrize("L", [1, 15, 16, 17, 63, 65, 200, 256])
+@pytest.mark.parametrize("cpb", [0, 1, 3])
+def test_attention_mfma_split(hip, H, Hkv, hd, L, cdt, cpb):
+    """The split on MFMA (mf=1: scores and the weighted sum as 16x16 MFMA
+    tiles, a wave per 16 cache rows) against the oracle at the 16-bit bars,
+    and against the VALU split (mf=2) within one output ulp: lengths inside
+    and at the edges of a 16-row tile, a 64-row chunk and a block of cpb
+    chunks; G = 1, 2, 4, 8; head dims 64 and 128."""
+    B, ms = 3, 256
+    say(f"case: attn mfma H={H} Hkv={Hkv} hd={hd} L={L} dt={cdt} cpb={cpb}")
+    rng = np.random.default_rng(H * 1000 + L + 13 * cpb + cdt)
+    qs, _ = rand_store(rng, (B, H, hd), cdt)
+    ks, _ = rand_store(rng, (B, Hkv, ms, hd), cdt)
+    vs, _ = rand_store(rng, (B, Hkv, ms, hd), cdt)
+    got, ww = run_attn(hip, qs, ks, vs, B, H, Hkv, hd, ms, L, cdt, cpb=cpb, mf=1)
+    assert attn_close(got, ww, cdt), np.max(np.abs(got - ww))
+    if H // Hkv == 8 and cpb > 1:
+        return                                   # the VALU split runs 8 heads one chunk per block
+    valu, _ = run_attn(hip, qs, ks, vs, B, H, Hkv, hd, ms, L, cdt, cpb=cpb, mf=2)
+    # the two roundings of nearly equal sums to the output type: one ulp,
+    # at most 2^-7 (bf16) or 2^-10 (fp16) of the value
+    ulp = 2.0 ** (-7 if cdt == DT_BF16 else -10)
+    assert np.all(np.abs(got - valu) <= ulp * np.abs(valu) + 1e-4), np.max(np.abs(got - valu))
+
+
+@pytest.mark.parametrize("mf", [1, 2])
+def test_attention_stale_rows_are_never_mixed(hip, mf):
+    """Cache rows at and past L hold NaN (a stale or never-written row):
+    neither split reads them into a product (zero weight times NaN would
+    still be NaN), at lengths inside a tile and a chunk."""
+    B, H, Hkv, hd, ms, cdt = 2, 32, 8, 128, 256, DT_BF16
+    rng = np.random.default_rng(77 + mf)
+    qs, _ = rand_store(rng, (B, H, hd), cdt)
+    ks, _ = rand_store(rng, (B, Hkv, ms, hd), cdt)
+    vs, _ = rand_store(rng, (B, Hkv, ms, hd), cdt)
+    for L in (5, 70, 130):
+        say(f"case: attn stale NaN rows mf={mf} L={L}")
+        k2, v2 = ks.copy(), vs.copy()
+        k2[:, :, L:, :] = 0x7FC0
+        v2[:, :, L:, :] = 0x7FC0
+        got, ww = run_attn(hip, qs, k2, v2, B, H, Hkv, hd, ms, L, cdt, mf=mf)
+        assert np.all(np.isfinite(got)) and attn_close(got, ww, cdt), L
+
+
+def test_attention_mfma_errors(hip):
+    """The MFMA split refuses f32 caches, more than 8 heads per kv head and
+    the one-launch form; mf out of range is an error."""
+    B, Hkv, hd, ms = 1, 1, 64, 128
+    for H, cdt, kw in ((4, DT_F32, dict(mf=1)), (16, DT_BF16, dict(mf=1)),
+                       (4, DT_BF16, dict(mf=1, fused=1)), (4, DT_BF16, dict(mf=3))):
+        z = np.zeros(B * H * hd, NP_STORE[cdt])
+        kv = np.zeros(B * Hkv * ms * hd, NP_STORE[cdt])
+        with pytest.raises(hip.ThvmHipError, match="mf|MFMA"):
+            run_attn(hip, z, kv, kv, B, H, Hkv, hd, ms, 5, cdt, **kw)
+
+
 def test_attention_cpb_errors(hip):
     B, H, Hkv, hd, ms, cdt = 1, 16, 2, 64, 128, DT_BF16
     z = np.zeros(B * H * hd, np.uint16)

@@ -153,7 +153,8 @@ static int attn_parse(const Spec *sp, ArgCtx *c, ThvmAttnArgs *a, int with_part)
       spec_u32(sp, "qt", &a->qdt, 0, THVM_DT_BF16) || spec_u32(sp, "ct", &a->cdt, 0, THVM_DT_BF16) ||
       spec_u32(sp, "ot", &a->odt, 0, THVM_DT_BF16) || spec_f32(sp, "scale", &a->scale, 1, 0) ||
       spec_u32(sp, "fused", &a->fused, 0, 0) || spec_u32(sp, "cpb", &a->cpb, 0, 0) ||
-      spec_u32(sp, "spec", &a->spec, 0, 0) || spec_u32(sp, "clk", &a->clk_cap, 0, 0))
+      spec_u32(sp, "spec", &a->spec, 0, 0) || spec_u32(sp, "clk", &a->clk_cap, 0, 0) ||
+      spec_u32(sp, "mf", &a->mf, 0, 0))
     return -1;
   if (a->chunk == 0) { hb_set_error("builtin attn: chunk=0"); return -1; }
   if (spec_u32(sp, "nsplit", &a->n_split, 0, (a->max_seq + a->chunk - 1) / a->chunk)) return -1;

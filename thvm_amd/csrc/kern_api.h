@@ -139,6 +139,9 @@ typedef struct ThvmAttnArgs {
                             * reads cache row 0 over L+b rows (causal)     */
   uint64_t *clk;           /* phase clock (measurement only; NULL = off)   */
   uint32_t clk_cap;        /* blocks recorded per launch (split, then merge) */
+  uint32_t mf;             /* the split on MFMA (16-bit caches, hd 64 / 128,
+                            * G <= 8, two launches): 0 picked from the shape
+                            * (batched decode), 1 on, 2 off                 */
 } ThvmAttnArgs;
 int thvm_k_attn_decode(const ThvmAttnArgs *a, hipStream_t s, char *err, int errlen);
 /* the chunks per split block thvm_k_attn_decode picks for cpb = 0 */

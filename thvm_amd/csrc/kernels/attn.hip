@@ -20,6 +20,7 @@
 //     in-kernel "last block merges" variant with device-scope fences measured
 //     3x slower on gfx950: the fences write back / invalidate L2 across XCDs.)
 #include "attn_core.h"
+#include "mfma_ops.h"
 #include "launch.h"
 #include <stdio.h>
 
@@ -297,6 +298,179 @@ __global__ __launch_bounds__(ATT_THREADS, 4) void k_attn_multi(ThvmAttnArgs a) {
   pclk_end(a.clk, a.clk_cap);
 }
 
+// ---- the split on MFMA (batched decode, 16-bit caches) -------------------
+// Where many split blocks run at once (batched decode) the VALU split is
+// bound by its arithmetic, not by HBM: ~400 VALU instructions per 8 cache
+// rows per wave for the dot products, the row-group DPP sums, the exp2s and
+// the accumulator FMAs.  Here both products run on MFMA, a wave per 16-row
+// tile of the cache (v_mfma_f32_16x16x32 for the scores, 16x16x16 for the
+// weighted sum), with no LDS in the tile loop:
+//   scores  S^T[row][head] = K[row][:] . q[head][:]: A = the K rows (lane l
+//           holds row l%16, d = 8 (l/16) + 32 ks + j: one 16-byte load
+//           straight from the cache), B = q^T (lane l holds head l%16, the
+//           same d; heads past G are zero).  The result puts rows 4 (l/16)
+//           + i and head l%16 in lane l;
+//   softmax online per head over the block's tiles: the tile max over a
+//           lane's 4 rows and the lanes 16 and 32 apart (permlane swaps),
+//           p = exp2(s - m) in the log2 domain, the lane's own row sums;
+//   mix     O^T[d][head] += V^T[d][rows] P^T[rows][head]: B = P^T is the
+//           score layout itself (lane l: rows 4 (l/16) + j, head l%16), so
+//           p needs no shuffle; A = V^T wants 4 rows of one column per lane,
+//           so lane l loads rows 4 (l/16) + j, d 8 (l%16) .. +8 (four 16-byte
+//           loads) and instruction e (0..7) takes column 8 (l%16) + e of its
+//           4 rows (v_perm_b32 pairs): instruction e yields O^T[8 m + e]
+//           [head] for m = 0..15 -- d permuted across the 8 instructions, and
+//           the accumulator of head l%16 stays in lane l's group, so the
+//           rescale by exp2(m_old - m_new) is lane-local (skipped when no
+//           max of the wave moved).
+// p enters as 16-bit hi + lo pairs (two MFMAs), so each weight keeps ~16
+// significant bits against the exact 16-bit V value.  A block runs cpb
+// chunks of 64 rows of one (row, kv head) as in the VALU form, tiles
+// round-robin over its 8 waves with the next tile's K and V in flight; the
+// waves meet once through LDS and the block writes the same partial (acc, m,
+// l) the merge kernel folds.  Rows at or past the block's end read zero
+// through the no-access offset (a stale cache row times a zero weight could
+// still be a NaN).
+#define MF_GMAX 8
+template <int HD, int AT>
+__global__ __launch_bounds__(ATT_THREADS) void k_attn_mf(ThvmAttnArgs a) {
+  static_assert(AT == AT_BF16 || AT == AT_F16, "16-bit caches");
+  constexpr int XT = AT == AT_BF16 ? GX_BF16 : GX_F16;
+  constexpr int KS = HD / 32;                    // score k-steps
+  constexpr int NC = HD / 8;                     // lane columns of the mix (8 d each)
+  static_assert(HD == 64 || HD == 128, "head dim 64 or 128");
+  __shared__ float wm[ATT_WAVES][MF_GMAX], wl[ATT_WAVES][MF_GMAX];
+  __shared__ __align__(16) float wacc[ATT_WAVES][MF_GMAX][HD + 4];
+  const uint32_t kvh = blockIdx.x, grp = blockIdx.y, b = blockIdx.z;
+  const uint32_t G = a.H / a.Hkv;
+  const int32_t L = attn_row_len(a, b);
+  const uint32_t c0 = grp * a.cpb;
+  if ((int32_t)(c0 * ATT_CHUNK) >= L) return;     // the merge reads only live partials
+  pclk(a.clk, a.clk_cap, 0);
+  const int tid = threadIdx.x, wv = tid >> 6, lane = tid & 63, lc = lane & 15, lg = lane >> 4;
+  const int32_t r0 = (int32_t)(c0 * ATT_CHUNK);
+  const int32_t r1 = min(L, (int32_t)((c0 + a.cpb) * ATT_CHUNK));
+  const int nt = (r1 - r0 + 15) / 16;             // 16-row tiles of the block
+  const uint64_t cbase = ((uint64_t)attn_cache_row(a, b) * a.Hkv + kvh) * a.max_seq * HD * 2;
+  const buf_t krs = buf_rsrc((const char *)a.kcache + cbase, a.max_seq * HD * 2);
+  const buf_t vrs = buf_rsrc((const char *)a.vcache + cbase, a.max_seq * HD * 2);
+  // q^T operands (head lc; heads past G read zero)
+  const buf_t qrs = buf_rsrc((const char *)a.q + ((uint64_t)b * a.H + kvh * G) * HD * 2, G * HD * 2);
+  uint4 qb[KS];
+#pragma unroll
+  for (int ks = 0; ks < KS; ks++)
+    qb[ks] = buf_ld16(qrs, (uint32_t)lc < G ? (uint32_t)(lc * HD + 8 * lg + 32 * ks) * 2 : BUF_OOB);
+  uint4 kb[2][KS], vb[2][4];
+  auto issue = [&](int buf, int t) {
+    const int32_t rk = r0 + 16 * t + lc, rv = r0 + 16 * t + 4 * lg;
+#pragma unroll
+    for (int ks = 0; ks < KS; ks++)
+      kb[buf][ks] = buf_ld_stream16(krs, rk < r1 ? (uint32_t)(rk * HD + 8 * lg + 32 * ks) * 2 : BUF_OOB);
+#pragma unroll
+    for (int j = 0; j < 4; j++)
+      vb[buf][j] = buf_ld_stream16(vrs, rv + j < r1 && lc < NC ? (uint32_t)((rv + j) * HD + 8 * lc) * 2 : BUF_OOB);
+  };
+  issue(0, wv);
+  issue(1, wv + ATT_WAVES);
+  const float qs = a.scale * LOG2E;
+  float m = -INFINITY, l = 0.0f;
+  f32x4_t acc[8];
+#pragma unroll
+  for (int e = 0; e < 8; e++) acc[e] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  auto tile = [&](int buf, int t) {
+    f32x4_t sc = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int ks = 0; ks < KS; ks++) sc = mfma16<XT>(kb[buf][ks], qb[ks], sc);
+    const int32_t rb = r0 + 16 * t + 4 * lg;
+    float sv[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) sv[i] = rb + i < r1 ? sc[i] * qs : -INFINITY;
+    float mx = fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3]));
+    mx = fmaxf(mx, xor16_f(mx));
+    mx = fmaxf(mx, xor32_f(mx));
+    const float mn = fmaxf(m, mx);
+    const float f = m == -INFINITY ? 0.0f : fexp2(m - mn);
+    float p[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) p[i] = sv[i] == -INFINITY ? 0.0f : fexp2(sv[i] - mn);
+    l = l * f + ((p[0] + p[1]) + (p[2] + p[3]));
+    m = mn;
+    if (__builtin_amdgcn_ballot_w64(f != 1.0f)) {
+#pragma unroll
+      for (int e = 0; e < 8; e++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) acc[e][i] *= f;
+    }
+    // P^T operands: hi = rnd(p), lo = rnd(p - hi) (p - hi exact in f32)
+    uint32_t ph[2], pl[2];
+#pragma unroll
+    for (int h = 0; h < 2; h++) {
+      if (AT == AT_BF16) {
+        ph[h] = pk_bf16(p[2 * h], p[2 * h + 1]);
+        pl[h] = pk_bf16(p[2 * h] - __uint_as_float(ph[h] << 16), p[2 * h + 1] - __uint_as_float(ph[h] & 0xffff0000u));
+      } else {
+        ph[h] = pk_f16(p[2 * h], p[2 * h + 1]);
+        pl[h] = pk_f16(p[2 * h] - h2f((f16_t)(ph[h] & 0xffffu)), p[2 * h + 1] - h2f((f16_t)(ph[h] >> 16)));
+      }
+    }
+    const uint32_t w[4][4] = {{vb[buf][0].x, vb[buf][0].y, vb[buf][0].z, vb[buf][0].w},
+                              {vb[buf][1].x, vb[buf][1].y, vb[buf][1].z, vb[buf][1].w},
+                              {vb[buf][2].x, vb[buf][2].y, vb[buf][2].z, vb[buf][2].w},
+                              {vb[buf][3].x, vb[buf][3].y, vb[buf][3].z, vb[buf][3].w}};
+#pragma unroll
+    for (int e = 0; e < 8; e++) {
+      // column 8 lc + e of rows 0..3: the low (e even) or high half of dword e/2
+      const uint32_t sel = (e & 1) ? 0x07060302u : 0x05040100u;
+      const uint32_t a01 = __builtin_amdgcn_perm(w[1][e >> 1], w[0][e >> 1], sel);
+      const uint32_t a23 = __builtin_amdgcn_perm(w[3][e >> 1], w[2][e >> 1], sel);
+      acc[e] = mfma16x16<XT>(a01, a23, ph[0], ph[1], acc[e]);
+      acc[e] = mfma16x16<XT>(a01, a23, pl[0], pl[1], acc[e]);
+    }
+  };
+  for (int t = wv; t < nt; t += 2 * ATT_WAVES) {  // two register sets, ping-pong
+    tile(0, t);
+    issue(0, t + 2 * ATT_WAVES);
+    if (t + ATT_WAVES >= nt) break;
+    tile(1, t + ATT_WAVES);
+    issue(1, t + 3 * ATT_WAVES);
+  }
+  pclk(a.clk, a.clk_cap, 3);
+  // a head's rows are spread over the lanes 16 and 32 apart
+  l += xor16_f(l);
+  l += xor32_f(l);
+  if (lg == 0 && (uint32_t)lc < G) { wm[wv][lc] = m; wl[wv][lc] = l; }
+  if ((uint32_t)lc < G) {
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const int mm = 4 * lg + i;                    // d = 8 mm + e
+      if (mm < NC) {
+        *(float4 *)&wacc[wv][lc][8 * mm] = make_float4(acc[0][i], acc[1][i], acc[2][i], acc[3][i]);
+        *(float4 *)&wacc[wv][lc][8 * mm + 4] = make_float4(acc[4][i], acc[5][i], acc[6][i], acc[7][i]);
+      }
+    }
+  }
+  __syncthreads();
+  pclk(a.clk, a.clk_cap, 5);
+  for (int o = tid; o < (int)(G * HD); o += ATT_THREADS) {
+    const int g = o / HD, d = o % HD;
+    float M = wm[0][g];
+#pragma unroll
+    for (int w = 1; w < ATT_WAVES; w++) M = fmaxf(M, wm[w][g]);
+    float sv = 0.0f, lt = 0.0f;
+#pragma unroll
+    for (int w = 0; w < ATT_WAVES; w++) {
+      const float mw = wm[w][g];
+      const float f = mw == -INFINITY ? 0.0f : fexp2(mw - M);
+      sv += wacc[w][g][d] * f;
+      lt += f * wl[w][g];
+    }
+    float *pp = a.part + (((uint64_t)b * a.H + kvh * G + g) * a.n_split + grp) * (HD + 2);
+    pp[d] = sv;
+    if (d == 0) { pp[HD] = M; pp[HD + 1] = lt; }
+  }
+  pclk_end(a.clk, a.clk_cap);
+}
+
 typedef void (*attn_fn)(ThvmAttnArgs);
 // (G = 8 heads per kv head would spill its accumulators: one chunk per block)
 template <int HD, int AT>
@@ -359,6 +533,35 @@ extern "C" uint32_t thvm_k_attn_auto_cpb(uint32_t B, uint32_t H, uint32_t Hkv, u
   return cpb > n_split ? n_split : cpb;
 }
 
+// chunks per block of the MFMA split for cpb = 0: the grid one round of
+// blocks per CU where the rows allow (at most 256 blocks of 8 waves)
+static uint32_t attn_mf_cpb(const ThvmAttnArgs *a) {
+  const uint32_t bh = a->B * a->Hkv, groups = bh >= 256 ? 1u : 256u / bh;
+  const uint32_t cpb = (a->n_split + groups - 1) / groups;
+  return cpb < 1 ? 1 : cpb;
+}
+
+static int attn_mf_launch(const ThvmAttnArgs *a, hipStream_t s, char *err, int errlen) {
+  const uint32_t G = a->H / a->Hkv;
+  const int at = a->cdt == THVM_DT_BF16 ? AT_BF16 : AT_F16;
+  attn_fn f = a->hd == 128 ? (at == AT_BF16 ? k_attn_mf<128, AT_BF16> : k_attn_mf<128, AT_F16>)
+                           : (at == AT_BF16 ? k_attn_mf<64, AT_BF16> : k_attn_mf<64, AT_F16>);
+  attn_fn fm = a->hd == 128 ? (at == AT_BF16 ? attn_pick_merge<128, AT_BF16>(G) : attn_pick_merge<128, AT_F16>(G))
+                            : (at == AT_BF16 ? attn_pick_merge<64, AT_BF16>(G) : attn_pick_merge<64, AT_F16>(G));
+  if (!fm) { snprintf(err, errlen, "attn: no merge kernel for G=%u", G); return -1; }
+  if ((uint64_t)a->B * a->H * a->n_split * (a->hd + 2) * 4 >= (1ull << 31)) {
+    snprintf(err, errlen, "attn: partials of 2 GiB or more");
+    return -1;
+  }
+  ThvmAttnArgs ak = *a;
+  ak.cpb = a->cpb ? (a->cpb < a->n_split ? a->cpb : a->n_split) : attn_mf_cpb(a);
+  thvm_launch(true, false, f, dim3(a->Hkv, (a->n_split + ak.cpb - 1) / ak.cpb, a->B), dim3(ATT_THREADS), 0, s, ak);
+  thvm_launch(false, true, fm, dim3(a->B * a->Hkv), dim3(MERGE_THREADS), 0, s, ak);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) { snprintf(err, errlen, "attn launch: %s", hipGetErrorString(e)); return -1; }
+  return 0;
+}
+
 extern "C" int thvm_k_attn_decode(const ThvmAttnArgs *a, hipStream_t s, char *err, int errlen) {
   if (a->H == 0 || a->Hkv == 0 || a->H % a->Hkv || a->B == 0 || a->max_seq == 0) {
     snprintf(err, errlen, "attn: bad head geometry H=%u Hkv=%u", a->H, a->Hkv);
@@ -384,6 +587,23 @@ extern "C" int thvm_k_attn_decode(const ThvmAttnArgs *a, hipStream_t s, char *er
   // 2.372 -> 2.285, C1 0.396 -> 0.390 ms per step), two launches at long ones
   // (C4: 11.1 against 11.9 us at L = 2051; B=16 3.50 against 3.59 ms).
   if (a->fused > 2) { snprintf(err, errlen, "attn: fused must be 0, 1 or 2"); return -1; }
+  if (a->mf > 2) { snprintf(err, errlen, "attn: mf must be 0, 1 or 2"); return -1; }
+  {
+    // the split on MFMA: forced (mf=1), or picked where the VALU split is
+    // bound by its arithmetic -- above 1024 split units (batched decode).  A
+    // speculative verify keeps the VALU split unless forced: its rows must
+    // fold the partials of its batch-1 base step
+    const uint32_t G = a->H / a->Hkv;
+    const bool can = a->cdt != THVM_DT_FP32 && (a->hd == 64 || a->hd == 128) && G <= MF_GMAX &&
+                     (G & (G - 1)) == 0 && a->fused != 1;
+    const uint64_t units = (uint64_t)a->B * a->Hkv * a->n_split;
+    if (a->mf == 1 && !can) {
+      snprintf(err, errlen, "attn: the MFMA split takes 16-bit caches, hd 64 or 128, G in 1, 2, 4, 8 "
+               "and two launches (hd=%u G=%u fused=%u)", a->hd, G, a->fused);
+      return -1;
+    }
+    if (a->mf == 1 || (a->mf == 0 && can && !a->spec && units > 1024)) return attn_mf_launch(a, s, err, errlen);
+  }
   const bool fused = a->fused == 1 || (a->fused == 2 && a->n_split <= 8);
   uint32_t cpb = a->cpb;
   if (cpb > a->n_split) cpb = a->n_split;          // one block takes every chunk

@@ -37,3 +37,24 @@ __device__ __forceinline__ f32x4_t mfma16(const uint4 &A, const uint4 &B, f32x4_
   return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8_t, A),
                                                 __builtin_bit_cast(f16x8_t, B), c, 0, 0, 0);
 }
+
+// two f32 -> a packed fp16 pair, round to nearest even; element 0 in the low half
+__device__ __forceinline__ uint32_t pk_f16(float a, float b) {
+  return (uint32_t)f2h(a) | ((uint32_t)f2h(b) << 16);
+}
+
+// v_mfma_f32_16x16x16_{bf16,f16}: A and B as two u32 each (4 16-bit values,
+// element 0 in the low half of the first); lane l holds A[m = l%16][k = 4
+// (l/16) + j] and B[k = 4 (l/16) + j][n = l%16], and gets D[4 (l/16) + i][l%16]
+typedef short s16x4_t __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x4_t __attribute__((ext_vector_type(4)));
+template <int XT>
+__device__ __forceinline__ f32x4_t mfma16x16(uint32_t a0, uint32_t a1, uint32_t b0, uint32_t b1, f32x4_t c) {
+  typedef uint32_t u2_t __attribute__((ext_vector_type(2)));
+  const u2_t A = {a0, a1}, B = {b0, b1};
+  if (XT == GX_BF16)
+    return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(s16x4_t, A),
+                                                     __builtin_bit_cast(s16x4_t, B), c, 0, 0, 0);
+  return __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(f16x4_t, A), __builtin_bit_cast(f16x4_t, B),
+                                               c, 0, 0, 0);
+}
