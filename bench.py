@@ -59,13 +59,17 @@ MODELS = {
 
 
 def _attn_on_mfma(cfg, batch) -> bool:
-    """Whether the attention builtin picks its MFMA split for this decode:
+    """Whether the attention builtin runs its MFMA split for this decode:
     16-bit caches, head dim 64 or 128, at most 8 heads per kv head (a power of
-    two), above 1024 split units (rows x kv heads x 64-row chunks)."""
+    two), where the attention runs as two launches (more than 8 chunks of 64
+    rows), unless the config forces a split."""
     G = cfg["n_heads"] // cfg["n_kv_heads"]
-    units = batch * cfg["n_kv_heads"] * ((cfg["max_seq"] + 63) // 64)
+    n_split = (cfg["max_seq"] + 63) // 64
+    one_launch = cfg.get("attn_fused", 0) == 1 or (cfg.get("attn_fused", 0) == 0 and n_split <= 8)
+    if cfg.get("attn_mf", 0):
+        return cfg["attn_mf"] == 1
     return (cfg.get("adtype") != 13 and cfg.get("head_dim") in (64, 128) and G <= 8 and (G & (G - 1)) == 0
-            and units > 1024)
+            and not one_launch)
 
 
 def log(*a):
@@ -149,6 +153,8 @@ def run_decode(thvm, key: str, batch: int, args) -> dict:
         cfg["moe_mode"] = args.moe_mode
     if args.attn_fused and spec["cfg"].get("arch") != 3:
         cfg["attn_fused"] = args.attn_fused
+    if args.attn_mf and spec["cfg"].get("arch") != 3:
+        cfg["attn_mf"] = args.attn_mf
     ctx = spec["ctx"]
     # the oracle decodes batch rows one after another on one core, so its rate
     # is the batch-1 rate; batches above 16 rows would take minutes and are
@@ -786,6 +792,8 @@ def main() -> int:
                     help="0: one launch per op (hipGraph); 1: the persistent one-launch step (LLAMA)")
     ap.add_argument("--attn-fused", type=int, default=0, choices=[0, 1, 2],
                     help="attention form: 0 auto, 1 one launch, 2 split + merge launches")
+    ap.add_argument("--attn-mf", type=int, default=0, choices=[0, 1, 2],
+                    help="attention split: 0 picked by the kernel, 1 MFMA, 2 VALU")
     ap.add_argument("--moe-mode", type=int, default=0, choices=[0, 1, 2],
                     help="DSV2 above 4 rows: expert-grouped MoE on MFMA (0/2) or on the VALU (1)")
     ap.add_argument("--layers", type=int, default=None, help="debug only: fewer layers (invalid metric)")

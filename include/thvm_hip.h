@@ -389,6 +389,10 @@ typedef struct ThvmDecodeConfig {
    * above), 1 one launch (the last split block of a row and kv head
    * merges), 2 two launches (split, then merge)                            */
   uint32_t attn_fused;
+  /* attention split: 0 auto (on MFMA for 16-bit caches of head dim 64 or
+   * 128 and up to 8 query heads per kv head, where the attention runs as two
+   * launches), 1 the MFMA split, 2 the VALU split                           */
+  uint32_t attn_mf;
 } ThvmDecodeConfig;
 
 /* Build the model on device: allocate, fill weights from `seed` (weights

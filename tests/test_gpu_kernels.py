@@ -648,7 +648,7 @@ def test_attention_decode(hip, H, Hkv, hd, L, cdt):
     hip.builtin("attn", [out, up(hip, qs), up(hip, ks), up(hip, vs),
                          up(hip, np.array([L], np.int32)), part],
                 b=B, h=H, hkv=Hkv, hd=hd, maxseq=ms, chunk=64, nsplit=nsplit, qt=cdt,
-                ct=cdt, ot=cdt, scale=scale)
+                ct=cdt, ot=cdt, scale=scale, mf=2)
     want = np.empty(B * H * hd, NP_STORE[cdt])
     O.oracle().or_attn_decode(want.ctypes.data, cdt, qs.ctypes.data, cdt, ks.ctypes.data,
                               vs.ctypes.data, cdt, B, H, Hkv, hd, ms, L, scale)
@@ -665,7 +665,7 @@ def test_attention_decode(hip, H, Hkv, hd, L, cdt):
     hip.builtin("attn", [out, up(hip, qs), up(hip, ks), up(hip, vs),
                          up(hip, np.array([L], np.int32)), part],
                 b=B, h=H, hkv=Hkv, hd=hd, maxseq=ms, chunk=64, nsplit=nsplit, qt=cdt,
-                ct=cdt, ot=cdt, scale=scale, cpb=1)
+                ct=cdt, ot=cdt, scale=scale, cpb=1, mf=2)
     assert attn_close(O.decode(out.read(NP_STORE[cdt]), cdt), ww, cdt)
     out2 = hip.Buffer(B * H * hd * SZ[cdt])
     part2 = hip.Buffer(B * H * nsplit * (hd + 2) * 4 + B * Hkv * 4)
@@ -715,16 +715,18 @@ def test_attention_multi_chunk(hip, H, Hkv, hd, L, cdt, cpb):
     qs, _ = rand_store(rng, (B, H, hd), cdt)
     ks, _ = rand_store(rng, (B, Hkv, ms, hd), cdt)
     vs, _ = rand_store(rng, (B, Hkv, ms, hd), cdt)
-    got, ww = run_attn(hip, qs, ks, vs, B, H, Hkv, hd, ms, L, cdt, cpb=cpb)
+    got, ww = run_attn(hip, qs, ks, vs, B, H, Hkv, hd, ms, L, cdt, cpb=cpb, mf=2)
     assert attn_close(got, ww, cdt), np.max(np.abs(got - ww))
 
 
-def test_attention_multi_chunk_auto_repeated(hip):
-    """The batched C4 head shape at 12 rows picks 4 chunks per block by
-    itself; one partial buffer across launches at changing lengths (stale
-    partials of a longer launch are never read)."""
+@pytest.mark.parametrize("mf", [0, 2])
+def test_attention_multi_chunk_auto_repeated(hip, mf):
+    """The batched C4 head shape at 12 rows with the chunks per block picked
+    by the kernel (mf=0: the MFMA split it picks; mf=2: the VALU split, 4
+    chunks per block); one partial buffer across launches at changing
+    lengths (stale partials of a longer launch are never read)."""
     B, H, Hkv, hd, ms, cdt = 12, 32, 8, 128, 2176, DT_BF16
-    say("case: attn multi-chunk auto, 12 rows, 5 launches")
+    say(f"case: attn multi-chunk auto, 12 rows, 5 launches, mf={mf}")
     rng = np.random.default_rng(9)
     qs, _ = rand_store(rng, (B, H, hd), cdt)
     ks, _ = rand_store(rng, (B, Hkv, ms, hd), cdt)
@@ -732,22 +734,24 @@ def test_attention_multi_chunk_auto_repeated(hip):
     nsplit = (ms + 63) // 64
     part = hip.Buffer(B * H * nsplit * (hd + 2) * 4 + B * Hkv * 4)
     for L in (2100, 700, 2176, 1, 257):
-        got, ww = run_attn(hip, qs, ks, vs, B, H, Hkv, hd, ms, L, cdt, part=part)
+        got, ww = run_attn(hip, qs, ks, vs, B, H, Hkv, hd, ms, L, cdt, part=part, mf=mf)
         assert attn_close(got, ww, cdt), (L, np.max(np.abs(got - ww)))
 
 
+@pytest.mark.parametrize("mf", [0, 2])
 @pytest.mark.parametrize("L,ms", [(20000, 20480), (131000, 131072)])
-def test_attention_long_context(hip, L, ms):
+def test_attention_long_context(hip, L, ms, mf):
     """Caches far past 8192 rows (up to the 131072-row limit): the automatic
     chunks per block and a merge of tens of partials per (row, kv head),
-    against the oracle."""
+    against the oracle; the split picked by the kernel (MFMA) and the VALU
+    split."""
     B, H, Hkv, hd, cdt = 1, 8, 2, 64, DT_BF16
-    say(f"case: attn long context L={L} max_seq={ms}")
+    say(f"case: attn long context L={L} max_seq={ms} mf={mf}")
     rng = np.random.default_rng(L)
     qs, _ = rand_store(rng, (B, H, hd), cdt)
     ks, _ = rand_store(rng, (B, Hkv, ms, hd), cdt)
     vs, _ = rand_store(rng, (B, Hkv, ms, hd), cdt)
-    got, ww = run_attn(hip, qs, ks, vs, B, H, Hkv, hd, ms, L, cdt)
+    got, ww = run_attn(hip, qs, ks, vs, B, H, Hkv, hd, ms, L, cdt, mf=mf)
     assert attn_close(got, ww, cdt), np.max(np.abs(got - ww))
 
 
@@ -816,8 +820,8 @@ def test_attention_cpb_errors(hip):
     for kw in (dict(cpb=2, fused=1), dict(cpb=3, fused=1)):
         with pytest.raises(hip.ThvmHipError):
             run_attn(hip, z, kv, kv, B, H, Hkv, hd, ms, 5, cdt, **kw)
-    with pytest.raises(hip.ThvmHipError):        # 8 heads per kv head: one chunk per block only
-        run_attn(hip, z, kv, kv, B, H, Hkv, hd, ms, 5, cdt, cpb=2)
+    with pytest.raises(hip.ThvmHipError):        # the VALU split, 8 heads per kv head: one chunk per block only
+        run_attn(hip, z, kv, kv, B, H, Hkv, hd, ms, 5, cdt, cpb=2, mf=2)
 
 
 def test_attention_fused_repeated(hip):
@@ -841,7 +845,7 @@ def test_attention_fused_repeated(hip):
             o = hip.Buffer(B * H * hd * 2)
             hip.builtin("attn", [o, qb, kb, vb, up(hip, np.array([L], np.int32)), pb], b=B, h=H,
                         hkv=Hkv, hd=hd, maxseq=ms, chunk=64, nsplit=nsplit, qt=cdt, ct=cdt, ot=cdt,
-                        scale=scale, fused=fused, cpb=1)
+                        scale=scale, fused=fused, cpb=1, mf=2)
             outs.append(o.read(np.uint16))
         assert np.array_equal(outs[0], outs[1]), L
 

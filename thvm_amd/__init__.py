@@ -55,7 +55,8 @@ class DecodeConfig(C.Structure):
                                   "n_shared", "top_k", "moe_inter", "first_dense", "step_mode",
                                   "moe_mode", "attn_cpb")] + [
         ("temperature", C.c_float), ("sample_seed_lo", C.c_uint32), ("sample_seed_hi", C.c_uint32),
-        ("spec_rows", C.c_uint32), ("spec_forced", C.c_uint32), ("attn_fused", C.c_uint32)]
+        ("spec_rows", C.c_uint32), ("spec_forced", C.c_uint32), ("attn_fused", C.c_uint32),
+        ("attn_mf", C.c_uint32)]
 
 
 class Uop(C.Structure):

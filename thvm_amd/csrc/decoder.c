@@ -315,6 +315,10 @@ static int cfg_check(const ThvmDecodeConfig *c) {
     hb_set_error("decoder: attn_fused is 0 (auto), 1 (one launch) or 2 (two launches)");
     return -1;
   }
+  if (c->attn_mf > 2) {
+    hb_set_error("decoder: attn_mf is 0 (auto), 1 (the MFMA split) or 2 (the VALU split)");
+    return -1;
+  }
   if (c->moe_mode > 2) {
     hb_set_error("decoder: moe_mode is 0 (auto), 1 (VALU grouped) or 2 (MFMA grouped)");
     return -1;
@@ -457,16 +461,27 @@ static int op_attn(Decoder *d, u32 l) {
   char p[320], kn[32], vn[32];
   snprintf(kn, sizeof kn, "l%u.kcache", l);
   snprintf(vn, sizeof vn, "l%u.vcache", l);
-  /* a verify row folds the partials as the one-row step does: same split
-   * blocks, so the one-row step's chunks per block */
-  const u32 cpb = d->spec && !c->attn_cpb
-                ? thvm_k_attn_auto_cpb(c->batch, c->n_heads, c->n_kv_heads, d->n_split, 0)
-                : c->attn_cpb;
+  const u32 fused = c->attn_fused == 1 ? 1u : c->attn_fused == 2 ? 0u : 2u;
+  /* a verify row folds the partials as the one-row step does: the same
+   * split (MFMA or VALU) and the same split blocks, so the one-row step's
+   * plan, passed explicitly */
+  u32 cpb = c->attn_cpb, mf = c->attn_mf;
+  if (d->spec) {
+    ThvmAttnArgs base;
+    memset(&base, 0, sizeof base);
+    base.B = c->batch; base.H = c->n_heads; base.Hkv = c->n_kv_heads; base.hd = c->head_dim;
+    base.max_seq = c->max_seq; base.chunk = 64; base.n_split = d->n_split;
+    base.qdt = base.cdt = base.odt = c->adtype; base.fused = fused; base.cpb = c->attn_cpb;
+    base.mf = c->attn_mf;
+    u32 bmf = 0;
+    thvm_k_attn_plan(&base, &bmf, &cpb);
+    mf = bmf ? 1u : 2u;
+  }
   snprintf(p, sizeof p,
-           "thvm-builtin:attn b=%u h=%u hkv=%u hd=%u maxseq=%u chunk=64 nsplit=%u qt=%u ct=%u ot=%u scale=%a cpb=%u fused=%u%s",
+           "thvm-builtin:attn b=%u h=%u hkv=%u hd=%u maxseq=%u chunk=64 nsplit=%u qt=%u ct=%u ot=%u scale=%a cpb=%u fused=%u mf=%u%s",
            d->rows, c->n_heads, c->n_kv_heads, c->head_dim, c->max_seq, d->n_split, c->adtype,
-           c->adtype, c->adtype, (float)(1.0 / sqrt((double)c->head_dim)), cpb,
-           c->attn_fused == 1 ? 1u : c->attn_fused == 2 ? 0u : 2u, d->spec ? " spec=1" : "");
+           c->adtype, c->adtype, (float)(1.0 / sqrt((double)c->head_dim)), cpb, fused, mf,
+           d->spec ? " spec=1" : "");
   u32 a[6] = {act(d, "att"), act(d, "q"), tens_find(d, kn), tens_find(d, vn),
               tens_find(d, "len"), act(d, "attn.part")};
   return op_add(d, "attn", p, a, 6);

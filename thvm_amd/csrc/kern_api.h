@@ -146,6 +146,9 @@ typedef struct ThvmAttnArgs {
 int thvm_k_attn_decode(const ThvmAttnArgs *a, hipStream_t s, char *err, int errlen);
 /* the chunks per split block thvm_k_attn_decode picks for cpb = 0 */
 uint32_t thvm_k_attn_auto_cpb(uint32_t B, uint32_t H, uint32_t Hkv, uint32_t n_split, uint32_t fused);
+/* the split thvm_k_attn_decode runs for these arguments: *mf 1 the MFMA
+ * split, 0 the VALU forms; *cpb its chunks per split block */
+void thvm_k_attn_plan(const ThvmAttnArgs *a, uint32_t *mf, uint32_t *cpb);
 uint64_t thvm_k_attn_part_bytes(uint32_t B, uint32_t H, uint32_t Hkv, uint32_t hd, uint32_t n_split);
 /* The same attention with a->part ignored: partials and merge counters in a
  * static device array of THVM_ATTN_SCRATCH_BYTES per GPU (no allocation).

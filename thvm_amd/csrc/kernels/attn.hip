@@ -533,12 +533,37 @@ extern "C" uint32_t thvm_k_attn_auto_cpb(uint32_t B, uint32_t H, uint32_t Hkv, u
   return cpb > n_split ? n_split : cpb;
 }
 
+// shapes the MFMA split takes
+static bool attn_mf_can(const ThvmAttnArgs *a) {
+  const uint32_t G = a->Hkv ? a->H / a->Hkv : 0;
+  return a->cdt != THVM_DT_FP32 && (a->hd == 64 || a->hd == 128) && G >= 1 && G <= MF_GMAX &&
+         (G & (G - 1)) == 0 && a->fused != 1;
+}
+
 // chunks per block of the MFMA split for cpb = 0: the grid one round of
 // blocks per CU where the rows allow (at most 256 blocks of 8 waves)
 static uint32_t attn_mf_cpb(const ThvmAttnArgs *a) {
   const uint32_t bh = a->B * a->Hkv, groups = bh >= 256 ? 1u : 256u / bh;
   const uint32_t cpb = (a->n_split + groups - 1) / groups;
   return cpb < 1 ? 1 : cpb;
+}
+
+// The split a launch with these arguments runs (*mf: 1 the MFMA split, 0
+// the VALU forms) and its chunks per block.  The MFMA split is picked
+// wherever it applies (measured on gfx950 at the C4 head shape, split +
+// merge per launch in a graph: batch 1 10.3 against 12.3 us, batch 4 15.1
+// against 20.3, batch 16 31.5 against 38.4), except where the VALU split
+// runs as one launch by default (at most 8 chunks: the kernel boundary it
+// saves outweighs its arithmetic, C3 and C1) and in a speculative verify,
+// whose rows follow the base step's plan, passed explicitly (mf, cpb).
+extern "C" void thvm_k_attn_plan(const ThvmAttnArgs *a, uint32_t *mf, uint32_t *cpb) {
+  const bool one_launch = a->fused == 1 || (a->fused == 2 && a->n_split <= 8);
+  const bool use = a->mf == 1 || (a->mf == 0 && !a->spec && !one_launch && attn_mf_can(a));
+  uint32_t c = a->cpb;
+  if (c > a->n_split) c = a->n_split;
+  if (c == 0) c = use ? attn_mf_cpb(a) : thvm_k_attn_auto_cpb(a->B, a->H, a->Hkv, a->n_split, one_launch);
+  *mf = use ? 1u : 0u;
+  *cpb = c;
 }
 
 static int attn_mf_launch(const ThvmAttnArgs *a, hipStream_t s, char *err, int errlen) {
@@ -554,7 +579,8 @@ static int attn_mf_launch(const ThvmAttnArgs *a, hipStream_t s, char *err, int e
     return -1;
   }
   ThvmAttnArgs ak = *a;
-  ak.cpb = a->cpb ? (a->cpb < a->n_split ? a->cpb : a->n_split) : attn_mf_cpb(a);
+  uint32_t mf = 0;
+  thvm_k_attn_plan(a, &mf, &ak.cpb);
   thvm_launch(true, false, f, dim3(a->Hkv, (a->n_split + ak.cpb - 1) / ak.cpb, a->B), dim3(ATT_THREADS), 0, s, ak);
   thvm_launch(false, true, fm, dim3(a->B * a->Hkv), dim3(MERGE_THREADS), 0, s, ak);
   hipError_t e = hipGetLastError();
@@ -589,20 +615,15 @@ extern "C" int thvm_k_attn_decode(const ThvmAttnArgs *a, hipStream_t s, char *er
   if (a->fused > 2) { snprintf(err, errlen, "attn: fused must be 0, 1 or 2"); return -1; }
   if (a->mf > 2) { snprintf(err, errlen, "attn: mf must be 0, 1 or 2"); return -1; }
   {
-    // the split on MFMA: forced (mf=1), or picked where the VALU split is
-    // bound by its arithmetic -- above 1024 split units (batched decode).  A
-    // speculative verify keeps the VALU split unless forced: its rows must
-    // fold the partials of its batch-1 base step
     const uint32_t G = a->H / a->Hkv;
-    const bool can = a->cdt != THVM_DT_FP32 && (a->hd == 64 || a->hd == 128) && G <= MF_GMAX &&
-                     (G & (G - 1)) == 0 && a->fused != 1;
-    const uint64_t units = (uint64_t)a->B * a->Hkv * a->n_split;
-    if (a->mf == 1 && !can) {
+    if (a->mf == 1 && !attn_mf_can(a)) {
       snprintf(err, errlen, "attn: the MFMA split takes 16-bit caches, hd 64 or 128, G in 1, 2, 4, 8 "
                "and two launches (hd=%u G=%u fused=%u)", a->hd, G, a->fused);
       return -1;
     }
-    if (a->mf == 1 || (a->mf == 0 && can && !a->spec && units > 1024)) return attn_mf_launch(a, s, err, errlen);
+    uint32_t mf = 0, cpb = 0;
+    thvm_k_attn_plan(a, &mf, &cpb);
+    if (mf) return attn_mf_launch(a, s, err, errlen);
   }
   const bool fused = a->fused == 1 || (a->fused == 2 && a->n_split <= 8);
   uint32_t cpb = a->cpb;
