@@ -23,7 +23,7 @@ DEFINE_VAR = 18
 CMPEQ, LOAD, CAST, BITCAST, RANGE, INDEX_E = 20, 21, 23, 24, 25, 26
 IADD, ISUB, IMUL, IDIV, IMOD, ILT, IAND, IWHERE, BUFFER, STORE = 27, 28, 29, 30, 31, 32, 33, 34, 36, 37
 IOR, IXOR, ISHL, ISHR, SIN = 41, 42, 44, 51, 55
-FLOATS = {11: np.float16, 12: None, 13: np.float32, 14: np.float64}
+FLOATS = {9: None, 11: np.float16, 12: None, 13: np.float32, 14: np.float64}
 NP_OF = {13: np.float32, 11: np.float16, 5: np.int32, 6: np.uint32, 7: np.int64, 0: np.uint8}
 
 
@@ -37,8 +37,12 @@ def _bf16_to_f32(u16):
 
 def narrow(x, dt):
     """x (float64 values) stored in float dtype dt and read back: f32 first,
-    then fp16 / bf16 round to nearest even (NaN kept)."""
+    then fp16 / bf16 round to nearest even (NaN kept), fp8 e4m3 by the
+    kernel-store narrowing (saturating)."""
     f = np.asarray(x, np.float64).astype(np.float32)
+    if dt == 9:                  # fp8 e4m3 through the oracle's kernel-store narrowing
+        import _oracle as O
+        return O.decode(O.encode(f, 9), 9).astype(np.float64)
     if dt == 11:
         return f.astype(np.float16).astype(np.float64)
     if dt == 12:
@@ -50,6 +54,9 @@ def narrow(x, dt):
 
 
 def decode_slot(raw: np.ndarray, dt: int) -> np.ndarray:
+    if dt == 9:
+        import _oracle as O
+        return O.decode(raw.view(np.uint8), 9).astype(np.float64)
     if dt == 12:
         return _bf16_to_f32(raw.view(np.uint16))
     return raw.view(NP_OF[dt]).astype(np.float64 if _isf(dt) else np.int64)

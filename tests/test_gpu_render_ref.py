@@ -213,3 +213,85 @@ def test_narrow_reference_kernel_under_opts(hip, k):
             assert "group" in str(e), (o, str(e))
             continue
         _narrow_check(k, got, dts, f"opts {o}")
+
+
+# ---- matmuls on MFMA, fp8 stores --------------------------------------------
+import _matmul_dag as MD  # noqa: E402
+import _oracle as O  # noqa: E402
+
+
+_SIZE = {9: 1, 11: 2, 12: 2, 13: 4}
+
+
+def _as_array(rows):
+    """DAG rows (op, dt, srcs, args) as the evaluator's [n, 10] int64 array."""
+    return np.array([[op, dt, *(list(sr) + [-1] * (4 - len(sr))), *(list(ar) + [0] * (4 - len(ar)))]
+                     for op, dt, sr, ar in rows], np.int64)
+
+
+def _run_rows(hip, rows, slots, out_dt, out_n, name):
+    src, info = hip.render_kernel(rows, name)
+    bufs = [hip.Buffer(max(16, out_n * _SIZE[out_dt]))] + [hip.Buffer.from_numpy(a) for a in slots]
+    hip.dispatch(name, src, bufs, grid=(int(info.grid_max), 1, 1), block=(int(info.block), 1, 1))
+    raw = bufs[0].read(np.uint8)[:out_n * _SIZE[out_dt]]
+    for b in bufs:
+        b.free()
+    return src, raw
+
+
+@pytest.mark.parametrize("dt", [MD.F16, MD.BF16])
+@pytest.mark.parametrize("form", ["f32out", "narrow_bias", "bt_x16", "wide"])
+def test_matmul_mfma_matches_walker(hip, dt, form):
+    """Lifted matmuls the renderer puts on MFMA tiles against the DAG
+    walker (f32 products and sums, narrowing at CAST / STORE): an f32 output
+    within f32 1e-5 of the sum of |a||b|; a 16-bit output (cast + bias
+    epilogue) within one storage rounding; B transposed with K = 48 (the
+    16x16x16 instruction); operands widened through CASTs."""
+    M, N, K = 64, 48, 96
+    kw = dict(f32out=dict(out_dt=MD.F32), narrow_bias=dict(out_dt=dt, bias=True, cast_to=dt),
+              bt_x16=dict(out_dt=MD.F32, b_trans=True), wide=dict(out_dt=MD.F32, widen=True, split=0))[form]
+    if form == "bt_x16":
+        K = 48
+    say(f"case: rendered MFMA matmul dt={dt} form={form} {M}x{N}x{K}")
+    rows = MD.matmul(M, N, K, dt, **kw)
+    rng = np.random.default_rng(31 + dt + len(form))
+    a = O.encode(rng.standard_normal((M, K)).astype(np.float32), dt)
+    b = O.encode(rng.standard_normal((N, K) if kw.get("b_trans") else (K, N)).astype(np.float32), dt)
+    slots = [a.ravel(), b.ravel()]
+    if kw.get("bias"):
+        slots.append(O.encode(rng.standard_normal(N).astype(np.float32), dt))
+    src, raw = _run_rows(hip, rows, slots, kw["out_dt"], M * N, f"mm_{dt}_{form}")
+    assert "mfma" in src
+    dec = {s + 1: E.decode_slot(x.view(np.uint8), dt) for s, x in enumerate(slots)}
+    want = E.evaluate(_as_array(rows), dec)
+    got = E.decode_slot(raw, kw["out_dt"])
+    af, bf = O.decode(a, dt).astype(np.float64), O.decode(b, dt).astype(np.float64)
+    floor = (np.abs(af) @ (np.abs(bf).T if kw.get("b_trans") else np.abs(bf))).ravel()
+    if kw["out_dt"] == MD.F32:
+        assert np.all(np.abs(got - want) <= 1e-5 * floor), np.max(np.abs(got - want) / floor)
+    else:
+        ok, exact = close_storage(got, want, kw["out_dt"])
+        assert ok, exact
+        say(f"  exact fraction {exact:.4f}")
+
+
+def test_fp8_store_matches_oracle_narrowing(hip):
+    """x * 1.0 stored as fp8 e4m3 by a rendered kernel: every byte equals the
+    oracle's kernel-store narrowing (saturating round to nearest even) over
+    all finite f32 classes the e4m3 grid meets -- ties either way, the
+    subnormals, the saturation edge -- and +-inf, NaN, +-0."""
+    rng = np.random.default_rng(8)
+    grid = O.decode(np.arange(256, dtype=np.uint8), 9)
+    fin = grid[np.isfinite(grid)]
+    mids = (np.sort(fin)[:-1] + np.sort(fin)[1:]) / 2            # exact ties
+    x = np.concatenate([fin, mids, np.nextafter(mids, np.inf), np.nextafter(mids, -np.inf),
+                        (rng.standard_normal(20000) * np.exp2(rng.integers(-12, 12, 20000))),
+                        [448.0, 464.0, 464.0001, 480.0, 1e6, -1e6, np.inf, -np.inf, np.nan, 0.0, -0.0,
+                         2.0 ** -9, 2.0 ** -10, 3 * 2.0 ** -11, 1e-30]]).astype(np.float32)
+    n = x.size
+    say(f"case: rendered fp8 e4m3 store over {n} values")
+    rows = MD.scale_store(n, MD.F32, MD.FP8, 0x3F800000)
+    _, raw = _run_rows(hip, rows, [x], MD.FP8, n, "fp8_store")
+    want = O.encode(x, 9)
+    bad = np.nonzero(raw != want)[0]
+    assert bad.size == 0, [(float(x[i]), int(raw[i]), int(want[i])) for i in bad[:8]]

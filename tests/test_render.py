@@ -222,3 +222,46 @@ def test_autotune_refuses_output_buffer_bound_as_input():
     nodes = [(36, 13, (), (0,)), (36, 13, (), (1,)), (37, 13, (1,), ())]
     with pytest.raises(H.ThvmHipError, match="reads its output buffer"):
         H.render_autotune(nodes, [7, 7])
+
+
+# ---------------------------------------------------- matmuls on MFMA, fp8 stores
+import _matmul_dag as MD  # noqa: E402
+
+
+@pytest.mark.parametrize("dt", [MD.F16, MD.BF16])
+@pytest.mark.parametrize("shape", [(32, 48, 64, 4, False), (16, 16, 48, 0, True), (64, 32, 32, 8, False)])
+def test_render_matmul_takes_mfma(tmp_path, dt, shape):
+    """A lifted fp16 / bf16 matmul with M, N, K multiples of 16 renders as
+    the MFMA tile kernel (16x16x32 where 32 divides K, else 16x16x16), one
+    wave per 16x16 tile; the source compiles for gfx950."""
+    M, N, K, split, bt = shape
+    src, info = hip.render_kernel(MD.matmul(M, N, K, dt, MD.F32, b_trans=bt, split=split), "k_mm")
+    assert "__builtin_amdgcn_mfma_f32_16x16x" in src
+    assert ("16x16x32" in src) == (K % 32 == 0)
+    assert info.block == 256 and info.grid_max == (M // 16) * (N // 16) // 4 + ((M // 16) * (N // 16) % 4 > 0)
+    compile_ok(src, tmp_path)
+
+
+def test_render_matmul_epilogue_and_fallbacks(tmp_path):
+    """The epilogue (a CAST and + bias[n]) runs on the tile's results; shapes
+    and forms outside the tile path (M = 4 as the reference's decode
+    schedules, f32 operands, explicit opts) keep the generic kernel."""
+    src, _ = hip.render_kernel(MD.matmul(32, 32, 64, MD.BF16, MD.BF16, bias=True, cast_to=MD.BF16), "k_mm_epi")
+    assert "mfma" in src and "rt_bf16" in src
+    compile_ok(src, tmp_path)
+    src, _ = hip.render_kernel(MD.matmul(32, 32, 64, MD.F16, MD.F32, widen=True), "k_mm_wide")
+    assert "mfma" in src
+    for rows, opts in ((MD.matmul(4, 32, 64, MD.F16, MD.F16), None),
+                       (MD.matmul(32, 32, 64, MD.F32, MD.F32), None),
+                       (MD.matmul(32, 32, 64, MD.F16, MD.F16), (256, 1, 1)),
+                       (MD.matmul(32, 32, 40, MD.F16, MD.F16, split=0), None)):
+        src, _ = hip.render_kernel(rows, "k_mm_generic", opts=opts)
+        assert "mfma" not in src
+
+
+def test_render_fp8_store(tmp_path):
+    """An fp8 e4m3 output renders with the store narrowing (saturating RNE)
+    and compiles."""
+    src, _ = hip.render_kernel(MD.scale_store(1000, MD.F32, MD.FP8, 0x3F800000), "k_fp8")
+    assert "f2fp8e4m3" in src
+    compile_ok(src, tmp_path)

@@ -23,6 +23,12 @@
  *     block, `upcast` consecutive outputs per thread (one thread per output
  *     otherwise); without opts the hand-coded choice (hand_opts below), and
  *     thvm_hip_render_autotune searches them on the device;
+ *   - fp8 e4m3 outputs store with the reference's kernel-store narrowing
+ *     (saturating round to nearest even, NaN -> S.1111.111), and a CAST to
+ *     fp8 rounds through it;
+ *   - a lifted fp16 / bf16 matmul (REDUCE_SUM of a product of two affine
+ *     reads, M, N, K multiples of 16) renders as MFMA 16x16 tiles with its
+ *     epilogue through the generic emitter (render_mfma below);
  *   - symbolic extents (DEFINE_VAR) are read from an int32 buffer argument,
  *     not passed by value, so a captured graph stays correct when a bound
  *     variable changes; the grid is sized at the variables' upper bounds and
@@ -119,6 +125,7 @@ static const char *alu_t(uint32_t dt) {
 static const char *round_fn(uint32_t dt) {
   if (dt == THVM_DT_FP16) return "rt_f16";
   if (dt == THVM_DT_BF16) return "rt_bf16";
+  if (dt == THVM_DT_FP8E4M3) return "rt_fp8e4m3";
   return "";
 }
 
@@ -140,6 +147,29 @@ static const char *PRELUDE =
     "  if (e == 15u && m == 7u) v = __uint_as_float(0x7fc00000u);\n"
     "  return (b & 0x80u) ? -v : v;\n"
     "}\n"
+    /* f32 -> e4m3 as the reference's kernel store narrows (src/dtype/fp8.c,
+     * tests/test_fp8_nonfinite.c): round to nearest even on the f32
+     * significand, subnormals kept, a finite overflow and +-inf saturate to
+     * +-448 (S.1111.110), a NaN stores S.1111.111 */
+    "__device__ __forceinline__ unsigned char f2fp8e4m3(float x) {\n"
+    "  const uint u = __float_as_uint(x), s = (u >> 24) & 0x80u, a = u & 0x7fffffffu;\n"
+    "  if (a > 0x7f800000u) return (unsigned char)(s | 0x7fu);\n"
+    "  if (a == 0x7f800000u) return (unsigned char)(s | 0x7eu);\n"
+    "  int ef = (int)(a >> 23); uint sig = a & 0x7fffffu;\n"
+    "  if (ef) sig |= 0x800000u; else ef = 1;\n"
+    "  int e = ef - 127; if (e < -6) e = -6;\n"
+    "  const int sh = (e - 3) - (ef - 150);\n"
+    "  uint n = 0u;\n"
+    "  if (sh <= 24) {\n"
+    "    const uint rem = sig & ((1u << sh) - 1u), half = 1u << (sh - 1);\n"
+    "    n = sig >> sh;\n"
+    "    if (rem > half || (rem == half && (n & 1u))) n++;\n"
+    "  }\n"
+    "  uint code = ((uint)(e + 6) << 3) + n;\n"
+    "  if (code > 0x7eu) code = 0x7eu;\n"
+    "  return (unsigned char)(s | code);\n"
+    "}\n"
+    "__device__ __forceinline__ float rt_fp8e4m3(float f) { return fp8e4m3_f(f2fp8e4m3(f)); }\n"
     "__device__ __forceinline__ float wsum(float v) {\n"
     "  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);\n"
     "  return v;\n"
@@ -469,6 +499,240 @@ static void hand_opts(int has_red, int nested, int64_t red_len, uint64_t outputs
   }
 }
 
+/* ---- matmuls on MFMA ------------------------------------------------------
+ * The reference renders a tensor-core matmul when its scheduler marks one
+ * (WMMA 16x16x16 tiles over shared-memory staging, src/codegen/render_uop.c
+ * :1690-1986, :2380-2560).  This target recognises the same computation in
+ * the lifted DAG itself:
+ *   STORE(out, f(m, n), epilogue(REDUCE_SUM over k (MUL(A[addr_a(m, k)],
+ *                                                        B[addr_b(k, n)]))))
+ * with A and B fp16 or bf16 of one type (read directly or through a widening
+ * CAST / LOAD), exactly two parallel axes m and n of static extents that are
+ * multiples of 16, one or two reduce axes forming a flat k (extent a
+ * multiple of 16; with two, the outer axis steps A and B by the inner one's
+ * extent times its step), and both addresses affine in m, n and k.  Each
+ * wave computes one 16x16 output tile with v_mfma_f32_16x16x32 (or x16 at a
+ * k extent that is not a multiple of 32): lane l reads A at m = l%16 and B at
+ * n = l%16 for the 8 (4) k of its lane group, products exact, f32
+ * accumulation; the four results of a lane (rows 4 (l/16) + i, column l%16)
+ * then run the DAG's own epilogue and store through the generic emitter, so
+ * bias, activation and the narrowing at CAST / STORE are the DAG's.  The sum
+ * differs from the walker's serial f32 sum only in its order.  Anything
+ * else, and every launch with explicit opts, takes the generic path. */
+#define MF_AX 64     /* axis ids the affine analysis tracks */
+
+/* x = c + sum_a coef[a] * axis_a, or 0 when the expression is not affine */
+static int affine(const ThvmUop *u, int i, int64_t *c, int64_t *coef, int depth) {
+  if (i < 0 || depth > 64) return 0;
+  const ThvmUop *x = &u[i];
+  memset(coef, 0, sizeof(int64_t) * MF_AX);
+  *c = 0;
+  switch (x->op) {
+    case U_CONST: *c = x->arg[0]; return 1;
+    case U_RANGE:
+      if (x->arg[0] < 0 || x->arg[0] >= MF_AX) return 0;
+      coef[x->arg[0]] = 1;
+      return 1;
+    case U_IADD: case U_ISUB: case U_IMUL: {
+      int64_t c0, c1, k0[MF_AX], k1[MF_AX];
+      if (!affine(u, x->src[0], &c0, k0, depth + 1) || !affine(u, x->src[1], &c1, k1, depth + 1)) return 0;
+      if (x->op == U_IMUL) {
+        int lin0 = 0, lin1 = 0;
+        for (int a = 0; a < MF_AX; a++) { lin0 |= k0[a] != 0; lin1 |= k1[a] != 0; }
+        if (lin0 && lin1) return 0;
+        const int64_t m = lin0 ? c1 : c0;
+        const int64_t *kk = lin0 ? k0 : k1;
+        *c = c0 * c1;
+        for (int a = 0; a < MF_AX; a++) coef[a] = kk[a] * m;
+        return 1;
+      }
+      const int64_t sg = x->op == U_ISUB ? -1 : 1;
+      *c = c0 + sg * c1;
+      for (int a = 0; a < MF_AX; a++) coef[a] = k0[a] + sg * k1[a];
+      return 1;
+    }
+    default: return 0;
+  }
+}
+
+/* the INDEX an operand of the MUL reads, through a widening CAST / LOAD */
+static int mf_operand(const ThvmUop *u, int i) {
+  for (int d = 0; d < 4 && i >= 0; d++) {
+    const ThvmUop *x = &u[i];
+    if (x->op == U_INDEX_E) return i;
+    if (x->op == U_LOAD) { i = x->src[0]; continue; }
+    if (x->op == U_CAST && (x->dtype == THVM_DT_FP32 || x->dtype == u[x->src[0]].dtype)) { i = x->src[0]; continue; }
+    return -1;
+  }
+  return -1;
+}
+
+typedef struct {
+  int red, ia, ib, m_ax, n_ax;
+  int64_t M, N, K, ca, cam, cak, cb, cbn, cbk, capa, capb;
+  int slot_a, slot_b;
+  uint32_t dt;
+} MfPlan;
+
+/* the MFMA plan of a DAG, or 0 */
+static int mf_match(const ThvmUop *u, uint32_t n, const int *par, int npar, const int *is_red_axis, MfPlan *p) {
+  memset(p, 0, sizeof *p);
+  p->red = -1;
+  for (uint32_t i = 0; i < n; i++) {
+    if (u[i].op == U_DEFINE_VAR) return 0;
+    if (u[i].op == U_REDUCE) { if (p->red >= 0) return 0; p->red = (int)i; }
+  }
+  if (p->red < 0 || npar != 2) return 0;
+  const ThvmUop *rd = &u[p->red];
+  if (rd->arg[0] != RED_SUM || rd->src[3] >= 0 || rd->src[1] < 0) return 0;
+  const ThvmUop *mul = &u[rd->src[0]];
+  if (mul->op != U_MUL) return 0;
+  p->ia = mf_operand(u, mul->src[0]);
+  p->ib = mf_operand(u, mul->src[1]);
+  if (p->ia < 0 || p->ib < 0) return 0;
+  const ThvmUop *ba = &u[u[p->ia].src[0]], *bb = &u[u[p->ib].src[0]];
+  if (ba->op != U_BUFFER || bb->op != U_BUFFER || ba->dtype != bb->dtype ||
+      (ba->dtype != THVM_DT_FP16 && ba->dtype != THVM_DT_BF16))
+    return 0;
+  p->dt = ba->dtype;
+  p->slot_a = (int)ba->arg[0];
+  p->slot_b = (int)bb->arg[0];
+  p->capa = ba->arg[1];
+  p->capb = bb->arg[1];
+  int64_t ka[MF_AX], kb[MF_AX];
+  if (!affine(u, u[p->ia].src[1], &p->ca, ka, 0) || !affine(u, u[p->ib].src[1], &p->cb, kb, 0)) return 0;
+  /* m and n: the parallel axes A and B read, one each */
+  for (int t = 0; t < 2; t++) {
+    const ThvmUop *rg = &u[par[t]];
+    if (rg->src[0] >= 0 || rg->arg[0] < 0 || rg->arg[0] >= MF_AX) return 0;
+  }
+  const int64_t a0 = u[par[0]].arg[0], a1 = u[par[1]].arg[0];
+  if (ka[a0] && !kb[a0] && kb[a1] && !ka[a1]) { p->m_ax = (int)a0; p->n_ax = (int)a1; p->M = u[par[0]].arg[2]; p->N = u[par[1]].arg[2]; }
+  else if (ka[a1] && !kb[a1] && kb[a0] && !ka[a0]) { p->m_ax = (int)a1; p->n_ax = (int)a0; p->M = u[par[1]].arg[2]; p->N = u[par[0]].arg[2]; }
+  else return 0;
+  p->cam = ka[p->m_ax];
+  p->cbn = kb[p->n_ax];
+  /* k: one axis, or two forming a flat index (outer step = inner extent x inner step) */
+  int ax[2] = {rd->src[1], rd->src[2]}, na = rd->src[2] >= 0 ? 2 : 1;
+  for (int t = 0; t < na; t++)
+    if (u[ax[t]].op != U_RANGE || u[ax[t]].src[0] >= 0 || u[ax[t]].arg[0] < 0 || u[ax[t]].arg[0] >= MF_AX ||
+        is_red_axis[ax[t]] < 0)
+      return 0;
+  if (na == 1) {
+    const int64_t k0 = u[ax[0]].arg[0];
+    p->K = u[ax[0]].arg[2];
+    p->cak = ka[k0];
+    p->cbk = kb[k0];
+  } else {
+    const int64_t k0 = u[ax[0]].arg[0], k1 = u[ax[1]].arg[0];
+    const int64_t e0 = u[ax[0]].arg[2], e1 = u[ax[1]].arg[2];
+    if (ka[k0] == e1 * ka[k1] && kb[k0] == e1 * kb[k1]) {          /* k = a0 * e1 + a1 */
+      p->cak = ka[k1]; p->cbk = kb[k1];
+    } else if (ka[k1] == e0 * ka[k0] && kb[k1] == e0 * kb[k0]) {   /* k = a1 * e0 + a0 */
+      p->cak = ka[k0]; p->cbk = kb[k0];
+    } else {
+      return 0;
+    }
+    p->K = e0 * e1;
+  }
+  /* no other axis in the operand addresses; a k step of 0 is a broadcast, not a matmul */
+  for (int a = 0; a < MF_AX; a++) {
+    const int used = a == p->m_ax || a == p->n_ax;
+    int isk = 0;
+    for (int t = 0; t < na; t++) isk |= u[ax[t]].arg[0] == a;
+    if (!used && !isk && (ka[a] || kb[a])) return 0;
+  }
+  if (p->cak == 0 || p->cbk == 0) return 0;
+  if (p->M <= 0 || p->N <= 0 || p->K <= 0 || p->M % 16 || p->N % 16 || p->K % 16) return 0;
+  if (p->M * p->N > (1ll << 31)) return 0;
+  return 1;
+}
+
+/* the STORE of the value node vi at address ai (a guard when the output's
+ * capacity is known), into out slot 0 of dtype odt */
+static void emit_store_line(Sb *sb, const ThvmUop *st, const ThvmUop *nodes, uint32_t odt, const char *cond0) {
+  char val[64];
+  const int vi = st->src[2], ai = st->src[1];
+  if (odt == THVM_DT_BF16) snprintf(val, sizeof val, "f2bf((float)v%d)", vi);
+  else if (odt == THVM_DT_FP16) snprintf(val, sizeof val, "(_Float16)(float)v%d", vi);
+  else if (odt == THVM_DT_BOOL) snprintf(val, sizeof val, "(unsigned char)(v%d != 0)", vi);
+  else if (odt == THVM_DT_FP8E4M3) snprintf(val, sizeof val, "f2fp8e4m3((float)v%d)", vi);
+  else snprintf(val, sizeof val, "(%s)v%d", store_t(odt), vi);
+  char guard[96] = "";
+  const int64_t cap0 = nodes[st->src[0]].arg[1];
+  if (cap0 > 0) snprintf(guard, sizeof guard, "(unsigned long long)v%d < %lldull", ai, (long long)cap0);
+  char cond[192];
+  snprintf(cond, sizeof cond, "%s%s%s", cond0, (cond0[0] && guard[0]) ? " && " : "", guard);
+  if (cond[0]) sb_put(sb, "  if (%s) s0[v%d] = %s;\n", cond, ai, val);
+  else sb_put(sb, "  s0[v%d] = %s;\n", ai, val);
+}
+
+static int render_mfma(R *r, const MfPlan *p, const char *name, const uint32_t *slot_dt, int nslot,
+                       ThvmRenderInfo *info) {
+  Sb *sb = r->s;
+  const ThvmUop *u = r->u, *st = &u[r->n - 1];
+  const int kw = p->K % 32 == 0 ? 32 : 16, per = kw / 4;     /* k per instruction, per lane */
+  const int64_t TN = p->N / 16, tiles = (p->M / 16) * TN;
+  const int bf = p->dt == THVM_DT_BF16;
+  sb_put(sb, "%s\n", PRELUDE);
+  sb_put(sb, "typedef float mf_f4 __attribute__((ext_vector_type(4)));\n");
+  if (kw == 32)
+    sb_put(sb, "typedef %s mf_op __attribute__((ext_vector_type(8)));\n", bf ? "__bf16" : "_Float16");
+  else
+    sb_put(sb, "typedef %s mf_op __attribute__((ext_vector_type(4)));\n", bf ? "short" : "_Float16");
+  sb_put(sb, "extern \"C\" __global__ void __launch_bounds__(256) %s(\n", name);
+  for (int k = 0; k < nslot; k++)
+    sb_put(sb, "    %s%s *__restrict__ s%d%s\n", k ? "const " : "", store_t(slot_dt[k]), k, k + 1 < nslot ? "," : "");
+  sb_put(sb, ") {\n");
+  sb_put(sb, "  /* MFMA matmul: %lldx%lldx%lld, one 16x16 tile per wave, k %d per instruction */\n",
+         (long long)p->M, (long long)p->N, (long long)p->K, kw);
+  sb_put(sb,
+         "  const long long tw_ = (long long)blockIdx.x * 4 + (threadIdx.x >> 6);\n"
+         "  if (tw_ >= %lldll) return;\n"
+         "  const int ln_ = (int)(threadIdx.x & 63u);\n"
+         "  const long long tm_ = tw_ / %lldll, tn_ = tw_ %% %lldll;\n"
+         "  const unsigned short *ra_ = (const unsigned short *)s%d, *rb_ = (const unsigned short *)s%d;\n"
+         "  const long long ab_ = %lldll + %lldll * (tm_ * 16 + (ln_ & 15));\n"
+         "  const long long bb_ = %lldll + %lldll * (tn_ * 16 + (ln_ & 15));\n"
+         "  mf_f4 acc_ = {0.f, 0.f, 0.f, 0.f};\n"
+         "  for (long long k0_ = 0; k0_ < %lldll; k0_ += %d) {\n"
+         "    unsigned short av_[%d], bv_[%d];\n"
+         "    for (int j = 0; j < %d; j++) {\n"
+         "      const long long k_ = k0_ + %d * (ln_ >> 4) + j;\n"
+         "      const long long ia_ = ab_ + %lldll * k_, ib_ = bb_ + %lldll * k_;\n",
+         (long long)tiles, (long long)TN, (long long)TN, p->slot_a, p->slot_b, (long long)p->ca, (long long)p->cam,
+         (long long)p->cb, (long long)p->cbn, (long long)p->K, kw, per, per, per, per, (long long)p->cak,
+         (long long)p->cbk);
+  if (p->capa > 0) sb_put(sb, "      av_[j] = (unsigned long long)ia_ < %lldull ? ra_[ia_] : (unsigned short)0;\n", (long long)p->capa);
+  else sb_put(sb, "      av_[j] = ra_[ia_];\n");
+  if (p->capb > 0) sb_put(sb, "      bv_[j] = (unsigned long long)ib_ < %lldull ? rb_[ib_] : (unsigned short)0;\n", (long long)p->capb);
+  else sb_put(sb, "      bv_[j] = rb_[ib_];\n");
+  sb_put(sb, "    }\n");
+  if (kw == 32)
+    sb_put(sb, "    acc_ = __builtin_amdgcn_mfma_f32_16x16x32_%s(__builtin_bit_cast(mf_op, av_), "
+           "__builtin_bit_cast(mf_op, bv_), acc_, 0, 0, 0);\n", bf ? "bf16" : "f16");
+  else
+    sb_put(sb, "    acc_ = __builtin_amdgcn_mfma_f32_16x16x16%s(__builtin_bit_cast(mf_op, av_), "
+           "__builtin_bit_cast(mf_op, bv_), acc_, 0, 0, 0);\n", bf ? "bf16_1k" : "f16");
+  sb_put(sb, "  }\n");
+  /* each lane's 4 results through the DAG's epilogue and store */
+  sb_put(sb, "  for (int i_ = 0; i_ < 4; i_++) {\n"
+         "  const int a%d = (int)(tm_ * 16 + 4 * (ln_ >> 4) + i_);\n"
+         "  const int a%d = (int)(tn_ * 16 + (ln_ & 15));\n"
+         "  const float v%d = acc_[i_];\n", p->m_ax, p->n_ax, p->red);
+  r->level[p->red] = 0;
+  if (emit(r, st->src[1]) < 0 || emit(r, st->src[2]) < 0) return -1;
+  emit_store_line(sb, st, u, slot_dt[0], "");
+  sb_put(sb, "  }\n}\n");
+  info->n_slots = (uint32_t)nslot;
+  info->kvar_slot = 0;
+  info->group = 1;
+  info->block = 256;
+  info->upcast = 1;
+  info->grid_max = (uint64_t)(tiles + 3) / 4;
+  return 0;
+}
+
 static int render_impl(const ThvmUop *nodes, uint32_t n, const char *name, const ThvmRenderOpts *opts,
                        char *out, uint64_t cap, ThvmRenderInfo *info) {
   if (!nodes || n == 0 || !name || !out || cap < 1024 || !info) {
@@ -604,6 +868,15 @@ static int render_impl(const ThvmUop *nodes, uint32_t n, const char *name, const
   }
   r.group = o.group > 1 ? (int)o.group : 0;
   r.block = (int)o.block;
+  if (!opts && nvar == 0) {      /* a matmul runs on MFMA (hand-coded path only) */
+    MfPlan mp;
+    if (mf_match(nodes, n, par, npar, r.is_red_axis, &mp)) {
+      if (render_mfma(&r, &mp, name, slot_dt, nslot, info) < 0) goto bad;
+      if (sb.bad) { hb_set_error("render: source exceeds %llu bytes", (unsigned long long)cap); goto done; }
+      rc = 0;
+      goto done;
+    }
+  }
 
   /* source */
   sb_put(&sb, "%s\n", PRELUDE);
@@ -649,23 +922,9 @@ static int render_impl(const ThvmUop *nodes, uint32_t n, const char *name, const
   sb_put(&sb, "  (void)q_;\n");
   if (emit(&r, st->src[1]) < 0 || emit(&r, st->src[2]) < 0) goto bad;
   {
-    const uint32_t odt = slot_dt[0];
-    const uint32_t vdt = nodes[st->src[2]].dtype;
-    char val[64];
-    if (odt == THVM_DT_BF16) snprintf(val, sizeof val, "f2bf((float)v%d)", st->src[2]);
-    else if (odt == THVM_DT_FP16) snprintf(val, sizeof val, "(_Float16)(float)v%d", st->src[2]);
-    else if (odt == THVM_DT_BOOL) snprintf(val, sizeof val, "(unsigned char)(v%d != 0)", st->src[2]);
-    else if (odt == THVM_DT_FP8E4M3) { hb_set_error("render: fp8 stores are not rendered"); goto done; }
-    else snprintf(val, sizeof val, "(%s)v%d", store_t(odt), st->src[2]);
-    (void)vdt;
-    char guard[96] = "";
-    const int64_t cap0 = nodes[st->src[0]].arg[1];
-    if (cap0 > 0) snprintf(guard, sizeof guard, "(unsigned long long)v%d < %lldull", st->src[1], (long long)cap0);
-    char cond[192];
-    snprintf(cond, sizeof cond, "%s%s%s%s%s", G ? "gl_ == 0" : "", G > 64 ? " && act_" : "",
-             (G && guard[0]) ? " && " : "", guard, "");
-    if (cond[0]) sb_put(&sb, "  if (%s) s0[v%d] = %s;\n", cond, st->src[1], val);
-    else sb_put(&sb, "  s0[v%d] = %s;\n", st->src[1], val);
+    char c0[32];
+    snprintf(c0, sizeof c0, "%s%s", G ? "gl_ == 0" : "", G > 64 ? " && act_" : "");
+    emit_store_line(&sb, st, nodes, slot_dt[0], c0);
     sb_put(&sb, "%s}\n", U > 1 && !G ? "  }\n" : "");
   }
   if (sb.bad) { hb_set_error("render: source exceeds %llu bytes", (unsigned long long)cap); goto done; }
