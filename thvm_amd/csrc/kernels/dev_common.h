@@ -180,6 +180,12 @@ __device__ __forceinline__ uint4 buf_ld16(buf_t r, uint32_t off) {
   u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
   return make_uint4(v[0], v[1], v[2], v[3]);
 }
+__device__ __forceinline__ uint32_t buf_ld4(buf_t r, uint32_t off) {
+  return __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0);
+}
+__device__ __forceinline__ uint32_t buf_ld2(buf_t r, uint32_t off) {
+  return (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(r, off, 0, 0);
+}
 __device__ __forceinline__ uint4 buf_ld_stream16(buf_t r, uint32_t off) {   // nontemporal
   u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 2);
   return make_uint4(v[0], v[1], v[2], v[3]);

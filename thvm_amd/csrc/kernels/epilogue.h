@@ -51,18 +51,32 @@ __device__ __forceinline__ float rnd_any(float v, uint32_t dt) {
   return dt == THVM_DT_BF16 ? rbf(v) : dt == THVM_DT_FP16 ? rh(v) : v;
 }
 
+// The epilogue operands of one row group, loaded ahead of the epilogue (the
+// GEMV issues them before its x and weight loads, so the epilogue waits for
+// no memory round trip of its own): row scales, the residual values (RESID),
+// the position and the RoPE pair of the group's one row pair (QKV*).
+template <int R, int M>
+struct EpiPre {
+  uint32_t sc[R];        // f32 bits of the row scales (read only with a.scale)
+  uint32_t rv[R][M];     // the residual values in their storage bits
+  float cs[M], sn[M];
+  int32_t pos;
+};
+
 // Rows n0..n0+R-1 of batch rows mb..mb+M-1; tot[r][m] is the raw f32 sum.
 // COH: y, res and the caches are read/written with system-scope accesses.
+// pre: the group's operands already loaded (else read here).
 template <int R, int M, bool COH = false>
 __device__ __forceinline__ void gemv_epilogue(const ThvmGemvArgs &a, const uint32_t n0,
                                               const float (&tot)[R][M],
-                                              const uint32_t mb = 0) {
+                                              const uint32_t mb = 0,
+                                              const EpiPre<R, M> *pre = nullptr) {
   const uint32_t N = a.N;
   float v[R][M];
 #pragma unroll
   for (int r = 0; r < R; r++) {
     uint32_t n = n0 + r;
-    float s = (a.scale != nullptr && n < N) ? a.scale[n] : 1.0f;
+    float s = (a.scale != nullptr && n < N) ? (pre ? __uint_as_float(pre->sc[r]) : a.scale[n]) : 1.0f;
     float bv = (a.bias != nullptr && n < N) ? ld_any(a.bias, n, a.ydt) : 0.0f;
 #pragma unroll
     for (int m = 0; m < M; m++) v[r][m] = tot[r][m] * s + bv;
@@ -84,7 +98,10 @@ __device__ __forceinline__ void gemv_epilogue(const ThvmGemvArgs &a, const uint3
 #pragma unroll
           for (int m = 0; m < M; m++) {
             uint64_t i = (uint64_t)(mb + m) * a.ldy + n0 + r;
-            float rv = ld_anyc<COH>(a.res, i, ydt);
+            const uint32_t rb = pre ? pre->rv[r][m] : 0u;
+            float rv = !pre ? ld_anyc<COH>(a.res, i, ydt)
+                     : ydt == THVM_DT_FP32 ? __uint_as_float(rb)
+                     : ydt == THVM_DT_BF16 ? bf2f((bf16_t)rb) : h2f((f16_t)rb);
             st_anyc<COH>(a.y, i, ydt, rv + rnd_any(v[r][m], ydt));
           }
       break;
@@ -115,7 +132,7 @@ __device__ __forceinline__ void gemv_epilogue(const ThvmGemvArgs &a, const uint3
       if (R % 2) break;
       const uint32_t hd = a.head_dim;
       const uint32_t Hq = a.n_heads * hd, Hk = a.n_kv_heads * hd;
-      const int32_t pos = a.len[0] - 1;
+      const int32_t pos = pre ? pre->pos : a.len[0] - 1;
       if (pos < 0 || (uint32_t)pos >= a.max_seq) break;   // no live row to write
       const bool rope = a.epi == THVM_EPI_QKV_ROPE;
 #pragma unroll
@@ -130,8 +147,13 @@ __device__ __forceinline__ void gemv_epilogue(const ThvmGemvArgs &a, const uint3
           if (pm >= a.max_seq) continue;
           float c = 1.0f, sn = 0.0f;
           if (rope && nn < Hq + Hk) {
-            c = a.rope_cos[(uint64_t)pm * (hd / 2) + d / 2];
-            sn = a.rope_sin[(uint64_t)pm * (hd / 2) + d / 2];
+            if (pre && R == 2) {
+              c = pre->cs[m];
+              sn = pre->sn[m];
+            } else {
+              c = a.rope_cos[(uint64_t)pm * (hd / 2) + d / 2];
+              sn = a.rope_sin[(uint64_t)pm * (hd / 2) + d / 2];
+            }
           }
           float xe = rnd_any(v[r][m], ydt), xo = rnd_any(v[r + 1][m], ydt);
           float oe = xe, oo = xo;

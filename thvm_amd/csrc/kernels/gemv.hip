@@ -82,8 +82,8 @@ extern "C" int thvm_k_gemv(const ThvmGemvArgs *a, hipStream_t s, char *err, int 
   // defaults from the gfx950 sweep over the C4 projection shapes (8 waves per
   // block, one row per wave unless the epilogue pairs rows, U=4, <= 512 blocks)
   uint32_t waves = a->tune_waves ? a->tune_waves : 8;
-  if (waves != 1 && waves != 2 && waves != 4 && waves != 8 && waves != 16) {
-    snprintf(err, errlen, "gemv: waves per block must be 1,2,4,8 or 16");
+  if (waves < 1 || waves > 16) {
+    snprintf(err, errlen, "gemv: waves per block must be 1..16");
     return -1;
   }
   int R = 1;
@@ -198,9 +198,13 @@ extern "C" int thvm_k_gemv(const ThvmGemvArgs *a, hipStream_t s, char *err, int 
   // o 6.8 -> 6.6 us.  Long rows (C4 down, U = 8: 14.0 -> 15.3 us) and rows
   // that leave lanes idle (C3 K = 1600 fp16, C1 K = 768 f32: slower steps)
   // keep 8.
+  // The wave count is the one that makes the grid exactly one block per CU
+  // (ceil(Gr / 256), 9..16 waves): C4 qkv's 3072 row pairs take 12-wave
+  // blocks, 256 of them, where 16-wave blocks had left 64 CUs idle (192
+  // blocks) and so read a third more bytes per busy CU.
   if (!a->tune_waves && Mk == 1 && chunks == 1 && (uint64_t)a->K * wsz / 16 == 64u * (uint32_t)U &&
       (Gr + 7) / 8 > 256 && (Gr + 15) / 16 <= 256) {
-    waves = 16;
+    waves = (Gr + 255) / 256;
   }
   uint32_t need = (Gr + waves - 1) / waves;
   uint32_t grid = need;

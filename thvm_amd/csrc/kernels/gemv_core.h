@@ -204,12 +204,15 @@ __device__ __forceinline__ float rnd_x(float v) {
 // epilogue with the raw sums.  COH selects system-scope x loads and epilogue
 // accesses (data shared between the blocks of one launch).  x staging uses
 // the first nthr threads (nw = nthr / 64 waves reduce a fused norm); the rest
-// of the block only joins its barriers.  Returns false when wait() did.
+// of the block only joins its barriers.  bdim is the block size, read once by
+// the caller (bdim inside a loop was re-read from the implicit kernel
+// arguments with a vector load and a full wait, between the early x loads).
+// Returns false when wait() did.
 template <int WT, int XD, int M, int R, int U, bool COH, class WaitF, class XRowF, class HookF>
 __device__ __forceinline__ bool gemv_core(const ThvmGemvArgs &a, unsigned char *xs_raw, float *red,
                                           const uint32_t g, const uint32_t gstride,
                                           const uint32_t nthr, const int nw, WaitF &&wait,
-                                          XRowF &&xrow, HookF &&hook) {
+                                          XRowF &&xrow, HookF &&hook, const uint32_t bdim) {
   constexpr int E = WTr<WT>::E;
   // LDS keeps x in its 16-bit storage type unless weights or x are f32
   constexpr int XT = (WT == WT_F32 || XD == XD_F32) ? XT_F32 : (XD == XD_BF16 ? XT_BF16 : XT_F16);
@@ -230,21 +233,65 @@ __device__ __forceinline__ bool gemv_core(const ThvmGemvArgs &a, unsigned char *
   // measured slower).  With more rows (x would hold too many registers across
   // the weight loads) and in the persistent kernel (COH: x is written by other
   // blocks of the launch and is read only after wait()), the weights go first.
-  uint4 wq[R][U];
-  auto load_batch = [&](uint32_t gg, uint32_t c0) {
-    const uint32_t n0 = gg * R;
+  // The weight loads of row group gg, chunk batch c0: raw buffer loads
+  // through a resource over the group's rows, so a row past N or a chunk past
+  // C reads zero by the hardware range check with no memory access and every
+  // wave issues the same load instructions whatever the bounds.  (A guarded
+  // load is branched around; the compiler then cannot count the loads issued
+  // after any earlier one and makes every wait drain all of them, vmcnt(0):
+  // x staging waited for the whole first weight batch and each row group's
+  // epilogue for the next batch.)  The resource base is wave-uniform.
+  auto wload = [&](uint4 (&X)[R][U], uint32_t gg, uint32_t c0) {
+    const bool gok = gg < G;
+    const uint32_t n0 = gok ? gg * R : 0u;
+    const uint32_t nr = gok ? (N - n0 < (uint32_t)R ? N - n0 : (uint32_t)R) : 0u;
+    const uint64_t base = (uint64_t)(uintptr_t)wb + (uint64_t)n0 * rowbytes;
+    const uint32_t blo = __builtin_amdgcn_readfirstlane((uint32_t)base);
+    const uint32_t bhi = __builtin_amdgcn_readfirstlane((uint32_t)(base >> 32));
+    const buf_t rs = buf_rsrc((const void *)(uintptr_t)(((uint64_t)bhi << 32) | blo),
+                              __builtin_amdgcn_readfirstlane(nr * (uint32_t)rowbytes));
 #pragma unroll
     for (int r = 0; r < R; r++) {
-      const bool rok = gg < G && (n0 + r) < N;
-      const char *rp = wb + (uint64_t)(n0 + r) * rowbytes;
 #pragma unroll
       for (int u = 0; u < U; u++) {
         const uint32_t c = c0 + u * 64 + lane;
-        if (rok && c < C) wq[r][u] = ld_stream16(rp + (uint64_t)c * 16);
-        else wq[r][u] = make_uint4(0, 0, 0, 0);
+        X[r][u] = buf_ld_stream16(rs, c < C ? (uint32_t)(r * rowbytes) + c * 16u : BUF_OOB);
       }
     }
   };
+  uint4 wq[R][U];
+  auto load_batch = [&](uint32_t gg, uint32_t c0) { wload(wq, gg, c0); };
+  // The first row group's epilogue operands (standalone kernel), issued
+  // before x and the weights so the epilogue waits for no round trip of its
+  // own (the qkv epilogue's len -> cos/sin chain was two): unconditional
+  // buffer loads, an operand the epilogue does not use reads zero through an
+  // empty range; the RoPE pair follows once the position is back (after x
+  // staging).  Values only: the epilogue's arithmetic is unchanged.
+  constexpr bool PRE = !COH;
+  EpiPre<R, M> pre;
+  uint32_t pre_len = 0;
+  const bool pre_qkv = a.epi == THVM_EPI_QKV || a.epi == THVM_EPI_QKV_ROPE;
+  const uint32_t pre_n0 = (g < G ? g : 0u) * R;
+  if (PRE) {
+    const buf_t rsc = buf_rsrc(a.scale, a.scale ? N * 4u : 0u);
+#pragma unroll
+    for (int r = 0; r < R; r++) pre.sc[r] = buf_ld4(rsc, (pre_n0 + r) * 4u);
+    const bool resid = a.epi == THVM_EPI_RESID && a.res != nullptr;
+    const uint32_t ys = a.ydt == THVM_DT_FP32 ? 4u : 2u;
+    const buf_t rrs = buf_rsrc(a.res, resid ? (uint32_t)M * a.ldy * ys : 0u);
+    // (two 16-bit halves per value whatever the type -- one load kind, so
+    // the instruction stream does not branch on the type)
+#pragma unroll
+    for (int r = 0; r < R; r++)
+#pragma unroll
+      for (int m = 0; m < M; m++) {
+        const uint32_t off = ((uint32_t)m * a.ldy + pre_n0 + r) * ys;
+        const uint32_t lo = buf_ld2(rrs, off), hi = buf_ld2(rrs, ys == 4u ? off + 2u : BUF_OOB);
+        pre.rv[r][m] = lo | (hi << 16);
+      }
+    const buf_t rls = buf_rsrc(a.len, pre_qkv ? 4u : 0u);
+    pre_len = buf_ld4(rls, 0);
+  }
   const uint32_t NVt = K / VE;           // x vectors per row
   // (with a fused norm, threads at or beyond nthr take no part in the staging
   // but join its block barriers: the norm's reduction order is that of an
@@ -254,7 +301,7 @@ __device__ __forceinline__ bool gemv_core(const ThvmGemvArgs &a, unsigned char *
   constexpr int NVN = XREG / VE;         // fused norm: x vectors per thread
   constexpr int NPRE = XN > NVN ? XN : NVN;
   // x row 0 as raw 16-byte vectors (!COH): the norm path's vectors tid + j*nthr,
-  // or the no-norm path's first pass threadIdx.x + j*blockDim.x (clamped
+  // or the no-norm path's first pass threadIdx.x + j*bdim (clamped
   // indices; out-of-row vectors are never stored)
   constexpr bool XPRE = !COH && M == 1 && XD != XD_F32;
   uint4 xpre[NPRE];
@@ -264,7 +311,7 @@ __device__ __forceinline__ bool gemv_core(const ThvmGemvArgs &a, unsigned char *
     for (int j = 0; j < NPRE; j++) {
       // (a uniform skip of vectors past the row for every thread: K below
       // the staging's reach needs fewer loads)
-      const uint32_t stride = a.norm == 0 ? blockDim.x : nthr;
+      const uint32_t stride = a.norm == 0 ? bdim : nthr;
       if ((a.norm == 0 ? j >= XN : j >= NVN) || j * stride >= NVt) break;
       const uint32_t v = (a.norm == 0 ? threadIdx.x : tid) + j * stride;
       const uint32_t vc = v < NVt ? v : 0;
@@ -312,12 +359,12 @@ __device__ __forceinline__ bool gemv_core(const ThvmGemvArgs &a, unsigned char *
     if (a.norm == 0) {
       // no reduction: every thread of the block stages, XN vectors of x in
       // flight per thread before the first LDS store
-      for (uint32_t v0 = threadIdx.x; v0 < NVt; v0 += XN * blockDim.x) {
+      for (uint32_t v0 = threadIdx.x; v0 < NVt; v0 += XN * bdim) {
         float f[XN][VE];
         const bool first = v0 == threadIdx.x;
 #pragma unroll
         for (int j = 0; j < XN; j++) {
-          const uint32_t v = v0 + j * blockDim.x;
+          const uint32_t v = v0 + j * bdim;
           if (v < NVt) {
             if (pre && first) xdec<XD>(xpre[j], f[j]);
             else xvec<XD, COH>(xr, (uint64_t)v * VE, f[j]);
@@ -325,7 +372,7 @@ __device__ __forceinline__ bool gemv_core(const ThvmGemvArgs &a, unsigned char *
         }
 #pragma unroll
         for (int j = 0; j < XN; j++) {
-          const uint32_t v = v0 + j * blockDim.x;
+          const uint32_t v = v0 + j * bdim;
           if (v < NVt) {
 #pragma unroll
             for (int i = 0; i < VE; i++) xs_store<XT>(xs_raw, xs_index<XT, E>(K, C, m, v * VE + i), f[j][i]);
@@ -383,6 +430,26 @@ __device__ __forceinline__ bool gemv_core(const ThvmGemvArgs &a, unsigned char *
   }
   __syncthreads();
   pclk(clk, a.clk_cap, 2);
+  if (PRE) {   // the position is back (loaded first): the RoPE pair's loads
+    // (the empty asm keeps the loaded length in a vector register and its
+    // first use here: read as a uniform value, the compiler moved it to a
+    // scalar register right after the load and waited for it before x)
+    asm volatile("" : "+v"(pre_len));
+    pre.pos = (int32_t)pre_len - 1;
+    const uint32_t hd = a.head_dim ? a.head_dim : 2u, half = hd / 2;
+    const bool rope = a.epi == THVM_EPI_QKV_ROPE && R == 2 && a.rope_cos && a.rope_sin;
+    const uint32_t tab = rope ? a.max_seq * half * 4u : 0u;
+    const buf_t rcs = buf_rsrc(a.rope_cos, tab), rsn = buf_rsrc(a.rope_sin, tab);
+    const uint32_t d = pre_n0 % hd;
+#pragma unroll
+    for (int m = 0; m < M; m++) {
+      const int32_t pm = pre.pos + (a.spec ? m : 0);
+      const uint32_t pmc = pm >= 0 && (uint32_t)pm < a.max_seq ? (uint32_t)pm : 0u;
+      const uint32_t off = (pmc * half + d / 2) * 4u;
+      pre.cs[m] = __uint_as_float(buf_ld4(rcs, off));
+      pre.sn[m] = __uint_as_float(buf_ld4(rsn, off));
+    }
+  }
 
   // ---- 3. stream the weight rows ----
   // A flat sequence of (row group, chunk batch) steps per wave; two register
@@ -487,25 +554,14 @@ __device__ __forceinline__ bool gemv_core(const ThvmGemvArgs &a, unsigned char *
         }
       if (lane == 0) {
         const uint32_t n0 = (g0 + gi * gstride) * R;
-        gemv_epilogue<R, M, COH>(a, n0, tot);
+        gemv_epilogue<R, M, COH>(a, n0, tot, 0, PRE && gi == 0 ? &pre : nullptr);
         hook(n0, tot);
       }
     }
   };
   auto load_step = [&](uint4 (&X)[R][U], uint32_t t) {
     const uint32_t gi = t / NB, bi = t - gi * NB;
-    const uint32_t gg = g0 + gi * gstride, n0 = gg * R, c0 = bi * 64 * U;
-#pragma unroll
-    for (int r = 0; r < R; r++) {
-      const bool rok = gg < G && (n0 + r) < N;
-      const char *rp = wb + (uint64_t)(n0 + r) * rowbytes;
-#pragma unroll
-      for (int u = 0; u < U; u++) {
-        const uint32_t c = c0 + u * 64 + lane;
-        if (rok && c < C) X[r][u] = ld_stream16(rp + (uint64_t)c * 16);
-        else X[r][u] = make_uint4(0, 0, 0, 0);
-      }
-    }
+    wload(X, g0 + gi * gstride, bi * 64 * U);
   };
   uint4 wq2[R][U];
   for (uint32_t t = 0; t < T; t += 2) {          // step 0 is already in wq

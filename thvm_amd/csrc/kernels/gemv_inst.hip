@@ -32,7 +32,7 @@ __global__ __launch_bounds__(1024) void k_gemv(ThvmGemvArgs a) {
   gemv_core<WT, XD, M, R, U, false>(
       a, xs_raw, red, g, gridDim.x * nw, nthr, (int)(nthr >> 6), [] { return true; },
       [&](int m) { return (const void *)((const char *)a.x + (uint64_t)m * a.ldx * XDr<XD>::B); },
-      [](uint32_t, const float (&)[R][M]) {});
+      [](uint32_t, const float (&)[R][M]) {}, (uint32_t)blockDim.x);
   pclk_end(a.clk, a.clk_cap);
 }
 

@@ -154,14 +154,15 @@ __device__ __attribute__((noinline)) bool step_gemv(const ThvmStepArgs &a, uint3
         if (st_better(v, (int32_t)n0, bv[m], bi[m])) { bv[m] = v; bi[m] = (int32_t)n0; }
       }
     };
-    ok = gemv_core<WT, XD, M, R, STEP_U, true>(ga, lds, red, g0, gstride, STAGE_THREADS, 8, wait, xr, amhook);
+    ok = gemv_core<WT, XD, M, R, STEP_U, true>(ga, lds, red, g0, gstride, STAGE_THREADS, 8, wait, xr, amhook,
+                                               (uint32_t)blockDim.x);
     if (ok && lane_id() == 0) {
 #pragma unroll
       for (int m = 0; m < M; m++) { step_amv[wv][m] = bv[m]; step_ami[wv][m] = bi[m]; }
     }
   } else {
     ok = gemv_core<WT, XD, M, R, STEP_U, true>(ga, lds, red, g0, gstride, STAGE_THREADS, 8, wait, xr,
-                                               [](uint32_t, const float (&)[R][M]) {});
+                                               [](uint32_t, const float (&)[R][M]) {}, (uint32_t)blockDim.x);
   }
   gs.dclock(sid, 2);
   vm_drain();
