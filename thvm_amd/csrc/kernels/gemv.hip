@@ -167,12 +167,13 @@ extern "C" int thvm_k_gemv(const ThvmGemvArgs *a, hipStream_t s, char *err, int 
     if ((pairs && a->tune_r == 1) || a->N % a->tune_r) { snprintf(err, errlen, "gemv: r=%u does not tile N/epilogue", a->tune_r); return -1; }
     R = (int)a->tune_r;
   }
-  // 16-byte chunks per lane in flight: 8 for one-row waves over long rows
-  // (>= 768 chunks: 2 batches instead of 3-4; measured on gfx950 at the C4
-  // down projection, K = 14336 fp8, 14.4 -> 13.9 us), else 4 (8 would leave
-  // half the lanes idle on 256-chunk rows, and doubles a row pair's registers)
-  const uint64_t row_chunks = (uint64_t)a->K * wsz / 16;
-  int U = a->tune_u ? (int)a->tune_u : (R == 1 && row_chunks >= 768) ? 8 : 4;
+  // 16-byte chunks per lane in flight: 4 (tune_u = 8 doubles them).  With
+  // the weight loads unguarded, so that a wave waits only for the batch it
+  // consumes while the next one is in flight, 4 beats 8 also on long rows
+  // (measured on gfx950 at the C4 down projection, K = 14336 fp8: 12.0
+  // against 12.6 us; before, when every wait drained all loads, 8 had won,
+  // 13.9 against 14.4); 8 would leave half the lanes idle on 256-chunk rows
+  int U = a->tune_u ? (int)a->tune_u : 4;
   if (U != 4 && U != 8) { snprintf(err, errlen, "gemv: u must be 4 or 8"); return -1; }
   uint32_t xsz = (a->xdt == THVM_DT_FP32 || a->wdt == THVM_DT_FP32) ? 4 : 2;
   uint64_t lds = (uint64_t)Mk * a->K * xsz;
