@@ -295,6 +295,19 @@ __global__ __launch_bounds__(MOE_THREADS) void k_moe_gateup(ThvmMoeArgs a) {
   const uint32_t p0 = (blockIdx.x * MOE_WAVES + wv) * PPW;
   const uint64_t rowb = (uint64_t)D * (FP8 ? 1 : 2);
   const uint32_t nch = (uint32_t)(rowb / 16);
+  // every pair's expert first (routed slots from the route picked above, or
+  // from sel in one round of unconditional loads), then all the pairs' row
+  // loads: buffer loads through a resource over the pair's (gate, up) rows,
+  // empty for a pair past P, so no load is branched around and each wait
+  // counts only the loads it needs (a guarded load made every wait drain all
+  // of them: the pairs' rows were requested one pair at a time)
+  const buf_t srs = buf_rsrc(a.sel, a.logits ? 0u : a.B * K * 4u);
+  uint32_t selv[PPW];
+#pragma unroll
+  for (int i = 0; i < PPW; i++) {
+    const uint32_t p = p0 + i, e = p < K * I ? p / I : 0u;
+    selv[i] = buf_ld4(srs, (b * K + e) * 4u);
+  }
   uint4 gq[PPW][NC], uq[PPW][NC];
   uint64_t row0[PPW];
   const float *scp[PPW];
@@ -310,7 +323,7 @@ __global__ __launch_bounds__(MOE_THREADS) void k_moe_gateup(ThvmMoeArgs a) {
 #pragma unroll
         for (uint32_t kk = 0; kk < MOE_MAXK; kk++) id = kk == e ? rids[kk] : id;
       } else {
-        id = a.sel[(uint64_t)b * K + e];
+        id = (int32_t)selv[i];
       }
       id = id < 0 ? 0 : id >= (int32_t)a.E ? (int32_t)a.E - 1 : id;   // a valid expert row
       row0[i] = (uint64_t)id * 2 * I + 2 * r;
@@ -321,8 +334,31 @@ __global__ __launch_bounds__(MOE_THREADS) void k_moe_gateup(ThvmMoeArgs a) {
       base = (const char *)a.wgu_s;
       scp[i] = a.sgu_s;
     }
-    load_row(gq[i], base + row0[i] * rowb, lane, nch, live);
-    load_row(uq[i], base + (row0[i] + 1) * rowb, lane, nch, live);
+    const uint64_t rp = (uint64_t)(uintptr_t)base + row0[i] * rowb;
+    const uint32_t plo = __builtin_amdgcn_readfirstlane((uint32_t)rp);
+    const uint32_t phi = __builtin_amdgcn_readfirstlane((uint32_t)(rp >> 32));
+    const buf_t rrs = buf_rsrc((const void *)(uintptr_t)(((uint64_t)phi << 32) | plo),
+                              __builtin_amdgcn_readfirstlane(live ? 2u * (uint32_t)rowb : 0u));
+#pragma unroll
+    for (int c = 0; c < NC; c++) {
+      const uint32_t ch = lane + 64u * c;
+      gq[i][c] = buf_ld_stream16(rrs, ch < nch ? ch * 16u : BUF_OOB);
+      uq[i][c] = buf_ld_stream16(rrs, ch < nch ? (uint32_t)rowb + ch * 16u : BUF_OOB);
+    }
+  }
+  // the pairs' row scales with the rows (an empty range without scales)
+  uint32_t scg[PPW], scu[PPW];
+#pragma unroll
+  for (int i = 0; i < PPW; i++) {
+    const bool live = p0 + i < P;
+    const uint64_t sp = (uint64_t)(uintptr_t)scp[i];
+    const uint32_t slo = __builtin_amdgcn_readfirstlane((uint32_t)sp);
+    const uint32_t shi = __builtin_amdgcn_readfirstlane((uint32_t)(sp >> 32));
+    const buf_t crs = buf_rsrc((const void *)(uintptr_t)(((uint64_t)shi << 32) | slo),
+                               __builtin_amdgcn_readfirstlane(live && scp[i] ? 0x7fffffffu : 0u));
+    const uint64_t so = row0[i] * 4u;
+    scg[i] = buf_ld4(crs, so < 0x7ffffff0ull ? (uint32_t)so : BUF_OOB);
+    scu[i] = buf_ld4(crs, so < 0x7ffffff0ull ? (uint32_t)so + 4u : BUF_OOB);
   }
   if (xpre) stage_store<true, FP8 ? 16 : 8>(xs, xv, D, 0, 1);
   else stage_swz<true, FP8 ? 16 : 8>(xs, a.x + (uint64_t)b * D, D, 0, 1);
@@ -334,7 +370,7 @@ __global__ __launch_bounds__(MOE_THREADS) void k_moe_gateup(ThvmMoeArgs a) {
     float G = wave_sum(chunk_dot<FP8>(gq[i], xs, lane, nch));
     float U = wave_sum(chunk_dot<FP8>(uq[i], xs, lane, nch));
     if (lane == 0) {
-      if (scp[i]) { G *= scp[i][row0[i]]; U *= scp[i][row0[i] + 1]; }
+      if (scp[i]) { G *= __uint_as_float(scg[i]); U *= __uint_as_float(scu[i]); }
       a.h[(uint64_t)b * P + p] = silu_f(G) * U;
     }
   }
