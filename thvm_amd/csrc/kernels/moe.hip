@@ -92,21 +92,32 @@ __global__ __launch_bounds__(RT_THREADS) void k_moe_gate(ThvmGateArgs a) {
   const uint64_t xo = (uint64_t)b * D;
   const float invK = 1.0f / (float)D;
   // x and the gains first: the loads return in issue order, so the norm
-  // runs while the expert rows are in flight
-  float xv[RT_NREG], gw[RT_NREG];
-  if (tid < RT_NORM_THREADS) {
+  // runs while the expert rows are in flight.  Every load is an unguarded
+  // buffer load (out-of-range offsets read zero with no access: threads past
+  // the norm's 256, elements past D, experts past E), so no load is branched
+  // around and each wait counts only the loads it needs.
+  const buf_t xr = buf_rsrc((const bf16_t *)a.x + xo, D * 2u);
+  const buf_t gr = buf_rsrc(a.w, a.w ? D * 4u : 0u);
+  const buf_t wr = buf_rsrc(W, E * C * 16u);
+  uint32_t xb[RT_NREG], gb[RT_NREG];
 #pragma unroll
-    for (int i = 0; i < RT_NREG; i++) {
-      const uint32_t k = tid + i * RT_NORM_THREADS, kc = k < D ? k : 0;
-      xv[i] = k < D ? bf2f(((const bf16_t *)a.x)[xo + k]) : 0.0f;
-      gw[i] = a.w ? a.w[kc] : 1.0f;
-    }
+  for (int i = 0; i < RT_NREG; i++) {
+    const uint32_t k = tid + i * RT_NORM_THREADS;
+    const bool ok = tid < RT_NORM_THREADS && k < D;
+    xb[i] = buf_ld2(xr, ok ? k * 2u : BUF_OOB);
+    gb[i] = buf_ld4(gr, ok ? k * 4u : BUF_OOB);
   }
   uint4 wq[NCH];
 #pragma unroll
   for (int t = 0; t < NCH; t++) {
     const uint32_t c = lane + 64u * t;
-    wq[t] = (e < E && c < C) ? ld_stream16((const char *)(W + (uint64_t)e * C + c)) : make_uint4(0, 0, 0, 0);
+    wq[t] = buf_ld_stream16(wr, e < E && c < C ? (e * C + c) * 16u : BUF_OOB);
+  }
+  float xv[RT_NREG], gw[RT_NREG];
+#pragma unroll
+  for (int i = 0; i < RT_NREG; i++) {
+    xv[i] = bf2f((bf16_t)xb[i]);               // 0 past D
+    gw[i] = a.w ? __uint_as_float(gb[i]) : 1.0f;
   }
   if (tid < RT_NORM_THREADS) {
     float s2 = 0.0f;
@@ -190,13 +201,22 @@ __device__ __forceinline__ float chunk_dot(const uint4 (&q)[NC], const float *v,
   return acc;
 }
 
+// one row's NC chunks per lane: unguarded buffer loads over the row (an
+// empty range when !ok, chunks past nch out of range: zeros, no access), so
+// the loads are never branched around and later waits count only what they
+// need; the row address is wave-uniform
 template <int NC>
 __device__ __forceinline__ void load_row(uint4 (&q)[NC], const char *row, uint32_t lane,
                                          uint32_t nch, bool ok) {
+  const uint64_t rp = (uint64_t)(uintptr_t)row;
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)rp);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(rp >> 32));
+  const buf_t r = buf_rsrc((const void *)(uintptr_t)(((uint64_t)hi << 32) | lo),
+                           __builtin_amdgcn_readfirstlane(ok ? nch * 16u : 0u));
 #pragma unroll
   for (int c = 0; c < NC; c++) {
     const uint32_t ch = lane + 64u * c;
-    q[c] = (ok && ch < nch) ? ld_stream16(row + (uint64_t)ch * 16) : make_uint4(0, 0, 0, 0);
+    q[c] = buf_ld_stream16(r, ch < nch ? ch * 16u : BUF_OOB);
   }
 }
 
