@@ -649,24 +649,41 @@ PHASES = {
     "attn": ["entry", "loads issued + q", "first chunk consumed", "chunks done", "row groups combined",
              "waves in LDS", "", "end (drained)"],
     "merge": ["entry", "partials folded", "partitions combined", "", "", "", "", "end (drained)"],
+    "mla_prep": ["entry", "q nope staged / latent row read", "", "", "", "", "", "end (drained)"],
+    "mla_split": ["entry", "q staged", "first chunk scored", "first chunk softmax", "chunks done",
+                  "rows issued", "t0 rows arrived", "end (drained)"],
+    "mla_out": ["entry", "split weights", "partials summed", "olat in LDS", "loads issued",
+                "t0 m,l arrived", "t0 W_uv arrived", "end (drained)"],
+    "moe_gate": ["entry", "loads issued", "x normalised", "", "", "", "", "end (drained)"],
+    "moe_gateup": ["entry", "top-K picked", "rows issued", "x staged", "t0 logits arrived", "t0 rows arrived",
+                   "", "end (drained)"],
+    "moe_down": ["entry", "rows issued", "h staged", "half sums", "t0 ids arrived", "t0 rows arrived", "",
+                 "end (drained)"],
 }
+# ops with phase-clock marks: kernel name -> (first launch's kind, second launch's kind or None)
+CLOCKED = {"gemv": ("gemv", None), "attn": ("attn", "merge"), "mla_prep": ("mla_prep", None),
+           "mla_attn": ("mla_split", "mla_out"), "moe_gate": ("moe_gate", None),
+           "moe_gateup": ("moe_gateup", None), "moe_down": ("moe_down", None)}
 
 
 def _clock_record(rec, name, kern, c):
     """Fold one launch's clock slots ([2][blocks][10]) into rec: per mark, the
     median and the maximum over blocks in us after the earliest block's entry,
-    and per XCD the earliest entry (launch stagger across the 8 XCDs)."""
+    and per XCD the earliest entry (launch stagger across the 8 XCDs).
+    Returns the op's earliest entry and latest end (clock ticks) for the
+    layer timeline."""
     import numpy as np
-    parts = [("gemv" if kern == "gemv" else "attn", c[0])]
-    if kern == "attn" and c[1, :, 0].any():
-        parts.append(("merge", c[1]))
+    k0, k1 = CLOCKED[kern]
+    parts = [(k0, c[0])]
+    if k1 and c[1, :, 0].any():
+        parts.append((k1, c[1]))
     if not (c[0, :, 0] > 0).any():
         raise RuntimeError(f"{name}: no phase-clock marks recorded (the kernels come from the "
                            "measurement build libthvm_hip_pclk.so: python -m thvm_amd.build --variant pclk)")
     t0 = min(int(p[p[:, 0] > 0, 0].min()) for _, p in parts)
     for pname, p in parts:
         live = p[p[:, 0] > 0]
-        key = f"{name}/{pname}" if pname == "merge" else name
+        key = f"{name}/{pname}" if pname == k1 else name
         r = rec.setdefault(key, {"kind": pname, "blocks": len(live), "marks": [], "xcd_entry": []})
         row = []
         for m in range(8):
@@ -678,10 +695,12 @@ def _clock_record(rec, name, kern, c):
         xe = [float((live[live[:, 8] == x, 0] - t0).min()) / 100.0 if (live[:, 8] == x).any() else None
               for x in range(8)]
         r["xcd_entry"].append(xe)
+    ends = [int(p[p[:, 7] > 0, 7].max()) for _, p in parts if (p[:, 7] > 0).any()]
+    return t0, (max(ends) if ends else t0)
 
 
 def run_phase_clock(thvm, args) -> dict:
-    """Per-phase clock of one layer's kernels inside an eager C4 step: the
+    """Per-phase clock of one layer's kernels inside an eager step: the
     step runs op by op; the ops of layer `--clock-layer` are re-dispatched
     with the builtin's clk= option (thread 0 of every block records the 100
     MHz wall clock at marks; see the kernels' pclk calls).  Per op and mark:
@@ -704,7 +723,7 @@ def run_phase_clock(thvm, args) -> dict:
     CAP, NS = 2048, 10
     clk = thvm.Buffer(CAP * 2 * NS * 8)
     zero = np.zeros(CAP * 2 * NS, np.uint64)
-    rec, raw = {}, {}
+    rec, raw, timeline = {}, {}, {}
     if args.clock_graph:
         # the whole step captured as one graph (as the decoder replays it), the
         # layer's GEMV / attention ops with clocks of their own
@@ -713,7 +732,7 @@ def run_phase_clock(thvm, args) -> dict:
             for i in range(len(tags)):
                 name, prog, ids = dec.op_info(i)
                 kern = prog.split()[0].split(":")[1]
-                if i in ops and kern in ("gemv", "attn"):
+                if i in ops and kern in CLOCKED:
                     bufs[i] = thvm.Buffer(CAP * 2 * NS * 8)
                     bufs[i].write(zero)
                     thvm.dispatch(name, prog + f" clk={CAP}", ids + [bufs[i].id])
@@ -725,10 +744,16 @@ def run_phase_clock(thvm, args) -> dict:
                 b.write(zero)
             j.replay()
             thvm.synchronize()
+            spans = {}
             for i, name, kern in info:
                 c = bufs[i].read(np.uint64).reshape(2, CAP, NS).astype(np.int64)
                 raw.setdefault(name, []).append(c.copy())
-                _clock_record(rec, name, kern, c)
+                spans[name] = _clock_record(rec, name, kern, c)
+            # the layer timeline: each op's first entry and last end after
+            # the layer's first op entered (launch gaps between the ops)
+            base = min(v[0] for v in spans.values())
+            for name, (t0, t1) in spans.items():
+                timeline.setdefault(name, []).append(((t0 - base) / 100.0, (t1 - base) / 100.0))
         j.drop()
     for s in range(0 if args.clock_graph else args.steps):
         i = 0
@@ -742,7 +767,7 @@ def run_phase_clock(thvm, args) -> dict:
                 continue
             name, prog, ids = dec.op_info(i)
             kern = prog.split()[0].split(":")[1]
-            if kern not in ("gemv", "attn"):
+            if kern not in CLOCKED:
                 dec.run_ops(i, 1)
                 i += 1
                 continue
@@ -769,9 +794,13 @@ def run_phase_clock(thvm, args) -> dict:
         xe = np.array([[v if v is not None else np.nan for v in row] for row in r["xcd_entry"]])
         stagger = [round(float(v), 2) for v in np.nanmedian(xe, 0)]
         out[key] = {"blocks": r["blocks"], "marks": marks, "xcd_first_entry_us": stagger}
+        if key in timeline:
+            tl = np.array(timeline[key])
+            out[key]["layer_span_us"] = [round(float(np.median(tl[:, 0])), 2), round(float(np.median(tl[:, 1])), 2)]
         log(f"[clock] {key} ({r['blocks']} blocks): " +
             ", ".join(f"{k} {v['median_us']}/{v['max_us']}" for k, v in marks.items()) +
-            f"; first entry per XCD {stagger}")
+            f"; first entry per XCD {stagger}" +
+            (f"; in layer {out[key]['layer_span_us']}" if "layer_span_us" in out[key] else ""))
     dec.close()
     return {"metric": "phase clock (us after the earliest block's entry: median/max over blocks)",
             "config": {"workload": spec["name"], "layer": layer, "batch": args.batch, "steps": args.steps,

@@ -311,7 +311,8 @@ int hb_builtin_launch(const char *program, const u32 *ids, u32 n, int check_only
          spec_f32(&sp, "eps", &a.eps, 0, 1e-6f) || spec_f32(&sp, "scale", &a.scale, !prep, 0));
     NEED(spec_u32(&sp, "ldq", &a.ldq, 0, a.H * (a.dn + a.dr) + a.kv + a.dr) ||
          spec_u32(&sp, "nsplit", &a.n_split, 0, (a.max_seq + 63) / 64) ||
-         spec_u32(&sp, "mode", &a.mode, 0, 0) || spec_u32(&sp, "cpb", &a.cpb, 0, 0));
+         spec_u32(&sp, "mode", &a.mode, 0, 0) || spec_u32(&sp, "cpb", &a.cpb, 0, 0) ||
+         spec_u32(&sp, "clk", &a.clk_cap, 0, 0));
     const u32 wsz = hb_dt_size(a.wdt);
     const int fp8 = a.wdt == THVM_DT_FP8E4M3;
     if (!wsz) { hb_set_error("builtin %s: bad weight dtype", K); return -1; }
@@ -342,6 +343,9 @@ int hb_builtin_launch(const char *program, const u32 *ids, u32 n, int check_only
       if (fp8) a.suv = (const float *)arg(&c, slot++, (u64)a.H * a.dv * 4);
       bytes = 0; /* live-length dependent: the decoder accounts for it */
     }
+    /* clk=<blocks>: a phase-clock buffer after the others (mla_attn: split
+     * blocks, then merge blocks) */
+    if (a.clk_cap) a.clk = (uint64_t *)arg(&c, slot++, (u64)a.clk_cap * (prep ? 1 : 2) * 80);
     if (c.bad) return -1;
     if (check_only) return 0;
     if (prof) hb_kprof_begin(K, &e0, &e1);
@@ -364,12 +368,14 @@ int hb_builtin_launch(const char *program, const u32 *ids, u32 n, int check_only
     ThvmGateArgs a;
     memset(&a, 0, sizeof a);
     NEED(spec_u32(&sp, "b", &a.B, 1, 0) || spec_u32(&sp, "d", &a.D, 1, 0) ||
-         spec_u32(&sp, "e", &a.E, 1, 0) || spec_f32(&sp, "eps", &a.eps, 0, 1e-6f));
+         spec_u32(&sp, "e", &a.E, 1, 0) || spec_f32(&sp, "eps", &a.eps, 0, 1e-6f) ||
+         spec_u32(&sp, "clk", &a.clk_cap, 0, 0));
     a.xn = (float *)arg(&c, 0, (u64)a.B * a.D * 4);
     a.logits = (float *)arg(&c, 1, (u64)a.B * a.E * 4);
     a.x = arg(&c, 2, (u64)a.B * a.D * 2);
     a.w = (const float *)arg(&c, 3, (u64)a.D * 4);
     a.gate = (const float *)arg(&c, 4, (u64)a.E * a.D * 4);
+    if (a.clk_cap) a.clk = (uint64_t *)arg(&c, 5, (u64)a.clk_cap * 80);
     if (c.bad) return -1;
     bytes = (u64)a.E * a.D * 4 + (u64)a.B * a.D * 6 + (u64)a.B * a.E * 4;
     if (check_only) return 0;
@@ -384,7 +390,8 @@ int hb_builtin_launch(const char *program, const u32 *ids, u32 n, int check_only
          spec_u32(&sp, "e", &a.E, 1, 0) || spec_u32(&sp, "k", &a.K, 1, 0) ||
          spec_u32(&sp, "i", &a.I, 1, 0) || spec_u32(&sp, "s", &a.S, 0, 0) ||
          spec_u32(&sp, "wt", &a.wdt, 0, THVM_DT_FP8E4M3) || spec_u32(&sp, "grouped", &a.grouped, 0, 0) ||
-         spec_u32(&sp, "route", &route, 0, 0) || spec_u32(&sp, "tiled", &a.wtiled, 0, 0));
+         spec_u32(&sp, "route", &route, 0, 0) || spec_u32(&sp, "tiled", &a.wtiled, 0, 0) ||
+         spec_u32(&sp, "clk", &a.clk_cap, 0, 0));
     if (route && !gu) { hb_set_error("builtin moe_down: route=1 is a gate/up key"); return -1; }
     const u32 wsz = hb_dt_size(a.wdt);
     const int fp8 = a.wdt == THVM_DT_FP8E4M3;
@@ -432,6 +439,7 @@ int hb_builtin_launch(const char *program, const u32 *ids, u32 n, int check_only
         bytes = 0;
       }
     }
+    if (a.clk_cap) a.clk = (uint64_t *)arg(&c, slot++, (u64)a.clk_cap * 80);
     if (c.bad) return -1;
     if (check_only) return 0;
     if (prof) hb_kprof_begin(K, &e0, &e1);

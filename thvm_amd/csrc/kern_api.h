@@ -188,6 +188,10 @@ typedef struct ThvmMlaArgs {
    * rope 64, the VALU split otherwise; 1 VALU; 2 MFMA) and 64-row chunks per
    * split block (0 auto; the MFMA split takes 1, 2 or 4) */
   uint32_t mode, cpb;
+  /* phase clock (measurement build only; NULL = off): mla_attn records the
+   * split's blocks, then the merge's, clk_cap blocks each */
+  uint64_t *clk;
+  uint32_t clk_cap;
 } ThvmMlaArgs;
 int thvm_k_mla_prep(const ThvmMlaArgs *a, hipStream_t s, char *err, int errlen);
 int thvm_k_mla_attn(const ThvmMlaArgs *a, hipStream_t s, char *err, int errlen);
@@ -212,6 +216,8 @@ typedef struct ThvmGateArgs {
   float *xn; float *logits;
   uint32_t B, D, E;
   float eps;
+  uint64_t *clk;           /* phase clock (measurement only; NULL = off) */
+  uint32_t clk_cap;
 } ThvmGateArgs;
 int thvm_k_moe_gate(const ThvmGateArgs *a, hipStream_t s, char *err, int errlen);
 
@@ -252,6 +258,8 @@ typedef struct ThvmMoeArgs {
    * tile layout of thvm_k_tile_w, 32 bytes per lane for gate/up and 16 for
    * down (each expert's rows a whole number of 16-row groups) */
   uint32_t wtiled;
+  uint64_t *clk;           /* phase clock (measurement only; NULL = off) */
+  uint32_t clk_cap;
 } ThvmMoeArgs;
 /* plan / part scratch sizes in bytes for the grouped form */
 uint64_t thvm_k_moe_plan_bytes(uint32_t B, uint32_t E, uint32_t K);

@@ -176,6 +176,15 @@ typedef __amdgpu_buffer_rsrc_t buf_t;
 __device__ __forceinline__ buf_t buf_rsrc(const void *p, uint32_t bytes) {
   return __builtin_amdgcn_make_buffer_rsrc((void *)p, 0, (int)bytes, 0x00020000);
 }
+// the same over a base and range that are wave-uniform but held in VGPRs:
+// their first lane's values (readfirstlane keeps the resource in SGPRs, where
+// a per-lane resource compiles to a waterfall loop around every load)
+__device__ __forceinline__ buf_t buf_rsrc_u(const void *p, uint32_t bytes) {
+  const uint64_t v = (uint64_t)(uintptr_t)p;
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+  return buf_rsrc((const void *)(uintptr_t)(((uint64_t)hi << 32) | lo), __builtin_amdgcn_readfirstlane(bytes));
+}
 __device__ __forceinline__ uint4 buf_ld16(buf_t r, uint32_t off) {
   u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
   return make_uint4(v[0], v[1], v[2], v[3]);
@@ -252,6 +261,17 @@ __device__ __forceinline__ void pclk(uint64_t *clk, uint32_t cap, int i) {
     p[8] = xcc;
     p[9] = hw;
   }
+}
+// mark i once thread 0 holds v (the empty asm needs v in a register, so the
+// wait for its load comes first)
+__device__ __forceinline__ void pclk_after(uint64_t *clk, uint32_t cap, int i, uint32_t v) {
+#ifndef THVM_PCLK
+  (void)clk; (void)cap; (void)i; (void)v;
+  return;
+#endif
+  if (clk == nullptr || threadIdx.x != 0) return;
+  asm volatile("" ::"v"(v));
+  pclk(clk, cap, i);
 }
 __device__ __forceinline__ void pclk_end(uint64_t *clk, uint32_t cap) {
 #ifndef THVM_PCLK

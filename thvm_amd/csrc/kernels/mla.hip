@@ -71,43 +71,68 @@ __device__ __forceinline__ float group_sum(float v, int G) {
 // block per (h, 64 rows) over all 32 rows of C5 batch 32 left 160 blocks,
 // each a 32-step serial loop: 33.7 us; groups of 8 rows give 512 blocks.)
 #define MLA_PREP_ROWS 8
+#define MLA_PREP_PASS 4    /* W_uk row passes requested at once */
 template <bool FP8>
 __global__ __launch_bounds__(256) void k_mla_prep(ThvmMlaArgs a) {
   extern __shared__ float sm[];
   const uint32_t H = a.H, dn = a.dn, dr = a.dr, kv = a.kv, half = dr / 2, qs = dn + dr;
   const uint32_t qoff = H * qs, QB = kv / 64, BG = (a.B + MLA_PREP_ROWS - 1) / MLA_PREP_ROWS;
   const int32_t pos = a.len[0] - 1;
+  // phase clock: 0 entry, 1 q nope staged (absorption blocks) or latent row
+  // read (the append block), 7 drained
+  pclk(a.clk, a.clk_cap, 0);
   if (blockIdx.x < H * QB * BG) {
     const uint32_t h = blockIdx.x / (QB * BG), rem = blockIdx.x % (QB * BG);
     const uint32_t k0 = (rem / BG) * 64, b0 = (rem % BG) * MLA_PREP_ROWS;
     const uint32_t nb = min(a.B - b0, (uint32_t)MLA_PREP_ROWS);
-    // q nope of the group's batch rows into LDS (f32)
-    for (uint32_t i = threadIdx.x; i < nb * dn; i += blockDim.x) {
-      const uint32_t b = i / dn, d = i % dn;
-      sm[i] = bfv(a.qkv, (uint64_t)(b0 + b) * a.ldq + h * qs + d);
-    }
-    __syncthreads();
     const uint32_t rowb = dn * (FP8 ? 1 : 2), LPR = rowb / 16;     // lanes per row
     const uint32_t lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
     const uint32_t rpp = 64 / LPR;                                 // rows per wave pass
     const uint32_t sub = lane / LPR, c = lane % LPR;
-    for (uint32_t r0 = wv * rpp; r0 < 64; r0 += 4 * rpp) {
-      const uint32_t k = k0 + r0 + sub;
-      const bool ok = r0 + sub < 64 && k < kv;
-      const uint64_t row = (uint64_t)h * kv + (ok ? k : 0);
-      const char *wp = (const char *)a.wuk + row * rowb + (uint64_t)c * 16;
-      uint4 q0 = ok ? ld_stream16(wp) : make_uint4(0, 0, 0, 0), q1 = make_uint4(0, 0, 0, 0);
-      float w[16];
-      w16<FP8>(q0, q1, w);
-      const uint32_t e0 = c * (FP8 ? 16 : 8), ne = FP8 ? 16 : 8;
-      const float s = a.suk ? a.suk[row] : 1.0f;
-      for (uint32_t b = 0; b < nb; b++) {
-        float acc = 0.0f;
-        for (uint32_t i = 0; i < ne; i++) acc += sm[b * dn + e0 + i] * w[i];
-        acc = group_sum(acc, (int)LPR);
-        if (ok && c == 0) a.qlat[((uint64_t)(b0 + b) * H + h) * kv + k] = acc * s;
+    const uint32_t npass = (64 + 4 * rpp - 1) / (4 * rpp);
+    // head h's W_uk rows and scales through buffer resources (rows past kv
+    // read zero): MLA_PREP_PASS passes' rows are requested before q nope is
+    // staged, so the block waits one round trip for both instead of one per
+    // pass
+    const buf_t wr = buf_rsrc((const char *)a.wuk + (uint64_t)h * kv * rowb, kv * rowb);
+    const buf_t sr = buf_rsrc(a.suk ? a.suk + (uint64_t)h * kv : nullptr, a.suk ? kv * 4u : 0u);
+    for (uint32_t pg = 0; pg < npass; pg += MLA_PREP_PASS) {
+      uint4 wq[MLA_PREP_PASS];
+      uint32_t sq[MLA_PREP_PASS];
+#pragma unroll
+      for (int p = 0; p < MLA_PREP_PASS; p++) {
+        const uint32_t r = wv * rpp + (pg + p) * 4 * rpp + sub, k = k0 + r;
+        const bool ok = pg + p < npass && r < 64 && k < kv;
+        wq[p] = buf_ld_stream16(wr, ok ? k * rowb + c * 16u : BUF_OOB);
+        sq[p] = buf_ld4(sr, ok ? k * 4u : BUF_OOB);
+      }
+      if (pg == 0) {
+        // q nope of the group's batch rows into LDS (f32)
+        for (uint32_t i = threadIdx.x; i < nb * dn; i += blockDim.x) {
+          const uint32_t b = i / dn, d = i % dn;
+          sm[i] = bfv(a.qkv, (uint64_t)(b0 + b) * a.ldq + h * qs + d);
+        }
+        __syncthreads();
+        pclk(a.clk, a.clk_cap, 1);
+      }
+#pragma unroll
+      for (int p = 0; p < MLA_PREP_PASS; p++) {
+        const uint32_t r = wv * rpp + (pg + p) * 4 * rpp + sub, k = k0 + r;
+        if (pg + p >= npass) break;                              // block-uniform
+        const bool ok = r < 64 && k < kv;
+        float w[16];
+        w16<FP8>(wq[p], make_uint4(0, 0, 0, 0), w);
+        const uint32_t e0 = c * (FP8 ? 16 : 8), ne = FP8 ? 16 : 8;
+        const float s = a.suk ? __uint_as_float(sq[p]) : 1.0f;
+        for (uint32_t b = 0; b < nb; b++) {
+          float acc = 0.0f;
+          for (uint32_t i = 0; i < ne; i++) acc += sm[b * dn + e0 + i] * w[i];
+          acc = group_sum(acc, (int)LPR);
+          if (ok && c == 0) a.qlat[((uint64_t)(b0 + b) * H + h) * kv + k] = acc * s;
+        }
       }
     }
+    pclk_end(a.clk, a.clk_cap);
     return;
   }
   const uint32_t b = blockIdx.x - H * QB * BG;
@@ -133,6 +158,7 @@ __global__ __launch_bounds__(256) void k_mla_prep(ThvmMlaArgs a) {
   float *red = sm + kv;
   if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
   __syncthreads();
+  pclk(a.clk, a.clk_cap, 1);
   float tot = 0.0f;
   for (uint32_t w = 0; w < blockDim.x / 64; w++) tot += red[w];
   const float inv = 1.0f / sqrtf(tot * (1.0f / (float)kv) + a.eps);
@@ -145,6 +171,7 @@ __global__ __launch_bounds__(256) void k_mla_prep(ThvmMlaArgs a) {
     prow[j] = f2bf(xe * c - xo * sn);
     prow[half + j] = f2bf(xo * c + xe * sn);
   }
+  pclk_end(a.clk, a.clk_cap);
 }
 
 // ---- k_mla_split --------------------------------------------------------
@@ -318,6 +345,8 @@ __global__ __launch_bounds__(MLA_THREADS) void k_mla_split(ThvmMlaArgs a) {
 #define MF_CADDR(k) ((k) * 16 + ((k) >> 3) * 16)   /* byte offset of column k in an 8-row group */
 #define MF_RGP (MF_CADDR(512) + 64)        /* LDS pitch of a staged 8-row group (bytes) */
 #define MF_PWP 68                          /* LDS pitch of a head's softmax weights (floats) */
+#define MF_QLP (MF_KV + 4)                 /* LDS pitch of a staged qlat row (floats) */
+static_assert(MF_H * MF_QLP * 4 <= 8 * MF_RGP, "qlat staging fits the latent staging area");
 #define MF_THREADS 512                     /* 8 waves: two per 16-row tile */
 #define MF_KH (MF_KS / 2)                  /* k-steps per wave */
 #define MF_LDS (8 * MF_RGP + MF_KS * 2 * 64 * 16 + MF_H * MF_PWP * 4 + 2 * 4 * MF_H * 4 + 4 * 64 * 16)
@@ -355,23 +384,24 @@ __global__ __launch_bounds__(MF_THREADS) void k_mla_split_mf(ThvmMlaArgs a) {
   const uint32_t cend = min(cbeg + cpb, ((uint32_t)L + 63) / 64);
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, li = lane & 15, lg = lane >> 4;
   const int rt = wv & 3, kh = wv >> 2;                               // row tile, k half
+  // phase clock: 0 entry, 1 q staged, 2 first chunk's scores, 3 first
+  // chunk's softmax, 4 chunks done, 7 drained
+  pclk(a.clk, a.clk_cap, 0);
   const char *ckv = (const char *)a.ckv + (uint64_t)b * a.max_seq * (MF_KV * 2);
   const char *kpe = (const char *)a.kpe + (uint64_t)b * a.max_seq * (MF_DR * 2);
 
   // q first (its staging waits for these loads only), then the first two
   // chunks' rows.  q as A operands (hi, lo) in LDS: fragment f = 64 ks +
   // lane holds head lane % 16, k = 32 ks + 8 (lane / 16) + j; k-steps 0..15
-  // from qlat (f32), 16..17 from qpe (bf16: exact, lo = 0)
+  // from qlat (f32), 16..17 from qpe (bf16: exact, lo = 0).  qlat [16][512]
+  // is read coalesced (thread t: float4s t, t + 512, ...) and regrouped
+  // through LDS -- a fragment's 16 heads lie 2 KB apart, so loading the
+  // fragments directly touched 64 cache lines per load instruction
   const float *ql = a.qlat + (uint64_t)b * MF_H * MF_KV;
   const bf16_t *qp = (const bf16_t *)a.qpe + (uint64_t)b * MF_H * MF_DR;
-  float4 qv[2][2];
-#pragma unroll
-  for (int i = 0; i < 2; i++) {
-    const uint32_t f = tid + MF_THREADS * i, l = f & 63;
-    const uint32_t k0 = (f >> 6) * 32 + (l >> 4) * 8;
-    qv[i][0] = *(const float4 *)(ql + (l & 15) * MF_KV + k0);
-    qv[i][1] = *(const float4 *)(ql + (l & 15) * MF_KV + k0 + 4);
-  }
+  static_assert(MF_H * MF_KV / 4 == 4 * MF_THREADS, "four qlat float4s per thread");
+  const float4 q0 = ((const float4 *)ql)[tid], q1 = ((const float4 *)ql)[tid + MF_THREADS];
+  const float4 q2 = ((const float4 *)ql)[tid + 2 * MF_THREADS], q3 = ((const float4 *)ql)[tid + 3 * MF_THREADS];
   const uint32_t fp = 16 * 64 + (tid & 127), lp = fp & 63;
   const uint4 qpv = *(const uint4 *)(qp + (lp & 15) * MF_DR + ((fp >> 6) - 16) * 32 + (lp >> 4) * 8);
 
@@ -392,13 +422,28 @@ __global__ __launch_bounds__(MF_THREADS) void k_mla_split_mf(ThvmMlaArgs a) {
     }
   };
   issue(cfa, cbeg);
-  if (cbeg + 1 < cend) issue(cfb, cbeg + 1);
 
+  // qlat rows into the latent staging area (free until the first chunk's
+  // scores are done), a head's 512 values at a pitch of MF_QLP floats; the
+  // second chunk's rows go out after these stores (qraw live across that
+  // branch spilled to scratch)
+  float *qs = (float *)cl;
+  pclk(a.clk, a.clk_cap, 5);
+  {
+    const uint32_t e = 4 * tid, r = e / MF_KV, k = e % MF_KV;   // element e + 2048 i: row r + 4 i
+    *(float4 *)(qs + r * MF_QLP + k) = q0;
+    *(float4 *)(qs + (r + 4) * MF_QLP + k) = q1;
+    *(float4 *)(qs + (r + 8) * MF_QLP + k) = q2;
+    *(float4 *)(qs + (r + 12) * MF_QLP + k) = q3;
+  }
+  if (cbeg + 1 < cend) issue(cfb, cbeg + 1);
+  __syncthreads();
 #pragma unroll
   for (int i = 0; i < 2; i++) {
-    const uint32_t f = tid + MF_THREADS * i;
+    const uint32_t f = tid + MF_THREADS * i, l = f & 63;
+    const float *src = qs + (l & 15) * MF_QLP + (f >> 6) * 32 + (l >> 4) * 8;
     uint4 hi, lo;
-    split8(qv[i][0], qv[i][1], hi, lo);
+    split8(*(const float4 *)src, *(const float4 *)(src + 4), hi, lo);
     qa[(f >> 6) * 128 + (f & 63)] = hi;
     qa[(f >> 6) * 128 + 64 + (f & 63)] = lo;
   }
@@ -407,6 +452,7 @@ __global__ __launch_bounds__(MF_THREADS) void k_mla_split_mf(ThvmMlaArgs a) {
     qa[(fp >> 6) * 128 + 64 + lp] = make_uint4(0, 0, 0, 0);
   }
   __syncthreads();
+  pclk(a.clk, a.clk_cap, 1);
 
   float m_run[4], l_run[4];
   f32x4_t oacc[4];
@@ -419,6 +465,7 @@ __global__ __launch_bounds__(MF_THREADS) void k_mla_split_mf(ThvmMlaArgs a) {
   // have consumed it
   auto chunk = [&](uint4 (&cf)[MF_KH], uint32_t c) {
     const uint32_t nj = min((uint32_t)L - c * 64, 64u);
+    if (c == cbeg) pclk_after(a.clk, a.clk_cap, 6, cf[MF_KH - 1].x);
     // 1. this wave's half of its tile's scores: lane holds S[head 4 lg + i]
     //    [row 16 rt + li] over its 9 k-steps (four independent chains)
     f32x4_t sc[4];
@@ -453,6 +500,7 @@ __global__ __launch_bounds__(MF_THREADS) void k_mla_split_mf(ThvmMlaArgs a) {
     if (kh == 1) spart[rt * 64 + lane] = part_s;
     if (c + 2 < cend) issue(cf, c + 2);   // in flight during two chunks' softmax and mix
     __syncthreads();
+    if (c == cbeg) pclk(a.clk, a.clk_cap, 2);
 
     // 2. softmax over the chunk's rows (the first-half waves hold the full
     //    scores), online across the block's chunks
@@ -491,6 +539,7 @@ __global__ __launch_bounds__(MF_THREADS) void k_mla_split_mf(ThvmMlaArgs a) {
       l_run[i] = l_run[i] * al[i] + l;
       m_run[i] = mn[i];
     }
+    if (c == cbeg) pclk(a.clk, a.clk_cap, 3);
     // 3. mix: olat tiles kt = 4 wv + t, lane holds O[head 4 lg + i][16 kt + li]
 #pragma unroll
     for (int t = 0; t < 4; t++)
@@ -515,19 +564,25 @@ __global__ __launch_bounds__(MF_THREADS) void k_mla_split_mf(ThvmMlaArgs a) {
     chunk(cfa, c);
     if (c + 1 < cend) chunk(cfb, c + 1);
   }
+  pclk(a.clk, a.clk_cap, 4);
 
+  // the partial goes out as streaming stores: the merge kernel reads it
+  // from memory, and lines left dirty in L2 would be written back at the
+  // kernel boundary, ahead of the merge
   float *part = a.part + ((uint64_t)b * a.n_split + grp) * MF_H * (MF_KV + 4);
 #pragma unroll
   for (int t = 0; t < 4; t++)
 #pragma unroll
-    for (int i = 0; i < 4; i++) part[(4 * lg + i) * (MF_KV + 4) + (wv * 4 + t) * 16 + li] = oacc[t][i];
+    for (int i = 0; i < 4; i++)
+      __builtin_nontemporal_store(oacc[t][i], part + (4 * lg + i) * (MF_KV + 4) + (wv * 4 + t) * 16 + li);
   if (wv == 0 && li == 0) {
 #pragma unroll
     for (int i = 0; i < 4; i++) {
-      part[(4 * lg + i) * (MF_KV + 4) + MF_KV] = m_run[i];
-      part[(4 * lg + i) * (MF_KV + 4) + MF_KV + 1] = l_run[i];
+      __builtin_nontemporal_store(m_run[i], part + (4 * lg + i) * (MF_KV + 4) + MF_KV);
+      __builtin_nontemporal_store(l_run[i], part + (4 * lg + i) * (MF_KV + 4) + MF_KV + 1);
     }
   }
+  pclk_end(a.clk, a.clk_cap);
 }
 
 // ---- k_mla_out ----------------------------------------------------------
@@ -549,17 +604,15 @@ __global__ __launch_bounds__(MLA_OUT_THREADS) void k_mla_out(ThvmMlaArgs a) {
   const uint32_t bh = blockIdx.x, b = bh / a.H, h = bh % a.H, kv = a.kv, dv = a.dv;
   const uint32_t tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   constexpr uint32_t nw = MLA_OUT_THREADS / 64;
+  // phase clock: the merge's blocks follow the split's in the clock buffer;
+  // 0 entry, 1 split weights, 2 partials summed per group, 3 olat in LDS,
+  // 7 drained
+  uint64_t *const clk = a.clk ? a.clk + (uint64_t)a.clk_cap * PCLK_MARKS : nullptr;
+  pclk(clk, a.clk_cap, 0);
   const uint32_t rowb = kv * (FP8 ? 1 : 2), LPR = rowb / 16;     // kv <= 512: LPR <= 64
   const uint32_t rpp = 64 / LPR, sub = lane / LPR, c = lane % LPR;
   const uint32_t rows_pb = (dv + gridDim.y - 1) / gridDim.y;
   const uint32_t m0 = blockIdx.y * rows_pb, m1 = min(m0 + rows_pb, dv);
-  uint4 wq[MLA_WPASS];
-#pragma unroll
-  for (int q = 0; q < MLA_WPASS; q++) {
-    const uint32_t mm = m0 + (wv + q * nw) * rpp + sub;
-    wq[q] = mm < m1 ? ld_stream16((const char *)a.wuv + ((uint64_t)h * dv + mm) * rowb + (uint64_t)c * 16)
-                    : make_uint4(0, 0, 0, 0);
-  }
   const int32_t L = min(a.len[0], (int32_t)a.max_seq);
   const uint32_t span = MLA_CHUNK * (a.cpb > 1 ? a.cpb : 1);   // cache rows per partial
   const uint32_t ns = L > 0 ? ((uint32_t)L + span - 1) / span : 0;
@@ -567,9 +620,15 @@ __global__ __launch_bounds__(MLA_OUT_THREADS) void k_mla_out(ThvmMlaArgs a) {
   const float *p0 = a.part + (uint64_t)b * a.n_split * pst + (uint64_t)h * (kv + 4);
   float *wsp = ol + kv, *grp = wsp + MLA_MAX_SPLITS;
   __shared__ float red[16];
+  // Every load is an unguarded buffer load (offsets past a range read zero
+  // with no access), issued in the order the merge consumes them: m and l,
+  // the partial vectors, then the W_uv rows and their scales.  Loads complete
+  // in issue order, so each wait covers only what its step needs (a guarded
+  // load made every wait drain all of them, W_uv included).
+  const buf_t prs = buf_rsrc_u(p0, (uint32_t)((uint64_t)ns * pst * 4u));
   // split weights w_s = exp(m_s - M) / sum_s exp(m_s - M) l_s (one split per thread)
-  float ms = -INFINITY, ls = 0.0f;
-  if (tid < ns) { ms = p0[tid * pst + kv]; ls = p0[tid * pst + kv + 1]; }
+  const uint32_t mlo = tid < ns ? (uint32_t)(((uint64_t)tid * pst + kv) * 4u) : BUF_OOB;
+  const uint32_t mb = buf_ld4(prs, mlo), lb = buf_ld4(prs, mlo == BUF_OOB ? BUF_OOB : mlo + 4u);
   // the thread's first OPRE partial vectors go out with m and l (they do not
   // depend on the weights): thread -> (float4 column c4, split group g),
   // splits g, g + nsg, ...; the weights' reductions then run while they are
@@ -584,8 +643,24 @@ __global__ __launch_bounds__(MLA_OUT_THREADS) void k_mla_out(ThvmMlaArgs a) {
 #pragma unroll
   for (int u = 0; u < OPRE; u++) {
     const uint32_t sp = g + u * nsg;
-    vp[u] = sp < ns ? *(const float4 *)(p0 + sp * pst + 4 * c4) : make_float4(0.f, 0.f, 0.f, 0.f);
+    const uint4 v = buf_ld16(prs, sp < ns ? (uint32_t)(((uint64_t)sp * pst + 4 * c4) * 4u) : BUF_OOB);
+    vp[u] = make_float4(__uint_as_float(v.x), __uint_as_float(v.y), __uint_as_float(v.z), __uint_as_float(v.w));
   }
+  // this block's W_uv rows and their scales (independent of the merge)
+  const buf_t wrs = buf_rsrc(a.wuv, a.H * dv * rowb);
+  const buf_t srs = buf_rsrc(a.suv, a.suv ? a.H * dv * 4u : 0u);
+  uint4 wq[MLA_WPASS];
+  uint32_t scw[MLA_WPASS];
+#pragma unroll
+  for (int q = 0; q < MLA_WPASS; q++) {
+    const uint32_t mm = m0 + (wv + q * nw) * rpp + sub;
+    wq[q] = buf_ld_stream16(wrs, mm < m1 ? (h * dv + mm) * rowb + c * 16u : BUF_OOB);
+    scw[q] = buf_ld4(srs, mm < m1 ? (h * dv + mm) * 4u : BUF_OOB);
+  }
+  pclk(clk, a.clk_cap, 4);
+  pclk_after(clk, a.clk_cap, 5, mb);
+  pclk_after(clk, a.clk_cap, 6, wq[0].x);
+  const float ms = tid < ns ? __uint_as_float(mb) : -INFINITY, ls = __uint_as_float(lb);
   float M = wave_max(ms);
   if (lane == 0) red[wv] = M;
   __syncthreads();
@@ -599,6 +674,7 @@ __global__ __launch_bounds__(MLA_OUT_THREADS) void k_mla_out(ThvmMlaArgs a) {
   for (uint32_t w = 0; w < MLA_OUT_THREADS / 64; w++) den += red[8 + w];
   if (tid < ns) wsp[tid] = ws / den;
   __syncthreads();
+  pclk(clk, a.clk_cap, 1);
   // partial merge: groups stride the splits
   float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
@@ -612,7 +688,8 @@ __global__ __launch_bounds__(MLA_OUT_THREADS) void k_mla_out(ThvmMlaArgs a) {
 #pragma unroll
     for (int u = 0; u < 4; u++) {
       const uint32_t s = s0 + u * nsg;
-      v[u] = s < ns ? *(const float4 *)(p0 + s * pst + 4 * c4) : make_float4(0.f, 0.f, 0.f, 0.f);
+      const uint4 r = buf_ld16(prs, s < ns ? (uint32_t)(((uint64_t)s * pst + 4 * c4) * 4u) : BUF_OOB);
+      v[u] = make_float4(__uint_as_float(r.x), __uint_as_float(r.y), __uint_as_float(r.z), __uint_as_float(r.w));
     }
 #pragma unroll
     for (int u = 0; u < 4; u++) {
@@ -623,6 +700,7 @@ __global__ __launch_bounds__(MLA_OUT_THREADS) void k_mla_out(ThvmMlaArgs a) {
   }
   ((float4 *)grp)[g * nc4 + c4] = acc;
   __syncthreads();
+  pclk(clk, a.clk_cap, 2);
   const uint32_t nchk = kv / EPC;
   if (tid < nc4) {
     float4 s = ((const float4 *)grp)[tid];
@@ -633,6 +711,7 @@ __global__ __launch_bounds__(MLA_OUT_THREADS) void k_mla_out(ThvmMlaArgs a) {
     ((float4 *)ol)[chunk_swz<EPC>(4 * tid, nchk) / 4] = s;   // W_uv chunk order
   }
   __syncthreads();
+  pclk(clk, a.clk_cap, 3);
 #pragma unroll
   for (int q = 0; q < MLA_WPASS; q++) {
     const uint32_t r0 = m0 + (wv + q * nw) * rpp;
@@ -650,10 +729,11 @@ __global__ __launch_bounds__(MLA_OUT_THREADS) void k_mla_out(ThvmMlaArgs a) {
     accw = group_sum(accw, (int)LPR);
     if (mm < m1 && c == 0) {
       const uint64_t row = (uint64_t)h * dv + mm;
-      const float s = a.suv ? a.suv[row] : 1.0f;
+      const float s = a.suv ? __uint_as_float(scw[q]) : 1.0f;
       ((bf16_t *)a.o)[(uint64_t)b * a.H * dv + row] = f2bf(accw * s);
     }
   }
+  pclk_end(clk, a.clk_cap);
 }
 
 // -------------------------------------------------------------------------

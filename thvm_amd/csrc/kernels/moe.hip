@@ -41,7 +41,8 @@
 __device__ __forceinline__ void route_wave(float g, uint32_t lane, uint32_t E, uint32_t K,
                                            int32_t (&ids)[MOE_MAXK], float (&pr)[MOE_MAXK]) {
   const float mx = wave_max(g);
-  const float sum = wave_sum(lane < E ? expf(g - mx) : 0.0f);
+  const float pe = lane < E ? expf(g - mx) : 0.0f;   // each lane's numerator, computed once
+  const float sum = wave_sum(pe);
   bool used = lane >= E;
 #pragma unroll
   for (uint32_t kk = 0; kk < MOE_MAXK; kk++) {
@@ -53,7 +54,7 @@ __device__ __forceinline__ void route_wave(float g, uint32_t lane, uint32_t E, u
     const int bi = m ? (int)__builtin_ctzll(m) : 0;
     if ((int)lane == bi) used = true;
     ids[kk] = bi;
-    pr[kk] = expf(bv - mx) / sum;
+    pr[kk] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(pe), bi)) / sum;   // expf(bv - mx)
   }
 }
 
@@ -70,24 +71,30 @@ __global__ __launch_bounds__(64) void k_route(ThvmRouteArgs a) {
 }
 
 // The post-attention RMSNorm (f32 out) and the f32 router GEMV in one
-// launch: grid (ceil(E / 8), B), 512 threads; each block renormalises its
+// launch: grid (ceil(E / EPB), B), 512 threads; each block renormalises its
 // row (the first 256 threads exactly as the norm kernel: the same elements
 // per thread, the same block sum over four waves, the same formula) and its
-// 8 waves take one expert each, lane l folding 16-byte chunks l, l + 64, ...
-// in order (four FMAs each) with one wave sum -- the GEMV's f32 path -- so
-// xn and the logits are those kernels' bits.  The expert row is in flight
-// before the norm starts.
+// first EPB waves take one expert each, lane l folding 16-byte chunks l,
+// l + 64, ... in order (four FMAs each) with one wave sum -- the GEMV's f32
+// path -- so xn and the logits are those kernels' bits.  The expert row is
+// in flight before the norm starts.  EPB = 1 for a few rows (64 blocks at
+// batch 1, each reading 8 KiB of router row and ~12 KiB of x and gains;
+// eight experts per block left 8 CUs pulling 76 KiB each: 2.87 -> 2.71 us
+// per launch in the phase clock), else 8.
 #define RT_THREADS 512
 #define RT_WAVES (RT_THREADS / 64)
 #define RT_NORM_THREADS 256
 #define RT_NREG 16       /* x elements per norm thread: D <= 4096 */
-template <int NCH>       /* 16-byte router chunks per lane: D <= 256 * NCH */
+template <int NCH, int EPB>   /* 16-byte router chunks per lane: D <= 256 * NCH; experts per block */
 __global__ __launch_bounds__(RT_THREADS) void k_moe_gate(ThvmGateArgs a) {
   __shared__ __align__(16) float xs[RT_NREG * RT_NORM_THREADS];
   __shared__ float red[RT_NORM_THREADS / 64];
   const uint32_t b = blockIdx.y, tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const uint32_t D = a.D, E = a.E, C = D / 4;
-  const uint32_t e = blockIdx.x * RT_WAVES + wv;
+  const bool ew = wv < (uint32_t)EPB;                 // a wave with an expert
+  const uint32_t e = blockIdx.x * EPB + (ew ? wv : 0u);
+  // phase clock: 0 entry, 1 loads issued, 2 x normalised in LDS, 7 drained
+  pclk(a.clk, a.clk_cap, 0);
   const float4 *W = (const float4 *)a.gate;
   const uint64_t xo = (uint64_t)b * D;
   const float invK = 1.0f / (float)D;
@@ -111,8 +118,9 @@ __global__ __launch_bounds__(RT_THREADS) void k_moe_gate(ThvmGateArgs a) {
 #pragma unroll
   for (int t = 0; t < NCH; t++) {
     const uint32_t c = lane + 64u * t;
-    wq[t] = buf_ld_stream16(wr, e < E && c < C ? (e * C + c) * 16u : BUF_OOB);
+    wq[t] = buf_ld_stream16(wr, ew && e < E && c < C ? (e * C + c) * 16u : BUF_OOB);
   }
+  pclk(a.clk, a.clk_cap, 1);
   float xv[RT_NREG], gw[RT_NREG];
 #pragma unroll
   for (int i = 0; i < RT_NREG; i++) {
@@ -144,6 +152,7 @@ __global__ __launch_bounds__(RT_THREADS) void k_moe_gate(ThvmGateArgs a) {
     }
   }
   __syncthreads();
+  pclk(a.clk, a.clk_cap, 2);
   const float4 *x4 = (const float4 *)xs;
   float acc = 0.0f;
 #pragma unroll
@@ -158,7 +167,8 @@ __global__ __launch_bounds__(RT_THREADS) void k_moe_gate(ThvmGateArgs a) {
     }
   }
   const float tot = wave_sum(acc);
-  if (e < E && lane == 0) a.logits[(uint64_t)b * E + e] = tot * 1.0f + 0.0f;   // the GEMV epilogue's scale, bias
+  if (ew && e < E && lane == 0) a.logits[(uint64_t)b * E + e] = tot * 1.0f + 0.0f;   // the GEMV epilogue's scale, bias
+  pclk_end(a.clk, a.clk_cap);
 }
 
 // decode one 16-byte chunk: 16 fp8 or 8 bf16 weights
@@ -208,11 +218,7 @@ __device__ __forceinline__ float chunk_dot(const uint4 (&q)[NC], const float *v,
 template <int NC>
 __device__ __forceinline__ void load_row(uint4 (&q)[NC], const char *row, uint32_t lane,
                                          uint32_t nch, bool ok) {
-  const uint64_t rp = (uint64_t)(uintptr_t)row;
-  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)rp);
-  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(rp >> 32));
-  const buf_t r = buf_rsrc((const void *)(uintptr_t)(((uint64_t)hi << 32) | lo),
-                           __builtin_amdgcn_readfirstlane(ok ? nch * 16u : 0u));
+  const buf_t r = buf_rsrc_u(row, ok ? nch * 16u : 0u);
 #pragma unroll
   for (int c = 0; c < NC; c++) {
     const uint32_t ch = lane + 64u * c;
@@ -258,11 +264,12 @@ __device__ __forceinline__ void stage_swz(float *dst, const float *src, uint32_t
 template <int NV>
 __device__ __forceinline__ void stage_load(float4 (&v)[NV], const float *src, uint32_t n) {
   const uint32_t tid = threadIdx.x, nt = blockDim.x, n4 = n / 4;
-  const float4 *s4 = (const float4 *)src;
+  const buf_t r = buf_rsrc_u(src, n4 * 16u);      // unguarded: past n reads zero
 #pragma unroll
   for (int u = 0; u < NV; u++) {
     const uint32_t j = tid + u * nt;
-    v[u] = j < n4 ? s4[j] : make_float4(0.f, 0.f, 0.f, 0.f);
+    const uint4 w = buf_ld16(r, j < n4 ? j * 16u : BUF_OOB);
+    v[u] = make_float4(__uint_as_float(w.x), __uint_as_float(w.y), __uint_as_float(w.z), __uint_as_float(w.w));
   }
 }
 template <bool RBF, int EPC, int NV>
@@ -295,23 +302,44 @@ __global__ __launch_bounds__(MOE_THREADS) void k_moe_gateup(ThvmMoeArgs a) {
   const uint32_t b = blockIdx.y, D = a.D, I = a.I, K = a.K;
   const uint32_t P = K * I + a.S;
   const uint32_t lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
-  // x first (staged into LDS while the rows are in flight)
+  // phase clock: 0 entry, 1 top-K picked, 2 rows and scales issued, 3 x
+  // staged, 7 drained
+  pclk(a.clk, a.clk_cap, 0);
+  // the row's router logits first (the top-K waits for them only), then x
+  // (staged into LDS while the rows are in flight)
+  const buf_t lrs = buf_rsrc(a.logits ? a.logits + (uint64_t)b * a.E : nullptr, a.logits ? a.E * 4u : 0u);
+  const uint32_t lgv = buf_ld4(lrs, lane < a.E ? lane * 4u : BUF_OOB);
+  __builtin_amdgcn_sched_barrier(0);              // keep the logits ahead of x in issue order
   const bool xpre = D / 4 <= MOE_XPRE * blockDim.x;
   float4 xv[MOE_XPRE];
-  if (xpre) stage_load(xv, a.x + (uint64_t)b * D, D);
-  // the row's top-K, as the route kernel picks it, by every wave with a
-  // routed pair (no barrier before the weight loads); block 0's wave 0
-  // publishes it for the down kernel
-  int32_t rids[MOE_MAXK];
-  float rpr[MOE_MAXK];
-  const uint32_t pw0 = (blockIdx.x * MOE_WAVES + wv) * PPW;
-  if (a.logits && (pw0 < K * I || (blockIdx.x == 0 && wv == 0))) {
-    route_wave(lane < a.E ? a.logits[(uint64_t)b * a.E + lane] : -INFINITY, lane, a.E, K, rids, rpr);
-    if (blockIdx.x == 0 && wv == 0 && lane == 0)
+  stage_load(xv, a.x + (uint64_t)b * D, D);      // unconditional: no branch around the loads
+  // the row's top-K, as the route kernel picks it, by wave 0 of a block
+  // with a routed pair and handed to the others through LDS (every wave
+  // routing for itself put four waves per SIMD on the same serial VALU
+  // chain); block 0 publishes it for the down kernel
+  __shared__ int32_t rsh[MOE_MAXK];
+  int32_t rids[MOE_MAXK] = {};
+  float rpr[MOE_MAXK] = {};
+  pclk_after(a.clk, a.clk_cap, 4, lgv);
+  if (a.logits && (blockIdx.x * MOE_WAVES * PPW < K * I || blockIdx.x == 0)) {   // block-uniform
+    if (wv == 0) {
+      route_wave(lane < a.E ? __uint_as_float(lgv) : -INFINITY, lane, a.E, K, rids, rpr);
+      if (lane < MOE_MAXK) {
+        int32_t v = 0;
 #pragma unroll
-      for (uint32_t kk = 0; kk < MOE_MAXK; kk++)
-        if (kk < K) { a.sel_out[(uint64_t)b * K + kk] = rids[kk]; a.probs_out[(uint64_t)b * K + kk] = rpr[kk]; }
+        for (uint32_t kk = 0; kk < MOE_MAXK; kk++) v = kk == lane ? rids[kk] : v;
+        rsh[lane] = v;
+      }
+      if (blockIdx.x == 0 && lane == 0)
+#pragma unroll
+        for (uint32_t kk = 0; kk < MOE_MAXK; kk++)
+          if (kk < K) { a.sel_out[(uint64_t)b * K + kk] = rids[kk]; a.probs_out[(uint64_t)b * K + kk] = rpr[kk]; }
+    }
+    __syncthreads();
+#pragma unroll
+    for (uint32_t kk = 0; kk < MOE_MAXK; kk++) rids[kk] = rsh[kk];
   }
+  pclk(a.clk, a.clk_cap, 1);
   const uint32_t p0 = (blockIdx.x * MOE_WAVES + wv) * PPW;
   const uint64_t rowb = (uint64_t)D * (FP8 ? 1 : 2);
   const uint32_t nch = (uint32_t)(rowb / 16);
@@ -380,9 +408,12 @@ __global__ __launch_bounds__(MOE_THREADS) void k_moe_gateup(ThvmMoeArgs a) {
     scg[i] = buf_ld4(crs, so < 0x7ffffff0ull ? (uint32_t)so : BUF_OOB);
     scu[i] = buf_ld4(crs, so < 0x7ffffff0ull ? (uint32_t)so + 4u : BUF_OOB);
   }
+  pclk(a.clk, a.clk_cap, 2);
   if (xpre) stage_store<true, FP8 ? 16 : 8>(xs, xv, D, 0, 1);
   else stage_swz<true, FP8 ? 16 : 8>(xs, a.x + (uint64_t)b * D, D, 0, 1);
   __syncthreads();
+  pclk(a.clk, a.clk_cap, 3);
+  pclk_after(a.clk, a.clk_cap, 5, uq[PPW - 1][NC - 1].x);
 #pragma unroll
   for (int i = 0; i < PPW; i++) {
     const uint32_t p = p0 + i;
@@ -394,6 +425,7 @@ __global__ __launch_bounds__(MOE_THREADS) void k_moe_gateup(ThvmMoeArgs a) {
       a.h[(uint64_t)b * P + p] = silu_f(G) * U;
     }
   }
+  pclk_end(a.clk, a.clk_cap);
 }
 
 // ---- down + residual ------------------------------------------------------
@@ -421,6 +453,9 @@ __global__ __launch_bounds__(MOE_THREADS, 4) void k_moe_down(ThvmMoeArgs a) {
   const uint32_t P = K * I + S;
   const uint32_t lane = threadIdx.x & 63, wv = threadIdx.x >> 6, hf = wv & 1, rw = wv >> 1;
   const uint32_t d = blockIdx.x * (MOE_WAVES / 2) + rw;
+  // phase clock: 0 entry, 1 rows issued, 2 h staged, 3 half sums done, 7
+  // drained
+  pclk(a.clk, a.clk_cap, 0);
   const bool live = d < D;
   const uint32_t c = moe_down_split(K, I, S);
   const uint32_t e0 = hf ? c : 0, e1 = hf ? K : c;          // this half's routed slots
@@ -430,14 +465,17 @@ __global__ __launch_bounds__(MOE_THREADS, 4) void k_moe_down(ThvmMoeArgs a) {
   int32_t ids[MOE_HALFK];
   // this half's routing ids requested at once (clamped, unconditional loads:
   // one round trip); the shared row, which needs no routing, goes out before
-  // the routed rows; h is staged into LDS behind them (its registers would
-  // cost the second block per CU)
+  // the routed rows, the rows' scales and the slots' probabilities after
+  // them (unguarded buffer loads: no wait after the dot products), and h is
+  // staged into LDS behind them (its registers would cost the second block
+  // per CU)
 #pragma unroll
   for (int j = 0; j < MOE_HALFK; j++) {
     const uint32_t e = e0 + j;
     ids[j] = a.sel[(uint64_t)b * K + (e < e1 ? e : 0u)];
   }
   load_row(qs, (const char *)a.wd_s + (uint64_t)(live ? d : 0) * rS, lane, nS, live && hf && S > 0);
+  pclk_after(a.clk, a.clk_cap, 4, (uint32_t)ids[0]);
 #pragma unroll
   for (int j = 0; j < MOE_HALFK; j++) {
     const bool ok = live && e0 + j < e1;
@@ -447,8 +485,25 @@ __global__ __launch_bounds__(MOE_THREADS, 4) void k_moe_down(ThvmMoeArgs a) {
     const uint64_t row = (uint64_t)id * D + (live ? d : 0);
     load_row(q[j], (const char *)a.wd_e + row * rI, lane, nI, ok);
   }
+  uint32_t scv[MOE_HALFK], pbv[MOE_HALFK], scs;
+  {
+    const buf_t srs = buf_rsrc_u(a.sd_e, a.sd_e ? 0x7fffffffu : 0u);
+    const buf_t prs = buf_rsrc(a.probs, a.B * K * 4u);
+#pragma unroll
+    for (int j = 0; j < MOE_HALFK; j++) {
+      const uint32_t e = e0 + j;
+      const uint64_t so = ((uint64_t)ids[j] * D + (live ? d : 0)) * 4u;
+      scv[j] = buf_ld4(srs, live && e < e1 && so < 0x7ffffff0ull ? (uint32_t)so : BUF_OOB);
+      pbv[j] = buf_ld4(prs, e < e1 ? (b * K + e) * 4u : BUF_OOB);
+    }
+    const buf_t ssr = buf_rsrc(a.sd_s, a.sd_s ? D * 4u : 0u);
+    scs = buf_ld4(ssr, live && hf ? d * 4u : BUF_OOB);
+  }
+  pclk(a.clk, a.clk_cap, 1);
   stage_swz<false, FP8 ? 16 : 8>(hs, a.h + (uint64_t)b * P, P, K, I);
   __syncthreads();
+  pclk(a.clk, a.clk_cap, 2);
+  pclk_after(a.clk, a.clk_cap, 5, q[MOE_HALFK - 1][NC - 1].x);
   // this half's segment values, in slot order
   float sv[MOE_HALFK];
 #pragma unroll
@@ -457,7 +512,7 @@ __global__ __launch_bounds__(MOE_THREADS, 4) void k_moe_down(ThvmMoeArgs a) {
     sv[j] = 0.0f;
     if (e >= e1) continue;                               // wave-uniform
     float t = wave_sum(chunk_dot<FP8>(q[j], hs + e * I, lane, nI));
-    if (a.sd_e) t *= a.sd_e[(uint64_t)ids[j] * D + (live ? d : 0)];
+    if (a.sd_e) t *= __uint_as_float(scv[j]);
     sv[j] = t;
   }
   float acc = 0.0f;
@@ -466,29 +521,32 @@ __global__ __launch_bounds__(MOE_THREADS, 4) void k_moe_down(ThvmMoeArgs a) {
     for (int j = 0; j < MOE_HALFK; j++) {
       const uint32_t e = j;
       if (e >= e1) break;
-      acc += a.probs[(uint64_t)b * K + e] * sv[j];
+      acc += __uint_as_float(pbv[j]) * sv[j];
     }
     if (lane == 0) part[rw] = acc;
   }
   float ssh = 0.0f;
   if (hf == 1 && S > 0) {
     ssh = wave_sum(chunk_dot<FP8>(qs, hs + K * I, lane, nS));
-    if (a.sd_s) ssh *= a.sd_s[live ? d : 0];
+    if (a.sd_s) ssh *= __uint_as_float(scs);
   }
   __syncthreads();
-  if (hf == 0 || !live) return;
-  acc = part[rw];
+  pclk(a.clk, a.clk_cap, 3);
+  if (hf == 1 && live) {                               // wave-uniform
+    acc = part[rw];
 #pragma unroll
-  for (int j = 0; j < MOE_HALFK; j++) {
-    const uint32_t e = e0 + j;
-    if (e >= e1) break;
-    acc += a.probs[(uint64_t)b * K + e] * sv[j];
+    for (int j = 0; j < MOE_HALFK; j++) {
+      const uint32_t e = e0 + j;
+      if (e >= e1) break;
+      acc += __uint_as_float(pbv[j]) * sv[j];
+    }
+    if (S > 0) acc += ssh;
+    if (lane == 0) {
+      bf16_t *r = (bf16_t *)a.res + (uint64_t)b * D + d;
+      r[0] = f2bf(bf2f(r[0]) + rbf(acc));
+    }
   }
-  if (S > 0) acc += ssh;
-  if (lane == 0) {
-    bf16_t *r = (bf16_t *)a.res + (uint64_t)b * D + d;
-    r[0] = f2bf(bf2f(r[0]) + rbf(acc));
-  }
+  pclk_end(a.clk, a.clk_cap);
 }
 
 // ---- expert-grouped form (batches above 4 rows) ---------------------------
@@ -902,8 +960,12 @@ extern "C" int thvm_k_moe_gate(const ThvmGateArgs *a, hipStream_t s, char *err, 
     return -1;
   }
   const uint32_t nch = (a->D / 4 + 63) / 64;
-  void (*f)(ThvmGateArgs) = nch <= 4 ? k_moe_gate<4> : nch <= 8 ? k_moe_gate<8> : k_moe_gate<16>;
-  thvm_launch(true, true, f, dim3((a->E + RT_WAVES - 1) / RT_WAVES, a->B), dim3(RT_THREADS), 0, s, *a);
+  const bool one = a->B <= 4;                     // one expert per block for a few rows
+  void (*f)(ThvmGateArgs) = nch <= 4 ? (one ? k_moe_gate<4, 1> : k_moe_gate<4, RT_WAVES>)
+                          : nch <= 8 ? (one ? k_moe_gate<8, 1> : k_moe_gate<8, RT_WAVES>)
+                                     : (one ? k_moe_gate<16, 1> : k_moe_gate<16, RT_WAVES>);
+  const uint32_t epb = one ? 1 : RT_WAVES;
+  thvm_launch(true, true, f, dim3((a->E + epb - 1) / epb, a->B), dim3(RT_THREADS), 0, s, *a);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) { snprintf(err, errlen, "moe_gate launch: %s", hipGetErrorString(e)); return -1; }
   return 0;
