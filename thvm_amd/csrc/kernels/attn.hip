@@ -347,7 +347,10 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attn_mf(ThvmAttnArgs a) {
   const uint32_t c0 = grp * a.cpb;
   if ((int32_t)(c0 * ATT_CHUNK) >= L) return;     // the merge reads only live partials
   pclk(a.clk, a.clk_cap, 0);
-  const int tid = threadIdx.x, wv = tid >> 6, lane = tid & 63, lc = lane & 15, lg = lane >> 4;
+  // wv through readfirstlane: the compiler then knows it is wave-uniform, so
+  // the tile loop below is a scalar loop rather than an exec-masked one
+  const int tid = threadIdx.x, wv = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63, lc = lane & 15,
+            lg = lane >> 4;
   const int32_t r0 = (int32_t)(c0 * ATT_CHUNK);
   const int32_t r1 = min(L, (int32_t)((c0 + a.cpb) * ATT_CHUNK));
   const int nt = (r1 - r0 + 15) / 16;             // 16-row tiles of the block
@@ -370,8 +373,6 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attn_mf(ThvmAttnArgs a) {
     for (int j = 0; j < 4; j++)
       vb[buf][j] = buf_ld_stream16(vrs, rv + j < r1 && lc < NC ? (uint32_t)((rv + j) * HD + 8 * lc) * 2 : BUF_OOB);
   };
-  issue(0, wv);
-  issue(1, wv + ATT_WAVES);
   const float qs = a.scale * LOG2E;
   float m = -INFINITY, l = 0.0f;
   f32x4_t acc[8];
@@ -427,12 +428,33 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attn_mf(ThvmAttnArgs a) {
       acc[e] = mfma16x16<XT>(a01, a23, pl[0], pl[1], acc[e]);
     }
   };
-  for (int t = wv; t < nt; t += 2 * ATT_WAVES) {  // two register sets, ping-pong
-    tile(0, t);
-    issue(0, t + 2 * ATT_WAVES);
-    if (t + ATT_WAVES >= nt) break;
-    tile(1, t + ATT_WAVES);
-    issue(1, t + 3 * ATT_WAVES);
+  if (nt <= ATT_WAVES) {                          // at most one tile per wave (block-uniform)
+    issue(0, wv);
+    if (wv < nt) tile(0, wv);
+  } else {
+    // q, then the two register sets, in this issue order (scheduling
+    // barriers: with q scheduled after the rows, the wait for q at the loop
+    // head drained every load in flight, in every iteration)
+    __builtin_amdgcn_sched_barrier(0);
+    issue(0, wv);
+    __builtin_amdgcn_sched_barrier(0);
+    issue(1, wv + ATT_WAVES);
+    __builtin_amdgcn_sched_barrier(0);
+    // two register sets, ping-pong: each tile waits only for its own rows,
+    // the other set's stay in flight.  Past the block's rows the second tile
+    // is skipped but the loop goes on to its end (the loads then read
+    // zeros): an early exit there split the loop state so that the loop head
+    // waited for every load in flight.
+    for (int t = wv; t < nt; t += 2 * ATT_WAVES) {
+      tile(0, t);
+      __builtin_amdgcn_sched_barrier(0);
+      issue(0, t + 2 * ATT_WAVES);
+      __builtin_amdgcn_sched_barrier(0);
+      if (t + ATT_WAVES < nt) tile(1, t + ATT_WAVES);   // wave-uniform
+      __builtin_amdgcn_sched_barrier(0);
+      issue(1, t + 3 * ATT_WAVES);
+      __builtin_amdgcn_sched_barrier(0);
+    }
   }
   pclk(a.clk, a.clk_cap, 3);
   // a head's rows are spread over the lanes 16 and 32 apart
