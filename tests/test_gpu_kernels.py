@@ -782,6 +782,24 @@ def test_attention_mfma_split(hip, H, Hkv, hd, L, cdt, cpb):
     assert np.all(np.abs(got - valu) <= ulp * np.abs(valu) + 1e-4), np.max(np.abs(got - valu))
 
 
+@pytest.mark.parametrize("H,Hkv,hd", [(32, 8, 128), (16, 2, 64)])
+@pytest.mark.parametrize("B,L", [(8, 17), (9, 200)])
+def test_attention_mfma_split_batched(hip, H, Hkv, hd, B, L):
+    """At 8 rows and more the MFMA path merges one block per (row, query
+    head) instead of per kv-head group: the same bars against the oracle and
+    the VALU split."""
+    ms, cdt = 256, DT_BF16
+    say(f"case: attn mfma batched B={B} H={H} Hkv={Hkv} hd={hd} L={L}")
+    rng = np.random.default_rng(B * 7 + H + L)
+    qs, _ = rand_store(rng, (B, H, hd), cdt)
+    ks, _ = rand_store(rng, (B, Hkv, ms, hd), cdt)
+    vs, _ = rand_store(rng, (B, Hkv, ms, hd), cdt)
+    got, ww = run_attn(hip, qs, ks, vs, B, H, Hkv, hd, ms, L, cdt, mf=1)
+    assert attn_close(got, ww, cdt), np.max(np.abs(got - ww))
+    valu, _ = run_attn(hip, qs, ks, vs, B, H, Hkv, hd, ms, L, cdt, mf=2)
+    assert np.all(np.abs(got - valu) <= 2.0 ** -7 * np.abs(valu) + 1e-4), np.max(np.abs(got - valu))
+
+
 @pytest.mark.parametrize("mf", [1, 2])
 def test_attention_stale_rows_are_never_mixed(hip, mf):
     """Cache rows at and past L hold NaN (a stale or never-written row):
