@@ -313,43 +313,50 @@ __global__ __launch_bounds__(MLA_THREADS) void k_mla_split(ThvmMlaArgs a) {
 // ---- k_mla_split_mf -----------------------------------------------------
 // The split on MFMA for the DeepSeek-V2 attention shape (16 heads, kv_lora
 // 512, rope 64): the 16 heads are the M side of v_mfma_f32_16x16x32_bf16.
+// A chunk's 64 cache rows (1152 bytes each: the latent row, then the pe row)
+// are loaded as contiguous 16-byte pieces -- thread t takes pieces t, t +
+// 512, ... of the chunk's 64 x 72 -- and staged row-major in LDS (pitch
+// MF_RP).  (Loading each lane's MFMA operand straight from HBM touched 16
+// rows per load instruction: a block's rows landed after ~2.9 us, against
+// ~1.5 us for contiguous pieces, measured on gfx950.)
 //   scores  S[h][row] = qlat[h] . c_row + qpe[h] . pe_row over k = 576 (18
-//           steps of 32): A = q (16 heads x 32 k), B = the cache rows (32 k x
-//           16 rows), two waves per 16-row tile (k-steps 0..8 and 9..17,
-//           summed through LDS); a lane's B operand is 8 consecutive values
-//           of one row, one 16-byte load straight from HBM;
+//           steps of 32): A = q (16 heads x 32 k), B = the staged rows (32 k
+//           x 16 rows: a lane's 8 consecutive values of one row, one 16-byte
+//           LDS read), two waves per 16-row tile (k-steps 0..8 and 9..17,
+//           summed through LDS);
 //   mix     olat[h][:] += p[h][row] c_row: A = p (16 heads x 32 rows), B =
-//           the latent rows staged in LDS (32 rows x 16 columns), 4 column
-//           tiles per wave.  The rows are staged column-major within each
-//           group of 8 rows ([row / 8][column][row % 8]), so a lane's B
-//           operand -- 8 rows of one column -- is one 16-byte LDS read; the
-//           transposing 2-byte writes need no wait.  16 bytes of padding
-//           after every 8 columns and a group pitch of 2320 dwords spread
-//           one store instruction's 64 lanes over 32 distinct dwords (two
-//           lanes per dword) with 32 or 64 banks alike: the 4 column groups
-//           of a row land 36 dwords apart, the two 8-row groups 16 banks
-//           apart.
+//           the staged rows (32 rows x 16 columns), 4 column tiles per wave.
+//           A lane's B operand is one column of 8 rows, read as 2-byte
+//           values; lane group g takes rows g, g + 4, ..., g + 28 of the 32,
+//           so the four groups' rows are consecutive and fall in distinct
+//           banks (pitch 292 dwords: 36 apart mod 64), and p is stored in the
+//           same row order, so A is one 8-float read.
 // q and p (f32) enter as bf16 hi + lo pairs (two MFMAs each), so a product
 // keeps ~16 significant bits of the f32 operand against the exact bf16 cache
 // value: f32-level agreement with the VALU split.  A block runs cpb
 // consecutive 64-row chunks of one batch row with an online softmax (olat and
 // the running sum rescaled by exp(m_old - m_new)), the next chunk's rows in
-// flight during the current chunk's softmax and mix, and writes one partial
-// (olat, m, l) at slot blockIdx.x; k_mla_out merges ceil(L / (64 cpb)) of
-// them.  MFMA operand k order: A and B give lane group g the same 8 k values
-// (k = 32 step + 8 g + j), so each instruction adds a full partial dot product.
+// flight during the current chunk, and writes one partial (olat, m, l) at
+// slot blockIdx.x; k_mla_out merges ceil(L / (64 cpb)) of them.  MFMA operand
+// k order: A and B give lane group g the same 8 k values (scores: k = 32
+// step + 8 g + j; mix: row 32 step + g + 4 j), so each instruction adds a
+// full partial dot product.
 #define MF_H 16
 #define MF_KV 512
 #define MF_DR 64
 #define MF_KS ((MF_KV + MF_DR) / 32)       /* 18 k-steps */
-#define MF_CADDR(k) ((k) * 16 + ((k) >> 3) * 16)   /* byte offset of column k in an 8-row group */
-#define MF_RGP (MF_CADDR(512) + 64)        /* LDS pitch of a staged 8-row group (bytes) */
+#define MF_ROWB ((MF_KV + MF_DR) * 2)      /* bytes of a staged row: latent, then pe */
+#define MF_RP (MF_ROWB + 16)               /* LDS pitch of a staged row (bytes) */
+#define MF_PC (MF_ROWB / 16)               /* 16-byte pieces per row (72) */
+#define MF_PT (64 * MF_PC / 512)           /* pieces per thread per chunk (9) */
 #define MF_PWP 68                          /* LDS pitch of a head's softmax weights (floats) */
 #define MF_QLP (MF_KV + 4)                 /* LDS pitch of a staged qlat row (floats) */
-static_assert(MF_H * MF_QLP * 4 <= 8 * MF_RGP, "qlat staging fits the latent staging area");
+static_assert(64 * MF_PC == MF_PT * 512 && MF_KV / 8 * 64 == (MF_PT - 1) * 512 && MF_DR / 8 * 64 == 512,
+              "a chunk's pieces: 8 latent loads and 1 pe load per thread");
+static_assert(MF_H * MF_QLP * 4 <= 64 * MF_RP, "qlat staging fits the row staging area");
 #define MF_THREADS 512                     /* 8 waves: two per 16-row tile */
 #define MF_KH (MF_KS / 2)                  /* k-steps per wave */
-#define MF_LDS (8 * MF_RGP + MF_KS * 2 * 64 * 16 + MF_H * MF_PWP * 4 + 2 * 4 * MF_H * 4 + 4 * 64 * 16)
+#define MF_LDS (64 * MF_RP + MF_KS * 2 * 64 * 16 + MF_H * MF_PWP * 4 + 2 * 4 * MF_H * 4 + 4 * 64 * 16)
 
 // eight f32 -> bf16 hi (RNE) and lo = bf16(v - hi), packed in operand order
 // (v - hi is exact in f32)
@@ -372,9 +379,9 @@ __device__ __forceinline__ void split8(const float4 &a, const float4 &b, uint4 &
 // tile, each chunk's phases ran at one wave per SIMD: ~5.5 us per chunk.)
 __global__ __launch_bounds__(MF_THREADS) void k_mla_split_mf(ThvmMlaArgs a) {
   extern __shared__ __align__(16) unsigned char lds_mf[];
-  unsigned char *cl = lds_mf;                                        // [8][MF_RGP]: [row/8][col][row%8]
-  uint4 *qa = (uint4 *)(lds_mf + 8 * MF_RGP);                        // [MF_KS][hi, lo][64 lanes]
-  float *pw = (float *)(lds_mf + 8 * MF_RGP + MF_KS * 2 * 64 * 16);  // [16 heads][MF_PWP]
+  unsigned char *cl = lds_mf;                                        // [64 rows][MF_RP]
+  uint4 *qa = (uint4 *)(lds_mf + 64 * MF_RP);                        // [MF_KS][hi, lo][64 lanes]
+  float *pw = (float *)(lds_mf + 64 * MF_RP + MF_KS * 2 * 64 * 16);  // [16 heads][MF_PWP]
   float *rmax = pw + MF_H * MF_PWP, *rsum = rmax + 4 * MF_H;         // [4 tiles][16 heads]
   float4 *spart = (float4 *)(rsum + 4 * MF_H);                       // [4 tiles][64 lanes]
   const uint32_t cpb = a.cpb, grp = blockIdx.x, b = blockIdx.y;
@@ -385,10 +392,13 @@ __global__ __launch_bounds__(MF_THREADS) void k_mla_split_mf(ThvmMlaArgs a) {
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, li = lane & 15, lg = lane >> 4;
   const int rt = wv & 3, kh = wv >> 2;                               // row tile, k half
   // phase clock: 0 entry, 1 q staged, 2 first chunk's scores, 3 first
-  // chunk's softmax, 4 chunks done, 7 drained
+  // chunk's softmax, 4 chunks done, 5 rows issued, 6 first rows arrived, 7
+  // drained
   pclk(a.clk, a.clk_cap, 0);
-  const char *ckv = (const char *)a.ckv + (uint64_t)b * a.max_seq * (MF_KV * 2);
-  const char *kpe = (const char *)a.kpe + (uint64_t)b * a.max_seq * (MF_DR * 2);
+  // the batch row's caches through buffer resources (rows past max_seq read
+  // zero; they are never live)
+  const buf_t crs = buf_rsrc((const char *)a.ckv + (uint64_t)b * a.max_seq * (MF_KV * 2), a.max_seq * (MF_KV * 2));
+  const buf_t prs = buf_rsrc((const char *)a.kpe + (uint64_t)b * a.max_seq * (MF_DR * 2), a.max_seq * (MF_DR * 2));
 
   // q first (its staging waits for these loads only), then the first two
   // chunks' rows.  q as A operands (hi, lo) in LDS: fragment f = 64 ks +
@@ -405,30 +415,30 @@ __global__ __launch_bounds__(MF_THREADS) void k_mla_split_mf(ThvmMlaArgs a) {
   const uint32_t fp = 16 * 64 + (tid & 127), lp = fp & 63;
   const uint4 qpv = *(const uint4 *)(qp + (lp & 15) * MF_DR + ((fp >> 6) - 16) * 32 + (lp >> 4) * 8);
 
-  // the B operands of chunk c for this wave's tile and k half: 8 consecutive
-  // values of one row per k-step (latent row for k-steps 0..15, pe row for
-  // 16..17); rows past L load a live row of the chunk and are masked out of
+  // chunk c's rows as this thread's MF_PT pieces: loads i < 8 the latent
+  // rows' pieces tid + 512 i (row f / 64, piece f % 64), load 8 the pe rows'
+  // (row tid / 8, piece 64 + tid % 8), so each load instruction reads one
+  // cache; rows past L load a live row of the chunk and are masked out of
   // the softmax
-  uint4 cfa[MF_KH], cfb[MF_KH];
-  auto issue = [&](uint4 (&cf)[MF_KH], uint32_t c) {
-    const uint32_t j = c * 64 + rt * 16 + li;
-    const uint32_t jc = j < (uint32_t)L ? j : c * 64;
-    const char *cr = ckv + (uint64_t)jc * (MF_KV * 2) + lg * 16;
-    const char *pr = kpe + (uint64_t)jc * (MF_DR * 2) + lg * 16;
+  uint4 cfa[MF_PT], cfb[MF_PT];
+  auto issue = [&](uint4 (&cf)[MF_PT], uint32_t c) {
 #pragma unroll
-    for (int st = 0; st < MF_KH; st++) {
-      const int ks = kh * MF_KH + st;
-      cf[st] = ld_stream16(ks < 16 ? cr + ks * 64 : pr + (ks - 16) * 64);
+    for (int i = 0; i < MF_PT; i++) {
+      const uint32_t r = i < MF_PT - 1 ? (tid + 512 * i) / 64 : tid / 8;
+      const uint32_t pc = i < MF_PT - 1 ? (tid + 512 * i) % 64 : tid % 8;
+      const uint32_t j = c * 64 + r, jc = j < (uint32_t)L ? j : c * 64;
+      cf[i] = i < MF_PT - 1 ? buf_ld_stream16(crs, jc * (MF_KV * 2) + pc * 16)
+                            : buf_ld_stream16(prs, jc * (MF_DR * 2) + pc * 16);
     }
   };
   issue(cfa, cbeg);
-
-  // qlat rows into the latent staging area (free until the first chunk's
-  // scores are done), a head's 512 values at a pitch of MF_QLP floats; the
-  // second chunk's rows go out after these stores (qraw live across that
-  // branch spilled to scratch)
-  float *qs = (float *)cl;
   pclk(a.clk, a.clk_cap, 5);
+
+  // qlat rows into the row staging area (free until the first chunk is
+  // staged), a head's 512 values at a pitch of MF_QLP floats; the second
+  // chunk's rows go out after these stores (q live across that branch
+  // spilled to scratch)
+  float *qs = (float *)cl;
   {
     const uint32_t e = 4 * tid, r = e / MF_KV, k = e % MF_KV;   // element e + 2048 i: row r + 4 i
     *(float4 *)(qs + r * MF_QLP + k) = q0;
@@ -461,36 +471,31 @@ __global__ __launch_bounds__(MF_THREADS) void k_mla_split_mf(ThvmMlaArgs a) {
 #pragma unroll
   for (int t = 0; t < 4; t++) oacc[t] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
 
-  // one chunk: its rows are in cf; chunk c + 2 goes into cf once the scores
-  // have consumed it
-  auto chunk = [&](uint4 (&cf)[MF_KH], uint32_t c) {
+  // one chunk: its rows are in cf; chunk c + 2 goes into cf once they are
+  // staged
+  auto chunk = [&](uint4 (&cf)[MF_PT], uint32_t c) {
     const uint32_t nj = min((uint32_t)L - c * 64, 64u);
-    if (c == cbeg) pclk_after(a.clk, a.clk_cap, 6, cf[MF_KH - 1].x);
+    if (c == cbeg) pclk_after(a.clk, a.clk_cap, 6, cf[MF_PT - 1].x);
+#pragma unroll
+    for (int i = 0; i < MF_PT; i++) {
+      const uint32_t r = i < MF_PT - 1 ? (tid + 512 * i) / 64 : tid / 8;
+      const uint32_t pc = i < MF_PT - 1 ? (tid + 512 * i) % 64 : MF_KV / 8 + tid % 8;
+      *(uint4 *)(cl + r * MF_RP + pc * 16) = cf[i];
+    }
+    __syncthreads();
+    if (c + 2 < cend) issue(cf, c + 2);   // in flight during this chunk and the next
     // 1. this wave's half of its tile's scores: lane holds S[head 4 lg + i]
     //    [row 16 rt + li] over its 9 k-steps (four independent chains)
     f32x4_t sc[4];
 #pragma unroll
     for (int u = 0; u < 4; u++) sc[u] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+    const unsigned char *rowp = cl + (rt * 16 + li) * MF_RP + lg * 16;
 #pragma unroll
     for (int st = 0; st < MF_KH; st++) {
       const int ks = kh * MF_KH + st;
-      sc[(st & 1) * 2] = mfma16<GX_BF16>(qa[ks * 128 + lane], cf[st], sc[(st & 1) * 2]);
-      sc[(st & 1) * 2 + 1] = mfma16<GX_BF16>(qa[ks * 128 + 64 + lane], cf[st], sc[(st & 1) * 2 + 1]);
-    }
-    // the latent part of the wave's rows into LDS for the mix: row r,
-    // column k at [r / 8][k][r % 8]
-    {
-      const uint32_t r = rt * 16 + li;
-      unsigned char *dst = cl + (r >> 3) * MF_RGP + (r & 7) * 2 + MF_CADDR(lg * 8);
-#pragma unroll
-      for (int st = 0; st < MF_KH; st++) {
-        const int ks = kh * MF_KH + st;
-        if (ks >= 16) break;                         // wave-uniform: the pe k-steps
-        const uint32_t w[4] = {cf[st].x, cf[st].y, cf[st].z, cf[st].w};
-#pragma unroll
-        for (int e = 0; e < 8; e++)                  // column ks*32 + lg*8 + e
-          *(uint16_t *)(dst + MF_CADDR(ks * 32) + e * 16) = (uint16_t)(w[e >> 1] >> ((e & 1) * 16));
-      }
+      const uint4 bv = *(const uint4 *)(rowp + ks * 64);
+      sc[(st & 1) * 2] = mfma16<GX_BF16>(qa[ks * 128 + lane], bv, sc[(st & 1) * 2]);
+      sc[(st & 1) * 2 + 1] = mfma16<GX_BF16>(qa[ks * 128 + 64 + lane], bv, sc[(st & 1) * 2 + 1]);
     }
     float4 part_s;
     part_s.x = (sc[0][0] + sc[1][0]) + (sc[2][0] + sc[3][0]);
@@ -498,13 +503,15 @@ __global__ __launch_bounds__(MF_THREADS) void k_mla_split_mf(ThvmMlaArgs a) {
     part_s.z = (sc[0][2] + sc[1][2]) + (sc[2][2] + sc[3][2]);
     part_s.w = (sc[0][3] + sc[1][3]) + (sc[2][3] + sc[3][3]);
     if (kh == 1) spart[rt * 64 + lane] = part_s;
-    if (c + 2 < cend) issue(cf, c + 2);   // in flight during two chunks' softmax and mix
     __syncthreads();
     if (c == cbeg) pclk(a.clk, a.clk_cap, 2);
 
     // 2. softmax over the chunk's rows (the first-half waves hold the full
-    //    scores), online across the block's chunks
-    const bool rok = (uint32_t)(rt * 16 + li) < nj;
+    //    scores), online across the block's chunks; p is stored in the mix's
+    //    row order: row r of a 32-row step at position 8 (r % 4) + r / 4
+    const uint32_t row = rt * 16 + li;
+    const bool rok = row < nj;
+    const uint32_t ppos = (row & 32) + (row & 3) * 8 + ((row & 31) >> 2);
     float sv[4];
     if (kh == 0) {
       const float4 o = spart[rt * 64 + lane];
@@ -528,7 +535,7 @@ __global__ __launch_bounds__(MF_THREADS) void k_mla_split_mf(ThvmMlaArgs a) {
         const float p = rok ? expf(sv[i] - mn[i]) : 0.0f;
         const float ps = row16_sum(p);
         if (li == 0) rsum[rt * MF_H + h] = ps;
-        pw[h * MF_PWP + rt * 16 + li] = p;
+        pw[h * MF_PWP + ppos] = p;
       }
     }
     __syncthreads();
@@ -550,10 +557,17 @@ __global__ __launch_bounds__(MF_THREADS) void k_mla_split_mf(ThvmMlaArgs a) {
       const float *pr = pw + li * MF_PWP + q * 32 + lg * 8;
       uint4 ah, alo;
       split8(*(const float4 *)pr, *(const float4 *)(pr + 4), ah, alo);
-      const unsigned char *rb = cl + (q * 4 + lg) * MF_RGP + MF_CADDR(li);
+      // rows 32 q + lg + 4 j, j = 0..7, of column (wv * 4 + t) * 16 + li
+      const unsigned char *cb = cl + (q * 32 + lg) * MF_RP + li * 2;
 #pragma unroll
-      for (int t = 0; t < 4; t++) {                // column (wv*4 + t)*16 + li
-        const uint4 bv = *(const uint4 *)(rb + MF_CADDR((wv * 4 + t) * 16));
+      for (int t = 0; t < 4; t++) {
+        const unsigned char *cp = cb + (wv * 4 + t) * 32;
+        uint32_t w[4];
+#pragma unroll
+        for (int j = 0; j < 4; j++)
+          w[j] = (uint32_t)*(const uint16_t *)(cp + (8 * j) * MF_RP) |
+                 ((uint32_t)*(const uint16_t *)(cp + (8 * j + 4) * MF_RP) << 16);
+        const uint4 bv = make_uint4(w[0], w[1], w[2], w[3]);
         oacc[t] = mfma16<GX_BF16>(ah, bv, oacc[t]);
         oacc[t] = mfma16<GX_BF16>(alo, bv, oacc[t]);
       }
