@@ -656,7 +656,7 @@ PHASES = {
                 "t0 m,l arrived", "t0 W_uv arrived", "end (drained)"],
     "moe_gate": ["entry", "loads issued", "x normalised", "", "", "", "", "end (drained)"],
     "moe_gateup": ["entry", "top-K picked", "rows issued", "x staged", "t0 logits arrived", "t0 rows arrived",
-                   "", "end (drained)"],
+                   "wave 0 routed", "end (drained)"],
     "moe_down": ["entry", "rows issued", "h staged", "half sums", "t0 ids arrived", "t0 rows arrived", "",
                  "end (drained)"],
 }

@@ -184,6 +184,24 @@ def test_route_topk_ties_bit_exact(hip):
         assert np.all(np.abs(g_p[b] - wp) <= 1e-6 * np.abs(wp) + 1e-9)
     assert list(g_sel[0, :3]) == [5, 9, 40] and list(g_sel[1]) == list(range(K))
     assert list(g_sel[2, :2]) == [0, 63]
+    # signed zeros tie (lowest id first), and fewer experts than lanes
+    for E2, K2 in ((64, 6), (20, 4), (3, 3)):
+        say(f"case: route zeros E={E2} K={K2}")
+        lz = -np.abs(rng.standard_normal((2, E2))).astype(np.float32) - 0.5
+        lz[0, [E2 - 1, 1, 0]] = np.array([0.0, -0.0, 0.0], np.float32)
+        lz[1, :] = rng.standard_normal(E2).astype(np.float32)
+        lz[1, E2 // 2] = lz[1].max()                     # a tie at the top across the middle
+        sel2, probs2 = hip.Buffer(2 * K2 * 4), hip.Buffer(2 * K2 * 4)
+        hip.builtin("route", [sel2, probs2, up(hip, lz)], b=2, e=E2, k=K2)
+        gs = sel2.read(np.int32).reshape(2, K2)
+        gp = probs2.read(np.float32).reshape(2, K2)
+        for b in range(2):
+            ws, wp = np.empty(K2, np.int32), np.empty(K2, np.float32)
+            O.oracle().or_route(ws.ctypes.data, wp.ctypes.data, np.ascontiguousarray(lz[b]).ctypes.data, E2, K2)
+            assert np.array_equal(gs[b], ws), (E2, b, gs[b], ws)
+            assert np.array_equal(gs[b], np.lexsort((np.arange(E2), -lz[b]))[:K2])
+            assert np.all(np.abs(gp[b] - wp) <= 1e-6 * np.abs(wp) + 1e-9)
+        assert list(gs[0, :3]) == [0, 1, E2 - 1]
 
 
 @pytest.mark.parametrize("wdt", [DT_FP8, DT_BF16])

@@ -52,15 +52,16 @@ __device__ __forceinline__ void w16(const uint4 &q0, const uint4 &q1, float o[16
 
 // sum over aligned groups of G lanes (G a power of two <= 64); every lane of
 // a group gets the sum.  DPP within a row of 16 lanes (quad pairs, quads,
-// half-row mirror, row mirror): VALU operations with no LDS round trip, where
-// a __shfl_xor butterfly compiles to dependent ds_bpermute waits.
+// half-row mirror, row mirror), then the permlane swaps across rows: VALU
+// operations with no LDS round trip, where a __shfl_xor butterfly compiles to
+// dependent ds_bpermute waits.
 __device__ __forceinline__ float group_sum(float v, int G) {
   if (G >= 2) v += dpp_f<0xB1>(v);     // quad_perm [1,0,3,2]
   if (G >= 4) v += dpp_f<0x4E>(v);     // quad_perm [2,3,0,1]
   if (G >= 8) v += dpp_f<0x141>(v);    // row_half_mirror
   if (G >= 16) v += dpp_f<0x140>(v);   // row_mirror
-  if (G >= 32) v += __shfl_xor(v, 16);
-  if (G >= 64) v += __shfl_xor(v, 32);
+  if (G >= 32) v += xor16_f(v);
+  if (G >= 64) v += xor32_f(v);
   return v;
 }
 

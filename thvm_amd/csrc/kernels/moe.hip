@@ -33,29 +33,52 @@
 
 // ---- router ---------------------------------------------------------------
 // top-K of one row's E <= 64 logits by one wave (lane e holds logit e):
-// every lane ends with the K ids and probabilities.  Each round takes the
-// wave max of the unused logits (DPP) and the lowest lane holding it (a
-// ballot): the winner of a (value desc, index asc) scan, ties to the lowest
-// expert id as the reference's serial scan picks them, with no cross-lane
-// shuffle round trips.
+// every lane ends with the K ids and probabilities.  The order is the
+// reference's serial scan: value descending, ties to the lowest expert id
+// (finite logits; NaN ones are put after every number, by id).  Each lane
+// builds a 64-bit key that orders its logit that way -- class (number 2,
+// NaN 1, lane past E 0), the order-preserving bits of the value (-0 taken
+// as +0, so the two tie), 63 - lane -- and counts the keys above its own
+// through LDS, 16 keys per batch of reads (all distinct: the rank of its
+// logit); slot k is the lane of rank k (a ballot).  (K rounds of a wave max
+// and a ballot each were a dependent chain of DPP steps on one wave.)
 __device__ __forceinline__ void route_wave(float g, uint32_t lane, uint32_t E, uint32_t K,
                                            int32_t (&ids)[MOE_MAXK], float (&pr)[MOE_MAXK]) {
+  __shared__ __align__(16) uint64_t rkey[64];
   const float mx = wave_max(g);
   const float pe = lane < E ? expf(g - mx) : 0.0f;   // each lane's numerator, computed once
   const float sum = wave_sum(pe);
-  bool used = lane >= E;
+  const uint32_t gb = __float_as_uint(g + 0.0f);       // -0 -> +0
+  const uint32_t ord = (gb & 0x80000000u) ? ~gb : (gb | 0x80000000u);
+  const uint64_t cls = lane >= E ? 0ull : (g != g) ? 1ull : 2ull;
+  const uint64_t key = (cls << 38) | ((cls == 2ull ? (uint64_t)ord : 0ull) << 6) | (63u - lane);
+  rkey[lane] = key;
+  // one wave writes and reads the keys, and its LDS operations complete in
+  // order: only the compiler must keep the order
+  __builtin_amdgcn_wave_barrier();
+  asm volatile("" ::: "memory");
+  uint32_t rank = 0;
+#pragma unroll 1
+  for (int jb = 0; jb < 64; jb += 16) {
+    uint4 kv[8];
+#pragma unroll
+    for (int i = 0; i < 8; i++) kv[i] = *(const uint4 *)&rkey[jb + 2 * i];
+#pragma unroll
+    for (int i = 0; i < 8; i++)
+      rank += (((uint64_t)kv[i].y << 32 | kv[i].x) > key ? 1u : 0u) +
+              (((uint64_t)kv[i].w << 32 | kv[i].z) > key ? 1u : 0u);
+  }
+  const float pl = pe / sum;                           // every lane's probability, in parallel
 #pragma unroll
   for (uint32_t kk = 0; kk < MOE_MAXK; kk++) {
     if (kk >= K) break;
-    const float v = used ? -INFINITY : g;
-    const float bv = wave_max(v);
-    uint64_t m = __ballot(!used && v == bv);
-    if (!m) m = __ballot(!used);            // no unused lane equals the max (NaN logits)
+    const uint64_t m = __ballot(rank == kk);           // exactly one lane
     const int bi = m ? (int)__builtin_ctzll(m) : 0;
-    if ((int)lane == bi) used = true;
     ids[kk] = bi;
-    pr[kk] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(pe), bi)) / sum;   // expf(bv - mx)
+    pr[kk] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(pl), bi));   // expf(g_bi - mx) / sum
   }
+  __builtin_amdgcn_wave_barrier();                     // rkey is rewritten by the next call
+  asm volatile("" ::: "memory");
 }
 
 __global__ __launch_bounds__(64) void k_route(ThvmRouteArgs a) {
@@ -334,6 +357,7 @@ __global__ __launch_bounds__(MOE_THREADS) void k_moe_gateup(ThvmMoeArgs a) {
 #pragma unroll
         for (uint32_t kk = 0; kk < MOE_MAXK; kk++)
           if (kk < K) { a.sel_out[(uint64_t)b * K + kk] = rids[kk]; a.probs_out[(uint64_t)b * K + kk] = rpr[kk]; }
+      pclk(a.clk, a.clk_cap, 6);
     }
     __syncthreads();
 #pragma unroll
@@ -429,7 +453,10 @@ __global__ __launch_bounds__(MOE_THREADS) void k_moe_gateup(ThvmMoeArgs a) {
 }
 
 // ---- down + residual ------------------------------------------------------
-// grid (ceil(D / 4), B): two waves per output row d.  The row's segments are
+// grid (ceil(D / (DW / 2)), B), DW waves: two waves per output row d.  (Every
+// block stages the whole h row in LDS, 45 KiB at C5; 16 waves per block
+// halved those reads but ended no sooner than 8: 8.23 against 8.08 us in the
+// phase clock, the wider block waiting on its slowest wave's rows.)  The row's segments are
 // split at routed slot c: wave half 0 takes slots [0, c), half 1 slots
 // [c, K) and the shared segment (c balances their bytes, each half at most
 // MOE_HALFK slots), so each wave holds half the rows in flight and a CU runs
@@ -445,14 +472,14 @@ __device__ __forceinline__ uint32_t moe_down_split(uint32_t K, uint32_t I, uint3
   if (c > K) c = K;
   return c;
 }
-template <bool FP8, int NC, int NCS>   /* 16-byte chunks per lane: routed rows, shared row */
-__global__ __launch_bounds__(MOE_THREADS, 4) void k_moe_down(ThvmMoeArgs a) {
+template <bool FP8, int NC, int NCS, int DW>   /* 16-byte chunks per lane: routed rows, shared row; waves */
+__global__ __launch_bounds__(64 * DW, 4) void k_moe_down(ThvmMoeArgs a) {
   extern __shared__ float hs[];
-  __shared__ float part[MOE_WAVES / 2];
+  __shared__ float part[DW / 2];
   const uint32_t b = blockIdx.y, D = a.D, I = a.I, K = a.K, S = a.S;
   const uint32_t P = K * I + S;
   const uint32_t lane = threadIdx.x & 63, wv = threadIdx.x >> 6, hf = wv & 1, rw = wv >> 1;
-  const uint32_t d = blockIdx.x * (MOE_WAVES / 2) + rw;
+  const uint32_t d = blockIdx.x * (DW / 2) + rw;
   // phase clock: 0 entry, 1 rows issued, 2 h staged, 3 half sums done, 7
   // drained
   pclk(a.clk, a.clk_cap, 0);
@@ -1169,22 +1196,23 @@ extern "C" int thvm_k_moe_down(const ThvmMoeArgs *a, hipStream_t s, char *err, i
   const uint32_t P = a->K * a->I + a->S;
   const uint32_t lds = P * 4;
   if (lds > 160 * 1024) { snprintf(err, errlen, "moe: K*I+S too large for LDS"); return -1; }
-  const dim3 grid((a->D + MOE_WAVES / 2 - 1) / (MOE_WAVES / 2), a->B);
-  // chunks per lane sized to the rows (registers: two blocks per CU)
+  constexpr int DW = 8;                           // waves per block: 4 output rows
+  const dim3 grid((a->D + DW / 2 - 1) / (DW / 2), a->B);
+  // chunks per lane sized to the rows (registers: 16 waves per CU)
   const uint32_t wsz = a->wdt == THVM_DT_FP8E4M3 ? 1 : 2;
   const bool nc2 = a->I * wsz / 16 <= 128, ncs4 = a->S * wsz / 16 <= 256;
   moe_fn f;
   if (a->wdt == THVM_DT_FP8E4M3)
-    f = nc2 ? (ncs4 ? k_moe_down<true, 2, 4> : k_moe_down<true, 2, 8>)
-            : (ncs4 ? k_moe_down<true, 4, 4> : k_moe_down<true, 4, 8>);
+    f = nc2 ? (ncs4 ? k_moe_down<true, 2, 4, DW> : k_moe_down<true, 2, 8, DW>)
+            : (ncs4 ? k_moe_down<true, 4, 4, DW> : k_moe_down<true, 4, 8, DW>);
   else
-    f = nc2 ? (ncs4 ? k_moe_down<false, 2, 4> : k_moe_down<false, 2, 8>)
-            : (ncs4 ? k_moe_down<false, 4, 4> : k_moe_down<false, 4, 8>);
+    f = nc2 ? (ncs4 ? k_moe_down<false, 2, 4, DW> : k_moe_down<false, 2, 8, DW>)
+            : (ncs4 ? k_moe_down<false, 4, 4, DW> : k_moe_down<false, 4, 8, DW>);
   if (lds > 64 * 1024) {
     hipError_t e = hipFuncSetAttribute((const void *)f, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     if (e != hipSuccess) { snprintf(err, errlen, "moe_down: hipFuncSetAttribute: %s", hipGetErrorString(e)); return -1; }
   }
-  thvm_launch(true, true, f, grid, dim3(MOE_THREADS), lds, s, *a);
+  thvm_launch(true, true, f, grid, dim3(64 * DW), lds, s, *a);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) { snprintf(err, errlen, "moe_down launch: %s", hipGetErrorString(e)); return -1; }
   return 0;
