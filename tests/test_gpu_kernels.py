@@ -820,11 +820,11 @@ def test_attention_stale_rows_are_never_mixed(hip, mf):
 
 
 def test_attention_mfma_errors(hip):
-    """The MFMA split refuses f32 caches, more than 8 heads per kv head and
-    the one-launch form; mf out of range is an error."""
+    """The MFMA split refuses f32 caches and more than 8 heads per kv head;
+    mf out of range is an error."""
     B, Hkv, hd, ms = 1, 1, 64, 128
-    for H, cdt, kw in ((4, DT_F32, dict(mf=1)), (16, DT_BF16, dict(mf=1)),
-                       (4, DT_BF16, dict(mf=1, fused=1)), (4, DT_BF16, dict(mf=3))):
+    for H, cdt, kw in ((4, DT_F32, dict(mf=1)), (16, DT_BF16, dict(mf=1)), (16, DT_BF16, dict(mf=1, fused=1)),
+                       (4, DT_BF16, dict(mf=3))):
         z = np.zeros(B * H * hd, NP_STORE[cdt])
         kv = np.zeros(B * Hkv * ms * hd, NP_STORE[cdt])
         with pytest.raises(hip.ThvmHipError, match="mf|MFMA"):
@@ -840,6 +840,29 @@ def test_attention_cpb_errors(hip):
             run_attn(hip, z, kv, kv, B, H, Hkv, hd, ms, 5, cdt, **kw)
     with pytest.raises(hip.ThvmHipError):        # the VALU split, 8 heads per kv head: one chunk per block only
         run_attn(hip, z, kv, kv, B, H, Hkv, hd, ms, 5, cdt, cpb=2, mf=2)
+
+
+@pytest.mark.parametrize("H,Hkv,hd", [(32, 8, 128), (8, 8, 64), (16, 2, 64)])
+def test_attention_mfma_one_launch_repeated(hip, H, Hkv, hd):
+    """The one-launch MFMA form (the last split block of a row and kv head
+    merges) on one partial buffer over changing lengths and chunks per block:
+    every merge finds its counter at zero, and the outputs are the two-launch
+    MFMA form's bit for bit (the same fold) and within the bars of the
+    oracle."""
+    B, ms, cdt = 2, 640, DT_BF16
+    rng = np.random.default_rng(H + hd)
+    qs, _ = rand_store(rng, (B, H, hd), cdt)
+    ks, _ = rand_store(rng, (B, Hkv, ms, hd), cdt)
+    vs, _ = rand_store(rng, (B, Hkv, ms, hd), cdt)
+    nsplit = (ms + 63) // 64
+    part1 = hip.Buffer(B * H * nsplit * (hd + 2) * 4 + B * Hkv * 4)
+    part2 = hip.Buffer(B * H * nsplit * (hd + 2) * 4 + B * Hkv * 4)
+    for L, cpb in ((640, 0), (1, 0), (65, 2), (300, 0), (17, 3), (129, 1), (640, 4), (64, 0)):
+        say(f"case: attn mfma one launch H={H} Hkv={Hkv} hd={hd} L={L} cpb={cpb}")
+        one, ww = run_attn(hip, qs, ks, vs, B, H, Hkv, hd, ms, L, cdt, part=part1, mf=1, fused=1, cpb=cpb)
+        two, _ = run_attn(hip, qs, ks, vs, B, H, Hkv, hd, ms, L, cdt, part=part2, mf=1, fused=0, cpb=cpb)
+        assert np.array_equal(one, two), (L, cpb, np.max(np.abs(one - two)))
+        assert attn_close(one, ww, cdt), (L, cpb, np.max(np.abs(one - ww)))
 
 
 def test_attention_fused_repeated(hip):

@@ -330,9 +330,12 @@ __global__ __launch_bounds__(ATT_THREADS, 4) void k_attn_multi(ThvmAttnArgs a) {
 // waves meet once through LDS and the block writes the same partial (acc, m,
 // l) the merge kernel folds.  Rows at or past the block's end read zero
 // through the no-access offset (a stale cache row times a zero weight could
-// still be a NaN).
+// still be a NaN).  GF > 0 (the one-launch form, G = GF heads per kv head):
+// the partial goes out with system-scope stores and the last split block of
+// the (row, kv head) merges the group in the same launch
+// (attn_handoff_merge: the merge kernel's fold, so the same outputs).
 #define MF_GMAX 8
-template <int HD, int AT>
+template <int HD, int AT, int GF = 0>
 __global__ __launch_bounds__(ATT_THREADS) void k_attn_mf(ThvmAttnArgs a) {
   static_assert(AT == AT_BF16 || AT == AT_F16, "16-bit caches");
   constexpr int XT = AT == AT_BF16 ? GX_BF16 : GX_F16;
@@ -486,9 +489,23 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attn_mf(ThvmAttnArgs a) {
       sv += wacc[w][g][d] * f;
       lt += f * wl[w][g];
     }
-    float *pp = a.part + (((uint64_t)b * a.H + kvh * G + g) * a.n_split + grp) * (HD + 2);
-    pp[d] = sv;
-    if (d == 0) { pp[HD] = M; pp[HD + 1] = lt; }
+    const uint64_t pi = (((uint64_t)b * a.H + kvh * G + g) * a.n_split + grp) * (HD + 2);
+    if (GF) {
+      coh_stf(a.part, (uint32_t)((pi + d) * 4), sv);
+      if (d == 0) {
+        coh_stf(a.part, (uint32_t)((pi + HD) * 4), M);
+        coh_stf(a.part, (uint32_t)((pi + HD + 1) * 4), lt);
+      }
+    } else {
+      float *pp = a.part + pi;
+      pp[d] = sv;
+      if (d == 0) { pp[HD] = M; pp[HD + 1] = lt; }
+    }
+  }
+  if (GF) {
+    __shared__ MergeFlatLds<HD, (GF ? GF : 1)> ms;
+    __shared__ uint32_t last;
+    attn_handoff_merge<HD, (GF ? GF : 1), AT>(a, b, kvh, attn_live(a, L), &last, ms);
   }
   pclk_end(a.clk, a.clk_cap);
 }
@@ -559,7 +576,7 @@ extern "C" uint32_t thvm_k_attn_auto_cpb(uint32_t B, uint32_t H, uint32_t Hkv, u
 static bool attn_mf_can(const ThvmAttnArgs *a) {
   const uint32_t G = a->Hkv ? a->H / a->Hkv : 0;
   return a->cdt != THVM_DT_FP32 && (a->hd == 64 || a->hd == 128) && G >= 1 && G <= MF_GMAX &&
-         (G & (G - 1)) == 0 && a->fused != 1;
+         (G & (G - 1)) == 0;
 }
 
 // chunks per block of the MFMA split for cpb = 0: the grid one round of
@@ -588,9 +605,37 @@ extern "C" void thvm_k_attn_plan(const ThvmAttnArgs *a, uint32_t *mf, uint32_t *
   *cpb = c;
 }
 
+// the one-launch MFMA split for G heads per kv head
+template <int HD, int AT>
+static attn_fn attn_pick_mf_fused(uint32_t G) {
+  switch (G) {
+    case 1: return k_attn_mf<HD, AT, 1>;
+    case 2: return k_attn_mf<HD, AT, 2>;
+    case 4: return k_attn_mf<HD, AT, 4>;
+    case 8: return k_attn_mf<HD, AT, 8>;
+    default: return nullptr;
+  }
+}
+
 static int attn_mf_launch(const ThvmAttnArgs *a, hipStream_t s, char *err, int errlen) {
   const uint32_t G = a->H / a->Hkv;
   const int at = a->cdt == THVM_DT_BF16 ? AT_BF16 : AT_F16;
+  if (a->fused == 1) {                            // split and merge in one launch
+    attn_fn ff = a->hd == 128 ? (at == AT_BF16 ? attn_pick_mf_fused<128, AT_BF16>(G) : attn_pick_mf_fused<128, AT_F16>(G))
+                              : (at == AT_BF16 ? attn_pick_mf_fused<64, AT_BF16>(G) : attn_pick_mf_fused<64, AT_F16>(G));
+    if (!ff) { snprintf(err, errlen, "attn: no one-launch MFMA split for G=%u", G); return -1; }
+    if ((uint64_t)a->B * a->H * a->n_split * (a->hd + 2) * 4 >= (1ull << 31)) {
+      snprintf(err, errlen, "attn: partials of 2 GiB or more");
+      return -1;
+    }
+    ThvmAttnArgs ak = *a;
+    uint32_t mf = 0;
+    thvm_k_attn_plan(a, &mf, &ak.cpb);
+    thvm_launch(true, true, ff, dim3(a->Hkv, (a->n_split + ak.cpb - 1) / ak.cpb, a->B), dim3(ATT_THREADS), 0, s, ak);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) { snprintf(err, errlen, "attn launch: %s", hipGetErrorString(e)); return -1; }
+    return 0;
+  }
   attn_fn f = a->hd == 128 ? (at == AT_BF16 ? k_attn_mf<128, AT_BF16> : k_attn_mf<128, AT_F16>)
                            : (at == AT_BF16 ? k_attn_mf<64, AT_BF16> : k_attn_mf<64, AT_F16>);
   // the merge: at 8 rows and more one block per (row, query head) -- the
@@ -650,7 +695,7 @@ extern "C" int thvm_k_attn_decode(const ThvmAttnArgs *a, hipStream_t s, char *er
     const uint32_t G = a->H / a->Hkv;
     if (a->mf == 1 && !attn_mf_can(a)) {
       snprintf(err, errlen, "attn: the MFMA split takes 16-bit caches, hd 64 or 128, G in 1, 2, 4, 8 "
-               "and two launches (hd=%u G=%u fused=%u)", a->hd, G, a->fused);
+               "(hd=%u G=%u)", a->hd, G);
       return -1;
     }
     uint32_t mf = 0, cpb = 0;
