@@ -644,8 +644,8 @@ def run_spec(thvm, args) -> dict:
 
 
 PHASES = {
-    "gemv": ["entry", "loads issued", "x staged", "first batch consumed", "rows done", "partials summed", "",
-             "end (drained)"],
+    "gemv": ["entry", "loads issued", "x staged", "first batch consumed", "rows done", "partials summed",
+             "t0 x arrived", "end (drained)"],
     "attn": ["entry", "loads issued + q", "first chunk consumed", "chunks done", "row groups combined",
              "waves in LDS", "", "end (drained)"],
     "merge": ["entry", "partials folded", "partitions combined", "", "", "", "", "end (drained)"],

@@ -46,7 +46,7 @@ __device__ __forceinline__ uint32_t attn_live(const ThvmAttnArgs &a, int32_t L) 
 }
 
 // one block per (row, kv head): the group's G heads
-template <int HD, int G, int AT>
+template <int HD, int G, int AT, int MC>
 __global__ __launch_bounds__(MERGE_THREADS) void k_attn_merge(ThvmAttnArgs a) {
   __shared__ MergeFlatLds<HD, G> s;
   const uint32_t b = blockIdx.x / a.Hkv, kvh = blockIdx.x % a.Hkv;
@@ -55,8 +55,9 @@ __global__ __launch_bounds__(MERGE_THREADS) void k_attn_merge(ThvmAttnArgs a) {
   uint64_t *const clk = a.clk ? a.clk + (uint64_t)a.clk_cap * PCLK_MARKS : nullptr;
   pclk(clk, a.clk_cap, 0);
   const uint32_t cpb = a.cpb > 1 ? a.cpb : 1u;
-  attn_merge_flat<HD, G, AT, false>(a, b, kvh, attn_live(a, attn_row_len(a, b)), threadIdx.x, true, s,
-                                    (a.n_split + cpb - 1) / cpb, clk, a.clk_cap);
+  // (the row length is read after the first partial loads are out)
+  attn_merge_flat_d<HD, G, AT, false, MC>(a, b, kvh, [&] { return attn_live(a, attn_row_len(a, b)); },
+                                      threadIdx.x, true, s, (a.n_split + cpb - 1) / cpb, clk, a.clk_cap);
   pclk_end(clk, a.clk_cap);
 }
 
@@ -65,10 +66,12 @@ __global__ __launch_bounds__(MERGE_THREADS) void k_attn_merge(ThvmAttnArgs a) {
 // agent-scope atomic, B*Hkv words after the partials, zero between launches
 // -- and merge the group when this block brings the count to n_live (then
 // reset the counter).  No fence: the partials never sit in an L2.
-template <int HD, int G, int AT>
+// PH: the group's heads merged one after another, each as a group of one
+// (the per-head merge kernel's fold; ms is then a MergeFlatLds<HD, 1>).
+template <int HD, int G, int AT, bool PH = false>
 __device__ __forceinline__ void attn_handoff_merge(const ThvmAttnArgs &a, uint32_t b, uint32_t kvh,
                                                    uint32_t n_live, uint32_t *last,
-                                                   MergeFlatLds<HD, G> &ms) {
+                                                   MergeFlatLds<HD, PH ? 1 : G> &ms) {
   vm_drain();
   __syncthreads();
   if (threadIdx.x == 0) {
@@ -79,7 +82,14 @@ __device__ __forceinline__ void attn_handoff_merge(const ThvmAttnArgs &a, uint32
   }
   __syncthreads();
   if (!*last) return;                              // block-uniform
-  attn_merge_flat<HD, G, AT, true>(a, b, kvh, n_live, threadIdx.x, true, ms);
+  if constexpr (PH) {
+    for (uint32_t g = 0; g < (uint32_t)G; g++) {
+      if (g) __syncthreads();                      // the previous head's LDS reads are done
+      attn_merge_flat<HD, 1, AT, true>(a, b, kvh * G + g, n_live, threadIdx.x, true, ms);
+    }
+  } else {
+    attn_merge_flat<HD, G, AT, true>(a, b, kvh, n_live, threadIdx.x, true, ms);
+  }
 }
 
 // Split and merge in one launch, one chunk per block: each split unit
@@ -332,8 +342,9 @@ __global__ __launch_bounds__(ATT_THREADS, 4) void k_attn_multi(ThvmAttnArgs a) {
 // through the no-access offset (a stale cache row times a zero weight could
 // still be a NaN).  GF > 0 (the one-launch form, G = GF heads per kv head):
 // the partial goes out with system-scope stores and the last split block of
-// the (row, kv head) merges the group in the same launch
-// (attn_handoff_merge: the merge kernel's fold, so the same outputs).
+// the (row, kv head) merges the group's heads in the same launch, one after
+// another (attn_handoff_merge: the per-head merge kernel's fold, so the same
+// outputs as the two-launch form).
 #define MF_GMAX 8
 template <int HD, int AT, int GF = 0>
 __global__ __launch_bounds__(ATT_THREADS) void k_attn_mf(ThvmAttnArgs a) {
@@ -503,9 +514,9 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attn_mf(ThvmAttnArgs a) {
     }
   }
   if (GF) {
-    __shared__ MergeFlatLds<HD, (GF ? GF : 1)> ms;
+    __shared__ MergeFlatLds<HD, 1> ms;
     __shared__ uint32_t last;
-    attn_handoff_merge<HD, (GF ? GF : 1), AT>(a, b, kvh, attn_live(a, L), &last, ms);
+    attn_handoff_merge<HD, (GF ? GF : 1), AT, true>(a, b, kvh, attn_live(a, L), &last, ms);
   }
   pclk_end(a.clk, a.clk_cap);
 }
@@ -521,13 +532,22 @@ static attn_fn attn_pick_multi(uint32_t G, bool fused) {
     default: return nullptr;
   }
 }
+template <int HD, int G, int AT>
+static attn_fn attn_pick_merge_mc(uint32_t mc) {
+  return mc <= 4 ? k_attn_merge<HD, G, AT, 4> : mc <= 8 ? k_attn_merge<HD, G, AT, 8> : k_attn_merge<HD, G, AT, MCH>;
+}
+// the merge for G heads per group and nmax partials: the load batch MC just
+// covers a partition's share of the partials (the loads past it would read
+// slot 0 again for nothing -- at 8 blocks the merge is bound by its load
+// instructions, not by bytes), at most MCH
 template <int HD, int AT>
-static attn_fn attn_pick_merge(uint32_t G) {
+static attn_fn attn_pick_merge(uint32_t G, uint32_t nmax) {
+  const uint32_t np = MERGE_THREADS / (G * HD / 2), mc = (nmax + np - 1) / np;
   switch (G) {
-    case 1: return k_attn_merge<HD, 1, AT>;
-    case 2: return k_attn_merge<HD, 2, AT>;
-    case 4: return k_attn_merge<HD, 4, AT>;
-    case 8: return k_attn_merge<HD, 8, AT>;
+    case 1: return attn_pick_merge_mc<HD, 1, AT>(mc);
+    case 2: return attn_pick_merge_mc<HD, 2, AT>(mc);
+    case 4: return attn_pick_merge_mc<HD, 4, AT>(mc);
+    case 8: return attn_pick_merge_mc<HD, 8, AT>(mc);
     default: return nullptr;
   }
 }
@@ -638,27 +658,26 @@ static int attn_mf_launch(const ThvmAttnArgs *a, hipStream_t s, char *err, int e
   }
   attn_fn f = a->hd == 128 ? (at == AT_BF16 ? k_attn_mf<128, AT_BF16> : k_attn_mf<128, AT_F16>)
                            : (at == AT_BF16 ? k_attn_mf<64, AT_BF16> : k_attn_mf<64, AT_F16>);
-  // the merge: at 8 rows and more one block per (row, query head) -- the
-  // G = 1 merge over the per-head partials, each query head taken as its own
-  // group (C4 batch 16: 2.990 -> 2.981 ms per step); below, one block per
-  // (row, kv head) (C4 batch 1: one block per head measured 2.004 against
-  // 1.991 ms).  A speculative verify (batch 1 base) keeps the group merge,
-  // so its rows fold as the base step's do.
-  const bool per_head = !a->spec && a->B >= 8;
-  const uint32_t Gm = per_head ? 1u : G;
-  attn_fn fm = a->hd == 128 ? (at == AT_BF16 ? attn_pick_merge<128, AT_BF16>(Gm) : attn_pick_merge<128, AT_F16>(Gm))
-                            : (at == AT_BF16 ? attn_pick_merge<64, AT_BF16>(Gm) : attn_pick_merge<64, AT_F16>(Gm));
+  // the merge: one block per (row, query head) -- the G = 1 merge over the
+  // per-head partials, each query head taken as its own group, with a load
+  // batch sized to the partials (C4 batch 16: 2.990 -> 2.981 ms per step;
+  // batch 1, against one block per (row, kv head): 1.984 -> 1.936 ms, the 8
+  // group blocks were bound by their load instructions).  Every MFMA form
+  // (the one-launch form and a speculative verify included) folds this way.
+  ThvmAttnArgs ak = *a;
+  uint32_t mf = 0;
+  thvm_k_attn_plan(a, &mf, &ak.cpb);
+  const uint32_t nmax = (a->n_split + ak.cpb - 1) / ak.cpb;
+  attn_fn fm = a->hd == 128 ? (at == AT_BF16 ? attn_pick_merge<128, AT_BF16>(1, nmax) : attn_pick_merge<128, AT_F16>(1, nmax))
+                            : (at == AT_BF16 ? attn_pick_merge<64, AT_BF16>(1, nmax) : attn_pick_merge<64, AT_F16>(1, nmax));
   if (!fm) { snprintf(err, errlen, "attn: no merge kernel for G=%u", G); return -1; }
   if ((uint64_t)a->B * a->H * a->n_split * (a->hd + 2) * 4 >= (1ull << 31)) {
     snprintf(err, errlen, "attn: partials of 2 GiB or more");
     return -1;
   }
-  ThvmAttnArgs ak = *a;
-  uint32_t mf = 0;
-  thvm_k_attn_plan(a, &mf, &ak.cpb);
   thvm_launch(true, false, f, dim3(a->Hkv, (a->n_split + ak.cpb - 1) / ak.cpb, a->B), dim3(ATT_THREADS), 0, s, ak);
   ThvmAttnArgs am = ak;
-  if (per_head) am.Hkv = a->H;                    // groups of one head
+  am.Hkv = a->H;                                  // groups of one head
   thvm_launch(false, true, fm, dim3(a->B * am.Hkv), dim3(MERGE_THREADS), 0, s, am);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) { snprintf(err, errlen, "attn launch: %s", hipGetErrorString(e)); return -1; }
@@ -709,14 +728,15 @@ extern "C" int thvm_k_attn_decode(const ThvmAttnArgs *a, hipStream_t s, char *er
   attn_fn f = nullptr, fm = nullptr;
   const uint32_t G = a->H / a->Hkv;
   const int at = a->cdt == THVM_DT_BF16 ? AT_BF16 : a->cdt == THVM_DT_FP16 ? AT_F16 : AT_F32;
+  const uint32_t nmax = (a->n_split + cpb - 1) / cpb;     // the merge's partial slots
   if (a->hd == 128) {
     f = cpb > 1 ? (at == AT_BF16 ? attn_pick_multi<128, AT_BF16>(G, fused) : at == AT_F16 ? attn_pick_multi<128, AT_F16>(G, fused) : attn_pick_multi<128, AT_F32>(G, fused))
         : at == AT_BF16 ? attn_pick<128, AT_BF16>(G, fused) : at == AT_F16 ? attn_pick<128, AT_F16>(G, fused) : attn_pick<128, AT_F32>(G, fused);
-    fm = at == AT_BF16 ? attn_pick_merge<128, AT_BF16>(G) : at == AT_F16 ? attn_pick_merge<128, AT_F16>(G) : attn_pick_merge<128, AT_F32>(G);
+    fm = at == AT_BF16 ? attn_pick_merge<128, AT_BF16>(G, nmax) : at == AT_F16 ? attn_pick_merge<128, AT_F16>(G, nmax) : attn_pick_merge<128, AT_F32>(G, nmax);
   } else if (a->hd == 64) {
     f = cpb > 1 ? (at == AT_BF16 ? attn_pick_multi<64, AT_BF16>(G, fused) : at == AT_F16 ? attn_pick_multi<64, AT_F16>(G, fused) : attn_pick_multi<64, AT_F32>(G, fused))
         : at == AT_BF16 ? attn_pick<64, AT_BF16>(G, fused) : at == AT_F16 ? attn_pick<64, AT_F16>(G, fused) : attn_pick<64, AT_F32>(G, fused);
-    fm = at == AT_BF16 ? attn_pick_merge<64, AT_BF16>(G) : at == AT_F16 ? attn_pick_merge<64, AT_F16>(G) : attn_pick_merge<64, AT_F32>(G);
+    fm = at == AT_BF16 ? attn_pick_merge<64, AT_BF16>(G, nmax) : at == AT_F16 ? attn_pick_merge<64, AT_F16>(G, nmax) : attn_pick_merge<64, AT_F32>(G, nmax);
   }
   if (!f || !fm) {
     snprintf(err, errlen, "attn: no kernel for hd=%u G=%u cpb=%u", a->hd, G, cpb);

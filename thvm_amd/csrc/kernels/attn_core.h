@@ -285,12 +285,16 @@ struct AttnSplit {
 // The G heads of query row b and kv head kvh, by 512 threads: thread t owns
 // the output pair (g, d) = (e / (HD/2), 2 (e % (HD/2))), e = t % PAIRS, and
 // folds the live partials s = p, p + NP, p + 2 NP, ... of its partition
-// p = t / PAIRS (NP = 512 / PAIRS partitions), loading up to MCH of them
-// before any arithmetic (one memory round trip for up to NP * MCH partials);
+// p = t / PAIRS (NP = 512 / PAIRS partitions), loading up to MC of them
+// before any arithmetic (one memory round trip for up to NP * MC partials;
+// MC only batches the loads, the fold order is the same for every MC);
 // partition 0 then folds partitions 1 .. NP-1 in order.  The fold of (m, l,
 // acc) into (mp, lp, ap): mn = max(mp, m), lp = lp 2^(mp-mn) + l 2^(m-mn),
 // likewise ap; out = ap / lp.  Every caller (the merge kernel, the one-launch
-// form, the persistent step) runs this function, so all give the same bits.
+// forms, the persistent step) runs this function, so all that group the heads
+// alike give the same bits (the VALU forms merge a kv head's G heads as one
+// group, the MFMA forms each head as a group of one: NP differs, and so does
+// the fold order).
 // COH: system-scope loads of the partials and stores of the output.
 #define MERGE_THREADS 512
 #define MCH 16
@@ -313,15 +317,17 @@ __device__ __forceinline__ void merge_fold(float &mp, float &lp, float &a0, floa
   mp = mn;
 }
 
-// n_live partials of the (row, kv head) are folded.  n_max >= n_live bounds
-// the slots the first batch of loads may touch (0: n_live): a bound known at
-// launch lets those loads go out before the row length (and so n_live) is
-// back from memory; slots past n_live are read but never folded.
-template <int HD, int G, int AT, bool COH>
-__device__ __forceinline__ void attn_merge_flat(const ThvmAttnArgs &a, uint32_t b, uint32_t kvh,
-                                                uint32_t n_live, int tid, bool active,
-                                                MergeFlatLds<HD, G> &s, uint32_t n_max = 0,
-                                                uint64_t *clk = nullptr, uint32_t clk_cap = 0) {
+// n_live partials of the (row, kv head) are folded; nl() gives n_live.
+// n_max >= n_live bounds the slots the first batch of loads may touch (0:
+// n_live): with a bound known at launch those loads go out first and nl()
+// is called only after them, so a row length read from memory there costs
+// no round trip of its own (it arrives with the partials); slots past
+// n_live are read but never folded.
+template <int HD, int G, int AT, bool COH, int MC = MCH, class NLive>
+__device__ __forceinline__ void attn_merge_flat_d(const ThvmAttnArgs &a, uint32_t b, uint32_t kvh,
+                                                  NLive &&nl, int tid, bool active,
+                                                  MergeFlatLds<HD, G> &s, uint32_t n_max = 0,
+                                                  uint64_t *clk = nullptr, uint32_t clk_cap = 0) {
   typedef MergeFlatLds<HD, G> FL;
   constexpr int PAIRS = FL::PAIRS, NP = FL::NP;
   static_assert(NP >= 1 && MERGE_THREADS % PAIRS == 0, "merge geometry");
@@ -329,15 +335,16 @@ __device__ __forceinline__ void attn_merge_flat(const ThvmAttnArgs &a, uint32_t 
   const int g = e / (HD / 2), d = (e % (HD / 2)) * 2;
   const uint64_t bh = (uint64_t)b * a.H + kvh * G + g;
   const uint64_t pbi = bh * a.n_split * (HD + 2);
-  const uint32_t nmax = n_max ? n_max : n_live;
   float mp = -INFINITY, lp = 0.0f, a0 = 0.0f, a1 = 0.0f;
   if (active && p < NP) {
-    for (uint32_t s0 = p; s0 < nmax; s0 += NP * MCH) {
-      float mv[MCH], lv[MCH];
-      float2 av[MCH];
+    float mv[MC], lv[MC];
+    float2 av[MC];
+    // loads of slots s0 + j NP (slots at or past `bound` read slot 0 instead:
+    // every load stays inside the group's partials; those are never folded)
+    auto load = [&](uint32_t s0, uint32_t bound) {
 #pragma unroll
-      for (int j = 0; j < MCH; j++) {            // loads first (clamped, unconditional)
-        const uint32_t sp = s0 + j * NP, spc = sp < nmax ? sp : s0;
+      for (int j = 0; j < MC; j++) {
+        const uint32_t sp = s0 + j * NP, spc = sp < bound ? sp : 0u;
         const uint64_t q = pbi + (uint64_t)spc * (HD + 2);
         if (COH) {
           const uint2 r = coh_ld8(a.part, (uint32_t)((q + d) * 4));
@@ -352,10 +359,19 @@ __device__ __forceinline__ void attn_merge_flat(const ThvmAttnArgs &a, uint32_t 
           lv[j] = ml.y;
         }
       }
+    };
+    const uint32_t nmax = n_max ? n_max : nl();
+    if (nmax > 0) load((uint32_t)p, nmax);        // (nmax is uniform)
+    __builtin_amdgcn_sched_barrier(0);
+    const uint32_t n_live = nl();
 #pragma unroll
-      for (int j = 0; j < MCH; j++)
+    for (int j = 0; j < MC; j++)
+      if (p + j * NP < n_live) merge_fold(mp, lp, a0, a1, mv[j], lv[j], av[j].x, av[j].y);
+    for (uint32_t s0 = p + NP * MC; s0 < n_live; s0 += NP * MC) {
+      load(s0, n_live);
+#pragma unroll
+      for (int j = 0; j < MC; j++)
         if (s0 + j * NP < n_live) merge_fold(mp, lp, a0, a1, mv[j], lv[j], av[j].x, av[j].y);
-      if (s0 + NP * MCH >= n_live) break;
     }
   }
   pclk(clk, clk_cap, 1);
@@ -373,4 +389,13 @@ __device__ __forceinline__ void attn_merge_flat(const ThvmAttnArgs &a, uint32_t 
     st_act<AT, COH>(a.out, oi, a0 * inv);
     st_act<AT, COH>(a.out, oi + 1, a1 * inv);
   }
+}
+// the same with n_live known at the call
+template <int HD, int G, int AT, bool COH>
+__device__ __forceinline__ void attn_merge_flat(const ThvmAttnArgs &a, uint32_t b, uint32_t kvh,
+                                                uint32_t n_live, int tid, bool active,
+                                                MergeFlatLds<HD, G> &s, uint32_t n_max = 0,
+                                                uint64_t *clk = nullptr, uint32_t clk_cap = 0) {
+  attn_merge_flat_d<HD, G, AT, COH>(a, b, kvh, [n_live] { return n_live; }, tid, active, s, n_max, clk,
+                                    clk_cap);
 }

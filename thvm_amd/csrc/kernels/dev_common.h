@@ -23,11 +23,14 @@ typedef uint16_t f16_t;
 __device__ __forceinline__ float bf2f(bf16_t h) {
   return __uint_as_float(((uint32_t)h) << 16);
 }
+// f32 -> bf16, round to nearest even; a NaN becomes the quiet NaN of its
+// sign.  Written as a select: the early-return form compiled to two exec-mask
+// branches per conversion.
 __device__ __forceinline__ bf16_t f2bf(float f) {
-  uint32_t b = __float_as_uint(f);
-  if ((b & 0x7f800000u) == 0x7f800000u && (b & 0x7fffffu) != 0u)
-    return (bf16_t)(((b & 0x80000000u) | 0x7f800000u | 0x400000u) >> 16);
-  return (bf16_t)((b + 0x7fffu + ((b >> 16) & 1u)) >> 16);
+  const uint32_t b = __float_as_uint(f);
+  const uint32_t r = (b + 0x7fffu + ((b >> 16) & 1u)) >> 16;
+  const uint32_t q = ((b >> 16) & 0x8000u) | 0x7fc0u;
+  return (bf16_t)((b & 0x7fffffffu) > 0x7f800000u ? q : r);
 }
 // round a float through bf16 storage
 __device__ __forceinline__ float rbf(float f) { return bf2f(f2bf(f)); }

@@ -140,24 +140,24 @@ __device__ __forceinline__ float dot2acc(uint32_t x, uint32_t w, float acc) {
   return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2_t, x), __builtin_bit_cast(f16x2_t, w), acc, false);
 }
 
-template <int XT>
-__device__ __forceinline__ void xs_store(void *xs, uint32_t idx, float v) {
-  if (XT == XT_BF16) ((bf16_t *)xs)[idx] = f2bf(v);
-  else if (XT == XT_F16) ((f16_t *)xs)[idx] = f2h(v);
-  else ((float *)xs)[idx] = v;
-}
-
+#define GEMV_MAX_WAVES 16
 __device__ __forceinline__ float block_sum_g(float v, float *red, int nwaves) {
   float w = wave_sum(v);
   __syncthreads();
   if (lane_id() == 0) red[threadIdx.x >> 6] = w;
   __syncthreads();
+  // (every slot read at once, in wave order; slots at or past nwaves add
+  // +0, which leaves the sum's bits as they are: it starts at +0 and so is
+  // never -0)
   float t = 0.0f;
-  for (int i = 0; i < nwaves; i++) t += red[i];
+#pragma unroll
+  for (int i = 0; i < GEMV_MAX_WAVES; i++) {
+    const float r = red[i];
+    t += i < nwaves ? r : 0.0f;
+  }
   return t;
 }
 
-#define GEMV_MAX_WAVES 16
 #define XREG 16   /* x elements per thread kept in registers by the staging */
 
 // the output stage of one row group (one lane, wave-uniform values)
@@ -195,6 +195,53 @@ __device__ __forceinline__ void xvec(const void *x, uint64_t e, float *o) {
 template <int XD>
 __device__ __forceinline__ float rnd_x(float v) {
   return XD == XD_BF16 ? rbf(v) : XD == XD_F16 ? rh(v) : v;
+}
+// 16 raw bytes of x at element e (COH as in xvec)
+template <int XD, bool COH = false>
+__device__ __forceinline__ uint4 xraw(const void *x, uint64_t e) {
+  return COH ? coh_ld16(x, (uint32_t)(e * XDr<XD>::B)) : ld16((const char *)x + e * XDr<XD>::B);
+}
+// Staging stores.  In the LDS layout the G elements from a multiple of G
+// are one aligned 16-byte word, so x vector v (VE elements) lands with one
+// 16-byte store per G elements, not one store per element.
+// xs_put_raw: vector v of row m as loaded (its storage bits are the LDS type
+// unless the weights are f32, where 16-bit x is widened exactly);
+// xs_put_f: VE values rounded to the x dtype, as a norm kernel would store
+// them.
+template <int XD, int XT, int E>
+__device__ __forceinline__ void xs_put_raw(unsigned char *xs, uint32_t K, uint32_t C, uint32_t m,
+                                           uint32_t v, const uint4 &q) {
+  constexpr int VE = XDr<XD>::VE;
+  if (XT != XT_F32 || XD == XD_F32) {
+    *(uint4 *)(xs + (size_t)xs_index<XT, E>(K, C, m, v * VE) * XTr<XT>::B) = q;
+  } else {
+    float f[VE];
+    xdec<XD>(q, f);
+#pragma unroll
+    for (int h = 0; h < VE; h += 4)
+      *(uint4 *)(xs + (size_t)xs_index<XT, E>(K, C, m, v * VE + h) * 4u) =
+          make_uint4(__float_as_uint(f[h]), __float_as_uint(f[h + 1]),
+                     __float_as_uint(f[h + 2]), __float_as_uint(f[h + 3]));
+  }
+}
+template <int XD, int XT, int E>
+__device__ __forceinline__ void xs_put_f(unsigned char *xs, uint32_t K, uint32_t C, uint32_t m,
+                                         uint32_t v, const float *f) {
+  constexpr int VE = XDr<XD>::VE;
+  if (XT != XT_F32) {
+    uint32_t w[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+      w[i] = XT == XT_BF16 ? (uint32_t)f2bf(f[2 * i]) | ((uint32_t)f2bf(f[2 * i + 1]) << 16)
+                           : (uint32_t)f2h(f[2 * i]) | ((uint32_t)f2h(f[2 * i + 1]) << 16);
+    *(uint4 *)(xs + (size_t)xs_index<XT, E>(K, C, m, v * VE) * 2u) = make_uint4(w[0], w[1], w[2], w[3]);
+  } else {
+#pragma unroll
+    for (int h = 0; h < VE; h += 4)
+      *(uint4 *)(xs + (size_t)xs_index<XT, E>(K, C, m, v * VE + h) * 4u) =
+          make_uint4(__float_as_uint(rnd_x<XD>(f[h])), __float_as_uint(rnd_x<XD>(f[h + 1])),
+                     __float_as_uint(rnd_x<XD>(f[h + 2])), __float_as_uint(rnd_x<XD>(f[h + 3])));
+  }
 }
 
 // One block's share of a GEMV.  The calling wave owns row groups g, g +
@@ -351,6 +398,7 @@ __device__ __forceinline__ bool gemv_core(const ThvmGemvArgs &a, unsigned char *
   if (!early) load_batch(g, 0);
   if (!XPRE) load_gains();
   pclk(clk, a.clk_cap, 1);
+  if (XPRE) pclk_after(clk, a.clk_cap, 6, xpre[0].x);
 
   // ---- 2. stage x into LDS (16-byte loads), with the fused norm if asked ----
   for (int m = 0; m < M; m++) {
@@ -360,23 +408,17 @@ __device__ __forceinline__ bool gemv_core(const ThvmGemvArgs &a, unsigned char *
       // no reduction: every thread of the block stages, XN vectors of x in
       // flight per thread before the first LDS store
       for (uint32_t v0 = threadIdx.x; v0 < NVt; v0 += XN * bdim) {
-        float f[XN][VE];
+        uint4 q[XN];
         const bool first = v0 == threadIdx.x;
 #pragma unroll
         for (int j = 0; j < XN; j++) {
           const uint32_t v = v0 + j * bdim;
-          if (v < NVt) {
-            if (pre && first) xdec<XD>(xpre[j], f[j]);
-            else xvec<XD, COH>(xr, (uint64_t)v * VE, f[j]);
-          }
+          if (v < NVt) q[j] = (pre && first) ? xpre[j] : xraw<XD, COH>(xr, (uint64_t)v * VE);
         }
 #pragma unroll
         for (int j = 0; j < XN; j++) {
           const uint32_t v = v0 + j * bdim;
-          if (v < NVt) {
-#pragma unroll
-            for (int i = 0; i < VE; i++) xs_store<XT>(xs_raw, xs_index<XT, E>(K, C, m, v * VE + i), f[j][i]);
-          }
+          if (v < NVt) xs_put_raw<XD, XT, E>(xs_raw, K, C, m, v, q[j]);
         }
       }
     } else {
@@ -416,14 +458,15 @@ __device__ __forceinline__ bool gemv_core(const ThvmGemvArgs &a, unsigned char *
       for (int j = 0; j < NV; j++) {
         const uint32_t v = tid + j * nthr;
         if (v < NVt) {
+          float val[VE];
 #pragma unroll
           for (int i = 0; i < VE; i++) {
             // (x - mean) * inv * w (+ b), the norm kernel's own formula
-            float val = (xv[j][i] - mean) * inv;
-            if (a.norm_w) val = val * gw[j][i];
-            if (a.norm == 2 && a.norm_b) val = val + gb[j][i];
-            xs_store<XT>(xs_raw, xs_index<XT, E>(K, C, m, v * VE + i), rnd_x<XD>(val));
+            val[i] = (xv[j][i] - mean) * inv;
+            if (a.norm_w) val[i] = val[i] * gw[j][i];
+            if (a.norm == 2 && a.norm_b) val[i] = val[i] + gb[j][i];
           }
+          xs_put_f<XD, XT, E>(xs_raw, K, C, m, v, val);
         }
       }
     }

@@ -16,7 +16,7 @@
 template <int WT, int XD, int M, int R, int U>
 __global__ __launch_bounds__(1024) void k_gemv(ThvmGemvArgs a) {
   extern __shared__ __align__(16) unsigned char xs_raw[];
-  __shared__ float red[GEMV_MAX_WAVES];
+  __shared__ __align__(16) float red[GEMV_MAX_WAVES];
   const int nw = blockDim.x >> 6;
   const uint32_t g = blockIdx.x * nw + (threadIdx.x >> 6);
   if (blockIdx.y) {

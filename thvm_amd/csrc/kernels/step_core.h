@@ -83,7 +83,7 @@ __device__ __attribute__((noinline)) bool step_gemv(const ThvmStepArgs &a, uint3
   constexpr int XD = AtXd<AT>::XD;
   constexpr int R = (ST == 0 || ST == 3) ? 2 : 1;
   extern __shared__ __align__(16) unsigned char lds[];
-  __shared__ float red[GEMV_MAX_WAVES];
+  __shared__ __align__(16) float red[GEMV_MAX_WAVES];
   __shared__ uint32_t flag;
   const GridSync gs = step_sync(a, epoch);
   const int wv = threadIdx.x >> 6;
