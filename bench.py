@@ -155,6 +155,8 @@ def run_decode(thvm, key: str, batch: int, args) -> dict:
         cfg["attn_fused"] = args.attn_fused
     if args.attn_mf and spec["cfg"].get("arch") != 3:
         cfg["attn_mf"] = args.attn_mf
+    if args.attn_cpb and spec["cfg"].get("arch") != 3:
+        cfg["attn_cpb"] = args.attn_cpb
     ctx = spec["ctx"]
     # the oracle decodes batch rows one after another on one core, so its rate
     # is the batch-1 rate; batches above 16 rows would take minutes and are
@@ -823,6 +825,8 @@ def main() -> int:
                     help="attention form: 0 auto, 1 one launch, 2 split + merge launches")
     ap.add_argument("--attn-mf", type=int, default=0, choices=[0, 1, 2],
                     help="attention split: 0 picked by the kernel, 1 MFMA, 2 VALU")
+    ap.add_argument("--attn-cpb", type=int, default=0,
+                    help="attention split: 64-row chunks per block (0: picked by the kernel)")
     ap.add_argument("--moe-mode", type=int, default=0, choices=[0, 1, 2],
                     help="DSV2 above 4 rows: expert-grouped MoE on MFMA (0/2) or on the VALU (1)")
     ap.add_argument("--layers", type=int, default=None, help="debug only: fewer layers (invalid metric)")

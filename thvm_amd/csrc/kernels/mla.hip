@@ -327,11 +327,13 @@ __global__ __launch_bounds__(MLA_THREADS) void k_mla_split(ThvmMlaArgs a) {
 //           summed through LDS);
 //   mix     olat[h][:] += p[h][row] c_row: A = p (16 heads x 32 rows), B =
 //           the staged rows (32 rows x 16 columns), 4 column tiles per wave.
-//           A lane's B operand is one column of 8 rows, read as 2-byte
-//           values; lane group g takes rows g, g + 4, ..., g + 28 of the 32,
-//           so the four groups' rows are consecutive and fall in distinct
-//           banks (pitch 292 dwords: 36 apart mod 64), and p is stored in the
-//           same row order, so A is one 8-float read.
+//           A lane's B operand is one column of 8 consecutive rows (lane
+//           group g: rows 8 g .. 8 g + 7 of the 32), read with two LDS
+//           transpose reads (ds_read_b64_tr_b16: each 16-lane group reads a
+//           4-row x 16-column tile, lane s of the group the 4 columns
+//           4 (s % 4) .. of row s / 4, and lane i receives column i's 4
+//           rows) -- four 2-byte reads per lane before; p is stored in row
+//           order, so A is one 8-float read.
 // q and p (f32) enter as bf16 hi + lo pairs (two MFMAs each), so a product
 // keeps ~16 significant bits of the f32 operand against the exact bf16 cache
 // value: f32-level agreement with the VALU split.  A block runs cpb
@@ -340,7 +342,7 @@ __global__ __launch_bounds__(MLA_THREADS) void k_mla_split(ThvmMlaArgs a) {
 // flight during the current chunk, and writes one partial (olat, m, l) at
 // slot blockIdx.x; k_mla_out merges ceil(L / (64 cpb)) of them.  MFMA operand
 // k order: A and B give lane group g the same 8 k values (scores: k = 32
-// step + 8 g + j; mix: row 32 step + g + 4 j), so each instruction adds a
+// step + 8 g + j; mix: row 32 step + 8 g + j), so each instruction adds a
 // full partial dot product.
 #define MF_H 16
 #define MF_KV 512
@@ -358,6 +360,15 @@ static_assert(MF_H * MF_QLP * 4 <= 64 * MF_RP, "qlat staging fits the row stagin
 #define MF_THREADS 512                     /* 8 waves: two per 16-row tile */
 #define MF_KH (MF_KS / 2)                  /* k-steps per wave */
 #define MF_LDS (64 * MF_RP + MF_KS * 2 * 64 * 16 + MF_H * MF_PWP * 4 + 2 * 4 * MF_H * 4 + 4 * 64 * 16)
+
+// four 16-bit values of LDS by the gfx950 transpose read (the lane layout
+// above), as two packed dwords
+typedef short mf_v4s __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ uint2 lds_tr16(const unsigned char *p) {
+  const mf_v4s r = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (__attribute__((address_space(3))) mf_v4s *)(__attribute__((address_space(3))) unsigned char *)p);
+  return __builtin_bit_cast(uint2, r);
+}
 
 // eight f32 -> bf16 hi (RNE) and lo = bf16(v - hi), packed in operand order
 // (v - hi is exact in f32)
@@ -508,11 +519,10 @@ __global__ __launch_bounds__(MF_THREADS) void k_mla_split_mf(ThvmMlaArgs a) {
     if (c == cbeg) pclk(a.clk, a.clk_cap, 2);
 
     // 2. softmax over the chunk's rows (the first-half waves hold the full
-    //    scores), online across the block's chunks; p is stored in the mix's
-    //    row order: row r of a 32-row step at position 8 (r % 4) + r / 4
+    //    scores), online across the block's chunks; p is stored in row order
     const uint32_t row = rt * 16 + li;
     const bool rok = row < nj;
-    const uint32_t ppos = (row & 32) + (row & 3) * 8 + ((row & 31) >> 2);
+    const uint32_t ppos = row;
     float sv[4];
     if (kh == 0) {
       const float4 o = spart[rt * 64 + lane];
@@ -558,17 +568,15 @@ __global__ __launch_bounds__(MF_THREADS) void k_mla_split_mf(ThvmMlaArgs a) {
       const float *pr = pw + li * MF_PWP + q * 32 + lg * 8;
       uint4 ah, alo;
       split8(*(const float4 *)pr, *(const float4 *)(pr + 4), ah, alo);
-      // rows 32 q + lg + 4 j, j = 0..7, of column (wv * 4 + t) * 16 + li
-      const unsigned char *cb = cl + (q * 32 + lg) * MF_RP + li * 2;
+      // rows 32 q + 8 lg + j, j = 0..7, of column (wv * 4 + t) * 16 + li:
+      // lane li of the group reads row 32 q + 8 lg + li / 4 (+ 4), columns
+      // (wv * 4 + t) * 16 + 4 (li % 4) ..
+      const unsigned char *cb = cl + (q * 32 + lg * 8 + (li >> 2)) * MF_RP + (li & 3) * 8;
 #pragma unroll
       for (int t = 0; t < 4; t++) {
         const unsigned char *cp = cb + (wv * 4 + t) * 32;
-        uint32_t w[4];
-#pragma unroll
-        for (int j = 0; j < 4; j++)
-          w[j] = (uint32_t)*(const uint16_t *)(cp + (8 * j) * MF_RP) |
-                 ((uint32_t)*(const uint16_t *)(cp + (8 * j + 4) * MF_RP) << 16);
-        const uint4 bv = make_uint4(w[0], w[1], w[2], w[3]);
+        const uint2 r0 = lds_tr16(cp), r1 = lds_tr16(cp + 4 * MF_RP);
+        const uint4 bv = make_uint4(r0.x, r0.y, r1.x, r1.y);
         oacc[t] = mfma16<GX_BF16>(ah, bv, oacc[t]);
         oacc[t] = mfma16<GX_BF16>(alo, bv, oacc[t]);
       }
