@@ -620,7 +620,7 @@ __global__ __launch_bounds__(MF_THREADS) void k_mla_split_mf(ThvmMlaArgs a) {
 #define MLA_OUT_SPLIT 2
 #define MLA_WPASS 8
 #define MLA_OPRE_MAX 20   /* partial vectors per thread loaded up front, long caches */
-template <bool FP8, int OPRE>
+template <bool FP8, int OPRE, int WP>
 __global__ __launch_bounds__(MLA_OUT_THREADS) void k_mla_out(ThvmMlaArgs a) {
   extern __shared__ float ol[];                       // [kv] olat | [ns] weights | [nsg][kv]
   constexpr uint32_t EPC = FP8 ? 16 : 8;
@@ -672,10 +672,12 @@ __global__ __launch_bounds__(MLA_OUT_THREADS) void k_mla_out(ThvmMlaArgs a) {
   // this block's W_uv rows and their scales (independent of the merge)
   const buf_t wrs = buf_rsrc(a.wuv, a.H * dv * rowb);
   const buf_t srs = buf_rsrc(a.suv, a.suv ? a.H * dv * 4u : 0u);
-  uint4 wq[MLA_WPASS];
-  uint32_t scw[MLA_WPASS];
+  // (WP passes of 8 waves x rpp rows cover the block's rows: no pass of
+  // load instructions that would all read past them)
+  uint4 wq[WP];
+  uint32_t scw[WP];
 #pragma unroll
-  for (int q = 0; q < MLA_WPASS; q++) {
+  for (int q = 0; q < WP; q++) {
     const uint32_t mm = m0 + (wv + q * nw) * rpp + sub;
     wq[q] = buf_ld_stream16(wrs, mm < m1 ? (h * dv + mm) * rowb + c * 16u : BUF_OOB);
     scw[q] = buf_ld4(srs, mm < m1 ? (h * dv + mm) * 4u : BUF_OOB);
@@ -736,7 +738,7 @@ __global__ __launch_bounds__(MLA_OUT_THREADS) void k_mla_out(ThvmMlaArgs a) {
   __syncthreads();
   pclk(clk, a.clk_cap, 3);
 #pragma unroll
-  for (int q = 0; q < MLA_WPASS; q++) {
+  for (int q = 0; q < WP; q++) {
     const uint32_t r0 = m0 + (wv + q * nw) * rpp;
     if (r0 >= m1) break;                               // wave-uniform
     const uint32_t mm = r0 + sub;
@@ -869,8 +871,16 @@ extern "C" int thvm_k_mla_attn(const ThvmMlaArgs *a, hipStream_t s, char *err, i
   // partials per row at most: n_split / cpb; over 4 per split group -> 20 up front
   const uint32_t nsg = MLA_OUT_THREADS / (a->kv / 4);
   const bool longp = (a->n_split + ak.cpb - 1) / ak.cpb > 4 * nsg;
-  void (*fo)(ThvmMlaArgs) = a->wdt == THVM_DT_FP8E4M3 ? (longp ? k_mla_out<true, MLA_OPRE_MAX> : k_mla_out<true, 4>)
-                                                      : (longp ? k_mla_out<false, MLA_OPRE_MAX> : k_mla_out<false, 4>);
+  // W_uv passes: 8 waves x rpp rows each cover the block's share of d_v
+  const uint32_t rpp = 64 / (a->kv * wsz / 16), rows_pb = (a->dv + MLA_OUT_SPLIT - 1) / MLA_OUT_SPLIT;
+  const bool wp4 = (rows_pb + 8 * rpp - 1) / (8 * rpp) <= 4;
+  void (*fo)(ThvmMlaArgs);
+  if (a->wdt == THVM_DT_FP8E4M3)
+    fo = longp ? (wp4 ? k_mla_out<true, MLA_OPRE_MAX, 4> : k_mla_out<true, MLA_OPRE_MAX, MLA_WPASS>)
+               : (wp4 ? k_mla_out<true, 4, 4> : k_mla_out<true, 4, MLA_WPASS>);
+  else
+    fo = longp ? (wp4 ? k_mla_out<false, MLA_OPRE_MAX, 4> : k_mla_out<false, MLA_OPRE_MAX, MLA_WPASS>)
+               : (wp4 ? k_mla_out<false, 4, 4> : k_mla_out<false, 4, MLA_WPASS>);
   thvm_launch(false, true, fo, g2, dim3(MLA_OUT_THREADS), lds2, s, ak);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) { snprintf(err, errlen, "mla_attn launch: %s", hipGetErrorString(e)); return -1; }

@@ -94,7 +94,7 @@ __global__ __launch_bounds__(64) void k_route(ThvmRouteArgs a) {
 }
 
 // The post-attention RMSNorm (f32 out) and the f32 router GEMV in one
-// launch: grid (ceil(E / EPB), B), 512 threads; each block renormalises its
+// launch: grid (ceil(E / EPB), B), 512 threads (256 at EPB = 1); each block renormalises its
 // row (the first 256 threads exactly as the norm kernel: the same elements
 // per thread, the same block sum over four waves, the same formula) and its
 // first EPB waves take one expert each, lane l folding 16-byte chunks l,
@@ -992,7 +992,9 @@ extern "C" int thvm_k_moe_gate(const ThvmGateArgs *a, hipStream_t s, char *err, 
                           : nch <= 8 ? (one ? k_moe_gate<8, 1> : k_moe_gate<8, RT_WAVES>)
                                      : (one ? k_moe_gate<16, 1> : k_moe_gate<16, RT_WAVES>);
   const uint32_t epb = one ? 1 : RT_WAVES;
-  thvm_launch(true, true, f, dim3((a->E + epb - 1) / epb, a->B), dim3(RT_THREADS), 0, s, *a);
+  // (one expert per block: the norm's 256 threads only -- the other four
+  // waves had nothing to do but issue their share of the no-access loads)
+  thvm_launch(true, true, f, dim3((a->E + epb - 1) / epb, a->B), dim3(one ? RT_NORM_THREADS : RT_THREADS), 0, s, *a);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) { snprintf(err, errlen, "moe_gate launch: %s", hipGetErrorString(e)); return -1; }
   return 0;
