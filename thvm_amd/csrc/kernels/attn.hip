@@ -66,12 +66,12 @@ __global__ __launch_bounds__(MERGE_THREADS) void k_attn_merge(ThvmAttnArgs a) {
 // agent-scope atomic, B*Hkv words after the partials, zero between launches
 // -- and merge the group when this block brings the count to n_live (then
 // reset the counter).  No fence: the partials never sit in an L2.
-// PH: the group's heads merged one after another, each as a group of one
-// (the per-head merge kernel's fold; ms is then a MergeFlatLds<HD, 1>).
+// PH: the group's heads merged together, each as a group of one (the
+// per-head merge kernel's fold; ms is then G MergeFlatLds<HD, 1>).
 template <int HD, int G, int AT, bool PH = false>
 __device__ __forceinline__ void attn_handoff_merge(const ThvmAttnArgs &a, uint32_t b, uint32_t kvh,
                                                    uint32_t n_live, uint32_t *last,
-                                                   MergeFlatLds<HD, PH ? 1 : G> &ms) {
+                                                   MergeFlatLds<HD, PH ? 1 : G> *ms) {
   vm_drain();
   __syncthreads();
   if (threadIdx.x == 0) {
@@ -83,12 +83,9 @@ __device__ __forceinline__ void attn_handoff_merge(const ThvmAttnArgs &a, uint32
   __syncthreads();
   if (!*last) return;                              // block-uniform
   if constexpr (PH) {
-    for (uint32_t g = 0; g < (uint32_t)G; g++) {
-      if (g) __syncthreads();                      // the previous head's LDS reads are done
-      attn_merge_flat<HD, 1, AT, true>(a, b, kvh * G + g, n_live, threadIdx.x, true, ms);
-    }
+    attn_merge_heads<HD, G, AT, true, 4>(a, b, kvh, n_live, threadIdx.x, ms);
   } else {
-    attn_merge_flat<HD, G, AT, true>(a, b, kvh, n_live, threadIdx.x, true, ms);
+    attn_merge_flat<HD, G, AT, true>(a, b, kvh, n_live, threadIdx.x, true, *ms);
   }
 }
 
@@ -109,7 +106,7 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attn_fused(ThvmAttnArgs a) {
   AttnSplit<HD, G, AT, true, false> u;
   u.issue(a, kvh, split, b, wv, L);
   u.finish(a, kvh, split, b, wv, threadIdx.x, L, true, s);
-  attn_handoff_merge<HD, G, AT>(a, b, kvh, n_live, &last, ms);
+  attn_handoff_merge<HD, G, AT>(a, b, kvh, n_live, &last, &ms);
 }
 
 // Batched split: one block runs cpb (a.cpb) consecutive chunks of a (kv head, row),
@@ -304,7 +301,7 @@ __global__ __launch_bounds__(ATT_THREADS, 4) void k_attn_multi(ThvmAttnArgs a) {
       if (d == 0) { pp[HD] = M; pp[HD + 1] = lt; }
     }
   }
-  if (FUSE) attn_handoff_merge<HD, G, AT>(a, b, kvh, attn_live(a, L), &last, ms);
+  if (FUSE) attn_handoff_merge<HD, G, AT>(a, b, kvh, attn_live(a, L), &last, &ms);
   pclk_end(a.clk, a.clk_cap);
 }
 
@@ -342,8 +339,8 @@ __global__ __launch_bounds__(ATT_THREADS, 4) void k_attn_multi(ThvmAttnArgs a) {
 // through the no-access offset (a stale cache row times a zero weight could
 // still be a NaN).  GF > 0 (the one-launch form, G = GF heads per kv head):
 // the partial goes out with system-scope stores and the last split block of
-// the (row, kv head) merges the group's heads in the same launch, one after
-// another (attn_handoff_merge: the per-head merge kernel's fold, so the same
+// the (row, kv head) merges the group's heads in the same launch, all at
+// once (attn_handoff_merge: the per-head merge kernel's fold, so the same
 // outputs as the two-launch form).
 #define MF_GMAX 8
 template <int HD, int AT, int GF = 0>
@@ -514,7 +511,7 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attn_mf(ThvmAttnArgs a) {
     }
   }
   if (GF) {
-    __shared__ MergeFlatLds<HD, 1> ms;
+    __shared__ MergeFlatLds<HD, 1> ms[GF ? GF : 1];
     __shared__ uint32_t last;
     attn_handoff_merge<HD, (GF ? GF : 1), AT, true>(a, b, kvh, attn_live(a, L), &last, ms);
   }

@@ -390,6 +390,82 @@ __device__ __forceinline__ void attn_merge_flat_d(const ThvmAttnArgs &a, uint32_
     st_act<AT, COH>(a.out, oi + 1, a1 * inv);
   }
 }
+// NH heads at once, each merged as a group of one (the per-head merge's
+// fold: the same partitions, slot order and partition order, so the same
+// bits as attn_merge_flat<HD, 1> run head by head): every thread takes its
+// (pair, partition) of all NH heads, all their first-batch loads in flight
+// together, then one LDS round for all the heads.  Heads kvh * NH + gi of
+// row b; n_live partials; s holds NH per-head LDS areas.
+template <int HD, int NH, int AT, bool COH, int MC>
+__device__ __forceinline__ void attn_merge_heads(const ThvmAttnArgs &a, uint32_t b, uint32_t kvh,
+                                                 uint32_t n_live, int tid, MergeFlatLds<HD, 1> *s) {
+  typedef MergeFlatLds<HD, 1> FL;
+  constexpr int PAIRS = FL::PAIRS, NP = FL::NP;
+  static_assert(NP >= 1 && MERGE_THREADS % PAIRS == 0, "merge geometry");
+  const int e = tid % PAIRS, p = tid / PAIRS, d = e * 2;
+  float mp[NH], lp[NH], a0[NH], a1[NH];
+#pragma unroll
+  for (int gi = 0; gi < NH; gi++) { mp[gi] = -INFINITY; lp[gi] = 0.0f; a0[gi] = 0.0f; a1[gi] = 0.0f; }
+  if (p < NP) {
+    for (uint32_t s0 = p; s0 < n_live; s0 += NP * MC) {
+      float mv[NH][MC], lv[NH][MC];
+      float2 av[NH][MC];
+#pragma unroll
+      for (int gi = 0; gi < NH; gi++) {
+        const uint64_t pbi = ((uint64_t)b * a.H + kvh * NH + gi) * a.n_split * (HD + 2);
+#pragma unroll
+        for (int j = 0; j < MC; j++) {             // slots past n_live read slot 0, never folded
+          const uint32_t sp = s0 + j * NP, spc = sp < n_live ? sp : 0u;
+          const uint64_t q = pbi + (uint64_t)spc * (HD + 2);
+          if (COH) {
+            const uint2 r = coh_ld8(a.part, (uint32_t)((q + d) * 4));
+            const uint2 ml = coh_ld8(a.part, (uint32_t)((q + HD) * 4));
+            av[gi][j] = make_float2(__uint_as_float(r.x), __uint_as_float(r.y));
+            mv[gi][j] = __uint_as_float(ml.x);
+            lv[gi][j] = __uint_as_float(ml.y);
+          } else {
+            av[gi][j] = *(const float2 *)(a.part + q + d);
+            const float2 ml = *(const float2 *)(a.part + q + HD);
+            mv[gi][j] = ml.x;
+            lv[gi][j] = ml.y;
+          }
+        }
+      }
+#pragma unroll
+      for (int gi = 0; gi < NH; gi++)
+#pragma unroll
+        for (int j = 0; j < MC; j++)
+          if (s0 + j * NP < n_live)
+            merge_fold(mp[gi], lp[gi], a0[gi], a1[gi], mv[gi][j], lv[gi][j], av[gi][j].x, av[gi][j].y);
+    }
+  }
+  if (NP > 1) {
+    if (p < NP)
+#pragma unroll
+      for (int gi = 0; gi < NH; gi++) {
+        s[gi].m[p][e] = mp[gi];
+        s[gi].l[p][e] = lp[gi];
+        s[gi].a[p][e] = make_float2(a0[gi], a1[gi]);
+      }
+    __syncthreads();
+    if (p == 0)
+#pragma unroll
+      for (int gi = 0; gi < NH; gi++)
+#pragma unroll
+        for (int q = 1; q < NP; q++)
+          merge_fold(mp[gi], lp[gi], a0[gi], a1[gi], s[gi].m[q][e], s[gi].l[q][e], s[gi].a[q][e].x,
+                     s[gi].a[q][e].y);
+  }
+  if (p == 0) {
+#pragma unroll
+    for (int gi = 0; gi < NH; gi++) {
+      const float inv = lp[gi] > 0.0f ? 1.0f / lp[gi] : 0.0f;
+      const uint64_t oi = ((uint64_t)b * a.H + kvh * NH + gi) * HD + d;
+      st_act<AT, COH>(a.out, oi, a0[gi] * inv);
+      st_act<AT, COH>(a.out, oi + 1, a1[gi] * inv);
+    }
+  }
+}
 // the same with n_live known at the call
 template <int HD, int G, int AT, bool COH>
 __device__ __forceinline__ void attn_merge_flat(const ThvmAttnArgs &a, uint32_t b, uint32_t kvh,
