@@ -601,15 +601,20 @@ def test_norm(hip, ln, dt):
     assert np.all(np.abs(gw - ww) <= tol * np.abs(ww) + 1e-5), np.max(np.abs(gw - ww))
 
 
-def test_softmax(hip):
-    M, K = 4, 4096
-    say("case: softmax f16 [4,4096]")
-    rng = np.random.default_rng(12)
-    xs, xf = rand_store(rng, (M, K), DT_F16)
+@pytest.mark.parametrize("K,xt", [(4096, DT_F16), (1000, DT_BF16), (257, DT_F32), (1, DT_F16),
+                                  (5000, DT_F16)])
+def test_softmax(hip, K, xt):
+    """Rows up to 4096 run the register-resident typed kernel, longer rows
+    the looping one (K = 5000); ragged K leaves the last threads' slots
+    masked."""
+    M = 4
+    say(f"case: softmax dt {xt} [{M},{K}]")
+    rng = np.random.default_rng(12 + K)
+    xs, xf = rand_store(rng, (M, K), xt)
     y = hip.Buffer(M * K * 4)
-    hip.builtin("softmax", [y, up(hip, xs)], m=M, k=K, xt=DT_F16, yt=DT_F32)
+    hip.builtin("softmax", [y, up(hip, xs)], m=M, k=K, xt=xt, yt=DT_F32)
     want = np.empty(M * K, np.float32)
-    O.oracle().or_softmax(want.ctypes.data, DT_F32, xs.ctypes.data, DT_F16, M, K)
+    O.oracle().or_softmax(want.ctypes.data, DT_F32, np.ascontiguousarray(xs).ctypes.data, xt, M, K)
     got = y.read(np.float32)
     assert np.allclose(got, want, rtol=1e-5, atol=1e-9)
     assert np.allclose(got.reshape(M, K).sum(1), 1.0, atol=1e-5)

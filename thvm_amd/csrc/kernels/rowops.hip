@@ -211,12 +211,58 @@ __global__ __launch_bounds__(ROW_THREADS) void k_softmax(ThvmSoftmaxArgs a) {
     st_a(a.y, o + i, a.ydt, expf(ld_a(a.x, o + i, a.xdt) - mx) * r);
 }
 
+// the same softmax with the dtypes at compile time and the row in registers
+// (K <= 16 * 256): thread t's elements t, t + 256, ... loaded once, all
+// loads issued together, then the max, the sum (element order, the same
+// block sum) and the outputs -- the same bits as k_softmax, whose runtime
+// dtype switch put each of its 3 K / 256 loads in a branch of its own,
+// waiting for the one before (13 us for one 4096-element row)
+template <uint32_t XT, uint32_t YT>
+__global__ __launch_bounds__(ROW_THREADS) void k_softmax_reg(ThvmSoftmaxArgs a) {
+  __shared__ float red[ROW_WAVES];
+  const uint64_t o = (uint64_t)blockIdx.x * a.K;
+  float xv[NORM_REG];
+#pragma unroll
+  for (int i = 0; i < NORM_REG; i++) {
+    const uint32_t e = threadIdx.x + i * ROW_THREADS, ec = e < a.K ? e : 0;
+    const float x = ld_t<XT>(a.x, o + ec);
+    xv[i] = e < a.K ? x : -INFINITY;
+  }
+  float mx = -INFINITY;
+#pragma unroll
+  for (int i = 0; i < NORM_REG; i++) mx = fmaxf(mx, xv[i]);
+  mx = block_max(mx, red);
+  float sm = 0.0f;                 // +0 plus the masked +0 terms: the same bits
+#pragma unroll
+  for (int i = 0; i < NORM_REG; i++) sm += (threadIdx.x + i * ROW_THREADS) < a.K ? expf(xv[i] - mx) : 0.0f;
+  sm = block_sum(sm, red);
+  const float r = 1.0f / sm;
+#pragma unroll
+  for (int i = 0; i < NORM_REG; i++) {
+    const uint32_t e = threadIdx.x + i * ROW_THREADS;
+    if (e < a.K) st_t<YT>(a.y, o + e, expf(xv[i] - mx) * r);
+  }
+}
+typedef void (*softmax_fn)(ThvmSoftmaxArgs);
+template <uint32_t XT>
+static softmax_fn softmax_pick_y(uint32_t ydt) {
+  return ydt == THVM_DT_FP32 ? k_softmax_reg<XT, THVM_DT_FP32>
+       : ydt == THVM_DT_BF16 ? k_softmax_reg<XT, THVM_DT_BF16> : k_softmax_reg<XT, THVM_DT_FP16>;
+}
+
 extern "C" int thvm_k_softmax(const ThvmSoftmaxArgs *a, hipStream_t s, char *err, int errlen) {
   if (!act_dt(a->xdt) || !act_dt(a->ydt) || a->M == 0 || a->K == 0) {
     snprintf(err, errlen, "softmax: bad args");
     return -1;
   }
-  thvm_launch(true, true, k_softmax, dim3(a->M), dim3(ROW_THREADS), 0, s, *a);
+  if (a->K <= NORM_REG * ROW_THREADS) {
+    const softmax_fn f = a->xdt == THVM_DT_FP32 ? softmax_pick_y<THVM_DT_FP32>(a->ydt)
+                       : a->xdt == THVM_DT_BF16 ? softmax_pick_y<THVM_DT_BF16>(a->ydt)
+                                                : softmax_pick_y<THVM_DT_FP16>(a->ydt);
+    thvm_launch(true, true, f, dim3(a->M), dim3(ROW_THREADS), 0, s, *a);
+  } else {
+    thvm_launch(true, true, k_softmax, dim3(a->M), dim3(ROW_THREADS), 0, s, *a);
+  }
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) { snprintf(err, errlen, "softmax launch: %s", hipGetErrorString(e)); return -1; }
   return 0;
