@@ -100,10 +100,34 @@ def _reads(cfg):
         l, sub = divmod(tag, 2)
         if arch == 3:
             if sub == 0:
+                # one row: the MLA merge in latent quarters leaves four f32
+                # quarter sums (the o projection adds, scales and rounds them)
+                if _quarters(cfg):
+                    return ["x", "o4"] + ([f"l{l}.wuv.scale"] if cfg.get("wdtype", DT_FP8) == DT_FP8 else [])
                 return ["x", "o"]
             return ["x"] if l < first_dense else ["x", "xnf", f"l{l}.gate_logits", f"l{l}.sel", f"l{l}.probs"]
         return ["x", "q", "att"] if sub == 0 else ["x", "h"]
     return reads
+
+
+def _quarters(cfg):
+    """Whether the DSV2 decoder runs the MLA merge in latent quarters."""
+    return cfg["batch"] == 1 and cfg["kv_lora"] % 64 == 0
+
+
+def _mla_o(r, cfg, l):
+    """The attention output the o projection consumes: read as is, or, from
+    the quarter sums, bf16(scale * ((q0 + q1) + (q2 + q3))) in f32 -- the
+    GEMV's staging."""
+    B = cfg["batch"]
+    if "o4" not in r:
+        return _f32(r["o"], DT_BF16).reshape(B, -1)
+    q = r["o4"].view(np.float32).reshape(4, -1)
+    v = ((q[0] + q[1]) + (q[2] + q[3])).astype(np.float32)
+    sc = r.get(f"l{l}.wuv.scale")
+    if sc is not None:
+        v = (v * sc.view(np.float32)).astype(np.float32)
+    return _f32(O.encode(v, DT_BF16), DT_BF16).reshape(B, -1)
 
 
 def _device_step(dec, cfg, tok, pos):
@@ -149,7 +173,7 @@ def _teacher(dec, om, cfg, tok, pos, bars, label):
         r = got[t]
         if cfg["arch"] == 3:
             if sub == 0:
-                bars.check("o", _f32(r["o"], DT_BF16).reshape(B, -1), tp["o"][l], where)
+                bars.check("o", _mla_o(r, cfg, l), tp["o"][l], where)
             elif l >= cfg["first_dense"]:
                 _check_routing(dec, cfg, r, om, l, where)
         elif sub == 0:

@@ -12,7 +12,7 @@ import _oracle as O
 
 pytestmark = pytest.mark.gpu
 
-DT_FP8, DT_BF16, DT_F32 = 9, 12, 13
+DT_FP8, DT_F16, DT_BF16, DT_F32 = 9, 11, 12, 13
 
 
 def say(*a):
@@ -129,12 +129,68 @@ def test_mla_prep_and_attn(hip, shape, wdt):
         hip.builtin("mla_attn", args, b=B, h=H, dn=dn, dr=dr, kv=kv, dv=dv, maxseq=ms, nsplit=nsplit,
                     wt=wdt, scale=scale, mode=mode, cpb=cpb)
         g_o = unbf(o.read(np.uint16).reshape(B, H, dv))
-        for b in range(B):
-            # floor: |olat| <= max_j |ckv_j| per column
-            cmax = np.abs(unbf(g_ckv[b, :L])).max(0)
-            floor = np.abs(wuvf.reshape(H, dv, kv)) @ cmax
-            assert np.all(close_bf16(g_o[b], unbf(w_o[b]), floor)), \
-                (mode, cpb, np.max(np.abs(g_o[b] - unbf(w_o[b]))))
+        outs = [("o", g_o)]
+        if kv % 64 == 0:
+            # the merge in latent quarters: four f32 quarter sums, which the
+            # o projection adds, scales and rounds (quarter_x: its staging)
+            o4 = hip.Buffer(4 * B * H * dv * 4)
+            hip.builtin("mla_attn", [o4] + args[1:], b=B, h=H, dn=dn, dr=dr, kv=kv, dv=dv, maxseq=ms,
+                        nsplit=nsplit, wt=wdt, scale=scale, mode=mode, cpb=cpb, oq=1)
+            sc = np.tile(suv, B) if f8 else None
+            outs.append(("oq", unbf(quarter_x(o4.read(np.float32), sc)).reshape(B, H, dv)))
+        for name, got in outs:
+            for b in range(B):
+                # floor: |olat| <= max_j |ckv_j| per column
+                cmax = np.abs(unbf(g_ckv[b, :L])).max(0)
+                floor = np.abs(wuvf.reshape(H, dv, kv)) @ cmax
+                assert np.all(close_bf16(got[b], unbf(w_o[b]), floor)), \
+                    (name, mode, cpb, np.max(np.abs(got[b] - unbf(w_o[b]))))
+
+
+def quarter_x(o4, scale):
+    """bf16(scale * ((q0 + q1) + (q2 + q3))) in f32 over the four quarter sums
+    (a GEMV with norm=3 stages exactly this)."""
+    q = o4.reshape(4, -1)
+    v = ((q[0] + q[1]) + (q[2] + q[3])).astype(np.float32)
+    if scale is not None:
+        v = (v * scale.astype(np.float32)).astype(np.float32)
+    return O.encode(v, DT_BF16)
+
+
+@pytest.mark.parametrize("wdt,N,K,waves", [(DT_FP8, 2048, 2048, 0), (DT_BF16, 640, 1024, 0),
+                                           (DT_FP8, 256, 2048, 16), (DT_FP8, 96, 528, 0)])
+def test_gemv_summed_x_equals_staged_bf16(hip, wdt, N, K, waves):
+    """A GEMV with norm=3 stages x = bf16(g * ((x0 + x1) + (x2 + x3))) from four
+    f32 vectors: bit for bit the plain GEMV over that bf16 row (residual
+    epilogue, the o projection's), with and without gains; its limits are
+    refused."""
+    say(f"case: gemv summed x wdt={wdt} N={N} K={K} waves={waves}")
+    rng = np.random.default_rng(N + K + wdt)
+    xqs = K + 8
+    o4 = np.zeros((4, xqs), np.float32)
+    o4[:, :K] = rng.standard_normal((4, K)).astype(np.float32)
+    g = rng.uniform(0.5, 1.5, K).astype(np.float32)
+    w, sw, _ = weights(rng, N, K, wdt)
+    f8 = wdt == DT_FP8
+    res = bf(rng.standard_normal((1, N)))
+    for gain in (True, False):
+        xb = quarter_x(o4[:, :K].copy(), g if gain else None)
+        y1, y2 = up(hip, res), up(hip, res)
+        tune = dict(waves=waves) if waves else {}
+        hip.builtin("gemv", [y1, up(hip, o4), up(hip, w)] + ([up(hip, sw)] if f8 else []) +
+                    ([up(hip, g)] if gain else []) + [y1], m=1, n=N, k=K, wt=wdt, xt=DT_BF16, yt=DT_BF16,
+                    epi=1, norm=3, xqs=xqs, ngain=int(gain), **tune)
+        hip.builtin("gemv", [y2, up(hip, xb), up(hip, w)] + ([up(hip, sw)] if f8 else []) + [y2],
+                    m=1, n=N, k=K, wt=wdt, xt=DT_BF16, yt=DT_BF16, epi=1, **tune)
+        assert np.array_equal(y1.read(np.uint16), y2.read(np.uint16)), gain
+    # one x row only, bf16 staging, K within four elements per thread
+    for bad in (dict(m=2), dict(xt=DT_F16), dict(k=K, waves=1)):
+        kw = dict(m=1, n=N, k=K, wt=wdt, xt=DT_BF16, yt=DT_BF16, epi=1, norm=3, xqs=xqs, ngain=0)
+        kw.update(bad)
+        y = hip.Buffer(kw["m"] * N * 2)
+        with pytest.raises(Exception):
+            hip.builtin("gemv", [y, up(hip, np.zeros((4, xqs * kw["m"]), np.float32)), up(hip, w)] +
+                        ([up(hip, sw)] if f8 else []) + [y], **kw)
 
 
 def test_mla_closed_form_equal_rows(hip):

@@ -24,7 +24,9 @@ C_SOURCES = ["hip_backend.c", "hip_custom.c", "decoder.c", "render.c", "tune.c",
 # per (weight type, x type) so the twelve compile in parallel
 GEMV_UNITS = [("kernels/gemv_inst.hip", f"gemv_inst_{w}_{x}",
                [f"-DGEMV_WT={w}", f"-DGEMV_XD={x}", f"-DGEMV_PICK=gemv_pick_{w}_{x}"])
-              for w in range(4) for x in range(3)]
+              for w in range(4) for x in range(3)] + \
+             [("kernels/gemv_inst.hip", f"gemv_inst_{w}_3",   # summed x (norm = 3): bf16 / fp8 weights
+               [f"-DGEMV_WT={w}", "-DGEMV_XD=3", f"-DGEMV_PICK=gemv_pick_{w}_3"]) for w in (2, 3)]
 HIP_SOURCES = ["kernels/gemv.hip", "kernels/gemm.hip", "kernels/rowops.hip", "kernels/attn.hip",
                "kernels/mla.hip", "kernels/moe.hip", "kernels/step.hip", "kernels/step_m1.hip",
                "kernels/step_m2.hip", "kernels/step_m4.hip"]

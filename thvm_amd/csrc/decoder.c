@@ -949,6 +949,12 @@ static int build_dsv2(Decoder *d) {
       !tens_new(d, "h", THVM_DT_BF16, (u64)B * (F ? F : 1) * 2) ||
       !tens_new(d, "mla.part", THVM_DT_FP32, thvm_k_mla_part_bytes(B, H, kv, d->n_split)))
     return -1;
+  /* one row: the MLA merge in latent quarters (4 blocks per head instead of
+   * 2, each reading a quarter of the head's partials), its four f32 quarter
+   * sums added, scaled by the W_uv row scales and rounded to bf16 where the
+   * o projection's GEMV stages x (norm=3); "o" then stays unwritten */
+  const int oqm = B == 1 && kv % 64 == 0;
+  if (oqm && !tens_new(d, "o4", THVM_DT_FP32, (u64)4 * B * H * dv * 4)) return -1;
   /* batches above 4 rows: expert-grouped MoE scratch and its live-expert
    * counter; projections on the MFMA GEMM (bf16 inputs from separate norms) */
   /* (the MFMA form takes D in multiples of 128 and I, S of 64 for fp8
@@ -1017,20 +1023,26 @@ static int build_dsv2(Decoder *d) {
     if (op_add(d, "mla_prep", p, pa, pnn)) return -1;
 
     /* attn_cpb > 0 also sets the MFMA latent split's chunks per block */
+    const u32 o4 = oqm ? tens_find(d, "o4") : 0;
     snprintf(p, sizeof p,
-             "thvm-builtin:mla_attn b=%u h=%u dn=%u dr=%u kv=%u dv=%u maxseq=%u nsplit=%u wt=%u scale=%a cpb=%u",
-             B, H, dn, dr, kv, dv, c->max_seq, d->n_split, wdt, scale, c->attn_cpb);
+             "thvm-builtin:mla_attn b=%u h=%u dn=%u dr=%u kv=%u dv=%u maxseq=%u nsplit=%u wt=%u scale=%a cpb=%u oq=%u",
+             B, H, dn, dr, kv, dv, c->max_seq, d->n_split, wdt, scale, c->attn_cpb, oqm ? 1u : 0u);
     u32 aa[10], an = 0;
-    aa[an++] = o; aa[an++] = qlat; aa[an++] = qpe; aa[an++] = ckv; aa[an++] = kpe; aa[an++] = L;
+    aa[an++] = oqm ? o4 : o; aa[an++] = qlat; aa[an++] = qpe; aa[an++] = ckv; aa[an++] = kpe; aa[an++] = L;
     aa[an++] = tens_find(d, "mla.part"); aa[an++] = wuv;
     if (f8) aa[an++] = suv;
     if (op_add(d, "mla_attn", p, aa, an)) return -1;
 
-    snprintf(p, sizeof p, "thvm-builtin:gemv m=%u n=%u k=%u wt=%u xt=%u yt=%u epi=%u", B, D, H * dv,
-             wdt, THVM_DT_BF16, THVM_DT_BF16, THVM_EPI_RESID);
-    u32 oa[6], on = 0;
-    oa[on++] = x; oa[on++] = o; oa[on++] = wo;
+    if (oqm)
+      snprintf(p, sizeof p, "thvm-builtin:gemv m=%u n=%u k=%u wt=%u xt=%u yt=%u epi=%u norm=3 xqs=%u ngain=%u",
+               B, D, H * dv, wdt, THVM_DT_BF16, THVM_DT_BF16, THVM_EPI_RESID, B * H * dv, f8 ? 1u : 0u);
+    else
+      snprintf(p, sizeof p, "thvm-builtin:gemv m=%u n=%u k=%u wt=%u xt=%u yt=%u epi=%u", B, D, H * dv,
+               wdt, THVM_DT_BF16, THVM_DT_BF16, THVM_EPI_RESID);
+    u32 oa[7], on = 0;
+    oa[on++] = x; oa[on++] = oqm ? o4 : o; oa[on++] = wo;
     if (f8) oa[on++] = so;
+    if (oqm && f8) oa[on++] = suv;                 /* the W_uv row scales as the gain */
     oa[on++] = x;
     if (op_add(d, "gemv_o", p, oa, on)) return -1;
 

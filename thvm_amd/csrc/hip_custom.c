@@ -201,7 +201,8 @@ int hb_builtin_launch(const char *program, const u32 *ids, u32 n, int check_only
          spec_u32(&sp, "waves", &a.tune_waves, 0, 0) || spec_u32(&sp, "r", &a.tune_r, 0, 0) ||
          spec_u32(&sp, "u", &a.tune_u, 0, 0) || spec_u32(&sp, "blocks", &a.tune_blocks, 0, 0) ||
          spec_u32(&sp, "path", &a.tune_path, 0, 0) || spec_u32(&sp, "spec", &a.spec, 0, 0) ||
-         spec_u32(&sp, "tiled", &a.wtiled, 0, 0) || spec_u32(&sp, "clk", &a.clk_cap, 0, 0));
+         spec_u32(&sp, "tiled", &a.wtiled, 0, 0) || spec_u32(&sp, "clk", &a.clk_cap, 0, 0) ||
+         spec_u32(&sp, "xqs", &a.xqs, 0, a.K));
     {
       u32 ldy0 = a.epi == THVM_EPI_SWIGLU ? a.N / 2
                : (a.epi == THVM_EPI_QKV || a.epi == THVM_EPI_QKV_ROPE) ? a.n_heads * a.head_dim
@@ -219,7 +220,8 @@ int hb_builtin_launch(const char *program, const u32 *ids, u32 n, int check_only
     u64 ybytes = qkv ? ((u64)(a.M - 1) * a.ldy + (u64)a.n_heads * a.head_dim) * ysz
                      : ((u64)(a.M - 1) * a.ldy + ncols_out) * ysz;
     a.y = arg(&c, slot++, ybytes);
-    a.x = arg(&c, slot++, ((u64)(a.M - 1) * a.ldx + a.K) * xsz);
+    /* norm=3: x is four f32 vectors xqs elements apart (the MLA quarter sums) */
+    a.x = arg(&c, slot++, a.norm == 3 ? (3ull * a.xqs + a.K) * 4 : ((u64)(a.M - 1) * a.ldx + a.K) * xsz);
     a.w = arg(&c, slot++, (a.wtiled ? ((u64)a.N + 15) / 16 * 16 : (u64)a.N) * a.K * wsz);
     if (a.wdt == THVM_DT_FP8E4M3) a.scale = (const float *)arg(&c, slot++, (u64)a.N * 4);
     if (a.norm && ngain) a.norm_w = (const float *)arg(&c, slot++, (u64)a.K * 4);
@@ -239,7 +241,7 @@ int hb_builtin_launch(const char *program, const u32 *ids, u32 n, int check_only
     /* clk=<blocks>: a phase-clock buffer after the others (blocks x 10 u64) */
     if (a.clk_cap) a.clk = (uint64_t *)arg(&c, slot++, (u64)a.clk_cap * 80);
     if (c.bad) return -1;
-    bytes = (u64)a.N * a.K * wsz + (a.scale ? (u64)a.N * 4 : 0) + (u64)a.M * a.K * xsz +
+    bytes = (u64)a.N * a.K * wsz + (a.scale ? (u64)a.N * 4 : 0) + (u64)a.M * a.K * (a.norm == 3 ? 16 : xsz) +
             (u64)a.M * ncols_out * ysz * (a.res ? 2 : 1);
     if (check_only) return 0;
     if (prof) hb_kprof_begin(K, &e0, &e1);
@@ -312,7 +314,7 @@ int hb_builtin_launch(const char *program, const u32 *ids, u32 n, int check_only
     NEED(spec_u32(&sp, "ldq", &a.ldq, 0, a.H * (a.dn + a.dr) + a.kv + a.dr) ||
          spec_u32(&sp, "nsplit", &a.n_split, 0, (a.max_seq + 63) / 64) ||
          spec_u32(&sp, "mode", &a.mode, 0, 0) || spec_u32(&sp, "cpb", &a.cpb, 0, 0) ||
-         spec_u32(&sp, "clk", &a.clk_cap, 0, 0));
+         spec_u32(&sp, "clk", &a.clk_cap, 0, 0) || spec_u32(&sp, "oq", &a.oq, 0, 0));
     const u32 wsz = hb_dt_size(a.wdt);
     const int fp8 = a.wdt == THVM_DT_FP8E4M3;
     if (!wsz) { hb_set_error("builtin %s: bad weight dtype", K); return -1; }
@@ -332,7 +334,8 @@ int hb_builtin_launch(const char *program, const u32 *ids, u32 n, int check_only
       a.qpe = arg(&c, slot++, (u64)a.B * a.H * a.dr * 2);
       bytes = (u64)a.H * a.kv * a.dn * wsz + (u64)a.B * a.ldq * 2;
     } else {
-      a.o = arg(&c, slot++, (u64)a.B * a.H * a.dv * 2);
+      /* oq=1: the four f32 quarter sums of the latent-quarter merge */
+      a.o = arg(&c, slot++, (u64)a.B * a.H * a.dv * (a.oq ? 16 : 2));
       a.qlat = (float *)arg(&c, slot++, (u64)a.B * a.H * a.kv * 4);
       a.qpe = arg(&c, slot++, (u64)a.B * a.H * a.dr * 2);
       a.ckv = arg(&c, slot++, ckvb);

@@ -58,6 +58,10 @@ typedef struct ThvmGemvArgs {
   uint32_t norm;
   float    norm_eps;
   const float *norm_w;     /* [K] gain or NULL                                */
+  /* norm = 3 (GEMV, one x row, xdt bf16): x is f32 [4][xqs], and the staged
+   * row is bf16(norm_w * ((x0 + x1) + (x2 + x3))) -- the four quarter sums of
+   * the MLA merge in latent quarters, with the W_uv row scales as the gain */
+  uint32_t xqs;
   const float *norm_b;     /* [K] LayerNorm bias or NULL                      */
   /* launch tuning (0 = heuristic): waves per block, rows per wave (MFMA path:
    * 16-row weight tiles per block), chunks per lane in flight, grid blocks,
@@ -188,6 +192,10 @@ typedef struct ThvmMlaArgs {
    * rope 64, the VALU split otherwise; 1 VALU; 2 MFMA) and 64-row chunks per
    * split block (0 auto; the MFMA split takes 1, 2 or 4) */
   uint32_t mode, cpb;
+  /* mla_attn: 1 = the merge in latent quarters (k_mla_out_q): o is then f32
+   * [4][B][H*dv], the four unscaled quarter sums that a GEMV with norm = 3
+   * adds, scales and rounds while staging x; 0 = o is bf16 [B][H*dv] */
+  uint32_t oq;
   /* phase clock (measurement build only; NULL = off): mla_attn records the
    * split's blocks, then the merge's, clk_cap blocks each */
   uint64_t *clk;

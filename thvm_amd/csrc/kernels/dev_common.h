@@ -192,6 +192,11 @@ __device__ __forceinline__ uint4 buf_ld16(buf_t r, uint32_t off) {
   u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
   return make_uint4(v[0], v[1], v[2], v[3]);
 }
+typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint2 buf_ld8(buf_t r, uint32_t off) {
+  u32x2_t v = __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 0);
+  return make_uint2(v[0], v[1]);
+}
 __device__ __forceinline__ uint32_t buf_ld4(buf_t r, uint32_t off) {
   return __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0);
 }

@@ -19,15 +19,17 @@ typedef void (*gemv_fn)(ThvmGemvArgs);
 
 // one picker per (weight type, x type), each in its own gemv_inst.hip unit
 #define GEMV_PICKERS(X) \
-  X(0, 0) X(0, 1) X(0, 2) X(1, 0) X(1, 1) X(1, 2) X(2, 0) X(2, 1) X(2, 2) X(3, 0) X(3, 1) X(3, 2)
+  X(0, 0) X(0, 1) X(0, 2) X(1, 0) X(1, 1) X(1, 2) X(2, 0) X(2, 1) X(2, 2) X(3, 0) X(3, 1) X(3, 2) \
+  X(2, 3) X(3, 3)
 #define GEMV_DECL(w, x) gemv_fn gemv_pick_##w##_##x(uint32_t M, int R, int U);
 GEMV_PICKERS(GEMV_DECL)
 #undef GEMV_DECL
 
 template <int WT>
-static gemv_fn pick_x(uint32_t xdt, uint32_t M, int R, int U) {
-  static_assert(WT_F32 == 0 && WT_FP8 == 3 && XD_BF16 == 0 && XD_F32 == 2, "picker numbering");
-  const int xd = xdt == THVM_DT_BF16 ? XD_BF16 : xdt == THVM_DT_FP16 ? XD_F16 : xdt == THVM_DT_FP32 ? XD_F32 : -1;
+static gemv_fn pick_x(uint32_t xdt, uint32_t M, int R, int U, bool xsum = false) {
+  static_assert(WT_F32 == 0 && WT_FP8 == 3 && XD_BF16 == 0 && XD_F32 == 2 && XD_SUM4 == 3, "picker numbering");
+  const int xd = xsum ? XD_SUM4
+               : xdt == THVM_DT_BF16 ? XD_BF16 : xdt == THVM_DT_FP16 ? XD_F16 : xdt == THVM_DT_FP32 ? XD_F32 : -1;
 #define GEMV_CASE(w, x) if (WT == w && xd == x) return gemv_pick_##w##_##x(M, R, U);
   GEMV_PICKERS(GEMV_CASE)
 #undef GEMV_CASE
@@ -70,7 +72,18 @@ extern "C" int thvm_k_gemv(const ThvmGemvArgs *a, hipStream_t s, char *err, int 
     return -1;
   }
   if (a->ldx < a->K) { snprintf(err, errlen, "gemv: ldx < K"); return -1; }
-  {
+  const bool xsum = a->norm == 3;
+  if (xsum) {
+    // x = bf16(norm_w * ((x0 + x1) + (x2 + x3))) from four f32 vectors
+    if (a->M != 1 || a->xdt != THVM_DT_BF16 || (a->wdt != THVM_DT_FP8E4M3 && a->wdt != THVM_DT_BF16) ||
+        a->K % 8 || a->xqs < a->K || ((uintptr_t)a->x & 7) || ((uintptr_t)a->norm_w & 7) ||
+        a->tune_path == 2 || (3ull * a->xqs + a->K) * 4ull >= (1ull << 31)) {
+      snprintf(err, errlen, "gemv: norm=3 (summed x) takes one bf16 x row over fp8/bf16 weights, "
+               "K a multiple of 8, xqs >= K, 8-byte aligned x and gains");
+      return -1;
+    }
+  }
+  if (!xsum) {
     const uint32_t xs = a->xdt == THVM_DT_FP32 ? 4 : 2, ve = 16 / xs;
     if (a->K % ve || ((uint64_t)a->ldx * xs) % 16 || ((uintptr_t)a->x & 15) ||
         ((uintptr_t)a->norm_w & 15) || ((uintptr_t)a->norm_b & 15)) {
@@ -78,7 +91,7 @@ extern "C" int thvm_k_gemv(const ThvmGemvArgs *a, hipStream_t s, char *err, int 
       return -1;
     }
   }
-  if (a->norm > 2) { snprintf(err, errlen, "gemv: unknown norm %u", a->norm); return -1; }
+  if (a->norm > 3) { snprintf(err, errlen, "gemv: unknown norm %u", a->norm); return -1; }
   // defaults from the gfx950 sweep over the C4 projection shapes (8 waves per
   // block, one row per wave unless the epilogue pairs rows, U=4, <= 512 blocks)
   uint32_t waves = a->tune_waves ? a->tune_waves : 8;
@@ -135,7 +148,7 @@ extern "C" int thvm_k_gemv(const ThvmGemvArgs *a, hipStream_t s, char *err, int 
       return -1;
     }
     const uint32_t nw_norm = waves < 8 ? waves : 8;   // the norm runs on at most 512 threads
-    if (a->norm && a->K > (uint64_t)XREG * 64 * nw_norm) {
+    if (a->norm && !xsum && a->K > (uint64_t)XREG * 64 * nw_norm) {
       snprintf(err, errlen, "gemv: fused norm needs K <= %u for %u waves", XREG * 64 * nw_norm, waves);
       return -1;
     }
@@ -176,7 +189,7 @@ extern "C" int thvm_k_gemv(const ThvmGemvArgs *a, hipStream_t s, char *err, int 
   int U = a->tune_u ? (int)a->tune_u : 4;
   if (U != 4 && U != 8) { snprintf(err, errlen, "gemv: u must be 4 or 8"); return -1; }
   uint32_t xsz = (a->xdt == THVM_DT_FP32 || a->wdt == THVM_DT_FP32) ? 4 : 2;
-  uint64_t lds = (uint64_t)Mk * a->K * xsz;
+  uint64_t lds = (uint64_t)Mk * a->K * xsz + (xsum ? 16 : 0);   // (summed x: a spare word after the row)
   if (lds > 160 * 1024) {
     snprintf(err, errlen, "gemv: M*K=%llu x elements exceed LDS (use the MFMA GEMM)",
              (unsigned long long)Mk * a->K);
@@ -186,8 +199,8 @@ extern "C" int thvm_k_gemv(const ThvmGemvArgs *a, hipStream_t s, char *err, int 
   switch (a->wdt) {
     case THVM_DT_FP32: f = pick_x<WT_F32>(a->xdt, Mk, R, U); break;
     case THVM_DT_FP16: f = pick_x<WT_F16>(a->xdt, Mk, R, U); break;
-    case THVM_DT_BF16: f = pick_x<WT_BF16>(a->xdt, Mk, R, U); break;
-    case THVM_DT_FP8E4M3: f = pick_x<WT_FP8>(a->xdt, Mk, R, U); break;
+    case THVM_DT_BF16: f = pick_x<WT_BF16>(a->xdt, Mk, R, U, xsum); break;
+    case THVM_DT_FP8E4M3: f = pick_x<WT_FP8>(a->xdt, Mk, R, U, xsum); break;
   }
   if (!f) { snprintf(err, errlen, "gemv: no kernel instance (R=%d U=%d)", R, U); return -1; }
   uint32_t Gr = (a->N + R - 1) / R;
@@ -206,6 +219,10 @@ extern "C" int thvm_k_gemv(const ThvmGemvArgs *a, hipStream_t s, char *err, int 
   if (!a->tune_waves && Mk == 1 && chunks == 1 && (uint64_t)a->K * wsz / 16 == 64u * (uint32_t)U &&
       (Gr + 7) / 8 > 256 && (Gr + 15) / 16 <= 256) {
     waves = (Gr + 255) / 256;
+  }
+  if (xsum && a->K > 2u * GEMV_SQ * 64u * waves) {   // the staging's element pairs per thread
+    snprintf(err, errlen, "gemv: norm=3 needs K <= %u at %u waves per block", 2u * GEMV_SQ * 64u * waves, waves);
+    return -1;
   }
   uint32_t need = (Gr + waves - 1) / waves;
   uint32_t grid = need;

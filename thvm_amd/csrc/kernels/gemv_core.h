@@ -162,8 +162,13 @@ __device__ __forceinline__ float block_sum_g(float v, float *red, int nwaves) {
 
 // the output stage of one row group (one lane, wave-uniform values)
 // input x dtype (compile time): vector loads of 16 bytes
-enum { XD_BF16 = 0, XD_F16 = 1, XD_F32 = 2 };
-template <int XD> struct XDr { static constexpr int VE = XD == XD_F32 ? 4 : 8, B = XD == XD_F32 ? 4 : 2; };
+// XD_SUM4: x is the sum of four f32 vectors (stride a.xqs elements), each
+// element scaled by norm_w (when given) and rounded to bf16 as it is staged
+// -- the MLA merge in latent quarters (k_mla_out_q) hands the o projection
+// its four quarter sums this way (M = 1, a.norm = 3)
+enum { XD_BF16 = 0, XD_F16 = 1, XD_F32 = 2, XD_SUM4 = 3 };
+template <int XD> struct XDr { static constexpr int VE = XD == XD_F32 ? 4 : 8, B = XD == XD_BF16 || XD == XD_F16 ? 2 : 4; };
+#define GEMV_SQ 2   /* XD_SUM4: element pairs per thread (K <= 4 x block size) */
 
 // 16 bytes of x (its storage type) -> VE floats
 template <int XD>
@@ -262,7 +267,8 @@ __device__ __forceinline__ bool gemv_core(const ThvmGemvArgs &a, unsigned char *
                                           XRowF &&xrow, HookF &&hook, const uint32_t bdim) {
   constexpr int E = WTr<WT>::E;
   // LDS keeps x in its 16-bit storage type unless weights or x are f32
-  constexpr int XT = (WT == WT_F32 || XD == XD_F32) ? XT_F32 : (XD == XD_BF16 ? XT_BF16 : XT_F16);
+  constexpr int XT = (WT == WT_F32 || XD == XD_F32) ? XT_F32 : (XD == XD_BF16 || XD == XD_SUM4 ? XT_BF16 : XT_F16);
+  static_assert(XD != XD_SUM4 || (M == 1 && !COH && WT != WT_F32), "summed x: one row, standalone");
   constexpr int VE = XDr<XD>::VE;
   const uint32_t K = a.K, N = a.N;
   const uint32_t C = K / E;              // 16-byte weight chunks per row
@@ -350,7 +356,23 @@ __device__ __forceinline__ bool gemv_core(const ThvmGemvArgs &a, unsigned char *
   // x row 0 as raw 16-byte vectors (!COH): the norm path's vectors tid + j*nthr,
   // or the no-norm path's first pass threadIdx.x + j*bdim (clamped
   // indices; out-of-row vectors are never stored)
-  constexpr bool XPRE = !COH && M == 1 && XD != XD_F32;
+  constexpr bool XPRE = !COH && M == 1 && XD != XD_F32 && XD != XD_SUM4;
+  // summed x: thread t's element pairs 2 (t + j bdim) of the four quarters
+  // and their gains, requested before the weights (8-byte unguarded loads)
+  constexpr bool XSUM = XD == XD_SUM4;
+  uint2 sqv[XSUM ? GEMV_SQ : 1][4], sgv[XSUM ? GEMV_SQ : 1];
+  if constexpr (XSUM) {
+    const buf_t xr = buf_rsrc_u(a.x, (3u * a.xqs + K) * 4u);
+    const buf_t gr = buf_rsrc_u(a.norm_w, a.norm_w ? K * 4u : 0u);
+#pragma unroll
+    for (int j = 0; j < GEMV_SQ; j++) {
+      const uint32_t e = 2u * (threadIdx.x + j * bdim);
+      const bool ok = e < K;
+#pragma unroll
+      for (int q = 0; q < 4; q++) sqv[j][q] = buf_ld8(xr, ok ? (q * a.xqs + e) * 4u : BUF_OOB);
+      sgv[j] = buf_ld8(gr, ok ? e * 4u : BUF_OOB);
+    }
+  }
   uint4 xpre[NPRE];
   if (XPRE) {
     const char *x0 = (const char *)xrow(0);
@@ -370,7 +392,7 @@ __device__ __forceinline__ bool gemv_core(const ThvmGemvArgs &a, unsigned char *
   // own (clamped indices; lanes past the row never use them)
   float gw[NVN][VE], gb[NVN][VE];
   auto load_gains = [&] {
-    if (a.norm == 0) return;
+    if (XSUM || a.norm == 0) return;
     const bool hw = a.norm_w != nullptr, hb = a.norm == 2 && a.norm_b != nullptr;
 #pragma unroll
     for (int j = 0; j < NVN; j++) {
@@ -401,6 +423,27 @@ __device__ __forceinline__ bool gemv_core(const ThvmGemvArgs &a, unsigned char *
   if (XPRE) pclk_after(clk, a.clk_cap, 6, xpre[0].x);
 
   // ---- 2. stage x into LDS (16-byte loads), with the fused norm if asked ----
+  if constexpr (XSUM) {
+    // x = bf16(g * ((q0 + q1) + (q2 + q3))) per element, two per 4-byte
+    // store; pairs past K store into the spare word after the row (the host
+    // sizes LDS for it), so no store -- and no load -- sits in a branch
+#pragma unroll
+    for (int j = 0; j < GEMV_SQ; j++) {
+      const uint32_t e = 2u * (threadIdx.x + j * bdim);
+      float v[2];
+#pragma unroll
+      for (int h = 0; h < 2; h++) {
+        const float q0 = __uint_as_float(h ? sqv[j][0].y : sqv[j][0].x);
+        const float q1 = __uint_as_float(h ? sqv[j][1].y : sqv[j][1].x);
+        const float q2 = __uint_as_float(h ? sqv[j][2].y : sqv[j][2].x);
+        const float q3 = __uint_as_float(h ? sqv[j][3].y : sqv[j][3].x);
+        const float gn = a.norm_w ? __uint_as_float(h ? sgv[j].y : sgv[j].x) : 1.0f;
+        v[h] = ((q0 + q1) + (q2 + q3)) * gn;
+      }
+      const uint32_t hi = e < K ? xs_index<XT, E>(K, C, 0, e) : K;
+      *(uint32_t *)(xs_raw + (size_t)hi * 2u) = (uint32_t)f2bf(v[0]) | ((uint32_t)f2bf(v[1]) << 16);
+    }
+  } else
   for (int m = 0; m < M; m++) {
     const void *xr = xrow(m);
     const bool pre = XPRE && m == 0;     // row 0 already in xpre

@@ -6,7 +6,7 @@
 #include "gemv_core.h"
 
 #if !defined(GEMV_WT) || !defined(GEMV_XD) || !defined(GEMV_PICK)
-#error "gemv_inst.hip is compiled with -DGEMV_WT=<0..3> -DGEMV_XD=<0..2> -DGEMV_PICK=<name>"
+#error "gemv_inst.hip is compiled with -DGEMV_WT=<0..3> -DGEMV_XD=<0..3> -DGEMV_PICK=<name>"
 #endif
 
 // The standalone kernel: waves own row groups blockIdx*nw + wave, grid-stride.
@@ -41,12 +41,16 @@ typedef void (*gemv_fn)(ThvmGemvArgs);
 
 template <int WT, int XD, int R, int U>
 static gemv_fn pick_m(uint32_t M) {
-  switch (M) {
-    case 1: return k_gemv<WT, XD, 1, R, U>;
-    case 2: return k_gemv<WT, XD, 2, R, U>;
-    case 3: return k_gemv<WT, XD, 3, R, U>;
-    case 4: return k_gemv<WT, XD, 4, R, U>;
-    default: return nullptr;
+  if constexpr (XD == XD_SUM4) {
+    return M == 1 ? k_gemv<WT, XD, 1, R, U> : nullptr;   // one row only
+  } else {
+    switch (M) {
+      case 1: return k_gemv<WT, XD, 1, R, U>;
+      case 2: return k_gemv<WT, XD, 2, R, U>;
+      case 3: return k_gemv<WT, XD, 3, R, U>;
+      case 4: return k_gemv<WT, XD, 4, R, U>;
+      default: return nullptr;
+    }
   }
 }
 template <int WT, int XD>

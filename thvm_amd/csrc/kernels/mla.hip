@@ -761,6 +761,137 @@ __global__ __launch_bounds__(MLA_OUT_THREADS) void k_mla_out(ThvmMlaArgs a) {
   pclk_end(clk, a.clk_cap);
 }
 
+// ---- k_mla_out_q --------------------------------------------------------
+// The merge in latent quarters, for decodes whose o projection runs on the
+// GEMV (at most 4 rows): k_mla_out's 2 blocks per head each read all of the
+// head's partials (65 x 2 KB at C5 batch 1), and 32 blocks are bound by what
+// one CU can load.  Grid (B*H, MLA_OQ): block (b h, q) merges the live splits
+// over latent columns [q kv/4, (q+1) kv/4) -- the same split weights, each
+// column's partials summed in split-group order -- and applies that quarter
+// of W_uv, writing the unscaled quarter sum oq[q][b][h dv + m] (f32).  The o
+// projection's GEMV adds the four quarters, applies the W_uv row scale and
+// rounds to bf16 as it stages x (norm = 3), where k_mla_out rounds one sum
+// over all kv columns: another summation order, so not the same bits.
+#define MLA_OQ 4
+#define MLA_OQ_PRE 8     /* partial vectors per thread loaded up front */
+#define MLA_OQ_WP 4      /* W_uv load passes */
+template <bool FP8>
+__global__ __launch_bounds__(MLA_OUT_THREADS) void k_mla_out_q(ThvmMlaArgs a) {
+  constexpr uint32_t EPC = FP8 ? 16 : 8;
+  __shared__ float red[16];
+  __shared__ float wsp[MLA_MAX_SPLITS];
+  __shared__ __align__(16) float4 grp[MLA_OUT_THREADS];
+  __shared__ __align__(16) float olq[MF_KV / MLA_OQ];
+  const uint32_t bh = blockIdx.x, b = bh / a.H, h = bh % a.H, kv = a.kv, dv = a.dv, qd = blockIdx.y;
+  const uint32_t kq = kv / MLA_OQ;                                  // this quarter's columns
+  const uint32_t tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  constexpr uint32_t nw = MLA_OUT_THREADS / 64;
+  uint64_t *const clk = a.clk ? a.clk + (uint64_t)a.clk_cap * PCLK_MARKS : nullptr;
+  pclk(clk, a.clk_cap, 0);
+  const uint32_t rowq = kq * (FP8 ? 1 : 2), LPR = rowq / 16;          // lanes per W_uv row quarter
+  const uint32_t rpp = 64 / LPR, sub = lane / LPR, c = lane % LPR;
+  const int32_t L = min(a.len[0], (int32_t)a.max_seq);
+  const uint32_t span = MLA_CHUNK * (a.cpb > 1 ? a.cpb : 1);
+  const uint32_t ns = L > 0 ? ((uint32_t)L + span - 1) / span : 0;
+  const uint64_t pst = (uint64_t)a.H * (kv + 4);
+  const float *p0 = a.part + (uint64_t)b * a.n_split * pst + (uint64_t)h * (kv + 4);
+  // loads in consumption order: m and l, this quarter's partial vectors, the
+  // W_uv row quarters (unguarded buffer loads)
+  const buf_t prs = buf_rsrc_u(p0, (uint32_t)((uint64_t)ns * pst * 4u));
+  const uint32_t mlo = tid < ns ? (uint32_t)(((uint64_t)tid * pst + kv) * 4u) : BUF_OOB;
+  const uint32_t mb = buf_ld4(prs, mlo), lb = buf_ld4(prs, mlo == BUF_OOB ? BUF_OOB : mlo + 4u);
+  const uint32_t nc4 = kq / 4, nsg = MLA_OUT_THREADS / nc4;
+  const uint32_t c4 = tid % nc4, g = tid / nc4;
+  float4 vp[MLA_OQ_PRE];
+#pragma unroll
+  for (int u = 0; u < MLA_OQ_PRE; u++) {
+    const uint32_t sp = g + u * nsg;
+    const uint4 v = buf_ld16(prs, sp < ns ? (uint32_t)(((uint64_t)sp * pst + qd * kq + 4 * c4) * 4u) : BUF_OOB);
+    vp[u] = make_float4(__uint_as_float(v.x), __uint_as_float(v.y), __uint_as_float(v.z), __uint_as_float(v.w));
+  }
+  const buf_t wrs = buf_rsrc(a.wuv, a.H * dv * kv * (FP8 ? 1u : 2u));
+  uint4 wq[MLA_OQ_WP], wq2[MLA_OQ_WP];
+#pragma unroll
+  for (int q = 0; q < MLA_OQ_WP; q++) {
+    const uint32_t mm = (wv + q * nw) * rpp + sub;
+    const uint32_t off = (h * dv + mm) * (kv * (FP8 ? 1u : 2u)) + qd * rowq + c * 16u;
+    wq[q] = buf_ld_stream16(wrs, mm < dv ? off : BUF_OOB);
+    wq2[q] = make_uint4(0, 0, 0, 0);
+  }
+  pclk(clk, a.clk_cap, 4);
+  // split weights w_s = exp(m_s - M) / sum_s exp(m_s - M) l_s, as k_mla_out
+  const float ms = tid < ns ? __uint_as_float(mb) : -INFINITY, ls = __uint_as_float(lb);
+  float M = wave_max(ms);
+  if (lane == 0) red[wv] = M;
+  __syncthreads();
+  M = red[0];
+  for (uint32_t w = 1; w < nw; w++) M = fmaxf(M, red[w]);
+  const float ws = tid < ns ? expf(ms - M) : 0.0f;
+  const float dsum = wave_sum(ws * ls);
+  if (lane == 0) red[8 + wv] = dsum;
+  __syncthreads();
+  float den = 0.0f;
+  for (uint32_t w = 0; w < nw; w++) den += red[8 + w];
+  if (tid < ns) wsp[tid] = ws / den;
+  __syncthreads();
+  pclk(clk, a.clk_cap, 1);
+  float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+  for (int u = 0; u < MLA_OQ_PRE; u++) {
+    const uint32_t sp = g + u * nsg;
+    const float w = sp < ns ? wsp[sp] : 0.0f;
+    acc.x += w * vp[u].x; acc.y += w * vp[u].y; acc.z += w * vp[u].z; acc.w += w * vp[u].w;
+  }
+  for (uint32_t s0 = g + MLA_OQ_PRE * nsg; s0 < ns; s0 += 4 * nsg) {     // longer caches
+    float4 v[4];
+#pragma unroll
+    for (int u = 0; u < 4; u++) {
+      const uint32_t sp = s0 + u * nsg;
+      const uint4 r = buf_ld16(prs, sp < ns ? (uint32_t)(((uint64_t)sp * pst + qd * kq + 4 * c4) * 4u) : BUF_OOB);
+      v[u] = make_float4(__uint_as_float(r.x), __uint_as_float(r.y), __uint_as_float(r.z), __uint_as_float(r.w));
+    }
+#pragma unroll
+    for (int u = 0; u < 4; u++) {
+      const uint32_t sp = s0 + u * nsg;
+      const float w = sp < ns ? wsp[sp] : 0.0f;
+      acc.x += w * v[u].x; acc.y += w * v[u].y; acc.z += w * v[u].z; acc.w += w * v[u].w;
+    }
+  }
+  grp[g * nc4 + c4] = acc;
+  __syncthreads();
+  pclk(clk, a.clk_cap, 2);
+  const uint32_t nchk = kq / EPC;
+  if (tid < nc4) {
+    float4 t = grp[tid];
+    for (uint32_t q = 1; q < nsg; q++) {
+      const float4 v = grp[q * nc4 + tid];
+      t.x += v.x; t.y += v.y; t.z += v.z; t.w += v.w;
+    }
+    ((float4 *)olq)[chunk_swz<EPC>(4 * tid, nchk) / 4] = t;      // W_uv chunk order
+  }
+  __syncthreads();
+  pclk(clk, a.clk_cap, 3);
+  float *oq = (float *)a.o + (uint64_t)qd * a.B * a.H * dv + (uint64_t)b * a.H * dv;
+#pragma unroll
+  for (int q = 0; q < MLA_OQ_WP; q++) {
+    const uint32_t r0 = (wv + q * nw) * rpp;
+    if (r0 >= dv) break;                                           // wave-uniform
+    const uint32_t mm = r0 + sub;
+    float w[16];
+    w16<FP8>(wq[q], wq2[q], w);
+    const float4 *o4 = (const float4 *)olq;
+    float accw = 0.0f;
+#pragma unroll
+    for (uint32_t qd4 = 0; qd4 < EPC / 4; qd4++) {
+      const float4 x = o4[qd4 * nchk + c];
+      accw += x.x * w[4 * qd4] + x.y * w[4 * qd4 + 1] + x.z * w[4 * qd4 + 2] + x.w * w[4 * qd4 + 3];
+    }
+    accw = group_sum(accw, (int)LPR);
+    if (mm < dv && c == 0) oq[(uint64_t)h * dv + mm] = accw;
+  }
+  pclk_end(clk, a.clk_cap);
+}
+
 // -------------------------------------------------------------------------
 static int mla_common(const ThvmMlaArgs *a, char *err, int errlen) {
   if (a->B == 0 || a->H == 0 || a->dn == 0 || a->dr == 0 || a->dr % 2 || a->dr > 64 ||
@@ -865,6 +996,20 @@ extern "C" int thvm_k_mla_attn(const ThvmMlaArgs *a, hipStream_t s, char *err, i
       if (e != hipSuccess) { snprintf(err, errlen, "mla_attn: hipFuncSetAttribute: %s", hipGetErrorString(e)); return -1; }
     }
     thvm_launch(true, false, f, dim3(a->n_split, a->H / MLA_HG, a->B), dim3(MLA_THREADS), lds, s, ak);
+  }
+  if (a->oq) {                                    // the merge in latent quarters
+    const uint32_t kq = a->kv / MLA_OQ, lpr = kq * wsz / 16, rpp = lpr ? 64 / lpr : 0;
+    if (kq * wsz % 16 || lpr == 0 || lpr > 64 || kq % (wsz == 1 ? 16 : 8) ||
+        a->dv > MLA_OQ_WP * 8 * rpp) {
+      snprintf(err, errlen, "mla_attn: oq=1 needs kv/4 a multiple of the 16-byte chunk and d_v <= %u",
+               MLA_OQ_WP * 8 * rpp);
+      return -1;
+    }
+    thvm_launch(false, true, a->wdt == THVM_DT_FP8E4M3 ? k_mla_out_q<true> : k_mla_out_q<false>,
+                dim3(a->B * a->H, MLA_OQ), dim3(MLA_OUT_THREADS), 0, s, ak);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) { snprintf(err, errlen, "mla_attn launch: %s", hipGetErrorString(e)); return -1; }
+    return 0;
   }
   const dim3 g2(a->B * a->H, MLA_OUT_SPLIT);
   const uint32_t lds2 = (a->kv + MLA_MAX_SPLITS + MLA_OUT_THREADS * 4) * 4;
