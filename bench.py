@@ -331,9 +331,10 @@ def run_decode(thvm, key: str, batch: int, args) -> dict:
                                        "gemv_of_ceiling": round(gemv_gbs / ceil, 4)})},
         "attention": ({"kernel": "a stage of k_llama_step (its bytes are in the roofline line)"}
                       if persist else
-                      {"kernel": (("k_mla_split_mf (MFMA) + k_mla_out"
-                                   if (cfg["n_heads"], cfg["kv_lora"], cfg["d_rope"]) == (16, 512, 64)
-                                   else "k_mla_split + k_mla_out") if mla else
+                      {"kernel": (("k_mla_split_mf (MFMA)" if (cfg["n_heads"], cfg["kv_lora"], cfg["d_rope"]) == (16, 512, 64)
+                                   else "k_mla_split") +
+                                  (" + k_mla_out_q (latent quarters)" if batch == 1 and cfg["kv_lora"] % 64 == 0
+                                   else " + k_mla_out") if mla else
                                   "k_attn_mf (MFMA) + k_attn_merge" if _attn_on_mfma(cfg, batch) else
                                   "k_attn_multi + k_attn_merge" if cfg["n_heads"] // cfg["n_kv_heads"] <= 4
                                   else "k_attn + k_attn_merge"),
