@@ -860,10 +860,27 @@ __global__ __launch_bounds__(MLA_OUT_THREADS) void k_mla_out_q(ThvmMlaArgs a) {
   grp[g * nc4 + c4] = acc;
   __syncthreads();
   pclk(clk, a.clk_cap, 2);
-  const uint32_t nchk = kq / EPC;
+  // the nsg group sums of each column in two rounds (groups of 4, then the
+  // nsg / 4 of those, each in group order): a serial pass over nsg = 16
+  // groups by one thread per column had been 16 dependent LDS reads
+  const uint32_t nchk = kq / EPC, nsg4 = nsg / 4;
+  float4 r1 = make_float4(0.f, 0.f, 0.f, 0.f);
+  if (tid < nc4 * nsg4) {
+    const uint32_t cc = tid % nc4, gg = tid / nc4;
+    float4 t = grp[(4 * gg) * nc4 + cc];
+#pragma unroll
+    for (uint32_t q = 1; q < 4; q++) {
+      const float4 v = grp[(4 * gg + q) * nc4 + cc];
+      t.x += v.x; t.y += v.y; t.z += v.z; t.w += v.w;
+    }
+    r1 = t;
+  }
+  __syncthreads();
+  if (tid < nc4 * nsg4) grp[tid] = r1;                             // (gg, cc) at gg nc4 + cc
+  __syncthreads();
   if (tid < nc4) {
     float4 t = grp[tid];
-    for (uint32_t q = 1; q < nsg; q++) {
+    for (uint32_t q = 1; q < nsg4; q++) {
       const float4 v = grp[q * nc4 + tid];
       t.x += v.x; t.y += v.y; t.z += v.z; t.w += v.w;
     }
