@@ -16,6 +16,8 @@
 //     swizzled so the 64 lanes' 16-byte LDS reads hit distinct banks; a fused
 //     RMSNorm / LayerNorm writes the normalised row there already rounded to
 //     the activation dtype, exactly as the separate norm kernel would store it;
+//     a summed x (XD_SUM4, one row) is staged as bf16(g ((x0 + x1) + (x2 + x3)))
+//     from four f32 vectors -- the MLA merge's quarter sums;
 //   * 16-bit x against fp8 or same-type 16-bit weights runs on packed dot
 //     products (v_dot2c_f32_bf16 / _f16; fp8 pairs converted exactly with
 //     v_cvt_scalef32_pk_*_fp8); other pairings decode both operands to f32
