@@ -773,9 +773,11 @@ __global__ __launch_bounds__(MLA_OUT_THREADS) void k_mla_out(ThvmMlaArgs a) {
 // rounds to bf16 as it stages x (norm = 3), where k_mla_out rounds one sum
 // over all kv columns: another summation order, so not the same bits.
 #define MLA_OQ 4
-#define MLA_OQ_PRE 8     /* partial vectors per thread loaded up front */
-#define MLA_OQ_WP 4      /* W_uv load passes */
-template <bool FP8>
+#define MLA_OQ_WP 4      /* W_uv load passes at most */
+// PRE partial vectors per thread loaded up front (a longer cache's rest in a
+// loop), WP W_uv load passes: both chosen at launch to what the rows need --
+// load instructions that only read past the data still cost a CU's issue
+template <bool FP8, int PRE, int WP>
 __global__ __launch_bounds__(MLA_OUT_THREADS) void k_mla_out_q(ThvmMlaArgs a) {
   constexpr uint32_t EPC = FP8 ? 16 : 8;
   __shared__ float red[16];
@@ -802,17 +804,17 @@ __global__ __launch_bounds__(MLA_OUT_THREADS) void k_mla_out_q(ThvmMlaArgs a) {
   const uint32_t mb = buf_ld4(prs, mlo), lb = buf_ld4(prs, mlo == BUF_OOB ? BUF_OOB : mlo + 4u);
   const uint32_t nc4 = kq / 4, nsg = MLA_OUT_THREADS / nc4;
   const uint32_t c4 = tid % nc4, g = tid / nc4;
-  float4 vp[MLA_OQ_PRE];
+  float4 vp[PRE];
 #pragma unroll
-  for (int u = 0; u < MLA_OQ_PRE; u++) {
+  for (int u = 0; u < PRE; u++) {
     const uint32_t sp = g + u * nsg;
     const uint4 v = buf_ld16(prs, sp < ns ? (uint32_t)(((uint64_t)sp * pst + qd * kq + 4 * c4) * 4u) : BUF_OOB);
     vp[u] = make_float4(__uint_as_float(v.x), __uint_as_float(v.y), __uint_as_float(v.z), __uint_as_float(v.w));
   }
   const buf_t wrs = buf_rsrc(a.wuv, a.H * dv * kv * (FP8 ? 1u : 2u));
-  uint4 wq[MLA_OQ_WP], wq2[MLA_OQ_WP];
+  uint4 wq[WP], wq2[WP];
 #pragma unroll
-  for (int q = 0; q < MLA_OQ_WP; q++) {
+  for (int q = 0; q < WP; q++) {
     const uint32_t mm = (wv + q * nw) * rpp + sub;
     const uint32_t off = (h * dv + mm) * (kv * (FP8 ? 1u : 2u)) + qd * rowq + c * 16u;
     wq[q] = buf_ld_stream16(wrs, mm < dv ? off : BUF_OOB);
@@ -837,12 +839,12 @@ __global__ __launch_bounds__(MLA_OUT_THREADS) void k_mla_out_q(ThvmMlaArgs a) {
   pclk(clk, a.clk_cap, 1);
   float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
-  for (int u = 0; u < MLA_OQ_PRE; u++) {
+  for (int u = 0; u < PRE; u++) {
     const uint32_t sp = g + u * nsg;
     const float w = sp < ns ? wsp[sp] : 0.0f;
     acc.x += w * vp[u].x; acc.y += w * vp[u].y; acc.z += w * vp[u].z; acc.w += w * vp[u].w;
   }
-  for (uint32_t s0 = g + MLA_OQ_PRE * nsg; s0 < ns; s0 += 4 * nsg) {     // longer caches
+  for (uint32_t s0 = g + PRE * nsg; s0 < ns; s0 += 4 * nsg) {     // longer caches
     float4 v[4];
 #pragma unroll
     for (int u = 0; u < 4; u++) {
@@ -890,7 +892,7 @@ __global__ __launch_bounds__(MLA_OUT_THREADS) void k_mla_out_q(ThvmMlaArgs a) {
   pclk(clk, a.clk_cap, 3);
   float *oq = (float *)a.o + (uint64_t)qd * a.B * a.H * dv + (uint64_t)b * a.H * dv;
 #pragma unroll
-  for (int q = 0; q < MLA_OQ_WP; q++) {
+  for (int q = 0; q < WP; q++) {
     const uint32_t r0 = (wv + q * nw) * rpp;
     if (r0 >= dv) break;                                           // wave-uniform
     const uint32_t mm = r0 + sub;
@@ -1022,8 +1024,17 @@ extern "C" int thvm_k_mla_attn(const ThvmMlaArgs *a, hipStream_t s, char *err, i
                MLA_OQ_WP * 8 * rpp);
       return -1;
     }
-    thvm_launch(false, true, a->wdt == THVM_DT_FP8E4M3 ? k_mla_out_q<true> : k_mla_out_q<false>,
-                dim3(a->B * a->H, MLA_OQ), dim3(MLA_OUT_THREADS), 0, s, ak);
+    // up front: the partials a split group folds (65 at C5 batch 1, 16 groups:
+    // 5), else 8 and a loop; W_uv passes: 8 waves x rpp rows each over d_v
+    const uint32_t nsg = MLA_OUT_THREADS / (kq / 4), nsp = (a->n_split + ak.cpb - 1) / ak.cpb;
+    const bool pre5 = nsp <= 5 * nsg, wp2 = a->dv <= 2 * 8 * rpp;
+    const bool f8 = a->wdt == THVM_DT_FP8E4M3;
+    void (*fq)(ThvmMlaArgs) =
+        f8 ? (pre5 ? (wp2 ? k_mla_out_q<true, 5, 2> : k_mla_out_q<true, 5, 4>)
+                   : (wp2 ? k_mla_out_q<true, 8, 2> : k_mla_out_q<true, 8, 4>))
+           : (pre5 ? (wp2 ? k_mla_out_q<false, 5, 2> : k_mla_out_q<false, 5, 4>)
+                   : (wp2 ? k_mla_out_q<false, 8, 2> : k_mla_out_q<false, 8, 4>));
+    thvm_launch(false, true, fq, dim3(a->B * a->H, MLA_OQ), dim3(MLA_OUT_THREADS), 0, s, ak);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) { snprintf(err, errlen, "mla_attn launch: %s", hipGetErrorString(e)); return -1; }
     return 0;
